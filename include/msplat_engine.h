@@ -1,0 +1,271 @@
+/*
+ * msplat_engine.h -- C-ABI launch layer of the MI355X (gfx950) engine.
+ *
+ * This is the boundary between the C++ host (MTensor / Model / Trainer, the
+ * public C API in msplat_c_api.h) and the hand-written HIP kernels.  It
+ * replaces the reference's internal engine interface
+ * core/metal/bindings.h:7-158 (plain C++ functions taking MTensor&) with
+ * extern "C" entry points that take plain device pointers and sizes, so a
+ * cgo / ctypes / JNI caller can bind it directly.
+ *
+ * Conventions
+ *  - All pointers named *_dev are device pointers (hipMalloc memory, e.g.
+ *    from msplat_hip_alloc).  Host pointers are named *_host.
+ *  - Every entry point returns 0 on success and a negative MSPLAT_E_* code
+ *    on failure; msplat_hip_last_error() gives the message.  No C++
+ *    exception crosses this boundary.
+ *  - All work runs in order on the engine's single HIP stream (the
+ *    reference's serial dispatch queue, msplat_metal.mm:182,732).  Entry
+ *    points are asynchronous unless documented otherwise.
+ *  - One engine per process (the reference's g_tcache,
+ *    msplat_metal.mm:538): intermediate buffers are cached and reused.
+ */
+#ifndef MSPLAT_ENGINE_H
+#define MSPLAT_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MSPLAT_OK 0
+#define MSPLAT_E_HIP (-1)       /* a HIP runtime call failed            */
+#define MSPLAT_E_ARG (-2)       /* invalid argument / shape             */
+#define MSPLAT_E_NOMEM (-3)     /* device allocation failed             */
+#define MSPLAT_E_NODEV (-4)     /* no usable gfx950 device              */
+#define MSPLAT_E_CAPACITY (-5)  /* caller-provided capacity too small   */
+
+#define MSPLAT_TILE 16          /* BLOCK_X / BLOCK_Y, core/include/msplat.hpp:4-5 */
+#define MSPLAT_REC_FLOATS 20    /* per-gaussian splat record, see DESIGN    */
+#define MSPLAT_GRAD_FLOATS 16   /* per-gaussian raster-gradient record       */
+
+/* Camera + projection set-up: the arguments of msplat_train_step_2dgs /
+ * msplat_render (bindings.h:47-62, 145-155) that Model::prepareCam
+ * (core/src/model.cpp:500-544) computes. */
+typedef struct {
+    float viewmat[16];   /* world -> camera, row-major                   */
+    float projmat[16];   /* world -> clip (P*V), row-major               */
+    float cam_pos[3];
+    float fx, fy, cx, cy;
+    int32_t width, height;
+    int32_t tiles_x, tiles_y;
+    float glob_scale;    /* 1.0 in Model (model.cpp:550,782)             */
+    float clip_thresh;   /* 0.01 in Model                                */
+    int32_t degree;      /* SH degree of the features_rest layout        */
+    int32_t degrees_to_use;
+} MsplatCamera;
+
+/* The six parameter groups (Model::means ... opacities, model.hpp:81-86)
+ * as device pointers: means[N,3], scales[N,2] (log), quats[N,4] (w,x,y,z),
+ * opacities[N] (logit), features_dc[N,3], features_rest[N,K,3]. */
+typedef struct {
+    int32_t num_points;
+    float *means;
+    float *scales;
+    float *quats;
+    float *opacities;
+    float *features_dc;
+    float *features_rest;
+} MsplatGaussians;
+
+/* Adam state and step sizes for the six groups (model.cpp:806-826). */
+typedef struct {
+    float *exp_avg[6];
+    float *exp_avg_sq[6];
+    float step_size[6];  /* lr[g] / (1 - beta1^t)                        */
+    float beta1, beta2;
+    float bc2_sqrt;      /* sqrt(1 - beta2^t)                            */
+    float eps;
+} MsplatAdam;
+
+/* Model::prepareCam (core/src/model.cpp:500-544) without the downscale:
+ * viewmat = inverse of camToWorld after negating its columns 1 and 2
+ * (OpenGL -> OpenCV), projmat = P(fovX, fovY, near 0.001, far 1000) * V,
+ * cam_pos = translation, tiles = ceil(W/16) x ceil(H/16).  Host only. */
+int msplat_hip_prepare_camera(const float cam_to_world[16], float fx, float fy,
+                              float cx, float cy, int width, int height,
+                              int degree, int degrees_to_use,
+                              MsplatCamera *out);
+
+/* ---- context, memory, stream (bindings.h:7-25) -------------------------- */
+
+/* Creates the engine (device 0, one stream).  Idempotent.  Replaces the
+ * lazily created MetalContext (msplat_metal.mm:287-293). */
+int msplat_hip_init(void);
+/* Releases every cached buffer: cleanup_msplat_metal (bindings.h:8). */
+void msplat_hip_cleanup(void);
+const char *msplat_hip_last_error(void);
+/* Device name / gfx arch of the engine's device into buf. */
+int msplat_hip_device_name(char *buf, int len);
+
+/* gpu_empty / gpu_zeros (bindings.h:17-18). */
+void *msplat_hip_alloc(size_t bytes);
+int msplat_hip_free(void *ptr_dev);
+int msplat_hip_memset(void *ptr_dev, int value, size_t bytes);
+int msplat_hip_upload(void *dst_dev, const void *src_host, size_t bytes);
+int msplat_hip_download(void *dst_host, const void *src_dev, size_t bytes);
+int msplat_hip_copy(void *dst_dev, const void *src_dev, size_t bytes);
+/* msplat_commit (bindings.h:21): work is already queued; returns at once. */
+int msplat_hip_commit(void);
+/* msplat_gpu_sync (bindings.h:24): waits for the engine stream. */
+int msplat_hip_sync(void);
+
+/* ---- the training step and render path ---------------------------------- */
+
+/* msplat_train_step_2dgs (bindings.h:47-62): projection + SH, tile binning,
+ * per-tile depth sort, rasterize forward, SSIM + L1 loss forward/backward,
+ * rasterize backward, projection + SH backward.  Synchronous (reads the
+ * loss back, like msplat_metal.mm:1328-1330).
+ *  - gt_dev is the [H,W,3] target image;
+ *  - xys_grad_norm/vis_counts/max_2d_size are [N] densify statistics,
+ *    read-modify-write (model.cpp:771-775);
+ *  - adam == NULL: per-group gradients are written to the engine cache
+ *    (msplat_hip_last) for msplat_hip_fused_adam, as the reference does;
+ *  - adam != NULL: the six Adam updates are fused into the projection
+ *    backward and applied to g in place (no gradient tensors are written).
+ *  *loss_host receives the scalar loss; *num_isect_host (nullable) the
+ *  tile-intersection count. */
+int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g,
+                          const float *background_dev, const float *gt_dev,
+                          float lambda_l1, float lambda_dist,
+                          float lambda_dssim, float *xys_grad_norm_dev,
+                          float *vis_counts_dev, float *max_2d_size_dev,
+                          float inv_max_dim, const MsplatAdam *adam,
+                          float *loss_host, int64_t *num_isect_host);
+
+/* msplat_render (bindings.h:145-155): forward only; outputs in the cache
+ * (MSPLAT_LAST_OUT_IMG etc.).  Asynchronous apart from one mid-pipeline
+ * read of the intersection count. */
+int msplat_hip_render(const MsplatCamera *cam, const MsplatGaussians *g,
+                      const float *background_dev, int64_t *num_isect_host);
+
+/* msplat_fused_adam (bindings.h:135-140): one Adam step on n floats. */
+int msplat_hip_fused_adam(float *params_dev, const float *grads_dev,
+                          float *exp_avg_dev, float *exp_avg_sq_dev,
+                          int64_t n, float step_size, float beta1,
+                          float beta2, float bc2_sqrt, float eps);
+
+/* msplat_densify (bindings.h:143-158): classify, append split/dup children,
+ * cull, stable compaction of the 18 capacity-sized buffers.  params[6],
+ * exp_avg[6], exp_avg_sq[6] are the backing buffers (strides 3, 2, 4, 3,
+ * fr_stride, 1); random_samples_dev is [2N,3].  Synchronous; returns the
+ * new count in *new_count_host. */
+int msplat_hip_densify(int n, int capacity, float grad_thresh,
+                       float size_thresh, float screen_thresh,
+                       int check_screen, float cull_alpha_thresh,
+                       float cull_scale_thresh, float cull_screen_size,
+                       int check_huge, const float *xys_grad_norm_dev,
+                       const float *vis_counts_dev,
+                       const float *max_2d_size_dev, float half_max_dim,
+                       float *const params_dev[6], int fr_stride,
+                       float *const exp_avg_dev[6],
+                       float *const exp_avg_sq_dev[6],
+                       const float *random_samples_dev, int *new_count_host);
+
+/* ---- stage entry points (each one kernel of the step) -------------------- */
+
+/* ssim_* + loss_l1_distortion_2dgs + ssim_backward_* kernels
+ * (msplat_metal.metal:2704-3085) fused into two passes.  dL_dimg_dev
+ * [H,W,3] is overwritten; distortion_dev may be NULL when lambda_dist == 0.
+ * Synchronous (reads the loss). */
+int msplat_hip_loss_fwd_bwd(int width, int height, const float *img_dev,
+                            const float *gt_dev, const float *distortion_dev,
+                            float lambda_l1, float lambda_dist,
+                            float lambda_dssim, float *dL_dimg_dev,
+                            double *loss_host, double *ssim_sum_host);
+
+/* nd_rasterize_backward_2dgs (msplat_metal.metal:1705-1979) on the forward
+ * state of the most recent render / train step.  Per-pixel upstream
+ * gradients [H,W,{3,1}] may be NULL (zero).  grads16_dev [N,16] is
+ * accumulated into (caller zeroes it): dL_dtransMat[9], dL_dnormal3D[3],
+ * dL_dopacity (logit), dL_dcolors[3]. */
+int msplat_hip_raster_bwd(const float *dL_dimg_dev, const float *dL_ddepth_dev,
+                          const float *dL_dalpha_dev,
+                          const float *dL_dnormal_dev,
+                          const float *dL_dmedian_dev,
+                          const float *dL_ddistortion_dev, float *grads16_dev);
+
+/* project_and_sh_backward_2dgs (msplat_metal.metal:2003-2209) on explicit
+ * inputs (radii from the forward, grads16 from the raster backward).
+ * Outputs [N,3],[N,2],[N,4],[N,2],[N,3],[N,K,3] are overwritten; the three
+ * densify statistics are read-modify-write. */
+int msplat_hip_project_bwd(const MsplatCamera *cam, const MsplatGaussians *g,
+                           const int32_t *radii_dev, const float *grads16_dev,
+                           float *dL_dmeans_dev, float *dL_dscales_dev,
+                           float *dL_dquats_dev, float *dL_dmean2d_dev,
+                           float *dL_dfeatures_dc_dev,
+                           float *dL_dfeatures_rest_dev,
+                           float *xys_grad_norm_dev, float *vis_counts_dev,
+                           float *max_2d_size_dev, float inv_max_dim);
+
+/* The projection backward above with the six Adam updates fused in
+ * (Model::fullIteration's Adam loop, core/src/model.cpp:806-826, applied in
+ * registers): g's parameters and adam's moments are updated in place and no
+ * gradient tensor is written.  Bit-identical to msplat_hip_project_bwd
+ * followed by msplat_hip_fused_adam on each group. */
+int msplat_hip_project_bwd_adam(const MsplatCamera *cam,
+                                const MsplatGaussians *g,
+                                const int32_t *radii_dev,
+                                const float *grads16_dev,
+                                float *xys_grad_norm_dev,
+                                float *vis_counts_dev, float *max_2d_size_dev,
+                                float inv_max_dim, const MsplatAdam *adam);
+
+/* ---- cached buffers (the msplat_last_* accessors, bindings.h:36-42,
+ *      bindings.h:103-130) ------------------------------------------------ */
+enum {
+    MSPLAT_LAST_XYS = 0,          /* [N,2]  f32 (materialised)           */
+    MSPLAT_LAST_DEPTHS,           /* [N]    f32                          */
+    MSPLAT_LAST_RADII,            /* [N]    i32                          */
+    MSPLAT_LAST_NUM_TILES_HIT,    /* [N]    i32 (materialised)           */
+    MSPLAT_LAST_TRANSMATS,        /* [N,9]  f32 (materialised)           */
+    MSPLAT_LAST_COLORS_USED,      /* [N,3]  f32 max(raw+0.5,0) (mat.)    */
+    MSPLAT_LAST_OPACITY_SIGMOID,  /* [N]    f32 (materialised)           */
+    MSPLAT_LAST_NORMALS,          /* [N,3]  f32 (materialised)           */
+    MSPLAT_LAST_RECORDS,          /* [N,20] f32 splat records            */
+    MSPLAT_LAST_TILE_OFFSETS,     /* [T+1]  i32                          */
+    MSPLAT_LAST_GAUSSIAN_IDS,     /* [I]    i32 sorted per tile          */
+    MSPLAT_LAST_OUT_IMG,          /* [H,W,3] f32                         */
+    MSPLAT_LAST_FINAL_TS,         /* [H,W,3] f32 (T, M1, M2)             */
+    MSPLAT_LAST_FINAL_IDX,        /* [H,W,2] i32 (last, median)          */
+    MSPLAT_LAST_OUT_DEPTH,        /* [H,W]  f32                          */
+    MSPLAT_LAST_OUT_NORMAL,       /* [H,W,3] f32                         */
+    MSPLAT_LAST_OUT_ALPHA,        /* [H,W]  f32                          */
+    MSPLAT_LAST_OUT_MEDIAN_DEPTH, /* [H,W]  f32                          */
+    MSPLAT_LAST_OUT_DISTORTION,   /* [H,W]  f32                          */
+    MSPLAT_LAST_DL_DOUT_IMG,      /* [H,W,3] f32                         */
+    MSPLAT_LAST_GRADS16,          /* [N,16] f32 raster gradients         */
+    MSPLAT_LAST_DL_DTRANSMAT,     /* [N,9]  f32 (materialised)           */
+    MSPLAT_LAST_DL_DNORMAL3D,     /* [N,3]  f32 (materialised)           */
+    MSPLAT_LAST_DL_DOPACITY,      /* [N]    f32 (materialised)           */
+    MSPLAT_LAST_DL_DCOLORS,       /* [N,3]  f32 (materialised)           */
+    MSPLAT_LAST_DL_DMEAN3D,       /* [N,3]  f32 (unfused step only)      */
+    MSPLAT_LAST_DL_DSCALE,        /* [N,2]                               */
+    MSPLAT_LAST_DL_DQUAT,         /* [N,4]                               */
+    MSPLAT_LAST_DL_DMEAN2D,       /* [N,2]                               */
+    MSPLAT_LAST_DL_DFEATURES_DC,  /* [N,3]                               */
+    MSPLAT_LAST_DL_DFEATURES_REST,/* [N,K,3]                             */
+    MSPLAT_LAST_COUNT
+};
+/* Returns the device pointer and element count of a cached buffer (NULL /
+ * 0 if it does not exist yet).  Materialised entries are gathered from the
+ * packed records on each call (asynchronously, on the engine stream). */
+int msplat_hip_last(int which, void **ptr_dev, int64_t *numel);
+
+/* Per-kernel timings of the most recent train step / render, in ms, from
+ * HIP events recorded on the engine stream when timing is enabled
+ * (the PROFILE_GPU hooks of msplat_metal.mm:20-23).  names receives up to
+ * max entries of static strings. */
+int msplat_hip_enable_timing(int enable);
+int msplat_hip_stage_times(const char **names, float *ms, int max);
+/* Raster work counter of the most recent forward: (pixel, gaussian) pairs
+ * evaluated (enabled with timing). */
+int64_t msplat_hip_last_pairs_evaluated(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

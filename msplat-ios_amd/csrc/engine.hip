@@ -1,0 +1,712 @@
+// engine.hip -- the C-ABI launch layer (include/msplat_engine.h): one HIP
+// stream, a cache of intermediate device buffers that grows on demand, and
+// the stage sequencing of the reference's msplat_train_step_2dgs /
+// msplat_render / msplat_fused_adam / msplat_densify
+// (core/metal/msplat_metal.mm:545-1594).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <exception>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "kernels.h"
+#include "msplat_engine.h"
+
+namespace {
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+enum StageId { ST_PROJECT, ST_SCAN, ST_SCATTER_SORT, ST_RASTER_FWD, ST_LOSS, ST_RASTER_BWD, ST_PROJECT_BWD, ST_COUNT };
+const char *kStageNames[ST_COUNT] = {"project_fwd", "tile_scan", "scatter_sort", "raster_fwd",
+                                     "ssim_l1",     "raster_bwd", "project_bwd_adam"};
+
+struct Engine {
+    bool ready = false;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int *pinned_i = nullptr;     // small pinned readback area
+    double *pinned_d = nullptr;
+    float window[11];
+    // per-gaussian
+    DevBuf rec, depths, radii, rect, grads16, colors_raw;
+    // per-tile
+    DevBuf counts, offsets, cursor, stats, big_list;
+    // per-intersection
+    DevBuf keys, keys_tmp, ids;
+    // per-pixel
+    DevBuf out_img, final_Ts, final_idx, out_depth, out_normal, out_alpha, out_median, out_dist;
+    DevBuf dL_dimg, gm1, gs1, gs12, partials, loss;
+    // unfused gradients
+    DevBuf dmeans, dscales, dquats, dmean2d, dfdc, dfrest;
+    // materialised views
+    DevBuf mat[MSPLAT_LAST_COUNT];
+    // densify scratch
+    DevBuf dens_scratch[18], dens_flags, dens_scan;
+    DevBuf pair_counter;
+    // state of the most recent forward
+    int n = 0, W = 0, H = 0, tiles_x = 0, tiles_y = 0, K3 = 0;
+    int64_t num_isect = 0;
+    const float *bg = nullptr;
+    bool have_grads = false;
+    // timing
+    bool timing = false;
+    hipEvent_t ev[ST_COUNT + 1] = {};
+    float stage_ms[ST_COUNT] = {};
+    bool stage_valid[ST_COUNT] = {};
+    int64_t pairs = 0;
+};
+
+Engine g_eng;
+std::mutex g_mu;
+char g_err[1024] = "";
+
+void set_err(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+#define HIPC(expr)                                                                        \
+    do {                                                                                  \
+        hipError_t e_ = (expr);                                                           \
+        if (e_ != hipSuccess) {                                                           \
+            set_err("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, __LINE__); \
+            return MSPLAT_E_HIP;                                                          \
+        }                                                                                 \
+    } while (0)
+
+#define CHECK(expr)                   \
+    do {                              \
+        int r_ = (expr);              \
+        if (r_ != MSPLAT_OK) return r_; \
+    } while (0)
+
+int ensure(DevBuf &b, size_t bytes) {
+    if (bytes == 0) bytes = 16;
+    if (b.cap >= bytes) return MSPLAT_OK;
+    if (b.p) HIPC(hipFree(b.p));
+    b.p = nullptr;
+    b.cap = 0;
+    const size_t want = bytes + bytes / 8;  // headroom against small growth
+    if (hipMalloc(&b.p, want) != hipSuccess) {
+        (void)hipGetLastError();
+        set_err("hipMalloc(%zu bytes) failed", want);
+        b.p = nullptr;
+        return MSPLAT_E_NOMEM;
+    }
+    b.cap = want;
+    return MSPLAT_OK;
+}
+
+template <typename T>
+T *P(DevBuf &b) {
+    return static_cast<T *>(b.p);
+}
+
+int init_locked() {
+    if (g_eng.ready) return MSPLAT_OK;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        (void)hipGetLastError();
+        set_err("no HIP device available");
+        return MSPLAT_E_NODEV;
+    }
+    HIPC(hipSetDevice(g_eng.device));
+    hipDeviceProp_t prop;
+    HIPC(hipGetDeviceProperties(&prop, g_eng.device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        set_err("device arch %s is not gfx950", prop.gcnArchName);
+        return MSPLAT_E_NODEV;
+    }
+    HIPC(hipStreamCreateWithFlags(&g_eng.stream, hipStreamNonBlocking));
+    HIPC(hipHostMalloc((void **)&g_eng.pinned_i, 64 * sizeof(int), hipHostMallocDefault));
+    HIPC(hipHostMalloc((void **)&g_eng.pinned_d, 16 * sizeof(double), hipHostMallocDefault));
+    for (int i = 0; i <= ST_COUNT; ++i) HIPC(hipEventCreate(&g_eng.ev[i]));
+    // The 11-tap SSIM window exp(-(x-5)^2 / 4.5) / sum (the table of
+    // msplat_metal.metal:2804-2816), evaluated in double and rounded once.
+    double gsum = 0.0, gw[11];
+    for (int i = 0; i < 11; ++i) {
+        const double d = i - 5.0;
+        gw[i] = std::exp(-d * d / (2.0 * 1.5 * 1.5));
+        gsum += gw[i];
+    }
+    for (int i = 0; i < 11; ++i) g_eng.window[i] = (float)(gw[i] / gsum);
+    g_eng.ready = true;
+    return MSPLAT_OK;
+}
+
+#define ENSURE_INIT()                      \
+    do {                                   \
+        int r0_ = init_locked();           \
+        if (r0_ != MSPLAT_OK) return r0_;  \
+    } while (0)
+
+void stage_mark(int s) {
+    if (g_eng.timing) (void)hipEventRecord(g_eng.ev[s], g_eng.stream);
+}
+
+int validate_cam(const MsplatCamera *cam, const MsplatGaussians *g) {
+    if (!cam || !g) {
+        set_err("null camera or gaussians");
+        return MSPLAT_E_ARG;
+    }
+    if (cam->width <= 0 || cam->height <= 0 || cam->tiles_x != (cam->width + 15) / 16 ||
+        cam->tiles_y != (cam->height + 15) / 16 || cam->tiles_x > 65535 || cam->tiles_y > 65535) {
+        set_err("invalid image size %dx%d / tiles %dx%d", cam->width, cam->height, cam->tiles_x, cam->tiles_y);
+        return MSPLAT_E_ARG;
+    }
+    if (cam->degree < 0 || cam->degree > 4 || cam->degrees_to_use < 0 || cam->degrees_to_use > cam->degree) {
+        set_err("invalid SH degree %d / degrees_to_use %d", cam->degree, cam->degrees_to_use);
+        return MSPLAT_E_ARG;
+    }
+    if (g->num_points < 0 ||
+        (g->num_points > 0 && (!g->means || !g->scales || !g->quats || !g->opacities || !g->features_dc ||
+                               (cam->degree > 0 && !g->features_rest)))) {
+        set_err("invalid gaussian buffers");
+        return MSPLAT_E_ARG;
+    }
+    return MSPLAT_OK;
+}
+
+// Stages a3-a7: projection, binning, per-tile sort, rasterize forward.
+int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, int64_t *nisect) {
+    CHECK(validate_cam(cam, g));
+    if (!bg) {
+        set_err("null background");
+        return MSPLAT_E_ARG;
+    }
+    Engine &E = g_eng;
+    hipStream_t s = E.stream;
+    const int N = g->num_points, W = cam->width, H = cam->height;
+    const int T = cam->tiles_x * cam->tiles_y;
+    const size_t Pn = (size_t)W * H;
+    const int nb = cam->degree == 0 ? 1 : cam->degree == 1 ? 4 : cam->degree == 2 ? 9 : cam->degree == 3 ? 16 : 25;
+    CHECK(ensure(E.rec, (size_t)N * MSPLAT_REC_FLOATS * 4));
+    CHECK(ensure(E.depths, (size_t)N * 4));
+    CHECK(ensure(E.radii, (size_t)N * 4));
+    CHECK(ensure(E.rect, (size_t)N * 8));
+    CHECK(ensure(E.counts, (size_t)T * 4));
+    CHECK(ensure(E.offsets, (size_t)(T + 1) * 4));
+    CHECK(ensure(E.cursor, (size_t)T * 4));
+    CHECK(ensure(E.stats, 16));
+    CHECK(ensure(E.big_list, (size_t)T * 4));
+    CHECK(ensure(E.out_img, Pn * 12));
+    CHECK(ensure(E.final_Ts, Pn * 12));
+    CHECK(ensure(E.final_idx, Pn * 8));
+    CHECK(ensure(E.out_depth, Pn * 4));
+    CHECK(ensure(E.out_normal, Pn * 12));
+    CHECK(ensure(E.out_alpha, Pn * 4));
+    CHECK(ensure(E.out_median, Pn * 4));
+    CHECK(ensure(E.out_dist, Pn * 4));
+    CHECK(ensure(E.pair_counter, 8));
+    E.n = N;
+    E.W = W;
+    E.H = H;
+    E.tiles_x = cam->tiles_x;
+    E.tiles_y = cam->tiles_y;
+    E.K3 = (nb - 1) * 3;
+    E.bg = bg;
+    E.have_grads = false;
+    for (int i = 0; i < ST_COUNT; ++i) E.stage_valid[i] = false;
+
+    stage_mark(ST_PROJECT);
+    HIPC(hipMemsetAsync(E.counts.p, 0, (size_t)T * 4, s));
+    if (E.timing) HIPC(hipMemsetAsync(E.pair_counter.p, 0, 8, s));
+    mskern::launch_project_fwd(s, *cam, *g, P<float>(E.rec), P<float>(E.depths), P<int>(E.radii),
+                               P<uint32_t>(E.rect), P<int>(E.counts), nullptr);
+    stage_mark(ST_SCAN);
+    mskern::launch_scan_tiles(s, T, P<int>(E.counts), P<int>(E.offsets), P<int>(E.cursor), P<int>(E.stats));
+    HIPC(hipMemcpyAsync(E.pinned_i, E.stats.p, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
+    HIPC(hipStreamSynchronize(s));
+    const int I = E.pinned_i[0], max_count = E.pinned_i[1];
+    if (I < 0) {
+        set_err("tile intersection count overflowed int32");
+        return MSPLAT_E_CAPACITY;
+    }
+    E.num_isect = I;
+    if (nisect) *nisect = I;
+    stage_mark(ST_SCATTER_SORT);
+    CHECK(ensure(E.keys, (size_t)I * 8));
+    CHECK(ensure(E.ids, (size_t)I * 4));
+    if (max_count > 2048) CHECK(ensure(E.keys_tmp, (size_t)I * 8));
+    mskern::launch_scatter(s, N, cam->tiles_x, P<int>(E.radii), P<uint32_t>(E.rect), P<float>(E.depths),
+                           P<int>(E.cursor), P<uint64_t>(E.keys));
+    mskern::launch_sort_tiles(s, T, max_count, P<int>(E.offsets), P<uint64_t>(E.keys), P<uint64_t>(E.keys_tmp),
+                              P<int>(E.ids), P<int>(E.big_list), P<int>(E.stats));
+    stage_mark(ST_RASTER_FWD);
+    mskern::launch_raster_fwd(s, W, H, cam->tiles_x, cam->tiles_y, P<int>(E.offsets), P<int>(E.ids),
+                              P<float>(E.rec), bg, P<float>(E.out_img), P<float>(E.final_Ts), P<int>(E.final_idx),
+                              P<float>(E.out_depth), P<float>(E.out_normal), P<float>(E.out_alpha),
+                              P<float>(E.out_median), P<float>(E.out_dist),
+                              E.timing ? P<unsigned long long>(E.pair_counter) : nullptr);
+    HIPC(hipGetLastError());
+    return MSPLAT_OK;
+}
+
+int loss_locked(int W, int H, const float *img, const float *gt, const float *dist, float l1, float ldist,
+                float ldssim, float *dL) {
+    Engine &E = g_eng;
+    const size_t E3 = (size_t)W * H * 3;
+    CHECK(ensure(E.gm1, E3 * 4));
+    CHECK(ensure(E.gs1, E3 * 4));
+    CHECK(ensure(E.gs12, E3 * 4));
+    CHECK(ensure(E.partials, (size_t)mskern::ssim_num_blocks(W, H) * 16));
+    CHECK(ensure(E.loss, 16));
+    mskern::launch_loss_fwd_bwd(E.stream, W, H, img, gt, dist, l1, ldist, ldssim, E.window, P<float>(E.gm1),
+                                P<float>(E.gs1), P<float>(E.gs12), P<double>(E.partials), P<double>(E.loss), dL);
+    HIPC(hipGetLastError());
+    return MSPLAT_OK;
+}
+
+int last_locked(int which, void **ptr, int64_t *numel) {
+    Engine &E = g_eng;
+    *ptr = nullptr;
+    *numel = 0;
+    const int64_t N = E.n, Pn = (int64_t)E.W * E.H;
+    auto matf = [&](int idx, DevBuf &src, int stride, int off, int nf) -> int {
+        CHECK(ensure(E.mat[idx], (size_t)N * nf * 4));
+        mskern::launch_gather(E.stream, P<float>(src), stride, off, nf, P<float>(E.mat[idx]), (int)N);
+        *ptr = E.mat[idx].p;
+        *numel = N * nf;
+        return MSPLAT_OK;
+    };
+    switch (which) {
+        case MSPLAT_LAST_XYS: return matf(which, E.rec, 20, 9, 2);
+        case MSPLAT_LAST_DEPTHS: *ptr = E.depths.p; *numel = N; return MSPLAT_OK;
+        case MSPLAT_LAST_RADII: *ptr = E.radii.p; *numel = N; return MSPLAT_OK;
+        case MSPLAT_LAST_NUM_TILES_HIT:
+            CHECK(ensure(E.mat[which], (size_t)N * 4));
+            mskern::launch_tiles_hit(E.stream, P<uint32_t>(E.rect), P<int>(E.radii), P<int>(E.mat[which]), (int)N);
+            *ptr = E.mat[which].p;
+            *numel = N;
+            return MSPLAT_OK;
+        case MSPLAT_LAST_TRANSMATS: return matf(which, E.rec, 20, 0, 9);
+        case MSPLAT_LAST_COLORS_USED: return matf(which, E.rec, 20, 15, 3);
+        case MSPLAT_LAST_OPACITY_SIGMOID: return matf(which, E.rec, 20, 11, 1);
+        case MSPLAT_LAST_NORMALS: return matf(which, E.rec, 20, 12, 3);
+        case MSPLAT_LAST_RECORDS: *ptr = E.rec.p; *numel = N * 20; return MSPLAT_OK;
+        case MSPLAT_LAST_TILE_OFFSETS:
+            *ptr = E.offsets.p;
+            *numel = (int64_t)E.tiles_x * E.tiles_y + 1;
+            return MSPLAT_OK;
+        case MSPLAT_LAST_GAUSSIAN_IDS: *ptr = E.ids.p; *numel = E.num_isect; return MSPLAT_OK;
+        case MSPLAT_LAST_OUT_IMG: *ptr = E.out_img.p; *numel = Pn * 3; return MSPLAT_OK;
+        case MSPLAT_LAST_FINAL_TS: *ptr = E.final_Ts.p; *numel = Pn * 3; return MSPLAT_OK;
+        case MSPLAT_LAST_FINAL_IDX: *ptr = E.final_idx.p; *numel = Pn * 2; return MSPLAT_OK;
+        case MSPLAT_LAST_OUT_DEPTH: *ptr = E.out_depth.p; *numel = Pn; return MSPLAT_OK;
+        case MSPLAT_LAST_OUT_NORMAL: *ptr = E.out_normal.p; *numel = Pn * 3; return MSPLAT_OK;
+        case MSPLAT_LAST_OUT_ALPHA: *ptr = E.out_alpha.p; *numel = Pn; return MSPLAT_OK;
+        case MSPLAT_LAST_OUT_MEDIAN_DEPTH: *ptr = E.out_median.p; *numel = Pn; return MSPLAT_OK;
+        case MSPLAT_LAST_OUT_DISTORTION: *ptr = E.out_dist.p; *numel = Pn; return MSPLAT_OK;
+        case MSPLAT_LAST_DL_DOUT_IMG: *ptr = E.dL_dimg.p; *numel = E.dL_dimg.p ? Pn * 3 : 0; return MSPLAT_OK;
+        case MSPLAT_LAST_GRADS16: *ptr = E.grads16.p; *numel = E.grads16.p ? N * 16 : 0; return MSPLAT_OK;
+        case MSPLAT_LAST_DL_DTRANSMAT: return E.grads16.p ? matf(which, E.grads16, 16, 0, 9) : MSPLAT_OK;
+        case MSPLAT_LAST_DL_DNORMAL3D: return E.grads16.p ? matf(which, E.grads16, 16, 9, 3) : MSPLAT_OK;
+        case MSPLAT_LAST_DL_DOPACITY: return E.grads16.p ? matf(which, E.grads16, 16, 12, 1) : MSPLAT_OK;
+        case MSPLAT_LAST_DL_DCOLORS: return E.grads16.p ? matf(which, E.grads16, 16, 13, 3) : MSPLAT_OK;
+        case MSPLAT_LAST_DL_DMEAN3D: if (E.have_grads) { *ptr = E.dmeans.p; *numel = N * 3; } return MSPLAT_OK;
+        case MSPLAT_LAST_DL_DSCALE: if (E.have_grads) { *ptr = E.dscales.p; *numel = N * 2; } return MSPLAT_OK;
+        case MSPLAT_LAST_DL_DQUAT: if (E.have_grads) { *ptr = E.dquats.p; *numel = N * 4; } return MSPLAT_OK;
+        case MSPLAT_LAST_DL_DMEAN2D: if (E.have_grads) { *ptr = E.dmean2d.p; *numel = N * 2; } return MSPLAT_OK;
+        case MSPLAT_LAST_DL_DFEATURES_DC: if (E.have_grads) { *ptr = E.dfdc.p; *numel = N * 3; } return MSPLAT_OK;
+        case MSPLAT_LAST_DL_DFEATURES_REST:
+            if (E.have_grads) { *ptr = E.dfrest.p; *numel = N * E.K3; }
+            return MSPLAT_OK;
+        default: set_err("unknown buffer id %d", which); return MSPLAT_E_ARG;
+    }
+}
+
+}  // namespace
+
+#define API_BEGIN                      \
+    std::lock_guard<std::mutex> lk_(g_mu); \
+    try {
+#define API_END                                      \
+    }                                                \
+    catch (const std::exception &ex) {               \
+        set_err("exception: %s", ex.what());         \
+        return MSPLAT_E_ARG;                         \
+    }                                                \
+    catch (...) {                                    \
+        set_err("unknown exception");                \
+        return MSPLAT_E_ARG;                         \
+    }
+
+extern "C" {
+
+int msplat_hip_init(void) {
+    API_BEGIN
+    return init_locked();
+    API_END
+}
+
+void msplat_hip_cleanup(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    Engine &E = g_eng;
+    if (!E.ready) return;
+    (void)hipStreamSynchronize(E.stream);
+    DevBuf *all[] = {&E.rec, &E.depths, &E.radii, &E.rect, &E.grads16, &E.colors_raw, &E.counts, &E.offsets,
+                     &E.cursor, &E.stats, &E.big_list, &E.keys, &E.keys_tmp, &E.ids, &E.out_img, &E.final_Ts,
+                     &E.final_idx, &E.out_depth, &E.out_normal, &E.out_alpha, &E.out_median, &E.out_dist,
+                     &E.dL_dimg, &E.gm1, &E.gs1, &E.gs12, &E.partials, &E.loss, &E.dmeans, &E.dscales,
+                     &E.dquats, &E.dmean2d, &E.dfdc, &E.dfrest, &E.dens_flags, &E.dens_scan, &E.pair_counter};
+    for (DevBuf *b : all) {
+        if (b->p) (void)hipFree(b->p);
+        *b = DevBuf{};
+    }
+    for (auto &b : E.mat) {
+        if (b.p) (void)hipFree(b.p);
+        b = DevBuf{};
+    }
+    for (auto &b : E.dens_scratch) {
+        if (b.p) (void)hipFree(b.p);
+        b = DevBuf{};
+    }
+    E.n = 0;
+    E.num_isect = 0;
+    E.have_grads = false;
+}
+
+const char *msplat_hip_last_error(void) { return g_err; }
+
+int msplat_hip_device_name(char *buf, int len) {
+    API_BEGIN
+    ENSURE_INIT();
+    hipDeviceProp_t prop;
+    HIPC(hipGetDeviceProperties(&prop, g_eng.device));
+    snprintf(buf, (size_t)len, "%s (%s, %d CUs)", prop.name, prop.gcnArchName, prop.multiProcessorCount);
+    return MSPLAT_OK;
+    API_END
+}
+
+void *msplat_hip_alloc(size_t bytes) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (init_locked() != MSPLAT_OK) return nullptr;
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 16) != hipSuccess) {
+        (void)hipGetLastError();
+        set_err("hipMalloc(%zu) failed", bytes);
+        return nullptr;
+    }
+    return p;
+}
+
+int msplat_hip_free(void *p) {
+    API_BEGIN
+    if (!p) return MSPLAT_OK;
+    ENSURE_INIT();
+    HIPC(hipStreamSynchronize(g_eng.stream));
+    HIPC(hipFree(p));
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_memset(void *p, int v, size_t bytes) {
+    API_BEGIN
+    ENSURE_INIT();
+    HIPC(hipMemsetAsync(p, v, bytes, g_eng.stream));
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_upload(void *dst, const void *src, size_t bytes) {
+    API_BEGIN
+    ENSURE_INIT();
+    HIPC(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_eng.stream));
+    HIPC(hipStreamSynchronize(g_eng.stream));
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_download(void *dst, const void *src, size_t bytes) {
+    API_BEGIN
+    ENSURE_INIT();
+    HIPC(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_eng.stream));
+    HIPC(hipStreamSynchronize(g_eng.stream));
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_copy(void *dst, const void *src, size_t bytes) {
+    API_BEGIN
+    ENSURE_INIT();
+    HIPC(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_eng.stream));
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_commit(void) { return MSPLAT_OK; }
+
+int msplat_hip_sync(void) {
+    API_BEGIN
+    ENSURE_INIT();
+    HIPC(hipStreamSynchronize(g_eng.stream));
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_render(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, int64_t *nisect) {
+    API_BEGIN
+    ENSURE_INIT();
+    CHECK(forward_locked(cam, g, bg, nisect));
+    stage_mark(ST_LOSS);
+    if (g_eng.timing) {
+        HIPC(hipMemcpyAsync(g_eng.pinned_d, g_eng.pair_counter.p, 8, hipMemcpyDeviceToHost, g_eng.stream));
+        HIPC(hipStreamSynchronize(g_eng.stream));
+        std::memcpy(&g_eng.pairs, g_eng.pinned_d, 8);
+        for (int i = ST_PROJECT; i < ST_LOSS; ++i) {
+            HIPC(hipEventElapsedTime(&g_eng.stage_ms[i], g_eng.ev[i], g_eng.ev[i + 1]));
+            g_eng.stage_valid[i] = true;
+        }
+    }
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, const float *gt,
+                          float lambda_l1, float lambda_dist, float lambda_dssim, float *gnorm, float *vis,
+                          float *max2d, float inv_max_dim, const MsplatAdam *adam, float *loss_host,
+                          int64_t *nisect) {
+    API_BEGIN
+    ENSURE_INIT();
+    if (!gt || !gnorm || !vis || !max2d) {
+        set_err("null gt / densify statistics");
+        return MSPLAT_E_ARG;
+    }
+    Engine &E = g_eng;
+    hipStream_t s = E.stream;
+    CHECK(forward_locked(cam, g, bg, nisect));
+    const int N = g->num_points, W = cam->width, H = cam->height;
+    const size_t Pn = (size_t)W * H;
+    stage_mark(ST_LOSS);
+    CHECK(ensure(E.dL_dimg, Pn * 12));
+    CHECK(loss_locked(W, H, P<float>(E.out_img), gt, lambda_dist != 0.f ? P<float>(E.out_dist) : nullptr,
+                      lambda_l1, lambda_dist, lambda_dssim, P<float>(E.dL_dimg)));
+    HIPC(hipMemcpyAsync(E.pinned_d, E.loss.p, 2 * sizeof(double), hipMemcpyDeviceToHost, s));
+    stage_mark(ST_RASTER_BWD);
+    CHECK(ensure(E.grads16, (size_t)N * 64));
+    HIPC(hipMemsetAsync(E.grads16.p, 0, (size_t)N * 64, s));
+    const float inv_np = 1.0f / (float)((unsigned)H * (unsigned)W * 3u);
+    const float ddist_uniform = lambda_dist * (inv_np * 3.0f);
+    mskern::launch_raster_bwd(s, W, H, cam->tiles_x, cam->tiles_y, P<int>(E.offsets), P<int>(E.ids),
+                              P<float>(E.rec), bg, P<float>(E.final_Ts), P<int>(E.final_idx), P<float>(E.dL_dimg),
+                              nullptr, nullptr, nullptr, nullptr, nullptr, ddist_uniform, P<float>(E.grads16));
+    stage_mark(ST_PROJECT_BWD);
+    if (adam) {
+        mskern::launch_project_bwd(s, *cam, *g, P<int>(E.radii), P<float>(E.grads16), nullptr, nullptr, nullptr,
+                                   nullptr, nullptr, nullptr, gnorm, vis, max2d, inv_max_dim, adam);
+    } else {
+        CHECK(ensure(E.dmeans, (size_t)N * 12));
+        CHECK(ensure(E.dscales, (size_t)N * 8));
+        CHECK(ensure(E.dquats, (size_t)N * 16));
+        CHECK(ensure(E.dmean2d, (size_t)N * 8));
+        CHECK(ensure(E.dfdc, (size_t)N * 12));
+        CHECK(ensure(E.dfrest, (size_t)N * E.K3 * 4));
+        mskern::launch_project_bwd(s, *cam, *g, P<int>(E.radii), P<float>(E.grads16), P<float>(E.dmeans),
+                                   P<float>(E.dscales), P<float>(E.dquats), P<float>(E.dmean2d), P<float>(E.dfdc),
+                                   P<float>(E.dfrest), gnorm, vis, max2d, inv_max_dim, nullptr);
+        E.have_grads = true;
+    }
+    stage_mark(ST_COUNT);
+    HIPC(hipGetLastError());
+    HIPC(hipStreamSynchronize(s));
+    if (loss_host) *loss_host = (float)E.pinned_d[0];
+    if (E.timing) {
+        HIPC(hipMemcpy(&E.pairs, E.pair_counter.p, 8, hipMemcpyDeviceToHost));
+        for (int i = 0; i < ST_COUNT; ++i) {
+            HIPC(hipEventElapsedTime(&E.stage_ms[i], E.ev[i], E.ev[i + 1]));
+            E.stage_valid[i] = true;
+        }
+    }
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_fused_adam(float *p, const float *gr, float *m, float *v, int64_t n, float step, float b1, float b2,
+                          float bc2_sqrt, float eps) {
+    API_BEGIN
+    ENSURE_INIT();
+    if (n < 0 || (n > 0 && (!p || !gr || !m || !v))) {
+        set_err("invalid adam arguments");
+        return MSPLAT_E_ARG;
+    }
+    mskern::launch_adam(g_eng.stream, p, gr, m, v, n, step, b1, b2, bc2_sqrt, eps);
+    HIPC(hipGetLastError());
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_densify(int n, int capacity, float grad_thresh, float size_thresh, float screen_thresh,
+                       int check_screen, float cull_alpha_thresh, float cull_scale_thresh, float cull_screen_size,
+                       int check_huge, const float *gnorm, const float *vis, const float *max2d, float half_max_dim,
+                       float *const params[6], int fr_stride, float *const exp_avg[6], float *const exp_avg_sq[6],
+                       const float *random, int *new_count) {
+    API_BEGIN
+    ENSURE_INIT();
+    if (n < 0 || 3LL * n > capacity || fr_stride < 0 || !new_count) {
+        set_err("densify: 3*N (%lld) exceeds capacity %d or bad arguments", 3LL * n, capacity);
+        return MSPLAT_E_CAPACITY;
+    }
+    if (n == 0) {
+        *new_count = 0;
+        return MSPLAT_OK;
+    }
+    Engine &E = g_eng;
+    const int worst = 3 * n;
+    const int strides[6] = {3, 2, 4, 3, fr_stride, 1};
+    mskern::DensifyArgs a{};
+    a.n = n;
+    a.fr_stride = fr_stride;
+    a.grad_th = grad_thresh;
+    a.size_th = size_thresh;
+    a.screen_th = screen_thresh;
+    a.check_screen = check_screen;
+    a.cull_alpha = cull_alpha_thresh;
+    a.cull_scale = cull_scale_thresh;
+    a.cull_screen = cull_screen_size;
+    a.check_huge = check_huge;
+    a.grad_norm = gnorm;
+    a.vis = vis;
+    a.max2d = max2d;
+    a.half_max_dim = half_max_dim;
+    a.log_size_fac = std::log(1.6f);
+    a.random = random;
+    for (int gi = 0; gi < 6; ++gi) {
+        a.params[gi] = params[gi];
+        a.exp_avg[gi] = exp_avg[gi];
+        a.exp_avg_sq[gi] = exp_avg_sq[gi];
+        for (int r = 0; r < 3; ++r) {
+            CHECK(ensure(E.dens_scratch[6 * r + gi], (size_t)worst * std::max(1, strides[gi]) * 4));
+            a.scratch[6 * r + gi] = P<float>(E.dens_scratch[6 * r + gi]);
+        }
+    }
+    CHECK(ensure(E.dens_flags, (size_t)worst * 4 * 6));
+    CHECK(ensure(E.dens_scan, (size_t)mskern::scan_temp_ints(worst) * 4));
+    int *f = P<int>(E.dens_flags);
+    a.split = f;
+    a.dup = f + worst;
+    a.split_pre = f + 2 * worst;
+    a.dup_pre = f + 3 * worst;
+    a.keep = f + 4 * worst;
+    a.keep_pre = f + 5 * worst;
+    a.scan_temp = P<int>(E.dens_scan);
+    mskern::launch_densify(E.stream, a);
+    HIPC(hipGetLastError());
+    HIPC(hipMemcpyAsync(E.pinned_i, a.keep_pre + worst - 1, sizeof(int), hipMemcpyDeviceToHost, E.stream));
+    HIPC(hipStreamSynchronize(E.stream));
+    *new_count = E.pinned_i[0];
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_loss_fwd_bwd(int W, int H, const float *img, const float *gt, const float *dist, float l1,
+                            float ldist, float ldssim, float *dL, double *loss_host, double *ssim_host) {
+    API_BEGIN
+    ENSURE_INIT();
+    if (W <= 0 || H <= 0 || !img || !gt || !dL || (ldist != 0.f && !dist)) {
+        set_err("invalid loss arguments");
+        return MSPLAT_E_ARG;
+    }
+    CHECK(loss_locked(W, H, img, gt, ldist != 0.f ? dist : nullptr, l1, ldist, ldssim, dL));
+    HIPC(hipMemcpyAsync(g_eng.pinned_d, g_eng.loss.p, 2 * sizeof(double), hipMemcpyDeviceToHost, g_eng.stream));
+    HIPC(hipStreamSynchronize(g_eng.stream));
+    if (loss_host) *loss_host = g_eng.pinned_d[0];
+    if (ssim_host) *ssim_host = g_eng.pinned_d[1];
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_raster_bwd(const float *dL_dimg, const float *dL_ddepth, const float *dL_dalpha,
+                          const float *dL_dnormal, const float *dL_dmedian, const float *dL_ddist, float *grads16) {
+    API_BEGIN
+    ENSURE_INIT();
+    Engine &E = g_eng;
+    if (!E.rec.p || !E.bg || !dL_dimg || !grads16) {
+        set_err("raster_bwd needs a preceding forward and dL_dimg / grads16");
+        return MSPLAT_E_ARG;
+    }
+    mskern::launch_raster_bwd(E.stream, E.W, E.H, E.tiles_x, E.tiles_y, P<int>(E.offsets), P<int>(E.ids),
+                              P<float>(E.rec), E.bg, P<float>(E.final_Ts), P<int>(E.final_idx), dL_dimg, dL_ddepth,
+                              dL_dalpha, dL_dnormal, dL_dmedian, dL_ddist, 0.0f, grads16);
+    HIPC(hipGetLastError());
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_project_bwd(const MsplatCamera *cam, const MsplatGaussians *g, const int32_t *radii,
+                           const float *g16, float *dmeans, float *dscales, float *dquats, float *dmean2d,
+                           float *dfdc, float *dfrest, float *gnorm, float *vis, float *max2d, float inv_max_dim) {
+    API_BEGIN
+    ENSURE_INIT();
+    CHECK(validate_cam(cam, g));
+    if (!radii || !g16 || !dmeans || !dscales || !dquats || !dmean2d || !dfdc || (cam->degree > 0 && !dfrest) ||
+        !gnorm || !vis || !max2d) {
+        set_err("invalid project_bwd arguments");
+        return MSPLAT_E_ARG;
+    }
+    mskern::launch_project_bwd(g_eng.stream, *cam, *g, radii, g16, dmeans, dscales, dquats, dmean2d, dfdc, dfrest,
+                               gnorm, vis, max2d, inv_max_dim, nullptr);
+    HIPC(hipGetLastError());
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_project_bwd_adam(const MsplatCamera *cam, const MsplatGaussians *g, const int32_t *radii,
+                                const float *g16, float *gnorm, float *vis, float *max2d, float inv_max_dim,
+                                const MsplatAdam *adam) {
+    API_BEGIN
+    ENSURE_INIT();
+    CHECK(validate_cam(cam, g));
+    if (!radii || !g16 || !gnorm || !vis || !max2d || !adam) {
+        set_err("invalid project_bwd_adam arguments");
+        return MSPLAT_E_ARG;
+    }
+    mskern::launch_project_bwd(g_eng.stream, *cam, *g, radii, g16, nullptr, nullptr, nullptr, nullptr, nullptr,
+                               nullptr, gnorm, vis, max2d, inv_max_dim, adam);
+    HIPC(hipGetLastError());
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_last(int which, void **ptr, int64_t *numel) {
+    API_BEGIN
+    ENSURE_INIT();
+    if (!ptr || !numel) return MSPLAT_E_ARG;
+    CHECK(last_locked(which, ptr, numel));
+    HIPC(hipGetLastError());
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_enable_timing(int enable) {
+    API_BEGIN
+    ENSURE_INIT();
+    g_eng.timing = enable != 0;
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_stage_times(const char **names, float *ms, int max) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int k = 0;
+    for (int i = 0; i < ST_COUNT && k < max; ++i) {
+        if (!g_eng.stage_valid[i]) continue;
+        if (names) names[k] = kStageNames[i];
+        if (ms) ms[k] = g_eng.stage_ms[i];
+        ++k;
+    }
+    return k;
+}
+
+int64_t msplat_hip_last_pairs_evaluated(void) { return g_eng.pairs; }
+
+}  // extern "C"

@@ -1,0 +1,319 @@
+// k_project.hip -- per-gaussian projection + SH forward, projection + SH
+// backward (optionally fused with the six Adam updates), and the gathers
+// that materialise per-field views of the packed splat records.
+#include "kernels.h"
+#include "ms_device.h"
+
+using namespace msd;
+
+namespace {
+
+constexpr int kBlock = 256;
+
+// project_and_sh_forward_2dgs_kernel (msplat_metal.metal:1413-1521), with
+// the sigmoid of the sort/pack stage (:1684) and the raster's colour clamp
+// (:619) folded into the record.  Also builds the per-tile histogram that
+// the tile scan consumes (count pass of count -> scan -> scatter binning).
+__global__ __launch_bounds__(kBlock) void k_project_fwd(
+    MsplatCamera cam, int n, const float *__restrict__ means, const float *__restrict__ scales,
+    const float *__restrict__ quats, const float *__restrict__ opac, const float *__restrict__ fdc,
+    const float *__restrict__ frest, float4 *__restrict__ rec, float *__restrict__ depths,
+    int *__restrict__ radii, uint2 *__restrict__ rect, int *__restrict__ tile_counts,
+    float *__restrict__ colors_raw) {
+    const int i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= n) return;
+    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 *ro = rec + 5 * (size_t)i;
+    const float *vm = cam.viewmat, *pm = cam.projmat;
+    const float p[3] = {means[3 * (size_t)i], means[3 * (size_t)i + 1], means[3 * (size_t)i + 2]};
+    const float pz = vm[8] * p[0] + vm[9] * p[1] + vm[10] * p[2] + vm[11];
+
+    bool ok = pz > cam.clip_thresh;
+    f3 R0, R1, R2;
+    float cxp = 0.f, cyp = 0.f, radius = 0.f;
+    f3 T0, T1, T2;
+    int x0 = 0, y0 = 0, x1 = 0, y1 = 0;
+    if (ok) {
+        const float sx = ms_expf(scales[2 * (size_t)i]), sy = ms_expf(scales[2 * (size_t)i + 1]);
+        const float4 qv = reinterpret_cast<const float4 *>(quats)[i];
+        const float q[4] = {qv.x, qv.y, qv.z, qv.w};
+        quat_to_rotmat(q, R0, R1, R2);
+        const float sxg = sx * cam.glob_scale, syg = sy * cam.glob_scale;
+        const f3 tu = {R0.x * sxg, R0.y * sxg, R0.z * sxg};
+        const f3 tv = {R1.x * syg, R1.y * syg, R1.z * syg};
+        const ClipCols cc = clip_columns(p, tu, tv, pm);
+        const float halfW = 0.5f * (float)cam.width, halfH = 0.5f * (float)cam.height;
+        const float bx = cam.cx - 0.5f, by = cam.cy - 0.5f;
+        const f3 cu = {halfW * cc.tu[0] + bx * cc.tu[3], halfH * cc.tu[1] + by * cc.tu[3], cc.tu[3]};
+        const f3 cv = {halfW * cc.tv[0] + bx * cc.tv[3], halfH * cc.tv[1] + by * cc.tv[3], cc.tv[3]};
+        const f3 co = {halfW * cc.pc[0] + bx * cc.pc[3], halfH * cc.pc[1] + by * cc.pc[3], cc.pc[3]};
+        T0 = {cu.x, cv.x, co.x};
+        T1 = {cu.y, cv.y, co.y};
+        T2 = {cu.z, cv.z, co.z};
+        // compute_aabb_2dgs, cutoff 3 (msplat_metal.metal:302-330)
+        const float cutoff = 3.0f;
+        const f3 t = {cutoff * cutoff, cutoff * cutoff, -1.0f};
+        const float dd = dot3(t, mul3(T2, T2));
+        ok = dd != 0.0f;
+        if (ok) {
+            const float invd = 1.0f / dd;
+            const f3 f = {invd * t.x, invd * t.y, invd * t.z};
+            cxp = dot3(f, mul3(T0, T2));
+            cyp = dot3(f, mul3(T1, T2));
+            const float h0x = cxp * cxp - dot3(f, mul3(T0, T0));
+            const float h0y = cyp * cyp - dot3(f, mul3(T1, T1));
+            const float hx = __builtin_sqrtf(__builtin_fmaxf(1e-4f, h0x));
+            const float hy = __builtin_sqrtf(__builtin_fmaxf(1e-4f, h0y));
+            radius = __builtin_ceilf(__builtin_fmaxf(__builtin_fmaxf(hx, hy), cutoff * FILTER_SIZE));
+            // get_tile_bbox (msplat_metal.metal:62-92)
+            const float tcx = cxp / 16.0f, tcy = cyp / 16.0f, tr = radius / 16.0f;
+            x0 = min(max(0, f2i(tcx - tr)), cam.tiles_x);
+            x1 = min(max(0, f2i(tcx + tr + 1)), cam.tiles_x);
+            y0 = min(max(0, f2i(tcy - tr)), cam.tiles_y);
+            y1 = min(max(0, f2i(tcy + tr + 1)), cam.tiles_y);
+            ok = (x1 - x0) * (y1 - y0) > 0;
+        }
+    }
+    if (!ok) {
+        radii[i] = 0;
+        depths[i] = 0.f;
+        rect[i] = make_uint2(0u, 0u);
+#pragma unroll
+        for (int k = 0; k < 5; ++k) ro[k] = z4;
+        if (colors_raw) {
+            colors_raw[3 * (size_t)i] = colors_raw[3 * (size_t)i + 1] = colors_raw[3 * (size_t)i + 2] = 0.f;
+        }
+        return;
+    }
+    const f3 dir = normalize3({p[0] - cam.cam_pos[0], p[1] - cam.cam_pos[1], p[2] - cam.cam_pos[2]});
+    const int nb = num_sh_bases(cam.degree);
+    float col[3];
+    sh_eval(cam.degrees_to_use, dir, fdc + 3 * (size_t)i, frest + (size_t)(nb - 1) * 3 * i, col);
+    const float opa = ms_sigmoid(opac[i]);
+
+    radii[i] = (int)radius;
+    depths[i] = pz;
+    rect[i] = make_uint2((uint32_t)x0 | ((uint32_t)y0 << 16), (uint32_t)x1 | ((uint32_t)y1 << 16));
+    ro[0] = make_float4(T0.x, T0.y, T0.z, T1.x);
+    ro[1] = make_float4(T1.y, T1.z, T2.x, T2.y);
+    ro[2] = make_float4(T2.z, cxp, cyp, opa);
+    ro[3] = make_float4(R2.x, R2.y, R2.z, __builtin_fmaxf(col[0] + 0.5f, 0.0f));
+    ro[4] = make_float4(__builtin_fmaxf(col[1] + 0.5f, 0.0f), __builtin_fmaxf(col[2] + 0.5f, 0.0f), 0.f, 0.f);
+    if (colors_raw) {
+        colors_raw[3 * (size_t)i] = col[0];
+        colors_raw[3 * (size_t)i + 1] = col[1];
+        colors_raw[3 * (size_t)i + 2] = col[2];
+    }
+    for (int y = y0; y < y1; ++y)
+        for (int x = x0; x < x1; ++x) atomicAdd(&tile_counts[y * cam.tiles_x + x], 1);
+}
+
+// One Adam step on one element: fused_adam_kernel (msplat_metal.metal:1383-1406).
+__device__ __forceinline__ void adam_elem(float *p, float *m_, float *v_, size_t idx, float g, float step,
+                                          float b1, float b2, float bc2_sqrt, float eps) {
+    const float m = __builtin_fmaf(b1, m_[idx], (1.0f - b1) * g);
+    const float v = __builtin_fmaf(b2, v_[idx], (1.0f - b2) * g * g);
+    p[idx] -= step * m / (__builtin_sqrtf(v) / bc2_sqrt + eps);
+    m_[idx] = m;
+    v_[idx] = v;
+}
+
+struct AdamDev {
+    float *m[6];
+    float *v[6];
+    float step[6];
+    float b1, b2, bc2_sqrt, eps;
+};
+
+// project_and_sh_backward_2dgs_kernel (msplat_metal.metal:2003-2209).
+// FUSED: the per-gaussian gradients stay in registers and the six Adam
+// groups (model.cpp:806-826) are updated in place, so neither the 58-float
+// gradient nor a second pass over the parameters touches HBM.
+template <bool FUSED>
+__global__ __launch_bounds__(kBlock) void k_project_bwd(
+    MsplatCamera cam, int n, float *__restrict__ means, float *__restrict__ scales,
+    float *__restrict__ quats, float *__restrict__ opac, float *__restrict__ fdc,
+    float *__restrict__ frest, const int *__restrict__ radii, const float *__restrict__ g16,
+    float *__restrict__ dmeans, float *__restrict__ dscales, float *__restrict__ dquats,
+    float *__restrict__ dmean2d, float *__restrict__ dfdc, float *__restrict__ dfrest,
+    float *__restrict__ grad_norm, float *__restrict__ vis, float *__restrict__ max2d, float inv_max_dim,
+    AdamDev ad) {
+    const int i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= n) return;
+    const int nb = num_sh_bases(cam.degree);
+    const int K3 = (nb - 1) * 3;
+    const size_t si = (size_t)i;
+
+    float gm[3] = {0.f, 0.f, 0.f}, gs[2] = {0.f, 0.f}, gq[4] = {0.f, 0.f, 0.f, 0.f};
+    float gdc[3] = {0.f, 0.f, 0.f}, gm2[2] = {0.f, 0.f};
+    float vc[3] = {0.f, 0.f, 0.f};
+    float basis[24];
+    const bool vis_ok = radii[i] > 0;
+    int sh_deg = 0;
+    if (vis_ok) {
+        const float p[3] = {means[3 * si], means[3 * si + 1], means[3 * si + 2]};
+        const float sx = ms_expf(scales[2 * si]), sy = ms_expf(scales[2 * si + 1]);
+        const float4 qv = reinterpret_cast<const float4 *>(quats)[i];
+        const float q[4] = {qv.x, qv.y, qv.z, qv.w};
+        f3 R0, R1, R2;
+        quat_to_rotmat(q, R0, R1, R2);
+        const float sxg = sx * cam.glob_scale, syg = sy * cam.glob_scale;
+        const f3 tu = {R0.x * sxg, R0.y * sxg, R0.z * sxg};
+        const f3 tv = {R1.x * syg, R1.y * syg, R1.z * syg};
+        const float *pm = cam.projmat;
+        const ClipCols cc = clip_columns(p, tu, tv, pm);
+        const float W = (float)cam.width, H = (float)cam.height;
+        const float halfW = 0.5f * W, halfH = 0.5f * H;
+        const float bx = cam.cx - 0.5f, by = cam.cy - 0.5f;
+        const float4 *g4 = reinterpret_cast<const float4 *>(g16 + 16 * si);
+        const float4 ga = g4[0], gb = g4[1], gc = g4[2], gd = g4[3];
+        const float g[16] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w,
+                             gc.x, gc.y, gc.z, gc.w, gd.x, gd.y, gd.z, gd.w};
+        const f3 dcu = {g[0], g[3], g[6]}, dcv = {g[1], g[4], g[7]}, dco = {g[2], g[5], g[8]};
+        const float du[4] = {halfW * dcu.x, halfH * dcu.y, 0.0f, bx * dcu.x + by * dcu.y + dcu.z};
+        const float dv[4] = {halfW * dcv.x, halfH * dcv.y, 0.0f, bx * dcv.x + by * dcv.y + dcv.z};
+        const float dpc[4] = {halfW * dco.x, halfH * dco.y, 0.0f, bx * dco.x + by * dco.y + dco.z};
+        f3 gtu, gtv, gp;
+        gtu.x = pm[0] * du[0] + pm[4] * du[1] + pm[8] * du[2] + pm[12] * du[3];
+        gtu.y = pm[1] * du[0] + pm[5] * du[1] + pm[9] * du[2] + pm[13] * du[3];
+        gtu.z = pm[2] * du[0] + pm[6] * du[1] + pm[10] * du[2] + pm[14] * du[3];
+        gtv.x = pm[0] * dv[0] + pm[4] * dv[1] + pm[8] * dv[2] + pm[12] * dv[3];
+        gtv.y = pm[1] * dv[0] + pm[5] * dv[1] + pm[9] * dv[2] + pm[13] * dv[3];
+        gtv.z = pm[2] * dv[0] + pm[6] * dv[1] + pm[10] * dv[2] + pm[14] * dv[3];
+        gp.x = pm[0] * dpc[0] + pm[4] * dpc[1] + pm[8] * dpc[2] + pm[12] * dpc[3];
+        gp.y = pm[1] * dpc[0] + pm[5] * dpc[1] + pm[9] * dpc[2] + pm[13] * dpc[3];
+        gp.z = pm[2] * dpc[0] + pm[6] * dpc[1] + pm[10] * dpc[2] + pm[14] * dpc[3];
+        const float dsx = dot3(gtu, R0), dsy = dot3(gtv, R1);
+        gs[0] = dsx * sx * cam.glob_scale;
+        gs[1] = dsy * sy * cam.glob_scale;
+        const f3 vR[3] = {{gtu.x * sxg, gtu.y * sxg, gtu.z * sxg},
+                          {gtv.x * syg, gtv.y * syg, gtv.z * syg},
+                          {g[9], g[10], g[11]}};
+        quat_to_rotmat_vjp(q, vR, gq);
+        gm[0] = gp.x;
+        gm[1] = gp.y;
+        gm[2] = gp.z;
+        const f3 dir_un = {p[0] - cam.cam_pos[0], p[1] - cam.cam_pos[1], p[2] - cam.cam_pos[2]};
+        const f3 dir = normalize3(dir_un);
+        vc[0] = g[13];
+        vc[1] = g[14];
+        vc[2] = g[15];
+        sh_deg = cam.degrees_to_use;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) gdc[c] = SH_C0 * vc[c];
+        sh_vjp_basis(sh_deg, dir, basis);
+        if (sh_deg >= 1) {
+            const f3 dd = sh_dL_ddir(sh_deg, dir, frest + (size_t)K3 * si, vc);
+            const f3 dm = dnormvdv(dir_un, dd);
+            gm[0] += dm.x;
+            gm[1] += dm.y;
+            gm[2] += dm.z;
+        }
+        const float depth_fwd = cc.pc[3];
+        gm2[0] = g[6] * depth_fwd * 0.5f * W;
+        gm2[1] = g[7] * depth_fwd * 0.5f * H;
+        grad_norm[i] += __builtin_fabsf(gm2[0]) + __builtin_fabsf(gm2[1]);
+        vis[i] += 1.0f;
+        const float r_norm = (float)radii[i] * inv_max_dim;
+        if (r_norm > max2d[i]) max2d[i] = r_norm;
+    }
+    const int nrest = sh_deg >= 4 ? 24 : sh_deg == 3 ? 15 : sh_deg == 2 ? 8 : sh_deg == 1 ? 3 : 0;
+    // dL_dopacity is read for every splat, as the reference's Adam reads the
+    // raster's opacity-gradient buffer (zero for culled splats).
+    const float gop = g16[16 * si + 12];
+    if (!FUSED) {
+        for (int k = 0; k < 3; ++k) dmeans[3 * si + k] = gm[k];
+        for (int k = 0; k < 2; ++k) dscales[2 * si + k] = gs[k];
+        for (int k = 0; k < 4; ++k) dquats[4 * si + k] = gq[k];
+        for (int k = 0; k < 2; ++k) dmean2d[2 * si + k] = gm2[k];
+        for (int k = 0; k < 3; ++k) dfdc[3 * si + k] = gdc[k];
+        for (int k = 0; k < K3; ++k) {
+            const int b = k / 3, c = k - 3 * b;
+            dfrest[(size_t)K3 * si + k] = (b < nrest) ? basis[b] * vc[c] : 0.f;
+        }
+    } else {
+        for (int k = 0; k < 3; ++k) adam_elem(means, ad.m[0], ad.v[0], 3 * si + k, gm[k], ad.step[0], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+        for (int k = 0; k < 2; ++k) adam_elem(scales, ad.m[1], ad.v[1], 2 * si + k, gs[k], ad.step[1], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+        for (int k = 0; k < 4; ++k) adam_elem(quats, ad.m[2], ad.v[2], 4 * si + k, gq[k], ad.step[2], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+        for (int k = 0; k < 3; ++k) adam_elem(fdc, ad.m[3], ad.v[3], 3 * si + k, gdc[k], ad.step[3], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+        for (int k = 0; k < K3; ++k) {
+            const int b = k / 3, c = k - 3 * b;
+            const float gr = (b < nrest) ? basis[b] * vc[c] : 0.f;
+            adam_elem(frest, ad.m[4], ad.v[4], (size_t)K3 * si + k, gr, ad.step[4], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+        }
+        adam_elem(opac, ad.m[5], ad.v[5], si, gop, ad.step[5], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+    }
+}
+
+__global__ void k_gather(const float *__restrict__ src, int src_stride, int src_off, int nf,
+                         float *__restrict__ dst, int n) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (int64_t)n * nf) return;
+    const int64_t i = t / nf, k = t - i * nf;
+    dst[t] = src[i * src_stride + src_off + k];
+}
+
+__global__ void k_tiles_hit(const uint2 *__restrict__ rect, const int *__restrict__ radii, int *__restrict__ out, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint2 r = rect[i];
+    const int x0 = r.x & 0xffff, y0 = r.x >> 16, x1 = r.y & 0xffff, y1 = r.y >> 16;
+    out[i] = radii[i] > 0 ? (x1 - x0) * (y1 - y0) : 0;
+}
+
+inline unsigned blocks_for(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
+
+}  // namespace
+
+namespace mskern {
+
+void launch_project_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, float *rec,
+                        float *depths, int *radii, uint32_t *rect, int *tile_counts, float *colors_raw) {
+    if (g.num_points <= 0) return;
+    hipLaunchKernelGGL(k_project_fwd, dim3(blocks_for(g.num_points, kBlock)), dim3(kBlock), 0, s, cam,
+                       g.num_points, g.means, g.scales, g.quats, g.opacities, g.features_dc, g.features_rest,
+                       reinterpret_cast<float4 *>(rec), depths, radii, reinterpret_cast<uint2 *>(rect),
+                       tile_counts, colors_raw);
+}
+
+void launch_project_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, const int *radii,
+                        const float *g16, float *dmeans, float *dscales, float *dquats, float *dmean2d,
+                        float *dfdc, float *dfrest, float *grad_norm, float *vis, float *max2d,
+                        float inv_max_dim, const MsplatAdam *adam) {
+    if (g.num_points <= 0) return;
+    AdamDev ad{};
+    if (adam) {
+        for (int k = 0; k < 6; ++k) {
+            ad.m[k] = adam->exp_avg[k];
+            ad.v[k] = adam->exp_avg_sq[k];
+            ad.step[k] = adam->step_size[k];
+        }
+        ad.b1 = adam->beta1;
+        ad.b2 = adam->beta2;
+        ad.bc2_sqrt = adam->bc2_sqrt;
+        ad.eps = adam->eps;
+        hipLaunchKernelGGL(k_project_bwd<true>, dim3(blocks_for(g.num_points, kBlock)), dim3(kBlock), 0, s,
+                           cam, g.num_points, g.means, g.scales, g.quats, g.opacities, g.features_dc,
+                           g.features_rest, radii, g16, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                           grad_norm, vis, max2d, inv_max_dim, ad);
+    } else {
+        hipLaunchKernelGGL(k_project_bwd<false>, dim3(blocks_for(g.num_points, kBlock)), dim3(kBlock), 0, s,
+                           cam, g.num_points, g.means, g.scales, g.quats, g.opacities, g.features_dc,
+                           g.features_rest, radii, g16, dmeans, dscales, dquats, dmean2d, dfdc, dfrest,
+                           grad_norm, vis, max2d, inv_max_dim, ad);
+    }
+}
+
+void launch_gather(hipStream_t s, const float *src, int src_stride, int src_off, int nf, float *dst, int n) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_gather, dim3(blocks_for((int64_t)n * nf, 256)), dim3(256), 0, s, src, src_stride,
+                       src_off, nf, dst, n);
+}
+
+void launch_tiles_hit(hipStream_t s, const uint32_t *rect, const int *radii, int *out, int n) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_tiles_hit, dim3(blocks_for(n, 256)), dim3(256), 0, s,
+                       reinterpret_cast<const uint2 *>(rect), radii, out, n);
+}
+
+}  // namespace mskern

@@ -1,0 +1,71 @@
+// kernels.h -- host-side launchers of the gfx950 kernels (one translation
+// unit per kernel family; the engine calls these on its stream).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "msplat_engine.h"
+
+namespace mskern {
+
+// k_project.hip
+void launch_project_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, float *rec,
+                        float *depths, int *radii, uint32_t *rect, int *tile_counts, float *colors_raw);
+void launch_project_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, const int *radii,
+                        const float *g16, float *dmeans, float *dscales, float *dquats, float *dmean2d,
+                        float *dfdc, float *dfrest, float *grad_norm, float *vis, float *max2d,
+                        float inv_max_dim, const MsplatAdam *adam);
+void launch_gather(hipStream_t s, const float *src, int src_stride, int src_off, int nf, float *dst, int n);
+void launch_tiles_hit(hipStream_t s, const uint32_t *rect, const int *radii, int *out, int n);
+
+// k_binning.hip
+void launch_scan_tiles(hipStream_t s, int T, const int *counts, int *offsets, int *cursor, int *stats);
+void launch_scatter(hipStream_t s, int n, int tiles_x, const int *radii, const uint32_t *rect,
+                    const float *depths, int *cursor, uint64_t *keys);
+// Returns the buffer that holds the fully sorted keys (keys or keys_tmp).
+uint64_t *launch_sort_tiles(hipStream_t s, int T, int max_count, const int *offsets, uint64_t *keys,
+                            uint64_t *keys_tmp, int *ids, int *big_list, int *stats);
+
+// k_raster.hip
+void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
+                       const float *rec, const float *bg, float *out_img, float *final_Ts, int *final_idx,
+                       float *out_depth, float *out_normal, float *out_alpha, float *out_median, float *out_dist,
+                       unsigned long long *pair_counter);
+void launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
+                       const float *rec, const float *bg, const float *final_Ts, const int *final_idx,
+                       const float *dL_dimg, const float *dL_ddepth, const float *dL_daccum,
+                       const float *dL_dnormal, const float *dL_dmedian, const float *dL_ddist,
+                       float ddist_uniform, float *grads16);
+
+// k_ssim.hip
+int ssim_num_blocks(int W, int H);
+void launch_loss_fwd_bwd(hipStream_t s, int W, int H, const float *img, const float *gt, const float *dist,
+                         float lambda_l1, float lambda_dist, float lambda_dssim, const float window[11],
+                         float *gm1, float *gs1, float *gs12, double *partials, double *loss_out,
+                         float *dL_dimg);
+
+// k_optim.hip
+void launch_adam(hipStream_t s, float *p, const float *g, float *m, float *v, int64_t n, float step, float b1,
+                 float b2, float bc2_sqrt, float eps);
+int64_t scan_temp_ints(int64_t n);
+void launch_scan_i32(hipStream_t s, const int *in, int *out, int n, int *temp);
+
+struct DensifyArgs {
+    int n, fr_stride;
+    float grad_th, size_th, screen_th;
+    int check_screen;
+    float cull_alpha, cull_scale, cull_screen;
+    int check_huge;
+    const float *grad_norm, *vis, *max2d;
+    float half_max_dim, log_size_fac;
+    float *params[6], *exp_avg[6], *exp_avg_sq[6];
+    float *scratch[18];
+    const float *random;
+    int *split, *dup, *split_pre, *dup_pre, *keep, *keep_pre, *scan_temp;
+};
+void launch_densify(hipStream_t s, const DensifyArgs &a);
+
+}  // namespace mskern

@@ -1,0 +1,313 @@
+// ms_device.h -- device math shared by the gfx950 kernels.
+//
+// Arithmetic contract: every kernel is compiled with -ffp-contract=off, so
+// each multiply-add written here is either an explicit __builtin_fmaf or a
+// separately rounded multiply and add; '/' and sqrtf lower to IEEE
+// correctly-rounded sequences on gfx950; exp is ms_expf below.  Given
+// identical inputs the forward kernels therefore reproduce a scalar IEEE
+// restatement of the reference bit for bit.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "msplat_engine.h"
+
+namespace msd {
+
+struct f3 {
+    float x, y, z;
+};
+
+__device__ __forceinline__ float dot3(f3 a, f3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+__device__ __forceinline__ f3 mul3(f3 a, f3 b) { return {a.x * b.x, a.y * b.y, a.z * b.z}; }
+
+// Constants of msplat_metal.metal:19-44 and :204-212.
+constexpr float SH_C0 = 0.28209479177387814f;
+constexpr float SH_C1 = 0.4886025119029199f;
+__device__ constexpr float SH_C2[5] = {1.0925484305920792f, -1.0925484305920792f,
+                                       0.31539156525252005f, -1.0925484305920792f,
+                                       0.5462742152960396f};
+__device__ constexpr float SH_C3[7] = {-0.5900435899266435f, 2.890611442640554f,
+                                       -0.4570457994644658f, 0.3731763325901154f,
+                                       -0.4570457994644658f, 1.445305721320277f,
+                                       -0.5900435899266435f};
+__device__ constexpr float SH_C4[9] = {2.5033429417967046f, -1.7701307697799304f,
+                                       0.9461746957575601f, -0.6690465435572892f,
+                                       0.10578554691520431f, -0.6690465435572892f,
+                                       0.47308734787878004f, -1.7701307697799304f,
+                                       0.6258357354491761f};
+constexpr float FILTER_SIZE = 0.707106f;  // low-pass cutoff sqrt(2)/2
+constexpr float FILTER_INV_SQ = 2.0f;
+constexpr float NEAR_N = 0.2f;            // distortion-depth near / far
+constexpr float FAR_N = 100.0f;
+
+__device__ __forceinline__ int num_sh_bases(int degree) {
+    return degree == 0 ? 1 : degree == 1 ? 4 : degree == 2 ? 9 : degree == 3 ? 16 : 25;
+}
+
+// Single-precision exp after S. L. Moshier's Cephes expf: Cody-Waite
+// reduction x = k*ln2 + r (ln2 = 0.693359375 - 2.12194440e-4), a degree-7
+// polynomial for e^r, then an exact two-step scaling by 2^k (k split in two
+// halves so that both factors are normal numbers).
+__device__ __forceinline__ float ms_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.72283905206835f) return __builtin_inff();
+    if (x < -103.97208f) return 0.0f;
+    float z = __builtin_rintf(x * 1.44269504088896341f);
+    float r = __builtin_fmaf(z, -0.693359375f, x);
+    r = __builtin_fmaf(z, 2.12194440e-4f, r);
+    float r2 = r * r;
+    float p = 1.9875691500E-4f;
+    p = __builtin_fmaf(p, r, 1.3981999507E-3f);
+    p = __builtin_fmaf(p, r, 8.3334519073E-3f);
+    p = __builtin_fmaf(p, r, 4.1665795894E-2f);
+    p = __builtin_fmaf(p, r, 1.6666665459E-1f);
+    p = __builtin_fmaf(p, r, 5.0000001201E-1f);
+    p = __builtin_fmaf(p, r2, r);
+    p = p + 1.0f;
+    int k = (int)z;
+    int k1 = k / 2;
+    int k2 = k - k1;
+    float s1 = __int_as_float((k1 + 127) << 23);
+    float s2 = __int_as_float((k2 + 127) << 23);
+    return (p * s1) * s2;
+}
+
+__device__ __forceinline__ float ms_sigmoid(float x) { return 1.0f / (1.0f + ms_expf(-x)); }
+
+// Saturating truncation (the tile-rectangle (int) casts of get_bbox,
+// msplat_metal.metal:70-73, are undefined outside the int range).
+__device__ __forceinline__ int f2i(float x) {
+    x = __builtin_fmaxf(x, -2147483648.0f);
+    x = __builtin_fminf(x, 2147483520.0f);
+    return (int)x;
+}
+
+// quat_to_rotmat (msplat_metal.metal:116-136): columns of R.
+__device__ __forceinline__ void quat_to_rotmat(const float q[4], f3 &c0, f3 &c1, f3 &c2) {
+    float s = 1.0f / __builtin_sqrtf(q[3] * q[3] + q[0] * q[0] + q[1] * q[1] + q[2] * q[2]);
+    float w = q[0] * s, x = q[1] * s, y = q[2] * s, z = q[3] * s;
+    c0 = {1.f - 2.f * (y * y + z * z), 2.f * (x * y + w * z), 2.f * (x * z - w * y)};
+    c1 = {2.f * (x * y - w * z), 1.f - 2.f * (x * x + z * z), 2.f * (y * z + w * x)};
+    c2 = {2.f * (x * z + w * y), 2.f * (y * z - w * x), 1.f - 2.f * (x * x + y * y)};
+}
+
+// quat_to_rotmat_vjp (msplat_metal.metal:1252-1295); vR[c] is column c.
+__device__ __forceinline__ void quat_to_rotmat_vjp(const float q[4], const f3 vR[3], float out[4]) {
+    float s = 1.0f / __builtin_sqrtf(q[3] * q[3] + q[0] * q[0] + q[1] * q[1] + q[2] * q[2]);
+    float w = q[0] * s, x = q[1] * s, y = q[2] * s, z = q[3] * s;
+    const float R00 = vR[0].x, R01 = vR[0].y, R02 = vR[0].z;
+    const float R10 = vR[1].x, R11 = vR[1].y, R12 = vR[1].z;
+    const float R20 = vR[2].x, R21 = vR[2].y, R22 = vR[2].z;
+    out[0] = 2.f * (x * (R12 - R21) + y * (R20 - R02) + z * (R01 - R10));
+    out[1] = 2.f * (-2.f * x * (R11 + R22) + y * (R01 + R10) + z * (R02 + R20) + w * (R12 - R21));
+    out[2] = 2.f * (x * (R01 + R10) - 2.f * y * (R00 + R22) + z * (R12 + R21) + w * (R20 - R02));
+    out[3] = 2.f * (x * (R02 + R20) + y * (R12 + R21) - 2.f * z * (R00 + R11) + w * (R01 - R10));
+}
+
+// Rows 0..3 of projmat applied to the tangent vectors (w = 0) and the centre
+// (w = 1): the clip-space columns of compute_transmat_2dgs
+// (msplat_metal.metal:246-269).
+struct ClipCols {
+    float tu[4], tv[4], pc[4];
+};
+
+__device__ __forceinline__ ClipCols clip_columns(const float p[3], f3 tu, f3 tv, const float *pm) {
+    ClipCols c;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        c.tu[r] = pm[4 * r + 0] * tu.x + pm[4 * r + 1] * tu.y + pm[4 * r + 2] * tu.z;
+        c.tv[r] = pm[4 * r + 0] * tv.x + pm[4 * r + 1] * tv.y + pm[4 * r + 2] * tv.z;
+        c.pc[r] = pm[4 * r + 0] * p[0] + pm[4 * r + 1] * p[1] + pm[4 * r + 2] * p[2] + pm[4 * r + 3];
+    }
+    return c;
+}
+
+__device__ __forceinline__ f3 normalize3(f3 v) {
+    float inv = 1.0f / __builtin_sqrtf(v.x * v.x + v.y * v.y + v.z * v.z);
+    return {v.x * inv, v.y * inv, v.z * inv};
+}
+
+// sh_coeffs_to_color (msplat_metal.metal:756-823).
+__device__ __forceinline__ void sh_eval(int degree, f3 d, const float *dc, const float *r, float col[3]) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) col[c] = SH_C0 * dc[c];
+    if (degree < 1) return;
+    const float x = d.x, y = d.y, z = d.z;
+    const float xx = x * x, xy = x * y, xz = x * z, yy = y * y, yz = y * z, zz = z * z;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        col[c] += SH_C1 * (-y * r[0 * 3 + c] + z * r[1 * 3 + c] - x * r[2 * 3 + c]);
+        if (degree < 2) continue;
+        col[c] += (SH_C2[0] * xy * r[3 * 3 + c] + SH_C2[1] * yz * r[4 * 3 + c] +
+                   SH_C2[2] * (2.f * zz - xx - yy) * r[5 * 3 + c] + SH_C2[3] * xz * r[6 * 3 + c] +
+                   SH_C2[4] * (xx - yy) * r[7 * 3 + c]);
+        if (degree < 3) continue;
+        col[c] += (SH_C3[0] * y * (3.f * xx - yy) * r[8 * 3 + c] + SH_C3[1] * xy * z * r[9 * 3 + c] +
+                   SH_C3[2] * y * (4.f * zz - xx - yy) * r[10 * 3 + c] +
+                   SH_C3[3] * z * (2.f * zz - 3.f * xx - 3.f * yy) * r[11 * 3 + c] +
+                   SH_C3[4] * x * (4.f * zz - xx - yy) * r[12 * 3 + c] +
+                   SH_C3[5] * z * (xx - yy) * r[13 * 3 + c] + SH_C3[6] * x * (xx - 3.f * yy) * r[14 * 3 + c]);
+        if (degree < 4) continue;
+        col[c] += (SH_C4[0] * xy * (xx - yy) * r[15 * 3 + c] + SH_C4[1] * yz * (3.f * xx - yy) * r[16 * 3 + c] +
+                   SH_C4[2] * xy * (7.f * zz - 1.f) * r[17 * 3 + c] +
+                   SH_C4[3] * yz * (7.f * zz - 3.f) * r[18 * 3 + c] +
+                   SH_C4[4] * (zz * (35.f * zz - 30.f) + 3.f) * r[19 * 3 + c] +
+                   SH_C4[5] * xz * (7.f * zz - 3.f) * r[20 * 3 + c] +
+                   SH_C4[6] * (xx - yy) * (7.f * zz - 1.f) * r[21 * 3 + c] +
+                   SH_C4[7] * xz * (xx - 3.f * yy) * r[22 * 3 + c] +
+                   SH_C4[8] * (xx * (xx - 3.f * yy) - yy * (3.f * xx - yy)) * r[23 * 3 + c]);
+    }
+}
+
+// Basis values of sh_coeffs_to_color_vjp (msplat_metal.metal:825-912):
+// b[k-1] multiplies v_colors for rest basis k.  Only the first
+// num_sh_bases(degree)-1 entries are written.
+__device__ __forceinline__ void sh_vjp_basis(int degree, f3 d, float b[24]) {
+    if (degree < 1) return;
+    const float x = d.x, y = d.y, z = d.z;
+    const float xx = x * x, xy = x * y, xz = x * z, yy = y * y, yz = y * z, zz = z * z;
+    b[0] = -SH_C1 * y;
+    b[1] = SH_C1 * z;
+    b[2] = -SH_C1 * x;
+    if (degree < 2) return;
+    b[3] = SH_C2[0] * xy;
+    b[4] = SH_C2[1] * yz;
+    b[5] = SH_C2[2] * (2.f * zz - xx - yy);
+    b[6] = SH_C2[3] * xz;
+    b[7] = SH_C2[4] * (xx - yy);
+    if (degree < 3) return;
+    b[8] = SH_C3[0] * y * (3.f * xx - yy);
+    b[9] = SH_C3[1] * xy * z;
+    b[10] = SH_C3[2] * y * (4.f * zz - xx - yy);
+    b[11] = SH_C3[3] * z * (2.f * zz - 3.f * xx - 3.f * yy);
+    b[12] = SH_C3[4] * x * (4.f * zz - xx - yy);
+    b[13] = SH_C3[5] * z * (xx - yy);
+    b[14] = SH_C3[6] * x * (xx - 3.f * yy);
+    if (degree < 4) return;
+    b[15] = SH_C4[0] * xy * (xx - yy);
+    b[16] = SH_C4[1] * yz * (3.f * xx - yy);
+    b[17] = SH_C4[2] * xy * (7.f * zz - 1.f);
+    b[18] = SH_C4[3] * yz * (7.f * zz - 3.f);
+    b[19] = SH_C4[4] * (zz * (35.f * zz - 30.f) + 3.f);
+    b[20] = SH_C4[5] * xz * (7.f * zz - 3.f);
+    b[21] = SH_C4[6] * (xx - yy) * (7.f * zz - 1.f);
+    b[22] = SH_C4[7] * xz * (xx - 3.f * yy);
+    b[23] = SH_C4[8] * (xx * (xx - 3.f * yy) - yy * (3.f * xx - yy));
+}
+
+// sh_color_dL_ddir (msplat_metal.metal:925-1013); degree-4 bases do not
+// contribute to the view-direction gradient.
+__device__ __forceinline__ f3 sh_dL_ddir(int degree, f3 d, const float *fr, const float vc[3]) {
+    if (degree < 1) return {0.f, 0.f, 0.f};
+    const float x = d.x, y = d.y, z = d.z;
+    float dx[3], dy[3], dz[3];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        dx[c] = -SH_C1 * fr[2 * 3 + c];
+        dy[c] = -SH_C1 * fr[0 * 3 + c];
+        dz[c] = SH_C1 * fr[1 * 3 + c];
+    }
+    if (degree >= 2) {
+        const float xx = x * x, yy = y * y, zz = z * z;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const float s4 = fr[3 * 3 + c], s5 = fr[4 * 3 + c], s6 = fr[5 * 3 + c];
+            const float s7 = fr[6 * 3 + c], s8 = fr[7 * 3 + c];
+            dx[c] += SH_C2[0] * y * s4 + SH_C2[2] * (-2.f * x) * s6 + SH_C2[3] * z * s7 + SH_C2[4] * (2.f * x) * s8;
+            dy[c] += SH_C2[0] * x * s4 + SH_C2[1] * z * s5 + SH_C2[2] * (-2.f * y) * s6 + SH_C2[4] * (-2.f * y) * s8;
+            dz[c] += SH_C2[1] * y * s5 + SH_C2[2] * (4.f * z) * s6 + SH_C2[3] * x * s7;
+        }
+        if (degree >= 3) {
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                const float s9 = fr[8 * 3 + c], s10 = fr[9 * 3 + c], s11 = fr[10 * 3 + c];
+                const float s12 = fr[11 * 3 + c], s13 = fr[12 * 3 + c];
+                const float s14 = fr[13 * 3 + c], s15 = fr[14 * 3 + c];
+                dx[c] += SH_C3[0] * s9 * (6.f * x * y) + SH_C3[1] * s10 * (y * z) +
+                         SH_C3[2] * s11 * (-2.f * x * y) + SH_C3[3] * s12 * (-6.f * x * z) +
+                         SH_C3[4] * s13 * (-3.f * xx + 4.f * zz - yy) + SH_C3[5] * s14 * (2.f * x * z) +
+                         SH_C3[6] * s15 * (3.f * (xx - yy));
+                dy[c] += SH_C3[0] * s9 * (3.f * (xx - yy)) + SH_C3[1] * s10 * (x * z) +
+                         SH_C3[2] * s11 * (-3.f * yy + 4.f * zz - xx) + SH_C3[3] * s12 * (-6.f * y * z) +
+                         SH_C3[4] * s13 * (-2.f * x * y) + SH_C3[5] * s14 * (-2.f * y * z) +
+                         SH_C3[6] * s15 * (-6.f * x * y);
+                dz[c] += SH_C3[1] * s10 * (x * y) + SH_C3[2] * s11 * (8.f * y * z) +
+                         SH_C3[3] * s12 * (3.f * (2.f * zz - xx - yy)) + SH_C3[4] * s13 * (8.f * x * z) +
+                         SH_C3[5] * s14 * (xx - yy);
+            }
+        }
+    }
+    f3 r = {0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        r.x += dx[c] * vc[c];
+        r.y += dy[c] * vc[c];
+        r.z += dz[c] * vc[c];
+    }
+    return r;
+}
+
+// dnormvdv (msplat_metal.metal:1017-1025).
+__device__ __forceinline__ f3 dnormvdv(f3 v, f3 dv) {
+    float sum2 = v.x * v.x + v.y * v.y + v.z * v.z;
+    float invsum32 = 1.0f / __builtin_sqrtf(sum2 * sum2 * sum2);
+    return {((sum2 - v.x * v.x) * dv.x - v.y * v.x * dv.y - v.z * v.x * dv.z) * invsum32,
+            (-v.x * v.y * dv.x + (sum2 - v.y * v.y) * dv.y - v.z * v.y * dv.z) * invsum32,
+            (-v.x * v.z * dv.x - v.y * v.z * dv.y + (sum2 - v.z * v.z) * dv.z) * invsum32};
+}
+
+// Splat record (MSPLAT_REC_FLOATS = 20 floats, five float4):
+//   q0 = (Tu.x Tu.y Tu.z Tv.x)   q1 = (Tv.y Tv.z Tw.x Tw.y)
+//   q2 = (Tw.z xy.x xy.y opacity) q3 = (n.x n.y n.z r)   q4 = (g b 0 0)
+// with opacity = sigmoid(logit) and rgb = max(raw SH + 0.5, 0).
+struct Rec {
+    float4 q0, q1, q2, q3, q4;
+};
+
+// One (pixel, splat) evaluation: the ray-splat intersection, low-pass
+// filter and alpha of nd_rasterize_forward_2dgs_kernel
+// (msplat_metal.metal:663-701).  Shared verbatim by the forward and the
+// backward so both take identical skip decisions.
+struct PairEval {
+    f3 k, l, ray;
+    float u, v, rho3d, rho2d, depth, G, alpha;
+};
+
+__device__ __forceinline__ bool eval_pair(float px, float py, const float4 &q0, const float4 &q1,
+                                          const float4 &q2, PairEval &e) {
+    const float Tux = q0.x, Tuy = q0.y, Tuz = q0.z;
+    const float Tvx = q0.w, Tvy = q1.x, Tvz = q1.y;
+    const float Twx = q1.z, Twy = q1.w, Twz = q2.x;
+    e.k = {__builtin_fmaf(px, Twx, -Tux), __builtin_fmaf(px, Twy, -Tuy), __builtin_fmaf(px, Twz, -Tuz)};
+    e.l = {__builtin_fmaf(py, Twx, -Tvx), __builtin_fmaf(py, Twy, -Tvy), __builtin_fmaf(py, Twz, -Tvz)};
+    e.ray = {__builtin_fmaf(e.k.y, e.l.z, -(e.k.z * e.l.y)), __builtin_fmaf(e.k.z, e.l.x, -(e.k.x * e.l.z)),
+             __builtin_fmaf(e.k.x, e.l.y, -(e.k.y * e.l.x))};
+    if (e.ray.z == 0.0f) return false;
+    const float inv_z = 1.0f / e.ray.z;
+    e.u = e.ray.x * inv_z;
+    e.v = e.ray.y * inv_z;
+    e.rho3d = __builtin_fmaf(e.u, e.u, e.v * e.v);
+    const float dxs = q2.y - px, dys = q2.z - py;
+    e.rho2d = FILTER_INV_SQ * __builtin_fmaf(dxs, dxs, dys * dys);
+    const float rho = __builtin_fminf(e.rho3d, e.rho2d);
+    e.depth = __builtin_fmaf(e.u, Twx, __builtin_fmaf(e.v, Twy, Twz));
+    if (e.depth < NEAR_N) return false;
+    const float power = -0.5f * rho;
+    if (power > 0.0f) return false;
+    e.G = ms_expf(power);
+    e.alpha = __builtin_fminf(0.99f, q2.w * e.G);
+    if (e.alpha < 1.0f / 255.0f) return false;
+    return true;
+}
+
+// XCD-aware tile order: MI355X dispatches workgroup i to XCD (i mod 8), so
+// giving XCD x the contiguous band of tiles [x*per, (x+1)*per) keeps
+// neighbouring tiles -- which share splats -- in one XCD's L2.
+__device__ __forceinline__ int xcd_tile(int block, int num_tiles) {
+    const int per = (num_tiles + 7) >> 3;
+    return (block & 7) * per + (block >> 3);
+}
+
+}  // namespace msd

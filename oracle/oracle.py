@@ -1,0 +1,242 @@
+"""ctypes binding of the CPU golden model (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker.  See golden.h for the
+arithmetic contract and the deliberate deviations from the fork.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "liboracle.so"
+_lib = None
+
+f32p = C.POINTER(C.c_float)
+i32p = C.POINTER(C.c_int32)
+
+
+class OrcCamera(C.Structure):
+    _fields_ = [("viewmat", C.c_float * 16), ("projmat", C.c_float * 16), ("cam_pos", C.c_float * 3),
+                ("fx", C.c_float), ("fy", C.c_float), ("cx", C.c_float), ("cy", C.c_float),
+                ("width", C.c_int), ("height", C.c_int), ("tiles_x", C.c_int), ("tiles_y", C.c_int)]
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        L = C.CDLL(str(LIB))
+        P = C.c_void_p
+        L.orc_expf.restype = C.c_float
+        L.orc_expf.argtypes = [C.c_float]
+        L.orc_expf_array.argtypes = [C.c_int64, P, P]
+        L.orc_ssim_window.argtypes = [P]
+        L.orc_num_threads.restype = C.c_int
+        L.orc_prepare_cam.argtypes = [P, C.c_float, C.c_float, C.c_float, C.c_float, C.c_int, C.c_int,
+                                      C.POINTER(OrcCamera)]
+        L.orc_project_fwd.argtypes = [C.c_int] + [P] * 6 + [C.c_int, C.c_int, C.POINTER(OrcCamera), C.c_float,
+                                                            C.c_float] + [P] * 8
+        L.orc_count_tiles.restype = C.c_int64
+        L.orc_count_tiles.argtypes = [C.c_int, P, P, C.c_int, C.c_int, P]
+        L.orc_bin_sort.argtypes = [C.c_int, P, P, P, C.c_int, C.c_int, P, P, P, P]
+        L.orc_raster_fwd.argtypes = [C.POINTER(OrcCamera)] + [P] * 15 + [C.POINTER(C.c_int64)]
+        L.orc_loss_fwd_bwd.restype = C.c_double
+        L.orc_loss_fwd_bwd.argtypes = [C.c_int, C.c_int, P, P, P, C.c_float, C.c_float, C.c_float, P, P,
+                                       C.POINTER(C.c_double)]
+        L.orc_raster_bwd.argtypes = [C.POINTER(OrcCamera), C.c_int] + [P] * 16
+        L.orc_project_bwd.argtypes = [C.c_int, P, P, P, P, C.c_int, C.c_int, C.POINTER(OrcCamera), C.c_float,
+                                      P, P, P, P, P, P, P, P, P, P, P, C.c_float]
+        L.orc_adam.argtypes = [P, P, P, P, C.c_int64, C.c_float, C.c_float, C.c_float, C.c_float, C.c_float]
+        L.orc_densify.restype = C.c_int
+        L.orc_densify.argtypes = [C.c_int, C.c_int, C.c_float, C.c_float, C.c_float, C.c_int, C.c_float,
+                                  C.c_float, C.c_float, C.c_int, P, P, P, C.c_float, P * 6, C.c_int, P * 6,
+                                  P * 6, P]
+        L.orc_train_step.restype = C.c_double
+        L.orc_train_step.argtypes = [C.c_int] + [P] * 6 + [C.c_int, C.c_int, C.POINTER(OrcCamera), P, P,
+                                                          C.c_float, P * 6, P * 6, P, C.c_int, P, P, P, P, P,
+                                                          C.POINTER(C.c_int64)]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data
+
+
+def _f(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def expf(x: float) -> float:
+    return float(lib().orc_expf(float(x)))
+
+
+def expf_array(x: np.ndarray) -> np.ndarray:
+    x = _f(x)
+    y = np.empty_like(x)
+    lib().orc_expf_array(x.size, _p(x), _p(y))
+    return y
+
+
+def ssim_window() -> np.ndarray:
+    w = np.zeros(11, np.float32)
+    lib().orc_ssim_window(_p(w))
+    return w
+
+
+def num_threads() -> int:
+    return int(lib().orc_num_threads())
+
+
+def prepare_cam(cam_to_world, fx, fy, cx, cy, width, height) -> OrcCamera:
+    c2w = _f(cam_to_world).reshape(16)
+    cam = OrcCamera()
+    lib().orc_prepare_cam(c2w.ctypes.data, fx, fy, cx, cy, int(width), int(height), C.byref(cam))
+    return cam
+
+
+def project_fwd(scene_params: dict, cam: OrcCamera, degree: int, dtu: int, glob_scale=1.0, clip_thresh=0.01):
+    m = _f(scene_params["means"])
+    n = m.shape[0]
+    fr = _f(scene_params["features_rest"])
+    out = dict(xys=np.zeros((n, 2), np.float32), depths=np.zeros(n, np.float32), radii=np.zeros(n, np.int32),
+               transmats=np.zeros((n, 9), np.float32), normal_opac=np.zeros((n, 4), np.float32),
+               colors=np.zeros((n, 3), np.float32), tiles_hit=np.zeros(n, np.int32),
+               rect=np.zeros((n, 4), np.int32))
+    ins = [_f(scene_params[k]) for k in ("scales", "quats", "opacities", "features_dc")]
+    lib().orc_project_fwd(n, _p(m), _p(ins[0]), _p(ins[1]), _p(ins[2]), _p(ins[3]), _p(fr), degree, dtu,
+                          C.byref(cam), glob_scale, clip_thresh, *[_p(out[k]) for k in
+                                                                   ("xys", "depths", "radii", "transmats",
+                                                                    "normal_opac", "colors", "tiles_hit", "rect")])
+    return out
+
+
+def bin_sort(proj: dict, cam: OrcCamera):
+    n = proj["radii"].shape[0]
+    T = cam.tiles_x * cam.tiles_y
+    counts = np.zeros(T, np.int32)
+    I = lib().orc_count_tiles(n, _p(proj["radii"]), _p(proj["rect"]), cam.tiles_x, cam.tiles_y, _p(counts))
+    offsets = np.zeros(T + 1, np.int32)
+    keys = np.zeros(max(I, 1), np.uint64)
+    ids = np.zeros(max(I, 1), np.int32)
+    lib().orc_bin_sort(n, _p(proj["radii"]), _p(proj["rect"]), _p(proj["depths"]), cam.tiles_x, cam.tiles_y,
+                       _p(counts), _p(offsets), _p(keys), _p(ids))
+    return dict(tile_counts=counts, tile_offsets=offsets, keys=keys[:I], ids=ids[:I], num_intersections=int(I))
+
+
+def raster_fwd(proj: dict, bins: dict, cam: OrcCamera, background):
+    H, W = cam.height, cam.width
+    o = dict(out_img=np.zeros((H, W, 3), np.float32), final_Ts=np.zeros((H, W, 3), np.float32),
+             final_idx=np.zeros((H, W, 2), np.int32), out_depth=np.zeros((H, W), np.float32),
+             out_normal=np.zeros((H, W, 3), np.float32), out_alpha=np.zeros((H, W), np.float32),
+             out_median_depth=np.zeros((H, W), np.float32), out_distortion=np.zeros((H, W), np.float32))
+    pairs = C.c_int64()
+    bg = _f(background)
+    ids = bins["ids"] if bins["ids"].size else np.zeros(1, np.int32)
+    lib().orc_raster_fwd(C.byref(cam), _p(bins["tile_offsets"]), _p(ids), _p(proj["xys"]), _p(proj["transmats"]),
+                         _p(proj["normal_opac"]), _p(proj["colors"]), _p(bg),
+                         *[_p(o[k]) for k in ("out_img", "final_Ts", "final_idx", "out_depth", "out_normal",
+                                              "out_alpha", "out_median_depth", "out_distortion")],
+                         C.byref(pairs))
+    o["pairs_evaluated"] = int(pairs.value)
+    return o
+
+
+def render(scene, cam_index=0, degrees_to_use=None):
+    """Forward pass of the golden model for a synthetic Scene."""
+    c = scene.cameras[cam_index]
+    cam = prepare_cam(c.cam_to_world, c.fx, c.fy, c.cx, c.cy, c.width, c.height)
+    dtu = scene.sh_degree if degrees_to_use is None else degrees_to_use
+    params = dict(means=scene.means, scales=scene.scales, quats=scene.quats, opacities=scene.opacities,
+                  features_dc=scene.features_dc, features_rest=scene.features_rest)
+    proj = project_fwd(params, cam, scene.sh_degree, dtu)
+    bins = bin_sort(proj, cam)
+    fwd = raster_fwd(proj, bins, cam, scene.background)
+    return cam, proj, bins, fwd
+
+
+def loss_fwd_bwd(img, gt, distortion=None, lambda_l1=0.8, lambda_dist=0.0, lambda_dssim=0.2):
+    img, gt = _f(img), _f(gt)
+    H, W = img.shape[:2]
+    dL = np.zeros_like(img)
+    dd = np.zeros((H, W), np.float32)
+    ssim = C.c_double()
+    dist = None if distortion is None else _f(distortion)
+    loss = lib().orc_loss_fwd_bwd(W, H, _p(img), _p(gt), _p(dist), lambda_l1, lambda_dist, lambda_dssim, _p(dL),
+                                  _p(dd), C.byref(ssim))
+    return float(loss), dL, dd, float(ssim.value)
+
+
+def raster_bwd(proj, bins, fwd, cam, background, dL_dimg, dL_ddepth=None, dL_dalpha=None, dL_dnormal=None,
+               dL_dmedian=None, dL_ddist=None):
+    n = proj["radii"].shape[0]
+    g = np.zeros((n, 16), np.float32)
+    ids = bins["ids"] if bins["ids"].size else np.zeros(1, np.int32)
+    opt = [None if a is None else _f(a) for a in (dL_ddepth, dL_dalpha, dL_dnormal, dL_dmedian, dL_ddist)]
+    lib().orc_raster_bwd(C.byref(cam), n, _p(bins["tile_offsets"]), _p(ids), _p(proj["xys"]),
+                         _p(proj["transmats"]), _p(proj["normal_opac"]), _p(proj["colors"]), _p(_f(background)),
+                         _p(fwd["final_Ts"]), _p(fwd["final_idx"]), _p(_f(dL_dimg)), *[_p(a) for a in opt], _p(g))
+    return g
+
+
+def project_bwd(params: dict, cam, degree, dtu, radii, grads16, stats=None, glob_scale=1.0):
+    m = _f(params["means"])
+    n = m.shape[0]
+    K = (degree + 1) ** 2 - 1
+    out = dict(dmeans=np.zeros((n, 3), np.float32), dscales=np.zeros((n, 2), np.float32),
+               dquats=np.zeros((n, 4), np.float32), dmean2d=np.zeros((n, 2), np.float32),
+               dfdc=np.zeros((n, 3), np.float32), dfrest=np.zeros((n, max(K, 0), 3), np.float32))
+    if stats is None:
+        stats = dict(grad_norm=np.zeros(n, np.float32), vis=np.zeros(n, np.float32), max2d=np.zeros(n, np.float32))
+    inv_max_dim = np.float32(1.0) / np.float32(max(cam.width, cam.height))
+    lib().orc_project_bwd(n, _p(m), _p(_f(params["scales"])), _p(_f(params["quats"])),
+                          _p(_f(params["features_rest"])), degree, dtu, C.byref(cam), glob_scale,
+                          _p(np.ascontiguousarray(radii, np.int32)), _p(_f(grads16)),
+                          *[_p(out[k]) for k in ("dmeans", "dscales", "dquats", "dmean2d", "dfdc", "dfrest")],
+                          _p(stats["grad_norm"]), _p(stats["vis"]), _p(stats["max2d"]), float(inv_max_dim))
+    out.update(stats)
+    return out
+
+
+def adam(params, grads, m, v, step_size, beta1=0.9, beta2=0.999, bc2_sqrt=1.0, eps=1e-8):
+    lib().orc_adam(_p(params), _p(grads), _p(m), _p(v), params.size, step_size, beta1, beta2, bc2_sqrt, eps)
+
+
+def densify(n, capacity, params6, exp_avg6, exp_avg_sq6, fr_stride, stats, random_samples, grad_thresh=0.0002,
+            size_thresh=0.01, screen_thresh=0.05, check_screen=1, cull_alpha=0.1, cull_scale=0.5,
+            cull_screen=0.15, check_huge=1, half_max_dim=648.5):
+    P6 = C.c_void_p * 6
+    r = lib().orc_densify(n, capacity, grad_thresh, size_thresh, screen_thresh, check_screen, cull_alpha,
+                          cull_scale, cull_screen, check_huge, _p(stats["grad_norm"]), _p(stats["vis"]),
+                          _p(stats["max2d"]), half_max_dim, P6(*[_p(a) for a in params6]), fr_stride,
+                          P6(*[_p(a) for a in exp_avg6]), P6(*[_p(a) for a in exp_avg_sq6]),
+                          _p(_f(random_samples)))
+    return int(r)
+
+
+def train_step(params6, exp_avg6, exp_avg_sq6, cam, background, gt, degree, dtu, adam_lr, adam_step, stats,
+               ssim_weight=0.2):
+    """One golden-model training step in place; returns (loss, img, stage_ms, I)."""
+    m, s, q, dc, fr, op = params6
+    n = m.shape[0]
+    P6 = C.c_void_p * 6
+    img = np.zeros((cam.height, cam.width, 3), np.float32)
+    stage = np.zeros(8, np.float64)
+    nis = C.c_int64()
+    lr = np.asarray(adam_lr, np.float32)
+    loss = lib().orc_train_step(n, _p(m), _p(s), _p(q), _p(op), _p(dc), _p(fr), degree, dtu, C.byref(cam),
+                                _p(_f(background)), _p(_f(gt)), ssim_weight, P6(*[_p(a) for a in exp_avg6]),
+                                P6(*[_p(a) for a in exp_avg_sq6]), _p(lr), adam_step, _p(stats["grad_norm"]),
+                                _p(stats["vis"]), _p(stats["max2d"]), _p(img), _p(stage), C.byref(nis))
+    return float(loss), img, stage, int(nis.value)

@@ -1,0 +1,346 @@
+"""GPU parity: every stage of the HIP training step against the CPU golden
+model on identical seeded inputs, through the C-ABI.
+
+Bars (the oracle's arithmetic contract makes the non-atomic stages exact):
+  projection, binning, per-tile order, rasterize forward, loss gradient,
+  projection backward (given equal raster gradients), Adam, densify:
+  bit-exact;
+  rasterize backward (float atomics): max |gpu - oracle| <= 1e-3 * max|oracle|
+  per gradient component;
+  scalar loss: relative 1e-5 (fp64 reduction order differs).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+from msplat import _engine as E  # noqa: E402
+from msplat import device as D  # noqa: E402
+from msplat import synthetic as S  # noqa: E402
+
+
+def _cams(scene, idx, orc):
+    c = scene.cameras[idx]
+    return orc.prepare_cam(c.cam_to_world, c.fx, c.fy, c.cx, c.cy, c.width, c.height)
+
+
+def _params(scene):
+    return dict(means=scene.means, scales=scene.scales, quats=scene.quats, opacities=scene.opacities,
+                features_dc=scene.features_dc, features_rest=scene.features_rest)
+
+
+def _assert_bitexact(a, b, what):
+    a = np.asarray(a)
+    b = np.asarray(b)
+    assert a.shape == b.shape, (what, a.shape, b.shape)
+    if a.dtype.kind == "f":
+        bad = ~((a == b) | (np.isnan(a) & np.isnan(b)))
+    else:
+        bad = a != b
+    nbad = int(bad.sum())
+    if nbad:
+        idx = np.argwhere(bad)[:5]
+        raise AssertionError(f"{what}: {nbad} of {a.size} entries differ, first at {idx.tolist()}: "
+                             f"gpu={a[tuple(idx[0])]!r} oracle={b[tuple(idx[0])]!r}")
+
+
+def _forward_both(scene, cam_idx, orc, eng, dtu=None):
+    dtu = scene.sh_degree if dtu is None else dtu
+    ocam, proj, bins, fwd = orc.render(scene, cam_idx, dtu)
+    ds = D.DeviceScene(scene)
+    gcam = ds.camera(scene.cameras[cam_idx], dtu)
+    out = D.render(ds, gcam, outputs=("out_img", "final_Ts", "final_idx", "out_depth", "out_normal", "out_alpha",
+                                      "out_median_depth", "out_distortion"))
+    return ocam, proj, bins, fwd, ds, gcam, out
+
+
+SCENES = {
+    "fwd16k": lambda: S.make_scene(1),
+    "blob40k_sh3": lambda: S.make_scene(2, n=40_000, width=320, height=208, num_cameras=4),
+}
+
+
+@pytest.mark.parametrize("name", list(SCENES))
+def test_camera_setup_bitexact(name, orc, eng):
+    scene = SCENES[name]()
+    for idx in range(len(scene.cameras)):
+        c = scene.cameras[idx]
+        o = orc.prepare_cam(c.cam_to_world, c.fx, c.fy, c.cx, c.cy, c.width, c.height)
+        g = E.prepare_camera(c.cam_to_world, c.fx, c.fy, c.cx, c.cy, c.width, c.height, scene.sh_degree,
+                             scene.sh_degree)
+        _assert_bitexact(np.array(g.viewmat), np.array(o.viewmat), "viewmat")
+        _assert_bitexact(np.array(g.projmat), np.array(o.projmat), "projmat")
+        _assert_bitexact(np.array(g.cam_pos), np.array(o.cam_pos), "cam_pos")
+
+
+@pytest.mark.parametrize("name", list(SCENES))
+def test_project_and_binning_bitexact(name, orc, eng):
+    scene = SCENES[name]()
+    print(f"[project/binning] scene={name} n={scene.n}", flush=True)
+    ocam, proj, bins, fwd, ds, gcam, out = _forward_both(scene, 0, orc, eng)
+    n = scene.n
+    _assert_bitexact(E.last("radii"), proj["radii"], "radii")
+    _assert_bitexact(E.last("depths"), proj["depths"], "depths")
+    _assert_bitexact(E.last("xys", (n, 2)), proj["xys"], "xys")
+    _assert_bitexact(E.last("transmats", (n, 9)), proj["transmats"], "transmats")
+    _assert_bitexact(E.last("normals", (n, 3)), proj["normal_opac"][:, :3], "normals")
+    vis = proj["radii"] > 0
+    sig = np.zeros(n, np.float32)
+    for i in np.flatnonzero(vis):
+        sig[i] = np.float32(1.0) / (np.float32(1.0) + np.float32(orc.expf(-proj["normal_opac"][i, 3])))
+    _assert_bitexact(E.last("opacity_sigmoid"), sig, "opacity sigmoid")
+    used = np.where(vis[:, None], np.maximum(proj["colors"] + np.float32(0.5), np.float32(0.0)), 0).astype(np.float32)
+    _assert_bitexact(E.last("colors_used", (n, 3)), used, "colors (clamped)")
+    _assert_bitexact(E.last("num_tiles_hit"), proj["tiles_hit"], "tiles hit")
+    assert out["num_intersections"] == bins["num_intersections"]
+    _assert_bitexact(E.last("tile_offsets"), bins["tile_offsets"], "tile offsets")
+    _assert_bitexact(E.last("gaussian_ids"), bins["ids"], "per-tile sorted ids")
+
+
+@pytest.mark.parametrize("name", list(SCENES))
+def test_raster_forward_bitexact(name, orc, eng):
+    scene = SCENES[name]()
+    print(f"[raster fwd] scene={name}", flush=True)
+    ocam, proj, bins, fwd, ds, gcam, out = _forward_both(scene, 0, orc, eng)
+    for k in ("out_img", "final_Ts", "final_idx", "out_depth", "out_normal", "out_alpha", "out_median_depth",
+              "out_distortion"):
+        _assert_bitexact(out[k], fwd[k], k)
+
+
+def test_overflow_tiles_merge_path(orc, eng):
+    """Tiles far above 2048 intersections: the chunked LDS sort + global
+    merge must give the oracle's full (untruncated) per-tile order."""
+    scene = S.make_scene(4, n=100_000, width=480, height=270, num_cameras=2)
+    print(f"[overflow] n={scene.n}", flush=True)
+    ocam, proj, bins, fwd, ds, gcam, out = _forward_both(scene, 0, orc, eng)
+    assert bins["tile_counts"].max() > 8 * 2048, bins["tile_counts"].max()
+    _assert_bitexact(E.last("tile_offsets"), bins["tile_offsets"], "tile offsets")
+    _assert_bitexact(E.last("gaussian_ids"), bins["ids"], "per-tile sorted ids")
+    _assert_bitexact(out["out_img"], fwd["out_img"], "out_img")
+    _assert_bitexact(out["final_idx"], fwd["final_idx"], "final_idx")
+
+
+def test_empty_scene_renders_background(orc, eng):
+    scene = S.make_scene(1, n=64, width=48, height=40)
+    scene.means[:] = np.float32(-50.0)  # all behind the camera
+    ds = D.DeviceScene(scene)
+    out = D.render(ds, ds.camera(scene.cameras[0]))
+    assert out["num_intersections"] == 0
+    assert np.array_equal(out["out_img"], np.broadcast_to(scene.background, out["out_img"].shape))
+
+
+def _device(a):
+    return E.DeviceArray.from_numpy(np.ascontiguousarray(a, np.float32))
+
+
+@pytest.mark.parametrize("shape", [(208, 320), (37, 53), (1, 1), (11, 150)])
+def test_loss_fwd_bwd_bitexact(shape, orc, eng):
+    H, W = shape
+    rng = S.SplitMix64(17 + H * W)
+    img = rng.uniform(H * W * 3).reshape(H, W, 3).astype(np.float32)
+    gt = rng.uniform(H * W * 3).reshape(H, W, 3).astype(np.float32)
+    gt[: H // 2] = img[: H // 2]  # exact-equality pixels: sign(0) = 0
+    loss_o, dL_o, _, ssim_o = orc.loss_fwd_bwd(img, gt)
+    d_img, d_gt, d_dL = _device(img), _device(gt), E.DeviceArray((H, W, 3))
+    loss = C.c_double()
+    ssim = C.c_double()
+    E.check(E.lib().msplat_hip_loss_fwd_bwd(W, H, d_img.ptr, d_gt.ptr, None, 0.8, 0.0, 0.2, d_dL.ptr,
+                                           C.byref(loss), C.byref(ssim)))
+    _assert_bitexact(d_dL.numpy(), dL_o, "dL/dimg")
+    assert abs(loss.value - loss_o) <= 1e-5 * abs(loss_o) + 1e-9
+    assert abs(ssim.value - ssim_o) <= 1e-6 * abs(ssim_o) + 1e-6
+
+
+def _grad_close(g, o, what, rtol=1e-3):
+    g = np.asarray(g, np.float64)
+    o = np.asarray(o, np.float64)
+    scale = np.abs(o).max(axis=0)
+    err = np.abs(g - o).max(axis=0)
+    ok = err <= rtol * scale + 1e-12
+    assert ok.all(), f"{what}: err {err} scale {scale}"
+
+
+@pytest.mark.parametrize("name", list(SCENES))
+def test_raster_backward_close(name, orc, eng):
+    scene = SCENES[name]()
+    print(f"[raster bwd] scene={name}", flush=True)
+    ocam, proj, bins, fwd, ds, gcam, out = _forward_both(scene, 0, orc, eng)
+    target = scene.jittered(0.01, 99)
+    gt = orc.render(target, 0)[3]["out_img"]
+    _, dL, _, _ = orc.loss_fwd_bwd(fwd["out_img"], gt)
+    g_o = orc.raster_bwd(proj, bins, fwd, ocam, scene.background, dL)
+    d_dL = _device(dL)
+    g16 = E.DeviceArray.zeros((scene.n, 16))
+    E.check(E.lib().msplat_hip_raster_bwd(d_dL.ptr, None, None, None, None, None, g16.ptr))
+    g = g16.numpy()
+    assert np.abs(g_o).max() > 0
+    _grad_close(g, g_o, "grads16 [dT(9), dn(3), dopacity, dcolor(3)]")
+    # culled splats receive nothing
+    assert np.all(g[proj["radii"] <= 0] == 0)
+
+
+@pytest.mark.parametrize("name", list(SCENES))
+def test_project_backward_bitexact(name, orc, eng):
+    scene = SCENES[name]()
+    ocam, proj, bins, fwd, ds, gcam, out = _forward_both(scene, 0, orc, eng)
+    n = scene.n
+    rng = S.SplitMix64(5)
+    g16 = (rng.normal(n * 16, 0.0, 1e-3).reshape(n, 16)).astype(np.float32)
+    g16[proj["radii"] <= 0] = 0
+    stats0 = dict(grad_norm=rng.uniform(n).astype(np.float32), vis=np.floor(rng.uniform(n) * 3).astype(np.float32),
+                  max2d=(rng.uniform(n) * 0.05).astype(np.float32))
+    o = orc.project_bwd(_params(scene), ocam, scene.sh_degree, scene.sh_degree, proj["radii"], g16,
+                        {k: v.copy() for k, v in stats0.items()})
+    K3 = ((scene.sh_degree + 1) ** 2 - 1) * 3
+    outs = {k: E.DeviceArray.zeros(s) for k, s in dict(dmeans=(n, 3), dscales=(n, 2), dquats=(n, 4),
+                                                         dmean2d=(n, 2), dfdc=(n, 3), dfrest=(n, max(K3, 1))).items()}
+    st = {k: _device(v) for k, v in stats0.items()}
+    radii = E.DeviceArray.from_numpy(proj["radii"])
+    d16 = _device(g16)
+    E.check(E.lib().msplat_hip_project_bwd(C.byref(gcam), C.byref(ds.gaussians), radii.ptr, d16.ptr,
+                                           outs["dmeans"].ptr, outs["dscales"].ptr, outs["dquats"].ptr,
+                                           outs["dmean2d"].ptr, outs["dfdc"].ptr, outs["dfrest"].ptr,
+                                           st["grad_norm"].ptr, st["vis"].ptr, st["max2d"].ptr,
+                                           float(np.float32(1) / np.float32(max(gcam.width, gcam.height)))))
+    for k in ("dmeans", "dscales", "dquats", "dmean2d", "dfdc"):
+        _assert_bitexact(outs[k].numpy(), o[k], k)
+    if K3:
+        _assert_bitexact(outs["dfrest"].numpy().reshape(o["dfrest"].shape), o["dfrest"], "dfrest")
+    for k in ("grad_norm", "vis", "max2d"):
+        _assert_bitexact(st[k].numpy(), o[k], k)
+
+
+def test_adam_bitexact(orc, eng):
+    rng = S.SplitMix64(23)
+    n = 100_003
+    p = rng.normal(n).astype(np.float32)
+    g = (rng.normal(n) * 1e-3).astype(np.float32)
+    g[::7] = 0
+    m = (rng.normal(n) * 1e-4).astype(np.float32)
+    v = (rng.uniform(n) * 1e-6).astype(np.float32)
+    dp, dg, dm, dv = (_device(a) for a in (p, g, m, v))
+    step, bc2 = np.float32(0.005 / 0.271), np.float32(np.sqrt(np.float32(0.003)))
+    E.check(E.lib().msplat_hip_fused_adam(dp.ptr, dg.ptr, dm.ptr, dv.ptr, n, step, 0.9, 0.999, bc2, 1e-8))
+    orc.adam(p, g, m, v, step, 0.9, 0.999, bc2, 1e-8)
+    _assert_bitexact(dp.numpy(), p, "params")
+    _assert_bitexact(dm.numpy(), m, "exp_avg")
+    _assert_bitexact(dv.numpy(), v, "exp_avg_sq")
+
+
+def test_fused_adam_step_equals_unfused(orc, eng):
+    """Projection backward with the six Adam groups fused in must equal the
+    reference flow (gradients to memory, then msplat_fused_adam per group)
+    bit for bit, given the same raster gradients."""
+    scene = S.make_scene(2, n=30_000, width=256, height=160, num_cameras=2)
+    dsA, dsB = D.DeviceScene(scene), D.DeviceScene(scene)
+    gcam = dsA.camera(scene.cameras[0])
+    D.render(dsA, gcam)
+    radii = E.DeviceArray.from_numpy(E.last("radii"))
+    n = scene.n
+    rng = S.SplitMix64(8)
+    K3 = 45
+    inv_max_dim = float(np.float32(1) / np.float32(max(gcam.width, gcam.height)))
+    for step in range(3):
+        g16 = _device((rng.normal(n * 16, 0.0, 1e-3).reshape(n, 16)).astype(np.float32))
+        adamA = dsA.adam_struct()
+        E.check(E.lib().msplat_hip_project_bwd_adam(C.byref(gcam), C.byref(dsA.gaussians), radii.ptr, g16.ptr,
+                                                    dsA.grad_norm.ptr, dsA.vis.ptr, dsA.max2d.ptr, inv_max_dim,
+                                                    C.byref(adamA)))
+        outs = [E.DeviceArray.zeros(s) for s in ((n, 3), (n, 2), (n, 4), (n, 2), (n, 3), (n, K3))]
+        E.check(E.lib().msplat_hip_project_bwd(C.byref(gcam), C.byref(dsB.gaussians), radii.ptr, g16.ptr,
+                                               *[o.ptr for o in outs], dsB.grad_norm.ptr, dsB.vis.ptr, dsB.max2d.ptr,
+                                               inv_max_dim))
+        adamB = dsB.adam_struct()
+        ga = E.DeviceArray.from_numpy(g16.numpy()[:, 12].copy())
+        grads = [outs[0], outs[1], outs[2], outs[4], outs[5], ga]
+        for gi in range(6):
+            p = dsB.params[gi]
+            E.check(E.lib().msplat_hip_fused_adam(p.ptr, grads[gi].ptr, dsB.exp_avg[gi].ptr, dsB.exp_avg_sq[gi].ptr,
+                                                  int(np.prod(p.shape)), adamB.step_size[gi], adamB.beta1,
+                                                  adamB.beta2, adamB.bc2_sqrt, adamB.eps))
+        E.sync()
+    pa, pb = dsA.host_params(), dsB.host_params()
+    for k in pa:
+        _assert_bitexact(pa[k], pb[k], k)
+    for a, b in zip(dsA.exp_avg + dsA.exp_avg_sq, dsB.exp_avg + dsB.exp_avg_sq):
+        _assert_bitexact(a.numpy(), b.numpy(), "adam moment")
+
+
+def test_train_step_matches_oracle(orc, eng):
+    scene = S.make_scene(2, n=30_000, width=256, height=160, num_cameras=2)
+    target = scene.jittered(0.01, 4)
+    ocam, _, _, tf = orc.render(target, 0)
+    gt = tf["out_img"]
+    # oracle step
+    params = [p.copy() for p in scene.params()]
+    m6 = [np.zeros_like(p) for p in params]
+    v6 = [np.zeros_like(p) for p in params]
+    stats = dict(grad_norm=np.zeros(scene.n, np.float32), vis=np.zeros(scene.n, np.float32),
+                 max2d=np.zeros(scene.n, np.float32))
+    loss_o, img_o, _, nis_o = orc.train_step(params, m6, v6, ocam, scene.background, gt, 3, 3, D.LR_INIT, 1, stats)
+    # gpu step
+    ds = D.DeviceScene(scene)
+    gcam = ds.camera(scene.cameras[0])
+    d_gt = _device(gt)
+    loss, nis = D.train_step(ds, gcam, d_gt)
+    assert nis == nis_o
+    assert abs(loss - loss_o) <= 1e-5 * abs(loss_o)
+    _assert_bitexact(E.last("out_img", img_o.shape), img_o, "rendered image")
+    got = ds.host_params()
+    names = list(got)
+    for k, p_o, p0, lr in zip(names, params, scene.params(), D.LR_INIT):
+        diff = np.abs(got[k].astype(np.float64) - p_o)
+        frac = float((diff <= 1e-5).mean())
+        assert frac >= 0.999, (k, frac, diff.max())
+        # the few others are splats whose gradient is atomic-order noise near
+        # zero; Adam's first step moves any element by at most lr
+        assert diff.max() <= 2.0 * lr + 1e-6, (k, diff.max())
+    for k in stats:
+        got_s = {"grad_norm": ds.grad_norm, "vis": ds.vis, "max2d": ds.max2d}[k].numpy()
+        if k == "vis" or k == "max2d":
+            _assert_bitexact(got_s, stats[k], k)
+
+
+def _densify_inputs(scene, n, cap, seed):
+    rng = S.SplitMix64(seed)
+    K3 = ((scene.sh_degree + 1) ** 2 - 1) * 3
+    strides = [3, 2, 4, 3, K3, 1]
+    params = [np.zeros(cap * s, np.float32) for s in strides]
+    src = [scene.means, scene.scales, scene.quats, scene.features_dc, scene.features_rest, scene.opacities]
+    for p, s, st in zip(params, src, strides):
+        p[: n * st] = s.reshape(-1)[: n * st]
+    m6 = [np.zeros(cap * s, np.float32) for s in strides]
+    v6 = [np.zeros(cap * s, np.float32) for s in strides]
+    for a in m6 + v6:
+        a[: a.size // cap * n] = (rng.uniform(a.size // cap * n) * 1e-3).astype(np.float32)
+    stats = dict(grad_norm=(rng.uniform(n) * 0.02).astype(np.float32),
+                 vis=np.floor(rng.uniform(n) * 4).astype(np.float32),
+                 max2d=(rng.uniform(n) * 0.3).astype(np.float32))
+    rs = rng.normal(2 * n * 3).reshape(2 * n, 3).astype(np.float32)
+    return params, m6, v6, strides, stats, rs
+
+
+def test_densify_bitexact(orc, eng):
+    scene = S.make_scene(5, n=20_000, width=320, height=208, num_cameras=1)
+    scene.scales[::3] += np.float32(2.0)  # large splats: split candidates
+    scene.opacities[::11] = np.float32(-6.0)  # transparent splats: culled
+    n = scene.n
+    cap = 3 * n + 17
+    params, m6, v6, strides, stats, rs = _densify_inputs(scene, n, cap, 77)
+    dev = [_device(a) for a in params + m6 + v6]
+    dstats = {k: _device(v) for k, v in stats.items()}
+    d_rs = _device(rs)
+    P6 = C.c_void_p * 6
+    newc = C.c_int()
+    E.check(E.lib().msplat_hip_densify(n, cap, 0.0002, 0.01, 0.05, 1, 0.1, 0.5, 0.15, 1, dstats["grad_norm"].ptr,
+                                       dstats["vis"].ptr, dstats["max2d"].ptr, 648.5,
+                                       P6(*[d.ptr for d in dev[0:6]]), strides[4], P6(*[d.ptr for d in dev[6:12]]),
+                                       P6(*[d.ptr for d in dev[12:18]]), d_rs.ptr, C.byref(newc)))
+    new_o = orc.densify(n, cap, params, m6, v6, strides[4], stats, rs, half_max_dim=648.5)
+    assert newc.value == new_o
+    assert new_o != n
+    for i, (d, o) in enumerate(zip(dev, params + m6 + v6)):
+        s = strides[i % 6]
+        _assert_bitexact(d.numpy()[: new_o * s], o[: new_o * s], f"buffer {i}")
