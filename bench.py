@@ -1,0 +1,190 @@
+"""Benchmark: the full 2DGS training step (projection + SH, binning, per-tile
+sort, rasterize, SSIM + L1, backward, fused Adam on six groups) on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--workload 3] [--gpus 1]
+
+Default workload: 3M splats, SH degree 3, 5187x3361 (the train-step
+configuration of the headline metric).  Inputs are synthetic (seeded blob
+mixture, 32 orbit cameras; targets are renders of the scene with jittered
+means) and resident in HBM before the timed region.  Prints ONE JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "msplat-ios_amd"))
+
+METRIC = "train steps/s @3M splats 5187x3361; render FPS; % HBM peak per kernel"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+VALU_PEAK_LANE_OPS = 39.3e12   # 256 CU x 64 lanes x 2.4 GHz, non-packed
+
+
+def algorithmic_bytes(stage: str, N: int, I: int, P: int, T: int) -> float:
+    """Compulsory HBM bytes of one launch of each stage (fp32, SH degree 3)."""
+    return {
+        "project_fwd": 328.0 * N + 4.0 * T,          # 232 B params in, 96 B record/depth/radius/rect out
+        "tile_scan": 12.0 * T,                        # counts in, offsets + cursors out
+        "scatter_sort": 16.0 * N + 24.0 * I,          # rect/depth/radius in, key out+in, id out
+        "raster_fwd": 84.0 * I + 60.0 * P,            # id + 80 B record per intersection, 8 outputs
+        "ssim_l1": 132.0 * P,                         # img+gt in, 3 gradient maps out/in, dL/dimg out
+        "raster_bwd": 84.0 * I + 128.0 * N + 32.0 * P,  # records, gradient RMW, per-pixel state
+        "project_bwd_adam": 1484.0 * N,               # params+m+v RMW, raster grads, stats
+    }.get(stage, 0.0)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", type=int, default=3)
+    ap.add_argument("--render-frames", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: the training step is single-GPU (one camera per step); "
+              "multi-GPU runs are not part of this build (see DESIGN.md, 'How the step would shard').",
+              file=sys.stderr)
+        return 2
+
+    from msplat import _engine as E
+    from msplat import device as D
+    from msplat import synthetic as S
+
+    E.init()
+    t0 = time.time()
+    scene = S.make_scene(args.workload)
+    target_scene = scene.jittered(0.01, 0xC0FFEE + 100 + args.workload)
+    print(f"[bench] scene {scene.name}: n={scene.n} generated in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    ds = D.DeviceScene(scene)
+    tgt = D.DeviceScene(target_scene)
+    cams = [ds.camera(c) for c in scene.cameras]
+    gts = [D.render_to_device(tgt, c) for c in cams]
+    del tgt
+    E.sync()
+    W, H = scene.cameras[0].width, scene.cameras[0].height
+    P = W * H
+    T = cams[0].tiles_x * cams[0].tiles_y
+    print(f"[bench] targets rendered; warmup {args.warmup}", file=sys.stderr, flush=True)
+
+    for k in range(args.warmup):
+        D.train_step(ds, cams[k % len(cams)], gts[k % len(cams)])
+    E.enable_timing(True)
+    E.sync()
+    stage_sum: dict[str, float] = {}
+    isect = []
+    pairs = []
+    losses = []
+    t_start = time.perf_counter()
+    for k in range(args.steps):
+        ci = (args.warmup + k) % len(cams)
+        loss, nis = D.train_step(ds, cams[ci], gts[ci])
+        losses.append(loss)
+        isect.append(nis)
+        pairs.append(E.pairs_evaluated())
+        for name, ms in E.stage_times().items():
+            stage_sum[name] = stage_sum.get(name, 0.0) + ms
+    E.sync()
+    t_end = time.perf_counter()
+    ms_per_step = (t_end - t_start) * 1e3 / args.steps
+    print(f"[bench] {args.steps} steps: {ms_per_step:.2f} ms/step, loss {losses[0]:.4f} -> {losses[-1]:.4f}",
+          file=sys.stderr, flush=True)
+
+    # render-only frames (the FPS half of the metric)
+    E.enable_timing(False)
+    for k in range(3):
+        D.render(ds, cams[k % len(cams)], outputs=())
+    E.sync()
+    r0 = time.perf_counter()
+    for k in range(args.render_frames):
+        n = E.C.c_int64()
+        E.check(E.lib().msplat_hip_render(E.C.byref(cams[k % len(cams)]), E.C.byref(ds.gaussians),
+                                          ds.background.ptr, E.C.byref(n)))
+    E.sync()
+    render_ms = (time.perf_counter() - r0) * 1e3 / args.render_frames
+
+    N = scene.n
+    I = float(np.mean(isect))
+    kernels = {}
+    for name, tot in stage_sum.items():
+        avg = tot / args.steps
+        b = algorithmic_bytes(name, N, int(I), P, T)
+        gbs = b / (avg * 1e-3) / 1e9 if avg > 0 else 0.0
+        kernels[name] = {"ms": round(avg, 4), "algorithmic_GB": round(b / 1e9, 4), "GB_per_s": round(gbs, 1),
+                         "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    dominant = max(kernels, key=lambda k: kernels[k]["ms"])
+    dk = kernels[dominant]
+    pairs_mean = float(np.mean(pairs))
+    for name in ("raster_fwd", "raster_bwd"):
+        if name in kernels:
+            ops = 60.0 if name == "raster_fwd" else 180.0
+            kernels[name]["pairs_evaluated"] = int(pairs_mean)
+            kernels[name]["frac_valu_peak_est"] = round(pairs_mean * ops / (kernels[name]["ms"] * 1e-3)
+                                                        / VALU_PEAK_LANE_OPS, 4)
+
+    result = {
+        "metric": METRIC,
+        "value": round(1000.0 / ms_per_step, 4),
+        "unit": "train steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": scene.name, "splats": N, "width": W, "height": H, "sh_degree": scene.sh_degree,
+                   "tiles": T, "intersections_mean": int(I), "cameras": len(cams),
+                   "device": E.device_name()},
+        "render_fps": round(1000.0 / render_ms, 2),
+        "render_ms": round(render_ms, 3),
+        "kernels": kernels,
+        "roofline": {"kernel": dominant, "bound": "hbm", "achieved": dk["GB_per_s"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": dk["frac_hbm_peak"], "traffic": None},
+        "loss_first_last": [round(losses[0], 6), round(losses[-1], 6)],
+    }
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(scene, target_scene, args.cpu_threads)
+    print(json.dumps(result))
+    return 0
+
+
+def cpu_baseline(scene, target_scene, threads: int) -> dict:
+    """The golden model (scalar C++ restatement, OpenMP) timed on this host:
+    one full training step of the same workload on camera 0 (the target is
+    rendered by the golden model first, untimed)."""
+    os.environ["OMP_NUM_THREADS"] = str(threads)
+    sys.path.insert(0, str(REPO))
+    from oracle import oracle as O
+
+    c = scene.cameras[0]
+    cam = O.prepare_cam(c.cam_to_world, c.fx, c.fy, c.cx, c.cy, c.width, c.height)
+    gt = O.render(target_scene, 0)[3]["out_img"]
+    params = [p.copy() for p in scene.params()]
+    m6 = [np.zeros_like(p) for p in params]
+    v6 = [np.zeros_like(p) for p in params]
+    stats = dict(grad_norm=np.zeros(scene.n, np.float32), vis=np.zeros(scene.n, np.float32),
+                 max2d=np.zeros(scene.n, np.float32))
+    t0 = time.perf_counter()
+    loss, _, stage_ms, nis = O.train_step(params, m6, v6, cam, scene.background, gt, scene.sh_degree,
+                                          scene.sh_degree, (0.00016, 0.005, 0.001, 0.0025, 0.000125, 0.05), 1, stats)
+    dt = time.perf_counter() - t0
+    return {"value": round(1.0 / dt, 5), "unit": "train steps/s", "cores": O.num_threads(), "kind": "port",
+            "sample": f"1 full step of {scene.name} (camera 0, {nis} intersections) in {dt:.2f} s",
+            "stage_ms": [round(x, 1) for x in stage_ms[:7]]}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

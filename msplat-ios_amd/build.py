@@ -47,7 +47,7 @@ def _compile(src: Path) -> tuple[Path, str]:
     if src.suffix == ".hip":
         cmd = [HIPCC, *DEVICE, *COMMON, "-c", str(src), "-o", str(obj)]
     else:
-        cmd = [HIPCC, *COMMON, "-x", "c++", "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, *COMMON, "-fopenmp", "-x", "c++", "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
@@ -66,7 +66,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
                 print(log, file=sys.stderr)
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-           "-lpthread"]
+           "-fopenmp", "-lpthread"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -66,20 +66,27 @@ __global__ __launch_bounds__(1024) void k_scan_tiles(int T, const int *__restric
 
 // Scatter: every visible gaussian appends (depth bits << 32 | id) to each
 // tile of its rectangle at an atomically claimed slot of that tile's range.
+// The rectangles of a wave are enumerated cooperatively (wave_expand), so
+// the 64 lanes issue independent atomics instead of serial per-lane loops.
 __global__ __launch_bounds__(256) void k_scatter(int n, int tiles_x, const int *__restrict__ radii,
                                                  const uint2 *__restrict__ rect, const float *__restrict__ depths,
                                                  int *__restrict__ cursor, unsigned long long *__restrict__ keys) {
     const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= n || radii[i] <= 0) return;
-    const uint2 r = rect[i];
+    const bool ok = i < n && radii[i] > 0;
+    const uint2 r = ok ? rect[i] : make_uint2(0u, 0u);
     const int x0 = r.x & 0xffff, y0 = r.x >> 16, x1 = r.y & 0xffff, y1 = r.y >> 16;
-    const unsigned long long key =
-        ((unsigned long long)__float_as_uint(depths[i]) << 32) | (unsigned long long)(uint32_t)i;
-    for (int y = y0; y < y1; ++y)
-        for (int x = x0; x < x1; ++x) {
-            const int pos = atomicAdd(&cursor[y * tiles_x + x], 1);
-            keys[pos] = key;
+    const int w = ok ? x1 - x0 : 1;
+    const uint32_t dbits = ok ? __float_as_uint(depths[i]) : 0u;
+    msd::wave_expand(ok ? (x1 - x0) * (y1 - y0) : 0, [&](int owner, int k, bool active) {
+        const int ow = __shfl(w, owner, 64), ox = __shfl(x0, owner, 64), oy = __shfl(y0, owner, 64);
+        const uint32_t od = (uint32_t)__shfl((int)dbits, owner, 64);
+        const int oi = __shfl(i, owner, 64);
+        if (active) {
+            const int ty = k / ow;
+            const int pos = atomicAdd(&cursor[(oy + ty) * tiles_x + ox + (k - ty * ow)], 1);
+            keys[pos] = ((unsigned long long)od << 32) | (unsigned long long)(uint32_t)oi;
         }
+    });
 }
 
 // Ascending bitonic sort of `cnt` (<= kChunk) keys in LDS, padded to a power

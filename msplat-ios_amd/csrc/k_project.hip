@@ -20,15 +20,28 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
     const float *__restrict__ frest, float4 *__restrict__ rec, float *__restrict__ depths,
     int *__restrict__ radii, uint2 *__restrict__ rect, int *__restrict__ tile_counts,
     float *__restrict__ colors_raw) {
+    // The block's features_rest rows (up to 256 x 45 floats) are staged in LDS
+    // with coalesced loads; each thread then reads its own row from LDS.
+    __shared__ float s_fr[kBlock * 45];
+    const int K3 = (num_sh_bases(cam.degree) - 1) * 3;
+    const int b0 = blockIdx.x * kBlock;
+    const int cnt = min(kBlock, n - b0);
+    if (cam.degrees_to_use > 0 && K3 <= 45) {
+        const float *src = frest + (size_t)b0 * K3;
+        for (int e = threadIdx.x; e < cnt * K3; e += kBlock) s_fr[e] = src[e];
+        __syncthreads();
+    }
+    // No early return: every lane of the wave takes part in the tile count.
     const int i = blockIdx.x * kBlock + threadIdx.x;
-    if (i >= n) return;
+    const bool valid = i < n;
+    const int ii = valid ? i : 0;
     const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 *ro = rec + 5 * (size_t)i;
+    float4 *ro = rec + 5 * (size_t)ii;
     const float *vm = cam.viewmat, *pm = cam.projmat;
-    const float p[3] = {means[3 * (size_t)i], means[3 * (size_t)i + 1], means[3 * (size_t)i + 2]};
+    const float p[3] = {means[3 * (size_t)ii], means[3 * (size_t)ii + 1], means[3 * (size_t)ii + 2]};
     const float pz = vm[8] * p[0] + vm[9] * p[1] + vm[10] * p[2] + vm[11];
 
-    bool ok = pz > cam.clip_thresh;
+    bool ok = valid && pz > cam.clip_thresh;
     f3 R0, R1, R2;
     float cxp = 0.f, cyp = 0.f, radius = 0.f;
     f3 T0, T1, T2;
@@ -75,20 +88,21 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
         }
     }
     if (!ok) {
-        radii[i] = 0;
-        depths[i] = 0.f;
-        rect[i] = make_uint2(0u, 0u);
+        if (valid) {
+            radii[i] = 0;
+            depths[i] = 0.f;
+            rect[i] = make_uint2(0u, 0u);
 #pragma unroll
-        for (int k = 0; k < 5; ++k) ro[k] = z4;
-        if (colors_raw) {
-            colors_raw[3 * (size_t)i] = colors_raw[3 * (size_t)i + 1] = colors_raw[3 * (size_t)i + 2] = 0.f;
+            for (int k = 0; k < 5; ++k) ro[k] = z4;
+            if (colors_raw) {
+                colors_raw[3 * (size_t)i] = colors_raw[3 * (size_t)i + 1] = colors_raw[3 * (size_t)i + 2] = 0.f;
+            }
         }
-        return;
-    }
+    } else {
     const f3 dir = normalize3({p[0] - cam.cam_pos[0], p[1] - cam.cam_pos[1], p[2] - cam.cam_pos[2]});
-    const int nb = num_sh_bases(cam.degree);
     float col[3];
-    sh_eval(cam.degrees_to_use, dir, fdc + 3 * (size_t)i, frest + (size_t)(nb - 1) * 3 * i, col);
+    const float *fr_row = K3 <= 45 ? s_fr + threadIdx.x * K3 : frest + (size_t)K3 * i;
+    sh_eval(cam.degrees_to_use, dir, fdc + 3 * (size_t)i, fr_row, col);
     const float opa = ms_sigmoid(opac[i]);
 
     radii[i] = (int)radius;
@@ -98,14 +112,25 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
     ro[1] = make_float4(T1.y, T1.z, T2.x, T2.y);
     ro[2] = make_float4(T2.z, cxp, cyp, opa);
     ro[3] = make_float4(R2.x, R2.y, R2.z, __builtin_fmaxf(col[0] + 0.5f, 0.0f));
-    ro[4] = make_float4(__builtin_fmaxf(col[1] + 0.5f, 0.0f), __builtin_fmaxf(col[2] + 0.5f, 0.0f), 0.f, 0.f);
+    ro[4] = make_float4(__builtin_fmaxf(col[1] + 0.5f, 0.0f), __builtin_fmaxf(col[2] + 0.5f, 0.0f),
+                        splat_reach(opa), 0.f);
     if (colors_raw) {
         colors_raw[3 * (size_t)i] = col[0];
         colors_raw[3 * (size_t)i + 1] = col[1];
         colors_raw[3 * (size_t)i + 2] = col[2];
     }
-    for (int y = y0; y < y1; ++y)
-        for (int x = x0; x < x1; ++x) atomicAdd(&tile_counts[y * cam.tiles_x + x], 1);
+    }
+    // per-tile histogram (count pass of count -> scan -> scatter)
+    const int rw = ok ? x1 - x0 : 1;
+    const int area = ok ? (x1 - x0) * (y1 - y0) : 0;
+    const int tx = cam.tiles_x;
+    wave_expand(area, [&](int owner, int k, bool active) {
+        const int ow = __shfl(rw, owner, 64), ox = __shfl(x0, owner, 64), oy = __shfl(y0, owner, 64);
+        if (active) {
+            const int ty = k / ow;
+            atomicAdd(&tile_counts[(oy + ty) * tx + ox + (k - ty * ow)], 1);
+        }
+    });
 }
 
 // One Adam step on one element: fused_adam_kernel (msplat_metal.metal:1383-1406).
@@ -126,9 +151,14 @@ struct AdamDev {
 };
 
 // project_and_sh_backward_2dgs_kernel (msplat_metal.metal:2003-2209).
-// FUSED: the per-gaussian gradients stay in registers and the six Adam
-// groups (model.cpp:806-826) are updated in place, so neither the 58-float
-// gradient nor a second pass over the parameters touches HBM.
+// FUSED: the per-gaussian gradients stay on chip and the six Adam groups
+// (model.cpp:806-826) are updated in place, so neither the 58-float gradient
+// nor a second pass over the parameters touches HBM.
+// The 45-float features_rest rows (parameters, both Adam moments, the SH
+// gradient) dominate the traffic; they are moved with coalesced
+// element-per-thread loops: the block's rows are staged in LDS for the
+// view-direction gradient, and the SH gradient basis[b] * v_color[c] is
+// formed per element from per-splat (basis, v_color) kept in LDS.
 template <bool FUSED>
 __global__ __launch_bounds__(kBlock) void k_project_bwd(
     MsplatCamera cam, int n, float *__restrict__ means, float *__restrict__ scales,
@@ -138,22 +168,35 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
     float *__restrict__ dmean2d, float *__restrict__ dfdc, float *__restrict__ dfrest,
     float *__restrict__ grad_norm, float *__restrict__ vis, float *__restrict__ max2d, float inv_max_dim,
     AdamDev ad) {
-    const int i = blockIdx.x * kBlock + threadIdx.x;
-    if (i >= n) return;
+    __shared__ float s_fr[kBlock * 45];
+    __shared__ float s_basis[kBlock * 24];
+    __shared__ float s_vc[kBlock * 3];
     const int nb = num_sh_bases(cam.degree);
     const int K3 = (nb - 1) * 3;
-    const size_t si = (size_t)i;
+    const int b0 = blockIdx.x * kBlock;
+    const int cnt = min(kBlock, n - b0);
+    const bool staged = K3 <= 45;
+    const int sh_deg = cam.degrees_to_use;
+    if (staged && sh_deg > 0) {
+        const float *src = frest + (size_t)b0 * K3;
+        for (int e = threadIdx.x; e < cnt * K3; e += kBlock) s_fr[e] = src[e];
+        __syncthreads();
+    }
+    const int i = b0 + threadIdx.x;
+    const bool valid = i < n;
+    const size_t si = (size_t)(valid ? i : 0);
 
     float gm[3] = {0.f, 0.f, 0.f}, gs[2] = {0.f, 0.f}, gq[4] = {0.f, 0.f, 0.f, 0.f};
     float gdc[3] = {0.f, 0.f, 0.f}, gm2[2] = {0.f, 0.f};
     float vc[3] = {0.f, 0.f, 0.f};
     float basis[24];
-    const bool vis_ok = radii[i] > 0;
-    int sh_deg = 0;
+#pragma unroll
+    for (int k = 0; k < 24; ++k) basis[k] = 0.f;
+    const bool vis_ok = valid && radii[si] > 0;
     if (vis_ok) {
         const float p[3] = {means[3 * si], means[3 * si + 1], means[3 * si + 2]};
         const float sx = ms_expf(scales[2 * si]), sy = ms_expf(scales[2 * si + 1]);
-        const float4 qv = reinterpret_cast<const float4 *>(quats)[i];
+        const float4 qv = reinterpret_cast<const float4 *>(quats)[si];
         const float q[4] = {qv.x, qv.y, qv.z, qv.w};
         f3 R0, R1, R2;
         quat_to_rotmat(q, R0, R1, R2);
@@ -198,12 +241,12 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
         vc[0] = g[13];
         vc[1] = g[14];
         vc[2] = g[15];
-        sh_deg = cam.degrees_to_use;
 #pragma unroll
         for (int c = 0; c < 3; ++c) gdc[c] = SH_C0 * vc[c];
         sh_vjp_basis(sh_deg, dir, basis);
         if (sh_deg >= 1) {
-            const f3 dd = sh_dL_ddir(sh_deg, dir, frest + (size_t)K3 * si, vc);
+            const float *fr_row = staged ? s_fr + threadIdx.x * K3 : frest + (size_t)K3 * si;
+            const f3 dd = sh_dL_ddir(sh_deg, dir, fr_row, vc);
             const f3 dm = dnormvdv(dir_un, dd);
             gm[0] += dm.x;
             gm[1] += dm.y;
@@ -212,36 +255,50 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
         const float depth_fwd = cc.pc[3];
         gm2[0] = g[6] * depth_fwd * 0.5f * W;
         gm2[1] = g[7] * depth_fwd * 0.5f * H;
-        grad_norm[i] += __builtin_fabsf(gm2[0]) + __builtin_fabsf(gm2[1]);
-        vis[i] += 1.0f;
-        const float r_norm = (float)radii[i] * inv_max_dim;
-        if (r_norm > max2d[i]) max2d[i] = r_norm;
+        grad_norm[si] += __builtin_fabsf(gm2[0]) + __builtin_fabsf(gm2[1]);
+        vis[si] += 1.0f;
+        const float r_norm = (float)radii[si] * inv_max_dim;
+        if (r_norm > max2d[si]) max2d[si] = r_norm;
     }
     const int nrest = sh_deg >= 4 ? 24 : sh_deg == 3 ? 15 : sh_deg == 2 ? 8 : sh_deg == 1 ? 3 : 0;
     // dL_dopacity is read for every splat, as the reference's Adam reads the
     // raster's opacity-gradient buffer (zero for culled splats).
-    const float gop = g16[16 * si + 12];
-    if (!FUSED) {
-        for (int k = 0; k < 3; ++k) dmeans[3 * si + k] = gm[k];
-        for (int k = 0; k < 2; ++k) dscales[2 * si + k] = gs[k];
-        for (int k = 0; k < 4; ++k) dquats[4 * si + k] = gq[k];
-        for (int k = 0; k < 2; ++k) dmean2d[2 * si + k] = gm2[k];
-        for (int k = 0; k < 3; ++k) dfdc[3 * si + k] = gdc[k];
-        for (int k = 0; k < K3; ++k) {
-            const int b = k / 3, c = k - 3 * b;
-            dfrest[(size_t)K3 * si + k] = (b < nrest) ? basis[b] * vc[c] : 0.f;
+    const float gop = valid ? g16[16 * si + 12] : 0.f;
+    if (valid) {
+        if (!FUSED) {
+            for (int k = 0; k < 3; ++k) dmeans[3 * si + k] = gm[k];
+            for (int k = 0; k < 2; ++k) dscales[2 * si + k] = gs[k];
+            for (int k = 0; k < 4; ++k) dquats[4 * si + k] = gq[k];
+            for (int k = 0; k < 2; ++k) dmean2d[2 * si + k] = gm2[k];
+            for (int k = 0; k < 3; ++k) dfdc[3 * si + k] = gdc[k];
+        } else {
+            for (int k = 0; k < 3; ++k)
+                adam_elem(means, ad.m[0], ad.v[0], 3 * si + k, gm[k], ad.step[0], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+            for (int k = 0; k < 2; ++k)
+                adam_elem(scales, ad.m[1], ad.v[1], 2 * si + k, gs[k], ad.step[1], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+            for (int k = 0; k < 4; ++k)
+                adam_elem(quats, ad.m[2], ad.v[2], 4 * si + k, gq[k], ad.step[2], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+            for (int k = 0; k < 3; ++k)
+                adam_elem(fdc, ad.m[3], ad.v[3], 3 * si + k, gdc[k], ad.step[3], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+            adam_elem(opac, ad.m[5], ad.v[5], si, gop, ad.step[5], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
         }
-    } else {
-        for (int k = 0; k < 3; ++k) adam_elem(means, ad.m[0], ad.v[0], 3 * si + k, gm[k], ad.step[0], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
-        for (int k = 0; k < 2; ++k) adam_elem(scales, ad.m[1], ad.v[1], 2 * si + k, gs[k], ad.step[1], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
-        for (int k = 0; k < 4; ++k) adam_elem(quats, ad.m[2], ad.v[2], 4 * si + k, gq[k], ad.step[2], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
-        for (int k = 0; k < 3; ++k) adam_elem(fdc, ad.m[3], ad.v[3], 3 * si + k, gdc[k], ad.step[3], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
-        for (int k = 0; k < K3; ++k) {
-            const int b = k / 3, c = k - 3 * b;
-            const float gr = (b < nrest) ? basis[b] * vc[c] : 0.f;
-            adam_elem(frest, ad.m[4], ad.v[4], (size_t)K3 * si + k, gr, ad.step[4], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
-        }
-        adam_elem(opac, ad.m[5], ad.v[5], si, gop, ad.step[5], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+    }
+    if (K3 == 0) return;
+    // features_rest: gradient basis[b] * v_color[c] (sh_coeffs_to_color_vjp,
+    // msplat_metal.metal:825-912; zero above degrees_to_use and for culled
+    // splats), written or Adam-updated element by element, coalesced.
+    for (int k = 0; k < 24; ++k) s_basis[threadIdx.x * 24 + k] = (k < nrest) ? basis[k] : 0.f;
+    for (int c = 0; c < 3; ++c) s_vc[threadIdx.x * 3 + c] = vc[c];
+    __syncthreads();
+    const size_t base = (size_t)b0 * K3;
+    for (int e = threadIdx.x; e < cnt * K3; e += kBlock) {
+        const int gl = e / K3, k = e - gl * K3;
+        const int b = k / 3, c = k - 3 * b;
+        const float gr = (b < nrest) ? s_basis[gl * 24 + b] * s_vc[gl * 3 + c] : 0.f;
+        if (!FUSED)
+            dfrest[base + e] = gr;
+        else
+            adam_elem(frest, ad.m[4], ad.v[4], base + e, gr, ad.step[4], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
     }
 }
 

@@ -5,7 +5,10 @@
 // tile (the reference runs four 8x8 threadgroups per tile, each reloading
 // the list, msplat_metal.metal:8-10, 576-586).  Records are staged in LDS in
 // structure-of-arrays float4 planes so the cooperative load is bank-conflict
-// free and the per-pixel loop reads a broadcast.
+// free and the per-pixel loop reads a broadcast.  At load time each splat
+// also gets a 4-bit mask of the wave strips (16x4 pixels) its alpha >= 1/255
+// region can reach; a wave skips splats outside its strip with one uniform
+// test.
 #include "kernels.h"
 #include "ms_device.h"
 
@@ -15,6 +18,18 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr float kMScale = FAR_N / (FAR_N - NEAR_N);
+
+__device__ __forceinline__ void load_batch(const float4 *__restrict__ rec, int gid, float4 *s_rec, int *s_mask,
+                                           float sx0, float sy0) {
+    const float4 *r = rec + 5 * (size_t)gid;
+    float4 q[5];
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+        q[k] = r[k];
+        s_rec[k * kThreads + threadIdx.x] = q[k];
+    }
+    s_mask[threadIdx.x] = strip_mask(splat_box(q[0], q[1], q[2], q[4].z), sx0, sy0);
+}
 
 // nd_rasterize_forward_2dgs_kernel (msplat_metal.metal:553-754).
 __global__ __launch_bounds__(kThreads) void k_raster_fwd(
@@ -26,10 +41,13 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     const int tile = xcd_tile(blockIdx.x, T);
     if (tile >= T) return;
     __shared__ float4 s_rec[5 * kThreads];
+    __shared__ int s_mask[kThreads];
     const int tx = tile % tiles_x, ty = tile / tiles_x;
+    const int wave = threadIdx.x >> 6;
     const int pxi = tx * 16 + (threadIdx.x & 15), pyi = ty * 16 + (threadIdx.x >> 4);
     const bool inside = pxi < W && pyi < H;
     const float px = (float)pxi, py = (float)pyi;
+    const float sx0 = (float)(tx * 16), sy0 = (float)(ty * 16);
     const int start = offsets[tile], end = offsets[tile + 1];
     const float bg0 = bgp[0], bg1 = bgp[1], bg2 = bgp[2];
 
@@ -41,16 +59,13 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     for (int b0 = start; b0 < end; b0 += kThreads) {
         if (__syncthreads_and(done)) break;
         const int idx = b0 + (int)threadIdx.x;
-        if (idx < end) {
-            const float4 *r = rec + 5 * (size_t)ids[idx];
-#pragma unroll
-            for (int k = 0; k < 5; ++k) s_rec[k * kThreads + threadIdx.x] = r[k];
-        }
+        if (idx < end) load_batch(rec, ids[idx], s_rec, s_mask, sx0, sy0);
         __syncthreads();
-        if (done) continue;
         const int bs = min(kThreads, end - b0);
+        if (done) continue;
         for (int t = 0; t < bs; ++t) {
             ++contrib;
+            if (!((s_mask[t] >> wave) & 1)) continue;
             const float4 q0 = s_rec[t], q1 = s_rec[kThreads + t], q2 = s_rec[2 * kThreads + t];
             PairEval e;
             if (!eval_pair(px, py, q0, q1, q2, e)) continue;
@@ -154,10 +169,16 @@ __device__ __forceinline__ float wave_reduce16(float v[16], int lane) {
 
 // nd_rasterize_backward_2dgs_kernel (msplat_metal.metal:1705-1979).
 // Back-to-front replay starting at the tile's largest last_contributor (the
-// reference starts at the end of the full list).  Per-splat gradients
+// reference starts at the end of the full list).  The skip decisions reuse
+// the forward's exact arithmetic (eval_pair); quantities that only scale
+// gradients use hardware reciprocals.  Per-splat gradients
 // [dL_dtransMat 9, dL_dnormal3D 3, dL_dopacity 1, dL_dcolors 3] are reduced
 // across the wave, then across the four waves in LDS, and flushed with one
-// global float atomic per (tile, splat, float).
+// global float atomic per (tile, splat, component).
+// FULL = false is the training step's case: the only upstream gradient is
+// dL/dimage (depth, alpha, normal, median-depth and distortion gradients are
+// zero), so those terms are compiled out.
+template <bool FULL>
 __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     int W, int H, int tiles_x, int T, const int *__restrict__ offsets, const int *__restrict__ ids,
     const float4 *__restrict__ rec, const float *__restrict__ bgp, const float *__restrict__ final_Ts,
@@ -168,14 +189,16 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     const int tile = xcd_tile(blockIdx.x, T);
     if (tile >= T) return;
     __shared__ float4 s_rec[5 * kThreads];
+    __shared__ int s_mask[kThreads];
     __shared__ int s_id[kThreads];
     __shared__ float s_acc[kThreads * 16];
     __shared__ int s_maxlast;
-    const int lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int pxi = tx * 16 + (threadIdx.x & 15), pyi = ty * 16 + (threadIdx.x >> 4);
     const bool inside = pxi < W && pyi < H;
     const float px = (float)pxi, py = (float)pyi;
+    const float sx0 = (float)(tx * 16), sy0 = (float)(ty * 16);
     const int start = offsets[tile];
     const size_t pix = inside ? (size_t)pyi * W + pxi : 0;
 
@@ -185,22 +208,24 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     float ddepth = 0.f, daccum = 0.f, dmed = 0.f, dreg = 0.f;
     if (inside) {
         T_final = final_Ts[3 * pix];
-        final_D = final_Ts[3 * pix + 1];
-        final_D2 = final_Ts[3 * pix + 2];
         my_last = final_idx[2 * pix];
-        med_c = final_idx[2 * pix + 1];
         dpix[0] = dL_dimg[3 * pix];
         dpix[1] = dL_dimg[3 * pix + 1];
         dpix[2] = dL_dimg[3 * pix + 2];
-        if (dL_ddepth) ddepth = dL_ddepth[pix];
-        if (dL_daccum) daccum = dL_daccum[pix];
-        if (dL_dnormal) {
-            dn2[0] = dL_dnormal[3 * pix];
-            dn2[1] = dL_dnormal[3 * pix + 1];
-            dn2[2] = dL_dnormal[3 * pix + 2];
+        if (FULL) {
+            final_D = final_Ts[3 * pix + 1];
+            final_D2 = final_Ts[3 * pix + 2];
+            med_c = final_idx[2 * pix + 1];
+            if (dL_ddepth) ddepth = dL_ddepth[pix];
+            if (dL_daccum) daccum = dL_daccum[pix];
+            if (dL_dnormal) {
+                dn2[0] = dL_dnormal[3 * pix];
+                dn2[1] = dL_dnormal[3 * pix + 1];
+                dn2[2] = dL_dnormal[3 * pix + 2];
+            }
+            if (dL_dmedian) dmed = dL_dmedian[pix];
+            dreg = dL_ddist ? dL_ddist[pix] : ddist_uniform;
         }
-        if (dL_dmedian) dmed = dL_dmedian[pix];
-        dreg = dL_ddist ? dL_ddist[pix] : ddist_uniform;
     }
     const float final_A = 1.0f - T_final;
     const float bg_dot = bgp[0] * dpix[0] + bgp[1] * dpix[1] + bgp[2] * dpix[2];
@@ -223,13 +248,12 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
         if ((int)threadIdx.x < bs) {
             const int gid = ids[start + hi - 1 - (int)threadIdx.x];
             s_id[threadIdx.x] = gid;
-            const float4 *r = rec + 5 * (size_t)gid;
-#pragma unroll
-            for (int k = 0; k < 5; ++k) s_rec[k * kThreads + threadIdx.x] = r[k];
+            load_batch(rec, gid, s_rec, s_mask, sx0, sy0);
         }
         for (int k = threadIdx.x; k < bs * 16; k += kThreads) s_acc[k] = 0.f;
         __syncthreads();
         for (int t = 0; t < bs; ++t) {
+            if (!((s_mask[t] >> wave) & 1)) continue;
             const int c = hi - 1 - t;
             float v[16];
 #pragma unroll
@@ -242,8 +266,9 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                     has = true;
                     const float4 q3 = s_rec[3 * kThreads + t], q4 = s_rec[4 * kThreads + t];
                     const float alpha = e.alpha, G = e.G, opa = q2.w;
-                    Tr = Tr / (1.0f - alpha);
-                    const float dchannel = alpha * Tr;
+                    const float inv_1ma = __builtin_amdgcn_rcpf(1.0f - alpha);
+                    Tr = Tr * inv_1ma;
+                    const float aT = alpha * Tr;
                     float dL_dalpha = 0.0f;
                     const float cu[3] = {q3.w, q4.x, q4.y};
 #pragma unroll
@@ -252,41 +277,45 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                         accum_rec[ch] = last_alpha * last_color[ch] + (1.f - last_alpha) * accum_rec[ch];
                         last_color[ch] = cu[ch];
                         dL_dalpha += (cu[ch] - accum_rec[ch]) * dpix[ch];
-                        v[13 + ch] = dchannel * dpix[ch] * mask;
+                        v[13 + ch] = aT * dpix[ch] * mask;
                     }
-                    float dL_dz = 0.0f, dL_dweight = 0.0f;
-                    const float m_d = kMScale * (1.0f - NEAR_N / e.depth);
-                    const float dmd_dd = (FAR_N * NEAR_N) / ((FAR_N - NEAR_N) * e.depth * e.depth);
-                    if (c == med_c - 1) dL_dz += dmed;
-                    dL_dweight += (final_D2 + m_d * m_d * final_A - 2.0f * m_d * final_D) * dreg;
-                    dL_dalpha += dL_dweight - last_dL_dT;
-                    last_dL_dT = dL_dweight * alpha + (1.0f - alpha) * last_dL_dT;
-                    const float dL_dmd = 2.0f * (Tr * alpha) * (m_d * final_A - final_D) * dreg;
-                    dL_dz += dL_dmd * dmd_dd;
-                    accum_depth_rec = last_alpha * last_depth + (1.f - last_alpha) * accum_depth_rec;
-                    last_depth = e.depth;
-                    dL_dalpha += (e.depth - accum_depth_rec) * ddepth;
-                    accum_alpha_rec = last_alpha * 1.0f + (1.f - last_alpha) * accum_alpha_rec;
-                    dL_dalpha += (1.0f - accum_alpha_rec) * daccum;
-                    const float nrm[3] = {q3.x, q3.y, q3.z};
+                    float dL_dz = 0.0f;
+                    if (FULL) {
+                        float dL_dweight = 0.0f;
+                        const float inv_d = __builtin_amdgcn_rcpf(e.depth);
+                        const float m_d = kMScale * (1.0f - NEAR_N * inv_d);
+                        const float dmd_dd = (FAR_N * NEAR_N) / (FAR_N - NEAR_N) * inv_d * inv_d;
+                        if (c == med_c - 1) dL_dz += dmed;
+                        dL_dweight += (final_D2 + m_d * m_d * final_A - 2.0f * m_d * final_D) * dreg;
+                        dL_dalpha += dL_dweight - last_dL_dT;
+                        last_dL_dT = dL_dweight * alpha + (1.0f - alpha) * last_dL_dT;
+                        const float dL_dmd = 2.0f * aT * (m_d * final_A - final_D) * dreg;
+                        dL_dz += dL_dmd * dmd_dd;
+                        accum_depth_rec = last_alpha * last_depth + (1.f - last_alpha) * accum_depth_rec;
+                        last_depth = e.depth;
+                        dL_dalpha += (e.depth - accum_depth_rec) * ddepth;
+                        accum_alpha_rec = last_alpha * 1.0f + (1.f - last_alpha) * accum_alpha_rec;
+                        dL_dalpha += (1.0f - accum_alpha_rec) * daccum;
+                        const float nrm[3] = {q3.x, q3.y, q3.z};
 #pragma unroll
-                    for (int ch = 0; ch < 3; ++ch) {
-                        accum_normal_rec[ch] =
-                            last_alpha * last_normal[ch] + (1.f - last_alpha) * accum_normal_rec[ch];
-                        last_normal[ch] = nrm[ch];
-                        dL_dalpha += (nrm[ch] - accum_normal_rec[ch]) * dn2[ch];
-                        v[9 + ch] = alpha * Tr * dn2[ch];
+                        for (int ch = 0; ch < 3; ++ch) {
+                            accum_normal_rec[ch] =
+                                last_alpha * last_normal[ch] + (1.f - last_alpha) * accum_normal_rec[ch];
+                            last_normal[ch] = nrm[ch];
+                            dL_dalpha += (nrm[ch] - accum_normal_rec[ch]) * dn2[ch];
+                            v[9 + ch] = aT * dn2[ch];
+                        }
+                        dL_dz += aT * ddepth;
                     }
                     dL_dalpha *= Tr;
                     last_alpha = alpha;
-                    dL_dalpha += (-T_final / (1.f - alpha)) * bg_dot;
+                    dL_dalpha += (-T_final * inv_1ma) * bg_dot;
                     const float dL_dG = opa * dL_dalpha;
-                    dL_dz += alpha * Tr * ddepth;
                     const float Twx = q1.z, Twy = q1.w;
                     if (e.rho3d <= e.rho2d) {
                         const float dsx = dL_dG * -G * e.u + dL_dz * Twx;
                         const float dsy = dL_dG * -G * e.v + dL_dz * Twy;
-                        const float dsx_pz = dsx / e.ray.z, dsy_pz = dsy / e.ray.z;
+                        const float dsx_pz = dsx * e.inv_z, dsy_pz = dsy * e.inv_z;
                         const f3 dp = {dsx_pz, dsy_pz, -(dsx_pz * e.u + dsy_pz * e.v)};
                         const f3 &k = e.k, &l = e.l;
                         const f3 dk = {l.y * dp.z - l.z * dp.y, l.z * dp.x - l.x * dp.z, l.x * dp.y - l.y * dp.x};
@@ -299,14 +328,13 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                         v[5] = -dl.z;
                         v[6] = px * dk.x + py * dl.x + dL_dz * e.u;
                         v[7] = px * dk.y + py * dl.y + dL_dz * e.v;
-                        v[8] = px * dk.z + py * dl.z + dL_dz * 1.0f;
-                    } else {
+                        v[8] = px * dk.z + py * dl.z + dL_dz;
+                    } else if (FULL) {
                         v[6] = e.u * dL_dz;
                         v[7] = e.v * dL_dz;
                         v[8] = dL_dz;
                     }
-                    const float dsig = opa * (1.0f - opa);
-                    v[12] = G * dL_dalpha * dsig;
+                    v[12] = G * dL_dalpha * (opa * (1.0f - opa));
                 }
             }
             if (__any(has)) {
@@ -337,8 +365,8 @@ void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
     const int T = tiles_x * tiles_y;
     const int grid = ((T + 7) / 8) * 8;
     hipLaunchKernelGGL(k_raster_fwd, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
-                       reinterpret_cast<const float4 *>(rec), bg, out_img, final_Ts, final_idx,
-                       out_depth, out_normal, out_alpha, out_median, out_dist, pair_counter);
+                       reinterpret_cast<const float4 *>(rec), bg, out_img, final_Ts, final_idx, out_depth,
+                       out_normal, out_alpha, out_median, out_dist, pair_counter);
 }
 
 void launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
@@ -348,9 +376,15 @@ void launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
                        float ddist_uniform, float *grads16) {
     const int T = tiles_x * tiles_y;
     const int grid = ((T + 7) / 8) * 8;
-    hipLaunchKernelGGL(k_raster_bwd, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
-                       reinterpret_cast<const float4 *>(rec), bg, final_Ts, final_idx, dL_dimg,
-                       dL_ddepth, dL_daccum, dL_dnormal, dL_dmedian, dL_ddist, ddist_uniform, grads16);
+    const bool full = dL_ddepth || dL_daccum || dL_dnormal || dL_dmedian || dL_ddist || ddist_uniform != 0.0f;
+    if (full)
+        hipLaunchKernelGGL(k_raster_bwd<true>, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
+                           reinterpret_cast<const float4 *>(rec), bg, final_Ts, final_idx, dL_dimg, dL_ddepth,
+                           dL_daccum, dL_dnormal, dL_dmedian, dL_ddist, ddist_uniform, grads16);
+    else
+        hipLaunchKernelGGL(k_raster_bwd<false>, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
+                           reinterpret_cast<const float4 *>(rec), bg, final_Ts, final_idx, dL_dimg, dL_ddepth,
+                           dL_daccum, dL_dnormal, dL_dmedian, dL_ddist, ddist_uniform, grads16);
 }
 
 }  // namespace mskern

@@ -76,6 +76,28 @@ __device__ __forceinline__ float ms_expf(float x) {
 
 __device__ __forceinline__ float ms_sigmoid(float x) { return 1.0f / (1.0f + ms_expf(-x)); }
 
+// ms_expf for x <= 0 (or NaN), bit-identical to it wherever the result is at
+// least 2^-126 (x >= -87; for x in [-87, 0] the one-step scaling p * 2^k is
+// the same single rounding as the two-step one).  Below -87 it returns about
+// 1e-38 instead of the exact tiny value; the rasterizer only compares
+// opacity * G against 1/255 there, so every decision and output is unchanged.
+__device__ __forceinline__ float ms_expf_nonpos(float x) {
+    x = (x < -87.0f) ? -87.0f : x;  // NaN passes through
+    const float z = __builtin_rintf(x * 1.44269504088896341f);
+    float r = __builtin_fmaf(z, -0.693359375f, x);
+    r = __builtin_fmaf(z, 2.12194440e-4f, r);
+    const float r2 = r * r;
+    float p = 1.9875691500E-4f;
+    p = __builtin_fmaf(p, r, 1.3981999507E-3f);
+    p = __builtin_fmaf(p, r, 8.3334519073E-3f);
+    p = __builtin_fmaf(p, r, 4.1665795894E-2f);
+    p = __builtin_fmaf(p, r, 1.6666665459E-1f);
+    p = __builtin_fmaf(p, r, 5.0000001201E-1f);
+    p = __builtin_fmaf(p, r2, r);
+    p = p + 1.0f;
+    return p * __int_as_float(((int)z + 127) << 23);
+}
+
 // Saturating truncation (the tile-rectangle (int) casts of get_bbox,
 // msplat_metal.metal:70-73, are undefined outside the int range).
 __device__ __forceinline__ int f2i(float x) {
@@ -260,11 +282,56 @@ __device__ __forceinline__ f3 dnormvdv(f3 v, f3 dv) {
 
 // Splat record (MSPLAT_REC_FLOATS = 20 floats, five float4):
 //   q0 = (Tu.x Tu.y Tu.z Tv.x)   q1 = (Tv.y Tv.z Tw.x Tw.y)
-//   q2 = (Tw.z xy.x xy.y opacity) q3 = (n.x n.y n.z r)   q4 = (g b 0 0)
-// with opacity = sigmoid(logit) and rgb = max(raw SH + 0.5, 0).
+//   q2 = (Tw.z xy.x xy.y opacity) q3 = (n.x n.y n.z r)   q4 = (g b tau 0)
+// with opacity = sigmoid(logit), rgb = max(raw SH + 0.5, 0) and tau the
+// reach of the splat: alpha >= 1/255 needs min(rho3d, rho2d) <= tau.
 struct Rec {
     float4 q0, q1, q2, q3, q4;
 };
+
+// tau = 2 ln(255 opacity) with a margin that covers the rounding of rho, exp
+// and the alpha product; -1 when the splat can never reach alpha >= 1/255
+// (opacity * G <= opacity and G <= 1).
+__device__ __forceinline__ float splat_reach(float opa) {
+    const float a = 255.0f * opa;
+    if (!(a >= 0.999f)) return -1.0f;
+    const float t = __builtin_fmaxf(2.0f * __logf(a), 0.0f);
+    return t * 1.0001f + 1e-3f;
+}
+
+// Conservative screen box (xmin, xmax, ymin, ymax) of the pixels where a
+// splat can reach alpha >= 1/255: the union of the low-pass disc
+// rho2d <= tau and the image of the splat-plane disc u^2+v^2 <= tau, whose
+// bounding box follows compute_aabb_2dgs (msplat_metal.metal:302-330) with
+// cutoff sqrt(tau).  When that disc is not entirely in front of the camera
+// (d >= 0) or the bound degenerates, the box is unbounded.
+__device__ __forceinline__ float4 splat_box(const float4 &q0, const float4 &q1, const float4 &q2, float tau) {
+    const float inf = __builtin_inff();
+    if (!(tau >= 0.0f)) return make_float4(inf, -inf, inf, -inf);
+    const f3 T0 = {q0.x, q0.y, q0.z}, T1 = {q0.w, q1.x, q1.y}, T2 = {q1.z, q1.w, q2.x};
+    const float r2 = __builtin_sqrtf(0.5f * tau);
+    float x0 = q2.y - r2, x1 = q2.y + r2, y0 = q2.z - r2, y1 = q2.z + r2;
+    const float d = tau * (T2.x * T2.x + T2.y * T2.y) - T2.z * T2.z;
+    bool bounded = d < 0.0f;
+    if (bounded) {
+        const float inv = 1.0f / d;
+        const f3 f = {tau * inv, tau * inv, -inv};
+        const float cx = dot3(f, mul3(T0, T2)), cy = dot3(f, mul3(T1, T2));
+        const float hx2 = cx * cx - dot3(f, mul3(T0, T0)), hy2 = cy * cy - dot3(f, mul3(T1, T1));
+        bounded = hx2 >= 0.0f && hy2 >= 0.0f && cx == cx && cy == cy;
+        if (bounded) {
+            const float hx = __builtin_sqrtf(hx2), hy = __builtin_sqrtf(hy2);
+            x0 = __builtin_fminf(x0, cx - hx);
+            x1 = __builtin_fmaxf(x1, cx + hx);
+            y0 = __builtin_fminf(y0, cy - hy);
+            y1 = __builtin_fmaxf(y1, cy + hy);
+        }
+    }
+    if (!bounded) return make_float4(-inf, inf, -inf, inf);
+    const float mx = 1.0f + 1e-3f * (__builtin_fabsf(x0) + __builtin_fabsf(x1));
+    const float my = 1.0f + 1e-3f * (__builtin_fabsf(y0) + __builtin_fabsf(y1));
+    return make_float4(x0 - mx, x1 + mx, y0 - my, y1 + my);
+}
 
 // One (pixel, splat) evaluation: the ray-splat intersection, low-pass
 // filter and alpha of nd_rasterize_forward_2dgs_kernel
@@ -272,7 +339,7 @@ struct Rec {
 // backward so both take identical skip decisions.
 struct PairEval {
     f3 k, l, ray;
-    float u, v, rho3d, rho2d, depth, G, alpha;
+    float inv_z, u, v, rho3d, rho2d, depth, G, alpha;
 };
 
 __device__ __forceinline__ bool eval_pair(float px, float py, const float4 &q0, const float4 &q1,
@@ -285,9 +352,9 @@ __device__ __forceinline__ bool eval_pair(float px, float py, const float4 &q0, 
     e.ray = {__builtin_fmaf(e.k.y, e.l.z, -(e.k.z * e.l.y)), __builtin_fmaf(e.k.z, e.l.x, -(e.k.x * e.l.z)),
              __builtin_fmaf(e.k.x, e.l.y, -(e.k.y * e.l.x))};
     if (e.ray.z == 0.0f) return false;
-    const float inv_z = 1.0f / e.ray.z;
-    e.u = e.ray.x * inv_z;
-    e.v = e.ray.y * inv_z;
+    e.inv_z = 1.0f / e.ray.z;
+    e.u = e.ray.x * e.inv_z;
+    e.v = e.ray.y * e.inv_z;
     e.rho3d = __builtin_fmaf(e.u, e.u, e.v * e.v);
     const float dxs = q2.y - px, dys = q2.z - py;
     e.rho2d = FILTER_INV_SQ * __builtin_fmaf(dxs, dxs, dys * dys);
@@ -296,10 +363,57 @@ __device__ __forceinline__ bool eval_pair(float px, float py, const float4 &q0, 
     if (e.depth < NEAR_N) return false;
     const float power = -0.5f * rho;
     if (power > 0.0f) return false;
-    e.G = ms_expf(power);
+    e.G = ms_expf_nonpos(power);
     e.alpha = __builtin_fminf(0.99f, q2.w * e.G);
     if (e.alpha < 1.0f / 255.0f) return false;
     return true;
+}
+
+// Bit w (w = 0..3) set when the splat box meets the 16x4 pixel strip of wave
+// w of the tile whose top-left pixel is (sx0, sy0).
+__device__ __forceinline__ int strip_mask(const float4 &b, float sx0, float sy0) {
+    if (b.x > sx0 + 15.0f || b.y < sx0) return 0;
+    int m = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const float y0 = sy0 + 4.0f * w;
+        if (!(b.z > y0 + 3.0f || b.w < y0)) m |= 1 << w;
+    }
+    return m;
+}
+
+// Wave-cooperative enumeration of the tile rectangles held by the 64 lanes
+// of a wave.  Lane L owns `count` tiles (its rectangle area, 0 if none); the
+// wave walks the concatenation of all 64 lists 64 entries at a time, so each
+// lane issues independent per-tile work (no per-lane serial loops whose
+// length differs across lanes).  For entry j the owner is the smallest lane
+// whose inclusive prefix exceeds j (6-step binary search over shuffles).
+// Must be called by all 64 lanes; fn(owner, local_index, active) receives
+// owner-side values through shuffles taken by every lane.
+template <typename F>
+__device__ __forceinline__ void wave_expand(int count, F &&fn) {
+    const int lane = threadIdx.x & 63;
+    int incl = count;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += o;
+    }
+    const int total = __shfl(incl, 63, 64);
+    for (int base = 0; base < total; base += 64) {
+        const int j = base + lane;
+        int lo = 0, hi = 63;
+#pragma unroll
+        for (int s = 0; s < 6; ++s) {
+            const int mid = (lo + hi) >> 1;
+            if (__shfl(incl, mid, 64) <= j)
+                lo = mid + 1;
+            else
+                hi = mid;
+        }
+        const int o_excl = __shfl(incl, lo, 64) - __shfl(count, lo, 64);
+        fn(lo, j - o_excl, j < total);
+    }
 }
 
 // XCD-aware tile order: MI355X dispatches workgroup i to XCD (i mod 8), so

@@ -63,6 +63,7 @@ EXPORTS = [
     "msplat_hip_raster_bwd", "msplat_hip_project_bwd", "msplat_hip_project_bwd_adam", "msplat_hip_last", "msplat_hip_enable_timing",
     "msplat_hip_stage_times", "msplat_hip_last_pairs_evaluated",
 ]
+SYNTH_EXPORTS = ["msplat_synth_uniform", "msplat_synth_normal"]
 
 
 def lib() -> C.CDLL:
@@ -106,6 +107,8 @@ def lib() -> C.CDLL:
         "msplat_hip_enable_timing": (I, [I]),
         "msplat_hip_stage_times": (I, [C.POINTER(C.c_char_p), c_float_p, I]),
         "msplat_hip_last_pairs_evaluated": (I64, []),
+        "msplat_synth_uniform": (None, [C.c_uint64, C.c_uint64, I64, C.c_double, C.c_double, P]),
+        "msplat_synth_normal": (None, [C.c_uint64, C.c_uint64, I64, C.c_double, C.c_double, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

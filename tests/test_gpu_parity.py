@@ -181,6 +181,25 @@ def test_raster_backward_close(name, orc, eng):
     assert np.all(g[proj["radii"] <= 0] == 0)
 
 
+def test_raster_backward_all_upstream_gradients(orc, eng):
+    """The general backward (depth, alpha, normal, median-depth and
+    distortion gradients besides the image's) against the oracle."""
+    scene = S.make_scene(2, n=20_000, width=256, height=160, num_cameras=2)
+    ocam, proj, bins, fwd, ds, gcam, out = _forward_both(scene, 0, orc, eng)
+    H, W = gcam.height, gcam.width
+    rng = S.SplitMix64(12)
+    up = dict(img=rng.normal(H * W * 3, 0, 1e-3).reshape(H, W, 3), depth=rng.normal(H * W, 0, 1e-3).reshape(H, W),
+              alpha=rng.normal(H * W, 0, 1e-3).reshape(H, W), normal=rng.normal(H * W * 3, 0, 1e-3).reshape(H, W, 3),
+              median=rng.normal(H * W, 0, 1e-3).reshape(H, W), dist=rng.normal(H * W, 0, 1e-2).reshape(H, W))
+    g_o = orc.raster_bwd(proj, bins, fwd, ocam, scene.background, up["img"], up["depth"], up["alpha"], up["normal"],
+                         up["median"], up["dist"])
+    dev = {k: _device(v) for k, v in up.items()}
+    g16 = E.DeviceArray.zeros((scene.n, 16))
+    E.check(E.lib().msplat_hip_raster_bwd(dev["img"].ptr, dev["depth"].ptr, dev["alpha"].ptr, dev["normal"].ptr,
+                                          dev["median"].ptr, dev["dist"].ptr, g16.ptr))
+    _grad_close(g16.numpy(), g_o, "grads16 with all upstream gradients")
+
+
 @pytest.mark.parametrize("name", list(SCENES))
 def test_project_backward_bitexact(name, orc, eng):
     scene = SCENES[name]()
