@@ -164,6 +164,10 @@ int msplat_hip_densify(int n, int capacity, float grad_thresh,
                        float *const exp_avg_sq_dev[6],
                        const float *random_samples_dev, int *new_count_host);
 
+/* p[i] = min(p[i], value) on n floats: the opacity reset of Model::afterTrain
+ * (core/src/model.cpp:290-296), a host loop on unified memory there. */
+int msplat_hip_clamp_max(float *p_dev, int64_t n, float value);
+
 /* ---- stage entry points (each one kernel of the step) -------------------- */
 
 /* ssim_* + loss_l1_distortion_2dgs + ssim_backward_* kernels

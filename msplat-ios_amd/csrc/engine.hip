@@ -608,6 +608,19 @@ int msplat_hip_densify(int n, int capacity, float grad_thresh, float size_thresh
     API_END
 }
 
+int msplat_hip_clamp_max(float *p, int64_t n, float value) {
+    API_BEGIN
+    ENSURE_INIT();
+    if (n < 0 || (n > 0 && !p)) {
+        set_err("invalid clamp arguments");
+        return MSPLAT_E_ARG;
+    }
+    mskern::launch_clamp_max(g_eng.stream, p, n, value);
+    HIPC(hipGetLastError());
+    return MSPLAT_OK;
+    API_END
+}
+
 int msplat_hip_loss_fwd_bwd(int W, int H, const float *img, const float *gt, const float *dist, float l1,
                             float ldist, float ldssim, float *dL, double *loss_host, double *ssim_host) {
     API_BEGIN

@@ -22,6 +22,14 @@ __global__ __launch_bounds__(256) void k_adam(float *__restrict__ p, const float
     }
 }
 
+// p[i] = min(p[i], value): the opacity reset of Model::afterTrain
+// (model.cpp:290-296), which the reference runs as a host loop on unified
+// memory.
+__global__ void k_clamp_max(float *__restrict__ p, int64_t n, float value) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        if (p[i] > value) p[i] = value;
+}
+
 // ---- device-wide inclusive scan of int32 (reduce-then-scan) --------------
 constexpr int kScanBlock = 256, kScanItems = 4, kScanTile = kScanBlock * kScanItems;
 
@@ -246,6 +254,12 @@ void launch_adam(hipStream_t s, float *p, const float *g, float *m, float *v, in
     if (n <= 0) return;
     const int64_t blocks = std::min<int64_t>((n + 255) / 256, 65536);
     hipLaunchKernelGGL(k_adam, dim3((unsigned)blocks), dim3(256), 0, s, p, g, m, v, n, step, b1, b2, bc2_sqrt, eps);
+}
+
+void launch_clamp_max(hipStream_t s, float *p, int64_t n, float value) {
+    if (n <= 0) return;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 65536);
+    hipLaunchKernelGGL(k_clamp_max, dim3((unsigned)blocks), dim3(256), 0, s, p, n, value);
 }
 
 int64_t scan_temp_ints(int64_t n) { return (n + kScanTile - 1) / kScanTile + 1; }

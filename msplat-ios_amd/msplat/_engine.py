@@ -59,7 +59,7 @@ EXPORTS = [
     "msplat_hip_prepare_camera", "msplat_hip_init", "msplat_hip_cleanup", "msplat_hip_last_error",
     "msplat_hip_device_name", "msplat_hip_alloc", "msplat_hip_free", "msplat_hip_memset", "msplat_hip_upload",
     "msplat_hip_download", "msplat_hip_copy", "msplat_hip_commit", "msplat_hip_sync", "msplat_hip_train_step",
-    "msplat_hip_render", "msplat_hip_fused_adam", "msplat_hip_densify", "msplat_hip_loss_fwd_bwd",
+    "msplat_hip_render", "msplat_hip_fused_adam", "msplat_hip_densify", "msplat_hip_clamp_max", "msplat_hip_loss_fwd_bwd",
     "msplat_hip_raster_bwd", "msplat_hip_project_bwd", "msplat_hip_project_bwd_adam", "msplat_hip_last", "msplat_hip_enable_timing",
     "msplat_hip_stage_times", "msplat_hip_last_pairs_evaluated",
 ]
@@ -97,6 +97,7 @@ def lib() -> C.CDLL:
         "msplat_hip_fused_adam": (I, [P, P, P, P, I64, F, F, F, F, F]),
         "msplat_hip_densify": (I, [I, I, F, F, F, I, F, F, F, I, P, P, P, F, P * 6, I, P * 6, P * 6, P,
                                    C.POINTER(I)]),
+        "msplat_hip_clamp_max": (I, [P, I64, F]),
         "msplat_hip_loss_fwd_bwd": (I, [I, I, P, P, P, F, F, F, P, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
         "msplat_hip_raster_bwd": (I, [P, P, P, P, P, P, P]),
         "msplat_hip_project_bwd": (I, [C.POINTER(MsplatCamera), C.POINTER(MsplatGaussians), P, P, P, P, P, P, P, P,

@@ -88,14 +88,15 @@ def aabb_center(T):
 def composite(px, py, splats, background, near=0.2, far=100.0):
     """Front-to-back compositing of one pixel over `splats` (already in
     depth order): each a dict(T, xy, opac_logit, color_raw, normal).
-    Returns dict of the eight per-pixel outputs and the branch flags."""
+    Returns dict of the per-pixel outputs and `lowpass`, the number of
+    contributing splats that took the screen-space low-pass branch."""
     Tr = 1.0
     col = np.zeros(3)
     dep = 0.0
     nrm = np.zeros(3)
     M1 = M2 = dist = 0.0
     med = 0.0
-    lowpass_used = False
+    lowpass_used = 0
     for s in splats:
         T = s["T"]
         k = T[0] - px * T[2]
@@ -116,7 +117,7 @@ def composite(px, py, splats, background, near=0.2, far=100.0):
             continue
         if Tr * (1.0 - alpha) <= 1e-4:
             break
-        lowpass_used |= rho3 > rho2
+        lowpass_used += int(rho3 > rho2)
         w = alpha * Tr
         m = far / (far - near) * (1.0 - near / depth)
         dist += (m * m * (1.0 - Tr) + M2 - 2.0 * m * M1) * w
