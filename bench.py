@@ -40,8 +40,39 @@ def algorithmic_bytes(stage: str, N: int, I: int, P: int, T: int) -> float:
     }.get(stage, 0.0)
 
 
+def measured_traffic(stage: str, workload: str):
+    """HBM bytes per launch of `stage` on `workload` from the committed
+    rocprofv3 --pmc summaries (FETCH_SIZE + WRITE_SIZE, scaled by the
+    copy-kernel calibration); None when no summary covers it."""
+    for f in sorted((REPO / "profiles").glob("*.md")):
+        for line in f.read_text().splitlines():
+            if line.startswith("bench-traffic:"):
+                rec = json.loads(line.split(":", 1)[1])
+                if rec.get("stage") == stage and rec.get("workload") == workload:
+                    return rec["bytes"]
+    return None
+
+
+def copy_calibration(mib: int) -> int:
+    """A plain device-to-device copy of `mib` MiB, three times: the reference
+    kernel whose FETCH_SIZE / WRITE_SIZE counters calibrate the HBM traffic
+    figures (each launch reads and writes exactly mib MiB)."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n * 4, "launches": 3}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run the copy kernel used to calibrate rocprofv3 byte counters")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
@@ -55,6 +86,8 @@ def main() -> int:
               "multi-GPU runs are not part of this build (see DESIGN.md, 'How the step would shard').",
               file=sys.stderr)
         return 2
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
 
     from msplat import _engine as E
     from msplat import device as D
@@ -78,6 +111,7 @@ def main() -> int:
 
     for k in range(args.warmup):
         D.train_step(ds, cams[k % len(cams)], gts[k % len(cams)])
+    # HIP events on the engine stream bracket every stage of every timed step
     E.enable_timing(True)
     E.sync()
     stage_sum: dict[str, float] = {}
@@ -90,7 +124,6 @@ def main() -> int:
         loss, nis = D.train_step(ds, cams[ci], gts[ci])
         losses.append(loss)
         isect.append(nis)
-        pairs.append(E.pairs_evaluated())
         for name, ms in E.stage_times().items():
             stage_sum[name] = stage_sum.get(name, 0.0) + ms
     E.sync()
@@ -98,6 +131,13 @@ def main() -> int:
     ms_per_step = (t_end - t_start) * 1e3 / args.steps
     print(f"[bench] {args.steps} steps: {ms_per_step:.2f} ms/step, loss {losses[0]:.4f} -> {losses[-1]:.4f}",
           file=sys.stderr, flush=True)
+
+    # two untimed steps with the raster pair counter on (work per kernel)
+    E.enable_timing(False, pairs=True)
+    for k in range(2):
+        ci = (args.warmup + args.steps + k) % len(cams)
+        D.train_step(ds, cams[ci], gts[ci])
+        pairs.append(E.pairs_evaluated())
 
     # render-only frames (the FPS half of the metric)
     E.enable_timing(False)
@@ -110,7 +150,7 @@ def main() -> int:
         E.check(E.lib().msplat_hip_render(E.C.byref(cams[k % len(cams)]), E.C.byref(ds.gaussians),
                                           ds.background.ptr, E.C.byref(n)))
     E.sync()
-    render_ms = (time.perf_counter() - r0) * 1e3 / args.render_frames
+    render_ms = (time.perf_counter() - r0) * 1e3 / max(args.render_frames, 1)
 
     N = scene.n
     I = float(np.mean(isect))
@@ -147,11 +187,11 @@ def main() -> int:
         "config": {"workload": scene.name, "splats": N, "width": W, "height": H, "sh_degree": scene.sh_degree,
                    "tiles": T, "intersections_mean": int(I), "cameras": len(cams),
                    "device": E.device_name()},
-        "render_fps": round(1000.0 / render_ms, 2),
+        "render_fps": round(1000.0 / render_ms, 2) if args.render_frames else None,
         "render_ms": round(render_ms, 3),
         "kernels": kernels,
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": dk["GB_per_s"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": dk["frac_hbm_peak"], "traffic": None},
+                     "unit": "GB/s", "frac": dk["frac_hbm_peak"], "traffic": measured_traffic(dominant, scene.name)},
         "loss_first_last": [round(losses[0], 6), round(losses[-1], 6)],
     }
 

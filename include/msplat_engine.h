@@ -259,13 +259,15 @@ enum {
 int msplat_hip_last(int which, void **ptr_dev, int64_t *numel);
 
 /* Per-kernel timings of the most recent train step / render, in ms, from
- * HIP events recorded on the engine stream when timing is enabled
+ * HIP events recorded on the engine stream when MSPLAT_TIMING_EVENTS is set
  * (the PROFILE_GPU hooks of msplat_metal.mm:20-23).  names receives up to
- * max entries of static strings. */
-int msplat_hip_enable_timing(int enable);
+ * max entries of static strings.  MSPLAT_TIMING_PAIRS additionally counts
+ * the (pixel, gaussian) pairs the forward rasterizer evaluates, which costs
+ * one atomic per wave and tile. */
+enum { MSPLAT_TIMING_EVENTS = 1, MSPLAT_TIMING_PAIRS = 2 };
+int msplat_hip_enable_timing(int flags);
 int msplat_hip_stage_times(const char **names, float *ms, int max);
-/* Raster work counter of the most recent forward: (pixel, gaussian) pairs
- * evaluated (enabled with timing). */
+/* Pair counter of the most recent forward run with MSPLAT_TIMING_PAIRS. */
 int64_t msplat_hip_last_pairs_evaluated(void);
 
 #ifdef __cplusplus

@@ -57,7 +57,8 @@ struct Engine {
     const float *bg = nullptr;
     bool have_grads = false;
     // timing
-    bool timing = false;
+    bool timing = false;       // HIP events per stage
+    bool count_pairs = false;  // raster pair counter
     hipEvent_t ev[ST_COUNT + 1] = {};
     float stage_ms[ST_COUNT] = {};
     bool stage_valid[ST_COUNT] = {};
@@ -220,7 +221,7 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
 
     stage_mark(ST_PROJECT);
     HIPC(hipMemsetAsync(E.counts.p, 0, (size_t)T * 4, s));
-    if (E.timing) HIPC(hipMemsetAsync(E.pair_counter.p, 0, 8, s));
+    if (E.count_pairs) HIPC(hipMemsetAsync(E.pair_counter.p, 0, 8, s));
     mskern::launch_project_fwd(s, *cam, *g, P<float>(E.rec), P<float>(E.depths), P<int>(E.radii),
                                P<uint32_t>(E.rect), P<int>(E.counts), nullptr);
     stage_mark(ST_SCAN);
@@ -247,7 +248,7 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
                               P<float>(E.rec), bg, P<float>(E.out_img), P<float>(E.final_Ts), P<int>(E.final_idx),
                               P<float>(E.out_depth), P<float>(E.out_normal), P<float>(E.out_alpha),
                               P<float>(E.out_median), P<float>(E.out_dist),
-                              E.timing ? P<unsigned long long>(E.pair_counter) : nullptr);
+                              E.count_pairs ? P<unsigned long long>(E.pair_counter) : nullptr);
     HIPC(hipGetLastError());
     return MSPLAT_OK;
 }
@@ -383,7 +384,8 @@ int msplat_hip_device_name(char *buf, int len) {
     ENSURE_INIT();
     hipDeviceProp_t prop;
     HIPC(hipGetDeviceProperties(&prop, g_eng.device));
-    snprintf(buf, (size_t)len, "%s (%s, %d CUs)", prop.name, prop.gcnArchName, prop.multiProcessorCount);
+    snprintf(buf, (size_t)len, "%s (%s, %d CUs, %.0f GiB)", prop.name[0] ? prop.name : "AMD Instinct",
+             prop.gcnArchName, prop.multiProcessorCount, (double)prop.totalGlobalMem / (1ull << 30));
     return MSPLAT_OK;
     API_END
 }
@@ -459,10 +461,9 @@ int msplat_hip_render(const MsplatCamera *cam, const MsplatGaussians *g, const f
     ENSURE_INIT();
     CHECK(forward_locked(cam, g, bg, nisect));
     stage_mark(ST_LOSS);
+    if (g_eng.count_pairs) HIPC(hipMemcpy(&g_eng.pairs, g_eng.pair_counter.p, 8, hipMemcpyDeviceToHost));
     if (g_eng.timing) {
-        HIPC(hipMemcpyAsync(g_eng.pinned_d, g_eng.pair_counter.p, 8, hipMemcpyDeviceToHost, g_eng.stream));
         HIPC(hipStreamSynchronize(g_eng.stream));
-        std::memcpy(&g_eng.pairs, g_eng.pinned_d, 8);
         for (int i = ST_PROJECT; i < ST_LOSS; ++i) {
             HIPC(hipEventElapsedTime(&g_eng.stage_ms[i], g_eng.ev[i], g_eng.ev[i + 1]));
             g_eng.stage_valid[i] = true;
@@ -520,8 +521,8 @@ int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g, con
     HIPC(hipGetLastError());
     HIPC(hipStreamSynchronize(s));
     if (loss_host) *loss_host = (float)E.pinned_d[0];
+    if (E.count_pairs) HIPC(hipMemcpy(&E.pairs, E.pair_counter.p, 8, hipMemcpyDeviceToHost));
     if (E.timing) {
-        HIPC(hipMemcpy(&E.pairs, E.pair_counter.p, 8, hipMemcpyDeviceToHost));
         for (int i = 0; i < ST_COUNT; ++i) {
             HIPC(hipEventElapsedTime(&E.stage_ms[i], E.ev[i], E.ev[i + 1]));
             E.stage_valid[i] = true;
@@ -703,7 +704,8 @@ int msplat_hip_last(int which, void **ptr, int64_t *numel) {
 int msplat_hip_enable_timing(int enable) {
     API_BEGIN
     ENSURE_INIT();
-    g_eng.timing = enable != 0;
+    g_eng.timing = (enable & MSPLAT_TIMING_EVENTS) != 0;
+    g_eng.count_pairs = (enable & MSPLAT_TIMING_PAIRS) != 0;
     return MSPLAT_OK;
     API_END
 }

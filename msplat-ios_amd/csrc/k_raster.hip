@@ -6,9 +6,11 @@
 // the list, msplat_metal.metal:8-10, 576-586).  Records are staged in LDS in
 // structure-of-arrays float4 planes so the cooperative load is bank-conflict
 // free and the per-pixel loop reads a broadcast.  At load time each splat
-// also gets a 4-bit mask of the wave strips (16x4 pixels) its alpha >= 1/255
-// region can reach; a wave skips splats outside its strip with one uniform
-// test.
+// gets a 4-bit mask of the wave strips (16x4 pixels) whose pixel centres its
+// alpha >= 1/255 region can reach (strip_mask_fine), and the batch is
+// compacted into one ascending slot list per wave, so a wave only visits the
+// splats that can touch its strip and every visited splat is a full
+// evaluation.
 #include "kernels.h"
 #include "ms_device.h"
 
@@ -19,8 +21,10 @@ namespace {
 constexpr int kThreads = 256;
 constexpr float kMScale = FAR_N / (FAR_N - NEAR_N);
 
-__device__ __forceinline__ void load_batch(const float4 *__restrict__ rec, int gid, float4 *s_rec, int *s_mask,
-                                           float sx0, float sy0) {
+// Stages the record of splat gid in LDS slot threadIdx.x and returns its
+// wave-strip mask for the tile whose top-left pixel is (sx0, sy0).
+__device__ __forceinline__ int load_batch(const float4 *__restrict__ rec, int gid, float4 *s_rec, float sx0,
+                                          float sy0) {
     const float4 *r = rec + 5 * (size_t)gid;
     float4 q[5];
 #pragma unroll
@@ -28,7 +32,34 @@ __device__ __forceinline__ void load_batch(const float4 *__restrict__ rec, int g
         q[k] = r[k];
         s_rec[k * kThreads + threadIdx.x] = q[k];
     }
-    s_mask[threadIdx.x] = strip_mask(splat_box(q[0], q[1], q[2], q[4].z), sx0, sy0);
+    return strip_mask_fine(q[0], q[1], q[2], q[4].z, sx0, sy0);
+}
+
+// Per-wave slot lists of one batch: s_list[w][0..n_w) holds, in ascending
+// order, the slots whose mask m has bit w.  Returns n for the calling
+// thread's wave.  Called by all threads of the workgroup (two barriers).
+__device__ __forceinline__ int build_wave_lists(int m, unsigned char (*s_list)[kThreads], int (*s_cnt)[4]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    int pos[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const unsigned long long bal = __ballot((m >> w) & 1);
+        pos[w] = __popcll(bal & below);
+        if (lane == 0) s_cnt[wave][w] = __popcll(bal);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        if ((m >> w) & 1) {
+            int off = pos[w];
+            for (int wv = 0; wv < wave; ++wv) off += s_cnt[wv][w];
+            s_list[w][off] = (unsigned char)threadIdx.x;
+        }
+    }
+    const int n = s_cnt[0][wave] + s_cnt[1][wave] + s_cnt[2][wave] + s_cnt[3][wave];
+    __syncthreads();
+    return n;
 }
 
 // nd_rasterize_forward_2dgs_kernel (msplat_metal.metal:553-754).
@@ -41,7 +72,6 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     const int tile = xcd_tile(blockIdx.x, T);
     if (tile >= T) return;
     __shared__ float4 s_rec[5 * kThreads];
-    __shared__ int s_mask[kThreads];
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int wave = threadIdx.x >> 6;
     const int pxi = tx * 16 + (threadIdx.x & 15), pyi = ty * 16 + (threadIdx.x >> 4);
@@ -53,36 +83,40 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
 
     float Tr = 1.f, cr = 0.f, cg = 0.f, cb = 0.f, dep = 0.f, nx = 0.f, ny = 0.f, nz = 0.f;
     float M1 = 0.f, M2 = 0.f, dist = 0.f, med = 0.f;
-    int med_c = -1, contrib = 0, last_c = 0;
+    int med_c = -1, last_c = 0;
     bool done = !inside;
 
+    __shared__ unsigned char s_list[4][kThreads];
+    __shared__ int s_cnt[4][4];
+    int evals = 0;
     for (int b0 = start; b0 < end; b0 += kThreads) {
         if (__syncthreads_and(done)) break;
         const int idx = b0 + (int)threadIdx.x;
-        if (idx < end) load_batch(rec, ids[idx], s_rec, s_mask, sx0, sy0);
-        __syncthreads();
-        const int bs = min(kThreads, end - b0);
+        const int m = idx < end ? load_batch(rec, ids[idx], s_rec, sx0, sy0) : 0;
+        const int n = build_wave_lists(m, s_list, s_cnt);
         if (done) continue;
-        for (int t = 0; t < bs; ++t) {
-            ++contrib;
-            if (!((s_mask[t] >> wave) & 1)) continue;
+        const int base = b0 - start + 1;  // contributor number of slot 0 (1-based)
+        int j = 0;
+        for (; j < n; ++j) {
+            const int t = s_list[wave][j];
             const float4 q0 = s_rec[t], q1 = s_rec[kThreads + t], q2 = s_rec[2 * kThreads + t];
             PairEval e;
             if (!eval_pair(px, py, q0, q1, q2, e)) continue;
             const float next_T = Tr * (1.0f - e.alpha);
             if (next_T <= 1e-4f) {
                 done = true;
+                ++j;
                 break;
             }
             const float w = e.alpha * Tr;
             const float A = 1.f - Tr;
-            const float m = kMScale * (1.f - NEAR_N / e.depth);
-            dist = __builtin_fmaf(m * m * A + M2 - 2.f * m * M1, w, dist);
-            M1 = __builtin_fmaf(m, w, M1);
-            M2 = __builtin_fmaf(m * m, w, M2);
+            const float m_ = kMScale * (1.f - NEAR_N / e.depth);
+            dist = __builtin_fmaf(m_ * m_ * A + M2 - 2.f * m_ * M1, w, dist);
+            M1 = __builtin_fmaf(m_, w, M1);
+            M2 = __builtin_fmaf(m_ * m_, w, M2);
             if (Tr > 0.5f) {
                 med = e.depth;
-                med_c = contrib;
+                med_c = base + t;
             }
             const float4 q3 = s_rec[3 * kThreads + t], q4 = s_rec[4 * kThreads + t];
             cr = __builtin_fmaf(q3.w, w, cr);
@@ -93,15 +127,16 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
             ny = __builtin_fmaf(q3.y, w, ny);
             nz = __builtin_fmaf(q3.z, w, nz);
             Tr = next_T;
-            last_c = contrib;
+            last_c = base + t;
         }
+        evals += j;
     }
     if (pair_counter) {
         __shared__ unsigned int s_pairs;
         __syncthreads();
         if (threadIdx.x == 0) s_pairs = 0;
         __syncthreads();
-        atomicAdd(&s_pairs, (unsigned)contrib);
+        atomicAdd(&s_pairs, (unsigned)evals);
         __syncthreads();
         if (threadIdx.x == 0) atomicAdd(pair_counter, (unsigned long long)s_pairs);
     }
@@ -124,46 +159,56 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     out_dist[pix] = dist;
 }
 
-// Sum of v[0..15] over the 64 lanes of a wave with 17 shuffles: four
-// halving exchanges (xor 32, 16, 8, 4) leave each lane with one partial of
-// value index 8*b5 + 4*b4 + 2*b3 + b2 (bits of the lane id), two more
-// (xor 2, 1) complete the sum.
+// DPP lane permutations within a 16-lane row (CDNA3/4 dpp_ctrl codes).
+constexpr int kDppQuad1032 = 0xB1;   // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppQuad2301 = 0x4E;   // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppHalfMirror = 0x141;  // lane i of each 8-lane half row <- 7 - i
+constexpr int kDppRowMirror = 0x140;   // lane i of each row <- 15 - i
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum of v[0..15] over the 64 lanes of a wave (a transpose reduction):
+// v_permlane32_swap / v_permlane16_swap exchange half-waves / half-rows
+// between two value registers, so each of those steps halves the value
+// count with one swap and one add per pair and no lane select; two mirror
+// DPP steps (partners differ in lane bit 3, then bit 2) and two quad_perm
+// DPP adds finish.  Lane l ends with the total of value index
+// 8*b5 + 4*b4 + 2*b3 + b2 (b = bits of l); every lane of a quad holds it.
 __device__ __forceinline__ float wave_reduce16(float v[16], int lane) {
-    {
-        const bool hi = lane & 32;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float send = hi ? v[i] : v[i + 8];
-            const float keep = hi ? v[i + 8] : v[i];
-            v[i] = keep + __shfl_xor(send, 32, 64);
-        }
+    for (int i = 0; i < 8; ++i) {
+        // vdst lanes 32-63 <-> src lanes 0-31: lanes < 32 end with value i,
+        // lanes >= 32 with value i + 8
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 8]), false,
+                                                        false);
+        v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
-    {
-        const bool hi = lane & 16;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float send = hi ? v[i] : v[i + 4];
-            const float keep = hi ? v[i + 4] : v[i];
-            v[i] = keep + __shfl_xor(send, 16, 64);
-        }
+    for (int i = 0; i < 4; ++i) {
+        // odd rows of vdst <-> even rows of src: lane bit 4 selects i + 4
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 4]), false,
+                                                        false);
+        v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    const bool b3 = lane & 8, b2 = lane & 4;
+    {
+        const float x0 = v[0] + dpp<kDppRowMirror>(v[0]);
+        const float x2 = v[2] + dpp<kDppRowMirror>(v[2]);
+        const float x1 = v[1] + dpp<kDppRowMirror>(v[1]);
+        const float x3 = v[3] + dpp<kDppRowMirror>(v[3]);
+        v[0] = b3 ? x2 : x0;
+        v[1] = b3 ? x3 : x1;
     }
     {
-        const bool hi = lane & 8;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const float send = hi ? v[i] : v[i + 2];
-            const float keep = hi ? v[i + 2] : v[i];
-            v[i] = keep + __shfl_xor(send, 8, 64);
-        }
+        const float x0 = v[0] + dpp<kDppHalfMirror>(v[0]);
+        const float x1 = v[1] + dpp<kDppHalfMirror>(v[1]);
+        v[0] = b2 ? x1 : x0;
     }
-    {
-        const bool hi = lane & 4;
-        const float send = hi ? v[0] : v[1];
-        const float keep = hi ? v[1] : v[0];
-        v[0] = keep + __shfl_xor(send, 4, 64);
-    }
-    v[0] += __shfl_xor(v[0], 2, 64);
-    v[0] += __shfl_xor(v[0], 1, 64);
+    v[0] += dpp<kDppQuad1032>(v[0]);
+    v[0] += dpp<kDppQuad2301>(v[0]);
     return v[0];
 }
 
@@ -189,7 +234,8 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     const int tile = xcd_tile(blockIdx.x, T);
     if (tile >= T) return;
     __shared__ float4 s_rec[5 * kThreads];
-    __shared__ int s_mask[kThreads];
+    __shared__ unsigned char s_list[4][kThreads];
+    __shared__ int s_cnt[4][4];
     __shared__ int s_id[kThreads];
     __shared__ float s_acc[kThreads * 16];
     __shared__ int s_maxlast;
@@ -245,15 +291,16 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     for (int hi = n_it; hi > 0; hi -= kThreads) {
         const int bs = min(kThreads, hi);
         __syncthreads();
+        int m = 0;
         if ((int)threadIdx.x < bs) {
             const int gid = ids[start + hi - 1 - (int)threadIdx.x];
             s_id[threadIdx.x] = gid;
-            load_batch(rec, gid, s_rec, s_mask, sx0, sy0);
+            m = load_batch(rec, gid, s_rec, sx0, sy0);
         }
         for (int k = threadIdx.x; k < bs * 16; k += kThreads) s_acc[k] = 0.f;
-        __syncthreads();
-        for (int t = 0; t < bs; ++t) {
-            if (!((s_mask[t] >> wave) & 1)) continue;
+        const int n = build_wave_lists(m, s_list, s_cnt);
+        for (int j = 0; j < n; ++j) {
+            const int t = s_list[wave][j];
             const int c = hi - 1 - t;
             float v[16];
 #pragma unroll

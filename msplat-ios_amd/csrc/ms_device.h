@@ -19,8 +19,8 @@ struct f3 {
     float x, y, z;
 };
 
-__device__ __forceinline__ float dot3(f3 a, f3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
-__device__ __forceinline__ f3 mul3(f3 a, f3 b) { return {a.x * b.x, a.y * b.y, a.z * b.z}; }
+__host__ __device__ __forceinline__ float dot3(f3 a, f3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+__host__ __device__ __forceinline__ f3 mul3(f3 a, f3 b) { return {a.x * b.x, a.y * b.y, a.z * b.z}; }
 
 // Constants of msplat_metal.metal:19-44 and :204-212.
 constexpr float SH_C0 = 0.28209479177387814f;
@@ -305,7 +305,7 @@ __device__ __forceinline__ float splat_reach(float opa) {
 // bounding box follows compute_aabb_2dgs (msplat_metal.metal:302-330) with
 // cutoff sqrt(tau).  When that disc is not entirely in front of the camera
 // (d >= 0) or the bound degenerates, the box is unbounded.
-__device__ __forceinline__ float4 splat_box(const float4 &q0, const float4 &q1, const float4 &q2, float tau) {
+__host__ __device__ __forceinline__ float4 splat_box(const float4 &q0, const float4 &q1, const float4 &q2, float tau) {
     const float inf = __builtin_inff();
     if (!(tau >= 0.0f)) return make_float4(inf, -inf, inf, -inf);
     const f3 T0 = {q0.x, q0.y, q0.z}, T1 = {q0.w, q1.x, q1.y}, T2 = {q1.z, q1.w, q2.x};
@@ -371,13 +371,98 @@ __device__ __forceinline__ bool eval_pair(float px, float py, const float4 &q0, 
 
 // Bit w (w = 0..3) set when the splat box meets the 16x4 pixel strip of wave
 // w of the tile whose top-left pixel is (sx0, sy0).
-__device__ __forceinline__ int strip_mask(const float4 &b, float sx0, float sy0) {
+__host__ __device__ __forceinline__ int strip_mask(const float4 &b, float sx0, float sy0) {
     if (b.x > sx0 + 15.0f || b.y < sx0) return 0;
     int m = 0;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
         const float y0 = sy0 + 4.0f * w;
         if (!(b.z > y0 + 3.0f || b.w < y0)) m |= 1 << w;
+    }
+    return m;
+}
+
+// Minimum over y in [y0, y1] of the convex parabola c y^2 + 2 p y + r0
+// (c > 0), written as its value at the clamped vertex.
+__host__ __device__ __forceinline__ float parabola_min(float c, float p, float r0, float y_vertex, float y0, float y1) {
+    const float y = __builtin_fminf(__builtin_fmaxf(y_vertex, y0), y1);
+    return __builtin_fmaf(__builtin_fmaf(c, y, 2.0f * p), y, r0);
+}
+
+// Strip mask refined by an exact region test.  Bit w is set when a pixel
+// centre of strip w (tile rows 4w..4w+3) may reach alpha >= 1/255, i.e.
+// u^2+v^2 <= tau or rho2d <= tau.  The ray of pixel p is
+//   ray(p) = px (Tv x Tw) + py (Tw x Tu) + Tu x Tv       (= k x l),
+// linear in p, so u^2+v^2 <= tau is the quadratic region
+//   g(p) = ray.x^2 + ray.y^2 - tau ray.z^2 <= 0,
+// an ellipse when g's quadratic part is positive definite.  For such
+// splats the strip rectangle (grown by half a pixel) is tested against the
+// ellipse of a 1% larger tau by minimising the convex g over the rectangle
+// (interior vertex or the four edges), and against the low-pass disc.
+// Ill-conditioned or unbounded cases keep the box mask.  Every test is
+// conservative, so masked-out splats are exactly those eval_pair rejects.
+__host__ __device__ __forceinline__ int strip_mask_fine(const float4 &q0, const float4 &q1, const float4 &q2,
+                                                        float tau, float sx0, float sy0) {
+    const int mbox = strip_mask(splat_box(q0, q1, q2, tau), sx0, sy0);
+    if (mbox == 0) return 0;
+    const f3 Tu = {q0.x, q0.y, q0.z}, Tv = {q0.w, q1.x, q1.y}, Tw = {q1.z, q1.w, q2.x};
+    const f3 c0 = {Tv.y * Tw.z - Tv.z * Tw.y, Tv.z * Tw.x - Tv.x * Tw.z, Tv.x * Tw.y - Tv.y * Tw.x};
+    const f3 c1 = {Tw.y * Tu.z - Tw.z * Tu.y, Tw.z * Tu.x - Tw.x * Tu.z, Tw.x * Tu.y - Tw.y * Tu.x};
+    const f3 c2 = {Tu.y * Tv.z - Tu.z * Tv.y, Tu.z * Tv.x - Tu.x * Tv.z, Tu.x * Tv.y - Tu.y * Tv.x};
+    // coordinates relative to the tile's first pixel centre
+    const f3 r0 = {sx0 * c0.x + sy0 * c1.x + c2.x, sx0 * c0.y + sy0 * c1.y + c2.y, sx0 * c0.z + sy0 * c1.z + c2.z};
+    const float tt = tau * 1.01f;
+    const float a = c0.x * c0.x + c0.y * c0.y - tt * c0.z * c0.z;
+    const float b = c0.x * c1.x + c0.y * c1.y - tt * c0.z * c1.z;
+    const float c = c1.x * c1.x + c1.y * c1.y - tt * c1.z * c1.z;
+    const float d = c0.x * r0.x + c0.y * r0.y - tt * c0.z * r0.z;
+    const float e = c1.x * r0.x + c1.y * r0.y - tt * c1.z * r0.z;
+    const float f = r0.x * r0.x + r0.y * r0.y - tt * r0.z * r0.z;
+    const float det = a * c - b * b;
+    if (!(a > 0.0f && c > 0.0f && det > 1e-3f * (a * c))) return mbox;
+    // rounding allowance: 1e-5 of the largest term magnitude over the tile
+    const float st = __builtin_sqrtf(tt);
+    const float M = __builtin_fabsf(r0.x) + __builtin_fabsf(r0.y) + st * __builtin_fabsf(r0.z) +
+                    16.0f * (__builtin_fabsf(c0.x) + __builtin_fabsf(c0.y) + st * __builtin_fabsf(c0.z) +
+                             __builtin_fabsf(c1.x) + __builtin_fabsf(c1.y) + st * __builtin_fabsf(c1.z));
+    const float tol = 1e-5f * M * M;
+    const float inv_det = 1.0f / det;
+    const float xs = (b * e - c * d) * inv_det, ys = (b * d - a * e) * inv_det;
+    const float gmin = f + d * xs + e * ys;  // g at the ellipse centre
+    const float X0 = -0.5f, X1 = 15.5f;
+    // vertical edges x = X0, X1: g = c y^2 + 2 (b X + e) y + (a X^2 + 2 d X + f)
+    const float pv0 = b * X0 + e, pv1 = b * X1 + e;
+    const float rv0 = (a * X0 + 2.0f * d) * X0 + f, rv1 = (a * X1 + 2.0f * d) * X1 + f;
+    const float yv0 = -pv0 / c, yv1 = -pv1 / c;
+    const float inv_a = 1.0f / a;
+    const float lp_r2 = 0.5f * tt + 1e-3f;
+    const float dcx = q2.y - sx0, dcy = q2.z - sy0;
+    const float ddx = dcx - __builtin_fminf(__builtin_fmaxf(dcx, X0), X1);
+    int m = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        if (!((mbox >> w) & 1)) continue;
+        const float Y0 = 4.0f * w - 0.5f, Y1 = Y0 + 4.0f;
+        bool hit = false;
+        if (gmin <= tol) {
+            if (xs >= X0 && xs <= X1 && ys >= Y0 && ys <= Y1) {
+                hit = true;
+            } else {
+                // horizontal edges y = Y: g = a x^2 + 2 (b Y + d) x + (c Y^2 + 2 e Y + f)
+                const float ph0 = b * Y0 + d, ph1 = b * Y1 + d;
+                const float rh0 = (c * Y0 + 2.0f * e) * Y0 + f, rh1 = (c * Y1 + 2.0f * e) * Y1 + f;
+                float g = parabola_min(c, pv0, rv0, yv0, Y0, Y1);
+                g = __builtin_fminf(g, parabola_min(c, pv1, rv1, yv1, Y0, Y1));
+                g = __builtin_fminf(g, parabola_min(a, ph0, rh0, -ph0 * inv_a, X0, X1));
+                g = __builtin_fminf(g, parabola_min(a, ph1, rh1, -ph1 * inv_a, X0, X1));
+                hit = g <= tol;
+            }
+        }
+        if (!hit) {
+            const float ddy = dcy - __builtin_fminf(__builtin_fmaxf(dcy, Y0), Y1);
+            hit = ddx * ddx + ddy * ddy <= lp_r2;
+        }
+        if (hit) m |= 1 << w;
     }
     return m;
 }

@@ -230,8 +230,9 @@ def prepare_camera(cam_to_world, fx, fy, cx, cy, width, height, degree=0, degree
     return cam
 
 
-def enable_timing(on: bool = True) -> None:
-    check(lib().msplat_hip_enable_timing(1 if on else 0))
+def enable_timing(on: bool = True, pairs: bool = False) -> None:
+    """Per-stage HIP event timing; `pairs` also counts raster pairs."""
+    check(lib().msplat_hip_enable_timing((1 if on else 0) | (2 if pairs else 0)))
 
 
 def stage_times() -> dict[str, float]:
