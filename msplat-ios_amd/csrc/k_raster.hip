@@ -218,8 +218,11 @@ __device__ __forceinline__ float wave_reduce16(float v[16], int lane) {
 // the forward's exact arithmetic (eval_pair); quantities that only scale
 // gradients use hardware reciprocals.  Per-splat gradients
 // [dL_dtransMat 9, dL_dnormal3D 3, dL_dopacity 1, dL_dcolors 3] are reduced
-// across the wave, then across the four waves in LDS, and flushed with one
-// global float atomic per (tile, splat, component).
+// across the wave and added with one 16-lane global float atomic (one 64-byte
+// line) per (wave, splat); with the strip masks a splat is evaluated by
+// about 1.3 of the tile's four waves, so this issues no more atomic requests
+// than a per-tile merge in LDS would, without its LDS array, zeroing and
+// flush barrier.
 // FULL = false is the training step's case: the only upstream gradient is
 // dL/dimage (depth, alpha, normal, median-depth and distortion gradients are
 // zero), so those terms are compiled out.
@@ -237,7 +240,6 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     __shared__ unsigned char s_list[4][kThreads];
     __shared__ int s_cnt[4][4];
     __shared__ int s_id[kThreads];
-    __shared__ float s_acc[kThreads * 16];
     __shared__ int s_maxlast;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int tx = tile % tiles_x, ty = tile / tiles_x;
@@ -297,7 +299,6 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
             s_id[threadIdx.x] = gid;
             m = load_batch(rec, gid, s_rec, sx0, sy0);
         }
-        for (int k = threadIdx.x; k < bs * 16; k += kThreads) s_acc[k] = 0.f;
         const int n = build_wave_lists(m, s_list, s_cnt);
         for (int j = 0; j < n; ++j) {
             const int t = s_list[wave][j];
@@ -389,14 +390,9 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 if ((lane & 3) == 0) {
                     const int vi = ((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 +
                                    ((lane >> 2) & 1);
-                    if (s != 0.f) atomicAdd(&s_acc[t * 16 + vi], s);
+                    if (s != 0.f) unsafeAtomicAdd(&grads16[(size_t)s_id[t] * 16 + vi], s);
                 }
             }
-        }
-        __syncthreads();
-        for (int k = threadIdx.x; k < bs * 16; k += kThreads) {
-            const float a = s_acc[k];
-            if (a != 0.f) unsafeAtomicAdd(&grads16[(size_t)s_id[k >> 4] * 16 + (k & 15)], a);
         }
     }
 }
