@@ -24,19 +24,24 @@ sys.path.insert(0, str(REPO / "msplat-ios_amd"))
 
 METRIC = "train steps/s @3M splats 5187x3361; render FPS; % HBM peak per kernel"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
-VALU_PEAK_LANE_OPS = 39.3e12   # 256 CU x 64 lanes x 2.4 GHz, non-packed
 
 
 def algorithmic_bytes(stage: str, N: int, I: int, P: int, T: int) -> float:
-    """Compulsory HBM bytes of one launch of each stage (fp32, SH degree 3)."""
+    """Compulsory HBM bytes of one launch of each stage of a fused fp32 2DGS
+    step (N splats, I tile intersections, P pixels, T tiles): projection
+    232 B in + 80 B out per splat; binning 32 B per splat + 8 B per
+    intersection + 12 B per tile, sorting 12 B per intersection + 8 B per
+    tile; raster forward 76 B per intersection + 60 B per pixel; SSIM + L1
+    36 B per pixel; raster backward 140 B per intersection + 60 B per pixel +
+    64 B per splat; projection backward fused with Adam 1716 B per splat."""
     return {
-        "project_fwd": 328.0 * N + 4.0 * T,          # 232 B params in, 96 B record/depth/radius/rect out
-        "tile_scan": 12.0 * T,                        # counts in, offsets + cursors out
-        "scatter_sort": 16.0 * N + 24.0 * I,          # rect/depth/radius in, key out+in, id out
-        "raster_fwd": 84.0 * I + 60.0 * P,            # id + 80 B record per intersection, 8 outputs
-        "ssim_l1": 132.0 * P,                         # img+gt in, 3 gradient maps out/in, dL/dimg out
-        "raster_bwd": 84.0 * I + 128.0 * N + 32.0 * P,  # records, gradient RMW, per-pixel state
-        "project_bwd_adam": 1484.0 * N,               # params+m+v RMW, raster grads, stats
+        "project_fwd": 312.0 * N,
+        "tile_scan": 12.0 * T,
+        "scatter_sort": 32.0 * N + 20.0 * I + 8.0 * T,
+        "raster_fwd": 76.0 * I + 60.0 * P,
+        "ssim_l1": 36.0 * P,
+        "raster_bwd": 140.0 * I + 60.0 * P + 64.0 * N,
+        "project_bwd_adam": 1716.0 * N,
     }.get(stage, 0.0)
 
 
@@ -164,12 +169,7 @@ def main() -> int:
     dominant = max(kernels, key=lambda k: kernels[k]["ms"])
     dk = kernels[dominant]
     pairs_mean = float(np.mean(pairs))
-    for name in ("raster_fwd", "raster_bwd"):
-        if name in kernels:
-            ops = 60.0 if name == "raster_fwd" else 180.0
-            kernels[name]["pairs_evaluated"] = int(pairs_mean)
-            kernels[name]["frac_valu_peak_est"] = round(pairs_mean * ops / (kernels[name]["ms"] * 1e-3)
-                                                        / VALU_PEAK_LANE_OPS, 4)
+    kernels["raster_fwd"]["pairs_evaluated"] = int(pairs_mean)
 
     result = {
         "metric": METRIC,

@@ -65,8 +65,9 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
             if verbose and log.strip():
                 print(log, file=sys.stderr)
     tmp = LIB.with_suffix(".so.tmp")
+    # --no-undefined: a missing host symbol fails here, not at load time
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-           "-fopenmp", "-lpthread"]
+           "-fopenmp", "-lz", "-lpthread", "-Wl,--no-undefined"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -7,12 +7,17 @@
 // msplat_metal.metal:2704-3085, msplat_metal.mm:1077-1212).  Because
 // dL/dssim_map is a known constant (-lambda / 3HW), the per-pixel SSIM
 // partials can be produced in the same pass as the forward statistics:
-//   pass 1 (k_ssim_fwd): img, gt (+halo) -> 5 separable blurs in LDS ->
-//          SSIM map, loss partials, and the three per-pixel gradient maps
-//          (d/dmu1 folded, d/dsigma1^2, d/dsigma12);
-//   pass 2 (k_ssim_bwd): the three maps (+halo) -> adjoint blur in LDS ->
-//          dL/dimg = L1 gradient + blurred SSIM gradient.
-// HBM traffic: 24 + 36 B/px (pass 1) + 36 + 24 + 12 B/px (pass 2).
+//   pass 1 (k_ssim_fwd): img, gt (+halo, all three channels in one
+//          coalesced sweep of the interleaved rows) -> per channel: 5
+//          separable blurs in LDS -> SSIM map, loss partials and the three
+//          per-pixel gradient maps (d/dmu1 folded, d/dsigma1^2, d/dsigma12),
+//          stored channel-planar so every later access is a contiguous row;
+//   pass 2 (k_ssim_bwd): per channel the three planar maps (+halo) ->
+//          adjoint blur in LDS; the three channels of a pixel stay in the
+//          same thread, so dL/dimg = L1 gradient + blurred SSIM gradient is
+//          written once, interleaved.
+// HBM traffic per pixel: 24 B in + 36 B out (pass 1), 36 + 24 B in + 12 B
+// out (pass 2), plus the halo re-reads of neighbouring tiles.
 #include "kernels.h"
 #include "ms_device.h"
 
@@ -21,6 +26,7 @@ namespace {
 constexpr int TW = 64, TH = 16, RAD = 5;
 constexpr int RW = TW + 2 * RAD, RH = TH + 2 * RAD;
 constexpr int kThreads = 256;
+constexpr int kPix = TH * TW / kThreads;  // output pixels per thread
 
 struct Window {
     float w[11];
@@ -38,36 +44,44 @@ __device__ __forceinline__ double block_sum_d(double v, double *s_red) {
     return t;
 }
 
+// Loads the (RH x RW) region around the tile of an interleaved [H,W,3]
+// image into three planar LDS planes, zero outside the image.
+__device__ __forceinline__ void load_region3(const float *__restrict__ src, int W, int H, int x0, int y0,
+                                             float (*dst)[RH][RW]) {
+    for (int k = threadIdx.x; k < RH * RW * 3; k += kThreads) {
+        const int ry = k / (RW * 3), rem = k - ry * (RW * 3);
+        const int rx = rem / 3, c = rem - rx * 3;
+        const int gy = y0 - RAD + ry, gx = x0 - RAD + rx;
+        const bool inb = gx >= 0 && gx < W && gy >= 0 && gy < H;
+        dst[c][ry][rx] = inb ? src[((size_t)gy * W + gx) * 3 + c] : 0.f;
+    }
+}
+
 __global__ __launch_bounds__(kThreads) void k_ssim_fwd(int W, int H, const float *__restrict__ img,
                                                        const float *__restrict__ gt, const float *__restrict__ dist,
                                                        float lambda_l1, float lambda_dist, float inv_np, float g,
                                                        Window win, float *__restrict__ gm1,
                                                        float *__restrict__ gs1, float *__restrict__ gs12,
                                                        double *__restrict__ partials) {
-    __shared__ float s_a[RH][RW];
-    __shared__ float s_b[RH][RW];
+    __shared__ float s_a[3][RH][RW];
+    __shared__ float s_b[3][RH][RW];
     __shared__ float s_h[5][RH][TW];
     __shared__ double s_red[kThreads / 64];
     const int x0 = blockIdx.x * TW, y0 = blockIdx.y * TH;
+    const size_t plane = (size_t)W * H;
     const float C1 = 0.0001f, C2 = 0.0009f;
     double ssim_acc = 0.0, l1_acc = 0.0;
+    load_region3(img, W, H, x0, y0, s_a);
+    load_region3(gt, W, H, x0, y0, s_b);
+    __syncthreads();
     for (int c = 0; c < 3; ++c) {
-        for (int k = threadIdx.x; k < RH * RW; k += kThreads) {
-            const int ry = k / RW, rx = k - ry * RW;
-            const int gy = y0 - RAD + ry, gx = x0 - RAD + rx;
-            const bool inb = gx >= 0 && gx < W && gy >= 0 && gy < H;
-            const size_t o = ((size_t)gy * W + gx) * 3 + c;
-            s_a[ry][rx] = inb ? img[o] : 0.f;
-            s_b[ry][rx] = inb ? gt[o] : 0.f;
-        }
-        __syncthreads();
         // horizontal pass of ssim_blur_horiz_kernel (msplat_metal.metal:2847-2873)
         for (int k = threadIdx.x; k < RH * TW; k += kThreads) {
             const int ry = k / TW, x = k - ry * TW;
             float m1 = 0.f, m2 = 0.f, e11 = 0.f, e22 = 0.f, e12 = 0.f;
 #pragma unroll
             for (int j = 0; j < 11; ++j) {
-                const float a = s_a[ry][x + j], b = s_b[ry][x + j], w = win.w[j];
+                const float a = s_a[c][ry][x + j], b = s_b[c][ry][x + j], w = win.w[j];
                 m1 = __builtin_fmaf(w, a, m1);
                 m2 = __builtin_fmaf(w, b, m2);
                 e11 = __builtin_fmaf(w, a * a, e11);
@@ -83,7 +97,9 @@ __global__ __launch_bounds__(kThreads) void k_ssim_fwd(int W, int H, const float
         __syncthreads();
         // vertical pass + ssim_compute_kernel (:2910-2952) +
         // ssim_backward_compute_kernel (:2965-3047)
-        for (int k = threadIdx.x; k < TH * TW; k += kThreads) {
+#pragma unroll
+        for (int i = 0; i < kPix; ++i) {
+            const int k = threadIdx.x + i * kThreads;
             const int y = k / TW, x = k - y * TW;
             const int gy = y0 + y, gx = x0 + x;
             if (gx >= W || gy >= H) continue;
@@ -113,7 +129,7 @@ __global__ __launch_bounds__(kThreads) void k_ssim_fwd(int W, int H, const float
             const float g12 = g * ds12, g1 = g * ds1;
             gm += g1 * (-2.0f * m1);
             gm += g12 * (-m2);
-            const size_t o = ((size_t)gy * W + gx) * 3 + c;
+            const size_t o = c * plane + (size_t)gy * W + gx;
             gm1[o] = gm;
             gs1[o] = g1;
             gs12[o] = g12;
@@ -122,17 +138,18 @@ __global__ __launch_bounds__(kThreads) void k_ssim_fwd(int W, int H, const float
     }
     // per-pixel L1 + distortion loss of loss_l1_distortion_2dgs_kernel (:2704-2762)
     const float inv_HW = inv_np * 3.0f;
-    for (int k = threadIdx.x; k < TH * TW; k += kThreads) {
+#pragma unroll
+    for (int i = 0; i < kPix; ++i) {
+        const int k = threadIdx.x + i * kThreads;
         const int y = k / TW, x = k - y * TW;
         const int gy = y0 + y, gx = x0 + x;
         if (gx >= W || gy >= H) continue;
-        const size_t p = (size_t)gy * W + gx;
         float local = 0.0f;
         for (int c = 0; c < 3; ++c) {
-            const float diff = img[3 * p + c] - gt[3 * p + c];
+            const float diff = s_a[c][y + RAD][x + RAD] - s_b[c][y + RAD][x + RAD];
             local += lambda_l1 * __builtin_fabsf(diff) * inv_np;
         }
-        const float dd = dist ? dist[p] : 0.0f;
+        const float dd = dist ? dist[(size_t)gy * W + gx] : 0.0f;
         local += lambda_dist * dd * inv_HW;
         l1_acc += (double)local;
     }
@@ -155,15 +172,18 @@ __global__ __launch_bounds__(kThreads) void k_ssim_bwd(int W, int H, const float
     __shared__ float s_g[3][RH][RW];
     __shared__ float s_h[3][RH][TW];
     const int x0 = blockIdx.x * TW, y0 = blockIdx.y * TH;
+    const size_t plane = (size_t)W * H;
+    float blur[kPix][3][3];  // [pixel][channel][gm, g1, g12]
     for (int c = 0; c < 3; ++c) {
+        const float *m0 = gm1 + c * plane, *m1 = gs1 + c * plane, *m2 = gs12 + c * plane;
         for (int k = threadIdx.x; k < RH * RW; k += kThreads) {
             const int ry = k / RW, rx = k - ry * RW;
             const int gy = y0 - RAD + ry, gx = x0 - RAD + rx;
             const bool inb = gx >= 0 && gx < W && gy >= 0 && gy < H;
-            const size_t o = ((size_t)gy * W + gx) * 3 + c;
-            s_g[0][ry][rx] = inb ? gm1[o] : 0.f;
-            s_g[1][ry][rx] = inb ? gs1[o] : 0.f;
-            s_g[2][ry][rx] = inb ? gs12[o] : 0.f;
+            const size_t o = (size_t)gy * W + gx;
+            s_g[0][ry][rx] = inb ? m0[o] : 0.f;
+            s_g[1][ry][rx] = inb ? m1[o] : 0.f;
+            s_g[2][ry][rx] = inb ? m2[o] : 0.f;
         }
         __syncthreads();
         for (int k = threadIdx.x; k < RH * TW; k += kThreads) {
@@ -181,10 +201,10 @@ __global__ __launch_bounds__(kThreads) void k_ssim_bwd(int W, int H, const float
             s_h[2][ry][x] = h2;
         }
         __syncthreads();
-        for (int k = threadIdx.x; k < TH * TW; k += kThreads) {
+#pragma unroll
+        for (int i = 0; i < kPix; ++i) {
+            const int k = threadIdx.x + i * kThreads;
             const int y = k / TW, x = k - y * TW;
-            const int gy = y0 + y, gx = x0 + x;
-            if (gx >= W || gy >= H) continue;
             float bgm = 0.f, bg1 = 0.f, bg12 = 0.f;
 #pragma unroll
             for (int j = 0; j < 11; ++j) {
@@ -193,15 +213,28 @@ __global__ __launch_bounds__(kThreads) void k_ssim_bwd(int W, int H, const float
                 bg1 = __builtin_fmaf(w, s_h[1][y + j][x], bg1);
                 bg12 = __builtin_fmaf(w, s_h[2][y + j][x], bg12);
             }
-            const size_t o = ((size_t)gy * W + gx) * 3 + c;
-            const float a = img[o], b = gt[o];
+            blur[i][c][0] = bgm;
+            blur[i][c][1] = bg1;
+            blur[i][c][2] = bg12;
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < kPix; ++i) {
+        const int k = threadIdx.x + i * kThreads;
+        const int y = k / TW, x = k - y * TW;
+        const int gy = y0 + y, gx = x0 + x;
+        if (gx >= W || gy >= H) continue;
+        const size_t o = ((size_t)gy * W + gx) * 3;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const float a = img[o + c], b = gt[o + c];
             const float diff = a - b;
             const float sgn = (diff > 0.0f) ? 1.0f : ((diff < 0.0f) ? -1.0f : 0.0f);
             const float l1 = lambda_l1 * sgn * inv_np;
-            const float contrib = bgm + 2.0f * a * bg1 + b * bg12;
-            dL_dimg[o] = l1 + contrib;
+            const float contrib = blur[i][c][0] + 2.0f * a * blur[i][c][1] + b * blur[i][c][2];
+            dL_dimg[o + c] = l1 + contrib;
         }
-        __syncthreads();
     }
 }
 
