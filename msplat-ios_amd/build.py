@@ -72,7 +72,27 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    build_core()
     return LIB
+
+
+def build_core() -> Path:
+    """The msplat._core Python extension (pybind11) over the C++ trainer
+    API, linked against libmsplat_hip.so next to it."""
+    import sysconfig
+
+    import pybind11
+
+    out = OUT_DIR / ("_core" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_name(out.name + ".tmp")
+    cmd = [HIPCC, "-x", "c++", *COMMON, "-fvisibility=hidden", f"-I{pybind11.get_include()}",
+           f"-I{sysconfig.get_paths()['include']}", "-shared", "-o", str(tmp),
+           str(CSRC / "python" / "core_module.cpp"), f"-L{OUT_DIR}", "-lmsplat_hip", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"_core build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":

@@ -135,9 +135,6 @@ void initializeRandomPoints(InputData &data, int64_t numPoints, float extent) {
     data.points.count = numPoints;
 }
 
-// Points in a ball of radius 0.35 x (mean camera distance) about the origin
-// with near-black colours, for datasets without a point cloud
-// (input_data.cpp:371-420).
 void initializeRandomPointsCameraAware(InputData &data, int64_t numPoints, float radiusFrac) {
     if (data.cameras.empty()) {
         initializeRandomPoints(data, numPoints, 1.3f);

@@ -59,11 +59,11 @@ struct InputData {
     float translation[3] = {};
     Points points;
 
-    // All cameras sorted by image path (input_data.cpp:214-236; validation
-    // selection is not used by the trainer).
+    // All cameras (validate = false), or all but one validation camera
+    // (input_data.cpp:163-183).
     std::tuple<std::vector<Camera>, Camera *> getCameras(bool validate, const std::string &valImage = "random");
-    // Every testEvery-th camera (by sorted path) is held out
-    // (input_data.cpp:238-252).
+    // Cameras 0, testEvery, 2 testEvery, ... are held out for testing
+    // (input_data.cpp:185-195).
     std::tuple<std::vector<Camera>, std::vector<Camera>> splitTrainTest(int testEvery);
 };
 
@@ -80,6 +80,10 @@ void autoScaleAndCenter(InputData &data);
 // Fallback initialisation without a point cloud: uniform points in
 // [-extent, extent]^3 with random colours (input_data.cpp:351-369).
 void initializeRandomPoints(InputData &data, int64_t numPoints = 100000, float extent = 1.3f);
+// Fallback used by the loaders: points in a ball of radiusFrac x (mean
+// camera distance) about the origin, near-black colours
+// (input_data.cpp:371-420).
+void initializeRandomPointsCameraAware(InputData &data, int64_t numPoints = 100000, float radiusFrac = 0.35f);
 
 // Image utilities (core/src/loaders/image_io.cpp).
 Image imreadRGB(const std::string &path);

@@ -1,12 +1,55 @@
-"""msplat on MI355X: the 2DGS Gaussian-splatting training step as hand-written
-gfx950 HIP kernels behind msplat's C ABI.
+"""msplat on MI355X: 2D Gaussian Splatting training with hand-written gfx950
+HIP kernels.
 
-The public surface mirrors the reference package (python/msplat/__init__.py):
-TrainingConfig, TrainingStats, Dataset, GaussianTrainer, load_dataset, sync,
-cleanup.  Lower-level access to the engine lives in msplat._engine and
-msplat.device.
+The public surface is the reference package's (python/msplat/__init__.py):
+TrainingConfig, TrainingStats, Dataset, GaussianTrainer, sync, cleanup and
+load_dataset, implemented by the compiled msplat._core module over the C++
+trainer.  Dataset.from_arrays builds a dataset from in-memory images.
+Lower-level access to the engine's C ABI lives in msplat._engine and
+msplat.device; msplat.synthetic generates seeded test scenes.
 """
-from . import _engine, synthetic
-from ._engine import MsplatError, cleanup, sync
+import atexit
 
-__all__ = ["MsplatError", "cleanup", "sync", "synthetic", "_engine"]
+from msplat._core import (
+    Dataset,
+    GaussianTrainer,
+    TrainingConfig,
+    TrainingStats,
+    sync,
+)
+from msplat._core import cleanup as _cleanup_raw
+
+from . import _engine, synthetic
+from ._engine import MsplatError
+
+_cleaned_up = False
+
+
+def cleanup():
+    """Release all cached GPU resources. Safe to call multiple times."""
+    global _cleaned_up
+    if not _cleaned_up:
+        _cleaned_up = True
+        _cleanup_raw()
+
+
+atexit.register(cleanup)
+
+__all__ = [
+    "TrainingConfig",
+    "TrainingStats",
+    "Dataset",
+    "GaussianTrainer",
+    "sync",
+    "cleanup",
+    "load_dataset",
+    "MsplatError",
+    "synthetic",
+]
+
+__version__ = "1.1.3"
+
+
+def load_dataset(path: str, downscale_factor: float = 1.0, eval_mode: bool = False, test_every: int = 8) -> Dataset:
+    """Load a dataset (auto-detects COLMAP, Nerfstudio, Polycam)."""
+    return Dataset(path, downscale_factor, eval_mode, test_every)

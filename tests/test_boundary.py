@@ -15,8 +15,9 @@ LIB = REPO / "msplat-ios_amd" / "msplat" / "libmsplat_hip.so"
 def _declared(header: Path) -> list[str]:
     text = header.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"static inline[^{]*\{.*?\n\}", "", text, flags=re.S)  # header-only helpers
     names = re.findall(r"^[A-Za-z_][\w\s\*]*?\b(msplat_\w+)\s*\(", text, flags=re.M)
-    return sorted(set(n for n in names if "static inline" not in n))
+    return sorted(set(names))
 
 
 def _exported() -> set[str]:

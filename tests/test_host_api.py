@@ -1,0 +1,377 @@
+"""Host layer on the CPU: the trainer's C ABI exports, the Python surface of
+the reference's msplat._core stubs, image decoding and the dataset loaders
+(COLMAP / Nerfstudio / Polycam).  Nothing here touches the GPU."""
+from __future__ import annotations
+
+import ctypes as C
+import json
+import re
+import struct
+import zlib
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+REPO = Path(__file__).resolve().parents[1]
+
+
+def _header_functions(path: Path) -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", path.read_text(), flags=re.S)
+    text = re.sub(r"static inline[^{]*\{.*?\n\}", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(msplat_\w+)\s*\(", text)))
+
+
+def test_c_api_header_symbols_are_exported():
+    from msplat import _engine as E
+
+    lib = E.lib()
+    names = _header_functions(REPO / "include" / "msplat_c_api.h")
+    # every function of the reference's C ABI is declared (msplat_c_api.h:83-127)
+    reference = {
+        "msplat_dataset_create", "msplat_dataset_destroy", "msplat_dataset_num_train", "msplat_dataset_num_test",
+        "msplat_dataset_camera_pose", "msplat_trainer_create", "msplat_trainer_destroy", "msplat_trainer_step",
+        "msplat_trainer_train", "msplat_trainer_evaluate", "msplat_trainer_render", "msplat_trainer_render_pose",
+        "msplat_trainer_render_pose_to_buffer", "msplat_trainer_export_ply", "msplat_trainer_export_splat",
+        "msplat_trainer_extract_mesh", "msplat_trainer_save_checkpoint", "msplat_trainer_load_checkpoint",
+        "msplat_trainer_splat_count", "msplat_trainer_iteration", "msplat_set_metallib_path", "msplat_sync",
+        "msplat_cleanup",
+    }
+    assert reference <= set(names)
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_c_api_config_struct_layout():
+    """MsplatConfig is 16 fields (msplat_c_api.h:16-33): 13 x 4-byte fields,
+    a bool, a float and float[3], with natural alignment -> 72 bytes."""
+    class MsplatConfig(C.Structure):
+        _fields_ = [("iterations", C.c_int), ("shDegree", C.c_int), ("shDegreeInterval", C.c_int),
+                    ("ssimWeight", C.c_float), ("numDownscales", C.c_int), ("resolutionSchedule", C.c_int),
+                    ("refineEvery", C.c_int), ("warmupLength", C.c_int), ("resetAlphaEvery", C.c_int),
+                    ("densifyGradThresh", C.c_float), ("densifySizeThresh", C.c_float),
+                    ("stopScreenSizeAt", C.c_int), ("splitScreenSize", C.c_float), ("keepCrs", C.c_bool),
+                    ("downscaleFactor", C.c_float), ("bgColor", C.c_float * 3)]
+    assert C.sizeof(MsplatConfig) == 72
+    from msplat import _engine as E
+
+    lib = E.lib()
+    lib.msplat_dataset_create.restype = C.c_void_p
+    lib.msplat_last_error.restype = C.c_char_p
+    # a failing create returns NULL and records the message (no exception crosses the ABI)
+    assert lib.msplat_dataset_create(b"/nonexistent/dataset", C.c_float(1.0), False, 8) is None
+    assert b"Unrecognized dataset format" in lib.msplat_last_error()
+
+
+def test_python_surface_matches_reference_stubs():
+    import msplat
+
+    c = msplat.TrainingConfig()
+    expected = dict(iterations=30000, sh_degree=3, sh_degree_interval=1000, ssim_weight=0.2, num_downscales=2,
+                    resolution_schedule=3000, refine_every=100, warmup_length=500, reset_alpha_every=30,
+                    densify_grad_thresh=0.0002, densify_size_thresh=0.01, stop_screen_size_at=4000,
+                    split_screen_size=0.05, keep_crs=False, downscale_factor=1.0, output="splat.ply", save_every=-1)
+    for k, v in expected.items():
+        assert getattr(c, k) == pytest.approx(v), k
+    assert c.bg_color == pytest.approx([0.6130, 0.0101, 0.3984])
+    c2 = msplat.TrainingConfig(iterations=7, bg_color=[0.0, 0.5, 1.0])
+    assert c2.iterations == 7 and c2.bg_color == [0.0, 0.5, 1.0]
+    with pytest.raises(ValueError):
+        msplat.TrainingConfig(bg_color=[1.0, 2.0])
+    with pytest.raises(ValueError):
+        c2.bg_color = [1.0]
+    for name in ("step", "train", "evaluate", "render", "render_from_pose", "export_ply", "export_splat",
+                 "save_checkpoint", "load_checkpoint", "splat_count", "iteration"):
+        assert hasattr(msplat.GaussianTrainer, name), name
+    for name in ("num_train", "num_test", "camera_pose"):
+        assert hasattr(msplat.Dataset, name), name
+    for name in ("iteration", "splat_count", "ms_per_step"):
+        assert hasattr(msplat.TrainingStats, name), name
+    for name in ("TrainingConfig", "TrainingStats", "Dataset", "GaussianTrainer", "sync", "cleanup",
+                 "load_dataset"):
+        assert name in msplat.__all__
+    with pytest.raises(RuntimeError):
+        msplat.load_dataset("/nonexistent/dataset")
+
+
+# ---------------------------------------------------------------- images --
+
+def _png(path: Path, rows: np.ndarray, color_type: int, depth: int, palette=None, interlace=False, filters=None):
+    """Independent PNG encoder for the decoder test: rows is (H, W, C) of
+    integer samples; every scanline uses filters[y % len(filters)]."""
+    h, w = rows.shape[:2]
+    chans = rows.shape[2]
+    filters = filters or [0, 1, 2, 3, 4]
+
+    def pack(img):
+        out = []
+        for y in range(img.shape[0]):
+            samples = img[y].reshape(-1)
+            if depth == 16:
+                raw = b"".join(struct.pack(">H", int(s)) for s in samples)
+            elif depth == 8:
+                raw = bytes(int(s) for s in samples)
+            else:
+                bits = "".join(format(int(s), f"0{depth}b") for s in samples)
+                bits += "0" * (-len(bits) % 8)
+                raw = bytes(int(bits[i:i + 8], 2) for i in range(0, len(bits), 8))
+            out.append(raw)
+        return out
+
+    bpp = max(1, chans * depth // 8)
+
+    def filt(lines, y0):
+        res = b""
+        prev = bytes(len(lines[0])) if lines else b""
+        for y, line in enumerate(lines):
+            f = filters[(y0 + y) % len(filters)]
+            o = bytearray()
+            for i, x in enumerate(line):
+                a = line[i - bpp] if i >= bpp else 0
+                b = prev[i]
+                c = prev[i - bpp] if i >= bpp else 0
+                if f == 0:
+                    p = 0
+                elif f == 1:
+                    p = a
+                elif f == 2:
+                    p = b
+                elif f == 3:
+                    p = (a + b) // 2
+                else:
+                    pa, pb, pc = abs(b - c), abs(a - c), abs(a + b - 2 * c)
+                    p = a if pa <= pb and pa <= pc else (b if pb <= pc else c)
+                o.append((x - p) & 255)
+            res += bytes([f]) + bytes(o)
+            prev = line
+        return res
+
+    if not interlace:
+        data = filt(pack(rows), 0)
+    else:
+        data = b""
+        for sx, sy, dx, dy in ((0, 0, 8, 8), (4, 0, 8, 8), (0, 4, 4, 8), (2, 0, 4, 4), (0, 2, 2, 4), (1, 0, 2, 2),
+                               (0, 1, 1, 2)):
+            sub = rows[sy::dy, sx::dx]
+            if sub.shape[0] and sub.shape[1]:
+                data += filt(pack(sub), 0)
+
+    def chunk(t, d):
+        return struct.pack(">I", len(d)) + t + d + struct.pack(">I", zlib.crc32(t + d) & 0xFFFFFFFF)
+
+    ihdr = struct.pack(">IIBBBBB", w, h, depth, color_type, 0, 0, 1 if interlace else 0)
+    blob = b"\x89PNG\r\n\x1a\n" + chunk(b"IHDR", ihdr)
+    if palette is not None:
+        blob += chunk(b"PLTE", bytes(palette.astype(np.uint8).reshape(-1)))
+    blob += chunk(b"IDAT", zlib.compress(data)) + chunk(b"IEND", b"")
+    path.write_bytes(blob)
+
+
+@pytest.mark.parametrize("case", ["rgb8", "rgba8", "gray8", "gray16", "rgb16", "graya8", "gray1", "gray4",
+                                  "palette8", "palette2", "rgb8_adam7", "gray2_adam7"])
+def test_png_decoder(case, tmp_path):
+    from msplat import _core
+
+    rng = np.random.default_rng(hash(case) % 2**32)
+    h, w = 13, 11
+    if case.startswith("rgb8"):
+        s = rng.integers(0, 256, (h, w, 3))
+        exp = s / 255.0
+        _png(tmp_path / "a.png", s, 2, 8, interlace="adam7" in case)
+    elif case == "rgba8":
+        s = rng.integers(0, 256, (h, w, 4))
+        exp = s[..., :3] / 255.0
+        _png(tmp_path / "a.png", s, 6, 8)
+    elif case == "gray8":
+        s = rng.integers(0, 256, (h, w, 1))
+        exp = np.repeat(s / 255.0, 3, 2)
+        _png(tmp_path / "a.png", s, 0, 8)
+    elif case == "gray16":
+        s = rng.integers(0, 65536, (h, w, 1))
+        exp = np.repeat(s / 65535.0, 3, 2)
+        _png(tmp_path / "a.png", s, 0, 16)
+    elif case == "rgb16":
+        s = rng.integers(0, 65536, (h, w, 3))
+        exp = s / 65535.0
+        _png(tmp_path / "a.png", s, 2, 16)
+    elif case == "graya8":
+        s = rng.integers(0, 256, (h, w, 2))
+        exp = np.repeat(s[..., :1] / 255.0, 3, 2)
+        _png(tmp_path / "a.png", s, 4, 8)
+    elif case.startswith("gray") and case[4].isdigit():
+        d = int(case[4])
+        s = rng.integers(0, 2 ** d, (h, w, 1))
+        exp = np.repeat(s / (2 ** d - 1), 3, 2)
+        _png(tmp_path / "a.png", s, 0, d, interlace="adam7" in case)
+    else:  # palette
+        d = int(case[-1])
+        pal = rng.integers(0, 256, (2 ** d, 3))
+        s = rng.integers(0, 2 ** d, (h, w, 1))
+        exp = pal[s[..., 0]] / 255.0
+        _png(tmp_path / "a.png", s, 3, d, palette=pal)
+    got = _core._read_image(str(tmp_path / "a.png"))
+    assert got.shape == (h, w, 3)
+    assert np.abs(got - exp).max() < 1e-6
+    if case in ("rgb8", "rgba8", "gray8", "palette8", "rgb8_adam7"):
+        # the test's encoder agrees with an independent decoder
+        from PIL import Image
+
+        ref = np.asarray(Image.open(tmp_path / "a.png").convert("RGB"), np.float64) / 255.0
+        assert np.abs(ref - exp).max() < 1e-6
+
+
+def test_pnm_decoder(tmp_path):
+    from msplat import _core
+
+    rng = np.random.default_rng(3)
+    s = rng.integers(0, 256, (5, 7, 3)).astype(np.uint8)
+    (tmp_path / "a.ppm").write_bytes(b"P6\n# comment\n7 5\n255\n" + s.tobytes())
+    assert np.abs(_core._read_image(str(tmp_path / "a.ppm")) - s / 255.0).max() < 1e-6
+    g = rng.integers(0, 65536, (4, 3)).astype(">u2")
+    (tmp_path / "b.pgm").write_bytes(b"P5 3 4 65535\n" + g.tobytes())
+    assert np.abs(_core._read_image(str(tmp_path / "b.pgm")) - np.repeat(g[..., None] / 65535.0, 3, 2)).max() < 1e-6
+    with pytest.raises(RuntimeError):
+        _core._read_image(str(tmp_path / "missing.png"))
+
+
+# --------------------------------------------------------------- loaders --
+
+def _look_at_c2w(eye, target=(0.0, 0.0, 0.0)):
+    """Camera-to-world, OpenGL axes (x right, y up, z back)."""
+    eye = np.asarray(eye, np.float64)
+    z = eye - np.asarray(target)
+    z /= np.linalg.norm(z)
+    x = np.cross([0.0, 1.0, 0.0], z)
+    x /= np.linalg.norm(x)
+    y = np.cross(z, x)
+    m = np.eye(4)
+    m[:3, 0], m[:3, 1], m[:3, 2], m[:3, 3] = x, y, z, eye
+    return m
+
+
+def _normalised(poses):
+    """autoScaleAndCenter (input_data.cpp:124-160) in numpy."""
+    t = np.stack([p[:3, 3] for p in poses])
+    mean = t.mean(0)
+    t = t - mean
+    s = 1.0 / np.abs(t).max()
+    out = []
+    for p, ti in zip(poses, t):
+        q = p.copy()
+        q[:3, 3] = ti * s
+        out.append(q)
+    return out, mean, s
+
+
+def _write_images(folder: Path, n, h=12, w=16):
+    folder.mkdir(parents=True, exist_ok=True)
+    rng = np.random.default_rng(5)
+    imgs = []
+    for i in range(n):
+        s = rng.integers(0, 256, (h, w, 3))
+        _png(folder / f"frame_{i:03d}.png", s, 2, 8)
+        imgs.append(s / 255.0)
+    return imgs
+
+
+def test_nerfstudio_loader(tmp_path):
+    import msplat
+
+    poses = [_look_at_c2w((3 * np.cos(a), 1.0, 3 * np.sin(a))) for a in np.linspace(0, 5, 6)]
+    _write_images(tmp_path / "images", 6)
+    frames = [dict(file_path=f"images/frame_{i:03d}", transform_matrix=p.tolist()) for i, p in enumerate(poses)]
+    (tmp_path / "transforms.json").write_text(json.dumps(dict(w=16, h=12, fl_x=20.0, fl_y=21.0, cx=8.0, cy=6.0,
+                                                              frames=frames[::-1])))
+    pts = np.random.default_rng(1).normal(size=(40, 3)).astype(np.float32)
+    with open(tmp_path / "points3D.ply", "w") as f:
+        f.write("ply\nformat ascii 1.0\nelement vertex 40\nproperty float x\nproperty float y\nproperty float z\n"
+                "property uchar red\nproperty uchar green\nproperty uchar blue\nend_header\n")
+        for p in pts:
+            f.write(f"{p[0]} {p[1]} {p[2]} 10 20 30\n")
+    ds = msplat.Dataset(str(tmp_path), eval_mode=True, test_every=3)
+    assert (ds.num_train, ds.num_test) == (4, 2)
+    norm, _, _ = _normalised(poses)
+    train_ids = [i for i in range(6) if i % 3 != 0]  # frames sorted by path, every 3rd held out
+    for k, i in enumerate(train_ids):
+        assert np.abs(ds.camera_pose(k) - norm[i]).max() < 1e-5
+    with pytest.raises(RuntimeError):
+        ds.camera_pose(4)
+
+
+def test_nerfstudio_camera_angle_intrinsics(tmp_path):
+    """Original-NeRF transforms.json: only camera_angle_x; w, h come from the
+    first image (load_nerfstudio.cpp:78-118)."""
+    import msplat
+
+    poses = [_look_at_c2w((0.0, 0.0, 2.0 + i)) for i in range(2)]
+    _write_images(tmp_path, 2)
+    frames = [dict(file_path=f"frame_{i:03d}.png", transform_matrix=p.tolist()) for i, p in enumerate(poses)]
+    (tmp_path / "transforms.json").write_text(json.dumps(dict(camera_angle_x=0.8, frames=frames)))
+    ds = msplat.Dataset(str(tmp_path))
+    assert ds.num_train == 2
+
+
+def _qvec(R):
+    """Rotation matrix -> quaternion (w, x, y, z)."""
+    w = np.sqrt(max(0.0, 1 + R[0, 0] + R[1, 1] + R[2, 2])) / 2
+    x = np.copysign(np.sqrt(max(0.0, 1 + R[0, 0] - R[1, 1] - R[2, 2])) / 2, R[2, 1] - R[1, 2])
+    y = np.copysign(np.sqrt(max(0.0, 1 - R[0, 0] + R[1, 1] - R[2, 2])) / 2, R[0, 2] - R[2, 0])
+    z = np.copysign(np.sqrt(max(0.0, 1 - R[0, 0] - R[1, 1] + R[2, 2])) / 2, R[1, 0] - R[0, 1])
+    return np.array([w, x, y, z])
+
+
+def test_colmap_loader(tmp_path):
+    """COLMAP binary model: world-to-camera (q, t) in OpenCV axes become
+    OpenGL camera-to-world poses, then centred and scaled."""
+    import msplat
+
+    sp = tmp_path / "sparse" / "0"
+    sp.mkdir(parents=True)
+    _write_images(tmp_path / "images", 4)
+    poses_gl = [_look_at_c2w((2 * np.cos(a), 0.5, 2 * np.sin(a))) for a in (0.1, 1.2, 2.3, 3.4)]
+    with open(sp / "cameras.bin", "wb") as f:
+        f.write(struct.pack("<Q", 1))
+        f.write(struct.pack("<IiQQ", 1, 1, 16, 12) + struct.pack("<4d", 20.0, 21.0, 8.0, 6.0))  # PINHOLE
+    with open(sp / "images.bin", "wb") as f:
+        f.write(struct.pack("<Q", 4))
+        for i, c2w in enumerate(poses_gl):
+            cv = c2w.copy()
+            cv[:3, 1:3] *= -1  # OpenGL -> OpenCV camera axes
+            R = cv[:3, :3].T
+            t = -R @ cv[:3, 3]
+            f.write(struct.pack("<I", i + 1) + struct.pack("<4d", *_qvec(R)) + struct.pack("<3d", *t))
+            f.write(struct.pack("<I", 1) + f"frame_{i:03d}.png".encode() + b"\0")
+            f.write(struct.pack("<Q", 2) + struct.pack("<ddq", 1.0, 2.0, -1) * 2)
+    pts = np.random.default_rng(2).normal(size=(10, 3))
+    with open(sp / "points3D.bin", "wb") as f:
+        f.write(struct.pack("<Q", 10))
+        for k, p in enumerate(pts):
+            f.write(struct.pack("<Q3d3Bd", k, *p, 1, 2, 3, 0.5) + struct.pack("<Q", 1) + struct.pack("<II", 1, 0))
+    ds = msplat.Dataset(str(tmp_path))
+    assert ds.num_train == 4
+    norm, _, _ = _normalised(poses_gl)
+    for i in range(4):
+        assert np.abs(ds.camera_pose(i) - norm[i]).max() < 1e-5
+
+
+def test_polycam_cameras_json_loader(tmp_path):
+    import msplat
+
+    _write_images(tmp_path, 3)
+    poses = [_look_at_c2w((1.0 + i, 0.3, 2.0)) for i in range(3)]
+    frames = [dict(width=16, height=12, fx=20.0, fy=20.0, file_path=f"frame_{i:03d}.png",
+                   transform_matrix=p.tolist()) for i, p in enumerate(poses)]
+    (tmp_path / "cameras.json").write_text(json.dumps(dict(frames=frames)))
+    ds = msplat.Dataset(str(tmp_path), eval_mode=True, test_every=8)
+    assert (ds.num_train, ds.num_test) == (2, 1)
+
+
+def test_dataset_from_arrays_validation():
+    import msplat
+
+    img = np.zeros((8, 8, 3), np.float32)
+    with pytest.raises(ValueError):
+        msplat.Dataset.from_arrays([img], np.eye(4, dtype=np.float32)[None], np.zeros((1, 3), np.float32))
+    ds = msplat.Dataset.from_arrays([img, img], np.stack([np.eye(4)] * 2).astype(np.float32),
+                                    np.array([[10, 10, 4, 4]] * 2, np.float32))
+    assert ds.num_train == 2 and ds.num_test == 0
