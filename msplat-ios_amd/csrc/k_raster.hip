@@ -5,12 +5,12 @@
 // tile (the reference runs four 8x8 threadgroups per tile, each reloading
 // the list, msplat_metal.metal:8-10, 576-586).  Records are staged in LDS in
 // structure-of-arrays float4 planes so the cooperative load is bank-conflict
-// free and the per-pixel loop reads a broadcast.  At load time each splat
-// gets a 4-bit mask of the wave strips (16x4 pixels) whose pixel centres its
-// alpha >= 1/255 region can reach (strip_mask_fine), and the batch is
-// compacted into one ascending slot list per wave, so a wave only visits the
-// splats that can touch its strip and every visited splat is a full
-// evaluation.
+// free and the per-pixel loop reads a broadcast.  Each wave owns an 8x8
+// quadrant of the tile.  At load time each splat gets a 4-bit mask of the
+// quadrants whose pixel centres its alpha >= 1/255 region can reach
+// (strip_mask_fine), and the batch is compacted into one ascending slot list
+// per wave, so a wave only visits the splats that can touch its quadrant and
+// every visited splat is a full evaluation.
 #include "kernels.h"
 #include "ms_device.h"
 
@@ -74,7 +74,8 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     __shared__ float4 s_rec[5 * kThreads];
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int wave = threadIdx.x >> 6;
-    const int pxi = tx * 16 + (threadIdx.x & 15), pyi = ty * 16 + (threadIdx.x >> 4);
+    const int pxi = tx * 16 + lane_px(threadIdx.x >> 6, threadIdx.x & 63);
+    const int pyi = ty * 16 + lane_py(threadIdx.x >> 6, threadIdx.x & 63);
     const bool inside = pxi < W && pyi < H;
     const float px = (float)pxi, py = (float)pyi;
     const float sx0 = (float)(tx * 16), sy0 = (float)(ty * 16);
@@ -243,7 +244,8 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     __shared__ int s_maxlast;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int tx = tile % tiles_x, ty = tile / tiles_x;
-    const int pxi = tx * 16 + (threadIdx.x & 15), pyi = ty * 16 + (threadIdx.x >> 4);
+    const int pxi = tx * 16 + lane_px(threadIdx.x >> 6, threadIdx.x & 63);
+    const int pyi = ty * 16 + lane_py(threadIdx.x >> 6, threadIdx.x & 63);
     const bool inside = pxi < W && pyi < H;
     const float px = (float)pxi, py = (float)pyi;
     const float sx0 = (float)(tx * 16), sy0 = (float)(ty * 16);

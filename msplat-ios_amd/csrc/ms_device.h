@@ -369,15 +369,24 @@ __device__ __forceinline__ bool eval_pair(float px, float py, const float4 &q0, 
     return true;
 }
 
-// Bit w (w = 0..3) set when the splat box meets the 16x4 pixel strip of wave
-// w of the tile whose top-left pixel is (sx0, sy0).
+// Pixels of a 16x16 tile handled by wave w of a 256-thread rasterizer
+// workgroup: an 8x8 quadrant (w & 1 selects the column, w >> 1 the row), lane
+// l at (l & 7, l >> 3) inside it.  Square blocks meet fewer splat footprints
+// than 16x4 strips of the same area.
+constexpr int kWaveW = 8, kWaveH = 8;
+__host__ __device__ constexpr int wave_x0(int w) { return (w & 1) * kWaveW; }
+__host__ __device__ constexpr int wave_y0(int w) { return (w >> 1) * kWaveH; }
+__host__ __device__ constexpr int lane_px(int w, int lane) { return wave_x0(w) + (lane & 7); }
+__host__ __device__ constexpr int lane_py(int w, int lane) { return wave_y0(w) + (lane >> 3); }
+
+// Bit w (w = 0..3) set when the splat box meets the pixel block of wave w
+// of the tile whose top-left pixel is (sx0, sy0).
 __host__ __device__ __forceinline__ int strip_mask(const float4 &b, float sx0, float sy0) {
-    if (b.x > sx0 + 15.0f || b.y < sx0) return 0;
     int m = 0;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-        const float y0 = sy0 + 4.0f * w;
-        if (!(b.z > y0 + 3.0f || b.w < y0)) m |= 1 << w;
+        const float x0 = sx0 + wave_x0(w), y0 = sy0 + wave_y0(w);
+        if (!(b.x > x0 + (kWaveW - 1) || b.y < x0 || b.z > y0 + (kWaveH - 1) || b.w < y0)) m |= 1 << w;
     }
     return m;
 }
@@ -389,14 +398,14 @@ __host__ __device__ __forceinline__ float parabola_min(float c, float p, float r
     return __builtin_fmaf(__builtin_fmaf(c, y, 2.0f * p), y, r0);
 }
 
-// Strip mask refined by an exact region test.  Bit w is set when a pixel
-// centre of strip w (tile rows 4w..4w+3) may reach alpha >= 1/255, i.e.
+// Wave-block mask refined by an exact region test.  Bit w is set when a
+// pixel centre of wave w's block may reach alpha >= 1/255, i.e.
 // u^2+v^2 <= tau or rho2d <= tau.  The ray of pixel p is
 //   ray(p) = px (Tv x Tw) + py (Tw x Tu) + Tu x Tv       (= k x l),
 // linear in p, so u^2+v^2 <= tau is the quadratic region
 //   g(p) = ray.x^2 + ray.y^2 - tau ray.z^2 <= 0,
 // an ellipse when g's quadratic part is positive definite.  For such
-// splats the strip rectangle (grown by half a pixel) is tested against the
+// splats the block rectangle (grown by half a pixel) is tested against the
 // ellipse of a 1% larger tau by minimising the convex g over the rectangle
 // (interior vertex or the four edges), and against the low-pass disc.
 // Ill-conditioned or unbounded cases keep the box mask.  Every test is
@@ -429,36 +438,34 @@ __host__ __device__ __forceinline__ int strip_mask_fine(const float4 &q0, const 
     const float inv_det = 1.0f / det;
     const float xs = (b * e - c * d) * inv_det, ys = (b * d - a * e) * inv_det;
     const float gmin = f + d * xs + e * ys;  // g at the ellipse centre
-    const float X0 = -0.5f, X1 = 15.5f;
-    // vertical edges x = X0, X1: g = c y^2 + 2 (b X + e) y + (a X^2 + 2 d X + f)
-    const float pv0 = b * X0 + e, pv1 = b * X1 + e;
-    const float rv0 = (a * X0 + 2.0f * d) * X0 + f, rv1 = (a * X1 + 2.0f * d) * X1 + f;
-    const float yv0 = -pv0 / c, yv1 = -pv1 / c;
-    const float inv_a = 1.0f / a;
+    const float inv_a = 1.0f / a, inv_c = 1.0f / c;
     const float lp_r2 = 0.5f * tt + 1e-3f;
     const float dcx = q2.y - sx0, dcy = q2.z - sy0;
-    const float ddx = dcx - __builtin_fminf(__builtin_fmaxf(dcx, X0), X1);
     int m = 0;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
         if (!((mbox >> w) & 1)) continue;
-        const float Y0 = 4.0f * w - 0.5f, Y1 = Y0 + 4.0f;
+        const float X0 = wave_x0(w) - 0.5f, X1 = X0 + kWaveW, Y0 = wave_y0(w) - 0.5f, Y1 = Y0 + kWaveH;
         bool hit = false;
         if (gmin <= tol) {
             if (xs >= X0 && xs <= X1 && ys >= Y0 && ys <= Y1) {
                 hit = true;
             } else {
+                // vertical edges x = X: g = c y^2 + 2 (b X + e) y + (a X^2 + 2 d X + f);
                 // horizontal edges y = Y: g = a x^2 + 2 (b Y + d) x + (c Y^2 + 2 e Y + f)
+                const float pv0 = b * X0 + e, pv1 = b * X1 + e;
+                const float rv0 = (a * X0 + 2.0f * d) * X0 + f, rv1 = (a * X1 + 2.0f * d) * X1 + f;
                 const float ph0 = b * Y0 + d, ph1 = b * Y1 + d;
                 const float rh0 = (c * Y0 + 2.0f * e) * Y0 + f, rh1 = (c * Y1 + 2.0f * e) * Y1 + f;
-                float g = parabola_min(c, pv0, rv0, yv0, Y0, Y1);
-                g = __builtin_fminf(g, parabola_min(c, pv1, rv1, yv1, Y0, Y1));
+                float g = parabola_min(c, pv0, rv0, -pv0 * inv_c, Y0, Y1);
+                g = __builtin_fminf(g, parabola_min(c, pv1, rv1, -pv1 * inv_c, Y0, Y1));
                 g = __builtin_fminf(g, parabola_min(a, ph0, rh0, -ph0 * inv_a, X0, X1));
                 g = __builtin_fminf(g, parabola_min(a, ph1, rh1, -ph1 * inv_a, X0, X1));
                 hit = g <= tol;
             }
         }
         if (!hit) {
+            const float ddx = dcx - __builtin_fminf(__builtin_fmaxf(dcx, X0), X1);
             const float ddy = dcy - __builtin_fminf(__builtin_fmaxf(dcy, Y0), Y1);
             hit = ddx * ddx + ddy * ddy <= lp_r2;
         }
