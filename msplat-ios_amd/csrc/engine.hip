@@ -38,7 +38,7 @@ struct Engine {
     // per-gaussian
     DevBuf rec, depths, radii, rect, grads16, colors_raw;
     // per-tile
-    DevBuf counts, offsets, cursor, stats, big_list;
+    DevBuf tile_diff, counts, offsets, cursor, stats, big_list, scan_tmp;
     // per-intersection
     DevBuf keys, keys_tmp, ids;
     // per-pixel
@@ -195,7 +195,10 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     CHECK(ensure(E.depths, (size_t)N * 4));
     CHECK(ensure(E.radii, (size_t)N * 4));
     CHECK(ensure(E.rect, (size_t)N * 8));
+    const size_t ndiff = (size_t)(cam->tiles_x + 1) * (cam->tiles_y + 1);
+    CHECK(ensure(E.tile_diff, ndiff * 4));
     CHECK(ensure(E.counts, (size_t)T * 4));
+    CHECK(ensure(E.scan_tmp, (size_t)mskern::tile_scan_temp_ints(T) * 4));
     CHECK(ensure(E.offsets, (size_t)(T + 1) * 4));
     CHECK(ensure(E.cursor, (size_t)T * 4));
     CHECK(ensure(E.stats, 16));
@@ -220,12 +223,13 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     for (int i = 0; i < ST_COUNT; ++i) E.stage_valid[i] = false;
 
     stage_mark(ST_PROJECT);
-    HIPC(hipMemsetAsync(E.counts.p, 0, (size_t)T * 4, s));
+    HIPC(hipMemsetAsync(E.tile_diff.p, 0, ndiff * 4, s));
     if (E.count_pairs) HIPC(hipMemsetAsync(E.pair_counter.p, 0, 8, s));
     mskern::launch_project_fwd(s, *cam, *g, P<float>(E.rec), P<float>(E.depths), P<int>(E.radii),
-                               P<uint32_t>(E.rect), P<int>(E.counts), nullptr);
+                               P<uint32_t>(E.rect), P<int>(E.tile_diff), nullptr);
     stage_mark(ST_SCAN);
-    mskern::launch_scan_tiles(s, T, P<int>(E.counts), P<int>(E.offsets), P<int>(E.cursor), P<int>(E.stats));
+    mskern::launch_scan_tiles(s, cam->tiles_x, cam->tiles_y, P<int>(E.tile_diff), P<int>(E.counts),
+                              P<int>(E.offsets), P<int>(E.cursor), P<int>(E.stats), P<int>(E.scan_tmp));
     HIPC(hipMemcpyAsync(E.pinned_i, E.stats.p, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
     HIPC(hipStreamSynchronize(s));
     const int I = E.pinned_i[0], max_count = E.pinned_i[1];
@@ -355,7 +359,7 @@ void msplat_hip_cleanup(void) {
     Engine &E = g_eng;
     if (!E.ready) return;
     (void)hipStreamSynchronize(E.stream);
-    DevBuf *all[] = {&E.rec, &E.depths, &E.radii, &E.rect, &E.grads16, &E.colors_raw, &E.counts, &E.offsets,
+    DevBuf *all[] = {&E.rec, &E.depths, &E.radii, &E.rect, &E.grads16, &E.colors_raw, &E.tile_diff, &E.counts, &E.scan_tmp, &E.offsets,
                      &E.cursor, &E.stats, &E.big_list, &E.keys, &E.keys_tmp, &E.ids, &E.out_img, &E.final_Ts,
                      &E.final_idx, &E.out_depth, &E.out_normal, &E.out_alpha, &E.out_median, &E.out_dist,
                      &E.dL_dimg, &E.gm1, &E.gs1, &E.gs12, &E.partials, &E.loss, &E.dmeans, &E.dscales,

@@ -14,54 +14,150 @@ namespace {
 constexpr int kSortThreads = 256;
 constexpr int kChunk = 2048;  // keys per LDS sort (16 KB of u64)
 
-// Exclusive scan of the per-tile counts by one 1024-thread workgroup; also
-// seeds the scatter cursors and records the total and the largest tile.
-__global__ __launch_bounds__(1024) void k_scan_tiles(int T, const int *__restrict__ counts,
-                                                     int *__restrict__ offsets, int *__restrict__ cursor,
-                                                     int *__restrict__ stats) {
-    __shared__ int s_sum[16];
-    __shared__ int s_max[16];
-    const int tid = threadIdx.x;
-    const int chunk = (T + 1023) / 1024;
-    const int b = min(T, tid * chunk), e = min(T, b + chunk);
-    int sum = 0, mx = 0;
-    for (int i = b; i < e; ++i) {
-        const int c = counts[i];
-        sum += c;
-        mx = max(mx, c);
+// ---- tile counts and offsets ----------------------------------------------
+//
+// k_project_fwd records each visible splat's tile rectangle [x0,x1) x [y0,y1)
+// as four +-1 corner updates of a (tiles_y + 1) x (tiles_x + 1) difference
+// array (4 atomics per splat instead of one per covered tile); the tile
+// counts are its 2D inclusive prefix sum.  Then an exclusive scan gives the
+// tile offsets (prefix_sum_kernel, msplat_metal.metal:3093-3145), the
+// scatter cursors, the intersection total and the largest tile.
+
+constexpr int kScanT = 256, kScanI = 8, kScanChunk = kScanT * kScanI;
+
+// Inclusive scan of v over a 256-thread workgroup; *total receives the sum.
+__device__ __forceinline__ int block_scan_incl(int v, int *s_w, int *total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int incl = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += o;
     }
-    // wave64 inclusive scan
-    const int lane = tid & 63, wave = tid >> 6;
+    __syncthreads();
+    if (lane == 63) s_w[wave] = incl;
+    __syncthreads();
+    int off = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kScanT / 64; ++w) {
+        off += w < wave ? s_w[w] : 0;
+        tot += s_w[w];
+    }
+    *total = tot;
+    return off + incl;
+}
+
+// Row pass: rows[y][x] = sum over x' <= x of diff[y][x'].
+__global__ __launch_bounds__(kScanT) void k_diff_rows(int tx, const int *__restrict__ diff, int *__restrict__ rows,
+                                                      int *__restrict__ stats) {
+    __shared__ int s_w[kScanT / 64];
+    const int y = blockIdx.x;
+    const int *d = diff + (size_t)y * (tx + 1);
+    int *r = rows + (size_t)y * tx;
+    int carry = 0;
+    for (int base = 0; base < tx; base += kScanT) {
+        const int x = base + (int)threadIdx.x;
+        int total;
+        const int incl = block_scan_incl(x < tx ? d[x] : 0, s_w, &total);
+        if (x < tx) r[x] = carry + incl;
+        carry += total;
+    }
+    if (y == 0 && threadIdx.x == 0) {
+        stats[1] = 0;  // largest tile, filled by k_diff_cols
+        stats[2] = 0;  // big-tile list length, filled by k_sort_tiles
+    }
+}
+
+// Column pass, in place: counts[y][x] = sum over y' <= y of rows[y'][x].
+// 64 columns per workgroup, the rows split in four runs (one per wave).
+__global__ __launch_bounds__(kScanT) void k_diff_cols(int tx, int ty, int *__restrict__ counts,
+                                                      int *__restrict__ stats) {
+    __shared__ int s_part[4][64];
+    const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
+    const int col = blockIdx.x * 64 + lane;
+    const int run_len = (ty + 3) / 4, y0 = min(ty, g * run_len), y1 = min(ty, y0 + run_len);
+    int part = 0;
+    if (col < tx)
+        for (int y = y0; y < y1; ++y) part += counts[(size_t)y * tx + col];
+    s_part[g][lane] = part;
+    __syncthreads();
+    int run = 0;
+    for (int k = 0; k < g; ++k) run += s_part[k][lane];
+    int mx = 0;
+    if (col < tx)
+        for (int y = y0; y < y1; ++y) {
+            run += counts[(size_t)y * tx + col];
+            counts[(size_t)y * tx + col] = run;
+            mx = max(mx, run);
+        }
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) mx = max(mx, __shfl_xor(mx, d, 64));
+    if (lane == 0) atomicMax(&stats[1], mx);
+}
+
+// Exclusive scan of the T tile counts: local pass (2048 counts per
+// workgroup), block totals, add pass.
+__global__ __launch_bounds__(kScanT) void k_off_local(int T, const int *__restrict__ counts,
+                                                      int *__restrict__ offsets, int *__restrict__ totals) {
+    __shared__ int s_w[kScanT / 64];
+    const int base = blockIdx.x * kScanChunk + threadIdx.x * kScanI;
+    int v[kScanI], sum = 0;
+#pragma unroll
+    for (int k = 0; k < kScanI; ++k) {
+        v[k] = base + k < T ? counts[base + k] : 0;
+        sum += v[k];
+    }
+    int total;
+    int run = block_scan_incl(sum, s_w, &total) - sum;
+#pragma unroll
+    for (int k = 0; k < kScanI; ++k) {
+        if (base + k < T) offsets[base + k] = run;
+        run += v[k];
+    }
+    if (threadIdx.x == 0) totals[blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(1024) void k_off_totals(int nb, int *__restrict__ totals, int *__restrict__ stats) {
+    __shared__ int s_w[16];
+    const int chunk = (nb + 1023) / 1024;
+    const int b = min(nb, (int)threadIdx.x * chunk), e = min(nb, b + chunk);
+    int sum = 0;
+    for (int i = b; i < e; ++i) sum += totals[i];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     int incl = sum;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
         const int o = __shfl_up(incl, d, 64);
         if (lane >= d) incl += o;
     }
-    int wmax = mx;
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) wmax = max(wmax, __shfl_xor(wmax, d, 64));
-    if (lane == 63) s_sum[wave] = incl;
-    if (lane == 0) s_max[wave] = wmax;
+    if (lane == 63) s_w[wave] = incl;
     __syncthreads();
-    int wave_off = 0, total = 0, gmax = 0;
+    int off = 0, all = 0;
     for (int w = 0; w < 16; ++w) {
-        if (w < wave) wave_off += s_sum[w];
-        total += s_sum[w];
-        gmax = max(gmax, s_max[w]);
+        off += w < wave ? s_w[w] : 0;
+        all += s_w[w];
     }
-    int run = wave_off + incl - sum;
+    int run = off + incl - sum;
     for (int i = b; i < e; ++i) {
-        offsets[i] = run;
-        cursor[i] = run;
-        run += counts[i];
+        const int t = totals[i];
+        totals[i] = run;
+        run += t;
     }
-    if (tid == 0) {
-        offsets[T] = total;
-        stats[0] = total;
-        stats[1] = gmax;
-        stats[2] = 0;  // big-tile list length, filled by k_sort_tiles
-    }
+    if (threadIdx.x == 0) stats[0] = all;
+}
+
+__global__ __launch_bounds__(kScanT) void k_off_add(int T, int *__restrict__ offsets, int *__restrict__ cursor,
+                                                    const int *__restrict__ totals, const int *__restrict__ stats) {
+    const int base = blockIdx.x * kScanChunk + threadIdx.x * kScanI;
+    const int o = totals[blockIdx.x];
+#pragma unroll
+    for (int k = 0; k < kScanI; ++k)
+        if (base + k < T) {
+            const int v = offsets[base + k] + o;
+            offsets[base + k] = v;
+            cursor[base + k] = v;
+        }
+    if (blockIdx.x == 0 && threadIdx.x == 0) offsets[T] = stats[0];
 }
 
 // Scatter: every visible gaussian appends (depth bits << 32 | id) to each
@@ -193,8 +289,17 @@ __global__ __launch_bounds__(256) void k_big_ids(const int *__restrict__ offsets
 
 namespace mskern {
 
-void launch_scan_tiles(hipStream_t s, int T, const int *counts, int *offsets, int *cursor, int *stats) {
-    hipLaunchKernelGGL(k_scan_tiles, dim3(1), dim3(1024), 0, s, T, counts, offsets, cursor, stats);
+int64_t tile_scan_temp_ints(int T) { return (T + kScanChunk - 1) / kScanChunk + 1; }
+
+void launch_scan_tiles(hipStream_t s, int tiles_x, int tiles_y, const int *diff, int *counts, int *offsets,
+                       int *cursor, int *stats, int *temp) {
+    const int T = tiles_x * tiles_y;
+    const int nb = (T + kScanChunk - 1) / kScanChunk;
+    hipLaunchKernelGGL(k_diff_rows, dim3(tiles_y), dim3(kScanT), 0, s, tiles_x, diff, counts, stats);
+    hipLaunchKernelGGL(k_diff_cols, dim3((tiles_x + 63) / 64), dim3(kScanT), 0, s, tiles_x, tiles_y, counts, stats);
+    hipLaunchKernelGGL(k_off_local, dim3(nb), dim3(kScanT), 0, s, T, counts, offsets, temp);
+    hipLaunchKernelGGL(k_off_totals, dim3(1), dim3(1024), 0, s, nb, temp, stats);
+    hipLaunchKernelGGL(k_off_add, dim3(nb), dim3(kScanT), 0, s, T, offsets, cursor, temp, stats);
 }
 
 void launch_scatter(hipStream_t s, int n, int tiles_x, const int *radii, const uint32_t *rect,

@@ -18,7 +18,7 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
     MsplatCamera cam, int n, const float *__restrict__ means, const float *__restrict__ scales,
     const float *__restrict__ quats, const float *__restrict__ opac, const float *__restrict__ fdc,
     const float *__restrict__ frest, float4 *__restrict__ rec, float *__restrict__ depths,
-    int *__restrict__ radii, uint2 *__restrict__ rect, int *__restrict__ tile_counts,
+    int *__restrict__ radii, uint2 *__restrict__ rect, int *__restrict__ tile_diff,
     float *__restrict__ colors_raw) {
     // The block's features_rest rows (up to 256 x 45 floats) are staged in LDS
     // with coalesced loads; each thread then reads its own row from LDS.
@@ -120,17 +120,15 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
         colors_raw[3 * (size_t)i + 2] = col[2];
     }
     }
-    // per-tile histogram (count pass of count -> scan -> scatter)
-    const int rw = ok ? x1 - x0 : 1;
-    const int area = ok ? (x1 - x0) * (y1 - y0) : 0;
-    const int tx = cam.tiles_x;
-    wave_expand(area, [&](int owner, int k, bool active) {
-        const int ow = __shfl(rw, owner, 64), ox = __shfl(x0, owner, 64), oy = __shfl(y0, owner, 64);
-        if (active) {
-            const int ty = k / ow;
-            atomicAdd(&tile_counts[(oy + ty) * tx + ox + (k - ty * ow)], 1);
-        }
-    });
+    // tile histogram as a 2D difference array: +1 at (x0,y0) and (x1,y1),
+    // -1 at (x1,y0) and (x0,y1); its 2D prefix sum is the per-tile count
+    if (ok && x1 > x0 && y1 > y0) {
+        const int stride = cam.tiles_x + 1;
+        atomicAdd(&tile_diff[y0 * stride + x0], 1);
+        atomicAdd(&tile_diff[y0 * stride + x1], -1);
+        atomicAdd(&tile_diff[y1 * stride + x0], -1);
+        atomicAdd(&tile_diff[y1 * stride + x1], 1);
+    }
 }
 
 // One Adam step on one element: fused_adam_kernel (msplat_metal.metal:1383-1406).
@@ -325,12 +323,12 @@ inline unsigned blocks_for(int64_t n, int b) { return (unsigned)((n + b - 1) / b
 namespace mskern {
 
 void launch_project_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, float *rec,
-                        float *depths, int *radii, uint32_t *rect, int *tile_counts, float *colors_raw) {
+                        float *depths, int *radii, uint32_t *rect, int *tile_diff, float *colors_raw) {
     if (g.num_points <= 0) return;
     hipLaunchKernelGGL(k_project_fwd, dim3(blocks_for(g.num_points, kBlock)), dim3(kBlock), 0, s, cam,
                        g.num_points, g.means, g.scales, g.quats, g.opacities, g.features_dc, g.features_rest,
                        reinterpret_cast<float4 *>(rec), depths, radii, reinterpret_cast<uint2 *>(rect),
-                       tile_counts, colors_raw);
+                       tile_diff, colors_raw);
 }
 
 void launch_project_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, const int *radii,

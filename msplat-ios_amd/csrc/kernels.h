@@ -12,8 +12,10 @@
 namespace mskern {
 
 // k_project.hip
+// tile_diff: zeroed (tiles_y + 1) x (tiles_x + 1) array receiving the +-1
+// corner updates of every visible splat's tile rectangle.
 void launch_project_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, float *rec,
-                        float *depths, int *radii, uint32_t *rect, int *tile_counts, float *colors_raw);
+                        float *depths, int *radii, uint32_t *rect, int *tile_diff, float *colors_raw);
 void launch_project_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, const int *radii,
                         const float *g16, float *dmeans, float *dscales, float *dquats, float *dmean2d,
                         float *dfdc, float *dfrest, float *grad_norm, float *vis, float *max2d,
@@ -22,7 +24,12 @@ void launch_gather(hipStream_t s, const float *src, int src_stride, int src_off,
 void launch_tiles_hit(hipStream_t s, const uint32_t *rect, const int *radii, int *out, int n);
 
 // k_binning.hip
-void launch_scan_tiles(hipStream_t s, int T, const int *counts, int *offsets, int *cursor, int *stats);
+// diff: (tiles_y + 1) x (tiles_x + 1) tile-rectangle difference array from
+// launch_project_fwd; writes counts[T], offsets[T + 1], cursor[T] and
+// stats = {intersections, largest tile, 0}.  temp: tile_scan_temp_ints(T).
+int64_t tile_scan_temp_ints(int T);
+void launch_scan_tiles(hipStream_t s, int tiles_x, int tiles_y, const int *diff, int *counts, int *offsets,
+                       int *cursor, int *stats, int *temp);
 void launch_scatter(hipStream_t s, int n, int tiles_x, const int *radii, const uint32_t *rect,
                     const float *depths, int *cursor, uint64_t *keys);
 // Returns the buffer that holds the fully sorted keys (keys or keys_tmp).
