@@ -39,8 +39,9 @@ struct Engine {
     DevBuf rec, depths, radii, rect, grads16, colors_raw;
     // per-tile
     DevBuf tile_diff, counts, offsets, cursor, stats, big_list, scan_tmp;
+    DevBuf super_diff, super_counts, super_offsets, super_cursor, super_tmp;
     // per-intersection
-    DevBuf keys, keys_tmp, ids;
+    DevBuf keys, keys_tmp, ids;  // keys: per (splat, super-tile) pair
     // per-pixel
     DevBuf out_img, final_Ts, final_idx, out_depth, out_normal, out_alpha, out_median, out_dist;
     DevBuf dL_dimg, gm1, gs1, gs12, partials, loss;
@@ -201,8 +202,17 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     CHECK(ensure(E.scan_tmp, (size_t)mskern::tile_scan_temp_ints(T) * 4));
     CHECK(ensure(E.offsets, (size_t)(T + 1) * 4));
     CHECK(ensure(E.cursor, (size_t)T * 4));
-    CHECK(ensure(E.stats, 16));
-    CHECK(ensure(E.big_list, (size_t)T * 4));
+    const int sxn = (cam->tiles_x + mskern::kSuperTile - 1) / mskern::kSuperTile;
+    const int syn = (cam->tiles_y + mskern::kSuperTile - 1) / mskern::kSuperTile;
+    const int NS = sxn * syn;
+    const size_t nsdiff = (size_t)(sxn + 1) * (syn + 1);
+    CHECK(ensure(E.super_diff, nsdiff * 4));
+    CHECK(ensure(E.super_counts, (size_t)NS * 4));
+    CHECK(ensure(E.super_offsets, (size_t)(NS + 1) * 4));
+    CHECK(ensure(E.super_cursor, (size_t)NS * 4));
+    CHECK(ensure(E.super_tmp, (size_t)mskern::tile_scan_temp_ints(NS) * 4));
+    CHECK(ensure(E.stats, 64));  // [0..2] tiles: total, largest, 0; [4..6] super-tiles: total, largest, long lists
+    CHECK(ensure(E.big_list, (size_t)NS * 4));
     CHECK(ensure(E.out_img, Pn * 12));
     CHECK(ensure(E.final_Ts, Pn * 12));
     CHECK(ensure(E.final_idx, Pn * 8));
@@ -224,29 +234,32 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
 
     stage_mark(ST_PROJECT);
     HIPC(hipMemsetAsync(E.tile_diff.p, 0, ndiff * 4, s));
+    HIPC(hipMemsetAsync(E.super_diff.p, 0, nsdiff * 4, s));
     if (E.count_pairs) HIPC(hipMemsetAsync(E.pair_counter.p, 0, 8, s));
     mskern::launch_project_fwd(s, *cam, *g, P<float>(E.rec), P<float>(E.depths), P<int>(E.radii),
-                               P<uint32_t>(E.rect), P<int>(E.tile_diff), nullptr);
+                               P<uint32_t>(E.rect), P<int>(E.tile_diff), P<int>(E.super_diff), nullptr);
     stage_mark(ST_SCAN);
     mskern::launch_scan_tiles(s, cam->tiles_x, cam->tiles_y, P<int>(E.tile_diff), P<int>(E.counts),
                               P<int>(E.offsets), P<int>(E.cursor), P<int>(E.stats), P<int>(E.scan_tmp));
-    HIPC(hipMemcpyAsync(E.pinned_i, E.stats.p, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
+    mskern::launch_scan_tiles(s, sxn, syn, P<int>(E.super_diff), P<int>(E.super_counts), P<int>(E.super_offsets),
+                              P<int>(E.super_cursor), P<int>(E.stats) + 4, P<int>(E.super_tmp));
+    HIPC(hipMemcpyAsync(E.pinned_i, E.stats.p, 8 * sizeof(int), hipMemcpyDeviceToHost, s));
     HIPC(hipStreamSynchronize(s));
-    const int I = E.pinned_i[0], max_count = E.pinned_i[1];
-    if (I < 0) {
+    const int I = E.pinned_i[0], S_total = E.pinned_i[4], super_max = E.pinned_i[5];
+    if (I < 0 || S_total < 0) {
         set_err("tile intersection count overflowed int32");
         return MSPLAT_E_CAPACITY;
     }
     E.num_isect = I;
     if (nisect) *nisect = I;
     stage_mark(ST_SCATTER_SORT);
-    CHECK(ensure(E.keys, (size_t)I * 8));
+    CHECK(ensure(E.keys, (size_t)S_total * 8));
     CHECK(ensure(E.ids, (size_t)I * 4));
-    if (max_count > 2048) CHECK(ensure(E.keys_tmp, (size_t)I * 8));
-    mskern::launch_scatter(s, N, cam->tiles_x, P<int>(E.radii), P<uint32_t>(E.rect), P<float>(E.depths),
-                           P<int>(E.cursor), P<uint64_t>(E.keys));
-    mskern::launch_sort_tiles(s, T, max_count, P<int>(E.offsets), P<uint64_t>(E.keys), P<uint64_t>(E.keys_tmp),
-                              P<int>(E.ids), P<int>(E.big_list), P<int>(E.stats));
+    if (super_max > mskern::kSuperSortChunk) CHECK(ensure(E.keys_tmp, (size_t)S_total * 8));
+    mskern::launch_bin_tiles(s, N, cam->tiles_x, cam->tiles_y, P<int>(E.radii), P<uint32_t>(E.rect),
+                             P<float>(E.depths), P<int>(E.offsets), P<int>(E.super_offsets), P<int>(E.super_cursor),
+                             super_max, P<uint64_t>(E.keys), P<uint64_t>(E.keys_tmp), P<int>(E.big_list),
+                             P<int>(E.stats) + 4, P<int>(E.ids));
     stage_mark(ST_RASTER_FWD);
     mskern::launch_raster_fwd(s, W, H, cam->tiles_x, cam->tiles_y, P<int>(E.offsets), P<int>(E.ids),
                               P<float>(E.rec), bg, P<float>(E.out_img), P<float>(E.final_Ts), P<int>(E.final_idx),
@@ -359,7 +372,7 @@ void msplat_hip_cleanup(void) {
     Engine &E = g_eng;
     if (!E.ready) return;
     (void)hipStreamSynchronize(E.stream);
-    DevBuf *all[] = {&E.rec, &E.depths, &E.radii, &E.rect, &E.grads16, &E.colors_raw, &E.tile_diff, &E.counts, &E.scan_tmp, &E.offsets,
+    DevBuf *all[] = {&E.rec, &E.depths, &E.radii, &E.rect, &E.grads16, &E.colors_raw, &E.tile_diff, &E.counts, &E.scan_tmp, &E.super_diff, &E.super_counts, &E.super_offsets, &E.super_cursor, &E.super_tmp, &E.offsets,
                      &E.cursor, &E.stats, &E.big_list, &E.keys, &E.keys_tmp, &E.ids, &E.out_img, &E.final_Ts,
                      &E.final_idx, &E.out_depth, &E.out_normal, &E.out_alpha, &E.out_median, &E.out_dist,
                      &E.dL_dimg, &E.gm1, &E.gs1, &E.gs12, &E.partials, &E.loss, &E.dmeans, &E.dscales,

@@ -18,7 +18,7 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
     MsplatCamera cam, int n, const float *__restrict__ means, const float *__restrict__ scales,
     const float *__restrict__ quats, const float *__restrict__ opac, const float *__restrict__ fdc,
     const float *__restrict__ frest, float4 *__restrict__ rec, float *__restrict__ depths,
-    int *__restrict__ radii, uint2 *__restrict__ rect, int *__restrict__ tile_diff,
+    int *__restrict__ radii, uint2 *__restrict__ rect, int *__restrict__ tile_diff, int *__restrict__ super_diff,
     float *__restrict__ colors_raw) {
     // The block's features_rest rows (up to 256 x 45 floats) are staged in LDS
     // with coalesced loads; each thread then reads its own row from LDS.
@@ -128,6 +128,14 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
         atomicAdd(&tile_diff[y0 * stride + x1], -1);
         atomicAdd(&tile_diff[y1 * stride + x0], -1);
         atomicAdd(&tile_diff[y1 * stride + x1], 1);
+        // the same for the rectangle of 4x4-tile super-tiles it touches
+        constexpr int S = mskern::kSuperTile;
+        const int sstride = (cam.tiles_x + S - 1) / S + 1;
+        const int sx0 = x0 / S, sy0 = y0 / S, sx1 = (x1 + S - 1) / S, sy1 = (y1 + S - 1) / S;
+        atomicAdd(&super_diff[sy0 * sstride + sx0], 1);
+        atomicAdd(&super_diff[sy0 * sstride + sx1], -1);
+        atomicAdd(&super_diff[sy1 * sstride + sx0], -1);
+        atomicAdd(&super_diff[sy1 * sstride + sx1], 1);
     }
 }
 
@@ -323,12 +331,13 @@ inline unsigned blocks_for(int64_t n, int b) { return (unsigned)((n + b - 1) / b
 namespace mskern {
 
 void launch_project_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, float *rec,
-                        float *depths, int *radii, uint32_t *rect, int *tile_diff, float *colors_raw) {
+                        float *depths, int *radii, uint32_t *rect, int *tile_diff, int *super_diff,
+                        float *colors_raw) {
     if (g.num_points <= 0) return;
     hipLaunchKernelGGL(k_project_fwd, dim3(blocks_for(g.num_points, kBlock)), dim3(kBlock), 0, s, cam,
                        g.num_points, g.means, g.scales, g.quats, g.opacities, g.features_dc, g.features_rest,
                        reinterpret_cast<float4 *>(rec), depths, radii, reinterpret_cast<uint2 *>(rect),
-                       tile_diff, colors_raw);
+                       tile_diff, super_diff, colors_raw);
 }
 
 void launch_project_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, const int *radii,

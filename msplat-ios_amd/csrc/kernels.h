@@ -12,10 +12,12 @@
 namespace mskern {
 
 // k_project.hip
-// tile_diff: zeroed (tiles_y + 1) x (tiles_x + 1) array receiving the +-1
-// corner updates of every visible splat's tile rectangle.
+// tile_diff / super_diff: zeroed (tiles_y + 1) x (tiles_x + 1) and
+// (syn + 1) x (sxn + 1) arrays receiving the +-1 corner updates of every
+// visible splat's tile rectangle and 4x4-tile super-tile rectangle.
 void launch_project_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, float *rec,
-                        float *depths, int *radii, uint32_t *rect, int *tile_diff, float *colors_raw);
+                        float *depths, int *radii, uint32_t *rect, int *tile_diff, int *super_diff,
+                        float *colors_raw);
 void launch_project_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, const int *radii,
                         const float *g16, float *dmeans, float *dscales, float *dquats, float *dmean2d,
                         float *dfdc, float *dfrest, float *grad_norm, float *vis, float *max2d,
@@ -30,11 +32,17 @@ void launch_tiles_hit(hipStream_t s, const uint32_t *rect, const int *radii, int
 int64_t tile_scan_temp_ints(int T);
 void launch_scan_tiles(hipStream_t s, int tiles_x, int tiles_y, const int *diff, int *counts, int *offsets,
                        int *cursor, int *stats, int *temp);
-void launch_scatter(hipStream_t s, int n, int tiles_x, const int *radii, const uint32_t *rect,
-                    const float *depths, int *cursor, uint64_t *keys);
-// Returns the buffer that holds the fully sorted keys (keys or keys_tmp).
-uint64_t *launch_sort_tiles(hipStream_t s, int T, int max_count, const int *offsets, uint64_t *keys,
-                            uint64_t *keys_tmp, int *ids, int *big_list, int *stats);
+// Super-tiles are 4x4 tiles: sxn = ceil(tiles_x / 4), syn = ceil(tiles_y / 4).
+// super_offsets / super_cursor / super_stats come from launch_scan_tiles on
+// the super-tile difference array; super_max is its largest list,
+// super_keys_tmp is needed (size of super_keys) when super_max > 4096.
+// Writes the per-tile sorted gaussian ids at tile_offsets.
+void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
+                      const float *depths, const int *tile_offsets, const int *super_offsets, int *super_cursor,
+                      int super_max, uint64_t *super_keys, uint64_t *super_keys_tmp, int *big_list,
+                      int *super_stats, int *ids);
+constexpr int kSuperTile = 4;
+constexpr int kSuperSortChunk = 4096;
 
 // k_raster.hip
 void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
