@@ -42,6 +42,7 @@ struct Engine {
     DevBuf super_diff, super_counts, super_offsets, super_cursor, super_tmp;
     // per-intersection
     DevBuf keys, keys_tmp, ids;  // keys: per (splat, super-tile) pair
+    DevBuf blend_log, t_ckpt, wave_cnt;  // the raster forward's per-wave blend log
     // per-pixel
     DevBuf out_img, final_Ts, final_idx, out_depth, out_normal, out_alpha, out_median, out_dist;
     DevBuf dL_dimg, gm1, gs1, gs12, partials, loss;
@@ -57,6 +58,7 @@ struct Engine {
     int64_t num_isect = 0;
     const float *bg = nullptr;
     bool have_grads = false;
+    bool log_valid = false;  // blend log written by the most recent forward
     // timing
     bool timing = false;       // HIP events per stage
     bool count_pairs = false;  // raster pair counter
@@ -180,7 +182,32 @@ int validate_cam(const MsplatCamera *cam, const MsplatGaussians *g) {
 }
 
 // Stages a3-a7: projection, binning, per-tile sort, rasterize forward.
-int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, int64_t *nisect) {
+// With log, the raster forward also writes the blend log the backward replays.
+int raster_fwd_locked(bool log) {
+    Engine &E = g_eng;
+    uint32_t *lg = nullptr;
+    float *tc = nullptr;
+    int *wc = nullptr;
+    if (log) {
+        CHECK(ensure(E.blend_log, (size_t)4 * (size_t)E.num_isect * mskern::kBlendLogEntryBytes));
+        // a checkpoint is 64 floats from its log slot on, so the last wave's
+        // may reach 63 floats past 4 * I
+        CHECK(ensure(E.t_ckpt, ((size_t)4 * (size_t)E.num_isect + 64) * 4));
+        CHECK(ensure(E.wave_cnt, (size_t)4 * E.tiles_x * E.tiles_y * 4));
+        lg = P<uint32_t>(E.blend_log);
+        tc = P<float>(E.t_ckpt);
+        wc = P<int>(E.wave_cnt);
+    }
+    mskern::launch_raster_fwd(E.stream, E.W, E.H, E.tiles_x, E.tiles_y, P<int>(E.offsets), P<int>(E.ids),
+                              P<float>(E.rec), E.bg, P<float>(E.out_img), P<float>(E.final_Ts), P<int>(E.final_idx),
+                              P<float>(E.out_depth), P<float>(E.out_normal), P<float>(E.out_alpha),
+                              P<float>(E.out_median), P<float>(E.out_dist),
+                              E.count_pairs ? P<unsigned long long>(E.pair_counter) : nullptr, lg, tc, wc);
+    E.log_valid = log;
+    return MSPLAT_OK;
+}
+
+int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, int64_t *nisect, bool log) {
     CHECK(validate_cam(cam, g));
     if (!bg) {
         set_err("null background");
@@ -230,6 +257,7 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     E.K3 = (nb - 1) * 3;
     E.bg = bg;
     E.have_grads = false;
+    E.log_valid = false;
     for (int i = 0; i < ST_COUNT; ++i) E.stage_valid[i] = false;
 
     stage_mark(ST_PROJECT);
@@ -261,11 +289,7 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
                              super_max, P<uint64_t>(E.keys), P<uint64_t>(E.keys_tmp), P<int>(E.big_list),
                              P<int>(E.stats) + 4, P<int>(E.ids));
     stage_mark(ST_RASTER_FWD);
-    mskern::launch_raster_fwd(s, W, H, cam->tiles_x, cam->tiles_y, P<int>(E.offsets), P<int>(E.ids),
-                              P<float>(E.rec), bg, P<float>(E.out_img), P<float>(E.final_Ts), P<int>(E.final_idx),
-                              P<float>(E.out_depth), P<float>(E.out_normal), P<float>(E.out_alpha),
-                              P<float>(E.out_median), P<float>(E.out_dist),
-                              E.count_pairs ? P<unsigned long long>(E.pair_counter) : nullptr);
+    CHECK(raster_fwd_locked(log));
     HIPC(hipGetLastError());
     return MSPLAT_OK;
 }
@@ -373,7 +397,7 @@ void msplat_hip_cleanup(void) {
     if (!E.ready) return;
     (void)hipStreamSynchronize(E.stream);
     DevBuf *all[] = {&E.rec, &E.depths, &E.radii, &E.rect, &E.grads16, &E.colors_raw, &E.tile_diff, &E.counts, &E.scan_tmp, &E.super_diff, &E.super_counts, &E.super_offsets, &E.super_cursor, &E.super_tmp, &E.offsets,
-                     &E.cursor, &E.stats, &E.big_list, &E.keys, &E.keys_tmp, &E.ids, &E.out_img, &E.final_Ts,
+                     &E.cursor, &E.stats, &E.big_list, &E.keys, &E.keys_tmp, &E.ids, &E.blend_log, &E.t_ckpt, &E.wave_cnt, &E.out_img, &E.final_Ts,
                      &E.final_idx, &E.out_depth, &E.out_normal, &E.out_alpha, &E.out_median, &E.out_dist,
                      &E.dL_dimg, &E.gm1, &E.gs1, &E.gs12, &E.partials, &E.loss, &E.dmeans, &E.dscales,
                      &E.dquats, &E.dmean2d, &E.dfdc, &E.dfrest, &E.dens_flags, &E.dens_scan, &E.pair_counter};
@@ -392,6 +416,7 @@ void msplat_hip_cleanup(void) {
     E.n = 0;
     E.num_isect = 0;
     E.have_grads = false;
+    E.log_valid = false;
 }
 
 const char *msplat_hip_last_error(void) { return g_err; }
@@ -476,7 +501,7 @@ int msplat_hip_sync(void) {
 int msplat_hip_render(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, int64_t *nisect) {
     API_BEGIN
     ENSURE_INIT();
-    CHECK(forward_locked(cam, g, bg, nisect));
+    CHECK(forward_locked(cam, g, bg, nisect, false));
     stage_mark(ST_LOSS);
     if (g_eng.count_pairs) HIPC(hipMemcpy(&g_eng.pairs, g_eng.pair_counter.p, 8, hipMemcpyDeviceToHost));
     if (g_eng.timing) {
@@ -502,7 +527,7 @@ int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g, con
     }
     Engine &E = g_eng;
     hipStream_t s = E.stream;
-    CHECK(forward_locked(cam, g, bg, nisect));
+    CHECK(forward_locked(cam, g, bg, nisect, true));
     const int N = g->num_points, W = cam->width, H = cam->height;
     const size_t Pn = (size_t)W * H;
     stage_mark(ST_LOSS);
@@ -515,9 +540,10 @@ int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g, con
     HIPC(hipMemsetAsync(E.grads16.p, 0, (size_t)N * 64, s));
     const float inv_np = 1.0f / (float)((unsigned)H * (unsigned)W * 3u);
     const float ddist_uniform = lambda_dist * (inv_np * 3.0f);
-    mskern::launch_raster_bwd(s, W, H, cam->tiles_x, cam->tiles_y, P<int>(E.offsets), P<int>(E.ids),
-                              P<float>(E.rec), bg, P<float>(E.final_Ts), P<int>(E.final_idx), P<float>(E.dL_dimg),
-                              nullptr, nullptr, nullptr, nullptr, nullptr, ddist_uniform, P<float>(E.grads16));
+    mskern::launch_raster_bwd(s, W, H, cam->tiles_x, cam->tiles_y, P<int>(E.offsets), P<uint32_t>(E.blend_log),
+                              P<float>(E.t_ckpt), P<int>(E.wave_cnt), P<float>(E.rec), bg, P<float>(E.final_Ts),
+                              P<int>(E.final_idx), P<float>(E.dL_dimg), nullptr, nullptr, nullptr, nullptr, nullptr,
+                              ddist_uniform, P<float>(E.grads16));
     stage_mark(ST_PROJECT_BWD);
     if (adam) {
         mskern::launch_project_bwd(s, *cam, *g, P<int>(E.radii), P<float>(E.grads16), nullptr, nullptr, nullptr,
@@ -665,9 +691,13 @@ int msplat_hip_raster_bwd(const float *dL_dimg, const float *dL_ddepth, const fl
         set_err("raster_bwd needs a preceding forward and dL_dimg / grads16");
         return MSPLAT_E_ARG;
     }
-    mskern::launch_raster_bwd(E.stream, E.W, E.H, E.tiles_x, E.tiles_y, P<int>(E.offsets), P<int>(E.ids),
-                              P<float>(E.rec), E.bg, P<float>(E.final_Ts), P<int>(E.final_idx), dL_dimg, dL_ddepth,
-                              dL_dalpha, dL_dnormal, dL_dmedian, dL_ddist, 0.0f, grads16);
+    // a render-only forward skips the blend log; replay the (deterministic)
+    // raster forward with it
+    if (!E.log_valid) CHECK(raster_fwd_locked(true));
+    mskern::launch_raster_bwd(E.stream, E.W, E.H, E.tiles_x, E.tiles_y, P<int>(E.offsets), P<uint32_t>(E.blend_log),
+                              P<float>(E.t_ckpt), P<int>(E.wave_cnt), P<float>(E.rec), E.bg, P<float>(E.final_Ts),
+                              P<int>(E.final_idx), dL_dimg, dL_ddepth, dL_dalpha, dL_dnormal, dL_dmedian, dL_ddist,
+                              0.0f, grads16);
     HIPC(hipGetLastError());
     return MSPLAT_OK;
     API_END

@@ -57,30 +57,46 @@ __device__ __forceinline__ int build_wave_lists(int m, unsigned char (*s_list)[k
             s_list[w][off] = (unsigned char)threadIdx.x;
         }
     }
-    const int n = s_cnt[0][wave] + s_cnt[1][wave] + s_cnt[2][wave] + s_cnt[3][wave];
+    // wave-uniform: keeps the visit loop's control in scalar registers
+    const int n = __builtin_amdgcn_readfirstlane(s_cnt[0][wave] + s_cnt[1][wave] + s_cnt[2][wave] + s_cnt[3][wave]);
     __syncthreads();
     return n;
 }
 
 // nd_rasterize_forward_2dgs_kernel (msplat_metal.metal:553-754).
+// With LOG, every wave also writes its blend log for the backward: one entry
+// {ballot low, ballot high, list position, splat id} for each visited list
+// entry that at least one of its lanes blended, in visit (front-to-back)
+// order, at blend_log[4 * start + wave * len + k] (len = the tile's list
+// length, which bounds a wave's visits); wave_cnt[4 * tile + wave] receives
+// the entry count.  Bit l of the ballot is set when lane l's pixel blended
+// the splat, so the backward replays exactly the forward's decisions.  At
+// every log entry k > 0 with k % 64 == 0 each lane also stores its
+// transmittance before that splat (a prefix checkpoint) at
+// t_ckpt[4 * start + wave * len + k + lane].
+template <bool LOG>
 __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     int W, int H, int tiles_x, int T, const int *__restrict__ offsets, const int *__restrict__ ids,
     const float4 *__restrict__ rec, const float *__restrict__ bgp, float *__restrict__ out_img,
     float *__restrict__ final_Ts, int *__restrict__ final_idx, float *__restrict__ out_depth,
     float *__restrict__ out_normal, float *__restrict__ out_alpha, float *__restrict__ out_median,
-    float *__restrict__ out_dist, unsigned long long *__restrict__ pair_counter) {
+    float *__restrict__ out_dist, unsigned long long *__restrict__ pair_counter, uint4 *__restrict__ blend_log,
+    float *__restrict__ t_ckpt, int *__restrict__ wave_cnt) {
     const int tile = xcd_tile(blockIdx.x, T);
     if (tile >= T) return;
     __shared__ float4 s_rec[5 * kThreads];
+    __shared__ int s_id[LOG ? kThreads : 1];
     const int tx = tile % tiles_x, ty = tile / tiles_x;
-    const int wave = threadIdx.x >> 6;
-    const int pxi = tx * 16 + lane_px(threadIdx.x >> 6, threadIdx.x & 63);
-    const int pyi = ty * 16 + lane_py(threadIdx.x >> 6, threadIdx.x & 63);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int pxi = tx * 16 + lane_px(wave, lane);
+    const int pyi = ty * 16 + lane_py(wave, lane);
     const bool inside = pxi < W && pyi < H;
     const float px = (float)pxi, py = (float)pyi;
     const float sx0 = (float)(tx * 16), sy0 = (float)(ty * 16);
     const int start = offsets[tile], end = offsets[tile + 1];
     const float bg0 = bgp[0], bg1 = bgp[1], bg2 = bgp[2];
+    const size_t log_base = 4 * (size_t)start + (size_t)wave * (size_t)(end - start);
+    int nlog = 0;  // wave-uniform
 
     float Tr = 1.f, cr = 0.f, cg = 0.f, cb = 0.f, dep = 0.f, nx = 0.f, ny = 0.f, nz = 0.f;
     float M1 = 0.f, M2 = 0.f, dist = 0.f, med = 0.f;
@@ -93,45 +109,63 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     for (int b0 = start; b0 < end; b0 += kThreads) {
         if (__syncthreads_and(done)) break;
         const int idx = b0 + (int)threadIdx.x;
-        const int m = idx < end ? load_batch(rec, ids[idx], s_rec, sx0, sy0) : 0;
+        const int gid = idx < end ? ids[idx] : 0;
+        if (LOG) s_id[threadIdx.x] = gid;
+        const int m = idx < end ? load_batch(rec, gid, s_rec, sx0, sy0) : 0;
         const int n = build_wave_lists(m, s_list, s_cnt);
-        if (done) continue;
+        if (__all(done)) continue;
         const int base = b0 - start + 1;  // contributor number of slot 0 (1-based)
-        int j = 0;
-        for (; j < n; ++j) {
+        for (int j = 0; j < n; ++j) {
             const int t = s_list[wave][j];
-            const float4 q0 = s_rec[t], q1 = s_rec[kThreads + t], q2 = s_rec[2 * kThreads + t];
-            PairEval e;
-            if (!eval_pair(px, py, q0, q1, q2, e)) continue;
-            const float next_T = Tr * (1.0f - e.alpha);
-            if (next_T <= 1e-4f) {
-                done = true;
-                ++j;
-                break;
+            const float T_before = Tr;
+            bool blend = false;
+            if (!done) {
+                ++evals;
+                const float4 q0 = s_rec[t], q1 = s_rec[kThreads + t], q2 = s_rec[2 * kThreads + t];
+                PairEval e;
+                if (eval_pair(px, py, q0, q1, q2, e)) {
+                    const float next_T = Tr * (1.0f - e.alpha);
+                    if (next_T <= 1e-4f) {
+                        done = true;
+                    } else {
+                        blend = true;
+                        const float w = e.alpha * Tr;
+                        const float A = 1.f - Tr;
+                        const float m_ = kMScale * (1.f - NEAR_N / e.depth);
+                        dist = __builtin_fmaf(m_ * m_ * A + M2 - 2.f * m_ * M1, w, dist);
+                        M1 = __builtin_fmaf(m_, w, M1);
+                        M2 = __builtin_fmaf(m_ * m_, w, M2);
+                        if (Tr > 0.5f) {
+                            med = e.depth;
+                            med_c = base + t;
+                        }
+                        const float4 q3 = s_rec[3 * kThreads + t], q4 = s_rec[4 * kThreads + t];
+                        cr = __builtin_fmaf(q3.w, w, cr);
+                        cg = __builtin_fmaf(q4.x, w, cg);
+                        cb = __builtin_fmaf(q4.y, w, cb);
+                        dep = __builtin_fmaf(e.depth, w, dep);
+                        nx = __builtin_fmaf(q3.x, w, nx);
+                        ny = __builtin_fmaf(q3.y, w, ny);
+                        nz = __builtin_fmaf(q3.z, w, nz);
+                        Tr = next_T;
+                        last_c = base + t;
+                    }
+                }
             }
-            const float w = e.alpha * Tr;
-            const float A = 1.f - Tr;
-            const float m_ = kMScale * (1.f - NEAR_N / e.depth);
-            dist = __builtin_fmaf(m_ * m_ * A + M2 - 2.f * m_ * M1, w, dist);
-            M1 = __builtin_fmaf(m_, w, M1);
-            M2 = __builtin_fmaf(m_ * m_, w, M2);
-            if (Tr > 0.5f) {
-                med = e.depth;
-                med_c = base + t;
+            if (LOG) {
+                const unsigned long long bal = __ballot(blend);
+                if (bal) {
+                    if (lane == 0)
+                        blend_log[log_base + nlog] =
+                            make_uint4((unsigned)bal, (unsigned)(bal >> 32), (unsigned)(base - 1 + t), (unsigned)s_id[t]);
+                    if ((nlog & 63) == 0 && nlog > 0) t_ckpt[log_base + nlog + lane] = T_before;
+                    ++nlog;
+                }
             }
-            const float4 q3 = s_rec[3 * kThreads + t], q4 = s_rec[4 * kThreads + t];
-            cr = __builtin_fmaf(q3.w, w, cr);
-            cg = __builtin_fmaf(q4.x, w, cg);
-            cb = __builtin_fmaf(q4.y, w, cb);
-            dep = __builtin_fmaf(e.depth, w, dep);
-            nx = __builtin_fmaf(q3.x, w, nx);
-            ny = __builtin_fmaf(q3.y, w, ny);
-            nz = __builtin_fmaf(q3.z, w, nz);
-            Tr = next_T;
-            last_c = base + t;
+            if (__all(done)) break;
         }
-        evals += j;
     }
+    if (LOG && lane == 0) wave_cnt[4 * tile + wave] = nlog;
     if (pair_counter) {
         __shared__ unsigned int s_pairs;
         __syncthreads();
@@ -213,189 +247,250 @@ __device__ __forceinline__ float wave_reduce16(float v[16], int lane) {
     return v[0];
 }
 
-// nd_rasterize_backward_2dgs_kernel (msplat_metal.metal:1705-1979).
-// Back-to-front replay starting at the tile's largest last_contributor (the
-// reference starts at the end of the full list).  The skip decisions reuse
-// the forward's exact arithmetic (eval_pair); quantities that only scale
-// gradients use hardware reciprocals.  Per-splat gradients
-// [dL_dtransMat 9, dL_dnormal3D 3, dL_dopacity 1, dL_dcolors 3] are reduced
-// across the wave and added with one 16-lane global float atomic (one 64-byte
-// line) per (wave, splat); with the strip masks a splat is evaluated by
-// about 1.3 of the tile's four waves, so this issues no more atomic requests
-// than a per-tile merge in LDS would, without its LDS array, zeroing and
-// flush barrier.
+// Orders this wave's LDS stores before its later LDS loads (and the loads of
+// one chunk before the stores of the next): a wave's LDS operations execute
+// in program order, so only the compiler has to be kept from moving them.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// nd_rasterize_backward_2dgs_kernel (msplat_metal.metal:1705-1979) over the
+// forward's blend log, with prefix/suffix transmittance.
+//
+// Each wave replays its blend log back to front in 64-entry chunks.  The
+// log's ballots carry the forward's exact blend decisions, so the backward
+// needs neither the strip masks nor the forward's correctly rounded ray
+// division and exp: u, v, G and alpha only scale gradients and use the
+// hardware reciprocal and exp2.  The suffix sums (colour, and in the full
+// case depth, alpha, normal and the distortion term) follow the reference's
+// back-to-front recurrences (:1846-1916), whose rounding error scales with
+// the transmittance.  The transmittance itself is a prefix: at the end of
+// every chunk it is re-anchored to the forward's checkpoint (the exact
+// product the forward computed), and inside a chunk it is recovered by at
+// most 64 divisions T_i = T_{i+1} / (1 - alpha_i); the reference recovers it
+// by division over the whole list from T_final (:1858).
+// The 16 per-splat gradients [dL_dtransMat 9, dL_dnormal3D 3, dL_dopacity,
+// dL_dcolors 3] are reduced across the wave and added with one 16-lane
+// global float atomic (one 64-byte line) per (wave, splat).
 // FULL = false is the training step's case: the only upstream gradient is
-// dL/dimage (depth, alpha, normal, median-depth and distortion gradients are
-// zero), so those terms are compiled out.
+// dL/dimage, so the depth / alpha / normal / median / distortion terms are
+// compiled out, the colour suffix is carried as its projection on dL/dimage
+// and the per-splat factors (opacity, colour clamp masks) are applied once
+// after the wave reduction.
 template <bool FULL>
 __global__ __launch_bounds__(kThreads) void k_raster_bwd(
-    int W, int H, int tiles_x, int T, const int *__restrict__ offsets, const int *__restrict__ ids,
-    const float4 *__restrict__ rec, const float *__restrict__ bgp, const float *__restrict__ final_Ts,
-    const int *__restrict__ final_idx, const float *__restrict__ dL_dimg, const float *__restrict__ dL_ddepth,
-    const float *__restrict__ dL_daccum, const float *__restrict__ dL_dnormal,
-    const float *__restrict__ dL_dmedian, const float *__restrict__ dL_ddist, float ddist_uniform,
-    float *__restrict__ grads16) {
+    int W, int H, int tiles_x, int T, const int *__restrict__ offsets, const uint4 *__restrict__ blend_log,
+    const float *__restrict__ t_ckpt, const int *__restrict__ wave_cnt, const float4 *__restrict__ rec,
+    const float *__restrict__ bgp, const float *__restrict__ final_Ts, const int *__restrict__ final_idx,
+    const float *__restrict__ dL_dimg, const float *__restrict__ dL_ddepth, const float *__restrict__ dL_daccum,
+    const float *__restrict__ dL_dnormal, const float *__restrict__ dL_dmedian, const float *__restrict__ dL_ddist,
+    float ddist_uniform, float *__restrict__ grads16) {
     const int tile = xcd_tile(blockIdx.x, T);
     if (tile >= T) return;
-    __shared__ float4 s_rec[5 * kThreads];
-    __shared__ unsigned char s_list[4][kThreads];
-    __shared__ int s_cnt[4][4];
-    __shared__ int s_id[kThreads];
-    __shared__ int s_maxlast;
+    constexpr int kWave = 64;
+    __shared__ float4 s_r[4][5][kWave];
+    __shared__ uint4 s_e[4][kWave];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int tx = tile % tiles_x, ty = tile / tiles_x;
-    const int pxi = tx * 16 + lane_px(threadIdx.x >> 6, threadIdx.x & 63);
-    const int pyi = ty * 16 + lane_py(threadIdx.x >> 6, threadIdx.x & 63);
+    const int pxi = tx * 16 + lane_px(wave, lane);
+    const int pyi = ty * 16 + lane_py(wave, lane);
     const bool inside = pxi < W && pyi < H;
     const float px = (float)pxi, py = (float)pyi;
-    const float sx0 = (float)(tx * 16), sy0 = (float)(ty * 16);
-    const int start = offsets[tile];
+    const int start = offsets[tile], len = offsets[tile + 1] - start;
+    const int nlog = __builtin_amdgcn_readfirstlane(wave_cnt[4 * tile + wave]);
+    const size_t log_base = 4 * (size_t)start + (size_t)wave * (size_t)len;
+    const uint4 *lg = blend_log + log_base;
     const size_t pix = inside ? (size_t)pyi * W + pxi : 0;
 
-    float T_final = 0.f, final_D = 0.f, final_D2 = 0.f;
-    int my_last = 0, med_c = -1;
-    float dpix[3] = {0.f, 0.f, 0.f}, dn2[3] = {0.f, 0.f, 0.f};
-    float ddepth = 0.f, daccum = 0.f, dmed = 0.f, dreg = 0.f;
+    float T_final = 1.f, dp0 = 0.f, dp1 = 0.f, dp2 = 0.f;
+    float dn0 = 0.f, dn1 = 0.f, dn2 = 0.f, ddep = 0.f, dacc = 0.f, dmed = 0.f, dreg = 0.f;
+    float fD = 0.f, fD2 = 0.f;
+    int med_pos = -2;
     if (inside) {
         T_final = final_Ts[3 * pix];
-        my_last = final_idx[2 * pix];
-        dpix[0] = dL_dimg[3 * pix];
-        dpix[1] = dL_dimg[3 * pix + 1];
-        dpix[2] = dL_dimg[3 * pix + 2];
+        dp0 = dL_dimg[3 * pix];
+        dp1 = dL_dimg[3 * pix + 1];
+        dp2 = dL_dimg[3 * pix + 2];
         if (FULL) {
-            final_D = final_Ts[3 * pix + 1];
-            final_D2 = final_Ts[3 * pix + 2];
-            med_c = final_idx[2 * pix + 1];
-            if (dL_ddepth) ddepth = dL_ddepth[pix];
-            if (dL_daccum) daccum = dL_daccum[pix];
+            fD = final_Ts[3 * pix + 1];
+            fD2 = final_Ts[3 * pix + 2];
+            med_pos = final_idx[2 * pix + 1] - 1;
+            if (dL_ddepth) ddep = dL_ddepth[pix];
+            if (dL_daccum) dacc = dL_daccum[pix];
             if (dL_dnormal) {
-                dn2[0] = dL_dnormal[3 * pix];
-                dn2[1] = dL_dnormal[3 * pix + 1];
-                dn2[2] = dL_dnormal[3 * pix + 2];
+                dn0 = dL_dnormal[3 * pix];
+                dn1 = dL_dnormal[3 * pix + 1];
+                dn2 = dL_dnormal[3 * pix + 2];
             }
             if (dL_dmedian) dmed = dL_dmedian[pix];
             dreg = dL_ddist ? dL_ddist[pix] : ddist_uniform;
         }
     }
-    const float final_A = 1.0f - T_final;
-    const float bg_dot = bgp[0] * dpix[0] + bgp[1] * dpix[1] + bgp[2] * dpix[2];
+    const float fA = 1.0f - T_final;
+    const float bgT = -T_final * (bgp[0] * dp0 + bgp[1] * dp1 + bgp[2] * dp2);
+    // lane l of the reduction ends with component vi (see wave_reduce16)
+    const int vi = ((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 + ((lane >> 2) & 1);
+    // post-reduction factor in the image-only case: opa for the T rows (the
+    // sign of the last column folded in), opa (1 - opa) for the opacity
+    // logit, 1 for the colours, 0 for the normals
+    const float fa = vi < 6 ? 1.f : vi < 9 ? -1.f : vi == 12 ? 1.f : 0.f;
+    const float fb = vi == 12 ? -1.f : 0.f;
+    const float fc = vi >= 13 ? 1.f : 0.f;
+    const int ch = vi - 13;
 
-    if (threadIdx.x == 0) s_maxlast = 0;
-    __syncthreads();
-    if (my_last > 0) atomicMax(&s_maxlast, my_last);
-    __syncthreads();
-    const int n_it = s_maxlast;
+    // suffix state of the reference's recurrences (image-only: the colour
+    // suffix projected on dL/dimage)
+    float last_alpha = 0.f, acc_v = 0.f, last_v = 0.f;
+    float acc_c[3] = {0.f, 0.f, 0.f}, last_c[3] = {0.f, 0.f, 0.f};
+    float acc_d = 0.f, last_d = 0.f, acc_a = 0.f, last_dLdT = 0.f;
+    float acc_n[3] = {0.f, 0.f, 0.f}, last_n[3] = {0.f, 0.f, 0.f};
 
-    float Tr = T_final;
-    float accum_rec[3] = {0.f, 0.f, 0.f}, last_color[3] = {0.f, 0.f, 0.f};
-    float last_alpha = 0.f, accum_depth_rec = 0.f, last_depth = 0.f, accum_alpha_rec = 0.f;
-    float accum_normal_rec[3] = {0.f, 0.f, 0.f}, last_normal[3] = {0.f, 0.f, 0.f};
-    float last_dL_dT = 0.f;
-
-    for (int hi = n_it; hi > 0; hi -= kThreads) {
-        const int bs = min(kThreads, hi);
-        __syncthreads();
-        int m = 0;
-        if ((int)threadIdx.x < bs) {
-            const int gid = ids[start + hi - 1 - (int)threadIdx.x];
-            s_id[threadIdx.x] = gid;
-            m = load_batch(rec, gid, s_rec, sx0, sy0);
+    const int nchunks = (nlog + kWave - 1) / kWave;
+    for (int c = nchunks - 1; c >= 0; --c) {
+        const int c0 = c * kWave;
+        const int m = min(kWave, nlog - c0);
+        // transmittance after the chunk's last splat: the next chunk's
+        // prefix checkpoint, or the final transmittance
+        float Tr = c == nchunks - 1 ? T_final : t_ckpt[log_base + c0 + kWave + lane];
+        if (lane < m) {
+            const uint4 e = lg[c0 + lane];
+            const float4 *r = rec + 5 * (size_t)e.w;
+#pragma unroll
+            for (int k = 0; k < 5; ++k) s_r[wave][k][lane] = r[k];
+            s_e[wave][lane] = e;
         }
-        const int n = build_wave_lists(m, s_list, s_cnt);
-        for (int j = 0; j < n; ++j) {
-            const int t = s_list[wave][j];
-            const int c = hi - 1 - t;
-            float v[16];
+        wave_lds_sync();
+        for (int j = m - 1; j >= 0; --j) {
+            const uint4 e = s_e[wave][j];
+            const unsigned bal = lane < 32 ? e.x : e.y;
+            const bool has = (bal >> (lane & 31)) & 1u;
+            const float4 q0 = s_r[wave][0][j], q1 = s_r[wave][1][j], q2 = s_r[wave][2][j];
+            const float4 q3 = s_r[wave][3][j], q4 = s_r[wave][4][j];
+            const float Tux = q0.x, Tuy = q0.y, Tuz = q0.z, Tvx = q0.w, Tvy = q1.x, Tvz = q1.y;
+            const float Twx = q1.z, Twy = q1.w, Twz = q2.x, opa = q2.w;
+            const f3 k = {__builtin_fmaf(px, Twx, -Tux), __builtin_fmaf(px, Twy, -Tuy),
+                          __builtin_fmaf(px, Twz, -Tuz)};
+            const f3 l = {__builtin_fmaf(py, Twx, -Tvx), __builtin_fmaf(py, Twy, -Tvy),
+                          __builtin_fmaf(py, Twz, -Tvz)};
+            // the forward's ray.z, bit for bit (non-zero wherever the lane blended)
+            const float rz = __builtin_fmaf(k.x, l.y, -(k.y * l.x));
+            const float inv_z = has ? __builtin_amdgcn_rcpf(rz) : 0.f;
+            const float u = __builtin_fmaf(k.y, l.z, -(k.z * l.y)) * inv_z;
+            const float v = __builtin_fmaf(k.z, l.x, -(k.x * l.z)) * inv_z;
+            const float rho3d = __builtin_fmaf(u, u, v * v);
+            const float dxs = q2.y - px, dys = q2.z - py;
+            const float rho2d = FILTER_INV_SQ * __builtin_fmaf(dxs, dxs, dys * dys);
+            const bool use3d = rho3d <= rho2d;
+            const float G = __builtin_amdgcn_exp2f(__builtin_fminf(rho3d, rho2d) * -0.72134752044448170368f);
+            const float alpha = has ? __builtin_fminf(0.99f, opa * G) : 0.f;
+            const float inv_om = __builtin_amdgcn_rcpf(1.0f - alpha);
+            Tr *= inv_om;  // transmittance before this splat (unchanged where it did not blend)
+            const float aT = alpha * Tr;
+            float v16[16];
+            if (!FULL) {
+                const float vv = dp0 * q3.w + dp1 * q4.x + dp2 * q4.y;  // dL/dimage . colour
+                const float acc_new = __builtin_fmaf(last_alpha, last_v - acc_v, acc_v);
+                acc_v = has ? acc_new : acc_v;
+                last_v = has ? vv : last_v;
+                last_alpha = has ? alpha : last_alpha;
+                const float dLda = __builtin_fmaf(vv - acc_v, Tr, bgT * inv_om);
+                const float gg = has ? dLda * G : 0.f;
+                const float gT = use3d ? gg : 0.f;
+                // dL/d(ray-splat point) up to the factor -opa: (gT u, gT v) / ray.z
+                const float dsx = gT * u * inv_z, dsy = gT * v * inv_z;
+                const float dpz = -__builtin_fmaf(dsx, u, dsy * v);
+                const f3 dk = {l.y * dpz - l.z * dsy, l.z * dsx - l.x * dpz, l.x * dsy - l.y * dsx};
+                const f3 dl = {dsy * k.z - dpz * k.y, dpz * k.x - dsx * k.z, dsx * k.y - dsy * k.x};
+                v16[0] = dk.x;
+                v16[1] = dk.y;
+                v16[2] = dk.z;
+                v16[3] = dl.x;
+                v16[4] = dl.y;
+                v16[5] = dl.z;
+                v16[6] = __builtin_fmaf(px, dk.x, py * dl.x);
+                v16[7] = __builtin_fmaf(px, dk.y, py * dl.y);
+                v16[8] = __builtin_fmaf(px, dk.z, py * dl.z);
+                v16[9] = 0.f;
+                v16[10] = 0.f;
+                v16[11] = 0.f;
+                v16[12] = gg;
+                v16[13] = aT * dp0;
+                v16[14] = aT * dp1;
+                v16[15] = aT * dp2;
+            } else {
+                // lanes that did not blend get a finite stand-in (their terms are zeroed)
+                const float depth = has ? __builtin_fmaf(u, Twx, __builtin_fmaf(v, Twy, Twz)) : 1.0f;
+                const float cu[3] = {q3.w, q4.x, q4.y}, nrm[3] = {q3.x, q3.y, q3.z};
+                const float dpix[3] = {dp0, dp1, dp2}, dn[3] = {dn0, dn1, dn2};
+                float dL_dalpha = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 16; ++k) v[k] = 0.f;
-            bool has = false;
-            if (c < my_last) {
-                const float4 q0 = s_rec[t], q1 = s_rec[kThreads + t], q2 = s_rec[2 * kThreads + t];
-                PairEval e;
-                if (eval_pair(px, py, q0, q1, q2, e)) {
-                    has = true;
-                    const float4 q3 = s_rec[3 * kThreads + t], q4 = s_rec[4 * kThreads + t];
-                    const float alpha = e.alpha, G = e.G, opa = q2.w;
-                    const float inv_1ma = __builtin_amdgcn_rcpf(1.0f - alpha);
-                    Tr = Tr * inv_1ma;
-                    const float aT = alpha * Tr;
-                    float dL_dalpha = 0.0f;
-                    const float cu[3] = {q3.w, q4.x, q4.y};
-#pragma unroll
-                    for (int ch = 0; ch < 3; ++ch) {
-                        const float mask = cu[ch] > 0.0f ? 1.0f : 0.0f;
-                        accum_rec[ch] = last_alpha * last_color[ch] + (1.f - last_alpha) * accum_rec[ch];
-                        last_color[ch] = cu[ch];
-                        dL_dalpha += (cu[ch] - accum_rec[ch]) * dpix[ch];
-                        v[13 + ch] = aT * dpix[ch] * mask;
-                    }
-                    float dL_dz = 0.0f;
-                    if (FULL) {
-                        float dL_dweight = 0.0f;
-                        const float inv_d = __builtin_amdgcn_rcpf(e.depth);
-                        const float m_d = kMScale * (1.0f - NEAR_N * inv_d);
-                        const float dmd_dd = (FAR_N * NEAR_N) / (FAR_N - NEAR_N) * inv_d * inv_d;
-                        if (c == med_c - 1) dL_dz += dmed;
-                        dL_dweight += (final_D2 + m_d * m_d * final_A - 2.0f * m_d * final_D) * dreg;
-                        dL_dalpha += dL_dweight - last_dL_dT;
-                        last_dL_dT = dL_dweight * alpha + (1.0f - alpha) * last_dL_dT;
-                        const float dL_dmd = 2.0f * aT * (m_d * final_A - final_D) * dreg;
-                        dL_dz += dL_dmd * dmd_dd;
-                        accum_depth_rec = last_alpha * last_depth + (1.f - last_alpha) * accum_depth_rec;
-                        last_depth = e.depth;
-                        dL_dalpha += (e.depth - accum_depth_rec) * ddepth;
-                        accum_alpha_rec = last_alpha * 1.0f + (1.f - last_alpha) * accum_alpha_rec;
-                        dL_dalpha += (1.0f - accum_alpha_rec) * daccum;
-                        const float nrm[3] = {q3.x, q3.y, q3.z};
-#pragma unroll
-                        for (int ch = 0; ch < 3; ++ch) {
-                            accum_normal_rec[ch] =
-                                last_alpha * last_normal[ch] + (1.f - last_alpha) * accum_normal_rec[ch];
-                            last_normal[ch] = nrm[ch];
-                            dL_dalpha += (nrm[ch] - accum_normal_rec[ch]) * dn2[ch];
-                            v[9 + ch] = aT * dn2[ch];
-                        }
-                        dL_dz += aT * ddepth;
-                    }
-                    dL_dalpha *= Tr;
-                    last_alpha = alpha;
-                    dL_dalpha += (-T_final * inv_1ma) * bg_dot;
-                    const float dL_dG = opa * dL_dalpha;
-                    const float Twx = q1.z, Twy = q1.w;
-                    if (e.rho3d <= e.rho2d) {
-                        const float dsx = dL_dG * -G * e.u + dL_dz * Twx;
-                        const float dsy = dL_dG * -G * e.v + dL_dz * Twy;
-                        const float dsx_pz = dsx * e.inv_z, dsy_pz = dsy * e.inv_z;
-                        const f3 dp = {dsx_pz, dsy_pz, -(dsx_pz * e.u + dsy_pz * e.v)};
-                        const f3 &k = e.k, &l = e.l;
-                        const f3 dk = {l.y * dp.z - l.z * dp.y, l.z * dp.x - l.x * dp.z, l.x * dp.y - l.y * dp.x};
-                        const f3 dl = {dp.y * k.z - dp.z * k.y, dp.z * k.x - dp.x * k.z, dp.x * k.y - dp.y * k.x};
-                        v[0] = -dk.x;
-                        v[1] = -dk.y;
-                        v[2] = -dk.z;
-                        v[3] = -dl.x;
-                        v[4] = -dl.y;
-                        v[5] = -dl.z;
-                        v[6] = px * dk.x + py * dl.x + dL_dz * e.u;
-                        v[7] = px * dk.y + py * dl.y + dL_dz * e.v;
-                        v[8] = px * dk.z + py * dl.z + dL_dz;
-                    } else if (FULL) {
-                        v[6] = e.u * dL_dz;
-                        v[7] = e.v * dL_dz;
-                        v[8] = dL_dz;
-                    }
-                    v[12] = G * dL_dalpha * (opa * (1.0f - opa));
+                for (int q = 0; q < 3; ++q) {
+                    const float an = last_alpha * last_c[q] + (1.f - last_alpha) * acc_c[q];
+                    acc_c[q] = has ? an : acc_c[q];
+                    last_c[q] = has ? cu[q] : last_c[q];
+                    dL_dalpha += (cu[q] - acc_c[q]) * dpix[q];
+                    v16[13 + q] = cu[q] > 0.0f ? aT * dpix[q] : 0.f;
                 }
-            }
-            if (__any(has)) {
-                const float s = wave_reduce16(v, lane);
-                if ((lane & 3) == 0) {
-                    const int vi = ((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 +
-                                   ((lane >> 2) & 1);
-                    if (s != 0.f) unsafeAtomicAdd(&grads16[(size_t)s_id[t] * 16 + vi], s);
+                const float inv_d = __builtin_amdgcn_rcpf(depth);
+                const float m_d = kMScale * (1.0f - NEAR_N * inv_d);
+                const float dmd_dd = (FAR_N * NEAR_N) / (FAR_N - NEAR_N) * inv_d * inv_d;
+                float dL_dz = (has && (int)e.z == med_pos) ? dmed : 0.f;
+                const float dL_dweight = (fD2 + m_d * m_d * fA - 2.0f * m_d * fD) * dreg;
+                dL_dalpha += dL_dweight - last_dLdT;
+                const float ldt = dL_dweight * alpha + (1.0f - alpha) * last_dLdT;
+                last_dLdT = has ? ldt : last_dLdT;
+                dL_dz += 2.0f * aT * (m_d * fA - fD) * dreg * dmd_dd;
+                const float ad = last_alpha * last_d + (1.f - last_alpha) * acc_d;
+                acc_d = has ? ad : acc_d;
+                last_d = has ? depth : last_d;
+                dL_dalpha += (depth - acc_d) * ddep;
+                const float aa = last_alpha + (1.f - last_alpha) * acc_a;
+                acc_a = has ? aa : acc_a;
+                dL_dalpha += (1.0f - acc_a) * dacc;
+#pragma unroll
+                for (int q = 0; q < 3; ++q) {
+                    const float an = last_alpha * last_n[q] + (1.f - last_alpha) * acc_n[q];
+                    acc_n[q] = has ? an : acc_n[q];
+                    last_n[q] = has ? nrm[q] : last_n[q];
+                    dL_dalpha += (nrm[q] - acc_n[q]) * dn[q];
+                    v16[9 + q] = aT * dn[q];
                 }
+                dL_dz += aT * ddep;
+                dL_dalpha = __builtin_fmaf(dL_dalpha, Tr, bgT * inv_om);
+                last_alpha = has ? alpha : last_alpha;
+                dL_dz = has ? dL_dz : 0.f;
+                const float dL_dG = has ? opa * dL_dalpha : 0.f;
+                float dsx = 0.f, dsy = 0.f;
+                if (use3d) {
+                    dsx = -dL_dG * G * u + dL_dz * Twx;
+                    dsy = -dL_dG * G * v + dL_dz * Twy;
+                }
+                const float dsx_pz = dsx * inv_z, dsy_pz = dsy * inv_z;
+                const float dpz = -(dsx_pz * u + dsy_pz * v);
+                const f3 dk = {l.y * dpz - l.z * dsy_pz, l.z * dsx_pz - l.x * dpz, l.x * dsy_pz - l.y * dsx_pz};
+                const f3 dl = {dsy_pz * k.z - dpz * k.y, dpz * k.x - dsx_pz * k.z, dsx_pz * k.y - dsy_pz * k.x};
+                v16[0] = -dk.x;
+                v16[1] = -dk.y;
+                v16[2] = -dk.z;
+                v16[3] = -dl.x;
+                v16[4] = -dl.y;
+                v16[5] = -dl.z;
+                v16[6] = px * dk.x + py * dl.x + dL_dz * u;
+                v16[7] = px * dk.y + py * dl.y + dL_dz * v;
+                v16[8] = px * dk.z + py * dl.z + dL_dz;
+                v16[12] = G * dL_dG * (1.0f - opa);
             }
+            float s = wave_reduce16(v16, lane);
+            if (!FULL) {
+                const float cc = ch == 0 ? q3.w : ch == 1 ? q4.x : q4.y;
+                const float f = __builtin_fmaf(opa, __builtin_fmaf(fb, opa, fa), fc);
+                s = (fc != 0.f && !(cc > 0.f)) ? 0.f : s * f;
+            }
+            if ((lane & 3) == 0 && s != 0.f) unsafeAtomicAdd(&grads16[(size_t)e.w * 16 + vi], s);
         }
+        wave_lds_sync();
     }
 }
 
@@ -406,30 +501,37 @@ namespace mskern {
 void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
                        const float *rec, const float *bg, float *out_img, float *final_Ts, int *final_idx,
                        float *out_depth, float *out_normal, float *out_alpha, float *out_median, float *out_dist,
-                       unsigned long long *pair_counter) {
+                       unsigned long long *pair_counter, uint32_t *blend_log, float *t_ckpt, int *wave_cnt) {
     const int T = tiles_x * tiles_y;
     const int grid = ((T + 7) / 8) * 8;
-    hipLaunchKernelGGL(k_raster_fwd, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
-                       reinterpret_cast<const float4 *>(rec), bg, out_img, final_Ts, final_idx, out_depth,
-                       out_normal, out_alpha, out_median, out_dist, pair_counter);
+    auto *lg = reinterpret_cast<uint4 *>(blend_log);
+    if (blend_log)
+        hipLaunchKernelGGL(k_raster_fwd<true>, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
+                           reinterpret_cast<const float4 *>(rec), bg, out_img, final_Ts, final_idx, out_depth,
+                           out_normal, out_alpha, out_median, out_dist, pair_counter, lg, t_ckpt, wave_cnt);
+    else
+        hipLaunchKernelGGL(k_raster_fwd<false>, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
+                           reinterpret_cast<const float4 *>(rec), bg, out_img, final_Ts, final_idx, out_depth,
+                           out_normal, out_alpha, out_median, out_dist, pair_counter, lg, t_ckpt, wave_cnt);
 }
 
-void launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
-                       const float *rec, const float *bg, const float *final_Ts, const int *final_idx,
-                       const float *dL_dimg, const float *dL_ddepth, const float *dL_daccum,
-                       const float *dL_dnormal, const float *dL_dmedian, const float *dL_ddist,
-                       float ddist_uniform, float *grads16) {
+void launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets,
+                       const uint32_t *blend_log, const float *t_ckpt, const int *wave_cnt, const float *rec,
+                       const float *bg, const float *final_Ts, const int *final_idx, const float *dL_dimg,
+                       const float *dL_ddepth, const float *dL_daccum, const float *dL_dnormal,
+                       const float *dL_dmedian, const float *dL_ddist, float ddist_uniform, float *grads16) {
     const int T = tiles_x * tiles_y;
     const int grid = ((T + 7) / 8) * 8;
+    const auto *lg = reinterpret_cast<const uint4 *>(blend_log);
     const bool full = dL_ddepth || dL_daccum || dL_dnormal || dL_dmedian || dL_ddist || ddist_uniform != 0.0f;
     if (full)
-        hipLaunchKernelGGL(k_raster_bwd<true>, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
-                           reinterpret_cast<const float4 *>(rec), bg, final_Ts, final_idx, dL_dimg, dL_ddepth,
-                           dL_daccum, dL_dnormal, dL_dmedian, dL_ddist, ddist_uniform, grads16);
+        hipLaunchKernelGGL(k_raster_bwd<true>, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, lg,
+                           t_ckpt, wave_cnt, reinterpret_cast<const float4 *>(rec), bg, final_Ts, final_idx, dL_dimg,
+                           dL_ddepth, dL_daccum, dL_dnormal, dL_dmedian, dL_ddist, ddist_uniform, grads16);
     else
-        hipLaunchKernelGGL(k_raster_bwd<false>, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
-                           reinterpret_cast<const float4 *>(rec), bg, final_Ts, final_idx, dL_dimg, dL_ddepth,
-                           dL_daccum, dL_dnormal, dL_dmedian, dL_ddist, ddist_uniform, grads16);
+        hipLaunchKernelGGL(k_raster_bwd<false>, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, lg,
+                           t_ckpt, wave_cnt, reinterpret_cast<const float4 *>(rec), bg, final_Ts, final_idx, dL_dimg,
+                           dL_ddepth, dL_daccum, dL_dnormal, dL_dmedian, dL_ddist, ddist_uniform, grads16);
 }
 
 }  // namespace mskern

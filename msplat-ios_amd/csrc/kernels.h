@@ -45,15 +45,19 @@ constexpr int kSuperTile = 4;
 constexpr int kSuperSortChunk = 4096;
 
 // k_raster.hip
+// blend_log (4 * I entries of 16 bytes), t_ckpt (4 * I floats) and wave_cnt
+// (4 * T ints) receive the per-wave blend log and transmittance checkpoints
+// the backward replays; pass nullptr for render-only frames.
 void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
                        const float *rec, const float *bg, float *out_img, float *final_Ts, int *final_idx,
                        float *out_depth, float *out_normal, float *out_alpha, float *out_median, float *out_dist,
-                       unsigned long long *pair_counter);
-void launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
-                       const float *rec, const float *bg, const float *final_Ts, const int *final_idx,
-                       const float *dL_dimg, const float *dL_ddepth, const float *dL_daccum,
-                       const float *dL_dnormal, const float *dL_dmedian, const float *dL_ddist,
-                       float ddist_uniform, float *grads16);
+                       unsigned long long *pair_counter, uint32_t *blend_log, float *t_ckpt, int *wave_cnt);
+void launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets,
+                       const uint32_t *blend_log, const float *t_ckpt, const int *wave_cnt, const float *rec,
+                       const float *bg, const float *final_Ts, const int *final_idx, const float *dL_dimg,
+                       const float *dL_ddepth, const float *dL_daccum, const float *dL_dnormal,
+                       const float *dL_dmedian, const float *dL_ddist, float ddist_uniform, float *grads16);
+constexpr int kBlendLogEntryBytes = 16;
 
 // k_ssim.hip
 int ssim_num_blocks(int W, int H);
