@@ -7,15 +7,19 @@
 // msplat_metal.metal:2704-3085, msplat_metal.mm:1077-1212).  Because
 // dL/dssim_map is a known constant (-lambda / 3HW), the per-pixel SSIM
 // partials can be produced in the same pass as the forward statistics:
-//   pass 1 (k_ssim_fwd): img, gt (+halo, all three channels in one
-//          coalesced sweep of the interleaved rows) -> per channel: 5
-//          separable blurs in LDS -> SSIM map, loss partials and the three
-//          per-pixel gradient maps (d/dmu1 folded, d/dsigma1^2, d/dsigma12),
-//          stored channel-planar so every later access is a contiguous row;
+//   pass 1 (k_ssim_fwd): per channel, img and gt (+5-pixel halo) -> the 5
+//          separable blurs (horizontal, then vertical, as the reference) ->
+//          SSIM map, loss partials and the three per-pixel gradient maps
+//          (d/dmu1 folded, d/dsigma1^2, d/dsigma12), stored channel-planar;
 //   pass 2 (k_ssim_bwd): per channel the three planar maps (+halo) ->
-//          adjoint blur in LDS; the three channels of a pixel stay in the
-//          same thread, so dL/dimg = L1 gradient + blurred SSIM gradient is
+//          adjoint blur (the same symmetric blur) + the L1 gradient; the
+//          three channels of a pixel stay in one thread, so dL/dimg is
 //          written once, interleaved.
+// Both passes work on 32x32 output tiles one channel at a time (45 / 40 KB
+// of LDS) with register blocking: a horizontal work item produces 4
+// adjacent outputs from 14 staged inputs, a vertical one 4 outputs of a
+// column from 14 rows, each output accumulating its taps in ascending order
+// (the order of the reference's blur kernels).
 // HBM traffic per pixel: 24 B in + 36 B out (pass 1), 36 + 24 B in + 12 B
 // out (pass 2), plus the halo re-reads of neighbouring tiles.
 #include "kernels.h"
@@ -23,10 +27,12 @@
 
 namespace {
 
-constexpr int TW = 64, TH = 16, RAD = 5;
-constexpr int RW = TW + 2 * RAD, RH = TH + 2 * RAD;
+constexpr int TS = 32, RAD = 5;   // output tile TS x TS
+constexpr int RS = TS + 2 * RAD;  // 42: region rows / columns with halo
+constexpr int AST = 44;           // LDS row stride of a staged region
+constexpr int BST = 36;           // LDS row stride of horizontal results
 constexpr int kThreads = 256;
-constexpr int kPix = TH * TW / kThreads;  // output pixels per thread
+constexpr int kHItems = RS * (TS / 4);  // 336 horizontal items (row, 4 columns)
 
 struct Window {
     float w[11];
@@ -44,16 +50,43 @@ __device__ __forceinline__ double block_sum_d(double v, double *s_red) {
     return t;
 }
 
-// Loads the (RH x RW) region around the tile of an interleaved [H,W,3]
-// image into three planar LDS planes, zero outside the image.
-__device__ __forceinline__ void load_region3(const float *__restrict__ src, int W, int H, int x0, int y0,
-                                             float (*dst)[RH][RW]) {
-    for (int k = threadIdx.x; k < RH * RW * 3; k += kThreads) {
-        const int ry = k / (RW * 3), rem = k - ry * (RW * 3);
-        const int rx = rem / 3, c = rem - rx * 3;
-        const int gy = y0 - RAD + ry, gx = x0 - RAD + rx;
-        const bool inb = gx >= 0 && gx < W && gy >= 0 && gy < H;
-        dst[c][ry][rx] = inb ? src[((size_t)gy * W + gx) * 3 + c] : 0.f;
+constexpr int kStage = (RS * RS + kThreads - 1) / kThreads;  // 7 staged elements per thread
+
+// Loads this thread's kStage elements of the (RS x RS) region around the
+// tile of plane `src` (element stride `stride`, offset `off`), zero outside
+// the image.  All loads are issued before any is used.
+__device__ __forceinline__ void stage_load(const float *__restrict__ src, int W, int H, int x0, int y0, int stride,
+                                           int off, float v[kStage]) {
+#pragma unroll
+    for (int i = 0; i < kStage; ++i) {
+        const int k = (int)threadIdx.x + i * kThreads;
+        const int ry = k / RS, rx = k - ry * RS;
+        const int sy = y0 - RAD + ry, sx = x0 - RAD + rx;
+        const bool inb = k < RS * RS && sx >= 0 && sx < W && sy >= 0 && sy < H;
+        v[i] = inb ? src[((size_t)sy * W + sx) * stride + off] : 0.f;
+    }
+}
+
+__device__ __forceinline__ void stage_store(float (*dst)[AST], const float v[kStage]) {
+#pragma unroll
+    for (int i = 0; i < kStage; ++i) {
+        const int k = (int)threadIdx.x + i * kThreads;
+        if (k < RS * RS) {
+            const int ry = k / RS, rx = k - ry * RS;
+            dst[ry][rx] = v[i];
+        }
+    }
+}
+
+// 14 consecutive floats of an LDS row starting at a multiple of 4.
+__device__ __forceinline__ void lds_row14(const float *p, float v[16]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float4 q = reinterpret_cast<const float4 *>(p)[k];
+        v[4 * k + 0] = q.x;
+        v[4 * k + 1] = q.y;
+        v[4 * k + 2] = q.z;
+        v[4 * k + 3] = q.w;
     }
 }
 
@@ -63,95 +96,114 @@ __global__ __launch_bounds__(kThreads) void k_ssim_fwd(int W, int H, const float
                                                        Window win, float *__restrict__ gm1,
                                                        float *__restrict__ gs1, float *__restrict__ gs12,
                                                        double *__restrict__ partials) {
-    __shared__ float s_a[3][RH][RW];
-    __shared__ float s_b[3][RH][RW];
-    __shared__ float s_h[5][RH][TW];
+    __shared__ __align__(16) float s_a[RS][AST];
+    __shared__ __align__(16) float s_b[RS][AST];
+    __shared__ __align__(16) float s_h[5][RS][BST];
     __shared__ double s_red[kThreads / 64];
-    const int x0 = blockIdx.x * TW, y0 = blockIdx.y * TH;
+    const int x0 = blockIdx.x * TS, y0 = blockIdx.y * TS;
     const size_t plane = (size_t)W * H;
     const float C1 = 0.0001f, C2 = 0.0009f;
-    double ssim_acc = 0.0, l1_acc = 0.0;
-    load_region3(img, W, H, x0, y0, s_a);
-    load_region3(gt, W, H, x0, y0, s_b);
-    __syncthreads();
+    // vertical work item of this thread: column vx, output rows 4 vq .. 4 vq + 3
+    const int vx = threadIdx.x & (TS - 1), vq = threadIdx.x >> 5;
+    const int gx = x0 + vx;
+    double ssim_acc = 0.0;
+    float l1[4] = {0.f, 0.f, 0.f, 0.f};
+    // channel c + 1 is loaded into registers while channel c is computed
+    float na[kStage], nb[kStage];
+    stage_load(img, W, H, x0, y0, 3, 0, na);
+    stage_load(gt, W, H, x0, y0, 3, 0, nb);
     for (int c = 0; c < 3; ++c) {
-        // horizontal pass of ssim_blur_horiz_kernel (msplat_metal.metal:2847-2873)
-        for (int k = threadIdx.x; k < RH * TW; k += kThreads) {
-            const int ry = k / TW, x = k - ry * TW;
-            float m1 = 0.f, m2 = 0.f, e11 = 0.f, e22 = 0.f, e12 = 0.f;
-#pragma unroll
-            for (int j = 0; j < 11; ++j) {
-                const float a = s_a[c][ry][x + j], b = s_b[c][ry][x + j], w = win.w[j];
-                m1 = __builtin_fmaf(w, a, m1);
-                m2 = __builtin_fmaf(w, b, m2);
-                e11 = __builtin_fmaf(w, a * a, e11);
-                e22 = __builtin_fmaf(w, b * b, e22);
-                e12 = __builtin_fmaf(w, a * b, e12);
-            }
-            s_h[0][ry][x] = m1;
-            s_h[1][ry][x] = m2;
-            s_h[2][ry][x] = e11;
-            s_h[3][ry][x] = e22;
-            s_h[4][ry][x] = e12;
-        }
+        stage_store(s_a, na);
+        stage_store(s_b, nb);
         __syncthreads();
-        // vertical pass + ssim_compute_kernel (:2910-2952) +
-        // ssim_backward_compute_kernel (:2965-3047)
-#pragma unroll
-        for (int i = 0; i < kPix; ++i) {
-            const int k = threadIdx.x + i * kThreads;
-            const int y = k / TW, x = k - y * TW;
-            const int gy = y0 + y, gx = x0 + x;
-            if (gx >= W || gy >= H) continue;
-            float mu1 = 0.f, mu2 = 0.f, b11 = 0.f, b22 = 0.f, b12 = 0.f;
+        if (c < 2) {
+            stage_load(img, W, H, x0, y0, 3, c + 1, na);
+            stage_load(gt, W, H, x0, y0, 3, c + 1, nb);
+        }
+        // horizontal pass of ssim_blur_horiz_kernel (msplat_metal.metal:2847-2873)
+        for (int it = threadIdx.x; it < kHItems; it += kThreads) {
+            const int ry = it >> 3, xg = (it & 7) * 4;
+            float a[16], b[16];
+            lds_row14(&s_a[ry][xg], a);
+            lds_row14(&s_b[ry][xg], b);
+            float m1[4] = {0.f, 0.f, 0.f, 0.f}, m2[4] = {0.f, 0.f, 0.f, 0.f}, e11[4] = {0.f, 0.f, 0.f, 0.f},
+                  e22[4] = {0.f, 0.f, 0.f, 0.f}, e12[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 11; ++j) {
                 const float w = win.w[j];
-                mu1 = __builtin_fmaf(w, s_h[0][y + j][x], mu1);
-                mu2 = __builtin_fmaf(w, s_h[1][y + j][x], mu2);
-                b11 = __builtin_fmaf(w, s_h[2][y + j][x], b11);
-                b22 = __builtin_fmaf(w, s_h[3][y + j][x], b22);
-                b12 = __builtin_fmaf(w, s_h[4][y + j][x], b12);
+#pragma unroll
+                for (int o = 0; o < 4; ++o) {
+                    const float av = a[o + j], bv = b[o + j];
+                    m1[o] = __builtin_fmaf(w, av, m1[o]);
+                    m2[o] = __builtin_fmaf(w, bv, m2[o]);
+                    e11[o] = __builtin_fmaf(w, av * av, e11[o]);
+                    e22[o] = __builtin_fmaf(w, bv * bv, e22[o]);
+                    e12[o] = __builtin_fmaf(w, av * bv, e12[o]);
+                }
             }
-            const float m1 = mu1, m2 = mu2;
-            const float m1_sq = m1 * m1, m2_sq = m2 * m2, m1m2 = m1 * m2;
-            const float s1_sq = b11 - m1_sq, s2_sq = b22 - m2_sq, s12 = b12 - m1m2;
-            const float A = 2.0f * m1m2 + C1, B = 2.0f * s12 + C2;
-            const float Cd = m1_sq + m2_sq + C1, Dd = s1_sq + s2_sq + C2;
-            const float val = (A * B) / (Cd * Dd);
-            ssim_acc += (double)val;
-            const float CD = Cd * Dd, AB = A * B;
-            const float inv_CD = 1.0f / CD, inv_Cd = 1.0f / Cd, inv_Dd = 1.0f / Dd;
-            const float dmu1 = 2.0f * inv_CD * (m2 * B - m1 * AB * inv_Cd);
-            const float ds12 = 2.0f * A * inv_CD;
-            const float ds1 = -AB * inv_CD * inv_Dd;
-            float gm = g * dmu1;
-            const float g12 = g * ds12, g1 = g * ds1;
-            gm += g1 * (-2.0f * m1);
-            gm += g12 * (-m2);
-            const size_t o = c * plane + (size_t)gy * W + gx;
-            gm1[o] = gm;
-            gs1[o] = g1;
-            gs12[o] = g12;
+            *reinterpret_cast<float4 *>(&s_h[0][ry][xg]) = make_float4(m1[0], m1[1], m1[2], m1[3]);
+            *reinterpret_cast<float4 *>(&s_h[1][ry][xg]) = make_float4(m2[0], m2[1], m2[2], m2[3]);
+            *reinterpret_cast<float4 *>(&s_h[2][ry][xg]) = make_float4(e11[0], e11[1], e11[2], e11[3]);
+            *reinterpret_cast<float4 *>(&s_h[3][ry][xg]) = make_float4(e22[0], e22[1], e22[2], e22[3]);
+            *reinterpret_cast<float4 *>(&s_h[4][ry][xg]) = make_float4(e12[0], e12[1], e12[2], e12[3]);
+        }
+        __syncthreads();
+        // vertical pass + ssim_compute_kernel (:2910-2952) +
+        // ssim_backward_compute_kernel (:2965-3047), 4 rows of column vx
+        {
+            float st[5][4];
+#pragma unroll
+            for (int s = 0; s < 5; ++s) {
+                float col[14];
+#pragma unroll
+                for (int i = 0; i < 14; ++i) col[i] = s_h[s][4 * vq + i][vx];
+#pragma unroll
+                for (int o = 0; o < 4; ++o) {
+                    float acc = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 11; ++j) acc = __builtin_fmaf(win.w[j], col[o + j], acc);
+                    st[s][o] = acc;
+                }
+            }
+#pragma unroll
+            for (int o = 0; o < 4; ++o) {
+                const int gy = y0 + 4 * vq + o;
+                if (gx >= W || gy >= H) continue;
+                const float m1 = st[0][o], m2 = st[1][o];
+                const float m1_sq = m1 * m1, m2_sq = m2 * m2, m1m2 = m1 * m2;
+                const float s1_sq = st[2][o] - m1_sq, s2_sq = st[3][o] - m2_sq, s12 = st[4][o] - m1m2;
+                const float A = 2.0f * m1m2 + C1, B = 2.0f * s12 + C2;
+                const float Cd = m1_sq + m2_sq + C1, Dd = s1_sq + s2_sq + C2;
+                const float val = (A * B) / (Cd * Dd);
+                ssim_acc += (double)val;
+                const float CD = Cd * Dd, AB = A * B;
+                const float inv_CD = 1.0f / CD, inv_Cd = 1.0f / Cd, inv_Dd = 1.0f / Dd;
+                const float dmu1 = 2.0f * inv_CD * (m2 * B - m1 * AB * inv_Cd);
+                const float ds12 = 2.0f * A * inv_CD;
+                const float ds1 = -AB * inv_CD * inv_Dd;
+                float gm = g * dmu1;
+                const float g12 = g * ds12, g1 = g * ds1;
+                gm += g1 * (-2.0f * m1);
+                gm += g12 * (-m2);
+                const size_t o2 = c * plane + (size_t)gy * W + gx;
+                gm1[o2] = gm;
+                gs1[o2] = g1;
+                gs12[o2] = g12;
+                // L1 term of loss_l1_distortion_2dgs_kernel (:2704-2762), channel order
+                const float diff = s_a[4 * vq + o + RAD][vx + RAD] - s_b[4 * vq + o + RAD][vx + RAD];
+                l1[o] += lambda_l1 * __builtin_fabsf(diff) * inv_np;
+            }
         }
         __syncthreads();
     }
-    // per-pixel L1 + distortion loss of loss_l1_distortion_2dgs_kernel (:2704-2762)
+    double l1_acc = 0.0;
     const float inv_HW = inv_np * 3.0f;
 #pragma unroll
-    for (int i = 0; i < kPix; ++i) {
-        const int k = threadIdx.x + i * kThreads;
-        const int y = k / TW, x = k - y * TW;
-        const int gy = y0 + y, gx = x0 + x;
+    for (int o = 0; o < 4; ++o) {
+        const int gy = y0 + 4 * vq + o;
         if (gx >= W || gy >= H) continue;
-        float local = 0.0f;
-        for (int c = 0; c < 3; ++c) {
-            const float diff = s_a[c][y + RAD][x + RAD] - s_b[c][y + RAD][x + RAD];
-            local += lambda_l1 * __builtin_fabsf(diff) * inv_np;
-        }
         const float dd = dist ? dist[(size_t)gy * W + gx] : 0.0f;
-        local += lambda_dist * dd * inv_HW;
-        l1_acc += (double)local;
+        l1_acc += (double)(l1[o] + lambda_dist * dd * inv_HW);
     }
     const double ts = block_sum_d(ssim_acc, s_red);
     const double tl = block_sum_d(l1_acc, s_red);
@@ -169,88 +221,118 @@ __global__ __launch_bounds__(kThreads) void k_ssim_bwd(int W, int H, const float
                                                        const float *__restrict__ gs1,
                                                        const float *__restrict__ gs12, float lambda_l1, float inv_np,
                                                        Window win, float *__restrict__ dL_dimg) {
-    __shared__ float s_g[3][RH][RW];
-    __shared__ float s_h[3][RH][TW];
-    const int x0 = blockIdx.x * TW, y0 = blockIdx.y * TH;
+    __shared__ __align__(16) float s_g[3][RS][AST];
+    __shared__ __align__(16) float s_h[3][RS][BST];
+    const int x0 = blockIdx.x * TS, y0 = blockIdx.y * TS;
     const size_t plane = (size_t)W * H;
-    float blur[kPix][3][3];  // [pixel][channel][gm, g1, g12]
+    const int vx = threadIdx.x & (TS - 1), vq = threadIdx.x >> 5;
+    const int gx = x0 + vx;
+    float dl[4][3];
+    // img / gt of this thread's four pixels, all channels
+    float pa[4][3], pb[4][3];
+#pragma unroll
+    for (int o = 0; o < 4; ++o) {
+        const int gy = y0 + 4 * vq + o;
+        const bool inb = gx < W && gy < H;
+        const size_t p3 = inb ? ((size_t)gy * W + gx) * 3 : 0;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            pa[o][c] = inb ? img[p3 + c] : 0.f;
+            pb[o][c] = inb ? gt[p3 + c] : 0.f;
+        }
+    }
+    // the maps of channel c + 1 are loaded into registers while channel c is computed
+    float n0[kStage], n1[kStage], n2[kStage];
+    stage_load(gm1, W, H, x0, y0, 1, 0, n0);
+    stage_load(gs1, W, H, x0, y0, 1, 0, n1);
+    stage_load(gs12, W, H, x0, y0, 1, 0, n2);
     for (int c = 0; c < 3; ++c) {
-        const float *m0 = gm1 + c * plane, *m1 = gs1 + c * plane, *m2 = gs12 + c * plane;
-        for (int k = threadIdx.x; k < RH * RW; k += kThreads) {
-            const int ry = k / RW, rx = k - ry * RW;
-            const int gy = y0 - RAD + ry, gx = x0 - RAD + rx;
-            const bool inb = gx >= 0 && gx < W && gy >= 0 && gy < H;
-            const size_t o = (size_t)gy * W + gx;
-            s_g[0][ry][rx] = inb ? m0[o] : 0.f;
-            s_g[1][ry][rx] = inb ? m1[o] : 0.f;
-            s_g[2][ry][rx] = inb ? m2[o] : 0.f;
+        stage_store(s_g[0], n0);
+        stage_store(s_g[1], n1);
+        stage_store(s_g[2], n2);
+        __syncthreads();
+        if (c < 2) {
+            const size_t po = (size_t)(c + 1) * plane;
+            stage_load(gm1 + po, W, H, x0, y0, 1, 0, n0);
+            stage_load(gs1 + po, W, H, x0, y0, 1, 0, n1);
+            stage_load(gs12 + po, W, H, x0, y0, 1, 0, n2);
+        }
+        for (int it = threadIdx.x; it < kHItems; it += kThreads) {
+            const int ry = it >> 3, xg = (it & 7) * 4;
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+                float v[16];
+                lds_row14(&s_g[m][ry][xg], v);
+                float h[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 11; ++j)
+#pragma unroll
+                    for (int o = 0; o < 4; ++o) h[o] = __builtin_fmaf(win.w[j], v[o + j], h[o]);
+                *reinterpret_cast<float4 *>(&s_h[m][ry][xg]) = make_float4(h[0], h[1], h[2], h[3]);
+            }
         }
         __syncthreads();
-        for (int k = threadIdx.x; k < RH * TW; k += kThreads) {
-            const int ry = k / TW, x = k - ry * TW;
-            float h0 = 0.f, h1 = 0.f, h2 = 0.f;
+        float bl[3][4];
 #pragma unroll
-            for (int j = 0; j < 11; ++j) {
-                const float w = win.w[j];
-                h0 = __builtin_fmaf(w, s_g[0][ry][x + j], h0);
-                h1 = __builtin_fmaf(w, s_g[1][ry][x + j], h1);
-                h2 = __builtin_fmaf(w, s_g[2][ry][x + j], h2);
+        for (int m = 0; m < 3; ++m) {
+            float col[14];
+#pragma unroll
+            for (int i = 0; i < 14; ++i) col[i] = s_h[m][4 * vq + i][vx];
+#pragma unroll
+            for (int o = 0; o < 4; ++o) {
+                float acc = 0.f;
+#pragma unroll
+                for (int j = 0; j < 11; ++j) acc = __builtin_fmaf(win.w[j], col[o + j], acc);
+                bl[m][o] = acc;
             }
-            s_h[0][ry][x] = h0;
-            s_h[1][ry][x] = h1;
-            s_h[2][ry][x] = h2;
         }
-        __syncthreads();
 #pragma unroll
-        for (int i = 0; i < kPix; ++i) {
-            const int k = threadIdx.x + i * kThreads;
-            const int y = k / TW, x = k - y * TW;
-            float bgm = 0.f, bg1 = 0.f, bg12 = 0.f;
-#pragma unroll
-            for (int j = 0; j < 11; ++j) {
-                const float w = win.w[j];
-                bgm = __builtin_fmaf(w, s_h[0][y + j][x], bgm);
-                bg1 = __builtin_fmaf(w, s_h[1][y + j][x], bg1);
-                bg12 = __builtin_fmaf(w, s_h[2][y + j][x], bg12);
-            }
-            blur[i][c][0] = bgm;
-            blur[i][c][1] = bg1;
-            blur[i][c][2] = bg12;
+        for (int o = 0; o < 4; ++o) {
+            const int gy = y0 + 4 * vq + o;
+            dl[o][c] = 0.f;
+            if (gx >= W || gy >= H) continue;
+            const float a = pa[o][c], b = pb[o][c];
+            const float diff = a - b;
+            const float sgn = (diff > 0.0f) ? 1.0f : ((diff < 0.0f) ? -1.0f : 0.0f);
+            const float contrib = bl[0][o] + 2.0f * a * bl[1][o] + b * bl[2][o];
+            dl[o][c] = lambda_l1 * sgn * inv_np + contrib;
         }
         __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < kPix; ++i) {
-        const int k = threadIdx.x + i * kThreads;
-        const int y = k / TW, x = k - y * TW;
-        const int gy = y0 + y, gx = x0 + x;
+    for (int o = 0; o < 4; ++o) {
+        const int gy = y0 + 4 * vq + o;
         if (gx >= W || gy >= H) continue;
-        const size_t o = ((size_t)gy * W + gx) * 3;
-#pragma unroll
-        for (int c = 0; c < 3; ++c) {
-            const float a = img[o + c], b = gt[o + c];
-            const float diff = a - b;
-            const float sgn = (diff > 0.0f) ? 1.0f : ((diff < 0.0f) ? -1.0f : 0.0f);
-            const float l1 = lambda_l1 * sgn * inv_np;
-            const float contrib = blur[i][c][0] + 2.0f * a * blur[i][c][1] + b * blur[i][c][2];
-            dL_dimg[o + c] = l1 + contrib;
-        }
+        float *d = dL_dimg + ((size_t)gy * W + gx) * 3;
+        d[0] = dl[o][0];
+        d[1] = dl[o][1];
+        d[2] = dl[o][2];
     }
 }
 
 // Fixed-order fp64 reduction of the per-workgroup partials.
-__global__ __launch_bounds__(256) void k_loss_final(int nblocks, const double *__restrict__ partials,
-                                                    float lambda_dssim, float inv_np, double *__restrict__ out) {
-    __shared__ double s_s[256], s_l[256];
+__global__ __launch_bounds__(1024) void k_loss_final(int nblocks, const double *__restrict__ partials,
+                                                     float lambda_dssim, float inv_np, double *__restrict__ out) {
+    __shared__ double s_s[1024], s_l[1024];
     double s = 0.0, l = 0.0;
-    for (int b = threadIdx.x; b < nblocks; b += 256) {
-        s += partials[2 * b];
-        l += partials[2 * b + 1];
+    // each thread sums a fixed strided subset, four loads in flight
+    for (int b0 = threadIdx.x; b0 < nblocks; b0 += 4 * 1024) {
+        double2 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int b = b0 + u * 1024;
+            v[u] = b < nblocks ? reinterpret_cast<const double2 *>(partials)[b] : make_double2(0.0, 0.0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            s += v[u].x;
+            l += v[u].y;
+        }
     }
     s_s[threadIdx.x] = s;
     s_l[threadIdx.x] = l;
     __syncthreads();
-    for (int d = 128; d > 0; d >>= 1) {
+    for (int d = 512; d > 0; d >>= 1) {
         if ((int)threadIdx.x < d) {
             s_s[threadIdx.x] += s_s[threadIdx.x + d];
             s_l[threadIdx.x] += s_l[threadIdx.x + d];
@@ -268,7 +350,7 @@ __global__ __launch_bounds__(256) void k_loss_final(int nblocks, const double *_
 
 namespace mskern {
 
-int ssim_num_blocks(int W, int H) { return ((W + TW - 1) / TW) * ((H + TH - 1) / TH); }
+int ssim_num_blocks(int W, int H) { return ((W + TS - 1) / TS) * ((H + TS - 1) / TS); }
 
 void launch_loss_fwd_bwd(hipStream_t s, int W, int H, const float *img, const float *gt, const float *dist,
                          float lambda_l1, float lambda_dist, float lambda_dssim, const float window[11],
@@ -278,12 +360,12 @@ void launch_loss_fwd_bwd(hipStream_t s, int W, int H, const float *img, const fl
     const float g = -lambda_dssim * inv_np;
     Window win;
     for (int j = 0; j < 11; ++j) win.w[j] = window[j];
-    const dim3 grid((W + TW - 1) / TW, (H + TH - 1) / TH);
+    const dim3 grid((W + TS - 1) / TS, (H + TS - 1) / TS);
     hipLaunchKernelGGL(k_ssim_fwd, grid, dim3(kThreads), 0, s, W, H, img, gt, dist, lambda_l1, lambda_dist, inv_np,
                        g, win, gm1, gs1, gs12, partials);
     hipLaunchKernelGGL(k_ssim_bwd, grid, dim3(kThreads), 0, s, W, H, img, gt, gm1, gs1, gs12, lambda_l1, inv_np,
                        win, dL_dimg);
-    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(256), 0, s, (int)(grid.x * grid.y), partials, lambda_dssim,
+    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(1024), 0, s, (int)(grid.x * grid.y), partials, lambda_dssim,
                        inv_np, loss_out);
 }
 
