@@ -10,6 +10,25 @@ namespace {
 
 constexpr int kBlock = 256;
 
+// Copies `count` consecutive floats from global memory to LDS with every
+// thread's loads of a round (kStageU per thread) in flight together.
+constexpr int kStageU = 12;
+__device__ __forceinline__ void stage_rows(float *__restrict__ dst, const float *__restrict__ src, int count) {
+    for (int e0 = threadIdx.x; e0 < count; e0 += kStageU * kBlock) {
+        float v[kStageU];
+#pragma unroll
+        for (int u = 0; u < kStageU; ++u) {
+            const int e = e0 + u * kBlock;
+            v[u] = e < count ? src[e] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < kStageU; ++u) {
+            const int e = e0 + u * kBlock;
+            if (e < count) dst[e] = v[u];
+        }
+    }
+}
+
 // project_and_sh_forward_2dgs_kernel (msplat_metal.metal:1413-1521), with
 // the sigmoid of the sort/pack stage (:1684) and the raster's colour clamp
 // (:619) folded into the record.  Also builds the per-tile histogram that
@@ -27,8 +46,7 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
     const int b0 = blockIdx.x * kBlock;
     const int cnt = min(kBlock, n - b0);
     if (cam.degrees_to_use > 0 && K3 <= 45) {
-        const float *src = frest + (size_t)b0 * K3;
-        for (int e = threadIdx.x; e < cnt * K3; e += kBlock) s_fr[e] = src[e];
+        stage_rows(s_fr, frest + (size_t)b0 * K3, cnt * K3);
         __syncthreads();
     }
     // No early return: every lane of the wave takes part in the tile count.
@@ -183,9 +201,9 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
     const int cnt = min(kBlock, n - b0);
     const bool staged = K3 <= 45;
     const int sh_deg = cam.degrees_to_use;
-    if (staged && sh_deg > 0) {
-        const float *src = frest + (size_t)b0 * K3;
-        for (int e = threadIdx.x; e < cnt * K3; e += kBlock) s_fr[e] = src[e];
+    const bool have_rows = staged && sh_deg > 0;
+    if (have_rows) {
+        stage_rows(s_fr, frest + (size_t)b0 * K3, cnt * K3);
         __syncthreads();
     }
     const int i = b0 + threadIdx.x;
@@ -297,14 +315,47 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
     for (int c = 0; c < 3; ++c) s_vc[threadIdx.x * 3 + c] = vc[c];
     __syncthreads();
     const size_t base = (size_t)b0 * K3;
-    for (int e = threadIdx.x; e < cnt * K3; e += kBlock) {
-        const int gl = e / K3, k = e - gl * K3;
-        const int b = k / 3, c = k - 3 * b;
-        const float gr = (b < nrest) ? s_basis[gl * 24 + b] * s_vc[gl * 3 + c] : 0.f;
-        if (!FUSED)
-            dfrest[base + e] = gr;
-        else
-            adam_elem(frest, ad.m[4], ad.v[4], base + e, gr, ad.step[4], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+    const int total = cnt * K3;
+    // element e = (splat gl, coefficient k) of the block's rows, advanced
+    // by kBlock elements per step without a division
+    int gl = (int)threadIdx.x / K3, k = (int)threadIdx.x - gl * K3;
+    const int dgl = kBlock / K3, dk = kBlock - dgl * K3;
+    constexpr int U = 8;  // elements per thread with loads in flight together
+    for (int e0 = threadIdx.x; e0 < total; e0 += U * kBlock) {
+        float gr[U], pv[U], mv[U], vv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int e = e0 + u * kBlock;
+            const bool act = e < total;
+            const int b = k / 3, c = k - 3 * b;
+            gr[u] = (act && b < nrest) ? s_basis[gl * 24 + b] * s_vc[gl * 3 + c] : 0.f;
+            if (FUSED && act) {
+                pv[u] = have_rows ? s_fr[e] : frest[base + e];
+                mv[u] = ad.m[4][base + e];
+                vv[u] = ad.v[4][base + e];
+            }
+            gl += dgl;
+            k += dk;
+            if (k >= K3) {
+                k -= K3;
+                ++gl;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int e = e0 + u * kBlock;
+            if (e >= total) continue;
+            if (!FUSED) {
+                dfrest[base + e] = gr[u];
+            } else {
+                // fused_adam_kernel (msplat_metal.metal:1383-1406), as adam_elem
+                const float m = __builtin_fmaf(ad.b1, mv[u], (1.0f - ad.b1) * gr[u]);
+                const float v = __builtin_fmaf(ad.b2, vv[u], (1.0f - ad.b2) * gr[u] * gr[u]);
+                frest[base + e] = pv[u] - ad.step[4] * m / (__builtin_sqrtf(v) / ad.bc2_sqrt + ad.eps);
+                ad.m[4][base + e] = m;
+                ad.v[4][base + e] = v;
+            }
+        }
     }
 }
 
