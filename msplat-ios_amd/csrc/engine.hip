@@ -38,8 +38,8 @@ struct Engine {
     // per-gaussian
     DevBuf rec, depths, radii, rect, grads16, colors_raw;
     // per-tile
-    DevBuf tile_diff, counts, offsets, cursor, stats, big_list, scan_tmp;
-    DevBuf super_diff, super_counts, super_offsets, super_cursor, super_tmp;
+    DevBuf counts, offsets, stats, big_list, scan_tmp;
+    DevBuf super_counts, super_offsets, super_cursor, super_tmp;
     // per-intersection
     DevBuf keys, keys_tmp, ids;  // keys: per (splat, super-tile) pair
     DevBuf blend_log, t_ckpt, wave_cnt;  // the raster forward's per-wave blend log
@@ -223,22 +223,19 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     CHECK(ensure(E.depths, (size_t)N * 4));
     CHECK(ensure(E.radii, (size_t)N * 4));
     CHECK(ensure(E.rect, (size_t)N * 8));
-    const size_t ndiff = (size_t)(cam->tiles_x + 1) * (cam->tiles_y + 1);
-    CHECK(ensure(E.tile_diff, ndiff * 4));
     CHECK(ensure(E.counts, (size_t)T * 4));
     CHECK(ensure(E.scan_tmp, (size_t)mskern::tile_scan_temp_ints(T) * 4));
     CHECK(ensure(E.offsets, (size_t)(T + 1) * 4));
-    CHECK(ensure(E.cursor, (size_t)T * 4));
     const int sxn = (cam->tiles_x + mskern::kSuperTile - 1) / mskern::kSuperTile;
     const int syn = (cam->tiles_y + mskern::kSuperTile - 1) / mskern::kSuperTile;
     const int NS = sxn * syn;
-    const size_t nsdiff = (size_t)(sxn + 1) * (syn + 1);
-    CHECK(ensure(E.super_diff, nsdiff * 4));
     CHECK(ensure(E.super_counts, (size_t)NS * 4));
     CHECK(ensure(E.super_offsets, (size_t)(NS + 1) * 4));
     CHECK(ensure(E.super_cursor, (size_t)NS * 4));
     CHECK(ensure(E.super_tmp, (size_t)mskern::tile_scan_temp_ints(NS) * 4));
-    CHECK(ensure(E.stats, 64));  // [0..2] tiles: total, largest, 0; [4..6] super-tiles: total, largest, long lists
+    // stats (ints): [0..1] tiles: total, largest; [4..6] super-tiles: total,
+    // largest, long lists; [8..9] 64-bit intersection count from the projection
+    CHECK(ensure(E.stats, 64));
     CHECK(ensure(E.big_list, (size_t)NS * 4));
     CHECK(ensure(E.out_img, Pn * 12));
     CHECK(ensure(E.final_Ts, Pn * 12));
@@ -261,23 +258,26 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     for (int i = 0; i < ST_COUNT; ++i) E.stage_valid[i] = false;
 
     stage_mark(ST_PROJECT);
-    HIPC(hipMemsetAsync(E.tile_diff.p, 0, ndiff * 4, s));
-    HIPC(hipMemsetAsync(E.super_diff.p, 0, nsdiff * 4, s));
+    HIPC(hipMemsetAsync(E.stats.p, 0, 64, s));
+    HIPC(hipMemsetAsync(E.super_counts.p, 0, (size_t)NS * 4, s));
     if (E.count_pairs) HIPC(hipMemsetAsync(E.pair_counter.p, 0, 8, s));
     mskern::launch_project_fwd(s, *cam, *g, P<float>(E.rec), P<float>(E.depths), P<int>(E.radii),
-                               P<uint32_t>(E.rect), P<int>(E.tile_diff), P<int>(E.super_diff), nullptr);
+                               P<uint32_t>(E.rect), reinterpret_cast<unsigned long long *>(P<int>(E.stats) + 8),
+                               nullptr);
     stage_mark(ST_SCAN);
-    mskern::launch_scan_tiles(s, cam->tiles_x, cam->tiles_y, P<int>(E.tile_diff), P<int>(E.counts),
-                              P<int>(E.offsets), P<int>(E.cursor), P<int>(E.stats), P<int>(E.scan_tmp));
-    mskern::launch_scan_tiles(s, sxn, syn, P<int>(E.super_diff), P<int>(E.super_counts), P<int>(E.super_offsets),
-                              P<int>(E.super_cursor), P<int>(E.stats) + 4, P<int>(E.super_tmp));
-    HIPC(hipMemcpyAsync(E.pinned_i, E.stats.p, 8 * sizeof(int), hipMemcpyDeviceToHost, s));
+    mskern::launch_super_count(s, N, cam->tiles_x, cam->tiles_y, P<int>(E.radii), P<uint32_t>(E.rect),
+                               P<int>(E.super_counts), P<int>(E.super_offsets), P<int>(E.super_cursor),
+                               P<int>(E.stats) + 4, P<int>(E.super_tmp));
+    HIPC(hipMemcpyAsync(E.pinned_i, E.stats.p, 16 * sizeof(int), hipMemcpyDeviceToHost, s));
     HIPC(hipStreamSynchronize(s));
-    const int I = E.pinned_i[0], S_total = E.pinned_i[4], super_max = E.pinned_i[5];
-    if (I < 0 || S_total < 0) {
-        set_err("tile intersection count overflowed int32");
+    unsigned long long isect64;
+    std::memcpy(&isect64, E.pinned_i + 8, sizeof(isect64));
+    const int S_total = E.pinned_i[4], super_max = E.pinned_i[5];
+    if (isect64 > 0x7fffffffull || S_total < 0) {
+        set_err("tile intersection count %llu overflows int32", isect64);
         return MSPLAT_E_CAPACITY;
     }
+    const int I = (int)isect64;
     E.num_isect = I;
     if (nisect) *nisect = I;
     stage_mark(ST_SCATTER_SORT);
@@ -285,9 +285,10 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     CHECK(ensure(E.ids, (size_t)I * 4));
     if (super_max > mskern::kSuperSortChunk) CHECK(ensure(E.keys_tmp, (size_t)S_total * 8));
     mskern::launch_bin_tiles(s, N, cam->tiles_x, cam->tiles_y, P<int>(E.radii), P<uint32_t>(E.rect),
-                             P<float>(E.depths), P<int>(E.offsets), P<int>(E.super_offsets), P<int>(E.super_cursor),
-                             super_max, P<uint64_t>(E.keys), P<uint64_t>(E.keys_tmp), P<int>(E.big_list),
-                             P<int>(E.stats) + 4, P<int>(E.ids));
+                             P<float>(E.depths), P<int>(E.super_offsets), P<int>(E.super_cursor), super_max,
+                             P<uint64_t>(E.keys), P<uint64_t>(E.keys_tmp), P<int>(E.big_list), P<int>(E.stats) + 4,
+                             P<int>(E.counts), P<int>(E.offsets), P<int>(E.stats), P<int>(E.scan_tmp),
+                             P<int>(E.ids));
     stage_mark(ST_RASTER_FWD);
     CHECK(raster_fwd_locked(log));
     HIPC(hipGetLastError());
@@ -396,8 +397,8 @@ void msplat_hip_cleanup(void) {
     Engine &E = g_eng;
     if (!E.ready) return;
     (void)hipStreamSynchronize(E.stream);
-    DevBuf *all[] = {&E.rec, &E.depths, &E.radii, &E.rect, &E.grads16, &E.colors_raw, &E.tile_diff, &E.counts, &E.scan_tmp, &E.super_diff, &E.super_counts, &E.super_offsets, &E.super_cursor, &E.super_tmp, &E.offsets,
-                     &E.cursor, &E.stats, &E.big_list, &E.keys, &E.keys_tmp, &E.ids, &E.blend_log, &E.t_ckpt, &E.wave_cnt, &E.out_img, &E.final_Ts,
+    DevBuf *all[] = {&E.rec, &E.depths, &E.radii, &E.rect, &E.grads16, &E.colors_raw, &E.counts, &E.scan_tmp, &E.super_counts, &E.super_offsets, &E.super_cursor, &E.super_tmp, &E.offsets,
+                     &E.stats, &E.big_list, &E.keys, &E.keys_tmp, &E.ids, &E.blend_log, &E.t_ckpt, &E.wave_cnt, &E.out_img, &E.final_Ts,
                      &E.final_idx, &E.out_depth, &E.out_normal, &E.out_alpha, &E.out_median, &E.out_dist,
                      &E.dL_dimg, &E.gm1, &E.gs1, &E.gs12, &E.partials, &E.loss, &E.dmeans, &E.dscales,
                      &E.dquats, &E.dmean2d, &E.dfdc, &E.dfrest, &E.dens_flags, &E.dens_scan, &E.pair_counter};

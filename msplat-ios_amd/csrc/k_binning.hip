@@ -6,14 +6,22 @@
 // tile list separately.  Here every intersection is kept and the per-tile
 // order is (depth bits, gaussian id), as the reference's keys define it.
 //
-//   1. counts: each visible splat adds its tile rectangle, and its rectangle
-//      of 4x4-tile super-tiles, to two 2D difference arrays (k_project_fwd);
-//      2D prefix sums + exclusive scans give tile offsets (the layout of
-//      the id list the rasterizers read) and super-tile offsets;
-//   2. k_scatter_super: one (depth bits << 32 | id) key per (splat,
-//      super-tile) pair -- about 2.5 per splat instead of one per tile;
-//   3. k_sort_super: each super-tile's keys sorted in LDS (bitonic, up to
-//      4096 keys), larger lists in 4096-key runs merged by k_merge_pass;
+// Device-scope atomics run at about 28 G/s on this part whether or not they
+// collide, so no stage issues one per tile entry:
+//   1. k_super_hist: one workgroup per chunk of several thousand splats
+//      counts its (splat, 4x4-tile super-tile) pairs in an LDS histogram and
+//      adds the non-zero bins to the global super-tile counts; an exclusive
+//      scan gives the super-tile offsets;
+//   2. k_scatter_super: each workgroup recounts its chunk, reserves one
+//      range per super-tile with a single global atomic, and places its
+//      (depth bits << 32 | id) keys with LDS atomics -- about 2.5 keys per
+//      splat instead of one per tile;
+//   3. k_sort_super: each super-tile counts the entries of its 16 tiles
+//      (the tile histogram, no atomics: a super-tile owns its tiles) and
+//      sorts its keys in LDS (bitonic, up to 4096 keys), larger lists in
+//      4096-key runs merged by k_merge_pass; an exclusive scan of the tile
+//      counts gives the tile offsets (the layout of the id list the
+//      rasterizers read);
 //   4. k_emit_tiles: each super-tile's sorted list is filtered, in order,
 //      into the id lists of its 16 tiles (wave ballots keep the order), so
 //      every tile list comes out sorted without a per-tile sort.
@@ -26,14 +34,12 @@ constexpr int kSortThreads = 256;
 constexpr int kChunk = 4096;  // keys per LDS sort (32 KB of u64)
 constexpr int kSuper = 4;     // tiles per super-tile side
 
-// ---- tile counts and offsets ----------------------------------------------
+// ---- counts -> offsets ------------------------------------------------------
 //
-// k_project_fwd records each visible splat's tile rectangle [x0,x1) x [y0,y1)
-// as four +-1 corner updates of a (tiles_y + 1) x (tiles_x + 1) difference
-// array (4 atomics per splat instead of one per covered tile); the tile
-// counts are its 2D inclusive prefix sum.  Then an exclusive scan gives the
-// tile offsets (prefix_sum_kernel, msplat_metal.metal:3093-3145), the
-// scatter cursors, the intersection total and the largest tile.
+// Exclusive scan of a count array (prefix_sum_kernel,
+// msplat_metal.metal:3093-3145): local pass over 2048 counts per workgroup,
+// block totals, add pass.  stats[0] receives the total, stats[1] the
+// largest count (stats[1] must be zero on entry).
 
 constexpr int kScanT = 256, kScanI = 8, kScanChunk = kScanT * kScanI;
 
@@ -59,66 +65,21 @@ __device__ __forceinline__ int block_scan_incl(int v, int *s_w, int *total) {
     return off + incl;
 }
 
-// Row pass: rows[y][x] = sum over x' <= x of diff[y][x'].
-__global__ __launch_bounds__(kScanT) void k_diff_rows(int tx, const int *__restrict__ diff, int *__restrict__ rows,
-                                                      int *__restrict__ stats) {
-    __shared__ int s_w[kScanT / 64];
-    const int y = blockIdx.x;
-    const int *d = diff + (size_t)y * (tx + 1);
-    int *r = rows + (size_t)y * tx;
-    int carry = 0;
-    for (int base = 0; base < tx; base += kScanT) {
-        const int x = base + (int)threadIdx.x;
-        int total;
-        const int incl = block_scan_incl(x < tx ? d[x] : 0, s_w, &total);
-        if (x < tx) r[x] = carry + incl;
-        carry += total;
-    }
-    if (y == 0 && threadIdx.x == 0) {
-        stats[1] = 0;  // largest tile, filled by k_diff_cols
-        stats[2] = 0;  // long-list count, filled by k_sort_super
-    }
-}
-
-// Column pass, in place: counts[y][x] = sum over y' <= y of rows[y'][x].
-// 64 columns per workgroup, the rows split in four runs (one per wave).
-__global__ __launch_bounds__(kScanT) void k_diff_cols(int tx, int ty, int *__restrict__ counts,
-                                                      int *__restrict__ stats) {
-    __shared__ int s_part[4][64];
-    const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
-    const int col = blockIdx.x * 64 + lane;
-    const int run_len = (ty + 3) / 4, y0 = min(ty, g * run_len), y1 = min(ty, y0 + run_len);
-    int part = 0;
-    if (col < tx)
-        for (int y = y0; y < y1; ++y) part += counts[(size_t)y * tx + col];
-    s_part[g][lane] = part;
-    __syncthreads();
-    int run = 0;
-    for (int k = 0; k < g; ++k) run += s_part[k][lane];
-    int mx = 0;
-    if (col < tx)
-        for (int y = y0; y < y1; ++y) {
-            run += counts[(size_t)y * tx + col];
-            counts[(size_t)y * tx + col] = run;
-            mx = max(mx, run);
-        }
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) mx = max(mx, __shfl_xor(mx, d, 64));
-    if (lane == 0) atomicMax(&stats[1], mx);
-}
-
-// Exclusive scan of the T tile counts: local pass (2048 counts per
-// workgroup), block totals, add pass.
 __global__ __launch_bounds__(kScanT) void k_off_local(int T, const int *__restrict__ counts,
-                                                      int *__restrict__ offsets, int *__restrict__ totals) {
+                                                      int *__restrict__ offsets, int *__restrict__ totals,
+                                                      int *__restrict__ stats) {
     __shared__ int s_w[kScanT / 64];
     const int base = blockIdx.x * kScanChunk + threadIdx.x * kScanI;
-    int v[kScanI], sum = 0;
+    int v[kScanI], sum = 0, mx = 0;
 #pragma unroll
     for (int k = 0; k < kScanI; ++k) {
         v[k] = base + k < T ? counts[base + k] : 0;
         sum += v[k];
+        mx = max(mx, v[k]);
     }
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) mx = max(mx, __shfl_xor(mx, d, 64));
+    if ((threadIdx.x & 63) == 0 && mx > 0) atomicMax(&stats[1], mx);
     int total;
     int run = block_scan_incl(sum, s_w, &total) - sum;
 #pragma unroll
@@ -167,38 +128,111 @@ __global__ __launch_bounds__(kScanT) void k_off_add(int T, int *__restrict__ off
         if (base + k < T) {
             const int v = offsets[base + k] + o;
             offsets[base + k] = v;
-            cursor[base + k] = v;
+            if (cursor) cursor[base + k] = v;
         }
     if (blockIdx.x == 0 && threadIdx.x == 0) offsets[T] = stats[0];
 }
 
-// One key per (visible splat, super-tile of its rectangle) at an atomically
-// claimed slot of the super-tile's range.  The rectangles of a wave are
-// enumerated cooperatively (wave_expand), so the 64 lanes issue independent
-// atomics instead of serial per-lane loops.
-__global__ __launch_bounds__(256) void k_scatter_super(int n, int sxn, const int *__restrict__ radii,
-                                                       const uint2 *__restrict__ rect,
-                                                       const float *__restrict__ depths, int *__restrict__ cursor,
-                                                       unsigned long long *__restrict__ keys) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    const bool vis = i < n && radii[i] > 0;
-    const uint2 r = vis ? rect[i] : make_uint2(0u, 0u);
-    const int x0 = r.x & 0xffff, y0 = r.x >> 16, x1 = r.y & 0xffff, y1 = r.y >> 16;
-    const bool ok = vis && x1 > x0 && y1 > y0;
-    const int sx0 = x0 / kSuper, sy0 = y0 / kSuper;
-    const int sw = ok ? (x1 + kSuper - 1) / kSuper - sx0 : 1;
-    const int sh = ok ? (y1 + kSuper - 1) / kSuper - sy0 : 0;
-    const uint32_t dbits = ok ? __float_as_uint(depths[i]) : 0u;
-    msd::wave_expand(ok ? sw * sh : 0, [&](int owner, int k, bool active) {
-        const int ow = __shfl(sw, owner, 64), ox = __shfl(sx0, owner, 64), oy = __shfl(sy0, owner, 64);
-        const uint32_t od = (uint32_t)__shfl((int)dbits, owner, 64);
-        const int oi = __shfl(i, owner, 64);
-        if (active) {
-            const int ry = k / ow;
-            const int pos = atomicAdd(&cursor[(oy + ry) * sxn + ox + (k - ry * ow)], 1);
-            keys[pos] = ((unsigned long long)od << 32) | (unsigned long long)(uint32_t)oi;
+// ---- super-tile histogram and scatter -------------------------------------
+//
+// Both kernels give workgroup b the splats [b * chunk, (b + 1) * chunk) and
+// count their (splat, super-tile) pairs in an LDS histogram, in windows of
+// kHistBins super-tiles.  The rectangles of a wave are enumerated
+// cooperatively (wave_expand), so the 64 lanes issue independent LDS atomics
+// instead of serial per-lane loops of different lengths.
+
+constexpr int kBinThreads = 1024;
+constexpr int kHistBins = 16384;  // super-tiles per LDS window (64 KB)
+
+struct SuperRect {
+    int sx0, sy0, sw, sh;  // super-tile rectangle, sw * sh pairs (0 if none)
+};
+
+__device__ __forceinline__ SuperRect super_rect(int i, int n, const int *__restrict__ radii,
+                                                const uint2 *__restrict__ rect) {
+    SuperRect r{0, 0, 1, 0};
+    if (i < n && radii[i] > 0) {
+        const uint2 q = rect[i];
+        const int x0 = q.x & 0xffff, y0 = q.x >> 16, x1 = q.y & 0xffff, y1 = q.y >> 16;
+        if (x1 > x0 && y1 > y0) {
+            r.sx0 = x0 / kSuper;
+            r.sy0 = y0 / kSuper;
+            r.sw = (x1 + kSuper - 1) / kSuper - r.sx0;
+            r.sh = (y1 + kSuper - 1) / kSuper - r.sy0;
         }
-    });
+    }
+    return r;
+}
+
+// fn(bin, splat) for every (splat, super-tile) pair of this workgroup's
+// chunk whose super-tile index lies in [w0, w0 + nbin).
+template <typename F>
+__device__ __forceinline__ void for_pairs(int n, int chunk, int sxn, int w0, int nbin, const int *__restrict__ radii,
+                                          const uint2 *__restrict__ rect, F &&fn) {
+    const int c0 = blockIdx.x * chunk, c1 = min(n, c0 + chunk);
+    for (int base = c0; base < c1; base += kBinThreads) {
+        const int i = base + (int)threadIdx.x;
+        const SuperRect r = super_rect(i < c1 ? i : n, n, radii, rect);
+        msd::wave_expand(r.sw * r.sh, [&](int owner, int k, bool active) {
+            const int ow = __shfl(r.sw, owner, 64), ox = __shfl(r.sx0, owner, 64), oy = __shfl(r.sy0, owner, 64);
+            const int oi = __shfl(i, owner, 64);
+            if (active) {
+                const int ry = k / ow;
+                const int bin = (oy + ry) * sxn + ox + (k - ry * ow) - w0;
+                if (bin >= 0 && bin < nbin) fn(bin, oi);
+            }
+        });
+    }
+}
+
+// Pair counts per super-tile: the LDS histogram of each window is added to
+// super_counts (zeroed by the caller) with one atomic per non-zero bin.
+__global__ __launch_bounds__(kBinThreads) void k_super_hist(int n, int chunk, int sxn, int NS,
+                                                            const int *__restrict__ radii,
+                                                            const uint2 *__restrict__ rect,
+                                                            int *__restrict__ super_counts) {
+    __shared__ int s_h[kHistBins];
+    for (int w0 = 0; w0 < NS; w0 += kHistBins) {
+        const int nbin = min(kHistBins, NS - w0);
+        for (int k = threadIdx.x; k < nbin; k += kBinThreads) s_h[k] = 0;
+        __syncthreads();
+        for_pairs(n, chunk, sxn, w0, nbin, radii, rect, [&](int bin, int) { atomicAdd(&s_h[bin], 1); });
+        __syncthreads();
+        for (int k = threadIdx.x; k < nbin; k += kBinThreads)
+            if (s_h[k]) atomicAdd(&super_counts[w0 + k], s_h[k]);
+        __syncthreads();
+    }
+}
+
+// One (depth bits << 32 | id) key per (visible splat, super-tile) pair.  Per
+// window the workgroup recounts its pairs, claims one range per non-zero
+// super-tile from super_cursor (the scanned offsets) with a single global
+// atomic, and places its keys in that range with LDS atomics.  The order
+// inside a super-tile list is arbitrary; k_sort_super orders it.
+__global__ __launch_bounds__(kBinThreads) void k_scatter_super(int n, int chunk, int sxn, int NS,
+                                                               const int *__restrict__ radii,
+                                                               const uint2 *__restrict__ rect,
+                                                               const float *__restrict__ depths,
+                                                               int *__restrict__ super_cursor,
+                                                               unsigned long long *__restrict__ keys) {
+    __shared__ int s_h[kHistBins];
+    for (int w0 = 0; w0 < NS; w0 += kHistBins) {
+        const int nbin = min(kHistBins, NS - w0);
+        for (int k = threadIdx.x; k < nbin; k += kBinThreads) s_h[k] = 0;
+        __syncthreads();
+        for_pairs(n, chunk, sxn, w0, nbin, radii, rect, [&](int bin, int) { atomicAdd(&s_h[bin], 1); });
+        __syncthreads();
+        for (int k = threadIdx.x; k < nbin; k += kBinThreads) {
+            const int c = s_h[k];
+            s_h[k] = c ? atomicAdd(&super_cursor[w0 + k], c) : 0;
+        }
+        __syncthreads();
+        for_pairs(n, chunk, sxn, w0, nbin, radii, rect, [&](int bin, int gid) {
+            const int pos = atomicAdd(&s_h[bin], 1);
+            keys[pos] = ((unsigned long long)__float_as_uint(depths[gid]) << 32) | (unsigned long long)(uint32_t)gid;
+        });
+        __syncthreads();
+    }
 }
 
 // Ascending bitonic sort of `cnt` (<= kChunk) keys in LDS, padded to a power
@@ -225,15 +259,51 @@ __device__ void lds_bitonic(unsigned long long *s, const unsigned long long *src
     }
 }
 
-// Sorts each super-tile list in place; lists longer than kChunk are sorted
-// in kChunk runs and queued on big_list for the merge passes.
-__global__ __launch_bounds__(kSortThreads) void k_sort_super(const int *__restrict__ offsets,
+// Counts the entries of the super-tile's 16 tiles (each entry covers the
+// tiles of its rectangle inside the super-tile) into tile_counts, then sorts
+// the super-tile list in place; lists longer than kChunk are sorted in
+// kChunk runs and queued on big_list for the merge passes.
+__global__ __launch_bounds__(kSortThreads) void k_sort_super(int tiles_x, int tiles_y, int sxn,
+                                                             const int *__restrict__ offsets,
                                                              unsigned long long *__restrict__ keys,
+                                                             const uint2 *__restrict__ rect,
+                                                             int *__restrict__ tile_counts,
                                                              int *__restrict__ big_list, int *__restrict__ stats) {
     __shared__ unsigned long long s[kChunk];
+    __shared__ int s_tc[kSuper * kSuper];
     const int t = blockIdx.x;
     const int start = offsets[t], end = offsets[t + 1];
     const int cnt = end - start;
+    const int stx = (t % sxn) * kSuper, sty = (t / sxn) * kSuper;
+    if (threadIdx.x < kSuper * kSuper) s_tc[threadIdx.x] = 0;
+    __syncthreads();
+    {
+        int tc[kSuper * kSuper];
+#pragma unroll
+        for (int q = 0; q < kSuper * kSuper; ++q) tc[q] = 0;
+        for (int e = threadIdx.x; e < cnt; e += kSortThreads) {
+            const uint2 r = rect[(uint32_t)(keys[start + e] & 0xffffffffull)];
+            const int rx0 = max((int)(r.x & 0xffff) - stx, 0), rx1 = min((int)(r.y & 0xffff) - stx, kSuper);
+            const int ry0 = max((int)(r.x >> 16) - sty, 0), ry1 = min((int)(r.y >> 16) - sty, kSuper);
+#pragma unroll
+            for (int q = 0; q < kSuper * kSuper; ++q) {
+                const int lx = q % kSuper, ly = q / kSuper;
+                tc[q] += (lx >= rx0 && lx < rx1 && ly >= ry0 && ly < ry1) ? 1 : 0;
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < kSuper * kSuper; ++q) {
+            int v = tc[q];
+#pragma unroll
+            for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+            if ((threadIdx.x & 63) == 0 && v) atomicAdd(&s_tc[q], v);
+        }
+        __syncthreads();
+        if (threadIdx.x < kSuper * kSuper) {
+            const int tx = stx + (int)threadIdx.x % kSuper, ty = sty + (int)threadIdx.x / kSuper;
+            if (tx < tiles_x && ty < tiles_y) tile_counts[ty * tiles_x + tx] = s_tc[threadIdx.x];
+        }
+    }
     if (cnt <= 1) return;
     for (int c0 = start; c0 < end; c0 += kChunk) {
         const int c = min(kChunk, end - c0);
@@ -360,29 +430,48 @@ namespace mskern {
 
 int64_t tile_scan_temp_ints(int T) { return (T + kScanChunk - 1) / kScanChunk + 1; }
 
-void launch_scan_tiles(hipStream_t s, int tiles_x, int tiles_y, const int *diff, int *counts, int *offsets,
-                       int *cursor, int *stats, int *temp) {
-    const int T = tiles_x * tiles_y;
+// Exclusive scan of counts[T] into offsets[T + 1] (and cursor[T] if given);
+// stats[0] = total, stats[1] = max(stats[1], largest count).
+static void launch_scan_counts(hipStream_t s, int T, const int *counts, int *offsets, int *cursor, int *stats,
+                               int *temp) {
     const int nb = (T + kScanChunk - 1) / kScanChunk;
-    hipLaunchKernelGGL(k_diff_rows, dim3(tiles_y), dim3(kScanT), 0, s, tiles_x, diff, counts, stats);
-    hipLaunchKernelGGL(k_diff_cols, dim3((tiles_x + 63) / 64), dim3(kScanT), 0, s, tiles_x, tiles_y, counts, stats);
-    hipLaunchKernelGGL(k_off_local, dim3(nb), dim3(kScanT), 0, s, T, counts, offsets, temp);
+    hipLaunchKernelGGL(k_off_local, dim3(nb), dim3(kScanT), 0, s, T, counts, offsets, temp, stats);
     hipLaunchKernelGGL(k_off_totals, dim3(1), dim3(1024), 0, s, nb, temp, stats);
     hipLaunchKernelGGL(k_off_add, dim3(nb), dim3(kScanT), 0, s, T, offsets, cursor, temp, stats);
 }
 
-void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
-                      const float *depths, const int *tile_offsets, const int *super_offsets, int *super_cursor,
-                      int super_max, uint64_t *super_keys, uint64_t *super_keys_tmp, int *big_list,
-                      int *super_stats, int *ids) {
+static void bin_chunks(int n, int *blocks, int *chunk) {
+    *blocks = std::max(1, std::min(256, (n + 2047) / 2048));
+    *chunk = (n + *blocks - 1) / *blocks;
+}
+
+void launch_super_count(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
+                        int *super_counts, int *super_offsets, int *super_cursor, int *super_stats, int *temp) {
     const int sxn = (tiles_x + kSuper - 1) / kSuper, syn = (tiles_y + kSuper - 1) / kSuper, NS = sxn * syn;
+    int blocks, chunk;
+    bin_chunks(n, &blocks, &chunk);
+    if (n > 0)
+        hipLaunchKernelGGL(k_super_hist, dim3(blocks), dim3(kBinThreads), 0, s, n, chunk, sxn, NS, radii,
+                           reinterpret_cast<const uint2 *>(rect), super_counts);
+    launch_scan_counts(s, NS, super_counts, super_offsets, super_cursor, super_stats, temp);
+}
+
+void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
+                      const float *depths, const int *super_offsets, int *super_cursor, int super_max,
+                      uint64_t *super_keys, uint64_t *super_keys_tmp, int *big_list, int *super_stats,
+                      int *tile_counts, int *tile_offsets, int *tile_stats, int *tile_temp, int *ids) {
+    const int sxn = (tiles_x + kSuper - 1) / kSuper, syn = (tiles_y + kSuper - 1) / kSuper, NS = sxn * syn;
+    const int T = tiles_x * tiles_y;
     auto *k = reinterpret_cast<unsigned long long *>(super_keys);
     auto *kt = reinterpret_cast<unsigned long long *>(super_keys_tmp);
     const uint2 *r2 = reinterpret_cast<const uint2 *>(rect);
+    int blocks, chunk;
+    bin_chunks(n, &blocks, &chunk);
     if (n > 0)
-        hipLaunchKernelGGL(k_scatter_super, dim3((n + 255) / 256), dim3(256), 0, s, n, sxn, radii, r2, depths,
-                           super_cursor, k);
-    hipLaunchKernelGGL(k_sort_super, dim3(NS), dim3(kSortThreads), 0, s, super_offsets, k, big_list, super_stats);
+        hipLaunchKernelGGL(k_scatter_super, dim3(blocks), dim3(kBinThreads), 0, s, n, chunk, sxn, NS, radii, r2,
+                           depths, super_cursor, k);
+    hipLaunchKernelGGL(k_sort_super, dim3(NS), dim3(kSortThreads), 0, s, tiles_x, tiles_y, sxn, super_offsets, k,
+                       r2, tile_counts, big_list, super_stats);
     unsigned long long *src = k, *dst = kt;
     for (int L = kChunk; L < super_max; L <<= 1) {
         hipLaunchKernelGGL(k_merge_pass, dim3(64, 64), dim3(256), 0, s, L, super_offsets, big_list, super_stats, src,
@@ -393,6 +482,7 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
     // every list is in super_keys for the emission
     if (src != k)
         hipLaunchKernelGGL(k_copy_big, dim3(64, 64), dim3(256), 0, s, super_offsets, big_list, super_stats, src, k);
+    launch_scan_counts(s, T, tile_counts, tile_offsets, nullptr, tile_stats, tile_temp);
     hipLaunchKernelGGL(k_emit_tiles, dim3(NS), dim3(256), 0, s, tiles_x, tiles_y, sxn, super_offsets, k, r2,
                        tile_offsets, ids);
 }

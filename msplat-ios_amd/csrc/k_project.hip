@@ -31,13 +31,14 @@ __device__ __forceinline__ void stage_rows(float *__restrict__ dst, const float 
 
 // project_and_sh_forward_2dgs_kernel (msplat_metal.metal:1413-1521), with
 // the sigmoid of the sort/pack stage (:1684) and the raster's colour clamp
-// (:619) folded into the record.  Also builds the per-tile histogram that
-// the tile scan consumes (count pass of count -> scan -> scatter binning).
+// (:619) folded into the record.  Also sums the visible splats' tile
+// rectangle areas, the number of tile intersections the binning will emit
+// (one 64-bit atomic per workgroup).
 __global__ __launch_bounds__(kBlock) void k_project_fwd(
     MsplatCamera cam, int n, const float *__restrict__ means, const float *__restrict__ scales,
     const float *__restrict__ quats, const float *__restrict__ opac, const float *__restrict__ fdc,
     const float *__restrict__ frest, float4 *__restrict__ rec, float *__restrict__ depths,
-    int *__restrict__ radii, uint2 *__restrict__ rect, int *__restrict__ tile_diff, int *__restrict__ super_diff,
+    int *__restrict__ radii, uint2 *__restrict__ rect, unsigned long long *__restrict__ isect_total,
     float *__restrict__ colors_raw) {
     // The block's features_rest rows (up to 256 x 45 floats) are staged in LDS
     // with coalesced loads; each thread then reads its own row from LDS.
@@ -49,7 +50,7 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
         stage_rows(s_fr, frest + (size_t)b0 * K3, cnt * K3);
         __syncthreads();
     }
-    // No early return: every lane of the wave takes part in the tile count.
+    // No early return: every thread takes part in the intersection sum.
     const int i = blockIdx.x * kBlock + threadIdx.x;
     const bool valid = i < n;
     const int ii = valid ? i : 0;
@@ -138,22 +139,17 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
         colors_raw[3 * (size_t)i + 2] = col[2];
     }
     }
-    // tile histogram as a 2D difference array: +1 at (x0,y0) and (x1,y1),
-    // -1 at (x1,y0) and (x0,y1); its 2D prefix sum is the per-tile count
-    if (ok && x1 > x0 && y1 > y0) {
-        const int stride = cam.tiles_x + 1;
-        atomicAdd(&tile_diff[y0 * stride + x0], 1);
-        atomicAdd(&tile_diff[y0 * stride + x1], -1);
-        atomicAdd(&tile_diff[y1 * stride + x0], -1);
-        atomicAdd(&tile_diff[y1 * stride + x1], 1);
-        // the same for the rectangle of 4x4-tile super-tiles it touches
-        constexpr int S = mskern::kSuperTile;
-        const int sstride = (cam.tiles_x + S - 1) / S + 1;
-        const int sx0 = x0 / S, sy0 = y0 / S, sx1 = (x1 + S - 1) / S, sy1 = (y1 + S - 1) / S;
-        atomicAdd(&super_diff[sy0 * sstride + sx0], 1);
-        atomicAdd(&super_diff[sy0 * sstride + sx1], -1);
-        atomicAdd(&super_diff[sy1 * sstride + sx0], -1);
-        atomicAdd(&super_diff[sy1 * sstride + sx1], 1);
+    // intersections: sum of the rectangle areas over the workgroup
+    __shared__ unsigned long long s_area[kBlock / 64];
+    unsigned long long area = ok ? (unsigned long long)((x1 - x0) * (y1 - y0)) : 0ull;
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) area += __shfl_xor(area, d, 64);
+    if ((threadIdx.x & 63) == 0) s_area[threadIdx.x >> 6] = area;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long t = 0;
+        for (int w = 0; w < kBlock / 64; ++w) t += s_area[w];
+        if (t) atomicAdd(isect_total, t);
     }
 }
 
@@ -382,13 +378,13 @@ inline unsigned blocks_for(int64_t n, int b) { return (unsigned)((n + b - 1) / b
 namespace mskern {
 
 void launch_project_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, float *rec,
-                        float *depths, int *radii, uint32_t *rect, int *tile_diff, int *super_diff,
+                        float *depths, int *radii, uint32_t *rect, unsigned long long *isect_total,
                         float *colors_raw) {
     if (g.num_points <= 0) return;
     hipLaunchKernelGGL(k_project_fwd, dim3(blocks_for(g.num_points, kBlock)), dim3(kBlock), 0, s, cam,
                        g.num_points, g.means, g.scales, g.quats, g.opacities, g.features_dc, g.features_rest,
                        reinterpret_cast<float4 *>(rec), depths, radii, reinterpret_cast<uint2 *>(rect),
-                       tile_diff, super_diff, colors_raw);
+                       isect_total, colors_raw);
 }
 
 void launch_project_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, const int *radii,

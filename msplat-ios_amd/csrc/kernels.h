@@ -12,11 +12,10 @@
 namespace mskern {
 
 // k_project.hip
-// tile_diff / super_diff: zeroed (tiles_y + 1) x (tiles_x + 1) and
-// (syn + 1) x (sxn + 1) arrays receiving the +-1 corner updates of every
-// visible splat's tile rectangle and 4x4-tile super-tile rectangle.
+// isect_total (64-bit, zeroed by the caller) receives the number of tile
+// intersections, the sum of the visible splats' tile-rectangle areas.
 void launch_project_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, float *rec,
-                        float *depths, int *radii, uint32_t *rect, int *tile_diff, int *super_diff,
+                        float *depths, int *radii, uint32_t *rect, unsigned long long *isect_total,
                         float *colors_raw);
 void launch_project_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, const int *radii,
                         const float *g16, float *dmeans, float *dscales, float *dquats, float *dmean2d,
@@ -26,21 +25,22 @@ void launch_gather(hipStream_t s, const float *src, int src_stride, int src_off,
 void launch_tiles_hit(hipStream_t s, const uint32_t *rect, const int *radii, int *out, int n);
 
 // k_binning.hip
-// diff: (tiles_y + 1) x (tiles_x + 1) tile-rectangle difference array from
-// launch_project_fwd; writes counts[T], offsets[T + 1], cursor[T] and
-// stats = {intersections, largest tile, 0}.  temp: tile_scan_temp_ints(T).
+// Super-tiles are 4x4 tiles: sxn = ceil(tiles_x / 4), syn = ceil(tiles_y / 4),
+// NS = sxn * syn.  Scan temporaries: tile_scan_temp_ints(count) ints.
 int64_t tile_scan_temp_ints(int T);
-void launch_scan_tiles(hipStream_t s, int tiles_x, int tiles_y, const int *diff, int *counts, int *offsets,
-                       int *cursor, int *stats, int *temp);
-// Super-tiles are 4x4 tiles: sxn = ceil(tiles_x / 4), syn = ceil(tiles_y / 4).
-// super_offsets / super_cursor / super_stats come from launch_scan_tiles on
-// the super-tile difference array; super_max is its largest list,
-// super_keys_tmp is needed (size of super_keys) when super_max > 4096.
-// Writes the per-tile sorted gaussian ids at tile_offsets.
+// (splat, super-tile) pair counts -> super_offsets[NS + 1], super_cursor[NS];
+// super_stats = {pairs, largest list, long-list count}.  super_counts[NS]
+// and super_stats[0..2] must be zero on entry.
+void launch_super_count(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
+                        int *super_counts, int *super_offsets, int *super_cursor, int *super_stats, int *temp);
+// Scatter, per-super-tile sort (super_keys_tmp, the size of super_keys, is
+// needed when super_max > 4096), tile counts and offsets (tile_offsets[T + 1],
+// tile_stats = {intersections, largest tile}, zero on entry) and the
+// per-tile sorted gaussian ids.
 void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
-                      const float *depths, const int *tile_offsets, const int *super_offsets, int *super_cursor,
-                      int super_max, uint64_t *super_keys, uint64_t *super_keys_tmp, int *big_list,
-                      int *super_stats, int *ids);
+                      const float *depths, const int *super_offsets, int *super_cursor, int super_max,
+                      uint64_t *super_keys, uint64_t *super_keys_tmp, int *big_list, int *super_stats,
+                      int *tile_counts, int *tile_offsets, int *tile_stats, int *tile_temp, int *ids);
 constexpr int kSuperTile = 4;
 constexpr int kSuperSortChunk = 4096;
 
