@@ -58,7 +58,8 @@ struct Engine {
     int64_t num_isect = 0;
     const float *bg = nullptr;
     bool have_grads = false;
-    bool log_valid = false;  // blend log written by the most recent forward
+    bool log_valid = false;   // blend log written for the most recent forward
+    bool full_valid = false;  // depth / normal / alpha / median / distortion outputs written
     // timing
     bool timing = false;       // HIP events per stage
     bool count_pairs = false;  // raster pair counter
@@ -182,8 +183,12 @@ int validate_cam(const MsplatCamera *cam, const MsplatGaussians *g) {
 }
 
 // Stages a3-a7: projection, binning, per-tile sort, rasterize forward.
-// With log, the raster forward also writes the blend log the backward replays.
-int raster_fwd_locked(bool log) {
+// With log, the raster forward also writes the blend log the backward
+// replays; with full, it also produces the depth, normal, alpha, median and
+// distortion outputs.  The forward is deterministic, so running it again on
+// the same tile lists (to add the log or the full outputs on demand)
+// reproduces every value it wrote before.
+int raster_fwd_locked(bool log, bool full) {
     Engine &E = g_eng;
     uint32_t *lg = nullptr;
     float *tc = nullptr;
@@ -202,12 +207,14 @@ int raster_fwd_locked(bool log) {
                               P<float>(E.rec), E.bg, P<float>(E.out_img), P<float>(E.final_Ts), P<int>(E.final_idx),
                               P<float>(E.out_depth), P<float>(E.out_normal), P<float>(E.out_alpha),
                               P<float>(E.out_median), P<float>(E.out_dist),
-                              E.count_pairs ? P<unsigned long long>(E.pair_counter) : nullptr, lg, tc, wc);
-    E.log_valid = log;
+                              E.count_pairs ? P<unsigned long long>(E.pair_counter) : nullptr, lg, tc, wc, full);
+    E.log_valid = E.log_valid || log;
+    E.full_valid = E.full_valid || full;
     return MSPLAT_OK;
 }
 
-int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, int64_t *nisect, bool log) {
+int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, int64_t *nisect, bool log,
+                   bool full) {
     CHECK(validate_cam(cam, g));
     if (!bg) {
         set_err("null background");
@@ -255,6 +262,7 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     E.bg = bg;
     E.have_grads = false;
     E.log_valid = false;
+    E.full_valid = false;
     for (int i = 0; i < ST_COUNT; ++i) E.stage_valid[i] = false;
 
     stage_mark(ST_PROJECT);
@@ -290,7 +298,7 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
                              P<int>(E.counts), P<int>(E.offsets), P<int>(E.stats), P<int>(E.scan_tmp),
                              P<int>(E.ids));
     stage_mark(ST_RASTER_FWD);
-    CHECK(raster_fwd_locked(log));
+    CHECK(raster_fwd_locked(log, full));
     HIPC(hipGetLastError());
     return MSPLAT_OK;
 }
@@ -314,6 +322,15 @@ int last_locked(int which, void **ptr, int64_t *numel) {
     Engine &E = g_eng;
     *ptr = nullptr;
     *numel = 0;
+    switch (which) {
+        case MSPLAT_LAST_FINAL_TS: case MSPLAT_LAST_FINAL_IDX: case MSPLAT_LAST_OUT_DEPTH:
+        case MSPLAT_LAST_OUT_NORMAL: case MSPLAT_LAST_OUT_ALPHA: case MSPLAT_LAST_OUT_MEDIAN_DEPTH:
+        case MSPLAT_LAST_OUT_DISTORTION:
+            // produced on demand after an image-only forward
+            if (E.rec.p && !E.full_valid) CHECK(raster_fwd_locked(false, true));
+            break;
+        default: break;
+    }
     const int64_t N = E.n, Pn = (int64_t)E.W * E.H;
     auto matf = [&](int idx, DevBuf &src, int stride, int off, int nf) -> int {
         CHECK(ensure(E.mat[idx], (size_t)N * nf * 4));
@@ -418,6 +435,7 @@ void msplat_hip_cleanup(void) {
     E.num_isect = 0;
     E.have_grads = false;
     E.log_valid = false;
+    E.full_valid = false;
 }
 
 const char *msplat_hip_last_error(void) { return g_err; }
@@ -502,7 +520,7 @@ int msplat_hip_sync(void) {
 int msplat_hip_render(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, int64_t *nisect) {
     API_BEGIN
     ENSURE_INIT();
-    CHECK(forward_locked(cam, g, bg, nisect, false));
+    CHECK(forward_locked(cam, g, bg, nisect, false, false));
     stage_mark(ST_LOSS);
     if (g_eng.count_pairs) HIPC(hipMemcpy(&g_eng.pairs, g_eng.pair_counter.p, 8, hipMemcpyDeviceToHost));
     if (g_eng.timing) {
@@ -528,7 +546,7 @@ int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g, con
     }
     Engine &E = g_eng;
     hipStream_t s = E.stream;
-    CHECK(forward_locked(cam, g, bg, nisect, true));
+    CHECK(forward_locked(cam, g, bg, nisect, true, lambda_dist != 0.f));
     const int N = g->num_points, W = cam->width, H = cam->height;
     const size_t Pn = (size_t)W * H;
     stage_mark(ST_LOSS);
@@ -692,9 +710,10 @@ int msplat_hip_raster_bwd(const float *dL_dimg, const float *dL_ddepth, const fl
         set_err("raster_bwd needs a preceding forward and dL_dimg / grads16");
         return MSPLAT_E_ARG;
     }
-    // a render-only forward skips the blend log; replay the (deterministic)
-    // raster forward with it
-    if (!E.log_valid) CHECK(raster_fwd_locked(true));
+    // a render-only forward skips the blend log, a training forward the full
+    // outputs; replay the deterministic raster forward with what is missing
+    const bool need_full = dL_ddepth || dL_dalpha || dL_dnormal || dL_dmedian || dL_ddist;
+    if (!E.log_valid || (need_full && !E.full_valid)) CHECK(raster_fwd_locked(true, need_full || E.full_valid));
     mskern::launch_raster_bwd(E.stream, E.W, E.H, E.tiles_x, E.tiles_y, P<int>(E.offsets), P<uint32_t>(E.blend_log),
                               P<float>(E.t_ckpt), P<int>(E.wave_cnt), P<float>(E.rec), E.bg, P<float>(E.final_Ts),
                               P<int>(E.final_idx), dL_dimg, dL_ddepth, dL_dalpha, dL_dnormal, dL_dmedian, dL_ddist,

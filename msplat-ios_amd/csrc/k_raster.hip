@@ -74,7 +74,12 @@ __device__ __forceinline__ int build_wave_lists(int m, unsigned char (*s_list)[k
 // every log entry k > 0 with k % 64 == 0 each lane also stores its
 // transmittance before that splat (a prefix checkpoint) at
 // t_ckpt[4 * start + wave * len + k + lane].
-template <bool LOG>
+// With FULL_OUT = false only what the image-only training step consumes is
+// produced: out_img, final_Ts[.][0] (T) and final_idx[.][0] (last
+// contributor); the depth, normal, alpha, median and distortion outputs and
+// the distortion moments are neither accumulated nor written.  Every
+// decision, and so every produced value, is the same as with FULL_OUT.
+template <bool LOG, bool FULL_OUT>
 __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     int W, int H, int tiles_x, int T, const int *__restrict__ offsets, const int *__restrict__ ids,
     const float4 *__restrict__ rec, const float *__restrict__ bgp, float *__restrict__ out_img,
@@ -130,23 +135,25 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
                     } else {
                         blend = true;
                         const float w = e.alpha * Tr;
-                        const float A = 1.f - Tr;
-                        const float m_ = kMScale * (1.f - NEAR_N / e.depth);
-                        dist = __builtin_fmaf(m_ * m_ * A + M2 - 2.f * m_ * M1, w, dist);
-                        M1 = __builtin_fmaf(m_, w, M1);
-                        M2 = __builtin_fmaf(m_ * m_, w, M2);
-                        if (Tr > 0.5f) {
-                            med = e.depth;
-                            med_c = base + t;
-                        }
                         const float4 q3 = s_rec[3 * kThreads + t], q4 = s_rec[4 * kThreads + t];
+                        if (FULL_OUT) {
+                            const float A = 1.f - Tr;
+                            const float m_ = kMScale * (1.f - NEAR_N / e.depth);
+                            dist = __builtin_fmaf(m_ * m_ * A + M2 - 2.f * m_ * M1, w, dist);
+                            M1 = __builtin_fmaf(m_, w, M1);
+                            M2 = __builtin_fmaf(m_ * m_, w, M2);
+                            if (Tr > 0.5f) {
+                                med = e.depth;
+                                med_c = base + t;
+                            }
+                            dep = __builtin_fmaf(e.depth, w, dep);
+                            nx = __builtin_fmaf(q3.x, w, nx);
+                            ny = __builtin_fmaf(q3.y, w, ny);
+                            nz = __builtin_fmaf(q3.z, w, nz);
+                        }
                         cr = __builtin_fmaf(q3.w, w, cr);
                         cg = __builtin_fmaf(q4.x, w, cg);
                         cb = __builtin_fmaf(q4.y, w, cb);
-                        dep = __builtin_fmaf(e.depth, w, dep);
-                        nx = __builtin_fmaf(q3.x, w, nx);
-                        ny = __builtin_fmaf(q3.y, w, ny);
-                        nz = __builtin_fmaf(q3.z, w, nz);
                         Tr = next_T;
                         last_c = base + t;
                     }
@@ -178,13 +185,14 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     if (!inside) return;
     const size_t pix = (size_t)pyi * W + pxi;
     final_Ts[3 * pix + 0] = Tr;
-    final_Ts[3 * pix + 1] = M1;
-    final_Ts[3 * pix + 2] = M2;
     final_idx[2 * pix + 0] = last_c;
-    final_idx[2 * pix + 1] = med_c;
     out_img[3 * pix + 0] = __builtin_fmaf(bg0, Tr, cr);
     out_img[3 * pix + 1] = __builtin_fmaf(bg1, Tr, cg);
     out_img[3 * pix + 2] = __builtin_fmaf(bg2, Tr, cb);
+    if (!FULL_OUT) return;
+    final_Ts[3 * pix + 1] = M1;
+    final_Ts[3 * pix + 2] = M2;
+    final_idx[2 * pix + 1] = med_c;
     out_depth[pix] = dep;
     out_normal[3 * pix + 0] = nx;
     out_normal[3 * pix + 1] = ny;
@@ -501,18 +509,20 @@ namespace mskern {
 void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
                        const float *rec, const float *bg, float *out_img, float *final_Ts, int *final_idx,
                        float *out_depth, float *out_normal, float *out_alpha, float *out_median, float *out_dist,
-                       unsigned long long *pair_counter, uint32_t *blend_log, float *t_ckpt, int *wave_cnt) {
+                       unsigned long long *pair_counter, uint32_t *blend_log, float *t_ckpt, int *wave_cnt,
+                       bool full_outputs) {
     const int T = tiles_x * tiles_y;
     const int grid = ((T + 7) / 8) * 8;
     auto *lg = reinterpret_cast<uint4 *>(blend_log);
+    auto launch = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
+                           reinterpret_cast<const float4 *>(rec), bg, out_img, final_Ts, final_idx, out_depth,
+                           out_normal, out_alpha, out_median, out_dist, pair_counter, lg, t_ckpt, wave_cnt);
+    };
     if (blend_log)
-        hipLaunchKernelGGL(k_raster_fwd<true>, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
-                           reinterpret_cast<const float4 *>(rec), bg, out_img, final_Ts, final_idx, out_depth,
-                           out_normal, out_alpha, out_median, out_dist, pair_counter, lg, t_ckpt, wave_cnt);
+        full_outputs ? launch(k_raster_fwd<true, true>) : launch(k_raster_fwd<true, false>);
     else
-        hipLaunchKernelGGL(k_raster_fwd<false>, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
-                           reinterpret_cast<const float4 *>(rec), bg, out_img, final_Ts, final_idx, out_depth,
-                           out_normal, out_alpha, out_median, out_dist, pair_counter, lg, t_ckpt, wave_cnt);
+        full_outputs ? launch(k_raster_fwd<false, true>) : launch(k_raster_fwd<false, false>);
 }
 
 void launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets,

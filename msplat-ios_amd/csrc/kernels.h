@@ -45,13 +45,16 @@ constexpr int kSuperTile = 4;
 constexpr int kSuperSortChunk = 4096;
 
 // k_raster.hip
-// blend_log (4 * I entries of 16 bytes), t_ckpt (4 * I floats) and wave_cnt
-// (4 * T ints) receive the per-wave blend log and transmittance checkpoints
-// the backward replays; pass nullptr for render-only frames.
+// blend_log (4 * I entries of 16 bytes), t_ckpt (4 * I + 64 floats) and
+// wave_cnt (4 * T ints) receive the per-wave blend log and transmittance
+// checkpoints the backward replays; pass nullptr for render-only frames.
+// full_outputs = false produces only out_img, final_Ts[.][0] and
+// final_idx[.][0] (what the image-only training step consumes).
 void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
                        const float *rec, const float *bg, float *out_img, float *final_Ts, int *final_idx,
                        float *out_depth, float *out_normal, float *out_alpha, float *out_median, float *out_dist,
-                       unsigned long long *pair_counter, uint32_t *blend_log, float *t_ckpt, int *wave_cnt);
+                       unsigned long long *pair_counter, uint32_t *blend_log, float *t_ckpt, int *wave_cnt,
+                       bool full_outputs);
 void launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets,
                        const uint32_t *blend_log, const float *t_ckpt, const int *wave_cnt, const float *rec,
                        const float *bg, const float *final_Ts, const int *final_idx, const float *dL_dimg,

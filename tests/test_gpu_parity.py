@@ -307,6 +307,12 @@ def test_train_step_matches_oracle(orc, eng):
     assert nis == nis_o
     assert abs(loss - loss_o) <= 1e-5 * abs(loss_o)
     _assert_bitexact(E.last("out_img", img_o.shape), img_o, "rendered image")
+    # the outputs the image-only training forward skips are produced on
+    # demand, bit-identical to a full forward of the same (pre-step) splats
+    _, _, _, full_o = orc.render(scene, 0)
+    for k in ("final_Ts", "final_idx", "out_depth", "out_normal", "out_alpha", "out_median_depth",
+              "out_distortion"):
+        _assert_bitexact(E.last(k, full_o[k].shape), full_o[k], k)
     got = ds.host_params()
     names = list(got)
     for k, p_o, p0, lr in zip(names, params, scene.params(), D.LR_INIT):
