@@ -34,15 +34,16 @@ def algorithmic_bytes(stage: str, N: int, I: int, P: int, T: int) -> float:
     tile; raster forward 76 B per intersection + 20 B per pixel (the
     training forward produces the image, the final transmittance and the
     last contributor; the other per-pixel outputs are made on demand); SSIM + L1
-    36 B per pixel; raster backward 140 B per intersection + 60 B per pixel +
-    64 B per splat; projection backward fused with Adam 1716 B per splat."""
+    36 B per pixel; raster backward 140 B per intersection + 16 B per pixel
+    (the final transmittance and dL/dimage) + 64 B per splat; projection
+    backward fused with Adam 1716 B per splat."""
     return {
         "project_fwd": 312.0 * N,
         "tile_scan": 12.0 * T,
         "scatter_sort": 32.0 * N + 20.0 * I + 8.0 * T,
         "raster_fwd": 76.0 * I + 20.0 * P,
         "ssim_l1": 36.0 * P,
-        "raster_bwd": 140.0 * I + 60.0 * P + 64.0 * N,
+        "raster_bwd": 140.0 * I + 16.0 * P + 64.0 * N,
         "project_bwd_adam": 1716.0 * N,
     }.get(stage, 0.0)
 
