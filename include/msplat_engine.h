@@ -269,6 +269,12 @@ int msplat_hip_enable_timing(int flags);
 int msplat_hip_stage_times(const char **names, float *ms, int max);
 /* Pair counter of the most recent forward run with MSPLAT_TIMING_PAIRS. */
 int64_t msplat_hip_last_pairs_evaluated(void);
+/* Counters of the same forward: out[0] = (pixel, gaussian) pairs evaluated,
+ * out[1] = blend-log entries (visits of a wave in which at least one pixel
+ * blended the gaussian; 0 for a forward without the log), out[2] =
+ * (pixel, gaussian) pairs blended.  No counterpart in the reference: it
+ * measures the rasterizers' work. */
+int msplat_hip_last_raster_counts(int64_t out[3]);
 
 #ifdef __cplusplus
 }

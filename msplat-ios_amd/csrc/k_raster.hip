@@ -110,7 +110,7 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
 
     __shared__ unsigned char s_list[4][kThreads];
     __shared__ int s_cnt[4][4];
-    int evals = 0;
+    int evals = 0, blends = 0;
     for (int b0 = start; b0 < end; b0 += kThreads) {
         if (__syncthreads_and(done)) break;
         const int idx = b0 + (int)threadIdx.x;
@@ -134,6 +134,7 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
                         done = true;
                     } else {
                         blend = true;
+                        ++blends;
                         const float w = e.alpha * Tr;
                         const float4 q3 = s_rec[3 * kThreads + t], q4 = s_rec[4 * kThreads + t];
                         if (FULL_OUT) {
@@ -174,13 +175,16 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     }
     if (LOG && lane == 0) wave_cnt[4 * tile + wave] = nlog;
     if (pair_counter) {
-        __shared__ unsigned int s_pairs;
+        // {pairs evaluated, log entries, pairs blended}
+        __shared__ unsigned int s_cnt3[3];
         __syncthreads();
-        if (threadIdx.x == 0) s_pairs = 0;
+        if (threadIdx.x < 3) s_cnt3[threadIdx.x] = 0;
         __syncthreads();
-        atomicAdd(&s_pairs, (unsigned)evals);
+        atomicAdd(&s_cnt3[0], (unsigned)evals);
+        atomicAdd(&s_cnt3[2], (unsigned)blends);
+        if (lane == 0) atomicAdd(&s_cnt3[1], (unsigned)nlog);
         __syncthreads();
-        if (threadIdx.x == 0) atomicAdd(pair_counter, (unsigned long long)s_pairs);
+        if (threadIdx.x < 3) atomicAdd(pair_counter + threadIdx.x, (unsigned long long)s_cnt3[threadIdx.x]);
     }
     if (!inside) return;
     const size_t pix = (size_t)pyi * W + pxi;

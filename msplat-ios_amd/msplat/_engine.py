@@ -61,7 +61,7 @@ EXPORTS = [
     "msplat_hip_download", "msplat_hip_copy", "msplat_hip_commit", "msplat_hip_sync", "msplat_hip_train_step",
     "msplat_hip_render", "msplat_hip_fused_adam", "msplat_hip_densify", "msplat_hip_clamp_max", "msplat_hip_loss_fwd_bwd",
     "msplat_hip_raster_bwd", "msplat_hip_project_bwd", "msplat_hip_project_bwd_adam", "msplat_hip_last", "msplat_hip_enable_timing",
-    "msplat_hip_stage_times", "msplat_hip_last_pairs_evaluated",
+    "msplat_hip_stage_times", "msplat_hip_last_pairs_evaluated", "msplat_hip_last_raster_counts",
 ]
 SYNTH_EXPORTS = ["msplat_synth_uniform", "msplat_synth_normal"]
 
@@ -108,6 +108,7 @@ def lib() -> C.CDLL:
         "msplat_hip_enable_timing": (I, [I]),
         "msplat_hip_stage_times": (I, [C.POINTER(C.c_char_p), c_float_p, I]),
         "msplat_hip_last_pairs_evaluated": (I64, []),
+        "msplat_hip_last_raster_counts": (I, [P]),
         "msplat_synth_uniform": (None, [C.c_uint64, C.c_uint64, I64, C.c_double, C.c_double, P]),
         "msplat_synth_normal": (None, [C.c_uint64, C.c_uint64, I64, C.c_double, C.c_double, P]),
     }
@@ -244,3 +245,10 @@ def stage_times() -> dict[str, float]:
 
 def pairs_evaluated() -> int:
     return int(lib().msplat_hip_last_pairs_evaluated())
+
+
+def raster_counts() -> dict:
+    """Counters of the most recent forward with the pair counter on."""
+    out = (C.c_int64 * 3)()
+    check(lib().msplat_hip_last_raster_counts(C.cast(out, C.c_void_p)))
+    return {"pairs_evaluated": int(out[0]), "log_entries": int(out[1]), "pairs_blended": int(out[2])}
