@@ -255,7 +255,10 @@ enum {
 };
 /* Returns the device pointer and element count of a cached buffer (NULL /
  * 0 if it does not exist yet).  Materialised entries are gathered from the
- * packed records on each call (asynchronously, on the engine stream). */
+ * packed records on each call (asynchronously, on the engine stream).  The
+ * raster gradients (GRADS16, DL_DTRANSMAT, DL_DNORMAL3D, DL_DOPACITY,
+ * DL_DCOLORS) are those of the most recent train step and exist until the
+ * next forward. */
 int msplat_hip_last(int which, void **ptr_dev, int64_t *numel);
 
 /* Per-kernel timings of the most recent train step / render, in ms, from

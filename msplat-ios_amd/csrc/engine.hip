@@ -58,6 +58,8 @@ struct Engine {
     int64_t num_isect = 0;
     const float *bg = nullptr;
     bool have_grads = false;
+    bool raster_grads = false;  // grads16 belongs to the current forward
+    bool g16_moments = false;   // grads16[0..8] hold ray moments, not dL/dtransMat
     bool log_valid = false;   // blend log written for the most recent forward
     bool full_valid = false;  // depth / normal / alpha / median / distortion outputs written
     // timing
@@ -261,6 +263,8 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     E.K3 = (nb - 1) * 3;
     E.bg = bg;
     E.have_grads = false;
+    E.raster_grads = false;
+    E.g16_moments = false;
     E.log_valid = false;
     E.full_valid = false;
     for (int i = 0; i < ST_COUNT; ++i) E.stage_valid[i] = false;
@@ -328,6 +332,16 @@ int last_locked(int which, void **ptr, int64_t *numel) {
         case MSPLAT_LAST_OUT_DISTORTION:
             // produced on demand after an image-only forward
             if (E.rec.p && !E.full_valid) CHECK(raster_fwd_locked(false, true));
+            break;
+        case MSPLAT_LAST_GRADS16: case MSPLAT_LAST_DL_DTRANSMAT: case MSPLAT_LAST_DL_DNORMAL3D:
+        case MSPLAT_LAST_DL_DOPACITY: case MSPLAT_LAST_DL_DCOLORS:
+            if (!E.raster_grads) return MSPLAT_OK;  // none for the current forward
+            // the image-only backward leaves ray moments; turn them into the
+            // reference's dL/dtransMat with this forward's records
+            if (E.g16_moments) {
+                mskern::launch_moments_to_dT(E.stream, E.n, P<float>(E.rec), P<float>(E.grads16));
+                E.g16_moments = false;
+            }
             break;
         default: break;
     }
@@ -434,6 +448,8 @@ void msplat_hip_cleanup(void) {
     E.n = 0;
     E.num_isect = 0;
     E.have_grads = false;
+    E.raster_grads = false;
+    E.g16_moments = false;
     E.log_valid = false;
     E.full_valid = false;
 }
@@ -559,14 +575,15 @@ int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g, con
     HIPC(hipMemsetAsync(E.grads16.p, 0, (size_t)N * 64, s));
     const float inv_np = 1.0f / (float)((unsigned)H * (unsigned)W * 3u);
     const float ddist_uniform = lambda_dist * (inv_np * 3.0f);
-    mskern::launch_raster_bwd(s, W, H, cam->tiles_x, cam->tiles_y, P<int>(E.offsets), P<uint32_t>(E.blend_log),
+    const bool t_moments = mskern::launch_raster_bwd(s, W, H, cam->tiles_x, cam->tiles_y, P<int>(E.offsets), P<uint32_t>(E.blend_log),
                               P<float>(E.t_ckpt), P<int>(E.wave_cnt), P<float>(E.rec), bg, P<float>(E.final_Ts),
                               P<int>(E.final_idx), P<float>(E.dL_dimg), nullptr, nullptr, nullptr, nullptr, nullptr,
                               ddist_uniform, P<float>(E.grads16));
     stage_mark(ST_PROJECT_BWD);
     if (adam) {
         mskern::launch_project_bwd(s, *cam, *g, P<int>(E.radii), P<float>(E.grads16), nullptr, nullptr, nullptr,
-                                   nullptr, nullptr, nullptr, gnorm, vis, max2d, inv_max_dim, adam);
+                                   nullptr, nullptr, nullptr, gnorm, vis, max2d, inv_max_dim, adam,
+                                   t_moments ? P<float>(E.rec) : nullptr);
     } else {
         CHECK(ensure(E.dmeans, (size_t)N * 12));
         CHECK(ensure(E.dscales, (size_t)N * 8));
@@ -576,9 +593,12 @@ int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g, con
         CHECK(ensure(E.dfrest, (size_t)N * E.K3 * 4));
         mskern::launch_project_bwd(s, *cam, *g, P<int>(E.radii), P<float>(E.grads16), P<float>(E.dmeans),
                                    P<float>(E.dscales), P<float>(E.dquats), P<float>(E.dmean2d), P<float>(E.dfdc),
-                                   P<float>(E.dfrest), gnorm, vis, max2d, inv_max_dim, nullptr);
+                                   P<float>(E.dfrest), gnorm, vis, max2d, inv_max_dim, nullptr,
+                                   t_moments ? P<float>(E.rec) : nullptr);
         E.have_grads = true;
     }
+    E.raster_grads = true;
+    E.g16_moments = t_moments;
     stage_mark(ST_COUNT);
     HIPC(hipGetLastError());
     HIPC(hipStreamSynchronize(s));
@@ -714,10 +734,11 @@ int msplat_hip_raster_bwd(const float *dL_dimg, const float *dL_ddepth, const fl
     // outputs; replay the deterministic raster forward with what is missing
     const bool need_full = dL_ddepth || dL_dalpha || dL_dnormal || dL_dmedian || dL_ddist;
     if (!E.log_valid || (need_full && !E.full_valid)) CHECK(raster_fwd_locked(true, need_full || E.full_valid));
-    mskern::launch_raster_bwd(E.stream, E.W, E.H, E.tiles_x, E.tiles_y, P<int>(E.offsets), P<uint32_t>(E.blend_log),
-                              P<float>(E.t_ckpt), P<int>(E.wave_cnt), P<float>(E.rec), E.bg, P<float>(E.final_Ts),
-                              P<int>(E.final_idx), dL_dimg, dL_ddepth, dL_dalpha, dL_dnormal, dL_dmedian, dL_ddist,
-                              0.0f, grads16);
+    const bool t_moments = mskern::launch_raster_bwd(
+        E.stream, E.W, E.H, E.tiles_x, E.tiles_y, P<int>(E.offsets), P<uint32_t>(E.blend_log), P<float>(E.t_ckpt),
+        P<int>(E.wave_cnt), P<float>(E.rec), E.bg, P<float>(E.final_Ts), P<int>(E.final_idx), dL_dimg, dL_ddepth,
+        dL_dalpha, dL_dnormal, dL_dmedian, dL_ddist, 0.0f, grads16);
+    if (t_moments) mskern::launch_moments_to_dT(E.stream, E.n, P<float>(E.rec), grads16);
     HIPC(hipGetLastError());
     return MSPLAT_OK;
     API_END
@@ -735,7 +756,7 @@ int msplat_hip_project_bwd(const MsplatCamera *cam, const MsplatGaussians *g, co
         return MSPLAT_E_ARG;
     }
     mskern::launch_project_bwd(g_eng.stream, *cam, *g, radii, g16, dmeans, dscales, dquats, dmean2d, dfdc, dfrest,
-                               gnorm, vis, max2d, inv_max_dim, nullptr);
+                               gnorm, vis, max2d, inv_max_dim, nullptr, nullptr);
     HIPC(hipGetLastError());
     return MSPLAT_OK;
     API_END
@@ -752,7 +773,7 @@ int msplat_hip_project_bwd_adam(const MsplatCamera *cam, const MsplatGaussians *
         return MSPLAT_E_ARG;
     }
     mskern::launch_project_bwd(g_eng.stream, *cam, *g, radii, g16, nullptr, nullptr, nullptr, nullptr, nullptr,
-                               nullptr, gnorm, vis, max2d, inv_max_dim, adam);
+                               nullptr, gnorm, vis, max2d, inv_max_dim, adam, nullptr);
     HIPC(hipGetLastError());
     return MSPLAT_OK;
     API_END

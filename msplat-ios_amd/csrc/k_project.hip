@@ -170,7 +170,39 @@ struct AdamDev {
     float b1, b2, bc2_sqrt, eps;
 };
 
+// Nine transMat gradients from the ray moments the image-only raster
+// backward accumulates about the splat centre (xs, ys): S0 = sum dp,
+// X = sum (xs - px) dp, Y = sum (ys - py) dp over the pixels (dp = the
+// upstream gradient of the pixel's ray).  With Tu' = Tu - xs Tw and
+// Tv' = Tv - ys Tw, k = px Tw - Tu = (px - xs) Tw - Tu' and l likewise, so
+// the reference's per-pixel terms -l x dp, -dp x k and px (l x dp) +
+// py (dp x k) (msplat_metal.metal:1930-1955) sum to the expressions below;
+// the (px - xs)(py - ys) terms cancel exactly.  Centring keeps every
+// product at the splat's own scale (absolute pixel coordinates would make
+// the cross products cancel catastrophically).
+__device__ __forceinline__ void moments_to_dT(f3 Tu, f3 Tv, f3 Tw, float xs, float ys, float g[9]) {
+    const f3 S0 = {g[0], g[1], g[2]}, X = {g[3], g[4], g[5]}, Y = {g[6], g[7], g[8]};
+    const f3 Tu_ = {Tu.x - xs * Tw.x, Tu.y - xs * Tw.y, Tu.z - xs * Tw.z};
+    const f3 Tv_ = {Tv.x - ys * Tw.x, Tv.y - ys * Tw.y, Tv.z - ys * Tw.z};
+    const f3 a = cross3(Tw, Y), b = cross3(Tv_, S0);
+    const f3 c = cross3(X, Tw), d = cross3(S0, Tu_);
+    const f3 dU = {a.x + b.x, a.y + b.y, a.z + b.z};
+    const f3 dV = {c.x + d.x, c.y + d.y, c.z + d.z};
+    const f3 e = cross3(Tv_, X), f = cross3(Tu_, Y);
+    g[0] = dU.x;
+    g[1] = dU.y;
+    g[2] = dU.z;
+    g[3] = dV.x;
+    g[4] = dV.y;
+    g[5] = dV.z;
+    g[6] = e.x - f.x - xs * dU.x - ys * dV.x;
+    g[7] = e.y - f.y - xs * dU.y - ys * dV.y;
+    g[8] = e.z - f.z - xs * dU.z - ys * dV.z;
+}
+
 // project_and_sh_backward_2dgs_kernel (msplat_metal.metal:2003-2209).
+// t_moments: grads16[0..8] hold the ray moments (see moments_to_dT) instead
+// of dL/dtransMat.
 // FUSED: the per-gaussian gradients stay on chip and the six Adam groups
 // (model.cpp:806-826) are updated in place, so neither the 58-float gradient
 // nor a second pass over the parameters touches HBM.
@@ -187,7 +219,7 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
     float *__restrict__ dmeans, float *__restrict__ dscales, float *__restrict__ dquats,
     float *__restrict__ dmean2d, float *__restrict__ dfdc, float *__restrict__ dfrest,
     float *__restrict__ grad_norm, float *__restrict__ vis, float *__restrict__ max2d, float inv_max_dim,
-    AdamDev ad) {
+    AdamDev ad, const float4 *__restrict__ rec) {
     __shared__ float s_fr[kBlock * 45];
     __shared__ float s_basis[kBlock * 24];
     __shared__ float s_vc[kBlock * 3];
@@ -230,8 +262,17 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
         const float bx = cam.cx - 0.5f, by = cam.cy - 0.5f;
         const float4 *g4 = reinterpret_cast<const float4 *>(g16 + 16 * si);
         const float4 ga = g4[0], gb = g4[1], gc = g4[2], gd = g4[3];
-        const float g[16] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w,
-                             gc.x, gc.y, gc.z, gc.w, gd.x, gd.y, gd.z, gd.w};
+        float g[16] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w,
+                       gc.x, gc.y, gc.z, gc.w, gd.x, gd.y, gd.z, gd.w};
+        if (rec) {
+            // ray moments: the transMat rows as k_project_fwd builds them,
+            // the centre from the splat's record
+            const f3 cu = {halfW * cc.tu[0] + bx * cc.tu[3], halfH * cc.tu[1] + by * cc.tu[3], cc.tu[3]};
+            const f3 cv = {halfW * cc.tv[0] + bx * cc.tv[3], halfH * cc.tv[1] + by * cc.tv[3], cc.tv[3]};
+            const f3 co = {halfW * cc.pc[0] + bx * cc.pc[3], halfH * cc.pc[1] + by * cc.pc[3], cc.pc[3]};
+            const float4 q2 = rec[5 * si + 2];
+            moments_to_dT({cu.x, cv.x, co.x}, {cu.y, cv.y, co.y}, {cu.z, cv.z, co.z}, q2.y, q2.z, g);
+        }
         const f3 dcu = {g[0], g[3], g[6]}, dcv = {g[1], g[4], g[7]}, dco = {g[2], g[5], g[8]};
         const float du[4] = {halfW * dcu.x, halfH * dcu.y, 0.0f, bx * dcu.x + by * dcu.y + dcu.z};
         const float dv[4] = {halfW * dcv.x, halfH * dcv.y, 0.0f, bx * dcv.x + by * dcv.y + dcv.z};
@@ -355,6 +396,21 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
     }
 }
 
+// grads16[0..8]: ray moments -> dL/dtransMat, with the rows of the splat
+// records (the image-only raster backward's output made the reference's).
+__global__ void k_moments_to_dT(int n, const float4 *__restrict__ rec, float *__restrict__ g16) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float4 q0 = rec[5 * (size_t)i], q1 = rec[5 * (size_t)i + 1], q2 = rec[5 * (size_t)i + 2];
+    float *g = g16 + 16 * (size_t)i;
+    float v[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) v[k] = g[k];
+    moments_to_dT({q0.x, q0.y, q0.z}, {q0.w, q1.x, q1.y}, {q1.z, q1.w, q2.x}, q2.y, q2.z, v);
+#pragma unroll
+    for (int k = 0; k < 9; ++k) g[k] = v[k];
+}
+
 __global__ void k_gather(const float *__restrict__ src, int src_stride, int src_off, int nf,
                          float *__restrict__ dst, int n) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -390,8 +446,9 @@ void launch_project_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaus
 void launch_project_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, const int *radii,
                         const float *g16, float *dmeans, float *dscales, float *dquats, float *dmean2d,
                         float *dfdc, float *dfrest, float *grad_norm, float *vis, float *max2d,
-                        float inv_max_dim, const MsplatAdam *adam) {
+                        float inv_max_dim, const MsplatAdam *adam, const float *moments_rec) {
     if (g.num_points <= 0) return;
+    const auto *mrec = reinterpret_cast<const float4 *>(moments_rec);
     AdamDev ad{};
     if (adam) {
         for (int k = 0; k < 6; ++k) {
@@ -406,13 +463,19 @@ void launch_project_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaus
         hipLaunchKernelGGL(k_project_bwd<true>, dim3(blocks_for(g.num_points, kBlock)), dim3(kBlock), 0, s,
                            cam, g.num_points, g.means, g.scales, g.quats, g.opacities, g.features_dc,
                            g.features_rest, radii, g16, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
-                           grad_norm, vis, max2d, inv_max_dim, ad);
+                           grad_norm, vis, max2d, inv_max_dim, ad, mrec);
     } else {
         hipLaunchKernelGGL(k_project_bwd<false>, dim3(blocks_for(g.num_points, kBlock)), dim3(kBlock), 0, s,
                            cam, g.num_points, g.means, g.scales, g.quats, g.opacities, g.features_dc,
                            g.features_rest, radii, g16, dmeans, dscales, dquats, dmean2d, dfdc, dfrest,
-                           grad_norm, vis, max2d, inv_max_dim, ad);
+                           grad_norm, vis, max2d, inv_max_dim, ad, mrec);
     }
+}
+
+void launch_moments_to_dT(hipStream_t s, int n, const float *rec, float *g16) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_moments_to_dT, dim3(blocks_for(n, 256)), dim3(256), 0, s, n,
+                       reinterpret_cast<const float4 *>(rec), g16);
 }
 
 void launch_gather(hipStream_t s, const float *src, int src_stride, int src_off, int nf, float *dst, int n) {

@@ -344,10 +344,10 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     const float bgT = -T_final * (bgp[0] * dp0 + bgp[1] * dp1 + bgp[2] * dp2);
     // lane l of the reduction ends with component vi (see wave_reduce16)
     const int vi = ((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 + ((lane >> 2) & 1);
-    // post-reduction factor in the image-only case: opa for the T rows (the
-    // sign of the last column folded in), opa (1 - opa) for the opacity
-    // logit, 1 for the colours, 0 for the normals
-    const float fa = vi < 6 ? 1.f : vi < 9 ? -1.f : vi == 12 ? 1.f : 0.f;
+    // post-reduction factor in the image-only case: -opa for the nine ray
+    // moments, opa (1 - opa) for the opacity logit, 1 for the colours, 0 for
+    // the normals
+    const float fa = vi < 9 ? -1.f : vi == 12 ? 1.f : 0.f;
     const float fb = vi == 12 ? -1.f : 0.f;
     const float fc = vi >= 13 ? 1.f : 0.f;
     const int ch = vi - 13;
@@ -369,8 +369,30 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
         if (lane < m) {
             const uint4 e = lg[c0 + lane];
             const float4 *r = rec + 5 * (size_t)e.w;
+            if (FULL) {
 #pragma unroll
-            for (int k = 0; k < 5; ++k) s_r[wave][k][lane] = r[k];
+                for (int k = 0; k < 5; ++k) s_r[wave][k][lane] = r[k];
+            } else {
+                // The ray of pixel p, k x l with k = px Tw - Tu and
+                // l = py Tw - Tv, expanded about the splat centre (xs, ys):
+                //   ray = R0 + (px - xs) Ax + (py - ys) Ay,
+                // R0 = kc x lc, Ax = Tw x lc, Ay = kc x Tw (kc = xs Tw - Tu,
+                // lc = ys Tw - Tv); the (px - xs)(py - ys) term is Tw x Tw = 0.
+                // Every term stays at the splat's scale (an expansion about
+                // the image origin would cancel large terms).
+                const float4 q0 = r[0], q1 = r[1], q2 = r[2], q3 = r[3], q4 = r[4];
+                const f3 Tu = {q0.x, q0.y, q0.z}, Tv = {q0.w, q1.x, q1.y}, Tw = {q1.z, q1.w, q2.x};
+                const float xs = q2.y, ys = q2.z;
+                const f3 kc = {__builtin_fmaf(xs, Tw.x, -Tu.x), __builtin_fmaf(xs, Tw.y, -Tu.y),
+                               __builtin_fmaf(xs, Tw.z, -Tu.z)};
+                const f3 lc = {__builtin_fmaf(ys, Tw.x, -Tv.x), __builtin_fmaf(ys, Tw.y, -Tv.y),
+                               __builtin_fmaf(ys, Tw.z, -Tv.z)};
+                const f3 R0 = cross3(kc, lc), Ax = cross3(Tw, lc), Ay = cross3(kc, Tw);
+                s_r[wave][0][lane] = make_float4(R0.x, R0.y, R0.z, Ax.x);
+                s_r[wave][1][lane] = make_float4(Ax.y, Ax.z, Ay.x, Ay.y);
+                s_r[wave][2][lane] = make_float4(Ay.z, xs, ys, q2.w);
+                s_r[wave][3][lane] = make_float4(q3.w, q4.x, q4.y, 0.f);
+            }
             s_e[wave][lane] = e;
         }
         wave_lds_sync();
@@ -378,52 +400,51 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
             const uint4 e = s_e[wave][j];
             const unsigned bal = lane < 32 ? e.x : e.y;
             const bool has = (bal >> (lane & 31)) & 1u;
-            const float4 q0 = s_r[wave][0][j], q1 = s_r[wave][1][j], q2 = s_r[wave][2][j];
-            const float4 q3 = s_r[wave][3][j], q4 = s_r[wave][4][j];
-            const float Tux = q0.x, Tuy = q0.y, Tuz = q0.z, Tvx = q0.w, Tvy = q1.x, Tvz = q1.y;
-            const float Twx = q1.z, Twy = q1.w, Twz = q2.x, opa = q2.w;
-            const f3 k = {__builtin_fmaf(px, Twx, -Tux), __builtin_fmaf(px, Twy, -Tuy),
-                          __builtin_fmaf(px, Twz, -Tuz)};
-            const f3 l = {__builtin_fmaf(py, Twx, -Tvx), __builtin_fmaf(py, Twy, -Tvy),
-                          __builtin_fmaf(py, Twz, -Tvz)};
-            // the forward's ray.z, bit for bit (non-zero wherever the lane blended)
-            const float rz = __builtin_fmaf(k.x, l.y, -(k.y * l.x));
-            const float inv_z = has ? __builtin_amdgcn_rcpf(rz) : 0.f;
-            const float u = __builtin_fmaf(k.y, l.z, -(k.z * l.y)) * inv_z;
-            const float v = __builtin_fmaf(k.z, l.x, -(k.x * l.z)) * inv_z;
-            const float rho3d = __builtin_fmaf(u, u, v * v);
-            const float dxs = q2.y - px, dys = q2.z - py;
-            const float rho2d = FILTER_INV_SQ * __builtin_fmaf(dxs, dxs, dys * dys);
-            const bool use3d = rho3d <= rho2d;
-            const float G = __builtin_amdgcn_exp2f(__builtin_fminf(rho3d, rho2d) * -0.72134752044448170368f);
-            const float alpha = has ? __builtin_fminf(0.99f, opa * G) : 0.f;
-            const float inv_om = __builtin_amdgcn_rcpf(1.0f - alpha);
-            Tr *= inv_om;  // transmittance before this splat (unchanged where it did not blend)
-            const float aT = alpha * Tr;
             float v16[16];
+            float opa;
             if (!FULL) {
-                const float vv = dp0 * q3.w + dp1 * q4.x + dp2 * q4.y;  // dL/dimage . colour
+                const float4 q0 = s_r[wave][0][j], q1 = s_r[wave][1][j], q2 = s_r[wave][2][j];
+                const float4 q3 = s_r[wave][3][j];
+                opa = q2.w;
+                const float dxs = q2.y - px, dys = q2.z - py;
+                const float rx = q0.x - __builtin_fmaf(dxs, q0.w, dys * q1.z);
+                const float ry = q0.y - __builtin_fmaf(dxs, q1.x, dys * q1.w);
+                const float rz = q0.z - __builtin_fmaf(dxs, q1.y, dys * q2.x);
+                const float inv_z = has ? __builtin_amdgcn_rcpf(rz) : 0.f;
+                const float u = rx * inv_z, v = ry * inv_z;
+                const float rho3d = __builtin_fmaf(u, u, v * v);
+                const float rho2d = FILTER_INV_SQ * __builtin_fmaf(dxs, dxs, dys * dys);
+                const bool use3d = rho3d <= rho2d;
+                const float G = __builtin_amdgcn_exp2f(__builtin_fminf(rho3d, rho2d) * -0.72134752044448170368f);
+                const float alpha = has ? __builtin_fminf(0.99f, opa * G) : 0.f;
+                const float inv_om = __builtin_amdgcn_rcpf(1.0f - alpha);
+                Tr *= inv_om;  // transmittance before this splat (unchanged where it did not blend)
+                const float aT = alpha * Tr;
+                const float vv = dp0 * q3.x + dp1 * q3.y + dp2 * q3.z;  // dL/dimage . colour
                 const float acc_new = __builtin_fmaf(last_alpha, last_v - acc_v, acc_v);
                 acc_v = has ? acc_new : acc_v;
                 last_v = has ? vv : last_v;
                 last_alpha = has ? alpha : last_alpha;
                 const float dLda = __builtin_fmaf(vv - acc_v, Tr, bgT * inv_om);
                 const float gg = has ? dLda * G : 0.f;
-                const float gT = use3d ? gg : 0.f;
-                // dL/d(ray-splat point) up to the factor -opa: (gT u, gT v) / ray.z
-                const float dsx = gT * u * inv_z, dsy = gT * v * inv_z;
-                const float dpz = -__builtin_fmaf(dsx, u, dsy * v);
-                const f3 dk = {l.y * dpz - l.z * dsy, l.z * dsx - l.x * dpz, l.x * dsy - l.y * dsx};
-                const f3 dl = {dsy * k.z - dpz * k.y, dpz * k.x - dsx * k.z, dsx * k.y - dsy * k.x};
-                v16[0] = dk.x;
-                v16[1] = dk.y;
-                v16[2] = dk.z;
-                v16[3] = dl.x;
-                v16[4] = dl.y;
-                v16[5] = dl.z;
-                v16[6] = __builtin_fmaf(px, dk.x, py * dl.x);
-                v16[7] = __builtin_fmaf(px, dk.y, py * dl.y);
-                v16[8] = __builtin_fmaf(px, dk.z, py * dl.z);
+                // dL/d(ray), up to the factor -opa, on the 3D branch: the
+                // ray-splat point (gg u, gg v) / ray.z pulled back through
+                // (u, v) = ray.xy / ray.z; its moments over the wave's pixels
+                // about the splat centre (sum dp, sum (xs - px) dp,
+                // sum (ys - py) dp) determine the nine transMat gradients
+                const float t = gg * inv_z;
+                const float dsx = use3d ? t * u : 0.f;
+                const float dsy = use3d ? t * v : 0.f;
+                const float dpz = use3d ? -__builtin_fmaf(dsx, u, dsy * v) : 0.f;
+                v16[0] = dsx;
+                v16[1] = dsy;
+                v16[2] = dpz;
+                v16[3] = dxs * dsx;
+                v16[4] = dxs * dsy;
+                v16[5] = dxs * dpz;
+                v16[6] = dys * dsx;
+                v16[7] = dys * dsy;
+                v16[8] = dys * dpz;
                 v16[9] = 0.f;
                 v16[10] = 0.f;
                 v16[11] = 0.f;
@@ -432,6 +453,29 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 v16[14] = aT * dp1;
                 v16[15] = aT * dp2;
             } else {
+                const float4 q0 = s_r[wave][0][j], q1 = s_r[wave][1][j], q2 = s_r[wave][2][j];
+                const float4 q3 = s_r[wave][3][j], q4 = s_r[wave][4][j];
+                const float Tux = q0.x, Tuy = q0.y, Tuz = q0.z, Tvx = q0.w, Tvy = q1.x, Tvz = q1.y;
+                const float Twx = q1.z, Twy = q1.w, Twz = q2.x;
+                opa = q2.w;
+                const f3 k = {__builtin_fmaf(px, Twx, -Tux), __builtin_fmaf(px, Twy, -Tuy),
+                              __builtin_fmaf(px, Twz, -Tuz)};
+                const f3 l = {__builtin_fmaf(py, Twx, -Tvx), __builtin_fmaf(py, Twy, -Tvy),
+                              __builtin_fmaf(py, Twz, -Tvz)};
+                // the forward's ray.z, bit for bit (non-zero wherever the lane blended)
+                const float rz = __builtin_fmaf(k.x, l.y, -(k.y * l.x));
+                const float inv_z = has ? __builtin_amdgcn_rcpf(rz) : 0.f;
+                const float u = __builtin_fmaf(k.y, l.z, -(k.z * l.y)) * inv_z;
+                const float v = __builtin_fmaf(k.z, l.x, -(k.x * l.z)) * inv_z;
+                const float rho3d = __builtin_fmaf(u, u, v * v);
+                const float dxs = q2.y - px, dys = q2.z - py;
+                const float rho2d = FILTER_INV_SQ * __builtin_fmaf(dxs, dxs, dys * dys);
+                const bool use3d = rho3d <= rho2d;
+                const float G = __builtin_amdgcn_exp2f(__builtin_fminf(rho3d, rho2d) * -0.72134752044448170368f);
+                const float alpha = has ? __builtin_fminf(0.99f, opa * G) : 0.f;
+                const float inv_om = __builtin_amdgcn_rcpf(1.0f - alpha);
+                Tr *= inv_om;  // transmittance before this splat (unchanged where it did not blend)
+                const float aT = alpha * Tr;
                 // lanes that did not blend get a finite stand-in (their terms are zeroed)
                 const float depth = has ? __builtin_fmaf(u, Twx, __builtin_fmaf(v, Twy, Twz)) : 1.0f;
                 const float cu[3] = {q3.w, q4.x, q4.y}, nrm[3] = {q3.x, q3.y, q3.z};
@@ -474,13 +518,11 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 last_alpha = has ? alpha : last_alpha;
                 dL_dz = has ? dL_dz : 0.f;
                 const float dL_dG = has ? opa * dL_dalpha : 0.f;
-                float dsx = 0.f, dsy = 0.f;
-                if (use3d) {
-                    dsx = -dL_dG * G * u + dL_dz * Twx;
-                    dsy = -dL_dG * G * v + dL_dz * Twy;
-                }
-                const float dsx_pz = dsx * inv_z, dsy_pz = dsy * inv_z;
-                const float dpz = -(dsx_pz * u + dsy_pz * v);
+                // the T rows get gradient only on the 3D branch (selects, not
+                // products with zero: u and 1 / ray.z may be huge there)
+                const float dsx_pz = use3d ? (-dL_dG * G * u + dL_dz * Twx) * inv_z : 0.f;
+                const float dsy_pz = use3d ? (-dL_dG * G * v + dL_dz * Twy) * inv_z : 0.f;
+                const float dpz = use3d ? -(dsx_pz * u + dsy_pz * v) : 0.f;
                 const f3 dk = {l.y * dpz - l.z * dsy_pz, l.z * dsx_pz - l.x * dpz, l.x * dsy_pz - l.y * dsx_pz};
                 const f3 dl = {dsy_pz * k.z - dpz * k.y, dpz * k.x - dsx_pz * k.z, dsx_pz * k.y - dsy_pz * k.x};
                 v16[0] = -dk.x;
@@ -496,7 +538,8 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
             }
             float s = wave_reduce16(v16, lane);
             if (!FULL) {
-                const float cc = ch == 0 ? q3.w : ch == 1 ? q4.x : q4.y;
+                const float4 q3 = s_r[wave][3][j];
+                const float cc = ch == 0 ? q3.x : ch == 1 ? q3.y : q3.z;
                 const float f = __builtin_fmaf(opa, __builtin_fmaf(fb, opa, fa), fc);
                 s = (fc != 0.f && !(cc > 0.f)) ? 0.f : s * f;
             }
@@ -529,7 +572,7 @@ void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
         full_outputs ? launch(k_raster_fwd<false, true>) : launch(k_raster_fwd<false, false>);
 }
 
-void launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets,
+bool launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets,
                        const uint32_t *blend_log, const float *t_ckpt, const int *wave_cnt, const float *rec,
                        const float *bg, const float *final_Ts, const int *final_idx, const float *dL_dimg,
                        const float *dL_ddepth, const float *dL_daccum, const float *dL_dnormal,
@@ -546,6 +589,7 @@ void launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
         hipLaunchKernelGGL(k_raster_bwd<false>, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, lg,
                            t_ckpt, wave_cnt, reinterpret_cast<const float4 *>(rec), bg, final_Ts, final_idx, dL_dimg,
                            dL_ddepth, dL_daccum, dL_dnormal, dL_dmedian, dL_ddist, ddist_uniform, grads16);
+    return !full;
 }
 
 }  // namespace mskern

@@ -309,10 +309,16 @@ def test_train_step_matches_oracle(orc, eng):
     _assert_bitexact(E.last("out_img", img_o.shape), img_o, "rendered image")
     # the outputs the image-only training forward skips are produced on
     # demand, bit-identical to a full forward of the same (pre-step) splats
-    _, _, _, full_o = orc.render(scene, 0)
+    _, proj_o, bins_o, full_o = orc.render(scene, 0)
     for k in ("final_Ts", "final_idx", "out_depth", "out_normal", "out_alpha", "out_median_depth",
               "out_distortion"):
         _assert_bitexact(E.last(k, full_o[k].shape), full_o[k], k)
+    # the step's cached raster gradients (ray moments inside the step,
+    # dL/dtransMat through the accessor) against the golden model's raster
+    # backward of the same forward and loss gradient
+    _, dL_o, _, _ = orc.loss_fwd_bwd(full_o["out_img"], gt)
+    g_o = orc.raster_bwd(proj_o, bins_o, full_o, ocam, scene.background, dL_o)
+    _grad_close(E.last("grads16", (scene.n, 16)), g_o, "train step grads16")
     got = ds.host_params()
     names = list(got)
     for k, p_o, p0, lr in zip(names, params, scene.params(), D.LR_INIT):
