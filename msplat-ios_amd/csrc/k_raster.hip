@@ -123,43 +123,39 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
         for (int j = 0; j < n; ++j) {
             const int t = s_list[wave][j];
             const float T_before = Tr;
-            bool blend = false;
-            if (!done) {
-                ++evals;
-                const float4 q0 = s_rec[t], q1 = s_rec[kThreads + t], q2 = s_rec[2 * kThreads + t];
-                PairEval e;
-                if (eval_pair(px, py, q0, q1, q2, e)) {
-                    const float next_T = Tr * (1.0f - e.alpha);
-                    if (next_T <= 1e-4f) {
-                        done = true;
-                    } else {
-                        blend = true;
-                        ++blends;
-                        const float w = e.alpha * Tr;
-                        const float4 q3 = s_rec[3 * kThreads + t], q4 = s_rec[4 * kThreads + t];
-                        if (FULL_OUT) {
-                            const float A = 1.f - Tr;
-                            const float m_ = kMScale * (1.f - NEAR_N / e.depth);
-                            dist = __builtin_fmaf(m_ * m_ * A + M2 - 2.f * m_ * M1, w, dist);
-                            M1 = __builtin_fmaf(m_, w, M1);
-                            M2 = __builtin_fmaf(m_ * m_, w, M2);
-                            if (Tr > 0.5f) {
-                                med = e.depth;
-                                med_c = base + t;
-                            }
-                            dep = __builtin_fmaf(e.depth, w, dep);
-                            nx = __builtin_fmaf(q3.x, w, nx);
-                            ny = __builtin_fmaf(q3.y, w, ny);
-                            nz = __builtin_fmaf(q3.z, w, nz);
-                        }
-                        cr = __builtin_fmaf(q3.w, w, cr);
-                        cg = __builtin_fmaf(q4.x, w, cg);
-                        cb = __builtin_fmaf(q4.y, w, cb);
-                        Tr = next_T;
-                        last_c = base + t;
-                    }
-                }
+            // predicated: a lane that is done or rejects the pair adds
+            // colour * 0 (bit-identical sums) and keeps its state
+            evals += done ? 0 : 1;
+            const float4 q0 = s_rec[t], q1 = s_rec[kThreads + t], q2 = s_rec[2 * kThreads + t];
+            PairEval e;
+            const bool act = eval_pair(px, py, q0, q1, q2, e) & !done;
+            const float next_T = Tr * (1.0f - e.alpha);
+            const bool term = act & (next_T <= 1e-4f);
+            const bool blend = act & !term;
+            done = done | term;
+            blends += blend ? 1 : 0;
+            const float w = blend ? e.alpha * Tr : 0.0f;
+            const float4 q3 = s_rec[3 * kThreads + t], q4 = s_rec[4 * kThreads + t];
+            if (FULL_OUT) {
+                const float A = 1.f - Tr;
+                const float dep_s = blend ? e.depth : 1.0f;  // finite stand-in off the blend
+                const float m_ = kMScale * (1.f - NEAR_N / dep_s);
+                dist = __builtin_fmaf(m_ * m_ * A + M2 - 2.f * m_ * M1, w, dist);
+                M1 = __builtin_fmaf(m_, w, M1);
+                M2 = __builtin_fmaf(m_ * m_, w, M2);
+                const bool med_now = blend & (Tr > 0.5f);
+                med = med_now ? e.depth : med;
+                med_c = med_now ? base + t : med_c;
+                dep = __builtin_fmaf(dep_s, w, dep);
+                nx = __builtin_fmaf(q3.x, w, nx);
+                ny = __builtin_fmaf(q3.y, w, ny);
+                nz = __builtin_fmaf(q3.z, w, nz);
             }
+            cr = __builtin_fmaf(q3.w, w, cr);
+            cg = __builtin_fmaf(q4.x, w, cg);
+            cb = __builtin_fmaf(q4.y, w, cb);
+            Tr = blend ? next_T : Tr;
+            last_c = blend ? base + t : last_c;
             if (LOG) {
                 const unsigned long long bal = __ballot(blend);
                 if (bal) {
@@ -224,9 +220,13 @@ __device__ __forceinline__ float dpp(float x) {
 // DPP steps (partners differ in lane bit 3, then bit 2) and two quad_perm
 // DPP adds finish.  Lane l ends with the total of value index
 // 8*b5 + 4*b4 + 2*b3 + b2 (b = bits of l); every lane of a quad holds it.
+// ZERO3: v[3] and v[11] are zero in every lane, so their first-stage pair
+// is skipped (it would sum to zero).
+template <bool ZERO3 = false>
 __device__ __forceinline__ float wave_reduce16(float v[16], int lane) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
+        if (ZERO3 && i == 3) continue;
         // vdst lanes 32-63 <-> src lanes 0-31: lanes < 32 end with value i,
         // lanes >= 32 with value i + 8
         const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 8]), false,
@@ -302,7 +302,8 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     const int tile = xcd_tile(blockIdx.x, T);
     if (tile >= T) return;
     constexpr int kWave = 64;
-    __shared__ float4 s_r[4][5][kWave];
+    // record planes per staged entry: the image-only path stages 4, the full one 5
+    __shared__ float4 s_r[4][FULL ? 5 : 4][kWave];
     __shared__ uint4 s_e[4][kWave];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int tx = tile % tiles_x, ty = tile / tiles_x;
@@ -342,15 +343,17 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     }
     const float fA = 1.0f - T_final;
     const float bgT = -T_final * (bgp[0] * dp0 + bgp[1] * dp1 + bgp[2] * dp2);
-    // lane l of the reduction ends with component vi (see wave_reduce16)
+    // lane l of the reduction ends with slot vi (see wave_reduce16), which
+    // holds grads16 index gi (the image-only layout exchanges 3 / 9, 10 / 11)
     const int vi = ((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 + ((lane >> 2) & 1);
+    const int gi = FULL ? vi : vi == 3 ? 9 : vi == 9 ? 3 : vi == 10 ? 11 : vi == 11 ? 10 : vi;
     // post-reduction factor in the image-only case: -opa for the nine ray
     // moments, opa (1 - opa) for the opacity logit, 1 for the colours, 0 for
     // the normals
-    const float fa = vi < 9 ? -1.f : vi == 12 ? 1.f : 0.f;
-    const float fb = vi == 12 ? -1.f : 0.f;
-    const float fc = vi >= 13 ? 1.f : 0.f;
-    const int ch = vi - 13;
+    const float fa = gi < 9 ? -1.f : gi == 12 ? 1.f : 0.f;
+    const float fb = gi == 12 ? -1.f : 0.f;
+    const float fc = gi >= 13 ? 1.f : 0.f;
+    const int ch = gi - 13;
 
     // suffix state of the reference's recurrences (image-only: the colour
     // suffix projected on dL/dimage)
@@ -387,10 +390,11 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                                __builtin_fmaf(xs, Tw.z, -Tu.z)};
                 const f3 lc = {__builtin_fmaf(ys, Tw.x, -Tv.x), __builtin_fmaf(ys, Tw.y, -Tv.y),
                                __builtin_fmaf(ys, Tw.z, -Tv.z)};
-                const f3 R0 = cross3(kc, lc), Ax = cross3(Tw, lc), Ay = cross3(kc, Tw);
-                s_r[wave][0][lane] = make_float4(R0.x, R0.y, R0.z, Ax.x);
-                s_r[wave][1][lane] = make_float4(Ax.y, Ax.z, Ay.x, Ay.y);
-                s_r[wave][2][lane] = make_float4(Ay.z, xs, ys, q2.w);
+                // stored: R0, -Ax, -Ay (the pixel loop uses xs - px, ys - py)
+                const f3 R0 = cross3(kc, lc), nAx = cross3(lc, Tw), nAy = cross3(Tw, kc);
+                s_r[wave][0][lane] = make_float4(R0.x, R0.y, R0.z, nAx.x);
+                s_r[wave][1][lane] = make_float4(nAx.y, nAx.z, nAy.x, nAy.y);
+                s_r[wave][2][lane] = make_float4(nAy.z, xs, ys, q2.w);
                 s_r[wave][3][lane] = make_float4(q3.w, q4.x, q4.y, 0.f);
             }
             s_e[wave][lane] = e;
@@ -407,9 +411,9 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 const float4 q3 = s_r[wave][3][j];
                 opa = q2.w;
                 const float dxs = q2.y - px, dys = q2.z - py;
-                const float rx = q0.x - __builtin_fmaf(dxs, q0.w, dys * q1.z);
-                const float ry = q0.y - __builtin_fmaf(dxs, q1.x, dys * q1.w);
-                const float rz = q0.z - __builtin_fmaf(dxs, q1.y, dys * q2.x);
+                const float rx = __builtin_fmaf(dxs, q0.w, __builtin_fmaf(dys, q1.z, q0.x));
+                const float ry = __builtin_fmaf(dxs, q1.x, __builtin_fmaf(dys, q1.w, q0.y));
+                const float rz = __builtin_fmaf(dxs, q1.y, __builtin_fmaf(dys, q2.x, q0.z));
                 const float inv_z = has ? __builtin_amdgcn_rcpf(rz) : 0.f;
                 const float u = rx * inv_z, v = ry * inv_z;
                 const float rho3d = __builtin_fmaf(u, u, v * v);
@@ -420,7 +424,7 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 const float inv_om = __builtin_amdgcn_rcpf(1.0f - alpha);
                 Tr *= inv_om;  // transmittance before this splat (unchanged where it did not blend)
                 const float aT = alpha * Tr;
-                const float vv = dp0 * q3.x + dp1 * q3.y + dp2 * q3.z;  // dL/dimage . colour
+                const float vv = __builtin_fmaf(dp0, q3.x, __builtin_fmaf(dp1, q3.y, dp2 * q3.z));  // dL/dimage . colour
                 const float acc_new = __builtin_fmaf(last_alpha, last_v - acc_v, acc_v);
                 acc_v = has ? acc_new : acc_v;
                 last_v = has ? vv : last_v;
@@ -436,16 +440,19 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 const float dsx = use3d ? t * u : 0.f;
                 const float dsy = use3d ? t * v : 0.f;
                 const float dpz = use3d ? -__builtin_fmaf(dsx, u, dsy * v) : 0.f;
+                // reduction slots: grads16 index k in slot k, except that
+                // slots 3 / 9 and 10 / 11 are exchanged (kSlotImg), which puts
+                // two of the three zero normals in one first-stage pair
                 v16[0] = dsx;
                 v16[1] = dsy;
                 v16[2] = dpz;
-                v16[3] = dxs * dsx;
+                v16[9] = dxs * dsx;
                 v16[4] = dxs * dsy;
                 v16[5] = dxs * dpz;
                 v16[6] = dys * dsx;
                 v16[7] = dys * dsy;
                 v16[8] = dys * dpz;
-                v16[9] = 0.f;
+                v16[3] = 0.f;
                 v16[10] = 0.f;
                 v16[11] = 0.f;
                 v16[12] = gg;
@@ -536,14 +543,14 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 v16[8] = px * dk.z + py * dl.z + dL_dz;
                 v16[12] = G * dL_dG * (1.0f - opa);
             }
-            float s = wave_reduce16(v16, lane);
+            float s = FULL ? wave_reduce16(v16, lane) : wave_reduce16<true>(v16, lane);
             if (!FULL) {
                 const float4 q3 = s_r[wave][3][j];
                 const float cc = ch == 0 ? q3.x : ch == 1 ? q3.y : q3.z;
                 const float f = __builtin_fmaf(opa, __builtin_fmaf(fb, opa, fa), fc);
                 s = (fc != 0.f && !(cc > 0.f)) ? 0.f : s * f;
             }
-            if ((lane & 3) == 0 && s != 0.f) unsafeAtomicAdd(&grads16[(size_t)e.w * 16 + vi], s);
+            if ((lane & 3) == 0 && s != 0.f) unsafeAtomicAdd(&grads16[(size_t)e.w * 16 + gi], s);
         }
         wave_lds_sync();
     }

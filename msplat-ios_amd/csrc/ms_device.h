@@ -79,26 +79,30 @@ __device__ __forceinline__ float ms_expf(float x) {
 
 __device__ __forceinline__ float ms_sigmoid(float x) { return 1.0f / (1.0f + ms_expf(-x)); }
 
-// ms_expf for x <= 0 (or NaN), bit-identical to it wherever the result is at
-// least 2^-126 (x >= -87; for x in [-87, 0] the one-step scaling p * 2^k is
-// the same single rounding as the two-step one).  Below -87 it returns about
-// 1e-38 instead of the exact tiny value; the rasterizer only compares
-// opacity * G against 1/255 there, so every decision and output is unchanged.
-__device__ __forceinline__ float ms_expf_nonpos(float x) {
-    x = (x < -87.0f) ? -87.0f : x;  // NaN passes through
-    const float z = __builtin_rintf(x * 1.44269504088896341f);
-    float r = __builtin_fmaf(z, -0.693359375f, x);
-    r = __builtin_fmaf(z, 2.12194440e-4f, r);
-    const float r2 = r * r;
-    float p = 1.9875691500E-4f;
-    p = __builtin_fmaf(p, r, 1.3981999507E-3f);
-    p = __builtin_fmaf(p, r, 8.3334519073E-3f);
-    p = __builtin_fmaf(p, r, 4.1665795894E-2f);
-    p = __builtin_fmaf(p, r, 1.6666665459E-1f);
-    p = __builtin_fmaf(p, r, 5.0000001201E-1f);
-    p = __builtin_fmaf(p, r2, r);
-    p = p + 1.0f;
-    return p * __int_as_float(((int)z + 127) << 23);
+// exp(x) for x <= 0 in the rasterizer's alpha (the Gaussian falloff
+// exp(-rho / 2)), shared bit for bit with the golden model's
+// orc_exp_gauss: x is clamped to [-86, 0] (NaN becomes -86), then
+// t = x log2(e) is formed as t_hi + t_lo, z = rint(t_hi),
+// f = (t_hi - z) + t_lo, and 2^f on [-1/2, 1/2] is the degree-6 Taylor
+// polynomial of e^(f ln 2) (truncation error below 1.2e-7 relative) scaled
+// by ldexp(., z).  A few ulp from exp, and a normal number everywhere
+// (>= 3e-38), which is all the 1/255 alpha threshold needs far out.
+__host__ __device__ __forceinline__ float ms_exp_gauss(float x) {
+    x = __builtin_fmaxf(x, -86.0f);
+    // t = x log2(e) carried as t_hi + t_lo: the product's rounding error
+    // (fma) and the error of log2(e) as a float (1.925963e-8)
+    const float t = x * 1.44269502162933349609375f;
+    const float t_lo = __builtin_fmaf(x, 1.925963033500011079e-8f, __builtin_fmaf(x, 1.44269502162933349609375f, -t));
+    const float z = __builtin_rintf(t);
+    const float f = (t - z) + t_lo;
+    float p = 1.5403530393381606e-4f;
+    p = __builtin_fmaf(p, f, 1.3333558146428443e-3f);
+    p = __builtin_fmaf(p, f, 9.6181291076284772e-3f);
+    p = __builtin_fmaf(p, f, 5.5504108664821580e-2f);
+    p = __builtin_fmaf(p, f, 2.4022650695910071e-1f);
+    p = __builtin_fmaf(p, f, 6.9314718055994531e-1f);
+    p = __builtin_fmaf(p, f, 1.0f);
+    return __builtin_ldexpf(p, (int)z);
 }
 
 // Saturating truncation (the tile-rectangle (int) casts of get_bbox,
@@ -347,6 +351,10 @@ struct PairEval {
 
 __device__ __forceinline__ bool eval_pair(float px, float py, const float4 &q0, const float4 &q1,
                                           const float4 &q2, PairEval &e) {
+    // Straight-line: every value is computed, then one predicate applies the
+    // reference's four rejections with their exact comparisons (a NaN
+    // compares false in each, as in the reference's early returns), so the
+    // wave needs no exec-mask branches per rejection.
     const float Tux = q0.x, Tuy = q0.y, Tuz = q0.z;
     const float Tvx = q0.w, Tvy = q1.x, Tvz = q1.y;
     const float Twx = q1.z, Twy = q1.w, Twz = q2.x;
@@ -354,8 +362,7 @@ __device__ __forceinline__ bool eval_pair(float px, float py, const float4 &q0, 
     e.l = {__builtin_fmaf(py, Twx, -Tvx), __builtin_fmaf(py, Twy, -Tvy), __builtin_fmaf(py, Twz, -Tvz)};
     e.ray = {__builtin_fmaf(e.k.y, e.l.z, -(e.k.z * e.l.y)), __builtin_fmaf(e.k.z, e.l.x, -(e.k.x * e.l.z)),
              __builtin_fmaf(e.k.x, e.l.y, -(e.k.y * e.l.x))};
-    if (e.ray.z == 0.0f) return false;
-    e.inv_z = 1.0f / e.ray.z;
+    e.inv_z = 1.0f / e.ray.z;  // infinite when ray.z == 0; that pair is rejected below
     e.u = e.ray.x * e.inv_z;
     e.v = e.ray.y * e.inv_z;
     e.rho3d = __builtin_fmaf(e.u, e.u, e.v * e.v);
@@ -363,13 +370,10 @@ __device__ __forceinline__ bool eval_pair(float px, float py, const float4 &q0, 
     e.rho2d = FILTER_INV_SQ * __builtin_fmaf(dxs, dxs, dys * dys);
     const float rho = __builtin_fminf(e.rho3d, e.rho2d);
     e.depth = __builtin_fmaf(e.u, Twx, __builtin_fmaf(e.v, Twy, Twz));
-    if (e.depth < NEAR_N) return false;
     const float power = -0.5f * rho;
-    if (power > 0.0f) return false;
-    e.G = ms_expf_nonpos(power);
+    e.G = ms_exp_gauss(power);
     e.alpha = __builtin_fminf(0.99f, q2.w * e.G);
-    if (e.alpha < 1.0f / 255.0f) return false;
-    return true;
+    return !(e.ray.z == 0.0f) & !(e.depth < NEAR_N) & !(power > 0.0f) & !(e.alpha < 1.0f / 255.0f);
 }
 
 // Pixels of a 16x16 tile handled by wave w of a 256-thread rasterizer

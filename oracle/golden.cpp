@@ -302,7 +302,7 @@ inline bool eval_pair(float px, float py, const float *Tm, const float *xy,
     if (e.depth < NEAR_N) return false;
     const float power = -0.5f * rho;
     if (power > 0.0f) return false;
-    e.G = orc_expf(power);
+    e.G = orc_exp_gauss(power);
     e.alpha = fminf(0.99f, opac * e.G);
     if (e.alpha < 1.0f / 255.0f) return false;
     return true;
@@ -397,6 +397,35 @@ extern "C" float orc_expf(float x) {
     memcpy(&s1, &b1, 4);
     memcpy(&s2, &b2, 4);
     return (p * s1) * s2;
+}
+
+/* The rasterizer's Gaussian falloff exp(x), x <= 0: clamp to [-86, 0] (NaN
+ * becomes -86), t = x log2(e) as t_hi + t_lo (the product's rounding error by
+ * fma, plus the error of log2(e) as a float), z = rint(t_hi),
+ * f = (t_hi - z) + t_lo, 2^f as the degree-6 Taylor polynomial of
+ * e^(f ln 2) on [-1/2, 1/2] (truncation error below 1.2e-7 relative), then
+ * ldexp(., z).  The same IEEE operations as the kernels' ms_exp_gauss, so both
+ * agree bit for bit; a few ulp from exp, never below 3e-38. */
+extern "C" float orc_exp_gauss(float x) {
+    x = fmaxf(x, -86.0f);
+    // t = x log2(e) carried as t_hi + t_lo: the product's rounding error
+    // (fma) and the error of log2(e) as a float (1.925963e-8)
+    const float t = x * 1.44269502162933349609375f;
+    const float t_lo = fmaf(x, 1.925963033500011079e-8f, fmaf(x, 1.44269502162933349609375f, -t));
+    const float z = rintf(t);
+    const float f = (t - z) + t_lo;
+    float p = 1.5403530393381606e-4f;
+    p = fmaf(p, f, 1.3333558146428443e-3f);
+    p = fmaf(p, f, 9.6181291076284772e-3f);
+    p = fmaf(p, f, 5.5504108664821580e-2f);
+    p = fmaf(p, f, 2.4022650695910071e-1f);
+    p = fmaf(p, f, 6.9314718055994531e-1f);
+    p = fmaf(p, f, 1.0f);
+    return ldexpf(p, (int)z);
+}
+
+extern "C" void orc_exp_gauss_array(int64_t n, const float *x, float *y) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_exp_gauss(x[i]);
 }
 
 /* Model::prepareCam (core/src/model.cpp:500-544). */

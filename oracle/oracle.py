@@ -41,6 +41,9 @@ def lib() -> C.CDLL:
         L.orc_expf.restype = C.c_float
         L.orc_expf.argtypes = [C.c_float]
         L.orc_expf_array.argtypes = [C.c_int64, P, P]
+        L.orc_exp_gauss.argtypes = [C.c_float]
+        L.orc_exp_gauss.restype = C.c_float
+        L.orc_exp_gauss_array.argtypes = [C.c_int64, P, P]
         L.orc_ssim_window.argtypes = [P]
         L.orc_num_threads.restype = C.c_int
         L.orc_prepare_cam.argtypes = [P, C.c_float, C.c_float, C.c_float, C.c_float, C.c_int, C.c_int,
@@ -86,6 +89,17 @@ def expf_array(x: np.ndarray) -> np.ndarray:
     x = _f(x)
     y = np.empty_like(x)
     lib().orc_expf_array(x.size, _p(x), _p(y))
+    return y
+
+
+def exp_gauss(x: float) -> float:
+    return float(lib().orc_exp_gauss(x))
+
+
+def exp_gauss_array(x: np.ndarray) -> np.ndarray:
+    x = _f(x)
+    y = np.zeros_like(x)
+    lib().orc_exp_gauss_array(x.size, _p(x), _p(y))
     return y
 
 

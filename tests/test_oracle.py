@@ -51,6 +51,28 @@ def test_expf_special_values(orc):
     assert orc.expf(-103.0) > 0.0  # subnormal range is kept
 
 
+def test_exp_gauss_accuracy(orc):
+    """The rasterizer's Gaussian falloff exp: within 3 ulp of exp where
+    alpha can reach 1/255 (x >= -5.6), within 3e-7 relative down to -80,
+    and clamped (never below 3e-38) further down."""
+    x = np.linspace(-5.6, 0.0, 400_001, dtype=np.float32)
+    y = orc.exp_gauss_array(x).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
+    assert (np.abs(y - ref) / ulp).max() <= 3.0
+    x = np.linspace(-80.0, 0.0, 200_001, dtype=np.float32)
+    y = orc.exp_gauss_array(x).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    assert (np.abs(y - ref) / ref).max() <= 3e-7
+    assert orc.exp_gauss(0.0) == 1.0
+    assert orc.exp_gauss(-1e9) >= 3e-38
+    assert orc.exp_gauss(float("nan")) >= 3e-38  # NaN is clamped like -inf
+    # monotone non-increasing in |x| on a dense grid (no reduction seams)
+    x = np.linspace(-20.0, 0.0, 1_000_001, dtype=np.float32)
+    y = orc.exp_gauss_array(x)
+    assert np.all(np.diff(y.astype(np.float64)) >= 0.0)
+
+
 # ----------------------------------------------------------------- SH ----
 def test_sh_basis_is_orthonormal():
     # closed-form constants must give an orthonormal basis on the sphere
