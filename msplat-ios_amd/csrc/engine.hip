@@ -59,7 +59,7 @@ struct Engine {
     const float *bg = nullptr;
     bool have_grads = false;
     bool raster_grads = false;  // grads16 belongs to the current forward
-    bool g16_moments = false;   // grads16[0..8] hold ray moments, not dL/dtransMat
+    bool g16_moments = false;   // grads16 holds the image-only backward's unfinished sums
     bool log_valid = false;   // blend log written for the most recent forward
     bool full_valid = false;  // depth / normal / alpha / median / distortion outputs written
     // timing
@@ -339,7 +339,7 @@ int last_locked(int which, void **ptr, int64_t *numel) {
             // the image-only backward leaves ray moments; turn them into the
             // reference's dL/dtransMat with this forward's records
             if (E.g16_moments) {
-                mskern::launch_moments_to_dT(E.stream, E.n, P<float>(E.rec), P<float>(E.grads16));
+                mskern::launch_finish_image_grads(E.stream, E.n, P<float>(E.rec), P<float>(E.grads16));
                 E.g16_moments = false;
             }
             break;
@@ -738,7 +738,7 @@ int msplat_hip_raster_bwd(const float *dL_dimg, const float *dL_ddepth, const fl
         E.stream, E.W, E.H, E.tiles_x, E.tiles_y, P<int>(E.offsets), P<uint32_t>(E.blend_log), P<float>(E.t_ckpt),
         P<int>(E.wave_cnt), P<float>(E.rec), E.bg, P<float>(E.final_Ts), P<int>(E.final_idx), dL_dimg, dL_ddepth,
         dL_dalpha, dL_dnormal, dL_dmedian, dL_ddist, 0.0f, grads16);
-    if (t_moments) mskern::launch_moments_to_dT(E.stream, E.n, P<float>(E.rec), grads16);
+    if (t_moments) mskern::launch_finish_image_grads(E.stream, E.n, P<float>(E.rec), grads16);
     HIPC(hipGetLastError());
     return MSPLAT_OK;
     API_END

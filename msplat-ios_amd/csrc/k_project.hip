@@ -200,9 +200,29 @@ __device__ __forceinline__ void moments_to_dT(f3 Tu, f3 Tv, f3 Tw, float xs, flo
     g[8] = e.z - f.z - xs * dU.z - ys * dV.z;
 }
 
+// The image-only raster backward leaves per-splat sums without their
+// per-splat factors; this applies them: the nine ray moments times
+// -opacity, the opacity sum times the sigmoid's derivative opacity
+// (1 - opacity) (msplat_metal.metal:1976), the colour sums masked where the
+// colour was clamped at zero (:1873-1880; the record holds the clamped
+// colour, positive exactly where the clamp passes the gradient).  Then the
+// moments become dL/dtransMat.
+__device__ __forceinline__ void finish_image_grads(f3 Tu, f3 Tv, f3 Tw, float4 q2, float4 q3, float4 q4,
+                                                   float g[16]) {
+    const float opa = q2.w;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) g[k] *= -opa;
+    g[12] *= opa * (1.0f - opa);
+    g[13] = q3.w > 0.0f ? g[13] : 0.0f;
+    g[14] = q4.x > 0.0f ? g[14] : 0.0f;
+    g[15] = q4.y > 0.0f ? g[15] : 0.0f;
+    moments_to_dT(Tu, Tv, Tw, q2.y, q2.z, g);
+}
+
 // project_and_sh_backward_2dgs_kernel (msplat_metal.metal:2003-2209).
-// t_moments: grads16[0..8] hold the ray moments (see moments_to_dT) instead
-// of dL/dtransMat.
+// rec non-null: grads16 holds the image-only raster backward's sums (see
+// finish_image_grads), finished here with the transMat rows recomputed from
+// the parameters and the rest of the splat's record.
 // FUSED: the per-gaussian gradients stay on chip and the six Adam groups
 // (model.cpp:806-826) are updated in place, so neither the 58-float gradient
 // nor a second pass over the parameters touches HBM.
@@ -245,6 +265,7 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
 #pragma unroll
     for (int k = 0; k < 24; ++k) basis[k] = 0.f;
     const bool vis_ok = valid && radii[si] > 0;
+    float g_opa = 0.f;  // the visible splat's (finished) opacity-logit gradient
     if (vis_ok) {
         const float p[3] = {means[3 * si], means[3 * si + 1], means[3 * si + 2]};
         const float sx = ms_expf(scales[2 * si]), sy = ms_expf(scales[2 * si + 1]);
@@ -270,8 +291,8 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
             const f3 cu = {halfW * cc.tu[0] + bx * cc.tu[3], halfH * cc.tu[1] + by * cc.tu[3], cc.tu[3]};
             const f3 cv = {halfW * cc.tv[0] + bx * cc.tv[3], halfH * cc.tv[1] + by * cc.tv[3], cc.tv[3]};
             const f3 co = {halfW * cc.pc[0] + bx * cc.pc[3], halfH * cc.pc[1] + by * cc.pc[3], cc.pc[3]};
-            const float4 q2 = rec[5 * si + 2];
-            moments_to_dT({cu.x, cv.x, co.x}, {cu.y, cv.y, co.y}, {cu.z, cv.z, co.z}, q2.y, q2.z, g);
+            finish_image_grads({cu.x, cv.x, co.x}, {cu.y, cv.y, co.y}, {cu.z, cv.z, co.z}, rec[5 * si + 2],
+                               rec[5 * si + 3], rec[5 * si + 4], g);
         }
         const f3 dcu = {g[0], g[3], g[6]}, dcv = {g[1], g[4], g[7]}, dco = {g[2], g[5], g[8]};
         const float du[4] = {halfW * dcu.x, halfH * dcu.y, 0.0f, bx * dcu.x + by * dcu.y + dcu.z};
@@ -299,6 +320,7 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
         gm[2] = gp.z;
         const f3 dir_un = {p[0] - cam.cam_pos[0], p[1] - cam.cam_pos[1], p[2] - cam.cam_pos[2]};
         const f3 dir = normalize3(dir_un);
+        g_opa = g[12];
         vc[0] = g[13];
         vc[1] = g[14];
         vc[2] = g[15];
@@ -324,7 +346,7 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
     const int nrest = sh_deg >= 4 ? 24 : sh_deg == 3 ? 15 : sh_deg == 2 ? 8 : sh_deg == 1 ? 3 : 0;
     // dL_dopacity is read for every splat, as the reference's Adam reads the
     // raster's opacity-gradient buffer (zero for culled splats).
-    const float gop = valid ? g16[16 * si + 12] : 0.f;
+    const float gop = vis_ok ? g_opa : valid ? g16[16 * si + 12] : 0.f;
     if (valid) {
         if (!FUSED) {
             for (int k = 0; k < 3; ++k) dmeans[3 * si + k] = gm[k];
@@ -396,19 +418,26 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
     }
 }
 
-// grads16[0..8]: ray moments -> dL/dtransMat, with the rows of the splat
-// records (the image-only raster backward's output made the reference's).
-__global__ void k_moments_to_dT(int n, const float4 *__restrict__ rec, float *__restrict__ g16) {
+// The image-only raster backward's grads16 rows -> the reference's raster
+// gradients (finish_image_grads), in place, with the splat records' rows.
+__global__ void k_finish_image_grads(int n, const float4 *__restrict__ rec, float *__restrict__ g16) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    const float4 q0 = rec[5 * (size_t)i], q1 = rec[5 * (size_t)i + 1], q2 = rec[5 * (size_t)i + 2];
-    float *g = g16 + 16 * (size_t)i;
-    float v[9];
+    const float4 *r = rec + 5 * (size_t)i;
+    const float4 q0 = r[0], q1 = r[1];
+    float4 *g4 = reinterpret_cast<float4 *>(g16 + 16 * (size_t)i);
+    float v[16];
 #pragma unroll
-    for (int k = 0; k < 9; ++k) v[k] = g[k];
-    moments_to_dT({q0.x, q0.y, q0.z}, {q0.w, q1.x, q1.y}, {q1.z, q1.w, q2.x}, q2.y, q2.z, v);
+    for (int k = 0; k < 4; ++k) {
+        const float4 t = g4[k];
+        v[4 * k] = t.x;
+        v[4 * k + 1] = t.y;
+        v[4 * k + 2] = t.z;
+        v[4 * k + 3] = t.w;
+    }
+    finish_image_grads({q0.x, q0.y, q0.z}, {q0.w, q1.x, q1.y}, {q1.z, q1.w, r[2].x}, r[2], r[3], r[4], v);
 #pragma unroll
-    for (int k = 0; k < 9; ++k) g[k] = v[k];
+    for (int k = 0; k < 4; ++k) g4[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
 }
 
 __global__ void k_gather(const float *__restrict__ src, int src_stride, int src_off, int nf,
@@ -472,9 +501,9 @@ void launch_project_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaus
     }
 }
 
-void launch_moments_to_dT(hipStream_t s, int n, const float *rec, float *g16) {
+void launch_finish_image_grads(hipStream_t s, int n, const float *rec, float *g16) {
     if (n <= 0) return;
-    hipLaunchKernelGGL(k_moments_to_dT, dim3(blocks_for(n, 256)), dim3(256), 0, s, n,
+    hipLaunchKernelGGL(k_finish_image_grads, dim3(blocks_for(n, 256)), dim3(256), 0, s, n,
                        reinterpret_cast<const float4 *>(rec), g16);
 }
 

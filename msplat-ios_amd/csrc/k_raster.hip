@@ -288,9 +288,11 @@ __device__ __forceinline__ void wave_lds_sync() {
 // global float atomic (one 64-byte line) per (wave, splat).
 // FULL = false is the training step's case: the only upstream gradient is
 // dL/dimage, so the depth / alpha / normal / median / distortion terms are
-// compiled out, the colour suffix is carried as its projection on dL/dimage
-// and the per-splat factors (opacity, colour clamp masks) are applied once
-// after the wave reduction.
+// compiled out and the colour suffix is carried as its projection on
+// dL/dimage.  Its grads16 rows hold per-splat sums without their per-splat
+// factors: the nine ray moments without -opacity, the opacity-logit sum
+// without opacity (1 - opacity), the colour sums without the clamp mask;
+// finish_image_grads applies them once per splat.
 template <bool FULL>
 __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     int W, int H, int tiles_x, int T, const int *__restrict__ offsets, const uint4 *__restrict__ blend_log,
@@ -304,8 +306,10 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     constexpr int kWave = 64;
     // record planes per staged entry: the image-only path stages 4, the full one 5
     __shared__ float4 s_r[4][FULL ? 5 : 4][kWave];
-    __shared__ uint4 s_e[4][kWave];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ uint4 s_e[4][FULL ? kWave : 1];
+    const int lane = threadIdx.x & 63;
+    // uniform, so that the log entries of the image-only loop are scalar loads
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int pxi = tx * 16 + lane_px(wave, lane);
     const int pyi = ty * 16 + lane_py(wave, lane);
@@ -347,17 +351,10 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     // holds grads16 index gi (the image-only layout exchanges 3 / 9, 10 / 11)
     const int vi = ((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 + ((lane >> 2) & 1);
     const int gi = FULL ? vi : vi == 3 ? 9 : vi == 9 ? 3 : vi == 10 ? 11 : vi == 11 ? 10 : vi;
-    // post-reduction factor in the image-only case: -opa for the nine ray
-    // moments, opa (1 - opa) for the opacity logit, 1 for the colours, 0 for
-    // the normals
-    const float fa = gi < 9 ? -1.f : gi == 12 ? 1.f : 0.f;
-    const float fb = gi == 12 ? -1.f : 0.f;
-    const float fc = gi >= 13 ? 1.f : 0.f;
-    const int ch = gi - 13;
 
     // suffix state of the reference's recurrences (image-only: the colour
-    // suffix projected on dL/dimage)
-    float last_alpha = 0.f, acc_v = 0.f, last_v = 0.f;
+    // suffix projected on dL/dimage, updated as soon as a splat is done)
+    float last_alpha = 0.f, acc_v = 0.f;
     float acc_c[3] = {0.f, 0.f, 0.f}, last_c[3] = {0.f, 0.f, 0.f};
     float acc_d = 0.f, last_d = 0.f, acc_a = 0.f, last_dLdT = 0.f;
     float acc_n[3] = {0.f, 0.f, 0.f}, last_n[3] = {0.f, 0.f, 0.f};
@@ -397,19 +394,20 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 s_r[wave][2][lane] = make_float4(nAy.z, xs, ys, q2.w);
                 s_r[wave][3][lane] = make_float4(q3.w, q4.x, q4.y, 0.f);
             }
-            s_e[wave][lane] = e;
+            if (FULL) s_e[wave][lane] = e;
         }
         wave_lds_sync();
         for (int j = m - 1; j >= 0; --j) {
-            const uint4 e = s_e[wave][j];
-            const unsigned bal = lane < 32 ? e.x : e.y;
-            const bool has = (bal >> (lane & 31)) & 1u;
+            // image-only: the entry's address is uniform (scalar load) and
+            // its ballot is the lane mask of `has` itself
+            const uint4 e = FULL ? s_e[wave][j] : lg[c0 + j];
+            const bool has = FULL ? (((lane < 32 ? e.x : e.y) >> (lane & 31)) & 1u)
+                                  : __builtin_amdgcn_inverse_ballot_w64(((uint64_t)e.y << 32) | e.x);
             float v16[16];
-            float opa;
             if (!FULL) {
                 const float4 q0 = s_r[wave][0][j], q1 = s_r[wave][1][j], q2 = s_r[wave][2][j];
                 const float4 q3 = s_r[wave][3][j];
-                opa = q2.w;
+                const float opa = q2.w;
                 const float dxs = q2.y - px, dys = q2.z - py;
                 const float rx = __builtin_fmaf(dxs, q0.w, __builtin_fmaf(dys, q1.z, q0.x));
                 const float ry = __builtin_fmaf(dxs, q1.x, __builtin_fmaf(dys, q1.w, q0.y));
@@ -419,27 +417,33 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 const float rho3d = __builtin_fmaf(u, u, v * v);
                 const float rho2d = FILTER_INV_SQ * __builtin_fmaf(dxs, dxs, dys * dys);
                 const bool use3d = rho3d <= rho2d;
-                const float G = __builtin_amdgcn_exp2f(__builtin_fminf(rho3d, rho2d) * -0.72134752044448170368f);
-                const float alpha = has ? __builtin_fminf(0.99f, opa * G) : 0.f;
+                // zero where the lane did not blend: alpha, the transmittance
+                // factor, the suffix update and every gradient term follow
+                const float G =
+                    has ? __builtin_amdgcn_exp2f(__builtin_fminf(rho3d, rho2d) * -0.72134752044448170368f) : 0.f;
+                const float alpha = __builtin_fminf(0.99f, opa * G);
                 const float inv_om = __builtin_amdgcn_rcpf(1.0f - alpha);
                 Tr *= inv_om;  // transmittance before this splat (unchanged where it did not blend)
                 const float aT = alpha * Tr;
                 const float vv = __builtin_fmaf(dp0, q3.x, __builtin_fmaf(dp1, q3.y, dp2 * q3.z));  // dL/dimage . colour
-                const float acc_new = __builtin_fmaf(last_alpha, last_v - acc_v, acc_v);
-                acc_v = has ? acc_new : acc_v;
-                last_v = has ? vv : last_v;
-                last_alpha = has ? alpha : last_alpha;
-                const float dLda = __builtin_fmaf(vv - acc_v, Tr, bgT * inv_om);
-                const float gg = has ? dLda * G : 0.f;
+                // acc_v is the suffix behind this splat.  The reference
+                // folds a splat in when the next blended splat is reached
+                // (last_alpha / last_color, :1875-1876, :1919); folding it
+                // in as soon as it is done uses the same values, and
+                // alpha = 0 leaves the suffix unchanged without a select
+                const float dv = vv - acc_v;
+                const float dLda = __builtin_fmaf(dv, Tr, bgT * inv_om);
+                acc_v = __builtin_fmaf(alpha, dv, acc_v);
+                const float gg = dLda * G;
                 // dL/d(ray), up to the factor -opa, on the 3D branch: the
                 // ray-splat point (gg u, gg v) / ray.z pulled back through
                 // (u, v) = ray.xy / ray.z; its moments over the wave's pixels
                 // about the splat centre (sum dp, sum (xs - px) dp,
                 // sum (ys - py) dp) determine the nine transMat gradients
-                const float t = gg * inv_z;
-                const float dsx = use3d ? t * u : 0.f;
-                const float dsy = use3d ? t * v : 0.f;
-                const float dpz = use3d ? -__builtin_fmaf(dsx, u, dsy * v) : 0.f;
+                const float t = (use3d ? gg : 0.f) * inv_z;
+                const float dsx = t * u;
+                const float dsy = t * v;
+                const float dpz = -__builtin_fmaf(dsx, u, dsy * v);
                 // reduction slots: grads16 index k in slot k, except that
                 // slots 3 / 9 and 10 / 11 are exchanged (kSlotImg), which puts
                 // two of the three zero normals in one first-stage pair
@@ -464,7 +468,7 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 const float4 q3 = s_r[wave][3][j], q4 = s_r[wave][4][j];
                 const float Tux = q0.x, Tuy = q0.y, Tuz = q0.z, Tvx = q0.w, Tvy = q1.x, Tvz = q1.y;
                 const float Twx = q1.z, Twy = q1.w, Twz = q2.x;
-                opa = q2.w;
+                const float opa = q2.w;
                 const f3 k = {__builtin_fmaf(px, Twx, -Tux), __builtin_fmaf(px, Twy, -Tuy),
                               __builtin_fmaf(px, Twz, -Tuz)};
                 const f3 l = {__builtin_fmaf(py, Twx, -Tvx), __builtin_fmaf(py, Twy, -Tvy),
@@ -543,13 +547,7 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 v16[8] = px * dk.z + py * dl.z + dL_dz;
                 v16[12] = G * dL_dG * (1.0f - opa);
             }
-            float s = FULL ? wave_reduce16(v16, lane) : wave_reduce16<true>(v16, lane);
-            if (!FULL) {
-                const float4 q3 = s_r[wave][3][j];
-                const float cc = ch == 0 ? q3.x : ch == 1 ? q3.y : q3.z;
-                const float f = __builtin_fmaf(opa, __builtin_fmaf(fb, opa, fa), fc);
-                s = (fc != 0.f && !(cc > 0.f)) ? 0.f : s * f;
-            }
+            const float s = FULL ? wave_reduce16(v16, lane) : wave_reduce16<true>(v16, lane);
             if ((lane & 3) == 0 && s != 0.f) unsafeAtomicAdd(&grads16[(size_t)e.w * 16 + gi], s);
         }
         wave_lds_sync();

@@ -17,14 +17,16 @@ namespace mskern {
 void launch_project_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, float *rec,
                         float *depths, int *radii, uint32_t *rect, unsigned long long *isect_total,
                         float *colors_raw);
-// moments_rec (the forward's splat records) non-null: g16[0..8] hold the
-// image-only raster backward's ray moments instead of dL/dtransMat.
+// moments_rec (the forward's splat records) non-null: g16 holds the
+// image-only raster backward's sums (ray moments and unscaled per-splat
+// sums), finished inside the kernel.
 void launch_project_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, const int *radii,
                         const float *g16, float *dmeans, float *dscales, float *dquats, float *dmean2d,
                         float *dfdc, float *dfrest, float *grad_norm, float *vis, float *max2d,
                         float inv_max_dim, const MsplatAdam *adam, const float *moments_rec);
-// g16[0..8]: ray moments -> dL/dtransMat, in place (rows from the records).
-void launch_moments_to_dT(hipStream_t s, int n, const float *rec, float *g16);
+// The image-only raster backward's g16 rows -> the reference's raster
+// gradients (dL/dtransMat, dL/dopacity logit, dL/dcolors), in place.
+void launch_finish_image_grads(hipStream_t s, int n, const float *rec, float *g16);
 void launch_gather(hipStream_t s, const float *src, int src_stride, int src_off, int nf, float *dst, int n);
 void launch_tiles_hit(hipStream_t s, const uint32_t *rect, const int *radii, int *out, int n);
 
@@ -59,8 +61,8 @@ void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
                        float *out_depth, float *out_normal, float *out_alpha, float *out_median, float *out_dist,
                        unsigned long long *pair_counter, uint32_t *blend_log, float *t_ckpt, int *wave_cnt,
                        bool full_outputs);
-// Returns true when the image-only kernel ran: grads16[0..8] then hold the
-// ray moments (launch_moments_to_dT / launch_project_bwd convert them).
+// Returns true when the image-only kernel ran: grads16 then holds its sums
+// (launch_finish_image_grads / launch_project_bwd finish them).
 bool launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets,
                        const uint32_t *blend_log, const float *t_ckpt, const int *wave_cnt, const float *rec,
                        const float *bg, const float *final_Ts, const int *final_idx, const float *dL_dimg,
