@@ -21,24 +21,27 @@ namespace {
 constexpr int kThreads = 256;
 constexpr float kMScale = FAR_N / (FAR_N - NEAR_N);
 
-// Stages the record of splat gid in LDS slot threadIdx.x and returns its
-// wave-strip mask for the tile whose top-left pixel is (sx0, sy0).
-__device__ __forceinline__ int load_batch(const float4 *__restrict__ rec, int gid, float4 *s_rec, float sx0,
-                                          float sy0) {
+// Stages the record of splat gid, list position pos, in LDS slot
+// threadIdx.x and returns its wave-block mask for the tile whose top-left
+// pixel is (sx0, sy0).  Planes: 0..2 the record's first three float4
+// (transMat rows, centre, opacity), 3 = (colour, pos), 4 = (normal, gid).
+__device__ __forceinline__ int load_batch(const float4 *__restrict__ rec, int gid, int pos, float4 *s_rec,
+                                          float sx0, float sy0) {
     const float4 *r = rec + 5 * (size_t)gid;
-    float4 q[5];
-#pragma unroll
-    for (int k = 0; k < 5; ++k) {
-        q[k] = r[k];
-        s_rec[k * kThreads + threadIdx.x] = q[k];
-    }
-    return strip_mask_fine(q[0], q[1], q[2], q[4].z, sx0, sy0);
+    const float4 q0 = r[0], q1 = r[1], q2 = r[2], q3 = r[3], q4 = r[4];
+    s_rec[threadIdx.x] = q0;
+    s_rec[kThreads + threadIdx.x] = q1;
+    s_rec[2 * kThreads + threadIdx.x] = q2;
+    s_rec[3 * kThreads + threadIdx.x] = make_float4(q3.w, q4.x, q4.y, __int_as_float(pos));
+    s_rec[4 * kThreads + threadIdx.x] = make_float4(q3.x, q3.y, q3.z, __int_as_float(gid));
+    return strip_mask_fine(q0, q1, q2, q4.z, sx0, sy0);
 }
 
 // Per-wave slot lists of one batch: s_list[w][0..n_w) holds, in ascending
-// order, the slots whose mask m has bit w.  Returns n for the calling
-// thread's wave.  Called by all threads of the workgroup (two barriers).
-__device__ __forceinline__ int build_wave_lists(int m, unsigned char (*s_list)[kThreads], int (*s_cnt)[4]) {
+// order, the byte offsets (16 * slot) of the slots whose mask m has bit w.
+// Returns n for the calling thread's wave.  Called by all threads of the
+// workgroup (two barriers).
+__device__ __forceinline__ int build_wave_lists(int m, int (*s_list)[kThreads], int (*s_cnt)[4]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const unsigned long long below = (1ull << lane) - 1ull;
     int pos[4];
@@ -54,7 +57,7 @@ __device__ __forceinline__ int build_wave_lists(int m, unsigned char (*s_list)[k
         if ((m >> w) & 1) {
             int off = pos[w];
             for (int wv = 0; wv < wave; ++wv) off += s_cnt[wv][w];
-            s_list[w][off] = (unsigned char)threadIdx.x;
+            s_list[w][off] = 16 * (int)threadIdx.x;
         }
     }
     // wave-uniform: keeps the visit loop's control in scalar registers
@@ -75,9 +78,9 @@ __device__ __forceinline__ int build_wave_lists(int m, unsigned char (*s_list)[k
 // transmittance before that splat (a prefix checkpoint) at
 // t_ckpt[4 * start + wave * len + k + lane].
 // With FULL_OUT = false only what the image-only training step consumes is
-// produced: out_img, final_Ts[.][0] (T) and final_idx[.][0] (last
-// contributor); the depth, normal, alpha, median and distortion outputs and
-// the distortion moments are neither accumulated nor written.  Every
+// produced: out_img and final_Ts[.][0] (T); the last and median contributor
+// indices, the depth, normal, alpha, median and distortion outputs and the
+// distortion moments are neither accumulated nor written.  Every
 // decision, and so every produced value, is the same as with FULL_OUT.
 template <bool LOG, bool FULL_OUT>
 __global__ __launch_bounds__(kThreads) void k_raster_fwd(
@@ -89,10 +92,10 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     float *__restrict__ t_ckpt, int *__restrict__ wave_cnt) {
     const int tile = xcd_tile(blockIdx.x, T);
     if (tile >= T) return;
-    __shared__ float4 s_rec[5 * kThreads];
-    __shared__ int s_id[LOG ? kThreads : 1];
+    __shared__ float4 s_rec[5 * kThreads];  // the batch's records (load_batch planes)
     const int tx = tile % tiles_x, ty = tile / tiles_x;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int pxi = tx * 16 + lane_px(wave, lane);
     const int pyi = ty * 16 + lane_py(wave, lane);
     const bool inside = pxi < W && pyi < H;
@@ -101,42 +104,51 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     const int start = offsets[tile], end = offsets[tile + 1];
     const float bg0 = bgp[0], bg1 = bgp[1], bg2 = bgp[2];
     const size_t log_base = 4 * (size_t)start + (size_t)wave * (size_t)(end - start);
+    uint4 *wave_log = LOG ? blend_log + log_base : nullptr;
     int nlog = 0;  // wave-uniform
+    const char *s_bytes = reinterpret_cast<const char *>(s_rec);
 
     float Tr = 1.f, cr = 0.f, cg = 0.f, cb = 0.f, dep = 0.f, nx = 0.f, ny = 0.f, nz = 0.f;
     float M1 = 0.f, M2 = 0.f, dist = 0.f, med = 0.f;
     int med_c = -1, last_c = 0;
-    bool done = !inside;
+    // the wave's lanes whose pixel is finished (outside the image or
+    // terminated); the visit loop keeps every lane decision as a lane mask
+    uint64_t done_m = __builtin_amdgcn_ballot_w64(!inside);
 
-    __shared__ unsigned char s_list[4][kThreads];
+    __shared__ int s_list[4][kThreads];
     __shared__ int s_cnt[4][4];
-    int evals = 0, blends = 0;
+    // wave totals of the work counters (scalar: ballot popcounts)
+    unsigned evals = 0, blends = 0;
+    const bool count = pair_counter != nullptr;
     for (int b0 = start; b0 < end; b0 += kThreads) {
-        if (__syncthreads_and(done)) break;
+        if (__syncthreads_and(done_m == ~0ull)) break;
         const int idx = b0 + (int)threadIdx.x;
         const int gid = idx < end ? ids[idx] : 0;
-        if (LOG) s_id[threadIdx.x] = gid;
-        const int m = idx < end ? load_batch(rec, gid, s_rec, sx0, sy0) : 0;
+        const int m = idx < end ? load_batch(rec, gid, idx - start, s_rec, sx0, sy0) : 0;
         const int n = build_wave_lists(m, s_list, s_cnt);
-        if (__all(done)) continue;
-        const int base = b0 - start + 1;  // contributor number of slot 0 (1-based)
+        if (done_m == ~0ull) continue;
         for (int j = 0; j < n; ++j) {
-            const int t = s_list[wave][j];
+            const int to = s_list[wave][j];  // byte offset of the slot in a record plane
+            const auto plane = [&](int k) {
+                return *reinterpret_cast<const float4 *>(s_bytes + k * (kThreads * 16) + to);
+            };
             const float T_before = Tr;
             // predicated: a lane that is done or rejects the pair adds
             // colour * 0 (bit-identical sums) and keeps its state
-            evals += done ? 0 : 1;
-            const float4 q0 = s_rec[t], q1 = s_rec[kThreads + t], q2 = s_rec[2 * kThreads + t];
+            if (count) evals += __builtin_popcountll(~done_m);
+            const float4 q0 = plane(0), q1 = plane(1), q2 = plane(2);
             PairEval e;
-            const bool act = eval_pair(px, py, q0, q1, q2, e) & !done;
+            const uint64_t act = eval_pair(px, py, q0, q1, q2, e) & ~done_m;
             const float next_T = Tr * (1.0f - e.alpha);
-            const bool term = act & (next_T <= 1e-4f);
-            const bool blend = act & !term;
-            done = done | term;
-            blends += blend ? 1 : 0;
+            const uint64_t term = act & __builtin_amdgcn_ballot_w64(next_T <= 1e-4f);
+            const uint64_t bal = act & ~term;  // the lanes that blend the splat
+            done_m |= term;
+            const bool blend = __builtin_amdgcn_inverse_ballot_w64(bal);
             const float w = blend ? e.alpha * Tr : 0.0f;
-            const float4 q3 = s_rec[3 * kThreads + t], q4 = s_rec[4 * kThreads + t];
+            const float4 q3 = plane(3), q4 = plane(4);
             if (FULL_OUT) {
+                // 1-based list position of the splat (the reference's contributor count)
+                const int contrib = __float_as_int(q3.w) + 1;
                 const float A = 1.f - Tr;
                 const float dep_s = blend ? e.depth : 1.0f;  // finite stand-in off the blend
                 const float m_ = kMScale * (1.f - NEAR_N / dep_s);
@@ -145,28 +157,26 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
                 M2 = __builtin_fmaf(m_ * m_, w, M2);
                 const bool med_now = blend & (Tr > 0.5f);
                 med = med_now ? e.depth : med;
-                med_c = med_now ? base + t : med_c;
+                med_c = med_now ? contrib : med_c;
                 dep = __builtin_fmaf(dep_s, w, dep);
-                nx = __builtin_fmaf(q3.x, w, nx);
-                ny = __builtin_fmaf(q3.y, w, ny);
-                nz = __builtin_fmaf(q3.z, w, nz);
+                nx = __builtin_fmaf(q4.x, w, nx);
+                ny = __builtin_fmaf(q4.y, w, ny);
+                nz = __builtin_fmaf(q4.z, w, nz);
+                last_c = blend ? contrib : last_c;
             }
-            cr = __builtin_fmaf(q3.w, w, cr);
-            cg = __builtin_fmaf(q4.x, w, cg);
-            cb = __builtin_fmaf(q4.y, w, cb);
+            cr = __builtin_fmaf(q3.x, w, cr);
+            cg = __builtin_fmaf(q3.y, w, cg);
+            cb = __builtin_fmaf(q3.z, w, cb);
             Tr = blend ? next_T : Tr;
-            last_c = blend ? base + t : last_c;
-            if (LOG) {
-                const unsigned long long bal = __ballot(blend);
-                if (bal) {
-                    if (lane == 0)
-                        blend_log[log_base + nlog] =
-                            make_uint4((unsigned)bal, (unsigned)(bal >> 32), (unsigned)(base - 1 + t), (unsigned)s_id[t]);
-                    if ((nlog & 63) == 0 && nlog > 0) t_ckpt[log_base + nlog + lane] = T_before;
-                    ++nlog;
-                }
+            if (count) blends += __builtin_popcountll(bal);
+            if (LOG && bal) {
+                if (lane == 0)
+                    wave_log[nlog] = make_uint4((unsigned)bal, (unsigned)(bal >> 32), __float_as_uint(q3.w),
+                                                __float_as_uint(q4.w));
+                if ((nlog & 63) == 0 && nlog > 0) t_ckpt[log_base + nlog + lane] = T_before;
+                ++nlog;
             }
-            if (__all(done)) break;
+            if (done_m == ~0ull) break;
         }
     }
     if (LOG && lane == 0) wave_cnt[4 * tile + wave] = nlog;
@@ -176,20 +186,22 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
         __syncthreads();
         if (threadIdx.x < 3) s_cnt3[threadIdx.x] = 0;
         __syncthreads();
-        atomicAdd(&s_cnt3[0], (unsigned)evals);
-        atomicAdd(&s_cnt3[2], (unsigned)blends);
-        if (lane == 0) atomicAdd(&s_cnt3[1], (unsigned)nlog);
+        if (lane == 0) {
+            atomicAdd(&s_cnt3[0], evals);
+            atomicAdd(&s_cnt3[2], blends);
+            atomicAdd(&s_cnt3[1], (unsigned)nlog);
+        }
         __syncthreads();
         if (threadIdx.x < 3) atomicAdd(pair_counter + threadIdx.x, (unsigned long long)s_cnt3[threadIdx.x]);
     }
     if (!inside) return;
     const size_t pix = (size_t)pyi * W + pxi;
     final_Ts[3 * pix + 0] = Tr;
-    final_idx[2 * pix + 0] = last_c;
     out_img[3 * pix + 0] = __builtin_fmaf(bg0, Tr, cr);
     out_img[3 * pix + 1] = __builtin_fmaf(bg1, Tr, cg);
     out_img[3 * pix + 2] = __builtin_fmaf(bg2, Tr, cb);
     if (!FULL_OUT) return;
+    final_idx[2 * pix + 0] = last_c;
     final_Ts[3 * pix + 1] = M1;
     final_Ts[3 * pix + 2] = M2;
     final_idx[2 * pix + 1] = med_c;

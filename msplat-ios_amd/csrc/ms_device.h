@@ -79,22 +79,18 @@ __device__ __forceinline__ float ms_expf(float x) {
 
 __device__ __forceinline__ float ms_sigmoid(float x) { return 1.0f / (1.0f + ms_expf(-x)); }
 
-// exp(x) for x <= 0 in the rasterizer's alpha (the Gaussian falloff
-// exp(-rho / 2)), shared bit for bit with the golden model's
-// orc_exp_gauss: x is clamped to [-86, 0] (NaN becomes -86), then
-// t = x log2(e) is formed as t_hi + t_lo, z = rint(t_hi),
-// f = (t_hi - z) + t_lo, and 2^f on [-1/2, 1/2] is the degree-6 Taylor
-// polynomial of e^(f ln 2) (truncation error below 1.2e-7 relative) scaled
-// by ldexp(., z).  A few ulp from exp, and a normal number everywhere
-// (>= 3e-38), which is all the 1/255 alpha threshold needs far out.
-__host__ __device__ __forceinline__ float ms_exp_gauss(float x) {
-    x = __builtin_fmaxf(x, -86.0f);
-    // t = x log2(e) carried as t_hi + t_lo: the product's rounding error
-    // (fma) and the error of log2(e) as a float (1.925963e-8)
-    const float t = x * 1.44269502162933349609375f;
-    const float t_lo = __builtin_fmaf(x, 1.925963033500011079e-8f, __builtin_fmaf(x, 1.44269502162933349609375f, -t));
+// The rasterizer's Gaussian falloff exp(-rho / 2), rho >= 0, shared bit for
+// bit with the golden model's orc_gauss: t = rho * (-log2(e) / 2) (one
+// rounding; the constant is log2(e) as a float, halved exactly), clamped at
+// -124 (NaN becomes -124), z = rint(t), f = t - z (exact, |f| <= 1/2), 2^f
+// as the degree-6 Taylor polynomial of e^(f ln 2) (truncation error below
+// 1.2e-7 relative), then ldexp(., z).  The rounding of t dominates: within
+// 8 ulp (5e-7 relative) of exp, and a normal number everywhere (>= 4e-38),
+// which is all the 1/255 alpha threshold needs far out.
+__host__ __device__ __forceinline__ float ms_gauss(float rho) {
+    const float t = __builtin_fmaxf(rho * -0.721347510814666748046875f, -124.0f);
     const float z = __builtin_rintf(t);
-    const float f = (t - z) + t_lo;
+    const float f = t - z;
     float p = 1.5403530393381606e-4f;
     p = __builtin_fmaf(p, f, 1.3333558146428443e-3f);
     p = __builtin_fmaf(p, f, 9.6181291076284772e-3f);
@@ -349,12 +345,13 @@ struct PairEval {
     float inv_z, u, v, rho3d, rho2d, depth, G, alpha;
 };
 
-__device__ __forceinline__ bool eval_pair(float px, float py, const float4 &q0, const float4 &q1,
+__device__ __forceinline__ uint64_t eval_pair(float px, float py, const float4 &q0, const float4 &q1,
                                           const float4 &q2, PairEval &e) {
-    // Straight-line: every value is computed, then one predicate applies the
-    // reference's four rejections with their exact comparisons (a NaN
-    // compares false in each, as in the reference's early returns), so the
-    // wave needs no exec-mask branches per rejection.
+    // Straight-line: every value is computed, then the reference's
+    // rejections are applied with their exact comparisons (a NaN compares
+    // false in each, as in the reference's early returns), each as the
+    // wave's lane mask, so the wave needs no exec-mask branches.  Returns the
+    // mask of the wave's lanes whose pair passes; called by the whole wave.
     const float Tux = q0.x, Tuy = q0.y, Tuz = q0.z;
     const float Tvx = q0.w, Tvy = q1.x, Tvz = q1.y;
     const float Twx = q1.z, Twy = q1.w, Twz = q2.x;
@@ -370,10 +367,13 @@ __device__ __forceinline__ bool eval_pair(float px, float py, const float4 &q0, 
     e.rho2d = FILTER_INV_SQ * __builtin_fmaf(dxs, dxs, dys * dys);
     const float rho = __builtin_fminf(e.rho3d, e.rho2d);
     e.depth = __builtin_fmaf(e.u, Twx, __builtin_fmaf(e.v, Twy, Twz));
-    const float power = -0.5f * rho;
-    e.G = ms_exp_gauss(power);
+    // The reference's power > 0 rejection (msplat_metal.metal:676-677) never
+    // fires: rho is a minimum of sums of squares (>= 0, +inf or NaN), so
+    // power = -rho / 2 is <= 0, -inf or NaN.
+    e.G = ms_gauss(rho);
     e.alpha = __builtin_fminf(0.99f, q2.w * e.G);
-    return !(e.ray.z == 0.0f) & !(e.depth < NEAR_N) & !(power > 0.0f) & !(e.alpha < 1.0f / 255.0f);
+    return __builtin_amdgcn_ballot_w64(!(e.ray.z == 0.0f)) & __builtin_amdgcn_ballot_w64(!(e.depth < NEAR_N)) &
+           __builtin_amdgcn_ballot_w64(!(e.alpha < 1.0f / 255.0f));
 }
 
 // Pixels of a 16x16 tile handled by wave w of a 256-thread rasterizer

@@ -300,9 +300,10 @@ inline bool eval_pair(float px, float py, const float *Tm, const float *xy,
     const float rho = fminf(e.rho3d, e.rho2d);
     e.depth = fmaf(e.u, Tw.x, fmaf(e.v, Tw.y, Tw.z));
     if (e.depth < NEAR_N) return false;
-    const float power = -0.5f * rho;
-    if (power > 0.0f) return false;
-    e.G = orc_exp_gauss(power);
+    /* The reference's power > 0 rejection (msplat_metal.metal:676-677) never
+     * fires: rho is a minimum of sums of squares (>= 0, +inf or NaN), so
+     * -rho / 2 is <= 0, -inf or NaN. */
+    e.G = orc_gauss(rho);
     e.alpha = fminf(0.99f, opac * e.G);
     if (e.alpha < 1.0f / 255.0f) return false;
     return true;
@@ -399,21 +400,18 @@ extern "C" float orc_expf(float x) {
     return (p * s1) * s2;
 }
 
-/* The rasterizer's Gaussian falloff exp(x), x <= 0: clamp to [-86, 0] (NaN
- * becomes -86), t = x log2(e) as t_hi + t_lo (the product's rounding error by
- * fma, plus the error of log2(e) as a float), z = rint(t_hi),
- * f = (t_hi - z) + t_lo, 2^f as the degree-6 Taylor polynomial of
- * e^(f ln 2) on [-1/2, 1/2] (truncation error below 1.2e-7 relative), then
- * ldexp(., z).  The same IEEE operations as the kernels' ms_exp_gauss, so both
- * agree bit for bit; a few ulp from exp, never below 3e-38. */
-extern "C" float orc_exp_gauss(float x) {
-    x = fmaxf(x, -86.0f);
-    // t = x log2(e) carried as t_hi + t_lo: the product's rounding error
-    // (fma) and the error of log2(e) as a float (1.925963e-8)
-    const float t = x * 1.44269502162933349609375f;
-    const float t_lo = fmaf(x, 1.925963033500011079e-8f, fmaf(x, 1.44269502162933349609375f, -t));
+/* The rasterizer's Gaussian falloff exp(-rho / 2), rho >= 0:
+ * t = rho * (-log2(e) / 2) with one rounding (log2(e) as a float, halved
+ * exactly), clamped at -124 (NaN becomes -124), z = rint(t), f = t - z
+ * (exact), 2^f as the degree-6 Taylor polynomial of e^(f ln 2) on
+ * [-1/2, 1/2] (truncation error below 1.2e-7 relative), then ldexp(., z).
+ * The same IEEE operations as the kernels' ms_gauss, so both agree bit for
+ * bit; within 8 ulp of exp (the rounding of t dominates), never below
+ * 4e-38. */
+extern "C" float orc_gauss(float rho) {
+    const float t = fmaxf(rho * -0.721347510814666748046875f, -124.0f);
     const float z = rintf(t);
-    const float f = (t - z) + t_lo;
+    const float f = t - z;
     float p = 1.5403530393381606e-4f;
     p = fmaf(p, f, 1.3333558146428443e-3f);
     p = fmaf(p, f, 9.6181291076284772e-3f);
@@ -424,8 +422,8 @@ extern "C" float orc_exp_gauss(float x) {
     return ldexpf(p, (int)z);
 }
 
-extern "C" void orc_exp_gauss_array(int64_t n, const float *x, float *y) {
-    for (int64_t i = 0; i < n; ++i) y[i] = orc_exp_gauss(x[i]);
+extern "C" void orc_gauss_array(int64_t n, const float *rho, float *y) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_gauss(rho[i]);
 }
 
 /* Model::prepareCam (core/src/model.cpp:500-544). */

@@ -13,7 +13,7 @@
  *     fmaf() call;
  *   - '/' and sqrtf are IEEE correctly rounded; rsqrt is written 1/sqrtf;
  *   - exp is orc_expf (Cephes-style polynomial with Cody-Waite reduction),
- *     not libm, and the rasterizer's Gaussian falloff is orc_exp_gauss
+ *     not libm, and the rasterizer's Gaussian falloff is orc_gauss
  *     (exp2 reduction + degree-6 polynomial + ldexp), so host and device
  *     agree exactly;
  *   - float->int truncation saturates (orc_f2i) instead of invoking UB.
@@ -55,8 +55,8 @@ void  orc_prepare_cam(const float cam_to_world[16], float fx, float fy,
 
 float orc_expf(float x);
 void  orc_expf_array(int64_t n, const float *x, float *y);
-float orc_exp_gauss(float x);
-void  orc_exp_gauss_array(int64_t n, const float *x, float *y);
+float orc_gauss(float rho);
+void  orc_gauss_array(int64_t n, const float *rho, float *y);
 void  orc_ssim_window(float w[11]);
 int   orc_num_threads(void);
 

@@ -41,9 +41,9 @@ def lib() -> C.CDLL:
         L.orc_expf.restype = C.c_float
         L.orc_expf.argtypes = [C.c_float]
         L.orc_expf_array.argtypes = [C.c_int64, P, P]
-        L.orc_exp_gauss.argtypes = [C.c_float]
-        L.orc_exp_gauss.restype = C.c_float
-        L.orc_exp_gauss_array.argtypes = [C.c_int64, P, P]
+        L.orc_gauss.argtypes = [C.c_float]
+        L.orc_gauss.restype = C.c_float
+        L.orc_gauss_array.argtypes = [C.c_int64, P, P]
         L.orc_ssim_window.argtypes = [P]
         L.orc_num_threads.restype = C.c_int
         L.orc_prepare_cam.argtypes = [P, C.c_float, C.c_float, C.c_float, C.c_float, C.c_int, C.c_int,
@@ -92,14 +92,15 @@ def expf_array(x: np.ndarray) -> np.ndarray:
     return y
 
 
-def exp_gauss(x: float) -> float:
-    return float(lib().orc_exp_gauss(x))
+def gauss(rho: float) -> float:
+    """The rasterizer's Gaussian falloff exp(-rho / 2)."""
+    return float(lib().orc_gauss(rho))
 
 
-def exp_gauss_array(x: np.ndarray) -> np.ndarray:
-    x = _f(x)
-    y = np.zeros_like(x)
-    lib().orc_exp_gauss_array(x.size, _p(x), _p(y))
+def gauss_array(rho: np.ndarray) -> np.ndarray:
+    rho = _f(rho)
+    y = np.zeros_like(rho)
+    lib().orc_gauss_array(rho.size, _p(rho), _p(y))
     return y
 
 

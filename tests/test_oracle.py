@@ -51,26 +51,36 @@ def test_expf_special_values(orc):
     assert orc.expf(-103.0) > 0.0  # subnormal range is kept
 
 
-def test_exp_gauss_accuracy(orc):
-    """The rasterizer's Gaussian falloff exp: within 3 ulp of exp where
-    alpha can reach 1/255 (x >= -5.6), within 3e-7 relative down to -80,
-    and clamped (never below 3e-38) further down."""
-    x = np.linspace(-5.6, 0.0, 400_001, dtype=np.float32)
-    y = orc.exp_gauss_array(x).astype(np.float64)
-    ref = np.exp(x.astype(np.float64))
+def test_gauss_accuracy(orc):
+    """The rasterizer's Gaussian falloff exp(-rho / 2): within 8 ulp of exp
+    where alpha can reach 1/255 (rho <= 11.2), within the rounding of its
+    exponent up to rho = 160, exact at 0, clamped (never below 4e-38)
+    further out, NaN treated like +inf, and monotone."""
+    rho = np.linspace(0.0, 11.2, 400_001, dtype=np.float32)
+    y = orc.gauss_array(rho).astype(np.float64)
+    ref = np.exp(-0.5 * rho.astype(np.float64))
     ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
-    assert (np.abs(y - ref) / ulp).max() <= 3.0
-    x = np.linspace(-80.0, 0.0, 200_001, dtype=np.float32)
-    y = orc.exp_gauss_array(x).astype(np.float64)
-    ref = np.exp(x.astype(np.float64))
-    assert (np.abs(y - ref) / ref).max() <= 3e-7
-    assert orc.exp_gauss(0.0) == 1.0
-    assert orc.exp_gauss(-1e9) >= 3e-38
-    assert orc.exp_gauss(float("nan")) >= 3e-38  # NaN is clamped like -inf
-    # monotone non-increasing in |x| on a dense grid (no reduction seams)
-    x = np.linspace(-20.0, 0.0, 1_000_001, dtype=np.float32)
-    y = orc.exp_gauss_array(x)
-    assert np.all(np.diff(y.astype(np.float64)) >= 0.0)
+    assert (np.abs(y - ref) / ulp).max() <= 8.0
+    # further out the exponent t = -rho log2(e) / 2 dominates: its rounding
+    # (half an ulp of t) and the float log2(e) (1.34e-8 relative), each
+    # times ln 2, relative
+    rho = np.linspace(0.0, 160.0, 200_001, dtype=np.float32)
+    y = orc.gauss_array(rho).astype(np.float64)
+    ref = np.exp(-0.5 * rho.astype(np.float64))
+    t = rho.astype(np.float64) * 0.72134752
+    t_ulp = np.spacing(t.astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(y - ref) / ref <= 2.5e-7 + 0.4 * t_ulp + 1.0e-8 * t)
+    assert orc.gauss(0.0) == 1.0
+    # a plausible slip in the reduction (a dropped halving, a wrong-sign
+    # exponent) is far outside these bounds
+    assert abs(orc.gauss(2.0) - np.exp(-1.0)) <= 2e-7 * np.exp(-1.0)
+    assert orc.gauss(1e9) >= 4e-38
+    assert orc.gauss(float("inf")) >= 4e-38
+    assert orc.gauss(float("nan")) == orc.gauss(float("inf"))
+    # monotone non-increasing in rho on a dense grid (no reduction seams)
+    rho = np.linspace(0.0, 40.0, 1_000_001, dtype=np.float32)
+    y = orc.gauss_array(rho)
+    assert np.all(np.diff(y.astype(np.float64)) <= 0.0)
 
 
 # ----------------------------------------------------------------- SH ----
