@@ -38,10 +38,10 @@ __device__ __forceinline__ int load_batch(const float4 *__restrict__ rec, int gi
 }
 
 // Per-wave slot lists of one batch: s_list[w][0..n_w) holds, in ascending
-// order, the byte offsets (16 * slot) of the slots whose mask m has bit w.
+// order, the slots whose mask m has bit w.
 // Returns n for the calling thread's wave.  Called by all threads of the
 // workgroup (two barriers).
-__device__ __forceinline__ int build_wave_lists(int m, int (*s_list)[kThreads], int (*s_cnt)[4]) {
+__device__ __forceinline__ int build_wave_lists(int m, unsigned char (*s_list)[kThreads], int (*s_cnt)[4]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const unsigned long long below = (1ull << lane) - 1ull;
     int pos[4];
@@ -57,7 +57,7 @@ __device__ __forceinline__ int build_wave_lists(int m, int (*s_list)[kThreads], 
         if ((m >> w) & 1) {
             int off = pos[w];
             for (int wv = 0; wv < wave; ++wv) off += s_cnt[wv][w];
-            s_list[w][off] = 16 * (int)threadIdx.x;
+            s_list[w][off] = (unsigned char)threadIdx.x;
         }
     }
     // wave-uniform: keeps the visit loop's control in scalar registers
@@ -73,16 +73,19 @@ __device__ __forceinline__ int build_wave_lists(int m, int (*s_list)[kThreads], 
 // order, at blend_log[4 * start + wave * len + k] (len = the tile's list
 // length, which bounds a wave's visits); wave_cnt[4 * tile + wave] receives
 // the entry count.  Bit l of the ballot is set when lane l's pixel blended
-// the splat, so the backward replays exactly the forward's decisions.  At
-// every log entry k > 0 with k % 64 == 0 each lane also stores its
-// transmittance before that splat (a prefix checkpoint) at
-// t_ckpt[4 * start + wave * len + k + lane].
+// the splat, so the backward replays exactly the forward's decisions.  For
+// every k > 0 with k % 64 == 0 each lane also stores its transmittance
+// before log entry k (a prefix checkpoint) at
+// t_ckpt[4 * start + wave * len + k + lane], as soon as entry k - 1 is
+// logged (so also when the log ends at k entries).
+// COUNT adds the work counters {pairs evaluated, log entries, pairs
+// blended} to pair_counter.
 // With FULL_OUT = false only what the image-only training step consumes is
 // produced: out_img and final_Ts[.][0] (T); the last and median contributor
 // indices, the depth, normal, alpha, median and distortion outputs and the
 // distortion moments are neither accumulated nor written.  Every
 // decision, and so every produced value, is the same as with FULL_OUT.
-template <bool LOG, bool FULL_OUT>
+template <bool LOG, bool FULL_OUT, bool COUNT>
 __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     int W, int H, int tiles_x, int T, const int *__restrict__ offsets, const int *__restrict__ ids,
     const float4 *__restrict__ rec, const float *__restrict__ bgp, float *__restrict__ out_img,
@@ -115,11 +118,10 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     // terminated); the visit loop keeps every lane decision as a lane mask
     uint64_t done_m = __builtin_amdgcn_ballot_w64(!inside);
 
-    __shared__ int s_list[4][kThreads];
+    __shared__ unsigned char s_list[4][kThreads];
     __shared__ int s_cnt[4][4];
     // wave totals of the work counters (scalar: ballot popcounts)
     unsigned evals = 0, blends = 0;
-    const bool count = pair_counter != nullptr;
     for (int b0 = start; b0 < end; b0 += kThreads) {
         if (__syncthreads_and(done_m == ~0ull)) break;
         const int idx = b0 + (int)threadIdx.x;
@@ -128,14 +130,13 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
         const int n = build_wave_lists(m, s_list, s_cnt);
         if (done_m == ~0ull) continue;
         for (int j = 0; j < n; ++j) {
-            const int to = s_list[wave][j];  // byte offset of the slot in a record plane
+            const int to = 16 * (int)s_list[wave][j];  // byte offset of the slot in a record plane
             const auto plane = [&](int k) {
                 return *reinterpret_cast<const float4 *>(s_bytes + k * (kThreads * 16) + to);
             };
-            const float T_before = Tr;
             // predicated: a lane that is done or rejects the pair adds
             // colour * 0 (bit-identical sums) and keeps its state
-            if (count) evals += __builtin_popcountll(~done_m);
+            if (COUNT) evals += __builtin_popcountll(~done_m);
             const float4 q0 = plane(0), q1 = plane(1), q2 = plane(2);
             PairEval e;
             const uint64_t act = eval_pair(px, py, q0, q1, q2, e) & ~done_m;
@@ -168,19 +169,21 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
             cg = __builtin_fmaf(q3.y, w, cg);
             cb = __builtin_fmaf(q3.z, w, cb);
             Tr = blend ? next_T : Tr;
-            if (count) blends += __builtin_popcountll(bal);
+            if (COUNT) blends += __builtin_popcountll(bal);
             if (LOG && bal) {
                 if (lane == 0)
-                    wave_log[nlog] = make_uint4((unsigned)bal, (unsigned)(bal >> 32), __float_as_uint(q3.w),
-                                                __float_as_uint(q4.w));
-                if ((nlog & 63) == 0 && nlog > 0) t_ckpt[log_base + nlog + lane] = T_before;
-                ++nlog;
+                    *wave_log = make_uint4((unsigned)bal, (unsigned)(bal >> 32), __float_as_uint(q3.w),
+                                           __float_as_uint(q4.w));
+                ++wave_log;
+                // the transmittance before the next logged splat is the
+                // current one (a visit no lane blends changes nothing)
+                if ((++nlog & 63) == 0) t_ckpt[log_base + nlog + lane] = Tr;
             }
             if (done_m == ~0ull) break;
         }
     }
     if (LOG && lane == 0) wave_cnt[4 * tile + wave] = nlog;
-    if (pair_counter) {
+    if (COUNT) {
         // {pairs evaluated, log entries, pairs blended}
         __shared__ unsigned int s_cnt3[3];
         __syncthreads();
@@ -583,10 +586,18 @@ void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
                            reinterpret_cast<const float4 *>(rec), bg, out_img, final_Ts, final_idx, out_depth,
                            out_normal, out_alpha, out_median, out_dist, pair_counter, lg, t_ckpt, wave_cnt);
     };
-    if (blend_log)
-        full_outputs ? launch(k_raster_fwd<true, true>) : launch(k_raster_fwd<true, false>);
-    else
-        full_outputs ? launch(k_raster_fwd<false, true>) : launch(k_raster_fwd<false, false>);
+    // the work counters are a separate instantiation (profiling only)
+    if (pair_counter) {
+        if (blend_log)
+            full_outputs ? launch(k_raster_fwd<true, true, true>) : launch(k_raster_fwd<true, false, true>);
+        else
+            full_outputs ? launch(k_raster_fwd<false, true, true>) : launch(k_raster_fwd<false, false, true>);
+    } else {
+        if (blend_log)
+            full_outputs ? launch(k_raster_fwd<true, true, false>) : launch(k_raster_fwd<true, false, false>);
+        else
+            full_outputs ? launch(k_raster_fwd<false, true, false>) : launch(k_raster_fwd<false, false, false>);
+    }
 }
 
 bool launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets,
