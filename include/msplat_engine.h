@@ -278,6 +278,14 @@ int64_t msplat_hip_last_pairs_evaluated(void);
  * (pixel, gaussian) pairs blended.  No counterpart in the reference: it
  * measures the rasterizers' work. */
 int msplat_hip_last_raster_counts(int64_t out[3]);
+/* Self-check of the rasterizer's arithmetic: *mismatches receives the
+ * number of floats with exponent field efield_lo..efield_hi (1..254, both
+ * signs, every mantissa) where the fast reciprocal it uses for 1 / ray.z
+ * (hardware reciprocal + one Newton step) differs from the correctly rounded
+ * division.  Zero is required for efield 1..252 (|x| in [2^-126, 2^126));
+ * the rasterizer divides outside that range.  msplat_hip_init runs it over
+ * [1, 2) and fails on a mismatch.  No counterpart in the reference. */
+int msplat_hip_check_fast_rcp(int efield_lo, int efield_hi, int64_t *mismatches);
 
 #ifdef __cplusplus
 }

@@ -43,6 +43,7 @@ struct Engine {
     // per-intersection
     DevBuf keys, keys_tmp, ids;  // keys: per (splat, super-tile) pair
     DevBuf blend_log, t_ckpt, wave_cnt;  // the raster forward's per-wave blend log
+    DevBuf selfcheck;                    // counter of the arithmetic self-check
     // per-pixel
     DevBuf out_img, final_Ts, final_idx, out_depth, out_normal, out_alpha, out_median, out_dist;
     DevBuf dL_dimg, gm1, gs1, gs12, partials, loss;
@@ -119,6 +120,8 @@ T *P(DevBuf &b) {
     return static_cast<T *>(b.p);
 }
 
+int check_rcp_locked(int lo, int hi, int64_t *bad);
+
 int init_locked() {
     if (g_eng.ready) return MSPLAT_OK;
     int count = 0;
@@ -147,7 +150,31 @@ int init_locked() {
         gsum += gw[i];
     }
     for (int i = 0; i < 11; ++i) g_eng.window[i] = (float)(gw[i] / gsum);
+    // The rasterizer takes 1 / ray.z as the hardware reciprocal plus one
+    // Newton step, which must equal the correctly rounded division (the
+    // golden model's); verified here over [1, 2) and (-2, -1].
+    int64_t bad = 0;
+    CHECK(check_rcp_locked(127, 127, &bad));
+    if (bad != 0) {
+        set_err("fast reciprocal differs from division on %lld floats of [1, 2)", (long long)bad);
+        return MSPLAT_E_NODEV;
+    }
     g_eng.ready = true;
+    return MSPLAT_OK;
+}
+
+// Floats of exponent fields lo..hi where the rasterizer's fast reciprocal
+// differs from the correctly rounded division (synchronous).
+int check_rcp_locked(int lo, int hi, int64_t *bad) {
+    Engine &E = g_eng;
+    CHECK(ensure(E.selfcheck, 8));
+    HIPC(hipMemsetAsync(E.selfcheck.p, 0, 8, E.stream));
+    for (int ef = lo; ef <= hi; ++ef) mskern::launch_check_rcp(E.stream, ef, P<unsigned long long>(E.selfcheck));
+    HIPC(hipGetLastError());
+    unsigned long long h = 0;
+    HIPC(hipMemcpyAsync(&h, E.selfcheck.p, 8, hipMemcpyDeviceToHost, E.stream));
+    HIPC(hipStreamSynchronize(E.stream));
+    *bad = (int64_t)h;
     return MSPLAT_OK;
 }
 
@@ -429,7 +456,7 @@ void msplat_hip_cleanup(void) {
     if (!E.ready) return;
     (void)hipStreamSynchronize(E.stream);
     DevBuf *all[] = {&E.rec, &E.depths, &E.radii, &E.rect, &E.grads16, &E.colors_raw, &E.counts, &E.scan_tmp, &E.super_counts, &E.super_offsets, &E.super_cursor, &E.super_tmp, &E.offsets,
-                     &E.stats, &E.big_list, &E.keys, &E.keys_tmp, &E.ids, &E.blend_log, &E.t_ckpt, &E.wave_cnt, &E.out_img, &E.final_Ts,
+                     &E.stats, &E.big_list, &E.keys, &E.keys_tmp, &E.ids, &E.blend_log, &E.t_ckpt, &E.wave_cnt, &E.selfcheck, &E.out_img, &E.final_Ts,
                      &E.final_idx, &E.out_depth, &E.out_normal, &E.out_alpha, &E.out_median, &E.out_dist,
                      &E.dL_dimg, &E.gm1, &E.gs1, &E.gs12, &E.partials, &E.loss, &E.dmeans, &E.dscales,
                      &E.dquats, &E.dmean2d, &E.dfdc, &E.dfrest, &E.dens_flags, &E.dens_scan, &E.pair_counter};
@@ -817,6 +844,14 @@ int msplat_hip_last_raster_counts(int64_t out[3]) {
     if (!out) return MSPLAT_E_ARG;
     for (int i = 0; i < 3; ++i) out[i] = g_eng.pairs[i];
     return MSPLAT_OK;
+}
+
+int msplat_hip_check_fast_rcp(int efield_lo, int efield_hi, int64_t *mismatches) {
+    API_BEGIN
+    if (!mismatches || efield_lo < 1 || efield_hi > 254 || efield_lo > efield_hi) return MSPLAT_E_ARG;
+    ENSURE_INIT();
+    return check_rcp_locked(efield_lo, efield_hi, mismatches);
+    API_END
 }
 
 }  // extern "C"

@@ -21,19 +21,24 @@ namespace {
 constexpr int kThreads = 256;
 constexpr float kMScale = FAR_N / (FAR_N - NEAR_N);
 
-// Stages the record of splat gid, list position pos, in LDS slot
-// threadIdx.x and returns its wave-block mask for the tile whose top-left
-// pixel is (sx0, sy0).  Planes: 0..2 the record's first three float4
-// (transMat rows, centre, opacity), 3 = (colour, pos), 4 = (normal, gid).
+// Stages splat gid, list position pos, in LDS slot threadIdx.x and returns
+// its wave-block mask for the tile whose top-left pixel is (sx0, sy0).
+// Planes: 0..2 the centred ray rows, centre and opacity (eval_pair's
+// p0..p2), 3 = (Tw, pos), 4 = (colour, gid), 5 = (normal, 0) when NORMAL.
+template <bool NORMAL>
 __device__ __forceinline__ int load_batch(const float4 *__restrict__ rec, int gid, int pos, float4 *s_rec,
                                           float sx0, float sy0) {
     const float4 *r = rec + 5 * (size_t)gid;
     const float4 q0 = r[0], q1 = r[1], q2 = r[2], q3 = r[3], q4 = r[4];
-    s_rec[threadIdx.x] = q0;
-    s_rec[kThreads + threadIdx.x] = q1;
-    s_rec[2 * kThreads + threadIdx.x] = q2;
-    s_rec[3 * kThreads + threadIdx.x] = make_float4(q3.w, q4.x, q4.y, __int_as_float(pos));
-    s_rec[4 * kThreads + threadIdx.x] = make_float4(q3.x, q3.y, q3.z, __int_as_float(gid));
+    const f3 Tw = {q1.z, q1.w, q2.x};
+    f3 R0, nAx, nAy;
+    centred_rows({q0.x, q0.y, q0.z}, {q0.w, q1.x, q1.y}, Tw, q2.y, q2.z, R0, nAx, nAy);
+    s_rec[threadIdx.x] = make_float4(R0.x, R0.y, R0.z, nAx.x);
+    s_rec[kThreads + threadIdx.x] = make_float4(nAx.y, nAx.z, nAy.x, nAy.y);
+    s_rec[2 * kThreads + threadIdx.x] = make_float4(nAy.z, q2.y, q2.z, q2.w);
+    s_rec[3 * kThreads + threadIdx.x] = make_float4(Tw.x, Tw.y, Tw.z, __int_as_float(pos));
+    s_rec[4 * kThreads + threadIdx.x] = make_float4(q3.w, q4.x, q4.y, __int_as_float(gid));
+    if (NORMAL) s_rec[5 * kThreads + threadIdx.x] = make_float4(q3.x, q3.y, q3.z, 0.f);
     return strip_mask_fine(q0, q1, q2, q4.z, sx0, sy0);
 }
 
@@ -95,14 +100,17 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     float *__restrict__ t_ckpt, int *__restrict__ wave_cnt) {
     const int tile = xcd_tile(blockIdx.x, T);
     if (tile >= T) return;
-    __shared__ float4 s_rec[5 * kThreads];  // the batch's records (load_batch planes)
+    __shared__ float4 s_rec[(FULL_OUT ? 6 : 5) * kThreads];  // the batch's records (load_batch planes)
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int pxi = tx * 16 + lane_px(wave, lane);
     const int pyi = ty * 16 + lane_py(wave, lane);
     const bool inside = pxi < W && pyi < H;
-    const float px = (float)pxi, py = (float)pyi;
+    float px = (float)pxi, py = (float)pyi;
+    // kept in registers (the compiler would otherwise convert them again on
+    // every visit)
+    asm volatile("" : "+v"(px), "+v"(py));
     const float sx0 = (float)(tx * 16), sy0 = (float)(ty * 16);
     const int start = offsets[tile], end = offsets[tile + 1];
     const float bg0 = bgp[0], bg1 = bgp[1], bg2 = bgp[2];
@@ -126,7 +134,7 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
         if (__syncthreads_and(done_m == ~0ull)) break;
         const int idx = b0 + (int)threadIdx.x;
         const int gid = idx < end ? ids[idx] : 0;
-        const int m = idx < end ? load_batch(rec, gid, idx - start, s_rec, sx0, sy0) : 0;
+        const int m = idx < end ? load_batch<FULL_OUT>(rec, gid, idx - start, s_rec, sx0, sy0) : 0;
         const int n = build_wave_lists(m, s_list, s_cnt);
         if (done_m == ~0ull) continue;
         for (int j = 0; j < n; ++j) {
@@ -137,16 +145,16 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
             // predicated: a lane that is done or rejects the pair adds
             // colour * 0 (bit-identical sums) and keeps its state
             if (COUNT) evals += __builtin_popcountll(~done_m);
-            const float4 q0 = plane(0), q1 = plane(1), q2 = plane(2);
+            const float4 q0 = plane(0), q1 = plane(1), q2 = plane(2), q3 = plane(3);
             PairEval e;
-            const uint64_t act = eval_pair(px, py, q0, q1, q2, e) & ~done_m;
+            const uint64_t act = eval_pair(px, py, q0, q1, q2, q3, e) & ~done_m;
             const float next_T = Tr * (1.0f - e.alpha);
             const uint64_t term = act & __builtin_amdgcn_ballot_w64(next_T <= 1e-4f);
             const uint64_t bal = act & ~term;  // the lanes that blend the splat
             done_m |= term;
             const bool blend = __builtin_amdgcn_inverse_ballot_w64(bal);
             const float w = blend ? e.alpha * Tr : 0.0f;
-            const float4 q3 = plane(3), q4 = plane(4);
+            const float4 q4 = plane(4);
             if (FULL_OUT) {
                 // 1-based list position of the splat (the reference's contributor count)
                 const int contrib = __float_as_int(q3.w) + 1;
@@ -160,14 +168,15 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
                 med = med_now ? e.depth : med;
                 med_c = med_now ? contrib : med_c;
                 dep = __builtin_fmaf(dep_s, w, dep);
-                nx = __builtin_fmaf(q4.x, w, nx);
-                ny = __builtin_fmaf(q4.y, w, ny);
-                nz = __builtin_fmaf(q4.z, w, nz);
+                const float4 q5 = plane(5);
+                nx = __builtin_fmaf(q5.x, w, nx);
+                ny = __builtin_fmaf(q5.y, w, ny);
+                nz = __builtin_fmaf(q5.z, w, nz);
                 last_c = blend ? contrib : last_c;
             }
-            cr = __builtin_fmaf(q3.x, w, cr);
-            cg = __builtin_fmaf(q3.y, w, cg);
-            cb = __builtin_fmaf(q3.z, w, cb);
+            cr = __builtin_fmaf(q4.x, w, cr);
+            cg = __builtin_fmaf(q4.y, w, cg);
+            cb = __builtin_fmaf(q4.z, w, cb);
             Tr = blend ? next_T : Tr;
             if (COUNT) blends += __builtin_popcountll(bal);
             if (LOG && bal) {
@@ -319,8 +328,8 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     const int tile = xcd_tile(blockIdx.x, T);
     if (tile >= T) return;
     constexpr int kWave = 64;
-    // record planes per staged entry: the image-only path stages 4, the full one 5
-    __shared__ float4 s_r[4][FULL ? 5 : 4][kWave];
+    // record planes per staged entry: the image-only path stages 4, the full one 7
+    __shared__ float4 s_r[4][FULL ? 7 : 4][kWave];
     __shared__ uint4 s_e[4][FULL ? kWave : 1];
     const int lane = threadIdx.x & 63;
     // uniform, so that the log entries of the image-only loop are scalar loads
@@ -384,29 +393,20 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
         if (lane < m) {
             const uint4 e = lg[c0 + lane];
             const float4 *r = rec + 5 * (size_t)e.w;
+            // the forward's centred ray rows (centred_rows), then the colour;
+            // the full case adds the raw transMat rows and the normal
+            const float4 q0 = r[0], q1 = r[1], q2 = r[2], q3 = r[3], q4 = r[4];
+            f3 R0, nAx, nAy;
+            centred_rows({q0.x, q0.y, q0.z}, {q0.w, q1.x, q1.y}, {q1.z, q1.w, q2.x}, q2.y, q2.z, R0, nAx, nAy);
+            s_r[wave][0][lane] = make_float4(R0.x, R0.y, R0.z, nAx.x);
+            s_r[wave][1][lane] = make_float4(nAx.y, nAx.z, nAy.x, nAy.y);
+            s_r[wave][2][lane] = make_float4(nAy.z, q2.y, q2.z, q2.w);
             if (FULL) {
-#pragma unroll
-                for (int k = 0; k < 5; ++k) s_r[wave][k][lane] = r[k];
+                s_r[wave][3][lane] = q0;
+                s_r[wave][4][lane] = q1;
+                s_r[wave][5][lane] = make_float4(q2.x, q3.w, q4.x, q4.y);
+                s_r[wave][6][lane] = make_float4(q3.x, q3.y, q3.z, 0.f);
             } else {
-                // The ray of pixel p, k x l with k = px Tw - Tu and
-                // l = py Tw - Tv, expanded about the splat centre (xs, ys):
-                //   ray = R0 + (px - xs) Ax + (py - ys) Ay,
-                // R0 = kc x lc, Ax = Tw x lc, Ay = kc x Tw (kc = xs Tw - Tu,
-                // lc = ys Tw - Tv); the (px - xs)(py - ys) term is Tw x Tw = 0.
-                // Every term stays at the splat's scale (an expansion about
-                // the image origin would cancel large terms).
-                const float4 q0 = r[0], q1 = r[1], q2 = r[2], q3 = r[3], q4 = r[4];
-                const f3 Tu = {q0.x, q0.y, q0.z}, Tv = {q0.w, q1.x, q1.y}, Tw = {q1.z, q1.w, q2.x};
-                const float xs = q2.y, ys = q2.z;
-                const f3 kc = {__builtin_fmaf(xs, Tw.x, -Tu.x), __builtin_fmaf(xs, Tw.y, -Tu.y),
-                               __builtin_fmaf(xs, Tw.z, -Tu.z)};
-                const f3 lc = {__builtin_fmaf(ys, Tw.x, -Tv.x), __builtin_fmaf(ys, Tw.y, -Tv.y),
-                               __builtin_fmaf(ys, Tw.z, -Tv.z)};
-                // stored: R0, -Ax, -Ay (the pixel loop uses xs - px, ys - py)
-                const f3 R0 = cross3(kc, lc), nAx = cross3(lc, Tw), nAy = cross3(Tw, kc);
-                s_r[wave][0][lane] = make_float4(R0.x, R0.y, R0.z, nAx.x);
-                s_r[wave][1][lane] = make_float4(nAx.y, nAx.z, nAy.x, nAy.y);
-                s_r[wave][2][lane] = make_float4(nAy.z, xs, ys, q2.w);
                 s_r[wave][3][lane] = make_float4(q3.w, q4.x, q4.y, 0.f);
             }
             if (FULL) s_e[wave][lane] = e;
@@ -479,22 +479,27 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 v16[14] = aT * dp1;
                 v16[15] = aT * dp2;
             } else {
-                const float4 q0 = s_r[wave][0][j], q1 = s_r[wave][1][j], q2 = s_r[wave][2][j];
-                const float4 q3 = s_r[wave][3][j], q4 = s_r[wave][4][j];
+                const float4 c0 = s_r[wave][0][j], c1 = s_r[wave][1][j], c2 = s_r[wave][2][j];
+                const float4 q0 = s_r[wave][3][j], q1 = s_r[wave][4][j], q5 = s_r[wave][5][j];
+                const float4 q6 = s_r[wave][6][j];
                 const float Tux = q0.x, Tuy = q0.y, Tuz = q0.z, Tvx = q0.w, Tvy = q1.x, Tvz = q1.y;
-                const float Twx = q1.z, Twy = q1.w, Twz = q2.x;
-                const float opa = q2.w;
+                const float Twx = q1.z, Twy = q1.w, Twz = q5.x;
+                const float opa = c2.w;
+                // k and l carry the transMat gradients; the ray is the
+                // forward's centred one, bit for bit (so ray.z is non-zero
+                // wherever the lane blended)
                 const f3 k = {__builtin_fmaf(px, Twx, -Tux), __builtin_fmaf(px, Twy, -Tuy),
                               __builtin_fmaf(px, Twz, -Tuz)};
                 const f3 l = {__builtin_fmaf(py, Twx, -Tvx), __builtin_fmaf(py, Twy, -Tvy),
                               __builtin_fmaf(py, Twz, -Tvz)};
-                // the forward's ray.z, bit for bit (non-zero wherever the lane blended)
-                const float rz = __builtin_fmaf(k.x, l.y, -(k.y * l.x));
+                const float dxs = c2.y - px, dys = c2.z - py;
+                const float rx = __builtin_fmaf(dxs, c0.w, __builtin_fmaf(dys, c1.z, c0.x));
+                const float ry = __builtin_fmaf(dxs, c1.x, __builtin_fmaf(dys, c1.w, c0.y));
+                const float rz = __builtin_fmaf(dxs, c1.y, __builtin_fmaf(dys, c2.x, c0.z));
                 const float inv_z = has ? __builtin_amdgcn_rcpf(rz) : 0.f;
-                const float u = __builtin_fmaf(k.y, l.z, -(k.z * l.y)) * inv_z;
-                const float v = __builtin_fmaf(k.z, l.x, -(k.x * l.z)) * inv_z;
+                const float u = rx * inv_z;
+                const float v = ry * inv_z;
                 const float rho3d = __builtin_fmaf(u, u, v * v);
-                const float dxs = q2.y - px, dys = q2.z - py;
                 const float rho2d = FILTER_INV_SQ * __builtin_fmaf(dxs, dxs, dys * dys);
                 const bool use3d = rho3d <= rho2d;
                 const float G = __builtin_amdgcn_exp2f(__builtin_fminf(rho3d, rho2d) * -0.72134752044448170368f);
@@ -504,7 +509,7 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 const float aT = alpha * Tr;
                 // lanes that did not blend get a finite stand-in (their terms are zeroed)
                 const float depth = has ? __builtin_fmaf(u, Twx, __builtin_fmaf(v, Twy, Twz)) : 1.0f;
-                const float cu[3] = {q3.w, q4.x, q4.y}, nrm[3] = {q3.x, q3.y, q3.z};
+                const float cu[3] = {q5.y, q5.z, q5.w}, nrm[3] = {q6.x, q6.y, q6.z};
                 const float dpix[3] = {dp0, dp1, dp2}, dn[3] = {dn0, dn1, dn2};
                 float dL_dalpha = 0.0f;
 #pragma unroll
@@ -569,9 +574,24 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     }
 }
 
+// ms_rcp_nr against the correctly rounded division for every float of
+// exponent field efield (both signs, all 2^23 mantissas); bad counts the
+// differences.  One thread per float, 2^24 threads.
+__global__ __launch_bounds__(256) void k_check_rcp(uint32_t efield, unsigned long long *__restrict__ bad) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    const float x = __uint_as_float(((i >> 23) << 31) | (efield << 23) | (i & 0x7fffffu));
+    const bool differ = __float_as_uint(ms_rcp_nr(x)) != __float_as_uint(1.0f / x);
+    const unsigned long long n = __builtin_popcountll(__builtin_amdgcn_ballot_w64(differ));
+    if ((threadIdx.x & 63) == 0 && n) atomicAdd(bad, n);
+}
+
 }  // namespace
 
 namespace mskern {
+
+void launch_check_rcp(hipStream_t s, int efield, unsigned long long *bad) {
+    hipLaunchKernelGGL(k_check_rcp, dim3((1u << 24) / 256), dim3(256), 0, s, (uint32_t)efield, bad);
+}
 
 void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
                        const float *rec, const float *bg, float *out_img, float *final_Ts, int *final_idx,

@@ -69,6 +69,10 @@ bool launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
                        const float *dL_ddepth, const float *dL_daccum, const float *dL_dnormal,
                        const float *dL_dmedian, const float *dL_ddist, float ddist_uniform, float *grads16);
 constexpr int kBlendLogEntryBytes = 16;
+// Adds to *bad the number of floats of exponent field efield (1..254, both
+// signs, every mantissa) where the rasterizer's fast reciprocal differs from
+// the correctly rounded 1 / x.
+void launch_check_rcp(hipStream_t s, int efield, unsigned long long *bad);
 
 // k_ssim.hip
 int ssim_num_blocks(int W, int H);

@@ -336,42 +336,79 @@ __host__ __device__ __forceinline__ float4 splat_box(const float4 &q0, const flo
     return make_float4(x0 - mx, x1 + mx, y0 - my, y1 + my);
 }
 
+// The ray of pixel p through a splat, k x l with k = px Tw - Tu and
+// l = py Tw - Tv (msplat_metal.metal:655-658), expanded about the splat
+// centre (xs, ys): ray(p) = R0 + (xs - px) nAx + (ys - py) nAy with
+// kc = xs Tw - Tu, lc = ys Tw - Tv, R0 = kc x lc, nAx = lc x Tw,
+// nAy = Tw x kc (the (px - xs)(py - ys) term is Tw x Tw = 0).  Exact in real
+// arithmetic; every term stays at the splat's own scale, and a pixel needs
+// six fmas.  Computed once per splat, shared with the golden model.
+__host__ __device__ __forceinline__ void centred_rows(f3 Tu, f3 Tv, f3 Tw, float xs, float ys, f3 &R0, f3 &nAx,
+                                                      f3 &nAy) {
+    const f3 kc = {__builtin_fmaf(xs, Tw.x, -Tu.x), __builtin_fmaf(xs, Tw.y, -Tu.y), __builtin_fmaf(xs, Tw.z, -Tu.z)};
+    const f3 lc = {__builtin_fmaf(ys, Tw.x, -Tv.x), __builtin_fmaf(ys, Tw.y, -Tv.y), __builtin_fmaf(ys, Tw.z, -Tv.z)};
+    R0 = cross3(kc, lc);
+    nAx = cross3(lc, Tw);
+    nAy = cross3(Tw, kc);
+}
+
+// 1 / x: the hardware reciprocal and one Newton step.  Equal to the
+// correctly rounded 1 / x for every normal |x| < 2^126 (checked
+// exhaustively on gfx950, and at every library initialisation over one
+// binade); outside that range callers fall back to the division.
+__device__ __forceinline__ float ms_rcp_nr(float x) {
+    const float y = __builtin_amdgcn_rcpf(x);
+    return __builtin_fmaf(__builtin_fmaf(-x, y, 1.0f), y, y);
+}
+__device__ __forceinline__ bool ms_rcp_nr_exact(float x) {
+    const float a = __builtin_fabsf(x);
+    return a >= 0x1p-126f && a < 0x1p126f;
+}
+
 // One (pixel, splat) evaluation: the ray-splat intersection, low-pass
 // filter and alpha of nd_rasterize_forward_2dgs_kernel
-// (msplat_metal.metal:663-701).  Shared verbatim by the forward and the
-// backward so both take identical skip decisions.
+// (msplat_metal.metal:651-683), on the centred ray (centred_rows) of the
+// staged planes p0 = (R0, nAx.x), p1 = (nAx.yz, nAy.xy), p2 = (nAy.z, xs,
+// ys, opacity), p3 = (Tw, .).  Bit for bit the golden model's eval_pair.
 struct PairEval {
-    f3 k, l, ray;
+    f3 ray;
     float inv_z, u, v, rho3d, rho2d, depth, G, alpha;
 };
 
-__device__ __forceinline__ uint64_t eval_pair(float px, float py, const float4 &q0, const float4 &q1,
-                                          const float4 &q2, PairEval &e) {
+__device__ __forceinline__ uint64_t eval_pair(float px, float py, const float4 &p0, const float4 &p1,
+                                              const float4 &p2, const float4 &p3, PairEval &e) {
     // Straight-line: every value is computed, then the reference's
     // rejections are applied with their exact comparisons (a NaN compares
     // false in each, as in the reference's early returns), each as the
     // wave's lane mask, so the wave needs no exec-mask branches.  Returns the
     // mask of the wave's lanes whose pair passes; called by the whole wave.
-    const float Tux = q0.x, Tuy = q0.y, Tuz = q0.z;
-    const float Tvx = q0.w, Tvy = q1.x, Tvz = q1.y;
-    const float Twx = q1.z, Twy = q1.w, Twz = q2.x;
-    e.k = {__builtin_fmaf(px, Twx, -Tux), __builtin_fmaf(px, Twy, -Tuy), __builtin_fmaf(px, Twz, -Tuz)};
-    e.l = {__builtin_fmaf(py, Twx, -Tvx), __builtin_fmaf(py, Twy, -Tvy), __builtin_fmaf(py, Twz, -Tvz)};
-    e.ray = {__builtin_fmaf(e.k.y, e.l.z, -(e.k.z * e.l.y)), __builtin_fmaf(e.k.z, e.l.x, -(e.k.x * e.l.z)),
-             __builtin_fmaf(e.k.x, e.l.y, -(e.k.y * e.l.x))};
-    e.inv_z = 1.0f / e.ray.z;  // infinite when ray.z == 0; that pair is rejected below
+    const float dxs = p2.y - px, dys = p2.z - py;
+    e.ray = {__builtin_fmaf(dxs, p0.w, __builtin_fmaf(dys, p1.z, p0.x)),
+             __builtin_fmaf(dxs, p1.x, __builtin_fmaf(dys, p1.w, p0.y)),
+             __builtin_fmaf(dxs, p1.y, __builtin_fmaf(dys, p2.x, p0.z))};
+    // infinite when ray.z == 0; that pair is rejected below
+    e.inv_z = ms_rcp_nr(e.ray.z);
+    {
+        // the division only where some lane's ray.z is outside the exact
+        // range (a wave-uniform branch, so the common case skips it)
+        const bool odd = !ms_rcp_nr_exact(e.ray.z);
+        if (__builtin_amdgcn_ballot_w64(odd)) {
+            float z = e.ray.z;
+            asm volatile("" : "+v"(z));  // keeps the division inside the branch
+            if (odd) e.inv_z = 1.0f / z;
+        }
+    }
     e.u = e.ray.x * e.inv_z;
     e.v = e.ray.y * e.inv_z;
     e.rho3d = __builtin_fmaf(e.u, e.u, e.v * e.v);
-    const float dxs = q2.y - px, dys = q2.z - py;
     e.rho2d = FILTER_INV_SQ * __builtin_fmaf(dxs, dxs, dys * dys);
     const float rho = __builtin_fminf(e.rho3d, e.rho2d);
-    e.depth = __builtin_fmaf(e.u, Twx, __builtin_fmaf(e.v, Twy, Twz));
+    e.depth = __builtin_fmaf(e.u, p3.x, __builtin_fmaf(e.v, p3.y, p3.z));
     // The reference's power > 0 rejection (msplat_metal.metal:676-677) never
     // fires: rho is a minimum of sums of squares (>= 0, +inf or NaN), so
     // power = -rho / 2 is <= 0, -inf or NaN.
     e.G = ms_gauss(rho);
-    e.alpha = __builtin_fminf(0.99f, q2.w * e.G);
+    e.alpha = __builtin_fminf(0.99f, p2.w * e.G);
     return __builtin_amdgcn_ballot_w64(!(e.ray.z == 0.0f)) & __builtin_amdgcn_ballot_w64(!(e.depth < NEAR_N)) &
            __builtin_amdgcn_ballot_w64(!(e.alpha < 1.0f / 255.0f));
 }

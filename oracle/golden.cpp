@@ -281,21 +281,57 @@ struct PairEval {
     float u, v, rho3d, rho2d, dxs, dys, depth, G, alpha;
 };
 
-inline bool eval_pair(float px, float py, const float *Tm, const float *xy,
+inline f3 cross3(f3 a, f3 b) {
+    return {a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x};
+}
+
+/* The reference builds k = px Tw - Tu, l = py Tw - Tv and the ray k x l per
+ * pixel (msplat_metal.metal:655-658).  The same ray expanded about the splat
+ * centre (xs, ys): ray = R0 + (xs - px) nAx + (ys - py) nAy with
+ * kc = xs Tw - Tu, lc = ys Tw - Tv, R0 = kc x lc, nAx = lc x Tw,
+ * nAy = Tw x kc (the (px - xs)(py - ys) term is Tw x Tw = 0).  Exact in real
+ * arithmetic, every term at the splat's own scale; C = (R0, nAx, nAy) once
+ * per splat, by the kernels' operations (centred_rows). */
+inline void centred_rows(const float *Tm, const float *xy, float *C) {
+    const f3 Tu = {Tm[0], Tm[1], Tm[2]}, Tv = {Tm[3], Tm[4], Tm[5]},
+             Tw = {Tm[6], Tm[7], Tm[8]};
+    const float xs = xy[0], ys = xy[1];
+    const f3 kc = {fmaf(xs, Tw.x, -Tu.x), fmaf(xs, Tw.y, -Tu.y), fmaf(xs, Tw.z, -Tu.z)};
+    const f3 lc = {fmaf(ys, Tw.x, -Tv.x), fmaf(ys, Tw.y, -Tv.y), fmaf(ys, Tw.z, -Tv.z)};
+    const f3 R0 = cross3(kc, lc), nAx = cross3(lc, Tw), nAy = cross3(Tw, kc);
+    const float v[9] = {R0.x, R0.y, R0.z, nAx.x, nAx.y, nAx.z, nAy.x, nAy.y, nAy.z};
+    for (int k = 0; k < 9; ++k) C[k] = v[k];
+}
+
+/* centred_rows of every splat a tile list names. */
+static std::vector<float> all_centred_rows(int64_t I, const int32_t *ids, const float *xys,
+                                           const float *transmats) {
+    int32_t n = 0;
+    for (int64_t j = 0; j < I; ++j) n = ids[j] + 1 > n ? ids[j] + 1 : n;
+    std::vector<float> C((size_t)n * 9);
+#pragma omp parallel for schedule(static)
+    for (int32_t g = 0; g < n; ++g) centred_rows(transmats + 9 * (size_t)g, xys + 2 * (size_t)g, C.data() + 9 * (size_t)g);
+    return C;
+}
+
+/* One (pixel, splat) evaluation of nd_rasterize_forward_2dgs_kernel
+ * (msplat_metal.metal:651-683) on the centred ray; k and l (the reference's
+ * per-pixel planes) are kept for the backward's transMat gradients. */
+inline bool eval_pair(float px, float py, const float *C, const float *Tm, const float *xy,
                       float opac, PairEval &e) {
     const f3 Tu = {Tm[0], Tm[1], Tm[2]}, Tv = {Tm[3], Tm[4], Tm[5]},
              Tw = {Tm[6], Tm[7], Tm[8]};
     e.k = {fmaf(px, Tw.x, -Tu.x), fmaf(px, Tw.y, -Tu.y), fmaf(px, Tw.z, -Tu.z)};
     e.l = {fmaf(py, Tw.x, -Tv.x), fmaf(py, Tw.y, -Tv.y), fmaf(py, Tw.z, -Tv.z)};
-    e.ray = {fmaf(e.k.y, e.l.z, -(e.k.z * e.l.y)), fmaf(e.k.z, e.l.x, -(e.k.x * e.l.z)),
-             fmaf(e.k.x, e.l.y, -(e.k.y * e.l.x))};
+    e.dxs = xy[0] - px;
+    e.dys = xy[1] - py;
+    e.ray = {fmaf(e.dxs, C[3], fmaf(e.dys, C[6], C[0])), fmaf(e.dxs, C[4], fmaf(e.dys, C[7], C[1])),
+             fmaf(e.dxs, C[5], fmaf(e.dys, C[8], C[2]))};
     if (e.ray.z == 0.0f) return false;
     const float inv_z = 1.0f / e.ray.z;
     e.u = e.ray.x * inv_z;
     e.v = e.ray.y * inv_z;
     e.rho3d = fmaf(e.u, e.u, e.v * e.v);
-    e.dxs = xy[0] - px;
-    e.dys = xy[1] - py;
     e.rho2d = FILTER_INV_SQ * fmaf(e.dxs, e.dxs, e.dys * e.dys);
     const float rho = fminf(e.rho3d, e.rho2d);
     e.depth = fmaf(e.u, Tw.x, fmaf(e.v, Tw.y, Tw.z));
@@ -610,6 +646,7 @@ extern "C" void orc_raster_fwd(const OrcCamera *cam, const int32_t *tile_offsets
                                int64_t *pairs_evaluated) {
     const int W = cam->width, H = cam->height, TX = cam->tiles_x;
     const float mscale = FAR_N / (FAR_N - NEAR_N);
+    const std::vector<float> crow = all_centred_rows(tile_offsets[TX * cam->tiles_y], ids, xys, transmats);
     int64_t pairs = 0;
 #pragma omp parallel for schedule(dynamic, 4) reduction(+ : pairs)
     for (int py_i = 0; py_i < H; ++py_i) {
@@ -626,7 +663,7 @@ extern "C" void orc_raster_fwd(const OrcCamera *cam, const int32_t *tile_offsets
                 const float *no = normal_opac + 4 * g;
                 const float opac = sigmoid(no[3]);
                 PairEval e;
-                if (!eval_pair(px, py, transmats + 9 * g, xys + 2 * g, opac, e)) continue;
+                if (!eval_pair(px, py, crow.data() + 9 * (size_t)g, transmats + 9 * g, xys + 2 * g, opac, e)) continue;
                 const float next_T = T * (1.0f - e.alpha);
                 if (next_T <= 1e-4f) break;
                 const float w = e.alpha * T;
@@ -766,6 +803,7 @@ extern "C" void orc_raster_bwd(const OrcCamera *cam, int n, const int32_t *tile_
     const int64_t I = tile_offsets[T_tiles];
     std::vector<double> acc((size_t)I * 16, 0.0);
     const float mscale = FAR_N / (FAR_N - NEAR_N);
+    const std::vector<float> crow = all_centred_rows(I, ids, xys, transmats);
 
 #pragma omp parallel for schedule(dynamic, 1)
     for (int tile = 0; tile < T_tiles; ++tile) {
@@ -808,7 +846,7 @@ extern "C" void orc_raster_bwd(const OrcCamera *cam, int n, const int32_t *tile_
                     const float opa = sigmoid(no[3]);
                     const float *Tm = transmats + 9 * g;
                     PairEval e;
-                    if (!eval_pair(px, py, Tm, xys + 2 * g, opa, e)) continue;
+                    if (!eval_pair(px, py, crow.data() + 9 * (size_t)g, Tm, xys + 2 * g, opa, e)) continue;
                     const float alpha = e.alpha, G = e.G;
                     T = T / (1.0f - alpha);
                     const float dchannel_dcolor = alpha * T;

@@ -109,6 +109,17 @@ def test_raster_forward_bitexact(name, orc, eng):
         _assert_bitexact(out[k], fwd[k], k)
 
 
+def test_fast_reciprocal_is_the_division(eng):
+    """The rasterizer's 1 / ray.z (hardware reciprocal + one Newton step)
+    equals the correctly rounded division, the golden model's, for every
+    normal float of magnitude below 2^126 (exponent fields 1..252, both
+    signs, all 2^23 mantissas: 4.2e9 floats).  Above, 1 / x is subnormal and
+    the rasterizer takes the division itself."""
+    bad = C.c_int64(-1)
+    E.check(E.lib().msplat_hip_check_fast_rcp(1, 252, C.byref(bad)))
+    assert bad.value == 0
+
+
 def test_overflow_tiles_merge_path(orc, eng):
     """Tiles far above 2048 intersections: the chunked LDS sort + global
     merge must give the oracle's full (untruncated) per-tile order."""
