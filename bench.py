@@ -171,7 +171,7 @@ def main() -> int:
                          "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
     dominant = max(kernels, key=lambda k: kernels[k]["ms"])
     dk = kernels[dominant]
-    for key in ("pairs_evaluated", "pairs_blended", "log_entries"):
+    for key in ("pairs_evaluated", "pairs_blended", "log_entries", "visits", "visit_slots"):
         kernels["raster_fwd"][key] = int(np.mean([c[key] for c in pairs]))
 
     result = {

@@ -275,9 +275,11 @@ int64_t msplat_hip_last_pairs_evaluated(void);
 /* Counters of the same forward: out[0] = (pixel, gaussian) pairs evaluated,
  * out[1] = blend-log entries (visits of a wave in which at least one pixel
  * blended the gaussian; 0 for a forward without the log), out[2] =
- * (pixel, gaussian) pairs blended.  No counterpart in the reference: it
- * measures the rasterizers' work. */
-int msplat_hip_last_raster_counts(int64_t out[3]);
+ * (pixel, gaussian) pairs blended, out[3] = (wave, gaussian) visits,
+ * out[4] = visit slots (per 256-entry batch, four times the largest wave's
+ * visit count: the visits the batch's barriers allow for).  No counterpart
+ * in the reference: it measures the rasterizers' work. */
+int msplat_hip_last_raster_counts(int64_t out[5]);
 /* Self-check of the rasterizer's arithmetic: *mismatches receives the
  * number of floats with exponent field efield_lo..efield_hi (1..254, both
  * signs, every mantissa) where the fast reciprocal it uses for 1 / ray.z

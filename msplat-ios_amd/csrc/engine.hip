@@ -69,7 +69,7 @@ struct Engine {
     hipEvent_t ev[ST_COUNT + 1] = {};
     float stage_ms[ST_COUNT] = {};
     bool stage_valid[ST_COUNT] = {};
-    int64_t pairs[3] = {0, 0, 0};  // evaluated, log entries, blended
+    int64_t pairs[5] = {0, 0, 0, 0, 0};  // evaluated, log entries, blended, visits, visit slots
 };
 
 Engine g_eng;
@@ -281,7 +281,7 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     CHECK(ensure(E.out_alpha, Pn * 4));
     CHECK(ensure(E.out_median, Pn * 4));
     CHECK(ensure(E.out_dist, Pn * 4));
-    CHECK(ensure(E.pair_counter, 24));
+    CHECK(ensure(E.pair_counter, 40));
     E.n = N;
     E.W = W;
     E.H = H;
@@ -299,7 +299,7 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     stage_mark(ST_PROJECT);
     HIPC(hipMemsetAsync(E.stats.p, 0, 64, s));
     HIPC(hipMemsetAsync(E.super_counts.p, 0, (size_t)NS * 4, s));
-    if (E.count_pairs) HIPC(hipMemsetAsync(E.pair_counter.p, 0, 24, s));
+    if (E.count_pairs) HIPC(hipMemsetAsync(E.pair_counter.p, 0, 40, s));
     mskern::launch_project_fwd(s, *cam, *g, P<float>(E.rec), P<float>(E.depths), P<int>(E.radii),
                                P<uint32_t>(E.rect), reinterpret_cast<unsigned long long *>(P<int>(E.stats) + 8),
                                nullptr);
@@ -565,7 +565,7 @@ int msplat_hip_render(const MsplatCamera *cam, const MsplatGaussians *g, const f
     ENSURE_INIT();
     CHECK(forward_locked(cam, g, bg, nisect, false, false));
     stage_mark(ST_LOSS);
-    if (g_eng.count_pairs) HIPC(hipMemcpy(g_eng.pairs, g_eng.pair_counter.p, 24, hipMemcpyDeviceToHost));
+    if (g_eng.count_pairs) HIPC(hipMemcpy(g_eng.pairs, g_eng.pair_counter.p, 40, hipMemcpyDeviceToHost));
     if (g_eng.timing) {
         HIPC(hipStreamSynchronize(g_eng.stream));
         for (int i = ST_PROJECT; i < ST_LOSS; ++i) {
@@ -630,7 +630,7 @@ int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g, con
     HIPC(hipGetLastError());
     HIPC(hipStreamSynchronize(s));
     if (loss_host) *loss_host = (float)E.pinned_d[0];
-    if (E.count_pairs) HIPC(hipMemcpy(E.pairs, E.pair_counter.p, 24, hipMemcpyDeviceToHost));
+    if (E.count_pairs) HIPC(hipMemcpy(E.pairs, E.pair_counter.p, 40, hipMemcpyDeviceToHost));
     if (E.timing) {
         for (int i = 0; i < ST_COUNT; ++i) {
             HIPC(hipEventElapsedTime(&E.stage_ms[i], E.ev[i], E.ev[i + 1]));
@@ -839,10 +839,10 @@ int msplat_hip_stage_times(const char **names, float *ms, int max) {
 
 int64_t msplat_hip_last_pairs_evaluated(void) { return g_eng.pairs[0]; }
 
-int msplat_hip_last_raster_counts(int64_t out[3]) {
+int msplat_hip_last_raster_counts(int64_t out[5]) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (!out) return MSPLAT_E_ARG;
-    for (int i = 0; i < 3; ++i) out[i] = g_eng.pairs[i];
+    for (int i = 0; i < 5; ++i) out[i] = g_eng.pairs[i];
     return MSPLAT_OK;
 }
 

@@ -84,7 +84,7 @@ __device__ __forceinline__ int build_wave_lists(int m, unsigned char (*s_list)[k
 // t_ckpt[4 * start + wave * len + k + lane], as soon as entry k - 1 is
 // logged (so also when the log ends at k entries).
 // COUNT adds the work counters {pairs evaluated, log entries, pairs
-// blended} to pair_counter.
+// blended, (wave, splat) visits, visit slots} to pair_counter.
 // With FULL_OUT = false only what the image-only training step consumes is
 // produced: out_img and final_Ts[.][0] (T); the last and median contributor
 // indices, the depth, normal, alpha, median and distortion outputs and the
@@ -130,14 +130,22 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     __shared__ int s_cnt[4][4];
     // wave totals of the work counters (scalar: ballot popcounts)
     unsigned evals = 0, blends = 0;
+    // COUNT: each wave's visits in the current batch; a batch lasts as long
+    // as its busiest wave (the barriers), so it accounts for 4 x max slots
+    __shared__ int s_vis[4];
+    unsigned visits = 0, slots = 0;
+    if (COUNT && threadIdx.x < 4) s_vis[threadIdx.x] = 0;
     for (int b0 = start; b0 < end; b0 += kThreads) {
         if (__syncthreads_and(done_m == ~0ull)) break;
+        if (COUNT && threadIdx.x == 0)
+            slots += 4u * (unsigned)max(max(s_vis[0], s_vis[1]), max(s_vis[2], s_vis[3]));
         const int idx = b0 + (int)threadIdx.x;
         const int gid = idx < end ? ids[idx] : 0;
         const int m = idx < end ? load_batch<FULL_OUT>(rec, gid, idx - start, s_rec, sx0, sy0) : 0;
         const int n = build_wave_lists(m, s_list, s_cnt);
-        if (done_m == ~0ull) continue;
-        for (int j = 0; j < n; ++j) {
+        int nv = 0;
+        for (int j = 0; j < n && done_m != ~0ull; ++j) {
+            if (COUNT) ++nv;
             const int to = 16 * (int)s_list[wave][j];  // byte offset of the slot in a record plane
             const auto plane = [&](int k) {
                 return *reinterpret_cast<const float4 *>(s_bytes + k * (kThreads * 16) + to);
@@ -188,23 +196,30 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
                 // current one (a visit no lane blends changes nothing)
                 if ((++nlog & 63) == 0) t_ckpt[log_base + nlog + lane] = Tr;
             }
-            if (done_m == ~0ull) break;
+        }
+        if (COUNT) {
+            visits += (unsigned)nv;
+            if (lane == 0) s_vis[wave] = nv;
         }
     }
     if (LOG && lane == 0) wave_cnt[4 * tile + wave] = nlog;
     if (COUNT) {
-        // {pairs evaluated, log entries, pairs blended}
-        __shared__ unsigned int s_cnt3[3];
+        // {pairs evaluated, log entries, pairs blended, visits, visit slots}
+        __shared__ unsigned int s_cnt5[5];
         __syncthreads();
-        if (threadIdx.x < 3) s_cnt3[threadIdx.x] = 0;
+        if (threadIdx.x == 0)
+            slots += 4u * (unsigned)max(max(s_vis[0], s_vis[1]), max(s_vis[2], s_vis[3]));
+        if (threadIdx.x < 5) s_cnt5[threadIdx.x] = 0;
         __syncthreads();
         if (lane == 0) {
-            atomicAdd(&s_cnt3[0], evals);
-            atomicAdd(&s_cnt3[2], blends);
-            atomicAdd(&s_cnt3[1], (unsigned)nlog);
+            atomicAdd(&s_cnt5[0], evals);
+            atomicAdd(&s_cnt5[2], blends);
+            atomicAdd(&s_cnt5[1], (unsigned)nlog);
+            atomicAdd(&s_cnt5[3], visits);
         }
+        if (threadIdx.x == 0) atomicAdd(&s_cnt5[4], slots);
         __syncthreads();
-        if (threadIdx.x < 3) atomicAdd(pair_counter + threadIdx.x, (unsigned long long)s_cnt3[threadIdx.x]);
+        if (threadIdx.x < 5) atomicAdd(pair_counter + threadIdx.x, (unsigned long long)s_cnt5[threadIdx.x]);
     }
     if (!inside) return;
     const size_t pix = (size_t)pyi * W + pxi;

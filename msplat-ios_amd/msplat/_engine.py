@@ -251,6 +251,7 @@ def pairs_evaluated() -> int:
 
 def raster_counts() -> dict:
     """Counters of the most recent forward with the pair counter on."""
-    out = (C.c_int64 * 3)()
+    out = (C.c_int64 * 5)()
     check(lib().msplat_hip_last_raster_counts(C.cast(out, C.c_void_p)))
-    return {"pairs_evaluated": int(out[0]), "log_entries": int(out[1]), "pairs_blended": int(out[2])}
+    return {"pairs_evaluated": int(out[0]), "log_entries": int(out[1]), "pairs_blended": int(out[2]),
+            "visits": int(out[3]), "visit_slots": int(out[4])}
