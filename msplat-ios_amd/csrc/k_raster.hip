@@ -39,7 +39,7 @@ __device__ __forceinline__ int load_batch(const float4 *__restrict__ rec, int gi
     s_rec[3 * kThreads + threadIdx.x] = make_float4(Tw.x, Tw.y, Tw.z, __int_as_float(pos));
     s_rec[4 * kThreads + threadIdx.x] = make_float4(q3.w, q4.x, q4.y, __int_as_float(gid));
     if (NORMAL) s_rec[5 * kThreads + threadIdx.x] = make_float4(q3.x, q3.y, q3.z, 0.f);
-    return strip_mask_fine(q0, q1, q2, q4.z, sx0, sy0);
+    return strip_mask_fine(q0, q1, q2, q4.z, R0, nAx, nAy, sx0, sy0);
 }
 
 // Per-wave slot lists of one batch: s_list[w][0..n_w) holds, in ascending

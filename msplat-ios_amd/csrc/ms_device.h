@@ -444,26 +444,24 @@ __host__ __device__ __forceinline__ float parabola_min(float c, float p, float r
 
 // Wave-block mask refined by an exact region test.  Bit w is set when a
 // pixel centre of wave w's block may reach alpha >= 1/255, i.e.
-// u^2+v^2 <= tau or rho2d <= tau.  The ray of pixel p is
-//   ray(p) = px (Tv x Tw) + py (Tw x Tu) + Tu x Tv       (= k x l),
-// linear in p, so u^2+v^2 <= tau is the quadratic region
-//   g(p) = ray.x^2 + ray.y^2 - tau ray.z^2 <= 0,
+// u^2+v^2 <= tau or rho2d <= tau.  On the centred rows (centred_rows) the
+// ray of pixel p is, with delta = p - (xs, ys),
+//   ray = R0 - delta.x nAx - delta.y nAy,
+// linear in delta, so u^2+v^2 <= tau is the quadratic region
+//   g(delta) = ray.x^2 + ray.y^2 - tau ray.z^2 <= 0,
 // an ellipse when g's quadratic part is positive definite.  For such
 // splats the block rectangle (grown by half a pixel) is tested against the
 // ellipse of a 1% larger tau by minimising the convex g over the rectangle
 // (interior vertex or the four edges), and against the low-pass disc.
+// Every coefficient is at the splat's own scale (the ray written about the
+// image origin cancels catastrophically for thin splats far from it).
 // Ill-conditioned or unbounded cases keep the box mask.  Every test is
 // conservative, so masked-out splats are exactly those eval_pair rejects.
 __host__ __device__ __forceinline__ int strip_mask_fine(const float4 &q0, const float4 &q1, const float4 &q2,
-                                                        float tau, float sx0, float sy0) {
+                                                        float tau, f3 R0, f3 nAx, f3 nAy, float sx0, float sy0) {
     const int mbox = strip_mask(splat_box(q0, q1, q2, tau), sx0, sy0);
     if (mbox == 0) return 0;
-    const f3 Tu = {q0.x, q0.y, q0.z}, Tv = {q0.w, q1.x, q1.y}, Tw = {q1.z, q1.w, q2.x};
-    const f3 c0 = {Tv.y * Tw.z - Tv.z * Tw.y, Tv.z * Tw.x - Tv.x * Tw.z, Tv.x * Tw.y - Tv.y * Tw.x};
-    const f3 c1 = {Tw.y * Tu.z - Tw.z * Tu.y, Tw.z * Tu.x - Tw.x * Tu.z, Tw.x * Tu.y - Tw.y * Tu.x};
-    const f3 c2 = {Tu.y * Tv.z - Tu.z * Tv.y, Tu.z * Tv.x - Tu.x * Tv.z, Tu.x * Tv.y - Tu.y * Tv.x};
-    // coordinates relative to the tile's first pixel centre
-    const f3 r0 = {sx0 * c0.x + sy0 * c1.x + c2.x, sx0 * c0.y + sy0 * c1.y + c2.y, sx0 * c0.z + sy0 * c1.z + c2.z};
+    const f3 c0 = {-nAx.x, -nAx.y, -nAx.z}, c1 = {-nAy.x, -nAy.y, -nAy.z}, r0 = R0;
     const float tt = tau * 1.01f;
     const float a = c0.x * c0.x + c0.y * c0.y - tt * c0.z * c0.z;
     const float b = c0.x * c1.x + c0.y * c1.y - tt * c0.z * c1.z;
@@ -473,23 +471,26 @@ __host__ __device__ __forceinline__ int strip_mask_fine(const float4 &q0, const 
     const float f = r0.x * r0.x + r0.y * r0.y - tt * r0.z * r0.z;
     const float det = a * c - b * b;
     if (!(a > 0.0f && c > 0.0f && det > 1e-3f * (a * c))) return mbox;
+    // the tile's first pixel centre relative to the splat centre
+    const float ox = sx0 - q2.y, oy = sy0 - q2.z;
     // rounding allowance: 1e-5 of the largest term magnitude over the tile
     const float st = __builtin_sqrtf(tt);
+    const float ex = __builtin_fmaxf(__builtin_fabsf(ox - 0.5f), __builtin_fabsf(ox + 15.5f));
+    const float ey = __builtin_fmaxf(__builtin_fabsf(oy - 0.5f), __builtin_fabsf(oy + 15.5f));
     const float M = __builtin_fabsf(r0.x) + __builtin_fabsf(r0.y) + st * __builtin_fabsf(r0.z) +
-                    16.0f * (__builtin_fabsf(c0.x) + __builtin_fabsf(c0.y) + st * __builtin_fabsf(c0.z) +
-                             __builtin_fabsf(c1.x) + __builtin_fabsf(c1.y) + st * __builtin_fabsf(c1.z));
+                    ex * (__builtin_fabsf(c0.x) + __builtin_fabsf(c0.y) + st * __builtin_fabsf(c0.z)) +
+                    ey * (__builtin_fabsf(c1.x) + __builtin_fabsf(c1.y) + st * __builtin_fabsf(c1.z));
     const float tol = 1e-5f * M * M;
     const float inv_det = 1.0f / det;
     const float xs = (b * e - c * d) * inv_det, ys = (b * d - a * e) * inv_det;
     const float gmin = f + d * xs + e * ys;  // g at the ellipse centre
     const float inv_a = 1.0f / a, inv_c = 1.0f / c;
     const float lp_r2 = 0.5f * tt + 1e-3f;
-    const float dcx = q2.y - sx0, dcy = q2.z - sy0;
     int m = 0;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
         if (!((mbox >> w) & 1)) continue;
-        const float X0 = wave_x0(w) - 0.5f, X1 = X0 + kWaveW, Y0 = wave_y0(w) - 0.5f, Y1 = Y0 + kWaveH;
+        const float X0 = ox + (wave_x0(w) - 0.5f), X1 = X0 + kWaveW, Y0 = oy + (wave_y0(w) - 0.5f), Y1 = Y0 + kWaveH;
         bool hit = false;
         if (gmin <= tol) {
             if (xs >= X0 && xs <= X1 && ys >= Y0 && ys <= Y1) {
@@ -509,8 +510,9 @@ __host__ __device__ __forceinline__ int strip_mask_fine(const float4 &q0, const 
             }
         }
         if (!hit) {
-            const float ddx = dcx - __builtin_fminf(__builtin_fmaxf(dcx, X0), X1);
-            const float ddy = dcy - __builtin_fminf(__builtin_fmaxf(dcy, Y0), Y1);
+            // the low-pass disc is centred on the splat centre, delta = 0
+            const float ddx = __builtin_fminf(__builtin_fmaxf(0.0f, X0), X1);
+            const float ddy = __builtin_fminf(__builtin_fmaxf(0.0f, Y0), Y1);
             hit = ddx * ddx + ddy * ddy <= lp_r2;
         }
         if (hit) m |= 1 << w;
