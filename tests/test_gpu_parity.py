@@ -19,6 +19,7 @@ pytestmark = pytest.mark.gpu
 from msplat import _engine as E  # noqa: E402
 from msplat import device as D  # noqa: E402
 from msplat import synthetic as S  # noqa: E402
+from scenes import adversarial  # noqa: E402
 
 
 def _cams(scene, idx, orc):
@@ -59,6 +60,8 @@ def _forward_both(scene, cam_idx, orc, eng, dtu=None):
 SCENES = {
     "fwd16k": lambda: S.make_scene(1),
     "blob40k_sh3": lambda: S.make_scene(2, n=40_000, width=320, height=208, num_cameras=4),
+    # edge-on, needle-thin, huge, near-camera and off-screen splats
+    "adversarial": lambda: adversarial(3000, 21, width=200, height=136),
 }
 
 
