@@ -163,6 +163,35 @@ __device__ __forceinline__ void adam_elem(float *p, float *m_, float *v_, size_t
     v_[idx] = v;
 }
 
+// Adam on the N consecutive elements of one splat's row: all loads first,
+// then the updates (adam_elem's operations, element by element), then all
+// stores, so the row moves as vector loads and stores.
+template <int N>
+__device__ __forceinline__ void adam_row(float *p, float *m_, float *v_, size_t base, const float *g, float step,
+                                         float b1, float b2, float bc2_sqrt, float eps) {
+    float pv[N], mv[N], vv[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) pv[k] = p[base + k];
+#pragma unroll
+    for (int k = 0; k < N; ++k) mv[k] = m_[base + k];
+#pragma unroll
+    for (int k = 0; k < N; ++k) vv[k] = v_[base + k];
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const float m = __builtin_fmaf(b1, mv[k], (1.0f - b1) * g[k]);
+        const float v = __builtin_fmaf(b2, vv[k], (1.0f - b2) * g[k] * g[k]);
+        pv[k] -= step * m / (__builtin_sqrtf(v) / bc2_sqrt + eps);
+        mv[k] = m;
+        vv[k] = v;
+    }
+#pragma unroll
+    for (int k = 0; k < N; ++k) p[base + k] = pv[k];
+#pragma unroll
+    for (int k = 0; k < N; ++k) m_[base + k] = mv[k];
+#pragma unroll
+    for (int k = 0; k < N; ++k) v_[base + k] = vv[k];
+}
+
 struct AdamDev {
     float *m[6];
     float *v[6];
@@ -240,20 +269,13 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
     float *__restrict__ dmean2d, float *__restrict__ dfdc, float *__restrict__ dfrest,
     float *__restrict__ grad_norm, float *__restrict__ vis, float *__restrict__ max2d, float inv_max_dim,
     AdamDev ad, const float4 *__restrict__ rec) {
-    __shared__ float s_fr[kBlock * 45];
     __shared__ float s_basis[kBlock * 24];
     __shared__ float s_vc[kBlock * 3];
     const int nb = num_sh_bases(cam.degree);
     const int K3 = (nb - 1) * 3;
     const int b0 = blockIdx.x * kBlock;
     const int cnt = min(kBlock, n - b0);
-    const bool staged = K3 <= 45;
     const int sh_deg = cam.degrees_to_use;
-    const bool have_rows = staged && sh_deg > 0;
-    if (have_rows) {
-        stage_rows(s_fr, frest + (size_t)b0 * K3, cnt * K3);
-        __syncthreads();
-    }
     const int i = b0 + threadIdx.x;
     const bool valid = i < n;
     const size_t si = (size_t)(valid ? i : 0);
@@ -328,8 +350,7 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
         for (int c = 0; c < 3; ++c) gdc[c] = SH_C0 * vc[c];
         sh_vjp_basis(sh_deg, dir, basis);
         if (sh_deg >= 1) {
-            const float *fr_row = staged ? s_fr + threadIdx.x * K3 : frest + (size_t)K3 * si;
-            const f3 dd = sh_dL_ddir(sh_deg, dir, fr_row, vc);
+            const f3 dd = sh_dL_ddir(sh_deg, dir, frest + (size_t)K3 * si, vc);
             const f3 dm = dnormvdv(dir_un, dd);
             gm[0] += dm.x;
             gm[1] += dm.y;
@@ -355,15 +376,11 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
             for (int k = 0; k < 2; ++k) dmean2d[2 * si + k] = gm2[k];
             for (int k = 0; k < 3; ++k) dfdc[3 * si + k] = gdc[k];
         } else {
-            for (int k = 0; k < 3; ++k)
-                adam_elem(means, ad.m[0], ad.v[0], 3 * si + k, gm[k], ad.step[0], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
-            for (int k = 0; k < 2; ++k)
-                adam_elem(scales, ad.m[1], ad.v[1], 2 * si + k, gs[k], ad.step[1], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
-            for (int k = 0; k < 4; ++k)
-                adam_elem(quats, ad.m[2], ad.v[2], 4 * si + k, gq[k], ad.step[2], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
-            for (int k = 0; k < 3; ++k)
-                adam_elem(fdc, ad.m[3], ad.v[3], 3 * si + k, gdc[k], ad.step[3], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
-            adam_elem(opac, ad.m[5], ad.v[5], si, gop, ad.step[5], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+            adam_row<3>(means, ad.m[0], ad.v[0], 3 * si, gm, ad.step[0], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+            adam_row<2>(scales, ad.m[1], ad.v[1], 2 * si, gs, ad.step[1], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+            adam_row<4>(quats, ad.m[2], ad.v[2], 4 * si, gq, ad.step[2], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+            adam_row<3>(fdc, ad.m[3], ad.v[3], 3 * si, gdc, ad.step[3], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
+            adam_row<1>(opac, ad.m[5], ad.v[5], si, &gop, ad.step[5], ad.b1, ad.b2, ad.bc2_sqrt, ad.eps);
         }
     }
     if (K3 == 0) return;
@@ -389,7 +406,7 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
             const int b = k / 3, c = k - 3 * b;
             gr[u] = (act && b < nrest) ? s_basis[gl * 24 + b] * s_vc[gl * 3 + c] : 0.f;
             if (FUSED && act) {
-                pv[u] = have_rows ? s_fr[e] : frest[base + e];
+                pv[u] = frest[base + e];
                 mv[u] = ad.m[4][base + e];
                 vv[u] = ad.v[4][base + e];
             }
