@@ -307,6 +307,42 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// wave_reduce16 with its last three steps through LDS: after the two
+// permlane steps each lane holds 4 values (index i + 4 b4 + 8 b5), each a
+// sum over the 4 lanes that share lane bits 0-3; they are written to this
+// wave's 256-float scratch and read back transposed, so lane
+// 16 q + 4 i + k sums the 4 partials of value i from lanes 4 k .. 4 k + 3 of
+// its group q, and two quad DPP adds finish.  Lane l ends with the total of
+// value 8 b5 + 4 b4 + 2 b3 + b2, as wave_reduce16.  The scratch is swizzled
+// (group q of value i at 16-float block (q ^ i) & 3) so both the writes and
+// the 16-byte reads are free of bank conflicts.  wa[i] = this lane's write
+// address for value i, ra = its read address (loop invariants).
+template <bool ZERO3 = false>
+__device__ __forceinline__ float wave_reduce16_lds(float v[16], float *const wa[4], const float4 *ra) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if (ZERO3 && i == 3) continue;
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 8]), false,
+                                                        false);
+        v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 4]), false,
+                                                        false);
+        v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *wa[i] = v[i];
+    wave_lds_sync();
+    const float4 p = *ra;
+    wave_lds_sync();
+    float s = (p.x + p.y) + (p.z + p.w);
+    s += dpp<kDppQuad1032>(s);
+    s += dpp<kDppQuad2301>(s);
+    return s;
+}
+
 // nd_rasterize_backward_2dgs_kernel (msplat_metal.metal:1705-1979) over the
 // forward's blend log, with prefix/suffix transmittance.
 //
@@ -333,6 +369,19 @@ __device__ __forceinline__ void wave_lds_sync() {
 // without opacity (1 - opacity), the colour sums without the clamp mask;
 // finish_image_grads applies them once per splat.
 template <bool FULL>
+struct BwdLds;
+template <>
+struct BwdLds<true> {
+    float4 r[4][7][64];
+    uint4 e[4][64];
+};
+template <>
+struct BwdLds<false> {
+    float4 r[4][4][64];
+    float red[4][256];
+};
+
+template <bool FULL>
 __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     int W, int H, int tiles_x, int T, const int *__restrict__ offsets, const uint4 *__restrict__ blend_log,
     const float *__restrict__ t_ckpt, const int *__restrict__ wave_cnt, const float4 *__restrict__ rec,
@@ -343,9 +392,12 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     const int tile = xcd_tile(blockIdx.x, T);
     if (tile >= T) return;
     constexpr int kWave = 64;
-    // record planes per staged entry: the image-only path stages 4, the full one 7
-    __shared__ float4 s_r[4][FULL ? 7 : 4][kWave];
-    __shared__ uint4 s_e[4][FULL ? kWave : 1];
+    // per wave: the staged entries' record planes (the image-only path
+    // stages 4, the full one 7) and the log entries (full) or the reduction
+    // scratch (image-only, wave_reduce16_lds); 20 KB per workgroup for the
+    // image-only kernel
+    __shared__ BwdLds<FULL> L;
+    auto &s_r = L.r;
     const int lane = threadIdx.x & 63;
     // uniform, so that the log entries of the image-only loop are scalar loads
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -356,6 +408,15 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     const float px = (float)pxi, py = (float)pyi;
     const int start = offsets[tile], len = offsets[tile + 1] - start;
     const int nlog = __builtin_amdgcn_readfirstlane(wave_cnt[4 * tile + wave]);
+    float *red_wa[4];
+    const float4 *red_ra = nullptr;
+    if (!FULL) {
+        const int q = lane >> 4, jj = lane & 15, ri = (lane >> 2) & 3, rk = lane & 3;
+        float *red = reinterpret_cast<float *>(&L) + sizeof(L.r) / sizeof(float) + wave * 256;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red_wa[i] = red + i * 64 + (((q ^ i) & 3) << 4) + jj;
+        red_ra = reinterpret_cast<const float4 *>(red + ri * 64 + (((q ^ ri) & 3) << 4) + 4 * rk);
+    }
     const size_t log_base = 4 * (size_t)start + (size_t)wave * (size_t)len;
     const uint4 *lg = blend_log + log_base;
     const size_t pix = inside ? (size_t)pyi * W + pxi : 0;
@@ -416,7 +477,7 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
             s_r[wave][0][lane] = make_float4(R0.x, R0.y, R0.z, nAx.x);
             s_r[wave][1][lane] = make_float4(nAx.y, nAx.z, nAy.x, nAy.y);
             s_r[wave][2][lane] = make_float4(nAy.z, q2.y, q2.z, q2.w);
-            if (FULL) {
+            if constexpr (FULL) {
                 s_r[wave][3][lane] = q0;
                 s_r[wave][4][lane] = q1;
                 s_r[wave][5][lane] = make_float4(q2.x, q3.w, q4.x, q4.y);
@@ -424,17 +485,21 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
             } else {
                 s_r[wave][3][lane] = make_float4(q3.w, q4.x, q4.y, 0.f);
             }
-            if (FULL) s_e[wave][lane] = e;
+            if constexpr (FULL) L.e[wave][lane] = e;
         }
         wave_lds_sync();
         for (int j = m - 1; j >= 0; --j) {
             // image-only: the entry's address is uniform (scalar load) and
             // its ballot is the lane mask of `has` itself
-            const uint4 e = FULL ? s_e[wave][j] : lg[c0 + j];
+            uint4 e;
+            if constexpr (FULL)
+                e = L.e[wave][j];
+            else
+                e = lg[c0 + j];
             const bool has = FULL ? (((lane < 32 ? e.x : e.y) >> (lane & 31)) & 1u)
                                   : __builtin_amdgcn_inverse_ballot_w64(((uint64_t)e.y << 32) | e.x);
             float v16[16];
-            if (!FULL) {
+            if constexpr (!FULL) {
                 const float4 q0 = s_r[wave][0][j], q1 = s_r[wave][1][j], q2 = s_r[wave][2][j];
                 const float4 q3 = s_r[wave][3][j];
                 const float opa = q2.w;
@@ -582,7 +647,7 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 v16[8] = px * dk.z + py * dl.z + dL_dz;
                 v16[12] = G * dL_dG * (1.0f - opa);
             }
-            const float s = FULL ? wave_reduce16(v16, lane) : wave_reduce16<true>(v16, lane);
+            const float s = FULL ? wave_reduce16(v16, lane) : wave_reduce16_lds<true>(v16, red_wa, red_ra);
             if ((lane & 3) == 0 && s != 0.f) unsafeAtomicAdd(&grads16[(size_t)e.w * 16 + gi], s);
         }
         wave_lds_sync();
