@@ -90,8 +90,11 @@ __device__ __forceinline__ int build_wave_lists(int m, unsigned char (*s_list)[k
 // indices, the depth, normal, alpha, median and distortion outputs and the
 // distortion moments are neither accumulated nor written.  Every
 // decision, and so every produced value, is the same as with FULL_OUT.
+// 7 waves per SIMD: the LDS of the image-only kernel allows 7 workgroups
+// per CU, and at most 72 VGPRs keep all of them resident (the compiler
+// would otherwise use 79 and fit 6).
 template <bool LOG, bool FULL_OUT, bool COUNT>
-__global__ __launch_bounds__(kThreads) void k_raster_fwd(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))) void k_raster_fwd(
     int W, int H, int tiles_x, int T, const int *__restrict__ offsets, const int *__restrict__ ids,
     const float4 *__restrict__ rec, const float *__restrict__ bgp, float *__restrict__ out_img,
     float *__restrict__ final_Ts, int *__restrict__ final_idx, float *__restrict__ out_depth,
