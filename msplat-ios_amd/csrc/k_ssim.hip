@@ -19,7 +19,11 @@
 // of LDS) with register blocking: a horizontal work item produces 4
 // adjacent outputs from 14 staged inputs, a vertical one 4 outputs of a
 // column from 14 rows, each output accumulating its taps in ascending order
-// (the order of the reference's blur kernels).
+// (the order of the reference's blur kernels).  Pass 1 loads the three
+// channels of its region at once (each cache line of the interleaved images
+// is fetched once), and both passes walk the tiles in XCD bands
+// (msd::xcd_tile), so a tile's halo is mostly its neighbours' lines, already
+// in the same L2.
 // HBM traffic per pixel: 24 B in + 36 B out (pass 1), 36 + 24 B in + 12 B
 // out (pass 2), plus the halo re-reads of neighbouring tiles.
 #include "kernels.h"
@@ -67,6 +71,24 @@ __device__ __forceinline__ void stage_load(const float *__restrict__ src, int W,
     }
 }
 
+// All three channels of this thread's kStage pixels of the (RS x RS) region
+// of an interleaved RGB image, one 12-byte load per pixel, so that each
+// cache line of the region is fetched once for the three channel passes.
+__device__ __forceinline__ void stage_load_rgb(const float *__restrict__ src, int W, int H, int x0, int y0,
+                                               float v[3][kStage]) {
+#pragma unroll
+    for (int i = 0; i < kStage; ++i) {
+        const int k = (int)threadIdx.x + i * kThreads;
+        const int ry = k / RS, rx = k - ry * RS;
+        const int sy = y0 - RAD + ry, sx = x0 - RAD + rx;
+        const bool inb = k < RS * RS && sx >= 0 && sx < W && sy >= 0 && sy < H;
+        const float *p = src + (inb ? ((size_t)sy * W + sx) * 3 : 0);
+        v[0][i] = inb ? p[0] : 0.f;
+        v[1][i] = inb ? p[1] : 0.f;
+        v[2][i] = inb ? p[2] : 0.f;
+    }
+}
+
 __device__ __forceinline__ void stage_store(float (*dst)[AST], const float v[kStage]) {
 #pragma unroll
     for (int i = 0; i < kStage; ++i) {
@@ -90,7 +112,9 @@ __device__ __forceinline__ void lds_row14(const float *p, float v[16]) {
     }
 }
 
-__global__ __launch_bounds__(kThreads) void k_ssim_fwd(int W, int H, const float *__restrict__ img,
+// At most 168 VGPRs: the LDS allows 3 workgroups per CU, i.e. 3 waves per
+// SIMD (the compiler would otherwise use 177 and fit 2).
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 4))) void k_ssim_fwd(int W, int H, const float *__restrict__ img,
                                                        const float *__restrict__ gt, const float *__restrict__ dist,
                                                        float lambda_l1, float lambda_dist, float inv_np, float g,
                                                        Window win, float *__restrict__ gm1,
@@ -100,7 +124,10 @@ __global__ __launch_bounds__(kThreads) void k_ssim_fwd(int W, int H, const float
     __shared__ __align__(16) float s_b[RS][AST];
     __shared__ __align__(16) float s_h[5][RS][BST];
     __shared__ double s_red[kThreads / 64];
-    const int x0 = blockIdx.x * TS, y0 = blockIdx.y * TS;
+    const int tiles_x = (W + TS - 1) / TS, T = tiles_x * ((H + TS - 1) / TS);
+    const int tile = msd::xcd_tile(blockIdx.x, T);
+    if (tile >= T) return;
+    const int x0 = (tile % tiles_x) * TS, y0 = (tile / tiles_x) * TS;
     const size_t plane = (size_t)W * H;
     const float C1 = 0.0001f, C2 = 0.0009f;
     // vertical work item of this thread: column vx, output rows 4 vq .. 4 vq + 3
@@ -108,18 +135,15 @@ __global__ __launch_bounds__(kThreads) void k_ssim_fwd(int W, int H, const float
     const int gx = x0 + vx;
     double ssim_acc = 0.0;
     float l1[4] = {0.f, 0.f, 0.f, 0.f};
-    // channel c + 1 is loaded into registers while channel c is computed
-    float na[kStage], nb[kStage];
-    stage_load(img, W, H, x0, y0, 3, 0, na);
-    stage_load(gt, W, H, x0, y0, 3, 0, nb);
+    // the region of both images, all channels, in registers
+    float na[3][kStage], nb[3][kStage];
+    stage_load_rgb(img, W, H, x0, y0, na);
+    stage_load_rgb(gt, W, H, x0, y0, nb);
+#pragma unroll
     for (int c = 0; c < 3; ++c) {
-        stage_store(s_a, na);
-        stage_store(s_b, nb);
+        stage_store(s_a, na[c]);
+        stage_store(s_b, nb[c]);
         __syncthreads();
-        if (c < 2) {
-            stage_load(img, W, H, x0, y0, 3, c + 1, na);
-            stage_load(gt, W, H, x0, y0, 3, c + 1, nb);
-        }
         // horizontal pass of ssim_blur_horiz_kernel (msplat_metal.metal:2847-2873)
         for (int it = threadIdx.x; it < kHItems; it += kThreads) {
             const int ry = it >> 3, xg = (it & 7) * 4;
@@ -208,9 +232,8 @@ __global__ __launch_bounds__(kThreads) void k_ssim_fwd(int W, int H, const float
     const double ts = block_sum_d(ssim_acc, s_red);
     const double tl = block_sum_d(l1_acc, s_red);
     if (threadIdx.x == 0) {
-        const int b = blockIdx.y * gridDim.x + blockIdx.x;
-        partials[2 * b] = ts;
-        partials[2 * b + 1] = tl;
+        partials[2 * tile] = ts;
+        partials[2 * tile + 1] = tl;
     }
 }
 
@@ -223,7 +246,10 @@ __global__ __launch_bounds__(kThreads) void k_ssim_bwd(int W, int H, const float
                                                        Window win, float *__restrict__ dL_dimg) {
     __shared__ __align__(16) float s_g[3][RS][AST];
     __shared__ __align__(16) float s_h[3][RS][BST];
-    const int x0 = blockIdx.x * TS, y0 = blockIdx.y * TS;
+    const int tiles_x = (W + TS - 1) / TS, T = tiles_x * ((H + TS - 1) / TS);
+    const int tile = msd::xcd_tile(blockIdx.x, T);
+    if (tile >= T) return;
+    const int x0 = (tile % tiles_x) * TS, y0 = (tile / tiles_x) * TS;
     const size_t plane = (size_t)W * H;
     const int vx = threadIdx.x & (TS - 1), vq = threadIdx.x >> 5;
     const int gx = x0 + vx;
@@ -360,12 +386,14 @@ void launch_loss_fwd_bwd(hipStream_t s, int W, int H, const float *img, const fl
     const float g = -lambda_dssim * inv_np;
     Window win;
     for (int j = 0; j < 11; ++j) win.w[j] = window[j];
-    const dim3 grid((W + TS - 1) / TS, (H + TS - 1) / TS);
+    // one workgroup per 32x32 tile, the grid padded to a multiple of the 8 XCDs
+    const int T = ssim_num_blocks(W, H);
+    const dim3 grid(((T + 7) / 8) * 8);
     hipLaunchKernelGGL(k_ssim_fwd, grid, dim3(kThreads), 0, s, W, H, img, gt, dist, lambda_l1, lambda_dist, inv_np,
                        g, win, gm1, gs1, gs12, partials);
     hipLaunchKernelGGL(k_ssim_bwd, grid, dim3(kThreads), 0, s, W, H, img, gt, gm1, gs1, gs12, lambda_l1, inv_np,
                        win, dL_dimg);
-    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(1024), 0, s, (int)(grid.x * grid.y), partials, lambda_dssim,
+    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(1024), 0, s, T, partials, lambda_dssim,
                        inv_np, loss_out);
 }
 
