@@ -91,8 +91,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the training step is single-GPU (one camera per step); "
-              "multi-GPU runs are not part of this build (see DESIGN.md, 'How the step would shard').",
-              file=sys.stderr)
+              "multi-GPU runs are not supported.", file=sys.stderr)
         return 2
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)

@@ -38,7 +38,12 @@ extern "C" {
 #define MSPLAT_E_CAPACITY (-5)  /* caller-provided capacity too small   */
 
 #define MSPLAT_TILE 16          /* BLOCK_X / BLOCK_Y, core/include/msplat.hpp:4-5 */
-#define MSPLAT_REC_FLOATS 20    /* per-gaussian splat record, see DESIGN    */
+/* Per-gaussian splat record, 5 x float4: (Tu.xyz, Tv.x), (Tv.yz, Tw.xy),
+ * (Tw.z, x, y, sigmoid(opacity)), (normal.xyz, r), (g, b, tau, lp_r2);
+ * rgb = max(SH + 0.5, 0), tau = the largest rho at which alpha can still
+ * reach 1/255 (-1 if never), lp_r2 = squared radius of its low-pass disc as
+ * the quadrant masks use it. */
+#define MSPLAT_REC_FLOATS 20
 #define MSPLAT_GRAD_FLOATS 16   /* per-gaussian raster-gradient record       */
 
 /* Camera + projection set-up: the arguments of msplat_train_step_2dgs /

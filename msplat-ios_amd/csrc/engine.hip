@@ -36,6 +36,8 @@ struct Engine {
     double *pinned_d = nullptr;
     float window[11];
     // per-gaussian
+    // rec: N splat records (MSPLAT_REC_FLOATS each), followed by their N
+    // quadrant-mask records (msd::MaskRec, 12 floats each; mask_recs())
     DevBuf rec, depths, radii, rect, grads16, colors_raw;
     // per-tile
     DevBuf counts, offsets, stats, big_list, scan_tmp;
@@ -119,6 +121,10 @@ template <typename T>
 T *P(DevBuf &b) {
     return static_cast<T *>(b.p);
 }
+
+// The quadrant-mask records of the current frame's E.n splats, stored after
+// their splat records in E.rec.
+float *mask_recs() { return P<float>(g_eng.rec) + (size_t)g_eng.n * MSPLAT_REC_FLOATS; }
 
 int check_rcp_locked(int lo, int hi, int64_t *bad);
 
@@ -233,7 +239,8 @@ int raster_fwd_locked(bool log, bool full) {
         wc = P<int>(E.wave_cnt);
     }
     mskern::launch_raster_fwd(E.stream, E.W, E.H, E.tiles_x, E.tiles_y, P<int>(E.offsets), P<int>(E.ids),
-                              P<float>(E.rec), E.bg, P<float>(E.out_img), P<float>(E.final_Ts), P<int>(E.final_idx),
+                              P<float>(E.rec), mask_recs(), E.bg, P<float>(E.out_img), P<float>(E.final_Ts),
+                              P<int>(E.final_idx),
                               P<float>(E.out_depth), P<float>(E.out_normal), P<float>(E.out_alpha),
                               P<float>(E.out_median), P<float>(E.out_dist),
                               E.count_pairs ? P<unsigned long long>(E.pair_counter) : nullptr, lg, tc, wc, full);
@@ -255,7 +262,7 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     const int T = cam->tiles_x * cam->tiles_y;
     const size_t Pn = (size_t)W * H;
     const int nb = cam->degree == 0 ? 1 : cam->degree == 1 ? 4 : cam->degree == 2 ? 9 : cam->degree == 3 ? 16 : 25;
-    CHECK(ensure(E.rec, (size_t)N * MSPLAT_REC_FLOATS * 4));
+    CHECK(ensure(E.rec, (size_t)N * (MSPLAT_REC_FLOATS + 12) * 4));
     CHECK(ensure(E.depths, (size_t)N * 4));
     CHECK(ensure(E.radii, (size_t)N * 4));
     CHECK(ensure(E.rect, (size_t)N * 8));
@@ -300,7 +307,7 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     HIPC(hipMemsetAsync(E.stats.p, 0, 64, s));
     HIPC(hipMemsetAsync(E.super_counts.p, 0, (size_t)NS * 4, s));
     if (E.count_pairs) HIPC(hipMemsetAsync(E.pair_counter.p, 0, 40, s));
-    mskern::launch_project_fwd(s, *cam, *g, P<float>(E.rec), P<float>(E.depths), P<int>(E.radii),
+    mskern::launch_project_fwd(s, *cam, *g, P<float>(E.rec), mask_recs(), P<float>(E.depths), P<int>(E.radii),
                                P<uint32_t>(E.rect), reinterpret_cast<unsigned long long *>(P<int>(E.stats) + 8),
                                nullptr);
     stage_mark(ST_SCAN);

@@ -37,7 +37,7 @@ __device__ __forceinline__ void stage_rows(float *__restrict__ dst, const float 
 __global__ __launch_bounds__(kBlock) void k_project_fwd(
     MsplatCamera cam, int n, const float *__restrict__ means, const float *__restrict__ scales,
     const float *__restrict__ quats, const float *__restrict__ opac, const float *__restrict__ fdc,
-    const float *__restrict__ frest, float4 *__restrict__ rec, float *__restrict__ depths,
+    const float *__restrict__ frest, float4 *__restrict__ rec, float4 *__restrict__ mrec, float *__restrict__ depths,
     int *__restrict__ radii, uint2 *__restrict__ rect, unsigned long long *__restrict__ isect_total,
     float *__restrict__ colors_raw) {
     // The block's features_rest rows (up to 256 x 45 floats) are staged in LDS
@@ -127,12 +127,23 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
     radii[i] = (int)radius;
     depths[i] = pz;
     rect[i] = make_uint2((uint32_t)x0 | ((uint32_t)y0 << 16), (uint32_t)x1 | ((uint32_t)y1 << 16));
-    ro[0] = make_float4(T0.x, T0.y, T0.z, T1.x);
-    ro[1] = make_float4(T1.y, T1.z, T2.x, T2.y);
-    ro[2] = make_float4(T2.z, cxp, cyp, opa);
+    const float4 q0 = make_float4(T0.x, T0.y, T0.z, T1.x), q1 = make_float4(T1.y, T1.z, T2.x, T2.y),
+                 q2 = make_float4(T2.z, cxp, cyp, opa);
+    // the splat-only part of the rasterizer's quadrant-mask test
+    const float tau = splat_reach(opa);
+    f3 CR0, CAx, CAy;
+    centred_rows(T0, T1, T2, cxp, cyp, CR0, CAx, CAy);
+    float lp_r2;
+    const MaskRec mr = mask_record(q0, q1, q2, tau, CR0, CAx, CAy, x0, y0, x1, y1, lp_r2);
+    ro[0] = q0;
+    ro[1] = q1;
+    ro[2] = q2;
     ro[3] = make_float4(R2.x, R2.y, R2.z, __builtin_fmaxf(col[0] + 0.5f, 0.0f));
-    ro[4] = make_float4(__builtin_fmaxf(col[1] + 0.5f, 0.0f), __builtin_fmaxf(col[2] + 0.5f, 0.0f),
-                        splat_reach(opa), 0.f);
+    ro[4] = make_float4(__builtin_fmaxf(col[1] + 0.5f, 0.0f), __builtin_fmaxf(col[2] + 0.5f, 0.0f), tau, lp_r2);
+    float4 *mo = mrec + 3 * (size_t)i;
+    mo[0] = mr.box;
+    mo[1] = mr.e;
+    mo[2] = mr.h;
     if (colors_raw) {
         colors_raw[3 * (size_t)i] = col[0];
         colors_raw[3 * (size_t)i + 1] = col[1];
@@ -480,13 +491,13 @@ inline unsigned blocks_for(int64_t n, int b) { return (unsigned)((n + b - 1) / b
 namespace mskern {
 
 void launch_project_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, float *rec,
-                        float *depths, int *radii, uint32_t *rect, unsigned long long *isect_total,
+                        float *mrec, float *depths, int *radii, uint32_t *rect, unsigned long long *isect_total,
                         float *colors_raw) {
     if (g.num_points <= 0) return;
     hipLaunchKernelGGL(k_project_fwd, dim3(blocks_for(g.num_points, kBlock)), dim3(kBlock), 0, s, cam,
                        g.num_points, g.means, g.scales, g.quats, g.opacities, g.features_dc, g.features_rest,
-                       reinterpret_cast<float4 *>(rec), depths, radii, reinterpret_cast<uint2 *>(rect),
-                       isect_total, colors_raw);
+                       reinterpret_cast<float4 *>(rec), reinterpret_cast<float4 *>(mrec), depths, radii,
+                       reinterpret_cast<uint2 *>(rect), isect_total, colors_raw);
 }
 
 void launch_project_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, const int *radii,

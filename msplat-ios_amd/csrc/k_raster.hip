@@ -8,7 +8,7 @@
 // free and the per-pixel loop reads a broadcast.  Each wave owns an 8x8
 // quadrant of the tile.  At load time each splat gets a 4-bit mask of the
 // quadrants whose pixel centres its alpha >= 1/255 region can reach
-// (strip_mask_fine), and the batch is compacted into one ascending slot list
+// (quad_mask on the splat's precomputed MaskRec), and the batch is compacted into one ascending slot list
 // per wave, so a wave only visits the splats that can touch its quadrant and
 // every visited splat is a full evaluation.
 #include "kernels.h"
@@ -22,14 +22,18 @@ constexpr int kThreads = 256;
 constexpr float kMScale = FAR_N / (FAR_N - NEAR_N);
 
 // Stages splat gid, list position pos, in LDS slot threadIdx.x and returns
-// its wave-block mask for the tile whose top-left pixel is (sx0, sy0).
-// Planes: 0..2 the centred ray rows, centre and opacity (eval_pair's
-// p0..p2), 3 = (Tw, pos), 4 = (colour, gid), 5 = (normal, 0) when NORMAL.
+// its wave-block mask for the tile whose top-left pixel is (sx0, sy0) (the
+// per-tile part of the quadrant-mask test, quad_mask, on the splat's
+// MaskRec).  Planes: 0..2 the centred ray rows, centre and opacity
+// (eval_pair's p0..p2), 3 = (Tw, pos), 4 = (colour, gid), 5 = (normal, 0)
+// when NORMAL.
 template <bool NORMAL>
-__device__ __forceinline__ int load_batch(const float4 *__restrict__ rec, int gid, int pos, float4 *s_rec,
-                                          float sx0, float sy0) {
+__device__ __forceinline__ int load_batch(const float4 *__restrict__ rec, const float4 *__restrict__ mrec, int gid,
+                                          int pos, float4 *s_rec, float sx0, float sy0) {
     const float4 *r = rec + 5 * (size_t)gid;
     const float4 q0 = r[0], q1 = r[1], q2 = r[2], q3 = r[3], q4 = r[4];
+    const float4 *mr = mrec + 3 * (size_t)gid;
+    const MaskRec m = {mr[0], mr[1], mr[2]};
     const f3 Tw = {q1.z, q1.w, q2.x};
     f3 R0, nAx, nAy;
     centred_rows({q0.x, q0.y, q0.z}, {q0.w, q1.x, q1.y}, Tw, q2.y, q2.z, R0, nAx, nAy);
@@ -39,34 +43,41 @@ __device__ __forceinline__ int load_batch(const float4 *__restrict__ rec, int gi
     s_rec[3 * kThreads + threadIdx.x] = make_float4(Tw.x, Tw.y, Tw.z, __int_as_float(pos));
     s_rec[4 * kThreads + threadIdx.x] = make_float4(q3.w, q4.x, q4.y, __int_as_float(gid));
     if (NORMAL) s_rec[5 * kThreads + threadIdx.x] = make_float4(q3.x, q3.y, q3.z, 0.f);
-    return strip_mask_fine(q0, q1, q2, q4.z, R0, nAx, nAy, sx0, sy0);
+    return quad_mask(m, q4.w, q2.y, q2.z, sx0, sy0);
 }
 
 // Per-wave slot lists of one batch: s_list[w][0..n_w) holds, in ascending
-// order, the slots whose mask m has bit w.
+// order, the slots whose mask m has bit w (this wave's ballot rank after the
+// counts of the waves below it).
 // Returns n for the calling thread's wave.  Called by all threads of the
 // workgroup (two barriers).
-__device__ __forceinline__ int build_wave_lists(int m, unsigned char (*s_list)[kThreads], int (*s_cnt)[4]) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+__device__ __forceinline__ int build_wave_lists(int m, unsigned char (*s_list)[kThreads], int4 *s_cnt) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const unsigned long long below = (1ull << lane) - 1ull;
-    int pos[4];
+    int pos[4], cnt[4];
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
         const unsigned long long bal = __ballot((m >> w) & 1);
         pos[w] = __popcll(bal & below);
-        if (lane == 0) s_cnt[wave][w] = __popcll(bal);
+        cnt[w] = __popcll(bal);
     }
+    if (lane == 0) s_cnt[wave] = make_int4(cnt[0], cnt[1], cnt[2], cnt[3]);
     __syncthreads();
+    // every wave's counts at once (broadcast reads); the slots of block w
+    // from waves below this one precede this wave's
+    const int4 c0 = s_cnt[0], c1 = s_cnt[1], c2 = s_cnt[2], c3 = s_cnt[3];
+    const int4 z = make_int4(0, 0, 0, 0);
+    const int4 p1 = wave > 0 ? c0 : z, p2 = wave > 1 ? c1 : z, p3 = wave > 2 ? c2 : z;
+    const int base[4] = {p1.x + p2.x + p3.x, p1.y + p2.y + p3.y, p1.z + p2.z + p3.z, p1.w + p2.w + p3.w};
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        if ((m >> w) & 1) {
-            int off = pos[w];
-            for (int wv = 0; wv < wave; ++wv) off += s_cnt[wv][w];
-            s_list[w][off] = (unsigned char)threadIdx.x;
-        }
-    }
-    // wave-uniform: keeps the visit loop's control in scalar registers
-    const int n = __builtin_amdgcn_readfirstlane(s_cnt[0][wave] + s_cnt[1][wave] + s_cnt[2][wave] + s_cnt[3][wave]);
+    for (int w = 0; w < 4; ++w)
+        if ((m >> w) & 1) s_list[w][base[w] + pos[w]] = (unsigned char)threadIdx.x;
+    // this wave's list length (wave-uniform: keeps the visit loop's control
+    // in scalar registers)
+    const int4 tot = make_int4(c0.x + c1.x + c2.x + c3.x, c0.y + c1.y + c2.y + c3.y, c0.z + c1.z + c2.z + c3.z,
+                               c0.w + c1.w + c2.w + c3.w);
+    const int n = __builtin_amdgcn_readfirstlane(wave == 0 ? tot.x : wave == 1 ? tot.y : wave == 2 ? tot.z : tot.w);
     __syncthreads();
     return n;
 }
@@ -96,8 +107,8 @@ __device__ __forceinline__ int build_wave_lists(int m, unsigned char (*s_list)[k
 template <bool LOG, bool FULL_OUT, bool COUNT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))) void k_raster_fwd(
     int W, int H, int tiles_x, int T, const int *__restrict__ offsets, const int *__restrict__ ids,
-    const float4 *__restrict__ rec, const float *__restrict__ bgp, float *__restrict__ out_img,
-    float *__restrict__ final_Ts, int *__restrict__ final_idx, float *__restrict__ out_depth,
+    const float4 *__restrict__ rec, const float4 *__restrict__ mrec, const float *__restrict__ bgp,
+    float *__restrict__ out_img, float *__restrict__ final_Ts, int *__restrict__ final_idx, float *__restrict__ out_depth,
     float *__restrict__ out_normal, float *__restrict__ out_alpha, float *__restrict__ out_median,
     float *__restrict__ out_dist, unsigned long long *__restrict__ pair_counter, uint4 *__restrict__ blend_log,
     float *__restrict__ t_ckpt, int *__restrict__ wave_cnt) {
@@ -120,6 +131,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
     const size_t log_base = 4 * (size_t)start + (size_t)wave * (size_t)(end - start);
     uint4 *wave_log = LOG ? blend_log + log_base : nullptr;
     int nlog = 0;  // wave-uniform
+    // the current 64-entry chunk of the wave's log: lane k holds entry k,
+    // and a full chunk is written with one coalesced store
+    uint4 lg_ent = make_uint4(0u, 0u, 0u, 0u);
     const char *s_bytes = reinterpret_cast<const char *>(s_rec);
 
     float Tr = 1.f, cr = 0.f, cg = 0.f, cb = 0.f, dep = 0.f, nx = 0.f, ny = 0.f, nz = 0.f;
@@ -130,7 +144,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
     uint64_t done_m = __builtin_amdgcn_ballot_w64(!inside);
 
     __shared__ unsigned char s_list[4][kThreads];
-    __shared__ int s_cnt[4][4];
+    __shared__ int4 s_cnt[4];  // s_cnt[wave] = the wave's slot counts per block
     // wave totals of the work counters (scalar: ballot popcounts)
     unsigned evals = 0, blends = 0;
     // COUNT: each wave's visits in the current batch; a batch lasts as long
@@ -144,7 +158,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
             slots += 4u * (unsigned)max(max(s_vis[0], s_vis[1]), max(s_vis[2], s_vis[3]));
         const int idx = b0 + (int)threadIdx.x;
         const int gid = idx < end ? ids[idx] : 0;
-        const int m = idx < end ? load_batch<FULL_OUT>(rec, gid, idx - start, s_rec, sx0, sy0) : 0;
+        const int m = idx < end ? load_batch<FULL_OUT>(rec, mrec, gid, idx - start, s_rec, sx0, sy0) : 0;
         const int n = build_wave_lists(m, s_list, s_cnt);
         int nv = 0;
         for (int j = 0; j < n && done_m != ~0ull; ++j) {
@@ -191,13 +205,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
             Tr = blend ? next_T : Tr;
             if (COUNT) blends += __builtin_popcountll(bal);
             if (LOG && bal) {
-                if (lane == 0)
-                    *wave_log = make_uint4((unsigned)bal, (unsigned)(bal >> 32), __float_as_uint(q3.w),
-                                           __float_as_uint(q4.w));
-                ++wave_log;
+                const bool mine = __builtin_amdgcn_inverse_ballot_w64(1ull << (nlog & 63));
+                lg_ent.x = mine ? (unsigned)bal : lg_ent.x;
+                lg_ent.y = mine ? (unsigned)(bal >> 32) : lg_ent.y;
+                lg_ent.z = mine ? __float_as_uint(q3.w) : lg_ent.z;
+                lg_ent.w = mine ? __float_as_uint(q4.w) : lg_ent.w;
                 // the transmittance before the next logged splat is the
                 // current one (a visit no lane blends changes nothing)
-                if ((++nlog & 63) == 0) t_ckpt[log_base + nlog + lane] = Tr;
+                if ((++nlog & 63) == 0) {
+                    wave_log[nlog - 64 + lane] = lg_ent;
+                    t_ckpt[log_base + nlog + lane] = Tr;
+                }
             }
         }
         if (COUNT) {
@@ -205,7 +223,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
             if (lane == 0) s_vis[wave] = nv;
         }
     }
-    if (LOG && lane == 0) wave_cnt[4 * tile + wave] = nlog;
+    if (LOG) {
+        // the last, partial chunk
+        if (lane < (nlog & 63)) wave_log[(nlog & ~63) + lane] = lg_ent;
+        if (lane == 0) wave_cnt[4 * tile + wave] = nlog;
+    }
     if (COUNT) {
         // {pairs evaluated, log entries, pairs blended, visits, visit slots}
         __shared__ unsigned int s_cnt5[5];
@@ -677,7 +699,7 @@ void launch_check_rcp(hipStream_t s, int efield, unsigned long long *bad) {
 }
 
 void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
-                       const float *rec, const float *bg, float *out_img, float *final_Ts, int *final_idx,
+                       const float *rec, const float *mrec, const float *bg, float *out_img, float *final_Ts, int *final_idx,
                        float *out_depth, float *out_normal, float *out_alpha, float *out_median, float *out_dist,
                        unsigned long long *pair_counter, uint32_t *blend_log, float *t_ckpt, int *wave_cnt,
                        bool full_outputs) {
@@ -686,7 +708,8 @@ void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
     auto *lg = reinterpret_cast<uint4 *>(blend_log);
     auto launch = [&](auto kern) {
         hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
-                           reinterpret_cast<const float4 *>(rec), bg, out_img, final_Ts, final_idx, out_depth,
+                           reinterpret_cast<const float4 *>(rec), reinterpret_cast<const float4 *>(mrec), bg,
+                           out_img, final_Ts, final_idx, out_depth,
                            out_normal, out_alpha, out_median, out_dist, pair_counter, lg, t_ckpt, wave_cnt);
     };
     // the work counters are a separate instantiation (profiling only)

@@ -14,8 +14,10 @@ namespace mskern {
 // k_project.hip
 // isect_total (64-bit, zeroed by the caller) receives the number of tile
 // intersections, the sum of the visible splats' tile-rectangle areas.
+// mrec receives the per-splat part of the rasterizer's quadrant-mask test
+// (msd::MaskRec, 12 floats per splat), read by launch_raster_fwd.
 void launch_project_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, float *rec,
-                        float *depths, int *radii, uint32_t *rect, unsigned long long *isect_total,
+                        float *mrec, float *depths, int *radii, uint32_t *rect, unsigned long long *isect_total,
                         float *colors_raw);
 // moments_rec (the forward's splat records) non-null: g16 holds the
 // image-only raster backward's sums (ray moments and unscaled per-splat
@@ -57,7 +59,7 @@ constexpr int kSuperSortChunk = 4096;
 // full_outputs = false produces only out_img, final_Ts[.][0] and
 // final_idx[.][0] (what the image-only training step consumes).
 void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
-                       const float *rec, const float *bg, float *out_img, float *final_Ts, int *final_idx,
+                       const float *rec, const float *mrec, const float *bg, float *out_img, float *final_Ts, int *final_idx,
                        float *out_depth, float *out_normal, float *out_alpha, float *out_median, float *out_dist,
                        unsigned long long *pair_counter, uint32_t *blend_log, float *t_ckpt, int *wave_cnt,
                        bool full_outputs);

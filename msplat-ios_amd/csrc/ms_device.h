@@ -435,34 +435,53 @@ __host__ __device__ __forceinline__ int strip_mask(const float4 &b, float sx0, f
     return m;
 }
 
-// Minimum over y in [y0, y1] of the convex parabola c y^2 + 2 p y + r0
-// (c > 0), written as its value at the clamped vertex.
-__host__ __device__ __forceinline__ float parabola_min(float c, float p, float r0, float y_vertex, float y0, float y1) {
-    const float y = __builtin_fminf(__builtin_fmaxf(y_vertex, y0), y1);
-    return __builtin_fmaf(__builtin_fmaf(c, y, 2.0f * p), y, r0);
-}
-
-// Wave-block mask refined by an exact region test.  Bit w is set when a
-// pixel centre of wave w's block may reach alpha >= 1/255, i.e.
-// u^2+v^2 <= tau or rho2d <= tau.  On the centred rows (centred_rows) the
-// ray of pixel p is, with delta = p - (xs, ys),
+// Quadrant masks.  Bit w of a (tile, splat) mask is set when a pixel centre
+// of wave w's 8x8 block may reach alpha >= 1/255, i.e. u^2+v^2 <= tau or
+// rho2d <= tau.  On the centred rows (centred_rows) the ray of pixel p is,
+// with delta = p - (xs, ys),
 //   ray = R0 - delta.x nAx - delta.y nAy,
 // linear in delta, so u^2+v^2 <= tau is the quadratic region
 //   g(delta) = ray.x^2 + ray.y^2 - tau ray.z^2 <= 0,
-// an ellipse when g's quadratic part is positive definite.  For such
-// splats the block rectangle (grown by half a pixel) is tested against the
-// ellipse of a 1% larger tau by minimising the convex g over the rectangle
-// (interior vertex or the four edges), and against the low-pass disc.
-// Every coefficient is at the splat's own scale (the ray written about the
-// image origin cancels catastrophically for thin splats far from it).
-// Ill-conditioned or unbounded cases keep the box mask.  Every test is
-// conservative, so masked-out splats are exactly those eval_pair rejects.
-__host__ __device__ __forceinline__ int strip_mask_fine(const float4 &q0, const float4 &q1, const float4 &q2,
-                                                        float tau, f3 R0, f3 nAx, f3 nAy, float sx0, float sy0) {
-    const int mbox = strip_mask(splat_box(q0, q1, q2, tau), sx0, sy0);
-    if (mbox == 0) return 0;
-    const f3 c0 = {-nAx.x, -nAx.y, -nAx.z}, c1 = {-nAy.x, -nAy.y, -nAy.z}, r0 = R0;
+//   g = a x^2 + 2 b x y + c y^2 + 2 d x + 2 e y + f,
+// an ellipse when g's quadratic part is positive definite.  A block
+// rectangle (grown by half a pixel) meets a convex region iff the region's
+// centre lies in it or one of its four edges meets the region.  On a
+// vertical line delta.x = X the ellipse {g <= tol} is the chord
+//   |y - (ye - kv (X - xe))| <= sqrt(Av - Bv (X - xe)^2)
+// about its centre (xe, ye), with kv = b / c, Av = (tol - gmin) / c,
+// Bv = det / c^2 (gmin = g(xe, ye), det = a c - b^2), and likewise on a
+// horizontal line with a for c.  Everything that depends on the splat alone
+// is computed once per splat (mask_record, in the projection); per tile the
+// 2x2 blocks share 3 vertical and 3 horizontal lines, so the test is six
+// chords, each compared with two edge segments through squared distances
+// (no root, no division), plus the low-pass disc.  The ellipse is that of
+// a 1% larger tau with a rounding allowance tol = 1e-5 M^2 (M bounds the
+// ray's magnitude over every tile of the splat's rectangle), so every test
+// is conservative: masked-out splats are exactly pairs eval_pair rejects.
+// Ill-conditioned or unbounded regions keep the screen-box mask.
+struct MaskRec {
+    float4 box;  // splat_box (xmin, xmax, ymin, ymax)
+    float4 e;    // (xe, ye, kv, kh): ellipse centre (delta frame), chord slopes
+    float4 h;    // (Av, Bv, Ah, Bh): chord half-width^2 = A - B t^2
+};
+
+// Per-splat part.  q0..q2 are the splat's first three record planes (T
+// rows, centre, opacity), tau its reach, R0 / nAx / nAy its centred rows and
+// [tx0, tx1) x [ty0, ty1) its tile rectangle; lp_r2 receives the squared
+// radius (delta frame) of its low-pass disc, -1 when it can never blend.
+__host__ __device__ __forceinline__ MaskRec mask_record(const float4 &q0, const float4 &q1, const float4 &q2,
+                                                        float tau, f3 R0, f3 nAx, f3 nAy, int tx0, int ty0, int tx1,
+                                                        int ty1, float &lp_r2) {
+    MaskRec m;
+    m.box = splat_box(q0, q1, q2, tau);
+    // no ellipse: every chord empty, centre outside every block
+    m.e = make_float4(1e15f, 1e15f, 0.f, 0.f);
+    m.h = make_float4(-1.f, 0.f, -1.f, 0.f);
+    lp_r2 = -1.f;
+    if (!(tau >= 0.0f)) return m;
     const float tt = tau * 1.01f;
+    lp_r2 = 0.5f * tt + 1e-3f;
+    const f3 c0 = {-nAx.x, -nAx.y, -nAx.z}, c1 = {-nAy.x, -nAy.y, -nAy.z}, r0 = R0;
     const float a = c0.x * c0.x + c0.y * c0.y - tt * c0.z * c0.z;
     const float b = c0.x * c1.x + c0.y * c1.y - tt * c0.z * c1.z;
     const float c = c1.x * c1.x + c1.y * c1.y - tt * c1.z * c1.z;
@@ -470,54 +489,87 @@ __host__ __device__ __forceinline__ int strip_mask_fine(const float4 &q0, const 
     const float e = c1.x * r0.x + c1.y * r0.y - tt * c1.z * r0.z;
     const float f = r0.x * r0.x + r0.y * r0.y - tt * r0.z * r0.z;
     const float det = a * c - b * b;
-    if (!(a > 0.0f && c > 0.0f && det > 1e-3f * (a * c))) return mbox;
-    // the tile's first pixel centre relative to the splat centre
-    const float ox = sx0 - q2.y, oy = sy0 - q2.z;
-    // rounding allowance: 1e-5 of the largest term magnitude over the tile
+    if (!(a > 0.0f && c > 0.0f && det > 1e-3f * (a * c))) {
+        // ill-conditioned: every chord covers every segment (the box decides)
+        m.e = make_float4(0.f, 0.f, 0.f, 0.f);
+        m.h = make_float4(1e30f, 0.f, 1e30f, 0.f);
+        return m;
+    }
+    // largest |delta| over the grown pixel rectangles of every listed tile
+    const float xs = q2.y, ys = q2.z;
+    const float ex = __builtin_fmaxf(__builtin_fabsf((float)(16 * tx0) - 0.5f - xs),
+                                     __builtin_fabsf((float)(16 * tx1) - 0.5f - xs));
+    const float ey = __builtin_fmaxf(__builtin_fabsf((float)(16 * ty0) - 0.5f - ys),
+                                     __builtin_fabsf((float)(16 * ty1) - 0.5f - ys));
     const float st = __builtin_sqrtf(tt);
-    const float ex = __builtin_fmaxf(__builtin_fabsf(ox - 0.5f), __builtin_fabsf(ox + 15.5f));
-    const float ey = __builtin_fmaxf(__builtin_fabsf(oy - 0.5f), __builtin_fabsf(oy + 15.5f));
     const float M = __builtin_fabsf(r0.x) + __builtin_fabsf(r0.y) + st * __builtin_fabsf(r0.z) +
                     ex * (__builtin_fabsf(c0.x) + __builtin_fabsf(c0.y) + st * __builtin_fabsf(c0.z)) +
                     ey * (__builtin_fabsf(c1.x) + __builtin_fabsf(c1.y) + st * __builtin_fabsf(c1.z));
     const float tol = 1e-5f * M * M;
     const float inv_det = 1.0f / det;
-    const float xs = (b * e - c * d) * inv_det, ys = (b * d - a * e) * inv_det;
-    const float gmin = f + d * xs + e * ys;  // g at the ellipse centre
-    const float inv_a = 1.0f / a, inv_c = 1.0f / c;
-    const float lp_r2 = 0.5f * tt + 1e-3f;
-    int m = 0;
+    const float xe = (b * e - c * d) * inv_det, ye = (b * d - a * e) * inv_det;
+    const float gmin = f + d * xe + e * ye;  // g at the ellipse centre
+    if (!(gmin <= tol)) return m;           // empty: the low-pass disc alone
+    const float span = tol - gmin;
+    // chord half-widths^2 with 1e-4 relative and 1e-4 px^2 absolute slack
+    // for the rounding of the per-tile evaluation (and of the reciprocals,
+    // a few ulp)
+    const float ic = 1.0f / c, ia = 1.0f / a;
+    m.e = make_float4(xe, ye, b * ic, b * ia);
+    m.h = make_float4(__builtin_fmaf(span * ic, 1.0001f, 1e-4f), det * ic * ic, __builtin_fmaf(span * ia, 1.0001f, 1e-4f),
+                      det * ia * ia);
+    return m;
+}
+
+// Squared distance from t to the segment [lo, hi].
+__host__ __device__ __forceinline__ float seg_dist2(float t, float lo, float hi) {
+    const float dd = __builtin_fmaxf(__builtin_fmaxf(lo - t, t - hi), 0.0f);
+    return dd * dd;
+}
+
+// Per-(tile, splat) part: the 4-bit mask for the tile whose top-left pixel
+// centre is (sx0, sy0), of the splat centred at (xs, ys).
+__host__ __device__ __forceinline__ int quad_mask(const MaskRec &m, float lp_r2, float xs, float ys, float sx0,
+                                                  float sy0) {
+    const int mbox = strip_mask(m.box, sx0, sy0);
+    if (mbox == 0) return 0;
+    // block edges in the delta frame: x = V[i], y = L[j], i, j = 0..2
+    const float ox = (sx0 - xs) - 0.5f, oy = (sy0 - ys) - 0.5f;
+    const float V[3] = {ox, ox + (float)kWaveW, ox + (float)(2 * kWaveW)};
+    const float L[3] = {oy, oy + (float)kWaveH, oy + (float)(2 * kWaveH)};
+    const float xe = m.e.x, ye = m.e.y;
+    // vh[i][j]: the chord on x = V[i] meets segment [L[j], L[j+1]];
+    // hh[j][i]: the chord on y = L[j] meets segment [V[i], V[i+1]]
+    bool vh[3][2], hh[3][2];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const float dx = V[k] - xe;
+        const float hv2 = __builtin_fmaf(-m.h.y, dx * dx, m.h.x);
+        const float ym = __builtin_fmaf(-m.e.z, dx, ye);
+        vh[k][0] = seg_dist2(ym, L[0], L[1]) <= hv2;
+        vh[k][1] = seg_dist2(ym, L[1], L[2]) <= hv2;
+        const float dy = L[k] - ye;
+        const float hh2 = __builtin_fmaf(-m.h.w, dy * dy, m.h.z);
+        const float xm = __builtin_fmaf(-m.e.w, dy, xe);
+        hh[k][0] = seg_dist2(xm, V[0], V[1]) <= hh2;
+        hh[k][1] = seg_dist2(xm, V[1], V[2]) <= hh2;
+    }
+    // low-pass disc, centred on the splat centre (delta = 0)
+    const float lx0 = __builtin_fminf(__builtin_fmaxf(0.0f, V[0]), V[1]);
+    const float lx1 = __builtin_fminf(__builtin_fmaxf(0.0f, V[1]), V[2]);
+    const float ly0 = __builtin_fminf(__builtin_fmaxf(0.0f, L[0]), L[1]);
+    const float ly1 = __builtin_fminf(__builtin_fmaxf(0.0f, L[1]), L[2]);
+    const float lxs[2] = {lx0 * lx0, lx1 * lx1}, lys[2] = {ly0 * ly0, ly1 * ly1};
+    int msk = 0;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-        if (!((mbox >> w) & 1)) continue;
-        const float X0 = ox + (wave_x0(w) - 0.5f), X1 = X0 + kWaveW, Y0 = oy + (wave_y0(w) - 0.5f), Y1 = Y0 + kWaveH;
-        bool hit = false;
-        if (gmin <= tol) {
-            if (xs >= X0 && xs <= X1 && ys >= Y0 && ys <= Y1) {
-                hit = true;
-            } else {
-                // vertical edges x = X: g = c y^2 + 2 (b X + e) y + (a X^2 + 2 d X + f);
-                // horizontal edges y = Y: g = a x^2 + 2 (b Y + d) x + (c Y^2 + 2 e Y + f)
-                const float pv0 = b * X0 + e, pv1 = b * X1 + e;
-                const float rv0 = (a * X0 + 2.0f * d) * X0 + f, rv1 = (a * X1 + 2.0f * d) * X1 + f;
-                const float ph0 = b * Y0 + d, ph1 = b * Y1 + d;
-                const float rh0 = (c * Y0 + 2.0f * e) * Y0 + f, rh1 = (c * Y1 + 2.0f * e) * Y1 + f;
-                float g = parabola_min(c, pv0, rv0, -pv0 * inv_c, Y0, Y1);
-                g = __builtin_fminf(g, parabola_min(c, pv1, rv1, -pv1 * inv_c, Y0, Y1));
-                g = __builtin_fminf(g, parabola_min(a, ph0, rh0, -ph0 * inv_a, X0, X1));
-                g = __builtin_fminf(g, parabola_min(a, ph1, rh1, -ph1 * inv_a, X0, X1));
-                hit = g <= tol;
-            }
-        }
-        if (!hit) {
-            // the low-pass disc is centred on the splat centre, delta = 0
-            const float ddx = __builtin_fminf(__builtin_fmaxf(0.0f, X0), X1);
-            const float ddy = __builtin_fminf(__builtin_fmaxf(0.0f, Y0), Y1);
-            hit = ddx * ddx + ddy * ddy <= lp_r2;
-        }
-        if (hit) m |= 1 << w;
+        const int i = w & 1, j = w >> 1;
+        const bool centre = xe >= V[i] && xe <= V[i + 1] && ye >= L[j] && ye <= L[j + 1];
+        const bool edge = vh[i][j] || vh[i + 1][j] || hh[j][i] || hh[j + 1][i];
+        const bool lp = lxs[i] + lys[j] <= lp_r2;
+        if (centre || edge || lp) msk |= 1 << w;
     }
-    return m;
+    return msk & mbox;
 }
 
 // Wave-cooperative enumeration of the tile rectangles held by the 64 lanes

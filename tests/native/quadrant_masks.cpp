@@ -1,5 +1,6 @@
 // Test helper (CPU only): checks that the rasterizer's quadrant masks
-// (msd::strip_mask_fine, compiled here for the host from the product header)
+// (msd::mask_record per splat and msd::quad_mask per tile, compiled here for
+// the host from the product header)
 // are conservative.  For every visible splat and every tile its screen box
 // meets, every pixel whose alpha reaches 1/255 in fp64 (with a 1e-4 relative
 // margin, far above the fp32 evaluation's rounding) must lie in a quadrant
@@ -49,18 +50,21 @@ extern "C" int64_t qm_check(int n, const float *transmats, const float *xys, con
         const float4 q2 = make_float4(T[8], xs, ys, opa);
         const float tau = reach(opa) * tau_scale;
         if (tau < 0.0f) continue;
-        const float4 box = splat_box(q0, q1, q2, tau);
         f3 R0, nAx, nAy;
         centred_rows({T[0], T[1], T[2]}, {T[3], T[4], T[5]}, {T[6], T[7], T[8]}, xs, ys, R0, nAx, nAy);
         const int *rc = rect + 4 * (size_t)g;
         const int tx0 = std::max(0, rc[0]), ty0 = std::max(0, rc[1]);
         const int tx1 = std::min(tiles_x, rc[2]) - 1, ty1 = std::min(tiles_y, rc[3]) - 1;
+        // the projection's per-splat part, over the splat's tile rectangle
+        float lp_r2;
+        const MaskRec mr = mask_record(q0, q1, q2, tau, R0, nAx, nAy, tx0, ty0, tx1 + 1, ty1 + 1, lp_r2);
+        const float4 box = mr.box;
         const double Tu[3] = {T[0], T[1], T[2]}, Tv[3] = {T[3], T[4], T[5]}, Tw[3] = {T[6], T[7], T[8]};
         for (int ty = ty0; ty <= ty1; ++ty)
             for (int tx = tx0; tx <= tx1; ++tx) {
                 const float sx0 = (float)(tx * 16), sy0 = (float)(ty * 16);
                 const int mbox = strip_mask(box, sx0, sy0);
-                const int m = strip_mask_fine(q0, q1, q2, tau, R0, nAx, nAy, sx0, sy0);
+                const int m = quad_mask(mr, lp_r2, xs, ys, sx0, sy0);
                 box_tiles += mbox != 0;
                 fine_tiles += m != 0;
                 box_bits += __builtin_popcount(mbox);

@@ -1,7 +1,8 @@
 """The rasterizer's quadrant masks are conservative (CPU).
 
 At load time k_raster_fwd gives each listed splat a 4-bit mask of the 8x8
-pixel quadrants of the tile that it can reach (strip_mask_fine), and a wave
+pixel quadrants of the tile that it can reach (quad_mask on the splat's
+MaskRec, the part the projection computes once per splat), and a wave
 evaluates only the splats whose bit is set.  That must never drop a pair
 the reference would blend: for every (tile, splat) pair the binning
 produces, every pixel whose alpha reaches 1/255 in an fp64 evaluation of
@@ -51,6 +52,7 @@ CASES = {
     # pixel coordinates in the thousands: the regime where the ray written
     # about the image origin cancels
     "adversarial-wide": lambda: _adversarial(1500, 13, width=1297, height=840),
+    "adversarial-c": lambda: _adversarial(2500, 14, width=333, height=250),
 }
 
 
