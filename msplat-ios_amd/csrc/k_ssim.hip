@@ -192,16 +192,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 4))
 #pragma unroll
             for (int o = 0; o < 4; ++o) {
                 const int gy = y0 + 4 * vq + o;
-                if (gx >= W || gy >= H) continue;
+                const bool live = gx < W && gy < H;
                 const float m1 = st[0][o], m2 = st[1][o];
                 const float m1_sq = m1 * m1, m2_sq = m2 * m2, m1m2 = m1 * m2;
                 const float s1_sq = st[2][o] - m1_sq, s2_sq = st[3][o] - m2_sq, s12 = st[4][o] - m1m2;
                 const float A = 2.0f * m1m2 + C1, B = 2.0f * s12 + C2;
                 const float Cd = m1_sq + m2_sq + C1, Dd = s1_sq + s2_sq + C2;
-                const float val = (A * B) / (Cd * Dd);
-                ssim_acc += (double)val;
                 const float CD = Cd * Dd, AB = A * B;
-                const float inv_CD = 1.0f / CD, inv_Cd = 1.0f / Cd, inv_Dd = 1.0f / Dd;
+                // the correctly rounded reciprocals (ms_recip, whole-wave);
+                // the SSIM value itself is AB * (1 / CD), within an ulp of
+                // the quotient (it only enters the loss sum)
+                const float inv_CD = msd::ms_recip(CD), inv_Cd = msd::ms_recip(Cd), inv_Dd = msd::ms_recip(Dd);
+                if (!live) continue;
+                const float val = AB * inv_CD;
+                ssim_acc += (double)val;
                 const float dmu1 = 2.0f * inv_CD * (m2 * B - m1 * AB * inv_Cd);
                 const float ds12 = 2.0f * A * inv_CD;
                 const float ds1 = -AB * inv_CD * inv_Dd;

@@ -365,6 +365,20 @@ __device__ __forceinline__ bool ms_rcp_nr_exact(float x) {
     return a >= 0x1p-126f && a < 0x1p126f;
 }
 
+// The correctly rounded 1 / x for every x: ms_rcp_nr, with the division
+// only where some lane's x is outside its exact range (a wave-uniform
+// branch, so the common case skips it).  Called by the whole wave.
+__device__ __forceinline__ float ms_recip(float x) {
+    float r = ms_rcp_nr(x);
+    const bool odd = !ms_rcp_nr_exact(x);
+    if (__builtin_amdgcn_ballot_w64(odd)) {
+        float z = x;
+        asm volatile("" : "+v"(z));  // keeps the division inside the branch
+        if (odd) r = 1.0f / z;
+    }
+    return r;
+}
+
 // One (pixel, splat) evaluation: the ray-splat intersection, low-pass
 // filter and alpha of nd_rasterize_forward_2dgs_kernel
 // (msplat_metal.metal:651-683), on the centred ray (centred_rows) of the
