@@ -112,8 +112,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
     float *__restrict__ out_normal, float *__restrict__ out_alpha, float *__restrict__ out_median,
     float *__restrict__ out_dist, unsigned long long *__restrict__ pair_counter, uint4 *__restrict__ blend_log,
     float *__restrict__ t_ckpt, int *__restrict__ wave_cnt) {
-    const int tile = xcd_tile(blockIdx.x, T);
-    if (tile >= T) return;
+    const int tile = xcd_strip_tile(blockIdx.x, tiles_x, T / tiles_x);
+    if (tile < 0) return;
     __shared__ float4 s_rec[(FULL_OUT ? 6 : 5) * kThreads];  // the batch's records (load_batch planes)
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int lane = threadIdx.x & 63;
@@ -414,8 +414,8 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     const float *__restrict__ dL_dimg, const float *__restrict__ dL_ddepth, const float *__restrict__ dL_daccum,
     const float *__restrict__ dL_dnormal, const float *__restrict__ dL_dmedian, const float *__restrict__ dL_ddist,
     float ddist_uniform, float *__restrict__ grads16) {
-    const int tile = xcd_tile(blockIdx.x, T);
-    if (tile >= T) return;
+    const int tile = xcd_strip_tile(blockIdx.x, tiles_x, T / tiles_x);
+    if (tile < 0) return;
     constexpr int kWave = 64;
     // per wave: the staged entries' record planes (the image-only path
     // stages 4, the full one 7) and the log entries (full) or the reduction
@@ -704,7 +704,7 @@ void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
                        unsigned long long *pair_counter, uint32_t *blend_log, float *t_ckpt, int *wave_cnt,
                        bool full_outputs) {
     const int T = tiles_x * tiles_y;
-    const int grid = ((T + 7) / 8) * 8;
+    const int grid = xcd_strip_grid(tiles_x, tiles_y);
     auto *lg = reinterpret_cast<uint4 *>(blend_log);
     auto launch = [&](auto kern) {
         hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
@@ -732,7 +732,7 @@ bool launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
                        const float *dL_ddepth, const float *dL_daccum, const float *dL_dnormal,
                        const float *dL_dmedian, const float *dL_ddist, float ddist_uniform, float *grads16) {
     const int T = tiles_x * tiles_y;
-    const int grid = ((T + 7) / 8) * 8;
+    const int grid = xcd_strip_grid(tiles_x, tiles_y);
     const auto *lg = reinterpret_cast<const uint4 *>(blend_log);
     const bool full = dL_ddepth || dL_daccum || dL_dnormal || dL_dmedian || dL_ddist || ddist_uniform != 0.0f;
     if (full)

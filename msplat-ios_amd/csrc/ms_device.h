@@ -628,4 +628,25 @@ __device__ __forceinline__ int xcd_tile(int block, int num_tiles) {
     return (block & 7) * per + (block >> 3);
 }
 
+// XCD bands walked in column strips: XCD x owns tile rows
+// [x * ty / 8, (x + 1) * ty / 8) (split as evenly as integers allow) and
+// takes them in strips kStripW tiles wide, each strip row by row, so the
+// ~200 workgroups an XCD runs at once cover a compact block of tiles whose
+// splats fit its L2, rather than most of one tile row.  Returns the tile of
+// workgroup `block`, or -1 for the padding of a grid of
+// xcd_strip_grid(tx, ty) workgroups.  A bijection onto [0, tx * ty).
+constexpr int kStripW = 8;
+__host__ __device__ __forceinline__ int xcd_strip_grid(int tx, int ty) { return 8 * ((ty + 7) / 8) * tx; }
+__host__ __device__ __forceinline__ int xcd_strip_tile(int block, int tx, int ty) {
+    const int x = block & 7, k = block >> 3;
+    const int base = ty >> 3, extra = ty & 7;
+    const int r0 = x * base + (x < extra ? x : extra), bh = base + (x < extra ? 1 : 0);
+    if (k >= bh * tx) return -1;
+    const int s = k / (kStripW * bh);
+    const int idx = k - s * kStripW * bh;
+    const int c0 = s * kStripW, w = tx - c0 < kStripW ? tx - c0 : kStripW;
+    const int row = idx / w;
+    return (r0 + row) * tx + c0 + (idx - row * w);
+}
+
 }  // namespace msd

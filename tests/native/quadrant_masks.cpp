@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <vector>
 
 #include "ms_device.h"
 
@@ -97,4 +98,21 @@ extern "C" int64_t qm_check(int n, const float *transmats, const float *xys, con
     out[3] = box_bits;
     out[4] = fine_bits;
     return misses;
+}
+
+// The rasterizers' workgroup -> tile order (msd::xcd_strip_tile): the
+// number of tiles of a tx x ty grid that the xcd_strip_grid(tx, ty)
+// workgroups do not cover exactly once (0 for a bijection), or -1 when a
+// workgroup maps outside the grid.
+extern "C" int64_t tile_order_check(int tx, int ty) {
+    const int T = tx * ty, G = xcd_strip_grid(tx, ty);
+    std::vector<int> hits(T, 0);
+    for (int b = 0; b < G; ++b) {
+        const int t = xcd_strip_tile(b, tx, ty);
+        if (t < -1 || t >= T) return -1;
+        if (t >= 0) ++hits[t];
+    }
+    int64_t bad = 0;
+    for (int t = 0; t < T; ++t) bad += hits[t] != 1;
+    return bad;
 }
