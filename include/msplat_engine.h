@@ -293,6 +293,13 @@ int msplat_hip_last_raster_counts(int64_t out[5]);
  * the rasterizer divides outside that range.  msplat_hip_init runs it over
  * [1, 2) and fails on a mismatch.  No counterpart in the reference. */
 int msplat_hip_check_fast_rcp(int efield_lo, int efield_hi, int64_t *mismatches);
+/* Binning self-test hook.  Below 2^24 gaussians the per-super-tile sort keys
+ * carry each gaussian's rectangle inside the super-tile (depth bits << 32 |
+ * id << 8 | rectangle); from 2^24 on they are depth bits << 32 | id and the
+ * rectangle is gathered.  on != 0 forces the wide layout at any size, so the
+ * tests can check it against the golden model on small scenes; the tile
+ * lists are the same either way.  No counterpart in the reference. */
+int msplat_hip_set_wide_keys(int on);
 
 #ifdef __cplusplus
 }

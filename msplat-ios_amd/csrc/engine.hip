@@ -68,6 +68,7 @@ struct Engine {
     // timing
     bool timing = false;       // HIP events per stage
     bool count_pairs = false;  // raster pair counter
+    bool wide_keys = false;    // binning test hook: the wide key layout at any N
     hipEvent_t ev[ST_COUNT + 1] = {};
     float stage_ms[ST_COUNT] = {};
     bool stage_valid[ST_COUNT] = {};
@@ -334,7 +335,7 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
                              P<float>(E.depths), P<int>(E.super_offsets), P<int>(E.super_cursor), super_max,
                              P<uint64_t>(E.keys), P<uint64_t>(E.keys_tmp), P<int>(E.big_list), P<int>(E.stats) + 4,
                              P<int>(E.counts), P<int>(E.offsets), P<int>(E.stats), P<int>(E.scan_tmp),
-                             P<int>(E.ids));
+                             P<int>(E.ids), E.wide_keys);
     stage_mark(ST_RASTER_FWD);
     CHECK(raster_fwd_locked(log, full));
     HIPC(hipGetLastError());
@@ -828,6 +829,14 @@ int msplat_hip_enable_timing(int enable) {
     ENSURE_INIT();
     g_eng.timing = (enable & MSPLAT_TIMING_EVENTS) != 0;
     g_eng.count_pairs = (enable & MSPLAT_TIMING_PAIRS) != 0;
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_set_wide_keys(int on) {
+    API_BEGIN
+    ENSURE_INIT();
+    g_eng.wide_keys = on != 0;
     return MSPLAT_OK;
     API_END
 }

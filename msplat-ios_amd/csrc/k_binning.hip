@@ -146,13 +146,35 @@ constexpr int kHistBins = 16384;  // super-tiles per LDS window (64 KB)
 
 struct SuperRect {
     int sx0, sy0, sw, sh;  // super-tile rectangle, sw * sh pairs (0 if none)
+    uint32_t t0, t1;       // the tile rectangle (x0 | y0 << 16, x1 | y1 << 16)
 };
+
+// Keys of the packed layout (fewer than 2^24 splats):
+// depth bits << 32 | id << 8 | local rectangle, the splat's tile rectangle
+// inside the (sx, sy) super-tile in 8 bits (x0, x1 - 1, y0, y1 - 1 in
+// 0..3).  Ids are unique within a super-tile list, so the order is still
+// (depth, id), and the sort and the emission read the rectangle from the
+// key instead of gathering rect[id].  The wide layout (depth bits << 32 |
+// id) gathers it.
+constexpr int kPackedMaxSplats = 1 << 24;
+__device__ __forceinline__ uint32_t local_rect(uint32_t t0, uint32_t t1, int sx, int sy) {
+    const int stx = sx * kSuper, sty = sy * kSuper;
+    const int rx0 = max((int)(t0 & 0xffff) - stx, 0), rx1 = min((int)(t1 & 0xffff) - stx, kSuper);
+    const int ry0 = max((int)(t0 >> 16) - sty, 0), ry1 = min((int)(t1 >> 16) - sty, kSuper);
+    return (uint32_t)(rx0 | ((rx1 - 1) << 2) | (ry0 << 4) | ((ry1 - 1) << 6));
+}
+// (x0, x1, y0, y1) of a local rectangle, half-open
+__device__ __forceinline__ int4 unpack_rect(uint32_t lr) {
+    return make_int4(lr & 3, ((lr >> 2) & 3) + 1, (lr >> 4) & 3, ((lr >> 6) & 3) + 1);
+}
 
 __device__ __forceinline__ SuperRect super_rect(int i, int n, const int *__restrict__ radii,
                                                 const uint2 *__restrict__ rect) {
-    SuperRect r{0, 0, 1, 0};
+    SuperRect r{0, 0, 1, 0, 0u, 0u};
     if (i < n && radii[i] > 0) {
         const uint2 q = rect[i];
+        r.t0 = q.x;
+        r.t1 = q.y;
         const int x0 = q.x & 0xffff, y0 = q.x >> 16, x1 = q.y & 0xffff, y1 = q.y >> 16;
         if (x1 > x0 && y1 > y0) {
             r.sx0 = x0 / kSuper;
@@ -164,9 +186,10 @@ __device__ __forceinline__ SuperRect super_rect(int i, int n, const int *__restr
     return r;
 }
 
-// fn(bin, splat) for every (splat, super-tile) pair of this workgroup's
-// chunk whose super-tile index lies in [w0, w0 + nbin).
-template <typename F>
+// fn(bin, splat, local rectangle) for every (splat, super-tile) pair of
+// this workgroup's chunk whose super-tile index lies in [w0, w0 + nbin)
+// (the local rectangle only with LR).
+template <bool LR = false, typename F>
 __device__ __forceinline__ void for_pairs(int n, int chunk, int sxn, int w0, int nbin, const int *__restrict__ radii,
                                           const uint2 *__restrict__ rect, F &&fn) {
     const int c0 = blockIdx.x * chunk, c1 = min(n, c0 + chunk);
@@ -176,10 +199,15 @@ __device__ __forceinline__ void for_pairs(int n, int chunk, int sxn, int w0, int
         msd::wave_expand(r.sw * r.sh, [&](int owner, int k, bool active) {
             const int ow = __shfl(r.sw, owner, 64), ox = __shfl(r.sx0, owner, 64), oy = __shfl(r.sy0, owner, 64);
             const int oi = __shfl(i, owner, 64);
+            uint32_t t0 = 0u, t1 = 0u;
+            if constexpr (LR) {
+                t0 = __shfl(r.t0, owner, 64);
+                t1 = __shfl(r.t1, owner, 64);
+            }
             if (active) {
-                const int ry = k / ow;
-                const int bin = (oy + ry) * sxn + ox + (k - ry * ow) - w0;
-                if (bin >= 0 && bin < nbin) fn(bin, oi);
+                const int ry = k / ow, rx = k - ry * ow;
+                const int bin = (oy + ry) * sxn + ox + rx - w0;
+                if (bin >= 0 && bin < nbin) fn(bin, oi, LR ? local_rect(t0, t1, ox + rx, oy + ry) : 0u);
             }
         });
     }
@@ -196,7 +224,7 @@ __global__ __launch_bounds__(kBinThreads) void k_super_hist(int n, int chunk, in
         const int nbin = min(kHistBins, NS - w0);
         for (int k = threadIdx.x; k < nbin; k += kBinThreads) s_h[k] = 0;
         __syncthreads();
-        for_pairs(n, chunk, sxn, w0, nbin, radii, rect, [&](int bin, int) { atomicAdd(&s_h[bin], 1); });
+        for_pairs(n, chunk, sxn, w0, nbin, radii, rect, [&](int bin, int, uint32_t) { atomicAdd(&s_h[bin], 1); });
         __syncthreads();
         for (int k = threadIdx.x; k < nbin; k += kBinThreads)
             if (s_h[k]) atomicAdd(&super_counts[w0 + k], s_h[k]);
@@ -209,6 +237,7 @@ __global__ __launch_bounds__(kBinThreads) void k_super_hist(int n, int chunk, in
 // super-tile from super_cursor (the scanned offsets) with a single global
 // atomic, and places its keys in that range with LDS atomics.  The order
 // inside a super-tile list is arbitrary; k_sort_super orders it.
+template <bool PACKED>
 __global__ __launch_bounds__(kBinThreads) void k_scatter_super(int n, int chunk, int sxn, int NS,
                                                                const int *__restrict__ radii,
                                                                const uint2 *__restrict__ rect,
@@ -220,16 +249,17 @@ __global__ __launch_bounds__(kBinThreads) void k_scatter_super(int n, int chunk,
         const int nbin = min(kHistBins, NS - w0);
         for (int k = threadIdx.x; k < nbin; k += kBinThreads) s_h[k] = 0;
         __syncthreads();
-        for_pairs(n, chunk, sxn, w0, nbin, radii, rect, [&](int bin, int) { atomicAdd(&s_h[bin], 1); });
+        for_pairs(n, chunk, sxn, w0, nbin, radii, rect, [&](int bin, int, uint32_t) { atomicAdd(&s_h[bin], 1); });
         __syncthreads();
         for (int k = threadIdx.x; k < nbin; k += kBinThreads) {
             const int c = s_h[k];
             s_h[k] = c ? atomicAdd(&super_cursor[w0 + k], c) : 0;
         }
         __syncthreads();
-        for_pairs(n, chunk, sxn, w0, nbin, radii, rect, [&](int bin, int gid) {
+        for_pairs<PACKED>(n, chunk, sxn, w0, nbin, radii, rect, [&](int bin, int gid, uint32_t lr) {
             const int pos = atomicAdd(&s_h[bin], 1);
-            keys[pos] = ((unsigned long long)__float_as_uint(depths[gid]) << 32) | (unsigned long long)(uint32_t)gid;
+            const uint32_t lo = PACKED ? ((uint32_t)gid << 8) | lr : (uint32_t)gid;
+            keys[pos] = ((unsigned long long)__float_as_uint(depths[gid]) << 32) | (unsigned long long)lo;
         });
         __syncthreads();
     }
@@ -263,6 +293,7 @@ __device__ void lds_bitonic(unsigned long long *s, const unsigned long long *src
 // tiles of its rectangle inside the super-tile) into tile_counts, then sorts
 // the super-tile list in place; lists longer than kChunk are sorted in
 // kChunk runs and queued on big_list for the merge passes.
+template <bool PACKED>
 __global__ __launch_bounds__(kSortThreads) void k_sort_super(int tiles_x, int tiles_y, int sxn,
                                                              const int *__restrict__ offsets,
                                                              unsigned long long *__restrict__ keys,
@@ -282,9 +313,15 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_super(int tiles_x, int ti
 #pragma unroll
         for (int q = 0; q < kSuper * kSuper; ++q) tc[q] = 0;
         for (int e = threadIdx.x; e < cnt; e += kSortThreads) {
-            const uint2 r = rect[(uint32_t)(keys[start + e] & 0xffffffffull)];
-            const int rx0 = max((int)(r.x & 0xffff) - stx, 0), rx1 = min((int)(r.y & 0xffff) - stx, kSuper);
-            const int ry0 = max((int)(r.x >> 16) - sty, 0), ry1 = min((int)(r.y >> 16) - sty, kSuper);
+            int rx0, rx1, ry0, ry1;
+            if constexpr (PACKED) {
+                const int4 lr = unpack_rect((uint32_t)keys[start + e] & 0xffu);
+                rx0 = lr.x, rx1 = lr.y, ry0 = lr.z, ry1 = lr.w;
+            } else {
+                const uint2 r = rect[(uint32_t)(keys[start + e] & 0xffffffffull)];
+                rx0 = max((int)(r.x & 0xffff) - stx, 0), rx1 = min((int)(r.y & 0xffff) - stx, kSuper);
+                ry0 = max((int)(r.x >> 16) - sty, 0), ry1 = min((int)(r.y >> 16) - sty, kSuper);
+            }
 #pragma unroll
             for (int q = 0; q < kSuper * kSuper; ++q) {
                 const int lx = q % kSuper, ly = q / kSuper;
@@ -373,6 +410,7 @@ constexpr int kWin = 2048;  // super-list entries staged in LDS per window
 // Wave w emits the 4 tiles of row w of the super-tile; within a 64-entry
 // chunk a lane's output slot is the popcount of the covering lanes below it,
 // so each tile list keeps the super-list (depth, id) order.
+template <bool PACKED>
 __global__ __launch_bounds__(256) void k_emit_tiles(int tiles_x, int tiles_y, int sxn,
                                                     const int *__restrict__ soffsets,
                                                     const unsigned long long *__restrict__ skeys,
@@ -397,11 +435,19 @@ __global__ __launch_bounds__(256) void k_emit_tiles(int tiles_x, int tiles_y, in
         const int wn = min(kWin, cnt - w0);
         __syncthreads();
         for (int k = threadIdx.x; k < wn; k += 256) {
-            const int gid = (int)(uint32_t)(skeys[start + w0 + k] & 0xffffffffull);
-            const uint2 r = rect[gid];
-            const int x0 = r.x & 0xffff, y0 = r.x >> 16, x1 = r.y & 0xffff, y1 = r.y >> 16;
-            const int rx0 = max(x0 - stx, 0), rx1 = min(x1 - stx, kSuper);
-            const int ry0 = max(y0 - sty, 0), ry1 = min(y1 - sty, kSuper);
+            const uint32_t lo = (uint32_t)(skeys[start + w0 + k] & 0xffffffffull);
+            int gid, rx0, rx1, ry0, ry1;
+            if constexpr (PACKED) {
+                gid = (int)(lo >> 8);
+                const int4 lr = unpack_rect(lo & 0xffu);
+                rx0 = lr.x, rx1 = lr.y, ry0 = lr.z, ry1 = lr.w;
+            } else {
+                gid = (int)lo;
+                const uint2 r = rect[gid];
+                const int x0 = r.x & 0xffff, y0 = r.x >> 16, x1 = r.y & 0xffff, y1 = r.y >> 16;
+                rx0 = max(x0 - stx, 0), rx1 = min(x1 - stx, kSuper);
+                ry0 = max(y0 - sty, 0), ry1 = min(y1 - sty, kSuper);
+            }
             s_gid[k] = gid;
             s_rr[k] = (unsigned short)(rx0 | (rx1 << 4) | (ry0 << 8) | (ry1 << 12));
         }
@@ -459,7 +505,8 @@ void launch_super_count(hipStream_t s, int n, int tiles_x, int tiles_y, const in
 void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
                       const float *depths, const int *super_offsets, int *super_cursor, int super_max,
                       uint64_t *super_keys, uint64_t *super_keys_tmp, int *big_list, int *super_stats,
-                      int *tile_counts, int *tile_offsets, int *tile_stats, int *tile_temp, int *ids) {
+                      int *tile_counts, int *tile_offsets, int *tile_stats, int *tile_temp, int *ids,
+                      bool force_wide_keys) {
     const int sxn = (tiles_x + kSuper - 1) / kSuper, syn = (tiles_y + kSuper - 1) / kSuper, NS = sxn * syn;
     const int T = tiles_x * tiles_y;
     auto *k = reinterpret_cast<unsigned long long *>(super_keys);
@@ -467,11 +514,12 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
     const uint2 *r2 = reinterpret_cast<const uint2 *>(rect);
     int blocks, chunk;
     bin_chunks(n, &blocks, &chunk);
+    const bool packed = n < kPackedMaxSplats && !force_wide_keys;
     if (n > 0)
-        hipLaunchKernelGGL(k_scatter_super, dim3(blocks), dim3(kBinThreads), 0, s, n, chunk, sxn, NS, radii, r2,
-                           depths, super_cursor, k);
-    hipLaunchKernelGGL(k_sort_super, dim3(NS), dim3(kSortThreads), 0, s, tiles_x, tiles_y, sxn, super_offsets, k,
-                       r2, tile_counts, big_list, super_stats);
+        hipLaunchKernelGGL(packed ? k_scatter_super<true> : k_scatter_super<false>, dim3(blocks), dim3(kBinThreads), 0,
+                           s, n, chunk, sxn, NS, radii, r2, depths, super_cursor, k);
+    hipLaunchKernelGGL(packed ? k_sort_super<true> : k_sort_super<false>, dim3(NS), dim3(kSortThreads), 0, s, tiles_x,
+                       tiles_y, sxn, super_offsets, k, r2, tile_counts, big_list, super_stats);
     unsigned long long *src = k, *dst = kt;
     for (int L = kChunk; L < super_max; L <<= 1) {
         hipLaunchKernelGGL(k_merge_pass, dim3(64, 64), dim3(256), 0, s, L, super_offsets, big_list, super_stats, src,
@@ -483,8 +531,8 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
     if (src != k)
         hipLaunchKernelGGL(k_copy_big, dim3(64, 64), dim3(256), 0, s, super_offsets, big_list, super_stats, src, k);
     launch_scan_counts(s, T, tile_counts, tile_offsets, nullptr, tile_stats, tile_temp);
-    hipLaunchKernelGGL(k_emit_tiles, dim3(NS), dim3(256), 0, s, tiles_x, tiles_y, sxn, super_offsets, k, r2,
-                       tile_offsets, ids);
+    hipLaunchKernelGGL(packed ? k_emit_tiles<true> : k_emit_tiles<false>, dim3(NS), dim3(256), 0, s, tiles_x, tiles_y,
+                       sxn, super_offsets, k, r2, tile_offsets, ids);
 }
 
 }  // namespace mskern

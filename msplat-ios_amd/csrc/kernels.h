@@ -48,7 +48,8 @@ void launch_super_count(hipStream_t s, int n, int tiles_x, int tiles_y, const in
 void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
                       const float *depths, const int *super_offsets, int *super_cursor, int super_max,
                       uint64_t *super_keys, uint64_t *super_keys_tmp, int *big_list, int *super_stats,
-                      int *tile_counts, int *tile_offsets, int *tile_stats, int *tile_temp, int *ids);
+                      int *tile_counts, int *tile_offsets, int *tile_stats, int *tile_temp, int *ids,
+                      bool force_wide_keys);
 constexpr int kSuperTile = 4;
 constexpr int kSuperSortChunk = 4096;
 

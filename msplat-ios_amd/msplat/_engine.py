@@ -62,7 +62,7 @@ EXPORTS = [
     "msplat_hip_render", "msplat_hip_fused_adam", "msplat_hip_densify", "msplat_hip_clamp_max", "msplat_hip_loss_fwd_bwd",
     "msplat_hip_raster_bwd", "msplat_hip_project_bwd", "msplat_hip_project_bwd_adam", "msplat_hip_last", "msplat_hip_enable_timing",
     "msplat_hip_stage_times", "msplat_hip_last_pairs_evaluated", "msplat_hip_last_raster_counts",
-    "msplat_hip_check_fast_rcp",
+    "msplat_hip_check_fast_rcp", "msplat_hip_set_wide_keys",
 ]
 SYNTH_EXPORTS = ["msplat_synth_uniform", "msplat_synth_normal"]
 
@@ -111,6 +111,7 @@ def lib() -> C.CDLL:
         "msplat_hip_last_pairs_evaluated": (I64, []),
         "msplat_hip_last_raster_counts": (I, [P]),
         "msplat_hip_check_fast_rcp": (I, [I, I, C.POINTER(C.c_int64)]),
+        "msplat_hip_set_wide_keys": (I, [I]),
         "msplat_synth_uniform": (None, [C.c_uint64, C.c_uint64, I64, C.c_double, C.c_double, P]),
         "msplat_synth_normal": (None, [C.c_uint64, C.c_uint64, I64, C.c_double, C.c_double, P]),
     }

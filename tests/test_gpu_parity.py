@@ -136,6 +136,25 @@ def test_overflow_tiles_merge_path(orc, eng):
     _assert_bitexact(out["final_idx"], fwd["final_idx"], "final_idx")
 
 
+@pytest.mark.parametrize("name", ["blob40k_sh3", "adversarial"])
+def test_wide_binning_keys_bitexact(name, orc, eng):
+    """The binning's wide key layout (depth bits << 32 | id, the rectangle
+    gathered per key), which scenes of 2^24 gaussians and more use, forced
+    on small scenes: the same tile offsets and per-tile order as the golden
+    model (the default packed layout is checked by every other test)."""
+    scene = SCENES[name]()
+    print(f"[wide keys] scene={name}", flush=True)
+    E.check(E.lib().msplat_hip_set_wide_keys(1))
+    try:
+        ocam, proj, bins, fwd, ds, gcam, out = _forward_both(scene, 0, orc, eng)
+    finally:
+        E.check(E.lib().msplat_hip_set_wide_keys(0))
+    assert out["num_intersections"] == bins["num_intersections"]
+    _assert_bitexact(E.last("tile_offsets"), bins["tile_offsets"], "tile offsets")
+    _assert_bitexact(E.last("gaussian_ids"), bins["ids"], "per-tile sorted ids")
+    _assert_bitexact(out["out_img"], fwd["out_img"], "out_img")
+
+
 def test_empty_scene_renders_background(orc, eng):
     scene = S.make_scene(1, n=64, width=48, height=40)
     scene.means[:] = np.float32(-50.0)  # all behind the camera
