@@ -41,7 +41,7 @@ struct Engine {
     DevBuf rec, depths, radii, rect, grads16, colors_raw;
     // per-tile
     DevBuf counts, offsets, stats, big_list, scan_tmp;
-    DevBuf super_counts, super_offsets, super_cursor, super_tmp;
+    DevBuf super_counts, super_offsets, super_cm, super_tmp;  // super_cm: per-(workgroup, super-tile) offsets
     // per-intersection
     DevBuf keys, keys_tmp, ids;  // keys: per (splat, super-tile) pair
     DevBuf blend_log, t_ckpt, wave_cnt;  // the raster forward's per-wave blend log
@@ -275,7 +275,7 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     const int NS = sxn * syn;
     CHECK(ensure(E.super_counts, (size_t)NS * 4));
     CHECK(ensure(E.super_offsets, (size_t)(NS + 1) * 4));
-    CHECK(ensure(E.super_cursor, (size_t)NS * 4));
+    CHECK(ensure(E.super_cm, (size_t)mskern::kBinMaxBlocks * NS * 4));
     CHECK(ensure(E.super_tmp, (size_t)mskern::tile_scan_temp_ints(NS) * 4));
     // stats (ints): [0..1] tiles: total, largest; [4..6] super-tiles: total,
     // largest, long lists; [8..9] 64-bit intersection count from the projection
@@ -306,14 +306,13 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
 
     stage_mark(ST_PROJECT);
     HIPC(hipMemsetAsync(E.stats.p, 0, 64, s));
-    HIPC(hipMemsetAsync(E.super_counts.p, 0, (size_t)NS * 4, s));
     if (E.count_pairs) HIPC(hipMemsetAsync(E.pair_counter.p, 0, 40, s));
     mskern::launch_project_fwd(s, *cam, *g, P<float>(E.rec), mask_recs(), P<float>(E.depths), P<int>(E.radii),
                                P<uint32_t>(E.rect), reinterpret_cast<unsigned long long *>(P<int>(E.stats) + 8),
                                nullptr);
     stage_mark(ST_SCAN);
     mskern::launch_super_count(s, N, cam->tiles_x, cam->tiles_y, P<int>(E.radii), P<uint32_t>(E.rect),
-                               P<int>(E.super_counts), P<int>(E.super_offsets), P<int>(E.super_cursor),
+                               P<int>(E.super_counts), P<int>(E.super_offsets), P<int>(E.super_cm),
                                P<int>(E.stats) + 4, P<int>(E.super_tmp));
     HIPC(hipMemcpyAsync(E.pinned_i, E.stats.p, 16 * sizeof(int), hipMemcpyDeviceToHost, s));
     HIPC(hipStreamSynchronize(s));
@@ -332,7 +331,7 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     CHECK(ensure(E.ids, (size_t)I * 4));
     if (super_max > mskern::kSuperSortChunk) CHECK(ensure(E.keys_tmp, (size_t)S_total * 8));
     mskern::launch_bin_tiles(s, N, cam->tiles_x, cam->tiles_y, P<int>(E.radii), P<uint32_t>(E.rect),
-                             P<float>(E.depths), P<int>(E.super_offsets), P<int>(E.super_cursor), super_max,
+                             P<float>(E.depths), P<int>(E.super_offsets), P<int>(E.super_cm), super_max,
                              P<uint64_t>(E.keys), P<uint64_t>(E.keys_tmp), P<int>(E.big_list), P<int>(E.stats) + 4,
                              P<int>(E.counts), P<int>(E.offsets), P<int>(E.stats), P<int>(E.scan_tmp),
                              P<int>(E.ids), E.wide_keys);
@@ -463,7 +462,7 @@ void msplat_hip_cleanup(void) {
     Engine &E = g_eng;
     if (!E.ready) return;
     (void)hipStreamSynchronize(E.stream);
-    DevBuf *all[] = {&E.rec, &E.depths, &E.radii, &E.rect, &E.grads16, &E.colors_raw, &E.counts, &E.scan_tmp, &E.super_counts, &E.super_offsets, &E.super_cursor, &E.super_tmp, &E.offsets,
+    DevBuf *all[] = {&E.rec, &E.depths, &E.radii, &E.rect, &E.grads16, &E.colors_raw, &E.counts, &E.scan_tmp, &E.super_counts, &E.super_offsets, &E.super_cm, &E.super_tmp, &E.offsets,
                      &E.stats, &E.big_list, &E.keys, &E.keys_tmp, &E.ids, &E.blend_log, &E.t_ckpt, &E.wave_cnt, &E.selfcheck, &E.out_img, &E.final_Ts,
                      &E.final_idx, &E.out_depth, &E.out_normal, &E.out_alpha, &E.out_median, &E.out_dist,
                      &E.dL_dimg, &E.gm1, &E.gs1, &E.gs12, &E.partials, &E.loss, &E.dmeans, &E.dscales,

@@ -10,12 +10,13 @@
 // collide, so no stage issues one per tile entry:
 //   1. k_super_hist: one workgroup per chunk of several thousand splats
 //      counts its (splat, 4x4-tile super-tile) pairs in an LDS histogram and
-//      adds the non-zero bins to the global super-tile counts; an exclusive
-//      scan gives the super-tile offsets;
-//   2. k_scatter_super: each workgroup recounts its chunk, reserves one
-//      range per super-tile with a single global atomic, and places its
-//      (depth bits << 32 | id) keys with LDS atomics -- about 2.5 keys per
-//      splat instead of one per tile;
+//      writes it as its row of a (workgroup x super-tile) count matrix;
+//      k_super_cols turns each column into the workgroups' offsets inside
+//      the super-tile and its total, and an exclusive scan of the totals
+//      gives the super-tile offsets;
+//   2. k_scatter_super: each workgroup places the keys of its chunk at its
+//      offsets with LDS atomics -- about 2.5 keys per splat instead of one
+//      per tile, with no global atomic and no second count pass;
 //   3. k_sort_super: each super-tile counts the entries of its 16 tiles
 //      (the tile histogram, no atomics: a super-tile owns its tiles) and
 //      sorts its keys in LDS (bitonic, up to 4096 keys), larger lists in
@@ -213,48 +214,68 @@ __device__ __forceinline__ void for_pairs(int n, int chunk, int sxn, int w0, int
     }
 }
 
-// Pair counts per super-tile: the LDS histogram of each window is added to
-// super_counts (zeroed by the caller) with one atomic per non-zero bin.
+// Pair counts per (workgroup, super-tile): the LDS histogram of each window
+// is written as the workgroup's row of the count matrix cm[blocks][NS].
 __global__ __launch_bounds__(kBinThreads) void k_super_hist(int n, int chunk, int sxn, int NS,
                                                             const int *__restrict__ radii,
-                                                            const uint2 *__restrict__ rect,
-                                                            int *__restrict__ super_counts) {
+                                                            const uint2 *__restrict__ rect, int *__restrict__ cm) {
     __shared__ int s_h[kHistBins];
+    int *row = cm + (size_t)blockIdx.x * NS;
     for (int w0 = 0; w0 < NS; w0 += kHistBins) {
         const int nbin = min(kHistBins, NS - w0);
         for (int k = threadIdx.x; k < nbin; k += kBinThreads) s_h[k] = 0;
         __syncthreads();
         for_pairs(n, chunk, sxn, w0, nbin, radii, rect, [&](int bin, int, uint32_t) { atomicAdd(&s_h[bin], 1); });
         __syncthreads();
-        for (int k = threadIdx.x; k < nbin; k += kBinThreads)
-            if (s_h[k]) atomicAdd(&super_counts[w0 + k], s_h[k]);
+        for (int k = threadIdx.x; k < nbin; k += kBinThreads) row[w0 + k] = s_h[k];
         __syncthreads();
     }
 }
 
-// One (depth bits << 32 | id) key per (visible splat, super-tile) pair.  Per
-// window the workgroup recounts its pairs, claims one range per non-zero
-// super-tile from super_cursor (the scanned offsets) with a single global
-// atomic, and places its keys in that range with LDS atomics.  The order
-// inside a super-tile list is arbitrary; k_sort_super orders it.
+// Column pass over the count matrix: super_counts[s] = sum over workgroups
+// of cm[g][s], and cm[g][s] becomes the exclusive prefix over g (the offset
+// of workgroup g's keys inside super-tile s's list).  64 columns per
+// workgroup, 16 waves each over a band of rows.
+constexpr int kColW = 64, kColWaves = 16;
+__global__ __launch_bounds__(kColW * kColWaves) void k_super_cols(int nb, int NS, int *__restrict__ cm,
+                                                                  int *__restrict__ super_counts) {
+    __shared__ int s_part[kColWaves][kColW];
+    const int lane = threadIdx.x & (kColW - 1), w = threadIdx.x / kColW;
+    const int s = blockIdx.x * kColW + lane;
+    const int rows = (nb + kColWaves - 1) / kColWaves, r0 = w * rows, r1 = min(nb, r0 + rows);
+    int sum = 0;
+    if (s < NS)
+        for (int r = r0; r < r1; ++r) sum += cm[(size_t)r * NS + s];
+    s_part[w][lane] = sum;
+    __syncthreads();
+    int run = 0;
+    for (int k = 0; k < w; ++k) run += s_part[k][lane];
+    if (s >= NS) return;
+    if (w == kColWaves - 1) super_counts[s] = run + sum;
+    for (int r = r0; r < r1; ++r) {
+        const int c = cm[(size_t)r * NS + s];
+        cm[(size_t)r * NS + s] = run;
+        run += c;
+    }
+}
+
+// One key per (visible splat, super-tile) pair.  Workgroup g's keys of
+// super-tile s go to super_offsets[s] + cm[g][s] onwards (the scanned count
+// matrix), placed with LDS atomics; the order inside a super-tile list is
+// arbitrary, k_sort_super orders it.
 template <bool PACKED>
 __global__ __launch_bounds__(kBinThreads) void k_scatter_super(int n, int chunk, int sxn, int NS,
                                                                const int *__restrict__ radii,
                                                                const uint2 *__restrict__ rect,
                                                                const float *__restrict__ depths,
-                                                               int *__restrict__ super_cursor,
+                                                               const int *__restrict__ super_offsets,
+                                                               const int *__restrict__ cm,
                                                                unsigned long long *__restrict__ keys) {
     __shared__ int s_h[kHistBins];
+    const int *row = cm + (size_t)blockIdx.x * NS;
     for (int w0 = 0; w0 < NS; w0 += kHistBins) {
         const int nbin = min(kHistBins, NS - w0);
-        for (int k = threadIdx.x; k < nbin; k += kBinThreads) s_h[k] = 0;
-        __syncthreads();
-        for_pairs(n, chunk, sxn, w0, nbin, radii, rect, [&](int bin, int, uint32_t) { atomicAdd(&s_h[bin], 1); });
-        __syncthreads();
-        for (int k = threadIdx.x; k < nbin; k += kBinThreads) {
-            const int c = s_h[k];
-            s_h[k] = c ? atomicAdd(&super_cursor[w0 + k], c) : 0;
-        }
+        for (int k = threadIdx.x; k < nbin; k += kBinThreads) s_h[k] = super_offsets[w0 + k] + row[w0 + k];
         __syncthreads();
         for_pairs<PACKED>(n, chunk, sxn, w0, nbin, radii, rect, [&](int bin, int gid, uint32_t lr) {
             const int pos = atomicAdd(&s_h[bin], 1);
@@ -525,23 +546,28 @@ static void launch_scan_counts(hipStream_t s, int T, const int *counts, int *off
 }
 
 static void bin_chunks(int n, int *blocks, int *chunk) {
-    *blocks = std::max(1, std::min(256, (n + 2047) / 2048));
+    *blocks = std::max(1, std::min(kBinMaxBlocks, (n + 2047) / 2048));
     *chunk = (n + *blocks - 1) / *blocks;
 }
 
 void launch_super_count(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
-                        int *super_counts, int *super_offsets, int *super_cursor, int *super_stats, int *temp) {
+                        int *super_counts, int *super_offsets, int *super_cm, int *super_stats, int *temp) {
     const int sxn = (tiles_x + kSuper - 1) / kSuper, syn = (tiles_y + kSuper - 1) / kSuper, NS = sxn * syn;
     int blocks, chunk;
     bin_chunks(n, &blocks, &chunk);
-    if (n > 0)
+    if (n > 0) {
         hipLaunchKernelGGL(k_super_hist, dim3(blocks), dim3(kBinThreads), 0, s, n, chunk, sxn, NS, radii,
-                           reinterpret_cast<const uint2 *>(rect), super_counts);
-    launch_scan_counts(s, NS, super_counts, super_offsets, super_cursor, super_stats, temp);
+                           reinterpret_cast<const uint2 *>(rect), super_cm);
+        hipLaunchKernelGGL(k_super_cols, dim3((NS + kColW - 1) / kColW), dim3(kColW * kColWaves), 0, s, blocks, NS,
+                           super_cm, super_counts);
+    } else {
+        hipMemsetAsync(super_counts, 0, (size_t)NS * 4, s);
+    }
+    launch_scan_counts(s, NS, super_counts, super_offsets, nullptr, super_stats, temp);
 }
 
 void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
-                      const float *depths, const int *super_offsets, int *super_cursor, int super_max,
+                      const float *depths, const int *super_offsets, const int *super_cm, int super_max,
                       uint64_t *super_keys, uint64_t *super_keys_tmp, int *big_list, int *super_stats,
                       int *tile_counts, int *tile_offsets, int *tile_stats, int *tile_temp, int *ids,
                       bool force_wide_keys) {
@@ -555,7 +581,7 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
     const bool packed = n < kPackedMaxSplats && !force_wide_keys;
     if (n > 0)
         hipLaunchKernelGGL(packed ? k_scatter_super<true> : k_scatter_super<false>, dim3(blocks), dim3(kBinThreads), 0,
-                           s, n, chunk, sxn, NS, radii, r2, depths, super_cursor, k);
+                           s, n, chunk, sxn, NS, radii, r2, depths, super_offsets, super_cm, k);
     hipLaunchKernelGGL(packed ? k_sort_super<true> : k_sort_super<false>, dim3(NS), dim3(kSortThreads), 0, s, tiles_x,
                        tiles_y, sxn, super_offsets, k, r2, tile_counts, big_list, super_stats);
     unsigned long long *src = k, *dst = kt;

@@ -36,17 +36,19 @@ void launch_tiles_hit(hipStream_t s, const uint32_t *rect, const int *radii, int
 // Super-tiles are 4x4 tiles: sxn = ceil(tiles_x / 4), syn = ceil(tiles_y / 4),
 // NS = sxn * syn.  Scan temporaries: tile_scan_temp_ints(count) ints.
 int64_t tile_scan_temp_ints(int T);
-// (splat, super-tile) pair counts -> super_offsets[NS + 1], super_cursor[NS];
-// super_stats = {pairs, largest list, long-list count}.  super_counts[NS]
-// and super_stats[0..2] must be zero on entry.
+// (splat, super-tile) pair counts -> super_counts[NS], super_offsets[NS + 1];
+// super_stats = {pairs, largest list, long-list count}, zero on entry.
+// super_cm (kBinMaxBlocks x NS ints) receives the per-(workgroup,
+// super-tile) key offsets that launch_bin_tiles places the keys at.
 void launch_super_count(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
-                        int *super_counts, int *super_offsets, int *super_cursor, int *super_stats, int *temp);
+                        int *super_counts, int *super_offsets, int *super_cm, int *super_stats, int *temp);
+constexpr int kBinMaxBlocks = 256;
 // Scatter, per-super-tile sort (super_keys_tmp, the size of super_keys, is
 // needed when super_max > 4096), tile counts and offsets (tile_offsets[T + 1],
 // tile_stats = {intersections, largest tile}, zero on entry) and the
 // per-tile sorted gaussian ids.
 void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
-                      const float *depths, const int *super_offsets, int *super_cursor, int super_max,
+                      const float *depths, const int *super_offsets, const int *super_cm, int super_max,
                       uint64_t *super_keys, uint64_t *super_keys_tmp, int *big_list, int *super_stats,
                       int *tile_counts, int *tile_offsets, int *tile_stats, int *tile_temp, int *ids,
                       bool force_wide_keys);
