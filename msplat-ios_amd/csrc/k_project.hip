@@ -55,7 +55,8 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
     const bool valid = i < n;
     const int ii = valid ? i : 0;
     const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 *ro = rec + 5 * (size_t)ii;
+    // this splat's record and quadrant-mask record, written out through LDS
+    float4 ro[5] = {z4, z4, z4, z4, z4}, mo[3] = {z4, z4, z4};
     const float *vm = cam.viewmat, *pm = cam.projmat;
     const float p[3] = {means[3 * (size_t)ii], means[3 * (size_t)ii + 1], means[3 * (size_t)ii + 2]};
     const float pz = vm[8] * p[0] + vm[9] * p[1] + vm[10] * p[2] + vm[11];
@@ -111,8 +112,6 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
             radii[i] = 0;
             depths[i] = 0.f;
             rect[i] = make_uint2(0u, 0u);
-#pragma unroll
-            for (int k = 0; k < 5; ++k) ro[k] = z4;
             if (colors_raw) {
                 colors_raw[3 * (size_t)i] = colors_raw[3 * (size_t)i + 1] = colors_raw[3 * (size_t)i + 2] = 0.f;
             }
@@ -140,7 +139,6 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
     ro[2] = q2;
     ro[3] = make_float4(R2.x, R2.y, R2.z, __builtin_fmaxf(col[0] + 0.5f, 0.0f));
     ro[4] = make_float4(__builtin_fmaxf(col[1] + 0.5f, 0.0f), __builtin_fmaxf(col[2] + 0.5f, 0.0f), tau, lp_r2);
-    float4 *mo = mrec + 3 * (size_t)i;
     mo[0] = mr.box;
     mo[1] = mr.e;
     mo[2] = mr.h;
@@ -149,6 +147,21 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
         colors_raw[3 * (size_t)i + 1] = col[1];
         colors_raw[3 * (size_t)i + 2] = col[2];
     }
+    }
+    // The block's records leave as contiguous rows: each thread's 5 + 3
+    // float4 go through LDS (the staged SH rows are no longer needed), then
+    // every store instruction writes 1 KB of consecutive float4s.
+    {
+        float4 *s4 = reinterpret_cast<float4 *>(s_fr);
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 5; ++k) s4[5 * threadIdx.x + k] = ro[k];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) s4[5 * kBlock + 3 * threadIdx.x + k] = mo[k];
+        __syncthreads();
+        float4 *rdst = rec + 5 * (size_t)b0, *mdst = mrec + 3 * (size_t)b0;
+        for (int e = threadIdx.x; e < 5 * cnt; e += kBlock) rdst[e] = s4[e];
+        for (int e = threadIdx.x; e < 3 * cnt; e += kBlock) mdst[e] = s4[5 * kBlock + e];
     }
     // intersections: sum of the rectangle areas over the workgroup
     __shared__ unsigned long long s_area[kBlock / 64];
