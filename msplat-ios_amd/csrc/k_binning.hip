@@ -555,14 +555,12 @@ void launch_super_count(hipStream_t s, int n, int tiles_x, int tiles_y, const in
     const int sxn = (tiles_x + kSuper - 1) / kSuper, syn = (tiles_y + kSuper - 1) / kSuper, NS = sxn * syn;
     int blocks, chunk;
     bin_chunks(n, &blocks, &chunk);
-    if (n > 0) {
+    if (n > 0)
         hipLaunchKernelGGL(k_super_hist, dim3(blocks), dim3(kBinThreads), 0, s, n, chunk, sxn, NS, radii,
                            reinterpret_cast<const uint2 *>(rect), super_cm);
-        hipLaunchKernelGGL(k_super_cols, dim3((NS + kColW - 1) / kColW), dim3(kColW * kColWaves), 0, s, blocks, NS,
-                           super_cm, super_counts);
-    } else {
-        hipMemsetAsync(super_counts, 0, (size_t)NS * 4, s);
-    }
+    // with no splats the matrix has no rows and every count is zero
+    hipLaunchKernelGGL(k_super_cols, dim3((NS + kColW - 1) / kColW), dim3(kColW * kColWaves), 0, s,
+                       n > 0 ? blocks : 0, NS, super_cm, super_counts);
     launch_scan_counts(s, NS, super_counts, super_offsets, nullptr, super_stats, temp);
 }
 

@@ -164,6 +164,21 @@ def test_empty_scene_renders_background(orc, eng):
     assert np.array_equal(out["out_img"], np.broadcast_to(scene.background, out["out_img"].shape))
 
 
+def test_zero_splats_render_background(orc, eng):
+    """No gaussians at all (the binning's count matrix has no rows): the
+    frame is the background and no intersection is emitted."""
+    import dataclasses
+    scene = S.make_scene(1, n=64, width=48, height=40)
+    empty = dataclasses.replace(scene, means=scene.means[:0], scales=scene.scales[:0], quats=scene.quats[:0],
+                                opacities=scene.opacities[:0], features_dc=scene.features_dc[:0],
+                                features_rest=scene.features_rest[:0])
+    assert empty.n == 0
+    ds = D.DeviceScene(empty)
+    out = D.render(ds, ds.camera(empty.cameras[0]))
+    assert out["num_intersections"] == 0
+    assert np.array_equal(out["out_img"], np.broadcast_to(empty.background, out["out_img"].shape))
+
+
 def _device(a):
     return E.DeviceArray.from_numpy(np.ascontiguousarray(a, np.float32))
 
