@@ -8,9 +8,10 @@
 // free and the per-pixel loop reads a broadcast.  Each wave owns an 8x8
 // quadrant of the tile.  At load time each splat gets a 4-bit mask of the
 // quadrants whose pixel centres its alpha >= 1/255 region can reach
-// (quad_mask on the splat's precomputed MaskRec), and the batch is compacted into one ascending slot list
-// per wave, so a wave only visits the splats that can touch its quadrant and
-// every visited splat is a full evaluation.
+// (quad_mask on the splat's MaskRec, precomputed by the projection), and the
+// batch is compacted into one ascending slot list per wave, so a wave only
+// visits the splats that can touch its quadrant and every visited splat is
+// a full evaluation.
 #include "kernels.h"
 #include "ms_device.h"
 
