@@ -80,9 +80,40 @@ def sh_color(mean, cam_pos, fdc, frest, degree):
     return basis @ coeffs[: basis.shape[-1]]
 
 
-def aabb_center(T):
-    f = np.array([9.0, 9.0, -1.0]) / np.dot([9.0, 9.0, -1.0], T[2] * T[2])
-    return np.array([np.dot(f, T[0] * T[2]), np.dot(f, T[1] * T[2])])
+def _extreme(fn, theta0, width, rounds=4, samples=257):
+    """Maximises fn(theta) [m, k] over each row's window around theta0 by
+    repeated grid zooming; returns the maxima [m]."""
+    best_t = theta0
+    for _ in range(rounds):
+        ts = best_t[:, None] + np.linspace(-width, width, samples)[None, :]
+        v = fn(ts)
+        i = np.argmax(v, axis=1)
+        best_t = ts[np.arange(len(ts)), i]
+        width = 2.0 * width / (samples - 1)
+    return fn(best_t[:, None])[:, 0]
+
+
+def circle_footprint(T, r=3.0, samples=4096):
+    """Bounding box of the circle u^2 + v^2 = r^2 mapped through the
+    homographies T [m,3,3] to pixels: (centre [m,2], half extent [m,2]).
+    Only valid where the whole circle is in front (T[2] . (u,v,1) > 0)."""
+    T = np.asarray(T, np.float64)
+
+    def coord(ts, row):
+        u, v = r * np.cos(ts), r * np.sin(ts)
+        h = T[:, row, 0, None] * u + T[:, row, 1, None] * v + T[:, row, 2, None]
+        w = T[:, 2, 0, None] * u + T[:, 2, 1, None] * v + T[:, 2, 2, None]
+        return h / w
+
+    grid = np.linspace(0.0, 2 * np.pi, samples, endpoint=False)[None, :].repeat(len(T), 0)
+    out_c, out_e = [], []
+    for row in (0, 1):
+        vals = coord(grid, row)
+        hi = _extreme(lambda ts: coord(ts, row), grid[0, np.argmax(vals, 1)], 2 * np.pi / samples)
+        lo = -_extreme(lambda ts: -coord(ts, row), grid[0, np.argmin(vals, 1)], 2 * np.pi / samples)
+        out_c.append(0.5 * (hi + lo))
+        out_e.append(0.5 * (hi - lo))
+    return np.stack(out_c, 1), np.stack(out_e, 1)
 
 
 def composite(px, py, splats, background, near=0.2, far=100.0):

@@ -115,7 +115,7 @@ def test_project_forward_matches_fp64_derivation(orc):
             assert np.abs(proj["normal_opac"][i, :3] - nrm).max() <= 2e-6
             col = R.sh_color(scene.means[i], cam.cam_pos, scene.features_dc[i], scene.features_rest[i], 3)
             assert np.abs(proj["colors"][i] - col).max() <= 2e-5
-            assert np.abs(proj["xys"][i] - R.aabb_center(T)).max() <= 2e-3
+            assert np.abs(proj["xys"][i] - R.circle_footprint(T[None])[0][0]).max() <= 2e-3
             assert proj["depths"][i] == pytest.approx(T[2, 2], rel=1e-5)
 
 
