@@ -185,6 +185,24 @@ int msplat_hip_loss_fwd_bwd(int width, int height, const float *img_dev,
                             float lambda_dssim, float *dL_dimg_dev,
                             double *loss_host, double *ssim_sum_host);
 
+/* msplat_hip_loss_fwd_bwd without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The scratch it needs lives in a fixed device array of the
+ * library (about 77 MB per GPU, held until the process ends): images up to
+ * 2^21 pixels (e.g. 2048x1024, 1920x1080); larger ones return
+ * MSPLAT_E_CAPACITY.  msplat_hip_init must have run (this call does no
+ * set-up).  Results are bit-identical to msplat_hip_loss_fwd_bwd.  Every
+ * call on a GPU shares that GPU's scratch: calls are serialised by the
+ * engine's lock and stream, and anything that ran these kernels
+ * concurrently on that array would race.  Synchronous. */
+int msplat_hip_loss_fwd_bwd_noalloc(int width, int height, const float *img_dev,
+                                    const float *gt_dev,
+                                    const float *distortion_dev,
+                                    float lambda_l1, float lambda_dist,
+                                    float lambda_dssim, float *dL_dimg_dev,
+                                    double *loss_host, double *ssim_sum_host);
+
 /* nd_rasterize_backward_2dgs (msplat_metal.metal:1705-1979) on the forward
  * state of the most recent render / train step.  Per-pixel upstream
  * gradients [H,W,{3,1}] may be NULL (zero).  grads16_dev [N,16] is

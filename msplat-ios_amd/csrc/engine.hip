@@ -17,7 +17,26 @@
 #include "kernels.h"
 #include "msplat_engine.h"
 
+// Scratch of msplat_hip_loss_fwd_bwd_noalloc, for callers that cannot
+// allocate: the three per-pixel SSIM partial maps (12 B per pixel each, at
+// fixed offsets sized for kNoAllocMaxPixels), then the per-workgroup loss
+// partials (16 B per 32x32 tile, kNoAllocMaxBlocks of them), then the two
+// loss doubles.  Every call on a GPU shares that GPU's copy and leaves its
+// contents behind; each call rewrites every element it later reads, so
+// nothing needs clearing.  In host code `scratch` is only a symbol: kernels
+// get the device address from hipGetSymbolAddress (g_scratch_dev).
+constexpr int64_t kNoAllocMaxPixels = int64_t(1) << 21;  // e.g. 2048 x 1024, 1920 x 1080
+constexpr int64_t kNoAllocMaxBlocks = int64_t(1) << 17;
+constexpr size_t kNoAllocMapBytes = (size_t)kNoAllocMaxPixels * 12;
+constexpr size_t kNoAllocPartialsOff = 3 * kNoAllocMapBytes;
+constexpr size_t kNoAllocLossOff = kNoAllocPartialsOff + (size_t)kNoAllocMaxBlocks * 16;
+constexpr size_t kNoAllocBytes = kNoAllocLossOff + 256;
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+void *g_scratch_dev[kMaxDevices] = {};  // device address of `scratch`, per device
 
 struct DevBuf {
     void *p = nullptr;
@@ -137,6 +156,10 @@ int init_locked() {
         set_err("no HIP device available");
         return MSPLAT_E_NODEV;
     }
+    if (g_eng.device < 0 || g_eng.device >= kMaxDevices) {
+        set_err("device %d out of range", g_eng.device);
+        return MSPLAT_E_NODEV;
+    }
     HIPC(hipSetDevice(g_eng.device));
     hipDeviceProp_t prop;
     HIPC(hipGetDeviceProperties(&prop, g_eng.device));
@@ -148,6 +171,16 @@ int init_locked() {
     HIPC(hipHostMalloc((void **)&g_eng.pinned_i, 64 * sizeof(int), hipHostMallocDefault));
     HIPC(hipHostMalloc((void **)&g_eng.pinned_d, 16 * sizeof(double), hipHostMallocDefault));
     for (int i = 0; i <= ST_COUNT; ++i) HIPC(hipEventCreate(&g_eng.ev[i]));
+    // this device's copy of the no-allocation entry point's scratch array
+    if (!g_scratch_dev[g_eng.device]) {
+        void *sp = nullptr;
+        HIPC(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)));
+        if (!sp) {
+            set_err("hipGetSymbolAddress(scratch) returned no address");
+            return MSPLAT_E_HIP;
+        }
+        g_scratch_dev[g_eng.device] = sp;
+    }
     // The 11-tap SSIM window exp(-(x-5)^2 / 4.5) / sum (the table of
     // msplat_metal.metal:2804-2816), evaluated in double and rounded once.
     double gsum = 0.0, gw[11];
@@ -751,6 +784,51 @@ int msplat_hip_loss_fwd_bwd(int W, int H, const float *img, const float *gt, con
     HIPC(hipStreamSynchronize(g_eng.stream));
     if (loss_host) *loss_host = g_eng.pinned_d[0];
     if (ssim_host) *ssim_host = g_eng.pinned_d[1];
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_loss_fwd_bwd_noalloc(int W, int H, const float *img, const float *gt, const float *dist, float l1,
+                                    float ldist, float ldssim, float *dL, double *loss_host, double *ssim_host) {
+    API_BEGIN
+    // no set-up here: msplat_hip_init allocated the stream and the pinned
+    // readback area and looked up this device's scratch array
+    if (!g_eng.ready) {
+        set_err("loss_fwd_bwd_noalloc: call msplat_hip_init first (this entry point allocates nothing)");
+        return MSPLAT_E_ARG;
+    }
+    if (W <= 0 || H <= 0 || !img || !gt || !dL || (ldist != 0.f && !dist)) {
+        set_err("invalid loss arguments");
+        return MSPLAT_E_ARG;
+    }
+    const int64_t pixels = (int64_t)W * H;
+    if (pixels > kNoAllocMaxPixels) {
+        set_err("loss_fwd_bwd_noalloc: %dx%d = %lld pixels exceeds the %lld-pixel scratch", W, H,
+                (long long)pixels, (long long)kNoAllocMaxPixels);
+        return MSPLAT_E_CAPACITY;
+    }
+    if ((int64_t)mskern::ssim_num_blocks(W, H) > kNoAllocMaxBlocks) {
+        set_err("loss_fwd_bwd_noalloc: %dx%d needs more than %lld tiles", W, H, (long long)kNoAllocMaxBlocks);
+        return MSPLAT_E_CAPACITY;
+    }
+    Engine &E = g_eng;
+    unsigned char *base = static_cast<unsigned char *>(g_scratch_dev[E.device]);
+    if (!base) {
+        set_err("loss_fwd_bwd_noalloc: no scratch address for device %d", E.device);
+        return MSPLAT_E_HIP;
+    }
+    float *gm1 = reinterpret_cast<float *>(base);
+    float *gs1 = reinterpret_cast<float *>(base + kNoAllocMapBytes);
+    float *gs12 = reinterpret_cast<float *>(base + 2 * kNoAllocMapBytes);
+    double *partials = reinterpret_cast<double *>(base + kNoAllocPartialsOff);
+    double *loss = reinterpret_cast<double *>(base + kNoAllocLossOff);
+    mskern::launch_loss_fwd_bwd(E.stream, W, H, img, gt, ldist != 0.f ? dist : nullptr, l1, ldist, ldssim, E.window,
+                                gm1, gs1, gs12, partials, loss, dL);
+    HIPC(hipGetLastError());
+    HIPC(hipMemcpyAsync(E.pinned_d, loss, 2 * sizeof(double), hipMemcpyDeviceToHost, E.stream));
+    HIPC(hipStreamSynchronize(E.stream));
+    if (loss_host) *loss_host = E.pinned_d[0];
+    if (ssim_host) *ssim_host = E.pinned_d[1];
     return MSPLAT_OK;
     API_END
 }

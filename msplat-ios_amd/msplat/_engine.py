@@ -60,6 +60,7 @@ EXPORTS = [
     "msplat_hip_device_name", "msplat_hip_alloc", "msplat_hip_free", "msplat_hip_memset", "msplat_hip_upload",
     "msplat_hip_download", "msplat_hip_copy", "msplat_hip_commit", "msplat_hip_sync", "msplat_hip_train_step",
     "msplat_hip_render", "msplat_hip_fused_adam", "msplat_hip_densify", "msplat_hip_clamp_max", "msplat_hip_loss_fwd_bwd",
+    "msplat_hip_loss_fwd_bwd_noalloc",
     "msplat_hip_raster_bwd", "msplat_hip_project_bwd", "msplat_hip_project_bwd_adam", "msplat_hip_last", "msplat_hip_enable_timing",
     "msplat_hip_stage_times", "msplat_hip_last_pairs_evaluated", "msplat_hip_last_raster_counts",
     "msplat_hip_check_fast_rcp", "msplat_hip_set_wide_keys",
@@ -100,6 +101,8 @@ def lib() -> C.CDLL:
                                    C.POINTER(I)]),
         "msplat_hip_clamp_max": (I, [P, I64, F]),
         "msplat_hip_loss_fwd_bwd": (I, [I, I, P, P, P, F, F, F, P, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+        "msplat_hip_loss_fwd_bwd_noalloc": (I, [I, I, P, P, P, F, F, F, P, C.POINTER(C.c_double),
+                                                C.POINTER(C.c_double)]),
         "msplat_hip_raster_bwd": (I, [P, P, P, P, P, P, P]),
         "msplat_hip_project_bwd": (I, [C.POINTER(MsplatCamera), C.POINTER(MsplatGaussians), P, P, P, P, P, P, P, P,
                                        P, P, P, F]),
