@@ -797,11 +797,15 @@ extern "C" void orc_raster_bwd(const OrcCamera *cam, int n, const int32_t *tile_
                                const float *dL_dimg, const float *dL_ddepth,
                                const float *dL_daccum, const float *dL_dnormal,
                                const float *dL_dmedian, const float *dL_dreg_map,
-                               float *grads) {
+                               float *grads, float *grads_abs) {
     const int W = cam->width, H = cam->height, TX = cam->tiles_x, TY = cam->tiles_y;
     const int T_tiles = TX * TY;
     const int64_t I = tile_offsets[T_tiles];
     std::vector<double> acc((size_t)I * 16, 0.0);
+    /* grads_abs (nullable): per component the sum of the magnitudes of every
+     * summand that went into it, the scale of a floating-point summation's
+     * rounding error (test instrumentation; not part of the reference) */
+    std::vector<double> acc_abs(grads_abs ? (size_t)I * 16 : 0, 0.0);
     const float mscale = FAR_N / (FAR_N - NEAR_N);
     const std::vector<float> crow = all_centred_rows(I, ids, xys, transmats);
 
@@ -852,6 +856,7 @@ extern "C" void orc_raster_bwd(const OrcCamera *cam, int n, const int32_t *tile_
                     const float dchannel_dcolor = alpha * T;
                     float dL_dalpha = 0.0f;
                     double *a = acc.data() + (size_t)j * 16;
+                    double *aa = grads_abs ? acc_abs.data() + (size_t)j * 16 : nullptr;
                     const float *crgb = colors + 3 * g;
                     for (int ch = 0; ch < 3; ch++) {
                         const float c_raw = crgb[ch];
@@ -862,6 +867,7 @@ extern "C" void orc_raster_bwd(const OrcCamera *cam, int n, const int32_t *tile_
                         last_color[ch] = c_used;
                         dL_dalpha += (c_used - accum_rec[ch]) * dpix[ch];
                         a[13 + ch] += (double)(dchannel_dcolor * dpix[ch] * mask);
+                        if (aa) aa[13 + ch] += std::fabs((double)(dchannel_dcolor * dpix[ch] * mask));
                     }
                     float dL_dz = 0.0f, dL_dweight = 0.0f;
                     const float m_d = mscale * (1.0f - NEAR_N / e.depth);
@@ -884,6 +890,7 @@ extern "C" void orc_raster_bwd(const OrcCamera *cam, int n, const int32_t *tile_
                         last_normal[ch] = no[ch];
                         dL_dalpha += (no[ch] - accum_normal_rec[ch]) * dn2[ch];
                         a[9 + ch] += (double)(alpha * T * dn2[ch]);
+                        if (aa) aa[9 + ch] += std::fabs((double)(alpha * T * dn2[ch]));
                     }
                     dL_dalpha *= T;
                     last_alpha = alpha;
@@ -910,13 +917,46 @@ extern "C" void orc_raster_bwd(const OrcCamera *cam, int n, const int32_t *tile_
                         a[6] += (double)(px * dk.x + py * dl.x + dL_dz * e.u);
                         a[7] += (double)(px * dk.y + py * dl.y + dL_dz * e.v);
                         a[8] += (double)(px * dk.z + py * dl.z + dL_dz * 1.0f);
+                        if (aa) {
+                            /* magnitudes of the parts each summand is formed
+                             * from: k = px Tw - Tu, l = py Tw - Tv, dp.z =
+                             * -(dp.x u + dp.y v), pushed through the cross
+                             * products */
+                            const double Tuv[2][3] = {{Tm[0], Tm[1], Tm[2]}, {Tm[3], Tm[4], Tm[5]}};
+                            const double Twv[3] = {Tm[6], Tm[7], Tm[8]};
+                            double km[3], lm[3];
+                            for (int q = 0; q < 3; ++q) {
+                                km[q] = std::fabs(px * Twv[q]) + std::fabs(Tuv[0][q]);
+                                lm[q] = std::fabs(py * Twv[q]) + std::fabs(Tuv[1][q]);
+                            }
+                            const double pm[3] = {std::fabs((double)dp.x), std::fabs((double)dp.y),
+                                                  std::fabs((double)dsx_pz * e.u) +
+                                                      std::fabs((double)dsy_pz * e.v)};
+                            const double dkm[3] = {lm[1] * pm[2] + lm[2] * pm[1], lm[2] * pm[0] + lm[0] * pm[2],
+                                                   lm[0] * pm[1] + lm[1] * pm[0]};
+                            const double dlm[3] = {pm[1] * km[2] + pm[2] * km[1], pm[2] * km[0] + pm[0] * km[2],
+                                                   pm[0] * km[1] + pm[1] * km[0]};
+                            const double uv1[3] = {e.u, e.v, 1.0};
+                            for (int q = 0; q < 3; ++q) {
+                                aa[q] += dkm[q];
+                                aa[3 + q] += dlm[q];
+                                aa[6 + q] += std::fabs(px) * dkm[q] + std::fabs(py) * dlm[q] +
+                                             std::fabs(dL_dz * uv1[q]);
+                            }
+                        }
                     } else {
                         a[6] += (double)(e.u * dL_dz);
                         a[7] += (double)(e.v * dL_dz);
                         a[8] += (double)dL_dz;
+                        if (aa) {
+                            aa[6] += std::fabs((double)(e.u * dL_dz));
+                            aa[7] += std::fabs((double)(e.v * dL_dz));
+                            aa[8] += std::fabs((double)dL_dz);
+                        }
                     }
                     const float dsig = opa * (1.0f - opa);
                     a[12] += (double)(G * dL_dalpha * dsig);
+                    if (aa) aa[12] += std::fabs((double)(G * dL_dalpha * dsig));
                 }
             }
     }
@@ -927,6 +967,15 @@ extern "C" void orc_raster_bwd(const OrcCamera *cam, int n, const int32_t *tile_
         for (int k = 0; k < 16; ++k) o[k] += a[k];
     }
     for (size_t k = 0; k < (size_t)n * 16; ++k) grads[k] = (float)gsum[k];
+    if (grads_abs) {
+        std::fill(gsum.begin(), gsum.end(), 0.0);
+        for (int64_t j = 0; j < I; ++j) {
+            const double *a = acc_abs.data() + (size_t)j * 16;
+            double *o = gsum.data() + (size_t)ids[j] * 16;
+            for (int k = 0; k < 16; ++k) o[k] += a[k];
+        }
+        for (size_t k = 0; k < (size_t)n * 16; ++k) grads_abs[k] = (float)gsum[k];
+    }
 }
 
 /* project_and_sh_backward_2dgs_kernel (msplat_metal.metal:2003-2209). */
@@ -1147,7 +1196,7 @@ extern "C" double orc_train_step(int n, float *means, float *scales, float *quat
                                  float *const exp_avg[6], float *const exp_avg_sq[6],
                                  const float adam_lr[6], int adam_step, float *xys_grad_norm,
                                  float *vis_counts, float *max_2d_size, float *out_img_out,
-                                 double *stage_ms, int64_t *num_isect) {
+                                 double *stage_ms, int64_t *num_isect, OrcStepDetail *detail) {
     using clk = std::chrono::steady_clock;
     auto t0 = clk::now();
     auto lap = [&](int s) {
@@ -1185,10 +1234,24 @@ extern "C" double orc_train_step(int n, float *means, float *scales, float *quat
                                    ddist.data(), nullptr);
     lap(3);
     std::vector<float> g16(16 * (size_t)n);
+    std::vector<float> g16_abs(detail && detail->want_grads ? 16 * (size_t)n : 0);
     orc_raster_bwd(cam, n, offs.data(), ids.data(), xys.data(), tm.data(), no.data(),
                    col.data(), bg, fT.data(), fidx.data(), dimg.data(), nullptr, nullptr,
-                   nullptr, nullptr, ddist.data(), g16.data());
+                   nullptr, nullptr, ddist.data(), g16.data(),
+                   g16_abs.empty() ? nullptr : g16_abs.data());
     lap(4);
+    if (detail) {
+        auto dup = [](const void *src, size_t bytes) {
+            void *d = malloc(bytes ? bytes : 1);
+            if (d && bytes) memcpy(d, src, bytes);
+            return d;
+        };
+        detail->num_isect = I;
+        detail->tile_offsets = (int32_t *)dup(offs.data(), offs.size() * 4);
+        detail->ids = (int32_t *)dup(ids.data(), ids.size() * 4);
+        detail->grads16 = detail->want_grads ? (float *)dup(g16.data(), g16.size() * 4) : nullptr;
+        detail->grads16_abs = detail->want_grads ? (float *)dup(g16_abs.data(), g16_abs.size() * 4) : nullptr;
+    }
     std::vector<float> dm(3 * (size_t)n), ds(2 * (size_t)n), dq(4 * (size_t)n),
         dm2(2 * (size_t)n), ddc(3 * (size_t)n), dfr((size_t)K * 3 * n), dop(n);
     const float inv_max_dim = 1.0f / (float)std::max(cam->width, cam->height);
@@ -1211,6 +1274,8 @@ extern "C" double orc_train_step(int n, float *means, float *scales, float *quat
     if (out_img_out) memcpy(out_img_out, img.data(), 3 * P * sizeof(float));
     return loss;
 }
+
+extern "C" void orc_free(void *p) { free(p); }
 
 /* Test helpers: vectorised exp and the SSIM window. */
 extern "C" void orc_expf_array(int64_t n, const float *x, float *y) {

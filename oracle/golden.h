@@ -109,7 +109,9 @@ double orc_loss_fwd_bwd(int width, int height, const float *img,
 
 /* nd_rasterize_backward_2dgs_kernel (msplat_metal.metal:1705-1979).
  * grads is [N,16] = (dL_dtransMat[9], dL_dnormal3D[3], dL_dopacity_logit,
- * dL_dcolors[3]), accumulated in fp64 in a fixed order and stored as float. */
+ * dL_dcolors[3]), accumulated in fp64 in a fixed order and stored as float.
+ * grads_abs (nullable, [N,16]) receives per component the sum of the
+ * magnitudes of its summands: the scale of a float summation's error. */
 void orc_raster_bwd(const OrcCamera *cam, int n, const int32_t *tile_offsets,
                     const int32_t *ids, const float *xys,
                     const float *transmats, const float *normal_opac,
@@ -118,7 +120,7 @@ void orc_raster_bwd(const OrcCamera *cam, int n, const int32_t *tile_offsets,
                     const float *dL_dimg, const float *dL_ddepth,
                     const float *dL_dalpha, const float *dL_dnormal,
                     const float *dL_dmedian, const float *dL_ddistortion,
-                    float *grads);
+                    float *grads, float *grads_abs);
 
 /* project_and_sh_backward_2dgs_kernel (msplat_metal.metal:2003-2209).
  * grads16 is the [N,16] raster-gradient record above.  xys_grad_norm,
@@ -154,6 +156,19 @@ int orc_densify(int n, int capacity, float grad_thresh, float size_thresh,
                 float *const exp_avg[6], float *const exp_avg_sq[6],
                 const float *random_samples);
 
+/* Optional intermediate results of orc_train_step, for comparing a whole
+ * step stage by stage (test instrumentation): arrays are malloc'd by the
+ * golden model and released with orc_free.  want_grads also fills grads16
+ * and grads16_abs (see orc_raster_bwd). */
+typedef struct {
+    int want_grads;
+    int64_t num_isect;
+    int32_t *tile_offsets; /* [T+1] */
+    int32_t *ids;          /* [I]   */
+    float *grads16;        /* [N,16] */
+    float *grads16_abs;    /* [N,16] */
+} OrcStepDetail;
+
 /* Timing helper for the CPU baseline: one full training step (forward,
  * SSIM+L1, backward, six Adam groups) in place on the given parameters.
  * adam_lr[6], bc1, bc2 as Model::fullIteration (model.cpp:767-826).
@@ -167,7 +182,10 @@ double orc_train_step(int n, float *means, float *scales, float *quats,
                       const float adam_lr[6], int adam_step,
                       float *xys_grad_norm, float *vis_counts,
                       float *max_2d_size, float *out_img, double *stage_ms,
-                      int64_t *num_intersections);
+                      int64_t *num_intersections, OrcStepDetail *detail);
+
+/* Frees an array the golden model handed out (OrcStepDetail). */
+void orc_free(void *p);
 
 #ifdef __cplusplus
 }

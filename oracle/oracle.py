@@ -20,6 +20,12 @@ f32p = C.POINTER(C.c_float)
 i32p = C.POINTER(C.c_int32)
 
 
+class OrcStepDetail(C.Structure):
+    _fields_ = [("want_grads", C.c_int), ("num_isect", C.c_int64), ("tile_offsets", C.POINTER(C.c_int32)),
+                ("ids", C.POINTER(C.c_int32)), ("grads16", C.POINTER(C.c_float)),
+                ("grads16_abs", C.POINTER(C.c_float))]
+
+
 class OrcCamera(C.Structure):
     _fields_ = [("viewmat", C.c_float * 16), ("projmat", C.c_float * 16), ("cam_pos", C.c_float * 3),
                 ("fx", C.c_float), ("fy", C.c_float), ("cx", C.c_float), ("cy", C.c_float),
@@ -57,7 +63,7 @@ def lib() -> C.CDLL:
         L.orc_loss_fwd_bwd.restype = C.c_double
         L.orc_loss_fwd_bwd.argtypes = [C.c_int, C.c_int, P, P, P, C.c_float, C.c_float, C.c_float, P, P,
                                        C.POINTER(C.c_double)]
-        L.orc_raster_bwd.argtypes = [C.POINTER(OrcCamera), C.c_int] + [P] * 16
+        L.orc_raster_bwd.argtypes = [C.POINTER(OrcCamera), C.c_int] + [P] * 17
         L.orc_project_bwd.argtypes = [C.c_int, P, P, P, P, C.c_int, C.c_int, C.POINTER(OrcCamera), C.c_float,
                                       P, P, P, P, P, P, P, P, P, P, P, C.c_float]
         L.orc_adam.argtypes = [P, P, P, P, C.c_int64, C.c_float, C.c_float, C.c_float, C.c_float, C.c_float]
@@ -68,7 +74,8 @@ def lib() -> C.CDLL:
         L.orc_train_step.restype = C.c_double
         L.orc_train_step.argtypes = [C.c_int] + [P] * 6 + [C.c_int, C.c_int, C.POINTER(OrcCamera), P, P,
                                                           C.c_float, P * 6, P * 6, P, C.c_int, P, P, P, P, P,
-                                                          C.POINTER(C.c_int64)]
+                                                          C.POINTER(C.c_int64), C.POINTER(OrcStepDetail)]
+        L.orc_free.argtypes = [P]
         _lib = L
     return _lib
 
@@ -194,15 +201,20 @@ def loss_fwd_bwd(img, gt, distortion=None, lambda_l1=0.8, lambda_dist=0.0, lambd
 
 
 def raster_bwd(proj, bins, fwd, cam, background, dL_dimg, dL_ddepth=None, dL_dalpha=None, dL_dnormal=None,
-               dL_dmedian=None, dL_ddist=None):
+               dL_dmedian=None, dL_ddist=None, with_abs=False):
+    """[N,16] raster gradients; with_abs also returns, per component, the
+    sum of the magnitudes of its summands (the scale of a float summation's
+    rounding error)."""
     n = proj["radii"].shape[0]
     g = np.zeros((n, 16), np.float32)
+    ga = np.zeros((n, 16), np.float32) if with_abs else None
     ids = bins["ids"] if bins["ids"].size else np.zeros(1, np.int32)
     opt = [None if a is None else _f(a) for a in (dL_ddepth, dL_dalpha, dL_dnormal, dL_dmedian, dL_ddist)]
     lib().orc_raster_bwd(C.byref(cam), n, _p(bins["tile_offsets"]), _p(ids), _p(proj["xys"]),
                          _p(proj["transmats"]), _p(proj["normal_opac"]), _p(proj["colors"]), _p(_f(background)),
-                         _p(fwd["final_Ts"]), _p(fwd["final_idx"]), _p(_f(dL_dimg)), *[_p(a) for a in opt], _p(g))
-    return g
+                         _p(fwd["final_Ts"]), _p(fwd["final_idx"]), _p(_f(dL_dimg)), *[_p(a) for a in opt], _p(g),
+                         _p(ga))
+    return (g, ga) if with_abs else g
 
 
 def project_bwd(params: dict, cam, degree, dtu, radii, grads16, stats=None, glob_scale=1.0):
@@ -241,8 +253,11 @@ def densify(n, capacity, params6, exp_avg6, exp_avg_sq6, fr_stride, stats, rando
 
 
 def train_step(params6, exp_avg6, exp_avg_sq6, cam, background, gt, degree, dtu, adam_lr, adam_step, stats,
-               ssim_weight=0.2):
-    """One golden-model training step in place; returns (loss, img, stage_ms, I)."""
+               ssim_weight=0.2, detail=None):
+    """One golden-model training step in place; returns (loss, img, stage_ms, I).
+    detail: None, "bins" or "grads" -- fills `detail_out` (a dict passed as
+    stats["detail"]) with the tile offsets and ids, plus the raster gradients
+    and their summand magnitudes for "grads"."""
     m, s, q, dc, fr, op = params6
     n = m.shape[0]
     P6 = C.c_void_p * 6
@@ -250,8 +265,25 @@ def train_step(params6, exp_avg6, exp_avg_sq6, cam, background, gt, degree, dtu,
     stage = np.zeros(8, np.float64)
     nis = C.c_int64()
     lr = np.asarray(adam_lr, np.float32)
+    det = OrcStepDetail(want_grads=1 if detail == "grads" else 0) if detail else None
     loss = lib().orc_train_step(n, _p(m), _p(s), _p(q), _p(op), _p(dc), _p(fr), degree, dtu, C.byref(cam),
                                 _p(_f(background)), _p(_f(gt)), ssim_weight, P6(*[_p(a) for a in exp_avg6]),
                                 P6(*[_p(a) for a in exp_avg_sq6]), _p(lr), adam_step, _p(stats["grad_norm"]),
-                                _p(stats["vis"]), _p(stats["max2d"]), _p(img), _p(stage), C.byref(nis))
+                                _p(stats["vis"]), _p(stats["max2d"]), _p(img), _p(stage), C.byref(nis),
+                                C.byref(det) if det is not None else None)
+    if det is not None:
+        out = stats.setdefault("detail", {})
+        T = cam.tiles_x * cam.tiles_y
+        I = int(det.num_isect)
+
+        def take(ptr, count, dtype):
+            a = np.ctypeslib.as_array(ptr, shape=(count,)).astype(dtype, copy=True) if count else np.zeros(0, dtype)
+            lib().orc_free(C.cast(ptr, C.c_void_p))
+            return a
+
+        out["tile_offsets"] = take(det.tile_offsets, T + 1, np.int32)
+        out["ids"] = take(det.ids, I, np.int32)
+        if det.want_grads:
+            out["grads16"] = take(det.grads16, 16 * n, np.float32).reshape(n, 16)
+            out["grads16_abs"] = take(det.grads16_abs, 16 * n, np.float32).reshape(n, 16)
     return float(loss), img, stage, int(nis.value)

@@ -5,8 +5,10 @@ Bars (the oracle's arithmetic contract makes the non-atomic stages exact):
   projection, binning, per-tile order, rasterize forward, loss gradient,
   projection backward (given equal raster gradients), Adam, densify:
   bit-exact;
-  rasterize backward (float atomics): max |gpu - oracle| <= 1e-3 * max|oracle|
-  per gradient component;
+  rasterize backward (float atomics): per element |gpu - oracle| <=
+  1e-3 |oracle| + 1e-4 A + 1e-7 max|oracle|, A the magnitude of its
+  summands (tests/parity.py), and that bound carried through the projection
+  backward and Adam for the post-Adam parameters;
   scalar loss: relative 1e-5 (fp64 reduction order differs).
 """
 import ctypes as C
@@ -19,6 +21,7 @@ pytestmark = pytest.mark.gpu
 from msplat import _engine as E  # noqa: E402
 from msplat import device as D  # noqa: E402
 from msplat import synthetic as S  # noqa: E402
+from parity import grad_close, param_grad_noise, post_adam_close  # noqa: E402
 from scenes import adversarial  # noqa: E402
 
 
@@ -201,15 +204,6 @@ def test_loss_fwd_bwd_bitexact(shape, orc, eng):
     assert abs(ssim.value - ssim_o) <= 1e-6 * abs(ssim_o) + 1e-6
 
 
-def _grad_close(g, o, what, rtol=1e-3):
-    g = np.asarray(g, np.float64)
-    o = np.asarray(o, np.float64)
-    scale = np.abs(o).max(axis=0)
-    err = np.abs(g - o).max(axis=0)
-    ok = err <= rtol * scale + 1e-12
-    assert ok.all(), f"{what}: err {err} scale {scale}"
-
-
 @pytest.mark.parametrize("name", list(SCENES))
 def test_raster_backward_close(name, orc, eng):
     scene = SCENES[name]()
@@ -218,13 +212,13 @@ def test_raster_backward_close(name, orc, eng):
     target = scene.jittered(0.01, 99)
     gt = orc.render(target, 0)[3]["out_img"]
     _, dL, _, _ = orc.loss_fwd_bwd(fwd["out_img"], gt)
-    g_o = orc.raster_bwd(proj, bins, fwd, ocam, scene.background, dL)
+    g_o, a_o = orc.raster_bwd(proj, bins, fwd, ocam, scene.background, dL, with_abs=True)
     d_dL = _device(dL)
     g16 = E.DeviceArray.zeros((scene.n, 16))
     E.check(E.lib().msplat_hip_raster_bwd(d_dL.ptr, None, None, None, None, None, g16.ptr))
     g = g16.numpy()
     assert np.abs(g_o).max() > 0
-    _grad_close(g, g_o, "grads16 [dT(9), dn(3), dopacity, dcolor(3)]")
+    grad_close(g, g_o, a_o, "grads16 [dT(9), dn(3), dopacity, dcolor(3)]")
     # culled splats receive nothing
     assert np.all(g[proj["radii"] <= 0] == 0)
 
@@ -239,13 +233,13 @@ def test_raster_backward_all_upstream_gradients(orc, eng):
     up = dict(img=rng.normal(H * W * 3, 0, 1e-3).reshape(H, W, 3), depth=rng.normal(H * W, 0, 1e-3).reshape(H, W),
               alpha=rng.normal(H * W, 0, 1e-3).reshape(H, W), normal=rng.normal(H * W * 3, 0, 1e-3).reshape(H, W, 3),
               median=rng.normal(H * W, 0, 1e-3).reshape(H, W), dist=rng.normal(H * W, 0, 1e-2).reshape(H, W))
-    g_o = orc.raster_bwd(proj, bins, fwd, ocam, scene.background, up["img"], up["depth"], up["alpha"], up["normal"],
-                         up["median"], up["dist"])
+    g_o, a_o = orc.raster_bwd(proj, bins, fwd, ocam, scene.background, up["img"], up["depth"], up["alpha"],
+                              up["normal"], up["median"], up["dist"], with_abs=True)
     dev = {k: _device(v) for k, v in up.items()}
     g16 = E.DeviceArray.zeros((scene.n, 16))
     E.check(E.lib().msplat_hip_raster_bwd(dev["img"].ptr, dev["depth"].ptr, dev["alpha"].ptr, dev["normal"].ptr,
                                           dev["median"].ptr, dev["dist"].ptr, g16.ptr))
-    _grad_close(g16.numpy(), g_o, "grads16 with all upstream gradients")
+    grad_close(g16.numpy(), g_o, a_o, "grads16 with all upstream gradients")
 
 
 @pytest.mark.parametrize("name", list(SCENES))
@@ -365,17 +359,12 @@ def test_train_step_matches_oracle(orc, eng):
     # dL/dtransMat through the accessor) against the golden model's raster
     # backward of the same forward and loss gradient
     _, dL_o, _, _ = orc.loss_fwd_bwd(full_o["out_img"], gt)
-    g_o = orc.raster_bwd(proj_o, bins_o, full_o, ocam, scene.background, dL_o)
-    _grad_close(E.last("grads16", (scene.n, 16)), g_o, "train step grads16")
+    g_o, a_o = orc.raster_bwd(proj_o, bins_o, full_o, ocam, scene.background, dL_o, with_abs=True)
+    grad_close(E.last("grads16", (scene.n, 16)), g_o, a_o, "train step grads16")
     got = ds.host_params()
     names = list(got)
-    for k, p_o, p0, lr in zip(names, params, scene.params(), D.LR_INIT):
-        diff = np.abs(got[k].astype(np.float64) - p_o)
-        frac = float((diff <= 1e-5).mean())
-        assert frac >= 0.999, (k, frac, diff.max())
-        # the few others are splats whose gradient is atomic-order noise near
-        # zero; Adam's first step moves any element by at most lr
-        assert diff.max() <= 2.0 * lr + 1e-6, (k, diff.max())
+    noise = param_grad_noise(orc, _params(scene), ocam, 3, 3, proj_o["radii"], g_o, a_o)
+    post_adam_close(names, [got[k] for k in names], params, [m.numpy() for m in ds.exp_avg], m6, noise, D.LR_INIT)
     for k in stats:
         got_s = {"grad_norm": ds.grad_norm, "vis": ds.vis, "max2d": ds.max2d}[k].numpy()
         if k == "vis" or k == "max2d":

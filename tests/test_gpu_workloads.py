@@ -1,10 +1,12 @@
 """The benchmark workloads at their full sizes on the GPU.
 
-The golden model finishes the 500k-splat train step at 1297x840 in seconds,
-so that step is compared with it directly (the bars of
-test_train_step_matches_oracle).  At 1M splats / 1920x1080 (the overflow
-workload, tiles far above 2048 entries) and 3M splats / 5187x3361 (the
-headline step) the checks are properties that do not depend on size:
+Each workload's full train step is compared with the golden model on the
+same inputs (the headline 3M-splat step takes the golden model about 20 s
+on the box's host cores), stage by stage: tile offsets and ids, the image,
+the loss, the raster gradients and the post-Adam parameters (the bars of
+tests/parity.py).  Besides, at 1M splats / 1920x1080 (the overflow
+workload, tiles far above 2048 entries) and 3M splats / 5187x3361 the
+binning is checked against properties that do not depend on the oracle:
   * every tile's entry count equals the number of visible splats whose tile
     rectangle covers it (a 2D difference array over the rectangles),
   * every entry's tile lies in its splat's rectangle,
@@ -132,32 +134,57 @@ def test_headline_workload_full_size(orc, eng):
     _full_step_finite(ds, scene, cam)
 
 
-def test_train_workload_matches_oracle_full_size(orc, eng):
-    """One full train step of the 500k-splat workload at 1297x840 against
-    the golden model: intersection count, image (bit-exact), loss (1e-5
-    relative) and post-Adam parameters (99.9% within 1e-5)."""
-    scene = S.make_scene(2, num_cameras=2)
-    print(f"[workload] {scene.name}", flush=True)
-    target = scene.jittered(0.01, 4)
-    ocam, _, _, tf = orc.render(target, 0)
-    gt = tf["out_img"]
+@pytest.mark.parametrize("workload", [2, 3, 4], ids=["500k-1297x840", "3M-5187x3361", "1M-overflow-1920x1080"])
+def test_full_step_matches_oracle_full_size(workload, orc, eng):
+    """One full train step of a benchmark workload at its full size against
+    the golden model on the same inputs: intersection count, tile offsets and
+    per-tile ids bit-exact, the image bit-exact, the loss to 1e-5 relative,
+    the raster gradients per element within their summation bound, and the
+    post-Adam parameters within the range that bound permits (1e-5 wherever
+    the gradient is resolved)."""
+    from parity import grad_close, param_grad_noise, post_adam_close
+
+    scene = S.make_scene(workload, num_cameras=2)
+    print(f"[full step] {scene.name}", flush=True)
+    c = scene.cameras[0]
+    # the target: the GPU render of the jittered scene (the forward is
+    # bit-identical to the golden model's, checked above and in the parity suite)
+    tgt = D.DeviceScene(scene.jittered(0.01, 4))
+    d_gt = D.render_to_device(tgt, tgt.camera(c))
+    del tgt
+    gt = d_gt.numpy().reshape(c.height, c.width, 3)
+    ds = D.DeviceScene(scene)
+    loss, nis = D.train_step(ds, ds.camera(c), d_gt)
+    g_off = E.last("tile_offsets")
+    g_ids = E.last("gaussian_ids")
+    g_img = E.last("out_img", (c.height, c.width, 3))
+    g_16 = E.last("grads16", (scene.n, 16))
+    got = ds.host_params()
+    got_m = [m.numpy() for m in ds.exp_avg]
+    del ds
+    print(f"[full step] gpu loss {loss:.6f}, {nis} intersections; running the golden model", flush=True)
+    ocam = orc.prepare_cam(c.cam_to_world, c.fx, c.fy, c.cx, c.cy, c.width, c.height)
     params = [p.copy() for p in scene.params()]
     m6 = [np.zeros_like(p) for p in params]
     v6 = [np.zeros_like(p) for p in params]
     stats = dict(grad_norm=np.zeros(scene.n, np.float32), vis=np.zeros(scene.n, np.float32),
                  max2d=np.zeros(scene.n, np.float32))
-    loss_o, img_o, _, nis_o = orc.train_step(params, m6, v6, ocam, scene.background, gt, 3, 3, D.LR_INIT, 1, stats)
-    ds = D.DeviceScene(scene)
-    loss, nis = D.train_step(ds, ds.camera(scene.cameras[0]), _device(gt))
-    print(f"[workload] loss {loss:.6f} oracle {loss_o:.6f}, {nis} intersections", flush=True)
+    loss_o, img_o, stage_ms, nis_o = orc.train_step(params, m6, v6, ocam, scene.background, gt, scene.sh_degree,
+                                                    scene.sh_degree, D.LR_INIT, 1, stats, detail="grads")
+    det = stats.pop("detail")
+    print(f"[full step] oracle loss {loss_o:.6f}, {nis_o} intersections, {sum(stage_ms) / 1e3:.1f} s", flush=True)
     assert nis == nis_o
+    assert np.array_equal(g_off, det["tile_offsets"]), "tile offsets differ"
+    assert np.array_equal(g_ids, det["ids"]), "per-tile sorted ids differ"
+    assert np.array_equal(g_img, img_o), f"image differs in {int((g_img != img_o).sum())} entries"
     assert abs(loss - loss_o) <= 1e-5 * abs(loss_o)
-    assert np.array_equal(E.last("out_img", img_o.shape), img_o)
-    for name, p_o, lr in zip(D.GROUPS, params, D.LR_INIT):
-        got = ds.host_params()[name].astype(np.float64)
-        diff = np.abs(got - p_o)
-        assert float((diff <= 1e-5).mean()) >= 0.999, (name, float((diff <= 1e-5).mean()))
-        assert diff.max() <= 2.0 * lr + 1e-6, (name, diff.max())
+    grad_close(g_16, det["grads16"], det["grads16_abs"], f"{scene.name} grads16")
+    pre = dict(means=scene.means, scales=scene.scales, quats=scene.quats, opacities=scene.opacities,
+               features_dc=scene.features_dc, features_rest=scene.features_rest)
+    radii = orc.project_fwd(pre, ocam, scene.sh_degree, scene.sh_degree)["radii"]
+    noise = param_grad_noise(orc, pre, ocam, scene.sh_degree, scene.sh_degree, radii, det["grads16"],
+                             det["grads16_abs"])
+    post_adam_close(D.GROUPS, [got[k] for k in D.GROUPS], params, got_m, m6, noise, D.LR_INIT)
 
 
 def test_densify_cycle_bitexact(orc, eng):
