@@ -224,6 +224,74 @@ def test_raster_forward_matches_fp64_compositing(orc):
     assert np.abs(fwd["out_distortion"] - outs["distortion"]).max() < 1e-5
 
 
+def _fp64_pixel(px, py, T, xy, opac_logit, color_raw, bg, near=0.2):
+    """Vectorised fp64 front-to-back compositing of one pixel over splats in
+    list order (the rules of refmath.composite): returns (colour, number
+    blended, smallest relative margin of any alpha / termination decision)."""
+    k = T[:, 0] - px * T[:, 2]
+    l = T[:, 1] - py * T[:, 2]
+    det = k[:, 0] * l[:, 1] - k[:, 1] * l[:, 0]
+    ok = det != 0.0
+    det = np.where(ok, det, 1.0)
+    u = (-k[:, 2] * l[:, 1] + k[:, 1] * l[:, 2]) / det
+    v = (-k[:, 0] * l[:, 2] + k[:, 2] * l[:, 0]) / det
+    d = xy - np.array([px, py])
+    rho = np.minimum(u * u + v * v, 2.0 * (d * d).sum(1))
+    depth = T[:, 2, 0] * u + T[:, 2, 1] * v + T[:, 2, 2]
+    alpha = np.minimum(0.99, 1.0 / (1.0 + np.exp(-opac_logit)) * np.exp(-0.5 * rho))
+    thr = 1.0 / 255.0
+    use = ok & (depth >= near) & (alpha >= thr)
+    a = np.where(use, alpha, 0.0)
+    Tb = np.concatenate([[1.0], np.cumprod(1.0 - a)[:-1]])  # transmittance before each splat
+    stop = use & (Tb * (1.0 - a) <= 1e-4)
+    end = int(np.argmax(stop)) if stop.any() else len(a)
+    w = (a * Tb)[:end]
+    col = (np.maximum(color_raw[:end] + 0.5, 0.0) * w[:, None]).sum(0) + bg * Tb[end] if end < len(a) else \
+        (np.maximum(color_raw + 0.5, 0.0) * w[:, None]).sum(0) + bg * np.prod(1.0 - a)
+    margins = [np.abs(alpha[ok & (depth >= near)] - thr).min(initial=1.0) / thr]
+    if use.any():
+        margins.append((np.abs(Tb * (1.0 - a) - 1e-4)[use]).min() / 1e-4)
+    return col, int(use[:end].sum()), min(margins)
+
+
+def test_raster_forward_matches_fp64_compositing_deep_lists(orc):
+    """Pixels that blend hundreds of splats: the golden model's fp32
+    compositing (the kernels' arithmetic) against fp64 compositing of the
+    same splats, to the 1e-4 image bar.  Pixels where any alpha or
+    termination decision lies within 1e-5 relative of its threshold (a
+    decision fp32 rounding may flip) are excluded and counted."""
+    from msplat import synthetic as S
+    rng = np.random.default_rng(3)
+    n = 20_000
+    scene = S.make_scene(1, n=n, width=64, height=48)
+    scene.means[:] = rng.uniform(-1.2, 1.2, (n, 3)).astype(np.float32)
+    scene.scales[:] = rng.normal(-1.6, 0.2, (n, 2)).astype(np.float32)
+    scene.opacities[:] = rng.normal(-4.3, 0.3, (n, 1)).astype(np.float32)
+    cam, proj, bins, fwd = orc.render(scene)
+    H, W = cam.height, cam.width
+    pix = rng.choice(H * W, 300, replace=False)
+    diffs, blended, skipped = [], [], 0
+    for p in pix:
+        py, px = divmod(int(p), W)
+        t = (py // 16) * cam.tiles_x + px // 16
+        lst = bins["ids"][bins["tile_offsets"][t]:bins["tile_offsets"][t + 1]]
+        T = proj["transmats"][lst].reshape(-1, 3, 3).astype(np.float64)
+        col, nb, margin = _fp64_pixel(px, py, T, proj["xys"][lst].astype(np.float64),
+                                      proj["normal_opac"][lst, 3].astype(np.float64),
+                                      proj["colors"][lst].astype(np.float64), scene.background.astype(np.float64))
+        if margin < 1e-5:
+            skipped += 1
+            continue
+        diffs.append(np.abs(fwd["out_img"][py, px] - col).max())
+        blended.append(nb)
+    blended = np.array(blended)
+    print(f"[deep] {len(diffs)} pixels, blended splats median {np.median(blended):.0f} max {blended.max()}, "
+          f"max |diff| {max(diffs):.3g}, {skipped} pixels at a threshold tie")
+    assert np.median(blended) >= 100  # realistic list depth
+    assert skipped <= 6
+    assert max(diffs) < 1e-4
+
+
 def test_raster_single_fronto_parallel_splat_closed_form(orc):
     """A splat facing the camera centred on a pixel: alpha there is
     min(0.99, sigmoid(o)) and the pixel is c*alpha + bg*(1-alpha)."""
