@@ -1,19 +1,30 @@
-"""Benchmark: the full 2DGS training step (projection + SH, binning, per-tile
-sort, rasterize, SSIM + L1, backward, fused Adam on six groups) on one MI355X.
+"""Benchmark: the 2DGS training step (projection + SH, binning, per-tile
+sort, rasterize, SSIM + L1, backward, fused Adam on six groups) on one
+MI355X, for every synthetic workload.
 
-    python bench.py [--steps K] [--warmup W] [--workload 3] [--gpus 1]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-configs] [--no-cpu-baseline]
 
-Default workload: 3M splats, SH degree 3, 5187x3361 (the train-step
-configuration of the headline metric).  Inputs are synthetic (seeded blob
-mixture, 32 orbit cameras; targets are renders of the scene with jittered
-means) and resident in HBM before the timed region.  Prints ONE JSON line.
+The headline line (`value`) is the train-step throughput of the 3M-splat,
+5187x3361, SH-degree-3 workload; `configs` adds the other workloads:
+  C1 forward-16k-256        render FPS
+  C2 train-500k-1297x840    train steps/s, render FPS
+  C3 train-3M-5187x3361     (the headline) + render FPS through the C ABI
+  C4 overflow-1M-1920x1080  train steps/s, render FPS
+  C5 densify-200k-1297x840  1500 steps with densification every 100
+each next to the golden model (scalar C++, OpenMP) timed on this host.
+Inputs are synthetic (seeded; targets are renders of the scene with
+jittered means) and resident in HBM before every timed region.  Prints ONE
+JSON line.
 """
 from __future__ import annotations
 
 import argparse
+import ctypes as C
+import gc
 import json
 import os
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -24,57 +35,343 @@ sys.path.insert(0, str(REPO / "msplat-ios_amd"))
 
 METRIC = "train steps/s @3M splats 5187x3361; render FPS; % HBM peak per kernel"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+# Issue cost of a simple VALU instruction (v_fma_f32 class) per wave64 and
+# SIMD, measured on gfx950 with 8 waves per SIMD and independent chains;
+# 1024 SIMDs (256 CUs x 4) give the issue peak.
+VALU_NS_PER_INST = 1.3
+VALU_PEAK_GIPS = 1024 / VALU_NS_PER_INST
+LR = (0.00016, 0.005, 0.001, 0.0025, 0.000125, 0.05)
+BOUND = {"project_fwd": "hbm", "tile_scan": "latency", "scatter_sort": "hbm", "raster_fwd": "valu",
+         "ssim_l1": "valu", "raster_bwd": "valu", "project_bwd_adam": "hbm"}
 
 
 def algorithmic_bytes(stage: str, N: int, I: int, P: int, T: int) -> float:
-    """Compulsory HBM bytes of one launch of each stage of a fused fp32 2DGS
-    step (N splats, I tile intersections, P pixels, T tiles): projection
-    232 B in + 80 B out per splat; binning 32 B per splat + 8 B per
-    intersection + 12 B per tile, sorting 12 B per intersection + 8 B per
-    tile; raster forward 76 B per intersection + 20 B per pixel (the
-    training forward produces the image, the final transmittance and the
-    last contributor; the other per-pixel outputs are made on demand); SSIM + L1
-    36 B per pixel; raster backward 140 B per intersection + 16 B per pixel
-    (the final transmittance and dL/dimage) + 64 B per splat; projection
+    """Compulsory HBM bytes of one launch of each stage (fp32, 2DGS, SH
+    degree 3, fused dataflow; N splats, I tile intersections, P pixels, T
+    tiles): projection 232 B in + 80 B out per splat; binning 32 B per splat
+    + 8 B per intersection + 12 B per tile (count + scan + scatter), the
+    per-tile sort 12 B per intersection + 8 B per tile; raster forward 76 B
+    per intersection (id + record) + 60 B per pixel (the reference's eight
+    per-pixel outputs); SSIM + L1 36 B per pixel; raster backward 140 B per
+    intersection + 60 B per pixel + 64 B per splat (zero fill); projection
     backward fused with Adam 1716 B per splat."""
     return {
         "project_fwd": 312.0 * N,
         "tile_scan": 12.0 * T,
         "scatter_sort": 32.0 * N + 20.0 * I + 8.0 * T,
-        "raster_fwd": 76.0 * I + 20.0 * P,
+        "raster_fwd": 76.0 * I + 60.0 * P,
         "ssim_l1": 36.0 * P,
-        "raster_bwd": 140.0 * I + 16.0 * P + 64.0 * N,
+        "raster_bwd": 140.0 * I + 60.0 * P + 64.0 * N,
         "project_bwd_adam": 1716.0 * N,
     }.get(stage, 0.0)
 
 
-def measured_traffic(stage: str, workload: str):
-    """HBM bytes per launch of `stage` on `workload` from the committed
-    rocprofv3 --pmc summaries (FETCH_SIZE + WRITE_SIZE, scaled by the
-    copy-kernel calibration); None when no summary covers it."""
+def profile_record(kind: str, stage: str, workload: str):
+    """A `bench-<kind>:` record for (stage, workload) from the committed
+    rocprofv3 summaries under profiles/ (None when none covers it)."""
     for f in sorted((REPO / "profiles").glob("*.md")):
         for line in f.read_text().splitlines():
-            if line.startswith("bench-traffic:"):
+            if line.startswith(f"bench-{kind}:"):
                 rec = json.loads(line.split(":", 1)[1])
                 if rec.get("stage") == stage and rec.get("workload") == workload:
-                    return rec["bytes"]
+                    return rec
     return None
 
 
 def copy_calibration(mib: int) -> int:
-    """A plain device-to-device copy of `mib` MiB, three times: the reference
-    kernel whose FETCH_SIZE / WRITE_SIZE counters calibrate the HBM traffic
-    figures (each launch reads and writes exactly mib MiB)."""
-    import torch
+    """A plain device-to-device copy of `mib` MiB through the engine, three
+    times: the kernel whose FETCH_SIZE / WRITE_SIZE counters calibrate the
+    HBM traffic figures (each launch reads and writes exactly mib MiB)."""
+    from msplat import _engine as E
 
-    n = mib * (1 << 20) // 4
-    src = torch.ones(n, dtype=torch.float32, device="cuda")
-    dst = torch.empty_like(src)
+    E.init()
+    n = mib * (1 << 20)
+    src = E.DeviceArray((n,), np.uint8)
+    dst = E.DeviceArray((n,), np.uint8)
+    E.check(E.lib().msplat_hip_memset(src.ptr, 1, n))
     for _ in range(3):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    print(json.dumps({"copy_calibration_bytes": n * 4, "launches": 3}))
+        E.check(E.lib().msplat_hip_copy(dst.ptr, src.ptr, n))
+    E.sync()
+    print(json.dumps({"copy_calibration_bytes": n, "launches": 3}))
     return 0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ GPU --
+def gpu_train(workload: int, steps: int, warmup: int, render_frames: int, counters: bool):
+    """Train steps (timed between synchronisations, HIP events per stage)
+    and device-resident render frames of one workload."""
+    from msplat import _engine as E
+    from msplat import device as D
+    from msplat import synthetic as S
+
+    scene = S.make_scene(workload)
+    ds = D.DeviceScene(scene)
+    tgt = D.DeviceScene(scene.jittered(0.01, 0xC0FFEE + 100 + workload))
+    cams = [ds.camera(c) for c in scene.cameras]
+    gts = [D.render_to_device(tgt, c) for c in cams]
+    del tgt
+    E.sync()
+    for k in range(warmup):
+        D.train_step(ds, cams[k % len(cams)], gts[k % len(cams)])
+    E.enable_timing(True)
+    E.sync()
+    stage_sum: dict[str, float] = {}
+    isect, losses = [], []
+    t0 = time.perf_counter()
+    for k in range(steps):
+        ci = (warmup + k) % len(cams)
+        loss, nis = D.train_step(ds, cams[ci], gts[ci])
+        losses.append(loss)
+        isect.append(nis)
+        for name, ms in E.stage_times().items():
+            stage_sum[name] = stage_sum.get(name, 0.0) + ms
+    E.sync()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / steps
+    E.enable_timing(False)
+    out = dict(scene=scene, ds=ds, cams=cams, ms_per_step=ms_per_step, losses=losses,
+               isect=float(np.mean(isect)), stage_ms={k: v / steps for k, v in stage_sum.items()})
+    if counters:
+        # two untimed steps with the raster work counters on
+        E.enable_timing(False, pairs=True)
+        pairs = []
+        for k in range(2):
+            ci = (warmup + steps + k) % len(cams)
+            D.train_step(ds, cams[ci], gts[ci])
+            pairs.append(E.raster_counts())
+        E.enable_timing(False)
+        out["raster_counts"] = {key: int(np.mean([p[key] for p in pairs])) for key in pairs[0]}
+    del gts
+    out["render_ms"] = gpu_render_ms(ds, cams, render_frames)
+    return out
+
+
+def gpu_render_ms(ds, cams, frames: int) -> float:
+    """Device-resident render-only frames (the image stays in HBM)."""
+    from msplat import _engine as E
+    from msplat import device as D
+
+    for k in range(3):
+        D.render(ds, cams[k % len(cams)], outputs=())
+    E.sync()
+    n = E.C.c_int64()
+    t0 = time.perf_counter()
+    for k in range(frames):
+        E.check(E.lib().msplat_hip_render(E.C.byref(cams[k % len(cams)]), E.C.byref(ds.gaussians),
+                                          ds.background.ptr, E.C.byref(n)))
+    E.sync()
+    return (time.perf_counter() - t0) * 1e3 / max(frames, 1)
+
+
+def gpu_render_to_buffer_ms(scene, frames: int) -> float:
+    """Render frames through the reference's public path: a Trainer (C ABI)
+    holding the scene (loaded from a .msplat checkpoint) renders poses with
+    msplat_trainer_render_pose_to_buffer into a host RGBA8 buffer, i.e.
+    render + RGBA8 conversion + the copy to host memory."""
+    from msplat import capi
+    from msplat import formats
+
+    import shutil
+
+    L = capi.lib()
+    c0 = scene.cameras[0]
+    need = scene.n * 58 * 4 * 3 + (1 << 28)  # parameters and both moments
+    dirs = [d for d in ("/dev/shm", tempfile.gettempdir(), str(REPO / "_build")) if os.path.isdir(d)]
+    dirs = [d for d in dirs if shutil.disk_usage(d).free > need]
+    if not dirs:
+        raise RuntimeError(f"no directory with {need >> 20} MiB free for the checkpoint")
+    with tempfile.TemporaryDirectory(dir=dirs[0]) as td:
+        ckpt = os.path.join(td, "scene.msplat")
+        params = dict(zip(formats.GROUPS, scene.params()))
+        formats.write_checkpoint(ckpt, params, scene.sh_degree, step=30000)
+        img = np.zeros((c0.height, c0.width, 3), np.float32)
+        cam = capi.CameraImage(width=c0.width, height=c0.height, fx=c0.fx, fy=c0.fy, cx=c0.cx, cy=c0.cy)
+        cam.camToWorld[:] = [float(v) for v in c0.cam_to_world.reshape(-1)]
+        cam.rgb = img.ctypes.data
+        pts = np.ascontiguousarray(scene.means[:1000], np.float32)
+        rgb = np.full((len(pts), 3), 128, np.uint8)
+        dset = L.msplat_dataset_create_from_memory(C.byref(cam), 1, pts.ctypes.data, rgb.ctypes.data, len(pts),
+                                                   False, 8)
+        if not dset:
+            raise RuntimeError(capi.last_error())
+        cfg = capi.default_config()
+        cfg.numDownscales = 0
+        tr = L.msplat_trainer_create(dset, cfg)
+        if not tr:
+            raise RuntimeError(capi.last_error())
+        try:
+            if L.msplat_trainer_load_checkpoint(tr, ckpt.encode()) < 0:
+                raise RuntimeError(capi.last_error())
+            assert L.msplat_trainer_splat_count(tr) == scene.n
+            buf = np.zeros((c0.height, c0.width, 4), np.uint8)
+            w, h = C.c_int(), C.c_int()
+            poses = [np.ascontiguousarray(c.cam_to_world, np.float32).reshape(-1) for c in scene.cameras]
+            fp = C.POINTER(C.c_float)
+            for k in range(2):
+                L.msplat_trainer_render_pose_to_buffer(tr, poses[k].ctypes.data_as(fp), 0, buf.ctypes.data,
+                                                       C.byref(w), C.byref(h))
+            t0 = time.perf_counter()
+            for k in range(frames):
+                L.msplat_trainer_render_pose_to_buffer(tr, poses[k % len(poses)].ctypes.data_as(fp), 0,
+                                                       buf.ctypes.data, C.byref(w), C.byref(h))
+            ms = (time.perf_counter() - t0) * 1e3 / max(frames, 1)
+            assert (w.value, h.value) == (c0.width, c0.height)
+        finally:
+            L.msplat_trainer_destroy(tr)
+            L.msplat_dataset_destroy(dset)
+    return ms
+
+
+def gpu_densify(total_steps: int = 1500, refine_every: int = 100, max_splats: int = 2_000_000,
+                cap: int = 4_000_000):
+    """The densification workload: training from 200k blob splats at
+    1297x840 with Model::afterTrain's schedule (densify every 100 steps from
+    step 200, the opacity reset at step 100), grad threshold 2e-4 and cull
+    opacity 0.005, and its capacity rule with the 250k cap raised to 2M (no
+    densification once N reaches it).  Returns per-cycle timings."""
+    from msplat import _engine as E
+    from msplat import device as D
+    from msplat import synthetic as S
+
+    scene = S.make_scene(5)
+    ds = D.CapacityScene(scene, cap)
+    tgt = D.DeviceScene(scene.jittered(0.01, 0xC0FFEE + 105))
+    gts = [D.render_to_device(tgt, tgt.camera(c)) for c in scene.cameras]
+    del tgt
+    cams = [ds.camera(c) for c in scene.cameras]
+    rng = S.SplitMix64(0xC0FFEE + 5)
+    half = 0.5 * max(scene.cameras[0].width, scene.cameras[0].height)
+    E.sync()
+    cycles = []
+    t_cycle = time.perf_counter()
+    t_all = t_cycle
+    for step in range(1, total_steps + 1):
+        ci = (step - 1) % len(cams)
+        D.train_step(ds, cams[ci], gts[ci])
+        dens, reset = D.densify_schedule(step, ds.n, max_splats, refine_every, num_cameras=len(cams))
+        if dens:
+            E.sync()
+            n0 = ds.n
+            rs = rng.normal(2 * n0 * 3).reshape(2 * n0, 3)
+            td = time.perf_counter()
+            ds.densify(rs, half, grad_thresh=0.0002, cull_alpha=0.005)
+            dms = (time.perf_counter() - td) * 1e3
+            now = time.perf_counter()
+            cycles.append(dict(step=step, n_before=n0, n_after=ds.n, densify_ms=round(dms, 3),
+                               cycle_ms=round((now - t_cycle) * 1e3, 2)))
+            log(f"densify at step {step}: {n0} -> {ds.n} ({cycles[-1]['cycle_ms']:.0f} ms cycle)")
+            t_cycle = now
+        if reset:
+            ds.reset_opacity()
+        if step % refine_every == 0:
+            ds.reset_stats()
+    E.sync()
+    total_ms = (time.perf_counter() - t_all) * 1e3
+    return dict(scene=scene, cycles=cycles, total_ms=total_ms, n_final=ds.n)
+
+
+# ------------------------------------------------------------------ CPU --
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _oracle():
+    sys.path.insert(0, str(REPO))
+    from oracle import oracle as O
+    return O
+
+
+def cpu_train_step_s(O, scene, target_img, reps: int, warm_scene=None, warm_img=None, fwd_s=None) -> list[float]:
+    """Seconds per golden-model train step (camera 0), `reps` timed steps
+    after one warm-up step (on warm_scene when given, e.g. a smaller one).
+    fwd_s (a list) receives each timed step's forward seconds (projection,
+    binning and sort, rasterize: a render)."""
+    c = scene.cameras[0]
+    cam = O.prepare_cam(c.cam_to_world, c.fx, c.fy, c.cx, c.cy, c.width, c.height)
+
+    def one(sc, img, cm):
+        params = [p.copy() for p in sc.params()]
+        m6 = [np.zeros_like(p) for p in params]
+        v6 = [np.zeros_like(p) for p in params]
+        stats = dict(grad_norm=np.zeros(sc.n, np.float32), vis=np.zeros(sc.n, np.float32),
+                     max2d=np.zeros(sc.n, np.float32))
+        t0 = time.perf_counter()
+        _, _, stage_ms, _ = O.train_step(params, m6, v6, cm, sc.background, img, sc.sh_degree, sc.sh_degree, LR,
+                                         1, stats)
+        return time.perf_counter() - t0, float(sum(stage_ms[:3])) / 1e3
+
+    if warm_scene is not None:
+        wc = warm_scene.cameras[0]
+        one(warm_scene, warm_img, O.prepare_cam(wc.cam_to_world, wc.fx, wc.fy, wc.cx, wc.cy, wc.width, wc.height))
+    else:
+        one(scene, target_img, cam)
+    runs = [one(scene, target_img, cam) for _ in range(reps)]
+    if fwd_s is not None:
+        fwd_s.extend(r[1] for r in runs)
+    return [r[0] for r in runs]
+
+
+def cpu_render_s(O, scene, reps: int) -> list[float]:
+    O.render(scene, 0)
+    out = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        O.render(scene, 0)
+        out.append(time.perf_counter() - t0)
+    return out
+
+
+def cpu_cell(O, per_s: list[float], unit: str, sample: str) -> dict:
+    med = float(np.median(per_s))
+    return {"value": round(1.0 / med, 5), "unit": unit, "cores": O.num_threads(), "kind": "port",
+            "cpu": cpu_model(), "median_s": round(med, 4), "runs_s": [round(x, 3) for x in per_s],
+            "sample": sample}
+
+
+# ----------------------------------------------------------------- main --
+def headline_roofline(kernels: dict, workload: str) -> dict:
+    """The dominant kernel against the bound that limits it: VALU issue for
+    the rasterizers (executed VALU instructions per launch from the
+    committed rocprofv3 counters over the HIP-event duration, against
+    1024 SIMDs / 1.3 ns), with its HBM fraction by the algorithmic bytes
+    beside it."""
+    dominant = max(kernels, key=lambda k: kernels[k]["ms"])
+    dk = kernels[dominant]
+    traffic = profile_record("traffic", dominant, workload)
+    cnt = profile_record("counters", dominant, workload)
+    hbm = {"achieved": dk["GB_per_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dk["frac_hbm_peak"]}
+    if BOUND.get(dominant) == "valu" and cnt is not None:
+        gips = cnt["valu_insts"] / (dk["ms"] * 1e-3) / 1e9
+        return {"kernel": dominant, "bound": "valu", "achieved": round(gips, 1), "peak": round(VALU_PEAK_GIPS, 1),
+                "unit": "G VALU instructions/s", "frac": round(gips / VALU_PEAK_GIPS, 4),
+                "traffic": traffic["bytes"] if traffic else None, "hbm": hbm,
+                "basis": f"{cnt['kernel']}: {cnt['valu_insts']:.4g} VALU instructions per launch (rocprofv3 "
+                         f"SQ_INSTS_VALU, profiles/), {VALU_NS_PER_INST} ns per instruction per SIMD x 1024 SIMDs"}
+    return {"kernel": dominant, "bound": "hbm", "achieved": dk["GB_per_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": dk["frac_hbm_peak"], "traffic": traffic["bytes"] if traffic else None}
+
+
+def kernel_table(stage_ms: dict, N: int, I: int, P: int, T: int, workload: str) -> dict:
+    kernels = {}
+    for name, ms in stage_ms.items():
+        b = algorithmic_bytes(name, N, I, P, T)
+        gbs = b / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+        row = {"ms": round(ms, 4), "bound": BOUND.get(name, "hbm"), "algorithmic_GB": round(b / 1e9, 4),
+               "GB_per_s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        cnt = profile_record("counters", name, workload)
+        if cnt is not None and ms > 0:
+            row["frac_valu_issue"] = round(cnt["valu_insts"] * VALU_NS_PER_INST * 1e-9 / (ms * 1e-3 * 1024), 4)
+        kernels[name] = row
+    return kernels
 
 
 def main() -> int:
@@ -84,10 +381,13 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", type=int, default=3)
     ap.add_argument("--render-frames", type=int, default=20)
+    ap.add_argument("--no-configs", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-buffer-render", action="store_true",
+                    help="skip the render-to-host-buffer frames (e.g. under a profiler)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the training step is single-GPU (one camera per step); "
@@ -95,137 +395,150 @@ def main() -> int:
         return 2
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
+    os.environ.setdefault("OMP_NUM_THREADS", str(args.cpu_threads))
 
     from msplat import _engine as E
-    from msplat import device as D
     from msplat import synthetic as S
 
     E.init()
-    t0 = time.time()
-    scene = S.make_scene(args.workload)
-    target_scene = scene.jittered(0.01, 0xC0FFEE + 100 + args.workload)
-    print(f"[bench] scene {scene.name}: n={scene.n} generated in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
-    ds = D.DeviceScene(scene)
-    tgt = D.DeviceScene(target_scene)
-    cams = [ds.camera(c) for c in scene.cameras]
-    gts = [D.render_to_device(tgt, c) for c in cams]
-    del tgt
-    E.sync()
+    # ---- headline: C3 ----
+    h = gpu_train(3, args.steps, args.warmup, args.render_frames, counters=True)
+    scene = h["scene"]
     W, H = scene.cameras[0].width, scene.cameras[0].height
     P = W * H
-    T = cams[0].tiles_x * cams[0].tiles_y
-    print(f"[bench] targets rendered; warmup {args.warmup}", file=sys.stderr, flush=True)
-
-    for k in range(args.warmup):
-        D.train_step(ds, cams[k % len(cams)], gts[k % len(cams)])
-    # HIP events on the engine stream bracket every stage of every timed step
-    E.enable_timing(True)
-    E.sync()
-    stage_sum: dict[str, float] = {}
-    isect = []
-    pairs = []
-    losses = []
-    t_start = time.perf_counter()
-    for k in range(args.steps):
-        ci = (args.warmup + k) % len(cams)
-        loss, nis = D.train_step(ds, cams[ci], gts[ci])
-        losses.append(loss)
-        isect.append(nis)
-        for name, ms in E.stage_times().items():
-            stage_sum[name] = stage_sum.get(name, 0.0) + ms
-    E.sync()
-    t_end = time.perf_counter()
-    ms_per_step = (t_end - t_start) * 1e3 / args.steps
-    print(f"[bench] {args.steps} steps: {ms_per_step:.2f} ms/step, loss {losses[0]:.4f} -> {losses[-1]:.4f}",
-          file=sys.stderr, flush=True)
-
-    # two untimed steps with the raster pair counter on (work per kernel)
-    E.enable_timing(False, pairs=True)
-    for k in range(2):
-        ci = (args.warmup + args.steps + k) % len(cams)
-        D.train_step(ds, cams[ci], gts[ci])
-        pairs.append(E.raster_counts())
-
-    # render-only frames (the FPS half of the metric)
-    E.enable_timing(False)
-    for k in range(3):
-        D.render(ds, cams[k % len(cams)], outputs=())
-    E.sync()
-    r0 = time.perf_counter()
-    for k in range(args.render_frames):
-        n = E.C.c_int64()
-        E.check(E.lib().msplat_hip_render(E.C.byref(cams[k % len(cams)]), E.C.byref(ds.gaussians),
-                                          ds.background.ptr, E.C.byref(n)))
-    E.sync()
-    render_ms = (time.perf_counter() - r0) * 1e3 / max(args.render_frames, 1)
-
-    N = scene.n
-    I = float(np.mean(isect))
-    kernels = {}
-    for name, tot in stage_sum.items():
-        avg = tot / args.steps
-        b = algorithmic_bytes(name, N, int(I), P, T)
-        gbs = b / (avg * 1e-3) / 1e9 if avg > 0 else 0.0
-        kernels[name] = {"ms": round(avg, 4), "algorithmic_GB": round(b / 1e9, 4), "GB_per_s": round(gbs, 1),
-                         "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
-    dominant = max(kernels, key=lambda k: kernels[k]["ms"])
-    dk = kernels[dominant]
-    for key in ("pairs_evaluated", "pairs_blended", "log_entries", "visits", "visit_slots"):
-        kernels["raster_fwd"][key] = int(np.mean([c[key] for c in pairs]))
-
+    T = h["cams"][0].tiles_x * h["cams"][0].tiles_y
+    N, I = scene.n, h["isect"]
+    log(f"{scene.name}: {h['ms_per_step']:.3f} ms/step, render {h['render_ms']:.3f} ms")
+    kernels = kernel_table(h["stage_ms"], N, int(I), P, T, scene.name)
+    kernels["raster_fwd"].update(h["raster_counts"])
+    del h["ds"]
+    gc.collect()
+    buf_ms = None if args.no_buffer_render else gpu_render_to_buffer_ms(scene, max(args.render_frames // 2, 5))
+    if buf_ms:
+        log(f"{scene.name}: render_pose_to_buffer {buf_ms:.3f} ms")
     result = {
         "metric": METRIC,
-        "value": round(1000.0 / ms_per_step, 4),
+        "value": round(1000.0 / h["ms_per_step"], 4),
         "unit": "train steps/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 3),
+        "ms_per_step": round(h["ms_per_step"], 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": scene.name, "splats": N, "width": W, "height": H, "sh_degree": scene.sh_degree,
-                   "tiles": T, "intersections_mean": int(I), "cameras": len(cams),
+                   "tiles": T, "intersections_mean": int(I), "cameras": len(h["cams"]),
                    "device": E.device_name()},
-        "render_fps": round(1000.0 / render_ms, 2) if args.render_frames else None,
-        "render_ms": round(render_ms, 3),
+        "render_fps": round(1000.0 / h["render_ms"], 2),
+        "render_ms": round(h["render_ms"], 3),
+        "render_fps_to_buffer": round(1000.0 / buf_ms, 2) if buf_ms else None,
+        "render_ms_to_buffer": round(buf_ms, 3) if buf_ms else None,
         "kernels": kernels,
-        "roofline": {"kernel": dominant, "bound": "hbm", "achieved": dk["GB_per_s"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": dk["frac_hbm_peak"], "traffic": measured_traffic(dominant, scene.name)},
-        "loss_first_last": [round(losses[0], 6), round(losses[-1], 6)],
+        "roofline": headline_roofline(kernels, scene.name),
+        "loss_first_last": [round(h["losses"][0], 6), round(h["losses"][-1], 6)],
     }
+    del h
 
+    # ---- the other workloads ----
+    configs = {}
+    if not args.no_configs:
+        for wl, key in ((2, "C2"), (4, "C4")):
+            r = gpu_train(wl, max(args.steps, 30), args.warmup, args.render_frames, counters=False)
+            sc = r["scene"]
+            Tn = r["cams"][0].tiles_x * r["cams"][0].tiles_y
+            Pn = sc.cameras[0].width * sc.cameras[0].height
+            configs[key] = {"workload": sc.name, "splats": sc.n, "intersections_mean": int(r["isect"]),
+                            "train_steps_per_s": round(1000.0 / r["ms_per_step"], 3),
+                            "ms_per_step": round(r["ms_per_step"], 3),
+                            "render_fps": round(1000.0 / r["render_ms"], 2),
+                            "kernels": kernel_table(r["stage_ms"], sc.n, int(r["isect"]), Pn, Tn, sc.name)}
+            log(f"{sc.name}: {r['ms_per_step']:.3f} ms/step, render {r['render_ms']:.3f} ms")
+            del r
+            gc.collect()
+        from msplat import device as D
+        sc1 = S.make_scene(1)
+        ds1 = D.DeviceScene(sc1)
+        cams1 = [ds1.camera(c) for c in sc1.cameras]
+        r1 = gpu_render_ms(ds1, cams1, 200)
+        configs["C1"] = {"workload": sc1.name, "splats": sc1.n, "render_fps": round(1000.0 / r1, 1),
+                         "render_ms": round(r1, 4)}
+        log(f"{sc1.name}: render {r1:.4f} ms")
+        del ds1
+        d5 = gpu_densify()
+        cyc = d5["cycles"]
+        configs["C5"] = {"workload": d5["scene"].name, "steps": 1500, "max_splats": 2_000_000,
+                         "densify_cycles": len(cyc),
+                         "splats_start": d5["scene"].n, "splats_end": d5["n_final"],
+                         "total_s": round(d5["total_ms"] / 1e3, 3),
+                         "cycle_ms_mean": round(float(np.mean([c["cycle_ms"] for c in cyc])), 2),
+                         "densify_ms_mean": round(float(np.mean([c["densify_ms"] for c in cyc])), 3),
+                         "cycles": cyc}
+        log(f"{d5['scene'].name}: {d5['scene'].n} -> {d5['n_final']} splats in {d5['total_ms'] / 1e3:.2f} s")
+        gc.collect()
+        result["configs"] = configs
+
+    # ---- CPU baselines: the golden model on this host ----
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(scene, target_scene, args.cpu_threads)
+        O = _oracle()
+        from msplat import device as D
+        warm = S.make_scene(2, n=200_000)
+        warm_img = O.render(warm.jittered(0.01, 1), 0)[3]["out_img"]
+        gt3 = O.render(scene.jittered(0.01, 0xC0FFEE + 103), 0)[3]["out_img"]
+        fwd3 = []
+        runs = cpu_train_step_s(O, scene, gt3, args.cpu_reps, warm, warm_img, fwd3)
+        result["cpu_baseline"] = cpu_cell(O, runs, "train steps/s",
+                                          f"median of {len(runs)} full golden-model steps of {scene.name} "
+                                          f"(camera 0) after a warm-up step of 200k splats at 1297x840")
+        result["cpu_render_fps"] = cpu_cell(O, fwd3, "render FPS",
+                                            f"the forward stages (projection, binning + sort, rasterize) of the "
+                                            f"{len(fwd3)} timed steps")
+        log(f"cpu {scene.name}: {np.median(runs):.2f} s/step")
+        if configs:
+            for wl, key in ((2, "C2"), (4, "C4")):
+                sc = S.make_scene(wl, num_cameras=1)
+                gt = O.render(sc.jittered(0.01, 0xC0FFEE + 100 + wl), 0)[3]["out_img"]
+                runs = cpu_train_step_s(O, sc, gt, args.cpu_reps)
+                configs[key]["cpu_train"] = cpu_cell(O, runs, "train steps/s",
+                                                     f"median of {len(runs)} steps (camera 0) after one warm-up")
+                rr = cpu_render_s(O, sc, args.cpu_reps)
+                configs[key]["cpu_render"] = cpu_cell(O, rr, "render FPS", f"median of {len(rr)} renders")
+                log(f"cpu {sc.name}: {np.median(runs):.2f} s/step")
+            sc1 = S.make_scene(1)
+            rr = cpu_render_s(O, sc1, 10)
+            configs["C1"]["cpu_render"] = cpu_cell(O, rr, "render FPS", f"median of {len(rr)} renders")
+            # densify cycle: 100 golden-model steps + one compaction, from a
+            # timed step and a timed compaction at the starting size
+            sc5 = S.make_scene(5, num_cameras=1)
+            gt5 = O.render(sc5.jittered(0.01, 7), 0)[3]["out_img"]
+            step_s = float(np.median(cpu_train_step_s(O, sc5, gt5, 1)))
+            n5 = sc5.n
+            cap = 4 * n5  # the appended count reaches up to 4N
+            strides = [3, 2, 4, 3, 45, 1]
+            params = [np.zeros(cap * s, np.float32) for s in strides]
+            for p, a, s in zip(params, sc5.params(), strides):
+                p[: n5 * s] = a.reshape(-1)
+            m6 = [np.zeros(cap * s, np.float32) for s in strides]
+            v6 = [np.zeros(cap * s, np.float32) for s in strides]
+            rng = np.random.default_rng(5)
+            stats = dict(grad_norm=rng.uniform(0, 0.05, n5).astype(np.float32),
+                         vis=np.ones(n5, np.float32), max2d=rng.uniform(0, 0.1, n5).astype(np.float32))
+            rs = rng.normal(size=(2 * n5, 3)).astype(np.float32)
+            td = time.perf_counter()
+            O.densify(n5, cap, params, m6, v6, 45, stats, rs, grad_thresh=0.0002, cull_alpha=0.005,
+                      half_max_dim=648.5)
+            dens_s = time.perf_counter() - td
+            cyc_s = 100 * step_s + dens_s
+            configs["C5"]["cpu_cycle"] = {"value": round(1.0 / cyc_s, 6), "unit": "densify cycles/s",
+                                          "cores": O.num_threads(), "kind": "port", "cpu": cpu_model(),
+                                          "cycle_s": round(cyc_s, 2),
+                                          "sample": f"1 golden-model step ({step_s:.2f} s) and 1 compaction "
+                                                    f"({dens_s * 1e3:.0f} ms) at 200k splats, cycle = 100 steps "
+                                                    f"+ 1 compaction"}
     print(json.dumps(result))
     return 0
-
-
-def cpu_baseline(scene, target_scene, threads: int) -> dict:
-    """The golden model (scalar C++ restatement, OpenMP) timed on this host:
-    one full training step of the same workload on camera 0 (the target is
-    rendered by the golden model first, untimed)."""
-    os.environ["OMP_NUM_THREADS"] = str(threads)
-    sys.path.insert(0, str(REPO))
-    from oracle import oracle as O
-
-    c = scene.cameras[0]
-    cam = O.prepare_cam(c.cam_to_world, c.fx, c.fy, c.cx, c.cy, c.width, c.height)
-    gt = O.render(target_scene, 0)[3]["out_img"]
-    params = [p.copy() for p in scene.params()]
-    m6 = [np.zeros_like(p) for p in params]
-    v6 = [np.zeros_like(p) for p in params]
-    stats = dict(grad_norm=np.zeros(scene.n, np.float32), vis=np.zeros(scene.n, np.float32),
-                 max2d=np.zeros(scene.n, np.float32))
-    t0 = time.perf_counter()
-    loss, _, stage_ms, nis = O.train_step(params, m6, v6, cam, scene.background, gt, scene.sh_degree,
-                                          scene.sh_degree, (0.00016, 0.005, 0.001, 0.0025, 0.000125, 0.05), 1, stats)
-    dt = time.perf_counter() - t0
-    return {"value": round(1.0 / dt, 5), "unit": "train steps/s", "cores": O.num_threads(), "kind": "port",
-            "sample": f"1 full step of {scene.name} (camera 0, {nis} intersections) in {dt:.2f} s",
-            "stage_ms": [round(x, 1) for x in stage_ms[:7]]}
 
 
 if __name__ == "__main__":

@@ -146,6 +146,14 @@ int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g,
 int msplat_hip_render(const MsplatCamera *cam, const MsplatGaussians *g,
                       const float *background_dev, int64_t *num_isect_host);
 
+/* The RGBA8 conversion of Trainer::renderFromPoseToBuffer
+ * (core/src/msplat_api.mm:207-236, a host loop there): (uint8)(clamp(x, 0,
+ * 1) * 255) per channel, truncating, alpha 255, computed on the GPU from the
+ * [num_pixels,3] image img_dev; the 4-byte pixels are copied to rgba_host.
+ * Synchronous. */
+int msplat_hip_image_to_rgba8(const float *img_dev, int64_t num_pixels,
+                              uint8_t *rgba_host);
+
 /* msplat_fused_adam (bindings.h:135-140): one Adam step on n floats. */
 int msplat_hip_fused_adam(float *params_dev, const float *grads_dev,
                           float *exp_avg_dev, float *exp_avg_sq_dev,
@@ -156,7 +164,12 @@ int msplat_hip_fused_adam(float *params_dev, const float *grads_dev,
  * cull, stable compaction of the 18 capacity-sized buffers.  params[6],
  * exp_avg[6], exp_avg_sq[6] are the backing buffers (strides 3, 2, 4, 3,
  * fr_stride, 1); random_samples_dev is [2N,3].  Synchronous; returns the
- * new count in *new_count_host. */
+ * new count in *new_count_host.  The count after appending is N + 2 * splits
+ * + dups, up to 4N (a splat small in the world but wide on screen is both
+ * split and duplicated); when it exceeds capacity nothing is modified,
+ * *new_count_host receives the rows needed and MSPLAT_E_CAPACITY is
+ * returned, so the caller can grow the buffers and call again (the
+ * reference assumes 3N, msplat_metal.mm:1358, and overruns). */
 int msplat_hip_densify(int n, int capacity, float grad_thresh,
                        float size_thresh, float screen_thresh,
                        int check_screen, float cull_alpha_thresh,

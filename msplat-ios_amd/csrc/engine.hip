@@ -5,6 +5,7 @@
 // (core/metal/msplat_metal.mm:545-1594).
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -73,8 +74,9 @@ struct Engine {
     // materialised views
     DevBuf mat[MSPLAT_LAST_COUNT];
     // densify scratch
-    DevBuf dens_scratch[18], dens_flags, dens_scan;
+    DevBuf dens_scratch[18], dens_flags, dens_scan, dens_keep;
     DevBuf pair_counter;
+    DevBuf rgba;  // RGBA8 staging of msplat_hip_image_to_rgba8
     // state of the most recent forward
     int n = 0, W = 0, H = 0, tiles_x = 0, tiles_y = 0, K3 = 0;
     int64_t num_isect = 0;
@@ -499,7 +501,8 @@ void msplat_hip_cleanup(void) {
                      &E.stats, &E.big_list, &E.keys, &E.keys_tmp, &E.ids, &E.blend_log, &E.t_ckpt, &E.wave_cnt, &E.selfcheck, &E.out_img, &E.final_Ts,
                      &E.final_idx, &E.out_depth, &E.out_normal, &E.out_alpha, &E.out_median, &E.out_dist,
                      &E.dL_dimg, &E.gm1, &E.gs1, &E.gs12, &E.partials, &E.loss, &E.dmeans, &E.dscales,
-                     &E.dquats, &E.dmean2d, &E.dfdc, &E.dfrest, &E.dens_flags, &E.dens_scan, &E.pair_counter};
+                     &E.dquats, &E.dmean2d, &E.dfdc, &E.dfrest, &E.dens_flags, &E.dens_scan, &E.dens_keep, &E.pair_counter,
+                     &E.rgba};
     for (DevBuf *b : all) {
         if (b->p) (void)hipFree(b->p);
         *b = DevBuf{};
@@ -596,6 +599,24 @@ int msplat_hip_sync(void) {
     API_BEGIN
     ENSURE_INIT();
     HIPC(hipStreamSynchronize(g_eng.stream));
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_image_to_rgba8(const float *img, int64_t num_pixels, uint8_t *rgba_host) {
+    API_BEGIN
+    ENSURE_INIT();
+    if (num_pixels < 0 || (num_pixels > 0 && (!img || !rgba_host))) {
+        set_err("invalid rgba8 arguments");
+        return MSPLAT_E_ARG;
+    }
+    if (num_pixels == 0) return MSPLAT_OK;
+    Engine &E = g_eng;
+    CHECK(ensure(E.rgba, (size_t)num_pixels * 4));
+    mskern::launch_rgba8(E.stream, img, num_pixels, P<uint32_t>(E.rgba));
+    HIPC(hipGetLastError());
+    HIPC(hipMemcpyAsync(rgba_host, E.rgba.p, (size_t)num_pixels * 4, hipMemcpyDeviceToHost, E.stream));
+    HIPC(hipStreamSynchronize(E.stream));
     return MSPLAT_OK;
     API_END
 }
@@ -702,16 +723,15 @@ int msplat_hip_densify(int n, int capacity, float grad_thresh, float size_thresh
                        const float *random, int *new_count) {
     API_BEGIN
     ENSURE_INIT();
-    if (n < 0 || 3LL * n > capacity || fr_stride < 0 || !new_count) {
-        set_err("densify: 3*N (%lld) exceeds capacity %d or bad arguments", 3LL * n, capacity);
-        return MSPLAT_E_CAPACITY;
+    if (n < 0 || n > capacity || fr_stride < 0 || !new_count || !gnorm || !vis || !max2d || !random) {
+        set_err("densify: N (%d) exceeds capacity %d or bad arguments", n, capacity);
+        return MSPLAT_E_ARG;
     }
     if (n == 0) {
         *new_count = 0;
         return MSPLAT_OK;
     }
     Engine &E = g_eng;
-    const int worst = 3 * n;
     const int strides[6] = {3, 2, 4, 3, fr_stride, 1};
     mskern::DensifyArgs a{};
     a.n = n;
@@ -734,24 +754,43 @@ int msplat_hip_densify(int n, int capacity, float grad_thresh, float size_thresh
         a.params[gi] = params[gi];
         a.exp_avg[gi] = exp_avg[gi];
         a.exp_avg_sq[gi] = exp_avg_sq[gi];
-        for (int r = 0; r < 3; ++r) {
-            CHECK(ensure(E.dens_scratch[6 * r + gi], (size_t)worst * std::max(1, strides[gi]) * 4));
-            a.scratch[6 * r + gi] = P<float>(E.dens_scratch[6 * r + gi]);
-        }
     }
-    CHECK(ensure(E.dens_flags, (size_t)worst * 4 * 6));
-    CHECK(ensure(E.dens_scan, (size_t)mskern::scan_temp_ints(worst) * 4));
+    CHECK(ensure(E.dens_flags, (size_t)n * 4 * 4));
+    // the count after appending is at most 4N (a splat can be split and dup)
+    CHECK(ensure(E.dens_scan, (size_t)mskern::scan_temp_ints(4 * (int64_t)n) * 4));
     int *f = P<int>(E.dens_flags);
     a.split = f;
-    a.dup = f + worst;
-    a.split_pre = f + 2 * worst;
-    a.dup_pre = f + 3 * worst;
-    a.keep = f + 4 * worst;
-    a.keep_pre = f + 5 * worst;
+    a.dup = f + n;
+    a.split_pre = f + 2 * (size_t)n;
+    a.dup_pre = f + 3 * (size_t)n;
     a.scan_temp = P<int>(E.dens_scan);
-    mskern::launch_densify(E.stream, a);
+    mskern::launch_densify_classify(E.stream, a);
     HIPC(hipGetLastError());
-    HIPC(hipMemcpyAsync(E.pinned_i, a.keep_pre + worst - 1, sizeof(int), hipMemcpyDeviceToHost, E.stream));
+    HIPC(hipMemcpyAsync(E.pinned_i, a.split_pre + n - 1, sizeof(int), hipMemcpyDeviceToHost, E.stream));
+    HIPC(hipMemcpyAsync(E.pinned_i + 1, a.dup_pre + n - 1, sizeof(int), hipMemcpyDeviceToHost, E.stream));
+    HIPC(hipStreamSynchronize(E.stream));
+    // A splat that is small but wide on screen is classified both split and
+    // dup (msplat_metal.metal:3250-3262), so the appended count can exceed
+    // the reference's 3N worst case (msplat_metal.mm:1358, where the dup
+    // writes then run past the buffers).  Nothing has been written yet:
+    // refuse and report the rows needed, so the caller can grow and retry.
+    const int64_t n_new = (int64_t)n + 2 * (int64_t)E.pinned_i[0] + E.pinned_i[1];
+    if (n_new > capacity) {
+        *new_count = n_new > INT32_MAX ? INT32_MAX : (int)n_new;
+        set_err("densify: %lld rows needed after appending, capacity is %d", (long long)n_new, capacity);
+        return MSPLAT_E_CAPACITY;
+    }
+    for (int gi = 0; gi < 6; ++gi)
+        for (int r = 0; r < 3; ++r) {
+            CHECK(ensure(E.dens_scratch[6 * r + gi], (size_t)n_new * std::max(1, strides[gi]) * 4));
+            a.scratch[6 * r + gi] = P<float>(E.dens_scratch[6 * r + gi]);
+        }
+    CHECK(ensure(E.dens_keep, (size_t)n_new * 2 * 4));
+    a.keep = P<int>(E.dens_keep);
+    a.keep_pre = a.keep + n_new;
+    mskern::launch_densify_apply(E.stream, a, (int)n_new);
+    HIPC(hipGetLastError());
+    HIPC(hipMemcpyAsync(E.pinned_i, a.keep_pre + n_new - 1, sizeof(int), hipMemcpyDeviceToHost, E.stream));
     HIPC(hipStreamSynchronize(E.stream));
     *new_count = E.pinned_i[0];
     return MSPLAT_OK;

@@ -206,9 +206,14 @@ int msplat_densify(int N, int buf_capacity, float grad_thresh, float size_thresh
         v[k] = adam_exp_avg_sq_buf[k].data<float>();
     }
     int new_count = 0;
-    check(msplat_hip_densify(N, buf_capacity, grad_thresh, size_thresh, screen_thresh, check_screen,
-                             cull_alpha_thresh, cull_scale_thresh, cull_screen_size, check_huge,
-                             xys_grad_norm.data<float>(), vis_counts.data<float>(), max_2d_size.data<float>(),
-                             half_max_dim, params, fr_stride, m, v, random_samples.data<float>(), &new_count));
+    const int rc = msplat_hip_densify(N, buf_capacity, grad_thresh, size_thresh, screen_thresh, check_screen,
+                                      cull_alpha_thresh, cull_scale_thresh, cull_screen_size, check_huge,
+                                      xys_grad_norm.data<float>(), vis_counts.data<float>(),
+                                      max_2d_size.data<float>(), half_max_dim, params, fr_stride, m, v,
+                                      random_samples.data<float>(), &new_count);
+    // the buffers are too small for the appended splats: nothing was
+    // modified; the negated row count tells the caller what to grow to
+    if (rc == MSPLAT_E_CAPACITY) return -new_count;
+    check(rc);
     return new_count;
 }

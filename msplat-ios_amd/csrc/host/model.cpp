@@ -249,14 +249,23 @@ void Model::afterTrain(int step) {
         const float half_max_dim = 0.5f * (float)std::max(lastWidth, lastHeight);
         const int check_screen = step < stopScreenSizeAt ? 1 : 0;
         const bool checkHuge = step > refineEvery * resetAlphaEvery;
-        const int fr_stride = (int)featuresRest_buf.stride0();
         MTensor unused;
-        const int nc = msplat_densify(num_active, buf_capacity, densifyGradThresh, densifySizeThresh,
-                                      splitScreenSize, check_screen, cullAlphaThresh, 0.5f, 0.15f, checkHuge ? 1 : 0,
-                                      xysGradNorm, visCounts, max2DSize, half_max_dim, means_buf, scales_buf,
-                                      quats_buf, featuresDc_buf, featuresRest_buf, opacities_buf, fr_stride,
-                                      adam_exp_avg_buf, adam_exp_avg_sq_buf, unused, unused, unused, unused, unused,
-                                      unused, unused, unused, densify_random_samples);
+        auto densify = [&] {
+            const int fr_stride = (int)featuresRest_buf.stride0();
+            return msplat_densify(num_active, buf_capacity, densifyGradThresh, densifySizeThresh, splitScreenSize,
+                                  check_screen, cullAlphaThresh, 0.5f, 0.15f, checkHuge ? 1 : 0, xysGradNorm,
+                                  visCounts, max2DSize, half_max_dim, means_buf, scales_buf, quats_buf,
+                                  featuresDc_buf, featuresRest_buf, opacities_buf, fr_stride, adam_exp_avg_buf,
+                                  adam_exp_avg_sq_buf, unused, unused, unused, unused, unused, unused, unused,
+                                  unused, densify_random_samples);
+        };
+        int nc = densify();
+        if (nc < 0) {
+            // splats both split and duplicated need more than 3N rows:
+            // nothing was modified, grow to the reported count and redo
+            ensureCapacity(-nc);
+            nc = densify();
+        }
         num_active = nc;
         refreshViews();
         std::cout << "Densified: " << before << " -> " << num_active << " gaussians" << std::endl;

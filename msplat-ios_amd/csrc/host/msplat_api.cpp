@@ -16,6 +16,7 @@
 
 #include "msplat_c_api.h"
 #include "model.hpp"
+#include "msplat_engine.h"
 
 namespace msplat {
 
@@ -203,16 +204,14 @@ void Trainer::renderFromPoseToBuffer(const float camToWorld[16], int refCameraIn
         return;
     }
     Camera cam = impl->poseCamera(camToWorld, refCameraIndex);
-    PixelBuffer px = impl->renderCam(cam);
-    *outWidth = px.width;
-    *outHeight = px.height;
+    MTensor rgb = impl->model->render(cam, impl->currentStep);
+    *outWidth = (int)rgb.size(1);
+    *outHeight = (int)rgb.size(0);
     if (!outRGBA) return;
-    const size_t n = (size_t)px.width * px.height;
-    for (size_t i = 0; i < n; ++i) {
-        for (int c = 0; c < 3; ++c)
-            outRGBA[4 * i + c] = (uint8_t)(std::fmin(std::fmax(px.data[3 * i + c], 0.f), 1.f) * 255.f);
-        outRGBA[4 * i + 3] = 255;
-    }
+    // converted on the GPU: 4 bytes per pixel cross PCIe instead of 12
+    const int rc = msplat_hip_image_to_rgba8(static_cast<const float *>(rgb.data_ptr()),
+                                             (int64_t)rgb.size(0) * rgb.size(1), outRGBA);
+    if (rc != MSPLAT_OK) throw std::runtime_error(std::string("rgba8 conversion: ") + msplat_hip_last_error());
 }
 
 void Trainer::exportPly(const std::string &path) { impl->model->savePly(path, impl->currentStep); }

@@ -30,6 +30,22 @@ __global__ void k_clamp_max(float *__restrict__ p, int64_t n, float value) {
         if (p[i] > value) p[i] = value;
 }
 
+// RGBA8 of an [n,3] float image: (uint8)(clamp(x, 0, 1) * 255) per channel
+// (truncation, the host loop of renderFromPoseToBuffer, msplat_api.mm:207-236)
+// and alpha 255, one 4-byte store per pixel.
+__global__ void k_rgba8(const float *__restrict__ img, int64_t n, uint32_t *__restrict__ out) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const float *p = img + 3 * i;
+        uint32_t v = 0xff000000u;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const float x = __builtin_fminf(__builtin_fmaxf(p[c], 0.0f), 1.0f) * 255.0f;
+            v |= (uint32_t)x << (8 * c);
+        }
+        out[i] = v;
+    }
+}
+
 // ---- device-wide inclusive scan of int32 (reduce-then-scan) --------------
 constexpr int kScanBlock = 256, kScanItems = 4, kScanTile = kScanBlock * kScanItems;
 
@@ -262,6 +278,12 @@ void launch_clamp_max(hipStream_t s, float *p, int64_t n, float value) {
     hipLaunchKernelGGL(k_clamp_max, dim3((unsigned)blocks), dim3(256), 0, s, p, n, value);
 }
 
+void launch_rgba8(hipStream_t s, const float *img, int64_t n, uint32_t *out) {
+    if (n <= 0) return;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 65536);
+    hipLaunchKernelGGL(k_rgba8, dim3((unsigned)blocks), dim3(256), 0, s, img, n, out);
+}
+
 int64_t scan_temp_ints(int64_t n) { return (n + kScanTile - 1) / kScanTile + 1; }
 
 void launch_scan_i32(hipStream_t s, const int *in, int *out, int n, int *temp) {
@@ -272,8 +294,16 @@ void launch_scan_i32(hipStream_t s, const int *in, int *out, int n, int *temp) {
     hipLaunchKernelGGL(k_scan_add, dim3(nb), dim3(kScanBlock), 0, s, out, n, temp);
 }
 
-void launch_densify(hipStream_t s, const DensifyArgs &a) {
-    const int N = a.n, worst = 3 * N;
+void launch_densify_classify(hipStream_t s, const DensifyArgs &a) {
+    const int N = a.n;
+    hipLaunchKernelGGL(k_classify, dim3(nblk(N, 256)), dim3(256), 0, s, N, a.grad_norm, a.vis, a.params[1], a.max2d,
+                       a.half_max_dim, a.grad_th, a.size_th, a.screen_th, a.check_screen, a.split, a.dup);
+    launch_scan_i32(s, a.split, a.split_pre, N, a.scan_temp);
+    launch_scan_i32(s, a.dup, a.dup_pre, N, a.scan_temp);
+}
+
+void launch_densify_apply(hipStream_t s, const DensifyArgs &a, int n_new) {
+    const int N = a.n, worst = n_new;
     Bufs18 B{}, S{};
     const int strides[6] = {3, 2, 4, 3, a.fr_stride, 1};
     for (int gi = 0; gi < 6; ++gi) {
@@ -288,10 +318,6 @@ void launch_densify(hipStream_t s, const DensifyArgs &a) {
             S.stride[6 * r + gi] = strides[gi];
         }
     }
-    hipLaunchKernelGGL(k_classify, dim3(nblk(N, 256)), dim3(256), 0, s, N, a.grad_norm, a.vis, a.params[1], a.max2d,
-                       a.half_max_dim, a.grad_th, a.size_th, a.screen_th, a.check_screen, a.split, a.dup);
-    launch_scan_i32(s, a.split, a.split_pre, N, a.scan_temp);
-    launch_scan_i32(s, a.dup, a.dup_pre, N, a.scan_temp);
     hipLaunchKernelGGL(k_append_split, dim3(nblk(N, 256)), dim3(256), 0, s, N, a.split, a.split_pre, a.random,
                        a.log_size_fac, B);
     hipLaunchKernelGGL(k_append_dup, dim3(nblk(N, 256)), dim3(256), 0, s, N, a.dup, a.dup_pre, a.split_pre, B);

@@ -80,6 +80,7 @@ constexpr int kBlendLogEntryBytes = 16;
 void launch_check_rcp(hipStream_t s, int efield, unsigned long long *bad);
 
 // k_ssim.hip
+void launch_rgba8(hipStream_t s, const float *img, int64_t n, uint32_t *out);
 int ssim_num_blocks(int W, int H);
 void launch_loss_fwd_bwd(hipStream_t s, int W, int H, const float *img, const float *gt, const float *dist,
                          float lambda_l1, float lambda_dist, float lambda_dssim, const float window[11],
@@ -106,6 +107,11 @@ struct DensifyArgs {
     const float *random;
     int *split, *dup, *split_pre, *dup_pre, *keep, *keep_pre, *scan_temp;
 };
-void launch_densify(hipStream_t s, const DensifyArgs &a);
+// Classification and the split / dup prefix counts (the count after
+// appending is N + 2 * split_pre[N-1] + dup_pre[N-1]; a splat can be both).
+void launch_densify_classify(hipStream_t s, const DensifyArgs &a);
+// Append split children and dup copies, cull, compact; n_new is the count
+// after appending and must fit the buffers' capacity.
+void launch_densify_apply(hipStream_t s, const DensifyArgs &a, int n_new);
 
 }  // namespace mskern

@@ -17,6 +17,9 @@ _lib = None
 c_float_p = C.POINTER(C.c_float)
 
 
+MSPLAT_E_CAPACITY = -5
+
+
 class MsplatError(RuntimeError):
     pass
 
@@ -59,7 +62,7 @@ EXPORTS = [
     "msplat_hip_prepare_camera", "msplat_hip_init", "msplat_hip_cleanup", "msplat_hip_last_error",
     "msplat_hip_device_name", "msplat_hip_alloc", "msplat_hip_free", "msplat_hip_memset", "msplat_hip_upload",
     "msplat_hip_download", "msplat_hip_copy", "msplat_hip_commit", "msplat_hip_sync", "msplat_hip_train_step",
-    "msplat_hip_render", "msplat_hip_fused_adam", "msplat_hip_densify", "msplat_hip_clamp_max", "msplat_hip_loss_fwd_bwd",
+    "msplat_hip_render", "msplat_hip_image_to_rgba8", "msplat_hip_fused_adam", "msplat_hip_densify", "msplat_hip_clamp_max", "msplat_hip_loss_fwd_bwd",
     "msplat_hip_loss_fwd_bwd_noalloc",
     "msplat_hip_raster_bwd", "msplat_hip_project_bwd", "msplat_hip_project_bwd_adam", "msplat_hip_last", "msplat_hip_enable_timing",
     "msplat_hip_stage_times", "msplat_hip_last_pairs_evaluated", "msplat_hip_last_raster_counts",
@@ -96,6 +99,7 @@ def lib() -> C.CDLL:
         "msplat_hip_train_step": (I, [C.POINTER(MsplatCamera), C.POINTER(MsplatGaussians), P, P, F, F, F, P, P, P,
                                       F, C.POINTER(MsplatAdam), c_float_p, C.POINTER(I64)]),
         "msplat_hip_render": (I, [C.POINTER(MsplatCamera), C.POINTER(MsplatGaussians), P, C.POINTER(I64)]),
+        "msplat_hip_image_to_rgba8": (I, [P, I64, P]),
         "msplat_hip_fused_adam": (I, [P, P, P, P, I64, F, F, F, F, F]),
         "msplat_hip_densify": (I, [I, I, F, F, F, I, F, F, F, I, P, P, P, F, P * 6, I, P * 6, P * 6, P,
                                    C.POINTER(I)]),

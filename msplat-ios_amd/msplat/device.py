@@ -112,3 +112,117 @@ def train_step(ds: DeviceScene, cam: E.MsplatCamera, gt: E.DeviceArray, ssim_wei
                                                   adam.eps))
         E.sync()
     return float(loss.value), int(nis.value)
+
+
+STRIDES = (3, 2, 4, 3, 45, 1)  # floats per splat of each group at SH degree 3
+
+
+class CapacityScene(DeviceScene):
+    """A DeviceScene whose six groups, Adam moments and densify statistics
+    live in backing buffers of `cap` rows, the first `n` of them active
+    (Model's *_buf tensors, core/src/model.cpp:201-233), so that
+    msplat_hip_densify can append and compact in place."""
+
+    def __init__(self, scene: Scene, cap: int):
+        if scene.sh_degree != 3:
+            raise ValueError("CapacityScene holds SH degree 3 scenes")
+        self.sh_degree = 3
+        self.n = scene.n
+        self.cap = cap
+        host = [np.zeros(cap * s, np.float32) for s in STRIDES]
+        for h, a, s in zip(host, scene.params(), STRIDES):
+            h[: self.n * s] = a.reshape(-1)
+        self.params = [E.DeviceArray.from_numpy(h) for h in host]
+        self.background = E.DeviceArray.from_numpy(np.asarray(scene.background, np.float32))
+        self.exp_avg = [E.DeviceArray.zeros(cap * s) for s in STRIDES]
+        self.exp_avg_sq = [E.DeviceArray.zeros(cap * s) for s in STRIDES]
+        self.grad_norm, self.vis, self.max2d = (E.DeviceArray.zeros(cap) for _ in range(3))
+        self.adam_step = 0
+        self.lr = list(LR_INIT)
+
+    def ensure_capacity(self, rows: int) -> None:
+        """Grows the backing buffers to at least `rows` rows (doubling, as
+        Model::ensureCapacity), keeping the first n rows of every buffer."""
+        if rows <= self.cap:
+            return
+        cap = max(rows, 2 * self.cap)
+
+        def grown(old: E.DeviceArray, stride: int) -> E.DeviceArray:
+            new = E.DeviceArray.zeros(cap * stride)
+            E.check(E.lib().msplat_hip_copy(new.ptr, old.ptr, self.n * stride * 4))
+            return new
+
+        self.params = [grown(p, s) for p, s in zip(self.params, STRIDES)]
+        self.exp_avg = [grown(p, s) for p, s in zip(self.exp_avg, STRIDES)]
+        self.exp_avg_sq = [grown(p, s) for p, s in zip(self.exp_avg_sq, STRIDES)]
+        self.grad_norm, self.vis, self.max2d = (grown(a, 1) for a in (self.grad_norm, self.vis, self.max2d))
+        E.sync()
+        self.cap = cap
+
+    def _rows(self, a: E.DeviceArray, stride: int, count: int, rows: int) -> np.ndarray:
+        out = np.zeros(rows * stride, np.float32)
+        if count:
+            E.check(E.lib().msplat_hip_download(out.ctypes.data, a.ptr, count * stride * 4))
+        return out
+
+    def state(self, rows: int | None = None) -> tuple[list, list, list, dict]:
+        """Host copies of the first n rows of every backing buffer, in host
+        arrays of `rows` rows (default n, zero after n), and the first n
+        statistics."""
+        rows = self.n if rows is None else rows
+        n = self.n
+        stats = {k: self._rows(a, 1, n, n) for k, a in
+                 (("grad_norm", self.grad_norm), ("vis", self.vis), ("max2d", self.max2d))}
+        return ([self._rows(p, s, n, rows) for p, s in zip(self.params, STRIDES)],
+                [self._rows(p, s, n, rows) for p, s in zip(self.exp_avg, STRIDES)],
+                [self._rows(p, s, n, rows) for p, s in zip(self.exp_avg_sq, STRIDES)], stats)
+
+    def densify(self, random_normals: np.ndarray, half_max_dim: float, grad_thresh=0.0002, size_thresh=0.01,
+                screen_thresh=0.05, check_screen=1, cull_alpha=0.1, cull_scale=0.5, cull_screen=0.15,
+                check_huge=0) -> int:
+        """msplat_hip_densify with Model::afterTrain's arguments, after growing
+        the buffers to 3n rows (and again to the rows it reports when splats
+        that are both split and duplicated need more); random_normals is
+        [2n, 3].  Returns the new count."""
+        self.ensure_capacity(3 * self.n)
+        d_rs = E.DeviceArray.from_numpy(np.ascontiguousarray(random_normals, np.float32))
+        P6 = C.c_void_p * 6
+        newc = C.c_int()
+        for _ in range(2):
+            rc = E.lib().msplat_hip_densify(self.n, self.cap, grad_thresh, size_thresh, screen_thresh, check_screen,
+                                            cull_alpha, cull_scale, cull_screen, check_huge, self.grad_norm.ptr,
+                                            self.vis.ptr, self.max2d.ptr, half_max_dim,
+                                            P6(*[p.ptr for p in self.params]), STRIDES[4],
+                                            P6(*[m.ptr for m in self.exp_avg]),
+                                            P6(*[v.ptr for v in self.exp_avg_sq]), d_rs.ptr, C.byref(newc))
+            if rc != E.MSPLAT_E_CAPACITY:
+                break
+            # more than 3n rows after appending: nothing was modified
+            self.ensure_capacity(int(newc.value))
+        E.check(rc)
+        self.n = int(newc.value)
+        return self.n
+
+    def reset_stats(self) -> None:
+        for a in (self.grad_norm, self.vis, self.max2d):
+            a.zero_()
+
+    def reset_opacity(self, logit: float = -1.3862943611198906) -> None:
+        """Model::afterTrain's opacity reset: clamp to logit(0.2) and zero
+        the opacity group's Adam moments."""
+        E.check(E.lib().msplat_hip_clamp_max(self.params[5].ptr, self.n, logit))
+        self.exp_avg[5].zero_()
+        self.exp_avg_sq[5].zero_()
+
+
+def densify_schedule(step: int, n: int, max_splats: int = 250_000, refine_every: int = 100, warmup: int = 0,
+                     reset_every: int = 30, num_cameras: int = 32, stop_split_at: int = 29500) -> tuple[bool, bool]:
+    """(densify, reset opacity) after `step` with n splats under
+    Model::afterTrain's schedule and capacity rule (core/src/model.cpp:
+    240-306: no densification once n reaches max_splats)."""
+    if not (step % refine_every == 0 and step > warmup):
+        return False, False
+    interval = reset_every * refine_every
+    dens = step < stop_split_at and step % interval > num_cameras + refine_every and n < max_splats
+    reset = step < stop_split_at and step % interval == refine_every
+    return dens, reset

@@ -1088,7 +1088,7 @@ extern "C" int orc_densify(int N, int capacity, float grad_thresh, float size_th
                            float *const params[6], int fr_stride,
                            float *const exp_avg[6], float *const exp_avg_sq[6],
                            const float *rs) {
-    if (3 * N > capacity) return -1;
+    if (N > capacity) return -1;
     const int strides[6] = {3, 2, 4, 3, fr_stride, 1};
     float *means = params[0], *scales = params[1], *quats = params[2];
     float *opac = params[5];
@@ -1112,6 +1112,9 @@ extern "C" int orc_densify(int N, int capacity, float grad_thresh, float size_th
     acc = 0;
     for (int i = 0; i < N; ++i) dup_pre[i] = (acc += dup[i]);
     const int nS = N > 0 ? split_pre[N - 1] : 0, nD = N > 0 ? dup_pre[N - 1] : 0;
+    /* a splat can be both split and dup, so the appended count reaches up
+     * to 4N: report the rows needed (negated) before writing anything */
+    if ((int64_t)N + 2 * (int64_t)nS + nD > capacity) return -(N + 2 * nS + nD);
     const float log_size_fac = std::log(1.6f);
 
     auto zero_adam = [&](int dst) {

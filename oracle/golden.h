@@ -145,7 +145,9 @@ void orc_adam(float *params, const float *grads, float *exp_avg,
  * kernels of msplat_metal.metal:3231-3491.  Buffers are capacity-sized
  * backing buffers: params[6] = means(3), scales(2), quats(4), features_dc(3),
  * features_rest(fr_stride), opacities(1); exp_avg[6] / exp_avg_sq[6] the same
- * strides.  random_samples is [2N,3].  Returns the new gaussian count. */
+ * strides.  random_samples is [2N,3].  Returns the new gaussian count, or
+ * minus the rows needed (nothing modified) when the appended count exceeds
+ * capacity. */
 int orc_densify(int n, int capacity, float grad_thresh, float size_thresh,
                 float screen_thresh, int check_screen,
                 float cull_alpha_thresh, float cull_scale_thresh,

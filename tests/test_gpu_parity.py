@@ -412,3 +412,45 @@ def test_densify_bitexact(orc, eng):
     for i, (d, o) in enumerate(zip(dev, params + m6 + v6)):
         s = strides[i % 6]
         _assert_bitexact(d.numpy()[: new_o * s], o[: new_o * s], f"buffer {i}")
+
+
+def test_densify_split_and_dup_beyond_3n(orc, eng):
+    """Splats small in the world but wide on screen with a high gradient are
+    classified both split and dup (msplat_metal.metal:3250-3262), so the
+    appended count exceeds 3N.  At capacity 3N the call must leave every
+    buffer untouched and report the rows it needs; at that capacity it must
+    match the golden model bit for bit."""
+    scene = S.make_scene(5, n=5000, width=320, height=208, num_cameras=1)
+    n = scene.n
+    rng = S.SplitMix64(91)
+    scene.scales[:] = np.float32(-6.0)  # max scale 2.5e-3 < size threshold: not large
+    params, m6, v6, strides, stats, rs = _densify_inputs(scene, n, 4 * n, 92)
+    stats["grad_norm"][:] = np.float32(0.01)  # high gradient everywhere
+    stats["vis"][:] = np.float32(1.0)
+    stats["max2d"][:] = (0.04 + rng.uniform(n) * 0.04).astype(np.float32)  # about 3/4 above 0.05
+    P6 = C.c_void_p * 6
+    args = (0.0002, 0.01, 0.05, 1, 0.005, 0.5, 0.15, 0)
+    dstats = {k: _device(v) for k, v in stats.items()}
+    d_rs = _device(rs)
+    dev = [_device(a) for a in params + m6 + v6]
+
+    def call(cap):
+        newc = C.c_int()
+        rc = E.lib().msplat_hip_densify(n, cap, *args, dstats["grad_norm"].ptr, dstats["vis"].ptr,
+                                        dstats["max2d"].ptr, 160.0, P6(*[d.ptr for d in dev[0:6]]), strides[4],
+                                        P6(*[d.ptr for d in dev[6:12]]), P6(*[d.ptr for d in dev[12:18]]), d_rs.ptr,
+                                        C.byref(newc))
+        return rc, newc.value
+
+    rc, need = call(3 * n)
+    assert rc == E.MSPLAT_E_CAPACITY and need > 3 * n, (rc, need)
+    for i, (d, o) in enumerate(zip(dev, params + m6 + v6)):
+        _assert_bitexact(d.numpy(), o, f"buffer {i} after the refused call")
+    assert orc.densify(n, 3 * n, params, m6, v6, strides[4], stats, rs, *args, half_max_dim=160.0) == -need
+    rc, newc = call(need)
+    assert rc == 0
+    new_o = orc.densify(n, need, params, m6, v6, strides[4], stats, rs, *args, half_max_dim=160.0)
+    assert newc == new_o and new_o > n
+    for i, (d, o) in enumerate(zip(dev, params + m6 + v6)):
+        st = strides[i % 6]
+        _assert_bitexact(d.numpy()[: new_o * st], o[: new_o * st], f"buffer {i}")

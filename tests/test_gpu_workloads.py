@@ -16,9 +16,10 @@ binning is checked against properties that do not depend on the oracle:
     transmittance lies in (0, 1] and the image is finite,
   * a training step on the full workload gives a finite loss and finite,
     updated parameters.
-The densification cycle (growth from a blob scene through repeated
-clone / split / cull) is run at a reduced size with every compaction
-compared bit for bit with the golden model's on the same inputs.
+The densification workload (growth from 200k blob splats through
+repeated clone / split / cull over 1500 steps) runs at its size with every
+compaction compared bit for bit with the golden model's on the same inputs;
+a reduced cycle with a lower threshold checks three compactions quickly.
 """
 import ctypes as C
 
@@ -248,3 +249,50 @@ def test_densify_cycle_bitexact(orc, eng):
         counts.append(new_o)
     assert counts[-1] != counts[0]
     assert max(counts) > counts[0]  # the scene grew at least once
+
+
+def test_densify_workload_full_size(orc, eng):
+    """The densification workload at its size: 200k blob splats at 1297x840
+    trained for 1500 steps under Model::afterTrain's schedule (densify every
+    100 steps from step 200, opacity reset at step 100) with grad threshold
+    2e-4, cull opacity 0.005 and the capacity rule at 2M splats; every
+    compaction compared bit for bit with the golden model's on the GPU's own
+    pre-densify state."""
+    scene = S.make_scene(5)
+    print(f"[densify] {scene.name}", flush=True)
+    ds = D.CapacityScene(scene, 4_000_000)
+    tgt = D.DeviceScene(scene.jittered(0.01, 0xC0FFEE + 105))
+    gts = [D.render_to_device(tgt, tgt.camera(c)) for c in scene.cameras]
+    del tgt
+    cams = [ds.camera(c) for c in scene.cameras]
+    rng = S.SplitMix64(0xC0FFEE + 5)
+    half = 0.5 * max(scene.cameras[0].width, scene.cameras[0].height)
+    counts = [ds.n]
+    for step in range(1, 1501):
+        ci = (step - 1) % len(cams)
+        loss, _ = D.train_step(ds, cams[ci], gts[ci])
+        assert np.isfinite(loss), step
+        dens, reset = D.densify_schedule(step, ds.n, 2_000_000, num_cameras=len(cams))
+        if dens:
+            n = ds.n
+            params, m6, v6, stats = ds.state(3 * n)
+            rs = rng.normal(2 * n * 3).reshape(2 * n, 3).astype(np.float32)
+            new_o = orc.densify(n, 3 * n, params, m6, v6, 45, stats, rs, grad_thresh=0.0002, size_thresh=0.01,
+                                screen_thresh=0.05, check_screen=1, cull_alpha=0.005, cull_scale=0.5,
+                                cull_screen=0.15, check_huge=0, half_max_dim=half)
+            new_g = ds.densify(rs, half, grad_thresh=0.0002, cull_alpha=0.005)
+            print(f"[densify] step {step}: {n} -> gpu {new_g}, oracle {new_o}", flush=True)
+            assert new_g == new_o
+            gp, gm, gv, _ = ds.state()
+            for i, (g, o) in enumerate(zip(gp + gm + gv, params + m6 + v6)):
+                k = new_o * D.STRIDES[i % 6]
+                bad = g[:k] != o[:k]
+                assert not bad.any(), f"step {step}, buffer {i}: {int(bad.sum())} of {k} entries differ"
+            counts.append(new_g)
+        if reset:
+            ds.reset_opacity()
+        if step % 100 == 0:
+            ds.reset_stats()
+    print(f"[densify] splat counts per cycle: {counts}", flush=True)
+    assert len(counts) >= 4 and counts[-1] >= 2_000_000
+    assert all(b > a for a, b in zip(counts, counts[1:]))
