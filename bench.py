@@ -388,6 +388,8 @@ def main() -> int:
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-buffer-render", action="store_true",
                     help="skip the render-to-host-buffer frames (e.g. under a profiler)")
+    ap.add_argument("--profile-workload", type=int, default=0, metavar="N",
+                    help="only run the train steps and render frames of workload N (for a profiler)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the training step is single-GPU (one camera per step); "
@@ -401,6 +403,12 @@ def main() -> int:
     from msplat import synthetic as S
 
     E.init()
+    if args.profile_workload:
+        r = gpu_train(args.profile_workload, args.steps, args.warmup, args.render_frames, counters=False)
+        print(json.dumps({"workload": r["scene"].name, "ms_per_step": round(r["ms_per_step"], 3),
+                          "render_ms": round(r["render_ms"], 3), "intersections_mean": int(r["isect"]),
+                          "stage_ms": {k: round(v, 4) for k, v in r["stage_ms"].items()}}))
+        return 0
     # ---- headline: C3 ----
     h = gpu_train(3, args.steps, args.warmup, args.render_frames, counters=True)
     scene = h["scene"]

@@ -114,12 +114,24 @@ struct Trainer::Impl {
         rgb.copy_to_host(buf);
         return PixelBuffer(buf, w, h);
     }
+    // The intrinsics of the reference camera at a new pose.  Only those
+    // fields are taken: the camera's image, pyramid and GPU image cache stay
+    // behind (copying them cost a full-resolution image per frame).
     Camera poseCamera(const float camToWorld[16], int ref) {
-        Camera cam = ds->trainCams.at(ref);  // intrinsics of the reference camera
+        const Camera &src = ds->trainCams.at(ref);
+        Camera cam;
+        cam.width = src.width;
+        cam.height = src.height;
+        cam.fx = src.fx;
+        cam.fy = src.fy;
+        cam.cx = src.cx;
+        cam.cy = src.cy;
+        cam.k1 = src.k1;
+        cam.k2 = src.k2;
+        cam.k3 = src.k3;
+        cam.p1 = src.p1;
+        cam.p2 = src.p2;
         std::memcpy(cam.camToWorld, camToWorld, 16 * sizeof(float));
-        cam.image = Image();
-        cam.imagePyramids.clear();
-        cam.mtensorImageCache.clear();
         return cam;
     }
 };

@@ -348,10 +348,46 @@ __device__ void lds_bitonic(unsigned long long *s, const unsigned long long *src
     }
 }
 
-// Counts the entries of the super-tile's 16 tiles (each entry covers the
-// tiles of its rectangle inside the super-tile) into tile_counts, then sorts
-// the super-tile list in place; lists longer than kChunk are sorted in
-// kChunk runs and queued on big_list for the merge passes.
+// The tile counts of a super-tile's entries keys[0, cnt): each entry covers
+// the tiles of its rectangle inside the super-tile; s_tc[16] (zeroed by the
+// caller) receives the sums.  Block-uniform.
+template <bool PACKED>
+__device__ __forceinline__ void count_tiles(const unsigned long long *__restrict__ keys, int cnt, int stx, int sty,
+                                            const uint2 *__restrict__ rect, int *s_tc) {
+    int tc[kSuper * kSuper];
+#pragma unroll
+    for (int q = 0; q < kSuper * kSuper; ++q) tc[q] = 0;
+    for (int e = threadIdx.x; e < cnt; e += kSortThreads) {
+        int rx0, rx1, ry0, ry1;
+        if constexpr (PACKED) {
+            const int4 lr = unpack_rect((uint32_t)keys[e] & 0xffu);
+            rx0 = lr.x, rx1 = lr.y, ry0 = lr.z, ry1 = lr.w;
+        } else {
+            const uint2 r = rect[(uint32_t)(keys[e] & 0xffffffffull)];
+            rx0 = max((int)(r.x & 0xffff) - stx, 0), rx1 = min((int)(r.y & 0xffff) - stx, kSuper);
+            ry0 = max((int)(r.x >> 16) - sty, 0), ry1 = min((int)(r.y >> 16) - sty, kSuper);
+        }
+#pragma unroll
+        for (int q = 0; q < kSuper * kSuper; ++q) {
+            const int lx = q % kSuper, ly = q / kSuper;
+            tc[q] += (lx >= rx0 && lx < rx1 && ly >= ry0 && ly < ry1) ? 1 : 0;
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < kSuper * kSuper; ++q) {
+        int v = tc[q];
+#pragma unroll
+        for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+        if ((threadIdx.x & 63) == 0 && v) atomicAdd(&s_tc[q], v);
+    }
+    __syncthreads();
+}
+
+// Counts the entries of the super-tile's 16 tiles into tile_counts, then
+// sorts the super-tile list in place.  Lists longer than kChunk are only
+// queued on big_list (their tile counts zeroed): k_sort_chunks sorts them in
+// kChunk runs on many workgroups, the merge passes merge the runs, and
+// k_count_chunks / k_emit_chunks count and emit them chunk by chunk.
 template <bool PACKED>
 __global__ __launch_bounds__(kSortThreads) void k_sort_super(int tiles_x, int tiles_y, int sxn,
                                                              const int *__restrict__ offsets,
@@ -367,49 +403,106 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_super(int tiles_x, int ti
     const int stx = (t % sxn) * kSuper, sty = (t / sxn) * kSuper;
     if (threadIdx.x < kSuper * kSuper) s_tc[threadIdx.x] = 0;
     __syncthreads();
-    {
-        int tc[kSuper * kSuper];
-#pragma unroll
-        for (int q = 0; q < kSuper * kSuper; ++q) tc[q] = 0;
-        for (int e = threadIdx.x; e < cnt; e += kSortThreads) {
-            int rx0, rx1, ry0, ry1;
-            if constexpr (PACKED) {
-                const int4 lr = unpack_rect((uint32_t)keys[start + e] & 0xffu);
-                rx0 = lr.x, rx1 = lr.y, ry0 = lr.z, ry1 = lr.w;
-            } else {
-                const uint2 r = rect[(uint32_t)(keys[start + e] & 0xffffffffull)];
-                rx0 = max((int)(r.x & 0xffff) - stx, 0), rx1 = min((int)(r.y & 0xffff) - stx, kSuper);
-                ry0 = max((int)(r.x >> 16) - sty, 0), ry1 = min((int)(r.y >> 16) - sty, kSuper);
-            }
-#pragma unroll
-            for (int q = 0; q < kSuper * kSuper; ++q) {
-                const int lx = q % kSuper, ly = q / kSuper;
-                tc[q] += (lx >= rx0 && lx < rx1 && ly >= ry0 && ly < ry1) ? 1 : 0;
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < kSuper * kSuper; ++q) {
-            int v = tc[q];
-#pragma unroll
-            for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
-            if ((threadIdx.x & 63) == 0 && v) atomicAdd(&s_tc[q], v);
-        }
-        __syncthreads();
-        if (threadIdx.x < kSuper * kSuper) {
-            const int tx = stx + (int)threadIdx.x % kSuper, ty = sty + (int)threadIdx.x / kSuper;
-            if (tx < tiles_x && ty < tiles_y) tile_counts[ty * tiles_x + tx] = s_tc[threadIdx.x];
-        }
+    if (cnt <= kChunk) count_tiles<PACKED>(keys + start, cnt, stx, sty, rect, s_tc);
+    if (threadIdx.x < kSuper * kSuper) {
+        const int tx = stx + (int)threadIdx.x % kSuper, ty = sty + (int)threadIdx.x / kSuper;
+        if (tx < tiles_x && ty < tiles_y) tile_counts[ty * tiles_x + tx] = s_tc[threadIdx.x];
+    }
+    if (cnt > kChunk) {
+        if (threadIdx.x == 0) big_list[atomicAdd(&stats[2], 1)] = t;
+        return;
     }
     if (cnt <= 1) return;
-    for (int c0 = start; c0 < end; c0 += kChunk) {
-        const int c = min(kChunk, end - c0);
-        lds_bitonic(s, keys + c0, c);
-        for (int i = threadIdx.x; i < c; i += kSortThreads) keys[c0 + i] = s[sort_slot(i)];
+    lds_bitonic(s, keys + start, cnt);
+    for (int i = threadIdx.x; i < cnt; i += kSortThreads) keys[start + i] = s[sort_slot(i)];
+}
+
+// Chunk numbering of the long lists: chunk_base[b] = the number of kChunk
+// chunks of big lists 0 .. b-1, stats[3] = all of them.  One workgroup.
+__global__ __launch_bounds__(1024) void k_big_prep(const int *__restrict__ offsets, const int *__restrict__ big_list,
+                                                   int *__restrict__ stats, int *__restrict__ chunk_base) {
+    __shared__ int s_w[16];
+    const int nbig = stats[2];
+    int carry = 0;
+    for (int b0 = 0; b0 < nbig; b0 += 1024) {
+        const int b = b0 + (int)threadIdx.x;
+        int v = 0;
+        if (b < nbig) {
+            const int t = big_list[b];
+            v = (offsets[t + 1] - offsets[t] + kChunk - 1) / kChunk;
+        }
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        int incl = v;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int o = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += o;
+        }
         __syncthreads();
+        if (lane == 63) s_w[wave] = incl;
+        __syncthreads();
+        int off = 0, tot = 0;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) {
+            off += w < wave ? s_w[w] : 0;
+            tot += s_w[w];
+        }
+        if (b < nbig) chunk_base[b] = carry + off + incl - v;
+        carry += tot;
     }
-    if (cnt > kChunk && threadIdx.x == 0) {
-        const int b = atomicAdd(&stats[2], 1);
-        big_list[b] = t;
+    if (threadIdx.x == 0) stats[3] = carry;
+}
+
+// Sorts every kChunk run of the long lists in LDS, one run per workgroup
+// iteration (grid.y strides over the lists, grid.x over their runs).
+__global__ __launch_bounds__(kSortThreads) void k_sort_chunks(const int *__restrict__ offsets,
+                                                              const int *__restrict__ big_list,
+                                                              const int *__restrict__ stats,
+                                                              unsigned long long *__restrict__ keys) {
+    __shared__ unsigned long long s[kChunk];
+    const int nbig = stats[2];
+    for (int b = blockIdx.y; b < nbig; b += gridDim.y) {
+        const int t = big_list[b];
+        const int start = offsets[t], cnt = offsets[t + 1] - start;
+        for (int c0 = blockIdx.x * kChunk; c0 < cnt; c0 += gridDim.x * kChunk) {
+            const int c = min(kChunk, cnt - c0);
+            lds_bitonic(s, keys + start + c0, c);
+            for (int i = threadIdx.x; i < c; i += kSortThreads) keys[start + c0 + i] = s[sort_slot(i)];
+            __syncthreads();
+        }
+    }
+}
+
+// Tile counts of every kChunk chunk of the merged long lists:
+// chunk_counts[chunk_base[b] + c][16], summed into tile_counts.
+template <bool PACKED>
+__global__ __launch_bounds__(kSortThreads) void k_count_chunks(int tiles_x, int tiles_y, int sxn,
+                                                               const int *__restrict__ offsets,
+                                                               const int *__restrict__ big_list,
+                                                               const int *__restrict__ stats,
+                                                               const int *__restrict__ chunk_base,
+                                                               const unsigned long long *__restrict__ keys,
+                                                               const uint2 *__restrict__ rect,
+                                                               int *__restrict__ chunk_counts,
+                                                               int *__restrict__ tile_counts) {
+    __shared__ int s_tc[kSuper * kSuper];
+    const int nbig = stats[2];
+    for (int b = blockIdx.y; b < nbig; b += gridDim.y) {
+        const int t = big_list[b];
+        const int start = offsets[t], cnt = offsets[t + 1] - start;
+        const int stx = (t % sxn) * kSuper, sty = (t / sxn) * kSuper;
+        for (int c = blockIdx.x; c * kChunk < cnt; c += gridDim.x) {
+            if (threadIdx.x < kSuper * kSuper) s_tc[threadIdx.x] = 0;
+            __syncthreads();
+            count_tiles<PACKED>(keys + start + c * kChunk, min(kChunk, cnt - c * kChunk), stx, sty, rect, s_tc);
+            if (threadIdx.x < kSuper * kSuper) {
+                const int v = s_tc[threadIdx.x];
+                chunk_counts[(size_t)(chunk_base[b] + c) * (kSuper * kSuper) + threadIdx.x] = v;
+                const int tx = stx + (int)threadIdx.x % kSuper, ty = sty + (int)threadIdx.x / kSuper;
+                if (v && tx < tiles_x && ty < tiles_y) atomicAdd(&tile_counts[ty * tiles_x + tx], v);
+            }
+            __syncthreads();
+        }
     }
 }
 
@@ -465,36 +558,23 @@ __global__ __launch_bounds__(256) void k_copy_big(const int *__restrict__ offset
 
 constexpr int kWin = 2048;  // super-list entries staged in LDS per window
 
-// Filters each super-tile's sorted list into the id lists of its 16 tiles.
-// Wave w emits the 4 tiles of row w of the super-tile; within a 64-entry
-// chunk a lane's output slot is the popcount of the covering lanes below it,
-// so each tile list keeps the super-list (depth, id) order.
+// Filters the sorted super-list entries skeys[0, cnt) of the super-tile at
+// tile (stx, sty) into the id lists of its tiles: wave w emits the 4 tiles of
+// row w; out[lx] is the tile's list position of the first entry (-1 for a
+// tile outside the image).  Within a 64-entry chunk a lane's output slot is
+// the popcount of the covering lanes below it, so each tile list keeps the
+// super-list (depth, id) order.  Block-uniform.
 template <bool PACKED>
-__global__ __launch_bounds__(256) void k_emit_tiles(int tiles_x, int tiles_y, int sxn,
-                                                    const int *__restrict__ soffsets,
-                                                    const unsigned long long *__restrict__ skeys,
-                                                    const uint2 *__restrict__ rect,
-                                                    const int *__restrict__ toffsets, int *__restrict__ ids) {
-    __shared__ int s_gid[kWin];
-    __shared__ unsigned short s_rr[kWin];
-    const int st = blockIdx.x;
-    const int stx = (st % sxn) * kSuper, sty = (st / sxn) * kSuper;
-    const int start = soffsets[st], cnt = soffsets[st + 1] - start;
+__device__ __forceinline__ void emit_range(const unsigned long long *__restrict__ skeys, int cnt, int stx, int sty,
+                                           const uint2 *__restrict__ rect, int out[kSuper], int *s_gid,
+                                           unsigned short *s_rr, int *__restrict__ ids) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const unsigned long long below = (1ull << lane) - 1ull;
-    const int ty = sty + wave;
-    int out[kSuper], base[kSuper];
-#pragma unroll
-    for (int lx = 0; lx < kSuper; ++lx) {
-        const int tx = stx + lx;
-        out[lx] = (tx < tiles_x && ty < tiles_y) ? toffsets[ty * tiles_x + tx] : -1;
-        base[lx] = 0;
-    }
     for (int w0 = 0; w0 < cnt; w0 += kWin) {
         const int wn = min(kWin, cnt - w0);
         __syncthreads();
         for (int k = threadIdx.x; k < wn; k += 256) {
-            const uint32_t lo = (uint32_t)(skeys[start + w0 + k] & 0xffffffffull);
+            const uint32_t lo = (uint32_t)(skeys[w0 + k] & 0xffffffffull);
             int gid, rx0, rx1, ry0, ry1;
             if constexpr (PACKED) {
                 gid = (int)(lo >> 8);
@@ -522,9 +602,76 @@ __global__ __launch_bounds__(256) void k_emit_tiles(int tiles_x, int tiles_y, in
             for (int lx = 0; lx < kSuper; ++lx) {
                 const bool cov = row_in && rx0 <= lx && lx < rx1;
                 const unsigned long long bal = __ballot(cov);
-                if (cov && out[lx] >= 0) ids[out[lx] + base[lx] + __popcll(bal & below)] = gid;
-                base[lx] += __popcll(bal);
+                if (cov && out[lx] >= 0) ids[out[lx] + __popcll(bal & below)] = gid;
+                if (out[lx] >= 0) out[lx] += __popcll(bal);
             }
+        }
+    }
+}
+
+// Emits each super-tile list of at most kChunk entries into its 16 tile
+// lists (longer lists: k_emit_chunks).
+template <bool PACKED>
+__global__ __launch_bounds__(256) void k_emit_tiles(int tiles_x, int tiles_y, int sxn,
+                                                    const int *__restrict__ soffsets,
+                                                    const unsigned long long *__restrict__ skeys,
+                                                    const uint2 *__restrict__ rect,
+                                                    const int *__restrict__ toffsets, int *__restrict__ ids) {
+    __shared__ int s_gid[kWin];
+    __shared__ unsigned short s_rr[kWin];
+    const int st = blockIdx.x;
+    const int stx = (st % sxn) * kSuper, sty = (st / sxn) * kSuper;
+    const int start = soffsets[st], cnt = soffsets[st + 1] - start;
+    if (cnt > kChunk) return;
+    const int ty = sty + (int)(threadIdx.x >> 6);
+    int out[kSuper];
+#pragma unroll
+    for (int lx = 0; lx < kSuper; ++lx) {
+        const int tx = stx + lx;
+        out[lx] = (tx < tiles_x && ty < tiles_y) ? toffsets[ty * tiles_x + tx] : -1;
+    }
+    emit_range<PACKED>(skeys + start, cnt, stx, sty, rect, out, s_gid, s_rr, ids);
+}
+
+// Emits every kChunk chunk of the long lists: a chunk's entries start in
+// each tile list after those of the chunks before it (chunk_counts).
+template <bool PACKED>
+__global__ __launch_bounds__(256) void k_emit_chunks(int tiles_x, int tiles_y, int sxn,
+                                                     const int *__restrict__ soffsets,
+                                                     const int *__restrict__ big_list,
+                                                     const int *__restrict__ stats,
+                                                     const int *__restrict__ chunk_base,
+                                                     const int *__restrict__ chunk_counts,
+                                                     const unsigned long long *__restrict__ skeys,
+                                                     const uint2 *__restrict__ rect,
+                                                     const int *__restrict__ toffsets, int *__restrict__ ids) {
+    __shared__ int s_gid[kWin];
+    __shared__ unsigned short s_rr[kWin];
+    const int nbig = stats[2];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int b = blockIdx.y; b < nbig; b += gridDim.y) {
+        const int st = big_list[b];
+        const int stx = (st % sxn) * kSuper, sty = (st / sxn) * kSuper;
+        const int start = soffsets[st], cnt = soffsets[st + 1] - start;
+        const int ty = sty + wave;
+        for (int c = blockIdx.x; c * kChunk < cnt; c += gridDim.x) {
+            // entries of this wave's four tiles in the chunks before c
+            int before[kSuper] = {0, 0, 0, 0};
+            for (int k = lane; k < c; k += 64)
+#pragma unroll
+                for (int lx = 0; lx < kSuper; ++lx)
+                    before[lx] += chunk_counts[(size_t)(chunk_base[b] + k) * (kSuper * kSuper) + wave * kSuper + lx];
+            int out[kSuper];
+#pragma unroll
+            for (int lx = 0; lx < kSuper; ++lx) {
+                int v = before[lx];
+#pragma unroll
+                for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+                const int tx = stx + lx;
+                out[lx] = (tx < tiles_x && ty < tiles_y) ? toffsets[ty * tiles_x + tx] + v : -1;
+            }
+            emit_range<PACKED>(skeys + start + c * kChunk, min(kChunk, cnt - c * kChunk), stx, sty, rect, out, s_gid,
+                               s_rr, ids);
         }
     }
 }
@@ -567,8 +714,8 @@ void launch_super_count(hipStream_t s, int n, int tiles_x, int tiles_y, const in
 void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
                       const float *depths, const int *super_offsets, const int *super_cm, int super_max,
                       uint64_t *super_keys, uint64_t *super_keys_tmp, int *big_list, int *super_stats,
-                      int *tile_counts, int *tile_offsets, int *tile_stats, int *tile_temp, int *ids,
-                      bool force_wide_keys) {
+                      int *chunk_base, int *chunk_counts, int *tile_counts, int *tile_offsets, int *tile_stats,
+                      int *tile_temp, int *ids, bool force_wide_keys) {
     const int sxn = (tiles_x + kSuper - 1) / kSuper, syn = (tiles_y + kSuper - 1) / kSuper, NS = sxn * syn;
     const int T = tiles_x * tiles_y;
     auto *k = reinterpret_cast<unsigned long long *>(super_keys);
@@ -582,6 +729,13 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
                            s, n, chunk, sxn, NS, radii, r2, depths, super_offsets, super_cm, k);
     hipLaunchKernelGGL(packed ? k_sort_super<true> : k_sort_super<false>, dim3(NS), dim3(kSortThreads), 0, s, tiles_x,
                        tiles_y, sxn, super_offsets, k, r2, tile_counts, big_list, super_stats);
+    const bool big = super_max > kChunk;
+    // long lists: kChunk runs sorted on many workgroups, then merged
+    const dim3 big_grid(std::min(64, (super_max + kChunk - 1) / kChunk), 64);
+    if (big) {
+        hipLaunchKernelGGL(k_big_prep, dim3(1), dim3(1024), 0, s, super_offsets, big_list, super_stats, chunk_base);
+        hipLaunchKernelGGL(k_sort_chunks, big_grid, dim3(kSortThreads), 0, s, super_offsets, big_list, super_stats, k);
+    }
     unsigned long long *src = k, *dst = kt;
     for (int L = kChunk; L < super_max; L <<= 1) {
         hipLaunchKernelGGL(k_merge_pass, dim3(64, 64), dim3(256), 0, s, L, super_offsets, big_list, super_stats, src,
@@ -592,9 +746,17 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
     // every list is in super_keys for the emission
     if (src != k)
         hipLaunchKernelGGL(k_copy_big, dim3(64, 64), dim3(256), 0, s, super_offsets, big_list, super_stats, src, k);
+    if (big)
+        hipLaunchKernelGGL(packed ? k_count_chunks<true> : k_count_chunks<false>, big_grid, dim3(kSortThreads), 0, s,
+                           tiles_x, tiles_y, sxn, super_offsets, big_list, super_stats, chunk_base, k, r2,
+                           chunk_counts, tile_counts);
     launch_scan_counts(s, T, tile_counts, tile_offsets, nullptr, tile_stats, tile_temp);
     hipLaunchKernelGGL(packed ? k_emit_tiles<true> : k_emit_tiles<false>, dim3(NS), dim3(256), 0, s, tiles_x, tiles_y,
                        sxn, super_offsets, k, r2, tile_offsets, ids);
+    if (big)
+        hipLaunchKernelGGL(packed ? k_emit_chunks<true> : k_emit_chunks<false>, big_grid, dim3(256), 0, s, tiles_x,
+                           tiles_y, sxn, super_offsets, big_list, super_stats, chunk_base, chunk_counts, k, r2,
+                           tile_offsets, ids);
 }
 
 }  // namespace mskern
