@@ -61,7 +61,7 @@ struct Engine {
     DevBuf rec, depths, radii, rect, grads16, colors_raw;
     // per-tile
     DevBuf counts, offsets, stats, big_list, scan_tmp;
-    DevBuf chunk_base, chunk_counts;  // chunk numbering and tile counts of the long super-tile lists
+    DevBuf huge_list, chunk_base, chunk_counts;  // the longest super-tile lists, their chunk numbering and counts
     DevBuf super_counts, super_offsets, super_cm, super_tmp;  // super_cm: per-(workgroup, super-tile) offsets
     // per-intersection
     DevBuf keys, keys_tmp, ids;  // keys: per (splat, super-tile) pair
@@ -314,7 +314,8 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     CHECK(ensure(E.super_cm, (size_t)mskern::kBinMaxBlocks * NS * 4));
     CHECK(ensure(E.super_tmp, (size_t)mskern::tile_scan_temp_ints(NS) * 4));
     // stats (ints): [0..1] tiles: total, largest; [4..6] super-tiles: total,
-    // largest, long lists; [8..9] 64-bit intersection count from the projection
+    // largest, long lists; [8..9] 64-bit intersection count from the
+    // projection; [12..13] huge lists, their chunks
     CHECK(ensure(E.stats, 64));
     CHECK(ensure(E.big_list, (size_t)NS * 4));
     CHECK(ensure(E.out_img, Pn * 12));
@@ -365,16 +366,18 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     stage_mark(ST_SCATTER_SORT);
     CHECK(ensure(E.keys, (size_t)S_total * 8));
     CHECK(ensure(E.ids, (size_t)I * 4));
-    if (super_max > mskern::kSuperSortChunk) {
-        CHECK(ensure(E.keys_tmp, (size_t)S_total * 8));
+    if (super_max > mskern::kSuperSortChunk) CHECK(ensure(E.keys_tmp, (size_t)S_total * 8));
+    if (super_max > mskern::kSuperHugeList) {
+        CHECK(ensure(E.huge_list, (size_t)NS * 4));
         CHECK(ensure(E.chunk_base, (size_t)NS * 4));
         CHECK(ensure(E.chunk_counts, (size_t)mskern::big_chunk_ints(S_total, NS) * 4));
     }
     mskern::launch_bin_tiles(s, N, cam->tiles_x, cam->tiles_y, P<int>(E.radii), P<uint32_t>(E.rect),
                              P<float>(E.depths), P<int>(E.super_offsets), P<int>(E.super_cm), super_max,
                              P<uint64_t>(E.keys), P<uint64_t>(E.keys_tmp), P<int>(E.big_list), P<int>(E.stats) + 4,
-                             P<int>(E.chunk_base), P<int>(E.chunk_counts), P<int>(E.counts), P<int>(E.offsets),
-                             P<int>(E.stats), P<int>(E.scan_tmp), P<int>(E.ids), E.wide_keys);
+                             P<int>(E.huge_list), P<int>(E.stats) + 12, P<int>(E.chunk_base), P<int>(E.chunk_counts),
+                             P<int>(E.counts), P<int>(E.offsets), P<int>(E.stats), P<int>(E.scan_tmp), P<int>(E.ids),
+                             E.wide_keys);
     stage_mark(ST_RASTER_FWD);
     CHECK(raster_fwd_locked(log, full));
     HIPC(hipGetLastError());
@@ -503,7 +506,7 @@ void msplat_hip_cleanup(void) {
     if (!E.ready) return;
     (void)hipStreamSynchronize(E.stream);
     DevBuf *all[] = {&E.rec, &E.depths, &E.radii, &E.rect, &E.grads16, &E.colors_raw, &E.counts, &E.scan_tmp, &E.super_counts, &E.super_offsets, &E.super_cm, &E.super_tmp, &E.offsets,
-                     &E.stats, &E.big_list, &E.chunk_base, &E.chunk_counts, &E.keys, &E.keys_tmp, &E.ids, &E.blend_log, &E.t_ckpt, &E.wave_cnt, &E.selfcheck, &E.out_img, &E.final_Ts,
+                     &E.stats, &E.big_list, &E.huge_list, &E.chunk_base, &E.chunk_counts, &E.keys, &E.keys_tmp, &E.ids, &E.blend_log, &E.t_ckpt, &E.wave_cnt, &E.selfcheck, &E.out_img, &E.final_Ts,
                      &E.final_idx, &E.out_depth, &E.out_normal, &E.out_alpha, &E.out_median, &E.out_dist,
                      &E.dL_dimg, &E.gm1, &E.gs1, &E.gs12, &E.partials, &E.loss, &E.dmeans, &E.dscales,
                      &E.dquats, &E.dmean2d, &E.dfdc, &E.dfrest, &E.dens_flags, &E.dens_scan, &E.dens_keep, &E.pair_counter,

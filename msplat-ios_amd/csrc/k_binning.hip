@@ -33,6 +33,10 @@ namespace {
 
 constexpr int kSortThreads = 256;
 constexpr int kChunk = 4096;  // keys per LDS sort (32 KB of u64)
+// Lists longer than this are sorted, counted and emitted chunk-parallel
+// (their chunk sorts would otherwise hold one workgroup for longer than the
+// rest of the pass); shorter ones stay within their super-tile's workgroup.
+constexpr int kHuge = 4 * kChunk;
 constexpr int kSuper = 4;     // tiles per super-tile side
 
 // ---- counts -> offsets ------------------------------------------------------
@@ -384,17 +388,20 @@ __device__ __forceinline__ void count_tiles(const unsigned long long *__restrict
 }
 
 // Counts the entries of the super-tile's 16 tiles into tile_counts, then
-// sorts the super-tile list in place.  Lists longer than kChunk are only
-// queued on big_list (their tile counts zeroed): k_sort_chunks sorts them in
-// kChunk runs on many workgroups, the merge passes merge the runs, and
-// k_count_chunks / k_emit_chunks count and emit them chunk by chunk.
+// sorts the super-tile list in place: up to kChunk keys in one LDS sort,
+// up to kHuge in kChunk runs queued on big_list for the merge passes.
+// Longer lists are only queued, on big_list and huge_list (their tile counts
+// zeroed): k_sort_chunks sorts their runs on many workgroups, and after the
+// merge k_count_chunks / k_emit_chunks count and emit them chunk by chunk.
 template <bool PACKED>
 __global__ __launch_bounds__(kSortThreads) void k_sort_super(int tiles_x, int tiles_y, int sxn,
                                                              const int *__restrict__ offsets,
                                                              unsigned long long *__restrict__ keys,
                                                              const uint2 *__restrict__ rect,
                                                              int *__restrict__ tile_counts,
-                                                             int *__restrict__ big_list, int *__restrict__ stats) {
+                                                             int *__restrict__ big_list, int *__restrict__ stats,
+                                                             int *__restrict__ huge_list,
+                                                             int *__restrict__ huge_stats) {
     __shared__ unsigned long long s[kChunk];
     __shared__ int s_tc[kSuper * kSuper];
     const int t = blockIdx.x;
@@ -403,26 +410,31 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_super(int tiles_x, int ti
     const int stx = (t % sxn) * kSuper, sty = (t / sxn) * kSuper;
     if (threadIdx.x < kSuper * kSuper) s_tc[threadIdx.x] = 0;
     __syncthreads();
-    if (cnt <= kChunk) count_tiles<PACKED>(keys + start, cnt, stx, sty, rect, s_tc);
+    if (cnt <= kHuge) count_tiles<PACKED>(keys + start, cnt, stx, sty, rect, s_tc);
     if (threadIdx.x < kSuper * kSuper) {
         const int tx = stx + (int)threadIdx.x % kSuper, ty = sty + (int)threadIdx.x / kSuper;
         if (tx < tiles_x && ty < tiles_y) tile_counts[ty * tiles_x + tx] = s_tc[threadIdx.x];
     }
-    if (cnt > kChunk) {
-        if (threadIdx.x == 0) big_list[atomicAdd(&stats[2], 1)] = t;
+    if (cnt > kChunk && threadIdx.x == 0) big_list[atomicAdd(&stats[2], 1)] = t;
+    if (cnt > kHuge) {
+        if (threadIdx.x == 0) huge_list[atomicAdd(&huge_stats[0], 1)] = t;
         return;
     }
     if (cnt <= 1) return;
-    lds_bitonic(s, keys + start, cnt);
-    for (int i = threadIdx.x; i < cnt; i += kSortThreads) keys[start + i] = s[sort_slot(i)];
+    for (int c0 = start; c0 < end; c0 += kChunk) {
+        const int c = min(kChunk, end - c0);
+        lds_bitonic(s, keys + c0, c);
+        for (int i = threadIdx.x; i < c; i += kSortThreads) keys[c0 + i] = s[sort_slot(i)];
+        __syncthreads();
+    }
 }
 
-// Chunk numbering of the long lists: chunk_base[b] = the number of kChunk
-// chunks of big lists 0 .. b-1, stats[3] = all of them.  One workgroup.
+// Chunk numbering of the huge lists: chunk_base[b] = the number of kChunk
+// chunks of huge lists 0 .. b-1, huge_stats[1] = all of them.  One workgroup.
 __global__ __launch_bounds__(1024) void k_big_prep(const int *__restrict__ offsets, const int *__restrict__ big_list,
                                                    int *__restrict__ stats, int *__restrict__ chunk_base) {
     __shared__ int s_w[16];
-    const int nbig = stats[2];
+    const int nbig = stats[0];
     int carry = 0;
     for (int b0 = 0; b0 < nbig; b0 += 1024) {
         const int b = b0 + (int)threadIdx.x;
@@ -450,17 +462,17 @@ __global__ __launch_bounds__(1024) void k_big_prep(const int *__restrict__ offse
         if (b < nbig) chunk_base[b] = carry + off + incl - v;
         carry += tot;
     }
-    if (threadIdx.x == 0) stats[3] = carry;
+    if (threadIdx.x == 0) stats[1] = carry;
 }
 
-// Sorts every kChunk run of the long lists in LDS, one run per workgroup
+// Sorts every kChunk run of the huge lists in LDS, one run per workgroup
 // iteration (grid.y strides over the lists, grid.x over their runs).
 __global__ __launch_bounds__(kSortThreads) void k_sort_chunks(const int *__restrict__ offsets,
                                                               const int *__restrict__ big_list,
                                                               const int *__restrict__ stats,
                                                               unsigned long long *__restrict__ keys) {
     __shared__ unsigned long long s[kChunk];
-    const int nbig = stats[2];
+    const int nbig = stats[0];
     for (int b = blockIdx.y; b < nbig; b += gridDim.y) {
         const int t = big_list[b];
         const int start = offsets[t], cnt = offsets[t + 1] - start;
@@ -473,7 +485,7 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_chunks(const int *__restr
     }
 }
 
-// Tile counts of every kChunk chunk of the merged long lists:
+// Tile counts of every kChunk chunk of the merged huge lists:
 // chunk_counts[chunk_base[b] + c][16], summed into tile_counts.
 template <bool PACKED>
 __global__ __launch_bounds__(kSortThreads) void k_count_chunks(int tiles_x, int tiles_y, int sxn,
@@ -486,7 +498,7 @@ __global__ __launch_bounds__(kSortThreads) void k_count_chunks(int tiles_x, int 
                                                                int *__restrict__ chunk_counts,
                                                                int *__restrict__ tile_counts) {
     __shared__ int s_tc[kSuper * kSuper];
-    const int nbig = stats[2];
+    const int nbig = stats[0];
     for (int b = blockIdx.y; b < nbig; b += gridDim.y) {
         const int t = big_list[b];
         const int start = offsets[t], cnt = offsets[t + 1] - start;
@@ -609,7 +621,7 @@ __device__ __forceinline__ void emit_range(const unsigned long long *__restrict_
     }
 }
 
-// Emits each super-tile list of at most kChunk entries into its 16 tile
+// Emits each super-tile list of at most kHuge entries into its 16 tile
 // lists (longer lists: k_emit_chunks).
 template <bool PACKED>
 __global__ __launch_bounds__(256) void k_emit_tiles(int tiles_x, int tiles_y, int sxn,
@@ -622,7 +634,7 @@ __global__ __launch_bounds__(256) void k_emit_tiles(int tiles_x, int tiles_y, in
     const int st = blockIdx.x;
     const int stx = (st % sxn) * kSuper, sty = (st / sxn) * kSuper;
     const int start = soffsets[st], cnt = soffsets[st + 1] - start;
-    if (cnt > kChunk) return;
+    if (cnt > kHuge) return;
     const int ty = sty + (int)(threadIdx.x >> 6);
     int out[kSuper];
 #pragma unroll
@@ -633,7 +645,7 @@ __global__ __launch_bounds__(256) void k_emit_tiles(int tiles_x, int tiles_y, in
     emit_range<PACKED>(skeys + start, cnt, stx, sty, rect, out, s_gid, s_rr, ids);
 }
 
-// Emits every kChunk chunk of the long lists: a chunk's entries start in
+// Emits every kChunk chunk of the huge lists: a chunk's entries start in
 // each tile list after those of the chunks before it (chunk_counts).
 template <bool PACKED>
 __global__ __launch_bounds__(256) void k_emit_chunks(int tiles_x, int tiles_y, int sxn,
@@ -647,7 +659,7 @@ __global__ __launch_bounds__(256) void k_emit_chunks(int tiles_x, int tiles_y, i
                                                      const int *__restrict__ toffsets, int *__restrict__ ids) {
     __shared__ int s_gid[kWin];
     __shared__ unsigned short s_rr[kWin];
-    const int nbig = stats[2];
+    const int nbig = stats[0];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     for (int b = blockIdx.y; b < nbig; b += gridDim.y) {
         const int st = big_list[b];
@@ -714,8 +726,8 @@ void launch_super_count(hipStream_t s, int n, int tiles_x, int tiles_y, const in
 void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
                       const float *depths, const int *super_offsets, const int *super_cm, int super_max,
                       uint64_t *super_keys, uint64_t *super_keys_tmp, int *big_list, int *super_stats,
-                      int *chunk_base, int *chunk_counts, int *tile_counts, int *tile_offsets, int *tile_stats,
-                      int *tile_temp, int *ids, bool force_wide_keys) {
+                      int *huge_list, int *huge_stats, int *chunk_base, int *chunk_counts, int *tile_counts,
+                      int *tile_offsets, int *tile_stats, int *tile_temp, int *ids, bool force_wide_keys) {
     const int sxn = (tiles_x + kSuper - 1) / kSuper, syn = (tiles_y + kSuper - 1) / kSuper, NS = sxn * syn;
     const int T = tiles_x * tiles_y;
     auto *k = reinterpret_cast<unsigned long long *>(super_keys);
@@ -728,13 +740,13 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
         hipLaunchKernelGGL(packed ? k_scatter_super<true> : k_scatter_super<false>, dim3(blocks), dim3(kBinThreads), 0,
                            s, n, chunk, sxn, NS, radii, r2, depths, super_offsets, super_cm, k);
     hipLaunchKernelGGL(packed ? k_sort_super<true> : k_sort_super<false>, dim3(NS), dim3(kSortThreads), 0, s, tiles_x,
-                       tiles_y, sxn, super_offsets, k, r2, tile_counts, big_list, super_stats);
-    const bool big = super_max > kChunk;
-    // long lists: kChunk runs sorted on many workgroups, then merged
-    const dim3 big_grid(std::min(64, (super_max + kChunk - 1) / kChunk), 64);
+                       tiles_y, sxn, super_offsets, k, r2, tile_counts, big_list, super_stats, huge_list, huge_stats);
+    const bool big = super_max > kHuge;
+    // huge lists: kChunk runs sorted on many workgroups, then merged
+    const dim3 big_grid(std::min(256, (super_max + kChunk - 1) / kChunk), 16);
     if (big) {
-        hipLaunchKernelGGL(k_big_prep, dim3(1), dim3(1024), 0, s, super_offsets, big_list, super_stats, chunk_base);
-        hipLaunchKernelGGL(k_sort_chunks, big_grid, dim3(kSortThreads), 0, s, super_offsets, big_list, super_stats, k);
+        hipLaunchKernelGGL(k_big_prep, dim3(1), dim3(1024), 0, s, super_offsets, huge_list, huge_stats, chunk_base);
+        hipLaunchKernelGGL(k_sort_chunks, big_grid, dim3(kSortThreads), 0, s, super_offsets, huge_list, huge_stats, k);
     }
     unsigned long long *src = k, *dst = kt;
     for (int L = kChunk; L < super_max; L <<= 1) {
@@ -748,14 +760,14 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
         hipLaunchKernelGGL(k_copy_big, dim3(64, 64), dim3(256), 0, s, super_offsets, big_list, super_stats, src, k);
     if (big)
         hipLaunchKernelGGL(packed ? k_count_chunks<true> : k_count_chunks<false>, big_grid, dim3(kSortThreads), 0, s,
-                           tiles_x, tiles_y, sxn, super_offsets, big_list, super_stats, chunk_base, k, r2,
+                           tiles_x, tiles_y, sxn, super_offsets, huge_list, huge_stats, chunk_base, k, r2,
                            chunk_counts, tile_counts);
     launch_scan_counts(s, T, tile_counts, tile_offsets, nullptr, tile_stats, tile_temp);
     hipLaunchKernelGGL(packed ? k_emit_tiles<true> : k_emit_tiles<false>, dim3(NS), dim3(256), 0, s, tiles_x, tiles_y,
                        sxn, super_offsets, k, r2, tile_offsets, ids);
     if (big)
         hipLaunchKernelGGL(packed ? k_emit_chunks<true> : k_emit_chunks<false>, big_grid, dim3(256), 0, s, tiles_x,
-                           tiles_y, sxn, super_offsets, big_list, super_stats, chunk_base, chunk_counts, k, r2,
+                           tiles_y, sxn, super_offsets, huge_list, huge_stats, chunk_base, chunk_counts, k, r2,
                            tile_offsets, ids);
 }
 
