@@ -139,6 +139,11 @@ public:
     // model.cpp:273).
     void setMaxSplats(int maxSplats);
     void setCullAlphaThresh(float thresh);
+    // Replaces the scene with a Gaussian PLY (the reference CLI's --resume,
+    // Model::loadPly, core/src/model.cpp:329-340; 3-scale rows keep their
+    // first two scales) and resets the optimiser; the iteration becomes the
+    // step recorded in the file.  Returns it.
+    int loadPly(const std::string &path);
 
 private:
     struct Impl;

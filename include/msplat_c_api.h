@@ -148,6 +148,10 @@ const char *msplat_last_error(void);
  * threshold on sigmoid(opacity) (0.1 by default). */
 void msplat_trainer_set_max_splats(MsplatTrainer t, int maxSplats);
 void msplat_trainer_set_cull_alpha(MsplatTrainer t, float thresh);
+/* Scene from a Gaussian PLY, resuming at the step the file records: the
+ * reference CLI's --resume (Model::loadPly, core/src/model.cpp:329-340,
+ * cli/msplat.cpp:259).  Returns that step, or -1 (msplat_last_error). */
+int msplat_trainer_load_ply(MsplatTrainer t, const char *path);
 
 #ifdef __cplusplus
 }

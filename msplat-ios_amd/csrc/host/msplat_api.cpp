@@ -243,6 +243,12 @@ int Trainer::loadCheckpoint(const std::string &path) {
 
 int Trainer::splatCount() const { return (int)impl->model->means.size(0); }
 int Trainer::iteration() const { return impl->currentStep; }
+int Trainer::loadPly(const std::string &path) {
+    impl->currentStep = impl->model->loadPly(path);
+    impl->shuffleCameras();
+    return impl->currentStep;
+}
+
 void Trainer::setMaxSplats(int maxSplats) { impl->model->maxSplats = maxSplats; }
 void Trainer::setCullAlphaThresh(float thresh) { impl->model->cullAlphaThresh = thresh; }
 
@@ -425,6 +431,9 @@ int msplat_trainer_splat_count(MsplatTrainer t) {
 }
 int msplat_trainer_iteration(MsplatTrainer t) {
     return guarded(0, [&] { return T(t)->iteration(); });
+}
+int msplat_trainer_load_ply(MsplatTrainer t, const char *path) {
+    return guarded(-1, [&] { return T(t)->loadPly(path ? path : ""); });
 }
 void msplat_trainer_set_max_splats(MsplatTrainer t, int maxSplats) {
     guarded(0, [&] {

@@ -33,8 +33,14 @@ namespace {
 
 constexpr int TS = 32, RAD = 5;   // output tile TS x TS
 constexpr int RS = TS + 2 * RAD;  // 42: region rows / columns with halo
-constexpr int AST = 44;           // LDS row stride of a staged region
-constexpr int BST = 36;           // LDS row stride of horizontal results
+#ifndef MS_SSIM_AST
+#define MS_SSIM_AST 44
+#endif
+#ifndef MS_SSIM_BST
+#define MS_SSIM_BST 36
+#endif
+constexpr int AST = MS_SSIM_AST;  // LDS row stride of a staged region
+constexpr int BST = MS_SSIM_BST;  // LDS row stride of horizontal results
 constexpr int kThreads = 256;
 constexpr int kHItems = RS * (TS / 4);  // 336 horizontal items (row, 4 columns)
 
@@ -242,14 +248,22 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 4))
 }
 
 // Adjoint blur of the three gradient maps + ssim_backward_accumulate_kernel
-// (msplat_metal.metal:3059-3085) + the L1 gradient.
+// (msplat_metal.metal:3059-3085) + the L1 gradient.  The horizontal results
+// are held in registers across a barrier and written over the staged maps,
+// so a workgroup needs 22 KB of LDS (seven per CU).
+constexpr int kHIter = (kHItems + kThreads - 1) / kThreads;  // horizontal items per thread (2)
+
 __global__ __launch_bounds__(kThreads) void k_ssim_bwd(int W, int H, const float *__restrict__ img,
                                                        const float *__restrict__ gt, const float *__restrict__ gm1,
                                                        const float *__restrict__ gs1,
                                                        const float *__restrict__ gs12, float lambda_l1, float inv_np,
                                                        Window win, float *__restrict__ dL_dimg) {
-    __shared__ __align__(16) float s_g[3][RS][AST];
-    __shared__ __align__(16) float s_h[3][RS][BST];
+    // staged maps [3][RS][AST]; after the horizontal pass the same memory
+    // holds its results [3][RS][BST]
+    __shared__ __align__(16) float s_lds[3 * RS * AST];
+    float(*s_g)[RS][AST] = reinterpret_cast<float(*)[RS][AST]>(s_lds);
+    float(*s_h)[RS][BST] = reinterpret_cast<float(*)[RS][BST]>(s_lds);
+    static_assert(BST <= AST, "horizontal results alias the staged maps");
     const int tiles_x = (W + TS - 1) / TS, T = tiles_x * ((H + TS - 1) / TS);
     const int tile = msd::xcd_tile(blockIdx.x, T);
     if (tile >= T) return;
@@ -287,7 +301,11 @@ __global__ __launch_bounds__(kThreads) void k_ssim_bwd(int W, int H, const float
             stage_load(gs1 + po, W, H, x0, y0, 1, 0, n1);
             stage_load(gs12 + po, W, H, x0, y0, 1, 0, n2);
         }
-        for (int it = threadIdx.x; it < kHItems; it += kThreads) {
+        float hr[kHIter][3][4];
+#pragma unroll
+        for (int q = 0; q < kHIter; ++q) {
+            const int it = (int)threadIdx.x + q * kThreads;
+            if (it >= kHItems) continue;
             const int ry = it >> 3, xg = (it & 7) * 4;
 #pragma unroll
             for (int m = 0; m < 3; ++m) {
@@ -298,8 +316,20 @@ __global__ __launch_bounds__(kThreads) void k_ssim_bwd(int W, int H, const float
                 for (int j = 0; j < 11; ++j)
 #pragma unroll
                     for (int o = 0; o < 4; ++o) h[o] = __builtin_fmaf(win.w[j], v[o + j], h[o]);
-                *reinterpret_cast<float4 *>(&s_h[m][ry][xg]) = make_float4(h[0], h[1], h[2], h[3]);
+#pragma unroll
+                for (int o = 0; o < 4; ++o) hr[q][m][o] = h[o];
             }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < kHIter; ++q) {
+            const int it = (int)threadIdx.x + q * kThreads;
+            if (it >= kHItems) continue;
+            const int ry = it >> 3, xg = (it & 7) * 4;
+#pragma unroll
+            for (int m = 0; m < 3; ++m)
+                *reinterpret_cast<float4 *>(&s_h[m][ry][xg]) = make_float4(hr[q][m][0], hr[q][m][1], hr[q][m][2],
+                                                                           hr[q][m][3]);
         }
         __syncthreads();
         float bl[3][4];

@@ -297,6 +297,9 @@ PYBIND11_MODULE(_core, m) {
             "load_checkpoint", [](Trainer &t, const std::string &p) { t.t.loadCheckpoint(p); }, "path"_a,
             "Load a training checkpoint and resume from the saved iteration.")
         .def(
+            "load_ply", [](Trainer &t, const std::string &p) { return t.t.loadPly(p); }, "path"_a,
+            "Replace the scene with a Gaussian PLY and resume at the step it records.")
+        .def(
             "set_max_splats", [](Trainer &t, int n) { t.t.setMaxSplats(n); }, "max_splats"_a,
             "Densification cap (250000 by default).")
         .def(

@@ -84,6 +84,7 @@ def lib() -> C.CDLL:
         "msplat_trainer_load_checkpoint": (I, [V, P]),
         "msplat_trainer_splat_count": (I, [V]),
         "msplat_trainer_iteration": (I, [V]),
+        "msplat_trainer_load_ply": (I, [V, P]),
         "msplat_trainer_set_max_splats": (None, [V, I]),
         "msplat_trainer_set_cull_alpha": (None, [V, F]),
         "msplat_set_metallib_path": (None, [P]),

@@ -58,3 +58,14 @@ def test_prepare_camera_rejects_bad_sizes():
     from msplat import _engine as E
     with pytest.raises(E.MsplatError):
         E.prepare_camera(np.eye(4), 100.0, 100.0, 50.0, 50.0, 0, 10)
+
+
+def test_ctypes_binding_covers_c_api_header():
+    """msplat.capi binds every function of the public C ABI."""
+    import re as _re
+
+    from msplat import capi
+    src = (REPO / "msplat-ios_amd" / "msplat" / "capi.py").read_text()
+    bound = set(_re.findall(r'"(msplat_\w+)":', src))
+    assert sorted(bound) == _declared(REPO / "include" / "msplat_c_api.h")
+    capi.lib()  # every signature binds
