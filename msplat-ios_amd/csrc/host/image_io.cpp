@@ -2,8 +2,9 @@
 // input_data.cpp, and Brown-Conrady undistortion
 // (core/src/loaders/image_io.cpp of the reference, which decodes through
 // CoreGraphics).  Decoders here: PNG (bit depth 1-16, grey / grey+alpha /
-// RGB / RGBA / palette, non-interlaced and Adam7) through zlib, and binary
-// PPM/PGM.  Output is float32 RGB in [0,1]; alpha is dropped.
+// RGB / RGBA / palette, non-interlaced and Adam7) through zlib, binary
+// PPM/PGM, and JPEG (jpeg.cpp).  Output is float32 RGB in [0,1]; alpha is
+// dropped.
 #include <zlib.h>
 
 #include <algorithm>
@@ -232,12 +233,14 @@ void distort_point(float x, float y, float k1, float k2, float p1, float p2, flo
 
 }  // namespace
 
+// jpeg.cpp
+Image decode_jpeg(const std::vector<uint8_t> &f, const std::string &path);
+
 Image imreadRGB(const std::string &path) {
     const std::vector<uint8_t> f = read_file(path);
     if (f.size() >= 8 && f[0] == 137 && f[1] == 'P' && f[2] == 'N' && f[3] == 'G') return decode_png(f, path);
     if (f.size() >= 2 && f[0] == 'P' && (f[1] == '6' || f[1] == '5')) return decode_pnm(f, path);
-    if (f.size() >= 3 && f[0] == 0xFF && f[1] == 0xD8)
-        throw std::runtime_error("JPEG images are not decoded by this build; convert " + path + " to PNG");
+    if (f.size() >= 3 && f[0] == 0xFF && f[1] == 0xD8) return decode_jpeg(f, path);
     throw std::runtime_error("unrecognised image format: " + path);
 }
 

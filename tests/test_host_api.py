@@ -7,6 +7,8 @@ import ctypes as C
 import json
 import re
 import struct
+import subprocess
+import sys
 import zlib
 from pathlib import Path
 
@@ -232,6 +234,115 @@ def test_pnm_decoder(tmp_path):
     assert np.abs(_core._read_image(str(tmp_path / "b.pgm")) - np.repeat(g[..., None] / 65535.0, 3, 2)).max() < 1e-6
     with pytest.raises(RuntimeError):
         _core._read_image(str(tmp_path / "missing.png"))
+
+
+# ------------------------------------------------------------------ JPEG --
+JPEG_DIR = Path(__file__).resolve().parent / "golden" / "jpeg"
+
+
+def test_jpeg_decoder_matches_libjpeg_fixtures():
+    """Baseline (4:2:0, 4:2:2, 4:4:4, odd sizes, greyscale, optimised
+    tables, low quality), progressive and restart-interval JPEGs encoded by
+    PIL, against PIL's own decoding (tests/golden/make_jpeg_fixtures.py).
+    Both decoders run a compliant 8x8 inverse DCT, and two compliant
+    inverse DCTs may differ by one level per sample (IEEE 1180); the colour
+    transform carries a chroma difference into RGB scaled by up to 1.772.
+    So greyscale must agree to +-1, colour to +-3 with under 1% of samples
+    off by more than 1 and a mean difference under 0.1 levels."""
+    from msplat import _core
+    exp = np.load(JPEG_DIR / "jpeg_expected.npz")
+    assert len(exp.files) >= 12
+    for name in exp.files:
+        got = np.asarray(_core._read_image(str(JPEG_DIR / f"{name}.jpg")))
+        want = exp[name].astype(np.int32)
+        assert got.shape == want.shape, name
+        d = np.abs(np.round(got * 255.0).astype(np.int32) - want)
+        grey = "grey" in name
+        assert d.max() <= (1 if grey else 3), (name, d.max())
+        assert (d > 1).mean() < 0.01 and d.mean() < 0.1, (name, (d > 1).mean(), d.mean())
+
+
+def test_jpeg_decoder_rejects_bad_input(tmp_path):
+    """Truncated data, arithmetic coding, 12-bit samples and garbage raise
+    (a RuntimeError through the bindings), they do not crash."""
+    from msplat import _core
+    raw = (JPEG_DIR / "base420.jpg").read_bytes()
+    cases = {"trunc_header": raw[:40], "garbage": b"\xff\xd8" + bytes(range(256)) * 4}
+    sof = raw.index(b"\xff\xc0")
+    cases["arith"] = raw[:sof] + b"\xff\xc9" + raw[sof + 2:]
+    cases["12bit"] = raw[:sof + 4] + b"\x0c" + raw[sof + 5:]
+    for name, blob in cases.items():
+        (tmp_path / f"{name}.jpg").write_bytes(blob)
+        with pytest.raises(RuntimeError):
+            _core._read_image(str(tmp_path / f"{name}.jpg"))
+
+
+def test_jpeg_decoder_survives_corruption(tmp_path):
+    """Hundreds of randomly truncated or byte-flipped fixtures decode or
+    raise; the process must not crash (run in a child process)."""
+    script = tmp_path / "fuzz.py"
+    script.write_text(f"""
+import sys, random
+sys.path.insert(0, {str(Path(__file__).resolve().parent.parent / 'msplat-ios_amd')!r})
+from pathlib import Path
+from msplat import _core
+rng = random.Random(7)
+files = sorted(Path({str(JPEG_DIR)!r}).glob('*.jpg'))
+out = Path({str(tmp_path)!r}) / 'x.jpg'
+ok = bad = 0
+for k in range(400):
+    raw = bytearray(rng.choice(files).read_bytes())
+    if k % 2:
+        raw = raw[: rng.randrange(2, len(raw))]
+    for _ in range(rng.randrange(1, 6)):
+        raw[rng.randrange(2, len(raw))] = rng.randrange(256)
+    out.write_bytes(bytes(raw))
+    try:
+        _core._read_image(str(out))
+        ok += 1
+    except RuntimeError:
+        bad += 1
+print(ok, bad)
+""")
+    r = subprocess.run([sys.executable, str(script)], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    ok, bad = map(int, r.stdout.split())
+    assert ok + bad == 400
+
+
+def test_colmap_loader_with_jpeg_images(tmp_path):
+    """A COLMAP capture whose images are JPEG (as real captures ship) loads
+    through the dataset API; the decoded pixels reach the cameras."""
+    import msplat
+    from PIL import Image
+
+    sp = tmp_path / "sparse" / "0"
+    sp.mkdir(parents=True)
+    (tmp_path / "images").mkdir()
+    rng = np.random.default_rng(6)
+    for i in range(3):
+        s = (rng.uniform(0, 1, (12, 16, 3)) * 255).astype(np.uint8)
+        Image.fromarray(s).save(tmp_path / "images" / f"frame_{i:03d}.jpg", quality=90)
+    poses_gl = [_look_at_c2w((2 * np.cos(a), 0.5, 2 * np.sin(a))) for a in (0.1, 1.2, 2.3)]
+    with open(sp / "cameras.bin", "wb") as f:
+        f.write(struct.pack("<Q", 1))
+        f.write(struct.pack("<IiQQ", 1, 1, 16, 12) + struct.pack("<4d", 20.0, 21.0, 8.0, 6.0))
+    with open(sp / "images.bin", "wb") as f:
+        f.write(struct.pack("<Q", 3))
+        for i, c2w in enumerate(poses_gl):
+            cv = c2w.copy()
+            cv[:3, 1:3] *= -1
+            R = cv[:3, :3].T
+            t = -R @ cv[:3, 3]
+            f.write(struct.pack("<I", i + 1) + struct.pack("<4d", *_qvec(R)) + struct.pack("<3d", *t))
+            f.write(struct.pack("<I", 1) + f"frame_{i:03d}.jpg".encode() + b"\0")
+            f.write(struct.pack("<Q", 0))
+    with open(sp / "points3D.bin", "wb") as f:
+        f.write(struct.pack("<Q", 4))
+        for k, p in enumerate(rng.normal(size=(4, 3))):
+            f.write(struct.pack("<Q3d3Bd", k, *p, 1, 2, 3, 0.5) + struct.pack("<Q", 1) + struct.pack("<II", 1, 0))
+    ds = msplat.Dataset(str(tmp_path))
+    assert ds.num_train == 3
 
 
 # --------------------------------------------------------------- loaders --
