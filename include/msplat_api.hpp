@@ -125,10 +125,17 @@ public:
     void renderFromPoseToBuffer(const float camToWorld[16], int refCameraIndex, uint8_t *outRGBA, int *outWidth,
                                 int *outHeight);
     void exportPly(const std::string &path);
-    // TSDF fusion + marching cubes is not part of this build: throws.
+    // TSDF fusion of every training camera's render into a cube of side
+    // 2 * boundRadius around the origin (voxels of voxelSize, truncation
+    // truncMultiplier voxels), then marching cubes -> non-indexed triangle
+    // PLY at path; returns the triangle count (msplat_api.hpp:138-148).
     int64_t extractMesh(const std::string &path, float voxelSize = 0.004f, float boundRadius = 0.3f,
                         float alphaThresh = 0.5f, float truncMultiplier = 4.0f);
     void exportSplat(const std::string &path);
+    // The unprojected depth of every training camera as a coloured PLY
+    // point cloud (Model::exportPointCloud, driven by the reference CLI's
+    // --export-point-cloud, cli/msplat.cpp:285-291); returns the point count.
+    int64_t exportPointCloud(const std::string &path, float alphaThresh = 0.5f);
     void saveCheckpoint(const std::string &path);
     int loadCheckpoint(const std::string &path);
     int splatCount() const;

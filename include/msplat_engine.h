@@ -332,6 +332,62 @@ int msplat_hip_check_fast_rcp(int efield_lo, int efield_hi, int64_t *mismatches)
  * lists are the same either way.  No counterpart in the reference. */
 int msplat_hip_set_wide_keys(int on);
 
+/* ---- mesh extraction: TSDF fusion, marching cubes, depth unprojection ----
+ * The voxel grid is [Dz, Dy, Dx, 2] f32 (sdf, weight) in HBM, voxel (x, y, z)
+ * centred at origin + voxel_size * (index + 0.5) (Model::VoxelGrid,
+ * core/include/model.hpp:51-56). */
+
+/* One depth view of msplat_hip_tsdf_integrate: the per-camera inputs of
+ * tsdf_integrate_kernel (core/metal/msplat_metal.metal:2223-2234). */
+typedef struct {
+    float viewmat[16];       /* world -> camera (OpenCV), row-major         */
+    float fx, fy, cx, cy;    /* intrinsics at the depth map's resolution    */
+    int32_t width, height;   /* of the depth and alpha maps                 */
+    const float *depth_dev;  /* [H,W] surface depth (median depth)          */
+    const float *alpha_dev;  /* [H,W] accumulated alpha                     */
+} MsplatTsdfView;
+
+/* msplat_tsdf_integrate (bindings.h:82-93, msplat_metal.mm:836-881) for
+ * num_views views at once: every voxel folds the views in array order,
+ * which is what num_views successive single-view calls (the reference's
+ * loop, model.cpp:723-757) compute, reading and writing the grid once.
+ * views is host memory; the depth / alpha maps must stay valid until the
+ * work completes (asynchronous; msplat_hip_sync waits). */
+int msplat_hip_tsdf_integrate(float *grid_dev, int dx, int dy, int dz, const float origin[3],
+                              float voxel_size, const MsplatTsdfView *views, int num_views,
+                              float trunc_dist, float alpha_thresh);
+
+/* msplat_marching_cubes (bindings.h:66-77, msplat_metal.mm:790-834): one
+ * triangle list (9 floats per triangle, world space, non-indexed) from the
+ * grid; cells with a corner of weight <= 0 are skipped.  Triangles come in
+ * cell order (x fastest, then y, then z), each cell's in case-table order,
+ * so the output is deterministic; the first max_triangles of them are
+ * written to tris_dev [max_triangles, 9].  *num_triangles = the number
+ * written (the reference's return value), *num_emitted (optional) = the
+ * number the grid produces.  Synchronous. */
+int msplat_hip_marching_cubes(const float *grid_dev, int dx, int dy, int dz, const float origin[3],
+                              float voxel_size, int64_t max_triangles, float *tris_dev,
+                              int64_t *num_triangles, int64_t *num_emitted);
+
+/* The case table msplat_hip_marching_cubes uses (256 rows of 16 edge
+ * indices, 3 per triangle, -1 terminated; edges and corners numbered as
+ * msplat_metal.metal:2594-2604), generated from the corner signs; host
+ * only, no device needed. */
+int msplat_hip_mc_table(int8_t tri[256 * 16]);
+
+/* The unprojection of Model::exportPointCloud (core/src/model.cpp:565-640,
+ * a host loop there) for one rendered view: every pixel with alpha >=
+ * alpha_thresh and finite positive depth / alpha gives one world-space
+ * point (the OpenCV ray through the pixel centre, rotated by camToWorld
+ * with columns 1 and 2 negated) and its colour (uint8)(clamp(rgb * 255, 0,
+ * 255)).  Points come in pixel order (row-major).  xyz_dev [H*W, 3] and
+ * rgb_dev [H*W, 3] have room for every pixel; *num_points = points written.
+ * Synchronous. */
+int msplat_hip_unproject_depth(const float *img_dev, const float *depth_dev, const float *alpha_dev,
+                               int width, int height, float fx, float fy, float cx, float cy,
+                               const float cam_to_world[16], float alpha_thresh, float *xyz_dev,
+                               uint8_t *rgb_dev, int64_t *num_points);
+
 #ifdef __cplusplus
 }
 #endif

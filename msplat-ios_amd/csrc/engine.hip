@@ -78,6 +78,9 @@ struct Engine {
     DevBuf dens_scratch[18], dens_flags, dens_scan, dens_keep;
     DevBuf pair_counter;
     DevBuf rgba;  // RGBA8 staging of msplat_hip_image_to_rgba8
+    // mesh extraction: TSDF view records, marching-cubes case bytes, and the
+    // per-chunk counts / scanned offsets of the two compactions
+    DevBuf tsdf_views, mc_cases, chunk_cnt, chunk_off;
     // state of the most recent forward
     int n = 0, W = 0, H = 0, tiles_x = 0, tiles_y = 0, K3 = 0;
     int64_t num_isect = 0;
@@ -629,12 +632,137 @@ int msplat_hip_image_to_rgba8(const float *img, int64_t num_pixels, uint8_t *rgb
     API_END
 }
 
+// ---- mesh extraction ------------------------------------------------------
+
+int msplat_hip_mc_table(int8_t tri[256 * 16]) {
+    if (!tri) {
+        set_err("null table");
+        return MSPLAT_E_ARG;
+    }
+    mskern::mc_table_host(tri);
+    return MSPLAT_OK;
+}
+
+namespace {
+bool grid_args_ok(const float *grid, int dx, int dy, int dz, const float origin[3]) {
+    if (!grid || !origin || dx < 1 || dy < 1 || dz < 1 || dz > 65535 ||
+        (uint64_t)dx * (uint64_t)dy >= (uint64_t(1) << 32)) {
+        set_err("invalid voxel grid (%d x %d x %d)", dx, dy, dz);
+        return false;
+    }
+    return true;
+}
+}  // namespace
+
+int msplat_hip_tsdf_integrate(float *grid, int dx, int dy, int dz, const float origin[3], float voxel_size,
+                              const MsplatTsdfView *views, int num_views, float trunc_dist, float alpha_thresh) {
+    API_BEGIN
+    ENSURE_INIT();
+    if (!grid_args_ok(grid, dx, dy, dz, origin)) return MSPLAT_E_ARG;
+    if (num_views < 0 || (num_views > 0 && !views)) {
+        set_err("invalid TSDF views");
+        return MSPLAT_E_ARG;
+    }
+    for (int k = 0; k < num_views; ++k)
+        if (views[k].width < 1 || views[k].height < 1 || !views[k].depth_dev || !views[k].alpha_dev) {
+            set_err("TSDF view %d: empty map or null pointer", k);
+            return MSPLAT_E_ARG;
+        }
+    if (num_views == 0) return MSPLAT_OK;
+    Engine &E = g_eng;
+    const size_t bytes = (size_t)num_views * sizeof(MsplatTsdfView);
+    CHECK(ensure(E.tsdf_views, bytes));
+    HIPC(hipMemcpyAsync(E.tsdf_views.p, views, bytes, hipMemcpyHostToDevice, E.stream));
+    mskern::launch_tsdf_integrate(E.stream, grid, dx, dy, dz, origin, voxel_size, P<MsplatTsdfView>(E.tsdf_views),
+                                  num_views, trunc_dist, alpha_thresh);
+    HIPC(hipGetLastError());
+    // the view records are rewritten by the next call
+    HIPC(hipStreamSynchronize(E.stream));
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_marching_cubes(const float *grid, int dx, int dy, int dz, const float origin[3], float voxel_size,
+                              int64_t max_triangles, float *tris, int64_t *num_triangles, int64_t *num_emitted) {
+    API_BEGIN
+    ENSURE_INIT();
+    if (!grid_args_ok(grid, dx, dy, dz, origin)) return MSPLAT_E_ARG;
+    if (!num_triangles || max_triangles < 0 || (max_triangles > 0 && !tris)) {
+        set_err("invalid marching-cubes output");
+        return MSPLAT_E_ARG;
+    }
+    *num_triangles = 0;
+    if (num_emitted) *num_emitted = 0;
+    const int64_t nc = mskern::mc_num_cells(dx, dy, dz);
+    if (nc == 0) return MSPLAT_OK;
+    const int64_t nch = mskern::mesh_chunks(nc);
+    if (nch > (int64_t)INT_MAX) {
+        set_err("voxel grid too large");
+        return MSPLAT_E_ARG;
+    }
+    Engine &E = g_eng;
+    hipStream_t s = E.stream;
+    CHECK(ensure(E.mc_cases, (size_t)nch * mskern::kMeshChunk));
+    CHECK(ensure(E.chunk_cnt, (size_t)nch * 4));
+    CHECK(ensure(E.chunk_off, (size_t)(nch + 1) * 8));
+    mskern::launch_mc_classify(s, grid, dx, dy, dz, P<uint8_t>(E.mc_cases), P<uint32_t>(E.chunk_cnt));
+    mskern::launch_chunk_scan(s, P<uint32_t>(E.chunk_cnt), nch, P<uint64_t>(E.chunk_off));
+    if (max_triangles > 0)
+        mskern::launch_mc_emit(s, grid, dx, dy, dz, origin, voxel_size, P<uint8_t>(E.mc_cases),
+                               P<uint64_t>(E.chunk_off), max_triangles, tris);
+    HIPC(hipGetLastError());
+    HIPC(hipMemcpyAsync(E.pinned_d, P<uint64_t>(E.chunk_off) + nch, 8, hipMemcpyDeviceToHost, s));
+    HIPC(hipStreamSynchronize(s));
+    uint64_t total;
+    std::memcpy(&total, E.pinned_d, 8);
+    *num_triangles = std::min<int64_t>((int64_t)total, max_triangles);
+    if (num_emitted) *num_emitted = (int64_t)total;
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_unproject_depth(const float *img, const float *depth, const float *alpha, int width, int height,
+                               float fx, float fy, float cx, float cy, const float cam_to_world[16],
+                               float alpha_thresh, float *xyz, uint8_t *rgb, int64_t *num_points) {
+    API_BEGIN
+    ENSURE_INIT();
+    if (!num_points || !cam_to_world || width < 0 || height < 0 ||
+        ((int64_t)width * height > 0 && (!img || !depth || !alpha || !xyz || !rgb))) {
+        set_err("invalid unprojection arguments");
+        return MSPLAT_E_ARG;
+    }
+    *num_points = 0;
+    const int64_t np = (int64_t)width * height;
+    if (np == 0) return MSPLAT_OK;
+    const int64_t nch = mskern::mesh_chunks(np);
+    Engine &E = g_eng;
+    hipStream_t s = E.stream;
+    CHECK(ensure(E.chunk_cnt, (size_t)nch * 4));
+    CHECK(ensure(E.chunk_off, (size_t)(nch + 1) * 8));
+    mskern::launch_unproject_count(s, img, depth, alpha, width, height, fx, fy, cx, cy, cam_to_world, alpha_thresh,
+                                   P<uint32_t>(E.chunk_cnt));
+    mskern::launch_chunk_scan(s, P<uint32_t>(E.chunk_cnt), nch, P<uint64_t>(E.chunk_off));
+    mskern::launch_unproject_emit(s, img, depth, alpha, width, height, fx, fy, cx, cy, cam_to_world, alpha_thresh,
+                                  P<uint64_t>(E.chunk_off), xyz, rgb);
+    HIPC(hipGetLastError());
+    HIPC(hipMemcpyAsync(E.pinned_d, P<uint64_t>(E.chunk_off) + nch, 8, hipMemcpyDeviceToHost, s));
+    HIPC(hipStreamSynchronize(s));
+    uint64_t total;
+    std::memcpy(&total, E.pinned_d, 8);
+    *num_points = (int64_t)total;
+    return MSPLAT_OK;
+    API_END
+}
+
 int msplat_hip_render(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, int64_t *nisect) {
     API_BEGIN
     ENSURE_INIT();
     CHECK(forward_locked(cam, g, bg, nisect, false, false));
     stage_mark(ST_LOSS);
-    if (g_eng.count_pairs) HIPC(hipMemcpy(g_eng.pairs, g_eng.pair_counter.p, 40, hipMemcpyDeviceToHost));
+    if (g_eng.count_pairs) {
+        HIPC(hipMemcpyAsync(g_eng.pairs, g_eng.pair_counter.p, 40, hipMemcpyDeviceToHost, g_eng.stream));
+        HIPC(hipStreamSynchronize(g_eng.stream));
+    }
     if (g_eng.timing) {
         HIPC(hipStreamSynchronize(g_eng.stream));
         for (int i = ST_PROJECT; i < ST_LOSS; ++i) {
@@ -699,7 +827,10 @@ int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g, con
     HIPC(hipGetLastError());
     HIPC(hipStreamSynchronize(s));
     if (loss_host) *loss_host = (float)E.pinned_d[0];
-    if (E.count_pairs) HIPC(hipMemcpy(E.pairs, E.pair_counter.p, 40, hipMemcpyDeviceToHost));
+    if (E.count_pairs) {
+        HIPC(hipMemcpyAsync(E.pairs, E.pair_counter.p, 40, hipMemcpyDeviceToHost, s));
+        HIPC(hipStreamSynchronize(s));
+    }
     if (E.timing) {
         for (int i = 0; i < ST_COUNT; ++i) {
             HIPC(hipEventElapsedTime(&E.stage_ms[i], E.ev[i], E.ev[i + 1]));

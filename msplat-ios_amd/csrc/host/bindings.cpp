@@ -1,6 +1,8 @@
 // bindings.cpp -- C++ engine interface over the C-ABI launch layer.
 #include "bindings.hpp"
 
+#include <algorithm>
+#include <cstdint>
 #include <cstring>
 #include <stdexcept>
 #include <string>
@@ -216,4 +218,42 @@ int msplat_densify(int N, int buf_capacity, float grad_thresh, float size_thresh
     if (rc == MSPLAT_E_CAPACITY) return -new_count;
     check(rc);
     return new_count;
+}
+
+int64_t msplat_marching_cubes(MTensor &grid, int Dx, int Dy, int Dz, float origin_x, float origin_y, float origin_z,
+                              float voxelSize, int maxTriangles, std::vector<float> &triangles) {
+    if (!grid.isGpu() || grid.numel() != (int64_t)Dx * Dy * Dz * 2)
+        throw std::invalid_argument("marching cubes: grid must be a device [Dz, Dy, Dx, 2] tensor");
+    const float origin[3] = {origin_x, origin_y, origin_z};
+    const int64_t cap = std::max(maxTriangles, 0);
+    MTensor out = MTensor::device({std::max<int64_t>(cap, 1), 9}, DType::Float32);
+    int64_t written = 0;
+    check(msplat_hip_marching_cubes(grid.data<float>(), Dx, Dy, Dz, origin, voxelSize, cap, out.data<float>(),
+                                    &written, nullptr));
+    triangles.resize((size_t)written * 9);
+    if (written > 0) check(msplat_hip_download(triangles.data(), out.data_ptr(), (size_t)written * 36));
+    return written;
+}
+
+void msplat_tsdf_integrate(MTensor &grid, int Dx, int Dy, int Dz, float origin_x, float origin_y, float origin_z,
+                           float voxelSize, MTensor &viewmat, float fx, float fy, float cx, float cy, uint32_t imgW,
+                           uint32_t imgH, float truncDist, float alphaThresh, MTensor &depthMap, MTensor &alphaMap) {
+    if (!grid.isGpu() || grid.numel() != (int64_t)Dx * Dy * Dz * 2)
+        throw std::invalid_argument("TSDF: grid must be a device [Dz, Dy, Dx, 2] tensor");
+    if (!depthMap.isGpu() || !alphaMap.isGpu() || depthMap.numel() < (int64_t)imgW * imgH ||
+        alphaMap.numel() < (int64_t)imgW * imgH)
+        throw std::invalid_argument("TSDF: depth / alpha must be device [H, W] maps");
+    MsplatTsdfView v{};
+    host_copy16(viewmat, v.viewmat);
+    v.fx = fx;
+    v.fy = fy;
+    v.cx = cx;
+    v.cy = cy;
+    v.width = (int32_t)imgW;
+    v.height = (int32_t)imgH;
+    v.depth_dev = depthMap.data<float>();
+    v.alpha_dev = alphaMap.data<float>();
+    const float origin[3] = {origin_x, origin_y, origin_z};
+    check(msplat_hip_tsdf_integrate(grid.data<float>(), Dx, Dy, Dz, origin, voxelSize, &v, 1, truncDist,
+                                    alphaThresh));
 }

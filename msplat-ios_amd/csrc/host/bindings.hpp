@@ -86,3 +86,14 @@ int msplat_densify(int N, int buf_capacity, float grad_thresh, float size_thresh
                    MTensor &dup_flag, MTensor &split_prefix, MTensor &dup_prefix, MTensor &keep_flag,
                    MTensor &keep_prefix, MTensor &block_totals, MTensor &compact_scratch,
                    MTensor &random_samples);
+
+// bindings.h:66-77: marching cubes on a device [Dz, Dy, Dx, 2] (sdf, weight)
+// grid; `triangles` receives 9 floats per triangle (host), in cell order.
+// Returns the number of triangles written (at most maxTriangles).
+int64_t msplat_marching_cubes(MTensor &grid, int Dx, int Dy, int Dz, float origin_x, float origin_y, float origin_z,
+                              float voxelSize, int maxTriangles, std::vector<float> &triangles);
+
+// bindings.h:79-93: fold one rendered depth + alpha map into the grid.
+void msplat_tsdf_integrate(MTensor &grid, int Dx, int Dy, int Dz, float origin_x, float origin_y, float origin_z,
+                           float voxelSize, MTensor &viewmat, float fx, float fy, float cx, float cy, uint32_t imgW,
+                           uint32_t imgH, float truncDist, float alphaThresh, MTensor &depthMap, MTensor &alphaMap);

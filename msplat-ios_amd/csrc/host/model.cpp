@@ -466,3 +466,158 @@ int Model::loadCheckpoint(const std::string &filename) {
               << std::endl;
     return (int)head[0];
 }
+
+// ---- point cloud, TSDF fusion, mesh (model.cpp:565-757) ----
+
+namespace {
+
+void engine_check(int rc) {
+    if (rc != MSPLAT_OK) throw std::runtime_error(std::string("msplat engine: ") + msplat_hip_last_error());
+}
+
+}  // namespace
+
+int64_t Model::exportPointCloud(std::vector<Camera> &cameras, int step, float alphaThresh,
+                                const std::string &outPath) {
+    std::vector<float> xyz;
+    std::vector<uint8_t> rgb;
+    MTensor xyzDev, rgbDev;
+    for (auto &cam : cameras) {
+        const CamSetup s = prepareCam(cam, step);
+        MTensor img = render(cam, step);
+        MTensor depth = msplat_last_out_depth();  // alpha-weighted depth sum
+        MTensor alpha = msplat_last_out_alpha();
+        const int64_t np = (int64_t)s.width * s.height;
+        if (!xyzDev.defined() || xyzDev.numel() < np * 3) {
+            xyzDev = MTensor::device({std::max<int64_t>(np, 1), 3}, DType::Float32);
+            rgbDev = MTensor::device({std::max<int64_t>(np, 1), 3}, DType::UInt8);
+        }
+        int64_t n = 0;
+        engine_check(msplat_hip_unproject_depth(img.data<float>(), depth.data<float>(), alpha.data<float>(), s.width,
+                                                s.height, s.fx, s.fy, s.cx, s.cy, cam.camToWorld, alphaThresh,
+                                                xyzDev.data<float>(), rgbDev.data<uint8_t>(), &n));
+        const size_t off = xyz.size() / 3;
+        xyz.resize((off + n) * 3);
+        rgb.resize((off + n) * 3);
+        if (n > 0) {
+            engine_check(msplat_hip_download(xyz.data() + off * 3, xyzDev.data_ptr(), (size_t)n * 12));
+            engine_check(msplat_hip_download(rgb.data() + off * 3, rgbDev.data_ptr(), (size_t)n * 3));
+        }
+    }
+    const int64_t N = (int64_t)(xyz.size() / 3);
+    std::ofstream out(outPath, std::ios::binary);
+    if (!out.is_open()) throw std::runtime_error("Cannot open " + outPath);
+    out << "ply\nformat binary_little_endian 1.0\n";
+    out << "comment msplat 2c.0 point cloud (unprojected depth, " << cameras.size() << " views)\n";
+    out << "element vertex " << N << "\n";
+    out << "property float x\nproperty float y\nproperty float z\n";
+    out << "property uchar red\nproperty uchar green\nproperty uchar blue\n";
+    out << "end_header\n";
+    std::vector<char> body((size_t)N * 15);
+    for (int64_t i = 0; i < N; ++i) {
+        std::memcpy(&body[(size_t)i * 15], &xyz[(size_t)i * 3], 12);
+        std::memcpy(&body[(size_t)i * 15 + 12], &rgb[(size_t)i * 3], 3);
+    }
+    out.write(body.data(), (std::streamsize)body.size());
+    return N;
+}
+
+Model::VoxelGrid Model::makeVoxelGrid(const std::vector<Camera> &cameras, float voxelSize, float boundRadius,
+                                      int memoryCapMB) const {
+    if (cameras.empty()) throw std::runtime_error("makeVoxelGrid: no cameras");
+    if (!(voxelSize > 0.0f) || !(boundRadius > 0.0f))
+        throw std::invalid_argument("makeVoxelGrid: voxelSize and boundRadius must be positive");
+    VoxelGrid g;
+    g.origin[0] = g.origin[1] = g.origin[2] = -boundRadius;
+    const float dimf = std::ceil(2.0f * boundRadius / voxelSize);
+    if (!(dimf <= 65535.0f)) throw std::runtime_error("makeVoxelGrid: grid of more than 65535 voxels per axis");
+    const int dim = (int)dimf;
+    g.dims[0] = g.dims[1] = g.dims[2] = dim;
+    g.voxelSize = voxelSize;
+    const int64_t bytes = (int64_t)dim * dim * dim * 2 * 4;
+    if (bytes > (int64_t)memoryCapMB * 1024 * 1024)
+        throw std::runtime_error("makeVoxelGrid: " + std::to_string(bytes / (1024 * 1024)) + " MB exceeds " +
+                                 std::to_string(memoryCapMB) + " MB cap (dim=" + std::to_string(dim) +
+                                 ", voxelSize=" + std::to_string(voxelSize) + "m). " +
+                                 "Increase voxelSize or decrease boundRadius.");
+    g.data = gpu_zeros({dim, dim, dim, 2}, DType::Float32);
+    return g;
+}
+
+void Model::integrateTSDF(VoxelGrid &grid, std::vector<Camera> &cameras, int step, float truncDist,
+                          float alphaThresh) {
+    // Each camera's median depth (the surface depth, where T crosses 0.5)
+    // and alpha are staged in HBM; a batch of views is then folded into the
+    // grid in one pass, every voxel applying the views in camera order --
+    // the values the reference's one dispatch per camera produces.
+    constexpr size_t kStageFloats = size_t(1) << 28;  // 1 GiB of staged maps per pass
+    MTensor stage;
+    size_t used = 0;
+    std::vector<MsplatTsdfView> views;
+    auto flush = [&] {
+        if (!views.empty())
+            engine_check(msplat_hip_tsdf_integrate(grid.data.data<float>(), grid.dims[0], grid.dims[1], grid.dims[2],
+                                                   grid.origin, grid.voxelSize, views.data(), (int)views.size(),
+                                                   truncDist, alphaThresh));
+        views.clear();
+        used = 0;
+    };
+    for (auto &cam : cameras) {
+        const CamSetup s = prepareCam(cam, step);
+        render(cam, step);
+        MTensor depth = msplat_last_out_median_depth();
+        MTensor alpha = msplat_last_out_alpha();
+        const size_t np = (size_t)s.width * s.height;
+        if (used + 2 * np > (size_t)stage.numel()) {
+            flush();
+            if (2 * np > (size_t)stage.numel())
+                stage = MTensor::device({(int64_t)std::max(kStageFloats, 2 * np)}, DType::Float32);
+        }
+        float *d = stage.data<float>() + used;
+        engine_check(msplat_hip_copy(d, depth.data_ptr(), np * 4));
+        engine_check(msplat_hip_copy(d + np, alpha.data_ptr(), np * 4));
+        used += 2 * np;
+        MsplatTsdfView v{};
+        std::memcpy(v.viewmat, s.viewMat.data_ptr(), sizeof(v.viewmat));
+        v.fx = s.fx;
+        v.fy = s.fy;
+        v.cx = s.cx;
+        v.cy = s.cy;
+        v.width = s.width;
+        v.height = s.height;
+        v.depth_dev = d;
+        v.alpha_dev = d + np;
+        views.push_back(v);
+    }
+    flush();
+    msplat_gpu_sync();
+}
+
+int64_t Model::extractMesh(const VoxelGrid &grid, const std::string &outPath, int maxTriangles) {
+    std::vector<float> tris;
+    const int64_t nTri = msplat_marching_cubes(const_cast<MTensor &>(grid.data), grid.dims[0], grid.dims[1],
+                                               grid.dims[2], grid.origin[0], grid.origin[1], grid.origin[2],
+                                               grid.voxelSize, maxTriangles, tris);
+    std::ofstream out(outPath, std::ios::binary);
+    if (!out.is_open()) throw std::runtime_error("Cannot open " + outPath);
+    out << "ply\nformat binary_little_endian 1.0\n";
+    out << "comment msplat 2c.3 Marching Cubes mesh (non-indexed)\n";
+    out << "element vertex " << nTri * 3 << "\n";
+    out << "property float x\nproperty float y\nproperty float z\n";
+    out << "element face " << nTri << "\n";
+    out << "property list uchar int vertex_indices\n";
+    out << "end_header\n";
+    out.write(reinterpret_cast<const char *>(tris.data()), (std::streamsize)(nTri * 9 * sizeof(float)));
+    // each triangle owns its three vertices: faces (3, 3i, 3i+1, 3i+2)
+    std::vector<char> faces((size_t)nTri * 13);
+    for (int64_t i = 0; i < nTri; ++i) {
+        char *f = &faces[(size_t)i * 13];
+        f[0] = 3;
+        for (int k = 0; k < 3; ++k) {
+            const int32_t idx = (int32_t)(i * 3 + k);
+            std::memcpy(f + 1 + 4 * k, &idx, 4);
+        }
+    }
+    out.write(faces.data(), (std::streamsize)faces.size());
+    return nTri;
+}

@@ -63,6 +63,30 @@ struct Model {
     // valid until the next render or step).
     MTensor render(Camera &cam, int step);
 
+    // Point cloud, TSDF fusion and mesh extraction (model.hpp:42-77,
+    // model.cpp:565-757).  Every pixel with alpha >= alphaThresh of every
+    // camera's render becomes one (x, y, z, r, g, b) PLY vertex; returns the
+    // number written.
+    int64_t exportPointCloud(std::vector<Camera> &cameras, int step, float alphaThresh, const std::string &outPath);
+    // A [Dz, Dy, Dx, 2] f32 (sdf, weight) grid in HBM, zero-initialised by
+    // makeVoxelGrid.
+    struct VoxelGrid {
+        float origin[3];  // world position of voxel (0, 0, 0)'s corner
+        int dims[3];      // (Dx, Dy, Dz)
+        float voxelSize;
+        MTensor data;
+    };
+    // A cube of side 2 * boundRadius centred on the world origin, voxels of
+    // voxelSize; throws if it would exceed memoryCapMB.
+    VoxelGrid makeVoxelGrid(const std::vector<Camera> &cameras, float voxelSize, float boundRadius,
+                            int memoryCapMB = 512) const;
+    // Fold every camera's rendered median depth (weighted by its alpha) into
+    // the grid, truncated at +-truncDist.
+    void integrateTSDF(VoxelGrid &grid, std::vector<Camera> &cameras, int step, float truncDist, float alphaThresh);
+    // Marching cubes on the grid -> non-indexed triangle PLY; returns the
+    // number of triangles written (at most maxTriangles).
+    int64_t extractMesh(const VoxelGrid &grid, const std::string &outPath, int maxTriangles = 4'000'000);
+
     MTensor means, scales, quats, featuresDc, featuresRest, opacities;
 
     static constexpr int N_ADAM_GROUPS = 6;

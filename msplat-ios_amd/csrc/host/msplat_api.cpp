@@ -229,8 +229,17 @@ void Trainer::renderFromPoseToBuffer(const float camToWorld[16], int refCameraIn
 void Trainer::exportPly(const std::string &path) { impl->model->savePly(path, impl->currentStep); }
 void Trainer::exportSplat(const std::string &path) { impl->model->saveSplat(path); }
 
-int64_t Trainer::extractMesh(const std::string &, float, float, float, float) {
-    throw std::runtime_error("mesh extraction (TSDF fusion + marching cubes) is not part of this build");
+int64_t Trainer::extractMesh(const std::string &path, float voxelSize, float boundRadius, float alphaThresh,
+                             float truncMultiplier) {
+    // msplat_api.mm:242-250
+    auto grid = impl->model->makeVoxelGrid(impl->ds->trainCams, voxelSize, boundRadius);
+    const float truncDist = truncMultiplier * voxelSize;
+    impl->model->integrateTSDF(grid, impl->ds->trainCams, impl->currentStep, truncDist, alphaThresh);
+    return impl->model->extractMesh(grid, path);
+}
+
+int64_t Trainer::exportPointCloud(const std::string &path, float alphaThresh) {
+    return impl->model->exportPointCloud(impl->ds->trainCams, impl->currentStep, alphaThresh, path);
 }
 
 void Trainer::saveCheckpoint(const std::string &path) { impl->model->saveCheckpoint(path, impl->currentStep); }

@@ -120,4 +120,29 @@ void launch_densify_classify(hipStream_t s, const DensifyArgs &a);
 // after appending and must fit the buffers' capacity.
 void launch_densify_apply(hipStream_t s, const DensifyArgs &a, int n_new);
 
+// k_mesh.hip
+// The compaction passes work on chunks of kMeshChunk cells / pixels: one
+// uint32 count per chunk, scanned into mesh_chunks(n) + 1 uint64 offsets.
+// The marching-cubes case bytes need mesh_chunks(cells) * kMeshChunk bytes.
+constexpr int kMeshChunk = 4096;
+inline int64_t mesh_chunks(int64_t n) { return (n + kMeshChunk - 1) / kMeshChunk; }
+inline int64_t mc_num_cells(int nx, int ny, int nz) {
+    return nx < 2 || ny < 2 || nz < 2 ? 0 : (int64_t)(nx - 1) * (ny - 1) * (nz - 1);
+}
+void mc_table_host(int8_t *tri);  // 256 x 16
+// nx * ny < 2^32, nz <= 65535
+void launch_tsdf_integrate(hipStream_t s, float *grid, int nx, int ny, int nz, const float origin[3], float vs,
+                           const MsplatTsdfView *views_dev, int nviews, float trunc, float athr);
+void launch_mc_classify(hipStream_t s, const float *grid, int nx, int ny, int nz, uint8_t *cases,
+                        uint32_t *chunk_tris);
+void launch_chunk_scan(hipStream_t s, const uint32_t *counts, int64_t n, uint64_t *off);
+void launch_mc_emit(hipStream_t s, const float *grid, int nx, int ny, int nz, const float origin[3], float vs,
+                    const uint8_t *cases, const uint64_t *chunk_off, int64_t max_tris, float *out);
+void launch_unproject_count(hipStream_t s, const float *img, const float *depth, const float *alpha, int W, int H,
+                            float fx, float fy, float cx, float cy, const float c2w[16], float thr,
+                            uint32_t *chunk_pts);
+void launch_unproject_emit(hipStream_t s, const float *img, const float *depth, const float *alpha, int W, int H,
+                           float fx, float fy, float cx, float cy, const float c2w[16], float thr,
+                           const uint64_t *chunk_off, float *xyz, uint8_t *rgb);
+
 }  // namespace mskern

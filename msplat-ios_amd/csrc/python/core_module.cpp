@@ -291,6 +291,20 @@ PYBIND11_MODULE(_core, m) {
             "export_splat", [](Trainer &t, const std::string &p) { t.t.exportSplat(p); }, "path"_a,
             "Export the current Gaussians as a .splat file.")
         .def(
+            "extract_mesh",
+            [](Trainer &t, const std::string &p, float voxel_size, float bound_radius, float alpha_thresh,
+               float trunc_multiplier) {
+                return t.t.extractMesh(p, voxel_size, bound_radius, alpha_thresh, trunc_multiplier);
+            },
+            "path"_a, "voxel_size"_a = 0.004f, "bound_radius"_a = 0.3f, "alpha_thresh"_a = 0.5f,
+            "trunc_multiplier"_a = 4.0f,
+            "TSDF fusion of the training views + marching cubes; writes a triangle PLY, returns the triangle count.")
+        .def(
+            "export_point_cloud",
+            [](Trainer &t, const std::string &p, float alpha_thresh) { return t.t.exportPointCloud(p, alpha_thresh); },
+            "path"_a, "alpha_thresh"_a = 0.5f,
+            "Unproject every training view's depth into a coloured PLY point cloud; returns the point count.")
+        .def(
             "save_checkpoint", [](Trainer &t, const std::string &p) { t.t.saveCheckpoint(p); }, "path"_a,
             "Save a training checkpoint.")
         .def(

@@ -48,6 +48,13 @@ class MsplatAdam(C.Structure):
     ]
 
 
+class MsplatTsdfView(C.Structure):
+    _fields_ = [
+        ("viewmat", C.c_float * 16), ("fx", C.c_float), ("fy", C.c_float), ("cx", C.c_float), ("cy", C.c_float),
+        ("width", C.c_int32), ("height", C.c_int32), ("depth_dev", C.c_void_p), ("alpha_dev", C.c_void_p),
+    ]
+
+
 LAST = {name: i for i, name in enumerate([
     "xys", "depths", "radii", "num_tiles_hit", "transmats", "colors_used", "opacity_sigmoid", "normals",
     "records", "tile_offsets", "gaussian_ids", "out_img", "final_Ts", "final_idx", "out_depth", "out_normal",
@@ -66,7 +73,8 @@ EXPORTS = [
     "msplat_hip_loss_fwd_bwd_noalloc",
     "msplat_hip_raster_bwd", "msplat_hip_project_bwd", "msplat_hip_project_bwd_adam", "msplat_hip_last", "msplat_hip_enable_timing",
     "msplat_hip_stage_times", "msplat_hip_last_pairs_evaluated", "msplat_hip_last_raster_counts",
-    "msplat_hip_check_fast_rcp", "msplat_hip_set_wide_keys",
+    "msplat_hip_check_fast_rcp", "msplat_hip_set_wide_keys", "msplat_hip_tsdf_integrate",
+    "msplat_hip_marching_cubes", "msplat_hip_mc_table", "msplat_hip_unproject_depth",
 ]
 SYNTH_EXPORTS = ["msplat_synth_uniform", "msplat_synth_normal"]
 
@@ -119,6 +127,10 @@ def lib() -> C.CDLL:
         "msplat_hip_last_raster_counts": (I, [P]),
         "msplat_hip_check_fast_rcp": (I, [I, I, C.POINTER(C.c_int64)]),
         "msplat_hip_set_wide_keys": (I, [I]),
+        "msplat_hip_tsdf_integrate": (I, [P, I, I, I, c_float_p, F, C.POINTER(MsplatTsdfView), I, F, F]),
+        "msplat_hip_marching_cubes": (I, [P, I, I, I, c_float_p, F, I64, P, C.POINTER(I64), C.POINTER(I64)]),
+        "msplat_hip_mc_table": (I, [P]),
+        "msplat_hip_unproject_depth": (I, [P, P, P, I, I, F, F, F, F, c_float_p, F, P, P, C.POINTER(I64)]),
         "msplat_synth_uniform": (None, [C.c_uint64, C.c_uint64, I64, C.c_double, C.c_double, P]),
         "msplat_synth_normal": (None, [C.c_uint64, C.c_uint64, I64, C.c_double, C.c_double, P]),
     }
@@ -263,3 +275,63 @@ def raster_counts() -> dict:
     check(lib().msplat_hip_last_raster_counts(C.cast(out, C.c_void_p)))
     return {"pairs_evaluated": int(out[0]), "log_entries": int(out[1]), "pairs_blended": int(out[2]),
             "visits": int(out[3]), "visit_slots": int(out[4])}
+
+
+# ---- mesh extraction -------------------------------------------------------
+
+def mc_table() -> np.ndarray:
+    """The marching-cubes case table [256, 16] int8 (host only)."""
+    t = np.zeros((256, 16), np.int8)
+    check(lib().msplat_hip_mc_table(t.ctypes.data))
+    return t
+
+
+def _f3(v) -> C.Array:
+    return (C.c_float * 3)(*[float(x) for x in v])
+
+
+def tsdf_integrate(grid: "DeviceArray", origin, voxel_size, views, trunc_dist, alpha_thresh) -> None:
+    """Folds views [(viewmat[16], fx, fy, cx, cy, depth DeviceArray [H,W],
+    alpha DeviceArray [H,W]), ...] into grid (DeviceArray [Dz,Dy,Dx,2])."""
+    dz, dy, dx = grid.shape[:3]
+    arr = (MsplatTsdfView * max(len(views), 1))()
+    for k, (vm, fx, fy, cx, cy, depth, alpha) in enumerate(views):
+        arr[k].viewmat[:] = [float(x) for x in np.asarray(vm, np.float32).reshape(16)]
+        arr[k].fx, arr[k].fy, arr[k].cx, arr[k].cy = fx, fy, cx, cy
+        arr[k].height, arr[k].width = depth.shape
+        arr[k].depth_dev, arr[k].alpha_dev = depth.ptr, alpha.ptr
+    org = _f3(origin)
+    check(lib().msplat_hip_tsdf_integrate(grid.ptr, dx, dy, dz, org, voxel_size, arr, len(views), trunc_dist,
+                                          alpha_thresh))
+
+
+def marching_cubes(grid: "DeviceArray", origin, voxel_size, max_triangles: int) -> tuple[np.ndarray, int]:
+    """(triangles [n,3,3] float32 on the host, number the grid produces)."""
+    dz, dy, dx = grid.shape[:3]
+    out = DeviceArray((max(max_triangles, 1), 9))
+    n, total = C.c_int64(), C.c_int64()
+    org = _f3(origin)
+    check(lib().msplat_hip_marching_cubes(grid.ptr, dx, dy, dz, org, voxel_size, max_triangles, out.ptr,
+                                          C.byref(n), C.byref(total)))
+    tris = np.empty((n.value, 9), np.float32)
+    if n.value:
+        check(lib().msplat_hip_download(tris.ctypes.data, out.ptr, tris.nbytes))
+    return tris.reshape(-1, 3, 3), int(total.value)
+
+
+def unproject_depth(img: "DeviceArray", depth: "DeviceArray", alpha: "DeviceArray", fx, fy, cx, cy, cam_to_world,
+                    alpha_thresh) -> tuple[np.ndarray, np.ndarray]:
+    """(xyz [n,3] float32, rgb [n,3] uint8) of one view."""
+    h, w = depth.shape
+    xyz = DeviceArray((max(h * w, 1), 3))
+    rgb = DeviceArray((max(h * w, 1), 3), np.uint8)
+    c2w = np.ascontiguousarray(cam_to_world, np.float32).reshape(16)
+    n = C.c_int64()
+    check(lib().msplat_hip_unproject_depth(img.ptr, depth.ptr, alpha.ptr, w, h, fx, fy, cx, cy,
+                                           c2w.ctypes.data_as(c_float_p), alpha_thresh, xyz.ptr, rgb.ptr,
+                                           C.byref(n)))
+    hx, hr = np.empty((n.value, 3), np.float32), np.empty((n.value, 3), np.uint8)
+    if n.value:
+        check(lib().msplat_hip_download(hx.ctypes.data, xyz.ptr, hx.nbytes))
+        check(lib().msplat_hip_download(hr.ctypes.data, rgb.ptr, hr.nbytes))
+    return hx, hr

@@ -1287,3 +1287,126 @@ extern "C" void orc_expf_array(int64_t n, const float *x, float *y) {
 }
 
 extern "C" void orc_ssim_window(float *w) { ssim_window(w); }
+
+/* ---- mesh extraction ---------------------------------------------------
+ * Expressions are the reference's, left to right, no contraction. */
+
+/* tsdf_integrate_kernel (msplat_metal.metal:2223-2280), one thread's work
+ * per voxel, voxels in any order (they are independent). */
+void orc_tsdf_integrate(float *grid, int dx, int dy, int dz, const float origin[3],
+                        float voxel_size, const float viewmat[16], float fx, float fy,
+                        float cx, float cy, int width, int height, float trunc_dist,
+                        float alpha_thresh, const float *depth, const float *alpha) {
+    const float *m = viewmat;
+#pragma omp parallel for schedule(static)
+    for (int z = 0; z < dz; ++z)
+        for (int y = 0; y < dy; ++y)
+            for (int x = 0; x < dx; ++x) {
+                /* voxel centre (:2240-2243) */
+                const float wx = origin[0] + ((float)x + 0.5f) * voxel_size;
+                const float wy = origin[1] + ((float)y + 0.5f) * voxel_size;
+                const float wz = origin[2] + ((float)z + 0.5f) * voxel_size;
+                const float vx = m[0] * wx + m[1] * wy + m[2] * wz + m[3];
+                const float vy = m[4] * wx + m[5] * wy + m[6] * wz + m[7];
+                const float vz = m[8] * wx + m[9] * wy + m[10] * wz + m[11];
+                if (vz <= 0.01f) continue;
+                const float px = vx / vz * fx + cx;
+                const float py = vy / vz * fy + cy;
+                const int ix = f2i(px), iy = f2i(py);
+                if (ix < 0 || ix >= width || iy < 0 || iy >= height) continue;
+                const int64_t pid = (int64_t)iy * width + ix;
+                const float a = alpha[pid];
+                if (a < alpha_thresh) continue;
+                const float d = depth[pid];
+                if (!std::isfinite(d) || d <= 0.0f) continue;
+                float sdf = d - vz;
+                if (sdf < -trunc_dist) continue;
+                sdf = fminf(fmaxf(sdf, -trunc_dist), trunc_dist); /* Metal clamp */
+                float *g = grid + (((int64_t)z * dy + y) * dx + x) * 2;
+                const float old_sdf = g[0], old_w = g[1];
+                const float new_w = old_w + a;
+                g[0] = (old_sdf * old_w + sdf * a) / new_w;
+                g[1] = new_w;
+            }
+}
+
+/* marching_cubes_kernel (msplat_metal.metal:2606-2687). */
+int64_t orc_marching_cubes(const float *grid, int dx, int dy, int dz,
+                           const float origin[3], float voxel_size,
+                           const int8_t *table, int64_t max_triangles, float *out) {
+    static const int corner[8][3] = {{0, 0, 0}, {1, 0, 0}, {1, 1, 0}, {0, 1, 0},
+                                     {0, 0, 1}, {1, 0, 1}, {1, 1, 1}, {0, 1, 1}};
+    static const int edge[12][2] = {{0, 1}, {1, 2}, {2, 3}, {3, 0}, {4, 5}, {5, 6},
+                                    {6, 7}, {7, 4}, {0, 4}, {1, 5}, {2, 6}, {3, 7}};
+    int64_t count = 0;
+    for (int k = 0; k + 1 < dz; ++k)
+        for (int j = 0; j + 1 < dy; ++j)
+            for (int i = 0; i + 1 < dx; ++i) {
+                float sdf[8], wts[8];
+                for (int c = 0; c < 8; ++c) {
+                    const int64_t idx = (((int64_t)(k + corner[c][2]) * dy + (j + corner[c][1])) * dx +
+                                         (i + corner[c][0])) * 2;
+                    sdf[c] = grid[idx];
+                    wts[c] = grid[idx + 1];
+                }
+                bool skip = false;
+                for (int c = 0; c < 8; ++c)
+                    if (wts[c] <= 0.0f) skip = true;
+                if (skip) continue;
+                int cube = 0;
+                for (int c = 0; c < 8; ++c)
+                    if (sdf[c] < 0.0f) cube |= 1 << c;
+                const int8_t *row = table + cube * 16;
+                for (int t = 0; t < 16 && row[t] >= 0; t += 3, ++count) {
+                    if (count >= max_triangles) continue;
+                    float *dst = out + count * 9;
+                    for (int v = 0; v < 3; ++v) {
+                        const int e = row[t + v];
+                        const int a = edge[e][0], b = edge[e][1];
+                        const float s0 = sdf[a], s1 = sdf[b];
+                        const float tt = (s1 == s0) ? 0.5f : (-s0 / (s1 - s0));
+                        const int ia[3] = {i, j, k};
+                        for (int q = 0; q < 3; ++q) {
+                            const float p0 = origin[q] + voxel_size * ((float)(ia[q] + corner[a][q]) + 0.5f);
+                            const float p1 = origin[q] + voxel_size * ((float)(ia[q] + corner[b][q]) + 0.5f);
+                            dst[3 * v + q] = p0 + (p1 - p0) * tt; /* Metal mix */
+                        }
+                    }
+                }
+            }
+    return count;
+}
+
+/* Model::exportPointCloud's pixel loop (model.cpp:580-616). */
+int64_t orc_unproject_depth(const float *img, const float *depth, const float *alpha,
+                            int width, int height, float fx, float fy, float cx,
+                            float cy, const float c2w[16], float alpha_thresh,
+                            float *xyz, uint8_t *rgb) {
+    const float r00 = c2w[0], r01 = -c2w[1], r02 = -c2w[2];
+    const float r10 = c2w[4], r11 = -c2w[5], r12 = -c2w[6];
+    const float r20 = c2w[8], r21 = -c2w[9], r22 = -c2w[10];
+    const float t0 = c2w[3], t1 = c2w[7], t2 = c2w[11];
+    auto u8 = [](float v) { /* clamp(v * 255, 0, 255), NaN -> 0 */
+        return (uint8_t)fminf(fmaxf(v * 255.0f, 0.0f), 255.0f);
+    };
+    int64_t n = 0;
+    for (int py = 0; py < height; ++py)
+        for (int px = 0; px < width; ++px) {
+            const int64_t idx = (int64_t)py * width + px;
+            const float a = alpha[idx];
+            if (a < alpha_thresh) continue;
+            const float d = depth[idx] / a;
+            if (!std::isfinite(d) || d <= 0.0f) continue;
+            const float xc = ((float)px + 0.5f - cx) * d / fx;
+            const float yc = ((float)py + 0.5f - cy) * d / fy;
+            const float zc = d;
+            xyz[3 * n + 0] = r00 * xc + r01 * yc + r02 * zc + t0;
+            xyz[3 * n + 1] = r10 * xc + r11 * yc + r12 * zc + t1;
+            xyz[3 * n + 2] = r20 * xc + r21 * yc + r22 * zc + t2;
+            rgb[3 * n + 0] = u8(img[3 * idx + 0]);
+            rgb[3 * n + 1] = u8(img[3 * idx + 1]);
+            rgb[3 * n + 2] = u8(img[3 * idx + 2]);
+            ++n;
+        }
+    return n;
+}

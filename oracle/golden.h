@@ -189,6 +189,28 @@ double orc_train_step(int n, float *means, float *scales, float *quats,
 /* Frees an array the golden model handed out (OrcStepDetail). */
 void orc_free(void *p);
 
+/* tsdf_integrate_kernel (msplat_metal.metal:2223-2280): folds one depth
+ * view into the [dz, dy, dx, 2] (sdf, weight) grid in place. */
+void orc_tsdf_integrate(float *grid, int dx, int dy, int dz, const float origin[3],
+                        float voxel_size, const float viewmat[16], float fx, float fy,
+                        float cx, float cy, int width, int height, float trunc_dist,
+                        float alpha_thresh, const float *depth, const float *alpha);
+
+/* marching_cubes_kernel (msplat_metal.metal:2606-2687) with the case table
+ * `table` (256 x 16 edge indices, -1 terminated), cells visited in linear
+ * order (x fastest); the first max_triangles triangles are written to out
+ * (9 floats each).  Returns the number of triangles the grid produces. */
+int64_t orc_marching_cubes(const float *grid, int dx, int dy, int dz,
+                           const float origin[3], float voxel_size,
+                           const int8_t *table, int64_t max_triangles, float *out);
+
+/* The unprojection loop of Model::exportPointCloud (model.cpp:580-616) for
+ * one view: xyz [H*W,3], rgb [H*W,3]; returns the number of points. */
+int64_t orc_unproject_depth(const float *img, const float *depth, const float *alpha,
+                            int width, int height, float fx, float fy, float cx,
+                            float cy, const float cam_to_world[16], float alpha_thresh,
+                            float *xyz, uint8_t *rgb);
+
 #ifdef __cplusplus
 }
 #endif

@@ -76,6 +76,13 @@ def lib() -> C.CDLL:
                                                           C.c_float, P * 6, P * 6, P, C.c_int, P, P, P, P, P,
                                                           C.POINTER(C.c_int64), C.POINTER(OrcStepDetail)]
         L.orc_free.argtypes = [P]
+        F = C.c_float
+        L.orc_tsdf_integrate.argtypes = [P, C.c_int, C.c_int, C.c_int, P, F, P, F, F, F, F, C.c_int, C.c_int, F, F,
+                                         P, P]
+        L.orc_marching_cubes.restype = C.c_int64
+        L.orc_marching_cubes.argtypes = [P, C.c_int, C.c_int, C.c_int, P, F, P, C.c_int64, P]
+        L.orc_unproject_depth.restype = C.c_int64
+        L.orc_unproject_depth.argtypes = [P, P, P, C.c_int, C.c_int, F, F, F, F, P, F, P, P]
         _lib = L
     return _lib
 
@@ -210,10 +217,10 @@ def raster_bwd(proj, bins, fwd, cam, background, dL_dimg, dL_ddepth=None, dL_dal
     ga = np.zeros((n, 16), np.float32) if with_abs else None
     ids = bins["ids"] if bins["ids"].size else np.zeros(1, np.int32)
     opt = [None if a is None else _f(a) for a in (dL_ddepth, dL_dalpha, dL_dnormal, dL_dmedian, dL_ddist)]
+    bgf, dl = _f(background), _f(dL_dimg)  # converted arrays live until the call returns
     lib().orc_raster_bwd(C.byref(cam), n, _p(bins["tile_offsets"]), _p(ids), _p(proj["xys"]),
-                         _p(proj["transmats"]), _p(proj["normal_opac"]), _p(proj["colors"]), _p(_f(background)),
-                         _p(fwd["final_Ts"]), _p(fwd["final_idx"]), _p(_f(dL_dimg)), *[_p(a) for a in opt], _p(g),
-                         _p(ga))
+                         _p(proj["transmats"]), _p(proj["normal_opac"]), _p(proj["colors"]), _p(bgf),
+                         _p(fwd["final_Ts"]), _p(fwd["final_idx"]), _p(dl), *[_p(a) for a in opt], _p(g), _p(ga))
     return (g, ga) if with_abs else g
 
 
@@ -227,9 +234,9 @@ def project_bwd(params: dict, cam, degree, dtu, radii, grads16, stats=None, glob
     if stats is None:
         stats = dict(grad_norm=np.zeros(n, np.float32), vis=np.zeros(n, np.float32), max2d=np.zeros(n, np.float32))
     inv_max_dim = np.float32(1.0) / np.float32(max(cam.width, cam.height))
-    lib().orc_project_bwd(n, _p(m), _p(_f(params["scales"])), _p(_f(params["quats"])),
-                          _p(_f(params["features_rest"])), degree, dtu, C.byref(cam), glob_scale,
-                          _p(np.ascontiguousarray(radii, np.int32)), _p(_f(grads16)),
+    sc, qu, fr = _f(params["scales"]), _f(params["quats"]), _f(params["features_rest"])
+    rad, g16 = np.ascontiguousarray(radii, np.int32), _f(grads16)
+    lib().orc_project_bwd(n, _p(m), _p(sc), _p(qu), _p(fr), degree, dtu, C.byref(cam), glob_scale, _p(rad), _p(g16),
                           *[_p(out[k]) for k in ("dmeans", "dscales", "dquats", "dmean2d", "dfdc", "dfrest")],
                           _p(stats["grad_norm"]), _p(stats["vis"]), _p(stats["max2d"]), float(inv_max_dim))
     out.update(stats)
@@ -244,11 +251,12 @@ def densify(n, capacity, params6, exp_avg6, exp_avg_sq6, fr_stride, stats, rando
             size_thresh=0.01, screen_thresh=0.05, check_screen=1, cull_alpha=0.1, cull_scale=0.5,
             cull_screen=0.15, check_huge=1, half_max_dim=648.5):
     P6 = C.c_void_p * 6
+    rs = _f(random_samples)
     r = lib().orc_densify(n, capacity, grad_thresh, size_thresh, screen_thresh, check_screen, cull_alpha,
                           cull_scale, cull_screen, check_huge, _p(stats["grad_norm"]), _p(stats["vis"]),
                           _p(stats["max2d"]), half_max_dim, P6(*[_p(a) for a in params6]), fr_stride,
                           P6(*[_p(a) for a in exp_avg6]), P6(*[_p(a) for a in exp_avg_sq6]),
-                          _p(_f(random_samples)))
+                          _p(rs))
     return int(r)
 
 
@@ -266,8 +274,9 @@ def train_step(params6, exp_avg6, exp_avg_sq6, cam, background, gt, degree, dtu,
     nis = C.c_int64()
     lr = np.asarray(adam_lr, np.float32)
     det = OrcStepDetail(want_grads=1 if detail == "grads" else 0) if detail else None
+    bgf, gtf = _f(background), _f(gt)
     loss = lib().orc_train_step(n, _p(m), _p(s), _p(q), _p(op), _p(dc), _p(fr), degree, dtu, C.byref(cam),
-                                _p(_f(background)), _p(_f(gt)), ssim_weight, P6(*[_p(a) for a in exp_avg6]),
+                                _p(bgf), _p(gtf), ssim_weight, P6(*[_p(a) for a in exp_avg6]),
                                 P6(*[_p(a) for a in exp_avg_sq6]), _p(lr), adam_step, _p(stats["grad_norm"]),
                                 _p(stats["vis"]), _p(stats["max2d"]), _p(img), _p(stage), C.byref(nis),
                                 C.byref(det) if det is not None else None)
@@ -287,3 +296,42 @@ def train_step(params6, exp_avg6, exp_avg_sq6, cam, background, gt, degree, dtu,
             out["grads16"] = take(det.grads16, 16 * n, np.float32).reshape(n, 16)
             out["grads16_abs"] = take(det.grads16_abs, 16 * n, np.float32).reshape(n, 16)
     return float(loss), img, stage, int(nis.value)
+
+
+def tsdf_integrate(grid, origin, voxel_size, viewmat, fx, fy, cx, cy, depth, alpha, trunc_dist, alpha_thresh):
+    """Folds one view into grid ([Dz,Dy,Dx,2] float32, C-contiguous) in place."""
+    assert grid.dtype == np.float32 and grid.flags.c_contiguous and grid.ndim == 4 and grid.shape[3] == 2
+    dz, dy, dx = grid.shape[:3]
+    depth, alpha = _f(depth), _f(alpha)
+    h, w = depth.shape
+    assert alpha.shape == (h, w)
+    org, vm = _f(origin), _f(viewmat)  # held until the call returns
+    lib().orc_tsdf_integrate(_p(grid), dx, dy, dz, _p(org), voxel_size, _p(vm), fx, fy, cx, cy, w, h,
+                             trunc_dist, alpha_thresh, _p(depth), _p(alpha))
+
+
+def marching_cubes(grid, origin, voxel_size, table, max_triangles=None):
+    """(triangles [n, 3, 3] float32, number the grid produces) for a
+    [Dz,Dy,Dx,2] grid; table is the 256 x 16 int8 case table."""
+    grid = _f(grid)
+    dz, dy, dx = grid.shape[:3]
+    tab = np.ascontiguousarray(table, np.int8).reshape(256, 16)
+    org = _f(origin)
+    if max_triangles is None:
+        total = lib().orc_marching_cubes(_p(grid), dx, dy, dz, _p(org), voxel_size, _p(tab), 0, None)
+        max_triangles = total
+    out = np.zeros((max(max_triangles, 1), 9), np.float32)
+    total = lib().orc_marching_cubes(_p(grid), dx, dy, dz, _p(org), voxel_size, _p(tab), max_triangles, _p(out))
+    return out[:min(total, max_triangles)].reshape(-1, 3, 3), int(total)
+
+
+def unproject_depth(img, depth, alpha, fx, fy, cx, cy, cam_to_world, alpha_thresh):
+    """(xyz [n,3] float32, rgb [n,3] uint8) of one view."""
+    img, depth, alpha = _f(img), _f(depth), _f(alpha)
+    h, w = depth.shape
+    xyz = np.zeros((h * w, 3), np.float32)
+    rgb = np.zeros((h * w, 3), np.uint8)
+    c2w = _f(cam_to_world)
+    n = lib().orc_unproject_depth(_p(img), _p(depth), _p(alpha), w, h, fx, fy, cx, cy, _p(c2w), alpha_thresh,
+                                  _p(xyz), _p(rgb))
+    return xyz[:n], rgb[:n]
