@@ -11,6 +11,7 @@ The headline line (`value`) is the train-step throughput of the 3M-splat,
   C3 train-3M-5187x3361     (the headline) + render FPS through the C ABI
   C4 overflow-1M-1920x1080  train steps/s, render FPS
   C5 densify-200k-1297x840  1500 steps with densification every 100
+  mesh                      TSDF fusion of 32 depth views + marching cubes, 300^3
 each next to the golden model (scalar C++, OpenMP) timed on this host.
 Inputs are synthetic (seeded; targets are renders of the scene with
 jittered means) and resident in HBM before every timed region.  Prints ONE
@@ -274,6 +275,117 @@ def gpu_densify(total_steps: int = 1500, refine_every: int = 100, max_splats: in
 
 
 # ------------------------------------------------------------------ CPU --
+def mesh_views(n_views: int, W: int, H: int, radius: float, dist: float):
+    """Synthetic depth views of a sphere: cameras on a Fibonacci sphere of
+    radius `dist` looking at the origin (OpenCV viewmats), each with the
+    exact z-depth of its first sphere hit per pixel centre and alpha 1
+    there (0 elsewhere) -- the median depth and alpha a render of an opaque
+    sphere gives."""
+    fx = fy = 1.35 * W
+    cx, cy = W / 2, H / 2
+    u = (np.arange(W) + 0.5 - cx) / fx
+    v = (np.arange(H) + 0.5 - cy) / fy
+    d = np.stack(np.broadcast_arrays(u[None, :], v[:, None], np.ones((H, W))), -1)  # camera-frame rays, z = 1
+    views = []
+    for k in range(n_views):
+        z = 1 - 2 * (k + 0.5) / n_views
+        phi = k * np.pi * (3 - np.sqrt(5))
+        eye = dist * np.array([np.sqrt(1 - z * z) * np.cos(phi), np.sqrt(1 - z * z) * np.sin(phi), z])
+        fwd = -eye / np.linalg.norm(eye)
+        up0 = np.array([0.0, 0.0, 1.0]) if abs(fwd[2]) < 0.9 else np.array([1.0, 0.0, 0.0])
+        right = np.cross(fwd, up0)
+        right /= np.linalg.norm(right)
+        down = np.cross(fwd, right)
+        R = np.stack([right, down, fwd])  # world -> camera rows
+        w = d @ R  # world ray directions (z-depth parametrisation)
+        a = np.einsum("hwc,hwc->hw", w, w)
+        b = 2 * w @ eye
+        c = eye @ eye - radius * radius
+        disc = b * b - 4 * a * c
+        hit = disc >= 0
+        t = np.where(hit, (-b - np.sqrt(np.where(hit, disc, 0))) / (2 * a), 0.0)
+        vm = np.eye(4)
+        vm[:3, :3] = R
+        vm[:3, 3] = -R @ eye
+        views.append((vm.astype(np.float32), fx, fy, cx, cy, t.astype(np.float32), hit.astype(np.float32)))
+    return views
+
+
+def gpu_mesh(reps: int = 5):
+    """TSDF fusion + marching cubes at the reference's fine setting (2 mm
+    voxels, 0.3 m bound: a 300^3 grid, model.cpp:641-650) from 32 views of
+    1297x840 of a 0.2 m sphere seen from 1 m; entry points timed end to end
+    (views uploaded and the triangle count read back, triangles left in
+    HBM), median of `reps`."""
+    from msplat import _engine as E
+    dim, vs, bound, nviews, W, H = 300, 0.002, 0.3, 32, 1297, 840
+    origin = [-bound] * 3
+    views = mesh_views(nviews, W, H, 0.2, 1.0)
+    dev_maps = [(E.DeviceArray.from_numpy(v[5]), E.DeviceArray.from_numpy(v[6])) for v in views]
+    dviews = [v[:5] + m for v, m in zip(views, dev_maps)]
+    grid = E.DeviceArray((dim, dim, dim, 2)).zero_()
+    trunc, athr = 4 * vs, 0.5
+    t_tsdf = []
+    for r in range(reps + 1):
+        grid.zero_()
+        E.sync()
+        t0 = time.perf_counter()
+        E.tsdf_integrate(grid, origin, vs, dviews, trunc, athr)
+        if r:
+            t_tsdf.append((time.perf_counter() - t0) * 1e3)
+    w = grid.numpy()[..., 1]
+    updated = int((w > 0).sum())
+    del w
+    max_tris = 4_000_000
+    out = E.DeviceArray((max_tris, 9))
+    org = (C.c_float * 3)(*origin)
+    n, tot = C.c_int64(), C.c_int64()
+    t_mc = []
+    for r in range(reps + 1):
+        t0 = time.perf_counter()
+        E.check(E.lib().msplat_hip_marching_cubes(grid.ptr, dim, dim, dim, org, vs, max_tris, out.ptr, C.byref(n),
+                                                   C.byref(tot)))
+        if r:
+            t_mc.append((time.perf_counter() - t0) * 1e3)
+    V, Cc, P = dim ** 3, (dim - 1) ** 3, W * H
+    tsdf_ms, mc_ms = float(np.median(t_tsdf)), float(np.median(t_mc))
+    # compulsory bytes: each updated voxel read + written once, each view's
+    # depth + alpha read once; marching cubes reads the grid once, writes and
+    # rereads one case byte per cell, writes 36 B per triangle
+    tsdf_bytes = 16.0 * updated + 8.0 * P * nviews
+    mc_bytes = 8.0 * V + 2.0 * Cc + 36.0 * n.value
+    return {"workload": f"tsdf-mc-{dim}^3-2mm-{nviews}x{W}x{H}", "grid": [dim, dim, dim], "voxel_m": vs,
+            "views": nviews, "voxels_updated": updated, "triangles": int(n.value),
+            "tsdf_ms": round(tsdf_ms, 3), "tsdf_views_per_s": round(nviews * 1e3 / tsdf_ms, 1),
+            "tsdf_gbs": round(tsdf_bytes / tsdf_ms / 1e6, 1),
+            "tsdf_hbm_frac": round(tsdf_bytes / tsdf_ms / 1e6 / HBM_PEAK_GBS, 4),
+            "mc_ms": round(mc_ms, 3), "mc_gbs": round(mc_bytes / mc_ms / 1e6, 1),
+            "mc_hbm_frac": round(mc_bytes / mc_ms / 1e6 / HBM_PEAK_GBS, 4),
+            "timing": "entry points end to end (host wall clock, synchronous calls), median of %d" % reps,
+            "_views": views, "_origin": origin}
+
+
+def cpu_mesh(O, m: dict) -> dict:
+    """The golden model on the same workload: TSDF fusion of the 32 views
+    (OpenMP over z-slices, one view at a time as the reference dispatches
+    them) and marching cubes (one thread) over the fused grid."""
+    from msplat import _engine as E
+    dim = m["grid"][0]
+    grid = np.zeros((dim, dim, dim, 2), np.float32)
+    t0 = time.perf_counter()
+    for vm, fx, fy, cx, cy, depth, alpha in m["_views"]:
+        O.tsdf_integrate(grid, m["_origin"], m["voxel_m"], vm, fx, fy, cx, cy, depth, alpha, 4 * m["voxel_m"], 0.5)
+    tsdf_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    O.marching_cubes(grid, m["_origin"], m["voxel_m"], E.mc_table())
+    mc_s = time.perf_counter() - t0
+    nv = len(m["_views"])
+    return {"tsdf": {"value": round(nv / tsdf_s, 3), "unit": "views/s", "cores": O.num_threads(), "kind": "port",
+                     "cpu": cpu_model(), "sample": f"the {nv} views over the {dim}^3 grid, once"},
+            "mc": {"value": round(1.0 / mc_s, 4), "unit": "grids/s", "cores": 1, "kind": "port", "cpu": cpu_model(),
+                   "sample": f"one pass over the fused {dim}^3 grid"}}
+
+
 def cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -390,6 +502,8 @@ def main() -> int:
                     help="skip the render-to-host-buffer frames (e.g. under a profiler)")
     ap.add_argument("--profile-workload", type=int, default=0, metavar="N",
                     help="only run the train steps and render frames of workload N (for a profiler)")
+    ap.add_argument("--mesh-only", action="store_true",
+                    help="only the mesh workload (TSDF fusion + marching cubes; for a profiler)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the training step is single-GPU (one camera per step); "
@@ -403,6 +517,10 @@ def main() -> int:
     from msplat import synthetic as S
 
     E.init()
+    if args.mesh_only:
+        mesh = gpu_mesh()
+        print(json.dumps({k: v for k, v in mesh.items() if not k.startswith("_")}))
+        return 0
     if args.profile_workload:
         r = gpu_train(args.profile_workload, args.steps, args.warmup, args.render_frames, counters=False)
         print(json.dumps({"workload": r["scene"].name, "ms_per_step": round(r["ms_per_step"], 3),
@@ -486,6 +604,11 @@ def main() -> int:
                          "cycles": cyc}
         log(f"{d5['scene'].name}: {d5['scene'].n} -> {d5['n_final']} splats in {d5['total_ms'] / 1e3:.2f} s")
         gc.collect()
+        mesh = gpu_mesh()
+        log(f"{mesh['workload']}: TSDF {mesh['tsdf_ms']:.3f} ms, marching cubes {mesh['mc_ms']:.3f} ms, "
+            f"{mesh['triangles']} triangles")
+        configs["mesh"] = {k: v for k, v in mesh.items() if not k.startswith("_")}
+        gc.collect()
         result["configs"] = configs
 
     # ---- CPU baselines: the golden model on this host ----
@@ -539,6 +662,7 @@ def main() -> int:
                       half_max_dim=648.5)
             dens_s = time.perf_counter() - td
             cyc_s = 100 * step_s + dens_s
+            configs["mesh"]["cpu"] = cpu_mesh(O, mesh)
             configs["C5"]["cpu_cycle"] = {"value": round(1.0 / cyc_s, 6), "unit": "densify cycles/s",
                                           "cores": O.num_threads(), "kind": "port", "cpu": cpu_model(),
                                           "cycle_s": round(cyc_s, 2),

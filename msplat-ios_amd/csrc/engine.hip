@@ -78,9 +78,9 @@ struct Engine {
     DevBuf dens_scratch[18], dens_flags, dens_scan, dens_keep;
     DevBuf pair_counter;
     DevBuf rgba;  // RGBA8 staging of msplat_hip_image_to_rgba8
-    // mesh extraction: TSDF view records, marching-cubes case bytes, and the
-    // per-chunk counts / scanned offsets of the two compactions
-    DevBuf tsdf_views, mc_cases, chunk_cnt, chunk_off;
+    // mesh extraction: TSDF view records and pixel masks, marching-cubes case
+    // bytes, and the per-chunk counts / scanned offsets of the two compactions
+    DevBuf tsdf_views, tsdf_masks, mc_cases, chunk_cnt, chunk_off;
     // state of the most recent forward
     int n = 0, W = 0, H = 0, tiles_x = 0, tiles_y = 0, K3 = 0;
     int64_t num_isect = 0;
@@ -645,8 +645,10 @@ int msplat_hip_mc_table(int8_t tri[256 * 16]) {
 
 namespace {
 bool grid_args_ok(const float *grid, int dx, int dy, int dz, const float origin[3]) {
+    // (the TSDF launch needs its 8 x 8 x 4 bricks, padded to 8, in an int)
     if (!grid || !origin || dx < 1 || dy < 1 || dz < 1 || dz > 65535 ||
-        (uint64_t)dx * (uint64_t)dy >= (uint64_t(1) << 32)) {
+        (uint64_t)dx * (uint64_t)dy >= (uint64_t(1) << 32) ||
+        (int64_t)((dx + 7) / 8) * ((dy + 7) / 8) * ((dz + 3) / 4) > (int64_t)INT_MAX - 8) {
         set_err("invalid voxel grid (%d x %d x %d)", dx, dy, dz);
         return false;
     }
@@ -670,11 +672,32 @@ int msplat_hip_tsdf_integrate(float *grid, int dx, int dy, int dz, const float o
         }
     if (num_views == 0) return MSPLAT_OK;
     Engine &E = g_eng;
-    const size_t bytes = (size_t)num_views * sizeof(MsplatTsdfView);
+    // each view's pass mask, then the fold
+    std::vector<mskern::TsdfViewDev> dv((size_t)num_views);
+    size_t words = 0;
+    int64_t max_segs = 0;
+    for (int k = 0; k < num_views; ++k) {
+        dv[k].v = views[k];
+        dv[k].words_per_row = mskern::tsdf_mask_words(views[k].width);
+        words += (size_t)dv[k].words_per_row * views[k].height;
+        max_segs = std::max<int64_t>(max_segs, (int64_t)((views[k].width + 63) / 64) * views[k].height);
+    }
+    if (max_segs > (int64_t)INT_MAX) {
+        set_err("TSDF view too large");
+        return MSPLAT_E_ARG;
+    }
+    CHECK(ensure(E.tsdf_masks, words * 4));
+    size_t off = 0;
+    for (auto &d : dv) {
+        d.mask = P<uint32_t>(E.tsdf_masks) + off;
+        off += (size_t)d.words_per_row * d.v.height;
+    }
+    const size_t bytes = dv.size() * sizeof(mskern::TsdfViewDev);
     CHECK(ensure(E.tsdf_views, bytes));
-    HIPC(hipMemcpyAsync(E.tsdf_views.p, views, bytes, hipMemcpyHostToDevice, E.stream));
-    mskern::launch_tsdf_integrate(E.stream, grid, dx, dy, dz, origin, voxel_size, P<MsplatTsdfView>(E.tsdf_views),
-                                  num_views, trunc_dist, alpha_thresh);
+    HIPC(hipMemcpyAsync(E.tsdf_views.p, dv.data(), bytes, hipMemcpyHostToDevice, E.stream));
+    const auto *vdev = P<mskern::TsdfViewDev>(E.tsdf_views);
+    mskern::launch_tsdf_masks(E.stream, vdev, num_views, max_segs, alpha_thresh);
+    mskern::launch_tsdf_integrate(E.stream, grid, dx, dy, dz, origin, voxel_size, vdev, num_views, trunc_dist);
     HIPC(hipGetLastError());
     // the view records are rewritten by the next call
     HIPC(hipStreamSynchronize(E.stream));

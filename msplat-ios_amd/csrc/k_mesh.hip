@@ -67,18 +67,60 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t *lds, u
 }
 
 // ---- TSDF fusion --------------------------------------------------------
-// One thread per voxel of one z-slice (gridDim.y = Dz); each folds every
-// view in order with the reference kernel's update, reading the voxel on
-// its first update and writing it once at the end (untouched voxels are
-// neither read nor written, as in the reference).
-__global__ __launch_bounds__(kThreads) void k_tsdf_integrate(float2 *__restrict__ grid, int nx, int ny, float ox,
-                                                             float oy, float oz, float vs,
-                                                             const MsplatTsdfView *__restrict__ views, int nviews,
-                                                             float trunc, float athr) {
-    const uint32_t l = blockIdx.x * kThreads + threadIdx.x;
-    if (l >= (uint32_t)nx * (uint32_t)ny) return;
-    const int x = (int)(l % (uint32_t)nx), y = (int)(l / (uint32_t)nx), z = (int)blockIdx.y;
-    const int64_t vid = (int64_t)z * nx * ny + l;
+// A voxel-view pair reads the view's depth and alpha only where the pixel
+// passes the reference's pixel tests (alpha >= threshold, depth finite and
+// positive, msplat_metal.metal:2259-2265); a first pass packs that test into
+// one bit per pixel, so the pairs that land on background -- most of them
+// -- touch only an L2-resident bitmask instead of the alpha map.
+
+// One wave per 64-pixel run of a row (blockIdx.y = view).
+__global__ __launch_bounds__(kThreads) void k_tsdf_masks(const TsdfViewDev *__restrict__ views, float athr) {
+    const TsdfViewDev &D = views[blockIdx.y];
+    const int W = D.v.width, H = D.v.height;
+    const int segs = (W + 63) >> 6;
+    const int64_t wv = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (wv >= (int64_t)segs * H) return;  // uniform over the wave
+    const int row = (int)(wv / segs), seg = (int)(wv % segs);
+    const int px = seg * 64 + (threadIdx.x & 63);
+    bool pass = false;
+    if (px < W) {
+        const int64_t pid = (int64_t)row * W + px;
+        const float a = D.v.alpha_dev[pid];
+        const float d = D.v.depth_dev[pid];
+        pass = !(a < athr) && __builtin_isfinite(d) && d > 0.0f;
+    }
+    const unsigned long long bits = __ballot(pass);
+    if ((threadIdx.x & 63) == 0) {
+        uint32_t *w = D.mask + (int64_t)row * D.words_per_row + 2 * seg;
+        w[0] = (uint32_t)bits;
+        w[1] = (uint32_t)(bits >> 32);
+    }
+}
+
+// One thread per voxel; a workgroup owns an 8 x 8 x 4 brick and each wave a
+// 4 x 4 x 4 sub-brick, so a wave's voxels project to a compact patch of
+// every view rather than a long image-space line, and bricks go to the
+// XCDs in contiguous bands (msd::xcd_tile), so neighbouring bricks, whose
+// patches overlap, share an L2.  Every voxel folds the views in order with
+// the reference kernel's update, reads the voxel on its first update and
+// writes it once at the end (untouched voxels are neither read nor written,
+// as in the reference).
+constexpr int kBrickX = 8, kBrickY = 8, kBrickZ = 4;
+
+__global__ __launch_bounds__(kThreads) void k_tsdf_integrate(float2 *__restrict__ grid, int nx, int ny, int nz,
+                                                             int bx, int by, int nbricks, float ox, float oy,
+                                                             float oz, float vs,
+                                                             const TsdfViewDev *__restrict__ views, int nviews,
+                                                             float trunc) {
+    const int brick = msd::xcd_tile(blockIdx.x, nbricks);
+    if (brick >= nbricks) return;
+    const int b_x = brick % bx, b_y = (brick / bx) % by, b_z = brick / (bx * by);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int x = b_x * kBrickX + (wave & 1) * 4 + (lane & 3);
+    const int y = b_y * kBrickY + (wave >> 1) * 4 + ((lane >> 2) & 3);
+    const int z = b_z * kBrickZ + (lane >> 4);
+    if (x >= nx || y >= ny || z >= nz) return;
+    const int64_t vid = ((int64_t)z * ny + y) * nx + x;
     // voxel centre (msplat_metal.metal:2240-2243)
     const float wx = ox + ((float)x + 0.5f) * vs;
     const float wy = oy + ((float)y + 0.5f) * vs;
@@ -86,23 +128,23 @@ __global__ __launch_bounds__(kThreads) void k_tsdf_integrate(float2 *__restrict_
     float2 cur = make_float2(0.f, 0.f);
     bool have = false;
     for (int k = 0; k < nviews; ++k) {
-        const MsplatTsdfView &V = views[k];
-        const float *m = V.viewmat;
+        const TsdfViewDev &D = views[k];
+        const float *m = D.v.viewmat;
         // world -> view (:2246-2249)
         const float vx = m[0] * wx + m[1] * wy + m[2] * wz + m[3];
         const float vy = m[4] * wx + m[5] * wy + m[6] * wz + m[7];
         const float vz = m[8] * wx + m[9] * wy + m[10] * wz + m[11];
         if (vz <= 0.01f) continue;
         // pinhole projection (:2252-2256)
-        const float px = vx / vz * V.fx + V.cx;
-        const float py = vy / vz * V.fy + V.cy;
+        const float px = vx / vz * D.v.fx + D.v.cx;
+        const float py = vy / vz * D.v.fy + D.v.cy;
         const int ix = msd::f2i(px), iy = msd::f2i(py);
-        if (ix < 0 || ix >= V.width || iy < 0 || iy >= V.height) continue;
-        const int64_t pid = (int64_t)iy * V.width + ix;
-        const float a = V.alpha_dev[pid];
-        if (a < athr) continue;
-        const float depth = V.depth_dev[pid];
-        if (!__builtin_isfinite(depth) || depth <= 0.0f) continue;
+        if (ix < 0 || ix >= D.v.width || iy < 0 || iy >= D.v.height) continue;
+        // the pixel tests (:2259-2265), from the mask
+        if (!((D.mask[(int64_t)iy * D.words_per_row + (ix >> 5)] >> (ix & 31)) & 1u)) continue;
+        const int64_t pid = (int64_t)iy * D.v.width + ix;
+        const float a = D.v.alpha_dev[pid];
+        const float depth = D.v.depth_dev[pid];
         // truncated SDF and weighted running mean (:2267-2279)
         float sdf = depth - vz;
         if (sdf < -trunc) continue;
@@ -119,88 +161,51 @@ __global__ __launch_bounds__(kThreads) void k_tsdf_integrate(float2 *__restrict_
 }
 
 // ---- marching cubes -----------------------------------------------------
-// Cell c (x fastest) spans voxels (i..i+1, j..j+1, k..k+1); thread t of
-// chunk b owns cells b*4096 + 16t .. +15, which mostly share an x-row, so
-// each cell loads only its 4 new corners (x = i+1) and reuses the previous
-// cell's as its x = i corners.
-
-struct CellWalker {
-    int i, j, k;
-    int cx, cy;  // cells per row / per column
-    __device__ void start(int64_t c, int cx_, int cy_) {
-        cx = cx_;
-        cy = cy_;
-        i = (int)(c % cx);
-        const int64_t r = c / cx;
-        j = (int)(r % cy);
-        k = (int)(r / cy);
-    }
-    // true when the next cell starts a new x-row
-    __device__ bool advance() {
-        if (++i < cx) return false;
-        i = 0;
-        if (++j == cy) {
-            j = 0;
-            ++k;
-        }
-        return true;
-    }
-};
-
-// corners (0,3,4,7) at x = i or (1,2,5,6) at x = i+1 of the cell whose
-// corner 0 is voxel b
-__device__ __forceinline__ void load_face(const float2 *__restrict__ grid, int64_t b, int nx, int64_t nxy,
-                                          float2 f[4]) {
-    f[0] = grid[b];
-    f[1] = grid[b + nx];
-    f[2] = grid[b + nxy];
-    f[3] = grid[b + nxy + nx];
-}
-
-// case of a cell from its x = i face L and x = i+1 face R (corner order of
-// load_face); 0 when a corner's weight is <= 0 (:2628-2631)
-__device__ __forceinline__ uint32_t cell_case(const float2 L[4], const float2 R[4]) {
-    const float2 c[8] = {L[0], R[0], R[1], L[1], L[2], R[2], R[3], L[3]};
+// case of the cell whose corner 0 is voxel b; 0 when a corner's weight is
+// <= 0 (:2628-2631)
+__device__ __forceinline__ uint32_t cell_case(const float2 *__restrict__ grid, int64_t b, int nx, int64_t nxy) {
     uint32_t m = 0;
     bool skip = false;
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-        skip |= c[q].y <= 0.0f;
-        m |= (c[q].x < 0.0f ? 1u : 0u) << q;
+        const float2 v = grid[b + c_geom.corner[q][0] + c_geom.corner[q][1] * (int64_t)nx + c_geom.corner[q][2] * nxy];
+        skip |= v.y <= 0.0f;
+        m |= (v.x < 0.0f ? 1u : 0u) << q;
     }
     return skip ? 0u : m;
 }
 
+// Cell c (x fastest) spans voxels (i..i+1, j..j+1, k..k+1).  Chunk b holds
+// cells b*4096 .. +4095; here lane t takes cells b*4096 + 256r + t, so each
+// load instruction of a wave reads 64 consecutive voxels, and the chunks
+// go to the XCDs in contiguous bands (the cells of neighbouring rows and
+// slices share voxels).  The emit pass gives each thread 16 consecutive
+// cells instead (one 16-byte load of their case bytes, one scan).
 __global__ __launch_bounds__(kThreads) void k_mc_classify(const float2 *__restrict__ grid, int nx, int ny,
-                                                          int64_t ncells, uint8_t *__restrict__ cases,
+                                                          int64_t ncells, int64_t nchunks,
+                                                          uint8_t *__restrict__ cases,
                                                           uint32_t *__restrict__ chunk_tris) {
     __shared__ uint32_t lds[kThreads / 64];
-    const int64_t c0 = (int64_t)blockIdx.x * kMeshChunk + (int64_t)threadIdx.x * kPerThread;
+    const int64_t chunk = msd::xcd_tile(blockIdx.x, (int)nchunks);
+    if (chunk >= nchunks) return;
     const int64_t nxy = (int64_t)nx * ny;
+    const int cx = nx - 1, cy = ny - 1;
     uint32_t tris = 0;
-    if (c0 < ncells) {
-        uint32_t packed[4] = {0u, 0u, 0u, 0u};
-        CellWalker w;
-        w.start(c0, nx - 1, ny - 1);
-        float2 L[4], R[4];
-        bool fresh = true;
-        const int n = (int)(ncells - c0 < kPerThread ? ncells - c0 : kPerThread);
-        for (int q = 0; q < n; ++q) {
-            const int64_t b = ((int64_t)w.k * ny + w.j) * nx + w.i;
-            if (fresh) load_face(grid, b, nx, nxy, L);
-            load_face(grid, b + 1, nx, nxy, R);
-            const uint32_t m = cell_case(L, R);
-            packed[q >> 2] |= m << (8 * (q & 3));
+    for (int r = 0; r < kPerThread; ++r) {
+        const int64_t c = chunk * kMeshChunk + r * kThreads + threadIdx.x;
+        uint32_t m = 0;
+        if (c < ncells) {
+            const int i = (int)(c % cx);
+            const int64_t q = c / cx;
+            const int j = (int)(q % cy), k = (int)(q / cy);
+            m = cell_case(grid, ((int64_t)k * ny + j) * nx + i, nx, nxy);
             tris += c_mc.ntri[m];
-#pragma unroll
-            for (int f = 0; f < 4; ++f) L[f] = R[f];
-            fresh = w.advance();
         }
-        *reinterpret_cast<uint4 *>(cases + c0) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+        cases[c] = (uint8_t)m;  // the case buffer covers whole chunks
     }
     uint32_t total;
     (void)block_excl_scan(tris, lds, &total);
-    if (threadIdx.x == 0) chunk_tris[blockIdx.x] = total;
+    if (threadIdx.x == 0) chunk_tris[chunk] = total;
 }
 
 // Exclusive scan of n chunk counts into off[0..n] (off[n] = total) by one
@@ -235,15 +240,24 @@ __global__ __launch_bounds__(1024) void k_chunk_scan(const uint32_t *__restrict_
     }
 }
 
+// Emit: each thread counts the triangles of its 16 consecutive cells (one
+// 16-byte load of their case bytes); one block scan gives every cell's
+// triangle offset and its slot in an LDS list of the chunk's surface cells;
+// the threads then take the listed cells in turn, so the few surface cells
+// of a chunk spread over all lanes instead of serialising in the lanes
+// that own them.
 __global__ __launch_bounds__(kThreads) void k_mc_emit(const float2 *__restrict__ grid, int nx, int ny,
                                                       int64_t ncells, float ox, float oy, float oz, float vs,
                                                       const uint8_t *__restrict__ cases,
                                                       const uint64_t *__restrict__ chunk_off, int64_t max_tris,
                                                       float *__restrict__ out) {
     __shared__ uint32_t lds[kThreads / 64];
-    const int64_t c0 = (int64_t)blockIdx.x * kMeshChunk + (int64_t)threadIdx.x * kPerThread;
+    __shared__ uint32_t s_cell[kMeshChunk];  // (cell in chunk) << 8 | case
+    __shared__ uint16_t s_tri[kMeshChunk];   // first triangle of the cell, in the chunk
+    const int64_t base = (int64_t)blockIdx.x * kMeshChunk;
+    const int64_t c0 = base + (int64_t)threadIdx.x * kPerThread;
     uint32_t packed[4] = {0u, 0u, 0u, 0u};
-    uint32_t tris = 0;
+    uint32_t tris = 0, cells = 0;
     if (c0 < ncells) {
         const uint4 p = *reinterpret_cast<const uint4 *>(cases + c0);
         packed[0] = p.x;
@@ -251,36 +265,54 @@ __global__ __launch_bounds__(kThreads) void k_mc_emit(const float2 *__restrict__
         packed[2] = p.z;
         packed[3] = p.w;
 #pragma unroll
-        for (int q = 0; q < kPerThread; ++q) tris += c_mc.ntri[(packed[q >> 2] >> (8 * (q & 3))) & 255u];
+        for (int q = 0; q < kPerThread; ++q) {
+            const uint32_t nt = c_mc.ntri[(packed[q >> 2] >> (8 * (q & 3))) & 255u];
+            tris += nt;
+            cells += nt ? 1u : 0u;
+        }
     }
+    // triangles (< 20481) in the high half, surface cells (<= 4096) in the low
     uint32_t total;
-    const uint32_t pre = block_excl_scan(tris, lds, &total);
-    if (tris == 0) return;
-    uint64_t o = chunk_off[blockIdx.x] + pre;
-    if ((int64_t)o >= max_tris) return;
-    const int64_t nxy = (int64_t)nx * ny;
-    const int cx = nx - 1, cy = ny - 1;
+    const uint32_t pre = block_excl_scan(tris << 16 | cells, lds, &total);
+    const uint32_t ncell = total & 0xffffu;
+    if (ncell == 0) return;  // uniform over the workgroup
+    uint32_t tp = pre >> 16, cp = pre & 0xffffu;
+#pragma unroll
     for (int q = 0; q < kPerThread; ++q) {
         const uint32_t m = (packed[q >> 2] >> (8 * (q & 3))) & 255u;
-        const int nt = c_mc.ntri[m];
+        const uint32_t nt = c_mc.ntri[m];
         if (nt == 0) continue;
-        const int64_t c = c0 + q;
+        s_cell[cp] = (uint32_t)(threadIdx.x * kPerThread + q) << 8 | m;
+        s_tri[cp] = (uint16_t)tp;
+        ++cp;
+        tp += nt;
+    }
+    __syncthreads();
+    const uint64_t chunk_first = chunk_off[blockIdx.x];
+    const int64_t nxy = (int64_t)nx * ny;
+    const int cx = nx - 1, cy = ny - 1;
+    for (uint32_t e = threadIdx.x; e < ncell; e += kThreads) {
+        const uint32_t cm = s_cell[e];
+        const uint32_t m = cm & 255u;
+        uint64_t o = chunk_first + s_tri[e];
+        if ((int64_t)o >= max_tris) continue;
+        const int64_t c = base + (cm >> 8);
         const int i = (int)(c % cx);
         const int64_t r = c / cx;
         const int j = (int)(r % cy), k = (int)(r / cy);
         const int64_t b = ((int64_t)k * ny + j) * nx + i;
-        float s[8];
+        float sv[8];
 #pragma unroll
         for (int cn = 0; cn < 8; ++cn)
-            s[cn] = grid[b + c_geom.corner[cn][0] + c_geom.corner[cn][1] * (int64_t)nx +
-                         c_geom.corner[cn][2] * nxy].x;
-        for (int t = 0; t < nt; ++t, ++o) {
-            if ((int64_t)o >= max_tris) return;
+            sv[cn] = grid[b + c_geom.corner[cn][0] + c_geom.corner[cn][1] * (int64_t)nx +
+                          c_geom.corner[cn][2] * nxy].x;
+        const int nt = c_mc.ntri[m];
+        for (int t = 0; t < nt && (int64_t)o < max_tris; ++t, ++o) {
             float *dst = out + o * 9;
             for (int v = 0; v < 3; ++v) {
-                const int e = c_mc.tri[m][3 * t + v];
-                const int a = c_geom.edge[e][0], bb = c_geom.edge[e][1];
-                const float s0 = s[a], s1 = s[bb];
+                const int ed = c_mc.tri[m][3 * t + v];
+                const int a = c_geom.edge[ed][0], bb = c_geom.edge[ed][1];
+                const float s0 = sv[a], s1 = sv[bb];
                 // edge interpolation (:2644-2661)
                 const float tt = (s1 == s0) ? 0.5f : (-s0 / (s1 - s0));
                 const float p0x = ox + vs * ((float)(i + c_geom.corner[a][0]) + 0.5f);
@@ -375,19 +407,25 @@ void mc_table_host(int8_t *tri) {
     std::memcpy(tri, &t.tri[0][0], sizeof(t.tri));
 }
 
+void launch_tsdf_masks(hipStream_t s, const TsdfViewDev *views_dev, int nviews, int64_t max_segs, float athr) {
+    const dim3 g((unsigned)((max_segs + kThreads / 64 - 1) / (kThreads / 64)), (unsigned)nviews);
+    k_tsdf_masks<<<g, kThreads, 0, s>>>(views_dev, athr);
+}
+
 void launch_tsdf_integrate(hipStream_t s, float *grid, int nx, int ny, int nz, const float origin[3], float vs,
-                           const MsplatTsdfView *views_dev, int nviews, float trunc, float athr) {
-    const uint32_t slice = (uint32_t)nx * (uint32_t)ny;
-    const dim3 g((slice + kThreads - 1) / kThreads, (unsigned)nz);
-    k_tsdf_integrate<<<g, kThreads, 0, s>>>(reinterpret_cast<float2 *>(grid), nx, ny, origin[0], origin[1],
-                                            origin[2], vs, views_dev, nviews, trunc, athr);
+                           const TsdfViewDev *views_dev, int nviews, float trunc) {
+    const int bx = (nx + kBrickX - 1) / kBrickX, by = (ny + kBrickY - 1) / kBrickY, bz = (nz + kBrickZ - 1) / kBrickZ;
+    const int nb = bx * by * bz;
+    k_tsdf_integrate<<<(unsigned)(8 * ((nb + 7) / 8)), kThreads, 0, s>>>(
+        reinterpret_cast<float2 *>(grid), nx, ny, nz, bx, by, nb, origin[0], origin[1], origin[2], vs, views_dev,
+        nviews, trunc);
 }
 
 void launch_mc_classify(hipStream_t s, const float *grid, int nx, int ny, int nz, uint8_t *cases,
                         uint32_t *chunk_tris) {
-    const int64_t nc = mc_num_cells(nx, ny, nz);
-    k_mc_classify<<<(unsigned)mesh_chunks(nc), kThreads, 0, s>>>(reinterpret_cast<const float2 *>(grid), nx, ny,
-                                                                  nc, cases, chunk_tris);
+    const int64_t nc = mc_num_cells(nx, ny, nz), nch = mesh_chunks(nc);
+    k_mc_classify<<<(unsigned)(8 * ((nch + 7) / 8)), kThreads, 0, s>>>(reinterpret_cast<const float2 *>(grid), nx,
+                                                                        ny, nc, nch, cases, chunk_tris);
 }
 
 void launch_chunk_scan(hipStream_t s, const uint32_t *counts, int64_t n, uint64_t *off) {

@@ -130,9 +130,20 @@ inline int64_t mc_num_cells(int nx, int ny, int nz) {
     return nx < 2 || ny < 2 || nz < 2 ? 0 : (int64_t)(nx - 1) * (ny - 1) * (nz - 1);
 }
 void mc_table_host(int8_t *tri);  // 256 x 16
-// nx * ny < 2^32, nz <= 65535
+// A view as the TSDF kernels read it: the caller's record plus its pass
+// mask, 1 bit per pixel (alpha >= threshold, depth finite and positive),
+// row-major, tsdf_mask_words(W) 32-bit words per row.
+struct TsdfViewDev {
+    MsplatTsdfView v;
+    uint32_t *mask;
+    int32_t words_per_row;
+    int32_t pad_;
+};
+inline int tsdf_mask_words(int W) { return ((W + 63) / 64) * 2; }
+// Builds every view's mask; max_segs = the largest H * ceil(W / 64).
+void launch_tsdf_masks(hipStream_t s, const TsdfViewDev *views_dev, int nviews, int64_t max_segs, float athr);
 void launch_tsdf_integrate(hipStream_t s, float *grid, int nx, int ny, int nz, const float origin[3], float vs,
-                           const MsplatTsdfView *views_dev, int nviews, float trunc, float athr);
+                           const TsdfViewDev *views_dev, int nviews, float trunc);
 void launch_mc_classify(hipStream_t s, const float *grid, int nx, int ny, int nz, uint8_t *cases,
                         uint32_t *chunk_tris);
 void launch_chunk_scan(hipStream_t s, const uint32_t *counts, int64_t n, uint64_t *off);
