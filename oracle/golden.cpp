@@ -1410,3 +1410,441 @@ int64_t orc_unproject_depth(const float *img, const float *depth, const float *a
         }
     return n;
 }
+
+/* ---- 3DGS mode ---------------------------------------------------------
+ * Projection, compositing and their backward for 3D Gaussians, built on the
+ * reference's EWA helpers (scale_rot_to_cov3d msplat_metal.metal:160-176,
+ * project_cov3d_ewa :333-378, compute_cov2d_bounds :420-441, project_pix
+ * :444-452, and their VJPs :1059-1374), which the 2DGS fork keeps as dead
+ * code.  Its 3DGS compositing kernel was removed; the pair rule here is the
+ * published 3DGS one (Kerbl et al. 2023) in the fork's blending conventions
+ * (alpha = min(0.99, opacity exp(-sigma)), skip below 1/255, stop before T
+ * falls to 1e-4), sigma = 0.5 (a dx^2 + c dy^2) + b dx dy with the conic
+ * (a, b, c) and d = centre - pixel.  rho = 2 sigma is formed as
+ * fmaf(a dx, dx, fmaf(c dy, dy, 2 b dx dy)) and exp(-sigma) = orc_gauss(rho),
+ * the arithmetic the kernels use. */
+namespace {
+
+/* scale_rot_to_cov3d: M = R diag(glob s), cov = M M^T (upper triangle). */
+void cov3d_of(const float s[3], float glob, const float *q, float cov[6], f3 R[3]) {
+    quat_to_rotmat(q, R[0], R[1], R[2]);
+    const float g0 = glob * s[0], g1 = glob * s[1], g2 = glob * s[2];
+    /* rows of M: M[r][c] = R[c][r] * s_c */
+    const float M[3][3] = {{R[0].x * g0, R[1].x * g1, R[2].x * g2},
+                           {R[0].y * g0, R[1].y * g1, R[2].y * g2},
+                           {R[0].z * g0, R[1].z * g1, R[2].z * g2}};
+    auto mm = [&](int i, int j) { return M[i][0] * M[j][0] + M[i][1] * M[j][1] + M[i][2] * M[j][2]; };
+    cov[0] = mm(0, 0);
+    cov[1] = mm(0, 1);
+    cov[2] = mm(0, 2);
+    cov[3] = mm(1, 1);
+    cov[4] = mm(1, 2);
+    cov[5] = mm(2, 2);
+}
+
+/* The fov-clamped view position of project_cov3d_ewa (:345-347). */
+inline void ewa_clamp(float &px, float &py, float pz, float tan_fovx, float tan_fovy) {
+    const float lim_x = 1.3f * tan_fovx, lim_y = 1.3f * tan_fovy;
+    px = pz * fminf(lim_x, fmaxf(-lim_x, px / pz));
+    py = pz * fminf(lim_y, fmaxf(-lim_y, py / pz));
+}
+
+/* project_cov3d_ewa (:333-378): cov2d = T V T^T + 0.3 I, T = J W. */
+void ewa_cov2d(const float cov[6], const float *vm, float fx, float fy, float tan_fovx, float tan_fovy,
+               const float pv[3], float c2[3]) {
+    float px = pv[0], py = pv[1];
+    const float pz = pv[2];
+    ewa_clamp(px, py, pz, tan_fovx, tan_fovy);
+    const float rz = 1.f / pz, rz2 = rz * rz;
+    const float j00 = fx * rz, j11 = fy * rz;
+    const float j20 = -fx * px * rz2, j21 = -fy * py * rz2;
+    const f3 t0 = {j00 * vm[0] + j20 * vm[8], j00 * vm[1] + j20 * vm[9], j00 * vm[2] + j20 * vm[10]};
+    const f3 t1 = {j11 * vm[4] + j21 * vm[8], j11 * vm[5] + j21 * vm[9], j11 * vm[6] + j21 * vm[10]};
+    const float v00 = cov[0], v01 = cov[1], v02 = cov[2], v11 = cov[3], v12 = cov[4], v22 = cov[5];
+    const f3 tv0 = {t0.x * v00 + t0.y * v01 + t0.z * v02, t0.x * v01 + t0.y * v11 + t0.z * v12,
+                    t0.x * v02 + t0.y * v12 + t0.z * v22};
+    const f3 tv1 = {t1.x * v00 + t1.y * v01 + t1.z * v02, t1.x * v01 + t1.y * v11 + t1.z * v12,
+                    t1.x * v02 + t1.y * v12 + t1.z * v22};
+    c2[0] = dot3(tv0, t0) + 0.3f;
+    c2[1] = dot3(tv0, t1);
+    c2[2] = dot3(tv1, t1) + 0.3f;
+}
+
+/* compute_cov2d_bounds (:420-441). */
+bool cov2d_bounds(const float c2[3], float conic[3], float &radius) {
+    const float det = c2[0] * c2[2] - c2[1] * c2[1];
+    if (det == 0.f) return false;
+    const float inv_det = 1.f / det;
+    conic[0] = c2[2] * inv_det;
+    conic[1] = -c2[1] * inv_det;
+    conic[2] = c2[0] * inv_det;
+    const float b = 0.5f * (c2[0] + c2[2]);
+    const float disc = sqrtf(fmaxf(0.1f, b * b - det));
+    radius = ceilf(3.f * sqrtf(b + disc));
+    return true;
+}
+
+/* project_pix (:444-452) with ndc2pix (:58-60). */
+void project_pix(const float *pm, const float *p, int W, int H, float cx, float cy, float xy[2]) {
+    const float hx = pm[0] * p[0] + pm[1] * p[1] + pm[2] * p[2] + pm[3];
+    const float hy = pm[4] * p[0] + pm[5] * p[1] + pm[6] * p[2] + pm[7];
+    const float hw = pm[12] * p[0] + pm[13] * p[1] + pm[14] * p[2] + pm[15];
+    const float rw = 1.f / (hw + 1e-6f);
+    xy[0] = 0.5f * (float)W * (hx * rw) + cx - 0.5f;
+    xy[1] = 0.5f * (float)H * (hy * rw) + cy - 0.5f;
+}
+
+/* 2 sigma of a pixel for the conic (a, b, c), d = centre - pixel. */
+inline float conic_rho(const float *cn, float dx, float dy) {
+    return fmaf(cn[0] * dx, dx, fmaf(cn[2] * dy, dy, 2.f * cn[1] * dx * dy));
+}
+
+}  // namespace
+
+/* 3DGS projection + SH forward.  Per splat: xys[2], conics[3], depths,
+ * radii (0 = culled), rect (x0, y0, x1, y1), colors (raw SH) and
+ * cov2d[3] (nullable). */
+extern "C" void orc_project3d_fwd(int n, const float *means, const float *scales, const float *quats,
+                                  const float *fdc, const float *frest, int degree, int dtu,
+                                  const OrcCamera *cam, float glob_scale, float clip_thresh, float *xys,
+                                  float *conics, float *depths, int32_t *radii, int32_t *rect, float *colors,
+                                  float *cov2d) {
+    const float *vm = cam->viewmat, *pm = cam->projmat;
+    const int nb = num_sh_bases(degree);
+    const float tan_fovx = 0.5f * (float)cam->width / cam->fx, tan_fovy = 0.5f * (float)cam->height / cam->fy;
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < n; ++i) {
+        radii[i] = 0;
+        depths[i] = 0.f;
+        for (int k = 0; k < 2; ++k) xys[2 * i + k] = 0.f;
+        for (int k = 0; k < 3; ++k) conics[3 * i + k] = colors[3 * i + k] = 0.f;
+        if (cov2d)
+            for (int k = 0; k < 3; ++k) cov2d[3 * i + k] = 0.f;
+        for (int k = 0; k < 4; ++k) rect[4 * i + k] = 0;
+        const float *p = means + 3 * i;
+        /* clip_near_plane (:139-150) */
+        const float pv[3] = {vm[0] * p[0] + vm[1] * p[1] + vm[2] * p[2] + vm[3],
+                             vm[4] * p[0] + vm[5] * p[1] + vm[6] * p[2] + vm[7],
+                             vm[8] * p[0] + vm[9] * p[1] + vm[10] * p[2] + vm[11]};
+        if (pv[2] <= clip_thresh) continue;
+        const float s[3] = {orc_expf(scales[3 * i]), orc_expf(scales[3 * i + 1]), orc_expf(scales[3 * i + 2])};
+        float cov[6], c2[3], cn[3], radius;
+        f3 R[3];
+        cov3d_of(s, glob_scale, quats + 4 * i, cov, R);
+        ewa_cov2d(cov, vm, cam->fx, cam->fy, tan_fovx, tan_fovy, pv, c2);
+        if (!cov2d_bounds(c2, cn, radius)) continue;
+        float xy[2];
+        project_pix(pm, p, cam->width, cam->height, cam->cx, cam->cy, xy);
+        /* get_tile_bbox (:62-92) */
+        const float tcx = xy[0] / (float)BLOCK, tcy = xy[1] / (float)BLOCK, tr = radius / (float)BLOCK;
+        const int x0 = std::min(std::max(0, f2i(tcx - tr)), cam->tiles_x);
+        const int x1 = std::min(std::max(0, f2i(tcx + tr + 1)), cam->tiles_x);
+        const int y0 = std::min(std::max(0, f2i(tcy - tr)), cam->tiles_y);
+        const int y1 = std::min(std::max(0, f2i(tcy + tr + 1)), cam->tiles_y);
+        if ((x1 - x0) * (y1 - y0) <= 0) continue;
+        radii[i] = (int)radius;
+        depths[i] = pv[2];
+        xys[2 * i] = xy[0];
+        xys[2 * i + 1] = xy[1];
+        for (int k = 0; k < 3; ++k) conics[3 * i + k] = cn[k];
+        if (cov2d)
+            for (int k = 0; k < 3; ++k) cov2d[3 * i + k] = c2[k];
+        rect[4 * i + 0] = x0;
+        rect[4 * i + 1] = y0;
+        rect[4 * i + 2] = x1;
+        rect[4 * i + 3] = y1;
+        const f3 dir = normalize3({p[0] - cam->cam_pos[0], p[1] - cam->cam_pos[1], p[2] - cam->cam_pos[2]});
+        sh_eval(dtu, dir, fdc + 3 * i, frest + (size_t)(nb - 1) * 3 * i, colors + 3 * i);
+    }
+}
+
+/* 3DGS compositing forward: out_img, final_T (T per pixel) and
+ * final_index (the last contributor, 1-based list position). */
+extern "C" void orc_raster3d_fwd(const OrcCamera *cam, const int32_t *tile_offsets, const int32_t *ids,
+                                 const float *xys, const float *conics, const float *colors,
+                                 const float *opacities, const float *bg, float *out_img, float *final_T,
+                                 int32_t *final_index) {
+    const int W = cam->width, H = cam->height, TX = cam->tiles_x;
+#pragma omp parallel for schedule(dynamic, 4)
+    for (int py_i = 0; py_i < H; ++py_i)
+        for (int px_i = 0; px_i < W; ++px_i) {
+            const int tile = (py_i / BLOCK) * TX + (px_i / BLOCK);
+            const float px = (float)px_i, py = (float)py_i;
+            float T = 1.f, cr = 0.f, cg = 0.f, cb = 0.f;
+            int contributor = 0, last = 0;
+            for (int j = tile_offsets[tile]; j < tile_offsets[tile + 1]; ++j) {
+                contributor++;
+                const int g = ids[j];
+                const float dx = xys[2 * g] - px, dy = xys[2 * g + 1] - py;
+                const float rho = conic_rho(conics + 3 * g, dx, dy);
+                if (rho < 0.f) continue;
+                const float alpha = fminf(0.99f, sigmoid(opacities[g]) * orc_gauss(rho));
+                if (alpha < 1.0f / 255.0f) continue;
+                const float next_T = T * (1.0f - alpha);
+                if (next_T <= 1e-4f) break;
+                const float w = alpha * T;
+                const float *c = colors + 3 * g;
+                cr = fmaf(fmaxf(c[0] + 0.5f, 0.0f), w, cr);
+                cg = fmaf(fmaxf(c[1] + 0.5f, 0.0f), w, cg);
+                cb = fmaf(fmaxf(c[2] + 0.5f, 0.0f), w, cb);
+                T = next_T;
+                last = contributor;
+            }
+            const size_t pix = (size_t)py_i * W + px_i;
+            final_T[pix] = T;
+            final_index[pix] = last;
+            out_img[3 * pix + 0] = fmaf(bg[0], T, cr);
+            out_img[3 * pix + 1] = fmaf(bg[1], T, cg);
+            out_img[3 * pix + 2] = fmaf(bg[2], T, cb);
+        }
+}
+
+/* 3DGS compositing backward.  grads is [N,9] = (dL/dxy 2, dL/dconic 3 in
+ * the EWA helpers' convention -- the off-diagonal entry is the derivative by
+ * one of the two symmetric matrix entries, as cov2d_to_conic_vjp (:1080-1093)
+ * expects --, dL/dopacity logit, dL/dcolors 3 (zero where the +0.5 clamp is
+ * active)), summed in fp64 in a fixed order; grads_abs (nullable) the sums
+ * of the magnitudes of the summands' parts. */
+extern "C" void orc_raster3d_bwd(const OrcCamera *cam, int n, const int32_t *tile_offsets, const int32_t *ids,
+                                 const float *xys, const float *conics, const float *colors,
+                                 const float *opacities, const float *bg, const float *final_T,
+                                 const int32_t *final_index, const float *dL_dimg, float *grads,
+                                 float *grads_abs) {
+    const int W = cam->width, H = cam->height, TX = cam->tiles_x, TY = cam->tiles_y;
+    const int T_tiles = TX * TY;
+    const int64_t I = tile_offsets[T_tiles];
+    std::vector<double> acc((size_t)I * 9, 0.0), acc_abs(grads_abs ? (size_t)I * 9 : 0, 0.0);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int tile = 0; tile < T_tiles; ++tile) {
+        const int ty = tile / TX, tx = tile % TX;
+        const int start = tile_offsets[tile];
+        for (int ly = 0; ly < BLOCK; ++ly)
+            for (int lx = 0; lx < BLOCK; ++lx) {
+                const int py_i = ty * BLOCK + ly, px_i = tx * BLOCK + lx;
+                if (py_i >= H || px_i >= W) continue;
+                const size_t pix = (size_t)py_i * W + px_i;
+                const float px = (float)px_i, py = (float)py_i;
+                const float T_final = final_T[pix];
+                const float dpix[3] = {dL_dimg[3 * pix], dL_dimg[3 * pix + 1], dL_dimg[3 * pix + 2]};
+                const float bg_dot = bg[0] * dpix[0] + bg[1] * dpix[1] + bg[2] * dpix[2];
+                float T = T_final, last_alpha = 0.f;
+                float accum_rec[3] = {0, 0, 0}, last_color[3] = {0, 0, 0};
+                for (int c = final_index[pix] - 1; c >= 0; --c) {
+                    const int j = start + c;
+                    const int g = ids[j];
+                    const float *cn = conics + 3 * g;
+                    const float dx = xys[2 * g] - px, dy = xys[2 * g + 1] - py;
+                    const float rho = conic_rho(cn, dx, dy);
+                    if (rho < 0.f) continue;
+                    const float opa = sigmoid(opacities[g]);
+                    const float G = orc_gauss(rho);
+                    const float alpha = fminf(0.99f, opa * G);
+                    if (alpha < 1.0f / 255.0f) continue;
+                    T = T / (1.0f - alpha);
+                    double *a = acc.data() + (size_t)j * 9;
+                    double *aa = grads_abs ? acc_abs.data() + (size_t)j * 9 : nullptr;
+                    float dL_dalpha = 0.f;
+                    const float *crgb = colors + 3 * g;
+                    for (int ch = 0; ch < 3; ++ch) {
+                        const float c_raw = crgb[ch];
+                        const float c_used = fmaxf(c_raw + 0.5f, 0.0f);
+                        const float mask = (c_raw + 0.5f > 0.0f) ? 1.0f : 0.0f;
+                        accum_rec[ch] = last_alpha * last_color[ch] + (1.f - last_alpha) * accum_rec[ch];
+                        last_color[ch] = c_used;
+                        dL_dalpha += (c_used - accum_rec[ch]) * dpix[ch];
+                        a[6 + ch] += (double)(alpha * T * dpix[ch] * mask);
+                        if (aa) aa[6 + ch] += std::fabs((double)(alpha * T * dpix[ch] * mask));
+                    }
+                    dL_dalpha *= T;
+                    last_alpha = alpha;
+                    dL_dalpha += (-T_final / (1.f - alpha)) * bg_dot;
+                    /* alpha = opa exp(-sigma): dL/dsigma = -opa G dL/dalpha */
+                    const float v_sigma = -opa * G * dL_dalpha;
+                    a[0] += (double)(v_sigma * (cn[0] * dx + cn[1] * dy));
+                    a[1] += (double)(v_sigma * (cn[1] * dx + cn[2] * dy));
+                    a[2] += (double)(0.5f * v_sigma * dx * dx);
+                    a[3] += (double)(0.5f * v_sigma * dx * dy);
+                    a[4] += (double)(0.5f * v_sigma * dy * dy);
+                    const float dsig = opa * (1.0f - opa);
+                    a[5] += (double)(G * dL_dalpha * dsig);
+                    if (aa) {
+                        const double vs = std::fabs((double)v_sigma);
+                        aa[0] += vs * (std::fabs((double)cn[0] * dx) + std::fabs((double)cn[1] * dy));
+                        aa[1] += vs * (std::fabs((double)cn[1] * dx) + std::fabs((double)cn[2] * dy));
+                        aa[2] += 0.5 * vs * dx * dx;
+                        aa[3] += 0.5 * vs * std::fabs((double)dx * dy);
+                        aa[4] += 0.5 * vs * dy * dy;
+                        aa[5] += std::fabs((double)(G * dL_dalpha * dsig));
+                    }
+                }
+            }
+    }
+    std::vector<double> gsum((size_t)n * 9, 0.0);
+    for (int64_t j = 0; j < I; ++j)
+        for (int k = 0; k < 9; ++k) gsum[(size_t)ids[j] * 9 + k] += acc[(size_t)j * 9 + k];
+    for (size_t k = 0; k < (size_t)n * 9; ++k) grads[k] = (float)gsum[k];
+    if (grads_abs) {
+        std::fill(gsum.begin(), gsum.end(), 0.0);
+        for (int64_t j = 0; j < I; ++j)
+            for (int k = 0; k < 9; ++k) gsum[(size_t)ids[j] * 9 + k] += acc_abs[(size_t)j * 9 + k];
+        for (size_t k = 0; k < (size_t)n * 9; ++k) grads_abs[k] = (float)gsum[k];
+    }
+}
+
+/* 3DGS projection + SH backward: grads9 (orc_raster3d_bwd's layout) ->
+ * dL/dmeans [N,3], dL/dscales (log) [N,3], dL/dquats [N,4], dL/dfeatures_dc,
+ * dL/dfeatures_rest; dmean2d = dL/dxy in NDC units (0.5 W, 0.5 H per pixel),
+ * and the densification statistics (|dmean2d| L1 norm, visibility, largest
+ * radius / max(W, H)), read-modify-write. */
+extern "C" void orc_project3d_bwd(int n, const float *means, const float *scales, const float *quats,
+                                  const float *frest, int degree, int dtu, const OrcCamera *cam, float glob_scale,
+                                  const int32_t *radii, const float *grads9, float *dmeans, float *dscales,
+                                  float *dquats, float *dmean2d, float *dfdc, float *dfrest, float *xys_grad_norm,
+                                  float *vis_counts, float *max_2d_size, float inv_max_dim) {
+    const float *vm = cam->viewmat, *pm = cam->projmat;
+    const int K = num_sh_bases(degree) - 1;
+    const float tan_fovx = 0.5f * (float)cam->width / cam->fx, tan_fovy = 0.5f * (float)cam->height / cam->fy;
+    const float fx = cam->fx, fy = cam->fy;
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < n; ++i) {
+        float *dfr = dfrest + (size_t)K * 3 * i;
+        for (int k = 0; k < K * 3; ++k) dfr[k] = 0.f;
+        for (int k = 0; k < 3; ++k) dmeans[3 * i + k] = dscales[3 * i + k] = dfdc[3 * i + k] = 0.f;
+        for (int k = 0; k < 4; ++k) dquats[4 * i + k] = 0.f;
+        dmean2d[2 * i] = dmean2d[2 * i + 1] = 0.f;
+        if (radii[i] <= 0) continue;
+        const float *p = means + 3 * i;
+        const float *q = quats + 4 * i;
+        const float *g = grads9 + 9 * i;
+        const float pv[3] = {vm[0] * p[0] + vm[1] * p[1] + vm[2] * p[2] + vm[3],
+                             vm[4] * p[0] + vm[5] * p[1] + vm[6] * p[2] + vm[7],
+                             vm[8] * p[0] + vm[9] * p[1] + vm[10] * p[2] + vm[11]};
+        const float s[3] = {orc_expf(scales[3 * i]), orc_expf(scales[3 * i + 1]), orc_expf(scales[3 * i + 2])};
+        float cov[6], c2[3], cn[3], radius;
+        f3 R[3];
+        cov3d_of(s, glob_scale, q, cov, R);
+        ewa_cov2d(cov, vm, fx, fy, tan_fovx, tan_fovy, pv, c2);
+        cov2d_bounds(c2, cn, radius);
+        /* cov2d_to_conic_vjp (:1080-1093): v_Sigma = -X G X */
+        float vc2[3];
+        {
+            const float X00 = cn[0], X01 = cn[1], X11 = cn[2];
+            const float G00 = g[2], G01 = g[3], G11 = g[4];
+            /* XG */
+            const float A00 = X00 * G00 + X01 * G01, A01 = X00 * G01 + X01 * G11;
+            const float A10 = X01 * G00 + X11 * G01, A11 = X01 * G01 + X11 * G11;
+            /* -(XG)X */
+            const float S00 = -(A00 * X00 + A01 * X01), S01 = -(A00 * X01 + A01 * X11);
+            const float S10 = -(A10 * X00 + A11 * X01), S11 = -(A10 * X01 + A11 * X11);
+            vc2[0] = S00;
+            vc2[1] = S10 + S01;
+            vc2[2] = S11;
+        }
+        /* project_cov3d_ewa_vjp (:1110-1179) */
+        float vcov[6];
+        float vmean[3] = {0.f, 0.f, 0.f};
+        {
+            float px = pv[0], py = pv[1];
+            const float pz = pv[2];
+            ewa_clamp(px, py, pz, tan_fovx, tan_fovy);
+            const float rz = 1.f / pz, rz2 = rz * rz;
+            /* T = J W (rows), W = the view rotation (rows of vm) */
+            const float Wm[3][3] = {{vm[0], vm[1], vm[2]}, {vm[4], vm[5], vm[6]}, {vm[8], vm[9], vm[10]}};
+            const float J[3][3] = {{fx * rz, 0.f, -fx * px * rz2}, {0.f, fy * rz, -fy * py * rz2}, {0.f, 0.f, 0.f}};
+            float Tm[3][3];
+            for (int r = 0; r < 3; ++r)
+                for (int c = 0; c < 3; ++c) Tm[r][c] = J[r][0] * Wm[0][c] + J[r][1] * Wm[1][c] + J[r][2] * Wm[2][c];
+            const float V[3][3] = {{cov[0], cov[1], cov[2]}, {cov[1], cov[3], cov[4]}, {cov[2], cov[4], cov[5]}};
+            const float vC[3][3] = {{vc2[0], 0.5f * vc2[1], 0.f}, {0.5f * vc2[1], vc2[2], 0.f}, {0.f, 0.f, 0.f}};
+            /* v_V = T^T vC T */
+            float vCT[3][3], vV[3][3];
+            for (int r = 0; r < 3; ++r)
+                for (int c = 0; c < 3; ++c) vCT[r][c] = vC[r][0] * Tm[0][c] + vC[r][1] * Tm[1][c] + vC[r][2] * Tm[2][c];
+            for (int r = 0; r < 3; ++r)
+                for (int c = 0; c < 3; ++c) vV[r][c] = Tm[0][r] * vCT[0][c] + Tm[1][r] * vCT[1][c] + Tm[2][r] * vCT[2][c];
+            vcov[0] = vV[0][0];
+            vcov[1] = vV[0][1] + vV[1][0];
+            vcov[2] = vV[0][2] + vV[2][0];
+            vcov[3] = vV[1][1];
+            vcov[4] = vV[1][2] + vV[2][1];
+            vcov[5] = vV[2][2];
+            /* v_T = vC T V^T + vC^T T V = 2 vC T V (vC and V symmetric) */
+            float vT[3][3];
+            for (int r = 0; r < 3; ++r)
+                for (int c = 0; c < 3; ++c) {
+                    const float x = vCT[r][0] * V[0][c] + vCT[r][1] * V[1][c] + vCT[r][2] * V[2][c];
+                    vT[r][c] = x + x;
+                }
+            /* v_J = v_T W^T */
+            float vJ[3][3];
+            for (int r = 0; r < 3; ++r)
+                for (int c = 0; c < 3; ++c) vJ[r][c] = vT[r][0] * Wm[c][0] + vT[r][1] * Wm[c][1] + vT[r][2] * Wm[c][2];
+            const float fx_rz2 = fx * rz2, fy_rz2 = fy * rz2, rz3 = rz2 * rz;
+            /* dJ/d(p_view): J02 = -fx px rz2, J12 = -fy py rz2, J00 = fx rz, J11 = fy rz */
+            const float vt[3] = {-fx_rz2 * vJ[0][2], -fy_rz2 * vJ[1][2],
+                                 -fx_rz2 * vJ[0][0] + 2.f * fx * px * rz3 * vJ[0][2] - fy_rz2 * vJ[1][1] +
+                                     2.f * fy * py * rz3 * vJ[1][2]};
+            /* p_view = W p + t: v_mean = W^T v_t */
+            for (int k = 0; k < 3; ++k) vmean[k] = Wm[0][k] * vt[0] + Wm[1][k] * vt[1] + Wm[2][k] * vt[2];
+        }
+        /* scale_rot_to_cov3d_vjp (:1299-1339) */
+        {
+            const float vV[3][3] = {{vcov[0], 0.5f * vcov[1], 0.5f * vcov[2]},
+                                    {0.5f * vcov[1], vcov[3], 0.5f * vcov[4]},
+                                    {0.5f * vcov[2], 0.5f * vcov[4], vcov[5]}};
+            const float g3[3] = {glob_scale * s[0], glob_scale * s[1], glob_scale * s[2]};
+            /* M[r][c] = R[c][r] g_c; v_M = 2 v_V M */
+            float M[3][3];
+            for (int r = 0; r < 3; ++r) {
+                M[r][0] = (r == 0 ? R[0].x : r == 1 ? R[0].y : R[0].z) * g3[0];
+                M[r][1] = (r == 0 ? R[1].x : r == 1 ? R[1].y : R[1].z) * g3[1];
+                M[r][2] = (r == 0 ? R[2].x : r == 1 ? R[2].y : R[2].z) * g3[2];
+            }
+            float vM[3][3];
+            for (int r = 0; r < 3; ++r)
+                for (int c = 0; c < 3; ++c) {
+                    const float x = vV[r][0] * M[0][c] + vV[r][1] * M[1][c] + vV[r][2] * M[2][c];
+                    vM[r][c] = 2.f * x;
+                }
+            /* v_S_c = column c of R . column c of v_M; v_R = v_M S */
+            f3 vR[3];
+            for (int c = 0; c < 3; ++c) {
+                const float vs = R[c].x * vM[0][c] + R[c].y * vM[1][c] + R[c].z * vM[2][c];
+                dscales[3 * i + c] = vs * glob_scale * s[c];  /* d/d(log scale) */
+                vR[c] = {vM[0][c] * g3[c], vM[1][c] * g3[c], vM[2][c] * g3[c]};
+            }
+            quat_to_rotmat_vjp(q, vR, dquats + 4 * i);
+        }
+        /* project_pix_vjp (:1059-1077) */
+        {
+            const float hw = pm[12] * p[0] + pm[13] * p[1] + pm[14] * p[2] + pm[15];
+            const float rw = 1.f / (hw + 1e-6f);
+            const float hx = pm[0] * p[0] + pm[1] * p[1] + pm[2] * p[2] + pm[3];
+            const float hy = pm[4] * p[0] + pm[5] * p[1] + pm[6] * p[2] + pm[7];
+            const float vnx = 0.5f * (float)cam->width * g[0], vny = 0.5f * (float)cam->height * g[1];
+            /* xy = f(h.xy / h.w): d/dh.x = vnx rw, d/dh.y = vny rw,
+             * d/dh.w = -(vnx hx + vny hy) rw^2 */
+            const float vhx = vnx * rw, vhy = vny * rw, vhw = -(vnx * hx + vny * hy) * rw * rw;
+            for (int k = 0; k < 3; ++k) vmean[k] += pm[k] * vhx + pm[4 + k] * vhy + pm[12 + k] * vhw;
+            dmean2d[2 * i] = vnx;
+            dmean2d[2 * i + 1] = vny;
+        }
+        for (int k = 0; k < 3; ++k) dmeans[3 * i + k] = vmean[k];
+        /* SH backward (as the 2DGS projection backward) */
+        const f3 dir_un = {p[0] - cam->cam_pos[0], p[1] - cam->cam_pos[1], p[2] - cam->cam_pos[2]};
+        const f3 dir = normalize3(dir_un);
+        const float *vc = g + 6;
+        sh_vjp(dtu, dir, vc, dfdc + 3 * i, dfr);
+        if (dtu >= 1) {
+            const f3 dd = sh_dL_ddir(dtu, dir, frest + (size_t)K * 3 * i, vc);
+            const f3 dm = dnormvdv(dir_un, dd);
+            dmeans[3 * i + 0] += dm.x;
+            dmeans[3 * i + 1] += dm.y;
+            dmeans[3 * i + 2] += dm.z;
+        }
+        xys_grad_norm[i] += fabsf(dmean2d[2 * i]) + fabsf(dmean2d[2 * i + 1]);
+        vis_counts[i] += 1.0f;
+        const float r_norm = (float)radii[i] * inv_max_dim;
+        if (r_norm > max_2d_size[i]) max_2d_size[i] = r_norm;
+    }
+}

@@ -81,6 +81,11 @@ def lib() -> C.CDLL:
                                          P, P]
         L.orc_marching_cubes.restype = C.c_int64
         L.orc_marching_cubes.argtypes = [P, C.c_int, C.c_int, C.c_int, P, F, P, C.c_int64, P]
+        L.orc_project3d_fwd.argtypes = [C.c_int] + [P] * 5 + [C.c_int, C.c_int, C.POINTER(OrcCamera), F, F] + [P] * 7
+        L.orc_raster3d_fwd.argtypes = [C.POINTER(OrcCamera)] + [P] * 10
+        L.orc_raster3d_bwd.argtypes = [C.POINTER(OrcCamera), C.c_int] + [P] * 12
+        L.orc_project3d_bwd.argtypes = ([C.c_int] + [P] * 4 + [C.c_int, C.c_int, C.POINTER(OrcCamera), F] + [P] * 11
+                                        + [F])
         L.orc_unproject_depth.restype = C.c_int64
         L.orc_unproject_depth.argtypes = [P, P, P, C.c_int, C.c_int, F, F, F, F, P, F, P, P]
         _lib = L
@@ -335,3 +340,66 @@ def unproject_depth(img, depth, alpha, fx, fy, cx, cy, cam_to_world, alpha_thres
     n = lib().orc_unproject_depth(_p(img), _p(depth), _p(alpha), w, h, fx, fy, cx, cy, _p(c2w), alpha_thresh,
                                   _p(xyz), _p(rgb))
     return xyz[:n], rgb[:n]
+
+
+# ---- 3DGS mode ---------------------------------------------------------------
+
+def project3d_fwd(params: dict, cam: OrcCamera, degree: int, dtu: int, glob_scale=1.0, clip_thresh=0.01):
+    """3DGS projection: dict(xys, conics, depths, radii, rect, colors, cov2d).
+    params: means [N,3], scales [N,3] (log), quats [N,4], features_dc,
+    features_rest."""
+    m = _f(params["means"])
+    n = m.shape[0]
+    sc, qu, dc, fr = _f(params["scales"]), _f(params["quats"]), _f(params["features_dc"]), _f(params["features_rest"])
+    assert sc.shape == (n, 3)
+    out = dict(xys=np.zeros((n, 2), np.float32), conics=np.zeros((n, 3), np.float32),
+               depths=np.zeros(n, np.float32), radii=np.zeros(n, np.int32), rect=np.zeros((n, 4), np.int32),
+               colors=np.zeros((n, 3), np.float32), cov2d=np.zeros((n, 3), np.float32))
+    lib().orc_project3d_fwd(n, _p(m), _p(sc), _p(qu), _p(dc), _p(fr), degree, dtu, C.byref(cam), glob_scale,
+                            clip_thresh, _p(out["xys"]), _p(out["conics"]), _p(out["depths"]), _p(out["radii"]),
+                            _p(out["rect"]), _p(out["colors"]), _p(out["cov2d"]))
+    return out
+
+
+def raster3d_fwd(proj: dict, bins: dict, cam: OrcCamera, opacities, background):
+    H, W = cam.height, cam.width
+    out = dict(out_img=np.zeros((H, W, 3), np.float32), final_T=np.zeros((H, W), np.float32),
+               final_idx=np.zeros((H, W), np.int32))
+    ids = bins["ids"] if bins["ids"].size else np.zeros(1, np.int32)
+    op, bgf = _f(opacities).reshape(-1), _f(background)
+    lib().orc_raster3d_fwd(C.byref(cam), _p(bins["tile_offsets"]), _p(ids), _p(proj["xys"]), _p(proj["conics"]),
+                           _p(proj["colors"]), _p(op), _p(bgf), _p(out["out_img"]), _p(out["final_T"]),
+                           _p(out["final_idx"]))
+    return out
+
+
+def raster3d_bwd(proj, bins, fwd, cam, opacities, background, dL_dimg, with_abs=False):
+    """[N,9] = (dL/dxy 2, dL/dconic 3, dL/dopacity logit, dL/dcolor 3)."""
+    n = proj["radii"].shape[0]
+    g = np.zeros((n, 9), np.float32)
+    ga = np.zeros((n, 9), np.float32) if with_abs else None
+    ids = bins["ids"] if bins["ids"].size else np.zeros(1, np.int32)
+    op, bgf, dl = _f(opacities).reshape(-1), _f(background), _f(dL_dimg)
+    lib().orc_raster3d_bwd(C.byref(cam), n, _p(bins["tile_offsets"]), _p(ids), _p(proj["xys"]), _p(proj["conics"]),
+                           _p(proj["colors"]), _p(op), _p(bgf), _p(fwd["final_T"]), _p(fwd["final_idx"]), _p(dl),
+                           _p(g), _p(ga))
+    return (g, ga) if with_abs else g
+
+
+def project3d_bwd(params: dict, cam, degree, dtu, radii, grads9, stats=None, glob_scale=1.0):
+    m = _f(params["means"])
+    n = m.shape[0]
+    K = (degree + 1) ** 2 - 1
+    out = dict(dmeans=np.zeros((n, 3), np.float32), dscales=np.zeros((n, 3), np.float32),
+               dquats=np.zeros((n, 4), np.float32), dmean2d=np.zeros((n, 2), np.float32),
+               dfdc=np.zeros((n, 3), np.float32), dfrest=np.zeros((n, max(K, 0), 3), np.float32))
+    if stats is None:
+        stats = dict(grad_norm=np.zeros(n, np.float32), vis=np.zeros(n, np.float32), max2d=np.zeros(n, np.float32))
+    inv_max_dim = np.float32(1.0) / np.float32(max(cam.width, cam.height))
+    sc, qu, fr = _f(params["scales"]), _f(params["quats"]), _f(params["features_rest"])
+    rad, g9 = np.ascontiguousarray(radii, np.int32), _f(grads9)
+    lib().orc_project3d_bwd(n, _p(m), _p(sc), _p(qu), _p(fr), degree, dtu, C.byref(cam), glob_scale, _p(rad), _p(g9),
+                            *[_p(out[k]) for k in ("dmeans", "dscales", "dquats", "dmean2d", "dfdc", "dfrest")],
+                            _p(stats["grad_norm"]), _p(stats["vis"]), _p(stats["max2d"]), float(inv_max_dim))
+    out.update(stats)
+    return out

@@ -199,3 +199,52 @@ def loss(img, gt, lam=0.2):
     img = img.astype(np.float64)
     gt = gt.astype(np.float64)
     return (1.0 - lam) * np.abs(img - gt).mean() + lam * (1.0 - ssim_map(img, gt).mean())
+
+
+# ---- 3DGS (EWA splatting, Zwicker et al. 2002; Kerbl et al. 2023) ----------
+def ewa_project(mean, log_scale, quat, viewmat, projmat, fx, fy, W, H, cx, cy):
+    """fp64 projection of a 3D Gaussian: (xy [2], cov2d [2,2], conic [2,2],
+    depth).  The 2D covariance is J W Sigma W^T J^T + 0.3 I with the
+    perspective Jacobian J at the view-space mean (its x/z, y/z clamped to
+    1.3 tan(fov/2), as the reference's helper does), Sigma = R S S^T R^T."""
+    V = np.asarray(viewmat, np.float64).reshape(4, 4)
+    P = np.asarray(projmat, np.float64).reshape(4, 4)
+    m = np.asarray(mean, np.float64)
+    pv = V[:3, :3] @ m + V[:3, 3]
+    R = rotation(quat)
+    S = np.diag(np.exp(np.asarray(log_scale, np.float64)))
+    Sigma = R @ S @ S.T @ R.T
+    tx, ty = 0.5 * W / fx, 0.5 * H / fy
+    x = pv[2] * np.clip(pv[0] / pv[2], -1.3 * tx, 1.3 * tx)
+    y = pv[2] * np.clip(pv[1] / pv[2], -1.3 * ty, 1.3 * ty)
+    z = pv[2]
+    J = np.array([[fx / z, 0.0, -fx * x / (z * z)], [0.0, fy / z, -fy * y / (z * z)]])
+    Wr = V[:3, :3]
+    cov2d = J @ Wr @ Sigma @ Wr.T @ J.T + 0.3 * np.eye(2)
+    h = P @ np.append(m, 1.0)
+    xy = np.array([0.5 * W * h[0] / (h[3] + 1e-6) + cx - 0.5, 0.5 * H * h[1] / (h[3] + 1e-6) + cy - 0.5])
+    return xy, cov2d, np.linalg.inv(cov2d), z
+
+
+def composite3d(px, py, splats, background):
+    """fp64 front-to-back compositing of 3D Gaussians at pixel (px, py):
+    alpha = min(0.99, sigmoid(opacity) exp(-0.5 d^T C d)), d = centre -
+    pixel; skipped when the exponent is positive or alpha < 1/255, stopping
+    before the transmittance falls to 1e-4 (the fork's blending rules)."""
+    T = 1.0
+    col = np.zeros(3)
+    for s in splats:
+        d = np.asarray(s["xy"], np.float64) - np.array([px, py])
+        C = np.asarray(s["conic"], np.float64)
+        rho = d @ C @ d
+        if rho < 0:
+            continue
+        alpha = min(0.99, 1.0 / (1.0 + math.exp(-s["opac_logit"])) * math.exp(-0.5 * rho))
+        if alpha < 1.0 / 255.0:
+            continue
+        nT = T * (1.0 - alpha)
+        if nT <= 1e-4:
+            break
+        col += np.maximum(np.asarray(s["color_raw"], np.float64) + 0.5, 0.0) * alpha * T
+        T = nT
+    return col + np.asarray(background, np.float64) * T, T
