@@ -11,7 +11,8 @@
  *    msplat_last_error();
  *  - msplat_set_metallib_path is accepted and ignored (the GPU code is
  *    linked into the library);
- *  - msplat_trainer_extract_mesh returns -1 (mesh extraction is not built).
+ *  - msplat_trainer_extract_mesh returns the triangle count, or -1 with
+ *    msplat_last_error() set.
  * Threading: one trainer per process, as the reference (one engine
  * context and buffer cache). */
 #ifndef MSPLAT_C_API_H

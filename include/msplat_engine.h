@@ -332,6 +332,29 @@ int msplat_hip_check_fast_rcp(int efield_lo, int efield_hi, int64_t *mismatches)
  * lists are the same either way.  No counterpart in the reference. */
 int msplat_hip_set_wide_keys(int on);
 
+/* ---- 3DGS mode ------------------------------------------------------------
+ * 3D Gaussians (scales [N,3], log) projected with the reference's EWA
+ * helpers (scale_rot_to_cov3d, project_cov3d_ewa, compute_cov2d_bounds,
+ * project_pix: core/metal/msplat_metal.metal:152-459, VJPs :1059-1374,
+ * dead code in the 2DGS fork) and composited with the 3DGS pair rule in the
+ * fork's blending conventions.  The fork removed its 3DGS step
+ * (msplat_train_step, bindings.h:140); these are its replacement.  The
+ * binning, the loss and the densification statistics are the 2DGS path's.
+ * Outputs: MSPLAT_LAST_OUT_IMG and MSPLAT_LAST_FINAL_TS (first component);
+ * after a train step, MSPLAT_LAST_GRADS16 holds per splat [dL/dxy 2,
+ * dL/dconic 3, dL/dopacity logit, dL/dcolor 3] in its first 9 floats.
+ * Gaussians carry MsplatGaussians' layouts except scales [N,3]. */
+int msplat_hip_render_3dgs(const MsplatCamera *cam, const MsplatGaussians *g, const float *background_dev,
+                           int64_t *num_isect_host);
+/* One 3DGS training step: forward with the blend log, SSIM + L1 (no
+ * distortion term), backward, projection backward; adam non-null fuses
+ * the six Adam updates (scales [N,3]), NULL leaves the parameter gradients
+ * in the MSPLAT_LAST_DL_* buffers (DL_DSCALE [N,3]). */
+int msplat_hip_train_step_3dgs(const MsplatCamera *cam, const MsplatGaussians *g, const float *background_dev,
+                               const float *gt_dev, float lambda_l1, float lambda_dssim, float *xys_grad_norm_dev,
+                               float *vis_counts_dev, float *max_2d_size_dev, float inv_max_dim,
+                               const MsplatAdam *adam, float *loss_host, int64_t *num_isect_host);
+
 /* ---- mesh extraction: TSDF fusion, marching cubes, depth unprojection ----
  * The voxel grid is [Dz, Dy, Dx, 2] f32 (sdf, weight) in HBM, voxel (x, y, z)
  * centred at origin + voxel_size * (index + 0.5) (Model::VoxelGrid,

@@ -88,6 +88,7 @@ struct Engine {
     bool have_grads = false;
     bool raster_grads = false;  // grads16 belongs to the current forward
     bool g16_moments = false;   // grads16 holds the image-only backward's unfinished sums
+    bool gs3d = false;        // the most recent forward is the 3DGS mode's
     bool log_valid = false;   // blend log written for the most recent forward
     bool full_valid = false;  // depth / normal / alpha / median / distortion outputs written
     // timing
@@ -278,6 +279,17 @@ int raster_fwd_locked(bool log, bool full) {
         tc = P<float>(E.t_ckpt);
         wc = P<int>(E.wave_cnt);
     }
+    if (E.gs3d) {
+        if (full) {
+            set_err("the 3DGS mode produces the image and the transmittance only");
+            return MSPLAT_E_ARG;
+        }
+        mskern::launch_raster3d_fwd(E.stream, E.W, E.H, E.tiles_x, E.tiles_y, P<int>(E.offsets), P<int>(E.ids),
+                                    P<float>(E.rec), P<float>(E.rec) + (size_t)E.n * mskern::kRec3Floats, E.bg,
+                                    P<float>(E.out_img), P<float>(E.final_Ts), lg, tc, wc);
+        E.log_valid = E.log_valid || log;
+        return MSPLAT_OK;
+    }
     mskern::launch_raster_fwd(E.stream, E.W, E.H, E.tiles_x, E.tiles_y, P<int>(E.offsets), P<int>(E.ids),
                               P<float>(E.rec), mask_recs(), E.bg, P<float>(E.out_img), P<float>(E.final_Ts),
                               P<int>(E.final_idx),
@@ -290,7 +302,7 @@ int raster_fwd_locked(bool log, bool full) {
 }
 
 int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, int64_t *nisect, bool log,
-                   bool full) {
+                   bool full, bool gs3d = false) {
     CHECK(validate_cam(cam, g));
     if (!bg) {
         set_err("null background");
@@ -342,14 +354,20 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     E.g16_moments = false;
     E.log_valid = false;
     E.full_valid = false;
+    E.gs3d = gs3d;
     for (int i = 0; i < ST_COUNT; ++i) E.stage_valid[i] = false;
 
     stage_mark(ST_PROJECT);
     HIPC(hipMemsetAsync(E.stats.p, 0, 64, s));
     if (E.count_pairs) HIPC(hipMemsetAsync(E.pair_counter.p, 0, 40, s));
-    mskern::launch_project_fwd(s, *cam, *g, P<float>(E.rec), mask_recs(), P<float>(E.depths), P<int>(E.radii),
-                               P<uint32_t>(E.rect), reinterpret_cast<unsigned long long *>(P<int>(E.stats) + 8),
-                               nullptr);
+    if (gs3d)
+        mskern::launch_project3d_fwd(s, *cam, *g, P<float>(E.rec), P<float>(E.rec) + (size_t)N * mskern::kRec3Floats,
+                                     P<float>(E.depths), P<int>(E.radii), P<uint32_t>(E.rect),
+                                     reinterpret_cast<unsigned long long *>(P<int>(E.stats) + 8), nullptr);
+    else
+        mskern::launch_project_fwd(s, *cam, *g, P<float>(E.rec), mask_recs(), P<float>(E.depths), P<int>(E.radii),
+                                   P<uint32_t>(E.rect), reinterpret_cast<unsigned long long *>(P<int>(E.stats) + 8),
+                                   nullptr);
     stage_mark(ST_SCAN);
     mskern::launch_super_count(s, N, cam->tiles_x, cam->tiles_y, P<int>(E.radii), P<uint32_t>(E.rect),
                                P<int>(E.super_counts), P<int>(E.super_offsets), P<int>(E.super_cm),
@@ -407,7 +425,10 @@ int last_locked(int which, void **ptr, int64_t *numel) {
     *ptr = nullptr;
     *numel = 0;
     switch (which) {
-        case MSPLAT_LAST_FINAL_TS: case MSPLAT_LAST_FINAL_IDX: case MSPLAT_LAST_OUT_DEPTH:
+        case MSPLAT_LAST_FINAL_TS:
+            if (E.gs3d) break;  // the transmittance (its first component) is written by every 3DGS forward
+            [[fallthrough]];
+        case MSPLAT_LAST_FINAL_IDX: case MSPLAT_LAST_OUT_DEPTH:
         case MSPLAT_LAST_OUT_NORMAL: case MSPLAT_LAST_OUT_ALPHA: case MSPLAT_LAST_OUT_MEDIAN_DEPTH:
         case MSPLAT_LAST_OUT_DISTORTION:
             // produced on demand after an image-only forward
@@ -419,8 +440,21 @@ int last_locked(int which, void **ptr, int64_t *numel) {
             // the image-only backward leaves ray moments; turn them into the
             // reference's dL/dtransMat with this forward's records
             if (E.g16_moments) {
-                mskern::launch_finish_image_grads(E.stream, E.n, P<float>(E.rec), P<float>(E.grads16));
+                if (E.gs3d)
+                    mskern::launch_finish3d_grads(E.stream, E.n, P<float>(E.rec), P<float>(E.grads16));
+                else
+                    mskern::launch_finish_image_grads(E.stream, E.n, P<float>(E.rec), P<float>(E.grads16));
                 E.g16_moments = false;
+            }
+            if (E.gs3d && which != MSPLAT_LAST_GRADS16) {
+                set_err("buffer %d is a 2DGS raster gradient; the 3DGS mode's are in MSPLAT_LAST_GRADS16", which);
+                return MSPLAT_E_ARG;
+            }
+            break;
+        case MSPLAT_LAST_TRANSMATS: case MSPLAT_LAST_NORMALS:
+            if (E.gs3d) {
+                set_err("buffer %d does not exist in the 3DGS mode", which);
+                return MSPLAT_E_ARG;
             }
             break;
         default: break;
@@ -434,7 +468,7 @@ int last_locked(int which, void **ptr, int64_t *numel) {
         return MSPLAT_OK;
     };
     switch (which) {
-        case MSPLAT_LAST_XYS: return matf(which, E.rec, 20, 9, 2);
+        case MSPLAT_LAST_XYS: return E.gs3d ? matf(which, E.rec, 12, 0, 2) : matf(which, E.rec, 20, 9, 2);
         case MSPLAT_LAST_DEPTHS: *ptr = E.depths.p; *numel = N; return MSPLAT_OK;
         case MSPLAT_LAST_RADII: *ptr = E.radii.p; *numel = N; return MSPLAT_OK;
         case MSPLAT_LAST_NUM_TILES_HIT:
@@ -444,10 +478,11 @@ int last_locked(int which, void **ptr, int64_t *numel) {
             *numel = N;
             return MSPLAT_OK;
         case MSPLAT_LAST_TRANSMATS: return matf(which, E.rec, 20, 0, 9);
-        case MSPLAT_LAST_COLORS_USED: return matf(which, E.rec, 20, 15, 3);
-        case MSPLAT_LAST_OPACITY_SIGMOID: return matf(which, E.rec, 20, 11, 1);
+        case MSPLAT_LAST_COLORS_USED: return E.gs3d ? matf(which, E.rec, 12, 8, 3) : matf(which, E.rec, 20, 15, 3);
+        case MSPLAT_LAST_OPACITY_SIGMOID:
+            return E.gs3d ? matf(which, E.rec, 12, 5, 1) : matf(which, E.rec, 20, 11, 1);
         case MSPLAT_LAST_NORMALS: return matf(which, E.rec, 20, 12, 3);
-        case MSPLAT_LAST_RECORDS: *ptr = E.rec.p; *numel = N * 20; return MSPLAT_OK;
+        case MSPLAT_LAST_RECORDS: *ptr = E.rec.p; *numel = N * (E.gs3d ? mskern::kRec3Floats : 20); return MSPLAT_OK;
         case MSPLAT_LAST_TILE_OFFSETS:
             *ptr = E.offsets.p;
             *numel = (int64_t)E.tiles_x * E.tiles_y + 1;
@@ -468,7 +503,12 @@ int last_locked(int which, void **ptr, int64_t *numel) {
         case MSPLAT_LAST_DL_DOPACITY: return E.grads16.p ? matf(which, E.grads16, 16, 12, 1) : MSPLAT_OK;
         case MSPLAT_LAST_DL_DCOLORS: return E.grads16.p ? matf(which, E.grads16, 16, 13, 3) : MSPLAT_OK;
         case MSPLAT_LAST_DL_DMEAN3D: if (E.have_grads) { *ptr = E.dmeans.p; *numel = N * 3; } return MSPLAT_OK;
-        case MSPLAT_LAST_DL_DSCALE: if (E.have_grads) { *ptr = E.dscales.p; *numel = N * 2; } return MSPLAT_OK;
+        case MSPLAT_LAST_DL_DSCALE:
+            if (E.have_grads) {
+                *ptr = E.dscales.p;
+                *numel = N * (E.gs3d ? 3 : 2);
+            }
+            return MSPLAT_OK;
         case MSPLAT_LAST_DL_DQUAT: if (E.have_grads) { *ptr = E.dquats.p; *numel = N * 4; } return MSPLAT_OK;
         case MSPLAT_LAST_DL_DMEAN2D: if (E.have_grads) { *ptr = E.dmean2d.p; *numel = N * 2; } return MSPLAT_OK;
         case MSPLAT_LAST_DL_DFEATURES_DC: if (E.have_grads) { *ptr = E.dfdc.p; *numel = N * 3; } return MSPLAT_OK;
@@ -864,6 +904,82 @@ int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g, con
     API_END
 }
 
+// ---- 3DGS mode ----------------------------------------------------------
+
+int msplat_hip_render_3dgs(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, int64_t *nisect) {
+    API_BEGIN
+    ENSURE_INIT();
+    CHECK(forward_locked(cam, g, bg, nisect, false, false, true));
+    stage_mark(ST_LOSS);
+    if (g_eng.timing) {
+        HIPC(hipStreamSynchronize(g_eng.stream));
+        for (int i = ST_PROJECT; i < ST_LOSS; ++i) {
+            HIPC(hipEventElapsedTime(&g_eng.stage_ms[i], g_eng.ev[i], g_eng.ev[i + 1]));
+            g_eng.stage_valid[i] = true;
+        }
+    }
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_train_step_3dgs(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, const float *gt,
+                               float lambda_l1, float lambda_dssim, float *gnorm, float *vis, float *max2d,
+                               float inv_max_dim, const MsplatAdam *adam, float *loss_host, int64_t *nisect) {
+    API_BEGIN
+    ENSURE_INIT();
+    if (!gt || !gnorm || !vis || !max2d) {
+        set_err("null gt / densify statistics");
+        return MSPLAT_E_ARG;
+    }
+    Engine &E = g_eng;
+    hipStream_t s = E.stream;
+    CHECK(forward_locked(cam, g, bg, nisect, true, false, true));
+    const int N = g->num_points, W = cam->width, H = cam->height;
+    const size_t Pn = (size_t)W * H;
+    stage_mark(ST_LOSS);
+    CHECK(ensure(E.dL_dimg, Pn * 12));
+    CHECK(loss_locked(W, H, P<float>(E.out_img), gt, nullptr, lambda_l1, 0.f, lambda_dssim, P<float>(E.dL_dimg)));
+    HIPC(hipMemcpyAsync(E.pinned_d, E.loss.p, 2 * sizeof(double), hipMemcpyDeviceToHost, s));
+    stage_mark(ST_RASTER_BWD);
+    CHECK(ensure(E.grads16, (size_t)N * 64));
+    HIPC(hipMemsetAsync(E.grads16.p, 0, (size_t)N * 64, s));
+    mskern::launch_raster3d_bwd(s, W, H, cam->tiles_x, cam->tiles_y, P<int>(E.offsets), P<uint32_t>(E.blend_log),
+                                P<float>(E.t_ckpt), P<int>(E.wave_cnt), P<float>(E.rec), bg, P<float>(E.final_Ts),
+                                P<float>(E.dL_dimg), P<float>(E.grads16));
+    stage_mark(ST_PROJECT_BWD);
+    if (adam) {
+        mskern::launch_project3d_bwd(s, *cam, *g, P<int>(E.radii), P<float>(E.grads16), nullptr, nullptr, nullptr,
+                                     nullptr, nullptr, nullptr, gnorm, vis, max2d, inv_max_dim, adam,
+                                     P<float>(E.rec));
+    } else {
+        CHECK(ensure(E.dmeans, (size_t)N * 12));
+        CHECK(ensure(E.dscales, (size_t)N * 12));
+        CHECK(ensure(E.dquats, (size_t)N * 16));
+        CHECK(ensure(E.dmean2d, (size_t)N * 8));
+        CHECK(ensure(E.dfdc, (size_t)N * 12));
+        CHECK(ensure(E.dfrest, (size_t)N * E.K3 * 4));
+        mskern::launch_project3d_bwd(s, *cam, *g, P<int>(E.radii), P<float>(E.grads16), P<float>(E.dmeans),
+                                     P<float>(E.dscales), P<float>(E.dquats), P<float>(E.dmean2d),
+                                     P<float>(E.dfdc), P<float>(E.dfrest), gnorm, vis, max2d, inv_max_dim, nullptr,
+                                     P<float>(E.rec));
+        E.have_grads = true;
+    }
+    E.raster_grads = true;
+    E.g16_moments = true;
+    stage_mark(ST_COUNT);
+    HIPC(hipGetLastError());
+    HIPC(hipStreamSynchronize(s));
+    if (loss_host) *loss_host = (float)E.pinned_d[0];
+    if (E.timing) {
+        for (int i = 0; i < ST_COUNT; ++i) {
+            HIPC(hipEventElapsedTime(&E.stage_ms[i], E.ev[i], E.ev[i + 1]));
+            E.stage_valid[i] = true;
+        }
+    }
+    return MSPLAT_OK;
+    API_END
+}
+
 int msplat_hip_fused_adam(float *p, const float *gr, float *m, float *v, int64_t n, float step, float b1, float b2,
                           float bc2_sqrt, float eps) {
     API_BEGIN
@@ -1041,6 +1157,10 @@ int msplat_hip_raster_bwd(const float *dL_dimg, const float *dL_ddepth, const fl
     Engine &E = g_eng;
     if (!E.rec.p || !E.bg || !dL_dimg || !grads16) {
         set_err("raster_bwd needs a preceding forward and dL_dimg / grads16");
+        return MSPLAT_E_ARG;
+    }
+    if (E.gs3d) {
+        set_err("raster_bwd is the 2DGS backward; the 3DGS mode's runs inside msplat_hip_train_step_3dgs");
         return MSPLAT_E_ARG;
     }
     // a render-only forward skips the blend log, a training forward the full

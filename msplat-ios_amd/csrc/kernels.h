@@ -30,6 +30,20 @@ void launch_project_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaus
 // gradients (dL/dtransMat, dL/dopacity logit, dL/dcolors), in place.
 void launch_finish_image_grads(hipStream_t s, int n, const float *rec, float *g16);
 void launch_gather(hipStream_t s, const float *src, int src_stride, int src_off, int nf, float *dst, int n);
+// 3DGS mode.  rec: N records of kRec3Floats, then N quadrant-mask boxes
+// (4 floats); scales are [N,3].  sums_rec non-null: g16 holds the 3DGS
+// raster backward's per-splat sums, finished inside the kernel.
+constexpr int kRec3Floats = 12;
+void launch_project3d_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, float *rec,
+                          float *boxes, float *depths, int *radii, uint32_t *rect, unsigned long long *isect_total,
+                          float *colors_raw);
+void launch_project3d_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, const int *radii,
+                          const float *g16, float *dmeans, float *dscales, float *dquats, float *dmean2d,
+                          float *dfdc, float *dfrest, float *grad_norm, float *vis, float *max2d,
+                          float inv_max_dim, const MsplatAdam *adam, const float *sums_rec);
+// The 3DGS raster backward's sums -> the raster gradients [dxy 2, dconic 3,
+// dopacity logit, dcolor 3] (the first 9 of each 16-float row), in place.
+void launch_finish3d_grads(hipStream_t s, int n, const float *rec, float *g16);
 void launch_tiles_hit(hipStream_t s, const uint32_t *rect, const int *radii, int *out, int n);
 
 // k_binning.hip
@@ -80,6 +94,17 @@ bool launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
                        const float *dL_ddepth, const float *dL_daccum, const float *dL_dnormal,
                        const float *dL_dmedian, const float *dL_ddist, float ddist_uniform, float *grads16);
 constexpr int kBlendLogEntryBytes = 16;
+
+// k_raster3d.hip (3DGS mode): rec = the 3DGS records (kRec3Floats each),
+// boxes = their quadrant-mask boxes.  blend_log / t_ckpt / wave_cnt as for
+// launch_raster_fwd (nullptr: render only).  The backward adds the per-splat
+// sums to grads16 (launch_finish3d_grads finishes them).
+void launch_raster3d_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
+                         const float *rec, const float *boxes, const float *bg, float *out_img, float *final_Ts,
+                         uint32_t *blend_log, float *t_ckpt, int *wave_cnt);
+void launch_raster3d_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets,
+                         const uint32_t *blend_log, const float *t_ckpt, const int *wave_cnt, const float *rec,
+                         const float *bg, const float *final_Ts, const float *dL_dimg, float *grads16);
 // Adds to *bad the number of floats of exponent field efield (1..254, both
 // signs, every mantissa) where the rasterizer's fast reciprocal differs from
 // the correctly rounded 1 / x.

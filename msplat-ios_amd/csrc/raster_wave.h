@@ -1,0 +1,153 @@
+// raster_wave.h -- wave-level building blocks shared by the 2DGS and 3DGS
+// rasterizers: per-wave slot lists of a staged batch (forward) and the
+// 16-value wave reduction of the per-splat gradients (backward).  All of it
+// assumes 256-thread workgroups of four wave64, wave w owning pixel block w
+// of a 16x16 tile.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace msr {
+
+constexpr int kThreads = 256;
+
+// Per-wave slot lists of one batch: s_list[w][0..n_w) holds, in ascending
+// order, the slots whose mask m has bit w (this wave's ballot rank after the
+// counts of the waves below it).
+// Returns n for the calling thread's wave.  Called by all threads of the
+// workgroup (two barriers).
+__device__ __forceinline__ int build_wave_lists(int m, unsigned char (*s_list)[kThreads], int4 *s_cnt) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const unsigned long long below = (1ull << lane) - 1ull;
+    int pos[4], cnt[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const unsigned long long bal = __ballot((m >> w) & 1);
+        pos[w] = __popcll(bal & below);
+        cnt[w] = __popcll(bal);
+    }
+    if (lane == 0) s_cnt[wave] = make_int4(cnt[0], cnt[1], cnt[2], cnt[3]);
+    __syncthreads();
+    // every wave's counts at once (broadcast reads); the slots of block w
+    // from waves below this one precede this wave's
+    const int4 c0 = s_cnt[0], c1 = s_cnt[1], c2 = s_cnt[2], c3 = s_cnt[3];
+    const int4 z = make_int4(0, 0, 0, 0);
+    const int4 p1 = wave > 0 ? c0 : z, p2 = wave > 1 ? c1 : z, p3 = wave > 2 ? c2 : z;
+    const int base[4] = {p1.x + p2.x + p3.x, p1.y + p2.y + p3.y, p1.z + p2.z + p3.z, p1.w + p2.w + p3.w};
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+        if ((m >> w) & 1) s_list[w][base[w] + pos[w]] = (unsigned char)threadIdx.x;
+    // this wave's list length (wave-uniform: keeps the visit loop's control
+    // in scalar registers)
+    const int4 tot = make_int4(c0.x + c1.x + c2.x + c3.x, c0.y + c1.y + c2.y + c3.y, c0.z + c1.z + c2.z + c3.z,
+                               c0.w + c1.w + c2.w + c3.w);
+    const int n = __builtin_amdgcn_readfirstlane(wave == 0 ? tot.x : wave == 1 ? tot.y : wave == 2 ? tot.z : tot.w);
+    __syncthreads();
+    return n;
+}
+
+// DPP lane permutations within a 16-lane row (CDNA3/4 dpp_ctrl codes).
+constexpr int kDppQuad1032 = 0xB1;   // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppQuad2301 = 0x4E;   // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppHalfMirror = 0x141;  // lane i of each 8-lane half row <- 7 - i
+constexpr int kDppRowMirror = 0x140;   // lane i of each row <- 15 - i
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum of v[0..15] over the 64 lanes of a wave (a transpose reduction):
+// v_permlane32_swap / v_permlane16_swap exchange half-waves / half-rows
+// between two value registers, so each of those steps halves the value
+// count with one swap and one add per pair and no lane select; two mirror
+// DPP steps (partners differ in lane bit 3, then bit 2) and two quad_perm
+// DPP adds finish.  Lane l ends with the total of value index
+// 8*b5 + 4*b4 + 2*b3 + b2 (b = bits of l); every lane of a quad holds it.
+// SKIP1: bit i set when v[i] and v[i + 8] are zero in every lane, so their
+// first-stage pair is skipped (it would sum to zero).
+template <unsigned SKIP1 = 0>
+__device__ __forceinline__ float wave_reduce16(float v[16], int lane) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if ((SKIP1 >> i) & 1u) continue;
+        // vdst lanes 32-63 <-> src lanes 0-31: lanes < 32 end with value i,
+        // lanes >= 32 with value i + 8
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 8]), false,
+                                                        false);
+        v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // odd rows of vdst <-> even rows of src: lane bit 4 selects i + 4
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 4]), false,
+                                                        false);
+        v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    const bool b3 = lane & 8, b2 = lane & 4;
+    {
+        const float x0 = v[0] + dpp<kDppRowMirror>(v[0]);
+        const float x2 = v[2] + dpp<kDppRowMirror>(v[2]);
+        const float x1 = v[1] + dpp<kDppRowMirror>(v[1]);
+        const float x3 = v[3] + dpp<kDppRowMirror>(v[3]);
+        v[0] = b3 ? x2 : x0;
+        v[1] = b3 ? x3 : x1;
+    }
+    {
+        const float x0 = v[0] + dpp<kDppHalfMirror>(v[0]);
+        const float x1 = v[1] + dpp<kDppHalfMirror>(v[1]);
+        v[0] = b2 ? x1 : x0;
+    }
+    v[0] += dpp<kDppQuad1032>(v[0]);
+    v[0] += dpp<kDppQuad2301>(v[0]);
+    return v[0];
+}
+
+// Orders this wave's LDS stores before its later LDS loads (and the loads of
+// one chunk before the stores of the next): a wave's LDS operations execute
+// in program order, so only the compiler has to be kept from moving them.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// wave_reduce16 with its last three steps through LDS: after the two
+// permlane steps each lane holds 4 values (index i + 4 b4 + 8 b5), each a
+// sum over the 4 lanes that share lane bits 0-3; they are written to this
+// wave's 256-float scratch and read back transposed, so lane
+// 16 q + 4 i + k sums the 4 partials of value i from lanes 4 k .. 4 k + 3 of
+// its group q, and two quad DPP adds finish.  Lane l ends with the total of
+// value 8 b5 + 4 b4 + 2 b3 + b2, as wave_reduce16.  The scratch is swizzled
+// (group q of value i at 16-float block (q ^ i) & 3) so both the writes and
+// the 16-byte reads are free of bank conflicts.  wa[i] = this lane's write
+// address for value i, ra = its read address (loop invariants).
+template <unsigned SKIP1 = 0>
+__device__ __forceinline__ float wave_reduce16_lds(float v[16], float *const wa[4], const float4 *ra) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if ((SKIP1 >> i) & 1u) continue;
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 8]), false,
+                                                        false);
+        v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 4]), false,
+                                                        false);
+        v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *wa[i] = v[i];
+    wave_lds_sync();
+    const float4 p = *ra;
+    wave_lds_sync();
+    float s = (p.x + p.y) + (p.z + p.w);
+    s += dpp<kDppQuad1032>(s);
+    s += dpp<kDppQuad2301>(s);
+    return s;
+}
+
+}  // namespace msr

@@ -74,7 +74,8 @@ EXPORTS = [
     "msplat_hip_raster_bwd", "msplat_hip_project_bwd", "msplat_hip_project_bwd_adam", "msplat_hip_last", "msplat_hip_enable_timing",
     "msplat_hip_stage_times", "msplat_hip_last_pairs_evaluated", "msplat_hip_last_raster_counts",
     "msplat_hip_check_fast_rcp", "msplat_hip_set_wide_keys", "msplat_hip_tsdf_integrate",
-    "msplat_hip_marching_cubes", "msplat_hip_mc_table", "msplat_hip_unproject_depth",
+    "msplat_hip_marching_cubes", "msplat_hip_mc_table", "msplat_hip_unproject_depth", "msplat_hip_render_3dgs",
+    "msplat_hip_train_step_3dgs",
 ]
 SYNTH_EXPORTS = ["msplat_synth_uniform", "msplat_synth_normal"]
 
@@ -127,6 +128,9 @@ def lib() -> C.CDLL:
         "msplat_hip_last_raster_counts": (I, [P]),
         "msplat_hip_check_fast_rcp": (I, [I, I, C.POINTER(C.c_int64)]),
         "msplat_hip_set_wide_keys": (I, [I]),
+        "msplat_hip_render_3dgs": (I, [C.POINTER(MsplatCamera), C.POINTER(MsplatGaussians), P, C.POINTER(I64)]),
+        "msplat_hip_train_step_3dgs": (I, [C.POINTER(MsplatCamera), C.POINTER(MsplatGaussians), P, P, F, F, P, P, P,
+                                           F, C.POINTER(MsplatAdam), c_float_p, C.POINTER(I64)]),
         "msplat_hip_tsdf_integrate": (I, [P, I, I, I, c_float_p, F, C.POINTER(MsplatTsdfView), I, F, F]),
         "msplat_hip_marching_cubes": (I, [P, I, I, I, c_float_p, F, I64, P, C.POINTER(I64), C.POINTER(I64)]),
         "msplat_hip_mc_table": (I, [P]),

@@ -226,3 +226,48 @@ def densify_schedule(step: int, n: int, max_splats: int = 250_000, refine_every:
     dens = step < stop_split_at and step % interval > num_cameras + refine_every and n < max_splats
     reset = step < stop_split_at and step % interval == refine_every
     return dens, reset
+
+
+# ---- 3DGS mode ------------------------------------------------------------
+class DeviceScene3D(DeviceScene):
+    """DeviceScene of 3D Gaussians (scales [N,3]) for the 3DGS mode;
+    params in GROUPS order, as numpy arrays."""
+
+    def __init__(self, params: dict, background, sh_degree: int = 3):
+        self.sh_degree = sh_degree
+        self.n = int(params["means"].shape[0])
+        if params["scales"].shape != (self.n, 3):
+            raise ValueError("the 3DGS mode needs scales of shape [N, 3]")
+        self.params = [E.DeviceArray.from_numpy(np.ascontiguousarray(params[g], np.float32)) for g in GROUPS]
+        self.background = E.DeviceArray.from_numpy(np.asarray(background, np.float32))
+        self.exp_avg = [E.DeviceArray.zeros(p.shape) for p in self.params]
+        self.exp_avg_sq = [E.DeviceArray.zeros(p.shape) for p in self.params]
+        self.grad_norm = E.DeviceArray.zeros(self.n)
+        self.vis = E.DeviceArray.zeros(self.n)
+        self.max2d = E.DeviceArray.zeros(self.n)
+        self.adam_step = 0
+        self.lr = list(LR_INIT)
+
+
+def render3d(ds: DeviceScene3D, cam: E.MsplatCamera) -> dict[str, np.ndarray]:
+    n = C.c_int64()
+    E.check(E.lib().msplat_hip_render_3dgs(C.byref(cam), C.byref(ds.gaussians), ds.background.ptr, C.byref(n)))
+    H, W = cam.height, cam.width
+    return dict(out_img=E.last("out_img", (H, W, 3)), final_T=E.last("final_Ts", (H, W, 3))[..., 0],
+                num_intersections=int(n.value))
+
+
+def train_step3d(ds: DeviceScene3D, cam: E.MsplatCamera, gt: E.DeviceArray, ssim_weight: float = 0.2,
+                 fused_adam: bool = True) -> tuple[float, int]:
+    """One 3DGS training step (msplat_hip_train_step_3dgs): with fused_adam
+    the six Adam updates run inside the projection backward; without, the
+    parameter gradients stay in the engine cache (MSPLAT_LAST_DL_*)."""
+    loss = C.c_float()
+    nis = C.c_int64()
+    inv_max_dim = np.float32(1.0) / np.float32(max(cam.width, cam.height))
+    adam = ds.adam_struct() if fused_adam else None
+    E.check(E.lib().msplat_hip_train_step_3dgs(
+        C.byref(cam), C.byref(ds.gaussians), ds.background.ptr, gt.ptr, 1.0 - ssim_weight, ssim_weight,
+        ds.grad_norm.ptr, ds.vis.ptr, ds.max2d.ptr, float(inv_max_dim), C.byref(adam) if adam else None,
+        C.byref(loss), C.byref(nis)))
+    return float(loss.value), int(nis.value)

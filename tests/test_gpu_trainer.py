@@ -254,7 +254,12 @@ def test_c_abi_trainer(tmp_path):
     assert lib.msplat_trainer_load_checkpoint(tr, str(tmp_path / "c.msplat").encode()) == 5
     assert lib.msplat_trainer_load_checkpoint(tr, str(tmp_path / "missing.msplat").encode()) == -1
     assert b"Cannot open checkpoint" in lib.msplat_last_error()
-    assert lib.msplat_trainer_extract_mesh(tr, b"/tmp/mesh.ply", 0.004, 0.3, 0.5, 4.0) == -1
+    ntri = lib.msplat_trainer_extract_mesh(tr, str(tmp_path / "m.ply").encode(), 0.02, 1.0, 0.5, 4.0)
+    assert ntri > 0
+    head = (tmp_path / "m.ply").read_bytes()[:400]
+    assert f"element face {ntri}".encode() in head
+    assert lib.msplat_trainer_extract_mesh(tr, b"/nonexistent-dir/m.ply", 0.02, 1.0, 0.5, 4.0) == -1
+    assert lib.msplat_last_error()
     lib.msplat_trainer_destroy(tr)
     lib.msplat_dataset_destroy(ds)
 
