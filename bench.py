@@ -11,6 +11,7 @@ The headline line (`value`) is the train-step throughput of the 3M-splat,
   C3 train-3M-5187x3361     (the headline) + render FPS through the C ABI
   C4 overflow-1M-1920x1080  train steps/s, render FPS
   C5 densify-200k-1297x840  1500 steps with densification every 100
+  C3_3dgs                   the C3 splats as 3D Gaussians in the 3DGS mode
   mesh                      TSDF fusion of 32 depth views + marching cubes, 300^3
 each next to the golden model (scalar C++, OpenMP) timed on this host.
 Inputs are synthetic (seeded; targets are renders of the scene with
@@ -148,6 +149,53 @@ def gpu_train(workload: int, steps: int, warmup: int, render_frames: int, counte
     del gts
     out["render_ms"] = gpu_render_ms(ds, cams, render_frames)
     return out
+
+
+def gpu_train3d(workload: int, steps: int, warmup: int, render_frames: int):
+    """The 3DGS mode on a workload's splats as 3D Gaussians (Scene.as_3dgs):
+    train steps (msplat_hip_train_step_3dgs, fused Adam) and render frames."""
+    from msplat import _engine as E
+    from msplat import device as D
+    from msplat import synthetic as S
+
+    scene = S.make_scene(workload).as_3dgs()
+    ds = D.DeviceScene3D.from_scene(scene)
+    tgt = D.DeviceScene3D.from_scene(scene.jittered(0.01, 0xC0FFEE + 100 + workload))
+    cams = [ds.camera(c) for c in scene.cameras]
+    gts = [D.render3d_to_device(tgt, c) for c in cams]
+    del tgt
+    E.sync()
+    for k in range(warmup):
+        D.train_step3d(ds, cams[k % len(cams)], gts[k % len(cams)])
+    E.enable_timing(True)
+    E.sync()
+    stage_sum: dict[str, float] = {}
+    isect, losses = [], []
+    t0 = time.perf_counter()
+    for k in range(steps):
+        ci = (warmup + k) % len(cams)
+        loss, nis = D.train_step3d(ds, cams[ci], gts[ci])
+        losses.append(loss)
+        isect.append(nis)
+        for name, ms in E.stage_times().items():
+            stage_sum[name] = stage_sum.get(name, 0.0) + ms
+    E.sync()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / steps
+    E.enable_timing(False)
+    del gts
+    n = E.C.c_int64()
+    for k in range(3):
+        E.check(E.lib().msplat_hip_render_3dgs(E.C.byref(cams[k % len(cams)]), E.C.byref(ds.gaussians),
+                                               ds.background.ptr, E.C.byref(n)))
+    E.sync()
+    t0 = time.perf_counter()
+    for k in range(render_frames):
+        E.check(E.lib().msplat_hip_render_3dgs(E.C.byref(cams[k % len(cams)]), E.C.byref(ds.gaussians),
+                                               ds.background.ptr, E.C.byref(n)))
+    E.sync()
+    render_ms = (time.perf_counter() - t0) * 1e3 / max(render_frames, 1)
+    return dict(scene=scene, ms_per_step=ms_per_step, losses=losses, isect=float(np.mean(isect)),
+                stage_ms={k: v / steps for k, v in stage_sum.items()}, render_ms=render_ms)
 
 
 def gpu_render_ms(ds, cams, frames: int) -> float:
@@ -432,6 +480,32 @@ def cpu_train_step_s(O, scene, target_img, reps: int, warm_scene=None, warm_img=
     return [r[0] for r in runs]
 
 
+def cpu_train3d_step_s(O, scene, target_img, reps: int) -> list[float]:
+    """Seconds per golden-model 3DGS train step (camera 0): projection,
+    binning, compositing, SSIM + L1, both backwards and Adam on six groups."""
+    c = scene.cameras[0]
+    cam = O.prepare_cam(c.cam_to_world, c.fx, c.fy, c.cx, c.cy, c.width, c.height)
+    deg = scene.sh_degree
+    names = ("means", "scales", "quats", "features_dc", "features_rest", "opacities")
+    out = []
+    for _ in range(reps):
+        params = {k: v.copy() for k, v in zip(names, scene.params())}
+        t0 = time.perf_counter()
+        proj = O.project3d_fwd(params, cam, deg, deg)
+        bins = O.bin_sort(proj, cam)
+        fwd = O.raster3d_fwd(proj, bins, cam, params["opacities"], scene.background)
+        _, dL, _, _ = O.loss_fwd_bwd(fwd["out_img"], target_img)
+        g9 = O.raster3d_bwd(proj, bins, fwd, cam, params["opacities"], scene.background, dL)
+        g = O.project3d_bwd(params, cam, deg, deg, proj["radii"], g9)
+        grads = (g["dmeans"], g["dscales"], g["dquats"], g["dfdc"], g["dfrest"], g9[:, 5:6].copy())
+        for k, gr, lr in zip(names, grads, LR):
+            pk = params[k]
+            O.adam(pk, np.ascontiguousarray(gr, np.float32), np.zeros_like(pk), np.zeros_like(pk),
+                   float(np.float32(lr) / np.float32(0.1)), 0.9, 0.999, float(np.sqrt(np.float32(0.001))), 1e-8)
+        out.append(time.perf_counter() - t0)
+    return out
+
+
 def cpu_render_s(O, scene, reps: int) -> list[float]:
     O.render(scene, 0)
     out = []
@@ -440,6 +514,14 @@ def cpu_render_s(O, scene, reps: int) -> list[float]:
         O.render(scene, 0)
         out.append(time.perf_counter() - t0)
     return out
+
+
+def _cpu_render3d_inputs(O, scene):
+    c = scene.cameras[0]
+    cam = O.prepare_cam(c.cam_to_world, c.fx, c.fy, c.cx, c.cy, c.width, c.height)
+    params = dict(zip(("means", "scales", "quats", "features_dc", "features_rest", "opacities"), scene.params()))
+    proj = O.project3d_fwd(params, cam, scene.sh_degree, scene.sh_degree)
+    return proj, O.bin_sort(proj, cam), cam, params["opacities"], scene.background
 
 
 def cpu_cell(O, per_s: list[float], unit: str, sample: str) -> dict:
@@ -504,6 +586,8 @@ def main() -> int:
                     help="only run the train steps and render frames of workload N (for a profiler)")
     ap.add_argument("--mesh-only", action="store_true",
                     help="only the mesh workload (TSDF fusion + marching cubes; for a profiler)")
+    ap.add_argument("--3dgs-only", dest="gs3d_only", action="store_true",
+                    help="only the 3DGS-mode workload (the C3 splats as 3D Gaussians; for a profiler)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the training step is single-GPU (one camera per step); "
@@ -520,6 +604,13 @@ def main() -> int:
     if args.mesh_only:
         mesh = gpu_mesh()
         print(json.dumps({k: v for k, v in mesh.items() if not k.startswith("_")}))
+        return 0
+    if args.gs3d_only:
+        r = gpu_train3d(3, args.steps, args.warmup, args.render_frames)
+        print(json.dumps({"workload": r["scene"].name, "ms_per_step": round(r["ms_per_step"], 3),
+                          "render_ms": round(r["render_ms"], 3), "intersections_mean": int(r["isect"]),
+                          "stage_ms": {k: round(v, 4) for k, v in r["stage_ms"].items()},
+                          "loss_first_last": [round(r["losses"][0], 6), round(r["losses"][-1], 6)]}))
         return 0
     if args.profile_workload:
         r = gpu_train(args.profile_workload, args.steps, args.warmup, args.render_frames, counters=False)
@@ -604,6 +695,18 @@ def main() -> int:
                          "cycles": cyc}
         log(f"{d5['scene'].name}: {d5['scene'].n} -> {d5['n_final']} splats in {d5['total_ms'] / 1e3:.2f} s")
         gc.collect()
+        r3 = gpu_train3d(3, max(args.steps // 2, 5), args.warmup, max(args.render_frames // 2, 5))
+        sc3 = r3["scene"]
+        configs["C3_3dgs"] = {"workload": sc3.name, "splats": sc3.n, "intersections_mean": int(r3["isect"]),
+                              "train_steps_per_s": round(1000.0 / r3["ms_per_step"], 3),
+                              "ms_per_step": round(r3["ms_per_step"], 3),
+                              "render_fps": round(1000.0 / r3["render_ms"], 2),
+                              "render_ms": round(r3["render_ms"], 3),
+                              "stage_ms": {k: round(v, 4) for k, v in r3["stage_ms"].items()},
+                              "loss_first_last": [round(r3["losses"][0], 6), round(r3["losses"][-1], 6)]}
+        log(f"{sc3.name}: {r3['ms_per_step']:.3f} ms/step, render {r3['render_ms']:.3f} ms")
+        del r3
+        gc.collect()
         mesh = gpu_mesh()
         log(f"{mesh['workload']}: TSDF {mesh['tsdf_ms']:.3f} ms, marching cubes {mesh['mc_ms']:.3f} ms, "
             f"{mesh['triangles']} triangles")
@@ -663,6 +766,13 @@ def main() -> int:
             dens_s = time.perf_counter() - td
             cyc_s = 100 * step_s + dens_s
             configs["mesh"]["cpu"] = cpu_mesh(O, mesh)
+            sc3 = scene.as_3dgs()
+            gt3d = O.raster3d_fwd(*_cpu_render3d_inputs(O, sc3.jittered(0.01, 0xC0FFEE + 103)))["out_img"]
+            runs = cpu_train3d_step_s(O, sc3, gt3d, 1)
+            configs["C3_3dgs"]["cpu_train"] = cpu_cell(O, runs, "train steps/s",
+                                                       f"{len(runs)} golden-model 3DGS step of {sc3.name} "
+                                                       f"(camera 0) after the 2DGS runs")
+            log(f"cpu {sc3.name}: {np.median(runs):.2f} s/step")
             configs["C5"]["cpu_cycle"] = {"value": round(1.0 / cyc_s, 6), "unit": "densify cycles/s",
                                           "cores": O.num_threads(), "kind": "port", "cpu": cpu_model(),
                                           "cycle_s": round(cyc_s, 2),

@@ -233,6 +233,11 @@ class DeviceScene3D(DeviceScene):
     """DeviceScene of 3D Gaussians (scales [N,3]) for the 3DGS mode;
     params in GROUPS order, as numpy arrays."""
 
+    @classmethod
+    def from_scene(cls, scene: Scene) -> "DeviceScene3D":
+        """From a Scene whose scales are [N, 3] (Scene.as_3dgs)."""
+        return cls(dict(zip(GROUPS, scene.params())), scene.background, scene.sh_degree)
+
     def __init__(self, params: dict, background, sh_degree: int = 3):
         self.sh_degree = sh_degree
         self.n = int(params["means"].shape[0])
@@ -255,6 +260,16 @@ def render3d(ds: DeviceScene3D, cam: E.MsplatCamera) -> dict[str, np.ndarray]:
     H, W = cam.height, cam.width
     return dict(out_img=E.last("out_img", (H, W, 3)), final_T=E.last("final_Ts", (H, W, 3))[..., 0],
                 num_intersections=int(n.value))
+
+
+def render3d_to_device(ds: DeviceScene3D, cam: E.MsplatCamera) -> E.DeviceArray:
+    """Renders (3DGS mode) and copies the image into a new device array."""
+    n = C.c_int64()
+    E.check(E.lib().msplat_hip_render_3dgs(C.byref(cam), C.byref(ds.gaussians), ds.background.ptr, C.byref(n)))
+    ptr, numel = E.last_ptr("out_img")
+    out = E.DeviceArray((cam.height, cam.width, 3))
+    E.check(E.lib().msplat_hip_copy(out.ptr, ptr, numel * 4))
+    return out
 
 
 def train_step3d(ds: DeviceScene3D, cam: E.MsplatCamera, gt: E.DeviceArray, ssim_weight: float = 0.2,
