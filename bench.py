@@ -485,23 +485,17 @@ def cpu_train3d_step_s(O, scene, target_img, reps: int) -> list[float]:
     binning, compositing, SSIM + L1, both backwards and Adam on six groups."""
     c = scene.cameras[0]
     cam = O.prepare_cam(c.cam_to_world, c.fx, c.fy, c.cx, c.cy, c.width, c.height)
-    deg = scene.sh_degree
     names = ("means", "scales", "quats", "features_dc", "features_rest", "opacities")
     out = []
     for _ in range(reps):
-        params = {k: v.copy() for k, v in zip(names, scene.params())}
+        params = {k: np.ascontiguousarray(v, np.float32).copy() for k, v in zip(names, scene.params())}
+        m = {k: np.zeros_like(v) for k, v in params.items()}
+        v = {k: np.zeros_like(x) for k, x in params.items()}
+        stats = dict(grad_norm=np.zeros(scene.n, np.float32), vis=np.zeros(scene.n, np.float32),
+                     max2d=np.zeros(scene.n, np.float32))
         t0 = time.perf_counter()
-        proj = O.project3d_fwd(params, cam, deg, deg)
-        bins = O.bin_sort(proj, cam)
-        fwd = O.raster3d_fwd(proj, bins, cam, params["opacities"], scene.background)
-        _, dL, _, _ = O.loss_fwd_bwd(fwd["out_img"], target_img)
-        g9 = O.raster3d_bwd(proj, bins, fwd, cam, params["opacities"], scene.background, dL)
-        g = O.project3d_bwd(params, cam, deg, deg, proj["radii"], g9)
-        grads = (g["dmeans"], g["dscales"], g["dquats"], g["dfdc"], g["dfrest"], g9[:, 5:6].copy())
-        for k, gr, lr in zip(names, grads, LR):
-            pk = params[k]
-            O.adam(pk, np.ascontiguousarray(gr, np.float32), np.zeros_like(pk), np.zeros_like(pk),
-                   float(np.float32(lr) / np.float32(0.1)), 0.9, 0.999, float(np.sqrt(np.float32(0.001))), 1e-8)
+        O.train_step3d(params, m, v, cam, scene.background, target_img, scene.sh_degree, scene.sh_degree, LR, 1,
+                       stats)
         out.append(time.perf_counter() - t0)
     return out
 

@@ -106,10 +106,18 @@ private:
     std::unique_ptr<Impl> impl;
 };
 
+// The splat primitive a Trainer optimises (an extension: the reference
+// trains surfels only).
+enum class Primitive {
+    Surfel2D,    // 2DGS (the reference's step)
+    Gaussian3D,  // 3DGS: three scales, EWA projection, no depth outputs
+};
+
 class Trainer {
 public:
     // The dataset must outlive the trainer.
     Trainer(Dataset &dataset, const Config &config);
+    Trainer(Dataset &dataset, const Config &config, Primitive primitive);
     ~Trainer();
     Trainer(const Trainer &) = delete;
     Trainer &operator=(const Trainer &) = delete;
@@ -151,6 +159,7 @@ public:
     // first two scales) and resets the optimiser; the iteration becomes the
     // step recorded in the file.  Returns it.
     int loadPly(const std::string &path);
+    Primitive primitive() const;
 
 private:
     struct Impl;

@@ -153,6 +153,12 @@ void msplat_trainer_set_cull_alpha(MsplatTrainer t, float thresh);
  * reference CLI's --resume (Model::loadPly, core/src/model.cpp:329-340,
  * cli/msplat.cpp:259).  Returns that step, or -1 (msplat_last_error). */
 int msplat_trainer_load_ply(MsplatTrainer t, const char *path);
+/* A trainer of 3D Gaussians (the 3DGS mode: three scales per splat, EWA
+ * projection, the 3DGS compositing rule), with the arguments of
+ * msplat_trainer_create.  Every other call applies to it unchanged, except
+ * msplat_trainer_extract_mesh, which needs depth and returns -1.  PLY and
+ * .splat exports carry three scales. */
+MsplatTrainer msplat_trainer_create_3dgs(MsplatDataset ds, MsplatConfig config);
 
 #ifdef __cplusplus
 }

@@ -354,6 +354,22 @@ int msplat_hip_train_step_3dgs(const MsplatCamera *cam, const MsplatGaussians *g
                                const float *gt_dev, float lambda_l1, float lambda_dssim, float *xys_grad_norm_dev,
                                float *vis_counts_dev, float *max_2d_size_dev, float inv_max_dim,
                                const MsplatAdam *adam, float *loss_host, int64_t *num_isect_host);
+/* msplat_hip_densify for 3D Gaussians: the reference's densify kernels at
+ * kScaleDim = 3 (msplat_metal.metal:3253-3255, :3315-3317, :3339-3341):
+ * scales stride 3, the largest of three scales classifies and culls, split
+ * children are sampled along all three axes.  Same arguments, capacity
+ * contract and results otherwise. */
+int msplat_hip_densify_3dgs(int n, int capacity, float grad_thresh,
+                            float size_thresh, float screen_thresh,
+                            int check_screen, float cull_alpha_thresh,
+                            float cull_scale_thresh, float cull_screen_size,
+                            int check_huge, const float *xys_grad_norm_dev,
+                            const float *vis_counts_dev,
+                            const float *max_2d_size_dev, float half_max_dim,
+                            float *const params_dev[6], int fr_stride,
+                            float *const exp_avg_dev[6],
+                            float *const exp_avg_sq_dev[6],
+                            const float *random_samples_dev, int *new_count_host);
 
 /* ---- mesh extraction: TSDF fusion, marching cubes, depth unprojection ----
  * The voxel grid is [Dz, Dy, Dx, 2] f32 (sdf, weight) in HBM, voxel (x, y, z)

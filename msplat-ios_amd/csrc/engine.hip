@@ -994,13 +994,11 @@ int msplat_hip_fused_adam(float *p, const float *gr, float *m, float *v, int64_t
     API_END
 }
 
-int msplat_hip_densify(int n, int capacity, float grad_thresh, float size_thresh, float screen_thresh,
-                       int check_screen, float cull_alpha_thresh, float cull_scale_thresh, float cull_screen_size,
-                       int check_huge, const float *gnorm, const float *vis, const float *max2d, float half_max_dim,
-                       float *const params[6], int fr_stride, float *const exp_avg[6], float *const exp_avg_sq[6],
-                       const float *random, int *new_count) {
-    API_BEGIN
-    ENSURE_INIT();
+static int densify_impl(int scale_dim, int n, int capacity, float grad_thresh, float size_thresh,
+                        float screen_thresh, int check_screen, float cull_alpha_thresh, float cull_scale_thresh,
+                        float cull_screen_size, int check_huge, const float *gnorm, const float *vis,
+                        const float *max2d, float half_max_dim, float *const params[6], int fr_stride,
+                        float *const exp_avg[6], float *const exp_avg_sq[6], const float *random, int *new_count) {
     if (n < 0 || n > capacity || fr_stride < 0 || !new_count || !gnorm || !vis || !max2d || !random) {
         set_err("densify: N (%d) exceeds capacity %d or bad arguments", n, capacity);
         return MSPLAT_E_ARG;
@@ -1010,10 +1008,11 @@ int msplat_hip_densify(int n, int capacity, float grad_thresh, float size_thresh
         return MSPLAT_OK;
     }
     Engine &E = g_eng;
-    const int strides[6] = {3, 2, 4, 3, fr_stride, 1};
+    const int strides[6] = {3, scale_dim, 4, 3, fr_stride, 1};
     mskern::DensifyArgs a{};
     a.n = n;
     a.fr_stride = fr_stride;
+    a.scale_dim = scale_dim;
     a.grad_th = grad_thresh;
     a.size_th = size_thresh;
     a.screen_th = screen_thresh;
@@ -1072,6 +1071,32 @@ int msplat_hip_densify(int n, int capacity, float grad_thresh, float size_thresh
     HIPC(hipStreamSynchronize(E.stream));
     *new_count = E.pinned_i[0];
     return MSPLAT_OK;
+}
+
+int msplat_hip_densify(int n, int capacity, float grad_thresh, float size_thresh, float screen_thresh,
+                       int check_screen, float cull_alpha_thresh, float cull_scale_thresh, float cull_screen_size,
+                       int check_huge, const float *gnorm, const float *vis, const float *max2d, float half_max_dim,
+                       float *const params[6], int fr_stride, float *const exp_avg[6], float *const exp_avg_sq[6],
+                       const float *random, int *new_count) {
+    API_BEGIN
+    ENSURE_INIT();
+    return densify_impl(2, n, capacity, grad_thresh, size_thresh, screen_thresh, check_screen, cull_alpha_thresh,
+                        cull_scale_thresh, cull_screen_size, check_huge, gnorm, vis, max2d, half_max_dim, params,
+                        fr_stride, exp_avg, exp_avg_sq, random, new_count);
+    API_END
+}
+
+int msplat_hip_densify_3dgs(int n, int capacity, float grad_thresh, float size_thresh, float screen_thresh,
+                            int check_screen, float cull_alpha_thresh, float cull_scale_thresh,
+                            float cull_screen_size, int check_huge, const float *gnorm, const float *vis,
+                            const float *max2d, float half_max_dim, float *const params[6], int fr_stride,
+                            float *const exp_avg[6], float *const exp_avg_sq[6], const float *random,
+                            int *new_count) {
+    API_BEGIN
+    ENSURE_INIT();
+    return densify_impl(3, n, capacity, grad_thresh, size_thresh, screen_thresh, check_screen, cull_alpha_thresh,
+                        cull_scale_thresh, cull_screen_size, check_huge, gnorm, vis, max2d, half_max_dim, params,
+                        fr_stride, exp_avg, exp_avg_sq, random, new_count);
     API_END
 }
 

@@ -193,6 +193,53 @@ MTensor msplat_render(int num_points, MTensor &means3d, MTensor &scales, float g
     return msplat_last_out_img();
 }
 
+MTensor msplat_render_3dgs(int num_points, MTensor &means3d, MTensor &scales, float glob_scale, MTensor &quats,
+                           MTensor &viewmat, MTensor &projmat, float fx, float fy, float cx, float cy,
+                           unsigned img_height, unsigned img_width, const std::tuple<int, int, int> tile_bounds,
+                           float clip_thresh, unsigned degree, unsigned degrees_to_use, float cam_pos[3],
+                           MTensor &features_dc, MTensor &features_rest, MTensor &opacities, MTensor &background) {
+    MsplatCamera cam = make_camera(viewmat, projmat, fx, fy, cx, cy, img_height, img_width, tile_bounds,
+                                   clip_thresh, glob_scale, degree, degrees_to_use, cam_pos);
+    MsplatGaussians g = make_gaussians(num_points, means3d, scales, quats, opacities, features_dc, features_rest);
+    check(msplat_hip_render_3dgs(&cam, &g, background.data<float>(), nullptr));
+    g_n = num_points;
+    g_H = (int)img_height;
+    g_W = (int)img_width;
+    return msplat_last_out_img();
+}
+
+std::tuple<MTensor, float> msplat_train_step_3dgs_adam(
+    int num_points, MTensor &means3d, MTensor &scales, float glob_scale, MTensor &quats, MTensor &viewmat,
+    MTensor &projmat, float fx, float fy, float cx, float cy, unsigned img_height, unsigned img_width,
+    const std::tuple<int, int, int> tile_bounds, float clip_thresh, unsigned degree, unsigned degrees_to_use,
+    float cam_pos[3], MTensor &features_dc, MTensor &features_rest, MTensor &opacities, MTensor &background,
+    MTensor &gt, int features_rest_bases, float lambda_l1, float lambda_dssim, MTensor &xys_grad_norm,
+    MTensor &vis_counts, MTensor &max_2d_size, float inv_max_dim, MTensor exp_avg[6], MTensor exp_avg_sq[6],
+    const float step_size[6], float beta1, float beta2, float bc2_sqrt, float eps) {
+    MsplatAdam a{};
+    for (int k = 0; k < 6; ++k) {
+        a.exp_avg[k] = exp_avg[k].data<float>();
+        a.exp_avg_sq[k] = exp_avg_sq[k].data<float>();
+        a.step_size[k] = step_size[k];
+    }
+    a.beta1 = beta1;
+    a.beta2 = beta2;
+    a.bc2_sqrt = bc2_sqrt;
+    a.eps = eps;
+    MsplatCamera cam = make_camera(viewmat, projmat, fx, fy, cx, cy, img_height, img_width, tile_bounds,
+                                   clip_thresh, glob_scale, degree, degrees_to_use, cam_pos);
+    MsplatGaussians g = make_gaussians(num_points, means3d, scales, quats, opacities, features_dc, features_rest);
+    float loss = 0.f;
+    check(msplat_hip_train_step_3dgs(&cam, &g, background.data<float>(), gt.data<float>(), lambda_l1, lambda_dssim,
+                                     xys_grad_norm.data<float>(), vis_counts.data<float>(), max_2d_size.data<float>(),
+                                     inv_max_dim, &a, &loss, nullptr));
+    g_n = num_points;
+    g_H = (int)img_height;
+    g_W = (int)img_width;
+    g_K = features_rest_bases;
+    return {msplat_last_radii(), loss};
+}
+
 int msplat_densify(int N, int buf_capacity, float grad_thresh, float size_thresh, float screen_thresh,
                    int check_screen, float cull_alpha_thresh, float cull_scale_thresh, float cull_screen_size,
                    int check_huge, MTensor &xys_grad_norm, MTensor &vis_counts, MTensor &max_2d_size,
@@ -208,7 +255,9 @@ int msplat_densify(int N, int buf_capacity, float grad_thresh, float size_thresh
         v[k] = adam_exp_avg_sq_buf[k].data<float>();
     }
     int new_count = 0;
-    const int rc = msplat_hip_densify(N, buf_capacity, grad_thresh, size_thresh, screen_thresh, check_screen,
+    const int sd = scales_buf.ndim() == 2 ? (int)scales_buf.size(1) : 2;
+    if (sd != 2 && sd != 3) throw std::invalid_argument("densify: scales_buf must be [capacity, 2] or [capacity, 3]");
+    const int rc = (sd == 3 ? msplat_hip_densify_3dgs : msplat_hip_densify)(N, buf_capacity, grad_thresh, size_thresh, screen_thresh, check_screen,
                                       cull_alpha_thresh, cull_scale_thresh, cull_screen_size, check_huge,
                                       xys_grad_norm.data<float>(), vis_counts.data<float>(),
                                       max_2d_size.data<float>(), half_max_dim, params, fr_stride, m, v,

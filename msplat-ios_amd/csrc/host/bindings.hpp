@@ -74,9 +74,28 @@ MTensor msplat_render(int num_points, MTensor &means3d, MTensor &scales, float g
                       float clip_thresh, unsigned degree, unsigned degrees_to_use, float cam_pos[3],
                       MTensor &features_dc, MTensor &features_rest, MTensor &opacities, MTensor &background);
 
+// The 3DGS mode (scales [N,3]; no counterpart in the fork, whose 3DGS step
+// was removed, bindings.h:140): the render and the fused train step, with
+// the arguments of msplat_render and msplat_train_step_2dgs_adam (no
+// distortion weight).
+MTensor msplat_render_3dgs(int num_points, MTensor &means3d, MTensor &scales, float glob_scale, MTensor &quats,
+                           MTensor &viewmat, MTensor &projmat, float fx, float fy, float cx, float cy,
+                           unsigned img_height, unsigned img_width, const std::tuple<int, int, int> tile_bounds,
+                           float clip_thresh, unsigned degree, unsigned degrees_to_use, float cam_pos[3],
+                           MTensor &features_dc, MTensor &features_rest, MTensor &opacities, MTensor &background);
+std::tuple<MTensor, float> msplat_train_step_3dgs_adam(
+    int num_points, MTensor &means3d, MTensor &scales, float glob_scale, MTensor &quats, MTensor &viewmat,
+    MTensor &projmat, float fx, float fy, float cx, float cy, unsigned img_height, unsigned img_width,
+    const std::tuple<int, int, int> tile_bounds, float clip_thresh, unsigned degree, unsigned degrees_to_use,
+    float cam_pos[3], MTensor &features_dc, MTensor &features_rest, MTensor &opacities, MTensor &background,
+    MTensor &gt, int features_rest_bases, float lambda_l1, float lambda_dssim, MTensor &xys_grad_norm,
+    MTensor &vis_counts, MTensor &max_2d_size, float inv_max_dim, MTensor exp_avg[6], MTensor exp_avg_sq[6],
+    const float step_size[6], float beta1, float beta2, float bc2_sqrt, float eps);
+
 // bindings.h:143-158.  The flag / prefix / block / scratch tensors of the
 // reference are accepted for signature compatibility; the engine keeps its
-// own scratch.  Scales are compacted with their 2-float stride.
+// own scratch.  The scale stride follows scales_buf's shape (the reference's
+// kScaleDim): 2 for surfels, 3 for the 3DGS mode's Gaussians.
 int msplat_densify(int N, int buf_capacity, float grad_thresh, float size_thresh, float screen_thresh,
                    int check_screen, float cull_alpha_thresh, float cull_scale_thresh, float cull_screen_size,
                    int check_huge, MTensor &xys_grad_norm, MTensor &vis_counts, MTensor &max_2d_size,

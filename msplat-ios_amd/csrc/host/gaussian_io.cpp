@@ -115,8 +115,10 @@ void Model::saveSplat(const std::string &filename) {
 }
 
 // Reads a Gaussian PLY written by savePly (or 3DGS tooling with the same
-// property order); 3-scale rows keep their first two scales.  Replaces the
-// scene and resets the optimiser (model.cpp:319-330).
+// property order) into a model of scaleDim scales: a 2DGS model keeps the
+// first two of a 3-scale row; a 3DGS model gives a 2-scale row a third
+// scale equal to the smaller of its two.  Replaces the scene and resets the
+// optimiser (model.cpp:319-330).
 int Model::loadPly(const std::string &filename) {
     msplat_gpu_sync();
     std::ifstream f(filename, std::ios::binary);
@@ -148,7 +150,8 @@ int Model::loadPly(const std::string &filename) {
         throw std::runtime_error("PLY: unexpected Gaussian property layout");
     const int bases = nfr / 3;
     std::vector<float> row((size_t)nprops);
-    std::vector<float> m(3 * n), dc(3 * n), fr((size_t)n * nfr), op(n), s(2 * n), q(4 * n);
+    const int sd = scaleDim;
+    std::vector<float> m(3 * n), dc(3 * n), fr((size_t)n * nfr), op(n), s((size_t)sd * n), q(4 * n);
     for (int64_t i = 0; i < n; ++i) {
         f.read((char *)row.data(), (std::streamsize)(row.size() * sizeof(float)));
         if (!f) throw std::runtime_error("PLY: truncated vertex data");
@@ -160,9 +163,10 @@ int Model::loadPly(const std::string &filename) {
             for (int b = 0; b < bases; ++b) fr[(size_t)i * nfr + b * 3 + ch] = row[c++];
         op[i] = row[c++];
         for (int j = 0; j < ns; ++j) {
-            if (j < 2) s[2 * i + j] = row[c];
+            if (j < sd) s[(size_t)sd * i + j] = row[c];
             ++c;
         }
+        if (ns < sd) s[(size_t)sd * i + 2] = std::min(s[(size_t)sd * i], s[(size_t)sd * i + 1]);
         for (int j = 0; j < 4; ++j) q[4 * i + j] = row[c++];
     }
     if (keepCrs) {
@@ -176,7 +180,7 @@ int Model::loadPly(const std::string &filename) {
         return t;
     };
     means = up({n, 3}, m);
-    scales = up({n, 2}, s);
+    scales = up({n, (int64_t)sd}, s);
     quats = up({n, 4}, q);
     featuresDc = up({n, 3}, dc);
     featuresRest = up({n, (int64_t)bases, 3}, fr);

@@ -50,8 +50,9 @@ int numShBases(int degree) {
 Model::Model(const InputData &inputData, int numCameras, int numDownscales, int resolutionSchedule, int shDegree,
              int shDegreeInterval, int refineEvery, int warmupLength, int resetAlphaEvery, float densifyGradThresh,
              float densifySizeThresh, int stopScreenSizeAt, float splitScreenSize, int maxSteps, bool keepCrs,
-             const float *bgColor)
-    : numCameras(numCameras),
+             const float *bgColor, int scaleDim)
+    : scaleDim(scaleDim),
+      numCameras(numCameras),
       numDownscales(numDownscales),
       resolutionSchedule(resolutionSchedule),
       shDegree(shDegree),
@@ -67,6 +68,7 @@ Model::Model(const InputData &inputData, int numCameras, int numDownscales, int 
       maxSteps(maxSteps),
       keepCrs(keepCrs) {
     if (shDegree < 0 || shDegree > 4) throw std::invalid_argument("sh_degree must be in [0, 4]");
+    if (scaleDim != 2 && scaleDim != 3) throw std::invalid_argument("scaleDim must be 2 (2DGS) or 3 (3DGS)");
     if (refineEvery <= 0 || resetAlphaEvery <= 0 || shDegreeInterval <= 0 || resolutionSchedule <= 0)
         throw std::invalid_argument("refine_every, reset_alpha_every, sh_degree_interval and resolution_schedule "
                                     "must be positive");
@@ -79,10 +81,10 @@ Model::Model(const InputData &inputData, int numCameras, int numDownscales, int 
     means = upload({n, 3}, inputData.points.xyz.data());
     {
         const std::vector<float> d = knnMeanDistance(inputData.points.xyz.data(), n, 3);
-        std::vector<float> s((size_t)n * kScaleDim);
+        std::vector<float> s((size_t)n * scaleDim);
         for (int64_t i = 0; i < n; ++i)
-            for (int k = 0; k < kScaleDim; ++k) s[i * kScaleDim + k] = std::log(d[i]);
-        scales = upload({n, kScaleDim}, s.data());
+            for (int k = 0; k < scaleDim; ++k) s[i * scaleDim + k] = std::log(d[i]);
+        scales = upload({n, (int64_t)scaleDim}, s.data());
     }
     {
         // uniformly random rotations (model.cpp:79-93)
@@ -326,21 +328,31 @@ float Model::fullIteration(Camera &cam, int step, MTensor &gt, float ssimWeight)
     const float invMaxDim = 1.0f / (float)std::max(s.width, s.height);
     float step_size[N_ADAM_GROUPS];
     for (int g = 0; g < N_ADAM_GROUPS; ++g) step_size[g] = adam_lr[g] / bc1;
-    auto out = msplat_train_step_2dgs_adam(
-        n, means, scales, 1.0f, quats, s.viewMat, s.projViewMat, s.fx, s.fy, s.cx, s.cy, (unsigned)s.height,
-        (unsigned)s.width, s.tileBounds, 0.01f, (unsigned)s.degree, (unsigned)s.degreesToUse, s.cam_pos, featuresDc,
-        featuresRest, opacities, backgroundColor, gt, (int)featuresRest.size(-2), 1.0f - ssimWeight, 0.0f, ssimWeight,
-        xysGradNorm, visCounts, max2DSize, invMaxDim, adam_exp_avg, adam_exp_avg_sq, step_size, adam_beta1,
-        adam_beta2, std::sqrt(bc2), adam_eps);
+    auto out = scaleDim == 3
+                   ? msplat_train_step_3dgs_adam(
+                         n, means, scales, 1.0f, quats, s.viewMat, s.projViewMat, s.fx, s.fy, s.cx, s.cy,
+                         (unsigned)s.height, (unsigned)s.width, s.tileBounds, 0.01f, (unsigned)s.degree,
+                         (unsigned)s.degreesToUse, s.cam_pos, featuresDc, featuresRest, opacities, backgroundColor, gt,
+                         (int)featuresRest.size(-2), 1.0f - ssimWeight, ssimWeight, xysGradNorm, visCounts,
+                         max2DSize, invMaxDim, adam_exp_avg, adam_exp_avg_sq, step_size, adam_beta1, adam_beta2,
+                         std::sqrt(bc2), adam_eps)
+                   : msplat_train_step_2dgs_adam(
+                         n, means, scales, 1.0f, quats, s.viewMat, s.projViewMat, s.fx, s.fy, s.cx, s.cy,
+                         (unsigned)s.height, (unsigned)s.width, s.tileBounds, 0.01f, (unsigned)s.degree,
+                         (unsigned)s.degreesToUse, s.cam_pos, featuresDc, featuresRest, opacities, backgroundColor, gt,
+                         (int)featuresRest.size(-2), 1.0f - ssimWeight, 0.0f, ssimWeight, xysGradNorm, visCounts,
+                         max2DSize, invMaxDim, adam_exp_avg, adam_exp_avg_sq, step_size, adam_beta1, adam_beta2,
+                         std::sqrt(bc2), adam_eps);
     radii = std::get<0>(out);
     return std::get<1>(out);
 }
 
 MTensor Model::render(Camera &cam, int step) {
     CamSetup s = prepareCam(cam, step);
-    return msplat_render((int)means.size(0), means, scales, 1.0f, quats, s.viewMat, s.projViewMat, s.fx, s.fy, s.cx,
-                         s.cy, (unsigned)s.height, (unsigned)s.width, s.tileBounds, 0.01f, (unsigned)s.degree,
-                         (unsigned)s.degreesToUse, s.cam_pos, featuresDc, featuresRest, opacities, backgroundColor);
+    auto fn = scaleDim == 3 ? msplat_render_3dgs : msplat_render;
+    return fn((int)means.size(0), means, scales, 1.0f, quats, s.viewMat, s.projViewMat, s.fx, s.fy, s.cx, s.cy,
+              (unsigned)s.height, (unsigned)s.width, s.tileBounds, 0.01f, (unsigned)s.degree,
+              (unsigned)s.degreesToUse, s.cam_pos, featuresDc, featuresRest, opacities, backgroundColor);
 }
 
 // ---- checkpoints (model.cpp:343-498): little-endian, magic "MSPL",
@@ -431,7 +443,8 @@ int Model::loadCheckpoint(const std::string &filename) {
     for (int g = 0; g < 6; ++g)
         if (p[g].size(0) != n || m[g].shape() != p[g].shape() || v[g].shape() != p[g].shape())
             throw std::runtime_error("checkpoint: inconsistent tensor shapes");
-    if (p[1].ndim() != 2 || p[1].size(1) != kScaleDim) throw std::runtime_error("checkpoint: scales must be [N,2]");
+    if (p[1].ndim() != 2 || p[1].size(1) != scaleDim)
+        throw std::runtime_error("checkpoint: scales must be [N," + std::to_string(scaleDim) + "] for this model");
     releaseOptimizers();
     means = p[0];
     scales = p[1];
@@ -479,6 +492,7 @@ void engine_check(int rc) {
 
 int64_t Model::exportPointCloud(std::vector<Camera> &cameras, int step, float alphaThresh,
                                 const std::string &outPath) {
+    if (scaleDim != 2) throw std::runtime_error("point cloud export needs the 2DGS mode's depth");
     std::vector<float> xyz;
     std::vector<uint8_t> rgb;
     MTensor xyzDev, rgbDev;
@@ -546,6 +560,7 @@ Model::VoxelGrid Model::makeVoxelGrid(const std::vector<Camera> &cameras, float 
 
 void Model::integrateTSDF(VoxelGrid &grid, std::vector<Camera> &cameras, int step, float truncDist,
                           float alphaThresh) {
+    if (scaleDim != 2) throw std::runtime_error("TSDF fusion needs the 2DGS mode's median depth");
     // Each camera's median depth (the surface depth, where T crosses 0.5)
     // and alpha are staged in HBM; a batch of views is then folded into the
     // grid in one pass, every voxel applying the views in camera order --

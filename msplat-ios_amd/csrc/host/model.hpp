@@ -19,7 +19,8 @@ float psnr(const MTensor &rendered, const MTensor &gt);
 float l1_loss(const MTensor &rendered, const MTensor &gt);
 float ssim_eval(const MTensor &rendered, const MTensor &gt, int windowSize = 11, float sigma = 1.5f);
 
-// Scales per splat: kScaleDim = 2 (2DGS surfel, model.hpp:20).
+// Scales per splat: kScaleDim = 2 (2DGS surfel, model.hpp:20).  A Model
+// built with scaleDim 3 trains 3D Gaussians (the 3DGS mode).
 constexpr int kScaleDim = 2;
 
 // Mean distance of every point to its k nearest neighbours (the initial
@@ -30,7 +31,7 @@ struct Model {
     Model(const InputData &inputData, int numCameras, int numDownscales, int resolutionSchedule, int shDegree,
           int shDegreeInterval, int refineEvery, int warmupLength, int resetAlphaEvery, float densifyGradThresh,
           float densifySizeThresh, int stopScreenSizeAt, float splitScreenSize, int maxSteps, bool keepCrs,
-          const float *bgColor = nullptr);
+          const float *bgColor = nullptr, int scaleDim = kScaleDim);
     ~Model() { releaseOptimizers(); }
     Model(const Model &) = delete;
     Model &operator=(const Model &) = delete;
@@ -88,6 +89,11 @@ struct Model {
     int64_t extractMesh(const VoxelGrid &grid, const std::string &outPath, int maxTriangles = 4'000'000);
 
     MTensor means, scales, quats, featuresDc, featuresRest, opacities;
+    // 2: surfels (the reference's 2DGS step); 3: 3D Gaussians projected with
+    // the EWA helpers (render / train step / densify of the 3DGS mode).  The
+    // 3DGS mode renders image and transmittance only, so the point cloud and
+    // mesh exports, which need depth, are 2DGS-only.
+    int scaleDim = kScaleDim;
 
     static constexpr int N_ADAM_GROUPS = 6;
     MTensor adam_exp_avg[N_ADAM_GROUPS];

@@ -136,14 +136,16 @@ struct Trainer::Impl {
     }
 };
 
-Trainer::Trainer(Dataset &dataset, const Config &config) : impl(std::make_unique<Impl>()) {
+Trainer::Trainer(Dataset &dataset, const Config &config) : Trainer(dataset, config, Primitive::Surfel2D) {}
+
+Trainer::Trainer(Dataset &dataset, const Config &config, Primitive primitive) : impl(std::make_unique<Impl>()) {
     impl->config = config;
     impl->ds = static_cast<Dataset::Impl *>(dataset._handle());
     impl->model = std::make_unique<Model>(
         impl->ds->data, (int)impl->ds->trainCams.size(), config.numDownscales, config.resolutionSchedule,
         config.shDegree, config.shDegreeInterval, config.refineEvery, config.warmupLength, config.resetAlphaEvery,
         config.densifyGradThresh, config.densifySizeThresh, config.stopScreenSizeAt, config.splitScreenSize,
-        config.iterations, config.keepCrs, config.bgColor);
+        config.iterations, config.keepCrs, config.bgColor, primitive == Primitive::Gaussian3D ? 3 : 2);
     impl->camIndices.resize(impl->ds->trainCams.size());
     std::iota(impl->camIndices.begin(), impl->camIndices.end(), 0);
     impl->shuffleCameras();
@@ -252,6 +254,10 @@ int Trainer::loadCheckpoint(const std::string &path) {
 
 int Trainer::splatCount() const { return (int)impl->model->means.size(0); }
 int Trainer::iteration() const { return impl->currentStep; }
+Primitive Trainer::primitive() const {
+    return impl->model->scaleDim == 3 ? Primitive::Gaussian3D : Primitive::Surfel2D;
+}
+
 int Trainer::loadPly(const std::string &path) {
     impl->currentStep = impl->model->loadPly(path);
     impl->shuffleCameras();
@@ -368,6 +374,11 @@ void msplat_dataset_camera_pose(MsplatDataset ds, int cameraIndex, float camToWo
 MsplatTrainer msplat_trainer_create(MsplatDataset ds, MsplatConfig config) {
     return guarded<MsplatTrainer>(nullptr, [&]() -> MsplatTrainer {
         return new msplat::Trainer(*D(ds), config_from_c(config));
+    });
+}
+MsplatTrainer msplat_trainer_create_3dgs(MsplatDataset ds, MsplatConfig config) {
+    return guarded<MsplatTrainer>(nullptr, [&]() -> MsplatTrainer {
+        return new msplat::Trainer(*D(ds), config_from_c(config), msplat::Primitive::Gaussian3D);
     });
 }
 void msplat_trainer_destroy(MsplatTrainer t) { delete static_cast<msplat::Trainer *>(t); }

@@ -120,8 +120,15 @@ __global__ __launch_bounds__(kScanBlock) void k_scan_add(int *__restrict__ out, 
 
 // ---- densification (msplat_metal.metal:3231-3491) ------------------------
 
-// densify_classify_kernel (:3231-3266)
-__global__ void k_classify(int N, const float *__restrict__ gnorm, const float *__restrict__ vis,
+// The largest of a splat's SD scales (kScaleDim, :3253-3255).
+__device__ __forceinline__ float max_scale(const float *__restrict__ scales, size_t i, int SD) {
+    float ms = ms_expf(scales[(size_t)SD * i]);
+    for (int k = 1; k < SD; ++k) ms = __builtin_fmaxf(ms, ms_expf(scales[(size_t)SD * i + k]));
+    return ms;
+}
+
+// densify_classify_kernel (:3231-3266); SD floats of scale per splat.
+__global__ void k_classify(int N, int SD, const float *__restrict__ gnorm, const float *__restrict__ vis,
                            const float *__restrict__ scales, const float *__restrict__ max2d, float half_max_dim,
                            float grad_th, float size_th, float screen_th, int check_screen, int *__restrict__ split,
                            int *__restrict__ dup) {
@@ -135,9 +142,7 @@ __global__ void k_classify(int N, const float *__restrict__ gnorm, const float *
     }
     const float avg = (gnorm[i] / vc) * half_max_dim;
     const bool high = avg > grad_th;
-    float ms = ms_expf(scales[2 * (size_t)i]);
-    ms = __builtin_fmaxf(ms, ms_expf(scales[2 * (size_t)i + 1]));
-    const bool large = ms > size_th;
+    const bool large = max_scale(scales, i, SD) > size_th;
     bool sp = large;
     if (check_screen && max2d[i] > screen_th) sp = true;
     sp = sp && high;
@@ -160,8 +165,9 @@ __device__ __forceinline__ void zero_adam(const Bufs18 &B, size_t dst) {
     }
 }
 
-// densify_append_split_kernel (:3271-3361), 2-float scales (kScaleDim).
-__global__ void k_append_split(int N, const int *__restrict__ split, const int *__restrict__ split_pre,
+// densify_append_split_kernel (:3271-3361): children sampled along the SD
+// scale axes (the third is 0 for a surfel, :3315-3317).
+__global__ void k_append_split(int N, int SD, const int *__restrict__ split, const int *__restrict__ split_pre,
                                const float *__restrict__ rs, float log_size_fac, Bufs18 B) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= N || split[i] == 0) return;
@@ -174,7 +180,9 @@ __global__ void k_append_split(int N, const int *__restrict__ split, const int *
     qx /= qlen;
     qy /= qlen;
     qz /= qlen;
-    const float sx = ms_expf(scales[i * 2]), sy = ms_expf(scales[i * 2 + 1]), sz = 0.0f;
+    const size_t si = (size_t)i * SD;
+    const float sx = ms_expf(scales[si]), sy = ms_expf(scales[si + 1]);
+    const float sz = SD > 2 ? ms_expf(scales[si + 2]) : 0.0f;
     for (int k = 0; k < 2; ++k) {
         const size_t child = (size_t)c0 + k;
         const int ri = ord * 2 + k;
@@ -185,14 +193,14 @@ __global__ void k_append_split(int N, const int *__restrict__ split, const int *
         means[child * 3] = means[i * 3] + v0;
         means[child * 3 + 1] = means[i * 3 + 1] + v1;
         means[child * 3 + 2] = means[i * 3 + 2] + v2;
-        for (int j = 0; j < 2; ++j) scales[child * 2 + j] = scales[i * 2 + j] - log_size_fac;
+        for (int j = 0; j < SD; ++j) scales[child * SD + j] = scales[si + j] - log_size_fac;
         for (int gi = 2; gi < 6; ++gi) {
             const int s = B.stride[gi];
             for (int j = 0; j < s; ++j) B.b[gi][child * s + j] = B.b[gi][(size_t)i * s + j];
         }
         zero_adam(B, child);
     }
-    for (int j = 0; j < 2; ++j) scales[i * 2 + j] -= log_size_fac;
+    for (int j = 0; j < SD; ++j) scales[si + j] -= log_size_fac;
 }
 
 // densify_append_dup_kernel (:3365-3412)
@@ -210,7 +218,7 @@ __global__ void k_append_dup(int N, const int *__restrict__ dup, const int *__re
 }
 
 // densify_cull_classify_kernel (:3417-3456)
-__global__ void k_cull(int N_old, int worst, const int *__restrict__ split_pre, const int *__restrict__ dup_pre,
+__global__ void k_cull(int N_old, int worst, int SD, const int *__restrict__ split_pre, const int *__restrict__ dup_pre,
                        const int *__restrict__ split, const float *__restrict__ opac,
                        const float *__restrict__ scales, const float *__restrict__ max2d, float alpha_th,
                        float scale_th, float screen_size, int check_huge, int check_screen,
@@ -228,9 +236,7 @@ __global__ void k_cull(int N_old, int worst, const int *__restrict__ split_pre, 
     bool cull = os < alpha_th;
     if (i < N_old && split[i] != 0) cull = true;
     if (check_huge) {
-        float ms = ms_expf(scales[2 * (size_t)i]);
-        ms = __builtin_fmaxf(ms, ms_expf(scales[2 * (size_t)i + 1]));
-        if (ms > scale_th) cull = true;
+        if (max_scale(scales, i, SD) > scale_th) cull = true;
         if (check_screen && i < N_old && max2d[i] > screen_size) cull = true;
     }
     keep[i] = cull ? 0 : 1;
@@ -296,7 +302,7 @@ void launch_scan_i32(hipStream_t s, const int *in, int *out, int n, int *temp) {
 
 void launch_densify_classify(hipStream_t s, const DensifyArgs &a) {
     const int N = a.n;
-    hipLaunchKernelGGL(k_classify, dim3(nblk(N, 256)), dim3(256), 0, s, N, a.grad_norm, a.vis, a.params[1], a.max2d,
+    hipLaunchKernelGGL(k_classify, dim3(nblk(N, 256)), dim3(256), 0, s, N, a.scale_dim, a.grad_norm, a.vis, a.params[1], a.max2d,
                        a.half_max_dim, a.grad_th, a.size_th, a.screen_th, a.check_screen, a.split, a.dup);
     launch_scan_i32(s, a.split, a.split_pre, N, a.scan_temp);
     launch_scan_i32(s, a.dup, a.dup_pre, N, a.scan_temp);
@@ -305,7 +311,7 @@ void launch_densify_classify(hipStream_t s, const DensifyArgs &a) {
 void launch_densify_apply(hipStream_t s, const DensifyArgs &a, int n_new) {
     const int N = a.n, worst = n_new;
     Bufs18 B{}, S{};
-    const int strides[6] = {3, 2, 4, 3, a.fr_stride, 1};
+    const int strides[6] = {3, a.scale_dim, 4, 3, a.fr_stride, 1};
     for (int gi = 0; gi < 6; ++gi) {
         B.b[gi] = a.params[gi];
         B.b[6 + gi] = a.exp_avg[gi];
@@ -318,10 +324,10 @@ void launch_densify_apply(hipStream_t s, const DensifyArgs &a, int n_new) {
             S.stride[6 * r + gi] = strides[gi];
         }
     }
-    hipLaunchKernelGGL(k_append_split, dim3(nblk(N, 256)), dim3(256), 0, s, N, a.split, a.split_pre, a.random,
+    hipLaunchKernelGGL(k_append_split, dim3(nblk(N, 256)), dim3(256), 0, s, N, a.scale_dim, a.split, a.split_pre, a.random,
                        a.log_size_fac, B);
     hipLaunchKernelGGL(k_append_dup, dim3(nblk(N, 256)), dim3(256), 0, s, N, a.dup, a.dup_pre, a.split_pre, B);
-    hipLaunchKernelGGL(k_cull, dim3(nblk(worst, 256)), dim3(256), 0, s, N, worst, a.split_pre, a.dup_pre, a.split,
+    hipLaunchKernelGGL(k_cull, dim3(nblk(worst, 256)), dim3(256), 0, s, N, worst, a.scale_dim, a.split_pre, a.dup_pre, a.split,
                        a.params[5], a.params[1], a.max2d, a.cull_alpha, a.cull_scale, a.cull_screen, a.check_huge,
                        a.check_screen, a.keep);
     launch_scan_i32(s, a.keep, a.keep_pre, worst, a.scan_temp);

@@ -651,18 +651,7 @@ __global__ __launch_bounds__(kBlock) void k_project3d_fwd(
         ro[1] = make_float4(cn[2], opa, 0.f, 0.f);
         ro[2] = make_float4(__builtin_fmaxf(col[0] + 0.5f, 0.0f), __builtin_fmaxf(col[1] + 0.5f, 0.0f),
                             __builtin_fmaxf(col[2] + 0.5f, 0.0f), 0.f);
-        // alpha >= 1/255 needs d^T conic d <= tau: the ellipse's extent is
-        // sqrt(tau cov2d) along each axis (grown for the rounding of the
-        // conic and of the pixel's quadratic form)
-        const float tau = splat_reach(opa);
-        if (tau >= 0.0f) {
-            const float hx = __builtin_sqrtf(tau * c2[0]) * 1.001f + 1e-3f;
-            const float hy = __builtin_sqrtf(tau * c2[2]) * 1.001f + 1e-3f;
-            bo = make_float4(xy[0] - hx, xy[0] + hx, xy[1] - hy, xy[1] + hy);
-        } else {
-            const float inf = __builtin_inff();
-            bo = make_float4(inf, -inf, inf, -inf);
-        }
+        bo = gauss3_box(xy[0], xy[1], c2, splat_reach(opa));
         if (colors_raw) {
             colors_raw[3 * (size_t)i] = col[0];
             colors_raw[3 * (size_t)i + 1] = col[1];

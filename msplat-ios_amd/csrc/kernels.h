@@ -127,6 +127,7 @@ void launch_scan_i32(hipStream_t s, const int *in, int *out, int n, int *temp);
 
 struct DensifyArgs {
     int n, fr_stride;
+    int scale_dim;  // floats of scale per splat: 2 (surfels) or 3 (3D Gaussians)
     float grad_th, size_th, screen_th;
     int check_screen;
     float cull_alpha, cull_scale, cull_screen;

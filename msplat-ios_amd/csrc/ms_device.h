@@ -437,6 +437,34 @@ __host__ __device__ constexpr int wave_y0(int w) { return (w >> 1) * kWaveH; }
 __host__ __device__ constexpr int lane_px(int w, int lane) { return wave_x0(w) + (lane & 7); }
 __host__ __device__ constexpr int lane_py(int w, int lane) { return wave_y0(w) + (lane >> 3); }
 
+// The 3DGS mode's screen box (xmin, xmax, ymin, ymax) of the pixels where a
+// Gaussian centred at (xs, ys) with 2D covariance C = c2 (xx, xy, yy) can
+// reach alpha >= 1/255 under the fp32 pair rule on its fp32 conic K:
+// rho_f = fl(d^T K d) <= tau.
+//  - d^T C^-1 d <= T spans sqrt(T C_xx) in x and sqrt(T C_yy) in y.
+//  - Rounding: evaluating rho (five roundings over terms whose magnitudes
+//    sum to at most 3 cond rho, cond = lambda_max / lambda_min of C) and
+//    K's own rounding from C (the determinant cancels to ~2 cond ulp) keep
+//    rho_f >= d^T C^-1 d (1 - 40 u cond), u = 2^-24; so T = tau (1 + 40 u
+//    cond) / (1 - 40 u cond) bounds the reach.  Beyond 40 u cond = 1/4 the
+//    box is unbounded (the tile rectangle alone limits the splat).
+//  - The extents are grown by 0.1% and 1e-3 px for the rounding of the box
+//    itself.  Empty when tau < 0 (the Gaussian never reaches 1/255).
+__host__ __device__ __forceinline__ float4 gauss3_box(float xs, float ys, const float c2[3], float tau) {
+    const float inf = __builtin_inff();
+    if (!(tau >= 0.0f)) return make_float4(inf, -inf, inf, -inf);
+    const float b = 0.5f * (c2[0] + c2[2]);
+    const float det = c2[0] * c2[2] - c2[1] * c2[1];
+    const float lmax = b + __builtin_sqrtf(__builtin_fmaxf(b * b - det, 0.0f));
+    const float lmin = det / lmax;
+    const float k = 40.0f * 5.9604645e-8f * (lmax / lmin);
+    if (!(lmin > 0.0f) || !(k < 0.25f)) return make_float4(-inf, inf, -inf, inf);
+    const float t = tau * (1.0f + k) / (1.0f - k);
+    const float hx = __builtin_sqrtf(t * c2[0]) * 1.001f + 1e-3f;
+    const float hy = __builtin_sqrtf(t * c2[2]) * 1.001f + 1e-3f;
+    return make_float4(xs - hx, xs + hx, ys - hy, ys + hy);
+}
+
 // Bit w (w = 0..3) set when the splat box meets the pixel block of wave w
 // of the tile whose top-left pixel is (sx0, sy0).
 __host__ __device__ __forceinline__ int strip_mask(const float4 &b, float sx0, float sy0) {

@@ -82,8 +82,16 @@ struct Trainer {
     msplat::Trainer t;
     TrainingConfig config;
     int num_train, num_test;
-    Trainer(msplat::Dataset &ds, const TrainingConfig &cfg)
-        : t(ds, cfg.to_config()), config(cfg), num_train(ds.numTrain()), num_test(ds.numTest()) {}
+    Trainer(msplat::Dataset &ds, const TrainingConfig &cfg, const std::string &primitive)
+        : t(ds, cfg.to_config(), parse_primitive(primitive)),
+          config(cfg),
+          num_train(ds.numTrain()),
+          num_test(ds.numTest()) {}
+    static msplat::Primitive parse_primitive(const std::string &p) {
+        if (p == "2dgs") return msplat::Primitive::Surfel2D;
+        if (p == "3dgs") return msplat::Primitive::Gaussian3D;
+        throw std::invalid_argument("primitive must be '2dgs' or '3dgs'");
+    }
 };
 
 TrainingStats to_stats(const msplat::Stats &s) {
@@ -234,7 +242,12 @@ PYBIND11_MODULE(_core, m) {
             "index"_a, "Get camera-to-world pose (4x4 row-major, OpenGL convention) as numpy array.");
 
     py::class_<Trainer>(m, "GaussianTrainer", "2D Gaussian Splatting trainer. All computation runs on the GPU.")
-        .def(py::init<msplat::Dataset &, const TrainingConfig &>(), "dataset"_a, "config"_a, py::keep_alive<1, 2>())
+        .def(py::init<msplat::Dataset &, const TrainingConfig &, const std::string &>(), "dataset"_a, "config"_a,
+             "primitive"_a = "2dgs", py::keep_alive<1, 2>(),
+             "primitive: '2dgs' (surfels, the default) or '3dgs' (3D Gaussians; no mesh or point-cloud export).")
+        .def_property_readonly(
+            "primitive",
+            [](const Trainer &t) { return t.t.primitive() == msplat::Primitive::Gaussian3D ? "3dgs" : "2dgs"; })
         .def(
             "step", [](Trainer &t) { return to_stats(t.t.step()); },
             "Run a single training iteration. Returns TrainingStats.")

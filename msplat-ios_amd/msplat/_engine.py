@@ -75,7 +75,7 @@ EXPORTS = [
     "msplat_hip_stage_times", "msplat_hip_last_pairs_evaluated", "msplat_hip_last_raster_counts",
     "msplat_hip_check_fast_rcp", "msplat_hip_set_wide_keys", "msplat_hip_tsdf_integrate",
     "msplat_hip_marching_cubes", "msplat_hip_mc_table", "msplat_hip_unproject_depth", "msplat_hip_render_3dgs",
-    "msplat_hip_train_step_3dgs",
+    "msplat_hip_train_step_3dgs", "msplat_hip_densify_3dgs",
 ]
 SYNTH_EXPORTS = ["msplat_synth_uniform", "msplat_synth_normal"]
 
@@ -128,6 +128,8 @@ def lib() -> C.CDLL:
         "msplat_hip_last_raster_counts": (I, [P]),
         "msplat_hip_check_fast_rcp": (I, [I, I, C.POINTER(C.c_int64)]),
         "msplat_hip_set_wide_keys": (I, [I]),
+        "msplat_hip_densify_3dgs": (I, [I, I, F, F, F, I, F, F, F, I, P, P, P, F, P * 6, I, P * 6, P * 6, P,
+                                        C.POINTER(I)]),
         "msplat_hip_render_3dgs": (I, [C.POINTER(MsplatCamera), C.POINTER(MsplatGaussians), P, C.POINTER(I64)]),
         "msplat_hip_train_step_3dgs": (I, [C.POINTER(MsplatCamera), C.POINTER(MsplatGaussians), P, P, F, F, P, P, P,
                                            F, C.POINTER(MsplatAdam), c_float_p, C.POINTER(I64)]),

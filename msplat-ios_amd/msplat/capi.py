@@ -87,6 +87,7 @@ def lib() -> C.CDLL:
         "msplat_trainer_load_ply": (I, [V, P]),
         "msplat_trainer_set_max_splats": (None, [V, I]),
         "msplat_trainer_set_cull_alpha": (None, [V, F]),
+        "msplat_trainer_create_3dgs": (V, [V, Config]),
         "msplat_set_metallib_path": (None, [P]),
         "msplat_sync": (None, []),
         "msplat_cleanup": (None, []),

@@ -1079,17 +1079,19 @@ extern "C" void orc_adam(float *params, const float *grads, float *m_, float *v_
 
 /* msplat_densify (msplat_metal.mm:1339-1594): classify (metal:3231-3266),
  * append split (:3271-3361), append dup (:3365-3412), cull (:3417-3456) and
- * stable compaction (:3460-3491), run stage by stage. */
-extern "C" int orc_densify(int N, int capacity, float grad_thresh, float size_thresh,
-                           float screen_thresh, int check_screen, float cull_alpha_thresh,
-                           float cull_scale_thresh, float cull_screen_size, int check_huge,
-                           const float *xys_grad_norm, const float *vis_counts,
-                           const float *max_2d_size, float half_max_dim,
-                           float *const params[6], int fr_stride,
-                           float *const exp_avg[6], float *const exp_avg_sq[6],
-                           const float *rs) {
+ * stable compaction (:3460-3491), run stage by stage.  SD floats of scale
+ * per splat: the kernels' kScaleDim (2 for surfels, 3 for 3D Gaussians,
+ * :3253-3255, :3315-3317, :3339-3341). */
+static int densify_sd(int SD, int N, int capacity, float grad_thresh, float size_thresh,
+                      float screen_thresh, int check_screen, float cull_alpha_thresh,
+                      float cull_scale_thresh, float cull_screen_size, int check_huge,
+                      const float *xys_grad_norm, const float *vis_counts,
+                      const float *max_2d_size, float half_max_dim,
+                      float *const params[6], int fr_stride,
+                      float *const exp_avg[6], float *const exp_avg_sq[6],
+                      const float *rs) {
     if (N > capacity) return -1;
-    const int strides[6] = {3, 2, 4, 3, fr_stride, 1};
+    const int strides[6] = {3, SD, 4, 3, fr_stride, 1};
     float *means = params[0], *scales = params[1], *quats = params[2];
     float *opac = params[5];
     std::vector<int> split(N), dup(N), split_pre(N), dup_pre(N);
@@ -1098,8 +1100,8 @@ extern "C" int orc_densify(int N, int capacity, float grad_thresh, float size_th
         if (vc <= 0.0f) { split[i] = dup[i] = 0; continue; }
         float avg = (xys_grad_norm[i] / vc) * half_max_dim;
         bool high = avg > grad_thresh;
-        float ms = orc_expf(scales[2 * i]);
-        ms = fmaxf(ms, orc_expf(scales[2 * i + 1]));
+        float ms = orc_expf(scales[(size_t)SD * i]);
+        for (int k = 1; k < SD; ++k) ms = fmaxf(ms, orc_expf(scales[(size_t)SD * i + k]));
         bool large = ms > size_thresh;
         bool sp = large;
         if (check_screen && max_2d_size[i] > screen_thresh) sp = true;
@@ -1130,7 +1132,8 @@ extern "C" int orc_densify(int N, int capacity, float grad_thresh, float size_th
         float qw = quats[i * 4], qx = quats[i * 4 + 1], qy = quats[i * 4 + 2], qz = quats[i * 4 + 3];
         float qlen = sqrtf(qw * qw + qx * qx + qy * qy + qz * qz);
         qw /= qlen; qx /= qlen; qy /= qlen; qz /= qlen;
-        float sx = orc_expf(scales[i * 2]), sy = orc_expf(scales[i * 2 + 1]), sz = 0.0f;
+        float sx = orc_expf(scales[(size_t)i * SD]), sy = orc_expf(scales[(size_t)i * SD + 1]);
+        float sz = SD > 2 ? orc_expf(scales[(size_t)i * SD + 2]) : 0.0f;
         for (int k = 0; k < 2; ++k) {
             int child = c0 + k, ri = ord * 2 + k;
             float r0 = rs[ri * 3] * sx, r1 = rs[ri * 3 + 1] * sy, r2 = rs[ri * 3 + 2] * sz;
@@ -1143,14 +1146,14 @@ extern "C" int orc_densify(int N, int capacity, float grad_thresh, float size_th
             means[child * 3] = means[i * 3] + v0;
             means[child * 3 + 1] = means[i * 3 + 1] + v1;
             means[child * 3 + 2] = means[i * 3 + 2] + v2;
-            for (int j = 0; j < 2; ++j) scales[child * 2 + j] = scales[i * 2 + j] - log_size_fac;
+            for (int j = 0; j < SD; ++j) scales[(size_t)child * SD + j] = scales[(size_t)i * SD + j] - log_size_fac;
             for (int gi = 2; gi < 6; ++gi)
                 for (int j = 0; j < strides[gi]; ++j)
                     params[gi][(size_t)child * strides[gi] + j] =
                         params[gi][(size_t)i * strides[gi] + j];
             zero_adam(child);
         }
-        for (int j = 0; j < 2; ++j) scales[i * 2 + j] -= log_size_fac;
+        for (int j = 0; j < SD; ++j) scales[(size_t)i * SD + j] -= log_size_fac;
     }
     for (int i = 0; i < N; ++i) {
         if (!dup[i]) continue;
@@ -1167,8 +1170,8 @@ extern "C" int orc_densify(int N, int capacity, float grad_thresh, float size_th
         bool cull = os < cull_alpha_thresh;
         if (i < N && split[i] != 0) cull = true;
         if (check_huge) {
-            float ms = orc_expf(scales[i * 2]);
-            ms = fmaxf(ms, orc_expf(scales[i * 2 + 1]));
+            float ms = orc_expf(scales[(size_t)i * SD]);
+            for (int k = 1; k < SD; ++k) ms = fmaxf(ms, orc_expf(scales[(size_t)i * SD + k]));
             if (ms > cull_scale_thresh) cull = true;
             if (check_screen && i < N && max_2d_size[i] > cull_screen_size) cull = true;
         }
@@ -1188,6 +1191,32 @@ extern "C" int orc_densify(int N, int capacity, float grad_thresh, float size_th
         ++out;
     }
     return out;
+}
+
+extern "C" int orc_densify(int N, int capacity, float grad_thresh, float size_thresh,
+                           float screen_thresh, int check_screen, float cull_alpha_thresh,
+                           float cull_scale_thresh, float cull_screen_size, int check_huge,
+                           const float *xys_grad_norm, const float *vis_counts,
+                           const float *max_2d_size, float half_max_dim,
+                           float *const params[6], int fr_stride,
+                           float *const exp_avg[6], float *const exp_avg_sq[6],
+                           const float *rs) {
+    return densify_sd(2, N, capacity, grad_thresh, size_thresh, screen_thresh, check_screen, cull_alpha_thresh,
+                      cull_scale_thresh, cull_screen_size, check_huge, xys_grad_norm, vis_counts, max_2d_size,
+                      half_max_dim, params, fr_stride, exp_avg, exp_avg_sq, rs);
+}
+
+extern "C" int orc_densify_3dgs(int N, int capacity, float grad_thresh, float size_thresh,
+                                float screen_thresh, int check_screen, float cull_alpha_thresh,
+                                float cull_scale_thresh, float cull_screen_size, int check_huge,
+                                const float *xys_grad_norm, const float *vis_counts,
+                                const float *max_2d_size, float half_max_dim,
+                                float *const params[6], int fr_stride,
+                                float *const exp_avg[6], float *const exp_avg_sq[6],
+                                const float *rs) {
+    return densify_sd(3, N, capacity, grad_thresh, size_thresh, screen_thresh, check_screen, cull_alpha_thresh,
+                      cull_scale_thresh, cull_screen_size, check_huge, xys_grad_norm, vis_counts, max_2d_size,
+                      half_max_dim, params, fr_stride, exp_avg, exp_avg_sq, rs);
 }
 
 /* Model::fullIteration (core/src/model.cpp:762-829) + msplat_train_step_2dgs

@@ -157,6 +157,17 @@ int orc_densify(int n, int capacity, float grad_thresh, float size_thresh,
                 float *const params[6], int fr_stride,
                 float *const exp_avg[6], float *const exp_avg_sq[6],
                 const float *random_samples);
+/* The same with 3 scales per splat (the 3DGS mode): scales stride 3, split
+ * children sampled along all three axes. */
+int orc_densify_3dgs(int n, int capacity, float grad_thresh, float size_thresh,
+                     float screen_thresh, int check_screen,
+                     float cull_alpha_thresh, float cull_scale_thresh,
+                     float cull_screen_size, int check_huge,
+                     const float *xys_grad_norm, const float *vis_counts,
+                     const float *max_2d_size, float half_max_dim,
+                     float *const params[6], int fr_stride,
+                     float *const exp_avg[6], float *const exp_avg_sq[6],
+                     const float *random_samples);
 
 /* Optional intermediate results of orc_train_step, for comparing a whole
  * step stage by stage (test instrumentation): arrays are malloc'd by the

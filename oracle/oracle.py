@@ -71,6 +71,8 @@ def lib() -> C.CDLL:
         L.orc_densify.argtypes = [C.c_int, C.c_int, C.c_float, C.c_float, C.c_float, C.c_int, C.c_float,
                                   C.c_float, C.c_float, C.c_int, P, P, P, C.c_float, P * 6, C.c_int, P * 6,
                                   P * 6, P]
+        L.orc_densify_3dgs.restype = C.c_int
+        L.orc_densify_3dgs.argtypes = L.orc_densify.argtypes
         L.orc_train_step.restype = C.c_double
         L.orc_train_step.argtypes = [C.c_int] + [P] * 6 + [C.c_int, C.c_int, C.POINTER(OrcCamera), P, P,
                                                           C.c_float, P * 6, P * 6, P, C.c_int, P, P, P, P, P,
@@ -254,10 +256,12 @@ def adam(params, grads, m, v, step_size, beta1=0.9, beta2=0.999, bc2_sqrt=1.0, e
 
 def densify(n, capacity, params6, exp_avg6, exp_avg_sq6, fr_stride, stats, random_samples, grad_thresh=0.0002,
             size_thresh=0.01, screen_thresh=0.05, check_screen=1, cull_alpha=0.1, cull_scale=0.5,
-            cull_screen=0.15, check_huge=1, half_max_dim=648.5):
+            cull_screen=0.15, check_huge=1, half_max_dim=648.5, scale_dim=2):
+    """scale_dim 2 (surfels) or 3 (the 3DGS mode's Gaussians)."""
     P6 = C.c_void_p * 6
     rs = _f(random_samples)
-    r = lib().orc_densify(n, capacity, grad_thresh, size_thresh, screen_thresh, check_screen, cull_alpha,
+    fn = {2: lib().orc_densify, 3: lib().orc_densify_3dgs}[scale_dim]
+    r = fn(n, capacity, grad_thresh, size_thresh, screen_thresh, check_screen, cull_alpha,
                           cull_scale, cull_screen, check_huge, _p(stats["grad_norm"]), _p(stats["vis"]),
                           _p(stats["max2d"]), half_max_dim, P6(*[_p(a) for a in params6]), fr_stride,
                           P6(*[_p(a) for a in exp_avg6]), P6(*[_p(a) for a in exp_avg_sq6]),
@@ -403,3 +407,31 @@ def project3d_bwd(params: dict, cam, degree, dtu, radii, grads9, stats=None, glo
                             _p(stats["grad_norm"]), _p(stats["vis"]), _p(stats["max2d"]), float(inv_max_dim))
     out.update(stats)
     return out
+
+
+def train_step3d(params: dict, exp_avg: dict, exp_avg_sq: dict, cam, background, gt, degree, dtu, adam_lr,
+                 adam_step, stats, ssim_weight=0.2):
+    """One golden-model 3DGS training step in place (Model::fullIteration,
+    core/src/model.cpp:762-829, in the 3DGS mode): projection, binning,
+    compositing, SSIM + L1 (no distortion), the raster and projection
+    backwards, Adam on the six groups with the step's bias corrections
+    (model.cpp:767-768).  params / exp_avg / exp_avg_sq: dicts of the six
+    groups (scales [N,3]).  Returns (loss, image, intersections)."""
+    proj = project3d_fwd(params, cam, degree, dtu)
+    bins = bin_sort(proj, cam)
+    fwd = raster3d_fwd(proj, bins, cam, params["opacities"], background)
+    loss, dL, _, _ = loss_fwd_bwd(fwd["out_img"], gt, lambda_l1=1.0 - ssim_weight, lambda_dssim=ssim_weight)
+    g9 = raster3d_bwd(proj, bins, fwd, cam, params["opacities"], background, dL)
+    g = project3d_bwd(params, cam, degree, dtu, proj["radii"], g9, stats)
+    grads = dict(means=g["dmeans"], scales=g["dscales"], quats=g["dquats"], features_dc=g["dfdc"],
+                 features_rest=g["dfrest"], opacities=np.ascontiguousarray(g9[:, 5:6]))
+    b1, b2 = np.float32(0.9), np.float32(0.999)
+    bc1 = np.float32(1.0 - np.power(np.float64(b1), adam_step))
+    bc2 = np.float32(1.0 - np.power(np.float64(b2), adam_step))
+    bc2_sqrt = float(np.sqrt(bc2, dtype=np.float32))
+    for k, lr in zip(("means", "scales", "quats", "features_dc", "features_rest", "opacities"), adam_lr):
+        pk = params[k]
+        assert pk.dtype == np.float32 and pk.flags.c_contiguous
+        adam(pk, np.ascontiguousarray(grads[k], np.float32).reshape(pk.shape), exp_avg[k], exp_avg_sq[k],
+             float(np.float32(lr) / bc1), float(b1), float(b2), bc2_sqrt, 1e-8)
+    return float(loss), fwd["out_img"], int(bins["num_intersections"])

@@ -100,6 +100,56 @@ extern "C" int64_t qm_check(int n, const float *transmats, const float *xys, con
     return misses;
 }
 
+// The 3DGS mode's masks (msd::gauss3_box per splat, msd::strip_mask per
+// tile).  xys [n,2], conics [n,3] (a, b, c), cov2d [n,3] (xx, xy, yy),
+// opacity logits [n], radii [n], rect [n,4] as qm_check.  A pixel passes
+// when alpha = min(0.99, opacity exp(-rho / 2)) reaches 1/255 for some rho
+// within the fp32 evaluation's rounding of rho = a dx^2 + c dy^2 + 2 b dx dy
+// (fp64, from the fp32 conic; 6 units of roundoff of the sum of the terms'
+// magnitudes, above the five roundings of the fp32 evaluation).
+// Returns the passing pixels whose quadrant bit is clear; out as qm_check
+// (out[2] = out[1], out[4] = out[3]: there is no finer mask).
+extern "C" int64_t qm3_check(int n, const float *xys, const float *conics, const float *cov2d,
+                             const float *opac_logit, const int32_t *radii, const int32_t *rect, int W, int H,
+                             float tau_scale, int64_t out[5]) {
+    const int tiles_x = (W + 15) / 16, tiles_y = (H + 15) / 16;
+    int64_t misses = 0, checked = 0, box_tiles = 0, box_bits = 0;
+    const double ulp = std::ldexp(1.0, -24);
+    for (int g = 0; g < n; ++g) {
+        if (radii[g] <= 0) continue;
+        const float xs = xys[2 * g], ys = xys[2 * g + 1];
+        const float opa = 1.0f / (1.0f + std::exp(-opac_logit[g]));
+        const float tau = reach(opa) * tau_scale;
+        const float4 box = gauss3_box(xs, ys, cov2d + 3 * (size_t)g, tau);
+        const double a = conics[3 * g], b = conics[3 * g + 1], c = conics[3 * g + 2];
+        const int *rc = rect + 4 * (size_t)g;
+        const int tx0 = std::max(0, rc[0]), ty0 = std::max(0, rc[1]);
+        const int tx1 = std::min(tiles_x, rc[2]) - 1, ty1 = std::min(tiles_y, rc[3]) - 1;
+        for (int ty = ty0; ty <= ty1; ++ty)
+            for (int tx = tx0; tx <= tx1; ++tx) {
+                const int m = strip_mask(box, (float)(tx * 16), (float)(ty * 16));
+                box_tiles += m != 0;
+                box_bits += __builtin_popcount(m);
+                for (int w = 0; w < 4; ++w)
+                    for (int l = 0; l < 64; ++l) {
+                        const int pxi = tx * 16 + lane_px(w, l), pyi = ty * 16 + lane_py(w, l);
+                        if (pxi >= W || pyi >= H) continue;
+                        const double dx = (double)(xs - (float)pxi), dy = (double)(ys - (float)pyi);
+                        const double t1 = a * dx * dx, t2 = c * dy * dy, t3 = 2.0 * b * dx * dy;
+                        const double rho = t1 + t2 + t3;
+                        const double err = 6.0 * ulp * (std::fabs(t1) + std::fabs(t2) + std::fabs(t3));
+                        const double alpha = std::fmin(0.99, opa * std::exp(-0.5 * std::fmax(rho - err, 0.0)));
+                        ++checked;
+                        if (alpha >= (1.0 / 255.0) * (1.0 - 1e-6) && !((m >> w) & 1)) ++misses;
+                    }
+            }
+    }
+    out[0] = checked;
+    out[1] = out[2] = box_tiles;
+    out[3] = out[4] = box_bits;
+    return misses;
+}
+
 // The rasterizers' workgroup -> tile order (msd::xcd_strip_tile): the
 // number of tiles of a tx x ty grid that the xcd_strip_grid(tx, ty)
 // workgroups do not cover exactly once (0 for a bijection), or -1 when a

@@ -3,6 +3,8 @@ tile lists and images bit for bit (also for needle-thin, near-opaque and
 off-screen Gaussians, which stress the quadrant masks), raster gradients
 within the float-atomic bound, the projection backward bit for bit from
 the GPU's own raster gradients, the fused Adam step, and training."""
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -71,6 +73,23 @@ def test_render3d_matches_oracle(orc, eng, needles):
     assert np.array_equal(eng.last("colors_used", (n, 3))[vis], cols[vis])
     assert np.array_equal(eng.last("tile_offsets", (ocam.tiles_x * ocam.tiles_y + 1,)), bins["tile_offsets"])
     assert np.array_equal(eng.last("gaussian_ids", (bins["num_intersections"],)), bins["ids"])
+    assert np.array_equal(out["out_img"], fwd["out_img"])
+    assert np.array_equal(out["final_T"], fwd["final_T"])
+
+
+def test_render3d_ill_conditioned_needles(orc, eng):
+    """Long near-opaque needles at 1297x840 (2D covariances with condition
+    numbers up to ~6e4), where a box without the rounding allowance for the
+    conic's conditioning drops boundary pixels: images bit-exact."""
+    from msplat import device as D
+    from test_quadrant_masks import _scene3d
+    p, c = _scene3d(4, 1500, 1297, 840, "needles")
+    bg = np.float32([0.1, 0.2, 0.3])
+    ocam = orc.prepare_cam(*c)
+    gcam = eng.prepare_camera(*c, 3, 3)
+    proj, bins, fwd = _oracle_render(orc, p, ocam, bg)
+    out = D.render3d(D.DeviceScene3D(p, bg), gcam)
+    assert out["num_intersections"] == bins["num_intersections"]
     assert np.array_equal(out["out_img"], fwd["out_img"])
     assert np.array_equal(out["final_T"], fwd["final_T"])
 
@@ -150,3 +169,154 @@ def test_training3d_reduces_the_loss(orc, eng):
     losses = [D.train_step3d(ds, gcam, gt_dev, 0.2)[0] for _ in range(40)]
     assert np.isfinite(losses).all()
     assert losses[-1] < 0.7 * losses[0]
+
+
+def test_densify3d_bitexact(orc, eng):
+    """msplat_hip_densify_3dgs against the golden model's 3-scale densify:
+    classification on the largest of three scales, children along three
+    axes, splats both split and duplicated, culling and compaction."""
+    from test_oracle3d import STRIDES3, _dens_inputs
+    E = eng
+    n, cap, params, m6, v6, stats, rs = _dens_inputs(n=20_000, seed=21)
+    stats["grad_norm"][::7] = 0.0
+    params[5][: n][::13] = -6.0  # transparent: culled
+    dev = [E.DeviceArray.from_numpy(a) for a in params + m6 + v6]
+    dstats = {k: E.DeviceArray.from_numpy(v) for k, v in stats.items()}
+    d_rs = E.DeviceArray.from_numpy(rs)
+    P6 = C.c_void_p * 6
+    newc = C.c_int()
+    E.check(E.lib().msplat_hip_densify_3dgs(n, cap, 0.0002, 0.05, 0.05, 1, 0.1, 0.5, 0.15, 1,
+                                            dstats["grad_norm"].ptr, dstats["vis"].ptr, dstats["max2d"].ptr, 100.0,
+                                            P6(*[d.ptr for d in dev[0:6]]), 45, P6(*[d.ptr for d in dev[6:12]]),
+                                            P6(*[d.ptr for d in dev[12:18]]), d_rs.ptr, C.byref(newc)))
+    new_o = orc.densify(n, cap, params, m6, v6, 45, stats, rs, size_thresh=0.05, half_max_dim=100.0, scale_dim=3)
+    assert newc.value == new_o and new_o != n
+    for i, (d, o) in enumerate(zip(dev, params + m6 + v6)):
+        s = STRIDES3[i % 6]
+        assert np.array_equal(d.numpy()[: new_o * s], o[: new_o * s]), f"buffer {i}"
+
+
+def test_trainer3d_step_matches_golden_model(tmp_path):
+    """GaussianTrainer(primitive='3dgs'): model init (three scales) ->
+    export -> one step -> export, against the golden model's 3DGS step from
+    the exported initial parameters through the trainer's own camera, bias
+    corrections and learning rates."""
+    import msplat
+    from oracle import oracle as O
+    from test_gpu_trainer import _dataset_inputs, _read_gaussian_ply
+
+    scene, images, c2w, intr, xyz, rgb = _dataset_inputs(n_cams=1)
+    ds = msplat.Dataset.from_arrays(images, c2w, intr, xyz, rgb)
+    bg = [float(v) for v in scene.background]
+    cfg = msplat.TrainingConfig(iterations=100, num_downscales=0, bg_color=bg)
+    tr = msplat.GaussianTrainer(ds, cfg, primitive="3dgs")
+    assert tr.primitive == "3dgs"
+    tr.export_ply(str(tmp_path / "p0.ply"))
+    p0 = _read_gaussian_ply(tmp_path / "p0.ply")
+    assert p0["scales"].shape == (len(xyz), 3)
+    stats = tr.step()
+    tr.export_ply(str(tmp_path / "p1.ply"))
+    p1 = _read_gaussian_ply(tmp_path / "p1.ply")
+    assert stats.iteration == 1 and stats.splat_count == len(xyz)
+
+    c = scene.cameras[0]
+    ocam = O.prepare_cam(c.cam_to_world, c.fx, c.fy, c.cx, c.cy, c.width, c.height)
+    params = {k: np.ascontiguousarray(p0[k], np.float32) for k in GROUPS}
+    m = {k: np.zeros_like(v) for k, v in params.items()}
+    v = {k: np.zeros_like(x) for k, x in params.items()}
+    st = dict(grad_norm=np.zeros(len(xyz), np.float32), vis=np.zeros(len(xyz), np.float32),
+              max2d=np.zeros(len(xyz), np.float32))
+    lrs = (0.00016, 0.005, 0.001, 0.0025, 0.000125, 0.05)
+    loss_o, _, _ = O.train_step3d(params, m, v, ocam, np.float32(bg), images[0], 3, 0, lrs, 1, st)
+    assert abs(stats.loss - loss_o) <= 1e-5 * abs(loss_o)
+    for k in GROUPS:
+        assert np.abs(p1[k] - params[k]).max() <= 1e-5 * max(1.0, np.abs(params[k]).max()), k
+    assert np.abs(p1["means"] - p0["means"]).max() > 0
+
+
+def test_trainer3d_training_densify_and_formats(tmp_path):
+    """The 3DGS trainer end to end: training with densification (three-scale
+    compaction), PLY / .splat / checkpoint round trips, and the depth-based
+    exports refused."""
+    import math
+
+    import msplat
+    from test_gpu_trainer import _dataset_inputs, _read_gaussian_ply
+
+    scene, images, c2w, intr, xyz, rgb = _dataset_inputs(n_cams=4)
+    ds = msplat.Dataset.from_arrays(images, c2w, intr, xyz, rgb)
+    cfg = msplat.TrainingConfig(iterations=2000, num_downscales=0, refine_every=10, warmup_length=10,
+                                reset_alpha_every=3, densify_grad_thresh=1e-6)
+    tr = msplat.GaussianTrainer(ds, cfg, primitive="3dgs")
+    steps = [tr.step() for _ in range(55)]
+    counts = [s.splat_count for s in steps]
+    losses = [s.loss for s in steps]
+    assert all(math.isfinite(x) for x in losses)
+    assert counts[18] == len(xyz) and counts[19] != counts[18]  # densified at step 20
+    assert counts[49] != counts[48]  # and at step 50
+    assert np.mean(losses[-5:]) < np.mean(losses[:5])
+
+    tr.export_ply(str(tmp_path / "g.ply"))
+    g = _read_gaussian_ply(tmp_path / "g.ply")
+    assert g["scales"].shape == (tr.splat_count, 3)
+    assert [k for k in g["names"] if k.startswith("scale_")] == ["scale_0", "scale_1", "scale_2"]
+    tr.export_splat(str(tmp_path / "g.splat"))
+    assert (tmp_path / "g.splat").stat().st_size == 32 * tr.splat_count
+    img = tr.render(0)
+    tr.save_checkpoint(str(tmp_path / "g.msplat"))
+    for _ in range(3):
+        tr.step()
+    assert not np.array_equal(tr.render(0), img)
+    tr.load_checkpoint(str(tmp_path / "g.msplat"))
+    assert tr.iteration == 55
+    assert np.array_equal(tr.render(0), img)
+    # the 3-scale PLY resumes into a 3DGS trainer with the same render
+    tr2 = msplat.GaussianTrainer(ds, cfg, primitive="3dgs")
+    assert tr2.load_ply(str(tmp_path / "g.ply")) == 55
+    assert np.array_equal(tr2.render(0), img)
+    with pytest.raises(RuntimeError):
+        tr.extract_mesh(str(tmp_path / "m.ply"))
+    with pytest.raises(RuntimeError):
+        tr.export_point_cloud(str(tmp_path / "pc.ply"))
+    # a surfel trainer refuses the 3-scale checkpoint
+    tr_2d = msplat.GaussianTrainer(ds, cfg)
+    with pytest.raises(RuntimeError):
+        tr_2d.load_checkpoint(str(tmp_path / "g.msplat"))
+    with pytest.raises(Exception):
+        msplat.GaussianTrainer(ds, cfg, primitive="4dgs")
+
+
+def test_c_abi_trainer_3dgs(tmp_path):
+    """msplat_trainer_create_3dgs through the C ABI binding (msplat.capi):
+    training steps, a 3-scale PLY, and extract_mesh refused with a message."""
+    from msplat import capi
+    from test_gpu_trainer import _dataset_inputs, _read_gaussian_ply
+
+    L = capi.lib()
+    scene, images, c2w, intr, xyz, rgb = _dataset_inputs(n_cams=3)
+    imgs = [np.ascontiguousarray(i, np.float32) for i in images]
+    cams = (capi.CameraImage * 3)()
+    for i in range(3):
+        cams[i].width, cams[i].height = imgs[i].shape[1], imgs[i].shape[0]
+        cams[i].fx, cams[i].fy, cams[i].cx, cams[i].cy = (float(v) for v in intr[i])
+        cams[i].camToWorld[:] = [float(v) for v in c2w[i].reshape(-1)]
+        cams[i].rgb = imgs[i].ctypes.data
+    pts = np.ascontiguousarray(xyz, np.float32)
+    cols = np.ascontiguousarray(rgb, np.uint8)
+    ds = L.msplat_dataset_create_from_memory(cams, 3, pts.ctypes.data, cols.ctypes.data, len(pts), False, 8)
+    assert ds, capi.last_error()
+    cfg = capi.default_config()
+    cfg.numDownscales = 0
+    tr = L.msplat_trainer_create_3dgs(ds, cfg)
+    assert tr, capi.last_error()
+    try:
+        losses = [L.msplat_trainer_step(tr).loss for _ in range(20)]
+        assert np.isfinite(losses).all() and np.mean(losses[-3:]) < np.mean(losses[:3])
+        assert L.msplat_trainer_iteration(tr) == 20
+        L.msplat_trainer_export_ply(tr, str(tmp_path / "c3.ply").encode())
+        assert _read_gaussian_ply(tmp_path / "c3.ply")["scales"].shape == (len(pts), 3)
+        assert L.msplat_trainer_extract_mesh(tr, str(tmp_path / "m.ply").encode(), 0.02, 1.0, 0.5, 4.0) == -1
+        assert "depth" in capi.last_error()
+    finally:
+        L.msplat_trainer_destroy(tr)
+        L.msplat_dataset_destroy(ds)

@@ -33,7 +33,8 @@ def _read_gaussian_ply(path):
     col = {k: i for i, k in enumerate(names)}
     nfr = sum(k.startswith("f_rest_") for k in names) // 3
     fr = np.stack([rows[:, col[f"f_rest_{ch * nfr + b}"]] for b in range(nfr) for ch in range(3)], 1)
-    return dict(means=rows[:, [col["x"], col["y"], col["z"]]], scales=rows[:, [col["scale_0"], col["scale_1"]]],
+    ns = sum(k.startswith("scale_") for k in names)
+    return dict(means=rows[:, [col["x"], col["y"], col["z"]]], scales=rows[:, [col[f"scale_{i}"] for i in range(ns)]],
                 quats=rows[:, [col[f"rot_{i}"] for i in range(4)]],
                 features_dc=rows[:, [col[f"f_dc_{i}"] for i in range(3)]],
                 features_rest=fr.reshape(n, nfr, 3), opacities=rows[:, [col["opacity"]]], names=names)

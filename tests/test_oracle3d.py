@@ -245,3 +245,116 @@ def test_project3d_backward_matches_finite_differences(orc):
             assert out["dfrest"][i].reshape(-1)[k] == pytest.approx(fd(4, k), rel=2e-3, abs=1e-6)
         # the densification statistic is dL/dxy in NDC units
         assert out["dmean2d"][i] == pytest.approx([g9[i, 0] * c["W"] / 2, g9[i, 1] * c["H"] / 2], rel=1e-6)
+
+
+# ---- densification with three scales --------------------------------------
+STRIDES3 = (3, 3, 4, 3, 45, 1)
+
+
+def _dens_inputs(n=64, seed=5):
+    rng = np.random.default_rng(seed)
+    cap = 4 * n + 8
+    p = dict(means=rng.uniform(-1, 1, (n, 3)), scales=rng.uniform(-4.5, -2.5, (n, 3)),
+             quats=rng.normal(0, 1, (n, 4)), features_dc=rng.normal(0, 1, (n, 3)),
+             features_rest=rng.normal(0, 0.1, (n, 45)), opacities=rng.uniform(-1, 3, (n, 1)))
+    keys = ("means", "scales", "quats", "features_dc", "features_rest", "opacities")
+    params = []
+    for k, s in zip(keys, STRIDES3):
+        a = np.zeros(cap * s, np.float32)
+        a[: n * s] = p[k].astype(np.float32).reshape(-1)
+        params.append(a)
+    m6 = [np.zeros(cap * s, np.float32) for s in STRIDES3]
+    v6 = [np.zeros(cap * s, np.float32) for s in STRIDES3]
+    stats = dict(grad_norm=rng.uniform(0, 0.004, n).astype(np.float32), vis=np.ones(n, np.float32),
+                 max2d=rng.uniform(0, 0.1, n).astype(np.float32))
+    rs = rng.normal(0, 1, (2 * n, 3)).astype(np.float32)
+    return n, cap, params, m6, v6, stats, rs
+
+
+def _quat_R(q):
+    w, x, y, z = np.asarray(q, np.float64) / np.linalg.norm(np.asarray(q, np.float64))
+    return np.array([[1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y)],
+                     [2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x)],
+                     [2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)]])
+
+
+def test_densify3d_children_sampled_along_three_axes(orc):
+    """Every split child sits at parent + R (r * exp(s)) with all three
+    axes (the surfel form drops the third), carries the parent's scales
+    minus log 1.6 on all three, and the split parent is culled."""
+    n, cap, params, m6, v6, stats, rs = _dens_inputs()
+    stats["grad_norm"][:] = 0.004  # all high-gradient
+    stats["max2d"][:] = 0.0  # no split by screen size
+    p0 = [a.copy() for a in params]
+    new = orc.densify(n, cap, params, m6, v6, 45, stats, rs, size_thresh=0.05, check_huge=0, cull_alpha=0.0,
+                      half_max_dim=100.0, scale_dim=3)
+    sc0 = p0[1][: 3 * n].reshape(n, 3).astype(np.float64)
+    large = np.exp(sc0).max(axis=1) > 0.05
+    split = large
+    ns, nd = int(split.sum()), int((~large).sum())
+    assert 0 < ns < n and nd > 0
+    assert new == n - ns + 2 * ns + nd
+    # compaction keeps order: survivors (non-split originals), then children, then dups
+    means = params[0][: 3 * new].reshape(new, 3).astype(np.float64)
+    scales = params[1][: 3 * new].reshape(new, 3).astype(np.float64)
+    m_orig = p0[0][: 3 * n].reshape(n, 3).astype(np.float64)
+    q_orig = p0[2][: 4 * n].reshape(n, 4)
+    base = n - ns
+    ords = np.flatnonzero(split)
+    third = []
+    for o, i in enumerate(ords):
+        R = _quat_R(q_orig[i])
+        for k in range(2):
+            c = base + 2 * o + k
+            local = R.T @ (means[c] - m_orig[i])
+            want = rs[2 * o + k].astype(np.float64) * np.exp(sc0[i])
+            assert np.allclose(local, want, rtol=2e-4, atol=2e-6 * np.abs(m_orig[i]).max()), (i, k)
+            third.append(abs(want[2]))
+            assert np.allclose(scales[c], sc0[i] - math.log(1.6), atol=1e-6)
+    assert max(third) > 1e-3  # the third axis moved children
+
+
+def test_densify3d_third_scale_classifies_and_culls(orc):
+    """A splat small in two axes but large in the third is split (large), not
+    duplicated; with check_huge it is culled by the third scale alone."""
+    n, cap, params, m6, v6, stats, rs = _dens_inputs(n=8)
+    sc = params[1][: 3 * n].reshape(n, 3)
+    sc[:, :] = np.log(0.001)
+    sc[0, 2] = np.log(0.5)
+    stats["grad_norm"][:] = 0.004
+    stats["max2d"][:] = 0.0
+    a = [x.copy() for x in params]
+    new = orc.densify(n, cap, a, [x.copy() for x in m6], [x.copy() for x in v6], 45, stats, rs, size_thresh=0.02,
+                      check_huge=0, cull_alpha=0.0, half_max_dim=100.0, scale_dim=3)
+    assert new == (n - 1) + 2 + (n - 1)  # one split (two children), seven dups
+    b = [x.copy() for x in params]
+    sc_b = b[1][: 3 * n].reshape(n, 3)
+    sc_b[0, 2] = np.log(0.9)
+    stats["grad_norm"][:] = 0.0  # no densification, cull only
+    new = orc.densify(n, cap, b, [x.copy() for x in m6], [x.copy() for x in v6], 45, stats, rs, check_huge=1,
+                      cull_scale=0.5, cull_alpha=0.0, half_max_dim=100.0, scale_dim=3)
+    assert new == n - 1
+    assert np.array_equal(b[0][: 3 * (n - 1)], params[0][3: 3 * n])
+
+
+def test_densify3d_reduces_to_surfels_when_the_third_scale_vanishes(orc):
+    """With exp(third scale) = 0 the 3-scale densify equals the surfel one
+    bit for bit on every other buffer (the offsets' third term is exactly 0)."""
+    n, cap, params, m6, v6, stats, rs = _dens_inputs(n=96, seed=9)
+    sc3 = params[1][: 3 * n].reshape(n, 3)
+    sc3[:, 2] = -200.0
+    assert orc.expf(-200.0) == 0.0
+    two = [a.copy() for a in params]
+    two[1] = np.zeros(cap * 2, np.float32)
+    two[1][: 2 * n] = sc3[:, :2].reshape(-1)
+    m2 = [np.zeros(cap * s, np.float32) for s in (3, 2, 4, 3, 45, 1)]
+    v2 = [np.zeros(cap * s, np.float32) for s in (3, 2, 4, 3, 45, 1)]
+    three = [a.copy() for a in params]
+    n3 = orc.densify(n, cap, three, m6, v6, 45, stats, rs, half_max_dim=300.0, scale_dim=3)
+    n2 = orc.densify(n, cap, two, m2, v2, 45, stats, rs, half_max_dim=300.0, scale_dim=2)
+    assert n3 == n2 and n3 != n
+    for g in (0, 2, 3, 4, 5):
+        s = STRIDES3[g]
+        assert np.array_equal(three[g][: n3 * s], two[g][: n3 * s]), g
+    s3 = three[1][: 3 * n3].reshape(n3, 3)
+    assert np.array_equal(s3[:, :2].reshape(-1), two[1][: 2 * n3])
