@@ -313,8 +313,9 @@ int64_t msplat_hip_last_pairs_evaluated(void);
  * blended the gaussian; 0 for a forward without the log), out[2] =
  * (pixel, gaussian) pairs blended, out[3] = (wave, gaussian) visits,
  * out[4] = visit slots (per 256-entry batch, four times the largest wave's
- * visit count: the visits the batch's barriers allow for).  No counterpart
- * in the reference: it measures the rasterizers' work. */
+ * visit count: the visits the batch's barriers allow for); all zero after
+ * a 3DGS forward.  No counterpart in the reference: it measures the
+ * rasterizers' work. */
 int msplat_hip_last_raster_counts(int64_t out[5]);
 /* Self-check of the rasterizer's arithmetic: *mismatches receives the
  * number of floats with exponent field efield_lo..efield_hi (1..254, both

@@ -5,6 +5,7 @@
 // (core/metal/msplat_metal.mm:545-1594).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cmath>
 #include <cstdarg>
@@ -360,6 +361,8 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     stage_mark(ST_PROJECT);
     HIPC(hipMemsetAsync(E.stats.p, 0, 64, s));
     if (E.count_pairs) HIPC(hipMemsetAsync(E.pair_counter.p, 0, 40, s));
+    // the 3DGS rasterizers count nothing: no counters for this forward
+    if (gs3d) std::fill(E.pairs, E.pairs + 5, int64_t(0));
     if (gs3d)
         mskern::launch_project3d_fwd(s, *cam, *g, P<float>(E.rec), P<float>(E.rec) + (size_t)N * mskern::kRec3Floats,
                                      P<float>(E.depths), P<int>(E.radii), P<uint32_t>(E.rect),

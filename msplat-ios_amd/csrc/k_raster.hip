@@ -267,7 +267,7 @@ struct BwdLds<true> {
 template <>
 struct BwdLds<false> {
     float4 r[4][4][64];
-    float red[4][256];
+    float red[4][512];
 };
 
 template <bool FULL>
@@ -283,7 +283,7 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     constexpr int kWave = 64;
     // per wave: the staged entries' record planes (the image-only path
     // stages 4, the full one 7) and the log entries (full) or the reduction
-    // scratch (image-only, wave_reduce16_lds); 20 KB per workgroup for the
+    // scratch (image-only, wave_reduce16_lds8); 24 KB per workgroup for the
     // image-only kernel
     __shared__ BwdLds<FULL> L;
     auto &s_r = L.r;
@@ -297,14 +297,10 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     const float px = (float)pxi, py = (float)pyi;
     const int start = offsets[tile], len = offsets[tile + 1] - start;
     const int nlog = __builtin_amdgcn_readfirstlane(wave_cnt[4 * tile + wave]);
-    float *red_wa[4];
-    const float4 *red_ra = nullptr;
+    Red8 red8;
     if (!FULL) {
-        const int q = lane >> 4, jj = lane & 15, ri = (lane >> 2) & 3, rk = lane & 3;
-        float *red = reinterpret_cast<float *>(&L) + sizeof(L.r) / sizeof(float) + wave * 256;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) red_wa[i] = red + i * 64 + (((q ^ i) & 3) << 4) + jj;
-        red_ra = reinterpret_cast<const float4 *>(red + ri * 64 + (((q ^ ri) & 3) << 4) + 4 * rk);
+        red8.init(reinterpret_cast<float *>(&L) + sizeof(L.r) / sizeof(float) + wave * 512, lane);
+        red8.zero_skipped<0x08>();
     }
     const size_t log_base = 4 * (size_t)start + (size_t)wave * (size_t)len;
     const uint4 *lg = blend_log + log_base;
@@ -536,7 +532,7 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 v16[8] = px * dk.z + py * dl.z + dL_dz;
                 v16[12] = G * dL_dG * (1.0f - opa);
             }
-            const float s = FULL ? wave_reduce16(v16, lane) : wave_reduce16_lds<0x08>(v16, red_wa, red_ra);
+            const float s = FULL ? wave_reduce16(v16, lane) : wave_reduce16_lds8<0x08>(v16, red8);
             if ((lane & 3) == 0 && s != 0.f) unsafeAtomicAdd(&grads16[(size_t)e.w * 16 + gi], s);
         }
         wave_lds_sync();

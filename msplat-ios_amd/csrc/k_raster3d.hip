@@ -142,7 +142,8 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_fwd(int W, int H, int til
 // grads16 row (slots 0..8) with one 16-lane atomic; launch_finish3d_grads /
 // k_project3d_bwd turn them into the raster gradients (finish3d_grads).
 // The sums go to reduction slots 0..4 and 8..11, so three first-stage
-// pairs of the reduction are empty and skipped.
+// pairs of the reduction are empty and skipped (their scratch rows hold
+// zeros).
 __global__ __launch_bounds__(kThreads) void k_raster3d_bwd(int W, int H, int tiles_x, int T,
                                                            const int *__restrict__ offsets,
                                                            const uint4 *__restrict__ blend_log,
@@ -157,7 +158,7 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_bwd(int W, int H, int til
     if (tile < 0) return;
     constexpr int kWave = 64;
     __shared__ float4 s_r[4][3][64];
-    __shared__ float s_red[4][256];
+    __shared__ float s_red[4][512];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tx = tile % tiles_x, ty = tile / tiles_x;
@@ -167,15 +168,9 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_bwd(int W, int H, int til
     const float px = (float)pxi, py = (float)pyi;
     const int start = offsets[tile], len = offsets[tile + 1] - start;
     const int nlog = __builtin_amdgcn_readfirstlane(wave_cnt[4 * tile + wave]);
-    float *red_wa[4];
-    const float4 *red_ra;
-    {
-        const int q = lane >> 4, jj = lane & 15, ri = (lane >> 2) & 3, rk = lane & 3;
-        float *red = &s_red[wave][0];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) red_wa[i] = red + i * 64 + (((q ^ i) & 3) << 4) + jj;
-        red_ra = reinterpret_cast<const float4 *>(red + ri * 64 + (((q ^ ri) & 3) << 4) + 4 * rk);
-    }
+    Red8 red8;
+    red8.init(&s_red[wave][0], lane);
+    red8.zero_skipped<0xE0>();
     const size_t log_base = 4 * (size_t)start + (size_t)wave * (size_t)len;
     const uint4 *lg = blend_log + log_base;
     const size_t pix = inside ? (size_t)pyi * W + pxi : 0;
@@ -241,7 +236,7 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_bwd(int W, int H, int til
             v16[13] = 0.f;
             v16[14] = 0.f;
             v16[15] = 0.f;
-            const float s = wave_reduce16_lds<0xE0>(v16, red_wa, red_ra);
+            const float s = wave_reduce16_lds8<0xE0>(v16, red8);
             if ((lane & 3) == 0 && s != 0.f) unsafeAtomicAdd(&grads16[(size_t)e.w * 16 + gi], s);
         }
         wave_lds_sync();
