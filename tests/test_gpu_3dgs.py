@@ -381,3 +381,30 @@ def test_full_step3d_matches_oracle_full_size(workload, orc, eng):
         assert np.array_equal(got_m[g], m), name
     for k in got_s:
         assert np.array_equal(got_s[k], ref[k]), k
+
+
+def test_empty_and_culled_scenes_3dgs(orc, eng):
+    """No Gaussians, and Gaussians all behind the camera: the frame is the
+    background, no intersection is emitted, and a training step gives a
+    finite loss, zero raster gradients and unchanged parameters."""
+    from msplat import _engine as E
+    from msplat import device as D
+    p, c = _scene(5, 300, 64, 48)
+    bg = np.float32([0.3, 0.6, 0.9])
+    ocam, gcam = _cams(orc, eng, c)
+    gt = E.DeviceArray.from_numpy(np.full((48, 64, 3), 0.5, np.float32))
+    empty = {k: v[:0] for k, v in p.items()}
+    behind = dict(p)
+    behind["means"] = p["means"] + np.float32([0.0, 0.0, 5.0])  # the camera sits at z = 3.2 looking down -z
+    for name, params in (("empty", empty), ("behind", behind)):
+        ds = D.DeviceScene3D(params, bg)
+        out = D.render3d(ds, gcam)
+        assert out["num_intersections"] == 0, name
+        assert np.array_equal(out["out_img"], np.broadcast_to(bg, out["out_img"].shape)), name
+        loss, nis = D.train_step3d(ds, gcam, gt)
+        assert nis == 0 and np.isfinite(loss), name
+        if params["means"].shape[0]:
+            assert np.array_equal(eng.last("radii", (300,)), np.zeros(300, np.int32))
+            assert not eng.last("grads16", (300, 16))[:, :9].any()
+            for g, k in enumerate(GROUPS):
+                assert np.array_equal(ds.params[g].numpy(), params[k]), k
