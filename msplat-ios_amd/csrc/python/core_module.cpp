@@ -241,7 +241,7 @@ PYBIND11_MODULE(_core, m) {
             },
             "index"_a, "Get camera-to-world pose (4x4 row-major, OpenGL convention) as numpy array.");
 
-    py::class_<Trainer>(m, "GaussianTrainer", "2D Gaussian Splatting trainer. All computation runs on the GPU.")
+    py::class_<Trainer>(m, "GaussianTrainer", "Gaussian Splatting trainer (2DGS surfels, or 3D Gaussians with primitive='3dgs'). All computation runs on the GPU.")
         .def(py::init<msplat::Dataset &, const TrainingConfig &, const std::string &>(), "dataset"_a, "config"_a,
              "primitive"_a = "2dgs", py::keep_alive<1, 2>(),
              "primitive: '2dgs' (surfels, the default) or '3dgs' (3D Gaussians; no mesh or point-cloud export).")
@@ -345,7 +345,7 @@ PYBIND11_MODULE(_core, m) {
             std::memcpy(a.mutable_data(), im.ptr(), im.data.size() * sizeof(float));
             return a;
         },
-        "path"_a, "Decode an image file the way datasets do (PNG / PPM / PGM) to (H, W, 3) float32 in [0, 1].");
+        "path"_a, "Decode an image file the way datasets do (PNG / PPM / PGM / JPEG) to (H, W, 3) float32 in [0, 1].");
     m.def("sync", &msplat::sync, "Synchronize GPU (wait for all commands to complete)");
     m.def("cleanup", &msplat::cleanup, "Release all cached GPU resources");
 }

@@ -96,6 +96,35 @@ def test_python_surface_matches_reference_stubs():
         msplat.load_dataset("/nonexistent/dataset")
 
 
+def test_core_stub_matches_module():
+    """msplat/_core.pyi declares exactly the module's public classes,
+    functions, methods and properties."""
+    import ast
+
+    from msplat import _core
+
+    stub = ast.parse((REPO / "msplat-ios_amd" / "msplat" / "_core.pyi").read_text())
+    declared = {}
+    for node in stub.body:
+        if isinstance(node, ast.ClassDef):
+            members = set()
+            for item in node.body:
+                if isinstance(item, ast.FunctionDef) and not item.name.startswith("__"):
+                    members.add(item.name)
+                elif isinstance(item, ast.AnnAssign):
+                    members.add(item.target.id)
+            declared[node.name] = members
+        elif isinstance(node, ast.FunctionDef):
+            declared[node.name] = None
+    public = {n for n in dir(_core) if not n.startswith("_")}
+    assert set(declared) == public
+    for name, members in declared.items():
+        if members is None:
+            continue
+        actual = {m for m in dir(getattr(_core, name)) if not m.startswith("_")}
+        assert members == actual, (name, members ^ actual)
+
+
 # ---------------------------------------------------------------- images --
 
 def _png(path: Path, rows: np.ndarray, color_type: int, depth: int, palette=None, interlace=False, filters=None):
