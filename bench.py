@@ -69,15 +69,25 @@ def algorithmic_bytes(stage: str, N: int, I: int, P: int, T: int) -> float:
 
 
 def profile_record(kind: str, stage: str, workload: str):
-    """A `bench-<kind>:` record for (stage, workload) from the committed
-    rocprofv3 summaries under profiles/ (None when none covers it)."""
+    """The `bench-<kind>:` records for (stage, workload) from the committed
+    rocprofv3 summaries under profiles/, merged over the stage's kernels
+    (instruction counts and bytes summed, kernel names joined); None when
+    none covers it."""
+    recs = []
     for f in sorted((REPO / "profiles").glob("*.md")):
         for line in f.read_text().splitlines():
             if line.startswith(f"bench-{kind}:"):
                 rec = json.loads(line.split(":", 1)[1])
                 if rec.get("stage") == stage and rec.get("workload") == workload:
-                    return rec
-    return None
+                    recs.append(rec)
+    if not recs:
+        return None
+    out = dict(recs[0])
+    out["kernel"] = " + ".join(r["kernel"] for r in recs)
+    for key in ("valu_insts", "salu_insts", "waves", "bytes"):
+        if key in out:
+            out[key] = sum(r[key] for r in recs)
+    return out
 
 
 def copy_calibration(mib: int) -> int:
@@ -562,6 +572,24 @@ def kernel_table(stage_ms: dict, N: int, I: int, P: int, T: int, workload: str) 
     return kernels
 
 
+def issue_table(stage_ms: dict, workload: str) -> dict:
+    """Stage times with, where the committed profiles hold the stage's
+    kernel counters, the VALU issue fraction and the measured HBM rate (the
+    3DGS mode: its algorithmic bytes differ from the 2DGS table's)."""
+    out = {}
+    for name, ms in stage_ms.items():
+        row = {"ms": round(ms, 4), "bound": BOUND.get(name, "hbm")}
+        cnt = profile_record("counters", name, workload)
+        if cnt is not None and ms > 0:
+            row["kernel"] = cnt["kernel"]
+            row["frac_valu_issue"] = round(cnt["valu_insts"] * VALU_NS_PER_INST * 1e-9 / (ms * 1e-3 * 1024), 4)
+        tr = profile_record("traffic", name, workload)
+        if tr is not None and ms > 0:
+            row["hbm_GB_per_s_measured"] = round(tr["bytes"] / (ms * 1e-3) / 1e9, 1)
+        out[name] = row
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -696,7 +724,7 @@ def main() -> int:
                               "ms_per_step": round(r3["ms_per_step"], 3),
                               "render_fps": round(1000.0 / r3["render_ms"], 2),
                               "render_ms": round(r3["render_ms"], 3),
-                              "stage_ms": {k: round(v, 4) for k, v in r3["stage_ms"].items()},
+                              "kernels": issue_table(r3["stage_ms"], sc3.name),
                               "loss_first_last": [round(r3["losses"][0], 6), round(r3["losses"][-1], 6)]}
         log(f"{sc3.name}: {r3['ms_per_step']:.3f} ms/step, render {r3['render_ms']:.3f} ms")
         del r3
