@@ -113,6 +113,36 @@ def log(msg: str) -> None:
 
 
 # ------------------------------------------------------------------ GPU --
+def _timed_steps(E, step, first: int, steps: int, ncams: int):
+    """Exactly `steps` train steps (cameras first, first + 1, ... cyclic)
+    between two device synchronisations, with the engine's stage timing
+    off.  Returns (ms per step, losses, intersection counts)."""
+    losses, isect = [], []
+    E.enable_timing(False)
+    E.sync()
+    t0 = time.perf_counter()
+    for k in range(steps):
+        loss, nis = step((first + k) % ncams)
+        losses.append(loss)
+        isect.append(nis)
+    E.sync()
+    return (time.perf_counter() - t0) * 1e3 / steps, losses, isect
+
+
+def _stage_breakdown(E, step, first: int, steps: int, ncams: int) -> dict[str, float]:
+    """Mean per-stage milliseconds (HIP events on the engine stream around
+    every stage) over `steps` further train steps, outside the timed run."""
+    total: dict[str, float] = {}
+    E.enable_timing(True)
+    for k in range(steps):
+        step((first + k) % ncams)
+        for name, ms in E.stage_times().items():
+            total[name] = total.get(name, 0.0) + ms
+    E.enable_timing(False)
+    return {k: v / steps for k, v in total.items()}
+
+
+
 def gpu_train(workload: int, steps: int, warmup: int, render_frames: int, counters: bool):
     """Train steps (timed between synchronisations, HIP events per stage)
     and device-resident render frames of one workload."""
@@ -129,23 +159,12 @@ def gpu_train(workload: int, steps: int, warmup: int, render_frames: int, counte
     E.sync()
     for k in range(warmup):
         D.train_step(ds, cams[k % len(cams)], gts[k % len(cams)])
-    E.enable_timing(True)
-    E.sync()
-    stage_sum: dict[str, float] = {}
-    isect, losses = [], []
-    t0 = time.perf_counter()
-    for k in range(steps):
-        ci = (warmup + k) % len(cams)
-        loss, nis = D.train_step(ds, cams[ci], gts[ci])
-        losses.append(loss)
-        isect.append(nis)
-        for name, ms in E.stage_times().items():
-            stage_sum[name] = stage_sum.get(name, 0.0) + ms
-    E.sync()
-    ms_per_step = (time.perf_counter() - t0) * 1e3 / steps
-    E.enable_timing(False)
+    ms_per_step, losses, isect = _timed_steps(E, lambda ci: D.train_step(ds, cams[ci], gts[ci]), warmup, steps,
+                                              len(cams))
+    stage_ms = _stage_breakdown(E, lambda ci: D.train_step(ds, cams[ci], gts[ci]), warmup + steps,
+                                min(steps, 10), len(cams))
     out = dict(scene=scene, ds=ds, cams=cams, ms_per_step=ms_per_step, losses=losses,
-               isect=float(np.mean(isect)), stage_ms={k: v / steps for k, v in stage_sum.items()})
+               isect=float(np.mean(isect)), stage_ms=stage_ms)
     if counters:
         # two untimed steps with the raster work counters on
         E.enable_timing(False, pairs=True)
@@ -177,21 +196,10 @@ def gpu_train3d(workload: int, steps: int, warmup: int, render_frames: int):
     E.sync()
     for k in range(warmup):
         D.train_step3d(ds, cams[k % len(cams)], gts[k % len(cams)])
-    E.enable_timing(True)
-    E.sync()
-    stage_sum: dict[str, float] = {}
-    isect, losses = [], []
-    t0 = time.perf_counter()
-    for k in range(steps):
-        ci = (warmup + k) % len(cams)
-        loss, nis = D.train_step3d(ds, cams[ci], gts[ci])
-        losses.append(loss)
-        isect.append(nis)
-        for name, ms in E.stage_times().items():
-            stage_sum[name] = stage_sum.get(name, 0.0) + ms
-    E.sync()
-    ms_per_step = (time.perf_counter() - t0) * 1e3 / steps
-    E.enable_timing(False)
+    ms_per_step, losses, isect = _timed_steps(E, lambda ci: D.train_step3d(ds, cams[ci], gts[ci]), warmup, steps,
+                                              len(cams))
+    stage_ms = _stage_breakdown(E, lambda ci: D.train_step3d(ds, cams[ci], gts[ci]), warmup + steps,
+                                min(steps, 10), len(cams))
     del gts
     n = E.C.c_int64()
     for k in range(3):
@@ -205,7 +213,7 @@ def gpu_train3d(workload: int, steps: int, warmup: int, render_frames: int):
     E.sync()
     render_ms = (time.perf_counter() - t0) * 1e3 / max(render_frames, 1)
     return dict(scene=scene, ms_per_step=ms_per_step, losses=losses, isect=float(np.mean(isect)),
-                stage_ms={k: v / steps for k, v in stage_sum.items()}, render_ms=render_ms)
+                stage_ms=stage_ms, render_ms=render_ms)
 
 
 def gpu_render_ms(ds, cams, frames: int) -> float:

@@ -4,15 +4,23 @@ core/src/model.cpp:546-554 and 762-829, driven from Python)."""
 from __future__ import annotations
 
 import ctypes as C
+import math
+import struct
 
 import numpy as np
 
 from . import _engine as E
 from .synthetic import Camera, Scene
 
+def _f32(x: float) -> float:
+    """x rounded to float32."""
+    return struct.unpack("f", struct.pack("f", x))[0]
+
+
 # Model::setupOptimizers learning rates (core/src/model.cpp:142).
 LR_INIT = (0.00016, 0.005, 0.001, 0.0025, 0.000125, 0.05)
 BETA1, BETA2, EPS = 0.9, 0.999, 1e-8
+_F32_BETA1, _F32_BETA2 = _f32(BETA1), _f32(BETA2)
 GROUPS = ("means", "scales", "quats", "features_dc", "features_rest", "opacities")
 
 
@@ -48,17 +56,22 @@ class DeviceScene:
 
     def adam_struct(self) -> E.MsplatAdam:
         """Advances the Adam step and returns the fused-update arguments
-        (bias corrections computed as Model::fullIteration does)."""
+        (bias corrections computed as Model::fullIteration does: the power
+        in double, then float32)."""
         self.adam_step += 1
-        bc1 = np.float32(1.0 - np.power(np.float64(np.float32(BETA1)), self.adam_step))
-        bc2 = np.float32(1.0 - np.power(np.float64(np.float32(BETA2)), self.adam_step))
-        a = E.MsplatAdam()
+        bc1 = _f32(1.0 - _F32_BETA1 ** self.adam_step)
+        bc2 = _f32(1.0 - _F32_BETA2 ** self.adam_step)
+        a = getattr(self, "_adam", None)
+        if a is None:
+            a = self._adam = E.MsplatAdam()
+            a.beta1, a.beta2, a.eps = BETA1, BETA2, EPS
         for g in range(6):
             a.exp_avg[g] = self.exp_avg[g].ptr
             a.exp_avg_sq[g] = self.exp_avg_sq[g].ptr
-            a.step_size[g] = float(np.float32(np.float32(self.lr[g]) / bc1))
-        a.beta1, a.beta2, a.eps = BETA1, BETA2, EPS
-        a.bc2_sqrt = float(np.sqrt(bc2, dtype=np.float32))
+            # float32 lr / bc1 and sqrt(bc2), rounded once from double (exact
+            # for a quotient or root of float32 operands)
+            a.step_size[g] = _f32(_f32(self.lr[g]) / bc1)
+        a.bc2_sqrt = _f32(math.sqrt(bc2))
         return a
 
 
