@@ -29,6 +29,41 @@ __device__ __forceinline__ void stage_rows(float *__restrict__ dst, const float 
     }
 }
 
+// LDS of the projection forwards: half a block's features_rest rows (128 x
+// 45 floats), reused to stage the outgoing records (up to 5 float4 per
+// thread).  23 KB, so six workgroups share a CU.
+constexpr int kStageRows = kBlock / 2;
+constexpr int kStageFloats = kStageRows * 45;
+static_assert(kStageFloats * 4 >= kBlock * 5 * 16, "record staging fits the SH staging buffer");
+
+// The colour of this thread's splat (sh_coeffs_to_color, sh_eval) with the
+// block's features_rest rows staged through s_fr with coalesced loads, half
+// the block's rows at a time: threads [0, 128) evaluate from the first half,
+// then [128, 256) from the second.  Rows of more than 45 floats (degree 4)
+// are read from global memory.  Called by every thread of the block (it
+// holds barriers); threads with `active` false only take part in them.
+__device__ __forceinline__ void sh_color_staged(const MsplatCamera &cam, int K3, int b0, int cnt,
+                                                const float *__restrict__ frest, const float *__restrict__ fdc,
+                                                const float p[3], bool active, float *s_fr, float col[3]) {
+    const int i = b0 + (int)threadIdx.x;
+    const f3 dir = normalize3({p[0] - cam.cam_pos[0], p[1] - cam.cam_pos[1], p[2] - cam.cam_pos[2]});
+    const float *dc = fdc + 3 * (size_t)(active ? i : 0);
+    if (cam.degrees_to_use <= 0 || K3 > 45) {
+        if (active) sh_eval(cam.degrees_to_use, dir, dc, frest + (size_t)K3 * i, col);
+        return;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int r0 = h * kStageRows, rows = min(kStageRows, cnt - r0);
+        if (rows <= 0) break;  // uniform
+        if (h) __syncthreads();
+        stage_rows(s_fr, frest + (size_t)(b0 + r0) * K3, rows * K3);
+        __syncthreads();
+        const int t = (int)threadIdx.x - r0;
+        if (active && t >= 0 && t < kStageRows) sh_eval(cam.degrees_to_use, dir, dc, s_fr + t * K3, col);
+    }
+}
+
 // project_and_sh_forward_2dgs_kernel (msplat_metal.metal:1413-1521), with
 // the sigmoid of the sort/pack stage (:1684) and the raster's colour clamp
 // (:619) folded into the record.  Also sums the visible splats' tile
@@ -40,16 +75,13 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
     const float *__restrict__ frest, float4 *__restrict__ rec, float4 *__restrict__ mrec, float *__restrict__ depths,
     int *__restrict__ radii, uint2 *__restrict__ rect, unsigned long long *__restrict__ isect_total,
     float *__restrict__ colors_raw) {
-    // The block's features_rest rows (up to 256 x 45 floats) are staged in LDS
-    // with coalesced loads; each thread then reads its own row from LDS.
-    __shared__ float s_fr[kBlock * 45];
+    // The block's features_rest rows (up to 45 floats each) pass through LDS
+    // with coalesced loads, half a block's rows at a time (sh_color_staged);
+    // the same 23 KB then stage the outgoing records.
+    __shared__ float s_fr[kStageFloats];
     const int K3 = (num_sh_bases(cam.degree) - 1) * 3;
     const int b0 = blockIdx.x * kBlock;
     const int cnt = min(kBlock, n - b0);
-    if (cam.degrees_to_use > 0 && K3 <= 45) {
-        stage_rows(s_fr, frest + (size_t)b0 * K3, cnt * K3);
-        __syncthreads();
-    }
     // No early return: every thread takes part in the intersection sum.
     const int i = blockIdx.x * kBlock + threadIdx.x;
     const bool valid = i < n;
@@ -116,52 +148,53 @@ __global__ __launch_bounds__(kBlock) void k_project_fwd(
                 colors_raw[3 * (size_t)i] = colors_raw[3 * (size_t)i + 1] = colors_raw[3 * (size_t)i + 2] = 0.f;
             }
         }
-    } else {
-    const f3 dir = normalize3({p[0] - cam.cam_pos[0], p[1] - cam.cam_pos[1], p[2] - cam.cam_pos[2]});
+    }
     float col[3];
-    const float *fr_row = K3 <= 45 ? s_fr + threadIdx.x * K3 : frest + (size_t)K3 * i;
-    sh_eval(cam.degrees_to_use, dir, fdc + 3 * (size_t)i, fr_row, col);
-    const float opa = ms_sigmoid(opac[i]);
+    sh_color_staged(cam, K3, b0, cnt, frest, fdc, p, ok, s_fr, col);
+    if (ok) {
+        const float opa = ms_sigmoid(opac[i]);
 
-    radii[i] = (int)radius;
-    depths[i] = pz;
-    rect[i] = make_uint2((uint32_t)x0 | ((uint32_t)y0 << 16), (uint32_t)x1 | ((uint32_t)y1 << 16));
-    const float4 q0 = make_float4(T0.x, T0.y, T0.z, T1.x), q1 = make_float4(T1.y, T1.z, T2.x, T2.y),
-                 q2 = make_float4(T2.z, cxp, cyp, opa);
-    // the splat-only part of the rasterizer's quadrant-mask test
-    const float tau = splat_reach(opa);
-    f3 CR0, CAx, CAy;
-    centred_rows(T0, T1, T2, cxp, cyp, CR0, CAx, CAy);
-    float lp_r2;
-    const MaskRec mr = mask_record(q0, q1, q2, tau, CR0, CAx, CAy, x0, y0, x1, y1, lp_r2);
-    ro[0] = q0;
-    ro[1] = q1;
-    ro[2] = q2;
-    ro[3] = make_float4(R2.x, R2.y, R2.z, __builtin_fmaxf(col[0] + 0.5f, 0.0f));
-    ro[4] = make_float4(__builtin_fmaxf(col[1] + 0.5f, 0.0f), __builtin_fmaxf(col[2] + 0.5f, 0.0f), tau, lp_r2);
-    mo[0] = mr.box;
-    mo[1] = mr.e;
-    mo[2] = mr.h;
-    if (colors_raw) {
-        colors_raw[3 * (size_t)i] = col[0];
-        colors_raw[3 * (size_t)i + 1] = col[1];
-        colors_raw[3 * (size_t)i + 2] = col[2];
+        radii[i] = (int)radius;
+        depths[i] = pz;
+        rect[i] = make_uint2((uint32_t)x0 | ((uint32_t)y0 << 16), (uint32_t)x1 | ((uint32_t)y1 << 16));
+        const float4 q0 = make_float4(T0.x, T0.y, T0.z, T1.x), q1 = make_float4(T1.y, T1.z, T2.x, T2.y),
+                     q2 = make_float4(T2.z, cxp, cyp, opa);
+        // the splat-only part of the rasterizer's quadrant-mask test
+        const float tau = splat_reach(opa);
+        f3 CR0, CAx, CAy;
+        centred_rows(T0, T1, T2, cxp, cyp, CR0, CAx, CAy);
+        float lp_r2;
+        const MaskRec mr = mask_record(q0, q1, q2, tau, CR0, CAx, CAy, x0, y0, x1, y1, lp_r2);
+        ro[0] = q0;
+        ro[1] = q1;
+        ro[2] = q2;
+        ro[3] = make_float4(R2.x, R2.y, R2.z, __builtin_fmaxf(col[0] + 0.5f, 0.0f));
+        ro[4] = make_float4(__builtin_fmaxf(col[1] + 0.5f, 0.0f), __builtin_fmaxf(col[2] + 0.5f, 0.0f), tau, lp_r2);
+        mo[0] = mr.box;
+        mo[1] = mr.e;
+        mo[2] = mr.h;
+        if (colors_raw) {
+            colors_raw[3 * (size_t)i] = col[0];
+            colors_raw[3 * (size_t)i + 1] = col[1];
+            colors_raw[3 * (size_t)i + 2] = col[2];
+        }
     }
-    }
-    // The block's records leave as contiguous rows: each thread's 5 + 3
-    // float4 go through LDS (the staged SH rows are no longer needed), then
-    // every store instruction writes 1 KB of consecutive float4s.
+    // The block's records leave as contiguous rows: each thread's 5 float4
+    // (then its 3 mask float4) go through LDS, and every store instruction
+    // writes 1 KB of consecutive float4s.
     {
         float4 *s4 = reinterpret_cast<float4 *>(s_fr);
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < 5; ++k) s4[5 * threadIdx.x + k] = ro[k];
-#pragma unroll
-        for (int k = 0; k < 3; ++k) s4[5 * kBlock + 3 * threadIdx.x + k] = mo[k];
         __syncthreads();
         float4 *rdst = rec + 5 * (size_t)b0, *mdst = mrec + 3 * (size_t)b0;
         for (int e = threadIdx.x; e < 5 * cnt; e += kBlock) rdst[e] = s4[e];
-        for (int e = threadIdx.x; e < 3 * cnt; e += kBlock) mdst[e] = s4[5 * kBlock + e];
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 3; ++k) s4[3 * threadIdx.x + k] = mo[k];
+        __syncthreads();
+        for (int e = threadIdx.x; e < 3 * cnt; e += kBlock) mdst[e] = s4[e];
     }
     // intersections: sum of the rectangle areas over the workgroup
     __shared__ unsigned long long s_area[kBlock / 64];
@@ -581,14 +614,10 @@ __global__ __launch_bounds__(kBlock) void k_project3d_fwd(
     const float *__restrict__ frest, float4 *__restrict__ rec, float4 *__restrict__ boxes,
     float *__restrict__ depths, int *__restrict__ radii, uint2 *__restrict__ rect,
     unsigned long long *__restrict__ isect_total, float *__restrict__ colors_raw) {
-    __shared__ float s_fr[kBlock * 45];
+    __shared__ float s_fr[kStageFloats];
     const int K3 = (num_sh_bases(cam.degree) - 1) * 3;
     const int b0 = blockIdx.x * kBlock;
     const int cnt = min(kBlock, n - b0);
-    if (cam.degrees_to_use > 0 && K3 <= 45) {
-        stage_rows(s_fr, frest + (size_t)b0 * K3, cnt * K3);
-        __syncthreads();
-    }
     const int i = blockIdx.x * kBlock + threadIdx.x;
     const bool valid = i < n;
     const int ii = valid ? i : 0;
@@ -638,11 +667,10 @@ __global__ __launch_bounds__(kBlock) void k_project3d_fwd(
             rect[i] = make_uint2(0u, 0u);
             if (colors_raw) colors_raw[3 * (size_t)i] = colors_raw[3 * (size_t)i + 1] = colors_raw[3 * (size_t)i + 2] = 0.f;
         }
-    } else {
-        const f3 dir = normalize3({p[0] - cam.cam_pos[0], p[1] - cam.cam_pos[1], p[2] - cam.cam_pos[2]});
-        float col[3];
-        const float *fr_row = K3 <= 45 ? s_fr + threadIdx.x * K3 : frest + (size_t)K3 * i;
-        sh_eval(cam.degrees_to_use, dir, fdc + 3 * (size_t)i, fr_row, col);
+    }
+    float col[3];
+    sh_color_staged(cam, K3, b0, cnt, frest, fdc, p, ok, s_fr, col);
+    if (ok) {
         const float opa = ms_sigmoid(opac[i]);
         radii[i] = (int)radius;
         depths[i] = pv[2];
