@@ -19,6 +19,9 @@
 #include "kernels.h"
 #include "msplat_engine.h"
 
+// host side (host/hostcopy.cpp): memcpy split over a few OpenMP threads
+void ms_parallel_memcpy(void *dst, const void *src, size_t bytes);
+
 // Scratch of msplat_hip_loss_fwd_bwd_noalloc, for callers that cannot
 // allocate: the three per-pixel SSIM partial maps (12 B per pixel each, at
 // fixed offsets sized for kNoAllocMaxPixels), then the per-workgroup loss
@@ -49,12 +52,18 @@ enum StageId { ST_PROJECT, ST_SCAN, ST_SCATTER_SORT, ST_RASTER_FWD, ST_LOSS, ST_
 const char *kStageNames[ST_COUNT] = {"project_fwd", "tile_scan", "scatter_sort", "raster_fwd",
                                      "ssim_l1",     "raster_bwd", "project_bwd_adam"};
 
+constexpr size_t kD2HChunk = size_t(8) << 20;  // bytes per pinned download chunk
+
 struct Engine {
     bool ready = false;
     int device = 0;
     hipStream_t stream = nullptr;
     int *pinned_i = nullptr;     // small pinned readback area
     double *pinned_d = nullptr;
+    // two pinned chunks of kD2HChunk bytes for large downloads (RGBA8
+    // frames) and the events of their DMAs
+    unsigned char *stage = nullptr;
+    hipEvent_t stage_ev[2] = {nullptr, nullptr};
     float window[11];
     // per-gaussian
     // rec: N splat records (MSPLAT_REC_FLOATS each), followed by their N
@@ -178,6 +187,8 @@ int init_locked() {
     HIPC(hipStreamCreateWithFlags(&g_eng.stream, hipStreamNonBlocking));
     HIPC(hipHostMalloc((void **)&g_eng.pinned_i, 64 * sizeof(int), hipHostMallocDefault));
     HIPC(hipHostMalloc((void **)&g_eng.pinned_d, 16 * sizeof(double), hipHostMallocDefault));
+    HIPC(hipHostMalloc((void **)&g_eng.stage, 2 * kD2HChunk, hipHostMallocDefault));
+    for (auto &e : g_eng.stage_ev) HIPC(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     for (int i = 0; i <= ST_COUNT; ++i) HIPC(hipEventCreate(&g_eng.ev[i]));
     // this device's copy of the no-allocation entry point's scratch array
     if (!g_scratch_dev[g_eng.device]) {
@@ -556,7 +567,7 @@ void msplat_hip_cleanup(void) {
                      &E.final_idx, &E.out_depth, &E.out_normal, &E.out_alpha, &E.out_median, &E.out_dist,
                      &E.dL_dimg, &E.gm1, &E.gs1, &E.gs12, &E.partials, &E.loss, &E.dmeans, &E.dscales,
                      &E.dquats, &E.dmean2d, &E.dfdc, &E.dfrest, &E.dens_flags, &E.dens_scan, &E.dens_keep, &E.pair_counter,
-                     &E.rgba};
+                     &E.rgba, &E.tsdf_views, &E.tsdf_masks, &E.mc_cases, &E.chunk_cnt, &E.chunk_off};
     for (DevBuf *b : all) {
         if (b->p) (void)hipFree(b->p);
         *b = DevBuf{};
@@ -669,8 +680,25 @@ int msplat_hip_image_to_rgba8(const float *img, int64_t num_pixels, uint8_t *rgb
     CHECK(ensure(E.rgba, (size_t)num_pixels * 4));
     mskern::launch_rgba8(E.stream, img, num_pixels, P<uint32_t>(E.rgba));
     HIPC(hipGetLastError());
-    HIPC(hipMemcpyAsync(rgba_host, E.rgba.p, (size_t)num_pixels * 4, hipMemcpyDeviceToHost, E.stream));
-    HIPC(hipStreamSynchronize(E.stream));
+    // chunked through the two pinned buffers: the DMA of chunk k + 1 runs
+    // while the host moves chunk k on to the caller's buffer
+    const size_t total = (size_t)num_pixels * 4;
+    const size_t nch = (total + kD2HChunk - 1) / kD2HChunk;
+    const unsigned char *src = P<unsigned char>(E.rgba);
+    auto issue = [&](size_t k) -> int {
+        const size_t off = k * kD2HChunk, len = std::min(kD2HChunk, total - off);
+        HIPC(hipMemcpyAsync(E.stage + (k & 1) * kD2HChunk, src + off, len, hipMemcpyDeviceToHost, E.stream));
+        HIPC(hipEventRecord(E.stage_ev[k & 1], E.stream));
+        return MSPLAT_OK;
+    };
+    CHECK(issue(0));
+    if (nch > 1) CHECK(issue(1));
+    for (size_t k = 0; k < nch; ++k) {
+        HIPC(hipEventSynchronize(E.stage_ev[k & 1]));
+        const size_t off = k * kD2HChunk, len = std::min(kD2HChunk, total - off);
+        ms_parallel_memcpy(rgba_host + off, E.stage + (k & 1) * kD2HChunk, len);
+        if (k + 2 < nch) CHECK(issue(k + 2));
+    }
     return MSPLAT_OK;
     API_END
 }
