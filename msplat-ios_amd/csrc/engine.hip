@@ -641,9 +641,35 @@ int msplat_hip_upload(void *dst, const void *src, size_t bytes) {
     API_END
 }
 
+// Device -> pageable host copy of `total` bytes through the two pinned
+// chunks: the DMA of chunk k + 1 runs while the host moves chunk k on.
+// Ordered after the work already on the engine stream; synchronous.
+static int download_staged(unsigned char *dst, const unsigned char *src, size_t total) {
+    Engine &E = g_eng;
+    const size_t nch = (total + kD2HChunk - 1) / kD2HChunk;
+    auto issue = [&](size_t k) -> int {
+        const size_t off = k * kD2HChunk, len = std::min(kD2HChunk, total - off);
+        HIPC(hipMemcpyAsync(E.stage + (k & 1) * kD2HChunk, src + off, len, hipMemcpyDeviceToHost, E.stream));
+        HIPC(hipEventRecord(E.stage_ev[k & 1], E.stream));
+        return MSPLAT_OK;
+    };
+    if (nch == 0) return MSPLAT_OK;
+    CHECK(issue(0));
+    if (nch > 1) CHECK(issue(1));
+    for (size_t k = 0; k < nch; ++k) {
+        HIPC(hipEventSynchronize(E.stage_ev[k & 1]));
+        const size_t off = k * kD2HChunk, len = std::min(kD2HChunk, total - off);
+        ms_parallel_memcpy(dst + off, E.stage + (k & 1) * kD2HChunk, len);
+        if (k + 2 < nch) CHECK(issue(k + 2));
+    }
+    return MSPLAT_OK;
+}
+
 int msplat_hip_download(void *dst, const void *src, size_t bytes) {
     API_BEGIN
     ENSURE_INIT();
+    if (bytes >= kD2HChunk)  // large: staged (pageable destinations copy ~3x faster)
+        return download_staged(static_cast<unsigned char *>(dst), static_cast<const unsigned char *>(src), bytes);
     HIPC(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_eng.stream));
     HIPC(hipStreamSynchronize(g_eng.stream));
     return MSPLAT_OK;
@@ -680,26 +706,7 @@ int msplat_hip_image_to_rgba8(const float *img, int64_t num_pixels, uint8_t *rgb
     CHECK(ensure(E.rgba, (size_t)num_pixels * 4));
     mskern::launch_rgba8(E.stream, img, num_pixels, P<uint32_t>(E.rgba));
     HIPC(hipGetLastError());
-    // chunked through the two pinned buffers: the DMA of chunk k + 1 runs
-    // while the host moves chunk k on to the caller's buffer
-    const size_t total = (size_t)num_pixels * 4;
-    const size_t nch = (total + kD2HChunk - 1) / kD2HChunk;
-    const unsigned char *src = P<unsigned char>(E.rgba);
-    auto issue = [&](size_t k) -> int {
-        const size_t off = k * kD2HChunk, len = std::min(kD2HChunk, total - off);
-        HIPC(hipMemcpyAsync(E.stage + (k & 1) * kD2HChunk, src + off, len, hipMemcpyDeviceToHost, E.stream));
-        HIPC(hipEventRecord(E.stage_ev[k & 1], E.stream));
-        return MSPLAT_OK;
-    };
-    CHECK(issue(0));
-    if (nch > 1) CHECK(issue(1));
-    for (size_t k = 0; k < nch; ++k) {
-        HIPC(hipEventSynchronize(E.stage_ev[k & 1]));
-        const size_t off = k * kD2HChunk, len = std::min(kD2HChunk, total - off);
-        ms_parallel_memcpy(rgba_host + off, E.stage + (k & 1) * kD2HChunk, len);
-        if (k + 2 < nch) CHECK(issue(k + 2));
-    }
-    return MSPLAT_OK;
+    return download_staged(rgba_host, P<unsigned char>(E.rgba), (size_t)num_pixels * 4);
     API_END
 }
 
