@@ -373,14 +373,19 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
             if constexpr (FULL) L.e[wave][lane] = e;
         }
         wave_lds_sync();
+        // image-only: the entries' addresses are uniform (scalar loads),
+        // each fetched one visit ahead so its latency is not waited on, and
+        // an entry's ballot is the lane mask of `has` itself
+        uint4 e_next;
+        if constexpr (!FULL) e_next = lg[c0 + m - 1];
         for (int j = m - 1; j >= 0; --j) {
-            // image-only: the entry's address is uniform (scalar load) and
-            // its ballot is the lane mask of `has` itself
             uint4 e;
-            if constexpr (FULL)
+            if constexpr (FULL) {
                 e = L.e[wave][j];
-            else
-                e = lg[c0 + j];
+            } else {
+                e = e_next;
+                e_next = lg[c0 + max(j - 1, 0)];
+            }
             const bool has = FULL ? (((lane < 32 ? e.x : e.y) >> (lane & 31)) & 1u)
                                   : __builtin_amdgcn_inverse_ballot_w64(((uint64_t)e.y << 32) | e.x);
             float v16[16];

@@ -101,6 +101,26 @@ __host__ __device__ __forceinline__ float ms_gauss(float rho) {
     return __builtin_ldexpf(p, (int)z);
 }
 
+// ms_gauss for 0 <= rho <= kGaussRhoCap, without the clamp: there t is at
+// least fl(171 * -log2(e) / 2) = -123.35 > -124, so the clamp never acts and
+// the result is ms_gauss(rho) bit for bit.  A caller that caps a larger rho
+// (or NaN) at kGaussRhoCap gets ms_gauss(171) ~ 1e-37 instead of
+// ms_gauss(rho) <= that, which is as far below any alpha threshold.
+constexpr float kGaussRhoCap = 171.0f;
+__host__ __device__ __forceinline__ float ms_gauss_capped(float rho) {
+    const float t = rho * -0.721347510814666748046875f;
+    const float z = __builtin_rintf(t);
+    const float f = t - z;
+    float p = 1.5403530393381606e-4f;
+    p = __builtin_fmaf(p, f, 1.3333558146428443e-3f);
+    p = __builtin_fmaf(p, f, 9.6181291076284772e-3f);
+    p = __builtin_fmaf(p, f, 5.5504108664821580e-2f);
+    p = __builtin_fmaf(p, f, 2.4022650695910071e-1f);
+    p = __builtin_fmaf(p, f, 6.9314718055994531e-1f);
+    p = __builtin_fmaf(p, f, 1.0f);
+    return __builtin_ldexpf(p, (int)z);
+}
+
 // Saturating truncation (the tile-rectangle (int) casts of get_bbox,
 // msplat_metal.metal:70-73, are undefined outside the int range).
 __device__ __forceinline__ int f2i(float x) {
@@ -416,12 +436,15 @@ __device__ __forceinline__ uint64_t eval_pair(float px, float py, const float4 &
     e.v = e.ray.y * e.inv_z;
     e.rho3d = __builtin_fmaf(e.u, e.u, e.v * e.v);
     e.rho2d = FILTER_INV_SQ * __builtin_fmaf(dxs, dxs, dys * dys);
-    const float rho = __builtin_fminf(e.rho3d, e.rho2d);
+    // capped for ms_gauss_capped (one v_min3): beyond the cap ms_gauss is
+    // below 1e-37, so alpha < 1/255 either way and every decision, hence
+    // every output, is the one ms_gauss(min(rho3d, rho2d)) gives
+    const float rho = __builtin_fminf(__builtin_fminf(e.rho3d, e.rho2d), kGaussRhoCap);
     e.depth = __builtin_fmaf(e.u, p3.x, __builtin_fmaf(e.v, p3.y, p3.z));
     // The reference's power > 0 rejection (msplat_metal.metal:676-677) never
     // fires: rho is a minimum of sums of squares (>= 0, +inf or NaN), so
     // power = -rho / 2 is <= 0, -inf or NaN.
-    e.G = ms_gauss(rho);
+    e.G = ms_gauss_capped(rho);
     e.alpha = __builtin_fminf(0.99f, p2.w * e.G);
     return __builtin_amdgcn_ballot_w64(!(e.ray.z == 0.0f)) & __builtin_amdgcn_ballot_w64(!(e.depth < NEAR_N)) &
            __builtin_amdgcn_ballot_w64(!(e.alpha < 1.0f / 255.0f));

@@ -186,19 +186,25 @@ def _device(a):
     return E.DeviceArray.from_numpy(np.ascontiguousarray(a, np.float32))
 
 
-@pytest.mark.parametrize("shape", [(208, 320), (37, 53), (1, 1), (11, 150)])
-def test_loss_fwd_bwd_bitexact(shape, orc, eng):
+@pytest.mark.parametrize("shape,ldist", [((208, 320), 0.0), ((37, 53), 0.0), ((1, 1), 0.0), ((11, 150), 0.0),
+                                          ((300, 517), 0.0), ((97, 203), 0.05)])
+def test_loss_fwd_bwd_bitexact(shape, ldist, orc, eng):
+    # (300, 517): mostly interior 32x32 tiles, whose staging skips the
+    # bounds checks, and a ragged right and bottom edge; (97, 203) adds the
+    # distortion term of the loss
     H, W = shape
     rng = S.SplitMix64(17 + H * W)
     img = rng.uniform(H * W * 3).reshape(H, W, 3).astype(np.float32)
     gt = rng.uniform(H * W * 3).reshape(H, W, 3).astype(np.float32)
     gt[: H // 2] = img[: H // 2]  # exact-equality pixels: sign(0) = 0
-    loss_o, dL_o, _, ssim_o = orc.loss_fwd_bwd(img, gt)
+    dist = rng.uniform(H * W).reshape(H, W).astype(np.float32)
+    loss_o, dL_o, _, ssim_o = orc.loss_fwd_bwd(img, gt, distortion=dist if ldist else None, lambda_dist=ldist)
     d_img, d_gt, d_dL = _device(img), _device(gt), E.DeviceArray((H, W, 3))
+    d_dist = _device(dist)
     loss = C.c_double()
     ssim = C.c_double()
-    E.check(E.lib().msplat_hip_loss_fwd_bwd(W, H, d_img.ptr, d_gt.ptr, None, 0.8, 0.0, 0.2, d_dL.ptr,
-                                           C.byref(loss), C.byref(ssim)))
+    E.check(E.lib().msplat_hip_loss_fwd_bwd(W, H, d_img.ptr, d_gt.ptr, d_dist.ptr if ldist else None, 0.8, ldist,
+                                           0.2, d_dL.ptr, C.byref(loss), C.byref(ssim)))
     _assert_bitexact(d_dL.numpy(), dL_o, "dL/dimg")
     assert abs(loss.value - loss_o) <= 1e-5 * abs(loss_o) + 1e-9
     assert abs(ssim.value - ssim_o) <= 1e-6 * abs(ssim_o) + 1e-6
