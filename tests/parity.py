@@ -121,3 +121,27 @@ def post_adam_close(names, got_params, orc_params, got_m, orc_m, noise, lrs, bet
         assert not bad.any(), (f"{name}: {int(bad.sum())} parameters outside the range their gradient's allowed "
                                f"error permits, worst ratio {(diff / limit).max():.3g}")
         assert not (diff > 1e-5)[~unresolved].any()
+
+
+def trainer_post_adam_close(name, got, orc, orc_m, lr, beta1=0.9, eps=1e-8):
+    """One trainer step against the golden model's step, per element, from
+    the golden model's first moments alone (the trainer keeps its gradients
+    on the GPU): with g_o = m_o / (1 - beta1), a gradient error of up to
+    RTOL |g_o| + FLOOR max|g_o| (float-atomic order, the GPU backward's
+    hardware exp2 against the golden model's Gaussian) moves Adam's first
+    step by at most reach = max |step(g_o +- err) - step(g_o)|.  Every
+    parameter must lie within max(1e-5 max(1, max|p|), reach + its own
+    rounding): the plain 1e-5 bar wherever the gradient is resolved."""
+    p = np.asarray(got, np.float64).reshape(-1)
+    po = np.asarray(orc, np.float64).reshape(-1)
+    go = np.asarray(orc_m, np.float64).reshape(-1) / (1.0 - beta1)
+    err = RTOL * np.abs(go) + FLOOR * np.abs(go).max() + 1e-30
+    s0 = adam_first_step(go, lr, eps)
+    reach = np.maximum(np.abs(adam_first_step(go + err, lr, eps) - s0), np.abs(adam_first_step(go - err, lr, eps) - s0))
+    bar = 1e-5 * max(1.0, np.abs(po).max())
+    limit = np.maximum(bar, reach + 2.5e-7 * np.maximum(np.abs(po), 1.0))
+    diff = np.abs(p - po)
+    print(f"[adam] {name}: max diff {diff.max():.3g}, {int((diff > bar).sum())} of {p.size} beyond 1e-5 "
+          f"(all within their gradient's reach: {bool((diff <= limit).all())})", flush=True)
+    assert (diff <= limit).all(), (
+        f"{name}: {int((diff > limit).sum())} parameters outside their reach; worst ratio {(diff / limit).max():.3g}")
