@@ -11,6 +11,9 @@ The headline line (`value`) is the train-step throughput of the 3M-splat,
   C3 train-3M-5187x3361     (the headline) + render FPS through the C ABI
   C4 overflow-1M-1920x1080  train steps/s, render FPS
   C5 densify-200k-1297x840  1500 steps with densification every 100
+  C3_shard8                 C3 camera 0 in 8 bands of tile rows, each trained as
+                            its own camera: one GPU's share of image-space
+                            sharding at its real shape
   C3_3dgs                   the C3 splats as 3D Gaussians in the 3DGS mode
   mesh                      TSDF fusion of 32 depth views + marching cubes, 300^3
 each next to the golden model (scalar C++, OpenMP) timed on this host.
@@ -178,6 +181,44 @@ def gpu_train(workload: int, steps: int, warmup: int, render_frames: int, counte
     del gts
     out["render_ms"] = gpu_render_ms(ds, cams, render_frames)
     return out
+
+
+def gpu_shard(scene, ds, bands: int, steps: int, warmup: int) -> dict:
+    """One GPU's share of image-space sharding at its real shape: camera 0
+    of the workload split into `bands` bands of tile rows (as even as the
+    tile rows allow), each trained as its own camera (the same intrinsics
+    with the principal point moved up by the band's first row, so it
+    renders exactly those rows of the full image, against those rows of the
+    full target).  Every band projects all splats and runs the projection
+    backward with Adam on all of them, as each GPU would after the gradient
+    all-reduce; the all-reduce itself and the SSIM halo exchange at band
+    edges (zero padding here) are not part of the measured step."""
+    from msplat import _engine as E
+    from msplat import device as D
+
+    c = scene.cameras[0]
+    tgt = D.DeviceScene(scene.jittered(0.01, 0xC0FFEE + 100 + 3))
+    full_gt = D.render_to_device(tgt, ds.camera(c))
+    del tgt
+    tiles_y = (c.height + 15) // 16
+    out = []
+    for b in range(bands):
+        r0, r1 = b * tiles_y // bands, (b + 1) * tiles_y // bands
+        y0, hb = 16 * r0, min(16 * (r1 - r0), c.height - 16 * r0)
+        cam = E.prepare_camera(c.cam_to_world, c.fx, c.fy, c.cx, c.cy - y0, c.width, hb, ds.sh_degree,
+                               ds.sh_degree)
+        gt = E.DeviceArray((hb, c.width, 3), ptr=full_gt.ptr + y0 * c.width * 12, owned=False)
+        for _ in range(warmup):
+            D.train_step(ds, cam, gt)
+        ms, losses, isect = _timed_steps(E, lambda ci: D.train_step(ds, cam, gt), 0, steps, 1)
+        out.append({"rows": [y0, y0 + hb], "ms_per_step": round(ms, 3), "intersections": int(np.mean(isect))})
+    del full_gt
+    return {"workload": f"{scene.name}, camera 0 in {bands} bands of tile rows (one band per GPU)",
+            "bands": out, "steps_per_band": steps,
+            "max_ms_per_step": max(r["ms_per_step"] for r in out),
+            "sum_ms_per_step": round(sum(r["ms_per_step"] for r in out), 3),
+            "excluded": "the all-reduce of the per-splat raster gradients (16 floats x N) before the projection "
+                        "backward, and the SSIM halo exchange at band edges"}
 
 
 def gpu_train3d(workload: int, steps: int, warmup: int, render_frames: int):
@@ -658,6 +699,11 @@ def main() -> int:
     log(f"{scene.name}: {h['ms_per_step']:.3f} ms/step, render {h['render_ms']:.3f} ms")
     kernels = kernel_table(h["stage_ms"], N, int(I), P, T, scene.name)
     kernels["raster_fwd"].update(h["raster_counts"])
+    shard = None
+    if not args.no_configs:
+        shard = gpu_shard(scene, h["ds"], 8, 10, 2)
+        log(f"{scene.name} in 8 bands: slowest band {shard['max_ms_per_step']:.3f} ms/step, "
+            f"all bands {shard['sum_ms_per_step']:.3f} ms")
     del h["ds"]
     gc.collect()
     buf_ms = None if args.no_buffer_render else gpu_render_to_buffer_ms(scene, max(args.render_frames // 2, 5))
@@ -691,6 +737,8 @@ def main() -> int:
 
     # ---- the other workloads ----
     configs = {}
+    if shard is not None:
+        configs["C3_shard8"] = shard
     if not args.no_configs:
         for wl, key in ((2, "C2"), (4, "C4")):
             r = gpu_train(wl, max(args.steps, 30), args.warmup, args.render_frames, counters=False)
