@@ -111,6 +111,29 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
+def lds_calibration() -> int:
+    """LDS loads of 4, 8 and 16 bytes per lane in five patterns (contiguous,
+    every 2nd, 4th and 32nd access, broadcast; msplat_hip_lds_calibration),
+    each timed on its own launch after a warm-up launch: the kernels whose
+    SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE counters are read against
+    measured time.  Prints one JSON line (ns per wave-wide load per CU)."""
+    from msplat import _engine as E
+
+    E.init()
+    L = E.lib()
+    ms = C.c_float()
+    loads_per_cu = 1024 * 4 * 2000 / 256  # wave loads per CU per launch
+    out = []
+    for width in (4, 8, 16):
+        for pattern, name in enumerate(("contiguous", "stride2", "stride4", "stride32", "broadcast")):
+            E.check(L.msplat_hip_lds_calibration(width, pattern, C.byref(ms)))
+            E.check(L.msplat_hip_lds_calibration(width, pattern, C.byref(ms)))
+            out.append({"bytes_per_lane": width, "pattern": name, "ms": round(ms.value, 4),
+                        "ns_per_wave_load_per_cu": round(ms.value * 1e6 / loads_per_cu, 3)})
+    print(json.dumps({"lds_calibration": out}))
+    return 0
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -643,6 +666,8 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run the copy kernel used to calibrate rocprofv3 byte counters")
+    ap.add_argument("--lds-calibration", action="store_true",
+                    help="only run the LDS access-pattern kernels used to read the LDS bank-conflict counters")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
@@ -666,6 +691,8 @@ def main() -> int:
         return 2
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
+    if args.lds_calibration:
+        return lds_calibration()
     os.environ.setdefault("OMP_NUM_THREADS", str(args.cpu_threads))
 
     from msplat import _engine as E

@@ -80,6 +80,7 @@ struct Engine {
     // per-pixel
     DevBuf out_img, final_Ts, final_idx, out_depth, out_normal, out_alpha, out_median, out_dist;
     DevBuf dL_dimg, gm1, gs1, gs12, partials, loss;
+    DevBuf calib;  // msplat_hip_lds_calibration's output
     // unfused gradients
     DevBuf dmeans, dscales, dquats, dmean2d, dfdc, dfrest;
     // materialised views
@@ -567,7 +568,7 @@ void msplat_hip_cleanup(void) {
                      &E.final_idx, &E.out_depth, &E.out_normal, &E.out_alpha, &E.out_median, &E.out_dist,
                      &E.dL_dimg, &E.gm1, &E.gs1, &E.gs12, &E.partials, &E.loss, &E.dmeans, &E.dscales,
                      &E.dquats, &E.dmean2d, &E.dfdc, &E.dfrest, &E.dens_flags, &E.dens_scan, &E.dens_keep, &E.pair_counter,
-                     &E.rgba, &E.tsdf_views, &E.tsdf_masks, &E.mc_cases, &E.chunk_cnt, &E.chunk_off};
+                     &E.rgba, &E.tsdf_views, &E.tsdf_masks, &E.mc_cases, &E.chunk_cnt, &E.chunk_off, &E.calib};
     for (DevBuf *b : all) {
         if (b->p) (void)hipFree(b->p);
         *b = DevBuf{};
@@ -1321,6 +1322,29 @@ int msplat_hip_last_raster_counts(int64_t out[5]) {
     if (!out) return MSPLAT_E_ARG;
     for (int i = 0; i < 5; ++i) out[i] = g_eng.pairs[i];
     return MSPLAT_OK;
+}
+
+int msplat_hip_lds_calibration(int bytes_per_lane, int pattern, float *ms_out) {
+    API_BEGIN
+    if (!ms_out || (bytes_per_lane != 4 && bytes_per_lane != 8 && bytes_per_lane != 16) || pattern < 0 ||
+        pattern > 4)
+        return MSPLAT_E_ARG;
+    ENSURE_INIT();
+    Engine &E = g_eng;
+    CHECK(ensure(E.calib, (size_t)mskern::lds_calib_out_floats() * 4));
+    hipEvent_t e0, e1;
+    HIPC(hipEventCreate(&e0));
+    HIPC(hipEventCreate(&e1));
+    HIPC(hipEventRecord(e0, E.stream));
+    mskern::launch_lds_calib(E.stream, bytes_per_lane, pattern, P<float>(E.calib));
+    HIPC(hipEventRecord(e1, E.stream));
+    HIPC(hipEventSynchronize(e1));
+    HIPC(hipEventElapsedTime(ms_out, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    HIPC(hipGetLastError());
+    return MSPLAT_OK;
+    API_END
 }
 
 int msplat_hip_check_fast_rcp(int efield_lo, int efield_hi, int64_t *mismatches) {

@@ -118,6 +118,12 @@ void launch_loss_fwd_bwd(hipStream_t s, int W, int H, const float *img, const fl
                          float *gm1, float *gs1, float *gs12, double *partials, double *loss_out,
                          float *dL_dimg);
 
+// k_calib.hip: LDS access-pattern calibration, kLdsCalibBlocks workgroups
+// of 256 threads, kLdsCalibReads loads per thread
+constexpr int kLdsCalibBlocks = 1024, kLdsCalibReads = 2000;
+int lds_calib_out_floats();
+void launch_lds_calib(hipStream_t s, int bytes_per_lane, int pattern, float *out);
+
 // k_optim.hip
 void launch_adam(hipStream_t s, float *p, const float *g, float *m, float *v, int64_t n, float step, float b1,
                  float b2, float bc2_sqrt, float eps);
