@@ -69,7 +69,9 @@ __device__ __forceinline__ int load_batch(const float4 *__restrict__ rec, const 
 // decision, and so every produced value, is the same as with FULL_OUT.
 // 7 waves per SIMD: the LDS of the image-only kernel allows 7 workgroups
 // per CU, and at most 72 VGPRs keep all of them resident (the compiler
-// would otherwise use 79 and fit 6).
+// would otherwise use more and fit 6; with two visits per iteration it
+// spills one value, reloaded once per batch, which costs less than the
+// seventh wave saves).
 template <bool LOG, bool FULL_OUT, bool COUNT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))) void k_raster_fwd(
     int W, int H, int tiles_x, int T, const int *__restrict__ offsets, const int *__restrict__ ids,
@@ -127,8 +129,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
         const int m = idx < end ? load_batch<FULL_OUT>(rec, mrec, gid, idx - start, s_rec, sx0, sy0) : 0;
         const int n = build_wave_lists(m, s_list, s_cnt);
         int nv = 0;
-        for (int j = 0; j < n && done_m != ~0ull; ++j) {
-            if (COUNT) ++nv;
+        // one visit of slot list entry j; a visit after the wave is done
+        // changes nothing (no lane is active, so nothing blends or is logged)
+        const auto visit = [&](int j) {
+            if (COUNT) nv += done_m != ~0ull;
             const int to = 16 * (int)s_list[wave][j];  // byte offset of the slot in a record plane
             const auto plane = [&](int k) {
                 return *reinterpret_cast<const float4 *>(s_bytes + k * (kThreads * 16) + to);
@@ -183,7 +187,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
                     t_ckpt[log_base + nlog + lane] = Tr;
                 }
             }
+        };
+        // two visits per iteration: the second's work up to alpha does not
+        // depend on the first's blend, so the two can be interleaved
+        int j = 0;
+        for (; j + 1 < n && done_m != ~0ull; j += 2) {
+            visit(j);
+            visit(j + 1);
         }
+        if (j < n && done_m != ~0ull) visit(j);
         if (COUNT) {
             visits += (unsigned)nv;
             if (lane == 0) s_vis[wave] = nv;
