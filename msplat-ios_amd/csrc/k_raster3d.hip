@@ -85,7 +85,9 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_fwd(int W, int H, int til
         const int gid = idx < end ? ids[idx] : 0;
         const int m = idx < end ? load_batch3(rec, boxes, gid, idx - start, s_rec, sx0, sy0) : 0;
         const int n = build_wave_lists(m, s_list, s_cnt);
-        for (int j = 0; j < n && done_m != ~0ull; ++j) {
+        // one visit of slot list entry j (a visit after the wave is done
+        // changes nothing); two per iteration, as the 2DGS forward
+        const auto visit = [&](int j) {
             const int to = 16 * (int)s_list[wave][j];
             const auto plane = [&](int k) {
                 return *reinterpret_cast<const float4 *>(s_bytes + k * (kThreads * 16) + to);
@@ -118,7 +120,13 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_fwd(int W, int H, int til
                     t_ckpt[log_base + nlog + lane] = Tr;
                 }
             }
+        };
+        int j = 0;
+        for (; j + 1 < n && done_m != ~0ull; j += 2) {
+            visit(j);
+            visit(j + 1);
         }
+        if (j < n && done_m != ~0ull) visit(j);
     }
     if (LOG) {
         if (lane < (nlog & 63)) wave_log[(nlog & ~63) + lane] = lg_ent;
