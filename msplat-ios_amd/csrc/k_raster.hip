@@ -282,6 +282,13 @@ struct BwdLds<false> {
     float red[4][512];
 };
 
+// The image-only reduction's slots: 13 non-zero sums in five permlane pairs
+// (rows 0, 2, 4, 6, 7) and three raw rows (1, 3, 5), so five permlane swaps
+// per visit instead of seven.  Nibble k of kImgGrad is the grads16 index of
+// reduction slot k (the unused upper slots of raw rows read 0).
+constexpr unsigned kImgRaw = 0x2A;
+constexpr unsigned long long kImgGrad = 0xfe0c0308d7654210ull;
+
 template <bool FULL>
 __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     int W, int H, int tiles_x, int T, const int *__restrict__ offsets, const uint4 *__restrict__ blend_log,
@@ -309,11 +316,8 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     const float px = (float)pxi, py = (float)pyi;
     const int start = offsets[tile], len = offsets[tile + 1] - start;
     const int nlog = __builtin_amdgcn_readfirstlane(wave_cnt[4 * tile + wave]);
-    Red8 red8;
-    if (!FULL) {
-        red8.init(reinterpret_cast<float *>(&L) + sizeof(L.r) / sizeof(float) + wave * 512, lane);
-        red8.zero_skipped<0x08>();
-    }
+    Red8<kImgRaw> red8;
+    if (!FULL) red8.init(reinterpret_cast<float *>(&L) + sizeof(L.r) / sizeof(float) + wave * 512, lane);
     const size_t log_base = 4 * (size_t)start + (size_t)wave * (size_t)len;
     const uint4 *lg = blend_log + log_base;
     const size_t pix = inside ? (size_t)pyi * W + pxi : 0;
@@ -345,9 +349,11 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     const float fA = 1.0f - T_final;
     const float bgT = -T_final * (bgp[0] * dp0 + bgp[1] * dp1 + bgp[2] * dp2);
     // lane l of the reduction ends with slot vi (see wave_reduce16), which
-    // holds grads16 index gi (the image-only layout exchanges 3 / 9, 10 / 11)
+    // holds grads16 index gi (image-only: slot red8.slot, its index in
+    // kImgGrad; only the lanes red8.adds marks hold a whole sum)
     const int vi = ((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 + ((lane >> 2) & 1);
-    const int gi = FULL ? vi : vi == 3 ? 9 : vi == 9 ? 3 : vi == 10 ? 11 : vi == 11 ? 10 : vi;
+    const int gi = FULL ? vi : (int)((kImgGrad >> (4 * red8.slot)) & 15u);
+    const bool adds = FULL ? (lane & 3) == 0 : red8.adds;
 
     // suffix state of the reference's recurrences (image-only: the colour
     // suffix projected on dL/dimage, updated as soon as a splat is done)
@@ -441,25 +447,23 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 const float dsx = t * u;
                 const float dsy = t * v;
                 const float dpz = -__builtin_fmaf(dsx, u, dsy * v);
-                // reduction slots: grads16 index k in slot k, except that
-                // slots 3 / 9 and 10 / 11 are exchanged (kSlotImg), which puts
-                // two of the three zero normals in one first-stage pair
+                // reduction slots (kImgRaw, kImgGrad): pairs (0, 8), (2, 10),
+                // (4, 12), (6, 14), (7, 15) and raw rows 1, 3, 5; the normal
+                // gradients (grads16 9-11) are zero here and take no slot
                 v16[0] = dsx;
+                v16[8] = dys * dpz;
                 v16[1] = dsy;
                 v16[2] = dpz;
-                v16[9] = dxs * dsx;
-                v16[4] = dxs * dsy;
-                v16[5] = dxs * dpz;
-                v16[6] = dys * dsx;
-                v16[7] = dys * dsy;
-                v16[8] = dys * dpz;
-                v16[3] = 0.f;
-                v16[10] = 0.f;
-                v16[11] = 0.f;
+                v16[10] = dxs * dsx;
+                v16[3] = dxs * dsy;
+                v16[4] = dxs * dpz;
                 v16[12] = gg;
-                v16[13] = aT * dp0;
+                v16[5] = dys * dsx;
+                v16[6] = dys * dsy;
                 v16[14] = aT * dp1;
+                v16[7] = aT * dp0;
                 v16[15] = aT * dp2;
+                v16[9] = v16[11] = v16[13] = 0.f;  // raw rows' partners: not read
             } else {
                 const float4 c0 = s_r[wave][0][j], c1 = s_r[wave][1][j], c2 = s_r[wave][2][j];
                 const float4 q0 = s_r[wave][3][j], q1 = s_r[wave][4][j], q5 = s_r[wave][5][j];
@@ -549,8 +553,8 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 v16[8] = px * dk.z + py * dl.z + dL_dz;
                 v16[12] = G * dL_dG * (1.0f - opa);
             }
-            const float s = FULL ? wave_reduce16(v16, lane) : wave_reduce16_lds8<0x08>(v16, red8);
-            if ((lane & 3) == 0 && s != 0.f) unsafeAtomicAdd(&grads16[(size_t)e.w * 16 + gi], s);
+            const float s = FULL ? wave_reduce16(v16, lane) : wave_reduce16_lds8<kImgRaw>(v16, red8);
+            if (adds && s != 0.f) unsafeAtomicAdd(&grads16[(size_t)e.w * 16 + gi], s);
         }
         wave_lds_sync();
     }

@@ -176,9 +176,9 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_bwd(int W, int H, int til
     const float px = (float)pxi, py = (float)pyi;
     const int start = offsets[tile], len = offsets[tile + 1] - start;
     const int nlog = __builtin_amdgcn_readfirstlane(wave_cnt[4 * tile + wave]);
-    Red8 red8;
+    Red8<0, 0xE0> red8;
     red8.init(&s_red[wave][0], lane);
-    red8.zero_skipped<0xE0>();
+    red8.zero_skipped();
     const size_t log_base = 4 * (size_t)start + (size_t)wave * (size_t)len;
     const uint4 *lg = blend_log + log_base;
     const size_t pix = inside ? (size_t)pyi * W + pxi : 0;
@@ -190,10 +190,12 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_bwd(int W, int H, int til
         dp2 = dL_dimg[3 * pix + 2];
     }
     const float bgT = -T_final * (bgp[0] * dp0 + bgp[1] * dp1 + bgp[2] * dp2);
-    // lane l ends the reduction with slot vi = 8 b5 + 4 b4 + 2 b3 + b2;
-    // slots 0..4 hold sums 0..4, slots 8..11 sums 5..8
-    const int vi = ((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 + ((lane >> 2) & 1);
-    const int gi = vi < 8 ? vi : vi - 3;
+    // the nine sums take five permlane pairs: slots 0..4 hold sums 0..4,
+    // slots 8..11 sums 5..8; rows 5..7 are empty and skipped.  (Raw rows
+    // save a permlane swap each but add a 256-byte row store per visit:
+    // six of them made this kernel 7% slower, its visits being short enough
+    // for that LDS traffic to bound it, and one was neutral.)
+    const int gi = red8.slot < 8 ? red8.slot : red8.slot - 3;
     float acc_v = 0.f;  // the colour suffix projected on dL/dimage
     const int nchunks = (nlog + kWave - 1) / kWave;
     for (int c = nchunks - 1; c >= 0; --c) {
@@ -233,19 +235,13 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_bwd(int W, int H, int til
             v16[2] = gy * dy;
             v16[3] = gx;
             v16[4] = gy;
-            v16[5] = 0.f;
-            v16[6] = 0.f;
-            v16[7] = 0.f;
             v16[8] = gg;
             v16[9] = aT * dp0;
             v16[10] = aT * dp1;
             v16[11] = aT * dp2;
-            v16[12] = 0.f;
-            v16[13] = 0.f;
-            v16[14] = 0.f;
-            v16[15] = 0.f;
-            const float s = wave_reduce16_lds8<0xE0>(v16, red8);
-            if ((lane & 3) == 0 && s != 0.f) unsafeAtomicAdd(&grads16[(size_t)e.w * 16 + gi], s);
+            v16[5] = v16[6] = v16[7] = v16[12] = v16[13] = v16[14] = v16[15] = 0.f;
+            const float s = wave_reduce16_lds8(v16, red8);
+            if (red8.adds && s != 0.f) unsafeAtomicAdd(&grads16[(size_t)e.w * 16 + gi], s);
         }
         wave_lds_sync();
     }

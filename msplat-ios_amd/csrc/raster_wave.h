@@ -114,47 +114,93 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// wave_reduce16 with one permlane step and the rest through LDS.  After the
-// permlane32 step register i holds, in lane L, value i + 8 b5(L) summed over
-// lanes L and L ^ 32.  Every register not skipped is written to row i of
-// this wave's 512-float scratch, lane L at column L ^ c(i), with
-// c(i) = 4 (i & 1) + 32 ((i >> 1) & 1); lane l then sums the eight partials
-// of value s = 8 b5 + 4 b4 + 2 b3 + b2 held by lanes 32 (s >> 3) + 8 k ..
-// + 7 (k = l & 3) with two 16-byte reads, and two quad DPP adds finish, so
-// lane l ends with the total of value s, as wave_reduce16.  Under the XOR
-// swizzle the 64-lane row writes and each 16-lane group of 16-byte reads
-// touch distinct banks.  The rows of skipped registers are never written:
-// Red8::zero_skipped clears them once.  (Measured at the 3M-splat step:
-// 5.6% faster than two permlane steps with a 256-float LDS tail; with no
-// permlane step at all, 4 KB of LDS traffic per visit made it 9% slower.)
+// wave_reduce16 with at most one permlane step and the rest through LDS.
+// Row i of this wave's 512-float scratch carries either a pair or one raw
+// value.  A pair row (bit i of RAW clear) holds, in lane L, value i + 8 b5(L)
+// summed over lanes L and L ^ 32 (one permlane32 swap + add).  A raw row (bit
+// i set) holds value i itself in every lane; v[i + 8] is then not read.
+// Lane L writes row i at column L ^ c(i), c(i) = 4 (i & 1) + 32 ((i >> 1) & 1).
+// Quad q = l >> 2 then takes slot s = (q >> 1) + 8 (q & 1) (s = q when no
+// row is raw, which measured 2% faster on the 3DGS backward): its four lanes
+// sum the entries of row s & 7 held by lanes 32 (s >> 3) + 8 k .. + 7
+// (k = l & 3) with two 16-byte reads, and two quad DPP adds finish.  For a
+// pair row that is the total of value s.  For a raw row the quads of slots
+// i and i + 8 hold the sums over the two half-waves; they are neighbours in
+// one 16-lane DPP row (quad q even, q + 1), so one DPP add (row_shl:4,
+// masked to those quads) gives slot i the total, and slot i + 8 is not
+// used.  Red8::adds marks the lanes that hold a total (one per quad), so the
+// caller's atomic never has two lanes on one address: same-address lanes of
+// one atomic instruction are serialised, which made an undivided version of
+// this scheme twice as slow.  A raw row saves a permlane swap and an add per
+// visit; the raw rows must be the rows 2R + j of a set of R times a set of j
+// (the DPP row and bank masks), and n values fit in 8 rows with up to
+// 16 - n of them raw.  Each row written is 256 bytes of LDS stores per
+// visit, so when a visit is short a raw row can cost more in LDS bandwidth
+// than its permlane swap.  Under the XOR swizzle the 64-lane row writes and each
+// 16-lane group of 16-byte reads touch distinct banks.  (Measured at the
+// 3M-splat step: one permlane step was 5.6% faster than two with a 256-float
+// LDS tail; no permlane step with 16 rows, 4 KB of LDS traffic per visit,
+// was 9% slower.)
+constexpr unsigned raw_dpp_rows(unsigned raw) {
+    unsigned m = 0;
+    for (int R = 0; R < 4; ++R)
+        if ((raw >> (2 * R)) & 3u) m |= 1u << R;
+    return m;
+}
+constexpr unsigned raw_dpp_banks(unsigned raw) {
+    unsigned m = 0;
+    for (int j = 0; j < 2; ++j)
+        if (raw & (0x55u << j)) m |= 1u << (2 * j);
+    return m;
+}
+constexpr bool raw_is_product(unsigned raw) {
+    unsigned p = 0;
+    for (int R = 0; R < 4; ++R)
+        for (int j = 0; j < 2; ++j)
+            if (((raw_dpp_rows(raw) >> R) & 1u) && ((raw_dpp_banks(raw) >> (2 * j)) & 1u)) p |= 1u << (2 * R + j);
+    return p == raw;
+}
+
+// SKIP: rows whose values are zero in every lane; they are never written
+// (zero_skipped clears them once).
+template <unsigned RAW, unsigned SKIP = 0>
 struct Red8 {
+    static_assert(raw_is_product(RAW), "raw rows must be a row set times a bank set");
+    static_assert((RAW & SKIP) == 0, "a row is raw or skipped");
     float *wb[4];        // scratch + (lane ^ c(j)), j = 0..3; register i writes at wb[i & 3] + 64 i
     const float4 *r0, *r1;  // this lane's two 16-byte read addresses
+    int slot;            // the reduction slot this lane ends with
+    bool adds;           // lane 0 of its quad, and its slot holds a total
 
     __device__ __forceinline__ void init(float *scratch, int lane) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) wb[j] = scratch + (lane ^ (4 * (j & 1) + 32 * ((j >> 1) & 1)));
-        const int sv = ((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 + ((lane >> 2) & 1);
-        const int row = sv & 7, c = 4 * (row & 1) + 32 * ((row >> 1) & 1);
-        const int L = 32 * (sv >> 3) + 8 * (lane & 3);
+        const int q = lane >> 2;
+        slot = RAW == 0 ? q : (q >> 1) + 8 * (q & 1);
+        const int row = slot & 7, c = 4 * (row & 1) + 32 * ((row >> 1) & 1);
+        const int L = 32 * (slot >> 3) + 8 * (lane & 3);
         r0 = reinterpret_cast<const float4 *>(scratch + 64 * row + (L ^ c));
         r1 = reinterpret_cast<const float4 *>(scratch + 64 * row + ((L + 4) ^ c));
+        adds = (lane & 3) == 0 && !(((RAW >> row) & 1u) && slot >= 8);
     }
-    // zeros in the rows of the registers SKIP1 marks (call before the first
-    // reduction; the caller's wave_lds_sync orders it)
-    template <unsigned SKIP1>
+    // zeros in the skipped rows (call before the first reduction; the
+    // caller's wave_lds_sync orders it)
     __device__ __forceinline__ void zero_skipped() const {
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            if ((SKIP1 >> i) & 1u) wb[i & 3][64 * i] = 0.0f;
+            if ((SKIP >> i) & 1u) wb[i & 3][64 * i] = 0.0f;
     }
 };
 
-template <unsigned SKIP1 = 0>
-__device__ __forceinline__ float wave_reduce16_lds8(float v[16], const Red8 &r) {
+template <unsigned RAW, unsigned SKIP>
+__device__ __forceinline__ float wave_reduce16_lds8(float v[16], const Red8<RAW, SKIP> &r) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        if ((SKIP1 >> i) & 1u) continue;
+        if ((SKIP >> i) & 1u) continue;
+        if ((RAW >> i) & 1u) {
+            r.wb[i & 3][64 * i] = v[i];
+            continue;
+        }
         const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 8]), false,
                                                         false);
         r.wb[i & 3][64 * i] = __uint_as_float(x[0]) + __uint_as_float(x[1]);
@@ -165,6 +211,14 @@ __device__ __forceinline__ float wave_reduce16_lds8(float v[16], const Red8 &r) 
     float s = ((p.x + p.y) + (p.z + p.w)) + ((q.x + q.y) + (q.z + q.w));
     s += dpp<kDppQuad1032>(s);
     s += dpp<kDppQuad2301>(s);
+    // one masked DPP add: lanes outside the row and bank masks are not
+    // written (the builtin's form is a mov, a constant and an add, since no
+    // float constant is an exact identity of the add); the nop covers the
+    // two wait states a DPP read needs after the VALU write of s
+    if constexpr (RAW != 0)
+        asm("s_nop 1\n\tv_add_f32_dpp %0, %0, %0 row_shl:4 row_mask:%1 bank_mask:%2"
+            : "+v"(s)
+            : "n"(raw_dpp_rows(RAW)), "n"(raw_dpp_banks(RAW)));
     return s;
 }
 
