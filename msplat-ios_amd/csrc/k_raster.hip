@@ -278,7 +278,7 @@ struct BwdLds<true> {
 };
 template <>
 struct BwdLds<false> {
-    float4 r[4][4][64];
+    float4 r[4][4][32];
     float red[4][512];
 };
 
@@ -302,7 +302,7 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     constexpr int kWave = 64;
     // per wave: the staged entries' record planes (the image-only path
     // stages 4, the full one 7) and the log entries (full) or the reduction
-    // scratch (image-only, wave_reduce16_lds8); 24 KB per workgroup for the
+    // scratch (image-only, wave_reduce16_lds8); 16 KB per workgroup for the
     // image-only kernel
     __shared__ BwdLds<FULL> L;
     auto &s_r = L.r;
@@ -362,13 +362,20 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     float acc_d = 0.f, last_d = 0.f, acc_a = 0.f, last_dLdT = 0.f;
     float acc_n[3] = {0.f, 0.f, 0.f}, last_n[3] = {0.f, 0.f, 0.f};
 
-    const int nchunks = (nlog + kWave - 1) / kWave;
+    // entries staged per chunk: 64 (full), 32 (image-only: 16 KB of LDS per
+    // workgroup, so that its 52 VGPRs, not LDS, set the waves per SIMD)
+    constexpr int kChunk = FULL ? kWave : kWave / 2;
+    const int nchunks = (nlog + kChunk - 1) / kChunk;
+    float Tr = T_final;
     for (int c = nchunks - 1; c >= 0; --c) {
-        const int c0 = c * kWave;
-        const int m = min(kWave, nlog - c0);
-        // transmittance after the chunk's last splat: the next chunk's
-        // prefix checkpoint, or the final transmittance
-        float Tr = c == nchunks - 1 ? T_final : t_ckpt[log_base + c0 + kWave + lane];
+        const int c0 = c * kChunk;
+        const int m = min(kChunk, nlog - c0);
+        // transmittance after the chunk's last splat: the final
+        // transmittance, the prefix checkpoint of the entry after it when
+        // that entry is a multiple of 64, else the value the recurrence of
+        // the chunk after it ended with (the same operations in the same
+        // order as one 64-entry chunk)
+        if (c != nchunks - 1 && ((c0 + kChunk) & (kWave - 1)) == 0) Tr = t_ckpt[log_base + c0 + kChunk + lane];
         if (lane < m) {
             const uint4 e = lg[c0 + lane];
             const float4 *r = rec + 5 * (size_t)e.w;
