@@ -111,29 +111,6 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
-def lds_calibration() -> int:
-    """LDS loads of 4, 8 and 16 bytes per lane in five patterns (contiguous,
-    every 2nd, 4th and 32nd access, broadcast; msplat_hip_lds_calibration),
-    each timed on its own launch after a warm-up launch: the kernels whose
-    SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE counters are read against
-    measured time.  Prints one JSON line (ns per wave-wide load per CU)."""
-    from msplat import _engine as E
-
-    E.init()
-    L = E.lib()
-    ms = C.c_float()
-    loads_per_cu = 1024 * 4 * 2000 / 256  # wave loads per CU per launch
-    out = []
-    for width in (4, 8, 16):
-        for pattern, name in enumerate(("contiguous", "stride2", "stride4", "stride32", "broadcast")):
-            E.check(L.msplat_hip_lds_calibration(width, pattern, C.byref(ms)))
-            E.check(L.msplat_hip_lds_calibration(width, pattern, C.byref(ms)))
-            out.append({"bytes_per_lane": width, "pattern": name, "ms": round(ms.value, 4),
-                        "ns_per_wave_load_per_cu": round(ms.value * 1e6 / loads_per_cu, 3)})
-    print(json.dumps({"lds_calibration": out}))
-    return 0
-
-
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -387,12 +364,14 @@ def gpu_densify(total_steps: int = 1500, refine_every: int = 100, max_splats: in
             E.sync()
             n0 = ds.n
             rs = rng.normal(2 * n0 * 3).reshape(2 * n0, 3)
+            ds.stage_samples(rs)  # the split samples are an input: resident before the timed call
+            E.sync()
             td = time.perf_counter()
-            ds.densify(rs, half, grad_thresh=0.0002, cull_alpha=0.005)
+            ds.densify(None, half, grad_thresh=0.0002, cull_alpha=0.005)
             dms = (time.perf_counter() - td) * 1e3
             now = time.perf_counter()
             cycles.append(dict(step=step, n_before=n0, n_after=ds.n, densify_ms=round(dms, 3),
-                               cycle_ms=round((now - t_cycle) * 1e3, 2)))
+                               grow_ms=round(ds.last_grow_ms, 3), cycle_ms=round((now - t_cycle) * 1e3, 2)))
             log(f"densify at step {step}: {n0} -> {ds.n} ({cycles[-1]['cycle_ms']:.0f} ms cycle)")
             t_cycle = now
         if reset:
@@ -666,8 +645,6 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run the copy kernel used to calibrate rocprofv3 byte counters")
-    ap.add_argument("--lds-calibration", action="store_true",
-                    help="only run the LDS access-pattern kernels used to read the LDS bank-conflict counters")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
@@ -682,6 +659,8 @@ def main() -> int:
                     help="only run the train steps and render frames of workload N (for a profiler)")
     ap.add_argument("--mesh-only", action="store_true",
                     help="only the mesh workload (TSDF fusion + marching cubes; for a profiler)")
+    ap.add_argument("--densify-only", action="store_true",
+                    help="only the densification workload (200k -> ~2.8M splats over 1500 steps; for a profiler)")
     ap.add_argument("--3dgs-only", dest="gs3d_only", action="store_true",
                     help="only the 3DGS-mode workload (the C3 splats as 3D Gaussians; for a profiler)")
     args = ap.parse_args()
@@ -691,8 +670,6 @@ def main() -> int:
         return 2
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
-    if args.lds_calibration:
-        return lds_calibration()
     os.environ.setdefault("OMP_NUM_THREADS", str(args.cpu_threads))
 
     from msplat import _engine as E
@@ -702,6 +679,11 @@ def main() -> int:
     if args.mesh_only:
         mesh = gpu_mesh()
         print(json.dumps({k: v for k, v in mesh.items() if not k.startswith("_")}))
+        return 0
+    if args.densify_only:
+        d5 = gpu_densify()
+        print(json.dumps({"workload": d5["scene"].name, "splats_end": d5["n_final"],
+                          "total_s": round(d5["total_ms"] / 1e3, 3), "cycles": d5["cycles"]}))
         return 0
     if args.gs3d_only:
         r = gpu_train3d(3, args.steps, args.warmup, args.render_frames)

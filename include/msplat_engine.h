@@ -325,14 +325,6 @@ int msplat_hip_last_raster_counts(int64_t out[5]);
  * the rasterizer divides outside that range.  msplat_hip_init runs it over
  * [1, 2) and fails on a mismatch.  No counterpart in the reference. */
 int msplat_hip_check_fast_rcp(int efield_lo, int efield_hi, int64_t *mismatches);
-/* LDS calibration: one launch of kLdsCalibBlocks (1024) workgroups of 256
- * threads, each thread issuing 2000 LDS loads of bytes_per_lane (4, 8 or 16)
- * bytes in pattern 0..4 (lane l at access W l, 2 W l, 4 W l, 32 W l, or
- * all lanes at one address; W = bytes_per_lane / 4 floats); *ms_out
- * receives its duration (HIP events on the engine stream).  For reading
- * rocprofv3's LDS bank-conflict counters against measured time.  No
- * counterpart in the reference. */
-int msplat_hip_lds_calibration(int bytes_per_lane, int pattern, float *ms_out);
 /* Binning self-test hook.  Below 2^24 gaussians the per-super-tile sort keys
  * carry each gaussian's rectangle inside the super-tile (depth bits << 32 |
  * id << 8 | rectangle); from 2^24 on they are depth bits << 32 | id and the

@@ -80,13 +80,13 @@ struct Engine {
     // per-pixel
     DevBuf out_img, final_Ts, final_idx, out_depth, out_normal, out_alpha, out_median, out_dist;
     DevBuf dL_dimg, gm1, gs1, gs12, partials, loss;
-    DevBuf calib;  // msplat_hip_lds_calibration's output
     // unfused gradients
     DevBuf dmeans, dscales, dquats, dmean2d, dfdc, dfrest;
     // materialised views
     DevBuf mat[MSPLAT_LAST_COUNT];
     // densify scratch
-    DevBuf dens_scratch[18], dens_flags, dens_scan, dens_keep;
+    DevBuf dens_ws, dens_flags, dens_scan, dens_keep;
+    int64_t dens_rows = 0;  // rows dens_ws and dens_keep are sized for
     DevBuf pair_counter;
     DevBuf rgba;  // RGBA8 staging of msplat_hip_image_to_rgba8
     // mesh extraction: TSDF view records and pixel masks, marching-cubes case
@@ -567,8 +567,8 @@ void msplat_hip_cleanup(void) {
                      &E.stats, &E.big_list, &E.huge_list, &E.chunk_base, &E.chunk_counts, &E.keys, &E.keys_tmp, &E.ids, &E.blend_log, &E.t_ckpt, &E.wave_cnt, &E.selfcheck, &E.out_img, &E.final_Ts,
                      &E.final_idx, &E.out_depth, &E.out_normal, &E.out_alpha, &E.out_median, &E.out_dist,
                      &E.dL_dimg, &E.gm1, &E.gs1, &E.gs12, &E.partials, &E.loss, &E.dmeans, &E.dscales,
-                     &E.dquats, &E.dmean2d, &E.dfdc, &E.dfrest, &E.dens_flags, &E.dens_scan, &E.dens_keep, &E.pair_counter,
-                     &E.rgba, &E.tsdf_views, &E.tsdf_masks, &E.mc_cases, &E.chunk_cnt, &E.chunk_off, &E.calib};
+                     &E.dquats, &E.dmean2d, &E.dfdc, &E.dfrest, &E.dens_flags, &E.dens_scan, &E.dens_keep, &E.dens_ws, &E.pair_counter,
+                     &E.rgba, &E.tsdf_views, &E.tsdf_masks, &E.mc_cases, &E.chunk_cnt, &E.chunk_off};
     for (DevBuf *b : all) {
         if (b->p) (void)hipFree(b->p);
         *b = DevBuf{};
@@ -577,10 +577,7 @@ void msplat_hip_cleanup(void) {
         if (b.p) (void)hipFree(b.p);
         b = DevBuf{};
     }
-    for (auto &b : E.dens_scratch) {
-        if (b.p) (void)hipFree(b.p);
-        b = DevBuf{};
-    }
+    E.dens_rows = 0;
     E.n = 0;
     E.num_isect = 0;
     E.have_grads = false;
@@ -1071,7 +1068,10 @@ static int densify_impl(int scale_dim, int n, int capacity, float grad_thresh, f
         a.exp_avg[gi] = exp_avg[gi];
         a.exp_avg_sq[gi] = exp_avg_sq[gi];
     }
-    CHECK(ensure(E.dens_flags, (size_t)n * 4 * 4));
+    // four int flags per splat; regrown to twice the splat count (at most
+    // the capacity) when it no longer fits
+    if (E.dens_flags.cap < (size_t)n * 16)
+        CHECK(ensure(E.dens_flags, (size_t)std::min<int64_t>(2 * (int64_t)n, capacity) * 16));
     // the count after appending is at most 4N (a splat can be split and dup)
     CHECK(ensure(E.dens_scan, (size_t)mskern::scan_temp_ints(4 * (int64_t)n) * 4));
     int *f = P<int>(E.dens_flags);
@@ -1097,14 +1097,27 @@ static int densify_impl(int scale_dim, int n, int capacity, float grad_thresh, f
         return MSPLAT_E_CAPACITY;
     }
     for (int gi = 0; gi < 6; ++gi)
-        for (int r = 0; r < 3; ++r) {
-            CHECK(ensure(E.dens_scratch[6 * r + gi], (size_t)n_new * std::max(1, strides[gi]) * 4));
-            a.scratch[6 * r + gi] = P<float>(E.dens_scratch[6 * r + gi]);
+        if (strides[gi] > 127) {
+            set_err("densify: row stride %d above 127 floats", strides[gi]);
+            return MSPLAT_E_ARG;
         }
-    CHECK(ensure(E.dens_keep, (size_t)n_new * 2 * 4));
+    // Workspace and row maps are sized for the caller's capacity (the bound
+    // on the rows after appending), so they are allocated once per capacity
+    // instead of once per cycle of a model that doubles every cycle.
+    const int64_t rows = capacity;
+    if (n_new > E.dens_rows) {
+        CHECK(ensure(E.dens_ws, (size_t)mskern::densify_workspace_floats((int)rows, scale_dim, fr_stride) * 4));
+        CHECK(ensure(E.dens_keep, (size_t)rows * 4 * 4));
+        E.dens_rows = rows;
+    } else {
+        CHECK(ensure(E.dens_ws, (size_t)mskern::densify_workspace_floats((int)n_new, scale_dim, fr_stride) * 4));
+    }
+    a.workspace = P<float>(E.dens_ws);
     a.keep = P<int>(E.dens_keep);
     a.keep_pre = a.keep + n_new;
-    mskern::launch_densify_apply(E.stream, a, (int)n_new);
+    a.src_of = a.keep + 2 * n_new;
+    a.parent = a.keep + 3 * n_new;
+    mskern::launch_densify_apply(E.stream, a, E.pinned_i[0], (int)n_new);
     HIPC(hipGetLastError());
     HIPC(hipMemcpyAsync(E.pinned_i, a.keep_pre + n_new - 1, sizeof(int), hipMemcpyDeviceToHost, E.stream));
     HIPC(hipStreamSynchronize(E.stream));
@@ -1322,29 +1335,6 @@ int msplat_hip_last_raster_counts(int64_t out[5]) {
     if (!out) return MSPLAT_E_ARG;
     for (int i = 0; i < 5; ++i) out[i] = g_eng.pairs[i];
     return MSPLAT_OK;
-}
-
-int msplat_hip_lds_calibration(int bytes_per_lane, int pattern, float *ms_out) {
-    API_BEGIN
-    if (!ms_out || (bytes_per_lane != 4 && bytes_per_lane != 8 && bytes_per_lane != 16) || pattern < 0 ||
-        pattern > 4)
-        return MSPLAT_E_ARG;
-    ENSURE_INIT();
-    Engine &E = g_eng;
-    CHECK(ensure(E.calib, (size_t)mskern::lds_calib_out_floats() * 4));
-    hipEvent_t e0, e1;
-    HIPC(hipEventCreate(&e0));
-    HIPC(hipEventCreate(&e1));
-    HIPC(hipEventRecord(e0, E.stream));
-    mskern::launch_lds_calib(E.stream, bytes_per_lane, pattern, P<float>(E.calib));
-    HIPC(hipEventRecord(e1, E.stream));
-    HIPC(hipEventSynchronize(e1));
-    HIPC(hipEventElapsedTime(ms_out, e0, e1));
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
-    HIPC(hipGetLastError());
-    return MSPLAT_OK;
-    API_END
 }
 
 int msplat_hip_check_fast_rcp(int efield_lo, int efield_hi, int64_t *mismatches) {

@@ -44,7 +44,15 @@ struct Huffman {
     uint8_t vals[256] = {};
     int32_t maxcode[18] = {}, valptr[17] = {}, mincode[17] = {};
     uint16_t fast[512] = {};  // (length << 8 | value) + 1 for codes of <= 9 bits, 0 otherwise
-    void build(const uint8_t counts[16], const uint8_t *v, int nv) {
+    // Returns false, having written nothing, when the counts do not form a
+    // prefix code: canonical assignment (T.81 C.2) must keep every code of
+    // length L below 2^L.
+    bool build(const uint8_t counts[16], const uint8_t *v, int nv) {
+        int64_t room = 1;  // codes of the current length still unassigned
+        for (int len = 1; len <= 16; ++len) {
+            room = 2 * room - counts[len - 1];
+            if (room < 0) return false;
+        }
         std::memcpy(vals, v, (size_t)nv);
         int code = 0, k = 0;
         std::memset(fast, 0, sizeof(fast));
@@ -60,6 +68,7 @@ struct Huffman {
         }
         maxcode[17] = 0x7fffffff;
         defined = true;
+        return true;
     }
 };
 
@@ -252,7 +261,14 @@ private:
             int total = 0;
             for (int k = 0; k < 16; ++k) total += s[i + 1 + k];
             if (total > 256 || i + 17 + total > n) fail(path_, "bad Huffman table");
-            (tc ? ac_[th] : dc_[th]).build(s + i + 1, s + i + 17, total);
+            // 8-bit samples: DC difference categories 0..11, AC magnitude
+            // sizes 0..10 (T.81 F.1.2.1, F.1.2.2; Table K.3 / K.5 ranges)
+            for (int k = 0; k < total; ++k) {
+                const int val = s[i + 17 + k];
+                if (tc ? (val & 15) > 10 : val > 11) fail(path_, "bad Huffman value");
+            }
+            if (!(tc ? ac_[th] : dc_[th]).build(s + i + 1, s + i + 17, total))
+                fail(path_, "Huffman code lengths do not form a prefix code");
             i += 17 + total;
         }
     }
@@ -279,6 +295,10 @@ private:
             hmax_ = std::max(hmax_, k.h);
             vmax_ = std::max(vmax_, k.v);
         }
+        // Components are upsampled by whole factors; a frame whose largest
+        // sampling factor is not a multiple of every component's is refused.
+        for (const Component &k : comps_)
+            if (hmax_ % k.h || vmax_ % k.v) fail(path_, "non-integral chroma sampling ratio");
         mcux_ = (width_ + 8 * hmax_ - 1) / (8 * hmax_);
         mcuy_ = (height_ + 8 * vmax_ - 1) / (8 * vmax_);
         for (Component &k : comps_) {
@@ -520,7 +540,7 @@ private:
             y = std::min(std::max(y, 0), ph - 1);
             return k.plane[(size_t)y * pw + x];
         };
-        if (fx == 1 && fy == 1) {
+        if (k.h == hmax_ && k.v == vmax_) {  // full resolution: ph >= height_, pw >= width_
             for (int y = 0; y < height_; ++y)
                 std::memcpy(&out[(size_t)y * width_], &k.plane[(size_t)y * pw], (size_t)width_);
         } else if (fx == 2 && fy == 1) {

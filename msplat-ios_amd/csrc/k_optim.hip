@@ -1,6 +1,7 @@
 // k_optim.hip -- Adam, a device-wide int32 inclusive scan, and the
-// GPU-resident densification cycle (classify -> scan -> append split/dup ->
-// cull -> stable compaction of the 18 parameter / optimizer buffers).
+// GPU-resident densification cycle (classify -> scans -> keep flags of the
+// old and appended rows -> one gather of every surviving row of the 18
+// parameter / optimizer buffers into a workspace -> copy back).
 #include "kernels.h"
 #include "ms_device.h"
 
@@ -150,31 +151,20 @@ __global__ void k_classify(int N, int SD, const float *__restrict__ gnorm, const
     dup[i] = (!large && high) ? 1 : 0;
 }
 
-struct Bufs18 {
-    float *b[18];
-    int stride[18];
-};
+// The rows after the compaction are a stable selection from the virtual
+// list [old rows 0..N) ++ [two children per split splat, in split order]
+// ++ [one copy per dup splat, in dup order] (msplat_metal.metal:3271-3412
+// append these rows, :3417-3491 cull and compact them).  Nothing is
+// appended here: every virtual row is a function of its parent's row, so
+// k_densify_keep decides each virtual row's fate from the parent alone,
+// and k_densify_gather writes each output row once, in output order.
 
-__device__ __forceinline__ void zero_adam(const Bufs18 &B, size_t dst) {
-    for (int gi = 0; gi < 6; ++gi) {
-        const int s = B.stride[gi];
-        for (int j = 0; j < s; ++j) {
-            B.b[6 + gi][dst * s + j] = 0.f;
-            B.b[12 + gi][dst * s + j] = 0.f;
-        }
-    }
-}
-
-// densify_append_split_kernel (:3271-3361): children sampled along the SD
-// scale axes (the third is 0 for a surfel, :3315-3317).
-__global__ void k_append_split(int N, int SD, const int *__restrict__ split, const int *__restrict__ split_pre,
-                               const float *__restrict__ rs, float log_size_fac, Bufs18 B) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= N || split[i] == 0) return;
-    float *means = B.b[0], *scales = B.b[1], *quats = B.b[2];
-    const int ord = split_pre[i] - 1;
-    const int c0 = N + 2 * ord;
-    float qw = quats[i * 4], qx = quats[i * 4 + 1], qy = quats[i * 4 + 2], qz = quats[i * 4 + 3];
+// The split offset of child k of parent i (the rotated, scaled normal
+// sample of :3285-3313), in the reference's operation order.
+__device__ __forceinline__ float3 split_offset(const float *__restrict__ quats, const float *__restrict__ scales,
+                                               const float *__restrict__ rs, int SD, int i, int ri) {
+    float qw = quats[(size_t)i * 4], qx = quats[(size_t)i * 4 + 1], qy = quats[(size_t)i * 4 + 2],
+          qz = quats[(size_t)i * 4 + 3];
     const float qlen = __builtin_sqrtf(qw * qw + qx * qx + qy * qy + qz * qz);
     qw /= qlen;
     qx /= qlen;
@@ -183,86 +173,184 @@ __global__ void k_append_split(int N, int SD, const int *__restrict__ split, con
     const size_t si = (size_t)i * SD;
     const float sx = ms_expf(scales[si]), sy = ms_expf(scales[si + 1]);
     const float sz = SD > 2 ? ms_expf(scales[si + 2]) : 0.0f;
-    for (int k = 0; k < 2; ++k) {
-        const size_t child = (size_t)c0 + k;
-        const int ri = ord * 2 + k;
-        const float r0 = rs[ri * 3] * sx, r1 = rs[ri * 3 + 1] * sy, r2 = rs[ri * 3 + 2] * sz;
-        const float v0 = (1 - 2 * (qy * qy + qz * qz)) * r0 + 2 * (qx * qy - qw * qz) * r1 + 2 * (qx * qz + qw * qy) * r2;
-        const float v1 = 2 * (qx * qy + qw * qz) * r0 + (1 - 2 * (qx * qx + qz * qz)) * r1 + 2 * (qy * qz - qw * qx) * r2;
-        const float v2 = 2 * (qx * qz - qw * qy) * r0 + 2 * (qy * qz + qw * qx) * r1 + (1 - 2 * (qx * qx + qy * qy)) * r2;
-        means[child * 3] = means[i * 3] + v0;
-        means[child * 3 + 1] = means[i * 3 + 1] + v1;
-        means[child * 3 + 2] = means[i * 3 + 2] + v2;
-        for (int j = 0; j < SD; ++j) scales[child * SD + j] = scales[si + j] - log_size_fac;
-        for (int gi = 2; gi < 6; ++gi) {
-            const int s = B.stride[gi];
-            for (int j = 0; j < s; ++j) B.b[gi][child * s + j] = B.b[gi][(size_t)i * s + j];
-        }
-        zero_adam(B, child);
-    }
-    for (int j = 0; j < SD; ++j) scales[si + j] -= log_size_fac;
+    const float r0 = rs[(size_t)ri * 3] * sx, r1 = rs[(size_t)ri * 3 + 1] * sy, r2 = rs[(size_t)ri * 3 + 2] * sz;
+    float3 v;
+    v.x = (1 - 2 * (qy * qy + qz * qz)) * r0 + 2 * (qx * qy - qw * qz) * r1 + 2 * (qx * qz + qw * qy) * r2;
+    v.y = 2 * (qx * qy + qw * qz) * r0 + (1 - 2 * (qx * qx + qz * qz)) * r1 + 2 * (qy * qz - qw * qx) * r2;
+    v.z = 2 * (qx * qz - qw * qy) * r0 + 2 * (qy * qz + qw * qx) * r1 + (1 - 2 * (qx * qx + qy * qy)) * r2;
+    return v;
 }
 
-// densify_append_dup_kernel (:3365-3412)
-__global__ void k_append_dup(int N, const int *__restrict__ dup, const int *__restrict__ dup_pre,
-                             const int *__restrict__ split_pre, Bufs18 B) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= N || dup[i] == 0) return;
-    const int nS = N > 0 ? split_pre[N - 1] : 0;
-    const size_t dst = (size_t)N + 2 * nS + dup_pre[i] - 1;
-    for (int gi = 0; gi < 6; ++gi) {
-        const int s = B.stride[gi];
-        for (int j = 0; j < s; ++j) B.b[gi][dst * s + j] = B.b[gi][(size_t)i * s + j];
-    }
-    zero_adam(B, dst);
-}
-
-// densify_cull_classify_kernel (:3417-3456)
-__global__ void k_cull(int N_old, int worst, int SD, const int *__restrict__ split_pre, const int *__restrict__ dup_pre,
-                       const int *__restrict__ split, const float *__restrict__ opac,
-                       const float *__restrict__ scales, const float *__restrict__ max2d, float alpha_th,
-                       float scale_th, float screen_size, int check_huge, int check_screen,
-                       int *__restrict__ keep) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= worst) return;
-    const int nS = N_old > 0 ? split_pre[N_old - 1] : 0;
-    const int nD = N_old > 0 ? dup_pre[N_old - 1] : 0;
-    const int N_new = N_old + 2 * nS + nD;
-    if (i >= N_new) {
-        keep[i] = 0;
-        return;
-    }
-    const float os = 1.0f / (1.0f + ms_expf(-opac[i]));
+// The reference's cull test (densify_cull_classify_kernel, :3417-3456) for
+// a row with opacity logit `opac` and scales `sc` (already reduced by
+// log 1.6 where the row is a child or the copy of a split splat).
+__device__ __forceinline__ bool culled(float opac, const float *sc, int SD, float alpha_th, float scale_th,
+                                       bool check_huge) {
+    const float os = 1.0f / (1.0f + ms_expf(-opac));
     bool cull = os < alpha_th;
-    if (i < N_old && split[i] != 0) cull = true;
     if (check_huge) {
-        if (max_scale(scales, i, SD) > scale_th) cull = true;
-        if (check_screen && i < N_old && max2d[i] > screen_size) cull = true;
+        float ms = ms_expf(sc[0]);
+        for (int k = 1; k < SD; ++k) ms = __builtin_fmaxf(ms, ms_expf(sc[k]));
+        if (ms > scale_th) cull = true;
     }
+    return cull;
+}
+
+// One thread per old row i: keep[] of row i and of the rows it appends
+// (children at N + 2 ord + k, the copy at N + 2 nS + dup ord), and the
+// parent of every appended row.  The appended rows carry the parent's
+// opacity; a child's scales are the parent's minus log 1.6, and so are a
+// copy's when its parent is also split (the reference appends the copy
+// after reducing the split parent's scales in place, :3358-3360).
+__global__ __launch_bounds__(256) void k_densify_keep(int N, int nS, int SD, const int *__restrict__ split,
+                                                      const int *__restrict__ dup,
+                                                      const int *__restrict__ split_pre,
+                                                      const int *__restrict__ dup_pre, const float *__restrict__ opac,
+                                                      const float *__restrict__ scales,
+                                                      const float *__restrict__ max2d, float log_size_fac,
+                                                      float alpha_th, float scale_th, float screen_size,
+                                                      int check_huge, int check_screen, int *__restrict__ keep,
+                                                      int *__restrict__ parent) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N) return;
+    const float op = opac[i];
+    float sc[3], sc_dec[3];
+    for (int k = 0; k < SD; ++k) {
+        sc[k] = scales[(size_t)i * SD + k];
+        sc_dec[k] = sc[k] - log_size_fac;
+    }
+    const bool sp = split[i] != 0;
+    bool cull = sp || culled(op, sc, SD, alpha_th, scale_th, check_huge);
+    if (check_huge && check_screen && max2d[i] > screen_size) cull = true;
     keep[i] = cull ? 0 : 1;
+    if (sp) {
+        const int a = 2 * (split_pre[i] - 1);
+        const int kc = culled(op, sc_dec, SD, alpha_th, scale_th, check_huge) ? 0 : 1;
+        keep[N + a] = kc;
+        keep[N + a + 1] = kc;
+        parent[a] = i;
+        parent[a + 1] = i;
+    }
+    if (dup[i]) {
+        const int a = 2 * nS + dup_pre[i] - 1;
+        keep[N + a] = culled(op, sp ? sc_dec : sc, SD, alpha_th, scale_th, check_huge) ? 0 : 1;
+        parent[a] = i;
+    }
 }
 
-// compact_scatter_kernel (:3460-3474) for all 18 buffers in one launch:
-// grid.y selects the buffer, grid.x runs over (element, component).
-__global__ void k_compact(int worst, const int *__restrict__ keep, const int *__restrict__ keep_pre, Bufs18 src,
-                          Bufs18 dst) {
-    const int b = blockIdx.y;
-    const int s = src.stride[b];
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= (int64_t)worst * s) return;
-    const int64_t e = t / s, sub = t - e * s;
-    if (keep[e] == 0) return;
-    dst.b[b][(int64_t)(keep_pre[e] - 1) * s + sub] = src.b[b][t];
+// src_of[output row] = virtual row, from the inclusive scan of keep[].
+__global__ __launch_bounds__(256) void k_densify_src(int n_virt, const int *__restrict__ keep,
+                                                     const int *__restrict__ keep_pre, int *__restrict__ src_of) {
+    const int v = blockIdx.x * blockDim.x + threadIdx.x;
+    if (v < n_virt && keep[v]) src_of[keep_pre[v] - 1] = v;
 }
 
-// compact_copy_back_kernel (:3478-3491)
-__global__ void k_copy_back(int worst, const int *__restrict__ keep_pre, Bufs18 src, Bufs18 dst) {
-    const int b = blockIdx.y;
-    const int s = src.stride[b];
-    const int new_count = keep_pre[worst - 1];
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= (int64_t)new_count * s) return;
-    dst.b[b][t] = src.b[b][t];
+// Output rows are written in blocks of kGatherRows rows of one buffer.
+constexpr int kGatherRows = 256, kMaxDensBufs = 18;
+
+struct GatherBuf {
+    const float *src;  // the caller's buffer (old rows)
+    float *dst;        // the compacted rows (workspace)
+    int stride;        // floats per row
+    uint32_t magic;    // ceil(2^24 / stride): j / stride = (j * magic) >> 24 for j < 2^15
+    int group;         // 0 means, 1 scales, 2.. other parameters
+    int moment;        // 1 for an Adam moment buffer (appended rows are zero)
+    int block0;        // first block of this buffer
+};
+struct GatherArgs {
+    GatherBuf b[kMaxDensBufs];
+    int nbuf, N, nS, SD, n_virt;
+    float log_size_fac;
+    const int *split, *parent, *src_of, *keep_pre;
+    const float *quats, *scales, *rs;  // the parent rows of the children
+};
+
+// Every output row of every buffer, once: workgroup = (buffer, block of
+// kGatherRows output rows), whose floats are contiguous in the output, so
+// each store instruction writes 1 KB of consecutive floats; reads follow
+// the kept rows, which are contiguous runs of old rows.  An old row is
+// copied, an appended row is derived from its parent (moments zero).
+__global__ __launch_bounds__(256) void k_densify_gather(GatherArgs g) {
+    __shared__ int s_src[kGatherRows];
+    int bi = 0;
+    while (bi + 1 < g.nbuf && (int)blockIdx.x >= g.b[bi + 1].block0) ++bi;
+    const GatherBuf B = g.b[bi];
+    const int new_count = g.keep_pre[g.n_virt - 1];
+    const int r0 = ((int)blockIdx.x - B.block0) * kGatherRows;
+    const int rows = min(kGatherRows, new_count - r0);
+    if (rows <= 0) return;
+    if ((int)threadIdx.x < rows) s_src[threadIdx.x] = g.src_of[r0 + threadIdx.x];
+    __syncthreads();
+    const int S = B.stride, total = rows * S;
+    const float *__restrict__ src = B.src;
+    float *__restrict__ dst = B.dst + (size_t)r0 * S;
+    constexpr int U = 4;
+    for (int j0 = threadIdx.x; j0 < total; j0 += 256 * U) {
+        float out[U];
+        int idx[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = j0 + u * 256;
+            idx[u] = j;
+            out[u] = 0.0f;
+            if (j >= total) continue;
+            const int lr = (int)(((uint64_t)(uint32_t)j * B.magic) >> 24);
+            const int c = j - lr * S;
+            const int v = s_src[lr];
+            if (v < g.N) {
+                out[u] = src[(size_t)v * S + c];
+            } else if (!B.moment) {
+                const int a = v - g.N;
+                const int p = g.parent[a];
+                const float val = src[(size_t)p * S + c];
+                const bool child = a < 2 * g.nS;
+                if (B.group == 0 && child) {
+                    const float3 o = split_offset(g.quats, g.scales, g.rs, g.SD, p, a);
+                    out[u] = val + (c == 0 ? o.x : c == 1 ? o.y : o.z);
+                } else if (B.group == 1 && (child || g.split[p])) {
+                    out[u] = val - g.log_size_fac;
+                } else {
+                    out[u] = val;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (idx[u] < total) dst[idx[u]] = out[u];
+    }
+}
+
+// The compacted rows back into the caller's buffers: the first
+// new_count * stride floats of each, in 4096-float blocks.
+constexpr int kCopyFloats = 4096;
+struct CopyArgs {
+    const float *src[kMaxDensBufs];
+    float *dst[kMaxDensBufs];
+    int stride[kMaxDensBufs], block0[kMaxDensBufs + 1];
+    int nbuf, n_virt;
+    const int *keep_pre;
+};
+__global__ __launch_bounds__(256) void k_densify_copy_back(CopyArgs a) {
+    int bi = 0;
+    while (bi + 1 < a.nbuf && (int)blockIdx.x >= a.block0[bi + 1]) ++bi;
+    const int64_t total = (int64_t)a.keep_pre[a.n_virt - 1] * a.stride[bi];
+    const int64_t base = (int64_t)((int)blockIdx.x - a.block0[bi]) * kCopyFloats;
+    if (base >= total) return;
+    const float *__restrict__ s = a.src[bi] + base;
+    float *__restrict__ d = a.dst[bi] + base;
+    const int n = (int)min<int64_t>(kCopyFloats, total - base);
+    constexpr int U = kCopyFloats / 256;
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int j = threadIdx.x + u * 256;
+        v[u] = j < n ? s[j] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int j = threadIdx.x + u * 256;
+        if (j < n) d[j] = v[u];
+    }
 }
 
 inline unsigned nblk(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
@@ -308,34 +396,68 @@ void launch_densify_classify(hipStream_t s, const DensifyArgs &a) {
     launch_scan_i32(s, a.dup, a.dup_pre, N, a.scan_temp);
 }
 
-void launch_densify_apply(hipStream_t s, const DensifyArgs &a, int n_new) {
-    const int N = a.n, worst = n_new;
-    Bufs18 B{}, S{};
+int64_t densify_workspace_floats(int n_virt, int scale_dim, int fr_stride) {
+    // 18 compacted buffers of n_virt rows, each padded to 64 floats
+    const int strides[6] = {3, scale_dim, 4, 3, fr_stride, 1};
+    int64_t f = 0;
+    for (int gi = 0; gi < 6; ++gi) f += 3 * (((int64_t)n_virt * strides[gi] + 63) / 64 * 64);
+    return f;
+}
+
+void launch_densify_apply(hipStream_t s, const DensifyArgs &a, int nS, int n_virt) {
+    const int N = a.n;
+    hipLaunchKernelGGL(k_densify_keep, dim3(nblk(N, 256)), dim3(256), 0, s, N, nS, a.scale_dim, a.split, a.dup,
+                       a.split_pre, a.dup_pre, a.params[5], a.params[1], a.max2d, a.log_size_fac, a.cull_alpha,
+                       a.cull_scale, a.cull_screen, a.check_huge, a.check_screen, a.keep, a.parent);
+    launch_scan_i32(s, a.keep, a.keep_pre, n_virt, a.scan_temp);
+    hipLaunchKernelGGL(k_densify_src, dim3(nblk(n_virt, 256)), dim3(256), 0, s, n_virt, a.keep, a.keep_pre,
+                       a.src_of);
     const int strides[6] = {3, a.scale_dim, 4, 3, a.fr_stride, 1};
+    GatherArgs g{};
+    CopyArgs c{};
+    g.N = N;
+    g.nS = nS;
+    g.SD = a.scale_dim;
+    g.n_virt = n_virt;
+    g.log_size_fac = a.log_size_fac;
+    g.split = a.split;
+    g.parent = a.parent;
+    g.src_of = a.src_of;
+    g.keep_pre = a.keep_pre;
+    g.quats = a.params[2];
+    g.scales = a.params[1];
+    g.rs = a.random;
+    c.n_virt = n_virt;
+    c.keep_pre = a.keep_pre;
+    const int row_blocks = (int)nblk(n_virt, kGatherRows);
+    float *ws = a.workspace;
+    int gb = 0, cb = 0, nb = 0;
     for (int gi = 0; gi < 6; ++gi) {
-        B.b[gi] = a.params[gi];
-        B.b[6 + gi] = a.exp_avg[gi];
-        B.b[12 + gi] = a.exp_avg_sq[gi];
-        S.b[gi] = a.scratch[gi];
-        S.b[6 + gi] = a.scratch[6 + gi];
-        S.b[12 + gi] = a.scratch[12 + gi];
+        if (strides[gi] <= 0) continue;
         for (int r = 0; r < 3; ++r) {
-            B.stride[6 * r + gi] = strides[gi];
-            S.stride[6 * r + gi] = strides[gi];
+            float *buf = r == 0 ? a.params[gi] : r == 1 ? a.exp_avg[gi] : a.exp_avg_sq[gi];
+            GatherBuf &B = g.b[nb];
+            B.src = buf;
+            B.dst = ws;
+            B.stride = strides[gi];
+            B.magic = (uint32_t)(((1u << 24) + strides[gi] - 1) / strides[gi]);
+            B.group = gi;
+            B.moment = r != 0;
+            B.block0 = gb;
+            gb += row_blocks;
+            c.src[nb] = ws;
+            c.dst[nb] = buf;
+            c.stride[nb] = strides[gi];
+            c.block0[nb] = cb;
+            cb += (int)nblk((int64_t)n_virt * strides[gi], kCopyFloats);
+            ws += ((int64_t)n_virt * strides[gi] + 63) / 64 * 64;
+            ++nb;
         }
     }
-    hipLaunchKernelGGL(k_append_split, dim3(nblk(N, 256)), dim3(256), 0, s, N, a.scale_dim, a.split, a.split_pre, a.random,
-                       a.log_size_fac, B);
-    hipLaunchKernelGGL(k_append_dup, dim3(nblk(N, 256)), dim3(256), 0, s, N, a.dup, a.dup_pre, a.split_pre, B);
-    hipLaunchKernelGGL(k_cull, dim3(nblk(worst, 256)), dim3(256), 0, s, N, worst, a.scale_dim, a.split_pre, a.dup_pre, a.split,
-                       a.params[5], a.params[1], a.max2d, a.cull_alpha, a.cull_scale, a.cull_screen, a.check_huge,
-                       a.check_screen, a.keep);
-    launch_scan_i32(s, a.keep, a.keep_pre, worst, a.scan_temp);
-    const int64_t maxs = a.fr_stride > 4 ? a.fr_stride : 4;
-    hipLaunchKernelGGL(k_compact, dim3(nblk((int64_t)worst * maxs, 256), 18), dim3(256), 0, s, worst, a.keep,
-                       a.keep_pre, B, S);
-    hipLaunchKernelGGL(k_copy_back, dim3(nblk((int64_t)worst * maxs, 256), 18), dim3(256), 0, s, worst, a.keep_pre,
-                       S, B);
+    g.nbuf = c.nbuf = nb;
+    c.block0[nb] = cb;
+    hipLaunchKernelGGL(k_densify_gather, dim3(gb), dim3(256), 0, s, g);
+    hipLaunchKernelGGL(k_densify_copy_back, dim3(cb), dim3(256), 0, s, c);
 }
 
 }  // namespace mskern

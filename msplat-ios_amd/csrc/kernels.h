@@ -118,12 +118,6 @@ void launch_loss_fwd_bwd(hipStream_t s, int W, int H, const float *img, const fl
                          float *gm1, float *gs1, float *gs12, double *partials, double *loss_out,
                          float *dL_dimg);
 
-// k_calib.hip: LDS access-pattern calibration, kLdsCalibBlocks workgroups
-// of 256 threads, kLdsCalibReads loads per thread
-constexpr int kLdsCalibBlocks = 1024, kLdsCalibReads = 2000;
-int lds_calib_out_floats();
-void launch_lds_calib(hipStream_t s, int bytes_per_lane, int pattern, float *out);
-
 // k_optim.hip
 void launch_adam(hipStream_t s, float *p, const float *g, float *m, float *v, int64_t n, float step, float b1,
                  float b2, float bc2_sqrt, float eps);
@@ -141,16 +135,21 @@ struct DensifyArgs {
     const float *grad_norm, *vis, *max2d;
     float half_max_dim, log_size_fac;
     float *params[6], *exp_avg[6], *exp_avg_sq[6];
-    float *scratch[18];
+    float *workspace;  // densify_workspace_floats(n_virt, scale_dim, fr_stride) floats
     const float *random;
-    int *split, *dup, *split_pre, *dup_pre, *keep, *keep_pre, *scan_temp;
+    int *split, *dup, *split_pre, *dup_pre, *scan_temp;
+    int *keep, *keep_pre, *src_of;  // n_virt entries each
+    int *parent;                    // n_virt - n entries
 };
 // Classification and the split / dup prefix counts (the count after
 // appending is N + 2 * split_pre[N-1] + dup_pre[N-1]; a splat can be both).
 void launch_densify_classify(hipStream_t s, const DensifyArgs &a);
-// Append split children and dup copies, cull, compact; n_new is the count
-// after appending and must fit the buffers' capacity.
-void launch_densify_apply(hipStream_t s, const DensifyArgs &a, int n_new);
+// Keep flags of the old and appended rows, the gather of every surviving
+// row into the workspace and its copy back into the caller's buffers.
+// n_virt = n + 2 nS + nD (the count after appending) must fit the buffers'
+// capacity; the new count is keep_pre[n_virt - 1].  Strides up to 127.
+int64_t densify_workspace_floats(int n_virt, int scale_dim, int fr_stride);
+void launch_densify_apply(hipStream_t s, const DensifyArgs &a, int nS, int n_virt);
 
 // k_mesh.hip
 // The compaction passes work on chunks of kMeshChunk cells / pixels: one

@@ -7,6 +7,8 @@ import ctypes as C
 import math
 import struct
 
+import time
+
 import numpy as np
 
 from . import _engine as E
@@ -190,28 +192,43 @@ class CapacityScene(DeviceScene):
                 [self._rows(p, s, n, rows) for p, s in zip(self.exp_avg, STRIDES)],
                 [self._rows(p, s, n, rows) for p, s in zip(self.exp_avg_sq, STRIDES)], stats)
 
-    def densify(self, random_normals: np.ndarray, half_max_dim: float, grad_thresh=0.0002, size_thresh=0.01,
+    def stage_samples(self, random_normals: np.ndarray) -> None:
+        """Uploads the [2n, 3] split samples into a device buffer kept across
+        cycles (grown by doubling)."""
+        rs = np.ascontiguousarray(random_normals, np.float32).reshape(-1)
+        have = self._rs.shape[0] if getattr(self, "_rs", None) is not None else 0
+        if have < rs.size:
+            self._rs = E.DeviceArray((max(rs.size, 2 * have),))
+        if rs.size:
+            E.check(E.lib().msplat_hip_upload(self._rs.ptr, rs.ctypes.data, rs.nbytes))
+
+    def densify(self, random_normals: np.ndarray | None, half_max_dim: float, grad_thresh=0.0002, size_thresh=0.01,
                 screen_thresh=0.05, check_screen=1, cull_alpha=0.1, cull_scale=0.5, cull_screen=0.15,
                 check_huge=0) -> int:
-        """msplat_hip_densify with Model::afterTrain's arguments, after growing
-        the buffers to 3n rows (and again to the rows it reports when splats
-        that are both split and duplicated need more); random_normals is
-        [2n, 3].  Returns the new count."""
-        self.ensure_capacity(3 * self.n)
-        d_rs = E.DeviceArray.from_numpy(np.ascontiguousarray(random_normals, np.float32))
+        """msplat_hip_densify with Model::afterTrain's arguments; random_normals
+        is [2n, 3] (None: the samples last staged by stage_samples).  The
+        backing buffers grow (doubling, as Model::ensureCapacity) only when
+        the rows after appending exceed them: the call then reports the rows
+        it needs and changes nothing, and runs again.  Returns the new count;
+        the growth time of this call is kept in `last_grow_ms`."""
+        if random_normals is not None:
+            self.stage_samples(random_normals)
         P6 = C.c_void_p * 6
         newc = C.c_int()
+        self.last_grow_ms = 0.0
         for _ in range(2):
             rc = E.lib().msplat_hip_densify(self.n, self.cap, grad_thresh, size_thresh, screen_thresh, check_screen,
                                             cull_alpha, cull_scale, cull_screen, check_huge, self.grad_norm.ptr,
                                             self.vis.ptr, self.max2d.ptr, half_max_dim,
                                             P6(*[p.ptr for p in self.params]), STRIDES[4],
                                             P6(*[m.ptr for m in self.exp_avg]),
-                                            P6(*[v.ptr for v in self.exp_avg_sq]), d_rs.ptr, C.byref(newc))
+                                            P6(*[v.ptr for v in self.exp_avg_sq]), self._rs.ptr, C.byref(newc))
             if rc != E.MSPLAT_E_CAPACITY:
                 break
-            # more than 3n rows after appending: nothing was modified
+            # more rows after appending than the buffers hold: nothing was modified
+            t0 = time.perf_counter()
             self.ensure_capacity(int(newc.value))
+            self.last_grow_ms = (time.perf_counter() - t0) * 1e3
         E.check(rc)
         self.n = int(newc.value)
         return self.n

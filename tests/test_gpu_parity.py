@@ -115,24 +115,6 @@ def test_raster_forward_bitexact(name, orc, eng):
         _assert_bitexact(out[k], fwd[k], k)
 
 
-def test_lds_calibration_entry(eng):
-    """msplat_hip_lds_calibration: every (width, pattern) case runs and is
-    timed; a 32-way-conflicting 4-byte pattern is slower than the contiguous
-    one; bad arguments are refused before any launch."""
-    ms = C.c_float()
-    times = {}
-    for width in (4, 8, 16):
-        for pattern in range(5):
-            # the second launch is timed (the first carries the kernel's load)
-            for _ in range(2):
-                E.check(E.lib().msplat_hip_lds_calibration(width, pattern, C.byref(ms)))
-            assert ms.value > 0.0
-            times[width, pattern] = ms.value
-    assert times[4, 3] > 3.0 * times[4, 0]
-    for width, pattern in ((2, 0), (16, 5), (4, -1)):
-        assert E.lib().msplat_hip_lds_calibration(width, pattern, C.byref(ms)) == -2
-
-
 def test_fast_reciprocal_is_the_division(eng):
     """The rasterizer's 1 / ray.z (hardware reciprocal + one Newton step)
     equals the correctly rounded division, the golden model's, for every

@@ -5,6 +5,7 @@ from __future__ import annotations
 
 import ctypes as C
 import json
+import os
 import re
 import struct
 import subprocess
@@ -515,3 +516,119 @@ def test_dataset_from_arrays_validation():
     ds = msplat.Dataset.from_arrays([img, img], np.stack([np.eye(4)] * 2).astype(np.float32),
                                     np.array([[10, 10, 4, 4]] * 2, np.float32))
     assert ds.num_train == 2 and ds.num_test == 0
+
+
+def _jpeg_segments(raw: bytes):
+    """(marker, payload offset, payload length) of each header segment of a
+    JPEG file up to its first scan."""
+    out, p = [], 2
+    while p + 4 <= len(raw):
+        marker, ln = raw[p + 1], int.from_bytes(raw[p + 2:p + 4], "big")
+        out.append((marker, p + 4, ln - 2))
+        if marker == 0xDA:
+            break
+        p += 2 + ln
+    return out
+
+
+def _jpeg_crafted() -> dict:
+    """Malformed variants of base420.jpg that a careless decoder would read
+    or write out of bounds on: DHT counts that are not a prefix code (a DC
+    and an AC table with every code at length 1), Huffman values outside
+    the 8-bit ranges (a DC category of 15, an AC size of 14), and a frame
+    with luma 3x3 and chroma 2x2 sampling (ratio 1.5)."""
+    raw = (JPEG_DIR / "base420.jpg").read_bytes()
+    seg = _jpeg_segments(raw)
+    tables = []  # (class, counts offset, values offset, total)
+    for marker, off, ln in seg:
+        if marker != 0xC4:
+            continue
+        i = off
+        while i < off + ln:
+            total = sum(raw[i + 1:i + 17])
+            tables.append((raw[i] >> 4, i + 1, i + 17, total))
+            i += 17 + total
+    out = {}
+    for cls, name in ((0, "dc"), (1, "ac")):
+        _, c_off, v_off, total = next(t for t in tables if t[0] == cls)
+        b = bytearray(raw)
+        b[c_off:c_off + 16] = bytes([total] + [0] * 15)  # all codes at length 1
+        out[f"overfull_{name}"] = bytes(b)
+        b = bytearray(raw)
+        b[v_off] = 15 if cls == 0 else 0x0E
+        out[f"badvalue_{name}"] = bytes(b)
+    marker, off, ln = next(s for s in seg if s[0] == 0xC0)
+    b = bytearray(raw)
+    b[off + 7] = 0x33  # Y 3x3
+    b[off + 10] = 0x22  # Cb 2x2
+    b[off + 13] = 0x22  # Cr 2x2
+    out["ratio_3_2"] = bytes(b)
+    return out
+
+
+def test_jpeg_decoder_rejects_malformed_tables(tmp_path):
+    """Each crafted variant raises cleanly, in a child process so that a
+    crash fails the test rather than ending the test run."""
+    paths = []
+    for name, blob in _jpeg_crafted().items():
+        (tmp_path / f"{name}.jpg").write_bytes(blob)
+        paths.append(str(tmp_path / f"{name}.jpg"))
+    script = tmp_path / "crafted.py"
+    script.write_text(f"""
+import sys
+sys.path.insert(0, {str(Path(__file__).resolve().parent.parent / 'msplat-ios_amd')!r})
+from msplat import _core
+for p in {paths!r}:
+    try:
+        _core._read_image(p)
+        print('decoded', p)
+    except RuntimeError as e:
+        print('raised', p, e)
+""")
+    r = subprocess.run([sys.executable, str(script)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = r.stdout.splitlines()
+    assert len(lines) == len(paths) and all(ln.startswith("raised") for ln in lines), lines
+
+
+def test_jpeg_decoder_under_address_sanitizer(tmp_path):
+    """The decoder built with AddressSanitizer and UBSan (tests/native/
+    jpeg_check.cpp, host code only) over every fixture, the crafted
+    malformed files and 300 random corruptions: no sanitizer report, the
+    fixtures decode, the crafted files are refused."""
+    import shutil
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not available")
+    repo = Path(__file__).resolve().parent.parent
+    exe = tmp_path / "jpeg_check"
+    cmd = [gxx, "-O1", "-g", "-std=c++17", "-fsanitize=address,undefined", "-fno-sanitize-recover=undefined",
+           "-fno-omit-frame-pointer", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+           f"-I{repo / 'msplat-ios_amd/csrc/host'}", f"-I{repo / 'include'}",
+           str(repo / "tests/native/jpeg_check.cpp"), str(repo / "msplat-ios_amd/csrc/host/jpeg.cpp"), "-o", str(exe)]
+    b = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    if b.returncode != 0:
+        pytest.skip(f"sanitizer build unavailable: {b.stderr[-500:]}")
+    fixtures = sorted(JPEG_DIR.glob("*.jpg"))
+    crafted = []
+    for name, blob in _jpeg_crafted().items():
+        (tmp_path / f"{name}.jpg").write_bytes(blob)
+        crafted.append(tmp_path / f"{name}.jpg")
+    rng = np.random.default_rng(11)
+    fuzz = []
+    for k in range(300):
+        raw = bytearray(fixtures[k % len(fixtures)].read_bytes())
+        if k % 2:
+            raw = raw[: int(rng.integers(2, len(raw)))]
+        for _ in range(int(rng.integers(1, 6))):
+            raw[int(rng.integers(2, len(raw)))] = int(rng.integers(256))
+        fuzz.append(tmp_path / f"f{k}.jpg")
+        fuzz[-1].write_bytes(bytes(raw))
+    files = fixtures + crafted + fuzz
+    r = subprocess.run([str(exe), *map(str, files)], capture_output=True, text=True, timeout=600,
+                       env={**os.environ, "ASAN_OPTIONS": "detect_leaks=0"})
+    assert r.returncode == 0 and "Sanitizer" not in r.stderr and "runtime error" not in r.stderr, r.stderr[-3000:]
+    lines = r.stdout.splitlines()
+    assert len(lines) == len(files)
+    assert all(ln.startswith("ok") for ln in lines[:len(fixtures)])
+    assert all(ln.startswith("error") for ln in lines[len(fixtures):len(fixtures) + len(crafted)])
