@@ -389,10 +389,13 @@ __device__ __forceinline__ void count_tiles(const unsigned long long *__restrict
 
 // Counts the entries of the super-tile's 16 tiles into tile_counts, then
 // sorts the super-tile list in place: up to kChunk keys in one LDS sort,
-// up to kHuge in kChunk runs queued on big_list for the merge passes.
+// up to huge_th in kChunk runs queued on big_list for the merge passes.
 // Longer lists are only queued, on big_list and huge_list (their tile counts
 // zeroed): k_sort_chunks sorts their runs on many workgroups, and after the
 // merge k_count_chunks / k_emit_chunks count and emit them chunk by chunk.
+// huge_th is kHuge, or kChunk when some list exceeds kHuge: the merge and
+// chunk passes then run anyway, and every list above kChunk joins them
+// instead of holding one workgroup for several serial chunk sorts.
 template <bool PACKED>
 __global__ __launch_bounds__(kSortThreads) void k_sort_super(int tiles_x, int tiles_y, int sxn,
                                                              const int *__restrict__ offsets,
@@ -401,7 +404,7 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_super(int tiles_x, int ti
                                                              int *__restrict__ tile_counts,
                                                              int *__restrict__ big_list, int *__restrict__ stats,
                                                              int *__restrict__ huge_list,
-                                                             int *__restrict__ huge_stats) {
+                                                             int *__restrict__ huge_stats, int huge_th) {
     __shared__ unsigned long long s[kChunk];
     __shared__ int s_tc[kSuper * kSuper];
     const int t = blockIdx.x;
@@ -410,13 +413,13 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_super(int tiles_x, int ti
     const int stx = (t % sxn) * kSuper, sty = (t / sxn) * kSuper;
     if (threadIdx.x < kSuper * kSuper) s_tc[threadIdx.x] = 0;
     __syncthreads();
-    if (cnt <= kHuge) count_tiles<PACKED>(keys + start, cnt, stx, sty, rect, s_tc);
+    if (cnt <= huge_th) count_tiles<PACKED>(keys + start, cnt, stx, sty, rect, s_tc);
     if (threadIdx.x < kSuper * kSuper) {
         const int tx = stx + (int)threadIdx.x % kSuper, ty = sty + (int)threadIdx.x / kSuper;
         if (tx < tiles_x && ty < tiles_y) tile_counts[ty * tiles_x + tx] = s_tc[threadIdx.x];
     }
     if (cnt > kChunk && threadIdx.x == 0) big_list[atomicAdd(&stats[2], 1)] = t;
-    if (cnt > kHuge) {
+    if (cnt > huge_th) {
         if (threadIdx.x == 0) huge_list[atomicAdd(&huge_stats[0], 1)] = t;
         return;
     }
@@ -518,40 +521,76 @@ __global__ __launch_bounds__(kSortThreads) void k_count_chunks(int tiles_x, int 
     }
 }
 
-// One merge pass over the lists longer than kChunk: runs of length L are
-// merged pairwise.  Each key lands at (its index in its run) + (number of
-// keys of the partner run that are smaller); keys are unique (the id is in
-// the low word), so this is a permutation.
-__global__ __launch_bounds__(256) void k_merge_pass(int L, const int *__restrict__ offsets,
+// ---- merge passes over the lists longer than kChunk ------------------------
+//
+// Runs of L sorted keys are merged pairwise, L = kChunk, 2 kChunk, ... .  A
+// pass is a merge path (Odeh et al., "Merge Path -- parallel merging made
+// simple", 2012): the merged output of a pair is cut into tiles of kMergeTile
+// keys; a workgroup finds where its tile's first and last diagonal cross the
+// two runs (one binary search each), stages the tile's keys of both runs in
+// LDS with coalesced loads, and each thread merges 8 outputs from its own
+// diagonal of the staged keys.  Every key is read and written once per pass
+// and the output leaves through LDS in coalesced 2 KB rows.  Keys are unique
+// (the id is in the low word), so the merge is a permutation.
+constexpr int kMergeTile = 2048, kMergeItems = kMergeTile / 256;
+
+// The number of keys of A among the first d keys of the merge of the
+// ascending runs A[0, la) and B[0, lb).
+template <typename K>
+__device__ __forceinline__ int merge_split(const K *__restrict__ A, int la, const K *__restrict__ B, int lb, int d) {
+    int lo = max(0, d - lb), hi = min(d, la);
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (A[mid] < B[d - mid - 1])
+            lo = mid + 1;
+        else
+            hi = mid;
+    }
+    return lo;
+}
+
+__global__ __launch_bounds__(256) void k_merge_path(int L, const int *__restrict__ offsets,
                                                     const int *__restrict__ big_list, const int *__restrict__ stats,
                                                     const unsigned long long *__restrict__ src,
                                                     unsigned long long *__restrict__ dst) {
+    __shared__ unsigned long long s_k[kMergeTile];
+    __shared__ int s_split[2];
     const int nbig = stats[2];
     for (int b = blockIdx.y; b < nbig; b += gridDim.y) {
         const int t = big_list[b];
         const int start = offsets[t], cnt = offsets[t + 1] - start;
-        for (int i = blockIdx.x * 256 + threadIdx.x; i < cnt; i += gridDim.x * 256) {
-            const int run = i / L;
-            const int rs = run * L;
-            const int pair_base = (run & ~1) * L;
-            const unsigned long long key = src[start + i];
-            int os, olen;
-            if (run & 1) {
-                os = rs - L;
-                olen = L;
-            } else {
-                os = rs + L;
-                olen = max(0, min(L, cnt - os));
+        // 2L is a multiple of kMergeTile, so no tile straddles two pairs
+        for (int o0 = blockIdx.x * kMergeTile; o0 < cnt; o0 += gridDim.x * kMergeTile) {
+            const int pair_base = o0 / (2 * L) * (2 * L);
+            const int la = min(L, cnt - pair_base), lb = max(0, min(L, cnt - pair_base - L));
+            const unsigned long long *A = src + start + pair_base, *B = A + la;
+            const int d0 = o0 - pair_base, d1 = min(d0 + kMergeTile, la + lb);
+            if (threadIdx.x < 2) s_split[threadIdx.x] = merge_split(A, la, B, lb, threadIdx.x ? d1 : d0);
+            __syncthreads();
+            const int a0 = s_split[0], a1 = s_split[1];
+            const int na = a1 - a0, n = d1 - d0;
+            const int b0 = d0 - a0;
+            for (int k = threadIdx.x; k < n; k += 256) s_k[k] = k < na ? A[a0 + k] : B[b0 + k - na];
+            __syncthreads();
+            const int dd = min(kMergeItems * (int)threadIdx.x, n);
+            const int nb = n - na;
+            int ia = merge_split(s_k, na, s_k + na, nb, dd), ib = dd - ia;
+            unsigned long long out[kMergeItems];
+#pragma unroll
+            for (int k = 0; k < kMergeItems; ++k) {
+                const unsigned long long x = ia < na ? s_k[ia] : ~0ull, y = ib < nb ? s_k[na + ib] : ~0ull;
+                const bool take_a = ib >= nb || (ia < na && x < y);
+                out[k] = take_a ? x : y;
+                ia += take_a ? 1 : 0;
+                ib += take_a ? 0 : 1;
             }
-            int lo = 0, hi = olen;
-            while (lo < hi) {
-                const int mid = (lo + hi) >> 1;
-                if (src[start + os + mid] < key)
-                    lo = mid + 1;
-                else
-                    hi = mid;
-            }
-            dst[start + pair_base + (i - rs) + lo] = key;
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < kMergeItems; ++k)
+                if (dd + k < n) s_k[dd + k] = out[k];
+            __syncthreads();
+            for (int k = threadIdx.x; k < n; k += 256) dst[start + o0 + k] = s_k[k];
+            __syncthreads();
         }
     }
 }
@@ -621,20 +660,21 @@ __device__ __forceinline__ void emit_range(const unsigned long long *__restrict_
     }
 }
 
-// Emits each super-tile list of at most kHuge entries into its 16 tile
+// Emits each super-tile list of at most huge_th entries into its 16 tile
 // lists (longer lists: k_emit_chunks).
 template <bool PACKED>
 __global__ __launch_bounds__(256) void k_emit_tiles(int tiles_x, int tiles_y, int sxn,
                                                     const int *__restrict__ soffsets,
                                                     const unsigned long long *__restrict__ skeys,
                                                     const uint2 *__restrict__ rect,
-                                                    const int *__restrict__ toffsets, int *__restrict__ ids) {
+                                                    const int *__restrict__ toffsets, int *__restrict__ ids,
+                                                    int huge_th) {
     __shared__ int s_gid[kWin];
     __shared__ unsigned short s_rr[kWin];
     const int st = blockIdx.x;
     const int stx = (st % sxn) * kSuper, sty = (st / sxn) * kSuper;
     const int start = soffsets[st], cnt = soffsets[st + 1] - start;
-    if (cnt > kHuge) return;
+    if (cnt > huge_th) return;
     const int ty = sty + (int)(threadIdx.x >> 6);
     int out[kSuper];
 #pragma unroll
@@ -739,9 +779,11 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
     if (n > 0)
         hipLaunchKernelGGL(packed ? k_scatter_super<true> : k_scatter_super<false>, dim3(blocks), dim3(kBinThreads), 0,
                            s, n, chunk, sxn, NS, radii, r2, depths, super_offsets, super_cm, k);
-    hipLaunchKernelGGL(packed ? k_sort_super<true> : k_sort_super<false>, dim3(NS), dim3(kSortThreads), 0, s, tiles_x,
-                       tiles_y, sxn, super_offsets, k, r2, tile_counts, big_list, super_stats, huge_list, huge_stats);
     const bool big = super_max > kHuge;
+    const int huge_th = big ? kChunk : kHuge;
+    hipLaunchKernelGGL(packed ? k_sort_super<true> : k_sort_super<false>, dim3(NS), dim3(kSortThreads), 0, s, tiles_x,
+                       tiles_y, sxn, super_offsets, k, r2, tile_counts, big_list, super_stats, huge_list, huge_stats,
+                       huge_th);
     // huge lists: kChunk runs sorted on many workgroups, then merged
     const dim3 big_grid(std::min(256, (super_max + kChunk - 1) / kChunk), 16);
     if (big) {
@@ -749,8 +791,9 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
         hipLaunchKernelGGL(k_sort_chunks, big_grid, dim3(kSortThreads), 0, s, super_offsets, huge_list, huge_stats, k);
     }
     unsigned long long *src = k, *dst = kt;
+    const dim3 merge_grid(std::min(512, (super_max + kMergeTile - 1) / kMergeTile), 16);
     for (int L = kChunk; L < super_max; L <<= 1) {
-        hipLaunchKernelGGL(k_merge_pass, dim3(64, 64), dim3(256), 0, s, L, super_offsets, big_list, super_stats, src,
+        hipLaunchKernelGGL(k_merge_path, merge_grid, dim3(256), 0, s, L, super_offsets, big_list, super_stats, src,
                            dst);
         std::swap(src, dst);
     }
@@ -764,7 +807,7 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
                            chunk_counts, tile_counts);
     launch_scan_counts(s, T, tile_counts, tile_offsets, nullptr, tile_stats, tile_temp);
     hipLaunchKernelGGL(packed ? k_emit_tiles<true> : k_emit_tiles<false>, dim3(NS), dim3(256), 0, s, tiles_x, tiles_y,
-                       sxn, super_offsets, k, r2, tile_offsets, ids);
+                       sxn, super_offsets, k, r2, tile_offsets, ids, huge_th);
     if (big)
         hipLaunchKernelGGL(packed ? k_emit_chunks<true> : k_emit_chunks<false>, big_grid, dim3(256), 0, s, tiles_x,
                            tiles_y, sxn, super_offsets, huge_list, huge_stats, chunk_base, chunk_counts, k, r2,

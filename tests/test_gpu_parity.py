@@ -126,12 +126,18 @@ def test_fast_reciprocal_is_the_division(eng):
     assert bad.value == 0
 
 
-def test_overflow_tiles_merge_path(orc, eng):
+@pytest.mark.parametrize("wide", [False, True], ids=["packed-keys", "wide-keys"])
+def test_overflow_tiles_merge_path(wide, orc, eng):
     """Tiles far above 2048 intersections: the chunked LDS sort + global
-    merge must give the oracle's full (untruncated) per-tile order."""
+    merge must give the oracle's full (untruncated) per-tile order, with
+    either key layout."""
     scene = S.make_scene(4, n=100_000, width=480, height=270, num_cameras=2)
-    print(f"[overflow] n={scene.n}", flush=True)
-    ocam, proj, bins, fwd, ds, gcam, out = _forward_both(scene, 0, orc, eng)
+    print(f"[overflow] n={scene.n} wide={wide}", flush=True)
+    E.check(E.lib().msplat_hip_set_wide_keys(1 if wide else 0))
+    try:
+        ocam, proj, bins, fwd, ds, gcam, out = _forward_both(scene, 0, orc, eng)
+    finally:
+        E.check(E.lib().msplat_hip_set_wide_keys(0))
     assert bins["tile_counts"].max() > 8 * 2048, bins["tile_counts"].max()
     _assert_bitexact(E.last("tile_offsets"), bins["tile_offsets"], "tile offsets")
     _assert_bitexact(E.last("gaussian_ids"), bins["ids"], "per-tile sorted ids")
