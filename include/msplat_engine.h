@@ -287,6 +287,9 @@ enum {
     MSPLAT_LAST_DL_DMEAN2D,       /* [N,2]                               */
     MSPLAT_LAST_DL_DFEATURES_DC,  /* [N,3]                               */
     MSPLAT_LAST_DL_DFEATURES_REST,/* [N,K,3]                             */
+    MSPLAT_LAST_BLEND_LOG,        /* [4I,4] u32 wave blend logs          */
+    MSPLAT_LAST_BLEND_CKPT,       /* [4I+64] f32 their checkpoints       */
+    MSPLAT_LAST_WAVE_COUNTS,      /* [T,4]  i32 entries per wave log     */
     MSPLAT_LAST_COUNT
 };
 /* Returns the device pointer and element count of a cached buffer (NULL /
@@ -294,7 +297,13 @@ enum {
  * packed records on each call (asynchronously, on the engine stream).  The
  * raster gradients (GRADS16, DL_DTRANSMAT, DL_DNORMAL3D, DL_DOPACITY,
  * DL_DCOLORS) are those of the most recent train step and exist until the
- * next forward. */
+ * next forward.  BLEND_LOG / BLEND_CKPT / WAVE_COUNTS are the rasterizer's
+ * per-wave blend logs (wave w of tile t: entries [0, WAVE_COUNTS[4t + w]) at
+ * 4 * offset(t) + w * len(t), each {ballot low, ballot high, list position,
+ * gaussian id}; checkpoint c of that wave, every 64th entry, at the same slot
+ * index + lane), written by the training forward or a backward's replay;
+ * they exist once such a forward ran on the current tile lists (a test
+ * accessor, no counterpart in the reference). */
 int msplat_hip_last(int which, void **ptr_dev, int64_t *numel);
 
 /* Per-kernel timings of the most recent train step / render, in ms, from
@@ -332,6 +341,13 @@ int msplat_hip_check_fast_rcp(int efield_lo, int efield_hi, int64_t *mismatches)
  * tests can check it against the golden model on small scenes; the tile
  * lists are the same either way.  No counterpart in the reference. */
 int msplat_hip_set_wide_keys(int on);
+/* Rasterizer self-test hook.  Tiles whose list holds at least len entries
+ * (4096 by default) are rendered pixel by pixel, each 2x2 pixel block on its
+ * own wave, instead of by one workgroup per tile; the outputs, blend log and
+ * checkpoints are the same either way.  A small len sends ordinary tiles
+ * down that path, so the tests can check it on small scenes; len <= 0
+ * restores the default.  No counterpart in the reference. */
+int msplat_hip_set_deep_tile_len(int len);
 
 /* ---- 3DGS mode ------------------------------------------------------------
  * 3D Gaussians (scales [N,3], log) projected with the reference's EWA

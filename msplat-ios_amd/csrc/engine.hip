@@ -54,6 +54,10 @@ const char *kStageNames[ST_COUNT] = {"project_fwd", "tile_scan", "scatter_sort",
 
 constexpr size_t kD2HChunk = size_t(8) << 20;  // bytes per pinned download chunk
 
+// Deep-tile threshold: no tile of the 500k and 3M-splat blob workloads holds
+// more than 3.3k entries; the overflow workload's cluster tiles hold up to 200k.
+constexpr int kDefaultDeepLen = 4096;
+
 struct Engine {
     bool ready = false;
     int device = 0;
@@ -106,6 +110,12 @@ struct Engine {
     bool timing = false;       // HIP events per stage
     bool count_pairs = false;  // raster pair counter
     bool wide_keys = false;    // binning test hook: the wide key layout at any N
+    // tiles whose list holds at least deep_len entries are rendered pixel by
+    // pixel (mskern::DeepTiles); n_deep of them in the current frame
+    int deep_len = kDefaultDeepLen, n_deep = 0;
+    DevBuf deep_list, deep_pos, deep_tb, deep_cnt;
+    hipStream_t deep_stream = nullptr;  // default priority, non-blocking
+    hipEvent_t deep_fork = nullptr, deep_join = nullptr;
     hipEvent_t ev[ST_COUNT + 1] = {};
     float stage_ms[ST_COUNT] = {};
     bool stage_valid[ST_COUNT] = {};
@@ -282,6 +292,29 @@ int raster_fwd_locked(bool log, bool full) {
     uint32_t *lg = nullptr;
     float *tc = nullptr;
     int *wc = nullptr;
+    mskern::DeepTiles deep;
+    if (E.n_deep > 0 && !E.gs3d) {
+        deep.n = E.n_deep;
+        deep.len = E.deep_len;
+        deep.list = P<int>(E.deep_list);
+        if (!E.deep_stream) {
+            HIPC(hipStreamCreateWithFlags(&E.deep_stream, hipStreamNonBlocking));
+            HIPC(hipEventCreateWithFlags(&E.deep_fork, hipEventDisableTiming));
+            HIPC(hipEventCreateWithFlags(&E.deep_join, hipEventDisableTiming));
+        }
+        deep.stream = E.deep_stream;
+        deep.fork = E.deep_fork;
+        deep.join = E.deep_join;
+        if (log) {
+            const size_t ent = (size_t)mskern::deep_pixel_entries(E.n_deep);
+            CHECK(ensure(E.deep_pos, ent * 4));
+            CHECK(ensure(E.deep_tb, ent * 4));
+            CHECK(ensure(E.deep_cnt, (size_t)E.n_deep * 256 * 4));
+            deep.pos = P<int>(E.deep_pos);
+            deep.tb = P<float>(E.deep_tb);
+            deep.cnt = P<int>(E.deep_cnt);
+        }
+    }
     if (log) {
         CHECK(ensure(E.blend_log, (size_t)4 * (size_t)E.num_isect * mskern::kBlendLogEntryBytes));
         // a checkpoint is 64 floats from its log slot on, so the last wave's
@@ -308,7 +341,8 @@ int raster_fwd_locked(bool log, bool full) {
                               P<int>(E.final_idx),
                               P<float>(E.out_depth), P<float>(E.out_normal), P<float>(E.out_alpha),
                               P<float>(E.out_median), P<float>(E.out_dist),
-                              E.count_pairs ? P<unsigned long long>(E.pair_counter) : nullptr, lg, tc, wc, full);
+                              E.count_pairs ? P<unsigned long long>(E.pair_counter) : nullptr, lg, tc, wc, full,
+                              deep);
     E.log_valid = E.log_valid || log;
     E.full_valid = E.full_valid || full;
     return MSPLAT_OK;
@@ -343,7 +377,7 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     CHECK(ensure(E.super_tmp, (size_t)mskern::tile_scan_temp_ints(NS) * 4));
     // stats (ints): [0..1] tiles: total, largest; [4..6] super-tiles: total,
     // largest, long lists; [8..9] 64-bit intersection count from the
-    // projection; [12..13] huge lists, their chunks
+    // projection; [12..13] huge lists, their chunks; [14] deep tiles
     CHECK(ensure(E.stats, 64));
     CHECK(ensure(E.big_list, (size_t)NS * 4));
     CHECK(ensure(E.out_img, Pn * 12));
@@ -414,6 +448,15 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
                              P<int>(E.huge_list), P<int>(E.stats) + 12, P<int>(E.chunk_base), P<int>(E.chunk_counts),
                              P<int>(E.counts), P<int>(E.offsets), P<int>(E.stats), P<int>(E.scan_tmp), P<int>(E.ids),
                              E.wide_keys);
+    // a tile's list is at most its super-tile's: no deep tile below that
+    E.n_deep = 0;
+    if (!gs3d && super_max >= E.deep_len) {
+        CHECK(ensure(E.deep_list, (size_t)T * 4));
+        mskern::launch_deep_tiles(s, T, P<int>(E.offsets), E.deep_len, P<int>(E.deep_list), P<int>(E.stats) + 14);
+        HIPC(hipMemcpyAsync(E.pinned_i + 14, P<int>(E.stats) + 14, sizeof(int), hipMemcpyDeviceToHost, s));
+        HIPC(hipStreamSynchronize(s));
+        E.n_deep = E.pinned_i[14];
+    }
     stage_mark(ST_RASTER_FWD);
     CHECK(raster_fwd_locked(log, full));
     HIPC(hipGetLastError());
@@ -530,6 +573,15 @@ int last_locked(int which, void **ptr, int64_t *numel) {
         case MSPLAT_LAST_DL_DFEATURES_REST:
             if (E.have_grads) { *ptr = E.dfrest.p; *numel = N * E.K3; }
             return MSPLAT_OK;
+        case MSPLAT_LAST_BLEND_LOG:
+            if (E.log_valid) { *ptr = E.blend_log.p; *numel = 16 * (int64_t)E.num_isect; }
+            return MSPLAT_OK;
+        case MSPLAT_LAST_BLEND_CKPT:
+            if (E.log_valid) { *ptr = E.t_ckpt.p; *numel = 4 * (int64_t)E.num_isect + 64; }
+            return MSPLAT_OK;
+        case MSPLAT_LAST_WAVE_COUNTS:
+            if (E.log_valid) { *ptr = E.wave_cnt.p; *numel = 4 * (int64_t)E.tiles_x * E.tiles_y; }
+            return MSPLAT_OK;
         default: set_err("unknown buffer id %d", which); return MSPLAT_E_ARG;
     }
 }
@@ -563,11 +615,12 @@ void msplat_hip_cleanup(void) {
     Engine &E = g_eng;
     if (!E.ready) return;
     (void)hipStreamSynchronize(E.stream);
+    if (E.deep_stream) (void)hipStreamSynchronize(E.deep_stream);
     DevBuf *all[] = {&E.rec, &E.depths, &E.radii, &E.rect, &E.grads16, &E.colors_raw, &E.counts, &E.scan_tmp, &E.super_counts, &E.super_offsets, &E.super_cm, &E.super_tmp, &E.offsets,
                      &E.stats, &E.big_list, &E.huge_list, &E.chunk_base, &E.chunk_counts, &E.keys, &E.keys_tmp, &E.ids, &E.blend_log, &E.t_ckpt, &E.wave_cnt, &E.selfcheck, &E.out_img, &E.final_Ts,
                      &E.final_idx, &E.out_depth, &E.out_normal, &E.out_alpha, &E.out_median, &E.out_dist,
                      &E.dL_dimg, &E.gm1, &E.gs1, &E.gs12, &E.partials, &E.loss, &E.dmeans, &E.dscales,
-                     &E.dquats, &E.dmean2d, &E.dfdc, &E.dfrest, &E.dens_flags, &E.dens_scan, &E.dens_keep, &E.dens_ws, &E.pair_counter,
+                     &E.dquats, &E.dmean2d, &E.dfdc, &E.dfrest, &E.dens_flags, &E.dens_scan, &E.dens_keep, &E.dens_ws, &E.deep_list, &E.deep_pos, &E.deep_tb, &E.deep_cnt, &E.pair_counter,
                      &E.rgba, &E.tsdf_views, &E.tsdf_masks, &E.mc_cases, &E.chunk_cnt, &E.chunk_off};
     for (DevBuf *b : all) {
         if (b->p) (void)hipFree(b->p);
@@ -578,6 +631,7 @@ void msplat_hip_cleanup(void) {
         b = DevBuf{};
     }
     E.dens_rows = 0;
+    E.n_deep = 0;
     E.n = 0;
     E.num_isect = 0;
     E.have_grads = false;
@@ -1312,6 +1366,14 @@ int msplat_hip_set_wide_keys(int on) {
     API_BEGIN
     ENSURE_INIT();
     g_eng.wide_keys = on != 0;
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_set_deep_tile_len(int len) {
+    API_BEGIN
+    ENSURE_INIT();
+    g_eng.deep_len = len > 0 ? len : kDefaultDeepLen;
     return MSPLAT_OK;
     API_END
 }

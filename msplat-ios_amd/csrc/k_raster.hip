@@ -79,7 +79,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
     float *__restrict__ out_img, float *__restrict__ final_Ts, int *__restrict__ final_idx, float *__restrict__ out_depth,
     float *__restrict__ out_normal, float *__restrict__ out_alpha, float *__restrict__ out_median,
     float *__restrict__ out_dist, unsigned long long *__restrict__ pair_counter, uint4 *__restrict__ blend_log,
-    float *__restrict__ t_ckpt, int *__restrict__ wave_cnt) {
+    float *__restrict__ t_ckpt, int *__restrict__ wave_cnt, int deep_len) {
     const int tile = xcd_strip_tile(blockIdx.x, tiles_x, T / tiles_x);
     if (tile < 0) return;
     __shared__ float4 s_rec[(FULL_OUT ? 6 : 5) * kThreads];  // the batch's records (load_batch planes)
@@ -95,6 +95,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
     asm volatile("" : "+v"(px), "+v"(py));
     const float sx0 = (float)(tx * 16), sy0 = (float)(ty * 16);
     const int start = offsets[tile], end = offsets[tile + 1];
+    if (end - start >= deep_len) return;  // k_raster_deep renders it
     const float bg0 = bgp[0], bg1 = bgp[1], bg2 = bgp[2];
     const size_t log_base = 4 * (size_t)start + (size_t)wave * (size_t)(end - start);
     uint4 *wave_log = LOG ? blend_log + log_base : nullptr;
@@ -578,6 +579,381 @@ __global__ __launch_bounds__(256) void k_check_rcp(uint32_t efield, unsigned lon
     if ((threadIdx.x & 63) == 0 && n) atomicAdd(bad, n);
 }
 
+
+// ---- deep tiles -----------------------------------------------------------
+//
+// A tile whose list holds thousands of entries (the overflow workload's
+// tiles over a dense cluster) is one workgroup's serial walk in
+// k_raster_fwd: each of its four waves visits most of the list, and a lone
+// wave issues a ~57-instruction visit only every few cycles, so such tiles
+// finish long after the rest of the image.  The deep-tile path walks each
+// pixel's list independently instead: a wave takes a 2x2 pixel block and 64
+// consecutive list entries at a time, one per lane; every lane evaluates
+// its entry against each pixel (eval_pair, the same arithmetic on the same
+// centred rows), and the entries that pass are blended in list order by a
+// scalar loop over the ballot, with the reference's front-to-back
+// recurrences.  Each pixel sees the same splats in the same order with the
+// same operations as in k_raster_fwd, so every output is bit-identical; a
+// deep tile's 256 pixels run on 64 waves instead of 4, on a stream of their
+// own beside the per-tile kernel.
+//
+// For the backward, the training forward also records each pixel's blended
+// entries (list position and the transmittance before the blend), and
+// k_deep_log turns a quadrant's 64 pixel lists into the wave blend log and
+// transmittance checkpoints k_raster_fwd would have written.
+
+// The most splats one pixel can blend: every blend multiplies T by at most
+// 1 - 1/255, and blending stops before T reaches 1e-4, so at most
+// ln(1e-4) / ln(254/255) = 2344.0 blends (fp32 rounding adds at most one).
+constexpr int kDeepMaxBlend = 2368;
+// Pixels per wave: a 2x2 block shares each step's record loads and centred
+// rows (measured faster than one pixel per wave, whose 4x as many waves
+// crowd the SIMDs that run the deepest walks).
+constexpr int kDeepPix = 4;
+constexpr int kDeepWaves = 256 / kDeepPix;  // waves per deep tile
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// deep_list[0, count) = the tiles whose list holds at least deep_len entries.
+__global__ __launch_bounds__(256) void k_deep_tiles(int T, const int *__restrict__ offsets, int deep_len,
+                                                    int *__restrict__ deep_list, int *__restrict__ count) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    const bool deep = t < T && offsets[t + 1] - offsets[t] >= deep_len;
+    const unsigned long long bal = __ballot(deep);
+    if (!bal) return;
+    const int lane = threadIdx.x & 63;
+    int base = 0;
+    if (lane == 0) base = atomicAdd(count, __popcll(bal));
+    base = __shfl(base, 0, 64);
+    if (deep) deep_list[base + __popcll(bal & ((1ull << lane) - 1ull))] = t;
+}
+
+// One wave per (deep tile k, pixel block g of kDeepPix pixels).  With
+// LOG, pixel slot k * 256 + 16 y + x (tile-local x, y) receives its blended
+// list positions and transmittances before the blend at
+// dpos / dtb[slot * kDeepMaxBlend + i] and their count in dcnt[slot].
+template <bool LOG, bool FULL_OUT>
+__global__ __launch_bounds__(kThreads) void k_raster_deep(
+    int W, int H, int tiles_x, int n_deep, const int *__restrict__ deep_list, const int *__restrict__ offsets,
+    const int *__restrict__ ids, const float4 *__restrict__ rec, const float *__restrict__ bgp,
+    float *__restrict__ out_img, float *__restrict__ final_Ts, int *__restrict__ final_idx,
+    float *__restrict__ out_depth, float *__restrict__ out_normal, float *__restrict__ out_alpha,
+    float *__restrict__ out_median, float *__restrict__ out_dist, int *__restrict__ dpos, float *__restrict__ dtb,
+    int *__restrict__ dcnt) {
+    const int lane = threadIdx.x & 63;
+    const int item = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (item >= n_deep * kDeepWaves) return;
+    const int k = item / kDeepWaves, g = item % kDeepWaves;
+    const int tile = deep_list[k];
+    const int tx = tile % tiles_x, ty = tile / tiles_x;
+    const int start = offsets[tile], end = offsets[tile + 1];
+    float px[kDeepPix], py[kDeepPix], Tr[kDeepPix], cr[kDeepPix], cg[kDeepPix], cb[kDeepPix];
+    float dep[kDeepPix], nx[kDeepPix], ny[kDeepPix], nz[kDeepPix], M1[kDeepPix], M2[kDeepPix], dist[kDeepPix],
+        med[kDeepPix];
+    int med_c[kDeepPix], last_c[kDeepPix], nb[kDeepPix], lp[kDeepPix];
+    float lt[kDeepPix];
+    unsigned done = 0;
+    // pixel q of block g (a 2x2 block for 4 pixels per wave)
+    const auto local_px = [&](int q) { return kDeepPix == 1 ? (g & 15) : 2 * (g & 7) + (q & 1); };
+    const auto local_py = [&](int q) { return kDeepPix == 1 ? (g >> 4) : 2 * (g >> 3) + (q >> 1); };
+#pragma unroll
+    for (int q = 0; q < kDeepPix; ++q) {
+        const int lx = local_px(q), ly = local_py(q);
+        const int pxi = tx * 16 + lx, pyi = ty * 16 + ly;
+        if (!(pxi < W && pyi < H)) done |= 1u << q;
+        px[q] = (float)pxi;
+        py[q] = (float)pyi;
+        Tr[q] = 1.f;
+        cr[q] = cg[q] = cb[q] = 0.f;
+        dep[q] = nx[q] = ny[q] = nz[q] = M1[q] = M2[q] = dist[q] = med[q] = 0.f;
+        med_c[q] = -1;
+        last_c[q] = 0;
+        nb[q] = 0;
+        lp[q] = 0;
+        lt[q] = 0.f;
+    }
+    const size_t slot0 = (size_t)k * 256;
+    auto slot_of = [&](int q) { return slot0 + (size_t)(16 * local_py(q) + local_px(q)); };
+    // each step's ids are loaded two steps ahead and its records one step
+    // ahead, so the loads overlap the evaluation of the current step
+    int gid_n = start + 64 + lane < end ? ids[start + 64 + lane] : 0;
+    float4 n0, n1, n2, n3, n4;
+    {
+        const float4 *r = rec + 5 * (size_t)(start + lane < end ? ids[start + lane] : 0);
+        n0 = r[0], n1 = r[1], n2 = r[2], n3 = r[3], n4 = r[4];
+    }
+    for (int j0 = start; j0 < end && done != (1u << kDeepPix) - 1u; j0 += 64) {
+        const int j = j0 + lane;
+        const bool valid = j < end;
+        const uint64_t valid_m = __builtin_amdgcn_ballot_w64(valid);
+        const float4 q0 = n0, q1 = n1, q2 = n2, q3 = n3, q4 = n4;
+        if (j0 + 64 < end) {
+            const float4 *r = rec + 5 * (size_t)gid_n;
+            n0 = r[0], n1 = r[1], n2 = r[2], n3 = r[3], n4 = r[4];
+            gid_n = j + 128 < end ? ids[j + 128] : 0;
+        }
+        const f3 Tw = {q1.z, q1.w, q2.x};
+        f3 R0, nAx, nAy;
+        centred_rows({q0.x, q0.y, q0.z}, {q0.w, q1.x, q1.y}, Tw, q2.y, q2.z, R0, nAx, nAy);
+        // eval_pair's planes, as load_batch stages them
+        const float4 p0 = make_float4(R0.x, R0.y, R0.z, nAx.x);
+        const float4 p1 = make_float4(nAx.y, nAx.z, nAy.x, nAy.y);
+        const float4 p2 = make_float4(nAy.z, q2.y, q2.z, q2.w);
+        const float4 p3 = make_float4(Tw.x, Tw.y, Tw.z, 0.f);
+#pragma unroll
+        for (int q = 0; q < kDeepPix; ++q) {
+            if ((done >> q) & 1u) continue;
+            PairEval e;
+            uint64_t act = eval_pair(px[q], py[q], p0, p1, p2, p3, e) & valid_m;
+            while (act) {
+                const int l = __builtin_ctzll(act);
+                act &= act - 1ull;
+                const float a = readlane_f(e.alpha, l);
+                const float next_T = Tr[q] * (1.0f - a);
+                if (__builtin_amdgcn_ballot_w64(next_T <= 1e-4f)) {
+                    done |= 1u << q;
+                    break;
+                }
+                const float w = a * Tr[q];
+                const int pos = j0 - start + l;
+                if (FULL_OUT) {
+                    const int contrib = pos + 1;
+                    const float A = 1.f - Tr[q];
+                    const float dep_s = readlane_f(e.depth, l);
+                    const float m_ = kMScale * (1.f - NEAR_N / dep_s);
+                    dist[q] = __builtin_fmaf(m_ * m_ * A + M2[q] - 2.f * m_ * M1[q], w, dist[q]);
+                    M1[q] = __builtin_fmaf(m_, w, M1[q]);
+                    M2[q] = __builtin_fmaf(m_ * m_, w, M2[q]);
+                    if (Tr[q] > 0.5f) {
+                        med[q] = dep_s;
+                        med_c[q] = contrib;
+                    }
+                    dep[q] = __builtin_fmaf(dep_s, w, dep[q]);
+                    nx[q] = __builtin_fmaf(readlane_f(q3.x, l), w, nx[q]);
+                    ny[q] = __builtin_fmaf(readlane_f(q3.y, l), w, ny[q]);
+                    nz[q] = __builtin_fmaf(readlane_f(q3.z, l), w, nz[q]);
+                    last_c[q] = contrib;
+                }
+                cr[q] = __builtin_fmaf(readlane_f(q3.w, l), w, cr[q]);
+                cg[q] = __builtin_fmaf(readlane_f(q4.x, l), w, cg[q]);
+                cb[q] = __builtin_fmaf(readlane_f(q4.y, l), w, cb[q]);
+                if (LOG && nb[q] < kDeepMaxBlend) {
+                    // entry nb goes to lane nb mod 64; a full chunk is one store
+                    const bool mine = lane == (nb[q] & 63);
+                    lp[q] = mine ? pos : lp[q];
+                    lt[q] = mine ? Tr[q] : lt[q];
+                    if ((++nb[q] & 63) == 0) {
+                        const size_t o = slot_of(q) * kDeepMaxBlend + (size_t)(nb[q] - 64) + lane;
+                        dpos[o] = lp[q];
+                        dtb[o] = lt[q];
+                    }
+                }
+                Tr[q] = next_T;
+            }
+        }
+    }
+    const float bg0 = bgp[0], bg1 = bgp[1], bg2 = bgp[2];
+#pragma unroll
+    for (int q = 0; q < kDeepPix; ++q) {
+        const int lx = local_px(q), ly = local_py(q);
+        const int pxi = tx * 16 + lx, pyi = ty * 16 + ly;
+        if (LOG) {
+            const size_t o = slot_of(q) * kDeepMaxBlend + (size_t)(nb[q] & ~63) + lane;
+            if (lane < (nb[q] & 63)) {
+                dpos[o] = lp[q];
+                dtb[o] = lt[q];
+            }
+            if (lane == 0) dcnt[slot_of(q)] = pxi < W && pyi < H ? nb[q] : 0;
+        }
+        if (lane != 0 || !(pxi < W && pyi < H)) continue;
+        const size_t pix = (size_t)pyi * W + pxi;
+        final_Ts[3 * pix + 0] = Tr[q];
+        out_img[3 * pix + 0] = __builtin_fmaf(bg0, Tr[q], cr[q]);
+        out_img[3 * pix + 1] = __builtin_fmaf(bg1, Tr[q], cg[q]);
+        out_img[3 * pix + 2] = __builtin_fmaf(bg2, Tr[q], cb[q]);
+        if (!FULL_OUT) continue;
+        final_idx[2 * pix + 0] = last_c[q];
+        final_Ts[3 * pix + 1] = M1[q];
+        final_Ts[3 * pix + 2] = M2[q];
+        final_idx[2 * pix + 1] = med_c[q];
+        out_depth[pix] = dep[q];
+        out_normal[3 * pix + 0] = nx[q];
+        out_normal[3 * pix + 1] = ny[q];
+        out_normal[3 * pix + 2] = nz[q];
+        out_alpha[pix] = 1.f - Tr[q];
+        out_median[pix] = med[q];
+        out_dist[pix] = dist[q];
+    }
+}
+
+// The blend log of quadrant w of a deep tile from its 64 pixels' lists: the
+// entries are the list positions some pixel of the quadrant blended, in
+// list order, each with the ballot of those pixels (bit l = pixel
+// (lane_px(w, l), lane_py(w, l)), as in k_raster_fwd), and checkpoint c
+// (every 64th entry) holds each pixel's transmittance before entry c.  One
+// 1024-thread workgroup per (deep tile, quadrant); every pass reads the
+// pixel lists in coalesced 64-entry rows (wave v takes pixels v, v + 16, ...),
+// in windows of kDeepWin list positions:
+//   1. the positions present are marked in an LDS bitmap;
+//   2. a block scan of the words' popcounts ranks them, and each present
+//      position's entry gets its list position and gaussian id;
+//   3. the ballots are assembled in LDS for kDeepBal ranks at a time;
+//   4. pixel entry i of rank r_i writes the checkpoints c in (r_{i-1}, r_i]
+//      (the transmittance changes only at the pixel's own blends), and
+//      after the pixel's last entry the final transmittance fills the rest.
+constexpr int kDeepWin = 131072, kDeepWords = kDeepWin / 32, kDeepBal = 2048;
+constexpr int kLogThreads = 1024, kLogWaves = kLogThreads / 64;
+__global__ __launch_bounds__(kLogThreads) void k_deep_log(int W, int H, int tiles_x, int n_deep,
+                                                  const int *__restrict__ deep_list, const int *__restrict__ offsets,
+                                                  const int *__restrict__ ids, const int *__restrict__ dpos,
+                                                  const float *__restrict__ dtb, const int *__restrict__ dcnt,
+                                                  const float *__restrict__ final_Ts, uint4 *__restrict__ blend_log,
+                                                  float *__restrict__ t_ckpt, int *__restrict__ wave_cnt) {
+    __shared__ uint32_t s_bits[kDeepWords];
+    __shared__ int s_woff[kDeepWords];
+    __shared__ uint32_t s_bal[2][kDeepBal];
+    __shared__ int s_cnt[64], s_i[64], s_e[64], s_last[64];
+    __shared__ float s_tf[64];
+    __shared__ int s_red[kLogWaves];
+    const int item = blockIdx.x;
+    if (item >= n_deep * 4) return;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int k = item >> 2, w = item & 3;
+    const int tile = deep_list[k];
+    const int tx = tile % tiles_x, ty = tile / tiles_x;
+    const int start = offsets[tile], len = offsets[tile + 1] - start;
+    const size_t log_base = 4 * (size_t)start + (size_t)w * (size_t)len;
+    auto slot_of = [&](int p) { return (size_t)k * 256 + 16 * lane_py(w, p) + lane_px(w, p); };
+    if (threadIdx.x < 64) {
+        const int p = threadIdx.x;
+        const int pxi = tx * 16 + lane_px(w, p), pyi = ty * 16 + lane_py(w, p);
+        const bool inside = pxi < W && pyi < H;
+        s_cnt[p] = inside ? dcnt[slot_of(p)] : 0;
+        s_tf[p] = inside ? final_Ts[3 * ((size_t)pyi * W + pxi)] : 1.0f;
+        s_i[p] = 0;
+        s_last[p] = -1;
+    }
+    __syncthreads();
+    int nlog = 0;
+    for (int P0 = 0;; P0 += kDeepWin) {
+        // any pixel entries left?
+        int left = 0;
+        if (threadIdx.x < 64) left = s_i[threadIdx.x] < s_cnt[threadIdx.x];
+        if (!__syncthreads_or(left)) break;
+        for (int q = threadIdx.x; q < kDeepWords; q += kLogThreads) s_bits[q] = 0u;
+        __syncthreads();
+        // 1. mark, and find each pixel's first entry beyond the window
+        for (int p = wv; p < 64; p += kLogWaves) {
+            const int *__restrict__ P_ = dpos + slot_of(p) * kDeepMaxBlend;
+            const int i0 = s_i[p], n = s_cnt[p];
+            int e = n;
+            for (int i = i0; i < n; i += 64) {
+                const int pos = i + lane < n ? P_[i + lane] : INT32_MAX;
+                const bool in = pos < P0 + kDeepWin;
+                if (in) {
+                    const int b = pos - P0;
+                    atomicOr(&s_bits[b >> 5], 1u << (b & 31));
+                }
+                const unsigned long long out = __ballot(!in);
+                if (out) {
+                    e = i + (int)__builtin_ctzll(out);
+                    break;
+                }
+            }
+            if (lane == 0) s_e[p] = e;
+        }
+        __syncthreads();
+        // 2. ranks: block scan of the words' popcounts (4 words per thread)
+        constexpr int WPT = kDeepWords / kLogThreads;
+        int wsum = 0;
+#pragma unroll
+        for (int q = 0; q < WPT; ++q) wsum += __popc(s_bits[threadIdx.x * WPT + q]);
+        int incl = wsum;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int o = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += o;
+        }
+        if (lane == 63) s_red[wv] = incl;
+        __syncthreads();
+        int woff = incl - wsum, n_w = 0;
+        for (int v = 0; v < kLogWaves; ++v) {
+            woff += v < wv ? s_red[v] : 0;
+            n_w += s_red[v];
+        }
+#pragma unroll
+        for (int q = 0; q < WPT; ++q) {
+            const int wd = threadIdx.x * WPT + q;
+            s_woff[wd] = woff;
+            for (uint32_t x = s_bits[wd]; x; x &= x - 1u) {
+                const int pos = P0 + 32 * wd + __builtin_ctz(x);
+                reinterpret_cast<uint2 *>(blend_log + log_base + nlog + woff)[1] =
+                    make_uint2((unsigned)pos, (unsigned)ids[start + pos]);
+                ++woff;
+            }
+        }
+        __syncthreads();
+        auto rank = [&](int pos) {
+            const int b = pos - P0;
+            return s_woff[b >> 5] + __popc(s_bits[b >> 5] & ((1u << (b & 31)) - 1u));
+        };
+        // 3. ballots, kDeepBal ranks at a time
+        for (int R0 = 0; R0 < n_w; R0 += kDeepBal) {
+            for (int r = threadIdx.x; r < kDeepBal; r += kLogThreads) {
+                s_bal[0][r] = 0u;
+                s_bal[1][r] = 0u;
+            }
+            __syncthreads();
+            for (int p = wv; p < 64; p += kLogWaves) {
+                const int *__restrict__ P_ = dpos + slot_of(p) * kDeepMaxBlend;
+                const int e = s_e[p];
+                for (int i = s_i[p] + lane; i < e; i += 64) {
+                    const int r = rank(P_[i]) - R0;
+                    if (r >= 0 && r < kDeepBal) atomicOr(&s_bal[p >> 5][r], 1u << (p & 31));
+                }
+            }
+            __syncthreads();
+            for (int r = threadIdx.x; r < min(kDeepBal, n_w - R0); r += kLogThreads)
+                reinterpret_cast<uint2 *>(blend_log + log_base + nlog + R0 + r)[0] = make_uint2(s_bal[0][r], s_bal[1][r]);
+            __syncthreads();
+        }
+        // 4. checkpoints up to each pixel entry
+        for (int p = wv; p < 64; p += kLogWaves) {
+            const int *__restrict__ P_ = dpos + slot_of(p) * kDeepMaxBlend;
+            const float *__restrict__ Tb = dtb + slot_of(p) * kDeepMaxBlend;
+            const int e = s_e[p];
+            int carry = s_last[p];
+            for (int i0 = s_i[p]; i0 < e; i0 += 64) {
+                const int i = i0 + lane;
+                const int r = i < e ? nlog + rank(P_[i]) : INT32_MAX;
+                int rp = __shfl_up(r, 1, 64);
+                if (lane == 0) rp = carry;
+                if (i < e) {
+                    const float tb = Tb[i];
+                    for (int c = max(64, (rp + 64) & ~63); c <= r; c += 64)
+                        t_ckpt[log_base + c + p] = tb;
+                }
+                carry = __shfl(r, min(63, e - 1 - i0), 64);
+            }
+            if (lane == 0) {
+                s_last[p] = carry;
+                s_i[p] = e;
+            }
+        }
+        nlog += n_w;
+        __syncthreads();
+    }
+    // the final transmittance for the checkpoints after each pixel's last entry
+    for (int p = wv; p < 64; p += kLogWaves) {
+        const float tf = s_tf[p];
+        for (int c = max(64, (s_last[p] + 64) & ~63) + 64 * lane; c <= nlog; c += 64 * 64)
+            t_ckpt[log_base + c + p] = tf;
+    }
+    if (threadIdx.x == 0) wave_cnt[4 * tile + w] = nlog;
+}
+
 }  // namespace
 
 namespace mskern {
@@ -590,15 +966,36 @@ void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
                        const float *rec, const float *mrec, const float *bg, float *out_img, float *final_Ts, int *final_idx,
                        float *out_depth, float *out_normal, float *out_alpha, float *out_median, float *out_dist,
                        unsigned long long *pair_counter, uint32_t *blend_log, float *t_ckpt, int *wave_cnt,
-                       bool full_outputs) {
+                       bool full_outputs, const DeepTiles &deep) {
     const int T = tiles_x * tiles_y;
     const int grid = xcd_strip_grid(tiles_x, tiles_y);
     auto *lg = reinterpret_cast<uint4 *>(blend_log);
+    const int deep_len = deep.n > 0 ? deep.len : INT32_MAX;
+    if (deep.n > 0) {
+        // the deep tiles on their own stream, beside the per-tile kernel
+        // (their walks are the longest; the outputs are disjoint)
+        (void)hipEventRecord(deep.fork, s);
+        (void)hipStreamWaitEvent(deep.stream, deep.fork, 0);
+        hipStream_t sd = deep.stream;
+        auto launch_deep = [&](auto kern) {
+            hipLaunchKernelGGL(kern, dim3(deep.n * kDeepWaves / 4), dim3(kThreads), 0, sd, W, H, tiles_x, deep.n, deep.list,
+                               offsets, ids, reinterpret_cast<const float4 *>(rec), bg, out_img, final_Ts, final_idx,
+                               out_depth, out_normal, out_alpha, out_median, out_dist, deep.pos, deep.tb, deep.cnt);
+        };
+        if (blend_log)
+            full_outputs ? launch_deep(k_raster_deep<true, true>) : launch_deep(k_raster_deep<true, false>);
+        else
+            full_outputs ? launch_deep(k_raster_deep<false, true>) : launch_deep(k_raster_deep<false, false>);
+        if (blend_log)
+            hipLaunchKernelGGL(k_deep_log, dim3(deep.n * 4), dim3(kLogThreads), 0, sd, W, H, tiles_x, deep.n, deep.list,
+                               offsets, ids, deep.pos, deep.tb, deep.cnt, final_Ts, lg, t_ckpt, wave_cnt);
+        (void)hipEventRecord(deep.join, sd);
+    }
     auto launch = [&](auto kern) {
         hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
                            reinterpret_cast<const float4 *>(rec), reinterpret_cast<const float4 *>(mrec), bg,
                            out_img, final_Ts, final_idx, out_depth,
-                           out_normal, out_alpha, out_median, out_dist, pair_counter, lg, t_ckpt, wave_cnt);
+                           out_normal, out_alpha, out_median, out_dist, pair_counter, lg, t_ckpt, wave_cnt, deep_len);
     };
     // the work counters are a separate instantiation (profiling only)
     if (pair_counter) {
@@ -612,7 +1009,14 @@ void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
         else
             full_outputs ? launch(k_raster_fwd<false, true, false>) : launch(k_raster_fwd<false, false, false>);
     }
+    if (deep.n > 0) (void)hipStreamWaitEvent(s, deep.join, 0);
 }
+
+void launch_deep_tiles(hipStream_t s, int T, const int *offsets, int deep_len, int *deep_list, int *count) {
+    hipLaunchKernelGGL(k_deep_tiles, dim3((T + 255) / 256), dim3(256), 0, s, T, offsets, deep_len, deep_list, count);
+}
+
+int64_t deep_pixel_entries(int n_deep) { return (int64_t)n_deep * 256 * kDeepMaxBlend; }
 
 bool launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets,
                        const uint32_t *blend_log, const float *t_ckpt, const int *wave_cnt, const float *rec,

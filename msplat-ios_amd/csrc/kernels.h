@@ -81,11 +81,29 @@ constexpr int kSuperSortChunk = 4096;
 // checkpoints the backward replays; pass nullptr for render-only frames.
 // full_outputs = false produces only out_img, final_Ts[.][0] and
 // final_idx[.][0] (what the image-only training step consumes).
+// Deep tiles (lists of at least len entries) are rendered pixel by pixel
+// (k_raster_deep) instead of by one workgroup; list[0, n) are their tile
+// indices (launch_deep_tiles), and with a blend log pos / tb / cnt hold
+// their pixels' blended entries (deep_pixel_entries(n) ints / floats, and
+// n * 256 counts), from which their wave logs are built.
+struct DeepTiles {
+    int n = 0, len = 0;
+    const int *list = nullptr;
+    int *pos = nullptr;
+    float *tb = nullptr;
+    int *cnt = nullptr;
+    // the deep tiles run on `stream` between `fork` (recorded on the
+    // caller's stream) and `join` (waited on by the caller's stream)
+    hipStream_t stream = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+void launch_deep_tiles(hipStream_t s, int T, const int *offsets, int deep_len, int *deep_list, int *count);
+int64_t deep_pixel_entries(int n_deep);
 void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
                        const float *rec, const float *mrec, const float *bg, float *out_img, float *final_Ts, int *final_idx,
                        float *out_depth, float *out_normal, float *out_alpha, float *out_median, float *out_dist,
                        unsigned long long *pair_counter, uint32_t *blend_log, float *t_ckpt, int *wave_cnt,
-                       bool full_outputs);
+                       bool full_outputs, const DeepTiles &deep);
 // Returns true when the image-only kernel ran: grads16 then holds its sums
 // (launch_finish_image_grads / launch_project_bwd finish them).
 bool launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets,
