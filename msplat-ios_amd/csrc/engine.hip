@@ -287,24 +287,34 @@ int validate_cam(const MsplatCamera *cam, const MsplatGaussians *g) {
 // distortion outputs.  The forward is deterministic, so running it again on
 // the same tile lists (to add the log or the full outputs on demand)
 // reproduces every value it wrote before.
+// The current frame's deep tiles (none in the 3DGS mode), with the stream
+// and events their kernels run between.
+int deep_tiles(mskern::DeepTiles &deep) {
+    Engine &E = g_eng;
+    deep = mskern::DeepTiles{};
+    if (E.n_deep <= 0 || E.gs3d) return MSPLAT_OK;
+    if (!E.deep_stream) {
+        HIPC(hipStreamCreateWithFlags(&E.deep_stream, hipStreamNonBlocking));
+        HIPC(hipEventCreateWithFlags(&E.deep_fork, hipEventDisableTiming));
+        HIPC(hipEventCreateWithFlags(&E.deep_join, hipEventDisableTiming));
+    }
+    deep.n = E.n_deep;
+    deep.len = E.deep_len;
+    deep.list = P<int>(E.deep_list);
+    deep.stream = E.deep_stream;
+    deep.fork = E.deep_fork;
+    deep.join = E.deep_join;
+    return MSPLAT_OK;
+}
+
 int raster_fwd_locked(bool log, bool full) {
     Engine &E = g_eng;
     uint32_t *lg = nullptr;
     float *tc = nullptr;
     int *wc = nullptr;
     mskern::DeepTiles deep;
-    if (E.n_deep > 0 && !E.gs3d) {
-        deep.n = E.n_deep;
-        deep.len = E.deep_len;
-        deep.list = P<int>(E.deep_list);
-        if (!E.deep_stream) {
-            HIPC(hipStreamCreateWithFlags(&E.deep_stream, hipStreamNonBlocking));
-            HIPC(hipEventCreateWithFlags(&E.deep_fork, hipEventDisableTiming));
-            HIPC(hipEventCreateWithFlags(&E.deep_join, hipEventDisableTiming));
-        }
-        deep.stream = E.deep_stream;
-        deep.fork = E.deep_fork;
-        deep.join = E.deep_join;
+    CHECK(deep_tiles(deep));
+    if (deep.n > 0) {
         if (log) {
             const size_t ent = (size_t)mskern::deep_pixel_entries(E.n_deep);
             CHECK(ensure(E.deep_pos, ent * 4));
@@ -952,10 +962,12 @@ int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g, con
     HIPC(hipMemsetAsync(E.grads16.p, 0, (size_t)N * 64, s));
     const float inv_np = 1.0f / (float)((unsigned)H * (unsigned)W * 3u);
     const float ddist_uniform = lambda_dist * (inv_np * 3.0f);
+    mskern::DeepTiles deep;
+    CHECK(deep_tiles(deep));
     const bool t_moments = mskern::launch_raster_bwd(s, W, H, cam->tiles_x, cam->tiles_y, P<int>(E.offsets), P<uint32_t>(E.blend_log),
                               P<float>(E.t_ckpt), P<int>(E.wave_cnt), P<float>(E.rec), bg, P<float>(E.final_Ts),
                               P<int>(E.final_idx), P<float>(E.dL_dimg), nullptr, nullptr, nullptr, nullptr, nullptr,
-                              ddist_uniform, P<float>(E.grads16));
+                              ddist_uniform, P<float>(E.grads16), deep);
     stage_mark(ST_PROJECT_BWD);
     if (adam) {
         mskern::launch_project_bwd(s, *cam, *g, P<int>(E.radii), P<float>(E.grads16), nullptr, nullptr, nullptr,
@@ -1298,10 +1310,12 @@ int msplat_hip_raster_bwd(const float *dL_dimg, const float *dL_ddepth, const fl
     // outputs; replay the deterministic raster forward with what is missing
     const bool need_full = dL_ddepth || dL_dalpha || dL_dnormal || dL_dmedian || dL_ddist;
     if (!E.log_valid || (need_full && !E.full_valid)) CHECK(raster_fwd_locked(true, need_full || E.full_valid));
+    mskern::DeepTiles deep;
+    CHECK(deep_tiles(deep));
     const bool t_moments = mskern::launch_raster_bwd(
         E.stream, E.W, E.H, E.tiles_x, E.tiles_y, P<int>(E.offsets), P<uint32_t>(E.blend_log), P<float>(E.t_ckpt),
         P<int>(E.wave_cnt), P<float>(E.rec), E.bg, P<float>(E.final_Ts), P<int>(E.final_idx), dL_dimg, dL_ddepth,
-        dL_dalpha, dL_dnormal, dL_dmedian, dL_ddist, 0.0f, grads16);
+        dL_dalpha, dL_dnormal, dL_dmedian, dL_ddist, 0.0f, grads16, deep);
     if (t_moments) mskern::launch_finish_image_grads(E.stream, E.n, P<float>(E.rec), grads16);
     HIPC(hipGetLastError());
     return MSPLAT_OK;

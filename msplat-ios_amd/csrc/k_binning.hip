@@ -595,18 +595,6 @@ __global__ __launch_bounds__(256) void k_merge_path(int L, const int *__restrict
     }
 }
 
-__global__ __launch_bounds__(256) void k_copy_big(const int *__restrict__ offsets, const int *__restrict__ big_list,
-                                                  const int *__restrict__ stats,
-                                                  const unsigned long long *__restrict__ src,
-                                                  unsigned long long *__restrict__ dst) {
-    const int nbig = stats[2];
-    for (int b = blockIdx.y; b < nbig; b += gridDim.y) {
-        const int t = big_list[b];
-        const int start = offsets[t], cnt = offsets[t + 1] - start;
-        for (int i = blockIdx.x * 256 + threadIdx.x; i < cnt; i += gridDim.x * 256) dst[start + i] = src[start + i];
-    }
-}
-
 constexpr int kWin = 2048;  // super-list entries staged in LDS per window
 
 // Filters the sorted super-list entries skeys[0, cnt) of the super-tile at
@@ -666,6 +654,7 @@ template <bool PACKED>
 __global__ __launch_bounds__(256) void k_emit_tiles(int tiles_x, int tiles_y, int sxn,
                                                     const int *__restrict__ soffsets,
                                                     const unsigned long long *__restrict__ skeys,
+                                                    const unsigned long long *__restrict__ merged,
                                                     const uint2 *__restrict__ rect,
                                                     const int *__restrict__ toffsets, int *__restrict__ ids,
                                                     int huge_th) {
@@ -675,6 +664,9 @@ __global__ __launch_bounds__(256) void k_emit_tiles(int tiles_x, int tiles_y, in
     const int stx = (st % sxn) * kSuper, sty = (st / sxn) * kSuper;
     const int start = soffsets[st], cnt = soffsets[st + 1] - start;
     if (cnt > huge_th) return;
+    // lists above kChunk went through the merge passes, which leave them in
+    // `merged`; the shorter ones were sorted in place
+    const unsigned long long *__restrict__ keys = cnt > kChunk ? merged : skeys;
     const int ty = sty + (int)(threadIdx.x >> 6);
     int out[kSuper];
 #pragma unroll
@@ -682,7 +674,7 @@ __global__ __launch_bounds__(256) void k_emit_tiles(int tiles_x, int tiles_y, in
         const int tx = stx + lx;
         out[lx] = (tx < tiles_x && ty < tiles_y) ? toffsets[ty * tiles_x + tx] : -1;
     }
-    emit_range<PACKED>(skeys + start, cnt, stx, sty, rect, out, s_gid, s_rr, ids);
+    emit_range<PACKED>(keys + start, cnt, stx, sty, rect, out, s_gid, s_rr, ids);
 }
 
 // Emits every kChunk chunk of the huge lists: a chunk's entries start in
@@ -797,20 +789,18 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
                            dst);
         std::swap(src, dst);
     }
-    // the merged lists of long super-tiles end in src; copy them back so
-    // every list is in super_keys for the emission
-    if (src != k)
-        hipLaunchKernelGGL(k_copy_big, dim3(64, 64), dim3(256), 0, s, super_offsets, big_list, super_stats, src, k);
+    // the lists longer than kChunk end in src (every merge pass covers all
+    // of them); the emission reads them there
     if (big)
         hipLaunchKernelGGL(packed ? k_count_chunks<true> : k_count_chunks<false>, big_grid, dim3(kSortThreads), 0, s,
-                           tiles_x, tiles_y, sxn, super_offsets, huge_list, huge_stats, chunk_base, k, r2,
+                           tiles_x, tiles_y, sxn, super_offsets, huge_list, huge_stats, chunk_base, src, r2,
                            chunk_counts, tile_counts);
     launch_scan_counts(s, T, tile_counts, tile_offsets, nullptr, tile_stats, tile_temp);
     hipLaunchKernelGGL(packed ? k_emit_tiles<true> : k_emit_tiles<false>, dim3(NS), dim3(256), 0, s, tiles_x, tiles_y,
-                       sxn, super_offsets, k, r2, tile_offsets, ids, huge_th);
+                       sxn, super_offsets, k, src, r2, tile_offsets, ids, huge_th);
     if (big)
         hipLaunchKernelGGL(packed ? k_emit_chunks<true> : k_emit_chunks<false>, big_grid, dim3(256), 0, s, tiles_x,
-                           tiles_y, sxn, super_offsets, huge_list, huge_stats, chunk_base, chunk_counts, k, r2,
+                           tiles_y, sxn, super_offsets, huge_list, huge_stats, chunk_base, chunk_counts, src, r2,
                            tile_offsets, ids);
 }
 

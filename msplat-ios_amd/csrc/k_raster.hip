@@ -297,9 +297,12 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     const float *__restrict__ bgp, const float *__restrict__ final_Ts, const int *__restrict__ final_idx,
     const float *__restrict__ dL_dimg, const float *__restrict__ dL_ddepth, const float *__restrict__ dL_daccum,
     const float *__restrict__ dL_dnormal, const float *__restrict__ dL_dmedian, const float *__restrict__ dL_ddist,
-    float ddist_uniform, float *__restrict__ grads16) {
-    const int tile = xcd_strip_tile(blockIdx.x, tiles_x, T / tiles_x);
+    float ddist_uniform, float *__restrict__ grads16, const int *__restrict__ tile_list, int deep_len) {
+    // tile_list: the deep tiles (their own launch); otherwise every other
+    // tile, XCD-mapped
+    const int tile = tile_list ? tile_list[blockIdx.x] : xcd_strip_tile(blockIdx.x, tiles_x, T / tiles_x);
     if (tile < 0) return;
+    if (!tile_list && offsets[tile + 1] - offsets[tile] >= deep_len) return;
     constexpr int kWave = 64;
     // per wave: the staged entries' record planes (the image-only path
     // stages 4, the full one 7) and the log entries (full) or the reduction
@@ -1022,19 +1025,36 @@ bool launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
                        const uint32_t *blend_log, const float *t_ckpt, const int *wave_cnt, const float *rec,
                        const float *bg, const float *final_Ts, const int *final_idx, const float *dL_dimg,
                        const float *dL_ddepth, const float *dL_daccum, const float *dL_dnormal,
-                       const float *dL_dmedian, const float *dL_ddist, float ddist_uniform, float *grads16) {
+                       const float *dL_dmedian, const float *dL_ddist, float ddist_uniform, float *grads16,
+                       const DeepTiles &deep) {
     const int T = tiles_x * tiles_y;
     const int grid = xcd_strip_grid(tiles_x, tiles_y);
     const auto *lg = reinterpret_cast<const uint4 *>(blend_log);
     const bool full = dL_ddepth || dL_daccum || dL_dnormal || dL_dmedian || dL_ddist || ddist_uniform != 0.0f;
-    if (full)
-        hipLaunchKernelGGL(k_raster_bwd<true>, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, lg,
-                           t_ckpt, wave_cnt, reinterpret_cast<const float4 *>(rec), bg, final_Ts, final_idx, dL_dimg,
-                           dL_ddepth, dL_daccum, dL_dnormal, dL_dmedian, dL_ddist, ddist_uniform, grads16);
-    else
-        hipLaunchKernelGGL(k_raster_bwd<false>, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, lg,
-                           t_ckpt, wave_cnt, reinterpret_cast<const float4 *>(rec), bg, final_Ts, final_idx, dL_dimg,
-                           dL_ddepth, dL_daccum, dL_dnormal, dL_dmedian, dL_ddist, ddist_uniform, grads16);
+    auto launch = [&](hipStream_t st, int blocks, const int *list, int deep_len) {
+        if (full)
+            hipLaunchKernelGGL(k_raster_bwd<true>, dim3(blocks), dim3(kThreads), 0, st, W, H, tiles_x, T, offsets, lg,
+                               t_ckpt, wave_cnt, reinterpret_cast<const float4 *>(rec), bg, final_Ts, final_idx,
+                               dL_dimg, dL_ddepth, dL_daccum, dL_dnormal, dL_dmedian, dL_ddist, ddist_uniform,
+                               grads16, list, deep_len);
+        else
+            hipLaunchKernelGGL(k_raster_bwd<false>, dim3(blocks), dim3(kThreads), 0, st, W, H, tiles_x, T, offsets,
+                               lg, t_ckpt, wave_cnt, reinterpret_cast<const float4 *>(rec), bg, final_Ts, final_idx,
+                               dL_dimg, dL_ddepth, dL_daccum, dL_dnormal, dL_dmedian, dL_ddist, ddist_uniform,
+                               grads16, list, deep_len);
+    };
+    if (deep.n > 0) {
+        // the deep tiles' long log replays start at once, on their own
+        // stream, beside the rest
+        (void)hipEventRecord(deep.fork, s);
+        (void)hipStreamWaitEvent(deep.stream, deep.fork, 0);
+        launch(deep.stream, deep.n, deep.list, 0);
+        (void)hipEventRecord(deep.join, deep.stream);
+        launch(s, grid, nullptr, deep.len);
+        (void)hipStreamWaitEvent(s, deep.join, 0);
+    } else {
+        launch(s, grid, nullptr, INT32_MAX);
+    }
     return !full;
 }
 

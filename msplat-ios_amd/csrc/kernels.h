@@ -110,7 +110,8 @@ bool launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
                        const uint32_t *blend_log, const float *t_ckpt, const int *wave_cnt, const float *rec,
                        const float *bg, const float *final_Ts, const int *final_idx, const float *dL_dimg,
                        const float *dL_ddepth, const float *dL_daccum, const float *dL_dnormal,
-                       const float *dL_dmedian, const float *dL_ddist, float ddist_uniform, float *grads16);
+                       const float *dL_dmedian, const float *dL_ddist, float ddist_uniform, float *grads16,
+                       const DeepTiles &deep);
 constexpr int kBlendLogEntryBytes = 16;
 
 // k_raster3d.hip (3DGS mode): rec = the 3DGS records (kRec3Floats each),
