@@ -199,9 +199,10 @@ int msplat_hip_loss_fwd_bwd(int width, int height, const float *img_dev,
                             double *loss_host, double *ssim_sum_host);
 
 /* msplat_hip_loss_fwd_bwd without any allocation.  No counterpart in the
- * reference: it is for callers that cannot allocate device memory (code
- * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc).  The scratch it needs lives in a fixed device array of the
+ * reference: it is for callers that cannot allocate device memory (tight
+ * serving loops, harnesses that forbid hipMalloc).  It is not capturable
+ * in a HIP graph: it reads the loss back into pinned host memory and
+ * synchronises the engine stream.  The scratch it needs lives in a fixed device array of the
  * library (about 77 MB per GPU, held until the process ends): images up to
  * 2^21 pixels (e.g. 2048x1024, 1920x1080); larger ones return
  * MSPLAT_E_CAPACITY.  msplat_hip_init must have run (this call does no
@@ -407,8 +408,9 @@ typedef struct {
  * num_views views at once: every voxel folds the views in array order,
  * which is what num_views successive single-view calls (the reference's
  * loop, model.cpp:723-757) compute, reading and writing the grid once.
- * views is host memory; the depth / alpha maps must stay valid until the
- * work completes (asynchronous; msplat_hip_sync waits). */
+ * views is host memory.  Synchronous: the call returns when the grid is
+ * updated (the next call rewrites the engine's copies of the view records
+ * and pass masks), so the depth / alpha maps may be released after it. */
 int msplat_hip_tsdf_integrate(float *grid_dev, int dx, int dy, int dz, const float origin[3],
                               float voxel_size, const MsplatTsdfView *views, int num_views,
                               float trunc_dist, float alpha_thresh);

@@ -122,6 +122,21 @@ void autoScaleAndCenter(InputData &data) {
         for (int k = 0; k < 3; ++k) data.points.xyz[3 * i + k] = (data.points.xyz[3 * i + k] - mean[k]) * data.scale;
 }
 
+void faceCenteredTransform(InputData &data, float faceDistance, float scaleFactor) {
+    if (data.cameras.empty()) return;
+    // the point faceDistance in front of the first camera (its -Z axis in
+    // the OpenGL convention): M0 (0, 0, -d, 1)
+    const float *M0 = data.cameras.front().camToWorld;
+    float face[3];
+    for (int k = 0; k < 3; ++k) face[k] = M0[4 * k + 2] * (-faceDistance) + M0[4 * k + 3];
+    for (int k = 0; k < 3; ++k) data.translation[k] = face[k];
+    data.scale = scaleFactor;
+    for (auto &c : data.cameras)
+        for (int k = 0; k < 3; ++k) c.camToWorld[4 * k + 3] = (c.camToWorld[4 * k + 3] - face[k]) * scaleFactor;
+    for (int64_t i = 0; i < data.points.count; ++i)
+        for (int k = 0; k < 3; ++k) data.points.xyz[3 * i + k] = (data.points.xyz[3 * i + k] - face[k]) * scaleFactor;
+}
+
 void initializeRandomPoints(InputData &data, int64_t numPoints, float extent) {
     std::mt19937 rng(42);
     std::uniform_real_distribution<float> dxyz(-extent, extent);

@@ -77,6 +77,14 @@ InputData inputDataFromX(const std::string &path, const std::string &colmapImage
 // largest coordinate is 1 (input_data.cpp:124-175).
 void autoScaleAndCenter(InputData &data);
 
+// The face-capture normalisation (input_data.cpp:82-110): the origin moves
+// to the point faceDistance in front of the first camera and every camera
+// position and point is scaled by scaleFactor about it.  The Nerfstudio
+// loader applies it instead of autoScaleAndCenter when the environment sets
+// MSPLAT_FACE_DISTANCE > 0 (MSPLAT_SCALE_FACTOR, default 10;
+// load_nerfstudio.cpp:135-146).
+void faceCenteredTransform(InputData &data, float faceDistance, float scaleFactor);
+
 // Fallback initialisation without a point cloud: uniform points in
 // [-extent, extent]^3 with random colours (input_data.cpp:351-369).
 void initializeRandomPoints(InputData &data, int64_t numPoints = 100000, float extent = 1.3f);

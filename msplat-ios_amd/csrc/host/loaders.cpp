@@ -260,7 +260,16 @@ InputData load_nerfstudio(const std::string &root) {
                 break;
             }
         }
-    autoScaleAndCenter(data);
+    const char *face = std::getenv("MSPLAT_FACE_DISTANCE");
+    if (face && std::atof(face) > 0.0) {
+        const char *sf = std::getenv("MSPLAT_SCALE_FACTOR");
+        const float scale = sf ? (float)std::atof(sf) : 10.0f;
+        std::cerr << "msplat: face-centred transform (face distance " << std::atof(face) << ", scale " << scale
+                  << ")\n";
+        faceCenteredTransform(data, (float)std::atof(face), scale);
+    } else {
+        autoScaleAndCenter(data);
+    }
     return data;
 }
 

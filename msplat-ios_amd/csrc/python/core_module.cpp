@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "input_data.hpp"
+#include "model.hpp"
 #include "msplat_api.hpp"
 
 namespace py = pybind11;
@@ -346,6 +347,26 @@ PYBIND11_MODULE(_core, m) {
             return a;
         },
         "path"_a, "Decode an image file the way datasets do (PNG / PPM / PGM / JPEG) to (H, W, 3) float32 in [0, 1].");
+    m.def(
+        "_metrics",
+        [](py::array_t<float, py::array::c_style | py::array::forcecast> rendered,
+           py::array_t<float, py::array::c_style | py::array::forcecast> gt) {
+            if (rendered.ndim() != 3 || gt.ndim() != 3) throw std::invalid_argument("images are (H, W, C)");
+            auto host = [](const py::array_t<float, py::array::c_style | py::array::forcecast> &a) {
+                MTensor t({(int64_t)a.shape(0), (int64_t)a.shape(1), (int64_t)a.shape(2)}, DType::Float32);
+                std::memcpy(t.data<float>(), a.data(), (size_t)a.size() * sizeof(float));
+                return t;
+            };
+            const MTensor r = host(rendered), g = host(gt);
+            py::dict d;
+            d["psnr"] = psnr(r, g);
+            d["ssim"] = ssim_eval(r, g);
+            d["l1"] = l1_loss(r, g);
+            return d;
+        },
+        "rendered"_a, "gt"_a,
+        "The evaluation metrics Trainer.evaluate reports (PSNR, SSIM with an 11-tap sigma-1.5 window and "
+        "clamp-to-edge padding, L1) of two (H, W, C) float32 images on the host.");
     m.def("sync", &msplat::sync, "Synchronize GPU (wait for all commands to complete)");
     m.def("cleanup", &msplat::cleanup, "Release all cached GPU resources");
 }

@@ -632,3 +632,103 @@ def test_jpeg_decoder_under_address_sanitizer(tmp_path):
     assert len(lines) == len(files)
     assert all(ln.startswith("ok") for ln in lines[:len(fixtures)])
     assert all(ln.startswith("error") for ln in lines[len(fixtures):len(fixtures) + len(crafted)])
+
+
+# ------------------------------------------------- evaluation metrics --
+def _ssim_brute(a, b, pad="clamp"):
+    """Mean SSIM over pixels and channels of (H, W, C) images with the 2D
+    11x11 Gaussian window (sigma 1.5) applied directly (no separable pass),
+    in float64: each window tap reads the pixel at the clamped coordinate
+    (pad="clamp") or zero outside the image (pad="zero")."""
+    H, W, C = a.shape
+    x = np.arange(11) - 5
+    g = np.exp(-(x * x) / (2 * 1.5 * 1.5))
+    g /= g.sum()
+    w2 = np.outer(g, g)
+    c1, c2 = 0.01 ** 2, 0.03 ** 2
+    tot = 0.0
+    for c in range(C):
+        def blur(img):
+            out = np.zeros((H, W))
+            for y in range(H):
+                for xx in range(W):
+                    s = 0.0
+                    for j in range(11):
+                        for k in range(11):
+                            yy, xk = y + j - 5, xx + k - 5
+                            if pad == "clamp":
+                                s += w2[j, k] * img[min(max(yy, 0), H - 1), min(max(xk, 0), W - 1)]
+                            elif 0 <= yy < H and 0 <= xk < W:
+                                s += w2[j, k] * img[yy, xk]
+                    out[y, xx] = s
+            return out
+        p, q = a[..., c].astype(np.float64), b[..., c].astype(np.float64)
+        m1, m2 = blur(p), blur(q)
+        s11, s22, s12 = blur(p * p) - m1 * m1, blur(q * q) - m2 * m2, blur(p * q) - m1 * m2
+        tot += (((2 * m1 * m2 + c1) * (2 * s12 + c2)) / ((m1 * m1 + m2 * m2 + c1) * (s11 + s22 + c2))).sum()
+    return tot / (H * W * C)
+
+
+def test_eval_metrics_known_answers():
+    """PSNR / SSIM / L1 of Trainer.evaluate (csrc/host/eval.cpp after
+    core/src/model.cpp:26-43 and core/src/ssim.cpp:37-123): identical images
+    give SSIM 1 and L1 0; a constant offset d gives L1 = d and PSNR =
+    -20 log10 d; SSIM equals a float64 brute-force 2D 11x11 window with
+    clamp-to-edge padding on small images (smaller than the window, so most
+    taps are clamped), and differs from the zero-padded one there, so a
+    padding, window or normaliser slip fails."""
+    from msplat import _core
+    rng = np.random.default_rng(5)
+    a = rng.uniform(0.1, 0.9, (9, 13, 3)).astype(np.float32)
+    m = _core._metrics(a, a)
+    assert abs(m["ssim"] - 1.0) < 1e-6 and m["l1"] == 0.0 and m["psnr"] > 200
+    for d in (0.05, 0.0625, 0.1):
+        b = a + np.float32(d)
+        m = _core._metrics(b, a)
+        dd = float(np.float32(b - a).mean())  # the offset after float32 rounding
+        assert abs(m["l1"] - dd) < 1e-6
+        mse = float(((b.astype(np.float64) - a) ** 2).mean())
+        assert abs(m["psnr"] - 10 * np.log10(1 / mse)) < 1e-4
+        assert abs(m["psnr"] + 20 * np.log10(d)) < 2e-3
+    for shape in ((9, 13, 3), (16, 7, 3), (5, 5, 1)):
+        p = rng.uniform(0, 1, shape).astype(np.float32)
+        q = np.clip(p + rng.normal(0, 0.1, shape), 0, 1).astype(np.float32)
+        got = _core._metrics(p, q)["ssim"]
+        want = _ssim_brute(p, q)
+        assert abs(got - want) < 2e-5, (shape, got, want)
+        assert abs(_ssim_brute(p, q, pad="zero") - want) > 1e-3  # the padding matters here
+    with pytest.raises(Exception):
+        _core._metrics(a, a[:8])
+
+
+@pytest.mark.parametrize("scale_env", [None, "5"])
+def test_nerfstudio_face_centred_transform(tmp_path, monkeypatch, scale_env):
+    """MSPLAT_FACE_DISTANCE = d > 0 replaces the auto centring with the
+    face-capture normalisation (load_nerfstudio.cpp:135-146,
+    input_data.cpp:82-110): the origin moves to the point d in front of the
+    first camera, M0 (0, 0, -d, 1), and positions (cameras and points) are
+    scaled by MSPLAT_SCALE_FACTOR (10 when unset) about it; rotations are
+    kept."""
+    import msplat
+
+    monkeypatch.setenv("MSPLAT_FACE_DISTANCE", "0.4")
+    if scale_env is None:
+        monkeypatch.delenv("MSPLAT_SCALE_FACTOR", raising=False)
+    else:
+        monkeypatch.setenv("MSPLAT_SCALE_FACTOR", scale_env)
+    scale = 10.0 if scale_env is None else float(scale_env)
+    poses = [_look_at_c2w((3 * np.cos(a), 1.0, 3 * np.sin(a))) for a in np.linspace(0, 2, 4)]
+    _write_images(tmp_path / "images", 4)
+    frames = [dict(file_path=f"images/frame_{i:03d}", transform_matrix=p.tolist()) for i, p in enumerate(poses)]
+    (tmp_path / "transforms.json").write_text(json.dumps(dict(w=16, h=12, fl_x=20.0, fl_y=21.0, cx=8.0, cy=6.0,
+                                                              frames=frames[::-1])))
+    ds = msplat.Dataset(str(tmp_path))
+    M0 = np.asarray(poses[0], np.float64)
+    face = M0[:3, 2] * -0.4 + M0[:3, 3]
+    for k in range(4):
+        got = ds.camera_pose(k)
+        want = np.asarray(poses[k], np.float64).copy()
+        want[:3, 3] = (want[:3, 3] - face) * scale
+        assert np.abs(got - want).max() < 1e-4 * scale, (k, got, want)
+    # the first camera now sits d * scale from the origin, looking at it
+    assert abs(np.linalg.norm(ds.camera_pose(0)[:3, 3]) - 0.4 * scale) < 1e-4 * scale
