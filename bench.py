@@ -40,11 +40,13 @@ sys.path.insert(0, str(REPO / "msplat-ios_amd"))
 
 METRIC = "train steps/s @3M splats 5187x3361; render FPS; % HBM peak per kernel"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
-# Issue cost of a simple VALU instruction (v_fma_f32 class) per wave64 and
-# SIMD, measured on gfx950 with 8 waves per SIMD and independent chains;
-# 1024 SIMDs (256 CUs x 4) give the issue peak.
-VALU_NS_PER_INST = 1.3
-VALU_PEAK_GIPS = 1024 / VALU_NS_PER_INST
+# The vector ALUs' ceiling: MI355X's published FP32 vector peak, 157.3
+# TFLOP/s = 256 CUs x 4 SIMDs x 32 FMA lanes x 2 flops x 2.4 GHz, is 32
+# lanes per cycle per SIMD, so no wave64 VALU instruction issues in fewer
+# than 2 cycles: at most 1024 SIMDs x 2.4 GHz / 2 = 1228.8 G wave-instructions
+# per second.  (A plain v_fma_f32 measured 1.3 ns per SIMD with 8 waves, 0.64
+# of this ceiling.)
+VALU_PEAK_GIPS = 1024 * 2.4 / 2.0
 LR = (0.00016, 0.005, 0.001, 0.0025, 0.000125, 0.05)
 BOUND = {"project_fwd": "hbm", "tile_scan": "latency", "scatter_sort": "hbm", "raster_fwd": "valu",
          "ssim_l1": "valu", "raster_bwd": "valu", "project_bwd_adam": "hbm"}
@@ -167,7 +169,7 @@ def gpu_train(workload: int, steps: int, warmup: int, render_frames: int, counte
     stage_ms = _stage_breakdown(E, lambda ci: D.train_step(ds, cams[ci], gts[ci]), warmup + steps,
                                 min(steps, 10), len(cams))
     out = dict(scene=scene, ds=ds, cams=cams, ms_per_step=ms_per_step, losses=losses,
-               isect=float(np.mean(isect)), stage_ms=stage_ms)
+               isect=float(np.mean(isect)), stage_ms=stage_ms, blend_log_mb=blend_log_mb(E))
     if counters:
         # two untimed steps with the raster work counters on
         E.enable_timing(False, pairs=True)
@@ -181,6 +183,13 @@ def gpu_train(workload: int, steps: int, warmup: int, render_frames: int, counte
     del gts
     out["render_ms"] = gpu_render_ms(ds, cams, render_frames)
     return out
+
+
+def blend_log_mb(E) -> float:
+    """Device memory the blend-log pool holds after the timed steps: its
+    chunks of 64 16-byte entries and 64 checkpoint floats, in MiB."""
+    _, n = E.last_ptr("blend_log")  # 4 u32 per entry
+    return round(n * 4 * 1.25 / 2**20, 1)
 
 
 def gpu_shard(scene, ds, bands: int, steps: int, warmup: int) -> dict:
@@ -274,34 +283,69 @@ def gpu_render_ms(ds, cams, frames: int) -> float:
     return (time.perf_counter() - t0) * 1e3 / max(frames, 1)
 
 
-def gpu_render_to_buffer_ms(scene, frames: int) -> float:
-    """Render frames through the reference's public path: a Trainer (C ABI)
-    holding the scene (loaded from a .msplat checkpoint) renders poses with
-    msplat_trainer_render_pose_to_buffer into a host RGBA8 buffer, i.e.
-    render + RGBA8 conversion + the copy to host memory."""
+class _StdoutToStderr:
+    """Sends what the C++ library prints on stdout (e.g. Model::load's
+    message) to stderr for the duration, so this script's stdout stays its
+    one JSON line."""
+
+    def __enter__(self):
+        sys.stdout.flush()
+        self.saved = os.dup(1)
+        os.dup2(2, 1)
+
+    def __exit__(self, *exc):
+        sys.stdout.flush()
+        os.dup2(self.saved, 1)
+        os.close(self.saved)
+
+
+def gpu_c_abi(scene, frames: int, steps: int, warmup: int, ncams: int = 4) -> dict:
+    """The reference's public path through the C ABI: a Trainer on a
+    dataset of `ncams` of the scene's cameras with host target images
+    (renders of the jittered scene), holding the scene's splats (loaded
+    from a .msplat checkpoint written at step 30000: SH degree 3 active,
+    full resolution, past densification).  Times `steps` msplat_trainer_step
+    calls (Trainer::step, msplat_api.mm:106-128: camera choice, prepareCam,
+    the fused step, the loss readback, schedulers, afterTrain) after
+    `warmup` untimed ones plus one per camera (each camera's target image
+    is uploaded to HBM on its first step and cached, as the reference
+    caches its Metal buffers), and `frames`
+    msplat_trainer_render_pose_to_buffer calls (render + RGBA8 conversion +
+    the copy to host memory)."""
+    from msplat import _engine as E
     from msplat import capi
+    from msplat import device as D
     from msplat import formats
 
     import shutil
 
     L = capi.lib()
-    c0 = scene.cameras[0]
+    cams = scene.cameras[:ncams]
     need = scene.n * 58 * 4 * 3 + (1 << 28)  # parameters and both moments
     dirs = [d for d in ("/dev/shm", tempfile.gettempdir(), str(REPO / "_build")) if os.path.isdir(d)]
     dirs = [d for d in dirs if shutil.disk_usage(d).free > need]
     if not dirs:
         raise RuntimeError(f"no directory with {need >> 20} MiB free for the checkpoint")
+    tgt = D.DeviceScene(scene.jittered(0.01, 0xC0FFEE + 103))
+    imgs = []
+    for c in cams:
+        g = D.render_to_device(tgt, tgt.camera(c))
+        imgs.append(np.ascontiguousarray(g.numpy().reshape(c.height, c.width, 3), np.float32))
+        del g
+    del tgt
+    gc.collect()
     with tempfile.TemporaryDirectory(dir=dirs[0]) as td:
         ckpt = os.path.join(td, "scene.msplat")
         params = dict(zip(formats.GROUPS, scene.params()))
         formats.write_checkpoint(ckpt, params, scene.sh_degree, step=30000)
-        img = np.zeros((c0.height, c0.width, 3), np.float32)
-        cam = capi.CameraImage(width=c0.width, height=c0.height, fx=c0.fx, fy=c0.fy, cx=c0.cx, cy=c0.cy)
-        cam.camToWorld[:] = [float(v) for v in c0.cam_to_world.reshape(-1)]
-        cam.rgb = img.ctypes.data
+        recs = (capi.CameraImage * len(cams))()
+        for r, c, img in zip(recs, cams, imgs):
+            r.width, r.height, r.fx, r.fy, r.cx, r.cy = c.width, c.height, c.fx, c.fy, c.cx, c.cy
+            r.camToWorld[:] = [float(v) for v in c.cam_to_world.reshape(-1)]
+            r.rgb = img.ctypes.data
         pts = np.ascontiguousarray(scene.means[:1000], np.float32)
         rgb = np.full((len(pts), 3), 128, np.uint8)
-        dset = L.msplat_dataset_create_from_memory(C.byref(cam), 1, pts.ctypes.data, rgb.ctypes.data, len(pts),
+        dset = L.msplat_dataset_create_from_memory(recs, len(cams), pts.ctypes.data, rgb.ctypes.data, len(pts),
                                                    False, 8)
         if not dset:
             raise RuntimeError(capi.last_error())
@@ -311,9 +355,21 @@ def gpu_render_to_buffer_ms(scene, frames: int) -> float:
         if not tr:
             raise RuntimeError(capi.last_error())
         try:
-            if L.msplat_trainer_load_checkpoint(tr, ckpt.encode()) < 0:
-                raise RuntimeError(capi.last_error())
+            with _StdoutToStderr():
+                if L.msplat_trainer_load_checkpoint(tr, ckpt.encode()) < 0:
+                    raise RuntimeError(capi.last_error())
             assert L.msplat_trainer_splat_count(tr) == scene.n
+            for _ in range(warmup + len(cams)):
+                L.msplat_trainer_step(tr)
+            E.sync()
+            losses = []
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                st = L.msplat_trainer_step(tr)
+                losses.append(st.loss)
+            step_ms = (time.perf_counter() - t0) * 1e3 / max(steps, 1)
+            assert L.msplat_trainer_splat_count(tr) == scene.n  # no densification on the way
+            c0 = cams[0]
             buf = np.zeros((c0.height, c0.width, 4), np.uint8)
             w, h = C.c_int(), C.c_int()
             poses = [np.ascontiguousarray(c.cam_to_world, np.float32).reshape(-1) for c in scene.cameras]
@@ -330,7 +386,7 @@ def gpu_render_to_buffer_ms(scene, frames: int) -> float:
         finally:
             L.msplat_trainer_destroy(tr)
             L.msplat_dataset_destroy(dset)
-    return ms
+    return dict(render_ms=ms, step_ms=step_ms, losses=losses, cameras=len(cams))
 
 
 def gpu_densify(total_steps: int = 1500, refine_every: int = 100, max_splats: int = 2_000_000,
@@ -588,25 +644,26 @@ def cpu_cell(O, per_s: list[float], unit: str, sample: str) -> dict:
 
 # ----------------------------------------------------------------- main --
 def headline_roofline(kernels: dict, workload: str) -> dict:
-    """The dominant kernel against the bound that limits it: VALU issue for
-    the rasterizers (executed VALU instructions per launch from the
-    committed rocprofv3 counters over the HIP-event duration, against
-    1024 SIMDs / 1.3 ns), with its HBM fraction by the algorithmic bytes
-    beside it."""
+    """The dominant kernel against HBM: algorithmic bytes per launch over its
+    HIP-event duration, against 8 TB/s, with the calibrated FETCH + WRITE
+    bytes per launch (traffic) from the committed rocprofv3 summaries.  Its
+    VALU issue rate sits beside it (`valu`): executed VALU instructions per
+    launch (rocprofv3 SQ_INSTS_VALU, profiles/) over the same duration,
+    against the VALU ceiling VALU_PEAK_GIPS."""
     dominant = max(kernels, key=lambda k: kernels[k]["ms"])
     dk = kernels[dominant]
     traffic = profile_record("traffic", dominant, workload)
     cnt = profile_record("counters", dominant, workload)
-    hbm = {"achieved": dk["GB_per_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dk["frac_hbm_peak"]}
-    if BOUND.get(dominant) == "valu" and cnt is not None:
+    out = {"kernel": dominant, "bound": "hbm", "achieved": dk["GB_per_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": dk["frac_hbm_peak"], "traffic": traffic["bytes"] if traffic else None,
+           "algorithmic_bytes": round(dk["algorithmic_GB"] * 1e9)}
+    if cnt is not None:
         gips = cnt["valu_insts"] / (dk["ms"] * 1e-3) / 1e9
-        return {"kernel": dominant, "bound": "valu", "achieved": round(gips, 1), "peak": round(VALU_PEAK_GIPS, 1),
-                "unit": "G VALU instructions/s", "frac": round(gips / VALU_PEAK_GIPS, 4),
-                "traffic": traffic["bytes"] if traffic else None, "hbm": hbm,
-                "basis": f"{cnt['kernel']}: {cnt['valu_insts']:.4g} VALU instructions per launch (rocprofv3 "
-                         f"SQ_INSTS_VALU, profiles/), {VALU_NS_PER_INST} ns per instruction per SIMD x 1024 SIMDs"}
-    return {"kernel": dominant, "bound": "hbm", "achieved": dk["GB_per_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": dk["frac_hbm_peak"], "traffic": traffic["bytes"] if traffic else None}
+        out["valu"] = {"achieved": round(gips, 1), "peak": round(VALU_PEAK_GIPS, 1),
+                       "unit": "G VALU wave-instructions/s", "frac": round(gips / VALU_PEAK_GIPS, 4),
+                       "basis": f"{cnt['kernel']}: {cnt['valu_insts']:.4g} VALU instructions per launch "
+                                f"(rocprofv3 SQ_INSTS_VALU, profiles/); ceiling 1024 SIMDs x 2.4 GHz / 2 cycles"}
+    return out
 
 
 def kernel_table(stage_ms: dict, N: int, I: int, P: int, T: int, workload: str) -> dict:
@@ -618,7 +675,7 @@ def kernel_table(stage_ms: dict, N: int, I: int, P: int, T: int, workload: str) 
                "GB_per_s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
         cnt = profile_record("counters", name, workload)
         if cnt is not None and ms > 0:
-            row["frac_valu_issue"] = round(cnt["valu_insts"] * VALU_NS_PER_INST * 1e-9 / (ms * 1e-3 * 1024), 4)
+            row["frac_valu_peak"] = round(cnt["valu_insts"] / (ms * 1e-3) / 1e9 / VALU_PEAK_GIPS, 4)
         kernels[name] = row
     return kernels
 
@@ -633,7 +690,7 @@ def issue_table(stage_ms: dict, workload: str) -> dict:
         cnt = profile_record("counters", name, workload)
         if cnt is not None and ms > 0:
             row["kernel"] = cnt["kernel"]
-            row["frac_valu_issue"] = round(cnt["valu_insts"] * VALU_NS_PER_INST * 1e-9 / (ms * 1e-3 * 1024), 4)
+            row["frac_valu_peak"] = round(cnt["valu_insts"] / (ms * 1e-3) / 1e9 / VALU_PEAK_GIPS, 4)
         tr = profile_record("traffic", name, workload)
         if tr is not None and ms > 0:
             row["hbm_GB_per_s_measured"] = round(tr["bytes"] / (ms * 1e-3) / 1e9, 1)
@@ -696,6 +753,7 @@ def main() -> int:
         r = gpu_train(args.profile_workload, args.steps, args.warmup, args.render_frames, counters=False)
         print(json.dumps({"workload": r["scene"].name, "ms_per_step": round(r["ms_per_step"], 3),
                           "render_ms": round(r["render_ms"], 3), "intersections_mean": int(r["isect"]),
+                          "blend_log_mb": r["blend_log_mb"],
                           "stage_ms": {k: round(v, 4) for k, v in r["stage_ms"].items()}}))
         return 0
     # ---- headline: C3 ----
@@ -715,9 +773,11 @@ def main() -> int:
             f"all bands {shard['sum_ms_per_step']:.3f} ms")
     del h["ds"]
     gc.collect()
-    buf_ms = None if args.no_buffer_render else gpu_render_to_buffer_ms(scene, max(args.render_frames // 2, 5))
-    if buf_ms:
-        log(f"{scene.name}: render_pose_to_buffer {buf_ms:.3f} ms")
+    capi_run = None if args.no_buffer_render else gpu_c_abi(scene, max(args.render_frames // 2, 5),
+                                                            max(args.steps // 2, 5), 2)
+    buf_ms = capi_run["render_ms"] if capi_run else None
+    if capi_run:
+        log(f"{scene.name}: render_pose_to_buffer {buf_ms:.3f} ms, msplat_trainer_step {capi_run['step_ms']:.3f} ms")
     result = {
         "metric": METRIC,
         "value": round(1000.0 / h["ms_per_step"], 4),
@@ -734,10 +794,16 @@ def main() -> int:
         "config": {"workload": scene.name, "splats": N, "width": W, "height": H, "sh_degree": scene.sh_degree,
                    "tiles": T, "intersections_mean": int(I), "cameras": len(h["cams"]),
                    "device": E.device_name()},
+        "blend_log_mb": h["blend_log_mb"],
         "render_fps": round(1000.0 / h["render_ms"], 2),
         "render_ms": round(h["render_ms"], 3),
         "render_fps_to_buffer": round(1000.0 / buf_ms, 2) if buf_ms else None,
         "render_ms_to_buffer": round(buf_ms, 3) if buf_ms else None,
+        "trainer_step": ({"train_steps_per_s": round(1000.0 / capi_run["step_ms"], 3),
+                          "ms_per_step": round(capi_run["step_ms"], 3),
+                          "cameras": capi_run["cameras"],
+                          "path": "msplat_trainer_step (C ABI), checkpoint of the same splats, host target images"}
+                         if capi_run else None),
         "kernels": kernels,
         "roofline": headline_roofline(kernels, scene.name),
         "loss_first_last": [round(h["losses"][0], 6), round(h["losses"][-1], 6)],

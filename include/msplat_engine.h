@@ -288,9 +288,10 @@ enum {
     MSPLAT_LAST_DL_DMEAN2D,       /* [N,2]                               */
     MSPLAT_LAST_DL_DFEATURES_DC,  /* [N,3]                               */
     MSPLAT_LAST_DL_DFEATURES_REST,/* [N,K,3]                             */
-    MSPLAT_LAST_BLEND_LOG,        /* [4I,4] u32 wave blend logs          */
-    MSPLAT_LAST_BLEND_CKPT,       /* [4I+64] f32 their checkpoints       */
+    MSPLAT_LAST_BLEND_LOG,        /* [C,64,4] u32 blend-log pool chunks  */
+    MSPLAT_LAST_BLEND_CKPT,       /* [C,64] f32 their checkpoints        */
     MSPLAT_LAST_WAVE_COUNTS,      /* [T,4]  i32 entries per wave log     */
+    MSPLAT_LAST_BLEND_CHUNKS,     /* i32 per-wave chunk tables           */
     MSPLAT_LAST_COUNT
 };
 /* Returns the device pointer and element count of a cached buffer (NULL /
@@ -298,13 +299,15 @@ enum {
  * packed records on each call (asynchronously, on the engine stream).  The
  * raster gradients (GRADS16, DL_DTRANSMAT, DL_DNORMAL3D, DL_DOPACITY,
  * DL_DCOLORS) are those of the most recent train step and exist until the
- * next forward.  BLEND_LOG / BLEND_CKPT / WAVE_COUNTS are the rasterizer's
- * per-wave blend logs (wave w of tile t: entries [0, WAVE_COUNTS[4t + w]) at
- * 4 * offset(t) + w * len(t), each {ballot low, ballot high, list position,
- * gaussian id}; checkpoint c of that wave, every 64th entry, at the same slot
- * index + lane), written by the training forward or a backward's replay;
- * they exist once such a forward ran on the current tile lists (a test
- * accessor, no counterpart in the reference). */
+ * next forward.  BLEND_LOG / BLEND_CKPT / WAVE_COUNTS / BLEND_CHUNKS are
+ * the rasterizer's per-wave blend logs in a pool of C chunks of 64 entries
+ * {ballot low, ballot high, list position, gaussian id}: wave w of tile t
+ * (list offset s, length n) has WAVE_COUNTS[4t + w] entries, its entries
+ * 64k .. 64k + 63 in chunk BLEND_CHUNKS[(4 s + w n) / 64 + 4t + w + k],
+ * whose 64 checkpoint floats are each lane's transmittance before entry
+ * 64 (k + 1).  They exist once the training forward or a backward's replay
+ * ran on the current tile lists (a test accessor, no counterpart in the
+ * reference). */
 int msplat_hip_last(int which, void **ptr_dev, int64_t *numel);
 
 /* Per-kernel timings of the most recent train step / render, in ms, from
@@ -349,6 +352,14 @@ int msplat_hip_set_wide_keys(int on);
  * down that path, so the tests can check it on small scenes; len <= 0
  * restores the default.  No counterpart in the reference. */
 int msplat_hip_set_deep_tile_len(int len);
+/* Blend-log pool self-test hook.  A frame's pool holds `chunks` chunks of
+ * 64 entries instead of the size estimated from its intersection count, or
+ * more once an overflow grew it: a step whose log overflows the pool
+ * changes nothing and is redone after the pool doubles (up to a size no log
+ * overflows), so a tiny pool exercises that path with the same results.
+ * Drops the grown size; chunks <= 0 restores the estimate.  No counterpart
+ * in the reference. */
+int msplat_hip_set_log_pool_chunks(int chunks);
 
 /* ---- 3DGS mode ------------------------------------------------------------
  * 3D Gaussians (scales [N,3], log) projected with the reference's EWA

@@ -36,6 +36,17 @@ DEVICE = [
 ]
 
 
+# Per-file device flags.  The rasterizers claim blend-log chunks with a
+# one-lane atomic whose result is used only once the chunk is full; the
+# atomic optimizer rewrites such an atomic into a wave reduction whose
+# result is broadcast at once, which waits for the atomic right where it is
+# issued.
+FILE_FLAGS = {
+    "k_raster.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+    "k_raster3d.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+}
+
+
 def sources() -> list[Path]:
     srcs = sorted(CSRC.glob("*.hip"))
     srcs += sorted((CSRC / "host").glob("*.cpp"))
@@ -45,7 +56,7 @@ def sources() -> list[Path]:
 def _compile(src: Path) -> tuple[Path, str]:
     obj = BUILD_DIR / (src.stem + (".hip.o" if src.suffix == ".hip" else ".cpp.o"))
     if src.suffix == ".hip":
-        cmd = [HIPCC, *DEVICE, *COMMON, "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, *DEVICE, *FILE_FLAGS.get(src.name, []), *COMMON, "-c", str(src), "-o", str(obj)]
     else:
         cmd = [HIPCC, *COMMON, "-fopenmp", "-x", "c++", "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)

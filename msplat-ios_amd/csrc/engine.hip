@@ -114,6 +114,13 @@ struct Engine {
     // pixel (mskern::DeepTiles); n_deep of them in the current frame
     int deep_len = kDefaultDeepLen, n_deep = 0;
     DevBuf deep_list, deep_pos, deep_tb, deep_cnt;
+    // blend-log pool (msr::BlendLog): blend_log / t_ckpt hold log_used chunks
+    // of 64 entries / checkpoints, log_table the per-wave chunk tables,
+    // log_ctr the sub-pool and spill counters; the overflow flag is stats[15]
+    DevBuf log_table, log_ctr;
+    int64_t log_cap = 0;   // the size overflows grew the pool to
+    int64_t log_used = 0;  // chunks of the current frame's pool
+    int64_t log_init = 0;  // estimate override in chunks (0: from the frame)
     hipStream_t deep_stream = nullptr;  // default priority, non-blocking
     hipEvent_t deep_fork = nullptr, deep_join = nullptr;
     hipEvent_t ev[ST_COUNT + 1] = {};
@@ -307,11 +314,74 @@ int deep_tiles(mskern::DeepTiles &deep) {
     return MSPLAT_OK;
 }
 
+// The most chunks the frame's logs can take: every wave's ceil(len / 64).
+int64_t log_worst_chunks(const Engine &E) { return 4 * (int64_t)E.num_isect / 64 + 4 * (int64_t)E.tiles_x * E.tiles_y; }
+int log_subpools(int64_t tiles) { return (int)std::min<int64_t>(256, std::max<int64_t>(1, tiles / 64)); }
+// The largest pool: a spill region of the worst case (no log can overflow
+// it, whatever the sub-pools' shares) beside sub-pools of three quarters
+// of it.
+int64_t log_max_chunks(const Engine &E) {
+    const int64_t worst = log_worst_chunks(E);
+    return worst + 3 * worst / 4 + log_subpools((int64_t)E.tiles_x * E.tiles_y);
+}
+
+// The frame's blend-log pool of `cap` chunks: a sub-pool per 64 tiles (at
+// most 256; wave w of tile t claims from sub-pool (4t + w) mod count) takes
+// three quarters, the spill region the rest, and the largest pool a spill
+// region of the worst case.  cap is the larger of the frame's estimate (one
+// chunk per 96 intersections plus a partial chunk per wave, about a sixth
+// of the worst case; the training step at 3M splats fills ~70% of it) and
+// the size earlier overflows grew the pool to (log_cap), at most the
+// largest pool; a step whose log overflows is redone after the pool grows
+// (grow_log_pool).
+int blend_log_desc(msr::BlendLog &L) {
+    Engine &E = g_eng;
+    const int64_t T = (int64_t)E.tiles_x * E.tiles_y;
+    const int64_t worst = log_worst_chunks(E), most = log_max_chunks(E);
+    if (most > INT32_MAX / 2) {
+        set_err("blend log: too many intersections for the pool's chunk indices");
+        return MSPLAT_E_ARG;
+    }
+    const int64_t estimate = E.log_init ? E.log_init : std::max<int64_t>(1024, (int64_t)E.num_isect / 96 + 4 * T);
+    const int64_t cap = std::min(std::max(E.log_cap, estimate), most);
+    E.log_used = cap;
+    CHECK(ensure(E.blend_log, (size_t)cap * 64 * mskern::kBlendLogEntryBytes));
+    CHECK(ensure(E.t_ckpt, (size_t)cap * 64 * 4));
+    CHECK(ensure(E.log_table, msr::log_table_ints(E.num_isect, (int)T) * 4));
+    CHECK(ensure(E.wave_cnt, (size_t)4 * T * 4));
+    const int nsub = log_subpools(T);
+    const int64_t spill = cap == most ? worst : cap / 4;
+    CHECK(ensure(E.log_ctr, (size_t)(nsub + 1) * 4));
+    L.ent = P<uint4>(E.blend_log);
+    L.ckpt = P<float>(E.t_ckpt);
+    L.table = P<int>(E.log_table);
+    L.wave_cnt = P<int>(E.wave_cnt);
+    L.counters = P<int>(E.log_ctr);
+    L.overflow = P<int>(E.stats) + 15;
+    L.nsub = nsub;
+    L.sub_cap = (int)((cap - spill) / nsub);
+    L.spill_cap = (int)spill;
+    return MSPLAT_OK;
+}
+
+// Zeroes the pool's counters and overflow flag before a forward that logs.
+int reset_log_pool(const msr::BlendLog &L) {
+    HIPC(hipMemsetAsync(L.counters, 0, (size_t)(L.nsub + 1) * 4, g_eng.stream));
+    HIPC(hipMemsetAsync(L.overflow, 0, sizeof(int), g_eng.stream));
+    return MSPLAT_OK;
+}
+
+// After an overflowed log: a pool twice as large as the one that
+// overflowed, at most the largest (in which no log overflows).
+void grow_log_pool() {
+    Engine &E = g_eng;
+    E.log_cap = std::min(log_max_chunks(E), std::max<int64_t>(2 * E.log_used, 64));
+    E.log_valid = false;
+}
+
 int raster_fwd_locked(bool log, bool full) {
     Engine &E = g_eng;
-    uint32_t *lg = nullptr;
-    float *tc = nullptr;
-    int *wc = nullptr;
+    msr::BlendLog blog{};
     mskern::DeepTiles deep;
     CHECK(deep_tiles(deep));
     if (deep.n > 0) {
@@ -326,14 +396,8 @@ int raster_fwd_locked(bool log, bool full) {
         }
     }
     if (log) {
-        CHECK(ensure(E.blend_log, (size_t)4 * (size_t)E.num_isect * mskern::kBlendLogEntryBytes));
-        // a checkpoint is 64 floats from its log slot on, so the last wave's
-        // may reach 63 floats past 4 * I
-        CHECK(ensure(E.t_ckpt, ((size_t)4 * (size_t)E.num_isect + 64) * 4));
-        CHECK(ensure(E.wave_cnt, (size_t)4 * E.tiles_x * E.tiles_y * 4));
-        lg = P<uint32_t>(E.blend_log);
-        tc = P<float>(E.t_ckpt);
-        wc = P<int>(E.wave_cnt);
+        CHECK(blend_log_desc(blog));
+        CHECK(reset_log_pool(blog));
     }
     if (E.gs3d) {
         if (full) {
@@ -342,7 +406,7 @@ int raster_fwd_locked(bool log, bool full) {
         }
         mskern::launch_raster3d_fwd(E.stream, E.W, E.H, E.tiles_x, E.tiles_y, P<int>(E.offsets), P<int>(E.ids),
                                     P<float>(E.rec), P<float>(E.rec) + (size_t)E.n * mskern::kRec3Floats, E.bg,
-                                    P<float>(E.out_img), P<float>(E.final_Ts), lg, tc, wc);
+                                    P<float>(E.out_img), P<float>(E.final_Ts), log ? &blog : nullptr);
         E.log_valid = E.log_valid || log;
         return MSPLAT_OK;
     }
@@ -351,11 +415,24 @@ int raster_fwd_locked(bool log, bool full) {
                               P<int>(E.final_idx),
                               P<float>(E.out_depth), P<float>(E.out_normal), P<float>(E.out_alpha),
                               P<float>(E.out_median), P<float>(E.out_dist),
-                              E.count_pairs ? P<unsigned long long>(E.pair_counter) : nullptr, lg, tc, wc, full,
-                              deep);
+                              E.count_pairs ? P<unsigned long long>(E.pair_counter) : nullptr, log ? &blog : nullptr,
+                              full, deep);
     E.log_valid = E.log_valid || log;
     E.full_valid = E.full_valid || full;
     return MSPLAT_OK;
+}
+
+// A forward replay with the blend log outside the training step: waits for
+// it and replays again with a larger pool until the log fits.
+int log_forward_checked(bool full) {
+    Engine &E = g_eng;
+    for (;;) {
+        CHECK(raster_fwd_locked(true, full));
+        HIPC(hipMemcpyAsync(E.pinned_i + 15, P<int>(E.stats) + 15, sizeof(int), hipMemcpyDeviceToHost, E.stream));
+        HIPC(hipStreamSynchronize(E.stream));
+        if (E.pinned_i[15] == 0) return MSPLAT_OK;
+        grow_log_pool();
+    }
 }
 
 int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, int64_t *nisect, bool log,
@@ -584,10 +661,16 @@ int last_locked(int which, void **ptr, int64_t *numel) {
             if (E.have_grads) { *ptr = E.dfrest.p; *numel = N * E.K3; }
             return MSPLAT_OK;
         case MSPLAT_LAST_BLEND_LOG:
-            if (E.log_valid) { *ptr = E.blend_log.p; *numel = 16 * (int64_t)E.num_isect; }
+            if (E.log_valid) { *ptr = E.blend_log.p; *numel = 64 * 4 * E.log_used; }
             return MSPLAT_OK;
         case MSPLAT_LAST_BLEND_CKPT:
-            if (E.log_valid) { *ptr = E.t_ckpt.p; *numel = 4 * (int64_t)E.num_isect + 64; }
+            if (E.log_valid) { *ptr = E.t_ckpt.p; *numel = 64 * E.log_used; }
+            return MSPLAT_OK;
+        case MSPLAT_LAST_BLEND_CHUNKS:
+            if (E.log_valid) {
+                *ptr = E.log_table.p;
+                *numel = (int64_t)msr::log_table_ints(E.num_isect, E.tiles_x * E.tiles_y);
+            }
             return MSPLAT_OK;
         case MSPLAT_LAST_WAVE_COUNTS:
             if (E.log_valid) { *ptr = E.wave_cnt.p; *numel = 4 * (int64_t)E.tiles_x * E.tiles_y; }
@@ -630,7 +713,7 @@ void msplat_hip_cleanup(void) {
                      &E.stats, &E.big_list, &E.huge_list, &E.chunk_base, &E.chunk_counts, &E.keys, &E.keys_tmp, &E.ids, &E.blend_log, &E.t_ckpt, &E.wave_cnt, &E.selfcheck, &E.out_img, &E.final_Ts,
                      &E.final_idx, &E.out_depth, &E.out_normal, &E.out_alpha, &E.out_median, &E.out_dist,
                      &E.dL_dimg, &E.gm1, &E.gs1, &E.gs12, &E.partials, &E.loss, &E.dmeans, &E.dscales,
-                     &E.dquats, &E.dmean2d, &E.dfdc, &E.dfrest, &E.dens_flags, &E.dens_scan, &E.dens_keep, &E.dens_ws, &E.deep_list, &E.deep_pos, &E.deep_tb, &E.deep_cnt, &E.pair_counter,
+                     &E.dquats, &E.dmean2d, &E.dfdc, &E.dfrest, &E.dens_flags, &E.dens_scan, &E.dens_keep, &E.dens_ws, &E.deep_list, &E.deep_pos, &E.deep_tb, &E.deep_cnt, &E.log_table, &E.log_ctr, &E.pair_counter,
                      &E.rgba, &E.tsdf_views, &E.tsdf_masks, &E.mc_cases, &E.chunk_cnt, &E.chunk_off};
     for (DevBuf *b : all) {
         if (b->p) (void)hipFree(b->p);
@@ -642,6 +725,8 @@ void msplat_hip_cleanup(void) {
     }
     E.dens_rows = 0;
     E.n_deep = 0;
+    E.log_cap = 0;
+    E.log_used = 0;
     E.n = 0;
     E.num_isect = 0;
     E.have_grads = false;
@@ -937,12 +1022,10 @@ int msplat_hip_render(const MsplatCamera *cam, const MsplatGaussians *g, const f
     API_END
 }
 
-int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, const float *gt,
+static int train_step_once(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, const float *gt,
                           float lambda_l1, float lambda_dist, float lambda_dssim, float *gnorm, float *vis,
                           float *max2d, float inv_max_dim, const MsplatAdam *adam, float *loss_host,
-                          int64_t *nisect) {
-    API_BEGIN
-    ENSURE_INIT();
+                          int64_t *nisect, bool *log_overflow) {
     if (!gt || !gnorm || !vis || !max2d) {
         set_err("null gt / densify statistics");
         return MSPLAT_E_ARG;
@@ -964,15 +1047,17 @@ int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g, con
     const float ddist_uniform = lambda_dist * (inv_np * 3.0f);
     mskern::DeepTiles deep;
     CHECK(deep_tiles(deep));
-    const bool t_moments = mskern::launch_raster_bwd(s, W, H, cam->tiles_x, cam->tiles_y, P<int>(E.offsets), P<uint32_t>(E.blend_log),
-                              P<float>(E.t_ckpt), P<int>(E.wave_cnt), P<float>(E.rec), bg, P<float>(E.final_Ts),
+    msr::BlendLog blog{};
+    CHECK(blend_log_desc(blog));
+    const bool t_moments = mskern::launch_raster_bwd(s, W, H, cam->tiles_x, cam->tiles_y, P<int>(E.offsets), blog,
+                              P<float>(E.rec), bg, P<float>(E.final_Ts),
                               P<int>(E.final_idx), P<float>(E.dL_dimg), nullptr, nullptr, nullptr, nullptr, nullptr,
                               ddist_uniform, P<float>(E.grads16), deep);
     stage_mark(ST_PROJECT_BWD);
     if (adam) {
         mskern::launch_project_bwd(s, *cam, *g, P<int>(E.radii), P<float>(E.grads16), nullptr, nullptr, nullptr,
                                    nullptr, nullptr, nullptr, gnorm, vis, max2d, inv_max_dim, adam,
-                                   t_moments ? P<float>(E.rec) : nullptr);
+                                   t_moments ? P<float>(E.rec) : nullptr, blog.overflow, 0);
     } else {
         CHECK(ensure(E.dmeans, (size_t)N * 12));
         CHECK(ensure(E.dscales, (size_t)N * 8));
@@ -983,14 +1068,20 @@ int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g, con
         mskern::launch_project_bwd(s, *cam, *g, P<int>(E.radii), P<float>(E.grads16), P<float>(E.dmeans),
                                    P<float>(E.dscales), P<float>(E.dquats), P<float>(E.dmean2d), P<float>(E.dfdc),
                                    P<float>(E.dfrest), gnorm, vis, max2d, inv_max_dim, nullptr,
-                                   t_moments ? P<float>(E.rec) : nullptr);
+                                   t_moments ? P<float>(E.rec) : nullptr, blog.overflow, 0);
         E.have_grads = true;
     }
     E.raster_grads = true;
     E.g16_moments = t_moments;
     stage_mark(ST_COUNT);
+    HIPC(hipMemcpyAsync(E.pinned_i + 15, blog.overflow, sizeof(int), hipMemcpyDeviceToHost, s));
     HIPC(hipGetLastError());
     HIPC(hipStreamSynchronize(s));
+    *log_overflow = E.pinned_i[15] != 0;
+    if (*log_overflow) {
+        E.have_grads = E.raster_grads = false;
+        return MSPLAT_OK;
+    }
     if (loss_host) *loss_host = (float)E.pinned_d[0];
     if (E.count_pairs) {
         HIPC(hipMemcpyAsync(E.pairs, E.pair_counter.p, 40, hipMemcpyDeviceToHost, s));
@@ -1003,6 +1094,22 @@ int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g, con
         }
     }
     return MSPLAT_OK;
+}
+
+int msplat_hip_train_step(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, const float *gt,
+                          float lambda_l1, float lambda_dist, float lambda_dssim, float *gnorm, float *vis,
+                          float *max2d, float inv_max_dim, const MsplatAdam *adam, float *loss_host,
+                          int64_t *nisect) {
+    API_BEGIN
+    ENSURE_INIT();
+    // a step whose blend log overflowed the pool changed nothing (its
+    // backward and Adam skip): redo it with a larger pool
+    for (;;) {
+        bool overflow = false;
+        CHECK(train_step_once(cam, g, bg, gt, lambda_l1, lambda_dist, lambda_dssim, gnorm, vis, max2d, inv_max_dim, adam, loss_host, nisect, &overflow));
+        if (!overflow) return MSPLAT_OK;
+        grow_log_pool();
+    }
     API_END
 }
 
@@ -1024,11 +1131,10 @@ int msplat_hip_render_3dgs(const MsplatCamera *cam, const MsplatGaussians *g, co
     API_END
 }
 
-int msplat_hip_train_step_3dgs(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, const float *gt,
+static int train_step3d_once(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, const float *gt,
                                float lambda_l1, float lambda_dssim, float *gnorm, float *vis, float *max2d,
-                               float inv_max_dim, const MsplatAdam *adam, float *loss_host, int64_t *nisect) {
-    API_BEGIN
-    ENSURE_INIT();
+                               float inv_max_dim, const MsplatAdam *adam, float *loss_host, int64_t *nisect,
+                               bool *log_overflow) {
     if (!gt || !gnorm || !vis || !max2d) {
         set_err("null gt / densify statistics");
         return MSPLAT_E_ARG;
@@ -1045,14 +1151,15 @@ int msplat_hip_train_step_3dgs(const MsplatCamera *cam, const MsplatGaussians *g
     stage_mark(ST_RASTER_BWD);
     CHECK(ensure(E.grads16, (size_t)N * 64));
     HIPC(hipMemsetAsync(E.grads16.p, 0, (size_t)N * 64, s));
-    mskern::launch_raster3d_bwd(s, W, H, cam->tiles_x, cam->tiles_y, P<int>(E.offsets), P<uint32_t>(E.blend_log),
-                                P<float>(E.t_ckpt), P<int>(E.wave_cnt), P<float>(E.rec), bg, P<float>(E.final_Ts),
-                                P<float>(E.dL_dimg), P<float>(E.grads16));
+    msr::BlendLog blog{};
+    CHECK(blend_log_desc(blog));
+    mskern::launch_raster3d_bwd(s, W, H, cam->tiles_x, cam->tiles_y, P<int>(E.offsets), blog, P<float>(E.rec), bg,
+                                P<float>(E.final_Ts), P<float>(E.dL_dimg), P<float>(E.grads16));
     stage_mark(ST_PROJECT_BWD);
     if (adam) {
         mskern::launch_project3d_bwd(s, *cam, *g, P<int>(E.radii), P<float>(E.grads16), nullptr, nullptr, nullptr,
                                      nullptr, nullptr, nullptr, gnorm, vis, max2d, inv_max_dim, adam,
-                                     P<float>(E.rec));
+                                     P<float>(E.rec), blog.overflow, 0);
     } else {
         CHECK(ensure(E.dmeans, (size_t)N * 12));
         CHECK(ensure(E.dscales, (size_t)N * 12));
@@ -1063,14 +1170,20 @@ int msplat_hip_train_step_3dgs(const MsplatCamera *cam, const MsplatGaussians *g
         mskern::launch_project3d_bwd(s, *cam, *g, P<int>(E.radii), P<float>(E.grads16), P<float>(E.dmeans),
                                      P<float>(E.dscales), P<float>(E.dquats), P<float>(E.dmean2d),
                                      P<float>(E.dfdc), P<float>(E.dfrest), gnorm, vis, max2d, inv_max_dim, nullptr,
-                                     P<float>(E.rec));
+                                     P<float>(E.rec), blog.overflow, 0);
         E.have_grads = true;
     }
     E.raster_grads = true;
     E.g16_moments = true;
     stage_mark(ST_COUNT);
+    HIPC(hipMemcpyAsync(E.pinned_i + 15, blog.overflow, sizeof(int), hipMemcpyDeviceToHost, s));
     HIPC(hipGetLastError());
     HIPC(hipStreamSynchronize(s));
+    *log_overflow = E.pinned_i[15] != 0;
+    if (*log_overflow) {
+        E.have_grads = E.raster_grads = false;
+        return MSPLAT_OK;
+    }
     if (loss_host) *loss_host = (float)E.pinned_d[0];
     if (E.timing) {
         for (int i = 0; i < ST_COUNT; ++i) {
@@ -1079,6 +1192,21 @@ int msplat_hip_train_step_3dgs(const MsplatCamera *cam, const MsplatGaussians *g
         }
     }
     return MSPLAT_OK;
+}
+
+int msplat_hip_train_step_3dgs(const MsplatCamera *cam, const MsplatGaussians *g, const float *bg, const float *gt,
+                               float lambda_l1, float lambda_dssim, float *gnorm, float *vis, float *max2d,
+                               float inv_max_dim, const MsplatAdam *adam, float *loss_host, int64_t *nisect) {
+    API_BEGIN
+    ENSURE_INIT();
+    // a step whose blend log overflowed the pool changed nothing (its
+    // backward and Adam skip): redo it with a larger pool
+    for (;;) {
+        bool overflow = false;
+        CHECK(train_step3d_once(cam, g, bg, gt, lambda_l1, lambda_dssim, gnorm, vis, max2d, inv_max_dim, adam, loss_host, nisect, &overflow));
+        if (!overflow) return MSPLAT_OK;
+        grow_log_pool();
+    }
     API_END
 }
 
@@ -1309,13 +1437,15 @@ int msplat_hip_raster_bwd(const float *dL_dimg, const float *dL_ddepth, const fl
     // a render-only forward skips the blend log, a training forward the full
     // outputs; replay the deterministic raster forward with what is missing
     const bool need_full = dL_ddepth || dL_dalpha || dL_dnormal || dL_dmedian || dL_ddist;
-    if (!E.log_valid || (need_full && !E.full_valid)) CHECK(raster_fwd_locked(true, need_full || E.full_valid));
+    if (!E.log_valid || (need_full && !E.full_valid)) CHECK(log_forward_checked(need_full || E.full_valid));
     mskern::DeepTiles deep;
     CHECK(deep_tiles(deep));
+    msr::BlendLog blog{};
+    CHECK(blend_log_desc(blog));
     const bool t_moments = mskern::launch_raster_bwd(
-        E.stream, E.W, E.H, E.tiles_x, E.tiles_y, P<int>(E.offsets), P<uint32_t>(E.blend_log), P<float>(E.t_ckpt),
-        P<int>(E.wave_cnt), P<float>(E.rec), E.bg, P<float>(E.final_Ts), P<int>(E.final_idx), dL_dimg, dL_ddepth,
-        dL_dalpha, dL_dnormal, dL_dmedian, dL_ddist, 0.0f, grads16, deep);
+        E.stream, E.W, E.H, E.tiles_x, E.tiles_y, P<int>(E.offsets), blog, P<float>(E.rec), E.bg,
+        P<float>(E.final_Ts), P<int>(E.final_idx), dL_dimg, dL_ddepth, dL_dalpha, dL_dnormal, dL_dmedian, dL_ddist,
+        0.0f, grads16, deep);
     if (t_moments) mskern::launch_finish_image_grads(E.stream, E.n, P<float>(E.rec), grads16);
     HIPC(hipGetLastError());
     return MSPLAT_OK;
@@ -1380,6 +1510,16 @@ int msplat_hip_set_wide_keys(int on) {
     API_BEGIN
     ENSURE_INIT();
     g_eng.wide_keys = on != 0;
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_set_log_pool_chunks(int chunks) {
+    API_BEGIN
+    ENSURE_INIT();
+    g_eng.log_init = chunks > 0 ? chunks : 0;
+    g_eng.log_cap = 0;
+    g_eng.log_valid = false;
     return MSPLAT_OK;
     API_END
 }

@@ -254,6 +254,10 @@ struct AdamDev {
     float *v[6];
     float step[6];
     float b1, b2, bc2_sqrt, eps;
+    // the launch does nothing when *skip > skip_above (an overflowed blend
+    // log: the raster gradients are incomplete and the step is redone)
+    const int *skip;
+    int skip_above;
 };
 
 // Nine transMat gradients from the ray moments the image-only raster
@@ -326,6 +330,7 @@ __global__ __launch_bounds__(kBlock) void k_project_bwd(
     float *__restrict__ dmean2d, float *__restrict__ dfdc, float *__restrict__ dfrest,
     float *__restrict__ grad_norm, float *__restrict__ vis, float *__restrict__ max2d, float inv_max_dim,
     AdamDev ad, const float4 *__restrict__ rec) {
+    if (ad.skip && *ad.skip > ad.skip_above) return;
     __shared__ float s_basis[kBlock * 24];
     __shared__ float s_vc[kBlock * 3];
     const int nb = num_sh_bases(cam.degree);
@@ -769,6 +774,7 @@ __global__ __launch_bounds__(kBlock) void k_project3d_bwd(
     float *__restrict__ dmean2d, float *__restrict__ dfdc, float *__restrict__ dfrest,
     float *__restrict__ grad_norm, float *__restrict__ vis, float *__restrict__ max2d, float inv_max_dim,
     AdamDev ad, const float4 *__restrict__ rec) {
+    if (ad.skip && *ad.skip > ad.skip_above) return;
     __shared__ float s_basis[kBlock * 24];
     __shared__ float s_vc[kBlock * 3];
     const int nb = num_sh_bases(cam.degree);
@@ -1013,10 +1019,12 @@ void launch_project_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaus
 void launch_project_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, const int *radii,
                         const float *g16, float *dmeans, float *dscales, float *dquats, float *dmean2d,
                         float *dfdc, float *dfrest, float *grad_norm, float *vis, float *max2d,
-                        float inv_max_dim, const MsplatAdam *adam, const float *moments_rec) {
+                        float inv_max_dim, const MsplatAdam *adam, const float *moments_rec, const int *skip_if, int skip_above) {
     if (g.num_points <= 0) return;
     const auto *mrec = reinterpret_cast<const float4 *>(moments_rec);
     AdamDev ad{};
+    ad.skip = skip_if;
+    ad.skip_above = skip_above;
     if (adam) {
         for (int k = 0; k < 6; ++k) {
             ad.m[k] = adam->exp_avg[k];
@@ -1052,10 +1060,12 @@ void launch_project3d_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGa
 void launch_project3d_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, const int *radii,
                           const float *g16, float *dmeans, float *dscales, float *dquats, float *dmean2d,
                           float *dfdc, float *dfrest, float *grad_norm, float *vis, float *max2d,
-                          float inv_max_dim, const MsplatAdam *adam, const float *sums_rec) {
+                          float inv_max_dim, const MsplatAdam *adam, const float *sums_rec, const int *skip_if, int skip_above) {
     if (g.num_points <= 0) return;
     const auto *r4 = reinterpret_cast<const float4 *>(sums_rec);
     AdamDev ad{};
+    ad.skip = skip_if;
+    ad.skip_above = skip_above;
     if (adam) {
         for (int k = 0; k < 6; ++k) {
             ad.m[k] = adam->exp_avg[k];

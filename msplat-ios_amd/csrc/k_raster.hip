@@ -52,14 +52,12 @@ __device__ __forceinline__ int load_batch(const float4 *__restrict__ rec, const 
 // With LOG, every wave also writes its blend log for the backward: one entry
 // {ballot low, ballot high, list position, splat id} for each visited list
 // entry that at least one of its lanes blended, in visit (front-to-back)
-// order, at blend_log[4 * start + wave * len + k] (len = the tile's list
-// length, which bounds a wave's visits); wave_cnt[4 * tile + wave] receives
-// the entry count.  Bit l of the ballot is set when lane l's pixel blended
-// the splat, so the backward replays exactly the forward's decisions.  For
-// every k > 0 with k % 64 == 0 each lane also stores its transmittance
-// before log entry k (a prefix checkpoint) at
-// t_ckpt[4 * start + wave * len + k + lane], as soon as entry k - 1 is
-// logged (so also when the log ends at k entries).
+// order, in 64-entry pool chunks (BlendLog); wave_cnt[4 * tile + wave]
+// receives the entry count.  Bit l of the ballot is set when lane l's pixel
+// blended the splat, so the backward replays exactly the forward's
+// decisions.  When a chunk is complete each lane also stores, as the
+// chunk's checkpoint, its transmittance before the next log entry (a prefix
+// checkpoint).
 // COUNT adds the work counters {pairs evaluated, log entries, pairs
 // blended, (wave, splat) visits, visit slots} to pair_counter.
 // With FULL_OUT = false only what the image-only training step consumes is
@@ -78,8 +76,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
     const float4 *__restrict__ rec, const float4 *__restrict__ mrec, const float *__restrict__ bgp,
     float *__restrict__ out_img, float *__restrict__ final_Ts, int *__restrict__ final_idx, float *__restrict__ out_depth,
     float *__restrict__ out_normal, float *__restrict__ out_alpha, float *__restrict__ out_median,
-    float *__restrict__ out_dist, unsigned long long *__restrict__ pair_counter, uint4 *__restrict__ blend_log,
-    float *__restrict__ t_ckpt, int *__restrict__ wave_cnt, int deep_len) {
+    float *__restrict__ out_dist, unsigned long long *__restrict__ pair_counter, BlendLog blog, int deep_len) {
     const int tile = xcd_strip_tile(blockIdx.x, tiles_x, T / tiles_x);
     if (tile < 0) return;
     __shared__ float4 s_rec[(FULL_OUT ? 6 : 5) * kThreads];  // the batch's records (load_batch planes)
@@ -97,8 +94,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
     const int start = offsets[tile], end = offsets[tile + 1];
     if (end - start >= deep_len) return;  // k_raster_deep renders it
     const float bg0 = bgp[0], bg1 = bgp[1], bg2 = bgp[2];
-    const size_t log_base = 4 * (size_t)start + (size_t)wave * (size_t)(end - start);
-    uint4 *wave_log = LOG ? blend_log + log_base : nullptr;
+    LogWriter lw;
+    lw.tb = LOG ? log_table_base(start, end - start, tile, wave) : 0;
+    lw.sp = LOG ? log_subpool(blog, tile, wave) : 0;
     int nlog = 0;  // wave-uniform
     // the current 64-entry chunk of the wave's log: lane k holds entry k,
     // and a full chunk is written with one coalesced store
@@ -176,6 +174,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
             Tr = blend ? next_T : Tr;
             if (COUNT) blends += __builtin_popcountll(bal);
             if (LOG && bal) {
+                if ((nlog & 63) == 0) lw.begin(blog, lane);
                 const bool mine = __builtin_amdgcn_inverse_ballot_w64(1ull << (nlog & 63));
                 lg_ent.x = mine ? (unsigned)bal : lg_ent.x;
                 lg_ent.y = mine ? (unsigned)(bal >> 32) : lg_ent.y;
@@ -183,10 +182,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
                 lg_ent.w = mine ? __float_as_uint(q4.w) : lg_ent.w;
                 // the transmittance before the next logged splat is the
                 // current one (a visit no lane blends changes nothing)
-                if ((++nlog & 63) == 0) {
-                    wave_log[nlog - 64 + lane] = lg_ent;
-                    t_ckpt[log_base + nlog + lane] = Tr;
-                }
+                if ((++nlog & 63) == 0) lw.full(blog, lane, nlog, lg_ent, Tr);
             }
         };
         // two visits per iteration: the second's work up to alpha does not
@@ -202,11 +198,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
             if (lane == 0) s_vis[wave] = nv;
         }
     }
-    if (LOG) {
-        // the last, partial chunk
-        if (lane < (nlog & 63)) wave_log[(nlog & ~63) + lane] = lg_ent;
-        if (lane == 0) wave_cnt[4 * tile + wave] = nlog;
-    }
+    if (LOG) lw.finish(blog, lane, nlog, lg_ent, tile, wave);  // the last, partial chunk
     if (COUNT) {
         // {pairs evaluated, log entries, pairs blended, visits, visit slots}
         __shared__ unsigned int s_cnt5[5];
@@ -292,8 +284,7 @@ constexpr unsigned long long kImgGrad = 0xfe0c0308d7654210ull;
 
 template <bool FULL>
 __global__ __launch_bounds__(kThreads) void k_raster_bwd(
-    int W, int H, int tiles_x, int T, const int *__restrict__ offsets, const uint4 *__restrict__ blend_log,
-    const float *__restrict__ t_ckpt, const int *__restrict__ wave_cnt, const float4 *__restrict__ rec,
+    int W, int H, int tiles_x, int T, const int *__restrict__ offsets, BlendLog blog, const float4 *__restrict__ rec,
     const float *__restrict__ bgp, const float *__restrict__ final_Ts, const int *__restrict__ final_idx,
     const float *__restrict__ dL_dimg, const float *__restrict__ dL_ddepth, const float *__restrict__ dL_daccum,
     const float *__restrict__ dL_dnormal, const float *__restrict__ dL_dmedian, const float *__restrict__ dL_ddist,
@@ -303,6 +294,7 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     const int tile = tile_list ? tile_list[blockIdx.x] : xcd_strip_tile(blockIdx.x, tiles_x, T / tiles_x);
     if (tile < 0) return;
     if (!tile_list && offsets[tile + 1] - offsets[tile] >= deep_len) return;
+    if (overflowed(blog)) return;  // an incomplete log: the step is redone with a larger pool
     constexpr int kWave = 64;
     // per wave: the staged entries' record planes (the image-only path
     // stages 4, the full one 7) and the log entries (full) or the reduction
@@ -319,11 +311,10 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     const bool inside = pxi < W && pyi < H;
     const float px = (float)pxi, py = (float)pyi;
     const int start = offsets[tile], len = offsets[tile + 1] - start;
-    const int nlog = __builtin_amdgcn_readfirstlane(wave_cnt[4 * tile + wave]);
+    const int nlog = __builtin_amdgcn_readfirstlane(blog.wave_cnt[4 * tile + wave]);
     Red8<kImgRaw> red8;
     if (!FULL) red8.init(reinterpret_cast<float *>(&L) + sizeof(L.r) / sizeof(float) + wave * 512, lane);
-    const size_t log_base = 4 * (size_t)start + (size_t)wave * (size_t)len;
-    const uint4 *lg = blend_log + log_base;
+    const int *__restrict__ chunk_of = blog.table + log_table_base(start, len, tile, wave);
     const size_t pix = inside ? (size_t)pyi * W + pxi : 0;
 
     float T_final = 1.f, dp0 = 0.f, dp1 = 0.f, dp2 = 0.f;
@@ -379,9 +370,12 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
         // that entry is a multiple of 64, else the value the recurrence of
         // the chunk after it ended with (the same operations in the same
         // order as one 64-entry chunk)
-        if (c != nchunks - 1 && ((c0 + kChunk) & (kWave - 1)) == 0) Tr = t_ckpt[log_base + c0 + kChunk + lane];
+        // the pool chunk holding entries c0 .. c0 + m - 1, and its checkpoint
+        const int cid = __builtin_amdgcn_readfirstlane(chunk_of[c0 >> 6]);
+        const uint4 *__restrict__ lg = blog.ent + 64 * (size_t)cid + (c0 & 63);
+        if (c != nchunks - 1 && ((c0 + kChunk) & (kWave - 1)) == 0) Tr = blog.ckpt[64 * (size_t)cid + lane];
         if (lane < m) {
-            const uint4 e = lg[c0 + lane];
+            const uint4 e = lg[lane];
             const float4 *r = rec + 5 * (size_t)e.w;
             // the forward's centred ray rows (centred_rows), then the colour;
             // the full case adds the raw transMat rows and the normal
@@ -406,14 +400,14 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
         // each fetched one visit ahead so its latency is not waited on, and
         // an entry's ballot is the lane mask of `has` itself
         uint4 e_next;
-        if constexpr (!FULL) e_next = lg[c0 + m - 1];
+        if constexpr (!FULL) e_next = lg[m - 1];
         for (int j = m - 1; j >= 0; --j) {
             uint4 e;
             if constexpr (FULL) {
                 e = L.e[wave][j];
             } else {
                 e = e_next;
-                e_next = lg[c0 + max(j - 1, 0)];
+                e_next = lg[max(j - 1, 0)];
             }
             const bool has = FULL ? (((lane < 32 ? e.x : e.y) >> (lane & 31)) & 1u)
                                   : __builtin_amdgcn_inverse_ballot_w64(((uint64_t)e.y << 32) | e.x);
@@ -812,14 +806,14 @@ __global__ __launch_bounds__(kLogThreads) void k_deep_log(int W, int H, int tile
                                                   const int *__restrict__ deep_list, const int *__restrict__ offsets,
                                                   const int *__restrict__ ids, const int *__restrict__ dpos,
                                                   const float *__restrict__ dtb, const int *__restrict__ dcnt,
-                                                  const float *__restrict__ final_Ts, uint4 *__restrict__ blend_log,
-                                                  float *__restrict__ t_ckpt, int *__restrict__ wave_cnt) {
+                                                  const float *__restrict__ final_Ts, BlendLog blog) {
     __shared__ uint32_t s_bits[kDeepWords];
     __shared__ int s_woff[kDeepWords];
     __shared__ uint32_t s_bal[2][kDeepBal];
     __shared__ int s_cnt[64], s_i[64], s_e[64], s_last[64];
     __shared__ float s_tf[64];
     __shared__ int s_red[kLogWaves];
+    __shared__ int s_ok;
     const int item = blockIdx.x;
     if (item >= n_deep * 4) return;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -827,7 +821,10 @@ __global__ __launch_bounds__(kLogThreads) void k_deep_log(int W, int H, int tile
     const int tile = deep_list[k];
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int start = offsets[tile], len = offsets[tile + 1] - start;
-    const size_t log_base = 4 * (size_t)start + (size_t)w * (size_t)len;
+    int *__restrict__ chunk_of = blog.table + log_table_base(start, len, tile, w);
+    // entry r of the log, and checkpoint c (the chunk of entry c - 1 holds it)
+    auto ent_at = [&](int r) { return blog.ent + 64 * (size_t)chunk_of[r >> 6] + (r & 63); };
+    auto ckpt_at = [&](int c, int p) { return blog.ckpt + 64 * (size_t)chunk_of[(c >> 6) - 1] + p; };
     auto slot_of = [&](int p) { return (size_t)k * 256 + 16 * lane_py(w, p) + lane_px(w, p); };
     if (threadIdx.x < 64) {
         const int p = threadIdx.x;
@@ -886,14 +883,28 @@ __global__ __launch_bounds__(kLogThreads) void k_deep_log(int W, int H, int tile
             woff += v < wv ? s_red[v] : 0;
             n_w += s_red[v];
         }
+        // pool chunks for the window's entries nlog .. nlog + n_w - 1
+        if (threadIdx.x == 0) {
+            const int have = (nlog + 63) >> 6, need = (nlog + n_w + 63) >> 6;
+            int ok = 1;
+            if (need > have) {
+                const int sp = log_subpool(blog, tile, w), n = need - have;
+                const int base = log_resolve(blog, sp, atomicAdd(&blog.counters[sp], n), n);
+                ok = base >= 0;
+                if (ok)
+                    for (int q = have; q < need; ++q) chunk_of[q] = base + (q - have);
+            }
+            s_ok = ok;
+        }
+        __syncthreads();
+        if (!s_ok) return;  // pool exhausted: the log is incomplete (overflowed)
 #pragma unroll
         for (int q = 0; q < WPT; ++q) {
             const int wd = threadIdx.x * WPT + q;
             s_woff[wd] = woff;
             for (uint32_t x = s_bits[wd]; x; x &= x - 1u) {
                 const int pos = P0 + 32 * wd + __builtin_ctz(x);
-                reinterpret_cast<uint2 *>(blend_log + log_base + nlog + woff)[1] =
-                    make_uint2((unsigned)pos, (unsigned)ids[start + pos]);
+                reinterpret_cast<uint2 *>(ent_at(nlog + woff))[1] = make_uint2((unsigned)pos, (unsigned)ids[start + pos]);
                 ++woff;
             }
         }
@@ -919,7 +930,7 @@ __global__ __launch_bounds__(kLogThreads) void k_deep_log(int W, int H, int tile
             }
             __syncthreads();
             for (int r = threadIdx.x; r < min(kDeepBal, n_w - R0); r += kLogThreads)
-                reinterpret_cast<uint2 *>(blend_log + log_base + nlog + R0 + r)[0] = make_uint2(s_bal[0][r], s_bal[1][r]);
+                reinterpret_cast<uint2 *>(ent_at(nlog + R0 + r))[0] = make_uint2(s_bal[0][r], s_bal[1][r]);
             __syncthreads();
         }
         // 4. checkpoints up to each pixel entry
@@ -935,8 +946,7 @@ __global__ __launch_bounds__(kLogThreads) void k_deep_log(int W, int H, int tile
                 if (lane == 0) rp = carry;
                 if (i < e) {
                     const float tb = Tb[i];
-                    for (int c = max(64, (rp + 64) & ~63); c <= r; c += 64)
-                        t_ckpt[log_base + c + p] = tb;
+                    for (int c = max(64, (rp + 64) & ~63); c <= r; c += 64) *ckpt_at(c, p) = tb;
                 }
                 carry = __shfl(r, min(63, e - 1 - i0), 64);
             }
@@ -951,10 +961,9 @@ __global__ __launch_bounds__(kLogThreads) void k_deep_log(int W, int H, int tile
     // the final transmittance for the checkpoints after each pixel's last entry
     for (int p = wv; p < 64; p += kLogWaves) {
         const float tf = s_tf[p];
-        for (int c = max(64, (s_last[p] + 64) & ~63) + 64 * lane; c <= nlog; c += 64 * 64)
-            t_ckpt[log_base + c + p] = tf;
+        for (int c = max(64, (s_last[p] + 64) & ~63) + 64 * lane; c <= nlog; c += 64 * 64) *ckpt_at(c, p) = tf;
     }
-    if (threadIdx.x == 0) wave_cnt[4 * tile + w] = nlog;
+    if (threadIdx.x == 0) blog.wave_cnt[4 * tile + w] = nlog;
 }
 
 }  // namespace
@@ -968,11 +977,11 @@ void launch_check_rcp(hipStream_t s, int efield, unsigned long long *bad) {
 void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
                        const float *rec, const float *mrec, const float *bg, float *out_img, float *final_Ts, int *final_idx,
                        float *out_depth, float *out_normal, float *out_alpha, float *out_median, float *out_dist,
-                       unsigned long long *pair_counter, uint32_t *blend_log, float *t_ckpt, int *wave_cnt,
-                       bool full_outputs, const DeepTiles &deep) {
+                       unsigned long long *pair_counter, const BlendLog *blog, bool full_outputs,
+                       const DeepTiles &deep) {
     const int T = tiles_x * tiles_y;
     const int grid = xcd_strip_grid(tiles_x, tiles_y);
-    auto *lg = reinterpret_cast<uint4 *>(blend_log);
+    const BlendLog lg = blog ? *blog : BlendLog{};
     const int deep_len = deep.n > 0 ? deep.len : INT32_MAX;
     if (deep.n > 0) {
         // the deep tiles on their own stream, beside the per-tile kernel
@@ -985,29 +994,29 @@ void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
                                offsets, ids, reinterpret_cast<const float4 *>(rec), bg, out_img, final_Ts, final_idx,
                                out_depth, out_normal, out_alpha, out_median, out_dist, deep.pos, deep.tb, deep.cnt);
         };
-        if (blend_log)
+        if (blog)
             full_outputs ? launch_deep(k_raster_deep<true, true>) : launch_deep(k_raster_deep<true, false>);
         else
             full_outputs ? launch_deep(k_raster_deep<false, true>) : launch_deep(k_raster_deep<false, false>);
-        if (blend_log)
+        if (blog)
             hipLaunchKernelGGL(k_deep_log, dim3(deep.n * 4), dim3(kLogThreads), 0, sd, W, H, tiles_x, deep.n, deep.list,
-                               offsets, ids, deep.pos, deep.tb, deep.cnt, final_Ts, lg, t_ckpt, wave_cnt);
+                               offsets, ids, deep.pos, deep.tb, deep.cnt, final_Ts, lg);
         (void)hipEventRecord(deep.join, sd);
     }
     auto launch = [&](auto kern) {
         hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
                            reinterpret_cast<const float4 *>(rec), reinterpret_cast<const float4 *>(mrec), bg,
                            out_img, final_Ts, final_idx, out_depth,
-                           out_normal, out_alpha, out_median, out_dist, pair_counter, lg, t_ckpt, wave_cnt, deep_len);
+                           out_normal, out_alpha, out_median, out_dist, pair_counter, lg, deep_len);
     };
     // the work counters are a separate instantiation (profiling only)
     if (pair_counter) {
-        if (blend_log)
+        if (blog)
             full_outputs ? launch(k_raster_fwd<true, true, true>) : launch(k_raster_fwd<true, false, true>);
         else
             full_outputs ? launch(k_raster_fwd<false, true, true>) : launch(k_raster_fwd<false, false, true>);
     } else {
-        if (blend_log)
+        if (blog)
             full_outputs ? launch(k_raster_fwd<true, true, false>) : launch(k_raster_fwd<true, false, false>);
         else
             full_outputs ? launch(k_raster_fwd<false, true, false>) : launch(k_raster_fwd<false, false, false>);
@@ -1022,24 +1031,23 @@ void launch_deep_tiles(hipStream_t s, int T, const int *offsets, int deep_len, i
 int64_t deep_pixel_entries(int n_deep) { return (int64_t)n_deep * 256 * kDeepMaxBlend; }
 
 bool launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets,
-                       const uint32_t *blend_log, const float *t_ckpt, const int *wave_cnt, const float *rec,
+                       const BlendLog &blog, const float *rec,
                        const float *bg, const float *final_Ts, const int *final_idx, const float *dL_dimg,
                        const float *dL_ddepth, const float *dL_daccum, const float *dL_dnormal,
                        const float *dL_dmedian, const float *dL_ddist, float ddist_uniform, float *grads16,
                        const DeepTiles &deep) {
     const int T = tiles_x * tiles_y;
     const int grid = xcd_strip_grid(tiles_x, tiles_y);
-    const auto *lg = reinterpret_cast<const uint4 *>(blend_log);
     const bool full = dL_ddepth || dL_daccum || dL_dnormal || dL_dmedian || dL_ddist || ddist_uniform != 0.0f;
     auto launch = [&](hipStream_t st, int blocks, const int *list, int deep_len) {
         if (full)
-            hipLaunchKernelGGL(k_raster_bwd<true>, dim3(blocks), dim3(kThreads), 0, st, W, H, tiles_x, T, offsets, lg,
-                               t_ckpt, wave_cnt, reinterpret_cast<const float4 *>(rec), bg, final_Ts, final_idx,
+            hipLaunchKernelGGL(k_raster_bwd<true>, dim3(blocks), dim3(kThreads), 0, st, W, H, tiles_x, T, offsets, blog,
+                               reinterpret_cast<const float4 *>(rec), bg, final_Ts, final_idx,
                                dL_dimg, dL_ddepth, dL_daccum, dL_dnormal, dL_dmedian, dL_ddist, ddist_uniform,
                                grads16, list, deep_len);
         else
             hipLaunchKernelGGL(k_raster_bwd<false>, dim3(blocks), dim3(kThreads), 0, st, W, H, tiles_x, T, offsets,
-                               lg, t_ckpt, wave_cnt, reinterpret_cast<const float4 *>(rec), bg, final_Ts, final_idx,
+                               blog, reinterpret_cast<const float4 *>(rec), bg, final_Ts, final_idx,
                                dL_dimg, dL_ddepth, dL_daccum, dL_dnormal, dL_dmedian, dL_ddist, ddist_uniform,
                                grads16, list, deep_len);
     };

@@ -43,9 +43,9 @@ __device__ __forceinline__ int load_batch3(const float4 *__restrict__ rec, const
 }
 
 // With LOG, every wave writes its blend log and prefix checkpoints exactly
-// as k_raster_fwd<true, ...> does (same layout: entry {ballot lo, ballot hi,
-// list position, splat id} at blend_log[4 * start + wave * len + k],
-// transmittance before entry k at t_ckpt[... + k + lane] for k % 64 == 0).
+// as k_raster_fwd<true, ...> does (entries {ballot lo, ballot hi, list
+// position, splat id} in 64-entry pool chunks with their checkpoints,
+// BlendLog).
 // Outputs: out_img and final_Ts[.][0] (the transmittance).
 template <bool LOG>
 __global__ __launch_bounds__(kThreads) void k_raster3d_fwd(int W, int H, int tiles_x, int T,
@@ -54,9 +54,7 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_fwd(int W, int H, int til
                                                            const float4 *__restrict__ rec,
                                                            const float4 *__restrict__ boxes,
                                                            const float *__restrict__ bgp, float *__restrict__ out_img,
-                                                           float *__restrict__ final_Ts,
-                                                           uint4 *__restrict__ blend_log, float *__restrict__ t_ckpt,
-                                                           int *__restrict__ wave_cnt) {
+                                                           float *__restrict__ final_Ts, BlendLog blog) {
     const int tile = xcd_strip_tile(blockIdx.x, tiles_x, T / tiles_x);
     if (tile < 0) return;
     __shared__ float4 s_rec[3 * kThreads];
@@ -72,8 +70,9 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_fwd(int W, int H, int til
     asm volatile("" : "+v"(px), "+v"(py));
     const float sx0 = (float)(tx * 16), sy0 = (float)(ty * 16);
     const int start = offsets[tile], end = offsets[tile + 1];
-    const size_t log_base = 4 * (size_t)start + (size_t)wave * (size_t)(end - start);
-    uint4 *wave_log = LOG ? blend_log + log_base : nullptr;
+    LogWriter lw;
+    lw.tb = LOG ? log_table_base(start, end - start, tile, wave) : 0;
+    lw.sp = LOG ? log_subpool(blog, tile, wave) : 0;
     int nlog = 0;
     uint4 lg_ent = make_uint4(0u, 0u, 0u, 0u);
     const char *s_bytes = reinterpret_cast<const char *>(s_rec);
@@ -110,15 +109,13 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_fwd(int W, int H, int til
             cb = __builtin_fmaf(p2.z, w, cb);
             Tr = blend ? next_T : Tr;
             if (LOG && bal) {
+                if ((nlog & 63) == 0) lw.begin(blog, lane);
                 const bool mine = __builtin_amdgcn_inverse_ballot_w64(1ull << (nlog & 63));
                 lg_ent.x = mine ? (unsigned)bal : lg_ent.x;
                 lg_ent.y = mine ? (unsigned)(bal >> 32) : lg_ent.y;
                 lg_ent.z = mine ? __float_as_uint(p1.z) : lg_ent.z;
                 lg_ent.w = mine ? __float_as_uint(p1.w) : lg_ent.w;
-                if ((++nlog & 63) == 0) {
-                    wave_log[nlog - 64 + lane] = lg_ent;
-                    t_ckpt[log_base + nlog + lane] = Tr;
-                }
+                if ((++nlog & 63) == 0) lw.full(blog, lane, nlog, lg_ent, Tr);
             }
         };
         int j = 0;
@@ -128,10 +125,7 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_fwd(int W, int H, int til
         }
         if (j < n && done_m != ~0ull) visit(j);
     }
-    if (LOG) {
-        if (lane < (nlog & 63)) wave_log[(nlog & ~63) + lane] = lg_ent;
-        if (lane == 0) wave_cnt[4 * tile + wave] = nlog;
-    }
+    if (LOG) lw.finish(blog, lane, nlog, lg_ent, tile, wave);
     if (!inside) return;
     const size_t pix = (size_t)pyi * W + pxi;
     final_Ts[3 * pix + 0] = Tr;
@@ -153,10 +147,7 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_fwd(int W, int H, int til
 // pairs of the reduction are empty and skipped (their scratch rows hold
 // zeros).
 __global__ __launch_bounds__(kThreads) void k_raster3d_bwd(int W, int H, int tiles_x, int T,
-                                                           const int *__restrict__ offsets,
-                                                           const uint4 *__restrict__ blend_log,
-                                                           const float *__restrict__ t_ckpt,
-                                                           const int *__restrict__ wave_cnt,
+                                                           const int *__restrict__ offsets, BlendLog blog,
                                                            const float4 *__restrict__ rec,
                                                            const float *__restrict__ bgp,
                                                            const float *__restrict__ final_Ts,
@@ -164,6 +155,7 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_bwd(int W, int H, int til
                                                            float *__restrict__ grads16) {
     const int tile = xcd_strip_tile(blockIdx.x, tiles_x, T / tiles_x);
     if (tile < 0) return;
+    if (overflowed(blog)) return;  // an incomplete log: the step is redone with a larger pool
     constexpr int kWave = 64;
     __shared__ float4 s_r[4][3][64];
     __shared__ float s_red[4][512];
@@ -175,12 +167,11 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_bwd(int W, int H, int til
     const bool inside = pxi < W && pyi < H;
     const float px = (float)pxi, py = (float)pyi;
     const int start = offsets[tile], len = offsets[tile + 1] - start;
-    const int nlog = __builtin_amdgcn_readfirstlane(wave_cnt[4 * tile + wave]);
+    const int nlog = __builtin_amdgcn_readfirstlane(blog.wave_cnt[4 * tile + wave]);
     Red8<0, 0xE0> red8;
     red8.init(&s_red[wave][0], lane);
     red8.zero_skipped();
-    const size_t log_base = 4 * (size_t)start + (size_t)wave * (size_t)len;
-    const uint4 *lg = blend_log + log_base;
+    const int *__restrict__ chunk_of = blog.table + log_table_base(start, len, tile, wave);
     const size_t pix = inside ? (size_t)pyi * W + pxi : 0;
     float T_final = 1.f, dp0 = 0.f, dp1 = 0.f, dp2 = 0.f;
     if (inside) {
@@ -201,9 +192,11 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_bwd(int W, int H, int til
     for (int c = nchunks - 1; c >= 0; --c) {
         const int c0 = c * kWave;
         const int m = min(kWave, nlog - c0);
-        float Tr = c == nchunks - 1 ? T_final : t_ckpt[log_base + c0 + kWave + lane];
+        const int cid = __builtin_amdgcn_readfirstlane(chunk_of[c]);
+        const uint4 *__restrict__ lg = blog.ent + 64 * (size_t)cid;
+        float Tr = c == nchunks - 1 ? T_final : blog.ckpt[64 * (size_t)cid + lane];
         if (lane < m) {
-            const uint4 e = lg[c0 + lane];
+            const uint4 e = lg[lane];
             const float4 *r = rec + 3 * (size_t)e.w;
             s_r[wave][0][lane] = r[0];
             s_r[wave][1][lane] = r[1];
@@ -211,7 +204,7 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_bwd(int W, int H, int til
         }
         wave_lds_sync();
         for (int j = m - 1; j >= 0; --j) {
-            const uint4 e = lg[c0 + j];
+            const uint4 e = lg[j];
             const bool has = __builtin_amdgcn_inverse_ballot_w64(((uint64_t)e.y << 32) | e.x);
             const float4 p0 = s_r[wave][0][j], p1 = s_r[wave][1][j], p2 = s_r[wave][2][j];
             float dx, dy;
@@ -253,28 +246,27 @@ namespace mskern {
 
 void launch_raster3d_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
                          const float *rec, const float *boxes, const float *bg, float *out_img, float *final_Ts,
-                         uint32_t *blend_log, float *t_ckpt, int *wave_cnt) {
+                         const BlendLog *blog) {
     const int T = tiles_x * tiles_y;
     if (T <= 0) return;
     const int grid = xcd_strip_grid(tiles_x, tiles_y);
     const auto *r4 = reinterpret_cast<const float4 *>(rec);
     const auto *b4 = reinterpret_cast<const float4 *>(boxes);
-    if (blend_log)
+    if (blog)
         hipLaunchKernelGGL(k_raster3d_fwd<true>, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
-                           r4, b4, bg, out_img, final_Ts, reinterpret_cast<uint4 *>(blend_log), t_ckpt, wave_cnt);
+                           r4, b4, bg, out_img, final_Ts, *blog);
     else
         hipLaunchKernelGGL(k_raster3d_fwd<false>, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
-                           r4, b4, bg, out_img, final_Ts, nullptr, nullptr, nullptr);
+                           r4, b4, bg, out_img, final_Ts, BlendLog{});
 }
 
 void launch_raster3d_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets,
-                         const uint32_t *blend_log, const float *t_ckpt, const int *wave_cnt, const float *rec,
-                         const float *bg, const float *final_Ts, const float *dL_dimg, float *grads16) {
+                         const BlendLog &blog, const float *rec, const float *bg, const float *final_Ts,
+                         const float *dL_dimg, float *grads16) {
     const int T = tiles_x * tiles_y;
     if (T <= 0) return;
     const int grid = xcd_strip_grid(tiles_x, tiles_y);
-    hipLaunchKernelGGL(k_raster3d_bwd, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets,
-                       reinterpret_cast<const uint4 *>(blend_log), t_ckpt, wave_cnt,
+    hipLaunchKernelGGL(k_raster3d_bwd, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, blog,
                        reinterpret_cast<const float4 *>(rec), bg, final_Ts, dL_dimg, grads16);
 }
 

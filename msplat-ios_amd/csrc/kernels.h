@@ -8,6 +8,7 @@
 #include <algorithm>
 
 #include "msplat_engine.h"
+#include "raster_wave.h"
 
 namespace mskern {
 
@@ -25,7 +26,8 @@ void launch_project_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaus
 void launch_project_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, const int *radii,
                         const float *g16, float *dmeans, float *dscales, float *dquats, float *dmean2d,
                         float *dfdc, float *dfrest, float *grad_norm, float *vis, float *max2d,
-                        float inv_max_dim, const MsplatAdam *adam, const float *moments_rec);
+                        float inv_max_dim, const MsplatAdam *adam, const float *moments_rec,
+                        const int *skip_if = nullptr, int skip_above = 0);
 // The image-only raster backward's g16 rows -> the reference's raster
 // gradients (dL/dtransMat, dL/dopacity logit, dL/dcolors), in place.
 void launch_finish_image_grads(hipStream_t s, int n, const float *rec, float *g16);
@@ -40,7 +42,8 @@ void launch_project3d_fwd(hipStream_t s, const MsplatCamera &cam, const MsplatGa
 void launch_project3d_bwd(hipStream_t s, const MsplatCamera &cam, const MsplatGaussians &g, const int *radii,
                           const float *g16, float *dmeans, float *dscales, float *dquats, float *dmean2d,
                           float *dfdc, float *dfrest, float *grad_norm, float *vis, float *max2d,
-                          float inv_max_dim, const MsplatAdam *adam, const float *sums_rec);
+                          float inv_max_dim, const MsplatAdam *adam, const float *sums_rec,
+                          const int *skip_if = nullptr, int skip_above = 0);
 // The 3DGS raster backward's sums -> the raster gradients [dxy 2, dconic 3,
 // dopacity logit, dcolor 3] (the first 9 of each 16-float row), in place.
 void launch_finish3d_grads(hipStream_t s, int n, const float *rec, float *g16);
@@ -76,11 +79,13 @@ constexpr int kSuperTile = 4;
 constexpr int kSuperSortChunk = 4096;
 
 // k_raster.hip
-// blend_log (4 * I entries of 16 bytes), t_ckpt (4 * I + 64 floats) and
-// wave_cnt (4 * T ints) receive the per-wave blend log and transmittance
-// checkpoints the backward replays; pass nullptr for render-only frames.
-// full_outputs = false produces only out_img, final_Ts[.][0] and
-// final_idx[.][0] (what the image-only training step consumes).
+// blog (msr::BlendLog: a pool of 64-entry chunks of 16-byte entries with
+// their 64-float checkpoints, the per-wave chunk table of
+// msr::log_table_ints(I, T) ints, the per-wave counts [4T] and the chunk
+// counter) receives the per-wave blend log and transmittance checkpoints the
+// backward replays; pass nullptr for render-only frames.  full_outputs =
+// false produces only out_img and final_Ts[.][0] (what the image-only
+// training step consumes).
 // Deep tiles (lists of at least len entries) are rendered pixel by pixel
 // (k_raster_deep) instead of by one workgroup; list[0, n) are their tile
 // indices (launch_deep_tiles), and with a blend log pos / tb / cnt hold
@@ -102,12 +107,12 @@ int64_t deep_pixel_entries(int n_deep);
 void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
                        const float *rec, const float *mrec, const float *bg, float *out_img, float *final_Ts, int *final_idx,
                        float *out_depth, float *out_normal, float *out_alpha, float *out_median, float *out_dist,
-                       unsigned long long *pair_counter, uint32_t *blend_log, float *t_ckpt, int *wave_cnt,
-                       bool full_outputs, const DeepTiles &deep);
+                       unsigned long long *pair_counter, const msr::BlendLog *blog, bool full_outputs,
+                       const DeepTiles &deep);
 // Returns true when the image-only kernel ran: grads16 then holds its sums
 // (launch_finish_image_grads / launch_project_bwd finish them).
 bool launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets,
-                       const uint32_t *blend_log, const float *t_ckpt, const int *wave_cnt, const float *rec,
+                       const msr::BlendLog &blog, const float *rec,
                        const float *bg, const float *final_Ts, const int *final_idx, const float *dL_dimg,
                        const float *dL_ddepth, const float *dL_daccum, const float *dL_dnormal,
                        const float *dL_dmedian, const float *dL_ddist, float ddist_uniform, float *grads16,
@@ -120,10 +125,10 @@ constexpr int kBlendLogEntryBytes = 16;
 // sums to grads16 (launch_finish3d_grads finishes them).
 void launch_raster3d_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets, const int *ids,
                          const float *rec, const float *boxes, const float *bg, float *out_img, float *final_Ts,
-                         uint32_t *blend_log, float *t_ckpt, int *wave_cnt);
+                         const msr::BlendLog *blog);
 void launch_raster3d_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, const int *offsets,
-                         const uint32_t *blend_log, const float *t_ckpt, const int *wave_cnt, const float *rec,
-                         const float *bg, const float *final_Ts, const float *dL_dimg, float *grads16);
+                         const msr::BlendLog &blog, const float *rec, const float *bg, const float *final_Ts,
+                         const float *dL_dimg, float *grads16);
 // Adds to *bad the number of floats of exponent field efield (1..254, both
 // signs, every mantissa) where the rasterizer's fast reciprocal differs from
 // the correctly rounded 1 / x.

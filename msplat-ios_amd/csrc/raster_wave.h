@@ -12,6 +12,94 @@ namespace msr {
 
 constexpr int kThreads = 256;
 
+// The blend logs of one frame, in 64-entry chunks taken from a pool as the
+// waves fill them.  Wave w of tile t (list [start, start + len)) logs at most
+// len entries; its k-th chunk (entries 64k .. 64k + 63) is pool chunk
+// c = table[log_table_base(start, len, t, w) + k], whose entries are
+// ent[64 c ..] and whose checkpoint, each lane's transmittance before entry
+// 64 (k + 1), is ckpt[64 c + lane].  wave_cnt[4 t + w] is the wave's entry
+// count.  The pool is split into nsub sub-pools of sub_cap chunks, each with
+// its own atomic counter (a single counter serialised the claims of every
+// wave and tripled the training forward's time), plus a shared spill region
+// of spill_cap chunks for sub-pools that run out; a claim past both stops
+// that wave's log and sets *overflow, so the log is then incomplete and its
+// consumers do nothing (overflowed()).
+struct BlendLog {
+    uint4 *ent;
+    float *ckpt;
+    int *table;
+    int *wave_cnt;
+    int *counters;  // [nsub + 1]: the sub-pools' and the spill region's
+    int *overflow;
+    int nsub, sub_cap, spill_cap;
+};
+
+// Wave (t, w)'s chunk-table range starts here: the ranges of successive
+// waves are disjoint, since a wave's ceil(len / 64) chunks fit between
+// floor(4 start + w len) / 64 + 4 t + w and the next wave's base.
+__host__ __device__ inline size_t log_table_base(int start, int len, int tile, int wave) {
+    return (4 * (size_t)start + (size_t)wave * (size_t)len) / 64 + 4 * (size_t)tile + (size_t)wave;
+}
+inline size_t log_table_ints(int64_t isect, int tiles) { return (size_t)(4 * isect) / 64 + 4 * (size_t)tiles + 1; }
+__device__ __forceinline__ bool overflowed(const BlendLog &L) { return *L.overflow != 0; }
+__device__ __forceinline__ int log_subpool(const BlendLog &L, int tile, int wave) { return (4 * tile + wave) % L.nsub; }
+
+// n chunks for sub-pool sp after its counter returned c (the base of a claim
+// of n): the chunk index of the first, from the spill region if the
+// sub-pool is full, or -1 (and *overflow set) if both are.
+__device__ __forceinline__ int log_resolve(const BlendLog &L, int sp, int c, int n) {
+    if (c + n <= L.sub_cap) return sp * L.sub_cap + c;
+    const int x = atomicAdd(&L.counters[L.nsub], n);
+    if (x + n <= L.spill_cap) return L.nsub * L.sub_cap + x;
+    atomicOr(L.overflow, 1);
+    return -1;
+}
+
+// A wave's log writer: entries are staged in lane (count mod 64) of lg_ent
+// by the caller; begin() issues the sub-pool claim of a chunk's first entry
+// (its result is only waited for when the chunk is written), full() writes
+// a completed chunk and its checkpoint, finish() the partial last chunk and
+// the count.  Wave-uniform control flow.
+struct LogWriter {
+    size_t tb;
+    int sp = 0;
+    int cid = 0;  // lane 0: the sub-pool counter's value
+    bool ok = true;
+    // cid is only written (and only read) in lane 0: a select over the
+    // other lanes would read the register the atomic is still returning
+    // into and wait for it on every logged visit
+    __device__ __forceinline__ void begin(const BlendLog &L, int lane) {
+        if (!ok) return;
+        if (lane == 0) cid = atomicAdd(&L.counters[sp], 1);
+    }
+    __device__ __forceinline__ int claimed(const BlendLog &L, int lane) {
+        int c = 0;
+        if (lane == 0) c = log_resolve(L, sp, cid, 1);
+        c = __builtin_amdgcn_readfirstlane(c);
+        if (c < 0) ok = false;
+        return c;
+    }
+    __device__ __forceinline__ void full(const BlendLog &L, int lane, int nlog, const uint4 &e, float T) {
+        if (!ok) return;
+        const int c = claimed(L, lane);
+        if (!ok) return;
+        L.ent[64 * (size_t)c + lane] = e;
+        L.ckpt[64 * (size_t)c + lane] = T;
+        if (lane == 0) L.table[tb + (size_t)((nlog >> 6) - 1)] = c;
+    }
+    __device__ __forceinline__ void finish(const BlendLog &L, int lane, int nlog, const uint4 &e, int tile,
+                                           int wave) {
+        if (ok && (nlog & 63)) {
+            const int c = claimed(L, lane);
+            if (ok) {
+                if (lane < (nlog & 63)) L.ent[64 * (size_t)c + lane] = e;
+                if (lane == 0) L.table[tb + (size_t)(nlog >> 6)] = c;
+            }
+        }
+        if (lane == 0) L.wave_cnt[4 * tile + wave] = nlog;
+    }
+};
+
 // Per-wave slot lists of one batch: s_list[w][0..n_w) holds, in ascending
 // order, the slots whose mask m has bit w (this wave's ballot rank after the
 // counts of the waves below it).

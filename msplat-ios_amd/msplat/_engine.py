@@ -60,9 +60,9 @@ LAST = {name: i for i, name in enumerate([
     "records", "tile_offsets", "gaussian_ids", "out_img", "final_Ts", "final_idx", "out_depth", "out_normal",
     "out_alpha", "out_median_depth", "out_distortion", "dL_dout_img", "grads16", "dL_dtransMat",
     "dL_dnormal3D", "dL_dopacity", "dL_dcolors", "dL_dmean3D", "dL_dscale", "dL_dquat", "dL_dmean2D",
-    "dL_dfeatures_dc", "dL_dfeatures_rest", "blend_log", "blend_ckpt", "wave_counts",
+    "dL_dfeatures_dc", "dL_dfeatures_rest", "blend_log", "blend_ckpt", "wave_counts", "blend_chunks",
 ])}
-_INT_BUFS = {"radii", "num_tiles_hit", "tile_offsets", "gaussian_ids", "final_idx", "blend_log", "wave_counts"}
+_INT_BUFS = {"radii", "num_tiles_hit", "tile_offsets", "gaussian_ids", "final_idx", "blend_log", "wave_counts", "blend_chunks"}
 
 # Every entry point declared in include/msplat_engine.h.
 EXPORTS = [
@@ -73,7 +73,8 @@ EXPORTS = [
     "msplat_hip_loss_fwd_bwd_noalloc",
     "msplat_hip_raster_bwd", "msplat_hip_project_bwd", "msplat_hip_project_bwd_adam", "msplat_hip_last", "msplat_hip_enable_timing",
     "msplat_hip_stage_times", "msplat_hip_last_pairs_evaluated", "msplat_hip_last_raster_counts",
-    "msplat_hip_check_fast_rcp", "msplat_hip_set_wide_keys", "msplat_hip_set_deep_tile_len", "msplat_hip_tsdf_integrate",
+    "msplat_hip_check_fast_rcp", "msplat_hip_set_wide_keys", "msplat_hip_set_deep_tile_len", "msplat_hip_set_log_pool_chunks",
+    "msplat_hip_tsdf_integrate",
     "msplat_hip_marching_cubes", "msplat_hip_mc_table", "msplat_hip_unproject_depth", "msplat_hip_render_3dgs",
     "msplat_hip_train_step_3dgs", "msplat_hip_densify_3dgs",
 ]
@@ -129,6 +130,7 @@ def lib() -> C.CDLL:
         "msplat_hip_check_fast_rcp": (I, [I, I, C.POINTER(C.c_int64)]),
         "msplat_hip_set_wide_keys": (I, [I]),
         "msplat_hip_set_deep_tile_len": (I, [I]),
+        "msplat_hip_set_log_pool_chunks": (I, [I]),
         "msplat_hip_densify_3dgs": (I, [I, I, F, F, F, I, F, F, F, I, P, P, P, F, P * 6, I, P * 6, P * 6, P,
                                         C.POINTER(I)]),
         "msplat_hip_render_3dgs": (I, [C.POINTER(MsplatCamera), C.POINTER(MsplatGaussians), P, C.POINTER(I64)]),

@@ -21,9 +21,38 @@ through the rest of the step:
 """
 from __future__ import annotations
 
+import json
+import os
+
 import numpy as np
 
 RTOL, CTOL, FLOOR = 1e-3, 1e-4, 1e-7
+
+
+def record(kind: str, what: str, **vals) -> None:
+    """Appends one JSON line {kind, what, ...} to the file named by
+    MSPLAT_PARITY_LOG, if set: how far the literal bars (gradients within
+    1e-3 relative, post-Adam parameters within 1e-5) hold on a run."""
+    path = os.environ.get("MSPLAT_PARITY_LOG")
+    if not path:
+        return
+    with open(path, "a") as f:
+        f.write(json.dumps(dict(kind=kind, what=what, **vals)) + "\n")
+
+
+def literal_rel(g, o, rtol=1e-3):
+    """The elements of g outside rtol |o| of o: count, and the same among
+    the significant elements (|o| above 1e-3 of the component's or array's
+    largest magnitude), with the worst relative error there."""
+    g = np.asarray(g, np.float64)
+    o = np.asarray(o, np.float64)
+    err = np.abs(g - o)
+    miss = err > rtol * np.abs(o)
+    scale = np.abs(o).max(axis=0) if o.ndim == 2 else np.abs(o).max()
+    sig = np.abs(o) > 1e-3 * scale
+    rel = np.where(sig, err / np.maximum(np.abs(o), 1e-300), 0.0)
+    return dict(elements=int(o.size), beyond_1e3_rel=int(miss.sum()), significant=int(sig.sum()),
+                significant_beyond_1e3_rel=int((miss & sig).sum()), worst_rel_significant=float(rel.max()))
 
 
 def raster_bound(o, a):
@@ -50,6 +79,7 @@ def grad_close(g, o, a, what):
     bad = ratio > 1.0
     floor_only = err > RTOL * np.abs(o) + CTOL * a
     tight = err > 1e-4 * np.abs(o) + 1e-6 * np.abs(o).max(axis=0)
+    record("raster_grads", what, worst_err_over_bound=float(ratio.max()), **literal_rel(g, o))
     print(f"[grad] {what}: worst err/bound {ratio.max():.3g}, misses {int(bad.sum())} of {bad.size}, "
           f"within the floor only {int((floor_only & ~bad).sum())}; outside 1e-4|o| + 1e-6 max|o|: "
           f"{int(tight.sum())} per component {tight.sum(axis=0).tolist()}", flush=True)
@@ -89,7 +119,7 @@ def adam_first_step(g, lr, eps=1e-8):
     return lr * g / (np.abs(g) + eps)
 
 
-def post_adam_close(names, got_params, orc_params, got_m, orc_m, noise, lrs, beta1=0.9):
+def post_adam_close(names, got_params, orc_params, got_m, orc_m, noise, lrs, beta1=0.9, label=""):
     """First Adam step.  Parameter gradients (recovered from the first
     moments, m = (1 - beta1) g) must lie within their allowed error; every
     parameter must lie within the range of steps that error allows, i.e.
@@ -114,6 +144,10 @@ def post_adam_close(names, got_params, orc_params, got_m, orc_m, noise, lrs, bet
         limit = reach + 2.5e-7 * np.maximum(np.abs(po), 1.0)
         diff = np.abs(p - po)
         unresolved = reach > 1e-5
+        record("param_grads", f"{label} {name}".strip(), **literal_rel(g, go))
+        record("post_adam", f"{label} {name}".strip(), elements=int(p.size), beyond_1e5=int((diff > 1e-5).sum()),
+               max_abs_diff=float(diff.max()), unresolved=int(unresolved.sum()),
+               beyond_1e5_resolved=int(((diff > 1e-5) & ~unresolved).sum()))
         print(f"[adam] {name}: {int(unresolved.sum())} of {p.size} steps not resolved to 1e-5 by the gradient's "
               f"allowed error; {int((diff > 1e-5).sum())} parameters beyond 1e-5 (max {diff.max():.3g}); "
               f"worst diff/limit {(diff / limit).max():.3g}", flush=True)

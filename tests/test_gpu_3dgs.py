@@ -4,11 +4,12 @@ off-screen Gaussians, which stress the quadrant masks), raster gradients
 within the float-atomic bound, the projection backward bit for bit from
 the GPU's own raster gradients, the fused Adam step, and training."""
 import ctypes as C
+import os
 
 import numpy as np
 import pytest
 
-from parity import raster_bound, trainer_post_adam_close
+from parity import literal_rel, raster_bound, record, trainer_post_adam_close
 
 pytestmark = pytest.mark.gpu
 
@@ -367,8 +368,32 @@ def test_full_step3d_matches_oracle_full_size(workload, orc, eng):
     bound = raster_bound(g_o, a_o)
     print(f"[full step 3dgs] raster gradients: worst err/bound {float((err / bound).max()):.3g}", flush=True)
     assert (err <= bound).all()
-    del g_o, a_o, err, bound
+    record("raster_grads", f"{scene.name} grads9", worst_err_over_bound=float((err / bound).max()),
+           **literal_rel(g9, g_o))
+    del a_o, err, bound
     ref = orc.project3d_bwd(pre, ocam, scene.sh_degree, scene.sh_degree, proj["radii"], g9)
+    if os.environ.get("MSPLAT_PARITY_LOG"):
+        # the literal bars against the golden model's own step (its raster
+        # gradients through its projection backward and Adam)
+        own = orc.project3d_bwd(pre, ocam, scene.sh_degree, scene.sh_degree, proj["radii"],
+                                np.ascontiguousarray(g_o, np.float32))
+        own_g = [own["dmeans"], own["dscales"], own["dquats"], own["dfdc"], own["dfrest"],
+                 np.ascontiguousarray(g_o[:, 5:6], np.float32)]
+        adam0 = D.DeviceScene3D(dict(zip(GROUPS, [p[:1] for p in scene.params()])), scene.background).adam_struct()
+        for gi, name in enumerate(GROUPS):
+            gg = [ref["dmeans"], ref["dscales"], ref["dquats"], ref["dfdc"], ref["dfrest"], g9[:, 5:6]][gi]
+            record("param_grads", f"{scene.name} {name}", **literal_rel(np.asarray(gg).reshape(-1),
+                                                                        np.asarray(own_g[gi]).reshape(-1)))
+            par = pre[name].copy()
+            mm = np.zeros_like(par)
+            vv = np.zeros_like(par)
+            orc.adam(par, np.ascontiguousarray(own_g[gi], np.float32).reshape(par.shape), mm, vv,
+                     adam0.step_size[gi], adam0.beta1, adam0.beta2, adam0.bc2_sqrt, adam0.eps)
+            diff = np.abs(got[gi].astype(np.float64).reshape(-1) - par.reshape(-1))
+            record("post_adam", f"{scene.name} {name}", elements=int(diff.size), beyond_1e5=int((diff > 1e-5).sum()),
+                   max_abs_diff=float(diff.max()))
+        del own, own_g
+    del g_o
     grads = [ref["dmeans"], ref["dscales"], ref["dquats"], ref["dfdc"], ref["dfrest"], np.ascontiguousarray(g9[:, 5:6])]
     adam = D.DeviceScene3D(dict(zip(GROUPS, [p[:1] for p in scene.params()])), scene.background).adam_struct()
     for g, name in enumerate(GROUPS):

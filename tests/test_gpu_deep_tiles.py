@@ -52,20 +52,24 @@ class deep_len:
 
 def _logs(offsets):
     """Per (tile, wave) log entries [0, count) and checkpoints of the last
-    forward that wrote a blend log, as a dict of arrays."""
+    forward that wrote a blend log (gathered from the pool chunks through
+    each wave's chunk table)."""
     T = offsets.size - 1
     cnt = E.last("wave_counts").reshape(T, 4)
-    log = E.last("blend_log").reshape(-1, 4)
-    ck = E.last("blend_ckpt")
+    log = E.last("blend_log").reshape(-1, 64, 4)
+    ck = E.last("blend_ckpt").reshape(-1, 64)
+    table = E.last("blend_chunks")
     ents, cks = [], []
     for t in range(T):
         s0, ln = int(offsets[t]), int(offsets[t + 1] - offsets[t])
         for w in range(4):
-            base = 4 * s0 + w * ln
+            tb = (4 * s0 + w * ln) // 64 + 4 * t + w
             c = int(cnt[t, w])
-            ents.append(log[base:base + c])
+            chunks = table[tb:tb + (c + 63) // 64]
+            if c:
+                ents.append(log[chunks].reshape(-1, 4)[:c])
             for k in range(64, c + 1, 64):
-                cks.append(ck[base + k:base + k + 64])
+                cks.append(ck[chunks[k // 64 - 1]])
     return cnt, np.concatenate(ents) if ents else np.zeros((0, 4), np.int32), \
         np.concatenate(cks) if cks else np.zeros(0, np.float32)
 

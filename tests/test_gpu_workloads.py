@@ -185,7 +185,7 @@ def test_full_step_matches_oracle_full_size(workload, orc, eng):
     radii = orc.project_fwd(pre, ocam, scene.sh_degree, scene.sh_degree)["radii"]
     noise = param_grad_noise(orc, pre, ocam, scene.sh_degree, scene.sh_degree, radii, det["grads16"],
                              det["grads16_abs"])
-    post_adam_close(D.GROUPS, [got[k] for k in D.GROUPS], params, got_m, m6, noise, D.LR_INIT)
+    post_adam_close(D.GROUPS, [got[k] for k in D.GROUPS], params, got_m, m6, noise, D.LR_INIT, label=scene.name)
 
 
 def test_densify_cycle_bitexact(orc, eng):
