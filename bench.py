@@ -164,12 +164,14 @@ def gpu_train(workload: int, steps: int, warmup: int, render_frames: int, counte
     E.sync()
     for k in range(warmup):
         D.train_step(ds, cams[k % len(cams)], gts[k % len(cams)])
+    redos = E.log_pool_stats()["redos"]
     ms_per_step, losses, isect = _timed_steps(E, lambda ci: D.train_step(ds, cams[ci], gts[ci]), warmup, steps,
                                               len(cams))
+    pool = log_pool(E, redos)
     stage_ms = _stage_breakdown(E, lambda ci: D.train_step(ds, cams[ci], gts[ci]), warmup + steps,
                                 min(steps, 10), len(cams))
     out = dict(scene=scene, ds=ds, cams=cams, ms_per_step=ms_per_step, losses=losses,
-               isect=float(np.mean(isect)), stage_ms=stage_ms, blend_log_mb=blend_log_mb(E))
+               isect=float(np.mean(isect)), stage_ms=stage_ms, log_pool=pool)
     if counters:
         # two untimed steps with the raster work counters on
         E.enable_timing(False, pairs=True)
@@ -185,11 +187,15 @@ def gpu_train(workload: int, steps: int, warmup: int, render_frames: int, counte
     return out
 
 
-def blend_log_mb(E) -> float:
-    """Device memory the blend-log pool holds after the timed steps: its
-    chunks of 64 16-byte entries and 64 checkpoint floats, in MiB."""
-    _, n = E.last_ptr("blend_log")  # 4 u32 per entry
-    return round(n * 4 * 1.25 / 2**20, 1)
+def log_pool(E, redos_before: int) -> dict:
+    """The blend-log pool after the timed steps: the device memory its
+    buffers hold in MiB (chunks of 64 16-byte entries and 64 checkpoint
+    floats, chunk tables, counts), the last frame's pool and the chunks its
+    step claimed, the worst case, and the overflowed (redone) steps among
+    the timed ones."""
+    st = E.log_pool_stats()
+    return {"device_mb": round(st["bytes"] / 2**20, 1), "chunks": st["chunks"], "claimed_last_step": st["taken"],
+            "worst_case_chunks": st["worst"], "redone_steps": st["redos"] - redos_before}
 
 
 def gpu_shard(scene, ds, bands: int, steps: int, warmup: int) -> dict:
@@ -753,7 +759,7 @@ def main() -> int:
         r = gpu_train(args.profile_workload, args.steps, args.warmup, args.render_frames, counters=False)
         print(json.dumps({"workload": r["scene"].name, "ms_per_step": round(r["ms_per_step"], 3),
                           "render_ms": round(r["render_ms"], 3), "intersections_mean": int(r["isect"]),
-                          "blend_log_mb": r["blend_log_mb"],
+                          "blend_log_pool": r["log_pool"],
                           "stage_ms": {k: round(v, 4) for k, v in r["stage_ms"].items()}}))
         return 0
     # ---- headline: C3 ----
@@ -794,7 +800,7 @@ def main() -> int:
         "config": {"workload": scene.name, "splats": N, "width": W, "height": H, "sh_degree": scene.sh_degree,
                    "tiles": T, "intersections_mean": int(I), "cameras": len(h["cams"]),
                    "device": E.device_name()},
-        "blend_log_mb": h["blend_log_mb"],
+        "blend_log_pool": h["log_pool"],
         "render_fps": round(1000.0 / h["render_ms"], 2),
         "render_ms": round(h["render_ms"], 3),
         "render_fps_to_buffer": round(1000.0 / buf_ms, 2) if buf_ms else None,
@@ -824,6 +830,7 @@ def main() -> int:
                             "train_steps_per_s": round(1000.0 / r["ms_per_step"], 3),
                             "ms_per_step": round(r["ms_per_step"], 3),
                             "render_fps": round(1000.0 / r["render_ms"], 2),
+                            "blend_log_pool": r["log_pool"],
                             "kernels": kernel_table(r["stage_ms"], sc.n, int(r["isect"]), Pn, Tn, sc.name)}
             log(f"{sc.name}: {r['ms_per_step']:.3f} ms/step, render {r['render_ms']:.3f} ms")
             del r

@@ -360,6 +360,16 @@ int msplat_hip_set_deep_tile_len(int len);
  * Drops the grown size; chunks <= 0 restores the estimate.  No counterpart
  * in the reference. */
 int msplat_hip_set_log_pool_chunks(int chunks);
+/* Blend-log pool counters: out[0] = chunks in the current frame's pool,
+ * out[1] = chunks the last forward that logged claimed (0 once the log is
+ * stale), out[2] = overflowed logs (steps and replays redone) since init,
+ * out[3] = the most chunks the frame's logs could take, out[4] = device
+ * bytes the pool's buffers hold (chunks, checkpoints, chunk tables,
+ * counts).  A frame's pool holds 1.25 times the largest share of a static
+ * estimate (one chunk per 96 intersections plus one per wave) that a log
+ * claimed so far, or more after an overflow.  Waits for the engine stream.
+ * No counterpart in the reference. */
+int msplat_hip_log_pool_stats(int64_t out[5]);
 
 /* ---- 3DGS mode ------------------------------------------------------------
  * 3D Gaussians (scales [N,3], log) projected with the reference's EWA

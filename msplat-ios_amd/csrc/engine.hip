@@ -63,6 +63,7 @@ struct Engine {
     int device = 0;
     hipStream_t stream = nullptr;
     int *pinned_i = nullptr;     // small pinned readback area
+    int *pinned_ctr = nullptr;   // the blend-log pool's counters
     double *pinned_d = nullptr;
     // two pinned chunks of kD2HChunk bytes for large downloads (RGBA8
     // frames) and the events of their DMAs
@@ -121,6 +122,10 @@ struct Engine {
     int64_t log_cap = 0;   // the size overflows grew the pool to
     int64_t log_used = 0;  // chunks of the current frame's pool
     int64_t log_init = 0;  // estimate override in chunks (0: from the frame)
+    int64_t log_redos = 0; // overflowed logs since init
+    int64_t log_demand = 0;  // chunks the last fitting log claimed
+    double log_fill = 0.0;   // the largest demand / static estimate seen
+    msr::BlendLog log_desc{};  // the current frame's pool layout
     hipStream_t deep_stream = nullptr;  // default priority, non-blocking
     hipEvent_t deep_fork = nullptr, deep_join = nullptr;
     hipEvent_t ev[ST_COUNT + 1] = {};
@@ -204,6 +209,7 @@ int init_locked() {
     }
     HIPC(hipStreamCreateWithFlags(&g_eng.stream, hipStreamNonBlocking));
     HIPC(hipHostMalloc((void **)&g_eng.pinned_i, 64 * sizeof(int), hipHostMallocDefault));
+    HIPC(hipHostMalloc((void **)&g_eng.pinned_ctr, 264 * sizeof(int), hipHostMallocDefault));
     HIPC(hipHostMalloc((void **)&g_eng.pinned_d, 16 * sizeof(double), hipHostMallocDefault));
     HIPC(hipHostMalloc((void **)&g_eng.stage, 2 * kD2HChunk, hipHostMallocDefault));
     for (auto &e : g_eng.stage_ev) HIPC(hipEventCreateWithFlags(&e, hipEventDisableTiming));
@@ -317,6 +323,10 @@ int deep_tiles(mskern::DeepTiles &deep) {
 // The most chunks the frame's logs can take: every wave's ceil(len / 64).
 int64_t log_worst_chunks(const Engine &E) { return 4 * (int64_t)E.num_isect / 64 + 4 * (int64_t)E.tiles_x * E.tiles_y; }
 int log_subpools(int64_t tiles) { return (int)std::min<int64_t>(256, std::max<int64_t>(1, tiles / 64)); }
+// One chunk per 96 intersections plus a partial chunk per wave.
+int64_t log_static_estimate(const Engine &E) {
+    return std::max<int64_t>(1024, (int64_t)E.num_isect / 96 + 4 * (int64_t)E.tiles_x * E.tiles_y);
+}
 // The largest pool: a spill region of the worst case (no log can overflow
 // it, whatever the sub-pools' shares) beside sub-pools of three quarters
 // of it.
@@ -328,12 +338,13 @@ int64_t log_max_chunks(const Engine &E) {
 // The frame's blend-log pool of `cap` chunks: a sub-pool per 64 tiles (at
 // most 256; wave w of tile t claims from sub-pool (4t + w) mod count) takes
 // three quarters, the spill region the rest, and the largest pool a spill
-// region of the worst case.  cap is the larger of the frame's estimate (one
-// chunk per 96 intersections plus a partial chunk per wave, about a sixth
-// of the worst case; the training step at 3M splats fills ~70% of it) and
+// region of the worst case.  cap is the larger of the frame's estimate and
 // the size earlier overflows grew the pool to (log_cap), at most the
-// largest pool; a step whose log overflows is redone after the pool grows
-// (grow_log_pool).
+// largest pool.  The estimate is a static one (about a sixth of the worst
+// case; the training step at 3M splats claims 45-62% of it) until a log
+// fitted, then that scaled by 1.25 times the largest ratio of claimed chunks
+// to it seen so far (log_fill).  A step whose log overflows is redone
+// after the pool grows (grow_log_pool).
 int blend_log_desc(msr::BlendLog &L) {
     Engine &E = g_eng;
     const int64_t T = (int64_t)E.tiles_x * E.tiles_y;
@@ -342,7 +353,10 @@ int blend_log_desc(msr::BlendLog &L) {
         set_err("blend log: too many intersections for the pool's chunk indices");
         return MSPLAT_E_ARG;
     }
-    const int64_t estimate = E.log_init ? E.log_init : std::max<int64_t>(1024, (int64_t)E.num_isect / 96 + 4 * T);
+    const int64_t base = log_static_estimate(E);
+    const int64_t estimate = E.log_init          ? E.log_init
+                             : E.log_fill > 0.0 ? std::max<int64_t>(1024, (int64_t)std::ceil(1.25 * E.log_fill * (double)base))
+                                                : base;
     const int64_t cap = std::min(std::max(E.log_cap, estimate), most);
     E.log_used = cap;
     CHECK(ensure(E.blend_log, (size_t)cap * 64 * mskern::kBlendLogEntryBytes));
@@ -361,7 +375,25 @@ int blend_log_desc(msr::BlendLog &L) {
     L.nsub = nsub;
     L.sub_cap = (int)((cap - spill) / nsub);
     L.spill_cap = (int)spill;
+    E.log_desc = L;
     return MSPLAT_OK;
+}
+
+// Queues the copy of the pool's counters after a logging forward; once the
+// stream has synchronised, log_account records the frame's demand (each
+// claim is counted in its sub-pool's counter, also when the spill region
+// served it) unless the log overflowed.
+int log_readback(const msr::BlendLog &L, hipStream_t s) {
+    HIPC(hipMemcpyAsync(g_eng.pinned_ctr, L.counters, (size_t)(L.nsub + 1) * 4, hipMemcpyDeviceToHost, s));
+    return MSPLAT_OK;
+}
+void log_account(const msr::BlendLog &L, bool overflow) {
+    Engine &E = g_eng;
+    if (overflow) return;
+    int64_t demand = 0;
+    for (int i = 0; i < L.nsub; ++i) demand += g_eng.pinned_ctr[i];
+    E.log_demand = demand;
+    E.log_fill = std::max(E.log_fill, (double)demand / (double)log_static_estimate(E));
 }
 
 // Zeroes the pool's counters and overflow flag before a forward that logs.
@@ -371,12 +403,13 @@ int reset_log_pool(const msr::BlendLog &L) {
     return MSPLAT_OK;
 }
 
-// After an overflowed log: a pool twice as large as the one that
+// After an overflowed log: a pool 1.5 times as large as the one that
 // overflowed, at most the largest (in which no log overflows).
 void grow_log_pool() {
     Engine &E = g_eng;
-    E.log_cap = std::min(log_max_chunks(E), std::max<int64_t>(2 * E.log_used, 64));
+    E.log_cap = std::min(log_max_chunks(E), std::max<int64_t>(E.log_used + E.log_used / 2, 64));
     E.log_valid = false;
+    ++E.log_redos;
 }
 
 int raster_fwd_locked(bool log, bool full) {
@@ -429,7 +462,9 @@ int log_forward_checked(bool full) {
     for (;;) {
         CHECK(raster_fwd_locked(true, full));
         HIPC(hipMemcpyAsync(E.pinned_i + 15, P<int>(E.stats) + 15, sizeof(int), hipMemcpyDeviceToHost, E.stream));
+        CHECK(log_readback(E.log_desc, E.stream));
         HIPC(hipStreamSynchronize(E.stream));
+        log_account(E.log_desc, E.pinned_i[15] != 0);
         if (E.pinned_i[15] == 0) return MSPLAT_OK;
         grow_log_pool();
     }
@@ -727,6 +762,8 @@ void msplat_hip_cleanup(void) {
     E.n_deep = 0;
     E.log_cap = 0;
     E.log_used = 0;
+    E.log_fill = 0.0;
+    E.log_desc = msr::BlendLog{};
     E.n = 0;
     E.num_isect = 0;
     E.have_grads = false;
@@ -1075,9 +1112,11 @@ static int train_step_once(const MsplatCamera *cam, const MsplatGaussians *g, co
     E.g16_moments = t_moments;
     stage_mark(ST_COUNT);
     HIPC(hipMemcpyAsync(E.pinned_i + 15, blog.overflow, sizeof(int), hipMemcpyDeviceToHost, s));
+    CHECK(log_readback(blog, s));
     HIPC(hipGetLastError());
     HIPC(hipStreamSynchronize(s));
     *log_overflow = E.pinned_i[15] != 0;
+    log_account(blog, *log_overflow);
     if (*log_overflow) {
         E.have_grads = E.raster_grads = false;
         return MSPLAT_OK;
@@ -1177,9 +1216,11 @@ static int train_step3d_once(const MsplatCamera *cam, const MsplatGaussians *g, 
     E.g16_moments = true;
     stage_mark(ST_COUNT);
     HIPC(hipMemcpyAsync(E.pinned_i + 15, blog.overflow, sizeof(int), hipMemcpyDeviceToHost, s));
+    CHECK(log_readback(blog, s));
     HIPC(hipGetLastError());
     HIPC(hipStreamSynchronize(s));
     *log_overflow = E.pinned_i[15] != 0;
+    log_account(blog, *log_overflow);
     if (*log_overflow) {
         E.have_grads = E.raster_grads = false;
         return MSPLAT_OK;
@@ -1551,6 +1592,27 @@ int msplat_hip_last_raster_counts(int64_t out[5]) {
     if (!out) return MSPLAT_E_ARG;
     for (int i = 0; i < 5; ++i) out[i] = g_eng.pairs[i];
     return MSPLAT_OK;
+}
+
+int msplat_hip_log_pool_stats(int64_t out[5]) {
+    API_BEGIN
+    if (!out) return MSPLAT_E_ARG;
+    ENSURE_INIT();
+    Engine &E = g_eng;
+    const msr::BlendLog &L = E.log_desc;
+    out[0] = E.log_used;
+    out[1] = 0;
+    out[2] = E.log_redos;
+    out[3] = E.n ? log_worst_chunks(E) : 0;
+    out[4] = (int64_t)(E.blend_log.cap + E.t_ckpt.cap + E.log_table.cap + E.wave_cnt.cap + E.log_ctr.cap);
+    if (E.log_valid && L.counters) {
+        std::vector<int> c((size_t)L.nsub + 1);
+        HIPC(hipMemcpyAsync(c.data(), L.counters, c.size() * 4, hipMemcpyDeviceToHost, E.stream));
+        HIPC(hipStreamSynchronize(E.stream));
+        for (int i = 0; i < L.nsub; ++i) out[1] += c[i];
+    }
+    return MSPLAT_OK;
+    API_END
 }
 
 int msplat_hip_check_fast_rcp(int efield_lo, int efield_hi, int64_t *mismatches) {

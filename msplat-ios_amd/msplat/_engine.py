@@ -73,7 +73,8 @@ EXPORTS = [
     "msplat_hip_loss_fwd_bwd_noalloc",
     "msplat_hip_raster_bwd", "msplat_hip_project_bwd", "msplat_hip_project_bwd_adam", "msplat_hip_last", "msplat_hip_enable_timing",
     "msplat_hip_stage_times", "msplat_hip_last_pairs_evaluated", "msplat_hip_last_raster_counts",
-    "msplat_hip_check_fast_rcp", "msplat_hip_set_wide_keys", "msplat_hip_set_deep_tile_len", "msplat_hip_set_log_pool_chunks",
+    "msplat_hip_check_fast_rcp", "msplat_hip_set_wide_keys", "msplat_hip_set_deep_tile_len",
+    "msplat_hip_set_log_pool_chunks", "msplat_hip_log_pool_stats",
     "msplat_hip_tsdf_integrate",
     "msplat_hip_marching_cubes", "msplat_hip_mc_table", "msplat_hip_unproject_depth", "msplat_hip_render_3dgs",
     "msplat_hip_train_step_3dgs", "msplat_hip_densify_3dgs",
@@ -131,6 +132,7 @@ def lib() -> C.CDLL:
         "msplat_hip_set_wide_keys": (I, [I]),
         "msplat_hip_set_deep_tile_len": (I, [I]),
         "msplat_hip_set_log_pool_chunks": (I, [I]),
+        "msplat_hip_log_pool_stats": (I, [P]),
         "msplat_hip_densify_3dgs": (I, [I, I, F, F, F, I, F, F, F, I, P, P, P, F, P * 6, I, P * 6, P * 6, P,
                                         C.POINTER(I)]),
         "msplat_hip_render_3dgs": (I, [C.POINTER(MsplatCamera), C.POINTER(MsplatGaussians), P, C.POINTER(I64)]),
@@ -284,6 +286,16 @@ def raster_counts() -> dict:
     check(lib().msplat_hip_last_raster_counts(C.cast(out, C.c_void_p)))
     return {"pairs_evaluated": int(out[0]), "log_entries": int(out[1]), "pairs_blended": int(out[2]),
             "visits": int(out[3]), "visit_slots": int(out[4])}
+
+
+def log_pool_stats() -> dict:
+    """The blend-log pool: chunks of the frame's pool, chunks the last
+    logging forward claimed, overflowed logs since init, worst-case chunks
+    of the frame, device bytes its buffers hold."""
+    out = (C.c_int64 * 5)()
+    check(lib().msplat_hip_log_pool_stats(C.cast(out, C.c_void_p)))
+    return {"chunks": int(out[0]), "taken": int(out[1]), "redos": int(out[2]), "worst": int(out[3]),
+            "bytes": int(out[4])}
 
 
 # ---- mesh extraction -------------------------------------------------------

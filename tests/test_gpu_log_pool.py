@@ -99,17 +99,20 @@ def test_overflowed_pool_train_step_3dgs(orc, eng):
 
 
 def test_pool_keeps_grown_size_across_frames(eng):
-    """A pool grown by an overflow keeps its size for later frames (whose
-    own estimate may be smaller), so a training run does not overflow and
-    redo again on every camera."""
+    """A pool grown by overflows keeps its size for later frames (whose own
+    estimate may be smaller): after one pass over the cameras a training
+    run does not overflow and redo again."""
     scene = S.make_scene(2, n=20_000, width=256, height=160, num_cameras=3)
     ds = D.DeviceScene(scene)
     cams = [ds.camera(c) for c in scene.cameras]
     gts = [D.render_to_device(ds, c) for c in cams]
     with pool_chunks(8):
-        D.train_step(ds, cams[0], gts[0])
-        grown = _pool_chunks_used()
-        for c, g in zip(cams[1:] + cams[:1], gts[1:] + gts[:1]):
+        r0 = E.log_pool_stats()["redos"]
+        for c, g in zip(cams, gts):
             D.train_step(ds, c, g)
-            assert _pool_chunks_used() >= grown
-    assert grown > 8
+        st = E.log_pool_stats()
+        assert st["redos"] > r0 and st["chunks"] > 8
+        assert 0 < st["taken"] <= st["chunks"] <= st["worst"] * 2
+        for c, g in zip(cams + cams, gts + gts):
+            D.train_step(ds, c, g)
+            assert E.log_pool_stats()["redos"] == st["redos"]
