@@ -110,6 +110,7 @@ struct Engine {
     // timing
     bool timing = false;       // HIP events per stage
     bool count_pairs = false;  // raster pair counter
+    bool defer_deep_log = false;  // set by the training step around its forward
     bool wide_keys = false;    // binning test hook: the wide key layout at any N
     // tiles whose list holds at least deep_len entries are rendered pixel by
     // pixel (mskern::DeepTiles); n_deep of them in the current frame
@@ -117,7 +118,7 @@ struct Engine {
     DevBuf deep_list, deep_pos, deep_tb, deep_cnt;
     // blend-log pool (msr::BlendLog): blend_log / t_ckpt hold log_used chunks
     // of 64 entries / checkpoints, log_table the per-wave chunk tables,
-    // log_ctr the sub-pool and spill counters; the overflow flag is stats[15]
+    // log_ctr the sub-pool and spill counters and the overflow flag
     DevBuf log_table, log_ctr;
     int64_t log_cap = 0;   // the size overflows grew the pool to
     int64_t log_used = 0;  // chunks of the current frame's pool
@@ -344,8 +345,9 @@ int64_t log_max_chunks(const Engine &E) {
 // case; the training step at 3M splats claims 45-62% of it) until a log
 // fitted, then that scaled by 1.25 times the largest ratio of claimed chunks
 // to it seen so far (log_fill).  A step whose log overflows is redone
-// after the pool grows (grow_log_pool).
-int blend_log_desc(msr::BlendLog &L) {
+// after the pool grows (grow_log_pool).  Planned by each forward that logs;
+// the backward reads the log through the plan kept in log_desc.
+int plan_log_pool(msr::BlendLog &L) {
     Engine &E = g_eng;
     const int64_t T = (int64_t)E.tiles_x * E.tiles_y;
     const int64_t worst = log_worst_chunks(E), most = log_max_chunks(E);
@@ -365,13 +367,13 @@ int blend_log_desc(msr::BlendLog &L) {
     CHECK(ensure(E.wave_cnt, (size_t)4 * T * 4));
     const int nsub = log_subpools(T);
     const int64_t spill = cap == most ? worst : cap / 4;
-    CHECK(ensure(E.log_ctr, (size_t)(nsub + 1) * 4));
+    CHECK(ensure(E.log_ctr, (size_t)(nsub + 2) * 4));
     L.ent = P<uint4>(E.blend_log);
     L.ckpt = P<float>(E.t_ckpt);
     L.table = P<int>(E.log_table);
     L.wave_cnt = P<int>(E.wave_cnt);
     L.counters = P<int>(E.log_ctr);
-    L.overflow = P<int>(E.stats) + 15;
+    L.overflow = P<int>(E.log_ctr) + nsub + 1;
     L.nsub = nsub;
     L.sub_cap = (int)((cap - spill) / nsub);
     L.spill_cap = (int)spill;
@@ -379,27 +381,27 @@ int blend_log_desc(msr::BlendLog &L) {
     return MSPLAT_OK;
 }
 
-// Queues the copy of the pool's counters after a logging forward; once the
-// stream has synchronised, log_account records the frame's demand (each
-// claim is counted in its sub-pool's counter, also when the spill region
-// served it) unless the log overflowed.
+// Queues the copy of the pool's counters and overflow flag after a logging
+// forward; once the stream has synchronised, log_account returns whether
+// the log overflowed and, if not, records the frame's demand (each claim is
+// counted in its sub-pool's counter, also when the spill region served it).
 int log_readback(const msr::BlendLog &L, hipStream_t s) {
-    HIPC(hipMemcpyAsync(g_eng.pinned_ctr, L.counters, (size_t)(L.nsub + 1) * 4, hipMemcpyDeviceToHost, s));
+    HIPC(hipMemcpyAsync(g_eng.pinned_ctr, L.counters, (size_t)(L.nsub + 2) * 4, hipMemcpyDeviceToHost, s));
     return MSPLAT_OK;
 }
-void log_account(const msr::BlendLog &L, bool overflow) {
+bool log_account(const msr::BlendLog &L) {
     Engine &E = g_eng;
-    if (overflow) return;
+    if (g_eng.pinned_ctr[L.nsub + 1] != 0) return true;
     int64_t demand = 0;
     for (int i = 0; i < L.nsub; ++i) demand += g_eng.pinned_ctr[i];
     E.log_demand = demand;
     E.log_fill = std::max(E.log_fill, (double)demand / (double)log_static_estimate(E));
+    return false;
 }
 
 // Zeroes the pool's counters and overflow flag before a forward that logs.
 int reset_log_pool(const msr::BlendLog &L) {
-    HIPC(hipMemsetAsync(L.counters, 0, (size_t)(L.nsub + 1) * 4, g_eng.stream));
-    HIPC(hipMemsetAsync(L.overflow, 0, sizeof(int), g_eng.stream));
+    HIPC(hipMemsetAsync(L.counters, 0, (size_t)(L.nsub + 2) * 4, g_eng.stream));
     return MSPLAT_OK;
 }
 
@@ -429,9 +431,10 @@ int raster_fwd_locked(bool log, bool full) {
         }
     }
     if (log) {
-        CHECK(blend_log_desc(blog));
+        CHECK(plan_log_pool(blog));
         CHECK(reset_log_pool(blog));
     }
+    deep.defer_log = log && E.defer_deep_log;
     if (E.gs3d) {
         if (full) {
             set_err("the 3DGS mode produces the image and the transmittance only");
@@ -461,11 +464,9 @@ int log_forward_checked(bool full) {
     Engine &E = g_eng;
     for (;;) {
         CHECK(raster_fwd_locked(true, full));
-        HIPC(hipMemcpyAsync(E.pinned_i + 15, P<int>(E.stats) + 15, sizeof(int), hipMemcpyDeviceToHost, E.stream));
         CHECK(log_readback(E.log_desc, E.stream));
         HIPC(hipStreamSynchronize(E.stream));
-        log_account(E.log_desc, E.pinned_i[15] != 0);
-        if (E.pinned_i[15] == 0) return MSPLAT_OK;
+        if (!log_account(E.log_desc)) return MSPLAT_OK;
         grow_log_pool();
     }
 }
@@ -564,18 +565,24 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
         CHECK(ensure(E.chunk_base, (size_t)NS * 4));
         CHECK(ensure(E.chunk_counts, (size_t)mskern::big_chunk_ints(S_total, NS) * 4));
     }
+    // a tile's list is at most its super-tile's: no deep tile below that
+    const bool scan_deep = !gs3d && super_max >= E.deep_len;
+    mskern::DeepScan dscan;
+    if (scan_deep) {
+        CHECK(ensure(E.deep_list, (size_t)T * 4));
+        dscan.len = E.deep_len;
+        dscan.list = P<int>(E.deep_list);
+        dscan.count = P<int>(E.stats) + 14;
+        dscan.host_count = E.pinned_i + 14;
+    }
     mskern::launch_bin_tiles(s, N, cam->tiles_x, cam->tiles_y, P<int>(E.radii), P<uint32_t>(E.rect),
                              P<float>(E.depths), P<int>(E.super_offsets), P<int>(E.super_cm), super_max,
                              P<uint64_t>(E.keys), P<uint64_t>(E.keys_tmp), P<int>(E.big_list), P<int>(E.stats) + 4,
                              P<int>(E.huge_list), P<int>(E.stats) + 12, P<int>(E.chunk_base), P<int>(E.chunk_counts),
                              P<int>(E.counts), P<int>(E.offsets), P<int>(E.stats), P<int>(E.scan_tmp), P<int>(E.ids),
-                             E.wide_keys);
-    // a tile's list is at most its super-tile's: no deep tile below that
+                             E.wide_keys, scan_deep ? &dscan : nullptr);
     E.n_deep = 0;
-    if (!gs3d && super_max >= E.deep_len) {
-        CHECK(ensure(E.deep_list, (size_t)T * 4));
-        mskern::launch_deep_tiles(s, T, P<int>(E.offsets), E.deep_len, P<int>(E.deep_list), P<int>(E.stats) + 14);
-        HIPC(hipMemcpyAsync(E.pinned_i + 14, P<int>(E.stats) + 14, sizeof(int), hipMemcpyDeviceToHost, s));
+    if (scan_deep) {
         HIPC(hipStreamSynchronize(s));
         E.n_deep = E.pinned_i[14];
     }
@@ -1069,7 +1076,12 @@ static int train_step_once(const MsplatCamera *cam, const MsplatGaussians *g, co
     }
     Engine &E = g_eng;
     hipStream_t s = E.stream;
-    CHECK(forward_locked(cam, g, bg, nisect, true, lambda_dist != 0.f));
+    // the deep tiles' log rebuild runs beside the loss (the raster
+    // backward's deep part follows it on the deep-tile stream)
+    E.defer_deep_log = true;
+    const int fr = forward_locked(cam, g, bg, nisect, true, lambda_dist != 0.f);
+    E.defer_deep_log = false;
+    CHECK(fr);
     const int N = g->num_points, W = cam->width, H = cam->height;
     const size_t Pn = (size_t)W * H;
     stage_mark(ST_LOSS);
@@ -1084,8 +1096,9 @@ static int train_step_once(const MsplatCamera *cam, const MsplatGaussians *g, co
     const float ddist_uniform = lambda_dist * (inv_np * 3.0f);
     mskern::DeepTiles deep;
     CHECK(deep_tiles(deep));
-    msr::BlendLog blog{};
-    CHECK(blend_log_desc(blog));
+    // the layout the logging forward planned (a new plan could reallocate
+    // the pool under the log)
+    const msr::BlendLog blog = E.log_desc;
     const bool t_moments = mskern::launch_raster_bwd(s, W, H, cam->tiles_x, cam->tiles_y, P<int>(E.offsets), blog,
                               P<float>(E.rec), bg, P<float>(E.final_Ts),
                               P<int>(E.final_idx), P<float>(E.dL_dimg), nullptr, nullptr, nullptr, nullptr, nullptr,
@@ -1111,12 +1124,10 @@ static int train_step_once(const MsplatCamera *cam, const MsplatGaussians *g, co
     E.raster_grads = true;
     E.g16_moments = t_moments;
     stage_mark(ST_COUNT);
-    HIPC(hipMemcpyAsync(E.pinned_i + 15, blog.overflow, sizeof(int), hipMemcpyDeviceToHost, s));
     CHECK(log_readback(blog, s));
     HIPC(hipGetLastError());
     HIPC(hipStreamSynchronize(s));
-    *log_overflow = E.pinned_i[15] != 0;
-    log_account(blog, *log_overflow);
+    *log_overflow = log_account(blog);
     if (*log_overflow) {
         E.have_grads = E.raster_grads = false;
         return MSPLAT_OK;
@@ -1190,8 +1201,9 @@ static int train_step3d_once(const MsplatCamera *cam, const MsplatGaussians *g, 
     stage_mark(ST_RASTER_BWD);
     CHECK(ensure(E.grads16, (size_t)N * 64));
     HIPC(hipMemsetAsync(E.grads16.p, 0, (size_t)N * 64, s));
-    msr::BlendLog blog{};
-    CHECK(blend_log_desc(blog));
+    // the layout the logging forward planned (a new plan could reallocate
+    // the pool under the log)
+    const msr::BlendLog blog = E.log_desc;
     mskern::launch_raster3d_bwd(s, W, H, cam->tiles_x, cam->tiles_y, P<int>(E.offsets), blog, P<float>(E.rec), bg,
                                 P<float>(E.final_Ts), P<float>(E.dL_dimg), P<float>(E.grads16));
     stage_mark(ST_PROJECT_BWD);
@@ -1215,12 +1227,10 @@ static int train_step3d_once(const MsplatCamera *cam, const MsplatGaussians *g, 
     E.raster_grads = true;
     E.g16_moments = true;
     stage_mark(ST_COUNT);
-    HIPC(hipMemcpyAsync(E.pinned_i + 15, blog.overflow, sizeof(int), hipMemcpyDeviceToHost, s));
     CHECK(log_readback(blog, s));
     HIPC(hipGetLastError());
     HIPC(hipStreamSynchronize(s));
-    *log_overflow = E.pinned_i[15] != 0;
-    log_account(blog, *log_overflow);
+    *log_overflow = log_account(blog);
     if (*log_overflow) {
         E.have_grads = E.raster_grads = false;
         return MSPLAT_OK;
@@ -1481,8 +1491,9 @@ int msplat_hip_raster_bwd(const float *dL_dimg, const float *dL_ddepth, const fl
     if (!E.log_valid || (need_full && !E.full_valid)) CHECK(log_forward_checked(need_full || E.full_valid));
     mskern::DeepTiles deep;
     CHECK(deep_tiles(deep));
-    msr::BlendLog blog{};
-    CHECK(blend_log_desc(blog));
+    // the layout the logging forward planned (a new plan could reallocate
+    // the pool under the log)
+    const msr::BlendLog blog = E.log_desc;
     const bool t_moments = mskern::launch_raster_bwd(
         E.stream, E.W, E.H, E.tiles_x, E.tiles_y, P<int>(E.offsets), blog, P<float>(E.rec), E.bg,
         P<float>(E.final_Ts), P<int>(E.final_idx), dL_dimg, dL_ddepth, dL_dalpha, dL_dnormal, dL_dmedian, dL_ddist,

@@ -759,7 +759,8 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
                       const float *depths, const int *super_offsets, const int *super_cm, int super_max,
                       uint64_t *super_keys, uint64_t *super_keys_tmp, int *big_list, int *super_stats,
                       int *huge_list, int *huge_stats, int *chunk_base, int *chunk_counts, int *tile_counts,
-                      int *tile_offsets, int *tile_stats, int *tile_temp, int *ids, bool force_wide_keys) {
+                      int *tile_offsets, int *tile_stats, int *tile_temp, int *ids, bool force_wide_keys,
+                      const DeepScan *deep) {
     const int sxn = (tiles_x + kSuper - 1) / kSuper, syn = (tiles_y + kSuper - 1) / kSuper, NS = sxn * syn;
     const int T = tiles_x * tiles_y;
     auto *k = reinterpret_cast<unsigned long long *>(super_keys);
@@ -796,6 +797,10 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
                            tiles_x, tiles_y, sxn, super_offsets, huge_list, huge_stats, chunk_base, src, r2,
                            chunk_counts, tile_counts);
     launch_scan_counts(s, T, tile_counts, tile_offsets, nullptr, tile_stats, tile_temp);
+    if (deep) {
+        launch_deep_tiles(s, T, tile_offsets, deep->len, deep->list, deep->count);
+        (void)hipMemcpyAsync(deep->host_count, deep->count, sizeof(int), hipMemcpyDeviceToHost, s);
+    }
     hipLaunchKernelGGL(packed ? k_emit_tiles<true> : k_emit_tiles<false>, dim3(NS), dim3(256), 0, s, tiles_x, tiles_y,
                        sxn, super_offsets, k, src, r2, tile_offsets, ids, huge_th);
     if (big)

@@ -998,10 +998,12 @@ void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
             full_outputs ? launch_deep(k_raster_deep<true, true>) : launch_deep(k_raster_deep<true, false>);
         else
             full_outputs ? launch_deep(k_raster_deep<false, true>) : launch_deep(k_raster_deep<false, false>);
+        const bool defer = blog && deep.defer_log;
+        if (defer) (void)hipEventRecord(deep.join, sd);
         if (blog)
             hipLaunchKernelGGL(k_deep_log, dim3(deep.n * 4), dim3(kLogThreads), 0, sd, W, H, tiles_x, deep.n, deep.list,
                                offsets, ids, deep.pos, deep.tb, deep.cnt, final_Ts, lg);
-        (void)hipEventRecord(deep.join, sd);
+        if (!defer) (void)hipEventRecord(deep.join, sd);
     }
     auto launch = [&](auto kern) {
         hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, ids,
@@ -1053,7 +1055,8 @@ bool launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
     };
     if (deep.n > 0) {
         // the deep tiles' long log replays start at once, on their own
-        // stream, beside the rest
+        // stream, beside the rest (after the deep tiles' log rebuild, if
+        // the forward left it running there)
         (void)hipEventRecord(deep.fork, s);
         (void)hipStreamWaitEvent(deep.stream, deep.fork, 0);
         launch(deep.stream, deep.n, deep.list, 0);

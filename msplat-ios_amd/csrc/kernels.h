@@ -66,11 +66,19 @@ constexpr int kBinMaxBlocks = 256;
 // super_keys_tmp (the size of super_keys); when super_max > kSuperHugeList
 // huge_list[NS], huge_stats[2] (zero on entry), chunk_base[NS] and
 // chunk_counts[big_chunk_ints(total, NS)].
+// The deep-tile scan launch_bin_tiles queues once the tile offsets exist
+// (before the emission kernels): the tiles with at least `len` entries into
+// `list`, their number into *count, copied to *host_count.
+struct DeepScan {
+    int len = 0;
+    int *list = nullptr, *count = nullptr, *host_count = nullptr;
+};
 void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
                       const float *depths, const int *super_offsets, const int *super_cm, int super_max,
                       uint64_t *super_keys, uint64_t *super_keys_tmp, int *big_list, int *super_stats,
                       int *huge_list, int *huge_stats, int *chunk_base, int *chunk_counts, int *tile_counts,
-                      int *tile_offsets, int *tile_stats, int *tile_temp, int *ids, bool force_wide_keys);
+                      int *tile_offsets, int *tile_stats, int *tile_temp, int *ids, bool force_wide_keys,
+                      const DeepScan *deep = nullptr);
 constexpr int kSuperHugeList = 4 * 4096;
 // Ints of chunk_counts: 16 per 4096-key chunk of the long lists, at most
 // total / 4096 + NS chunks.
@@ -98,9 +106,14 @@ struct DeepTiles {
     float *tb = nullptr;
     int *cnt = nullptr;
     // the deep tiles run on `stream` between `fork` (recorded on the
-    // caller's stream) and `join` (waited on by the caller's stream)
+    // caller's stream) and `join` (waited on by the caller's stream); with
+    // defer_log the forward's `join` follows the deep tiles' outputs only
+    // and their blend logs (k_deep_log) are rebuilt after it on `stream`,
+    // where the raster backward's deep part follows them (the caller's
+    // stream reaches them through the backward's `join`)
     hipStream_t stream = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
+    bool defer_log = false;
 };
 void launch_deep_tiles(hipStream_t s, int T, const int *offsets, int deep_len, int *deep_list, int *count);
 int64_t deep_pixel_entries(int n_deep);
