@@ -97,6 +97,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
     LogWriter lw;
     lw.tb = LOG ? log_table_base(start, end - start, tile, wave) : 0;
     lw.sp = LOG ? log_subpool(blog, tile, wave) : 0;
+    if (LOG && end > start) lw.start(blog, lane);  // an empty list logs nothing
     int nlog = 0;  // wave-uniform
     // the current 64-entry chunk of the wave's log: lane k holds entry k,
     // and a full chunk is written with one coalesced store
@@ -174,7 +175,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7, 8))
             Tr = blend ? next_T : Tr;
             if (COUNT) blends += __builtin_popcountll(bal);
             if (LOG && bal) {
-                if ((nlog & 63) == 0) lw.begin(blog, lane);
                 const bool mine = __builtin_amdgcn_inverse_ballot_w64(1ull << (nlog & 63));
                 lg_ent.x = mine ? (unsigned)bal : lg_ent.x;
                 lg_ent.y = mine ? (unsigned)(bal >> 32) : lg_ent.y;

@@ -73,6 +73,7 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_fwd(int W, int H, int til
     LogWriter lw;
     lw.tb = LOG ? log_table_base(start, end - start, tile, wave) : 0;
     lw.sp = LOG ? log_subpool(blog, tile, wave) : 0;
+    if (LOG && end > start) lw.start(blog, lane);  // an empty list logs nothing
     int nlog = 0;
     uint4 lg_ent = make_uint4(0u, 0u, 0u, 0u);
     const char *s_bytes = reinterpret_cast<const char *>(s_rec);
@@ -109,7 +110,6 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_fwd(int W, int H, int til
             cb = __builtin_fmaf(p2.z, w, cb);
             Tr = blend ? next_T : Tr;
             if (LOG && bal) {
-                if ((nlog & 63) == 0) lw.begin(blog, lane);
                 const bool mine = __builtin_amdgcn_inverse_ballot_w64(1ull << (nlog & 63));
                 lg_ent.x = mine ? (unsigned)bal : lg_ent.x;
                 lg_ent.y = mine ? (unsigned)(bal >> 32) : lg_ent.y;
@@ -146,8 +146,16 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_fwd(int W, int H, int til
 // The sums go to reduction slots 0..4 and 8..11, so three first-stage
 // pairs of the reduction are empty and skipped (their scratch rows hold
 // zeros).
+// The log arrives as separate read-only, non-aliasing pointers (not the
+// BlendLog struct) so that the compiler can load the wave-uniform entries
+// with scalar loads beside the loop's gradient atomics.
 __global__ __launch_bounds__(kThreads) void k_raster3d_bwd(int W, int H, int tiles_x, int T,
-                                                           const int *__restrict__ offsets, BlendLog blog,
+                                                           const int *__restrict__ offsets,
+                                                           const uint4 *__restrict__ log_ent,
+                                                           const float *__restrict__ log_ckpt,
+                                                           const int *__restrict__ log_table,
+                                                           const int *__restrict__ wave_cnt,
+                                                           const int *__restrict__ log_overflow,
                                                            const float4 *__restrict__ rec,
                                                            const float *__restrict__ bgp,
                                                            const float *__restrict__ final_Ts,
@@ -155,7 +163,7 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_bwd(int W, int H, int til
                                                            float *__restrict__ grads16) {
     const int tile = xcd_strip_tile(blockIdx.x, tiles_x, T / tiles_x);
     if (tile < 0) return;
-    if (overflowed(blog)) return;  // an incomplete log: the step is redone with a larger pool
+    if (*log_overflow) return;  // an incomplete log: the step is redone with a larger pool
     constexpr int kWave = 64;
     __shared__ float4 s_r[4][3][64];
     __shared__ float s_red[4][512];
@@ -167,11 +175,11 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_bwd(int W, int H, int til
     const bool inside = pxi < W && pyi < H;
     const float px = (float)pxi, py = (float)pyi;
     const int start = offsets[tile], len = offsets[tile + 1] - start;
-    const int nlog = __builtin_amdgcn_readfirstlane(blog.wave_cnt[4 * tile + wave]);
+    const int nlog = __builtin_amdgcn_readfirstlane(wave_cnt[4 * tile + wave]);
     Red8<0, 0xE0> red8;
     red8.init(&s_red[wave][0], lane);
     red8.zero_skipped();
-    const int *__restrict__ chunk_of = blog.table + log_table_base(start, len, tile, wave);
+    const int *__restrict__ chunk_of = log_table + log_table_base(start, len, tile, wave);
     const size_t pix = inside ? (size_t)pyi * W + pxi : 0;
     float T_final = 1.f, dp0 = 0.f, dp1 = 0.f, dp2 = 0.f;
     if (inside) {
@@ -193,8 +201,8 @@ __global__ __launch_bounds__(kThreads) void k_raster3d_bwd(int W, int H, int til
         const int c0 = c * kWave;
         const int m = min(kWave, nlog - c0);
         const int cid = __builtin_amdgcn_readfirstlane(chunk_of[c]);
-        const uint4 *__restrict__ lg = blog.ent + 64 * (size_t)cid;
-        float Tr = c == nchunks - 1 ? T_final : blog.ckpt[64 * (size_t)cid + lane];
+        const uint4 *__restrict__ lg = log_ent + 64 * (size_t)cid;
+        float Tr = c == nchunks - 1 ? T_final : log_ckpt[64 * (size_t)cid + lane];
         if (lane < m) {
             const uint4 e = lg[lane];
             const float4 *r = rec + 3 * (size_t)e.w;
@@ -266,8 +274,9 @@ void launch_raster3d_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, 
     const int T = tiles_x * tiles_y;
     if (T <= 0) return;
     const int grid = xcd_strip_grid(tiles_x, tiles_y);
-    hipLaunchKernelGGL(k_raster3d_bwd, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, blog,
-                       reinterpret_cast<const float4 *>(rec), bg, final_Ts, dL_dimg, grads16);
+    hipLaunchKernelGGL(k_raster3d_bwd, dim3(grid), dim3(kThreads), 0, s, W, H, tiles_x, T, offsets, blog.ent,
+                       blog.ckpt, blog.table, blog.wave_cnt, blog.overflow, reinterpret_cast<const float4 *>(rec), bg,
+                       final_Ts, dL_dimg, grads16);
 }
 
 }  // namespace mskern

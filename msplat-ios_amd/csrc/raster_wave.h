@@ -56,22 +56,25 @@ __device__ __forceinline__ int log_resolve(const BlendLog &L, int sp, int c, int
 }
 
 // A wave's log writer: entries are staged in lane (count mod 64) of lg_ent
-// by the caller; begin() issues the sub-pool claim of a chunk's first entry
-// (its result is only waited for when the chunk is written), full() writes
-// a completed chunk and its checkpoint, finish() the partial last chunk and
-// the count.  Wave-uniform control flow.
+// by the caller.  Each chunk is claimed one chunk ahead: start() (before the
+// visits) issues the sub-pool claim of the first, full() writes a completed
+// chunk and its checkpoint into the claimed chunk and issues the claim of
+// the next, and finish() writes the partial last chunk and the count.  A
+// claim's result is only waited for when its chunk is written, 64 entries
+// later, and the visit loop itself carries no claim code.  A wave whose log
+// ends on a chunk boundary (or is empty) leaves its last claim unused: at
+// most one chunk per wave, within the worst case of ceil(len / 64) chunks
+// per wave.  cid is written and read in lane 0 only.  Wave-uniform control
+// flow.
 struct LogWriter {
     size_t tb;
     int sp = 0;
-    int cid = 0;  // lane 0: the sub-pool counter's value
+    int cid = 0;  // lane 0: the sub-pool counter's value of the pending claim
     bool ok = true;
-    // cid is only written (and only read) in lane 0: a select over the
-    // other lanes would read the register the atomic is still returning
-    // into and wait for it on every logged visit
-    __device__ __forceinline__ void begin(const BlendLog &L, int lane) {
-        if (!ok) return;
+    __device__ __forceinline__ void claim_next(const BlendLog &L, int lane) {
         if (lane == 0) cid = atomicAdd(&L.counters[sp], 1);
     }
+    __device__ __forceinline__ void start(const BlendLog &L, int lane) { claim_next(L, lane); }
     __device__ __forceinline__ int claimed(const BlendLog &L, int lane) {
         int c = 0;
         if (lane == 0) c = log_resolve(L, sp, cid, 1);
@@ -86,6 +89,7 @@ struct LogWriter {
         L.ent[64 * (size_t)c + lane] = e;
         L.ckpt[64 * (size_t)c + lane] = T;
         if (lane == 0) L.table[tb + (size_t)((nlog >> 6) - 1)] = c;
+        claim_next(L, lane);
     }
     __device__ __forceinline__ void finish(const BlendLog &L, int lane, int nlog, const uint4 &e, int tile,
                                            int wave) {
