@@ -77,6 +77,7 @@ struct Engine {
     // per-tile
     DevBuf counts, offsets, stats, big_list, scan_tmp;
     DevBuf huge_list, chunk_base, chunk_counts;  // the longest super-tile lists, their chunk numbering and counts
+    DevBuf merge_base;                           // the merge-tile numbering of the lists above 4096 keys
     DevBuf super_counts, super_offsets, super_cm, super_tmp;  // super_cm: per-(workgroup, super-tile) offsets
     // per-intersection
     DevBuf keys, keys_tmp, ids;  // keys: per (splat, super-tile) pair
@@ -498,9 +499,10 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     CHECK(ensure(E.super_offsets, (size_t)(NS + 1) * 4));
     CHECK(ensure(E.super_cm, (size_t)mskern::kBinMaxBlocks * NS * 4));
     CHECK(ensure(E.super_tmp, (size_t)mskern::tile_scan_temp_ints(NS) * 4));
-    // stats (ints): [0..1] tiles: total, largest; [4..6] super-tiles: total,
-    // largest, long lists; [8..9] 64-bit intersection count from the
-    // projection; [12..13] huge lists, their chunks; [14] deep tiles
+    // stats (ints): [0..1] tiles: total, largest; [4..7] super-tiles: total,
+    // largest, long lists, their merge tiles; [8..9] 64-bit intersection
+    // count from the projection; [12..13] huge lists, their chunks; [14]
+    // deep tiles
     CHECK(ensure(E.stats, 64));
     CHECK(ensure(E.big_list, (size_t)NS * 4));
     CHECK(ensure(E.out_img, Pn * 12));
@@ -559,7 +561,10 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
     stage_mark(ST_SCATTER_SORT);
     CHECK(ensure(E.keys, (size_t)S_total * 8));
     CHECK(ensure(E.ids, (size_t)I * 4));
-    if (super_max > mskern::kSuperSortChunk) CHECK(ensure(E.keys_tmp, (size_t)S_total * 8));
+    if (super_max > mskern::kSuperSortChunk) {
+        CHECK(ensure(E.keys_tmp, (size_t)S_total * 8));
+        CHECK(ensure(E.merge_base, (size_t)NS * 4));
+    }
     if (super_max > mskern::kSuperHugeList) {
         CHECK(ensure(E.huge_list, (size_t)NS * 4));
         CHECK(ensure(E.chunk_base, (size_t)NS * 4));
@@ -579,8 +584,8 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
                              P<float>(E.depths), P<int>(E.super_offsets), P<int>(E.super_cm), super_max,
                              P<uint64_t>(E.keys), P<uint64_t>(E.keys_tmp), P<int>(E.big_list), P<int>(E.stats) + 4,
                              P<int>(E.huge_list), P<int>(E.stats) + 12, P<int>(E.chunk_base), P<int>(E.chunk_counts),
-                             P<int>(E.counts), P<int>(E.offsets), P<int>(E.stats), P<int>(E.scan_tmp), P<int>(E.ids),
-                             E.wide_keys, scan_deep ? &dscan : nullptr);
+                             P<int>(E.merge_base), S_total, P<int>(E.counts), P<int>(E.offsets), P<int>(E.stats),
+                             P<int>(E.scan_tmp), P<int>(E.ids), E.wide_keys, scan_deep ? &dscan : nullptr);
     E.n_deep = 0;
     if (scan_deep) {
         HIPC(hipStreamSynchronize(s));
@@ -752,7 +757,7 @@ void msplat_hip_cleanup(void) {
     (void)hipStreamSynchronize(E.stream);
     if (E.deep_stream) (void)hipStreamSynchronize(E.deep_stream);
     DevBuf *all[] = {&E.rec, &E.depths, &E.radii, &E.rect, &E.grads16, &E.colors_raw, &E.counts, &E.scan_tmp, &E.super_counts, &E.super_offsets, &E.super_cm, &E.super_tmp, &E.offsets,
-                     &E.stats, &E.big_list, &E.huge_list, &E.chunk_base, &E.chunk_counts, &E.keys, &E.keys_tmp, &E.ids, &E.blend_log, &E.t_ckpt, &E.wave_cnt, &E.selfcheck, &E.out_img, &E.final_Ts,
+                     &E.stats, &E.big_list, &E.huge_list, &E.chunk_base, &E.chunk_counts, &E.merge_base, &E.keys, &E.keys_tmp, &E.ids, &E.blend_log, &E.t_ckpt, &E.wave_cnt, &E.selfcheck, &E.out_img, &E.final_Ts,
                      &E.final_idx, &E.out_depth, &E.out_normal, &E.out_alpha, &E.out_median, &E.out_dist,
                      &E.dL_dimg, &E.gm1, &E.gs1, &E.gs12, &E.partials, &E.loss, &E.dmeans, &E.dscales,
                      &E.dquats, &E.dmean2d, &E.dfdc, &E.dfrest, &E.dens_flags, &E.dens_scan, &E.dens_keep, &E.dens_ws, &E.deep_list, &E.deep_pos, &E.deep_tb, &E.deep_cnt, &E.log_table, &E.log_ctr, &E.pair_counter,

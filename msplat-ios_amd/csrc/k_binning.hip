@@ -432,19 +432,22 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_super(int tiles_x, int ti
     }
 }
 
-// Chunk numbering of the huge lists: chunk_base[b] = the number of kChunk
-// chunks of huge lists 0 .. b-1, huge_stats[1] = all of them.  One workgroup.
-__global__ __launch_bounds__(1024) void k_big_prep(const int *__restrict__ offsets, const int *__restrict__ big_list,
-                                                   int *__restrict__ stats, int *__restrict__ chunk_base) {
+// Unit numbering of a list of super-tiles: base[b] = the number of `unit`-key
+// units (chunks, merge tiles) of lists 0 .. b-1, *total = all of them.  Every
+// listed super-tile holds more than `unit` keys, so base is strictly
+// increasing.  One workgroup.
+__global__ __launch_bounds__(1024) void k_list_prep(const int *__restrict__ offsets, const int *__restrict__ list,
+                                                    const int *__restrict__ count, int unit, int *__restrict__ base,
+                                                    int *__restrict__ total) {
     __shared__ int s_w[16];
-    const int nbig = stats[0];
+    const int n = *count;
     int carry = 0;
-    for (int b0 = 0; b0 < nbig; b0 += 1024) {
+    for (int b0 = 0; b0 < n; b0 += 1024) {
         const int b = b0 + (int)threadIdx.x;
         int v = 0;
-        if (b < nbig) {
-            const int t = big_list[b];
-            v = (offsets[t + 1] - offsets[t] + kChunk - 1) / kChunk;
+        if (b < n) {
+            const int t = list[b];
+            v = (offsets[t + 1] - offsets[t] + unit - 1) / unit;
         }
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
         int incl = v;
@@ -462,29 +465,46 @@ __global__ __launch_bounds__(1024) void k_big_prep(const int *__restrict__ offse
             off += w < wave ? s_w[w] : 0;
             tot += s_w[w];
         }
-        if (b < nbig) chunk_base[b] = carry + off + incl - v;
+        if (b < n) base[b] = carry + off + incl - v;
         carry += tot;
     }
-    if (threadIdx.x == 0) stats[1] = carry;
+    if (threadIdx.x == 0) *total = carry;
+}
+
+// The list of flattened unit g: the last b with base[b] <= g (base strictly
+// increasing from base[0] = 0).  Called with a wave-uniform g.
+__device__ __forceinline__ int list_of_unit(const int *__restrict__ base, int n, int g) {
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (base[mid] <= g)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    return lo;
 }
 
 // Sorts every kChunk run of the huge lists in LDS, one run per workgroup
-// iteration (grid.y strides over the lists, grid.x over their runs).
+// iteration: the grid strides over the runs of all the lists (chunk_base
+// numbers them), so every run has its own workgroup whatever the lists'
+// lengths.
 __global__ __launch_bounds__(kSortThreads) void k_sort_chunks(const int *__restrict__ offsets,
                                                               const int *__restrict__ big_list,
                                                               const int *__restrict__ stats,
+                                                              const int *__restrict__ chunk_base,
                                                               unsigned long long *__restrict__ keys) {
     __shared__ unsigned long long s[kChunk];
-    const int nbig = stats[0];
-    for (int b = blockIdx.y; b < nbig; b += gridDim.y) {
+    const int nbig = stats[0], nchunks = stats[1];
+    for (int g = blockIdx.x; g < nchunks; g += gridDim.x) {
+        const int b = list_of_unit(chunk_base, nbig, g);
         const int t = big_list[b];
         const int start = offsets[t], cnt = offsets[t + 1] - start;
-        for (int c0 = blockIdx.x * kChunk; c0 < cnt; c0 += gridDim.x * kChunk) {
-            const int c = min(kChunk, cnt - c0);
-            lds_bitonic(s, keys + start + c0, c);
-            for (int i = threadIdx.x; i < c; i += kSortThreads) keys[start + c0 + i] = s[sort_slot(i)];
-            __syncthreads();
-        }
+        const int c0 = (g - chunk_base[b]) * kChunk;
+        const int c = min(kChunk, cnt - c0);
+        lds_bitonic(s, keys + start + c0, c);
+        for (int i = threadIdx.x; i < c; i += kSortThreads) keys[start + c0 + i] = s[sort_slot(i)];
+        __syncthreads();
     }
 }
 
@@ -501,23 +521,23 @@ __global__ __launch_bounds__(kSortThreads) void k_count_chunks(int tiles_x, int 
                                                                int *__restrict__ chunk_counts,
                                                                int *__restrict__ tile_counts) {
     __shared__ int s_tc[kSuper * kSuper];
-    const int nbig = stats[0];
-    for (int b = blockIdx.y; b < nbig; b += gridDim.y) {
+    const int nbig = stats[0], nchunks = stats[1];
+    for (int g = blockIdx.x; g < nchunks; g += gridDim.x) {
+        const int b = list_of_unit(chunk_base, nbig, g);
         const int t = big_list[b];
         const int start = offsets[t], cnt = offsets[t + 1] - start;
         const int stx = (t % sxn) * kSuper, sty = (t / sxn) * kSuper;
-        for (int c = blockIdx.x; c * kChunk < cnt; c += gridDim.x) {
-            if (threadIdx.x < kSuper * kSuper) s_tc[threadIdx.x] = 0;
-            __syncthreads();
-            count_tiles<PACKED>(keys + start + c * kChunk, min(kChunk, cnt - c * kChunk), stx, sty, rect, s_tc);
-            if (threadIdx.x < kSuper * kSuper) {
-                const int v = s_tc[threadIdx.x];
-                chunk_counts[(size_t)(chunk_base[b] + c) * (kSuper * kSuper) + threadIdx.x] = v;
-                const int tx = stx + (int)threadIdx.x % kSuper, ty = sty + (int)threadIdx.x / kSuper;
-                if (v && tx < tiles_x && ty < tiles_y) atomicAdd(&tile_counts[ty * tiles_x + tx], v);
-            }
-            __syncthreads();
+        const int c = g - chunk_base[b];
+        if (threadIdx.x < kSuper * kSuper) s_tc[threadIdx.x] = 0;
+        __syncthreads();
+        count_tiles<PACKED>(keys + start + c * kChunk, min(kChunk, cnt - c * kChunk), stx, sty, rect, s_tc);
+        if (threadIdx.x < kSuper * kSuper) {
+            const int v = s_tc[threadIdx.x];
+            chunk_counts[(size_t)g * (kSuper * kSuper) + threadIdx.x] = v;
+            const int tx = stx + (int)threadIdx.x % kSuper, ty = sty + (int)threadIdx.x / kSuper;
+            if (v && tx < tiles_x && ty < tiles_y) atomicAdd(&tile_counts[ty * tiles_x + tx], v);
         }
+        __syncthreads();
     }
 }
 
@@ -549,18 +569,24 @@ __device__ __forceinline__ int merge_split(const K *__restrict__ A, int la, cons
     return lo;
 }
 
+// The grid strides over the merge tiles of all the lists (merge_base
+// numbers them), so every tile has its own workgroup whatever the lists'
+// lengths.
 __global__ __launch_bounds__(256) void k_merge_path(int L, const int *__restrict__ offsets,
                                                     const int *__restrict__ big_list, const int *__restrict__ stats,
+                                                    const int *__restrict__ merge_base,
                                                     const unsigned long long *__restrict__ src,
                                                     unsigned long long *__restrict__ dst) {
     __shared__ unsigned long long s_k[kMergeTile];
     __shared__ int s_split[2];
-    const int nbig = stats[2];
-    for (int b = blockIdx.y; b < nbig; b += gridDim.y) {
+    const int nbig = stats[2], ntiles = stats[3];
+    for (int g = blockIdx.x; g < ntiles; g += gridDim.x) {
+        const int b = list_of_unit(merge_base, nbig, g);
         const int t = big_list[b];
         const int start = offsets[t], cnt = offsets[t + 1] - start;
         // 2L is a multiple of kMergeTile, so no tile straddles two pairs
-        for (int o0 = blockIdx.x * kMergeTile; o0 < cnt; o0 += gridDim.x * kMergeTile) {
+        {
+            const int o0 = (g - merge_base[b]) * kMergeTile;
             const int pair_base = o0 / (2 * L) * (2 * L);
             const int la = min(L, cnt - pair_base), lb = max(0, min(L, cnt - pair_base - L));
             const unsigned long long *A = src + start + pair_base, *B = A + la;
@@ -691,32 +717,32 @@ __global__ __launch_bounds__(256) void k_emit_chunks(int tiles_x, int tiles_y, i
                                                      const int *__restrict__ toffsets, int *__restrict__ ids) {
     __shared__ int s_gid[kWin];
     __shared__ unsigned short s_rr[kWin];
-    const int nbig = stats[0];
+    const int nbig = stats[0], nchunks = stats[1];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int b = blockIdx.y; b < nbig; b += gridDim.y) {
+    for (int g = blockIdx.x; g < nchunks; g += gridDim.x) {
+        const int b = list_of_unit(chunk_base, nbig, g);
         const int st = big_list[b];
         const int stx = (st % sxn) * kSuper, sty = (st / sxn) * kSuper;
         const int start = soffsets[st], cnt = soffsets[st + 1] - start;
         const int ty = sty + wave;
-        for (int c = blockIdx.x; c * kChunk < cnt; c += gridDim.x) {
-            // entries of this wave's four tiles in the chunks before c
-            int before[kSuper] = {0, 0, 0, 0};
-            for (int k = lane; k < c; k += 64)
+        const int c = g - chunk_base[b];
+        // entries of this wave's four tiles in the chunks before c
+        int before[kSuper] = {0, 0, 0, 0};
+        for (int k = lane; k < c; k += 64)
 #pragma unroll
-                for (int lx = 0; lx < kSuper; ++lx)
-                    before[lx] += chunk_counts[(size_t)(chunk_base[b] + k) * (kSuper * kSuper) + wave * kSuper + lx];
-            int out[kSuper];
+            for (int lx = 0; lx < kSuper; ++lx)
+                before[lx] += chunk_counts[(size_t)(chunk_base[b] + k) * (kSuper * kSuper) + wave * kSuper + lx];
+        int out[kSuper];
 #pragma unroll
-            for (int lx = 0; lx < kSuper; ++lx) {
-                int v = before[lx];
+        for (int lx = 0; lx < kSuper; ++lx) {
+            int v = before[lx];
 #pragma unroll
-                for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
-                const int tx = stx + lx;
-                out[lx] = (tx < tiles_x && ty < tiles_y) ? toffsets[ty * tiles_x + tx] + v : -1;
-            }
-            emit_range<PACKED>(skeys + start + c * kChunk, min(kChunk, cnt - c * kChunk), stx, sty, rect, out, s_gid,
-                               s_rr, ids);
+            for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+            const int tx = stx + lx;
+            out[lx] = (tx < tiles_x && ty < tiles_y) ? toffsets[ty * tiles_x + tx] + v : -1;
         }
+        emit_range<PACKED>(skeys + start + c * kChunk, min(kChunk, cnt - c * kChunk), stx, sty, rect, out, s_gid,
+                           s_rr, ids);
     }
 }
 
@@ -758,9 +784,9 @@ void launch_super_count(hipStream_t s, int n, int tiles_x, int tiles_y, const in
 void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
                       const float *depths, const int *super_offsets, const int *super_cm, int super_max,
                       uint64_t *super_keys, uint64_t *super_keys_tmp, int *big_list, int *super_stats,
-                      int *huge_list, int *huge_stats, int *chunk_base, int *chunk_counts, int *tile_counts,
-                      int *tile_offsets, int *tile_stats, int *tile_temp, int *ids, bool force_wide_keys,
-                      const DeepScan *deep) {
+                      int *huge_list, int *huge_stats, int *chunk_base, int *chunk_counts, int *merge_base,
+                      int total_keys, int *tile_counts, int *tile_offsets, int *tile_stats, int *tile_temp, int *ids,
+                      bool force_wide_keys, const DeepScan *deep) {
     const int sxn = (tiles_x + kSuper - 1) / kSuper, syn = (tiles_y + kSuper - 1) / kSuper, NS = sxn * syn;
     const int T = tiles_x * tiles_y;
     auto *k = reinterpret_cast<unsigned long long *>(super_keys);
@@ -777,23 +803,31 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
     hipLaunchKernelGGL(packed ? k_sort_super<true> : k_sort_super<false>, dim3(NS), dim3(kSortThreads), 0, s, tiles_x,
                        tiles_y, sxn, super_offsets, k, r2, tile_counts, big_list, super_stats, huge_list, huge_stats,
                        huge_th);
-    // huge lists: kChunk runs sorted on many workgroups, then merged
-    const dim3 big_grid(std::min(256, (super_max + kChunk - 1) / kChunk), 16);
+    // huge lists: kChunk runs sorted on many workgroups, then merged.  The
+    // chunk and merge-tile kernels stride over units numbered across all
+    // their lists; their grids cover at most total_keys / unit + NS units
+    // (each list rounds up once)
+    const int big_grid = (int)std::min<int64_t>(4096, (int64_t)total_keys / kChunk + NS);
     if (big) {
-        hipLaunchKernelGGL(k_big_prep, dim3(1), dim3(1024), 0, s, super_offsets, huge_list, huge_stats, chunk_base);
-        hipLaunchKernelGGL(k_sort_chunks, big_grid, dim3(kSortThreads), 0, s, super_offsets, huge_list, huge_stats, k);
+        hipLaunchKernelGGL(k_list_prep, dim3(1), dim3(1024), 0, s, super_offsets, huge_list, huge_stats, kChunk,
+                           chunk_base, huge_stats + 1);
+        hipLaunchKernelGGL(k_sort_chunks, dim3(big_grid), dim3(kSortThreads), 0, s, super_offsets, huge_list,
+                           huge_stats, chunk_base, k);
     }
     unsigned long long *src = k, *dst = kt;
-    const dim3 merge_grid(std::min(512, (super_max + kMergeTile - 1) / kMergeTile), 16);
+    if (super_max > kChunk)
+        hipLaunchKernelGGL(k_list_prep, dim3(1), dim3(1024), 0, s, super_offsets, big_list, super_stats + 2,
+                           kMergeTile, merge_base, super_stats + 3);
+    const int merge_grid = (int)std::min<int64_t>(8192, (int64_t)total_keys / kMergeTile + NS);
     for (int L = kChunk; L < super_max; L <<= 1) {
-        hipLaunchKernelGGL(k_merge_path, merge_grid, dim3(256), 0, s, L, super_offsets, big_list, super_stats, src,
-                           dst);
+        hipLaunchKernelGGL(k_merge_path, dim3(merge_grid), dim3(256), 0, s, L, super_offsets, big_list, super_stats,
+                           merge_base, src, dst);
         std::swap(src, dst);
     }
     // the lists longer than kChunk end in src (every merge pass covers all
     // of them); the emission reads them there
     if (big)
-        hipLaunchKernelGGL(packed ? k_count_chunks<true> : k_count_chunks<false>, big_grid, dim3(kSortThreads), 0, s,
+        hipLaunchKernelGGL(packed ? k_count_chunks<true> : k_count_chunks<false>, dim3(big_grid), dim3(kSortThreads), 0, s,
                            tiles_x, tiles_y, sxn, super_offsets, huge_list, huge_stats, chunk_base, src, r2,
                            chunk_counts, tile_counts);
     launch_scan_counts(s, T, tile_counts, tile_offsets, nullptr, tile_stats, tile_temp);
@@ -804,7 +838,7 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
     hipLaunchKernelGGL(packed ? k_emit_tiles<true> : k_emit_tiles<false>, dim3(NS), dim3(256), 0, s, tiles_x, tiles_y,
                        sxn, super_offsets, k, src, r2, tile_offsets, ids, huge_th);
     if (big)
-        hipLaunchKernelGGL(packed ? k_emit_chunks<true> : k_emit_chunks<false>, big_grid, dim3(256), 0, s, tiles_x,
+        hipLaunchKernelGGL(packed ? k_emit_chunks<true> : k_emit_chunks<false>, dim3(big_grid), dim3(256), 0, s, tiles_x,
                            tiles_y, sxn, super_offsets, huge_list, huge_stats, chunk_base, chunk_counts, src, r2,
                            tile_offsets, ids);
 }

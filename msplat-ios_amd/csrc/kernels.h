@@ -63,9 +63,11 @@ constexpr int kBinMaxBlocks = 256;
 // Scatter, per-super-tile sort, tile counts and offsets (tile_offsets[T + 1],
 // tile_stats = {intersections, largest tile}, zero on entry) and the
 // per-tile sorted gaussian ids.  When super_max > 4096 the long lists need
-// super_keys_tmp (the size of super_keys); when super_max > kSuperHugeList
-// huge_list[NS], huge_stats[2] (zero on entry), chunk_base[NS] and
-// chunk_counts[big_chunk_ints(total, NS)].
+// super_keys_tmp (the size of super_keys) and merge_base[NS], and
+// super_stats[3] receives their merge-tile count; when super_max >
+// kSuperHugeList huge_list[NS], huge_stats[2] (zero on entry), chunk_base[NS]
+// and chunk_counts[big_chunk_ints(total, NS)].  total_keys = the pair count
+// (super_stats[0]).
 // The deep-tile scan launch_bin_tiles queues once the tile offsets exist
 // (before the emission kernels): the tiles with at least `len` entries into
 // `list`, their number into *count, copied to *host_count.
@@ -76,9 +78,9 @@ struct DeepScan {
 void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int *radii, const uint32_t *rect,
                       const float *depths, const int *super_offsets, const int *super_cm, int super_max,
                       uint64_t *super_keys, uint64_t *super_keys_tmp, int *big_list, int *super_stats,
-                      int *huge_list, int *huge_stats, int *chunk_base, int *chunk_counts, int *tile_counts,
-                      int *tile_offsets, int *tile_stats, int *tile_temp, int *ids, bool force_wide_keys,
-                      const DeepScan *deep = nullptr);
+                      int *huge_list, int *huge_stats, int *chunk_base, int *chunk_counts, int *merge_base,
+                      int total_keys, int *tile_counts, int *tile_offsets, int *tile_stats, int *tile_temp, int *ids,
+                      bool force_wide_keys, const DeepScan *deep = nullptr);
 constexpr int kSuperHugeList = 4 * 4096;
 // Ints of chunk_counts: 16 per 4096-key chunk of the long lists, at most
 // total / 4096 + NS chunks.
