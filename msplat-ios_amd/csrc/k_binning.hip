@@ -20,7 +20,7 @@
 //   3. k_sort_super: each super-tile counts the entries of its 16 tiles
 //      (the tile histogram, no atomics: a super-tile owns its tiles) and
 //      sorts its keys in LDS (bitonic, up to 4096 keys), larger lists in
-//      4096-key runs merged by k_merge_pass; an exclusive scan of the tile
+//      4096-key runs merged by k_merge_path; an exclusive scan of the tile
 //      counts gives the tile offsets (the layout of the id list the
 //      rasterizers read);
 //   4. k_emit_tiles: each super-tile's sorted list is filtered, in order,
@@ -38,6 +38,20 @@ constexpr int kChunk = 4096;  // keys per LDS sort (32 KB of u64)
 // rest of the pass); shorter ones stay within their super-tile's workgroup.
 constexpr int kHuge = 4 * kChunk;
 constexpr int kSuper = 4;     // tiles per super-tile side
+
+// The merge passes (k_merge_path) take a list of cnt > kChunk keys through
+// merge_passes(cnt) passes (L = kChunk, 2 kChunk, ... below cnt), pass p
+// reading the key buffer for even p and writing the second buffer, and the
+// reverse; merged_keys names where the list ends.
+__host__ __device__ __forceinline__ int merge_passes(int cnt) {
+    int p = 0;
+    for (int64_t L = kChunk; L < cnt; L <<= 1) ++p;
+    return p;
+}
+__device__ __forceinline__ const unsigned long long *merged_keys(int cnt, const unsigned long long *keys,
+                                                                  const unsigned long long *keys2) {
+    return (merge_passes(cnt) & 1) ? keys2 : keys;
+}
 
 // ---- counts -> offsets ------------------------------------------------------
 //
@@ -432,22 +446,24 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_super(int tiles_x, int ti
     }
 }
 
-// Unit numbering of a list of super-tiles: base[b] = the number of `unit`-key
-// units (chunks, merge tiles) of lists 0 .. b-1, *total = all of them.  Every
-// listed super-tile holds more than `unit` keys, so base is strictly
-// increasing.  One workgroup.
-__global__ __launch_bounds__(1024) void k_list_prep(const int *__restrict__ offsets, const int *__restrict__ list,
-                                                    const int *__restrict__ count, int unit, int *__restrict__ base,
-                                                    int *__restrict__ total) {
-    __shared__ int s_w[16];
-    const int n = *count;
+// Unit numbering of lists of super-tiles: base[b] = the number of
+// `unit`-key units (chunks, merge tiles) of lists 0 .. b-1, *total = all of
+// them.  Every listed super-tile holds more than `unit` keys, so base is
+// strictly increasing.
+struct UnitList {
+    const int *list, *count;
+    int unit;
+    int *base, *total;
+};
+__device__ __forceinline__ void number_units(const int *__restrict__ offsets, const UnitList &u, int *s_w) {
+    const int n = *u.count;
     int carry = 0;
     for (int b0 = 0; b0 < n; b0 += 1024) {
         const int b = b0 + (int)threadIdx.x;
         int v = 0;
         if (b < n) {
-            const int t = list[b];
-            v = (offsets[t + 1] - offsets[t] + unit - 1) / unit;
+            const int t = u.list[b];
+            v = (offsets[t + 1] - offsets[t] + u.unit - 1) / u.unit;
         }
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
         int incl = v;
@@ -465,10 +481,18 @@ __global__ __launch_bounds__(1024) void k_list_prep(const int *__restrict__ offs
             off += w < wave ? s_w[w] : 0;
             tot += s_w[w];
         }
-        if (b < n) base[b] = carry + off + incl - v;
+        if (b < n) u.base[b] = carry + off + incl - v;
         carry += tot;
     }
-    if (threadIdx.x == 0) *total = carry;
+    if (threadIdx.x == 0) *u.total = carry;
+}
+// One workgroup numbers both: the huge lists' chunks (when a.list is set)
+// and the long lists' merge tiles (when b.list is set).
+__global__ __launch_bounds__(1024) void k_list_prep(const int *__restrict__ offsets, UnitList a, UnitList b) {
+    __shared__ int s_w[16];
+    if (a.list) number_units(offsets, a, s_w);
+    __syncthreads();
+    if (b.list) number_units(offsets, b, s_w);
 }
 
 // The list of flattened unit g: the last b with base[b] <= g (base strictly
@@ -516,7 +540,8 @@ __global__ __launch_bounds__(kSortThreads) void k_count_chunks(int tiles_x, int 
                                                                const int *__restrict__ big_list,
                                                                const int *__restrict__ stats,
                                                                const int *__restrict__ chunk_base,
-                                                               const unsigned long long *__restrict__ keys,
+                                                               const unsigned long long *__restrict__ skeys,
+                                                               const unsigned long long *__restrict__ keys2,
                                                                const uint2 *__restrict__ rect,
                                                                int *__restrict__ chunk_counts,
                                                                int *__restrict__ tile_counts) {
@@ -528,6 +553,7 @@ __global__ __launch_bounds__(kSortThreads) void k_count_chunks(int tiles_x, int 
         const int start = offsets[t], cnt = offsets[t + 1] - start;
         const int stx = (t % sxn) * kSuper, sty = (t / sxn) * kSuper;
         const int c = g - chunk_base[b];
+        const unsigned long long *__restrict__ keys = merged_keys(cnt, skeys, keys2);
         if (threadIdx.x < kSuper * kSuper) s_tc[threadIdx.x] = 0;
         __syncthreads();
         count_tiles<PACKED>(keys + start + c * kChunk, min(kChunk, cnt - c * kChunk), stx, sty, rect, s_tc);
@@ -551,8 +577,12 @@ __global__ __launch_bounds__(kSortThreads) void k_count_chunks(int tiles_x, int 
 // LDS with coalesced loads, and each thread merges 8 outputs from its own
 // diagonal of the staged keys.  Every key is read and written once per pass
 // and the output leaves through LDS in coalesced 2 KB rows.  Keys are unique
-// (the id is in the low word), so the merge is a permutation.
+// (the id is in the low word), so the merge is a permutation.  A pass skips
+// the lists its L already covers: a list of cnt keys takes merge_passes(cnt)
+// passes, alternating from the key buffer into the second buffer and back,
+// and ends in the buffer merged_keys() names.
 constexpr int kMergeTile = 2048, kMergeItems = kMergeTile / 256;
+
 
 // The number of keys of A among the first d keys of the merge of the
 // ascending runs A[0, la) and B[0, lb).
@@ -572,6 +602,31 @@ __device__ __forceinline__ int merge_split(const K *__restrict__ A, int la, cons
 // The grid strides over the merge tiles of all the lists (merge_base
 // numbers them), so every tile has its own workgroup whatever the lists'
 // lengths.
+// merge_split by one wave, 64 probes per step: the predicate A[i] < B[d-1-i]
+// holds exactly for i below the split, so each step's ballot narrows the
+// range to one of 64 slices and a run of 262k keys takes three steps of
+// dependent loads instead of eighteen.  Called by all 64 lanes of a wave;
+// returns the split in every lane.
+template <typename K>
+__device__ __forceinline__ int merge_split_wave(const K *__restrict__ A, int la, const K *__restrict__ B, int lb,
+                                                int d) {
+    const int lane = threadIdx.x & 63;
+    int lo = max(0, d - lb), hi = min(d, la);  // the split lies in [lo, hi]
+    while (hi - lo > 64) {
+        const int step = (hi - lo + 63) >> 6;
+        const int i = lo + lane * step;
+        const bool below = i < hi && A[i] < B[d - i - 1];
+        const int f = __popcll(__ballot(below));  // probes below the split: lanes 0 .. f - 1
+        // split in (lo + (f - 1) step, lo + f step]
+        const int nlo = f > 0 ? lo + (f - 1) * step + 1 : lo;
+        hi = min(hi, lo + f * step);
+        lo = nlo;
+    }
+    const int i = lo + lane;
+    const bool below = i < hi && A[i] < B[d - i - 1];
+    return lo + __popcll(__ballot(below));
+}
+
 __global__ __launch_bounds__(256) void k_merge_path(int L, const int *__restrict__ offsets,
                                                     const int *__restrict__ big_list, const int *__restrict__ stats,
                                                     const int *__restrict__ merge_base,
@@ -584,6 +639,7 @@ __global__ __launch_bounds__(256) void k_merge_path(int L, const int *__restrict
         const int b = list_of_unit(merge_base, nbig, g);
         const int t = big_list[b];
         const int start = offsets[t], cnt = offsets[t + 1] - start;
+        if (cnt <= L) continue;  // merged by an earlier pass
         // 2L is a multiple of kMergeTile, so no tile straddles two pairs
         {
             const int o0 = (g - merge_base[b]) * kMergeTile;
@@ -591,7 +647,11 @@ __global__ __launch_bounds__(256) void k_merge_path(int L, const int *__restrict
             const int la = min(L, cnt - pair_base), lb = max(0, min(L, cnt - pair_base - L));
             const unsigned long long *A = src + start + pair_base, *B = A + la;
             const int d0 = o0 - pair_base, d1 = min(d0 + kMergeTile, la + lb);
-            if (threadIdx.x < 2) s_split[threadIdx.x] = merge_split(A, la, B, lb, threadIdx.x ? d1 : d0);
+            if (threadIdx.x < 128) {
+                const int w = threadIdx.x >> 6;  // wave 0: the tile's start, wave 1: its end
+                const int sp = merge_split_wave(A, la, B, lb, w ? d1 : d0);
+                if ((threadIdx.x & 63) == 0) s_split[w] = sp;
+            }
             __syncthreads();
             const int a0 = s_split[0], a1 = s_split[1];
             const int na = a1 - a0, n = d1 - d0;
@@ -680,7 +740,7 @@ template <bool PACKED>
 __global__ __launch_bounds__(256) void k_emit_tiles(int tiles_x, int tiles_y, int sxn,
                                                     const int *__restrict__ soffsets,
                                                     const unsigned long long *__restrict__ skeys,
-                                                    const unsigned long long *__restrict__ merged,
+                                                    const unsigned long long *__restrict__ keys2,
                                                     const uint2 *__restrict__ rect,
                                                     const int *__restrict__ toffsets, int *__restrict__ ids,
                                                     int huge_th) {
@@ -690,9 +750,9 @@ __global__ __launch_bounds__(256) void k_emit_tiles(int tiles_x, int tiles_y, in
     const int stx = (st % sxn) * kSuper, sty = (st / sxn) * kSuper;
     const int start = soffsets[st], cnt = soffsets[st + 1] - start;
     if (cnt > huge_th) return;
-    // lists above kChunk went through the merge passes, which leave them in
-    // `merged`; the shorter ones were sorted in place
-    const unsigned long long *__restrict__ keys = cnt > kChunk ? merged : skeys;
+    // lists above kChunk went through their merge passes (merged_keys); the
+    // shorter ones were sorted in place
+    const unsigned long long *__restrict__ keys = cnt > kChunk ? merged_keys(cnt, skeys, keys2) : skeys;
     const int ty = sty + (int)(threadIdx.x >> 6);
     int out[kSuper];
 #pragma unroll
@@ -713,6 +773,7 @@ __global__ __launch_bounds__(256) void k_emit_chunks(int tiles_x, int tiles_y, i
                                                      const int *__restrict__ chunk_base,
                                                      const int *__restrict__ chunk_counts,
                                                      const unsigned long long *__restrict__ skeys,
+                                                     const unsigned long long *__restrict__ keys2,
                                                      const uint2 *__restrict__ rect,
                                                      const int *__restrict__ toffsets, int *__restrict__ ids) {
     __shared__ int s_gid[kWin];
@@ -741,8 +802,8 @@ __global__ __launch_bounds__(256) void k_emit_chunks(int tiles_x, int tiles_y, i
             const int tx = stx + lx;
             out[lx] = (tx < tiles_x && ty < tiles_y) ? toffsets[ty * tiles_x + tx] + v : -1;
         }
-        emit_range<PACKED>(skeys + start + c * kChunk, min(kChunk, cnt - c * kChunk), stx, sty, rect, out, s_gid,
-                           s_rr, ids);
+        emit_range<PACKED>(merged_keys(cnt, skeys, keys2) + start + c * kChunk, min(kChunk, cnt - c * kChunk), stx,
+                           sty, rect, out, s_gid, s_rr, ids);
     }
 }
 
@@ -808,27 +869,26 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
     // their lists; their grids cover at most total_keys / unit + NS units
     // (each list rounds up once)
     const int big_grid = (int)std::min<int64_t>(4096, (int64_t)total_keys / kChunk + NS);
-    if (big) {
-        hipLaunchKernelGGL(k_list_prep, dim3(1), dim3(1024), 0, s, super_offsets, huge_list, huge_stats, kChunk,
-                           chunk_base, huge_stats + 1);
+    if (super_max > kChunk) {
+        const UnitList chunks{huge_list, huge_stats, kChunk, chunk_base, huge_stats + 1};
+        const UnitList tiles{big_list, super_stats + 2, kMergeTile, merge_base, super_stats + 3};
+        hipLaunchKernelGGL(k_list_prep, dim3(1), dim3(1024), 0, s, super_offsets, big ? chunks : UnitList{}, tiles);
+    }
+    if (big)
         hipLaunchKernelGGL(k_sort_chunks, dim3(big_grid), dim3(kSortThreads), 0, s, super_offsets, huge_list,
                            huge_stats, chunk_base, k);
-    }
     unsigned long long *src = k, *dst = kt;
-    if (super_max > kChunk)
-        hipLaunchKernelGGL(k_list_prep, dim3(1), dim3(1024), 0, s, super_offsets, big_list, super_stats + 2,
-                           kMergeTile, merge_base, super_stats + 3);
     const int merge_grid = (int)std::min<int64_t>(8192, (int64_t)total_keys / kMergeTile + NS);
     for (int L = kChunk; L < super_max; L <<= 1) {
         hipLaunchKernelGGL(k_merge_path, dim3(merge_grid), dim3(256), 0, s, L, super_offsets, big_list, super_stats,
                            merge_base, src, dst);
         std::swap(src, dst);
     }
-    // the lists longer than kChunk end in src (every merge pass covers all
-    // of them); the emission reads them there
+    // each list longer than kChunk ends in the buffer its last pass wrote
+    // (merged_keys); the emission reads it there
     if (big)
         hipLaunchKernelGGL(packed ? k_count_chunks<true> : k_count_chunks<false>, dim3(big_grid), dim3(kSortThreads), 0, s,
-                           tiles_x, tiles_y, sxn, super_offsets, huge_list, huge_stats, chunk_base, src, r2,
+                           tiles_x, tiles_y, sxn, super_offsets, huge_list, huge_stats, chunk_base, k, kt, r2,
                            chunk_counts, tile_counts);
     launch_scan_counts(s, T, tile_counts, tile_offsets, nullptr, tile_stats, tile_temp);
     if (deep) {
@@ -836,10 +896,10 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
         (void)hipMemcpyAsync(deep->host_count, deep->count, sizeof(int), hipMemcpyDeviceToHost, s);
     }
     hipLaunchKernelGGL(packed ? k_emit_tiles<true> : k_emit_tiles<false>, dim3(NS), dim3(256), 0, s, tiles_x, tiles_y,
-                       sxn, super_offsets, k, src, r2, tile_offsets, ids, huge_th);
+                       sxn, super_offsets, k, kt, r2, tile_offsets, ids, huge_th);
     if (big)
         hipLaunchKernelGGL(packed ? k_emit_chunks<true> : k_emit_chunks<false>, dim3(big_grid), dim3(256), 0, s, tiles_x,
-                           tiles_y, sxn, super_offsets, huge_list, huge_stats, chunk_base, chunk_counts, src, r2,
+                           tiles_y, sxn, super_offsets, huge_list, huge_stats, chunk_base, chunk_counts, k, kt, r2,
                            tile_offsets, ids);
 }
 
