@@ -794,13 +794,18 @@ __global__ __launch_bounds__(kThreads) void k_raster_deep(
 // pixel lists in coalesced 64-entry rows (wave v takes pixels v, v + 16, ...),
 // in windows of kDeepWin list positions:
 //   1. the positions present are marked in an LDS bitmap;
-//   2. a block scan of the words' popcounts ranks them, and each present
-//      position's entry gets its list position and gaussian id;
-//   3. the ballots are assembled in LDS for kDeepBal ranks at a time;
+//   2. a block scan of the words' popcounts ranks them;
+//   3. the ballots and positions are assembled in LDS for kDeepBal ranks at
+//      a time (each pixel's entries of a rank range are a run of its list,
+//      taken from a per-pixel cursor) and each entry is written once;
 //   4. pixel entry i of rank r_i writes the checkpoints c in (r_{i-1}, r_i]
 //      (the transmittance changes only at the pixel's own blends), and
 //      after the pixel's last entry the final transmittance fills the rest.
 constexpr int kDeepWin = 131072, kDeepWords = kDeepWin / 32, kDeepBal = 2048;
+// Log chunks whose pool index the workgroup keeps in LDS (the checkpoint
+// pass looks one up per checkpoint and pixel); longer logs read the rest of
+// the chunk table from global memory.
+constexpr int kDeepTbl = 4096;
 constexpr int kLogThreads = 1024, kLogWaves = kLogThreads / 64;
 __global__ __launch_bounds__(kLogThreads) void k_deep_log(int W, int H, int tiles_x, int n_deep,
                                                   const int *__restrict__ deep_list, const int *__restrict__ offsets,
@@ -810,7 +815,9 @@ __global__ __launch_bounds__(kLogThreads) void k_deep_log(int W, int H, int tile
     __shared__ uint32_t s_bits[kDeepWords];
     __shared__ int s_woff[kDeepWords];
     __shared__ uint32_t s_bal[2][kDeepBal];
-    __shared__ int s_cnt[64], s_i[64], s_e[64], s_last[64];
+    __shared__ int s_pos[kDeepBal];
+    __shared__ int s_chunk[kDeepTbl];
+    __shared__ int s_cnt[64], s_i[64], s_e[64], s_last[64], s_cur[64];
     __shared__ float s_tf[64];
     __shared__ int s_red[kLogWaves];
     __shared__ int s_ok;
@@ -823,8 +830,9 @@ __global__ __launch_bounds__(kLogThreads) void k_deep_log(int W, int H, int tile
     const int start = offsets[tile], len = offsets[tile + 1] - start;
     int *__restrict__ chunk_of = blog.table + log_table_base(start, len, tile, w);
     // entry r of the log, and checkpoint c (the chunk of entry c - 1 holds it)
-    auto ent_at = [&](int r) { return blog.ent + 64 * (size_t)chunk_of[r >> 6] + (r & 63); };
-    auto ckpt_at = [&](int c, int p) { return blog.ckpt + 64 * (size_t)chunk_of[(c >> 6) - 1] + p; };
+    auto pool_chunk = [&](int q) { return q < kDeepTbl ? s_chunk[q] : chunk_of[q]; };
+    auto ent_at = [&](int r) { return blog.ent + 64 * (size_t)pool_chunk(r >> 6) + (r & 63); };
+    auto ckpt_at = [&](int c, int p) { return blog.ckpt + 64 * (size_t)pool_chunk((c >> 6) - 1) + p; };
     auto slot_of = [&](int p) { return (size_t)k * 256 + 16 * lane_py(w, p) + lane_px(w, p); };
     if (threadIdx.x < 64) {
         const int p = threadIdx.x;
@@ -892,7 +900,10 @@ __global__ __launch_bounds__(kLogThreads) void k_deep_log(int W, int H, int tile
                 const int base = log_resolve(blog, sp, atomicAdd(&blog.counters[sp], n), n);
                 ok = base >= 0;
                 if (ok)
-                    for (int q = have; q < need; ++q) chunk_of[q] = base + (q - have);
+                    for (int q = have; q < need; ++q) {
+                        chunk_of[q] = base + (q - have);
+                        if (q < kDeepTbl) s_chunk[q] = base + (q - have);
+                    }
             }
             s_ok = ok;
         }
@@ -902,18 +913,18 @@ __global__ __launch_bounds__(kLogThreads) void k_deep_log(int W, int H, int tile
         for (int q = 0; q < WPT; ++q) {
             const int wd = threadIdx.x * WPT + q;
             s_woff[wd] = woff;
-            for (uint32_t x = s_bits[wd]; x; x &= x - 1u) {
-                const int pos = P0 + 32 * wd + __builtin_ctz(x);
-                reinterpret_cast<uint2 *>(ent_at(nlog + woff))[1] = make_uint2((unsigned)pos, (unsigned)ids[start + pos]);
-                ++woff;
-            }
+            woff += __popc(s_bits[wd]);
         }
         __syncthreads();
         auto rank = [&](int pos) {
             const int b = pos - P0;
             return s_woff[b >> 5] + __popc(s_bits[b >> 5] & ((1u << (b & 31)) - 1u));
         };
-        // 3. ballots, kDeepBal ranks at a time
+        // 3. ballots, kDeepBal ranks at a time.  A pixel's entries are in
+        // list order and ranks grow with the position, so the entries of one
+        // rank range are a run of its list: each pixel keeps a cursor, and
+        // every entry is visited once over all the ranges
+        if (threadIdx.x < 64) s_cur[threadIdx.x] = s_i[threadIdx.x];
         for (int R0 = 0; R0 < n_w; R0 += kDeepBal) {
             for (int r = threadIdx.x; r < kDeepBal; r += kLogThreads) {
                 s_bal[0][r] = 0u;
@@ -923,14 +934,31 @@ __global__ __launch_bounds__(kLogThreads) void k_deep_log(int W, int H, int tile
             for (int p = wv; p < 64; p += kLogWaves) {
                 const int *__restrict__ P_ = dpos + slot_of(p) * kDeepMaxBlend;
                 const int e = s_e[p];
-                for (int i = s_i[p] + lane; i < e; i += 64) {
-                    const int r = rank(P_[i]) - R0;
-                    if (r >= 0 && r < kDeepBal) atomicOr(&s_bal[p >> 5][r], 1u << (p & 31));
+                int i0 = s_cur[p];
+                for (; i0 < e; i0 += 64) {
+                    const int i = i0 + lane;
+                    const int pos = i < e ? P_[i] : 0;
+                    const int r = i < e ? rank(pos) - R0 : INT32_MAX;
+                    const bool in = r < kDeepBal;
+                    if (in) {
+                        atomicOr(&s_bal[p >> 5][r], 1u << (p & 31));
+                        s_pos[r] = pos;  // every pixel that blended rank r writes the same position
+                    }
+                    const unsigned long long past = __ballot(!in);
+                    if (past) {
+                        i0 += (int)__builtin_ctzll(past);  // the first entry of a later range
+                        break;
+                    }
                 }
+                if (lane == 0) s_cur[p] = min(i0, e);
             }
             __syncthreads();
-            for (int r = threadIdx.x; r < min(kDeepBal, n_w - R0); r += kLogThreads)
-                reinterpret_cast<uint2 *>(ent_at(nlog + R0 + r))[0] = make_uint2(s_bal[0][r], s_bal[1][r]);
+            // the range's entries {ballot, list position, gaussian id}, one
+            // 16-byte store each (consecutive ranks: consecutive slots)
+            for (int r = threadIdx.x; r < min(kDeepBal, n_w - R0); r += kLogThreads) {
+                const int pos = s_pos[r];
+                *ent_at(nlog + R0 + r) = make_uint4(s_bal[0][r], s_bal[1][r], (unsigned)pos, (unsigned)ids[start + pos]);
+            }
             __syncthreads();
         }
         // 4. checkpoints up to each pixel entry
