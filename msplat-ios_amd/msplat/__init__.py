@@ -26,7 +26,8 @@ _cleaned_up = False
 
 
 def cleanup():
-    """Release all cached GPU resources. Safe to call multiple times."""
+    """Frees the engine's device buffers, streams and pinned staging memory;
+    later calls do nothing (it also runs at interpreter exit)."""
     global _cleaned_up
     if not _cleaned_up:
         _cleaned_up = True
@@ -51,5 +52,8 @@ __version__ = "1.1.3"
 
 
 def load_dataset(path: str, downscale_factor: float = 1.0, eval_mode: bool = False, test_every: int = 8) -> Dataset:
-    """Load a dataset (auto-detects COLMAP, Nerfstudio, Polycam)."""
+    """A Dataset from a capture directory, its format (COLMAP, Nerfstudio or
+    Polycam) detected from the files present; images are box-downscaled by
+    downscale_factor, and with eval_mode every test_every-th image is held
+    out."""
     return Dataset(path, downscale_factor, eval_mode, test_every)
