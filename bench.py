@@ -252,8 +252,10 @@ def gpu_train3d(workload: int, steps: int, warmup: int, render_frames: int):
     E.sync()
     for k in range(warmup):
         D.train_step3d(ds, cams[k % len(cams)], gts[k % len(cams)])
+    redos = E.log_pool_stats()["redos"]
     ms_per_step, losses, isect = _timed_steps(E, lambda ci: D.train_step3d(ds, cams[ci], gts[ci]), warmup, steps,
                                               len(cams))
+    pool = log_pool(E, redos)
     stage_ms = _stage_breakdown(E, lambda ci: D.train_step3d(ds, cams[ci], gts[ci]), warmup + steps,
                                 min(steps, 10), len(cams))
     del gts
@@ -269,7 +271,7 @@ def gpu_train3d(workload: int, steps: int, warmup: int, render_frames: int):
     E.sync()
     render_ms = (time.perf_counter() - t0) * 1e3 / max(render_frames, 1)
     return dict(scene=scene, ms_per_step=ms_per_step, losses=losses, isect=float(np.mean(isect)),
-                stage_ms=stage_ms, render_ms=render_ms)
+                stage_ms=stage_ms, render_ms=render_ms, log_pool=pool)
 
 
 def gpu_render_ms(ds, cams, frames: int) -> float:
@@ -752,6 +754,7 @@ def main() -> int:
         r = gpu_train3d(3, args.steps, args.warmup, args.render_frames)
         print(json.dumps({"workload": r["scene"].name, "ms_per_step": round(r["ms_per_step"], 3),
                           "render_ms": round(r["render_ms"], 3), "intersections_mean": int(r["isect"]),
+                          "blend_log_pool": r["log_pool"],
                           "stage_ms": {k: round(v, 4) for k, v in r["stage_ms"].items()},
                           "loss_first_last": [round(r["losses"][0], 6), round(r["losses"][-1], 6)]}))
         return 0
@@ -862,6 +865,7 @@ def main() -> int:
                               "ms_per_step": round(r3["ms_per_step"], 3),
                               "render_fps": round(1000.0 / r3["render_ms"], 2),
                               "render_ms": round(r3["render_ms"], 3),
+                              "blend_log_pool": r3["log_pool"],
                               "kernels": issue_table(r3["stage_ms"], sc3.name),
                               "loss_first_last": [round(r3["losses"][0], 6), round(r3["losses"][-1], 6)]}
         log(f"{sc3.name}: {r3['ms_per_step']:.3f} ms/step, render {r3['render_ms']:.3f} ms")

@@ -126,10 +126,12 @@ struct Engine {
     int64_t log_init = 0;  // estimate override in chunks (0: from the frame)
     int64_t log_redos = 0; // overflowed logs since init
     int64_t log_demand = 0;  // chunks the last fitting log claimed
-    double log_fill = 0.0;   // the largest demand / static estimate seen
+    // the largest demand / static estimate seen, per mode (2DGS, 3DGS):
+    // their splats cover tiles differently
+    double log_fill[2] = {0.0, 0.0};
     msr::BlendLog log_desc{};  // the current frame's pool layout
     hipStream_t deep_stream = nullptr;  // default priority, non-blocking
-    hipEvent_t deep_fork = nullptr, deep_join = nullptr;
+    hipEvent_t deep_fork = nullptr, deep_join = nullptr, deep_logged = nullptr;
     hipEvent_t ev[ST_COUNT + 1] = {};
     float stage_ms[ST_COUNT] = {};
     bool stage_valid[ST_COUNT] = {};
@@ -312,6 +314,7 @@ int deep_tiles(mskern::DeepTiles &deep) {
         HIPC(hipStreamCreateWithFlags(&E.deep_stream, hipStreamNonBlocking));
         HIPC(hipEventCreateWithFlags(&E.deep_fork, hipEventDisableTiming));
         HIPC(hipEventCreateWithFlags(&E.deep_join, hipEventDisableTiming));
+        HIPC(hipEventCreateWithFlags(&E.deep_logged, hipEventDisableTiming));
     }
     deep.n = E.n_deep;
     deep.len = E.deep_len;
@@ -319,6 +322,7 @@ int deep_tiles(mskern::DeepTiles &deep) {
     deep.stream = E.deep_stream;
     deep.fork = E.deep_fork;
     deep.join = E.deep_join;
+    deep.logged = E.deep_logged;
     return MSPLAT_OK;
 }
 
@@ -345,7 +349,7 @@ int64_t log_max_chunks(const Engine &E) {
 // largest pool.  The estimate is a static one (about a sixth of the worst
 // case; the training step at 3M splats claims 45-62% of it) until a log
 // fitted, then that scaled by 1.25 times the largest ratio of claimed chunks
-// to it seen so far (log_fill).  A step whose log overflows is redone
+// to it seen so far in the frame's mode (log_fill).  A step whose log overflows is redone
 // after the pool grows (grow_log_pool).  Planned by each forward that logs;
 // the backward reads the log through the plan kept in log_desc.
 int plan_log_pool(msr::BlendLog &L) {
@@ -357,8 +361,9 @@ int plan_log_pool(msr::BlendLog &L) {
         return MSPLAT_E_ARG;
     }
     const int64_t base = log_static_estimate(E);
+    const double fill = E.log_fill[E.gs3d];
     const int64_t estimate = E.log_init          ? E.log_init
-                             : E.log_fill > 0.0 ? std::max<int64_t>(1024, (int64_t)std::ceil(1.25 * E.log_fill * (double)base))
+                             : fill > 0.0       ? std::max<int64_t>(1024, (int64_t)std::ceil(1.25 * fill * (double)base))
                                                 : base;
     const int64_t cap = std::min(std::max(E.log_cap, estimate), most);
     E.log_used = cap;
@@ -396,7 +401,8 @@ bool log_account(const msr::BlendLog &L) {
     int64_t demand = 0;
     for (int i = 0; i < L.nsub; ++i) demand += g_eng.pinned_ctr[i];
     E.log_demand = demand;
-    E.log_fill = std::max(E.log_fill, (double)demand / (double)log_static_estimate(E));
+    double &fill = E.log_fill[E.gs3d];
+    fill = std::max(fill, (double)demand / (double)log_static_estimate(E));
     return false;
 }
 
@@ -774,7 +780,7 @@ void msplat_hip_cleanup(void) {
     E.n_deep = 0;
     E.log_cap = 0;
     E.log_used = 0;
-    E.log_fill = 0.0;
+    E.log_fill[0] = E.log_fill[1] = 0.0;
     E.log_desc = msr::BlendLog{};
     E.n = 0;
     E.num_isect = 0;

@@ -1028,9 +1028,11 @@ void launch_raster_fwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
             full_outputs ? launch_deep(k_raster_deep<false, true>) : launch_deep(k_raster_deep<false, false>);
         const bool defer = blog && deep.defer_log;
         if (defer) (void)hipEventRecord(deep.join, sd);
-        if (blog)
+        if (blog) {
             hipLaunchKernelGGL(k_deep_log, dim3(deep.n * 4), dim3(kLogThreads), 0, sd, W, H, tiles_x, deep.n, deep.list,
                                offsets, ids, deep.pos, deep.tb, deep.cnt, final_Ts, lg);
+            (void)hipEventRecord(deep.logged, sd);
+        }
         if (!defer) (void)hipEventRecord(deep.join, sd);
     }
     auto launch = [&](auto kern) {
@@ -1084,7 +1086,9 @@ bool launch_raster_bwd(hipStream_t s, int W, int H, int tiles_x, int tiles_y, co
     if (deep.n > 0) {
         // the deep tiles' long log replays start at once, on their own
         // stream, beside the rest (after the deep tiles' log rebuild, if
-        // the forward left it running there)
+        // the forward left it running there: the per-tile launch waits for
+        // the rebuild too, so that both launches start together)
+        (void)hipStreamWaitEvent(s, deep.logged, 0);
         (void)hipEventRecord(deep.fork, s);
         (void)hipStreamWaitEvent(deep.stream, deep.fork, 0);
         launch(deep.stream, deep.n, deep.list, 0);

@@ -112,9 +112,13 @@ struct DeepTiles {
     // defer_log the forward's `join` follows the deep tiles' outputs only
     // and their blend logs (k_deep_log) are rebuilt after it on `stream`,
     // where the raster backward's deep part follows them (the caller's
-    // stream reaches them through the backward's `join`)
+    // stream reaches them through the backward's `join`).  `logged` is
+    // recorded on `stream` after every log rebuild; the backward's per-tile
+    // part waits for it, so the rebuild's large workgroups are not starved
+    // of CUs by the per-tile launch (which would delay the deep part behind
+    // the whole per-tile backward)
     hipStream_t stream = nullptr;
-    hipEvent_t fork = nullptr, join = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr, logged = nullptr;
     bool defer_log = false;
 };
 void launch_deep_tiles(hipStream_t s, int T, const int *offsets, int deep_len, int *deep_list, int *count);
