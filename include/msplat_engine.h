@@ -346,11 +346,12 @@ int msplat_hip_check_fast_rcp(int efield_lo, int efield_hi, int64_t *mismatches)
  * lists are the same either way.  No counterpart in the reference. */
 int msplat_hip_set_wide_keys(int on);
 /* Rasterizer self-test hook.  Tiles whose list holds at least len entries
- * (4096 by default) are rendered pixel by pixel, each 2x2 pixel block on its
- * own wave, instead of by one workgroup per tile; the outputs, blend log and
- * checkpoints are the same either way.  A small len sends ordinary tiles
- * down that path, so the tests can check it on small scenes; len <= 0
- * restores the default.  No counterpart in the reference. */
+ * are rendered pixel by pixel, each 2x2 pixel block on its own wave, instead
+ * of by one workgroup per tile; the outputs, blend log and checkpoints are
+ * the same either way.  A small len sends ordinary tiles down that path, so
+ * the tests can check it on small scenes; len <= 0 restores the default
+ * (lists of at least 4096 entries and 4x the frame's mean list).  No
+ * counterpart in the reference. */
 int msplat_hip_set_deep_tile_len(int len);
 /* Blend-log pool self-test hook.  A frame's pool holds `chunks` chunks of
  * 64 entries instead of the size estimated from its intersection count, or

@@ -56,7 +56,13 @@ constexpr size_t kD2HChunk = size_t(8) << 20;  // bytes per pinned download chun
 
 // Deep-tile threshold: no tile of the 500k and 3M-splat blob workloads holds
 // more than 3.3k entries; the overflow workload's cluster tiles hold up to 200k.
+// By default a deep tile also holds 4x the frame's mean list: the deep path's
+// per-pixel lists and log rebuild pay off only for lists far above the rest
+// (measured: the densify workload's end, 62 tiles of 4.4k-5.3k entries against
+// a 1.6k mean, trains 4% faster with them per tile; the overflow workload's
+// forward slows from 0.65 to 0.68 ms with a 6144 threshold instead of 4096).
 constexpr int kDefaultDeepLen = 4096;
+constexpr int kDeepMeanFactor = 4;
 
 struct Engine {
     bool ready = false;
@@ -113,9 +119,12 @@ struct Engine {
     bool count_pairs = false;  // raster pair counter
     bool defer_deep_log = false;  // set by the training step around its forward
     bool wide_keys = false;    // binning test hook: the wide key layout at any N
-    // tiles whose list holds at least deep_len entries are rendered pixel by
-    // pixel (mskern::DeepTiles); n_deep of them in the current frame
-    int deep_len = kDefaultDeepLen, n_deep = 0;
+    // tiles whose list holds at least deep_frame entries are rendered pixel
+    // by pixel (mskern::DeepTiles); n_deep of them in the current frame.
+    // deep_frame is deep_len when a test set it (deep_len_set), else the
+    // larger of deep_len and kDeepMeanFactor x the frame's mean list
+    int deep_len = kDefaultDeepLen, deep_frame = kDefaultDeepLen, n_deep = 0;
+    bool deep_len_set = false;
     DevBuf deep_list, deep_pos, deep_tb, deep_cnt;
     // blend-log pool (msr::BlendLog): blend_log / t_ckpt hold log_used chunks
     // of 64 entries / checkpoints, log_table the per-wave chunk tables,
@@ -317,7 +326,7 @@ int deep_tiles(mskern::DeepTiles &deep) {
         HIPC(hipEventCreateWithFlags(&E.deep_logged, hipEventDisableTiming));
     }
     deep.n = E.n_deep;
-    deep.len = E.deep_len;
+    deep.len = E.deep_frame;
     deep.list = P<int>(E.deep_list);
     deep.stream = E.deep_stream;
     deep.fork = E.deep_fork;
@@ -576,12 +585,14 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
         CHECK(ensure(E.chunk_base, (size_t)NS * 4));
         CHECK(ensure(E.chunk_counts, (size_t)mskern::big_chunk_ints(S_total, NS) * 4));
     }
+    E.deep_frame = E.deep_len_set ? E.deep_len
+                                  : (int)std::max<int64_t>(E.deep_len, kDeepMeanFactor * (int64_t)I / T);
     // a tile's list is at most its super-tile's: no deep tile below that
-    const bool scan_deep = !gs3d && super_max >= E.deep_len;
+    const bool scan_deep = !gs3d && super_max >= E.deep_frame;
     mskern::DeepScan dscan;
     if (scan_deep) {
         CHECK(ensure(E.deep_list, (size_t)T * 4));
-        dscan.len = E.deep_len;
+        dscan.len = E.deep_frame;
         dscan.list = P<int>(E.deep_list);
         dscan.count = P<int>(E.stats) + 14;
         dscan.host_count = E.pinned_i + 14;
@@ -1591,6 +1602,7 @@ int msplat_hip_set_deep_tile_len(int len) {
     API_BEGIN
     ENSURE_INIT();
     g_eng.deep_len = len > 0 ? len : kDefaultDeepLen;
+    g_eng.deep_len_set = len > 0;
     return MSPLAT_OK;
     API_END
 }
