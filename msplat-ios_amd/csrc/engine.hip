@@ -617,11 +617,13 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
 int loss_locked(int W, int H, const float *img, const float *gt, const float *dist, float l1, float ldist,
                 float ldssim, float *dL) {
     Engine &E = g_eng;
-    const size_t E3 = (size_t)W * H * 3;
-    CHECK(ensure(E.gm1, E3 * 4));
-    CHECK(ensure(E.gs1, E3 * 4));
-    CHECK(ensure(E.gs12, E3 * 4));
-    CHECK(ensure(E.partials, (size_t)mskern::ssim_num_blocks(W, H) * 16));
+    if (mskern::loss_needs_maps(W, H)) {
+        const size_t E3 = (size_t)W * H * 3;
+        CHECK(ensure(E.gm1, E3 * 4));
+        CHECK(ensure(E.gs1, E3 * 4));
+        CHECK(ensure(E.gs12, E3 * 4));
+    }
+    CHECK(ensure(E.partials, (size_t)mskern::loss_num_partials(W, H) * 16));
     CHECK(ensure(E.loss, 16));
     mskern::launch_loss_fwd_bwd(E.stream, W, H, img, gt, dist, l1, ldist, ldssim, E.window, P<float>(E.gm1),
                                 P<float>(E.gs1), P<float>(E.gs12), P<double>(E.partials), P<double>(E.loss), dL);
@@ -1468,7 +1470,7 @@ int msplat_hip_loss_fwd_bwd_noalloc(int W, int H, const float *img, const float 
                 (long long)pixels, (long long)kNoAllocMaxPixels);
         return MSPLAT_E_CAPACITY;
     }
-    if ((int64_t)mskern::ssim_num_blocks(W, H) > kNoAllocMaxBlocks) {
+    if ((int64_t)mskern::loss_num_partials(W, H) > kNoAllocMaxBlocks) {
         set_err("loss_fwd_bwd_noalloc: %dx%d needs more than %lld tiles", W, H, (long long)kNoAllocMaxBlocks);
         return MSPLAT_E_CAPACITY;
     }
@@ -1584,6 +1586,14 @@ int msplat_hip_set_wide_keys(int on) {
     API_BEGIN
     ENSURE_INIT();
     g_eng.wide_keys = on != 0;
+    return MSPLAT_OK;
+    API_END
+}
+
+int msplat_hip_set_loss_two_pass(int on) {
+    API_BEGIN
+    ENSURE_INIT();
+    mskern::set_loss_two_pass(on != 0);
     return MSPLAT_OK;
     API_END
 }

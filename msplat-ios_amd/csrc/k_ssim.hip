@@ -1,31 +1,37 @@
 // k_ssim.hip -- SSIM (11-tap Gaussian, sigma 1.5, zero padding) + L1 loss,
-// forward and backward, in two LDS-tiled passes.
+// forward and backward.
 //
 // The reference runs 19 separate dispatches per step over 19 full-image
 // scratch buffers (ssim_prep_products, 5+3 separable blur pairs,
 // ssim_compute, loss_l1_distortion, ssim_backward_compute/accumulate;
 // msplat_metal.metal:2704-3085, msplat_metal.mm:1077-1212).  Because
 // dL/dssim_map is a known constant (-lambda / 3HW), the per-pixel SSIM
-// partials can be produced in the same pass as the forward statistics:
-//   pass 1 (k_ssim_fwd): per channel, img and gt (+5-pixel halo) -> the 5
+// partials can be produced in the same pass as the forward statistics, and
+// the backward needs nothing else.  Two forms:
+//   - k_ssim_stream (every image whose buffer offsets fit in 32 bits): one
+//     kernel, one wave per (column strip, row segment, channel), carrying
+//     each pixel from its inputs to dL/dimg while the wave walks down the
+//     strip with the vertical blur windows in registers (see the section
+//     below);
+//   - the two-pass form for larger images:
+//     pass 1 (k_ssim_fwd): per channel, img and gt (+5-pixel halo) -> the 5
 //          separable blurs (horizontal, then vertical, as the reference) ->
 //          SSIM map, loss partials and the three per-pixel gradient maps
 //          (d/dmu1 folded, d/dsigma1^2, d/dsigma12), stored channel-planar;
-//   pass 2 (k_ssim_bwd): per channel the three planar maps (+halo) ->
+//     pass 2 (k_ssim_bwd): per channel the three planar maps (+halo) ->
 //          adjoint blur (the same symmetric blur) + the L1 gradient; the
 //          three channels of a pixel stay in one thread, so dL/dimg is
 //          written once, interleaved.
-// Both passes work on 32x32 output tiles one channel at a time (46 / 24 KB
-// of LDS) with register blocking: a horizontal work item produces 4
-// adjacent outputs from 14 staged inputs, a vertical one 4 outputs of a
-// column from 14 rows, each output accumulating its taps in ascending order
-// (the order of the reference's blur kernels).  Pass 1 loads the three
-// channels of its region at once (each cache line of the interleaved images
-// is fetched once), and both passes walk the tiles in XCD bands
-// (msd::xcd_tile), so a tile's halo is mostly its neighbours' lines, already
-// in the same L2.
-// HBM traffic per pixel: 24 B in + 36 B out (pass 1), 36 + 24 B in + 12 B
-// out (pass 2), plus the halo re-reads of neighbouring tiles.
+//     Both passes work on 32x32 output tiles one channel at a time (46 / 24
+//     KB of LDS) with register blocking: a horizontal work item produces 4
+//     adjacent outputs from 14 staged inputs, a vertical one 4 outputs of a
+//     column from 14 rows.  Pass 1 loads the three channels of its region at
+//     once (each cache line of the interleaved images is fetched once), and
+//     both passes walk the tiles in XCD bands (msd::xcd_tile), so a tile's
+//     halo is mostly its neighbours' lines, already in the same L2.
+// In both forms each output accumulates its taps in ascending order (the
+// order of the reference's blur kernels), so they give the same dL/dimg
+// bit for bit.
 #include "kernels.h"
 #include "ms_device.h"
 
@@ -379,6 +385,330 @@ __global__ __launch_bounds__(kThreads) void k_ssim_bwd(int W, int H, const float
     }
 }
 
+// ---------------------------------------------------------------------------
+// One-kernel form (k_ssim_stream): forward statistics, SSIM partials and
+// the adjoint blur in one pass.  Because dL/dssim_map is the constant
+// -lambda / 3HW, the backward needs nothing but the partial maps, and a
+// partial map is needed only 5 pixels around where it is made, so a single
+// wave can carry a pixel from its inputs to dL/dimg while it walks down a
+// column strip:
+//   - one wave per (column strip, row segment, channel); its 64 lanes are
+//     the 64 forward columns x0 - 5 .. x0 + 58 of the strip, whose partials
+//     the adjoint blur of the 54 output columns x0 .. x0 + 53 needs;
+//   - the rows stream through in passes of 4: the horizontal blur of the
+//     staged inputs (a lane takes 4 adjacent columns of one row, 14 staged
+//     inputs), then per row the vertical blur from a ring of the last 11
+//     horizontal results in the lane's registers, the SSIM partials, the
+//     horizontal adjoint blur of the partials (staged) and the vertical one
+//     from a second register ring; input row i makes the partials of row
+//     i - 5 and dL/dimg of row i - 10;
+//   - every row's horizontal results are made once (no vertical halo is
+//     recomputed except the 20 rows at a segment's start) and the partial
+//     maps never leave the CU.
+// The ring slot of row i is i mod 11 within an 11-row loop body of passes
+// of 4, 4 and 3 rows, so every register index is a compile-time constant.
+// Each tap still accumulates in ascending order, as in the two-pass form and
+// the reference, so dL/dimg is the same bit for bit.  Inputs are read with
+// buffer loads whose out-of-range lanes return 0: rows above or below the
+// image and columns outside it (their offsets are pushed past the buffer)
+// are the zero padding.
+constexpr int kSW = 64;               // forward columns of a strip (= lanes)
+constexpr int kSO = kSW - 2 * RAD;    // 54 output columns of a strip
+constexpr int kSIn = kSW + 2 * RAD;   // 74 staged input columns
+constexpr int kInSt = 80;             // LDS row stride of a staged input row
+constexpr int kPtSt = 68;             // LDS row stride of a partials row (reads reach column 65)
+constexpr int kRing = 2 * RAD + 1;    // 11 rows of a vertical window = the ring period
+constexpr int kPassRows = 4;
+constexpr int kLoads = (kPassRows * kSIn + 63) / 64;  // 5 staged inputs per lane per image
+constexpr uint32_t kOffPast = 0xC0000000u;  // offset base of a lane whose column is outside the image
+
+struct StreamLds {
+    float in[2][kPassRows][kInSt];   // staged img / gt rows of this pass
+    float hf[5][kPassRows][kSW];     // horizontal blurs of mu1, mu2, x1^2, x2^2, x1 x2
+    float pt[3][kPassRows][kPtSt];   // SSIM partials (d/dmu1 folded, d/dsigma1^2, d/dsigma12)
+    float hb[3][kPassRows][kSW];     // horizontal adjoint blurs of the partials
+};
+
+struct StreamArgs {
+    int W, H, nstrips, seg_rows, units;
+    float lambda_l1, lambda_dist, inv_np, inv_HW, g;
+};
+
+struct StreamState {
+    float hv[5][kRing];             // this lane's column of the last 11 horizontal forward rows
+    float gv[3][kRing];             // ... of the last 11 horizontal adjoint rows
+    uint32_t ao;                    // byte offset of output column x0 + lane, channel c, at row 0
+    float na[kLoads], nb[kLoads];   // the next pass's staged inputs, loaded one pass ahead
+    uint32_t lo[kLoads];            // byte offsets of those inputs at input row 0
+    int so[kLoads];                 // their LDS slots (row * kInSt + column), -1 if none
+    double ssim_acc, l1_acc;
+};
+
+__device__ __forceinline__ void stream_load(StreamState &S, __amdgpu_buffer_rsrc_t rimg,
+                                            __amdgpu_buffer_rsrc_t rgt, uint32_t row_off) {
+#pragma unroll
+    for (int m = 0; m < kLoads; ++m) {
+        const uint32_t off = S.lo[m] + row_off;
+        S.na[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rimg, off, 0, 0));
+        S.nb[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rgt, off, 0, 0));
+    }
+}
+
+// One pass of NP input rows starting at input row ib (slots P0 .. P0+NP-1
+// of the ring).
+template <int P0, int NP>
+__device__ __forceinline__ void stream_pass(const StreamArgs &A, const Window &win, StreamLds &L, StreamState &S,
+                                            __amdgpu_buffer_rsrc_t rimg, __amdgpu_buffer_rsrc_t rgt, int ib, int x0,
+                                            int y0, int y1, int c, const float *__restrict__ dist,
+                                            float *__restrict__ dL) {
+    const int lane = threadIdx.x;
+    const float C1 = 0.0001f, C2 = 0.0009f;
+    // img / gt at the output rows of this pass (rows ib - 10 ..): lines this
+    // wave read ten rows ago, loaded again (the cache's copy) rather than
+    // kept in registers
+    float fa[NP], fb[NP];
+#pragma unroll
+    for (int rr = 0; rr < NP; ++rr) {
+        const uint32_t off = S.ao + (uint32_t)(ib + rr - 2 * RAD) * (uint32_t)A.W * 12u;
+        fa[rr] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rimg, off, 0, 0));
+        fb[rr] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rgt, off, 0, 0));
+    }
+    // stage this pass's rows, then start loading the next pass's
+#pragma unroll
+    for (int m = 0; m < kLoads; ++m)
+        if (S.so[m] >= 0) {
+            (&L.in[0][0][0])[S.so[m]] = S.na[m];
+            (&L.in[1][0][0])[S.so[m]] = S.nb[m];
+        }
+    stream_load(S, rimg, rgt, (uint32_t)(ib + NP) * (uint32_t)A.W * 12u);
+    __syncthreads();
+    // horizontal pass of ssim_blur_horiz_kernel (msplat_metal.metal:2847-2873):
+    // lane (r, q) makes columns 4q .. 4q + 3 of row r
+    {
+        const int r = lane >> 4, q = lane & 15;
+        if (r < NP) {
+            float a[16], b[16];
+            lds_row14(&L.in[0][r][4 * q], a);
+            lds_row14(&L.in[1][r][4 * q], b);
+            float m1[4] = {0.f, 0.f, 0.f, 0.f}, m2[4] = {0.f, 0.f, 0.f, 0.f}, e11[4] = {0.f, 0.f, 0.f, 0.f},
+                  e22[4] = {0.f, 0.f, 0.f, 0.f}, e12[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 11; ++j) {
+                const float w = win.w[j];
+#pragma unroll
+                for (int o = 0; o < 4; ++o) {
+                    const float av = a[o + j], bv = b[o + j];
+                    m1[o] = __builtin_fmaf(w, av, m1[o]);
+                    m2[o] = __builtin_fmaf(w, bv, m2[o]);
+                    e11[o] = __builtin_fmaf(w, av * av, e11[o]);
+                    e22[o] = __builtin_fmaf(w, bv * bv, e22[o]);
+                    e12[o] = __builtin_fmaf(w, av * bv, e12[o]);
+                }
+            }
+            *reinterpret_cast<float4 *>(&L.hf[0][r][4 * q]) = make_float4(m1[0], m1[1], m1[2], m1[3]);
+            *reinterpret_cast<float4 *>(&L.hf[1][r][4 * q]) = make_float4(m2[0], m2[1], m2[2], m2[3]);
+            *reinterpret_cast<float4 *>(&L.hf[2][r][4 * q]) = make_float4(e11[0], e11[1], e11[2], e11[3]);
+            *reinterpret_cast<float4 *>(&L.hf[3][r][4 * q]) = make_float4(e22[0], e22[1], e22[2], e22[3]);
+            *reinterpret_cast<float4 *>(&L.hf[4][r][4 * q]) = make_float4(e12[0], e12[1], e12[2], e12[3]);
+        }
+    }
+    __syncthreads();
+    // per row: vertical pass + ssim_compute_kernel (:2910-2952) +
+    // ssim_backward_compute_kernel (:2965-3047) for row j = i - 5
+    const int fx = x0 - RAD + lane;
+    const bool fcol = (unsigned)fx < (unsigned)A.W;
+    const bool fown = fcol && lane >= RAD && lane < RAD + kSO;
+    // the vertical blurs of all NP rows, then their partials side by side
+    // (independent chains for the issue to interleave), with one
+    // wave-uniform branch for the pass's reciprocals
+    float st[NP][5];
+#pragma unroll
+    for (int rr = 0; rr < NP; ++rr) {
+        const int p = P0 + rr;
+#pragma unroll
+        for (int s = 0; s < 5; ++s) S.hv[s][p] = L.hf[s][rr][lane];
+#pragma unroll
+        for (int s = 0; s < 5; ++s) {
+            float acc = 0.f;
+#pragma unroll
+            for (int k = 0; k < kRing; ++k) acc = __builtin_fmaf(win.w[k], S.hv[s][(p + 1 + k) % kRing], acc);
+            st[rr][s] = acc;
+        }
+    }
+    float A_[NP], B[NP], AB[NP], CD[NP], Cd[NP], Dd[NP], inv_CD[NP], inv_Cd[NP], inv_Dd[NP];
+    bool odd = false;
+#pragma unroll
+    for (int rr = 0; rr < NP; ++rr) {
+        const float m1 = st[rr][0], m2 = st[rr][1];
+        const float m1_sq = m1 * m1, m2_sq = m2 * m2, m1m2 = m1 * m2;
+        const float s1_sq = st[rr][2] - m1_sq, s2_sq = st[rr][3] - m2_sq, s12 = st[rr][4] - m1m2;
+        A_[rr] = 2.0f * m1m2 + C1;
+        B[rr] = 2.0f * s12 + C2;
+        Cd[rr] = m1_sq + m2_sq + C1;
+        Dd[rr] = s1_sq + s2_sq + C2;
+        CD[rr] = Cd[rr] * Dd[rr];
+        AB[rr] = A_[rr] * B[rr];
+        // the correctly rounded reciprocals (as msd::ms_recip)
+        inv_CD[rr] = msd::ms_rcp_nr(CD[rr]);
+        inv_Cd[rr] = msd::ms_rcp_nr(Cd[rr]);
+        inv_Dd[rr] = msd::ms_rcp_nr(Dd[rr]);
+        odd = odd || !(msd::ms_rcp_nr_exact(CD[rr]) && msd::ms_rcp_nr_exact(Cd[rr]) && msd::ms_rcp_nr_exact(Dd[rr]));
+    }
+    if (__builtin_amdgcn_ballot_w64(odd)) {
+#pragma unroll
+        for (int rr = 0; rr < NP; ++rr) {
+            float z0 = CD[rr], z1 = Cd[rr], z2 = Dd[rr];
+            asm volatile("" : "+v"(z0), "+v"(z1), "+v"(z2));  // keeps the divisions inside the branch
+            if (!(msd::ms_rcp_nr_exact(z0) && msd::ms_rcp_nr_exact(z1) && msd::ms_rcp_nr_exact(z2))) {
+                inv_CD[rr] = 1.0f / z0;
+                inv_Cd[rr] = 1.0f / z1;
+                inv_Dd[rr] = 1.0f / z2;
+            }
+        }
+    }
+#pragma unroll
+    for (int rr = 0; rr < NP; ++rr) {
+        const int jrow = ib + rr - RAD;
+        const bool live = fcol && (unsigned)jrow < (unsigned)A.H;
+        const float m1 = st[rr][0], m2 = st[rr][1];
+        const float val = AB[rr] * inv_CD[rr];
+        if (fown && jrow >= y0 && jrow < y1) S.ssim_acc += (double)val;
+        const float dmu1 = 2.0f * inv_CD[rr] * (m2 * B[rr] - m1 * AB[rr] * inv_Cd[rr]);
+        const float ds12 = 2.0f * A_[rr] * inv_CD[rr];
+        const float ds1 = -AB[rr] * inv_CD[rr] * inv_Dd[rr];
+        float gm = A.g * dmu1;
+        const float g12 = A.g * ds12, g1 = A.g * ds1;
+        gm += g1 * (-2.0f * m1);
+        gm += g12 * (-m2);
+        // the partial maps are zero outside the image (the reference's
+        // adjoint blur skips those taps)
+        L.pt[0][rr][lane] = live ? gm : 0.f;
+        L.pt[1][rr][lane] = live ? g1 : 0.f;
+        L.pt[2][rr][lane] = live ? g12 : 0.f;
+    }
+    __syncthreads();
+    // horizontal adjoint blur (the same symmetric window): lane (r, q)
+    // makes output columns 4q .. 4q + 3 (q < 14) of row r
+    {
+        const int r = lane >> 4, q = lane & 15;
+        if (r < NP && q < (kSO + 3) / 4) {
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+                float v[16];
+                lds_row14(&L.pt[m][r][4 * q], v);
+                float h[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 11; ++j)
+#pragma unroll
+                    for (int o = 0; o < 4; ++o) h[o] = __builtin_fmaf(win.w[j], v[o + j], h[o]);
+                *reinterpret_cast<float4 *>(&L.hb[m][r][4 * q]) = make_float4(h[0], h[1], h[2], h[3]);
+            }
+        }
+    }
+    __syncthreads();
+    // per row: vertical adjoint blur + ssim_backward_accumulate_kernel
+    // (:3059-3085) + the L1 gradient and loss of output row o = i - 10
+    const int ox = x0 + lane;
+    const bool ocol = lane < kSO && ox < A.W;
+    float bl[NP][3];
+#pragma unroll
+    for (int rr = 0; rr < NP; ++rr) {
+        const int p = P0 + rr;
+#pragma unroll
+        for (int m = 0; m < 3; ++m) S.gv[m][p] = L.hb[m][rr][lane];
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            float acc = 0.f;
+#pragma unroll
+            for (int k = 0; k < kRing; ++k) acc = __builtin_fmaf(win.w[k], S.gv[m][(p + 1 + k) % kRing], acc);
+            bl[rr][m] = acc;
+        }
+    }
+#pragma unroll
+    for (int rr = 0; rr < NP; ++rr) {
+        const int orow = ib + rr - 2 * RAD;
+        if (ocol && orow >= y0 && orow < y1) {
+            const float a = fa[rr], b = fb[rr];
+            const float diff = a - b;
+            const float sgn = (diff > 0.0f) ? 1.0f : ((diff < 0.0f) ? -1.0f : 0.0f);
+            const float contrib = bl[rr][0] + 2.0f * a * bl[rr][1] + b * bl[rr][2];
+            const size_t px = (size_t)orow * A.W + ox;
+            dL[px * 3 + c] = A.lambda_l1 * sgn * A.inv_np + contrib;
+            // loss_l1_distortion_2dgs_kernel (:2704-2762); the distortion
+            // term once per pixel, with channel 0
+            double l = (double)(A.lambda_l1 * __builtin_fabsf(diff) * A.inv_np);
+            if (dist && c == 0) l += (double)(A.lambda_dist * dist[px] * A.inv_HW);
+            S.l1_acc += l;
+        }
+    }
+}
+
+__global__ __launch_bounds__(64) void k_ssim_stream(StreamArgs A, Window win, const float *__restrict__ img,
+                                                    const float *__restrict__ gt, const float *__restrict__ dist,
+                                                    float *__restrict__ dL, double *__restrict__ partials) {
+    __shared__ __align__(16) StreamLds L;
+    // units (segment, strip, channel), channel fastest, in 8 XCD bands: the
+    // three channel waves of a strip and its neighbouring strips, which
+    // read the same input lines, run in one XCD's L2
+    const int per = (A.units + 7) >> 3;
+    const int u = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+    if (u >= A.units) return;
+    const int c = u % 3, ss = u / 3;
+    const int strip = ss % A.nstrips, seg = ss / A.nstrips;
+    const int x0 = strip * kSO, y0 = seg * A.seg_rows;
+    const int y1 = y0 + A.seg_rows < A.H ? y0 + A.seg_rows : A.H;
+    const int lane = threadIdx.x;
+    // zero the LDS once: the columns past the written ones of the partials
+    // and adjoint rows are read (and ignored) by the last lanes
+    {
+        float *z = &L.in[0][0][0];
+        constexpr int n = (int)(sizeof(StreamLds) / sizeof(float));
+        for (int k = lane; k < n; k += 64) z[k] = 0.f;
+    }
+    StreamState S;
+#pragma unroll
+    for (int k = 0; k < kRing; ++k) {
+#pragma unroll
+        for (int s = 0; s < 5; ++s) S.hv[s][k] = 0.f;
+#pragma unroll
+        for (int m = 0; m < 3; ++m) S.gv[m][k] = 0.f;
+    }
+    S.ssim_acc = 0.0;
+    S.l1_acc = 0.0;
+    S.ao = (uint32_t)((x0 + lane) * 12 + 4 * c);
+#pragma unroll
+    for (int m = 0; m < kLoads; ++m) {
+        const int k = lane + 64 * m;
+        const int r = k / kSIn, col = k - r * kSIn;
+        const int x = x0 - 2 * RAD + col;
+        const bool ok = k < kPassRows * kSIn;
+        S.so[m] = ok ? r * kInSt + col : -1;
+        S.lo[m] = ok && (unsigned)x < (unsigned)A.W ? (uint32_t)((r * A.W + x) * 12 + 4 * c) : kOffPast;
+    }
+    const uint32_t nrec = (uint32_t)A.W * (uint32_t)A.H * 12u;
+    const __amdgpu_buffer_rsrc_t rimg = __builtin_amdgcn_make_buffer_rsrc((void *)img, (short)0, nrec, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rgt = __builtin_amdgcn_make_buffer_rsrc((void *)gt, (short)0, nrec, 0x00020000);
+    const int ib0 = y0 - 2 * RAD;
+    stream_load(S, rimg, rgt, (uint32_t)ib0 * (uint32_t)A.W * 12u);
+    const int nbody = (y1 - y0 + 4 * RAD + kRing - 1) / kRing;
+    for (int bi = 0; bi < nbody; ++bi) {
+        const int ib = ib0 + bi * kRing;
+        stream_pass<0, 4>(A, win, L, S, rimg, rgt, ib, x0, y0, y1, c, dist, dL);
+        stream_pass<4, 4>(A, win, L, S, rimg, rgt, ib + 4, x0, y0, y1, c, dist, dL);
+        stream_pass<8, 3>(A, win, L, S, rimg, rgt, ib + 8, x0, y0, y1, c, dist, dL);
+    }
+    double ts = S.ssim_acc, tl = S.l1_acc;
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) {
+        ts += __shfl_xor(ts, d, 64);
+        tl += __shfl_xor(tl, d, 64);
+    }
+    if (lane == 0) {
+        partials[2 * u] = ts;
+        partials[2 * u + 1] = tl;
+    }
+}
+
 // Fixed-order fp64 reduction of the per-workgroup partials.
 __global__ __launch_bounds__(1024) void k_loss_final(int nblocks, const double *__restrict__ partials,
                                                      float lambda_dssim, float inv_np, double *__restrict__ out) {
@@ -421,6 +751,41 @@ namespace mskern {
 
 int ssim_num_blocks(int W, int H) { return ((W + TS - 1) / TS) * ((H + TS - 1) / TS); }
 
+// The one-kernel form needs its buffer-load offsets (rows -10 .. H + 30 of
+// the 12-byte pixels, plus the out-of-image base) inside 32 bits.
+static bool g_two_pass = false;
+static bool stream_fits(int W, int H) {
+    return !g_two_pass && (int64_t)(H + 32) * W * 12 < (int64_t(1) << 30);
+}
+void set_loss_two_pass(bool on) { g_two_pass = on; }
+
+// Row segments of the one-kernel form.  Each wave re-makes the 20 rows
+// above its segment, so segments are long; the kernel holds 2 waves per
+// SIMD (its registers), and it is bound by VALU issue, so the segment count
+// is the largest whose waves (segments x strips x 3) all run at once on the
+// 1024 SIMDs of an MI355X -- a second, partial round of waves would leave
+// most SIMDs idle -- and one segment per 64 rows at most.
+constexpr int kStreamWaves = 2048;
+static void stream_plan(int W, int H, StreamArgs &A) {
+    A.nstrips = (W + kSO - 1) / kSO;
+    const int per_row = 3 * A.nstrips;
+    int nseg = kStreamWaves / per_row;
+    const int max_seg = (H + 63) / 64;
+    nseg = std::max(1, std::min(nseg, max_seg));
+    A.seg_rows = (H + nseg - 1) / nseg;
+    nseg = (H + A.seg_rows - 1) / A.seg_rows;
+    A.units = nseg * per_row;
+}
+
+int loss_num_partials(int W, int H) {
+    if (!stream_fits(W, H)) return ssim_num_blocks(W, H);
+    StreamArgs A;
+    stream_plan(W, H, A);
+    return A.units;
+}
+
+bool loss_needs_maps(int W, int H) { return !stream_fits(W, H); }
+
 void launch_loss_fwd_bwd(hipStream_t s, int W, int H, const float *img, const float *gt, const float *dist,
                          float lambda_l1, float lambda_dist, float lambda_dssim, const float window[11],
                          float *gm1, float *gs1, float *gs12, double *partials, double *loss_out,
@@ -429,15 +794,32 @@ void launch_loss_fwd_bwd(hipStream_t s, int W, int H, const float *img, const fl
     const float g = -lambda_dssim * inv_np;
     Window win;
     for (int j = 0; j < 11; ++j) win.w[j] = window[j];
-    // one workgroup per 32x32 tile, the grid padded to a multiple of the 8 XCDs
-    const int T = ssim_num_blocks(W, H);
-    const dim3 grid(((T + 7) / 8) * 8);
-    hipLaunchKernelGGL(k_ssim_fwd, grid, dim3(kThreads), 0, s, W, H, img, gt, dist, lambda_l1, lambda_dist, inv_np,
-                       g, win, gm1, gs1, gs12, partials);
-    hipLaunchKernelGGL(k_ssim_bwd, grid, dim3(kThreads), 0, s, W, H, img, gt, gm1, gs1, gs12, lambda_l1, inv_np,
-                       win, dL_dimg);
-    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(1024), 0, s, T, partials, lambda_dssim,
-                       inv_np, loss_out);
+    int nparts;
+    if (stream_fits(W, H)) {
+        StreamArgs A;
+        stream_plan(W, H, A);
+        A.W = W;
+        A.H = H;
+        A.lambda_l1 = lambda_l1;
+        A.lambda_dist = lambda_dist;
+        A.inv_np = inv_np;
+        A.inv_HW = inv_np * 3.0f;
+        A.g = g;
+        // one wave per unit, the grid padded to a multiple of the 8 XCDs
+        const dim3 grid(((A.units + 7) / 8) * 8);
+        hipLaunchKernelGGL(k_ssim_stream, grid, dim3(64), 0, s, A, win, img, gt, dist, dL_dimg, partials);
+        nparts = A.units;
+    } else {
+        // one workgroup per 32x32 tile, the grid padded to a multiple of the 8 XCDs
+        const int T = ssim_num_blocks(W, H);
+        const dim3 grid(((T + 7) / 8) * 8);
+        hipLaunchKernelGGL(k_ssim_fwd, grid, dim3(kThreads), 0, s, W, H, img, gt, dist, lambda_l1, lambda_dist,
+                           inv_np, g, win, gm1, gs1, gs12, partials);
+        hipLaunchKernelGGL(k_ssim_bwd, grid, dim3(kThreads), 0, s, W, H, img, gt, gm1, gs1, gs12, lambda_l1,
+                           inv_np, win, dL_dimg);
+        nparts = T;
+    }
+    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(1024), 0, s, nparts, partials, lambda_dssim, inv_np, loss_out);
 }
 
 }  // namespace mskern

@@ -156,6 +156,12 @@ void launch_check_rcp(hipStream_t s, int efield, unsigned long long *bad);
 // k_ssim.hip
 void launch_rgba8(hipStream_t s, const float *img, int64_t n, uint32_t *out);
 int ssim_num_blocks(int W, int H);
+// Loss partials (16 bytes each) that launch_loss_fwd_bwd writes, and whether
+// it uses the three gradient maps gm1 / gs1 / gs12 (the two-pass form, for
+// images too large for the one-kernel form's 32-bit offsets).
+int loss_num_partials(int W, int H);
+bool loss_needs_maps(int W, int H);
+void set_loss_two_pass(bool on);  // force the two-pass form (self-test hook)
 void launch_loss_fwd_bwd(hipStream_t s, int W, int H, const float *img, const float *gt, const float *dist,
                          float lambda_l1, float lambda_dist, float lambda_dssim, const float window[11],
                          float *gm1, float *gs1, float *gs12, double *partials, double *loss_out,
