@@ -353,13 +353,15 @@ int msplat_hip_set_wide_keys(int on);
  * (lists of at least 4096 entries and 4x the frame's mean list).  No
  * counterpart in the reference. */
 int msplat_hip_set_deep_tile_len(int len);
-/* Loss self-test hook.  The SSIM + L1 loss runs as one streaming kernel for
- * every image whose byte offsets fit in 32 bits (up to ~89 MP) and as two
- * tiled passes through three gradient maps beyond that; on != 0 forces the
- * two-pass form at any size, so the tests can check it against the golden
- * model on small images; dL/dimage is the same either way.  No counterpart
- * in the reference. */
-int msplat_hip_set_loss_two_pass(int on);
+/* Loss self-test hook.  The SSIM + L1 loss has two forms with the same
+ * dL/dimage bit for bit: one streaming kernel, used for images of about
+ * 4.7 MP and more (row segments of at least 128 rows) whose byte offsets fit
+ * in 32 bits (up to ~89 MP), and two tiled passes through three gradient
+ * maps otherwise.  form 1 forces the streaming form wherever it fits, form
+ * 2 the two-pass form, 0 restores the choice by size, so the tests can
+ * check both against the golden model on small images.  No counterpart in
+ * the reference. */
+int msplat_hip_set_loss_form(int form);
 /* Blend-log pool self-test hook.  A frame's pool holds `chunks` chunks of
  * 64 entries instead of the size estimated from its intersection count, or
  * more once an overflow grew it: a step whose log overflows the pool

@@ -1590,10 +1590,14 @@ int msplat_hip_set_wide_keys(int on) {
     API_END
 }
 
-int msplat_hip_set_loss_two_pass(int on) {
+int msplat_hip_set_loss_form(int form) {
     API_BEGIN
     ENSURE_INIT();
-    mskern::set_loss_two_pass(on != 0);
+    if (form < 0 || form > 2) {
+        set_err("loss form %d: expected 0 (by size), 1 (streaming) or 2 (two-pass)", form);
+        return MSPLAT_E_ARG;
+    }
+    mskern::set_loss_form(form);
     return MSPLAT_OK;
     API_END
 }

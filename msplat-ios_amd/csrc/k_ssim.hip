@@ -8,12 +8,12 @@
 // dL/dssim_map is a known constant (-lambda / 3HW), the per-pixel SSIM
 // partials can be produced in the same pass as the forward statistics, and
 // the backward needs nothing else.  Two forms:
-//   - k_ssim_stream (every image whose buffer offsets fit in 32 bits): one
-//     kernel, one wave per (column strip, row segment, channel), carrying
-//     each pixel from its inputs to dL/dimg while the wave walks down the
-//     strip with the vertical blur windows in registers (see the section
-//     below);
-//   - the two-pass form for larger images:
+//   - k_ssim_stream (images of about 4.7 MP and more, up to the ~89 MP its
+//     32-bit offsets allow): one kernel, one wave per (column strip, row
+//     segment, channel), carrying each pixel from its inputs to dL/dimg
+//     while the wave walks down the strip with the vertical blur windows in
+//     registers (see the section below);
+//   - the two-pass form for the other images:
 //     pass 1 (k_ssim_fwd): per channel, img and gt (+5-pixel halo) -> the 5
 //          separable blurs (horizontal, then vertical, as the reference) ->
 //          SSIM map, loss partials and the three per-pixel gradient maps
@@ -138,6 +138,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 4))
                                                        Window win, float *__restrict__ gm1,
                                                        float *__restrict__ gs1, float *__restrict__ gs12,
                                                        double *__restrict__ partials) {
+    // the window in VGPRs (a VALU instruction that reads an SGPR issues
+    // slower; see k_ssim_stream)
+    Window wv;
+#pragma unroll
+    for (int k = 0; k < 11; ++k) asm volatile("v_mov_b32 %0, %1" : "=v"(wv.w[k]) : "s"(win.w[k]));
     __shared__ __align__(16) float s_a[RS][AST];
     __shared__ __align__(16) float s_b[RS][AST];
     __shared__ __align__(16) float s_h[5][RS][BST];
@@ -173,7 +178,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 4))
                   e22[4] = {0.f, 0.f, 0.f, 0.f}, e12[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 11; ++j) {
-                const float w = win.w[j];
+                const float w = wv.w[j];
 #pragma unroll
                 for (int o = 0; o < 4; ++o) {
                     const float av = a[o + j], bv = b[o + j];
@@ -204,7 +209,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 4))
                 for (int o = 0; o < 4; ++o) {
                     float acc = 0.f;
 #pragma unroll
-                    for (int j = 0; j < 11; ++j) acc = __builtin_fmaf(win.w[j], col[o + j], acc);
+                    for (int j = 0; j < 11; ++j) acc = __builtin_fmaf(wv.w[j], col[o + j], acc);
                     st[s][o] = acc;
                 }
             }
@@ -688,14 +693,21 @@ __global__ __launch_bounds__(64) void k_ssim_stream(StreamArgs A, Window win, co
     const uint32_t nrec = (uint32_t)A.W * (uint32_t)A.H * 12u;
     const __amdgpu_buffer_rsrc_t rimg = __builtin_amdgcn_make_buffer_rsrc((void *)img, (short)0, nrec, 0x00020000);
     const __amdgpu_buffer_rsrc_t rgt = __builtin_amdgcn_make_buffer_rsrc((void *)gt, (short)0, nrec, 0x00020000);
+    // the window in VGPRs: a VALU instruction that reads an SGPR issues at
+    // about 60% of the rate of one whose operands are all VGPRs (gfx950,
+    // measured on independent FMA chains), and almost every instruction
+    // here is a tap of the window
+    Window wv;
+#pragma unroll
+    for (int k = 0; k < 11; ++k) asm volatile("v_mov_b32 %0, %1" : "=v"(wv.w[k]) : "s"(win.w[k]));
     const int ib0 = y0 - 2 * RAD;
     stream_load(S, rimg, rgt, (uint32_t)ib0 * (uint32_t)A.W * 12u);
     const int nbody = (y1 - y0 + 4 * RAD + kRing - 1) / kRing;
     for (int bi = 0; bi < nbody; ++bi) {
         const int ib = ib0 + bi * kRing;
-        stream_pass<0, 4>(A, win, L, S, rimg, rgt, ib, x0, y0, y1, c, dist, dL);
-        stream_pass<4, 4>(A, win, L, S, rimg, rgt, ib + 4, x0, y0, y1, c, dist, dL);
-        stream_pass<8, 3>(A, win, L, S, rimg, rgt, ib + 8, x0, y0, y1, c, dist, dL);
+        stream_pass<0, 4>(A, wv, L, S, rimg, rgt, ib, x0, y0, y1, c, dist, dL);
+        stream_pass<4, 4>(A, wv, L, S, rimg, rgt, ib + 4, x0, y0, y1, c, dist, dL);
+        stream_pass<8, 3>(A, wv, L, S, rimg, rgt, ib + 8, x0, y0, y1, c, dist, dL);
     }
     double ts = S.ssim_acc, tl = S.l1_acc;
 #pragma unroll
@@ -751,13 +763,8 @@ namespace mskern {
 
 int ssim_num_blocks(int W, int H) { return ((W + TS - 1) / TS) * ((H + TS - 1) / TS); }
 
-// The one-kernel form needs its buffer-load offsets (rows -10 .. H + 30 of
-// the 12-byte pixels, plus the out-of-image base) inside 32 bits.
-static bool g_two_pass = false;
-static bool stream_fits(int W, int H) {
-    return !g_two_pass && (int64_t)(H + 32) * W * 12 < (int64_t(1) << 30);
-}
-void set_loss_two_pass(bool on) { g_two_pass = on; }
+static int g_form = 0;
+void set_loss_form(int form) { g_form = form; }
 
 // Row segments of the one-kernel form.  Each wave re-makes the 20 rows
 // above its segment, so segments are long; the kernel holds 2 waves per
@@ -766,6 +773,10 @@ void set_loss_two_pass(bool on) { g_two_pass = on; }
 // 1024 SIMDs of an MI355X -- a second, partial round of waves would leave
 // most SIMDs idle -- and one segment per 64 rows at most.
 constexpr int kStreamWaves = 2048;
+// Below this many rows per segment the 20 re-made rows cost more than the
+// two-pass form's map round trip (measured: 1297x840 and 1920x1080 frames,
+// 60- and 64-row segments, ran 35% and 10% slower streaming).
+constexpr int kStreamMinRows = 128;
 static void stream_plan(int W, int H, StreamArgs &A) {
     A.nstrips = (W + kSO - 1) / kSO;
     const int per_row = 3 * A.nstrips;
@@ -777,14 +788,24 @@ static void stream_plan(int W, int H, StreamArgs &A) {
     A.units = nseg * per_row;
 }
 
+// The streaming form's offsets (rows -10 .. H + 30 of the 12-byte pixels,
+// plus the out-of-image base) must fit in 32 bits.
+static bool use_stream(int W, int H) {
+    if (g_form == 2 || (int64_t)(H + 32) * W * 12 >= (int64_t(1) << 30)) return false;
+    if (g_form == 1) return true;
+    StreamArgs A;
+    stream_plan(W, H, A);
+    return A.seg_rows >= kStreamMinRows;
+}
+
 int loss_num_partials(int W, int H) {
-    if (!stream_fits(W, H)) return ssim_num_blocks(W, H);
+    if (!use_stream(W, H)) return ssim_num_blocks(W, H);
     StreamArgs A;
     stream_plan(W, H, A);
     return A.units;
 }
 
-bool loss_needs_maps(int W, int H) { return !stream_fits(W, H); }
+bool loss_needs_maps(int W, int H) { return !use_stream(W, H); }
 
 void launch_loss_fwd_bwd(hipStream_t s, int W, int H, const float *img, const float *gt, const float *dist,
                          float lambda_l1, float lambda_dist, float lambda_dssim, const float window[11],
@@ -795,7 +816,7 @@ void launch_loss_fwd_bwd(hipStream_t s, int W, int H, const float *img, const fl
     Window win;
     for (int j = 0; j < 11; ++j) win.w[j] = window[j];
     int nparts;
-    if (stream_fits(W, H)) {
+    if (use_stream(W, H)) {
         StreamArgs A;
         stream_plan(W, H, A);
         A.W = W;

@@ -161,7 +161,7 @@ int ssim_num_blocks(int W, int H);
 // images too large for the one-kernel form's 32-bit offsets).
 int loss_num_partials(int W, int H);
 bool loss_needs_maps(int W, int H);
-void set_loss_two_pass(bool on);  // force the two-pass form (self-test hook)
+void set_loss_form(int form);  // 0: by size, 1: streaming, 2: two-pass (self-test hook)
 void launch_loss_fwd_bwd(hipStream_t s, int W, int H, const float *img, const float *gt, const float *dist,
                          float lambda_l1, float lambda_dist, float lambda_dssim, const float window[11],
                          float *gm1, float *gs1, float *gs12, double *partials, double *loss_out,

@@ -74,7 +74,7 @@ EXPORTS = [
     "msplat_hip_raster_bwd", "msplat_hip_project_bwd", "msplat_hip_project_bwd_adam", "msplat_hip_last", "msplat_hip_enable_timing",
     "msplat_hip_stage_times", "msplat_hip_last_pairs_evaluated", "msplat_hip_last_raster_counts",
     "msplat_hip_check_fast_rcp", "msplat_hip_set_wide_keys", "msplat_hip_set_deep_tile_len",
-    "msplat_hip_set_loss_two_pass",
+    "msplat_hip_set_loss_form",
     "msplat_hip_set_log_pool_chunks", "msplat_hip_log_pool_stats",
     "msplat_hip_tsdf_integrate",
     "msplat_hip_marching_cubes", "msplat_hip_mc_table", "msplat_hip_unproject_depth", "msplat_hip_render_3dgs",
@@ -132,7 +132,7 @@ def lib() -> C.CDLL:
         "msplat_hip_check_fast_rcp": (I, [I, I, C.POINTER(C.c_int64)]),
         "msplat_hip_set_wide_keys": (I, [I]),
         "msplat_hip_set_deep_tile_len": (I, [I]),
-        "msplat_hip_set_loss_two_pass": (I, [I]),
+        "msplat_hip_set_loss_form": (I, [I]),
         "msplat_hip_set_log_pool_chunks": (I, [I]),
         "msplat_hip_log_pool_stats": (I, [P]),
         "msplat_hip_densify_3dgs": (I, [I, I, F, F, F, I, F, F, F, I, P, P, P, F, P * 6, I, P * 6, P * 6, P,

@@ -192,21 +192,21 @@ def _device(a):
     return E.DeviceArray.from_numpy(np.ascontiguousarray(a, np.float32))
 
 
-@pytest.mark.parametrize("two_pass", [False, True], ids=["stream", "two_pass"])
+@pytest.mark.parametrize("form", [1, 2], ids=["stream", "two_pass"])
 @pytest.mark.parametrize("shape,ldist", [((208, 320), 0.0), ((37, 53), 0.0), ((1, 1), 0.0), ((11, 150), 0.0),
                                           ((300, 517), 0.0), ((97, 203), 0.05), ((1030, 1100), 0.0)])
-def test_loss_fwd_bwd_bitexact(shape, ldist, two_pass, orc, eng):
+def test_loss_fwd_bwd_bitexact(shape, ldist, form, orc, eng):
     # stream: one wave per (54-column strip, row segment, channel); (1030,
     # 1100) has 21 strips, the last one ragged, and 17 row segments.
     # two_pass: (300, 517) is mostly interior 32x32 tiles, whose staging
     # skips the bounds checks, with a ragged right and bottom edge.
     # (97, 203) adds the distortion term of the loss.
     H, W = shape
-    E.check(E.lib().msplat_hip_set_loss_two_pass(1 if two_pass else 0))
+    E.check(E.lib().msplat_hip_set_loss_form(form))
     try:
         _check_loss(H, W, ldist, orc)
     finally:
-        E.check(E.lib().msplat_hip_set_loss_two_pass(0))
+        E.check(E.lib().msplat_hip_set_loss_form(0))
 
 
 def _check_loss(H, W, ldist, orc):

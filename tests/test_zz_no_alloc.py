@@ -29,9 +29,19 @@ def _run(E, fn, W, H, d_img, d_gt, d_dist, ldist):
     return d_dL.numpy(), loss.value, ssim.value
 
 
-def test_noalloc_loss_matches_allocating_entry(eng):
+@pytest.mark.parametrize("form", [0, 1], ids=["by_size", "stream"])
+def test_noalloc_loss_matches_allocating_entry(form, eng):
     E = eng
     L = E.lib()
+    # form 0 picks the two-pass form at these sizes; form 1 forces the streaming one
+    E.check(L.msplat_hip_set_loss_form(form))
+    try:
+        _match_entries(E, L)
+    finally:
+        E.check(L.msplat_hip_set_loss_form(0))
+
+
+def _match_entries(E, L):
     # the largest accepted image, then a smaller, ragged one over the same scratch
     for (W, H), seed, ldist in [((2048, 1024), 1, 0.0), ((333, 217), 2, 0.05)]:
         print(f"[no_alloc] {W}x{H} seed {seed}", flush=True)
