@@ -57,8 +57,9 @@ __device__ __forceinline__ const unsigned long long *merged_keys(int cnt, const 
 //
 // Exclusive scan of a count array (prefix_sum_kernel,
 // msplat_metal.metal:3093-3145): local pass over 2048 counts per workgroup,
-// block totals, add pass.  stats[0] receives the total, stats[1] the
-// largest count (stats[1] must be zero on entry).
+// block totals, add pass; up to 32768 counts one workgroup does all three
+// (k_scan_small).  stats[0] receives the total, stats[1] the largest count
+// (stats[1] must be zero on entry).
 
 constexpr int kScanT = 256, kScanI = 8, kScanChunk = kScanT * kScanI;
 
@@ -150,6 +151,61 @@ __global__ __launch_bounds__(kScanT) void k_off_add(int T, int *__restrict__ off
             if (cursor) cursor[base + k] = v;
         }
     if (blockIdx.x == 0 && threadIdx.x == 0) offsets[T] = stats[0];
+}
+
+// The same scan in one workgroup of 1024 threads, for counts[] short enough
+// that launching three kernels costs more than walking them: 8192 counts
+// per round (8 consecutive per thread), the rounds chained by a carry.
+constexpr int kScanSmallT = 1024, kScanSmallChunk = kScanSmallT * kScanI;
+constexpr int kScanSmallMax = 4 * kScanSmallChunk;  // at most 4 rounds
+
+__global__ __launch_bounds__(kScanSmallT) void k_scan_small(int T, const int *__restrict__ counts,
+                                                            int *__restrict__ offsets, int *__restrict__ cursor,
+                                                            int *__restrict__ stats) {
+    __shared__ int s_w[kScanSmallT / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int carry = 0, mx = 0;
+    for (int base = 0; base < T; base += kScanSmallChunk) {
+        const int i0 = base + (int)threadIdx.x * kScanI;
+        int v[kScanI], sum = 0;
+#pragma unroll
+        for (int k = 0; k < kScanI; ++k) {
+            v[k] = i0 + k < T ? counts[i0 + k] : 0;
+            sum += v[k];
+            mx = max(mx, v[k]);
+        }
+        int incl = sum;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int o = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += o;
+        }
+        __syncthreads();  // the previous round's reads of s_w are done
+        if (lane == 63) s_w[wave] = incl;
+        __syncthreads();
+        int off = 0, tot = 0;
+#pragma unroll
+        for (int w = 0; w < kScanSmallT / 64; ++w) {
+            off += w < wave ? s_w[w] : 0;
+            tot += s_w[w];
+        }
+        int run = carry + off + incl - sum;
+#pragma unroll
+        for (int k = 0; k < kScanI; ++k)
+            if (i0 + k < T) {
+                offsets[i0 + k] = run;
+                if (cursor) cursor[i0 + k] = run;
+                run += v[k];
+            }
+        carry += tot;
+    }
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) mx = max(mx, __shfl_xor(mx, d, 64));
+    if (lane == 0 && mx > 0) atomicMax(&stats[1], mx);
+    if (threadIdx.x == 0) {
+        stats[0] = carry;
+        offsets[T] = carry;
+    }
 }
 
 // ---- super-tile histogram and scatter -------------------------------------
@@ -817,6 +873,10 @@ int64_t tile_scan_temp_ints(int T) { return (T + kScanChunk - 1) / kScanChunk + 
 // stats[0] = total, stats[1] = max(stats[1], largest count).
 static void launch_scan_counts(hipStream_t s, int T, const int *counts, int *offsets, int *cursor, int *stats,
                                int *temp) {
+    if (T <= kScanSmallMax) {
+        hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(kScanSmallT), 0, s, T, counts, offsets, cursor, stats);
+        return;
+    }
     const int nb = (T + kScanChunk - 1) / kScanChunk;
     hipLaunchKernelGGL(k_off_local, dim3(nb), dim3(kScanT), 0, s, T, counts, offsets, temp, stats);
     hipLaunchKernelGGL(k_off_totals, dim3(1), dim3(1024), 0, s, nb, temp, stats);
