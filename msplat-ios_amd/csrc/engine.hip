@@ -580,7 +580,7 @@ int forward_locked(const MsplatCamera *cam, const MsplatGaussians *g, const floa
         CHECK(ensure(E.keys_tmp, (size_t)S_total * 8));
         CHECK(ensure(E.merge_base, (size_t)NS * 4));
     }
-    if (super_max > mskern::kSuperHugeList) {
+    if (mskern::bin_chunk_parallel(super_max, NS)) {
         CHECK(ensure(E.huge_list, (size_t)NS * 4));
         CHECK(ensure(E.chunk_base, (size_t)NS * 4));
         CHECK(ensure(E.chunk_counts, (size_t)mskern::big_chunk_ints(S_total, NS) * 4));

@@ -38,6 +38,8 @@ constexpr int kChunk = 4096;  // keys per LDS sort (32 KB of u64)
 // rest of the pass); shorter ones stay within their super-tile's workgroup.
 constexpr int kHuge = 4 * kChunk;
 constexpr int kSuper = 4;     // tiles per super-tile side
+static_assert(kHuge == mskern::kSuperHugeList && kChunk == mskern::kSuperSortChunk && kSuper == mskern::kSuperTile,
+              "the host sizes the binning buffers with these");
 
 // The merge passes (k_merge_path) take a list of cnt > kChunk keys through
 // merge_passes(cnt) passes (L = kChunk, 2 kChunk, ... below cnt), pass p
@@ -463,9 +465,10 @@ __device__ __forceinline__ void count_tiles(const unsigned long long *__restrict
 // Longer lists are only queued, on big_list and huge_list (their tile counts
 // zeroed): k_sort_chunks sorts their runs on many workgroups, and after the
 // merge k_count_chunks / k_emit_chunks count and emit them chunk by chunk.
-// huge_th is kHuge, or kChunk when some list exceeds kHuge: the merge and
-// chunk passes then run anyway, and every list above kChunk joins them
-// instead of holding one workgroup for several serial chunk sorts.
+// huge_th is kHuge, or kChunk when the frame's long lists go chunk-parallel
+// (bin_chunk_parallel: some list exceeds kHuge): every list above kChunk
+// then joins the merge and chunk passes instead of holding one workgroup
+// for several serial chunk sorts.
 template <bool PACKED>
 __global__ __launch_bounds__(kSortThreads) void k_sort_super(int tiles_x, int tiles_y, int sxn,
                                                              const int *__restrict__ offsets,
@@ -919,7 +922,7 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
     if (n > 0)
         hipLaunchKernelGGL(packed ? k_scatter_super<true> : k_scatter_super<false>, dim3(blocks), dim3(kBinThreads), 0,
                            s, n, chunk, sxn, NS, radii, r2, depths, super_offsets, super_cm, k);
-    const bool big = super_max > kHuge;
+    const bool big = bin_chunk_parallel(super_max, NS);
     const int huge_th = big ? kChunk : kHuge;
     hipLaunchKernelGGL(packed ? k_sort_super<true> : k_sort_super<false>, dim3(NS), dim3(kSortThreads), 0, s, tiles_x,
                        tiles_y, sxn, super_offsets, k, r2, tile_counts, big_list, super_stats, huge_list, huge_stats,

@@ -64,10 +64,10 @@ constexpr int kBinMaxBlocks = 256;
 // tile_stats = {intersections, largest tile}, zero on entry) and the
 // per-tile sorted gaussian ids.  When super_max > 4096 the long lists need
 // super_keys_tmp (the size of super_keys) and merge_base[NS], and
-// super_stats[3] receives their merge-tile count; when super_max >
-// kSuperHugeList huge_list[NS], huge_stats[2] (zero on entry), chunk_base[NS]
-// and chunk_counts[big_chunk_ints(total, NS)].  total_keys = the pair count
-// (super_stats[0]).
+// super_stats[3] receives their merge-tile count; when
+// bin_chunk_parallel(super_max, NS) huge_list[NS], huge_stats[2] (zero on
+// entry), chunk_base[NS] and chunk_counts[big_chunk_ints(total, NS)].
+// total_keys = the pair count (super_stats[0]).
 // The deep-tile scan launch_bin_tiles queues once the tile offsets exist
 // (before the emission kernels): the tiles with at least `len` entries into
 // `list`, their number into *count, copied to *host_count.
@@ -82,6 +82,13 @@ void launch_bin_tiles(hipStream_t s, int n, int tiles_x, int tiles_y, const int 
                       int total_keys, int *tile_counts, int *tile_offsets, int *tile_stats, int *tile_temp, int *ids,
                       bool force_wide_keys, const DeepScan *deep = nullptr);
 constexpr int kSuperHugeList = 4 * 4096;
+// Whether the super-tile lists above 4096 keys are sorted, counted and
+// emitted chunk-parallel (k_sort_chunks, k_count_chunks, k_emit_chunks):
+// when some list exceeds kSuperHugeList, which a workgroup would otherwise
+// hold for several serial chunk sorts.  (Also taking that path for frames
+// with few super-tiles, e.g. 294 at 1297x840, measured 1-3% slower steps:
+// its extra launches cost more than the serial sorts of lists of <= 16k.)
+inline bool bin_chunk_parallel(int super_max, int /*num_super*/) { return super_max > kSuperHugeList; }
 // Ints of chunk_counts: 16 per 4096-key chunk of the long lists, at most
 // total / 4096 + NS chunks.
 inline int64_t big_chunk_ints(int64_t total_keys, int NS) { return (total_keys / 4096 + NS) * 16; }
