@@ -296,3 +296,36 @@ def test_densify_workload_full_size(orc, eng):
     print(f"[densify] splat counts per cycle: {counts}", flush=True)
     assert len(counts) >= 4 and counts[-1] >= 2_000_000
     assert all(b > a for a, b in zip(counts, counts[1:]))
+
+
+def test_loss_forms_agree_full_size(eng):
+    """The SSIM + L1 loss at the headline frame size (5187x3361: the
+    streaming form's size) against the two-pass form on the same images:
+    dL/dimage bit-identical, the loss and the SSIM sum equal up to the fp64
+    summation order.  Pins the streaming form at its real shape (97 strips,
+    7 row segments per strip) without the golden model's minutes."""
+    W, H = 5187, 3361
+    print(f"[loss forms] {W}x{H}", flush=True)
+    rng = np.random.default_rng(31)
+    gt = rng.uniform(0.0, 1.0, (H, W, 3)).astype(np.float32)
+    img = np.clip(gt + rng.normal(0.0, 0.05, gt.shape).astype(np.float32), 0.0, 1.0)
+    eq = rng.random((H, W)) < 0.1  # exact-equality pixels: sign(0) = 0 in the L1 gradient
+    img[eq] = gt[eq]
+    d_img, d_gt = _device(img), _device(gt)
+    out = {}
+    for form in (1, 2):
+        E.check(E.lib().msplat_hip_set_loss_form(form))
+        try:
+            d_dL = E.DeviceArray((H, W, 3))
+            loss, ssim = C.c_double(), C.c_double()
+            E.check(E.lib().msplat_hip_loss_fwd_bwd(W, H, d_img.ptr, d_gt.ptr, None, 0.8, 0.0, 0.2, d_dL.ptr,
+                                                   C.byref(loss), C.byref(ssim)))
+            out[form] = (d_dL.numpy(), loss.value, ssim.value)
+        finally:
+            E.check(E.lib().msplat_hip_set_loss_form(0))
+    (dl1, l1, s1), (dl2, l2, s2) = out[1], out[2]
+    assert np.isfinite(dl1).all()
+    nbad = int((dl1 != dl2).sum())
+    assert nbad == 0, f"{nbad} dL/dimage entries differ between the loss forms"
+    assert abs(l1 - l2) <= 1e-9 * abs(l2), (l1, l2)
+    assert abs(s1 - s2) <= 1e-9 * abs(s2), (s1, s2)
