@@ -135,16 +135,26 @@ def _timed_steps(E, step, first: int, steps: int, ncams: int):
 
 
 def _stage_breakdown(E, step, first: int, steps: int, ncams: int) -> dict[str, float]:
-    """Mean per-stage milliseconds (HIP events on the engine stream around
-    every stage) over `steps` further train steps, outside the timed run."""
-    total: dict[str, float] = {}
+    """Per-stage milliseconds (HIP events on the engine stream around every
+    stage) over `steps` further train steps, outside the timed run.  Each
+    stage's mean drops its highest and lowest sample when there are five or
+    more: the binning stage ends in a host synchronisation, so one step in
+    which the host thread stalls there would otherwise move that stage's
+    mean many times over."""
+    samples: dict[str, list[float]] = {}
     E.enable_timing(True)
     for k in range(steps):
         step((first + k) % ncams)
         for name, ms in E.stage_times().items():
-            total[name] = total.get(name, 0.0) + ms
+            samples.setdefault(name, []).append(ms)
     E.enable_timing(False)
-    return {k: v / steps for k, v in total.items()}
+    out = {}
+    for name, v in samples.items():
+        v = sorted(v)
+        if len(v) >= 5:
+            v = v[1:-1]
+        out[name] = sum(v) / len(v)
+    return out
 
 
 
