@@ -1115,7 +1115,7 @@ static int train_step_once(const MsplatCamera *cam, const MsplatGaussians *g, co
     HIPC(hipMemcpyAsync(E.pinned_d, E.loss.p, 2 * sizeof(double), hipMemcpyDeviceToHost, s));
     stage_mark(ST_RASTER_BWD);
     CHECK(ensure(E.grads16, (size_t)N * 64));
-    HIPC(hipMemsetAsync(E.grads16.p, 0, (size_t)N * 64, s));
+    mskern::launch_zero16(s, P<float>(E.grads16), (int64_t)N * 4);
     const float inv_np = 1.0f / (float)((unsigned)H * (unsigned)W * 3u);
     const float ddist_uniform = lambda_dist * (inv_np * 3.0f);
     mskern::DeepTiles deep;
@@ -1224,7 +1224,7 @@ static int train_step3d_once(const MsplatCamera *cam, const MsplatGaussians *g, 
     HIPC(hipMemcpyAsync(E.pinned_d, E.loss.p, 2 * sizeof(double), hipMemcpyDeviceToHost, s));
     stage_mark(ST_RASTER_BWD);
     CHECK(ensure(E.grads16, (size_t)N * 64));
-    HIPC(hipMemsetAsync(E.grads16.p, 0, (size_t)N * 64, s));
+    mskern::launch_zero16(s, P<float>(E.grads16), (int64_t)N * 4);
     // the layout the logging forward planned (a new plan could reallocate
     // the pool under the log)
     const msr::BlendLog blog = E.log_desc;

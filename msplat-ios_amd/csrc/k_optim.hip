@@ -31,6 +31,14 @@ __global__ void k_clamp_max(float *__restrict__ p, int64_t n, float value) {
         if (p[i] > value) p[i] = value;
 }
 
+// Zeroes n float4s, one 16-byte store per thread in a single pass.  It
+// clears the raster backward's per-splat gradient rows before each step:
+// 192 MB at 3M splats, which hipMemsetAsync wrote at about 2.3 TB/s.
+__global__ __launch_bounds__(256) void k_zero16(float4 *__restrict__ p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
 // RGBA8 of an [n,3] float image: (uint8)(clamp(x, 0, 1) * 255) per channel
 // (truncation, the host loop of renderFromPoseToBuffer, msplat_api.mm:207-236)
 // and alpha 255, one 4-byte store per pixel.
@@ -370,6 +378,12 @@ void launch_clamp_max(hipStream_t s, float *p, int64_t n, float value) {
     if (n <= 0) return;
     const int64_t blocks = std::min<int64_t>((n + 255) / 256, 65536);
     hipLaunchKernelGGL(k_clamp_max, dim3((unsigned)blocks), dim3(256), 0, s, p, n, value);
+}
+
+void launch_zero16(hipStream_t s, float *p, int64_t n_float4) {
+    if (n_float4 <= 0) return;
+    const int64_t blocks = (n_float4 + 255) / 256;
+    hipLaunchKernelGGL(k_zero16, dim3((unsigned)blocks), dim3(256), 0, s, reinterpret_cast<float4 *>(p), n_float4);
 }
 
 void launch_rgba8(hipStream_t s, const float *img, int64_t n, uint32_t *out) {

@@ -178,6 +178,8 @@ void launch_loss_fwd_bwd(hipStream_t s, int W, int H, const float *img, const fl
 void launch_adam(hipStream_t s, float *p, const float *g, float *m, float *v, int64_t n, float step, float b1,
                  float b2, float bc2_sqrt, float eps);
 void launch_clamp_max(hipStream_t s, float *p, int64_t n, float value);
+// p[0, 4 * n_float4) = 0; p 16-byte aligned.
+void launch_zero16(hipStream_t s, float *p, int64_t n_float4);
 int64_t scan_temp_ints(int64_t n);
 void launch_scan_i32(hipStream_t s, const int *in, int *out, int n, int *temp);
 
